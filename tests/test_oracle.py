@@ -1,0 +1,140 @@
+"""Pins of the CPU oracle: the reference VM's own outputs (tests/golden), its SplitMix64 vectors, and closed forms."""
+import json
+import math
+import struct
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import GOLDEN, REPO, golden_cases
+from kvm_amd import bundle as bl
+from kvm_amd import compiler, initgen
+from cases import W
+
+
+@pytest.mark.parametrize('case', golden_cases())
+def test_oracle_matches_reference_vm_bitwise(case):
+    d = GOLDEN / case
+    g = json.loads((d / 'golden.json').read_text())
+    r = oracle.run(d)
+    meta = json.loads((d / 'metadata.json').read_text())
+    for m, x in zip(meta['buffers'], r['buffers']):
+        want = np.array(g['buffers'][m['name']], np.int32 if m['dtype'] == 1 else np.float32)
+        assert np.array_equal(want.view(np.uint32), x.view(np.uint32)), m['name']
+    assert r['versions'] == g['versions']
+    assert [x['observed'] for x in g['reads']] == r['observed']
+
+
+def _vectors():
+    lines = (REPO / 'tests/golden/data/initgen_vectors.txt').read_text().split('\n')
+    for k in range(0, len(lines) - 1, 2):
+        seed, draws, bh, ch, n = lines[k].split()
+        f = lambda h: struct.unpack('<f', struct.pack('<I', int(h, 16)))[0]
+        yield int(seed), int(draws), f(bh), f(ch), int(n), [int(h, 16) for h in lines[k + 1].split()]
+
+
+def test_seeded_init_vectors():
+    """The reference's SplitMix64 known answers (tests/gpu/initgen_vectors.txt of the reference)."""
+    for seed, draws, bias, coef, n, want in _vectors():
+        assert initgen.seeded(seed, n, draws, bias, coef).view(np.uint32).tolist() == want
+        assert oracle.seeded(n, seed, draws, bias, coef).view(np.uint32).tolist() == want
+
+
+def _run_one(w):
+    b = compiler.compile_spec(w.spec())
+    return oracle.run(b), b
+
+
+def _get(r, b, name):
+    return r['buffers'][[m['name'] for m in b.metadata['buffers']].index(name)]
+
+
+def test_matmul_tile_closed_form():
+    """Tile GEMM against an fp64 product (a transposed operand or dropped term fails this)."""
+    w = W(3)
+    M, N, K = 70, 50, 33
+    w.buf('A', K, M), w.buf('B', N, K), w.buf('bias', 1, N), w.zeros('out', M, N)
+    for m0 in (0, 64):
+        w.task('matmul_tile', a='A', b='B', out='out', bias='bias', res=None, pre=None, m0=m0, n0=0, M=M, N=N, K=K, flags=3, alpha=0.5)
+    r, b = _run_one(w)
+    A, B, bias = (_get(r, b, n).astype(np.float64) for n in ('A', 'B', 'bias'))
+    want = 0.5 * (A.reshape(K, M).T @ B.reshape(N, K).T) + bias
+    got = _get(r, b, 'out').reshape(M, N)
+    assert np.abs(got - want).max() < 1e-5 * np.abs(want).max()
+
+
+def test_attention_closed_form_and_decode_consistency():
+    """Causal attention = softmax(QK^T*scale)V in fp64; decode attention of the last token = last row of the forward."""
+    w = W(4)
+    T, H, hd = 17, 2, 16
+    w.buf('q', T, H * hd), w.buf('k', T, H * hd), w.buf('v', T, H * hd)
+    w.zeros('o', T, H * hd), w.zeros('lse', H * T)
+    for h in range(H):
+        w.task('attn_fwd', q='q', k='k', v='v', o='o', lse='lse', b=0, h=h, q0=0, T=T, H=H, Hkv=H, hd=hd, scale=0.3)
+    r, b = _run_one(w)
+    q, k, v = (_get(r, b, n).astype(np.float64).reshape(T, H, hd) for n in 'qkv')
+    o = _get(r, b, 'o').reshape(T, H, hd)
+    for h in range(H):
+        s = q[:, h] @ k[:, h].T * 0.3
+        s[np.triu_indices(T, 1)] = -np.inf
+        p = np.exp(s - s.max(1, keepdims=True))
+        want = (p / p.sum(1, keepdims=True)) @ v[:, h]
+        assert np.abs(o[:, h] - want).max() < 1e-6
+    # decode: the cache holds k/v rows 0..T-1 (lens = T-1: the last token was just appended)
+    w2 = W(4)
+    w2.buf('q', T, H * hd), w2.buf('k', T, H * hd), w2.buf('v', T, H * hd)   # same seeds as above
+    qd = q[T - 1].reshape(1, -1).astype(np.float32)
+    w2.buf('qd', 1, H * hd, init={'kind': 'values', 'values': qd.ravel().tolist()})
+    for name, src in (('kc', k), ('vc', v)):
+        cache = np.zeros((H * T, hd), np.float32)
+        for h in range(H):
+            cache[h * T:(h + 1) * T] = src[:, h]
+        w2.buf(name, H * T, hd, init={'kind': 'values', 'values': cache.ravel().tolist()})
+    w2.ints('lens', [T - 1])
+    w2.zeros('od', 1, H * hd)
+    for h in range(H):
+        w2.task('attn_decode', q='qd', kc='kc', vc='vc', lens='lens', o='od', b=0, h=h, H=H, Hkv=H, hd=hd, Tmax=T, scale=0.3)
+    r2, b2 = _run_one(w2)
+    assert np.abs(_get(r2, b2, 'od') - o[T - 1].ravel()).max() < 1e-6
+
+
+def test_adamw_step1_fp64():
+    """AdamW at t=1 reduces to p(1-lr*wd) - lr*sign-like(g) (m/(1-b1) = g, v/(1-b2) = g^2)."""
+    w = W(5)
+    n = 64
+    w.buf('p', n), w.buf('g', n), w.zeros('m', n), w.zeros('v', n), w.ints('step', [1])
+    w.task('adamw', p='p', g='g', m='m', v='v', gscale=None, step='step', e0=0, e1=n, lr=1e-2, b1=0.9, b2=0.95, eps=1e-8, wd=0.1)
+    r, b = _run_one(w)
+    w0 = bl.materialize(b.metadata['buffers'][0]).astype(np.float64)
+    g = _get(r, b, 'g').astype(np.float64)
+    want = w0 * (1 - 1e-3) - 1e-2 * g / (np.abs(g) + 1e-8)
+    assert np.abs(_get(r, b, 'p') - want).max() < 1e-6
+
+
+def test_rope_inverse_and_head_rmsnorm():
+    w = W(6)
+    R, H, hd = 6, 2, 8
+    w.buf('x', R, H * hd), w.zeros('y', R, H * hd), w.zeros('z', R, H * hd), w.buf('g', hd), w.zeros('n', R, H * hd)
+    t = w.task('rope_fwd', x='x', out='y', pos=None, r0=0, r1=R, T=R, H=H, hd=hd, theta=1e6)
+    w.task('rope_bwd', after=[t], x='y', out='z', pos=None, r0=0, r1=R, T=R, H=H, hd=hd, theta=1e6)
+    w.task('head_rmsnorm', x='x', gamma='g', out='n', r0=0, r1=R, H=H, hd=hd, eps=1e-6)
+    r, b = _run_one(w)
+    x = _get(r, b, 'x').reshape(R, H, hd).astype(np.float64)
+    assert np.abs(_get(r, b, 'z').reshape(R, H, hd) - x).max() < 1e-5
+    g = _get(r, b, 'g').astype(np.float64)
+    want = x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6) * g
+    assert np.abs(_get(r, b, 'n').reshape(R, H, hd) - want).max() < 1e-5
+
+
+def test_gemv_bf16_closed_form():
+    """Decode GEMV with the RMSNorm prologue = bf16(rmsnorm(x)) @ W^T in fp64."""
+    w = W(7)
+    K, N = 64, 24
+    w.buf('x', 1, K), w.buf('gm', K), w.buf('w', N, K, 'bf16'), w.zeros('o', 1, N)
+    w.task('gemv_bf16', x='x', x2=None, gamma='gm', w='w', out='o', res=None, n0=0, n1=N, K=K, pro=1, eps=1e-6)
+    r, b = _run_one(w)
+    x, gm = (_get(r, b, n).astype(np.float64) for n in ('x', 'gm'))
+    W_ = _get(r, b, 'w').reshape(N, K).astype(np.float64)
+    v = bl.bf16_round((x / math.sqrt((x * x).mean() + 1e-6) * gm).astype(np.float32)).astype(np.float64)
+    assert np.abs(_get(r, b, 'o') - W_ @ v).max() < 1e-5

@@ -1,0 +1,112 @@
+// C ABI of the MI355X persistent task-graph executor (libkvm_exec.so).
+//
+// It replaces the reference's host executor class MvmExec (reference: mvm_exec.cu:492-1560) for one GPU: the caller
+// creates an executor, declares the buffer table, submits one or more ABI-v2 bundles, starts the persistent kernel and
+// collects the result. Plain pointers and sizes only; every function returns 0 (or a non-negative index) on success
+// and a negative KvmStatus on failure, with a message in kvm_last_error().
+#ifndef KVM_EXEC_H
+#define KVM_EXEC_H
+#include <stddef.h>
+#include <stdint.h>
+#include "mvm_task_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// Submit / call status (reference: MvmSubmit, mvm_exec.cu:410-413).
+enum KvmStatus {
+  KVM_STATUS_OK = 0, KVM_STATUS_BACKPRESSURE_TIMEOUT = -1, KVM_STATUS_TOO_BIG = -2, KVM_STATUS_DEVICE_ERROR = -3,
+  KVM_STATUS_CLOSED = -4, KVM_STATUS_INVALID = -5, KVM_STATUS_HIP_ERROR = -6,
+};
+
+// Executor sizing and behaviour (reference: MvmConfig, mvm_exec.cu:367-408; the fields this executor uses).
+typedef struct KvmConfig {
+  int blocks;                  // persistent workgroups; 0 = one per CU
+  int trace_on;                // 1: per-task timeline and execution witness (KvmTrace per task)
+  int num_vars;                // version variables
+  unsigned long long timeout_us;   // stall timeout: no task finished for this long while work is pending
+  int device;                  // HIP device ordinal
+} KvmConfig;
+
+// Buffer initialisation (reference: MvmInit, mvm_exec.cu:431-437).
+enum KvmInitKind { KVM_INIT_ZERO = 0, KVM_INIT_FILL = 1, KVM_INIT_VALUES = 2, KVM_INIT_SEEDED = 3 };
+typedef struct KvmInit {
+  int kind;
+  float value;                 // FILL (f32/bf16 value; i32 buffers take it as an integer)
+  const void* values;          // VALUES: rows*cols elements in the buffer's dtype (bf16 as raw uint16)
+  unsigned long long seed;     // SEEDED: SplitMix64 generator parameters as in the bundle metadata
+  int draws;
+  float bias, coef;
+} KvmInit;
+
+// One task's timeline (reference: MvmTrace, mvm_exec.cuh:167-174). Times are wall_clock64 ticks (100 MHz).
+typedef struct KvmTrace {
+  unsigned long long start, end;
+  int block, xcc, ver0, ver1;  // ver0/ver1: version of the task's wait variable at start / end (-1 none)
+  int exec_count, pad;         // exec_count: times the task ran (the exactly-once witness)
+} KvmTrace;
+
+typedef struct KvmResult {
+  int err_code, err_slot, err_a, err_b;   // first device error (0 none)
+  int done, admitted, grid;
+  float kernel_ms;
+} KvmResult;
+
+typedef struct KvmExec KvmExec;
+
+void kvm_config_default(KvmConfig* cfg);
+// Creates an executor on cfg->device. Returns NULL on failure (message in kvm_last_error(NULL)).
+KvmExec* kvm_create(const KvmConfig* cfg);
+void kvm_destroy(KvmExec* ex);
+const char* kvm_last_error(const KvmExec* ex);
+
+// Appends a buffer to the table (reference: MvmExec::add_buffer, mvm_exec.cu:582). dtype 0 f32, 1 i32, 2 bf16.
+// Returns the buffer index (dense, ascending).
+int kvm_add_buffer(KvmExec* ex, int rows, int cols, int dtype, const KvmInit* init);
+int kvm_nbufs(const KvmExec* ex);
+int kvm_buffer_dtype(const KvmExec* ex, int idx);
+// Device address of a buffer (for callers that share it with their own kernels), or NULL.
+void* kvm_buffer_device_ptr(const KvmExec* ex, int idx);
+// Overwrites a buffer with host data of its own dtype (bytes = rows*cols*element size).
+int kvm_write_buffer(KvmExec* ex, int idx, const void* host, size_t bytes);
+// Reads a buffer widened to f32 (i32 buffers: raw int32 bit patterns) (reference: read_buffer, mvm_exec.cu:1542-1553).
+int kvm_read_buffer(KvmExec* ex, int idx, float* out, size_t n);
+// Reads a buffer in its own dtype (bf16 as uint16).
+int kvm_read_raw(KvmExec* ex, int idx, void* out, size_t bytes);
+
+// Sets a version variable's value before start (reference: set_version).
+int kvm_set_version(KvmExec* ex, int var, int version);
+// Adds one bundle (reference: MvmExec::submit, mvm_exec.cu:742): its tasks' successor indices are bundle-local.
+// The host validates descriptors, arities, buffer indices/dtypes and operand extents; KVM_STATUS_INVALID on failure.
+// Bundles submitted before kvm_start run in one launch and share state only through version variables.
+int kvm_submit(KvmExec* ex, const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges,
+               const int32_t* args, int nargs);
+// Uploads the task graph, resets the scheduler state and launches the persistent kernel (asynchronous).
+int kvm_start(KvmExec* ex);
+// Waits for the launch, then fills `res` (reference: close/finish, mvm_exec.cu:1505-1540).
+int kvm_finish(KvmExec* ex, KvmResult* res);
+// Runs the whole submitted graph again on the current buffer contents (versions restart from their set values):
+// reset + launch, asynchronous. Used for repeated training steps / decode tokens; kvm_finish collects it.
+int kvm_relaunch(KvmExec* ex);
+// Launches `n` back-to-back runs without host synchronisation in between and returns the elapsed milliseconds
+// measured with HIP events around them (the timed region of the benchmark). Result of the last run via kvm_finish.
+int kvm_run_timed(KvmExec* ex, int n, float* ms);
+
+// Host-only validation of one bundle against a buffer table (shapes and dtypes in `bufs`; `p` unused): the checks
+// kvm_submit runs. Returns 0 when valid, else KVM_STATUS_INVALID with the reason in `err`. Needs no GPU.
+int kvm_validate(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs,
+                 const MvmBuf* bufs, int nbufs, int nvars, char* err, int errlen);
+
+int kvm_versions(KvmExec* ex, int32_t* out, int n);
+int kvm_trace(KvmExec* ex, KvmTrace* out, int n);
+int kvm_ntasks(const KvmExec* ex);
+// Name of a registry operator id, or NULL (reference: --check-ops).
+const char* kvm_op_name(int op_id);
+// Fills `out` with n SplitMix64 seeded values on the device and copies them back (initialiser known-answer test).
+int kvm_seeded_fill_test(unsigned long long seed, long long n, int draws, float bias, float coef, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,43 @@
+"""Builds the HIP executor library (kvm_amd/_build/libkvm_exec.so) and the kvm_exec CLI for gfx950 with hipcc."""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / 'csrc'
+OUT = HERE / '_build'
+LIB = OUT / 'libkvm_exec.so'
+CLI = OUT / 'kvm_exec'
+HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
+ARCH = os.environ.get('KVM_ARCH', 'gfx950')
+# Packed-FP32 instructions are disabled for all device code (they have given silently wrong results on these boxes).
+FLAGS = ['-O3', '-std=c++17', f'--offload-arch={ARCH}', '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+         '-Wno-unused-result', '-Wno-unused-value']
+
+
+def build(verbose: bool = False) -> Path:
+    OUT.mkdir(exist_ok=True)
+    srcs = sorted(CSRC.glob('*.h')) + sorted(CSRC.glob('*.hip')) + sorted((HERE.parent / 'include').glob('*'))
+    cmd = [HIPCC, *FLAGS, '-fPIC', '-shared', str(CSRC / 'exec.hip'), '-o', str(LIB)]
+    _run(cmd, verbose)
+    cli = [HIPCC, *FLAGS, str(CSRC / 'cli.cpp'), '-o', str(CLI), f'-L{OUT}', '-lkvm_exec', f'-Wl,-rpath,$ORIGIN']
+    _run(cli, verbose)
+    del srcs
+    return LIB
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(' '.join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError(f'hipcc failed ({r.returncode}): {" ".join(cmd)}')
+
+
+if __name__ == '__main__':
+    build(verbose=True)
+    print(LIB)

@@ -1,0 +1,195 @@
+// kvm_exec: command-line runner of ABI-v2 bundles on one MI355X, the counterpart of the reference's `mvm_exec` CLI
+// (reference: mvm_exec.cu:1962-2315). Prints "OK: d/a tasks, X ms[, golden match]" or "FAIL: ..." and exits 0 / 1
+// (2 for usage errors).
+//
+//   kvm_exec [--golden [--golden-tol R]] [--dump-bin DIR i,j,..] [--trace-csv FILE] [--repeat N] [--timeout-s N]
+//            [--blocks N] [--no-trace] [--quiet] [--check-ops] bundle_dir...
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <vector>
+#include "../../include/kvm_exec.h"
+
+// ---------------------------------------------------------------------------------------------- minimal JSON
+struct Json {
+  enum T { NUL, B, N, S, A, O } t = NUL;
+  double n = 0; bool b = false; std::string s; std::vector<Json> a; std::vector<std::pair<std::string, Json>> o;
+  const Json* get(const std::string& k) const { for (auto& kv : o) if (kv.first == k) return &kv.second; return nullptr; }
+  const Json& need(const std::string& k) const { const Json* j = get(k); if (!j) throw std::runtime_error("metadata: missing key " + k); return *j; }
+  double num(const std::string& k, double d) const { const Json* j = get(k); return j && j->t == N ? j->n : d; }
+};
+struct Parser {
+  const std::string& s; size_t p = 0;
+  explicit Parser(const std::string& x) : s(x) {}
+  void ws() { while (p < s.size() && isspace((unsigned char)s[p])) ++p; }
+  Json parse() {
+    ws(); Json j;
+    if (p >= s.size()) throw std::runtime_error("json: unexpected end");
+    char c = s[p];
+    if (c == '{') { ++p; j.t = Json::O; ws(); if (s[p] == '}') { ++p; return j; }
+      for (;;) { ws(); std::string k = str(); ws(); if (s[p++] != ':') throw std::runtime_error("json: ':' expected"); j.o.push_back({k, parse()}); ws();
+        if (s[p] == ',') { ++p; continue; } if (s[p] == '}') { ++p; return j; } throw std::runtime_error("json: ',' or '}' expected"); } }
+    if (c == '[') { ++p; j.t = Json::A; ws(); if (s[p] == ']') { ++p; return j; }
+      for (;;) { j.a.push_back(parse()); ws(); if (s[p] == ',') { ++p; continue; } if (s[p] == ']') { ++p; return j; } throw std::runtime_error("json: ',' or ']' expected"); } }
+    if (c == '"') { j.t = Json::S; j.s = str(); return j; }
+    if (!s.compare(p, 4, "true")) { p += 4; j.t = Json::B; j.b = true; return j; }
+    if (!s.compare(p, 5, "false")) { p += 5; j.t = Json::B; return j; }
+    if (!s.compare(p, 4, "null")) { p += 4; return j; }
+    if (!s.compare(p, 8, "Infinity")) { p += 8; j.t = Json::N; j.n = INFINITY; return j; }
+    if (!s.compare(p, 9, "-Infinity")) { p += 9; j.t = Json::N; j.n = -INFINITY; return j; }
+    if (!s.compare(p, 3, "NaN")) { p += 3; j.t = Json::N; j.n = NAN; return j; }
+    char* e; j.n = strtod(s.c_str() + p, &e); if (e == s.c_str() + p) throw std::runtime_error("json: bad value");
+    j.s = s.substr(p, (e - s.c_str()) - p); p = e - s.c_str(); j.t = Json::N; return j;
+  }
+  std::string str() {
+    if (s[p] != '"') throw std::runtime_error("json: string expected");
+    std::string out; ++p;
+    while (s[p] != '"') { if (s[p] == '\\') { ++p; char c = s[p++]; out += c == 'n' ? '\n' : c == 't' ? '\t' : c; } else out += s[p++]; }
+    ++p; return out;
+  }
+};
+static std::string read_file(const std::string& path) {
+  std::ifstream f(path, std::ios::binary); if (!f) throw std::runtime_error("cannot read " + path);
+  std::stringstream ss; ss << f.rdbuf(); return ss.str();
+}
+template <class T> static std::vector<T> read_bin(const std::string& path) {
+  std::string d = read_file(path); std::vector<T> v(d.size() / sizeof(T)); memcpy(v.data(), d.data(), v.size() * sizeof(T)); return v;
+}
+
+static void usage() {
+  fprintf(stderr, "usage: kvm_exec [options] bundle_dir...\n"
+                  "  --golden [--golden-tol R]   compare with <bundle_dir>/golden.json (one bundle): buffers (relative L2), versions, reads\n"
+                  "  --dump-bin DIR i,j,..       write buffers (widened to f32 / raw i32) to DIR/<index>.bin\n"
+                  "  --trace-csv FILE            per-task timeline   --repeat N   run the graph N times (timed)   --timeout-s N\n"
+                  "  --blocks N   --no-trace   --quiet   --check-ops\n");
+}
+
+int main(int argc, char** argv) {
+  std::vector<std::string> dirs; bool golden = false, quiet = false, trace = true; float tol = 1e-6f;
+  const char* csv = nullptr; std::string dump_dir; std::vector<int> dump_idx; int repeat = 1, blocks = 0; long long timeout_s = 20;
+  for (int i = 1; i < argc; ++i) {
+    std::string a = argv[i];
+    auto next = [&]() -> const char* { if (i + 1 >= argc) { usage(); exit(2); } return argv[++i]; };
+    if (a == "--golden") golden = true;
+    else if (a == "--golden-tol") tol = (float)atof(next());
+    else if (a == "--trace-csv") csv = next();
+    else if (a == "--repeat") repeat = atoi(next());
+    else if (a == "--timeout-s") timeout_s = atoll(next());
+    else if (a == "--blocks") blocks = atoi(next());
+    else if (a == "--no-trace") trace = false;
+    else if (a == "--quiet") quiet = true;
+    else if (a == "--dump-bin") { dump_dir = next(); for (char* p = (char*)next(); *p;) { char* e; long v = strtol(p, &e, 10); if (e == p) { usage(); return 2; } dump_idx.push_back((int)v); p = *e == ',' ? e + 1 : e; } }
+    else if (a == "--check-ops") { for (int id = 0; id < 400; ++id) if (const char* n = kvm_op_name(id)) printf("%3d %s\n", id, n); return 0; }
+    else if (a[0] == '-') { usage(); return 2; }
+    else dirs.push_back(a);
+  }
+  if (dirs.empty() || repeat < 1) { usage(); return 2; }
+  try {
+    std::vector<Json> metas;
+    int nvars = 1;
+    for (auto& d : dirs) {
+      metas.push_back(Parser(read_file(d + "/metadata.json")).parse());
+      if ((int)metas.back().num("abi_version", -1) != MVM_ABI_VERSION) throw std::runtime_error(d + ": abi_version is not 2");
+      nvars = std::max(nvars, (int)metas.back().need("variables").a.size());
+    }
+    KvmConfig cfg; kvm_config_default(&cfg);
+    cfg.num_vars = nvars; cfg.trace_on = (trace || golden || csv) ? 1 : 0; cfg.timeout_us = (unsigned long long)timeout_s * 1000000ull; cfg.blocks = blocks;
+    std::unique_ptr<KvmExec, void (*)(KvmExec*)> ex(kvm_create(&cfg), kvm_destroy);
+    if (!ex) throw std::runtime_error(std::string("kvm_create: ") + kvm_last_error(nullptr));
+    // buffers: the first bundle declares them; later bundles must name the same table (the reference's shared buffer model)
+    std::vector<std::string> names;
+    for (auto& jb : metas[0].need("buffers").a) {
+      int rows = (int)jb.num("rows", 1), cols = (int)jb.num("cols", 1), dt = (int)jb.num("dtype", 0);
+      const Json& in = jb.need("init"); std::string kind = in.need("kind").s;
+      KvmInit init{}; std::vector<float> vf; std::vector<int32_t> vi; std::vector<uint16_t> vh; std::string raw;
+      if (kind == "fill") { init.kind = KVM_INIT_FILL; init.value = (float)in.need("value").n; }
+      else if (kind == "values") {
+        init.kind = KVM_INIT_VALUES; const auto& vals = in.need("values").a;
+        if (dt == 1) { for (auto& v : vals) vi.push_back((int32_t)v.n); init.values = vi.data(); }
+        else if (dt == 2) { for (auto& v : vals) { float f = (float)v.n; uint32_t u; memcpy(&u, &f, 4); vh.push_back((uint16_t)(u >> 16)); } init.values = vh.data(); }
+        else { for (auto& v : vals) vf.push_back((float)v.n); init.values = vf.data(); }
+      } else if (kind == "seeded") {
+        init.kind = KVM_INIT_SEEDED; init.seed = strtoull(in.need("seed").s.c_str(), nullptr, 10); init.draws = (int)in.need("draws").n;
+        init.bias = (float)in.need("bias").n; init.coef = (float)in.need("coef").n;
+      } else if (kind == "file") { init.kind = KVM_INIT_VALUES; raw = read_file(dirs[0] + "/" + in.need("path").s); init.values = raw.data(); }
+      else throw std::runtime_error("unknown init kind " + kind);
+      if (kvm_add_buffer(ex.get(), rows, cols, dt, &init) < 0) throw std::runtime_error(std::string("add_buffer: ") + kvm_last_error(ex.get()));
+      names.push_back(jb.need("name").s);
+    }
+    for (auto& jv : metas[0].need("variables").a) kvm_set_version(ex.get(), (int)jv.num("id", 0), (int)jv.num("base_version", 0));
+    for (size_t k = 0; k < dirs.size(); ++k) {
+      auto t = read_bin<MvmTaskDesc>(dirs[k] + "/tasks.bin");
+      auto s = read_bin<int32_t>(dirs[k] + "/successors.bin");
+      auto a = read_bin<int32_t>(dirs[k] + "/args.bin");
+      if ((int)t.size() != (int)metas[k].num("task_count", -1)) throw std::runtime_error(dirs[k] + ": tasks.bin does not match task_count");
+      if (kvm_submit(ex.get(), t.data(), (int)t.size(), s.data(), (int)s.size(), a.data(), (int)a.size()) < 0)
+        throw std::runtime_error(dirs[k] + ": submit: " + kvm_last_error(ex.get()));
+    }
+    KvmResult r{}; float ms = 0;
+    if (repeat == 1) { if (kvm_start(ex.get()) < 0) throw std::runtime_error(kvm_last_error(ex.get())); }
+    else if (kvm_run_timed(ex.get(), repeat, &ms) < 0) throw std::runtime_error(kvm_last_error(ex.get()));
+    kvm_finish(ex.get(), &r);
+    if (repeat > 1) r.kernel_ms = ms / repeat;
+    if (r.err_code && !quiet) fprintf(stderr, "device error %d at task %d (a=%d b=%d)\n", r.err_code, r.err_slot, r.err_a, r.err_b);
+    int bad = 0;
+    std::vector<KvmTrace> tr;
+    if (cfg.trace_on) { tr.resize(kvm_ntasks(ex.get())); kvm_trace(ex.get(), tr.data(), (int)tr.size()); }
+    if (golden && r.err_code == 0) {
+      if (dirs.size() != 1) throw std::runtime_error("--golden needs exactly one bundle");
+      Json g = Parser(read_file(dirs[0] + "/golden.json")).parse();
+      float worst = 0;
+      for (auto& kv : g.need("buffers").o) {
+        int idx = -1; for (size_t i = 0; i < names.size(); ++i) if (names[i] == kv.first) idx = (int)i;
+        if (idx < 0) { ++bad; continue; }
+        size_t n = kv.second.a.size(); std::vector<float> got(n);
+        if (kvm_read_buffer(ex.get(), idx, got.data(), n) < 0) { ++bad; continue; }
+        bool is_int = kvm_buffer_dtype(ex.get(), idx) == 1; double num = 0, den = 0;
+        for (size_t i = 0; i < n; ++i) {
+          if (is_int) { int32_t gi; memcpy(&gi, &got[i], 4); if (gi != (int32_t)kv.second.a[i].n) ++bad; continue; }
+          double w = kv.second.a[i].n, d = got[i] - w; num += d * d; den += w * w;
+        }
+        float rel = (float)(std::sqrt(num) / std::max(1e-30, std::sqrt(den))); worst = std::max(worst, rel);
+        if (rel > tol) { if (!quiet) fprintf(stderr, "golden: buffer %s relative L2 %.3g > %.3g\n", kv.first.c_str(), rel, tol); ++bad; }
+      }
+      std::vector<int32_t> ver(nvars); kvm_versions(ex.get(), ver.data(), nvars);
+      std::map<std::string, int> vid; for (auto& jv : metas[0].need("variables").a) vid[jv.need("name").s] = (int)jv.num("id", 0);
+      for (auto& kv : g.need("versions").o) if (ver[vid[kv.first]] != (int)kv.second.n) { ++bad; if (!quiet) fprintf(stderr, "golden: version %s\n", kv.first.c_str()); }
+      for (auto& jr : metas[0].need("reads").a) {   // the task carrying each read's wait saw an admissible version
+        int slot = (int)jr.num("task", -1); const Json* gate = jr.get("gate"); if (gate && gate->t == Json::N) slot = (int)gate->n;
+        int want = (int)jr.num("version", 0); bool exact = jr.need("policy").s == "exact";
+        const KvmTrace& t = tr[slot]; bool ok = t.ver0 >= want && (!exact || (t.ver0 == want && t.ver1 == want));
+        bad += !ok;
+      }
+      if (!quiet) fprintf(stderr, "golden: worst buffer relative L2 %.3g (tolerance %.3g)\n", worst, tol);
+    }
+    if (csv) {
+      FILE* f = fopen(csv, "w");
+      if (f) { fprintf(f, "task,start,end,block,xcc,ver0,ver1,exec_count\n");
+        for (size_t i = 0; i < tr.size(); ++i) fprintf(f, "%zu,%llu,%llu,%d,%d,%d,%d,%d\n", i, tr[i].start, tr[i].end, tr[i].block, tr[i].xcc, tr[i].ver0, tr[i].ver1, tr[i].exec_count);
+        fclose(f); }
+    }
+    for (int idx : dump_idx) {
+      if (idx < 0 || idx >= kvm_nbufs(ex.get())) { fprintf(stderr, "--dump-bin: buffer %d out of range\n", idx); return 2; }
+      int dt = kvm_buffer_dtype(ex.get(), idx);
+      const Json& jb = metas[0].need("buffers").a[idx];
+      size_t n = (size_t)jb.num("rows", 1) * (size_t)jb.num("cols", 1);
+      std::vector<float> v(n); kvm_read_buffer(ex.get(), idx, v.data(), n); (void)dt;
+      FILE* f = fopen((dump_dir + "/" + std::to_string(idx) + ".bin").c_str(), "wb");
+      if (!f || fwrite(v.data(), 4, n, f) != n) { fprintf(stderr, "--dump-bin: cannot write\n"); return 2; }
+      fclose(f);
+    }
+    bool pass = r.err_code == 0 && bad == 0;
+    printf("%s: %d/%d tasks, %.3f ms%s\n", pass ? "OK" : "FAIL", r.done, r.admitted, r.kernel_ms, golden ? (bad ? ", golden MISMATCH" : ", golden match") : "");
+    return pass ? 0 : 1;
+  } catch (const std::exception& e) {
+    fprintf(stderr, "kvm_exec: %s\n", e.what());
+    return 1;
+  }
+}

@@ -1,0 +1,156 @@
+// Shared device/host definitions of the MI355X task-graph executor: error codes, device state, buffer views,
+// bf16 conversion and the memory-ordering primitives the scheduler is built on.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "../../include/mvm_task_abi.h"
+#include "../../include/kvm_exec.h"
+
+typedef uint16_t u16x8_t __attribute__((ext_vector_type(8)));
+
+#define KVM_THREADS 256          // every operator runs on one workgroup of 256 threads = four wave64s
+#define KVM_WAVES (KVM_THREADS / 64)
+#define KVM_MAX_ARGS 20
+#define KVM_LDS_BYTES (128 * 1024)   // LDS one task may use (gfx950 has 160 KiB per CU; the executor keeps the rest)
+
+// Device error codes. 0-20 keep the reference's numbering (reference: include/mvm_exec.cuh:148-164); operator
+// argument errors are 1000+k with the k of the operator registries' conventions.
+enum KvmErr {
+  KVM_OK = 0, KVM_ERR_BAD_OP = 1, KVM_ERR_BAD_ARITY = 2, KVM_ERR_BAD_BUF_INDEX = 3, KVM_ERR_BAD_BUF = 4,
+  KVM_ERR_BOUNDS = 5, KVM_ERR_BAD_VAR = 6, KVM_ERR_VERSION_GAP = 7, KVM_ERR_WAIT_VIOLATION = 8,
+  KVM_ERR_DOUBLE_EXEC = 9, KVM_ERR_BAD_TASK = 11, KVM_ERR_TIMEOUT = 15, KVM_ERR_QUEUE_OVERFLOW = 16,
+  KVM_ERR_BAD_CONFIG = 17,
+  KVM_ERR_OP_BUF = 1001, KVM_ERR_OP_DTYPE = 1002, KVM_ERR_OP_RANGE = 1003, KVM_ERR_OP_SHAPE = 1004,
+  KVM_ERR_OP_TOKEN = 1005, KVM_ERR_OP_KVLEN = 1006,
+};
+
+struct KvmCounters {
+  int done;            // tasks finished
+  int enq;             // tasks enqueued (== ready-queue tail)
+  int err_code, err_slot, err_a, err_b;
+  unsigned head;       // next ready-queue ticket
+  int pad;
+};
+
+// Everything the persistent kernel reads. One task graph per launch (the submitted bundles concatenated).
+struct KvmDevState {
+  const MvmTaskDesc* tasks;   // [ntasks]
+  const int32_t* succ;        // [nedges] global task indices
+  const int32_t* args;        // [nargs]
+  const MvmBuf* bufs;         // [nbufs]
+  int* indeg;                 // [ntasks] remaining predecessors
+  int* ready;                 // [ntasks] ready queue: cell t holds the t-th released task, -1 until then
+  int* state;                 // [ntasks] 0 not released, 1 parked on a version, 2 enqueued
+  int* park_next;             // [ntasks] park list links
+  int* version;               // [nvars]
+  int* park_head;             // [nvars] park list heads, -1 empty
+  KvmCounters* cnt;
+  KvmTrace* trace;            // [ntasks] or null
+  int ntasks, nbufs, nvars, trace_on;
+  unsigned long long timeout_ticks;   // stall timeout in wall_clock64 ticks (100 MHz)
+};
+
+// ---------------------------------------------------------------------------------------------- atomics
+// Agent-scope release/acquire through the HIP atomic builtins: on gfx950 the compiler emits the L2 write-back /
+// invalidate each XCD needs, so a release by a workgroup on one XCD is seen by an acquire on another.
+__device__ __forceinline__ int ld_relaxed(const int* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ unsigned ld_relaxed(const unsigned* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ int ld_acquire(const int* p) { return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st_release(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st_relaxed(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ int add_acqrel(int* p, int v) { return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ int add_relaxed(int* p, int v) { return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ unsigned add_relaxed(unsigned* p, unsigned v) { return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ bool cas_acqrel(int* p, int expect, int want) {
+  return __hip_atomic_compare_exchange_strong(p, &expect, want, __ATOMIC_ACQ_REL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int xchg_acqrel(int* p, int v) { return __hip_atomic_exchange(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void fence_seqcst() { __atomic_thread_fence(__ATOMIC_SEQ_CST); }
+__device__ __forceinline__ void fence_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+__device__ __forceinline__ void fence_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+
+// ---------------------------------------------------------------------------------------------- bf16
+__device__ __host__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+// float -> bf16, round to nearest even; NaN stays NaN (quiet bit set), inf stays inf.
+__device__ __forceinline__ uint16_t f2bf(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0x007fffffu) ? 0x40u : 0u));
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ float round_bf(float x) { return bf2f(f2bf(x)); }
+
+// ---------------------------------------------------------------------------------------------- views
+// A buffer argument as an operator sees it. ld()/st() widen / round bf16 storage; f/i give typed raw pointers.
+struct View {
+  void* p; int rows, cols, dtype;
+  __device__ bool ok() const { return p != nullptr; }
+  __device__ float* f() const { return (float*)p; }
+  __device__ int* i() const { return (int*)p; }
+  __device__ uint16_t* h() const { return (uint16_t*)p; }
+  __device__ float ld(long long k) const { return dtype == 2 ? bf2f(((const uint16_t*)p)[k]) : ((const float*)p)[k]; }
+  __device__ float at(long long r, long long c) const { return ld(r * cols + c); }
+  __device__ void st(long long k, float v) const { if (dtype == 2) ((uint16_t*)p)[k] = f2bf(v); else ((float*)p)[k] = v; }
+  __device__ long long n() const { return (long long)rows * cols; }
+};
+
+struct Ctx {
+  const MvmBuf* bufs;
+  const int32_t* a;          // argument words (in LDS)
+  char* smem;                // KVM_LDS_BYTES of LDS
+  KvmCounters* cnt;
+  int slot;
+  __device__ View buf(int k) const {
+    int idx = a[k];
+    if (idx < 0) return View{nullptr, 0, 0, 0};
+    const MvmBuf& b = bufs[idx];
+    return View{b.p, b.rows, b.cols, b.dtype};
+  }
+  __device__ int i(int k) const { return a[k]; }
+  __device__ float f(int k) const { return __int_as_float(a[k]); }
+  // First error wins; the task then returns. Data-dependent errors only: argument shapes were validated on the host.
+  __device__ void fail(int code, int x = 0, int y = 0) const {
+    int zero = 0;
+    if (__hip_atomic_compare_exchange_strong(&cnt->err_code, &zero, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+      cnt->err_slot = slot; cnt->err_a = x; cnt->err_b = y;
+    }
+  }
+};
+
+__device__ __forceinline__ int tid() { return threadIdx.x; }
+__device__ __forceinline__ int lane() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave() { return threadIdx.x >> 6; }
+
+// Block-wide reductions over 256 threads (four wave64s), result returned to every thread. `red` = 4 floats of LDS.
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane() == 0) red[wave()] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  __syncthreads();
+  if (lane() == 0) red[wave()] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ double block_sum_d(double v, double* red) {
+  v = wave_sum_d(v);
+  __syncthreads();
+  if (lane() == 0) red[wave()] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}

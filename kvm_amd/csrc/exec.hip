@@ -1,0 +1,590 @@
+// The persistent task-graph executor for MI355X (gfx950): device scheduler, operator dispatch and the C ABI host side.
+//
+// Device side (one workgroup of 256 threads per CU, all resident for the whole graph):
+//   * Ready queue: every task is enqueued exactly once (by the last predecessor to finish, by a version publisher,
+//     or at launch for roots), so the queue is a plain array of ntasks cells filled in enqueue order: enqueue takes
+//     the next tail slot and release-stores the task index; a worker takes the next head ticket and waits for that
+//     cell. Tickets >= ntasks mean the graph is drained and the worker exits. No cell is ever reused, so there is no
+//     ABA and no ring-capacity budget (reference design for comparison: include/mvm_sched.cuh:115-374).
+//   * Dependencies: after an operator, the workgroup barrier orders all its stores before wave 0's agent-scope
+//     release fence (on gfx950 this writes the XCD's L2 back so another XCD sees the data); wave 0 then decrements
+//     successor counters with acq_rel atomics and enqueues the ones that reach zero.
+//   * Versions: a task released with version[wait_var] < wait_ver is parked on the variable's lock-free list. The
+//     publisher CASes version from pub_ver-1 to pub_ver (else VERSION_GAP), then takes the whole list and enqueues
+//     what is now satisfied. Parker (push; seq_cst fence; re-read version) and publisher (CAS version; seq_cst fence;
+//     exchange list) form a Dekker pair, and a per-task state CAS makes the enqueue unique.
+//   * Errors: first error wins (CAS on err_code); every worker polls it while waiting and leaves. A stall timeout
+//     (no task finished for timeout_ticks while a worker waits) ends the run with TIMEOUT instead of hanging.
+#include <hip/hip_runtime.h>
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+#include "common.h"
+#include "ops_basic.h"
+#include "ops_gemm.h"
+#include "ops_attn.h"
+#include "validate.h"
+
+using namespace kvm;
+
+// ---------------------------------------------------------------------------------------------- scheduler
+__device__ __forceinline__ void enqueue(const KvmDevState& S, int t) {
+  int pos = add_relaxed(&S.cnt->enq, 1);
+  if (pos >= S.ntasks) {   // cannot happen when every task is enqueued once; reported, never written out of bounds
+    int z = 0;
+    __hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_QUEUE_OVERFLOW, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  st_release(&S.ready[pos], t);
+}
+
+__device__ void park(const KvmDevState& S, int t, int var, int want) {
+  int* head = &S.park_head[var];
+  int h = ld_relaxed(head);
+  do { st_relaxed(&S.park_next[t], h); } while (!__hip_atomic_compare_exchange_strong(head, &h, t, __ATOMIC_ACQ_REL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  fence_seqcst();
+  if (ld_acquire(&S.version[var]) >= want && cas_acqrel(&S.state[t], 1, 2)) enqueue(S, t);
+}
+
+// A task whose predecessors have all finished: run it when its version wait holds, else park it.
+__device__ void release(const KvmDevState& S, int t) {
+  const MvmTaskDesc& d = S.tasks[t];
+  int var = d.wait_var;
+  if (var < 0 || ld_acquire(&S.version[var]) >= d.wait_ver) { st_relaxed(&S.state[t], 2); enqueue(S, t); return; }
+  st_relaxed(&S.state[t], 1);
+  park(S, t, var, d.wait_ver);
+}
+
+__device__ void publish(const KvmDevState& S, int slot, int var, int ver) {
+  int expect = ver - 1;
+  if (!__hip_atomic_compare_exchange_strong(&S.version[var], &expect, ver, __ATOMIC_ACQ_REL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+    int z = 0;
+    if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_VERSION_GAP, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+      S.cnt->err_slot = slot; S.cnt->err_a = expect; S.cnt->err_b = ver;
+    }
+    return;
+  }
+  fence_seqcst();
+  int h = xchg_acqrel(&S.park_head[var], -1);
+  while (h >= 0) {
+    int nx = ld_relaxed(&S.park_next[h]);
+    if (ld_relaxed(&S.state[h]) == 1) {
+      int want = S.tasks[h].wait_ver;
+      if (ld_acquire(&S.version[var]) >= want) { if (cas_acqrel(&S.state[h], 1, 2)) enqueue(S, h); }
+      else park(S, h, var, want);
+    }
+    h = nx;
+  }
+}
+
+__device__ __forceinline__ int xcc_id() {
+  // HW_REG_XCC_ID (hwreg 20), bits [3:0]: the XCD this wave runs on
+  return __builtin_amdgcn_s_getreg((3 << 11) | 20) & 0xf;
+}
+
+__device__ void dispatch(int op, const Ctx& c) {
+  switch (op) {
+    case 0: break;
+    case 1: op_copy(c); break;
+    case 2: op_add(c); break;
+    case 3: op_scale(c); break;
+    case 4: op_relu(c); break;
+    case 5: op_sgd(c); break;
+    case 6: op_predict(c); break;
+    case 7: op_mse_grad(c); break;
+    case 8: op_matmul(c); break;
+    case 9: op_fill(c); break;
+    case 10: op_spin(c); break;
+    case 32: op_embedding_fwd(c); break;
+    case 33: op_embedding_bwd(c); break;
+    case 34: op_matmul_tile(c); break;
+    case 35: op_norm_fwd<false>(c); break;
+    case 36: op_norm_fwd<true>(c); break;
+    case 37: op_norm_bwd_dx<false>(c); break;
+    case 38: op_norm_bwd_dx<true>(c); break;
+    case 39: op_norm_bwd_params(c); break;
+    case 40: op_gelu_fwd(c); break;
+    case 41: op_gelu_bwd(c); break;
+    case 42: op_residual_add(c); break;
+    case 43: op_rope<1>(c); break;
+    case 44: op_rope<-1>(c); break;
+    case 45: op_attn_fwd(c); break;
+    case 46: op_attn_bwd_delta(c); break;
+    case 47: op_attn_bwd_dq(c); break;
+    case 48: op_attn_bwd_dkv(c); break;
+    case 49: op_kv_append(c); break;
+    case 50: op_attn_decode(c); break;
+    case 51: op_softmax_ce_fwd(c); break;
+    case 52: op_softmax_ce_reduce(c); break;
+    case 53: op_softmax_ce_bwd(c); break;
+    case 54: op_adamw(c); break;
+    case 55: op_gradnorm_partial(c); break;
+    case 56: op_gradnorm_finish(c); break;
+    case 57: op_sample(c); break;
+    case 58: op_argmax(c); break;
+    case 59: op_zero_buf(c); break;
+    case 60: op_counter_inc(c); break;
+    case 61: op_colsum(c); break;
+    case 62: op_select_window(c); break;
+    case 63: op_gather_rows(c); break;
+    case 96: op_act_fwd(c); break;
+    case 97: op_act_bwd(c); break;
+    case 98: op_silu_mul_fwd(c); break;
+    case 99: op_silu_mul_bwd(c); break;
+    case 100: op_softmax_rows_fwd(c); break;
+    case 101: op_softmax_rows_bwd(c); break;
+    case 102: op_gather_rows_scaled(c); break;
+    case 103: op_scatter_add_rows(c); break;
+    case 104: op_row_dot(c); break;
+    case 113: op_round_bf16(c); break;
+    case 114: op_matmul_tile_bf16(c); break;
+    case 115: op_adamw_lr(c); break;
+    case 116: op_lr_schedule(c); break;
+    case 117: op_scale_flat(c); break;
+    case 118: op_add_rowtile(c); break;
+    case 120: op_matmul_tile_silu_mul(c); break;
+    case 121: op_matmul_tile_silu_mul_bwd(c); break;
+    case 122: op_matmul_mma_bf16(c); break;
+    case 123: op_sgd_range(c); break;
+    case 126: op_round_tf32(c); break;
+    case 127: op_softmax_ce_fused(c); break;
+    case 134: op_gemv_bf16(c); break;
+    case 135: op_attn_decode_part(c); break;
+    case 136: op_attn_decode_merge(c); break;
+    case 300: op_head_rmsnorm(c); break;
+    default: if (threadIdx.x == 0) c.fail(KVM_ERR_BAD_OP, op, 0);
+  }
+}
+
+__global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S) {
+  __shared__ __attribute__((aligned(16))) char smem[KVM_LDS_BYTES];
+  __shared__ int s_slot;
+  __shared__ int32_t s_args[KVM_MAX_ARGS];
+  __shared__ MvmTaskDesc s_desc;
+  const int t = threadIdx.x;
+  for (;;) {
+    if (t == 0) {
+      unsigned ticket = add_relaxed(&S.cnt->head, 1u);
+      int slot = -1;
+      if (ticket < (unsigned)S.ntasks) {
+        unsigned long long since = wall_clock64();
+        int seen_done = ld_relaxed(&S.cnt->done);
+        for (;;) {
+          slot = ld_relaxed(&S.ready[ticket]);
+          if (slot >= 0) break;
+          if (ld_relaxed(&S.cnt->err_code) != 0) break;
+          __builtin_amdgcn_s_sleep(1);
+          int d = ld_relaxed(&S.cnt->done);
+          unsigned long long now = wall_clock64();
+          if (d != seen_done) { seen_done = d; since = now; }
+          else if (now - since > S.timeout_ticks) {
+            int z = 0;
+            if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_TIMEOUT, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+              S.cnt->err_slot = -1; S.cnt->err_a = (int)ticket; S.cnt->err_b = d;
+            }
+            break;
+          }
+        }
+        if (slot >= 0) fence_acquire();   // the enqueuer's release: predecessors' data is visible from here on
+      }
+      s_slot = ld_relaxed(&S.cnt->err_code) != 0 ? -1 : slot;
+    }
+    __syncthreads();
+    const int slot = s_slot;
+    if (slot < 0) break;
+    if (t < 16) ((int32_t*)&s_desc)[t] = ((const int32_t*)&S.tasks[slot])[t];
+    __syncthreads();
+    const int op = s_desc.op_id;
+    if (t < s_desc.args_words && t < KVM_MAX_ARGS) s_args[t] = S.args[s_desc.args_off + t];
+    if (t == 0 && S.trace_on) {
+      KvmTrace& tr = S.trace[slot];
+      tr.start = wall_clock64();
+      tr.block = blockIdx.x; tr.xcc = xcc_id();
+      tr.ver0 = s_desc.wait_var >= 0 ? ld_acquire(&S.version[s_desc.wait_var]) : -1;
+      tr.exec_count += 1;
+      if (s_desc.wait_var >= 0 && tr.ver0 < s_desc.wait_ver) {
+        int z = 0;
+        if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_WAIT_VIOLATION, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+          S.cnt->err_slot = slot;
+      }
+    }
+    __syncthreads();
+    Ctx c{S.bufs, s_args, smem, S.cnt, slot};
+    dispatch(op, c);
+    __syncthreads();
+    if (t < 64) {
+      fence_release();                   // every thread's stores are behind the barrier; make them agent-visible
+      if (t == 0) {
+        if (S.trace_on) {
+          KvmTrace& tr = S.trace[slot];
+          tr.ver1 = s_desc.wait_var >= 0 ? ld_acquire(&S.version[s_desc.wait_var]) : -1;
+          tr.end = wall_clock64();
+        }
+        if (s_desc.pub_var >= 0) publish(S, slot, s_desc.pub_var, s_desc.pub_ver);
+      }
+      for (int k = t; k < s_desc.succ_cnt; k += 64) {
+        int s = S.succ[s_desc.succ_off + k];
+        if (add_acqrel(&S.indeg[s], -1) == 1) release(S, s);
+      }
+      if (t == 0) add_acqrel(&S.cnt->done, 1);
+    }
+  }
+}
+
+// Launch-time state reset: counters, queue cells, park lists, versions; roots without a version wait go straight
+// into the first queue cells in index order, roots with one go through release().
+__global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions, const int* roots, int nroots) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
+  for (int k = i; k < S.ntasks; k += stride) {
+    S.indeg[k] = S.tasks[k].indegree; S.ready[k] = -1; S.state[k] = 0; S.park_next[k] = -1;
+    if (S.trace_on) { KvmTrace z = {}; z.ver0 = z.ver1 = -1; S.trace[k] = z; }
+  }
+  for (int k = i; k < S.nvars; k += stride) { S.version[k] = base_versions[k]; S.park_head[k] = -1; }
+  if (i == 0) { KvmCounters z = {}; *S.cnt = z; }
+}
+__global__ void kvm_seed_kernel(KvmDevState S, const int* roots, int nroots) {
+  // single workgroup: roots without waits take cells 0.. in order; the rest are released (parked) afterwards
+  __shared__ int n_direct;
+  if (threadIdx.x == 0) {
+    int n = 0;
+    for (int r = 0; r < nroots; ++r) {
+      const MvmTaskDesc& d = S.tasks[roots[r]];
+      if (d.wait_var < 0 || S.version[d.wait_var] >= d.wait_ver) { S.ready[n++] = roots[r]; S.state[roots[r]] = 2; }
+    }
+    S.cnt->enq = n;
+    n_direct = n;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int r = 0; r < nroots; ++r) if (S.state[roots[r]] == 0) release(S, roots[r]);
+  (void)n_direct;
+}
+
+// ---------------------------------------------------------------------------------------------- init kernels
+__device__ __forceinline__ float seeded_u(unsigned long long seed, unsigned long long j) {
+  unsigned long long z = seed + (j + 1ull) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  return (float)(z >> 40) * (1.0f / 16777216.0f);
+}
+// SplitMix64 counter-based initialiser, one correctly rounded f32 operation per step (runtime/initgen.py:1-58).
+__global__ void kvm_seeded_kernel(float* out, long long n, unsigned long long seed, int draws, float bias, float coef) {
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+    float acc;
+    if (draws == 1) acc = seeded_u(seed, i);
+    else {
+      unsigned long long j = (unsigned long long)i * 4ull;
+      acc = __fadd_rn(__fadd_rn(seeded_u(seed, j), seeded_u(seed, j + 1)), __fadd_rn(seeded_u(seed, j + 2), seeded_u(seed, j + 3)));
+    }
+    out[i] = __fmul_rn(__fsub_rn(acc, bias), coef);
+  }
+}
+__global__ void kvm_fill32_kernel(uint32_t* out, long long n, uint32_t v) {
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) out[i] = v;
+}
+__global__ void kvm_fill16_kernel(uint16_t* out, long long n, uint16_t v) {
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) out[i] = v;
+}
+
+// ---------------------------------------------------------------------------------------------- host executor
+static thread_local std::string g_err;
+
+struct BufRec { void* p; int rows, cols, dtype; size_t bytes; };
+
+struct KvmExec {
+  KvmConfig cfg;
+  int dev = 0, cus = 0, grid = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  std::vector<BufRec> bufs;
+  std::vector<MvmTaskDesc> tasks;
+  std::vector<int32_t> succ, args, roots;
+  std::vector<int> base_versions;
+  bool uploaded = false, launched = false;
+  std::string err;
+  // device memory
+  MvmTaskDesc* d_tasks = nullptr; int32_t *d_succ = nullptr, *d_args = nullptr; MvmBuf* d_bufs = nullptr;
+  int *d_indeg = nullptr, *d_ready = nullptr, *d_state = nullptr, *d_park_next = nullptr, *d_version = nullptr, *d_park_head = nullptr;
+  int *d_base = nullptr, *d_roots = nullptr;
+  KvmCounters* d_cnt = nullptr; KvmTrace* d_trace = nullptr;
+  KvmDevState S{};
+};
+
+#define HIPCK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { ex->err = std::string(#x) + ": " + hipGetErrorString(e_); return KVM_STATUS_HIP_ERROR; } } while (0)
+
+static size_t elem_bytes(int dtype) { return dtype == 2 ? 2 : 4; }
+
+template <class T> static hipError_t upload(T** dst, const std::vector<T>& v, hipStream_t s) {
+  size_t bytes = std::max<size_t>(1, v.size()) * sizeof(T);
+  hipError_t e = hipMalloc((void**)dst, bytes);
+  if (e != hipSuccess || v.empty()) return e;
+  e = hipMemcpyAsync(*dst, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return e;
+  return hipStreamSynchronize(s);
+}
+
+extern "C" {
+
+void kvm_config_default(KvmConfig* c) {
+  c->blocks = 0; c->trace_on = 1; c->num_vars = 64; c->timeout_us = 20ull * 1000000ull; c->device = 0;
+}
+
+const char* kvm_last_error(const KvmExec* ex) { return ex ? ex->err.c_str() : g_err.c_str(); }
+
+KvmExec* kvm_create(const KvmConfig* cfg) {
+  KvmConfig c; kvm_config_default(&c);
+  if (cfg) c = *cfg;
+  if (c.num_vars < 1 || c.num_vars > (1 << 20)) { g_err = "num_vars out of range"; return nullptr; }
+  if (hipSetDevice(c.device) != hipSuccess) { g_err = "hipSetDevice failed"; return nullptr; }
+  hipDeviceProp_t p;
+  if (hipGetDeviceProperties(&p, c.device) != hipSuccess) { g_err = "hipGetDeviceProperties failed"; return nullptr; }
+  KvmExec* ex = new KvmExec();
+  ex->cfg = c; ex->dev = c.device; ex->cus = p.multiProcessorCount;
+  ex->grid = c.blocks > 0 ? c.blocks : ex->cus;
+  ex->base_versions.assign(c.num_vars, 0);
+  if (hipStreamCreateWithFlags(&ex->stream, hipStreamNonBlocking) != hipSuccess || hipEventCreate(&ex->ev0) != hipSuccess ||
+      hipEventCreate(&ex->ev1) != hipSuccess) { g_err = "stream/event creation failed"; delete ex; return nullptr; }
+  return ex;
+}
+
+void kvm_destroy(KvmExec* ex) {
+  if (!ex) return;
+  hipSetDevice(ex->dev);
+  if (ex->stream) hipStreamSynchronize(ex->stream);
+  for (auto& b : ex->bufs) hipFree(b.p);
+  void* ptrs[] = {ex->d_tasks, ex->d_succ, ex->d_args, ex->d_bufs, ex->d_indeg, ex->d_ready, ex->d_state, ex->d_park_next,
+                  ex->d_version, ex->d_park_head, ex->d_base, ex->d_roots, ex->d_cnt, ex->d_trace};
+  for (void* q : ptrs) if (q) hipFree(q);
+  if (ex->ev0) hipEventDestroy(ex->ev0);
+  if (ex->ev1) hipEventDestroy(ex->ev1);
+  if (ex->stream) hipStreamDestroy(ex->stream);
+  delete ex;
+}
+
+static void launch_fill(KvmExec* ex, BufRec& b, float value) {
+  long long n = (long long)b.rows * b.cols;
+  int grid = (int)std::min<long long>(4096, (n + 255) / 256);
+  if (b.dtype == 2) {
+    uint32_t u; memcpy(&u, &value, 4);
+    uint32_t r = ((u & 0x7f800000u) == 0x7f800000u) ? (u >> 16) : ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    hipLaunchKernelGGL(kvm_fill16_kernel, dim3(grid), dim3(256), 0, ex->stream, (uint16_t*)b.p, n, (uint16_t)r);
+  } else {
+    uint32_t u;
+    if (b.dtype == 1) { int32_t iv = (int32_t)value; memcpy(&u, &iv, 4); } else memcpy(&u, &value, 4);
+    hipLaunchKernelGGL(kvm_fill32_kernel, dim3(grid), dim3(256), 0, ex->stream, (uint32_t*)b.p, n, u);
+  }
+}
+
+int kvm_add_buffer(KvmExec* ex, int rows, int cols, int dtype, const KvmInit* init) {
+  if (rows < 1 || cols < 1 || (long long)rows * cols > 0x7fffffffll || dtype < 0 || dtype > 2) { ex->err = "bad buffer shape or dtype"; return KVM_STATUS_INVALID; }
+  if (ex->uploaded) { ex->err = "buffers must be added before kvm_start"; return KVM_STATUS_INVALID; }
+  hipSetDevice(ex->dev);
+  BufRec b{nullptr, rows, cols, dtype, (size_t)rows * cols * elem_bytes(dtype)};
+  HIPCK(hipMalloc(&b.p, (b.bytes + 255) & ~(size_t)255));
+  KvmInit z{}; if (!init) init = &z;
+  switch (init->kind) {
+    case KVM_INIT_ZERO: HIPCK(hipMemsetAsync(b.p, 0, b.bytes, ex->stream)); break;
+    case KVM_INIT_FILL: launch_fill(ex, b, init->value); break;
+    case KVM_INIT_VALUES: HIPCK(hipMemcpyAsync(b.p, init->values, b.bytes, hipMemcpyHostToDevice, ex->stream)); HIPCK(hipStreamSynchronize(ex->stream)); break;
+    case KVM_INIT_SEEDED:
+      if (dtype != 0) { hipFree(b.p); ex->err = "seeded init needs an f32 buffer"; return KVM_STATUS_INVALID; }
+      hipLaunchKernelGGL(kvm_seeded_kernel, dim3(4096), dim3(256), 0, ex->stream, (float*)b.p, (long long)rows * cols, init->seed, init->draws, init->bias, init->coef);
+      break;
+    default: hipFree(b.p); ex->err = "unknown init kind"; return KVM_STATUS_INVALID;
+  }
+  HIPCK(hipGetLastError());
+  ex->bufs.push_back(b);
+  return (int)ex->bufs.size() - 1;
+}
+
+int kvm_nbufs(const KvmExec* ex) { return (int)ex->bufs.size(); }
+int kvm_buffer_dtype(const KvmExec* ex, int idx) { return idx >= 0 && idx < (int)ex->bufs.size() ? ex->bufs[idx].dtype : KVM_STATUS_INVALID; }
+void* kvm_buffer_device_ptr(const KvmExec* ex, int idx) { return idx >= 0 && idx < (int)ex->bufs.size() ? ex->bufs[idx].p : nullptr; }
+
+int kvm_write_buffer(KvmExec* ex, int idx, const void* host, size_t bytes) {
+  if (idx < 0 || idx >= (int)ex->bufs.size() || bytes != ex->bufs[idx].bytes) { ex->err = "kvm_write_buffer: bad index or size"; return KVM_STATUS_INVALID; }
+  hipSetDevice(ex->dev);
+  HIPCK(hipStreamSynchronize(ex->stream));
+  HIPCK(hipMemcpy(ex->bufs[idx].p, host, bytes, hipMemcpyHostToDevice));
+  return 0;
+}
+
+int kvm_read_raw(KvmExec* ex, int idx, void* out, size_t bytes) {
+  if (idx < 0 || idx >= (int)ex->bufs.size() || bytes != ex->bufs[idx].bytes) { ex->err = "kvm_read_raw: bad index or size"; return KVM_STATUS_INVALID; }
+  hipSetDevice(ex->dev);
+  HIPCK(hipStreamSynchronize(ex->stream));
+  HIPCK(hipMemcpy(out, ex->bufs[idx].p, bytes, hipMemcpyDeviceToHost));
+  return 0;
+}
+
+int kvm_read_buffer(KvmExec* ex, int idx, float* out, size_t n) {
+  if (idx < 0 || idx >= (int)ex->bufs.size() || n != (size_t)ex->bufs[idx].rows * ex->bufs[idx].cols) { ex->err = "kvm_read_buffer: bad index or size"; return KVM_STATUS_INVALID; }
+  const BufRec& b = ex->bufs[idx];
+  if (b.dtype != 2) return kvm_read_raw(ex, idx, out, b.bytes);
+  std::vector<uint16_t> h(n);
+  int rc = kvm_read_raw(ex, idx, h.data(), b.bytes);
+  if (rc) return rc;
+  for (size_t i = 0; i < n; ++i) { uint32_t u = (uint32_t)h[i] << 16; memcpy(&out[i], &u, 4); }
+  return 0;
+}
+
+int kvm_set_version(KvmExec* ex, int var, int version) {
+  if (var < 0 || var >= (int)ex->base_versions.size() || version < 0) { ex->err = "kvm_set_version: bad variable or version"; return KVM_STATUS_INVALID; }
+  ex->base_versions[var] = version;
+  return 0;
+}
+
+int kvm_submit(KvmExec* ex, const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs) {
+  if (ex->uploaded) { ex->err = "kvm_submit after kvm_start: this executor runs the bundles submitted before start"; return KVM_STATUS_CLOSED; }
+  if (ntasks < 1 || nedges < 0 || nargs < 0) { ex->err = "empty bundle"; return KVM_STATUS_INVALID; }
+  std::vector<MvmBuf> table(ex->bufs.size());
+  for (size_t i = 0; i < table.size(); ++i) table[i] = MvmBuf{ex->bufs[i].p, ex->bufs[i].rows, ex->bufs[i].cols, ex->bufs[i].cols, ex->bufs[i].dtype, {0, 0}};
+  std::string why;
+  if (!kvm_validate_bundle(tasks, ntasks, succ, nedges, args, nargs, table.data(), (int)table.size(), (int)ex->base_versions.size(), &why)) {
+    ex->err = why; return KVM_STATUS_INVALID;
+  }
+  if ((long long)ex->tasks.size() + ntasks > (1ll << 30)) { ex->err = "too many tasks"; return KVM_STATUS_TOO_BIG; }
+  int tbase = (int)ex->tasks.size(), sbase = (int)ex->succ.size(), abase = (int)ex->args.size();
+  for (int i = 0; i < ntasks; ++i) {
+    MvmTaskDesc d = tasks[i];
+    d.succ_off += sbase; d.args_off += abase; d.reserved0 = tbase;   // reserved0: the bundle's first global task index
+    ex->tasks.push_back(d);
+    if (d.indegree == 0) ex->roots.push_back(tbase + i);
+  }
+  for (int e = 0; e < nedges; ++e) ex->succ.push_back(succ[e] + tbase);
+  ex->args.insert(ex->args.end(), args, args + nargs);
+  return 0;
+}
+
+static int do_upload(KvmExec* ex) {
+  if (ex->tasks.empty()) { ex->err = "nothing submitted"; return KVM_STATUS_INVALID; }
+  int n = (int)ex->tasks.size(), nv = (int)ex->base_versions.size();
+  std::vector<MvmBuf> table(ex->bufs.size());
+  for (size_t i = 0; i < table.size(); ++i) table[i] = MvmBuf{ex->bufs[i].p, ex->bufs[i].rows, ex->bufs[i].cols, ex->bufs[i].cols, ex->bufs[i].dtype, {0, 0}};
+  HIPCK(upload(&ex->d_tasks, ex->tasks, ex->stream));
+  HIPCK(upload(&ex->d_succ, ex->succ, ex->stream));
+  HIPCK(upload(&ex->d_args, ex->args, ex->stream));
+  HIPCK(upload(&ex->d_bufs, table, ex->stream));
+  HIPCK(upload(&ex->d_roots, ex->roots, ex->stream));
+  HIPCK(hipMalloc(&ex->d_indeg, n * sizeof(int)));
+  HIPCK(hipMalloc(&ex->d_ready, n * sizeof(int)));
+  HIPCK(hipMalloc(&ex->d_state, n * sizeof(int)));
+  HIPCK(hipMalloc(&ex->d_park_next, n * sizeof(int)));
+  HIPCK(hipMalloc(&ex->d_version, nv * sizeof(int)));
+  HIPCK(hipMalloc(&ex->d_park_head, nv * sizeof(int)));
+  HIPCK(hipMalloc(&ex->d_base, nv * sizeof(int)));
+  HIPCK(hipMalloc(&ex->d_cnt, sizeof(KvmCounters)));
+  if (ex->cfg.trace_on) HIPCK(hipMalloc(&ex->d_trace, n * sizeof(KvmTrace)));
+  KvmDevState& S = ex->S;
+  S.tasks = ex->d_tasks; S.succ = ex->d_succ; S.args = ex->d_args; S.bufs = ex->d_bufs;
+  S.indeg = ex->d_indeg; S.ready = ex->d_ready; S.state = ex->d_state; S.park_next = ex->d_park_next;
+  S.version = ex->d_version; S.park_head = ex->d_park_head; S.cnt = ex->d_cnt; S.trace = ex->d_trace;
+  S.ntasks = n; S.nbufs = (int)ex->bufs.size(); S.nvars = nv; S.trace_on = ex->cfg.trace_on ? 1 : 0;
+  S.timeout_ticks = ex->cfg.timeout_us * 100ull;   // wall_clock64 runs at 100 MHz on gfx950
+  ex->uploaded = true;
+  return 0;
+}
+
+static int launch_once(KvmExec* ex) {
+  KvmDevState& S = ex->S;
+  HIPCK(hipMemcpyAsync(ex->d_base, ex->base_versions.data(), ex->base_versions.size() * sizeof(int), hipMemcpyHostToDevice, ex->stream));
+  hipLaunchKernelGGL(kvm_reset_kernel, dim3(std::min(1024, (S.ntasks + 255) / 256 + 1)), dim3(256), 0, ex->stream, S, (const int*)ex->d_base,
+                     (const int*)ex->d_roots, (int)ex->roots.size());
+  hipLaunchKernelGGL(kvm_seed_kernel, dim3(1), dim3(64), 0, ex->stream, S, (const int*)ex->d_roots, (int)ex->roots.size());
+  hipLaunchKernelGGL(kvm_exec_kernel, dim3(ex->grid), dim3(KVM_THREADS), 0, ex->stream, S);
+  HIPCK(hipGetLastError());
+  return 0;
+}
+
+int kvm_start(KvmExec* ex) {
+  hipSetDevice(ex->dev);
+  if (!ex->uploaded) { int rc = do_upload(ex); if (rc) return rc; }
+  HIPCK(hipStreamSynchronize(ex->stream));   // buffer initialisation done
+  HIPCK(hipEventRecord(ex->ev0, ex->stream));
+  int rc = launch_once(ex);
+  if (rc) return rc;
+  HIPCK(hipEventRecord(ex->ev1, ex->stream));
+  ex->launched = true;
+  return 0;
+}
+
+int kvm_relaunch(KvmExec* ex) {
+  if (!ex->uploaded) return kvm_start(ex);
+  hipSetDevice(ex->dev);
+  HIPCK(hipEventRecord(ex->ev0, ex->stream));
+  int rc = launch_once(ex);
+  if (rc) return rc;
+  HIPCK(hipEventRecord(ex->ev1, ex->stream));
+  ex->launched = true;
+  return 0;
+}
+
+int kvm_run_timed(KvmExec* ex, int n, float* ms) {
+  hipSetDevice(ex->dev);
+  if (!ex->uploaded) { int rc = do_upload(ex); if (rc) return rc; }
+  HIPCK(hipStreamSynchronize(ex->stream));
+  HIPCK(hipEventRecord(ex->ev0, ex->stream));
+  for (int i = 0; i < n; ++i) { int rc = launch_once(ex); if (rc) return rc; }
+  HIPCK(hipEventRecord(ex->ev1, ex->stream));
+  HIPCK(hipEventSynchronize(ex->ev1));
+  HIPCK(hipEventElapsedTime(ms, ex->ev0, ex->ev1));
+  ex->launched = true;
+  return 0;
+}
+
+int kvm_finish(KvmExec* ex, KvmResult* res) {
+  hipSetDevice(ex->dev);
+  HIPCK(hipStreamSynchronize(ex->stream));
+  KvmCounters c{};
+  if (ex->d_cnt) HIPCK(hipMemcpy(&c, ex->d_cnt, sizeof c, hipMemcpyDeviceToHost));
+  float ms = 0.f;
+  if (ex->launched) hipEventElapsedTime(&ms, ex->ev0, ex->ev1);
+  if (res) {
+    res->err_code = c.err_code; res->err_slot = c.err_slot; res->err_a = c.err_a; res->err_b = c.err_b;
+    res->done = c.done; res->admitted = (int)ex->tasks.size(); res->grid = ex->grid; res->kernel_ms = ms;
+  }
+  if (c.err_code) { ex->err = "device error " + std::to_string(c.err_code) + " at task " + std::to_string(c.err_slot); return KVM_STATUS_DEVICE_ERROR; }
+  return 0;
+}
+
+int kvm_versions(KvmExec* ex, int32_t* out, int n) {
+  if (!ex->d_version || n > (int)ex->base_versions.size()) { ex->err = "kvm_versions: not started or n too large"; return KVM_STATUS_INVALID; }
+  HIPCK(hipStreamSynchronize(ex->stream));
+  HIPCK(hipMemcpy(out, ex->d_version, n * sizeof(int), hipMemcpyDeviceToHost));
+  return 0;
+}
+
+int kvm_trace(KvmExec* ex, KvmTrace* out, int n) {
+  if (!ex->d_trace || n > (int)ex->tasks.size()) { ex->err = "kvm_trace: tracing off or n too large"; return KVM_STATUS_INVALID; }
+  HIPCK(hipStreamSynchronize(ex->stream));
+  HIPCK(hipMemcpy(out, ex->d_trace, n * sizeof(KvmTrace), hipMemcpyDeviceToHost));
+  return 0;
+}
+
+int kvm_validate(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs,
+                 const MvmBuf* bufs, int nbufs, int nvars, char* err, int errlen) {
+  std::string why;
+  if (ntasks < 1) why = "empty bundle";
+  else if (kvm_validate_bundle(tasks, ntasks, succ, nedges, args, nargs, bufs, nbufs, nvars, &why)) return 0;
+  if (err && errlen > 0) snprintf(err, errlen, "%s", why.c_str());
+  return KVM_STATUS_INVALID;
+}
+
+int kvm_ntasks(const KvmExec* ex) { return (int)ex->tasks.size(); }
+
+const char* kvm_op_name(int op_id) { return kvm_registry_name(op_id); }
+
+int kvm_seeded_fill_test(unsigned long long seed, long long n, int draws, float bias, float coef, float* out) {
+  float* d = nullptr;
+  if (hipMalloc(&d, std::max<long long>(n, 1) * 4) != hipSuccess) { g_err = "hipMalloc failed"; return KVM_STATUS_HIP_ERROR; }
+  hipLaunchKernelGGL(kvm_seeded_kernel, dim3(64), dim3(256), 0, 0, d, n, seed, draws, bias, coef);
+  hipError_t e = hipMemcpy(out, d, n * 4, hipMemcpyDeviceToHost);
+  hipFree(d);
+  if (e != hipSuccess) { g_err = hipGetErrorString(e); return KVM_STATUS_HIP_ERROR; }
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,299 @@
+// Attention and decode operators (registry ops 45-50, 134-136). Layouts: activations [B*T, H*hd]; lse/delta at
+// (b*H+h)*T+t; KV cache [B*Hkv*Tmax, hd]. Causal tasks cover 128 rows (reference: runtime/ref_gpt.py:13, 279-364).
+// Softmax statistics are fp32 with the online (running max) form; lse is the natural log.
+#pragma once
+#include "common.h"
+#include "ops_basic.h"
+
+namespace kvm {
+
+constexpr int ATTN_ROWS = 128;
+constexpr int ATTN_KT = 32;     // keys (or queries) staged per LDS slab
+
+// Stages rows [r0, r0+n) of column block [c0, c0+hd) of X into LDS as fp32 [n][hd+1] (zero rows past `valid`).
+__device__ __forceinline__ void stage_rows(float* dst, const View& X, long long r0, int n, int valid, int c0, int hd) {
+  for (int e = tid(); e < n * hd; e += KVM_THREADS) {
+    int r = e / hd, k = e % hd;
+    dst[r * (hd + 1) + k] = r < valid ? X.at(r0 + r, c0 + k) : 0.f;
+  }
+}
+
+// Two threads per row: thread pair (2*row, 2*row+1) splits the head dimension in halves; dot products combine with
+// one lane swap. Registers: q/do halves and the output accumulator halves (hd <= 128 -> 64 + 64 floats).
+__device__ void op_attn_fwd(const Ctx& c) {
+  View q = c.buf(0), k = c.buf(1), v = c.buf(2), o = c.buf(3), lse = c.buf(4);
+  int bb = c.i(5), h = c.i(6), q0 = c.i(7), T = c.i(8), H = c.i(9), Hkv = c.i(10), hd = c.i(11); float sc = c.f(12);
+  int kvh = h / (H / Hkv), half = hd / 2, row = tid() >> 1, part = tid() & 1;
+  int gq = q0 + row; bool active = gq < T;
+  float* Ks = (float*)c.smem; float* Vs = Ks + ATTN_KT * (hd + 1);
+  float qr[64], acc[64];
+  for (int i = 0; i < half; ++i) { qr[i] = active ? q.at((long long)bb * T + gq, h * hd + part * half + i) : 0.f; acc[i] = 0.f; }
+  float m = -INFINITY, l = 0.f;
+  int last = min(q0 + ATTN_ROWS, T);     // keys [0, last) can matter to this task
+  for (int j0 = 0; j0 < last; j0 += ATTN_KT) {
+    int nv = min(ATTN_KT, last - j0);
+    __syncthreads();
+    stage_rows(Ks, k, (long long)bb * T + j0, ATTN_KT, nv, kvh * hd, hd);
+    stage_rows(Vs, v, (long long)bb * T + j0, ATTN_KT, nv, kvh * hd, hd);
+    __syncthreads();
+    for (int jj = 0; jj < nv; ++jj) {
+      int j = j0 + jj;
+      float s = 0.f;
+      for (int i = 0; i < half; ++i) s += qr[i] * Ks[jj * (hd + 1) + part * half + i];
+      s += __shfl_xor(s, 1, 64);
+      s *= sc;
+      if (!active || j > gq) continue;
+      float nm = fmaxf(m, s), f = __expf(m - nm), p = __expf(s - nm);
+      l = l * f + p;
+      for (int i = 0; i < half; ++i) acc[i] = acc[i] * f + p * Vs[jj * (hd + 1) + part * half + i];
+      m = nm;
+    }
+  }
+  if (active) {
+    float inv = 1.f / l;
+    for (int i = 0; i < half; ++i) o.st(((long long)bb * T + gq) * o.cols + h * hd + part * half + i, acc[i] * inv);
+    if (part == 0) lse.f()[((long long)bb * H + h) * T + gq] = m + logf(l);
+  }
+}
+
+__device__ void op_attn_bwd_delta(const Ctx& c) {
+  View o = c.buf(0), d = c.buf(1), delta = c.buf(2); int r0 = c.i(3), r1 = c.i(4), T = c.i(5), H = c.i(6), hd = c.i(7);
+  for (int rh = r0 * H + wave(); rh < r1 * H; rh += KVM_WAVES) {
+    int r = rh / H, h = rh % H; float s = 0.f;
+    for (int k = lane(); k < hd; k += 64) s += o.at(r, h * hd + k) * d.at(r, h * hd + k);
+    s = wave_sum(s);
+    if (lane() == 0) delta.f()[((long long)(r / T) * H + h) * T + r % T] = s;
+  }
+}
+
+__device__ void op_attn_bwd_dq(const Ctx& c) {
+  View q = c.buf(0), k = c.buf(1), v = c.buf(2), d = c.buf(3), lse = c.buf(4), delta = c.buf(5), dq = c.buf(6);
+  int bb = c.i(7), h = c.i(8), q0 = c.i(9), T = c.i(10), H = c.i(11), Hkv = c.i(12), hd = c.i(13); float sc = c.f(14);
+  int kvh = h / (H / Hkv), half = hd / 2, row = tid() >> 1, part = tid() & 1;
+  int gq = q0 + row; bool active = gq < T;
+  float* Ks = (float*)c.smem; float* Vs = Ks + ATTN_KT * (hd + 1);
+  float qr[64], dr[64], acc[64];
+  long long qrow = (long long)bb * T + gq;
+  for (int i = 0; i < half; ++i) {
+    qr[i] = active ? q.at(qrow, h * hd + part * half + i) : 0.f;
+    dr[i] = active ? d.at(qrow, h * hd + part * half + i) : 0.f;
+    acc[i] = 0.f;
+  }
+  float li = active ? lse.f()[((long long)bb * H + h) * T + gq] : 0.f, di = active ? delta.f()[((long long)bb * H + h) * T + gq] : 0.f;
+  int last = min(q0 + ATTN_ROWS, T);
+  for (int j0 = 0; j0 < last; j0 += ATTN_KT) {
+    int nv = min(ATTN_KT, last - j0);
+    __syncthreads();
+    stage_rows(Ks, k, (long long)bb * T + j0, ATTN_KT, nv, kvh * hd, hd);
+    stage_rows(Vs, v, (long long)bb * T + j0, ATTN_KT, nv, kvh * hd, hd);
+    __syncthreads();
+    for (int jj = 0; jj < nv; ++jj) {
+      float s = 0.f, dp = 0.f;
+      for (int i = 0; i < half; ++i) { s += qr[i] * Ks[jj * (hd + 1) + part * half + i]; dp += dr[i] * Vs[jj * (hd + 1) + part * half + i]; }
+      s += __shfl_xor(s, 1, 64); dp += __shfl_xor(dp, 1, 64);
+      if (!active || j0 + jj > gq) continue;
+      float ds = __expf(s * sc - li) * (dp - di);
+      for (int i = 0; i < half; ++i) acc[i] += ds * Ks[jj * (hd + 1) + part * half + i];
+    }
+  }
+  if (active) for (int i = 0; i < half; ++i) dq.st(qrow * dq.cols + h * hd + part * half + i, acc[i] * sc);
+}
+
+// dK/dV for 128 keys of kv head kvh: sums over the GQA group's heads and every later query, fixed order.
+__device__ void op_attn_bwd_dkv(const Ctx& c) {
+  View q = c.buf(0), k = c.buf(1), v = c.buf(2), d = c.buf(3), lse = c.buf(4), delta = c.buf(5), dk = c.buf(6), dv = c.buf(7);
+  int bb = c.i(8), kvh = c.i(9), k0 = c.i(10), T = c.i(11), H = c.i(12), hd = c.i(13); float sc = c.f(14);
+  int G = H / (k.cols / hd), half = hd / 2, row = tid() >> 1, part = tid() & 1;
+  int gk = k0 + row; bool active = gk < T;
+  float* Qs = (float*)c.smem; float* Ds = Qs + ATTN_KT * (hd + 1); float* Ls = Ds + ATTN_KT * (hd + 1); float* Es = Ls + ATTN_KT;
+  long long krow = (long long)bb * T + gk;
+  float kr[64], vr[64], sk[64], sv[64];
+  for (int i = 0; i < half; ++i) {
+    kr[i] = active ? k.at(krow, kvh * hd + part * half + i) : 0.f;
+    vr[i] = active ? v.at(krow, kvh * hd + part * half + i) : 0.f;
+    sk[i] = sv[i] = 0.f;
+  }
+  for (int h = kvh * G; h < (kvh + 1) * G; ++h)
+    for (int j0 = k0; j0 < T; j0 += ATTN_KT) {   // queries before k0 never see these keys
+      int nv = min(ATTN_KT, T - j0);
+      __syncthreads();
+      stage_rows(Qs, q, (long long)bb * T + j0, ATTN_KT, nv, h * hd, hd);
+      stage_rows(Ds, d, (long long)bb * T + j0, ATTN_KT, nv, h * hd, hd);
+      for (int e = tid(); e < ATTN_KT; e += KVM_THREADS) {
+        Ls[e] = e < nv ? lse.f()[((long long)bb * H + h) * T + j0 + e] : 0.f;
+        Es[e] = e < nv ? delta.f()[((long long)bb * H + h) * T + j0 + e] : 0.f;
+      }
+      __syncthreads();
+      for (int jj = 0; jj < nv; ++jj) {
+        float s = 0.f, dp = 0.f;
+        for (int i = 0; i < half; ++i) { s += Qs[jj * (hd + 1) + part * half + i] * kr[i]; dp += Ds[jj * (hd + 1) + part * half + i] * vr[i]; }
+        s += __shfl_xor(s, 1, 64); dp += __shfl_xor(dp, 1, 64);
+        if (!active || j0 + jj < gk) continue;
+        float p = __expf(s * sc - Ls[jj]), w = p * (dp - Es[jj]);
+        for (int i = 0; i < half; ++i) { sv[i] += p * Ds[jj * (hd + 1) + part * half + i]; sk[i] += w * Qs[jj * (hd + 1) + part * half + i]; }
+      }
+    }
+  if (active) for (int i = 0; i < half; ++i) {
+    dk.st(krow * dk.cols + kvh * hd + part * half + i, sk[i] * sc);
+    dv.st(krow * dv.cols + kvh * hd + part * half + i, sv[i]);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- decode
+// One query row per (b, h) over cache positions [0, lens[b]] (registry op 50).
+__device__ void op_attn_decode(const Ctx& c) {
+  View q = c.buf(0), kc = c.buf(1), vc = c.buf(2), lens = c.buf(3), o = c.buf(4);
+  int bb = c.i(5), h = c.i(6), H = c.i(7), Hkv = c.i(8), hd = c.i(9), Tmax = c.i(10); float sc = c.f(11);
+  int n = lens.i()[bb] + 1;
+  if (n < 1 || n > Tmax) { if (tid() == 0) c.fail(KVM_ERR_OP_KVLEN, bb, n - 1); return; }
+  long long base = ((long long)bb * Hkv + h / (H / Hkv)) * Tmax;
+  float* qs = (float*)c.smem; float* s = qs + 128; float* red = s + n;
+  for (int k = tid(); k < hd; k += KVM_THREADS) qs[k] = q.at(bb, h * hd + k);
+  __syncthreads();
+  float mx = -INFINITY;
+  for (int j = tid(); j < n; j += KVM_THREADS) { float a = 0.f; for (int k = 0; k < hd; ++k) a += qs[k] * kc.at(base + j, k); s[j] = a * sc; mx = fmaxf(mx, s[j]); }
+  mx = block_max(mx, red);
+  float l = 0.f;
+  for (int j = tid(); j < n; j += KVM_THREADS) { s[j] = __expf(s[j] - mx); l += s[j]; }
+  l = block_sum(l, red + 4);
+  for (int k = tid(); k < hd; k += KVM_THREADS) {
+    float a = 0.f; for (int j = 0; j < n; ++j) a += s[j] * vc.at(base + j, k);
+    o.st((long long)bb * o.cols + h * hd + k, a / l);
+  }
+}
+
+constexpr float ATTN_EMPTY_M = -3.4028234663852886e38f;
+
+// Split-context decode attention (registry op 135): one task = (sequence b, kv head, split s) for the whole GQA group,
+// so each K/V row of the split is read once for G query heads. Optional fused RoPE of q and the new key, and the
+// KV append of the new token by the split that holds it (flags 1, 3).
+__device__ void op_attn_decode_part(const Ctx& c) {
+  View q = c.buf(0), kc = c.buf(1), vc = c.buf(2), lens = c.buf(3), part = c.buf(4), kn = c.buf(5), vn = c.buf(6);
+  int bb = c.i(7), kvh = c.i(8), s = c.i(9), S = c.i(10), H = c.i(11), Hkv = c.i(12), hd = c.i(13), Tmax = c.i(14);
+  float sc = c.f(15), th = c.f(16); int fl = c.i(17);
+  int L = lens.i()[bb], n = L + 1;
+  if (L < 0 || n > Tmax) { if (tid() == 0) c.fail(KVM_ERR_OP_KVLEN, bb, L); return; }
+  int chunk = (n + S - 1) / S, j0 = s * chunk, j1 = min(n, j0 + chunk), nk = max(0, j1 - j0);
+  int G = H / Hkv, half = hd / 2;
+  long long base = ((long long)bb * Hkv + kvh) * Tmax;
+  if ((8 * 128 + G * max(nk, 1) + 16) * 4 > KVM_LDS_BYTES) { if (tid() == 0) c.fail(KVM_ERR_OP_SHAPE, G, nk); return; }
+  float* qs = (float*)c.smem;             // [G][hd]
+  float* sc_ = qs + 8 * 128;              // [G][chunk] scores -> probabilities
+  float* red = sc_ + G * max(nk, 1);      // [G][2*KVM_WAVES]
+  for (int e = tid(); e < G * hd; e += KVM_THREADS) qs[e] = q.at(bb, (kvh * G + e / hd) * hd + e % hd);
+  __syncthreads();
+  if (fl & 1) {
+    for (int e = tid(); e < G * half; e += KVM_THREADS) {
+      int g = e / half, i = e % half; float sn, co; rope_sc(L, i, hd, th, sn, co);
+      float x1 = qs[g * hd + i], x2 = qs[g * hd + i + half], y1 = x1 * co - x2 * sn, y2 = x1 * sn + x2 * co;
+      if (fl & 2) { y1 = round_bf(y1); y2 = round_bf(y2); }
+      qs[g * hd + i] = y1; qs[g * hd + i + half] = y2;
+    }
+    if (j0 <= n - 1 && n - 1 < j1) {      // this split holds the new key: write it (rotated) and its value first
+      long long row = base + n - 1;
+      for (int i = tid(); i < half; i += KVM_THREADS) {
+        float sn, co; rope_sc(L, i, hd, th, sn, co);
+        float x1 = kn.at(bb, kvh * hd + i), x2 = kn.at(bb, kvh * hd + i + half);
+        kc.st(row * kc.cols + i, x1 * co - x2 * sn); kc.st(row * kc.cols + i + half, x1 * sn + x2 * co);
+      }
+      for (int k = tid(); k < hd; k += KVM_THREADS) vc.st(row * vc.cols + k, vn.at(bb, kvh * hd + k));
+    }
+    __syncthreads();
+  }
+  if (nk == 0) {
+    for (int e = tid(); e < G * (hd + 2); e += KVM_THREADS) {
+      int g = e / (hd + 2), k = e % (hd + 2); long long r = (((long long)bb * S + s) * H + kvh * G + g) * part.cols;
+      part.f()[r + k] = k < hd ? 0.f : (k == hd ? ATTN_EMPTY_M : 0.f);
+    }
+    return;
+  }
+  // scores: one thread per key, all G heads; K row read once as 16-byte vectors when bf16
+  for (int j = tid(); j < nk; j += KVM_THREADS) {
+    float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    long long kb = (base + j0 + j) * kc.cols;
+    if (kc.dtype == 2) {
+      for (int k = 0; k < hd; k += 8) {
+        u16x8_t w = *(const u16x8_t*)(kc.h() + kb + k);
+        for (int i = 0; i < 8; ++i) { float kv = bf2f(w[i]); for (int g = 0; g < G; ++g) a[g] += qs[g * hd + k + i] * kv; }
+      }
+    } else for (int k = 0; k < hd; ++k) { float kv = kc.f()[kb + k]; for (int g = 0; g < G; ++g) a[g] += qs[g * hd + k] * kv; }
+    for (int g = 0; g < G; ++g) sc_[g * nk + j] = a[g] * sc;
+  }
+  __syncthreads();
+  // per-head max and sum: wave w reduces heads w, w+4
+  for (int g = wave(); g < G; g += KVM_WAVES) {
+    float m = -INFINITY; for (int j = lane(); j < nk; j += 64) m = fmaxf(m, sc_[g * nk + j]);
+    m = wave_max(m);
+    float l = 0.f; for (int j = lane(); j < nk; j += 64) { float p = __expf(sc_[g * nk + j] - m); sc_[g * nk + j] = p; l += p; }
+    l = wave_sum(l);
+    if (lane() == 0) { red[g * 2] = m; red[g * 2 + 1] = l; }
+  }
+  __syncthreads();
+  for (int e = tid(); e < G * hd; e += KVM_THREADS) {
+    int g = e / hd, k = e % hd; float a = 0.f;
+    for (int j = 0; j < nk; ++j) a += sc_[g * nk + j] * vc.ld((base + j0 + j) * vc.cols + k);
+    long long r = (((long long)bb * S + s) * H + kvh * G + g) * part.cols;
+    part.f()[r + k] = a;
+    if (k == 0) { part.f()[r + hd] = red[g * 2]; part.f()[r + hd + 1] = red[g * 2 + 1]; }
+  }
+}
+__device__ void op_attn_decode_merge(const Ctx& c) {
+  View part = c.buf(0), o = c.buf(1); int bb = c.i(2), h0 = c.i(3), h1 = c.i(4), S = c.i(5), H = c.i(6), hd = c.i(7);
+  for (int e = tid(); e < (h1 - h0) * hd; e += KVM_THREADS) {
+    int h = h0 + e / hd, k = e % hd;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) { long long r = (((long long)bb * S + s) * H + h) * part.cols; if (part.f()[r + hd + 1] > 0.f) M = fmaxf(M, part.f()[r + hd]); }
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < S; ++s) {
+      long long r = (((long long)bb * S + s) * H + h) * part.cols;
+      float l = part.f()[r + hd + 1];
+      if (l > 0.f) { float w = __expf(part.f()[r + hd] - M); num += w * part.f()[r + k]; den += w * l; }
+    }
+    o.st((long long)bb * o.cols + h * hd + k, num / den);
+  }
+}
+
+// Decode GEMV (registry op 134): out[0,n] = sum_k v[k] w[n,k] (+ res) for rows [n0,n1) of a bf16 [N,K] weight, with
+// v = bf16(prologue(x)) staged in LDS. One wave streams one weight row at a time with 16-byte loads, several
+// loads in flight per lane; fp32 sums in a fixed order (lane partials, then the wave tree).
+__device__ void op_gemv_bf16(const Ctx& c) {
+  View x = c.buf(0), x2 = c.buf(1), g = c.buf(2), w = c.buf(3), out = c.buf(4), res = c.buf(5);
+  int n0 = c.i(6), n1 = c.i(7), K = c.i(8), pro = c.i(9); float eps = c.f(10);
+  float* vs = (float*)c.smem; float* red = vs + K;
+  if (pro == 1) {
+    float ss = 0.f; for (int k = tid(); k < K; k += KVM_THREADS) { float a = x.ld(k); ss += a * a; }
+    ss = block_sum(ss, red);
+    float rs = 1.f / sqrtf(ss / (float)K + eps);
+    for (int k = tid(); k < K; k += KVM_THREADS) vs[k] = round_bf(x.ld(k) * rs * g.f()[k]);
+  } else if (pro == 2) {
+    for (int k = tid(); k < K; k += KVM_THREADS) vs[k] = round_bf(silu_f(x.ld(k)) * x2.ld(k));
+  } else for (int k = tid(); k < K; k += KVM_THREADS) vs[k] = round_bf(x.ld(k));
+  __syncthreads();
+  const int l = lane();
+  for (int n = n0 + wave(); n < n1; n += KVM_WAVES) {
+    const u16x8_t* wr = (const u16x8_t*)(w.h() + (long long)n * w.cols);
+    float a = 0.f;
+    int nv = K / 8;
+    int q = l;
+    for (; q + 192 < nv; q += 256) {         // four 16-byte loads in flight per lane
+      u16x8_t w0 = wr[q], w1 = wr[q + 64], w2 = wr[q + 128], w3 = wr[q + 192];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a += bf2f(w0[i]) * vs[q * 8 + i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a += bf2f(w1[i]) * vs[(q + 64) * 8 + i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a += bf2f(w2[i]) * vs[(q + 128) * 8 + i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a += bf2f(w3[i]) * vs[(q + 192) * 8 + i];
+    }
+    for (; q < nv; q += 64) {
+      u16x8_t w0 = wr[q];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a += bf2f(w0[i]) * vs[q * 8 + i];
+    }
+    a = wave_sum(a);
+    if (l == 0) out.st(n, a + (res.ok() ? res.ld(n) : 0.f));
+  }
+}
+
+}  // namespace kvm

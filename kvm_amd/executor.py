@@ -1,0 +1,274 @@
+"""Python host side of the executor: a ctypes binding of libkvm_exec.so (include/kvm_exec.h).
+
+Mirrors the reference's MvmExec interface (reference: mvm_exec.cu:492-1560): create, add buffers, set versions, submit
+bundles, start, finish, read buffers, trace. The GPU path is the HIP library only: if it is not built, or no GPU is
+present, the calls raise; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+
+from . import bundle as bl
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / '_build' / 'libkvm_exec.so'
+HEADER = HERE.parent / 'include' / 'kvm_exec.h'
+_lib = None
+
+KVM_INIT_ZERO, KVM_INIT_FILL, KVM_INIT_VALUES, KVM_INIT_SEEDED = 0, 1, 2, 3
+ERRORS = {0: 'OK', 1: 'BAD_OP', 2: 'BAD_ARITY', 3: 'BAD_BUF_INDEX', 4: 'BAD_BUF', 5: 'BOUNDS', 6: 'BAD_VAR', 7: 'VERSION_GAP',
+          8: 'WAIT_VIOLATION', 9: 'DOUBLE_EXEC', 11: 'BAD_TASK', 15: 'TIMEOUT', 16: 'QUEUE_OVERFLOW', 17: 'BAD_CONFIG',
+          1001: 'OP_BUF', 1002: 'OP_DTYPE', 1003: 'OP_RANGE', 1004: 'OP_SHAPE', 1005: 'OP_TOKEN', 1006: 'OP_KVLEN'}
+
+
+class KvmConfig(ctypes.Structure):
+    _fields_ = [('blocks', ctypes.c_int), ('trace_on', ctypes.c_int), ('num_vars', ctypes.c_int), ('timeout_us', ctypes.c_ulonglong),
+                ('device', ctypes.c_int)]
+
+
+class KvmInit(ctypes.Structure):
+    _fields_ = [('kind', ctypes.c_int), ('value', ctypes.c_float), ('values', ctypes.c_void_p), ('seed', ctypes.c_ulonglong),
+                ('draws', ctypes.c_int), ('bias', ctypes.c_float), ('coef', ctypes.c_float)]
+
+
+class KvmTrace(ctypes.Structure):
+    _fields_ = [('start', ctypes.c_ulonglong), ('end', ctypes.c_ulonglong), ('block', ctypes.c_int), ('xcc', ctypes.c_int),
+                ('ver0', ctypes.c_int), ('ver1', ctypes.c_int), ('exec_count', ctypes.c_int), ('pad', ctypes.c_int)]
+
+
+class KvmResult(ctypes.Structure):
+    _fields_ = [('err_code', ctypes.c_int), ('err_slot', ctypes.c_int), ('err_a', ctypes.c_int), ('err_b', ctypes.c_int),
+                ('done', ctypes.c_int), ('admitted', ctypes.c_int), ('grid', ctypes.c_int), ('kernel_ms', ctypes.c_float)]
+
+
+TRACE_DTYPE = np.dtype([('start', '<u8'), ('end', '<u8'), ('block', '<i4'), ('xcc', '<i4'), ('ver0', '<i4'), ('ver1', '<i4'),
+                        ('exec_count', '<i4'), ('pad', '<i4')])
+
+
+def declared_symbols() -> list[str]:
+    """Every function include/kvm_exec.h declares."""
+    return re.findall(r'^\s*[\w\s\*]+?\b(kvm_\w+)\s*\(', HEADER.read_text(), re.M)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f'{LIB_PATH} is not built: run __graft_entry__.build() (or python kvm_amd/build.py)')
+        L = ctypes.CDLL(str(LIB_PATH))
+        P, I, U = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+        sig = {
+            'kvm_config_default': (None, [P]), 'kvm_create': (P, [P]), 'kvm_destroy': (None, [P]),
+            'kvm_last_error': (ctypes.c_char_p, [P]), 'kvm_add_buffer': (I, [P, I, I, I, P]), 'kvm_nbufs': (I, [P]),
+            'kvm_buffer_dtype': (I, [P, I]), 'kvm_buffer_device_ptr': (P, [P, I]), 'kvm_write_buffer': (I, [P, I, P, U]),
+            'kvm_read_buffer': (I, [P, I, P, U]), 'kvm_read_raw': (I, [P, I, P, U]), 'kvm_set_version': (I, [P, I, I]),
+            'kvm_submit': (I, [P, P, I, P, I, P, I]), 'kvm_start': (I, [P]), 'kvm_finish': (I, [P, P]), 'kvm_relaunch': (I, [P]),
+            'kvm_run_timed': (I, [P, I, P]), 'kvm_versions': (I, [P, P, I]), 'kvm_trace': (I, [P, P, I]), 'kvm_ntasks': (I, [P]),
+            'kvm_op_name': (ctypes.c_char_p, [I]),
+            'kvm_validate': (I, [P, I, P, I, P, I, P, I, I, ctypes.c_char_p, I]),
+            'kvm_seeded_fill_test': (I, [ctypes.c_ulonglong, ctypes.c_longlong, I, ctypes.c_float, ctypes.c_float, P]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype, f.argtypes = res, args
+        _lib = L
+    return _lib
+
+
+class KvmError(RuntimeError):
+    pass
+
+
+class Executor:
+    """One persistent-kernel executor on one GPU. Typical use::
+
+        ex = Executor.from_bundle(bundle_dir)   # buffers + versions from the metadata, bundle submitted
+        res = ex.run()                          # start + finish
+        x = ex.read('logits')
+    """
+
+    def __init__(self, num_vars: int = 64, trace: bool = True, timeout_s: float = 20.0, blocks: int = 0, device: int = 0):
+        L = lib()
+        cfg = KvmConfig()
+        L.kvm_config_default(ctypes.byref(cfg))
+        cfg.num_vars, cfg.trace_on, cfg.timeout_us, cfg.blocks, cfg.device = max(1, num_vars), int(trace), int(timeout_s * 1e6), blocks, device
+        self._h = L.kvm_create(ctypes.byref(cfg))
+        if not self._h:
+            raise KvmError(f'kvm_create: {L.kvm_last_error(None).decode()}')
+        self.names, self.shapes, self.dtypes = [], [], []
+        self.trace_on = trace
+        self.meta = None
+
+    def close(self):
+        if self._h:
+            lib().kvm_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc, what):
+        if rc < 0:
+            raise KvmError(f'{what}: {lib().kvm_last_error(self._h).decode()}')
+        return rc
+
+    # ------------------------------------------------------------------ buffers
+    def add_buffer(self, name, rows, cols, dtype, init: dict | None = None, data: np.ndarray | None = None, root=None) -> int:
+        ini = KvmInit()
+        keep = None
+        if data is not None:
+            keep = _as_storage(np.asarray(data), dtype)
+            ini.kind, ini.values = KVM_INIT_VALUES, keep.ctypes.data
+        elif init is None:
+            ini.kind = KVM_INIT_ZERO
+        elif init['kind'] == 'fill':
+            ini.kind, ini.value = KVM_INIT_FILL, float(init['value'])
+        elif init['kind'] == 'seeded':
+            ini.kind, ini.seed, ini.draws, ini.bias, ini.coef = KVM_INIT_SEEDED, init['seed'] % 2**64, init['draws'], init['bias'], init['coef']
+        else:
+            keep = _as_storage(bl.materialize({'rows': rows, 'cols': cols, 'dtype': dtype, 'init': init}, root), dtype)
+            ini.kind, ini.values = KVM_INIT_VALUES, keep.ctypes.data
+        idx = self._check(lib().kvm_add_buffer(self._h, rows, cols, dtype, ctypes.byref(ini)), f'add_buffer {name}')
+        self.names.append(name)
+        self.shapes.append((rows, cols))
+        self.dtypes.append(dtype)
+        return idx
+
+    def index(self, name) -> int:
+        return self.names.index(name) if isinstance(name, str) else int(name)
+
+    def read(self, name) -> np.ndarray:
+        """f32 (bf16 widened) or int32 contents, flat."""
+        i = self.index(name)
+        r, c = self.shapes[i]
+        if self.dtypes[i] == bl.DT_I32:
+            out = np.empty(r * c, np.int32)
+            self._check(lib().kvm_read_raw(self._h, i, out.ctypes.data, out.nbytes), 'read')
+            return out
+        out = np.empty(r * c, np.float32)
+        self._check(lib().kvm_read_buffer(self._h, i, out.ctypes.data, out.size), 'read')
+        return out
+
+    def read_raw(self, name) -> np.ndarray:
+        i = self.index(name)
+        r, c = self.shapes[i]
+        out = np.empty(r * c, {0: np.float32, 1: np.int32, 2: np.uint16}[self.dtypes[i]])
+        self._check(lib().kvm_read_raw(self._h, i, out.ctypes.data, out.nbytes), 'read_raw')
+        return out
+
+    def write(self, name, data: np.ndarray):
+        i = self.index(name)
+        arr = _as_storage(np.asarray(data), self.dtypes[i])
+        self._check(lib().kvm_write_buffer(self._h, i, arr.ctypes.data, arr.nbytes), 'write')
+
+    def device_ptr(self, name) -> int:
+        return lib().kvm_buffer_device_ptr(self._h, self.index(name))
+
+    # ------------------------------------------------------------------ graph
+    def set_version(self, var: int, v: int):
+        self._check(lib().kvm_set_version(self._h, var, v), 'set_version')
+
+    def submit(self, b: bl.LoadedBundle):
+        t = np.ascontiguousarray(b.tasks, np.int32)
+        s = np.ascontiguousarray(b.succ, np.int32) if b.succ.size else np.zeros(1, np.int32)
+        a = np.ascontiguousarray(b.args, np.int32) if b.args.size else np.zeros(1, np.int32)
+        self._check(lib().kvm_submit(self._h, t.ctypes.data, t.shape[0], s.ctypes.data, int(b.succ.size), a.ctypes.data, int(b.args.size)),
+                    'submit')
+
+    @classmethod
+    def from_bundle(cls, src, buffers: list | None = None, **kw) -> 'Executor':
+        """Executor with the bundle's buffer table (metadata init, or `buffers` arrays) and base versions; bundle submitted."""
+        b = src if isinstance(src, bl.LoadedBundle) else bl.load(src)
+        ex = cls(num_vars=len(b.metadata['variables']), **kw)
+        for i, m in enumerate(b.metadata['buffers']):
+            ex.add_buffer(m['name'], m['rows'], m['cols'], m['dtype'], init=m['init'], data=None if buffers is None else buffers[i], root=b.root)
+        for v in b.metadata['variables']:
+            ex.set_version(v['id'], v['base_version'])
+        ex.submit(b)
+        ex.meta = b.metadata
+        return ex
+
+    def start(self):
+        self._check(lib().kvm_start(self._h), 'start')
+
+    def relaunch(self):
+        self._check(lib().kvm_relaunch(self._h), 'relaunch')
+
+    def finish(self, check: bool = True) -> dict:
+        r = KvmResult()
+        rc = lib().kvm_finish(self._h, ctypes.byref(r))
+        res = {'err_code': r.err_code, 'err': ERRORS.get(r.err_code, str(r.err_code)), 'err_slot': r.err_slot, 'err_a': r.err_a,
+               'err_b': r.err_b, 'done': r.done, 'admitted': r.admitted, 'grid': r.grid, 'kernel_ms': r.kernel_ms}
+        if check and (rc < 0 or r.err_code):
+            raise KvmError(f'run failed: {res} {lib().kvm_last_error(self._h).decode()}')
+        return res
+
+    def run(self, check: bool = True) -> dict:
+        self.start()
+        return self.finish(check)
+
+    def run_timed(self, n: int) -> float:
+        ms = ctypes.c_float()
+        self._check(lib().kvm_run_timed(self._h, n, ctypes.byref(ms)), 'run_timed')
+        return ms.value
+
+    def versions(self, n: int | None = None) -> np.ndarray:
+        n = n if n is not None else max(1, len(self.meta['variables']) if self.meta else 1)
+        out = np.zeros(n, np.int32)
+        self._check(lib().kvm_versions(self._h, out.ctypes.data, n), 'versions')
+        return out
+
+    def trace(self) -> np.ndarray:
+        n = lib().kvm_ntasks(self._h)
+        out = np.zeros(n, TRACE_DTYPE)
+        self._check(lib().kvm_trace(self._h, out.ctypes.data, n), 'trace')
+        return out
+
+
+def _as_storage(x: np.ndarray, dtype: int) -> np.ndarray:
+    if dtype == bl.DT_I32:
+        return np.ascontiguousarray(x, np.int32)
+    if dtype == bl.DT_BF16:
+        if x.dtype == np.uint16:
+            return np.ascontiguousarray(x)
+        return bl.bf16_bits(np.asarray(x, np.float32))
+    return np.ascontiguousarray(x, np.float32)
+
+
+class MvmBuf(ctypes.Structure):
+    _fields_ = [('p', ctypes.c_void_p), ('rows', ctypes.c_int32), ('cols', ctypes.c_int32), ('ld', ctypes.c_int32),
+                ('dtype', ctypes.c_int32), ('reserved', ctypes.c_int32 * 2)]
+
+
+def validate(b: bl.LoadedBundle) -> str | None:
+    """Host-only bundle validation (the checks kvm_submit runs); None when valid, else the reason. Needs no GPU."""
+    meta = b.metadata
+    bufs = (MvmBuf * max(1, len(meta['buffers'])))()
+    for i, m in enumerate(meta['buffers']):
+        bufs[i] = MvmBuf(None, m['rows'], m['cols'], m['cols'], m['dtype'])
+    t = np.ascontiguousarray(b.tasks, np.int32)
+    s = np.ascontiguousarray(b.succ, np.int32) if b.succ.size else np.zeros(1, np.int32)
+    a = np.ascontiguousarray(b.args, np.int32) if b.args.size else np.zeros(1, np.int32)
+    err = ctypes.create_string_buffer(512)
+    rc = lib().kvm_validate(t.ctypes.data, t.shape[0], s.ctypes.data, int(b.succ.size), a.ctypes.data, int(b.args.size), bufs,
+                            len(meta['buffers']), max(1, len(meta['variables'])), err, 512)
+    return None if rc == 0 else err.value.decode()
+
+
+def op_name(op_id: int) -> str | None:
+    r = lib().kvm_op_name(op_id)
+    return r.decode() if r else None
+
+
+def seeded_fill_test(seed, n, draws, bias, coef) -> np.ndarray:
+    out = np.zeros(n, np.float32)
+    if lib().kvm_seeded_fill_test(seed % 2**64, n, draws, bias, coef, out.ctypes.data) < 0:
+        raise KvmError(lib().kvm_last_error(None).decode())
+    return out

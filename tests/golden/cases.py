@@ -123,10 +123,10 @@ def gpt_ops():
     ids = w.ints('ids', [w.rng.randrange(V) for _ in range(R)])
     wte, wpe = w.buf('wte', V, D, scale=0.5), w.buf('wpe', T, D, scale=0.5)
     emb = w.zeros('emb', R, D)
-    w.task('embedding_fwd', ids=ids, wte=wte, wpe=wpe, out=emb, r0=3, r1=R, T=T, d=D)
+    te = w.task('embedding_fwd', ids=ids, wte=wte, wpe=wpe, out=emb, r0=3, r1=R, T=T, d=D)
     dtab, dpos = w.zeros('dtab', V, D), w.zeros('dpos', T, D)
-    w.task('embedding_bwd', ids=ids, dout=emb, dtab=dtab, N=R, mod=0, v0=0, v1=V, d=D, acc=0)
-    w.task('embedding_bwd', ids=None, dout=emb, dtab=dpos, N=R, mod=T, v0=1, v1=T, d=D, acc=0)
+    w.task('embedding_bwd', after=[te], ids=ids, dout=emb, dtab=dtab, N=R, mod=0, v0=0, v1=V, d=D, acc=0)
+    w.task('embedding_bwd', after=[te], ids=None, dout=emb, dtab=dpos, N=R, mod=T, v0=1, v1=T, d=D, acc=0)
     # matmul_tile variants
     M, N, K = 70, 80, 24
     A, At, Bm, Bt = w.buf('A', M, K), w.buf('At', K, M), w.buf('Bm', K, N), w.buf('Bt', N, K)

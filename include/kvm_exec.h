@@ -35,7 +35,8 @@ typedef struct KvmInit {
   int kind;
   float value;                 // FILL (f32/bf16 value; i32 buffers take it as an integer)
   const void* values;          // VALUES: rows*cols elements in the buffer's dtype (bf16 as raw uint16)
-  unsigned long long seed;     // SEEDED: SplitMix64 generator parameters as in the bundle metadata
+  unsigned long long seed;     // SEEDED: SplitMix64 generator parameters as in the bundle metadata (bf16 buffers: each value
+                               //   rounded once to bf16, this executor's extension for bf16 weights)
   int draws;
   float bias, coef;
 } KvmInit;

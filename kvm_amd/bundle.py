@@ -67,8 +67,9 @@ def materialize(buf: dict, root: Path | None = None) -> np.ndarray:
         return np.full(n, init['value'], np_dt)
     if k == 'values':
         return np.asarray(init['values'], np_dt)
-    if k == 'seeded':
-        return initgen.seeded(init['seed'], n, init['draws'], init['bias'], init['coef'])
+    if k == 'seeded':   # bf16 buffers (an executor-side override, not a bundle init): rounded once to bf16
+        v = initgen.seeded(init['seed'], n, init['draws'], init['bias'], init['coef'])
+        return bf16_round(v) if dt == DT_BF16 else v
     if k == 'file':
         raw = (Path(root) / init['path']).read_bytes()
         if dt == DT_BF16:

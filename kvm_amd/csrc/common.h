@@ -7,6 +7,12 @@
 #include "../../include/kvm_exec.h"
 
 typedef uint16_t u16x8_t __attribute__((ext_vector_type(8)));
+// Address-space qualifiers: buffer data is global memory (addrspace 1), operator scratch is LDS (addrspace 3). Typing
+// pointers this way makes the compiler emit global_/ds_ instructions instead of flat ones, so LDS traffic does not
+// wait on outstanding HBM loads.
+#define GLOBAL __attribute__((address_space(1)))
+typedef float f32x4n __attribute__((ext_vector_type(4)));   // native 128-bit float vector (HIP's float4 is a class)
+#define LDS __attribute__((address_space(3)))
 
 #define KVM_THREADS 256          // every operator runs on one workgroup of 256 threads = four wave64s
 #define KVM_WAVES (KVM_THREADS / 64)
@@ -24,12 +30,21 @@ enum KvmErr {
   KVM_ERR_OP_TOKEN = 1005, KVM_ERR_OP_KVLEN = 1006,
 };
 
+// Successor edges as uploaded to the device: the task index plus a bit set when the successor has exactly one
+// predecessor and no version wait (it is released by that predecessor without a counter).
+#define KVM_EDGE_DIRECT (1 << 30)
+#define KVM_EDGE_INDEX (KVM_EDGE_DIRECT - 1)
+
 struct KvmCounters {
-  int done;            // tasks finished
-  int enq;             // tasks enqueued (== ready-queue tail)
   int err_code, err_slot, err_a, err_b;
-  unsigned head;       // next ready-queue ticket
-  int pad;
+  int pad[4];
+};
+
+// One ready queue. Head (consumer tickets) and tail (producer slots) sit on separate 128-byte lines.
+#define KVM_MAX_QUEUES 8
+struct KvmQueue {
+  unsigned head; int pad0[31];
+  int tail; int pad1[31];
 };
 
 // Everything the persistent kernel reads. One task graph per launch (the submitted bundles concatenated).
@@ -39,14 +54,17 @@ struct KvmDevState {
   const int32_t* args;        // [nargs]
   const MvmBuf* bufs;         // [nbufs]
   int* indeg;                 // [ntasks] remaining predecessors
-  int* ready;                 // [ntasks] ready queue: cell t holds the t-th released task, -1 until then
+  int* ready;                 // [nq * qcap] ready queues: cell q*qcap+i holds the i-th released task of queue q, -1 until then
+  KvmQueue* queues;           // [nq]
+  const int* qcount;          // [nq] tasks that go through queue q (task t goes to queue t % nq)
+  int* done_blk;              // [grid] tasks finished per worker (summed by the host; no shared counter per task)
   int* state;                 // [ntasks] 0 not released, 1 parked on a version, 2 enqueued
   int* park_next;             // [ntasks] park list links
   int* version;               // [nvars]
   int* park_head;             // [nvars] park list heads, -1 empty
   KvmCounters* cnt;
   KvmTrace* trace;            // [ntasks] or null
-  int ntasks, nbufs, nvars, trace_on;
+  int ntasks, nbufs, nvars, trace_on, nq, qcap, grid;
   unsigned long long timeout_ticks;   // stall timeout in wall_clock64 ticks (100 MHz)
 };
 
@@ -84,19 +102,19 @@ __device__ __forceinline__ float round_bf(float x) { return bf2f(f2bf(x)); }
 struct View {
   void* p; int rows, cols, dtype;
   __device__ bool ok() const { return p != nullptr; }
-  __device__ float* f() const { return (float*)p; }
-  __device__ int* i() const { return (int*)p; }
-  __device__ uint16_t* h() const { return (uint16_t*)p; }
-  __device__ float ld(long long k) const { return dtype == 2 ? bf2f(((const uint16_t*)p)[k]) : ((const float*)p)[k]; }
+  __device__ GLOBAL float* f() const { return (GLOBAL float*)p; }
+  __device__ GLOBAL int* i() const { return (GLOBAL int*)p; }
+  __device__ GLOBAL uint16_t* h() const { return (GLOBAL uint16_t*)p; }
+  __device__ float ld(long long k) const { return dtype == 2 ? bf2f(((const GLOBAL uint16_t*)p)[k]) : ((const GLOBAL float*)p)[k]; }
   __device__ float at(long long r, long long c) const { return ld(r * cols + c); }
-  __device__ void st(long long k, float v) const { if (dtype == 2) ((uint16_t*)p)[k] = f2bf(v); else ((float*)p)[k] = v; }
+  __device__ void st(long long k, float v) const { if (dtype == 2) ((GLOBAL uint16_t*)p)[k] = f2bf(v); else ((GLOBAL float*)p)[k] = v; }
   __device__ long long n() const { return (long long)rows * cols; }
 };
 
 struct Ctx {
   const MvmBuf* bufs;
-  const int32_t* a;          // argument words (in LDS)
-  char* smem;                // KVM_LDS_BYTES of LDS
+  const LDS int32_t* a;      // argument words (in LDS)
+  LDS char* smem;            // KVM_LDS_BYTES of LDS
   KvmCounters* cnt;
   int slot;
   __device__ View buf(int k) const {
@@ -129,14 +147,14 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
-__device__ __forceinline__ float block_sum(float v, float* red) {
+template <class P> __device__ __forceinline__ float block_sum(float v, P red) {
   v = wave_sum(v);
   __syncthreads();
   if (lane() == 0) red[wave()] = v;
   __syncthreads();
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
-__device__ __forceinline__ float block_max(float v, float* red) {
+template <class P> __device__ __forceinline__ float block_max(float v, P red) {
   v = wave_max(v);
   __syncthreads();
   if (lane() == 0) red[wave()] = v;
@@ -147,7 +165,7 @@ __device__ __forceinline__ double wave_sum_d(double v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
-__device__ __forceinline__ double block_sum_d(double v, double* red) {
+template <class P> __device__ __forceinline__ double block_sum_d(double v, P red) {
   v = wave_sum_d(v);
   __syncthreads();
   if (lane() == 0) red[wave()] = v;

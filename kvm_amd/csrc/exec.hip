@@ -1,11 +1,14 @@
 // The persistent task-graph executor for MI355X (gfx950): device scheduler, operator dispatch and the C ABI host side.
 //
 // Device side (one workgroup of 256 threads per CU, all resident for the whole graph):
-//   * Ready queue: every task is enqueued exactly once (by the last predecessor to finish, by a version publisher,
-//     or at launch for roots), so the queue is a plain array of ntasks cells filled in enqueue order: enqueue takes
-//     the next tail slot and release-stores the task index; a worker takes the next head ticket and waits for that
-//     cell. Tickets >= ntasks mean the graph is drained and the worker exits. No cell is ever reused, so there is no
-//     ABA and no ring-capacity budget (reference design for comparison: include/mvm_sched.cuh:115-374).
+//   * Ready queues: every task is enqueued exactly once (by the last predecessor to finish, by a version publisher,
+//     or at launch for roots), so a queue is a plain array of cells filled in enqueue order: enqueue takes the next
+//     tail slot and stores the task index; a worker takes the next head ticket and waits for that cell. Task t always
+//     goes to queue t % nq, so each queue knows how many tasks it will see, and a ticket past that count means the
+//     queue is drained and the worker exits. No cell is ever reused: no ABA, no ring-capacity budget (reference
+//     design for comparison: include/mvm_sched.cuh:115-374). There is one queue per XCD (workers of block b use queue
+//     b % nq; the hardware places block b on XCD b % 8), so the ticket and tail atomics of a phase's tasks spread over
+//     eight addresses instead of one.
 //   * Dependencies: after an operator, the workgroup barrier orders all its stores before wave 0's agent-scope
 //     release fence (on gfx950 this writes the XCD's L2 back so another XCD sees the data); wave 0 then decrements
 //     successor counters with acq_rel atomics and enqueues the ones that reach zero.
@@ -25,19 +28,21 @@
 #include "ops_basic.h"
 #include "ops_gemm.h"
 #include "ops_attn.h"
+#include "ops_decode.h"
 #include "validate.h"
 
 using namespace kvm;
 
 // ---------------------------------------------------------------------------------------------- scheduler
+__device__ __forceinline__ void queue_overflow(const KvmDevState& S) {
+  int z = 0;   // cannot happen when every task is enqueued once; reported, never written out of bounds
+  __hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_QUEUE_OVERFLOW, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ void enqueue(const KvmDevState& S, int t) {
-  int pos = add_relaxed(&S.cnt->enq, 1);
-  if (pos >= S.ntasks) {   // cannot happen when every task is enqueued once; reported, never written out of bounds
-    int z = 0;
-    __hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_QUEUE_OVERFLOW, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
-  st_release(&S.ready[pos], t);
+  const int q = t % S.nq;
+  int pos = add_relaxed(&S.queues[q].tail, 1);
+  if (pos >= S.qcap) { queue_overflow(S); return; }
+  st_release(&S.ready[q * S.qcap + pos], t);
 }
 
 __device__ void park(const KvmDevState& S, int t, int var, int want) {
@@ -154,6 +159,7 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 135: op_attn_decode_part(c); break;
     case 136: op_attn_decode_merge(c); break;
     case 300: op_head_rmsnorm(c); break;
+    case 301: op_gemv_bf16_rows(c); break;
     default: if (threadIdx.x == 0) c.fail(KVM_ERR_BAD_OP, op, 0);
   }
 }
@@ -166,25 +172,29 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
   const int t = threadIdx.x;
   for (;;) {
     if (t == 0) {
-      unsigned ticket = add_relaxed(&S.cnt->head, 1u);
+      const int q = blockIdx.x % S.nq;
+      unsigned ticket = add_relaxed(&S.queues[q].head, 1u);
       int slot = -1;
-      if (ticket < (unsigned)S.ntasks) {
+      if (ticket < (unsigned)S.qcount[q]) {
         unsigned long long since = wall_clock64();
-        int seen_done = ld_relaxed(&S.cnt->done);
-        for (;;) {
-          slot = ld_relaxed(&S.ready[ticket]);
+        int seen = -1;
+        for (unsigned polls = 0;; ++polls) {
+          slot = ld_relaxed(&S.ready[q * S.qcap + ticket]);
           if (slot >= 0) break;
           if (ld_relaxed(&S.cnt->err_code) != 0) break;
           __builtin_amdgcn_s_sleep(1);
-          int d = ld_relaxed(&S.cnt->done);
-          unsigned long long now = wall_clock64();
-          if (d != seen_done) { seen_done = d; since = now; }
-          else if (now - since > S.timeout_ticks) {
-            int z = 0;
-            if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_TIMEOUT, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-              S.cnt->err_slot = -1; S.cnt->err_a = (int)ticket; S.cnt->err_b = d;
+          if ((polls & 4095) == 4095) {      // stall check: has any worker finished a task since the last look?
+            int d = 0;
+            for (int w = 0; w < S.grid; ++w) d += ld_relaxed(&S.done_blk[w]);
+            unsigned long long now = wall_clock64();
+            if (d != seen) { seen = d; since = now; }
+            else if (now - since > S.timeout_ticks) {
+              int z = 0;
+              if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_TIMEOUT, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                S.cnt->err_slot = -1; S.cnt->err_a = (int)ticket; S.cnt->err_b = d;
+              }
+              break;
             }
-            break;
           }
         }
         if (slot >= 0) fence_acquire();   // the enqueuer's release: predecessors' data is visible from here on
@@ -202,8 +212,13 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
       KvmTrace& tr = S.trace[slot];
       tr.start = wall_clock64();
       tr.block = blockIdx.x; tr.xcc = xcc_id();
-      tr.ver0 = s_desc.wait_var >= 0 ? ld_acquire(&S.version[s_desc.wait_var]) : -1;
+      tr.ver0 = s_desc.wait_var >= 0 ? ld_relaxed(&S.version[s_desc.wait_var]) : -1;
       tr.exec_count += 1;
+      if (tr.exec_count > 1) {
+        int z = 0;
+        if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_DOUBLE_EXEC, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+          S.cnt->err_slot = slot;
+      }
       if (s_desc.wait_var >= 0 && tr.ver0 < s_desc.wait_ver) {
         int z = 0;
         if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_WAIT_VIOLATION, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
@@ -211,55 +226,96 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
       }
     }
     __syncthreads();
-    Ctx c{S.bufs, s_args, smem, S.cnt, slot};
+    Ctx c{S.bufs, (const LDS int32_t*)s_args, (LDS char*)smem, S.cnt, slot};
     dispatch(op, c);
     __syncthreads();
-    if (t < 64) {
-      fence_release();                   // every thread's stores are behind the barrier; make them agent-visible
+    // Completion. Waves that touch successors first make this task's stores agent-visible (release fence: the
+    // barrier above ordered every thread's stores before it). Edges carry a host-computed bit: KVM_EDGE_DIRECT means
+    // the successor has this task as its only predecessor and no version wait, so it is released with no counter
+    // and no descriptor read. Other successors count down with a relaxed atomic; the decrement that reaches zero
+    // acquires (fence) before releasing the task. Released tasks are enqueued in batches: per wave and per queue one
+    // tail reservation (issued by lanes 0..nq-1 in parallel) and one relaxed cell store per task.
+    const int nsucc = s_desc.succ_cnt;
+    const int nwaves = nsucc > 64 ? KVM_WAVES : 1;
+    if (wave() < nwaves) {
+      fence_release();
       if (t == 0) {
         if (S.trace_on) {
           KvmTrace& tr = S.trace[slot];
-          tr.ver1 = s_desc.wait_var >= 0 ? ld_acquire(&S.version[s_desc.wait_var]) : -1;
+          tr.ver1 = s_desc.wait_var >= 0 ? ld_relaxed(&S.version[s_desc.wait_var]) : -1;
           tr.end = wall_clock64();
         }
         if (s_desc.pub_var >= 0) publish(S, slot, s_desc.pub_var, s_desc.pub_ver);
       }
-      for (int k = t; k < s_desc.succ_cnt; k += 64) {
-        int s = S.succ[s_desc.succ_off + k];
-        if (add_acqrel(&S.indeg[s], -1) == 1) release(S, s);
+      const int l = lane();
+      for (int base = wave() * 64; base < nsucc; base += nwaves * 64) {
+        const int k = base + l;
+        int s = -1; bool direct = false;
+        if (k < nsucc) {
+          const int e = S.succ[s_desc.succ_off + k];
+          s = e & KVM_EDGE_INDEX;
+          if (e & KVM_EDGE_DIRECT) direct = true;
+          else if (add_relaxed(&S.indeg[s], -1) == 1) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "agent");
+            if (S.tasks[s].wait_var < 0) direct = true; else release(S, s);
+          }
+        }
+        const int sq = direct ? s % S.nq : -1;
+        int cnt_mine = 0;            // lane q < nq: how many of this round's tasks go to queue q
+        for (int q = 0; q < S.nq; ++q) {
+          const int c2 = __popcll(__ballot(sq == q));
+          if (l == q) cnt_mine = c2;
+        }
+        int pos_mine = 0;
+        if (l < S.nq && cnt_mine > 0) pos_mine = add_relaxed(&S.queues[l].tail, cnt_mine);
+        // rank of this lane among the lanes bound for the same queue
+        int rank = 0;
+        for (int q = 0; q < S.nq; ++q) {
+          const unsigned long long m2 = __ballot(sq == q);
+          if (sq == q) rank = __popcll(m2 & ((1ull << l) - 1ull));
+        }
+        const int base_pos = __shfl(pos_mine, sq < 0 ? 0 : sq, 64);
+        if (direct) {
+          const int pos = base_pos + rank;
+          if (pos < S.qcap) { st_relaxed(&S.state[s], 2); st_relaxed(&S.ready[sq * S.qcap + pos], s); }
+          else queue_overflow(S);
+        }
       }
-      if (t == 0) add_acqrel(&S.cnt->done, 1);
+    }
+    if (t == 0) {
+      st_relaxed(&S.done_blk[blockIdx.x], ld_relaxed(&S.done_blk[blockIdx.x]) + 1);
     }
   }
 }
 
 // Launch-time state reset: counters, queue cells, park lists, versions; roots without a version wait go straight
 // into the first queue cells in index order, roots with one go through release().
-__global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions, const int* roots, int nroots) {
+__global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
   int i = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
   for (int k = i; k < S.ntasks; k += stride) {
-    S.indeg[k] = S.tasks[k].indegree; S.ready[k] = -1; S.state[k] = 0; S.park_next[k] = -1;
+    S.indeg[k] = S.tasks[k].indegree; S.state[k] = 0; S.park_next[k] = -1;
     if (S.trace_on) { KvmTrace z = {}; z.ver0 = z.ver1 = -1; S.trace[k] = z; }
   }
+  for (long long k = i; k < (long long)S.nq * S.qcap; k += stride) S.ready[k] = -1;
   for (int k = i; k < S.nvars; k += stride) { S.version[k] = base_versions[k]; S.park_head[k] = -1; }
+  for (int k = i; k < S.grid; k += stride) S.done_blk[k] = 0;
+  if (i < S.nq) { KvmQueue z = {}; S.queues[i] = z; }
   if (i == 0) { KvmCounters z = {}; *S.cnt = z; }
 }
+// Roots (tasks with no predecessors), single thread, in index order: those without a version wait take the first
+// cells of their queues, the rest are released afterwards (they park until their version is published).
 __global__ void kvm_seed_kernel(KvmDevState S, const int* roots, int nroots) {
-  // single workgroup: roots without waits take cells 0.. in order; the rest are released (parked) afterwards
-  __shared__ int n_direct;
-  if (threadIdx.x == 0) {
-    int n = 0;
-    for (int r = 0; r < nroots; ++r) {
-      const MvmTaskDesc& d = S.tasks[roots[r]];
-      if (d.wait_var < 0 || S.version[d.wait_var] >= d.wait_ver) { S.ready[n++] = roots[r]; S.state[roots[r]] = 2; }
+  if (threadIdx.x != 0) return;
+  for (int r = 0; r < nroots; ++r) {
+    const int t = roots[r];
+    const MvmTaskDesc& d = S.tasks[t];
+    if (d.wait_var < 0 || S.version[d.wait_var] >= d.wait_ver) {
+      const int q = t % S.nq;
+      S.ready[q * S.qcap + S.queues[q].tail++] = t;
+      S.state[t] = 2;
     }
-    S.cnt->enq = n;
-    n_direct = n;
   }
-  __syncthreads();
-  if (threadIdx.x == 0)
-    for (int r = 0; r < nroots; ++r) if (S.state[roots[r]] == 0) release(S, roots[r]);
-  (void)n_direct;
+  for (int r = 0; r < nroots; ++r) if (S.state[roots[r]] == 0) release(S, roots[r]);
 }
 
 // ---------------------------------------------------------------------------------------------- init kernels
@@ -280,6 +336,19 @@ __global__ void kvm_seeded_kernel(float* out, long long n, unsigned long long se
       acc = __fadd_rn(__fadd_rn(seeded_u(seed, j), seeded_u(seed, j + 1)), __fadd_rn(seeded_u(seed, j + 2), seeded_u(seed, j + 3)));
     }
     out[i] = __fmul_rn(__fsub_rn(acc, bias), coef);
+  }
+}
+// The same generator rounded once to bf16 storage (this executor's extension for bf16 weights; the bundle format
+// keeps `seeded` for f32 buffers only).
+__global__ void kvm_seeded_bf16_kernel(uint16_t* out, long long n, unsigned long long seed, int draws, float bias, float coef) {
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+    float acc;
+    if (draws == 1) acc = seeded_u(seed, i);
+    else {
+      unsigned long long j = (unsigned long long)i * 4ull;
+      acc = __fadd_rn(__fadd_rn(seeded_u(seed, j), seeded_u(seed, j + 1)), __fadd_rn(seeded_u(seed, j + 2), seeded_u(seed, j + 3)));
+    }
+    out[i] = f2bf(__fmul_rn(__fsub_rn(acc, bias), coef));
   }
 }
 __global__ void kvm_fill32_kernel(uint32_t* out, long long n, uint32_t v) {
@@ -310,6 +379,7 @@ struct KvmExec {
   int *d_indeg = nullptr, *d_ready = nullptr, *d_state = nullptr, *d_park_next = nullptr, *d_version = nullptr, *d_park_head = nullptr;
   int *d_base = nullptr, *d_roots = nullptr;
   KvmCounters* d_cnt = nullptr; KvmTrace* d_trace = nullptr;
+  KvmQueue* d_queues = nullptr; int *d_qcount = nullptr, *d_done_blk = nullptr;
   KvmDevState S{};
 };
 
@@ -356,7 +426,8 @@ void kvm_destroy(KvmExec* ex) {
   if (ex->stream) hipStreamSynchronize(ex->stream);
   for (auto& b : ex->bufs) hipFree(b.p);
   void* ptrs[] = {ex->d_tasks, ex->d_succ, ex->d_args, ex->d_bufs, ex->d_indeg, ex->d_ready, ex->d_state, ex->d_park_next,
-                  ex->d_version, ex->d_park_head, ex->d_base, ex->d_roots, ex->d_cnt, ex->d_trace};
+                  ex->d_version, ex->d_park_head, ex->d_base, ex->d_roots, ex->d_cnt, ex->d_trace, ex->d_queues, ex->d_qcount,
+                  ex->d_done_blk};
   for (void* q : ptrs) if (q) hipFree(q);
   if (ex->ev0) hipEventDestroy(ex->ev0);
   if (ex->ev1) hipEventDestroy(ex->ev1);
@@ -390,8 +461,11 @@ int kvm_add_buffer(KvmExec* ex, int rows, int cols, int dtype, const KvmInit* in
     case KVM_INIT_FILL: launch_fill(ex, b, init->value); break;
     case KVM_INIT_VALUES: HIPCK(hipMemcpyAsync(b.p, init->values, b.bytes, hipMemcpyHostToDevice, ex->stream)); HIPCK(hipStreamSynchronize(ex->stream)); break;
     case KVM_INIT_SEEDED:
-      if (dtype != 0) { hipFree(b.p); ex->err = "seeded init needs an f32 buffer"; return KVM_STATUS_INVALID; }
-      hipLaunchKernelGGL(kvm_seeded_kernel, dim3(4096), dim3(256), 0, ex->stream, (float*)b.p, (long long)rows * cols, init->seed, init->draws, init->bias, init->coef);
+      if (dtype == 1) { hipFree(b.p); ex->err = "seeded init needs an f32 or bf16 buffer"; return KVM_STATUS_INVALID; }
+      if (dtype == 2)
+        hipLaunchKernelGGL(kvm_seeded_bf16_kernel, dim3(8192), dim3(256), 0, ex->stream, (uint16_t*)b.p, (long long)rows * cols, init->seed, init->draws, init->bias, init->coef);
+      else
+        hipLaunchKernelGGL(kvm_seeded_kernel, dim3(8192), dim3(256), 0, ex->stream, (float*)b.p, (long long)rows * cols, init->seed, init->draws, init->bias, init->coef);
       break;
     default: hipFree(b.p); ex->err = "unknown init kind"; return KVM_STATUS_INVALID;
   }
@@ -465,12 +539,21 @@ static int do_upload(KvmExec* ex) {
   std::vector<MvmBuf> table(ex->bufs.size());
   for (size_t i = 0; i < table.size(); ++i) table[i] = MvmBuf{ex->bufs[i].p, ex->bufs[i].rows, ex->bufs[i].cols, ex->bufs[i].cols, ex->bufs[i].dtype, {0, 0}};
   HIPCK(upload(&ex->d_tasks, ex->tasks, ex->stream));
-  HIPCK(upload(&ex->d_succ, ex->succ, ex->stream));
+  std::vector<int32_t> succ_dev(ex->succ);
+  for (auto& e : succ_dev) if (ex->tasks[e].indegree == 1 && ex->tasks[e].wait_var < 0) e |= KVM_EDGE_DIRECT;
+  HIPCK(upload(&ex->d_succ, succ_dev, ex->stream));
   HIPCK(upload(&ex->d_args, ex->args, ex->stream));
   HIPCK(upload(&ex->d_bufs, table, ex->stream));
   HIPCK(upload(&ex->d_roots, ex->roots, ex->stream));
   HIPCK(hipMalloc(&ex->d_indeg, n * sizeof(int)));
-  HIPCK(hipMalloc(&ex->d_ready, n * sizeof(int)));
+  const int nq = std::max(1, std::min(KVM_MAX_QUEUES, ex->grid));
+  const int qcap = (n + nq - 1) / nq;
+  std::vector<int> qcount(nq, 0);
+  for (int t = 0; t < n; ++t) ++qcount[t % nq];
+  HIPCK(hipMalloc(&ex->d_ready, (size_t)nq * qcap * sizeof(int)));
+  HIPCK(hipMalloc(&ex->d_queues, nq * sizeof(KvmQueue)));
+  HIPCK(hipMalloc(&ex->d_done_blk, ex->grid * sizeof(int)));
+  HIPCK(upload(&ex->d_qcount, qcount, ex->stream));
   HIPCK(hipMalloc(&ex->d_state, n * sizeof(int)));
   HIPCK(hipMalloc(&ex->d_park_next, n * sizeof(int)));
   HIPCK(hipMalloc(&ex->d_version, nv * sizeof(int)));
@@ -482,7 +565,9 @@ static int do_upload(KvmExec* ex) {
   S.tasks = ex->d_tasks; S.succ = ex->d_succ; S.args = ex->d_args; S.bufs = ex->d_bufs;
   S.indeg = ex->d_indeg; S.ready = ex->d_ready; S.state = ex->d_state; S.park_next = ex->d_park_next;
   S.version = ex->d_version; S.park_head = ex->d_park_head; S.cnt = ex->d_cnt; S.trace = ex->d_trace;
+  S.queues = ex->d_queues; S.qcount = ex->d_qcount; S.done_blk = ex->d_done_blk;
   S.ntasks = n; S.nbufs = (int)ex->bufs.size(); S.nvars = nv; S.trace_on = ex->cfg.trace_on ? 1 : 0;
+  S.nq = nq; S.qcap = qcap; S.grid = ex->grid;
   S.timeout_ticks = ex->cfg.timeout_us * 100ull;   // wall_clock64 runs at 100 MHz on gfx950
   ex->uploaded = true;
   return 0;
@@ -491,8 +576,7 @@ static int do_upload(KvmExec* ex) {
 static int launch_once(KvmExec* ex) {
   KvmDevState& S = ex->S;
   HIPCK(hipMemcpyAsync(ex->d_base, ex->base_versions.data(), ex->base_versions.size() * sizeof(int), hipMemcpyHostToDevice, ex->stream));
-  hipLaunchKernelGGL(kvm_reset_kernel, dim3(std::min(1024, (S.ntasks + 255) / 256 + 1)), dim3(256), 0, ex->stream, S, (const int*)ex->d_base,
-                     (const int*)ex->d_roots, (int)ex->roots.size());
+  hipLaunchKernelGGL(kvm_reset_kernel, dim3(std::min(1024, (S.ntasks + 255) / 256 + 1)), dim3(256), 0, ex->stream, S, (const int*)ex->d_base);
   hipLaunchKernelGGL(kvm_seed_kernel, dim3(1), dim3(64), 0, ex->stream, S, (const int*)ex->d_roots, (int)ex->roots.size());
   hipLaunchKernelGGL(kvm_exec_kernel, dim3(ex->grid), dim3(KVM_THREADS), 0, ex->stream, S);
   HIPCK(hipGetLastError());
@@ -539,12 +623,18 @@ int kvm_finish(KvmExec* ex, KvmResult* res) {
   hipSetDevice(ex->dev);
   HIPCK(hipStreamSynchronize(ex->stream));
   KvmCounters c{};
-  if (ex->d_cnt) HIPCK(hipMemcpy(&c, ex->d_cnt, sizeof c, hipMemcpyDeviceToHost));
+  int done = 0;
+  if (ex->d_cnt) {
+    HIPCK(hipMemcpy(&c, ex->d_cnt, sizeof c, hipMemcpyDeviceToHost));
+    std::vector<int> per(ex->grid);
+    HIPCK(hipMemcpy(per.data(), ex->d_done_blk, ex->grid * sizeof(int), hipMemcpyDeviceToHost));
+    for (int d : per) done += d;
+  }
   float ms = 0.f;
   if (ex->launched) hipEventElapsedTime(&ms, ex->ev0, ex->ev1);
   if (res) {
     res->err_code = c.err_code; res->err_slot = c.err_slot; res->err_a = c.err_a; res->err_b = c.err_b;
-    res->done = c.done; res->admitted = (int)ex->tasks.size(); res->grid = ex->grid; res->kernel_ms = ms;
+    res->done = done; res->admitted = (int)ex->tasks.size(); res->grid = ex->grid; res->kernel_ms = ms;
   }
   if (c.err_code) { ex->err = "device error " + std::to_string(c.err_code) + " at task " + std::to_string(c.err_slot); return KVM_STATUS_DEVICE_ERROR; }
   return 0;

@@ -11,7 +11,7 @@ constexpr int ATTN_ROWS = 128;
 constexpr int ATTN_KT = 32;     // keys (or queries) staged per LDS slab
 
 // Stages rows [r0, r0+n) of column block [c0, c0+hd) of X into LDS as fp32 [n][hd+1] (zero rows past `valid`).
-__device__ __forceinline__ void stage_rows(float* dst, const View& X, long long r0, int n, int valid, int c0, int hd) {
+__device__ __forceinline__ void stage_rows(LDS float* dst, const View& X, long long r0, int n, int valid, int c0, int hd) {
   for (int e = tid(); e < n * hd; e += KVM_THREADS) {
     int r = e / hd, k = e % hd;
     dst[r * (hd + 1) + k] = r < valid ? X.at(r0 + r, c0 + k) : 0.f;
@@ -25,7 +25,7 @@ __device__ void op_attn_fwd(const Ctx& c) {
   int bb = c.i(5), h = c.i(6), q0 = c.i(7), T = c.i(8), H = c.i(9), Hkv = c.i(10), hd = c.i(11); float sc = c.f(12);
   int kvh = h / (H / Hkv), half = hd / 2, row = tid() >> 1, part = tid() & 1;
   int gq = q0 + row; bool active = gq < T;
-  float* Ks = (float*)c.smem; float* Vs = Ks + ATTN_KT * (hd + 1);
+  LDS float* Ks = (LDS float*)c.smem; LDS float* Vs = Ks + ATTN_KT * (hd + 1);
   float qr[64], acc[64];
   for (int i = 0; i < half; ++i) { qr[i] = active ? q.at((long long)bb * T + gq, h * hd + part * half + i) : 0.f; acc[i] = 0.f; }
   float m = -INFINITY, l = 0.f;
@@ -71,7 +71,7 @@ __device__ void op_attn_bwd_dq(const Ctx& c) {
   int bb = c.i(7), h = c.i(8), q0 = c.i(9), T = c.i(10), H = c.i(11), Hkv = c.i(12), hd = c.i(13); float sc = c.f(14);
   int kvh = h / (H / Hkv), half = hd / 2, row = tid() >> 1, part = tid() & 1;
   int gq = q0 + row; bool active = gq < T;
-  float* Ks = (float*)c.smem; float* Vs = Ks + ATTN_KT * (hd + 1);
+  LDS float* Ks = (LDS float*)c.smem; LDS float* Vs = Ks + ATTN_KT * (hd + 1);
   float qr[64], dr[64], acc[64];
   long long qrow = (long long)bb * T + gq;
   for (int i = 0; i < half; ++i) {
@@ -105,7 +105,7 @@ __device__ void op_attn_bwd_dkv(const Ctx& c) {
   int bb = c.i(8), kvh = c.i(9), k0 = c.i(10), T = c.i(11), H = c.i(12), hd = c.i(13); float sc = c.f(14);
   int G = H / (k.cols / hd), half = hd / 2, row = tid() >> 1, part = tid() & 1;
   int gk = k0 + row; bool active = gk < T;
-  float* Qs = (float*)c.smem; float* Ds = Qs + ATTN_KT * (hd + 1); float* Ls = Ds + ATTN_KT * (hd + 1); float* Es = Ls + ATTN_KT;
+  LDS float* Qs = (LDS float*)c.smem; LDS float* Ds = Qs + ATTN_KT * (hd + 1); LDS float* Ls = Ds + ATTN_KT * (hd + 1); LDS float* Es = Ls + ATTN_KT;
   long long krow = (long long)bb * T + gk;
   float kr[64], vr[64], sk[64], sv[64];
   for (int i = 0; i < half; ++i) {
@@ -147,7 +147,7 @@ __device__ void op_attn_decode(const Ctx& c) {
   int n = lens.i()[bb] + 1;
   if (n < 1 || n > Tmax) { if (tid() == 0) c.fail(KVM_ERR_OP_KVLEN, bb, n - 1); return; }
   long long base = ((long long)bb * Hkv + h / (H / Hkv)) * Tmax;
-  float* qs = (float*)c.smem; float* s = qs + 128; float* red = s + n;
+  LDS float* qs = (LDS float*)c.smem; LDS float* s = qs + 128; LDS float* red = s + n;
   for (int k = tid(); k < hd; k += KVM_THREADS) qs[k] = q.at(bb, h * hd + k);
   __syncthreads();
   float mx = -INFINITY;
@@ -165,8 +165,10 @@ __device__ void op_attn_decode(const Ctx& c) {
 constexpr float ATTN_EMPTY_M = -3.4028234663852886e38f;
 
 // Split-context decode attention (registry op 135): one task = (sequence b, kv head, split s) for the whole GQA group,
-// so each K/V row of the split is read once for G query heads. Optional fused RoPE of q and the new key, and the
-// KV append of the new token by the split that holds it (flags 1, 3).
+// so each K/V row of the split is read once for G query heads. Keys go through LDS in chunks of 64 (16-byte loads,
+// all issued before use), with an online softmax across chunks. Optional fused RoPE of q and the new key, and the KV
+// append of the new token by the split that holds it (flags 1, 3).
+constexpr int DEC_KC = 64;
 __device__ void op_attn_decode_part(const Ctx& c) {
   View q = c.buf(0), kc = c.buf(1), vc = c.buf(2), lens = c.buf(3), part = c.buf(4), kn = c.buf(5), vn = c.buf(6);
   int bb = c.i(7), kvh = c.i(8), s = c.i(9), S = c.i(10), H = c.i(11), Hkv = c.i(12), hd = c.i(13), Tmax = c.i(14);
@@ -174,13 +176,15 @@ __device__ void op_attn_decode_part(const Ctx& c) {
   int L = lens.i()[bb], n = L + 1;
   if (L < 0 || n > Tmax) { if (tid() == 0) c.fail(KVM_ERR_OP_KVLEN, bb, L); return; }
   int chunk = (n + S - 1) / S, j0 = s * chunk, j1 = min(n, j0 + chunk), nk = max(0, j1 - j0);
-  int G = H / Hkv, half = hd / 2;
+  const int G = H / Hkv, half = hd / 2, HS = hd + 1;
   long long base = ((long long)bb * Hkv + kvh) * Tmax;
-  if ((8 * 128 + G * max(nk, 1) + 16) * 4 > KVM_LDS_BYTES) { if (tid() == 0) c.fail(KVM_ERR_OP_SHAPE, G, nk); return; }
-  float* qs = (float*)c.smem;             // [G][hd]
-  float* sc_ = qs + 8 * 128;              // [G][chunk] scores -> probabilities
-  float* red = sc_ + G * max(nk, 1);      // [G][2*KVM_WAVES]
+  LDS float* qs = (LDS float*)c.smem;          // [G][hd]
+  LDS float* Ks = qs + 8 * 128;                // [DEC_KC][hd+1]
+  LDS float* Vs = Ks + DEC_KC * 129;           // [DEC_KC][hd+1]
+  LDS float* P = Vs + DEC_KC * 129;            // [G][DEC_KC]
+  LDS float* st = P + 8 * DEC_KC;              // m_run[8], l_run[8], f[8]
   for (int e = tid(); e < G * hd; e += KVM_THREADS) qs[e] = q.at(bb, (kvh * G + e / hd) * hd + e % hd);
+  if (tid() < 8) { st[tid()] = -INFINITY; st[8 + tid()] = 0.f; st[16 + tid()] = 1.f; }
   __syncthreads();
   if (fl & 1) {
     for (int e = tid(); e < G * half; e += KVM_THREADS) {
@@ -207,92 +211,114 @@ __device__ void op_attn_decode_part(const Ctx& c) {
     }
     return;
   }
-  // scores: one thread per key, all G heads; K row read once as 16-byte vectors when bf16
-  for (int j = tid(); j < nk; j += KVM_THREADS) {
-    float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    long long kb = (base + j0 + j) * kc.cols;
-    if (kc.dtype == 2) {
-      for (int k = 0; k < hd; k += 8) {
-        u16x8_t w = *(const u16x8_t*)(kc.h() + kb + k);
-        for (int i = 0; i < 8; ++i) { float kv = bf2f(w[i]); for (int g = 0; g < G; ++g) a[g] += qs[g * hd + k + i] * kv; }
+  // outputs (g, k) owned by this thread: e = tid, tid + 256, ... over G*hd
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const int nvec = hd / 8;
+  for (int c0 = 0; c0 < nk; c0 += DEC_KC) {
+    const int cn = min(DEC_KC, nk - c0);
+    __syncthreads();
+    // stage K and V rows [j0+c0, j0+c0+cn): 16-byte loads, all issued before they are converted into LDS
+    if (kc.dtype == 2 && vc.dtype == 2) {
+      u16x8_t kv[4], vv[4]; int idx[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        idx[u] = tid() + u * KVM_THREADS;
+        int j = idx[u] / nvec, v8 = idx[u] % nvec;
+        if (idx[u] < cn * nvec) {
+          kv[u] = *(const GLOBAL u16x8_t*)(kc.h() + (base + j0 + c0 + j) * kc.cols + v8 * 8);
+          vv[u] = *(const GLOBAL u16x8_t*)(vc.h() + (base + j0 + c0 + j) * vc.cols + v8 * 8);
+        }
       }
-    } else for (int k = 0; k < hd; ++k) { float kv = kc.f()[kb + k]; for (int g = 0; g < G; ++g) a[g] += qs[g * hd + k] * kv; }
-    for (int g = 0; g < G; ++g) sc_[g * nk + j] = a[g] * sc;
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (idx[u] >= cn * nvec) continue;
+        int j = idx[u] / nvec, v8 = idx[u] % nvec;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { Ks[j * HS + v8 * 8 + i] = bf2f(kv[u][i]); Vs[j * HS + v8 * 8 + i] = bf2f(vv[u][i]); }
+      }
+      for (int e = 4 * KVM_THREADS + tid(); e < cn * nvec; e += KVM_THREADS) {   // hd*DEC_KC beyond 4 vectors/thread
+        int j = e / nvec, v8 = e % nvec;
+        u16x8_t a = *(const GLOBAL u16x8_t*)(kc.h() + (base + j0 + c0 + j) * kc.cols + v8 * 8);
+        u16x8_t b2 = *(const GLOBAL u16x8_t*)(vc.h() + (base + j0 + c0 + j) * vc.cols + v8 * 8);
+        for (int i = 0; i < 8; ++i) { Ks[j * HS + v8 * 8 + i] = bf2f(a[i]); Vs[j * HS + v8 * 8 + i] = bf2f(b2[i]); }
+      }
+    } else {
+      for (int e = tid(); e < cn * hd; e += KVM_THREADS) {
+        int j = e / hd, k = e % hd;
+        Ks[j * HS + k] = kc.ld((base + j0 + c0 + j) * kc.cols + k); Vs[j * HS + k] = vc.ld((base + j0 + c0 + j) * vc.cols + k);
+      }
+    }
+    __syncthreads();
+    for (int e = tid(); e < G * DEC_KC; e += KVM_THREADS) {     // scores of this chunk
+      int g = e / DEC_KC, j = e % DEC_KC; float a = -INFINITY;
+      if (j < cn) { a = 0.f; for (int k = 0; k < hd; ++k) a += qs[g * hd + k] * Ks[j * HS + k]; a *= sc; }
+      P[g * DEC_KC + j] = a;
+    }
+    __syncthreads();
+    for (int g = wave(); g < G; g += KVM_WAVES) {                 // online softmax update per head
+      float v = lane() < DEC_KC ? P[g * DEC_KC + lane()] : -INFINITY;
+      float cm = wave_max(v), mo = st[g], mn = fmaxf(mo, cm);
+      float p = lane() < cn ? __expf(v - mn) : 0.f;
+      if (lane() < DEC_KC) P[g * DEC_KC + lane()] = p;
+      float ps = wave_sum(p);
+      if (lane() == 0) { float f = __expf(mo - mn); st[16 + g] = f; st[8 + g] = st[8 + g] * f + ps; st[g] = mn; }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      int e = tid() + u * KVM_THREADS;
+      if (e >= G * hd) break;
+      int g = e / hd, k = e % hd; float a = acc[u] * st[16 + g];
+      for (int j = 0; j < cn; ++j) a += P[g * DEC_KC + j] * Vs[j * HS + k];
+      acc[u] = a;
+    }
   }
-  __syncthreads();
-  // per-head max and sum: wave w reduces heads w, w+4
-  for (int g = wave(); g < G; g += KVM_WAVES) {
-    float m = -INFINITY; for (int j = lane(); j < nk; j += 64) m = fmaxf(m, sc_[g * nk + j]);
-    m = wave_max(m);
-    float l = 0.f; for (int j = lane(); j < nk; j += 64) { float p = __expf(sc_[g * nk + j] - m); sc_[g * nk + j] = p; l += p; }
-    l = wave_sum(l);
-    if (lane() == 0) { red[g * 2] = m; red[g * 2 + 1] = l; }
-  }
-  __syncthreads();
-  for (int e = tid(); e < G * hd; e += KVM_THREADS) {
-    int g = e / hd, k = e % hd; float a = 0.f;
-    for (int j = 0; j < nk; ++j) a += sc_[g * nk + j] * vc.ld((base + j0 + j) * vc.cols + k);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    int e = tid() + u * KVM_THREADS;
+    if (e >= G * hd) break;
+    int g = e / hd, k = e % hd;
     long long r = (((long long)bb * S + s) * H + kvh * G + g) * part.cols;
-    part.f()[r + k] = a;
-    if (k == 0) { part.f()[r + hd] = red[g * 2]; part.f()[r + hd + 1] = red[g * 2 + 1]; }
+    part.f()[r + k] = acc[u];
+    if (k == 0) { part.f()[r + hd] = st[g]; part.f()[r + hd + 1] = st[8 + g]; }
   }
 }
+// Merge of the splits (registry op 136): per head, the split weights e_s = exp(m_s - max m) (live splits only) are
+// computed once into LDS, then each output element is one pass over the splits.
 __device__ void op_attn_decode_merge(const Ctx& c) {
   View part = c.buf(0), o = c.buf(1); int bb = c.i(2), h0 = c.i(3), h1 = c.i(4), S = c.i(5), H = c.i(6), hd = c.i(7);
-  for (int e = tid(); e < (h1 - h0) * hd; e += KVM_THREADS) {
-    int h = h0 + e / hd, k = e % hd;
+  LDS float* w = (LDS float*)c.smem;      // [h1-h0][S] split weights, then [h1-h0] 1/denominator
+  LDS float* inv = w + (h1 - h0) * S;
+  for (int h = h0 + wave(); h < h1; h += KVM_WAVES) {
     float M = -INFINITY;
-    for (int s = 0; s < S; ++s) { long long r = (((long long)bb * S + s) * H + h) * part.cols; if (part.f()[r + hd + 1] > 0.f) M = fmaxf(M, part.f()[r + hd]); }
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < S; ++s) {
+    for (int s = lane(); s < S; s += 64) { long long r = (((long long)bb * S + s) * H + h) * part.cols; if (part.f()[r + hd + 1] > 0.f) M = fmaxf(M, part.f()[r + hd]); }
+    M = wave_max(M);
+    float den = 0.f;
+    for (int s = lane(); s < S; s += 64) {
       long long r = (((long long)bb * S + s) * H + h) * part.cols;
-      float l = part.f()[r + hd + 1];
-      if (l > 0.f) { float w = __expf(part.f()[r + hd] - M); num += w * part.f()[r + k]; den += w * l; }
+      float l = part.f()[r + hd + 1], e = l > 0.f ? __expf(part.f()[r + hd] - M) : 0.f;
+      w[(h - h0) * S + s] = e; den += e * l;
     }
-    o.st((long long)bb * o.cols + h * hd + k, num / den);
+    den = wave_sum(den);
+    if (lane() == 0) inv[h - h0] = 1.f / den;
   }
-}
-
-// Decode GEMV (registry op 134): out[0,n] = sum_k v[k] w[n,k] (+ res) for rows [n0,n1) of a bf16 [N,K] weight, with
-// v = bf16(prologue(x)) staged in LDS. One wave streams one weight row at a time with 16-byte loads, several
-// loads in flight per lane; fp32 sums in a fixed order (lane partials, then the wave tree).
-__device__ void op_gemv_bf16(const Ctx& c) {
-  View x = c.buf(0), x2 = c.buf(1), g = c.buf(2), w = c.buf(3), out = c.buf(4), res = c.buf(5);
-  int n0 = c.i(6), n1 = c.i(7), K = c.i(8), pro = c.i(9); float eps = c.f(10);
-  float* vs = (float*)c.smem; float* red = vs + K;
-  if (pro == 1) {
-    float ss = 0.f; for (int k = tid(); k < K; k += KVM_THREADS) { float a = x.ld(k); ss += a * a; }
-    ss = block_sum(ss, red);
-    float rs = 1.f / sqrtf(ss / (float)K + eps);
-    for (int k = tid(); k < K; k += KVM_THREADS) vs[k] = round_bf(x.ld(k) * rs * g.f()[k]);
-  } else if (pro == 2) {
-    for (int k = tid(); k < K; k += KVM_THREADS) vs[k] = round_bf(silu_f(x.ld(k)) * x2.ld(k));
-  } else for (int k = tid(); k < K; k += KVM_THREADS) vs[k] = round_bf(x.ld(k));
   __syncthreads();
-  const int l = lane();
-  for (int n = n0 + wave(); n < n1; n += KVM_WAVES) {
-    const u16x8_t* wr = (const u16x8_t*)(w.h() + (long long)n * w.cols);
-    float a = 0.f;
-    int nv = K / 8;
-    int q = l;
-    for (; q + 192 < nv; q += 256) {         // four 16-byte loads in flight per lane
-      u16x8_t w0 = wr[q], w1 = wr[q + 64], w2 = wr[q + 128], w3 = wr[q + 192];
+  for (int e = tid(); e < (h1 - h0) * hd; e += KVM_THREADS) {
+    int hh = e / hd, k = e % hd; float num = 0.f;
+    const GLOBAL float* src = part.f() + (((long long)bb * S) * H + h0 + hh) * part.cols + k;
+    const long long step = (long long)H * part.cols;
+    int s = 0;
+    for (; s + 8 <= S; s += 8) {                 // eight independent loads in flight
+      float v[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a += bf2f(w0[i]) * vs[q * 8 + i];
+      for (int i = 0; i < 8; ++i) v[i] = src[(s + i) * step];
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a += bf2f(w1[i]) * vs[(q + 64) * 8 + i];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) a += bf2f(w2[i]) * vs[(q + 128) * 8 + i];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) a += bf2f(w3[i]) * vs[(q + 192) * 8 + i];
+      for (int i = 0; i < 8; ++i) num += w[hh * S + s + i] * v[i];
     }
-    for (; q < nv; q += 64) {
-      u16x8_t w0 = wr[q];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) a += bf2f(w0[i]) * vs[q * 8 + i];
-    }
-    a = wave_sum(a);
-    if (l == 0) out.st(n, a + (res.ok() ? res.ld(n) : 0.f));
+    for (; s < S; ++s) num += w[hh * S + s] * src[s * step];
+    o.st((long long)bb * o.cols + (h0 + hh) * hd + k, num * inv[hh]);
   }
 }
 

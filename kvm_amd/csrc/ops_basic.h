@@ -340,15 +340,22 @@ __device__ void adamw_body(const Ctx& c, View p, View g, View m, View v, View gs
   float bc1 = 1.f - (float)pow((double)b1, (double)t), bc2 = 1.f - (float)pow((double)b2, (double)t);
   long long a0 = ((long long)e0 + 3) & ~3ll, a1 = (long long)e1 & ~3ll;
   if (a0 > a1) { a0 = e1; a1 = e1; }
-  for (long long i = e0 + tid(); i < a0; i += KVM_THREADS) adamw_elem(p.f()[i], g.f()[i], m.f()[i], v.f()[i], gsc, b1, b2, lr, eps, wd, bc1, bc2);
-  for (long long i = a1 + tid(); i < e1; i += KVM_THREADS) adamw_elem(p.f()[i], g.f()[i], m.f()[i], v.f()[i], gsc, b1, b2, lr, eps, wd, bc1, bc2);
-  float4* P = (float4*)p.f(); const float4* G = (const float4*)g.f(); float4* M = (float4*)m.f(); float4* Vv = (float4*)v.f();
+  auto one = [&](long long i) {
+    float pp = p.f()[i], mm = m.f()[i], vv = v.f()[i];
+    adamw_elem(pp, g.f()[i], mm, vv, gsc, b1, b2, lr, eps, wd, bc1, bc2);
+    p.f()[i] = pp; m.f()[i] = mm; v.f()[i] = vv;
+  };
+  for (long long i = e0 + tid(); i < a0; i += KVM_THREADS) one(i);
+  for (long long i = a1 + tid(); i < e1; i += KVM_THREADS) one(i);
+  GLOBAL f32x4n* P = (GLOBAL f32x4n*)p.f(); const GLOBAL f32x4n* G = (const GLOBAL f32x4n*)g.f(); GLOBAL f32x4n* M = (GLOBAL f32x4n*)m.f(); GLOBAL f32x4n* Vv = (GLOBAL f32x4n*)v.f();
   for (long long q = a0 / 4 + tid(); q < a1 / 4; q += KVM_THREADS) {
-    float4 pp = P[q], gg = G[q], mm = M[q], vv = Vv[q];
-    adamw_elem(pp.x, gg.x, mm.x, vv.x, gsc, b1, b2, lr, eps, wd, bc1, bc2);
-    adamw_elem(pp.y, gg.y, mm.y, vv.y, gsc, b1, b2, lr, eps, wd, bc1, bc2);
-    adamw_elem(pp.z, gg.z, mm.z, vv.z, gsc, b1, b2, lr, eps, wd, bc1, bc2);
-    adamw_elem(pp.w, gg.w, mm.w, vv.w, gsc, b1, b2, lr, eps, wd, bc1, bc2);
+    f32x4n pp = P[q], gg = G[q], mm = M[q], vv = Vv[q];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float a = pp[j], b = mm[j], d = vv[j];
+      adamw_elem(a, gg[j], b, d, gsc, b1, b2, lr, eps, wd, bc1, bc2);
+      pp[j] = a; mm[j] = b; vv[j] = d;
+    }
     P[q] = pp; M[q] = mm; Vv[q] = vv;
   }
 }
@@ -383,7 +390,7 @@ __device__ void op_lr_schedule(const Ctx& c) {
 // ---------------------------------------------------------------------------------------------- token selection
 __device__ __forceinline__ uint32_t order_key(float x) { uint32_t b = __float_as_uint(x); return b ^ ((b >> 31) ? 0xFFFFFFFFu : 0x80000000u); }
 // Row argmax: largest value, lowest index on ties; NaN never wins (all-NaN row -> 0).
-__device__ int row_argmax(const View& lg, int r, int V, float* redv, int* redi) {
+template <class PF, class PI> __device__ int row_argmax(const View& lg, int r, int V, PF redv, PI redi) {
   float bv = -INFINITY; int bi = 0x7FFFFFFF;
   for (int j = tid(); j < V; j += KVM_THREADS) { float x = lg.at(r, j); if (x > bv || (x == bv && j < bi)) { bv = x; bi = j; } }
   for (int o = 32; o > 0; o >>= 1) {

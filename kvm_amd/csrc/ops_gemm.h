@@ -36,9 +36,9 @@ struct Epi {
 // 64x64 output block, 256 threads x (4x4) outputs, K in slabs of 16 through LDS. Operand access handles both
 // storage orders; accumulation is fp32 FMA in increasing k.
 __device__ void f32_block(const Ctx& c, View A, View B, int ta, int tb, int m0, int n0, int M, int N, int K, const Epi& e, bool bf16ops,
-                          float* out_tile /* optional: write raw alpha*acc here [64*64] instead of the epilogue */) {
-  float* As = (float*)c.smem;            // [16][65]
-  float* Bs = As + 16 * 65;              // [16][65]
+                          LDS float* out_tile /* optional: write raw alpha*acc here [64*64] instead of the epilogue */) {
+  LDS float* As = (LDS float*)c.smem;    // [16][65]
+  LDS float* Bs = As + 16 * 65;          // [16][65]
   int tx = tid() % 16, ty = tid() / 16;  // thread owns rows ty*4.., cols tx*4..
   float acc[4][4] = {};
   for (int k0 = 0; k0 < K; k0 += 16) {
@@ -86,7 +86,7 @@ __device__ void op_matmul_tile_silu_mul(const Ctx& c) {
   View A = c.buf(0), B = c.buf(1), out = c.buf(2), gate = c.buf(3), up = c.buf(4);
   int m0 = c.i(5), n0 = c.i(6), M = c.i(7), N = c.i(8), K = c.i(9), fl = c.i(10);
   Epi e{}; e.alpha = c.f(11);
-  float* t = (float*)(c.smem + 32 * 1024);
+  LDS float* t = (LDS float*)(c.smem + 32 * 1024);
   for (int dm = 0; dm < tile_m(fl); dm += 64) for (int dn = 0; dn < tile_n(fl); dn += 64) {
     int bm = m0 + dm, bn = n0 + dn;
     if (bm >= M || bn >= N) continue;
@@ -102,7 +102,7 @@ __device__ void op_matmul_tile_silu_mul_bwd(const Ctx& c) {
   View A = c.buf(0), B = c.buf(1), gate = c.buf(2), up = c.buf(3), dg = c.buf(4), du = c.buf(5);
   int m0 = c.i(6), n0 = c.i(7), M = c.i(8), N = c.i(9), K = c.i(10), fl = c.i(11);
   Epi e{}; e.alpha = c.f(12);
-  float* t = (float*)(c.smem + 32 * 1024);
+  LDS float* t = (LDS float*)(c.smem + 32 * 1024);
   for (int dm = 0; dm < tile_m(fl); dm += 64) for (int dn = 0; dn < tile_n(fl); dn += 64) {
     int bm = m0 + dm, bn = n0 + dn;
     if (bm >= M || bn >= N) continue;
@@ -124,9 +124,9 @@ __device__ void op_matmul_tile_silu_mul_bwd(const Ctx& c) {
 __device__ __forceinline__ u16x8_t load8(const View& X, long long base, int valid) {
   u16x8_t r;
   if (valid >= 8 && (base & 7) == 0) {
-    if (X.dtype == 2) return *(const u16x8_t*)(X.h() + base);
-    const float4* p = (const float4*)(X.f() + base);
-    float4 a = p[0], b = p[1];
+    if (X.dtype == 2) return *(const GLOBAL u16x8_t*)(X.h() + base);
+    const GLOBAL f32x4n* p = (const GLOBAL f32x4n*)(X.f() + base);
+    f32x4n a = p[0], b = p[1];
     r[0] = f2bf(a.x); r[1] = f2bf(a.y); r[2] = f2bf(a.z); r[3] = f2bf(a.w);
     r[4] = f2bf(b.x); r[5] = f2bf(b.y); r[6] = f2bf(b.z); r[7] = f2bf(b.w);
     return r;
@@ -159,14 +159,14 @@ template <int R, int KT> struct Stage {
       }
     }
   }
-  __device__ void store(uint16_t* lds, int trans) const {
+  __device__ void store(LDS uint16_t* lds, int trans) const {
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       int idx = tid() + q * KVM_THREADS;
       if (idx >= VEC) break;
       if (!trans) {
         int row = idx / (KT / 8), kv = idx % (KT / 8);
-        *(u16x8_t*)(lds + row * STRIDE + kv * 8) = v[q];
+        *(LDS u16x8_t*)(lds + row * STRIDE + kv * 8) = v[q];
       } else {
         int k = idx / (R / 8), rv = idx % (R / 8);
 #pragma unroll
@@ -182,8 +182,8 @@ template <int TM, int TN> __device__ void mfma_tile(const Ctx& c, View A, View B
   constexpr int KT = 32, WM = TM / 2, WN = TN / 2, BM = WM / 32, BN = WN / 32;
   typedef Stage<TM, KT> SA;
   typedef Stage<TN, KT> SB;
-  uint16_t* lA[2] = {(uint16_t*)c.smem, (uint16_t*)c.smem + TM * SA::STRIDE};
-  uint16_t* lB[2] = {lA[1] + TM * SA::STRIDE, lA[1] + TM * SA::STRIDE + TN * SB::STRIDE};
+  LDS uint16_t* lA[2] = {(LDS uint16_t*)c.smem, (LDS uint16_t*)c.smem + TM * SA::STRIDE};
+  LDS uint16_t* lB[2] = {lA[1] + TM * SA::STRIDE, lA[1] + TM * SA::STRIDE + TN * SB::STRIDE};
   const int wm0 = (wave() >> 1) * WM, wn0 = (wave() & 1) * WN, l = lane();
   f32x16 acc[BM][BN];
 #pragma unroll
@@ -200,13 +200,14 @@ template <int TM, int TN> __device__ void mfma_tile(const Ctx& c, View A, View B
   for (int k0 = 0; k0 < K; k0 += KT) {
     bool more = k0 + KT < K;
     if (more) { sa.fetch(A, ta, m0, M, k0 + KT, K); sb.fetch(B, !tb, n0, N, k0 + KT, K); }
+    __builtin_amdgcn_sched_barrier(0);     // the next slab's loads are in flight during this slab's MFMAs
 #pragma unroll
     for (int kk = 0; kk < KT; kk += 16) {
       bf16x8 af[BM], bfr[BN];
 #pragma unroll
-      for (int i = 0; i < BM; ++i) af[i] = *(const bf16x8*)(lA[buf] + (wm0 + i * 32 + (l & 31)) * SA::STRIDE + kk + (l >> 5) * 8);
+      for (int i = 0; i < BM; ++i) af[i] = *(const LDS bf16x8*)(lA[buf] + (wm0 + i * 32 + (l & 31)) * SA::STRIDE + kk + (l >> 5) * 8);
 #pragma unroll
-      for (int j = 0; j < BN; ++j) bfr[j] = *(const bf16x8*)(lB[buf] + (wn0 + j * 32 + (l & 31)) * SB::STRIDE + kk + (l >> 5) * 8);
+      for (int j = 0; j < BN; ++j) bfr[j] = *(const LDS bf16x8*)(lB[buf] + (wn0 + j * 32 + (l & 31)) * SB::STRIDE + kk + (l >> 5) * 8);
 #pragma unroll
       for (int i = 0; i < BM; ++i)
 #pragma unroll

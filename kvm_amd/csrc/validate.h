@@ -39,7 +39,7 @@ static const OpSig* find_op(int id) { for (const OpSig& o : kRegistry) if (o.id 
 static bool implemented(int id) {
   static const int ids[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 32, 33, 34, 35, 36, 37, 38, 39, 40, 41, 42, 43, 44, 45, 46, 47, 48, 49, 50,
                             51, 52, 53, 54, 55, 56, 57, 58, 59, 60, 61, 62, 63, 96, 97, 98, 99, 100, 101, 102, 103, 104, 113, 114, 115,
-                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300};
+                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301};
   for (int i : ids) if (i == id) return true;
   return false;
 }
@@ -101,6 +101,7 @@ static char arg_class(int op, const std::string& n) {
     case 135: return in({"lens"}) ? 'i' : in({"part"}) ? 'f' : 'a';
     case 136: return in({"o"}) ? 'a' : 'f';
     case 300: return in({"x", "out"}) ? 'a' : 'f';
+    case 301: return in({"gamma"}) ? 'f' : 'a';
     default: return 'f';
   }
 }
@@ -218,7 +219,7 @@ static void extents(int op, Check& k) {
       for (const char* n : {"out", "gate", "up", "dgate", "dup"}) if (k.idx(n) >= 0) k.ext(n, M, N); break; }
     case 134: { int n0 = k.I("n0"), n1 = k.I("n1"), K = k.I("K"), pro = k.I("pro");
       k.need(0 <= n0 && n0 < n1 && K > 0 && K % 8 == 0 && pro >= 0 && pro <= 2, "bad range, K or pro");
-      k.need((K + 64) * 4 <= 128 * 1024, "K too large for one task's LDS");
+      k.need((2 * K + 64) * 4 <= 128 * 1024, "K too large for one task's LDS");
       k.extn("x", K); k.extn("x2", K); k.extn("gamma", K); k.ext("w", n1, K); k.ext("out", 1, n1); k.ext("res", 1, n1);
       if (pro == 1) k.need(k.B("gamma") != nullptr, "pro 1 needs gamma");
       if (pro == 2) k.need(k.B("x2") != nullptr, "pro 2 needs x2");
@@ -235,7 +236,15 @@ static void extents(int op, Check& k) {
       break; }
     case 136: { int b = k.I("b"), h0 = k.I("h0"), h1 = k.I("h1"), S = k.I("S"), H = k.I("H"), hd = k.I("hd");
       k.need(b >= 0 && 0 <= h0 && h0 < h1 && h1 <= H && S > 0 && hd > 0, "bad b/h0/h1/S/H/hd");
+      k.need((long long)(h1 - h0) * (S + 1) * 4 <= 128 * 1024, "(h1-h0)*(S+1) too large for one task's LDS");
       long long n = b + 1; k.ext("part", n * S * H, hd + 2); k.ext("o", n, (long long)H * hd); break; }
+    case 301: { int n0 = k.I("n0"), n1 = k.I("n1"), K = k.I("K"), M = k.I("M"), pro = k.I("pro");
+      k.need(0 <= n0 && n0 < n1 && K > 0 && K % 64 == 0 && 1 <= M && M <= 16 && pro >= 0 && pro <= 2, "bad range, K (% 64), M (1..16) or pro");
+      k.ext("x", M, K); k.ext("x2", M, K); k.extn("gamma", K); k.ext("w", n1, K); k.ext("out", M, n1); k.ext("res", M, n1);
+      if (pro == 1) k.need(k.B("gamma") != nullptr, "pro 1 needs gamma");
+      if (pro == 2) k.need(k.B("x2") != nullptr, "pro 2 needs x2");
+      const MvmBuf* w = k.B("w"); if (w) k.need(w->dtype == 2 && w->cols % 8 == 0, "w must be bf16 storage with cols % 8 == 0");
+      break; }
     case 300: { int r1 = k.I("r1"), H = k.I("H"), hd = k.I("hd"); k.range(k.I("r0"), r1); k.need(H > 0 && hd > 0, "bad H/hd");
       k.ext("x", r1, (long long)H * hd); k.ext("out", r1, (long long)H * hd); k.extn("gamma", hd); break; }
     default: k.need(false, "no extent rule");

@@ -1,0 +1,161 @@
+"""Qwen3-8B-shape greedy decode step as a task graph (no generator exists in the reference).
+
+One step: embed the previous token -> 36 x [RMSNorm -> q, k, v projections -> per-head q/k RMSNorm -> RoPE + KV append +
+split-context attention (attn_decode_part, flags 1) -> merge -> o projection + residual -> RMSNorm -> gate / up ->
+SwiGLU -> down projection + residual] -> final RMSNorm -> untied LM head -> argmax -> the token buffer; then the cached
+length grows by one. Re-running the graph decodes the next token (the token buffer and lens carry over).
+
+Batch 1 uses the registry's one-row decode GEMV (gemv_bf16, RMSNorm / SwiGLU prologues fused) exactly as the
+reference's serving passes lay it out (reference: frontend/mvmfe/serve.py:243-315). Batch > 1 uses this executor's
+gemv_bf16_rows (op 301): the weights are streamed once for all sequences, with RMSNorm / SwiGLU as separate small
+tasks writing bf16 activations.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, asdict
+
+from . import Builder, Workload, split
+
+
+@dataclass
+class Qwen3Config:
+    layers: int = 36
+    hidden: int = 4096
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    ffn: int = 12288
+    vocab: int = 151936
+    ctx: int = 4096            # tokens already in the KV cache
+    batch: int = 1
+    max_new: int = 64          # cache room for this many decode steps
+    theta: float = 1e6
+    eps: float = 1e-6
+    seed: int = 1234
+    splits: int = 0            # attention splits per (sequence, kv head); 0 = auto (256 part tasks)
+    tasks_per_phase: int = 256
+
+    @staticmethod
+    def tiny(batch=1, **kw):
+        return Qwen3Config(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000, ctx=37, batch=batch,
+                           max_new=4, tasks_per_phase=16, **kw)
+
+
+def weight_elems(c: Qwen3Config) -> int:
+    D, hd = c.hidden, c.head_dim
+    per_layer = (c.heads * hd) * D + 2 * (c.kv_heads * hd) * D + D * (c.heads * hd) + 3 * c.ffn * D
+    return c.layers * per_layer + c.vocab * D
+
+
+def build(c: Qwen3Config) -> Workload:
+    b = Builder(c.seed)
+    B, D, H, Hkv, hd, F, V = c.batch, c.hidden, c.heads, c.kv_heads, c.head_dim, c.ffn, c.vocab
+    Tmax = c.ctx + c.max_new
+    S = c.splits or max(1, 256 // (B * Hkv))
+    rows_mode = B > 1
+    # ---- buffers
+    b.values('tok', [(7919 * (i + 1)) % V for i in range(B)], B, 1, 'i32')
+    b.values('lens', [c.ctx] * B, B, 1, 'i32')
+    b.normal('wte', V, D, 'f32')
+    b.fill('x', B, D)
+    b.fill('q', B, H * hd)
+    b.fill('k', B, Hkv * hd)
+    b.fill('v', B, Hkv * hd)
+    b.fill('part', B * S * H, hd + 2)
+    b.fill('att', B, H * hd, 'bf16' if rows_mode else 'f32')
+    b.fill('g', B, F)
+    b.fill('u', B, F)
+    if rows_mode:
+        b.fill('xn', B, D, 'bf16')
+        b.fill('h', B, F, 'bf16')
+        b.fill('rstd', B)
+    b.fill('logits', B, V)
+    for l in range(c.layers):
+        b.fill(f'ln1.{l}', D, value=1.0)
+        b.fill(f'ln2.{l}', D, value=1.0)
+        b.fill(f'qn.{l}', hd, value=1.0)
+        b.fill(f'kn.{l}', hd, value=1.0)
+        b.normal(f'wq.{l}', H * hd, D, 'bf16')
+        b.normal(f'wk.{l}', Hkv * hd, D, 'bf16')
+        b.normal(f'wv.{l}', Hkv * hd, D, 'bf16')
+        b.normal(f'wo.{l}', D, H * hd, 'bf16')
+        b.normal(f'wg.{l}', F, D, 'bf16')
+        b.normal(f'wu.{l}', F, D, 'bf16')
+        b.normal(f'wd.{l}', D, F, 'bf16')
+        b.normal(f'kc.{l}', B * Hkv * Tmax, hd, 'bf16', scale=1.0)
+        b.normal(f'vc.{l}', B * Hkv * Tmax, hd, 'bf16', scale=1.0)
+    b.fill('lnf', D, value=1.0)
+    b.normal('whead', V, D, 'bf16')
+
+    def proj(after, x, w, out, N, K, parts, pro=0, gamma=None, x2=None, res=None):
+        """Tasks computing out[:, 0:N] = prologue(x) @ w^T (+ res)."""
+        ts = []
+        if rows_mode:
+            for lo, hi in split(N // 16, max(1, min(parts, N // 16))):
+                ts.append(b.task('gemv_bf16_rows', after=after, x=x, x2=x2, gamma=gamma, w=w, out=out, res=res, n0=16 * lo, n1=16 * hi,
+                                 K=K, M=B, pro=pro, eps=c.eps))
+        else:
+            for lo, hi in split(N, parts):
+                ts.append(b.task('gemv_bf16', after=after, x=x, x2=x2, gamma=gamma, w=w, out=out, res=res, n0=lo, n1=hi, K=K, pro=pro,
+                                 eps=c.eps))
+        return ts
+
+    P = c.tasks_per_phase
+    prev = [b.task('embedding_fwd', ids='tok', wte='wte', wpe=None, out='x', r0=0, r1=B, T=1, d=D)]
+    last_parts = []
+    for l in range(c.layers):
+        nq, nkv = H * hd, Hkv * hd
+        tot = nq + 2 * nkv
+        pq, pk = max(1, round(P * nq / tot)), max(1, round(P * nkv / tot))
+        if rows_mode:
+            prev = [b.task('rmsnorm_fwd', after=prev, x='x', gamma=f'ln1.{l}', out='xn', rstd='rstd', r0=0, r1=B, d=D, eps=c.eps)]
+            tq = proj(prev, 'xn', f'wq.{l}', 'q', nq, D, pq)
+            tk = proj(prev, 'xn', f'wk.{l}', 'k', nkv, D, pk)
+            tv = proj(prev, 'xn', f'wv.{l}', 'v', nkv, D, pk)
+        else:
+            tq = proj(prev, 'x', f'wq.{l}', 'q', nq, D, pq, pro=1, gamma=f'ln1.{l}')
+            tk = proj(prev, 'x', f'wk.{l}', 'k', nkv, D, pk, pro=1, gamma=f'ln1.{l}')
+            tv = proj(prev, 'x', f'wv.{l}', 'v', nkv, D, pk, pro=1, gamma=f'ln1.{l}')
+        hq = b.task('head_rmsnorm', after=tq, x='q', gamma=f'qn.{l}', out='q', r0=0, r1=B, H=H, hd=hd, eps=c.eps)
+        hk = b.task('head_rmsnorm', after=tk, x='k', gamma=f'kn.{l}', out='k', r0=0, r1=B, H=Hkv, hd=hd, eps=c.eps)
+        vj = b.join(tv, 2 * S)
+        parts = []
+        for bb in range(B):
+            pb = [b.task('attn_decode_part', after=[hq, hk, *vj], q='q', kc=f'kc.{l}', vc=f'vc.{l}', lens='lens', part='part', knew='k',
+                         vnew='v', b=bb, kvh=kh, s=s, S=S, H=H, Hkv=Hkv, hd=hd, Tmax=Tmax, scale=1.0 / math.sqrt(hd), theta=c.theta,
+                         flags=1) for kh in range(Hkv) for s in range(S)]
+            parts.append(pb)
+        last_parts = [t for pb in parts for t in pb]
+        merges = []
+        for bb in range(B):
+            nm = max(1, min(H, 4 // B)) if B < 4 else 1
+            for h0, h1 in split(H, nm):
+                merges.append(b.task('attn_decode_merge', after=parts[bb], part='part', o='att', b=bb, h0=h0, h1=h1, S=S, H=H, hd=hd))
+        to = proj(merges, 'att', f'wo.{l}', 'x', D, H * hd, P, res='x')
+        if rows_mode:
+            r2 = [b.task('rmsnorm_fwd', after=to, x='x', gamma=f'ln2.{l}', out='xn', rstd='rstd', r0=0, r1=B, d=D, eps=c.eps)]
+            tg = proj(r2, 'xn', f'wg.{l}', 'g', F, D, P)
+            tu = proj(r2, 'xn', f'wu.{l}', 'u', F, D, P)
+            sm = [b.task('silu_mul_fwd', after=tg + tu, gate='g', up='u', out='h', e0=0, e1=B * F)]
+            td = proj(sm, 'h', f'wd.{l}', 'x', D, F, P, res='x')
+            prev = td if len(td) <= 256 else b.join(td, P)
+        else:
+            oj = b.join(to, 2 * P)
+            tg = proj(oj, 'x', f'wg.{l}', 'g', F, D, P, pro=1, gamma=f'ln2.{l}')
+            tu = proj(oj, 'x', f'wu.{l}', 'u', F, D, P, pro=1, gamma=f'ln2.{l}')
+            gj = b.join(tg + tu, P)
+            td = proj(gj, 'g', f'wd.{l}', 'x', D, F, P, pro=2, x2='u', res='x')
+            prev = b.join(td, P)
+    head_parts = 4 * P
+    if rows_mode:
+        rf = [b.task('rmsnorm_fwd', after=prev, x='x', gamma='lnf', out='xn', rstd='rstd', r0=0, r1=B, d=D, eps=c.eps)]
+        th = proj(rf, 'xn', 'whead', 'logits', V, D, head_parts)
+    else:
+        th = proj(prev, 'x', 'whead', 'logits', V, D, head_parts, pro=1, gamma='lnf')
+    for bb in range(B):
+        b.task('argmax', after=th, logits='logits', out='tok', r0=bb, r1=bb + 1, V=V)
+    b.task('counter_inc', after=last_parts, x='lens', i0=0, i1=B, delta=1)
+    info = {'config': asdict(c), 'weight_bytes': 2 * weight_elems(c),
+            'kv_bytes_per_step': c.layers * 2 * B * Hkv * (c.ctx + 1) * hd * 2, 'splits': S}
+    return Workload(b.spec('decode'), b.init_override, info)

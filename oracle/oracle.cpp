@@ -623,6 +623,25 @@ void op_head_rmsnorm(const Ctx& c) {   // this executor's own op: RMSNorm over e
   }
 }
 
+void op_gemv_bf16_rows(const Ctx& c) {   // this executor's op 301: gemv_bf16 for M rows sharing one weight stream
+  V x = c.buf(0), x2 = c.buf(1, true), g = c.buf(2, true), w = c.buf(3), out = c.buf(4), res = c.buf(5, true);
+  int n0 = c.i(6), n1 = c.i(7), K = c.i(8), M = c.i(9), pro = c.i(10); float eps = c.fl(11);
+  need(0 <= n0 && n0 < n1 && K > 0 && K % 64 == 0 && M >= 1 && M <= 16 && pro >= 0 && pro <= 2, "gemv_bf16_rows: bad args");
+  std::vector<double> v(K);
+  for (int m = 0; m < M; ++m) {
+    if (pro == 1) {
+      double ss = 0; for (int k = 0; k < K; ++k) ss += x.at(m, k) * x.at(m, k);
+      float rs = f32(1.0 / std::sqrt(ss / K + eps));
+      for (int k = 0; k < K; ++k) v[k] = bf16r(f32(x.at(m, k) * rs * g.f[k]));
+    } else if (pro == 2) { for (int k = 0; k < K; ++k) v[k] = bf16r(f32(silu(x.at(m, k)) * x2.at(m, k))); }
+    else for (int k = 0; k < K; ++k) v[k] = bf16r((float)x.at(m, k));
+    for (int n = n0; n < n1; ++n) {
+      double y = 0; for (int k = 0; k < K; ++k) y += v[k] * w.at(n, k);
+      out.st((long long)m * out.cols + n, (double)f32(y + (res.ok() ? res.at(m, n) : 0.0)));
+    }
+  }
+}
+
 typedef void (*OpFn)(const Ctx&);
 struct OpEnt { int id; OpFn fn; };
 const OpEnt kOps[] = {
@@ -639,7 +658,7 @@ const OpEnt kOps[] = {
   {101, op_softmax_rows_bwd}, {102, op_gather_rows_scaled}, {103, op_scatter_add_rows}, {104, op_row_dot},
   {113, op_round_bf16}, {114, op_matmul_tile_bf16}, {122, op_matmul_mma_bf16}, {134, op_gemv_bf16},
   {135, op_attn_decode_part}, {136, op_attn_decode_merge}, {115, op_adamw_lr}, {116, op_lr_schedule}, {117, op_scale_flat},
-  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm},
+  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows},
 };
 OpFn find_op(int id) { for (const OpEnt& e : kOps) if (e.id == id) return e.fn; return nullptr; }
 

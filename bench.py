@@ -93,6 +93,80 @@ def cpu_decode(batch):
                       f'{r["seconds"]:.2f} s, scaled x{full / qwen3.weight_elems(c1):.1f} by weight elements to 36 layers'}
 
 
+def gemm_task_flops(lb):
+    """FLOPs of every GEMM tile task (2*tm*tn*K clipped to the matrix) and of the attention tasks (their share of
+    the causal attention's algorithmic FLOPs: fwd 2 products, bwd 5), from the bundle's own arguments."""
+    import numpy as np
+    t, a = lb.tasks, lb.args
+    fl = np.zeros(t.shape[0])
+    for i in range(t.shape[0]):
+        op, off = t[i, 0], t[i, 6]
+        if op in (34, 114, 122):
+            m0, n0, M, N, K, f = (int(x) for x in a[off + 6:off + 12])
+            tm, tn = (128, 256) if op == 122 else ((256, 128) if f & 64 else (128, 128) if f & 32 else (64, 64))
+            fl[i] = 2.0 * (min(M, m0 + tm) - m0) * (min(N, n0 + tn) - n0) * K
+        elif op in (45, 47, 48):
+            q0, T, hd = int(a[off + (7 if op != 48 else 10)]), int(a[off + (8 if op != 48 else 11)]), int(a[off + (11 if op != 48 else 13)])
+            q1 = min(T, q0 + 128)
+            if op == 48:   # keys [q0, q1) meet queries [k, T): sum over keys of (T - k)
+                pairs = sum(T - k for k in range(q0, q1))
+            else:
+                pairs = sum(k + 1 for k in range(q0, q1))
+            fl[i] = 2.0 * hd * pairs * (2 if op == 45 else 2.5)
+    return fl
+
+
+def bench_gpt(steps, warmup, cpu):
+    import numpy as np
+    from kvm_amd.workloads import gpt
+    c = gpt.GPTConfig()
+    log('gpt-162m bf16 training step: building')
+    w = gpt.build(c)
+    ex, lb = build_executor(w, trace=True)
+    ms, res = time_steps(ex, steps, warmup)
+    flops = w.info['flops']['total']
+    tflops = flops / (ms / 1e3) / 1e12
+    # MFMA utilisation inside the GEMM / attention tasks, from the last run's per-task trace
+    tr = ex.trace()
+    dur = (tr['end'] - tr['start']).astype(np.float64) / 100e6     # s (wall_clock64 at 100 MHz)
+    fl = gemm_task_flops(lb)
+    ops = lb.tasks[:, 0]
+    gm = np.isin(ops, [34, 114, 122]); at = np.isin(ops, [45, 47, 48])
+    per_cu = BF16_PEAK_TFLOPS / 256 * 1e12
+    in_task = {'gemm': float(fl[gm].sum() / dur[gm].sum() / per_cu), 'attention': float(fl[at].sum() / dur[at].sum() / per_cu)}
+    busy = float(dur.sum() / (res['grid'] * (tr['end'].max() - tr['start'].min()) / 100e6))
+    names = [m['name'] for m in lb.metadata['buffers']]
+    loss = float(ex.read('loss')[0])
+    out = {'ms_per_step': round(ms, 3), 'tflops': round(tflops, 1), 'mfma_frac_step': round(tflops / BF16_PEAK_TFLOPS, 4),
+           'mfma_frac_in_gemm_tasks': round(in_task['gemm'], 4), 'mfma_frac_in_attention_tasks': round(in_task['attention'], 4),
+           'worker_busy_frac': round(busy, 4), 'tasks': lb.ntasks, 'edges': int(lb.succ.size), 'loss_after': loss,
+           'step_flops': flops, 'params': w.info['params']}
+    log(f'  gpt-162m: {ms:.2f} ms/step, {tflops:.1f} TFLOP/s ({tflops / BF16_PEAK_TFLOPS:.1%} of bf16 peak); in-task MFMA: '
+        f'GEMM {in_task["gemm"]:.1%}, attention {in_task["attention"]:.1%}; workers busy {busy:.1%}; loss {loss:.4f}')
+    ex.close()
+    if cpu:
+        out['cpu_baseline'] = cpu_gpt(w, lb)
+    return out
+
+
+def cpu_gpt(w, lb, limit=1300):
+    """Oracle on the first `limit` tasks of the same GPT-162M step graph (deterministic order); the measured time of its
+    GEMM tiles gives the CPU GEMM rate, and the step estimate is the step's total FLOPs at that rate."""
+    import numpy as np
+    import oracle
+    bufs = [oracle.materialize(m, w.init_override.get(m['name'])) for m in lb.metadata['buffers']]
+    r = oracle.run(lb, bufs, limit=limit)
+    order = r['order'][r['order'] >= 0]
+    fl = gemm_task_flops(lb)
+    mm = [i for i in order if lb.tasks[i, 0] in (34, 114, 122)]
+    rate = fl[mm].sum() / (r['task_us'][mm].sum() / 1e6)
+    est_ms = w.info['flops']['total'] / rate * 1e3
+    return {'value': round(est_ms, 1), 'unit': 'ms/step', 'cores': 1, 'kind': 'port',
+            'sample': f'C++ oracle (restated reference CPU VM + ops) on the first {len(order)} tasks of the same step graph '
+                      f'({len(mm)} GEMM tiles, {r["seconds"]:.1f} s): {rate / 1e9:.2f} GFLOP/s, step = {w.info["flops"]["total"] / 1e12:.3f} TFLOP '
+                      f'at that rate (non-GEMM work not counted)'}
+
+
 def bench_sched():
     """Dependent-hop latency (a chain of noops) and fan-out/fan-in cost (wide noop phases)."""
     from kvm_amd.workloads import Builder, Workload
@@ -135,9 +209,20 @@ def main():
     extra = {}
     if a.workload in ('all', 'sched'):
         extra['sched'] = bench_sched()
+    if a.workload in ('all', 'gpt162m'):
+        extra['gpt162m'] = bench_gpt(a.steps, a.warmup, cpu)
     if a.workload in ('all', 'decode'):
         extra['decode'] = [bench_decode(int(bs), a.steps, a.warmup, cpu) for bs in a.decode_batch.split(',')]
-    if a.workload in ('all', 'decode') and 'gpt162m' not in extra:
+    if 'gpt162m' in extra:
+        g = extra['gpt162m']
+        result.update({'value': g['ms_per_step'], 'unit': 'ms/step', 'higher_is_better': False, 'ms_per_step': g['ms_per_step'],
+                       'dtype': 'bf16', 'config': {'workload': 'gpt-162m training step (12L d768 T1024 B4 V50304, tied, bf16 storage, '
+                                                               'fp32 master AdamW)', 'global_batch': 4, 'seq_len': 1024},
+                       'roofline': {'bound': 'mfma', 'achieved': g['tflops'], 'peak': BF16_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                                    'frac': g['mfma_frac_step'], 'traffic': None}})
+        if 'cpu_baseline' in g:
+            result['cpu_baseline'] = g['cpu_baseline']
+    elif 'decode' in extra:
         d = extra['decode'][0]
         result.update({'value': d['tok_s'], 'unit': 'tok/s', 'higher_is_better': True, 'ms_per_step': d['ms_per_token_step'],
                        'dtype': 'bf16', 'config': {'workload': f'qwen3-8b-shape decode, batch {d["batch"]}, 4096-token KV cache'},

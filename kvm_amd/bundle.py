@@ -64,7 +64,7 @@ def materialize(buf: dict, root: Path | None = None) -> np.ndarray:
     np_dt = np.int32 if dt == DT_I32 else np.float32
     k = init['kind']
     if k == 'fill':
-        return np.full(n, init['value'], np_dt)
+        return np.zeros(n, np_dt) if init['value'] == 0 else np.full(n, init['value'], np_dt)
     if k == 'values':
         return np.asarray(init['values'], np_dt)
     if k == 'seeded':   # bf16 buffers (an executor-side override, not a bundle init): rounded once to bf16

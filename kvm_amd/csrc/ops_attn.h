@@ -10,53 +10,102 @@ namespace kvm {
 constexpr int ATTN_ROWS = 128;
 constexpr int ATTN_KT = 32;     // keys (or queries) staged per LDS slab
 
-// Stages rows [r0, r0+n) of column block [c0, c0+hd) of X into LDS as fp32 [n][hd+1] (zero rows past `valid`).
-__device__ __forceinline__ void stage_rows(LDS float* dst, const View& X, long long r0, int n, int valid, int c0, int hd) {
-  for (int e = tid(); e < n * hd; e += KVM_THREADS) {
-    int r = e / hd, k = e % hd;
-    dst[r * (hd + 1) + k] = r < valid ? X.at(r0 + r, c0 + k) : 0.f;
+// Stages rows [r0, r0+n) of column block [c0, c0+HD) of X into LDS as fp32 [n][HD+1] (zero rows past `valid`).
+// All of a thread's 16-byte loads are issued before any is converted (bf16 or f32 storage, 16-byte aligned columns).
+template <int HD> __device__ __forceinline__ void stage_rows(LDS float* dst, const View& X, long long r0, int n, int valid, int c0) {
+  constexpr int S = HD + 1;
+  if (X.dtype == 2 && (X.cols & 7) == 0 && (c0 & 7) == 0) {
+    constexpr int VPR = HD / 8;                        // 16-byte vectors per row
+    const int nv = n * VPR;
+    for (int base = 0; base < nv; base += 4 * KVM_THREADS) {
+      u16x8_t t[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = base + u * KVM_THREADS + tid(), r = e / VPR;
+        if (e < nv && r < valid) t[u] = *(const GLOBAL u16x8_t*)(X.h() + (r0 + r) * X.cols + c0 + (e % VPR) * 8);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = base + u * KVM_THREADS + tid(), r = e / VPR, k = (e % VPR) * 8;
+        if (e < nv)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) dst[r * S + k + i] = r < valid ? bf2f(t[u][i]) : 0.f;
+      }
+    }
+  } else if (X.dtype == 0 && (X.cols & 3) == 0 && (c0 & 3) == 0) {
+    constexpr int VPR = HD / 4;
+    const int nv = n * VPR;
+    for (int base = 0; base < nv; base += 4 * KVM_THREADS) {
+      f32x4n t[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = base + u * KVM_THREADS + tid(), r = e / VPR;
+        if (e < nv && r < valid) t[u] = *(const GLOBAL f32x4n*)(X.f() + (r0 + r) * X.cols + c0 + (e % VPR) * 4);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = base + u * KVM_THREADS + tid(), r = e / VPR, k = (e % VPR) * 4;
+        if (e < nv)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst[r * S + k + i] = r < valid ? t[u][i] : 0.f;
+      }
+    }
+  } else {
+    for (int e = tid(); e < n * HD; e += KVM_THREADS) {
+      int r = e / HD, k = e % HD;
+      dst[r * S + k] = r < valid ? X.at(r0 + r, c0 + k) : 0.f;
+    }
   }
 }
 
-// Two threads per row: thread pair (2*row, 2*row+1) splits the head dimension in halves; dot products combine with
-// one lane swap. Registers: q/do halves and the output accumulator halves (hd <= 128 -> 64 + 64 floats).
-__device__ void op_attn_fwd(const Ctx& c) {
+// Two threads per query row: thread pair (2*row, 2*row+1) splits the head dimension in halves; dot products combine
+// with one lane swap. HD is a template parameter so the per-thread halves live in registers.
+template <int HD> __device__ __noinline__ void attn_fwd_t(const Ctx& c) {
+  constexpr int HALF = HD / 2, S = HD + 1;
   View q = c.buf(0), k = c.buf(1), v = c.buf(2), o = c.buf(3), lse = c.buf(4);
-  int bb = c.i(5), h = c.i(6), q0 = c.i(7), T = c.i(8), H = c.i(9), Hkv = c.i(10), hd = c.i(11); float sc = c.f(12);
-  int kvh = h / (H / Hkv), half = hd / 2, row = tid() >> 1, part = tid() & 1;
+  int bb = c.i(5), h = c.i(6), q0 = c.i(7), T = c.i(8), H = c.i(9), Hkv = c.i(10); float sc = c.f(12);
+  int kvh = h / (H / Hkv), row = tid() >> 1, part = tid() & 1;
   int gq = q0 + row; bool active = gq < T;
-  LDS float* Ks = (LDS float*)c.smem; LDS float* Vs = Ks + ATTN_KT * (hd + 1);
-  float qr[64], acc[64];
-  for (int i = 0; i < half; ++i) { qr[i] = active ? q.at((long long)bb * T + gq, h * hd + part * half + i) : 0.f; acc[i] = 0.f; }
+  LDS float* Ks = (LDS float*)c.smem; LDS float* Vs = Ks + ATTN_KT * S;
+  float qr[HALF], acc[HALF];
+#pragma unroll
+  for (int i = 0; i < HALF; ++i) { qr[i] = active ? q.at((long long)bb * T + gq, h * HD + part * HALF + i) * sc : 0.f; acc[i] = 0.f; }
   float m = -INFINITY, l = 0.f;
   int last = min(q0 + ATTN_ROWS, T);     // keys [0, last) can matter to this task
   for (int j0 = 0; j0 < last; j0 += ATTN_KT) {
     int nv = min(ATTN_KT, last - j0);
     __syncthreads();
-    stage_rows(Ks, k, (long long)bb * T + j0, ATTN_KT, nv, kvh * hd, hd);
-    stage_rows(Vs, v, (long long)bb * T + j0, ATTN_KT, nv, kvh * hd, hd);
+    stage_rows<HD>(Ks, k, (long long)bb * T + j0, ATTN_KT, nv, kvh * HD);
+    stage_rows<HD>(Vs, v, (long long)bb * T + j0, ATTN_KT, nv, kvh * HD);
     __syncthreads();
+    const int jmax = min(nv, gq - j0 + 1);   // causal: keys j <= gq
     for (int jj = 0; jj < nv; ++jj) {
-      int j = j0 + jj;
       float s = 0.f;
-      for (int i = 0; i < half; ++i) s += qr[i] * Ks[jj * (hd + 1) + part * half + i];
+#pragma unroll
+      for (int i = 0; i < HALF; ++i) s += qr[i] * Ks[jj * S + part * HALF + i];
       s += __shfl_xor(s, 1, 64);
-      s *= sc;
-      if (!active || j > gq) continue;
+      if (!active || jj >= jmax) continue;
       float nm = fmaxf(m, s), f = __expf(m - nm), p = __expf(s - nm);
       l = l * f + p;
-      for (int i = 0; i < half; ++i) acc[i] = acc[i] * f + p * Vs[jj * (hd + 1) + part * half + i];
+#pragma unroll
+      for (int i = 0; i < HALF; ++i) acc[i] = acc[i] * f + p * Vs[jj * S + part * HALF + i];
       m = nm;
     }
   }
   if (active) {
     float inv = 1.f / l;
-    for (int i = 0; i < half; ++i) o.st(((long long)bb * T + gq) * o.cols + h * hd + part * half + i, acc[i] * inv);
+#pragma unroll
+    for (int i = 0; i < HALF; ++i) o.st(((long long)bb * T + gq) * o.cols + h * HD + part * HALF + i, acc[i] * inv);
     if (part == 0) lse.f()[((long long)bb * H + h) * T + gq] = m + logf(l);
   }
 }
+__device__ void op_attn_fwd(const Ctx& c) {
+  switch (c.i(11)) { case 16: attn_fwd_t<16>(c); break; case 32: attn_fwd_t<32>(c); break; case 64: attn_fwd_t<64>(c); break; default: attn_fwd_t<128>(c); }
+}
 
-__device__ void op_attn_bwd_delta(const Ctx& c) {
+__device__ __noinline__ void op_attn_bwd_delta(const Ctx& c) {
   View o = c.buf(0), d = c.buf(1), delta = c.buf(2); int r0 = c.i(3), r1 = c.i(4), T = c.i(5), H = c.i(6), hd = c.i(7);
   for (int rh = r0 * H + wave(); rh < r1 * H; rh += KVM_WAVES) {
     int r = rh / H, h = rh % H; float s = 0.f;
@@ -66,17 +115,19 @@ __device__ void op_attn_bwd_delta(const Ctx& c) {
   }
 }
 
-__device__ void op_attn_bwd_dq(const Ctx& c) {
+template <int HD> __device__ __noinline__ void attn_dq_t(const Ctx& c) {
+  constexpr int HALF = HD / 2, S = HD + 1;
   View q = c.buf(0), k = c.buf(1), v = c.buf(2), d = c.buf(3), lse = c.buf(4), delta = c.buf(5), dq = c.buf(6);
-  int bb = c.i(7), h = c.i(8), q0 = c.i(9), T = c.i(10), H = c.i(11), Hkv = c.i(12), hd = c.i(13); float sc = c.f(14);
-  int kvh = h / (H / Hkv), half = hd / 2, row = tid() >> 1, part = tid() & 1;
+  int bb = c.i(7), h = c.i(8), q0 = c.i(9), T = c.i(10), H = c.i(11), Hkv = c.i(12); float sc = c.f(14);
+  int kvh = h / (H / Hkv), row = tid() >> 1, part = tid() & 1;
   int gq = q0 + row; bool active = gq < T;
-  LDS float* Ks = (LDS float*)c.smem; LDS float* Vs = Ks + ATTN_KT * (hd + 1);
-  float qr[64], dr[64], acc[64];
+  LDS float* Ks = (LDS float*)c.smem; LDS float* Vs = Ks + ATTN_KT * S;
+  float qr[HALF], dr[HALF], acc[HALF];
   long long qrow = (long long)bb * T + gq;
-  for (int i = 0; i < half; ++i) {
-    qr[i] = active ? q.at(qrow, h * hd + part * half + i) : 0.f;
-    dr[i] = active ? d.at(qrow, h * hd + part * half + i) : 0.f;
+#pragma unroll
+  for (int i = 0; i < HALF; ++i) {
+    qr[i] = active ? q.at(qrow, h * HD + part * HALF + i) : 0.f;
+    dr[i] = active ? d.at(qrow, h * HD + part * HALF + i) : 0.f;
     acc[i] = 0.f;
   }
   float li = active ? lse.f()[((long long)bb * H + h) * T + gq] : 0.f, di = active ? delta.f()[((long long)bb * H + h) * T + gq] : 0.f;
@@ -84,64 +135,82 @@ __device__ void op_attn_bwd_dq(const Ctx& c) {
   for (int j0 = 0; j0 < last; j0 += ATTN_KT) {
     int nv = min(ATTN_KT, last - j0);
     __syncthreads();
-    stage_rows(Ks, k, (long long)bb * T + j0, ATTN_KT, nv, kvh * hd, hd);
-    stage_rows(Vs, v, (long long)bb * T + j0, ATTN_KT, nv, kvh * hd, hd);
+    stage_rows<HD>(Ks, k, (long long)bb * T + j0, ATTN_KT, nv, kvh * HD);
+    stage_rows<HD>(Vs, v, (long long)bb * T + j0, ATTN_KT, nv, kvh * HD);
     __syncthreads();
+    const int jmax = min(nv, gq - j0 + 1);
     for (int jj = 0; jj < nv; ++jj) {
       float s = 0.f, dp = 0.f;
-      for (int i = 0; i < half; ++i) { s += qr[i] * Ks[jj * (hd + 1) + part * half + i]; dp += dr[i] * Vs[jj * (hd + 1) + part * half + i]; }
+#pragma unroll
+      for (int i = 0; i < HALF; ++i) { s += qr[i] * Ks[jj * S + part * HALF + i]; dp += dr[i] * Vs[jj * S + part * HALF + i]; }
       s += __shfl_xor(s, 1, 64); dp += __shfl_xor(dp, 1, 64);
-      if (!active || j0 + jj > gq) continue;
+      if (!active || jj >= jmax) continue;
       float ds = __expf(s * sc - li) * (dp - di);
-      for (int i = 0; i < half; ++i) acc[i] += ds * Ks[jj * (hd + 1) + part * half + i];
+#pragma unroll
+      for (int i = 0; i < HALF; ++i) acc[i] += ds * Ks[jj * S + part * HALF + i];
     }
   }
-  if (active) for (int i = 0; i < half; ++i) dq.st(qrow * dq.cols + h * hd + part * half + i, acc[i] * sc);
+  if (active)
+#pragma unroll
+    for (int i = 0; i < HALF; ++i) dq.st(qrow * dq.cols + h * HD + part * HALF + i, acc[i] * sc);
+}
+__device__ void op_attn_bwd_dq(const Ctx& c) {
+  switch (c.i(13)) { case 16: attn_dq_t<16>(c); break; case 32: attn_dq_t<32>(c); break; case 64: attn_dq_t<64>(c); break; default: attn_dq_t<128>(c); }
 }
 
 // dK/dV for 128 keys of kv head kvh: sums over the GQA group's heads and every later query, fixed order.
-__device__ void op_attn_bwd_dkv(const Ctx& c) {
+template <int HD> __device__ __noinline__ void attn_dkv_t(const Ctx& c) {
+  constexpr int HALF = HD / 2, S = HD + 1;
   View q = c.buf(0), k = c.buf(1), v = c.buf(2), d = c.buf(3), lse = c.buf(4), delta = c.buf(5), dk = c.buf(6), dv = c.buf(7);
-  int bb = c.i(8), kvh = c.i(9), k0 = c.i(10), T = c.i(11), H = c.i(12), hd = c.i(13); float sc = c.f(14);
-  int G = H / (k.cols / hd), half = hd / 2, row = tid() >> 1, part = tid() & 1;
+  int bb = c.i(8), kvh = c.i(9), k0 = c.i(10), T = c.i(11), H = c.i(12); float sc = c.f(14);
+  int G = H / (k.cols / HD), row = tid() >> 1, part = tid() & 1;
   int gk = k0 + row; bool active = gk < T;
-  LDS float* Qs = (LDS float*)c.smem; LDS float* Ds = Qs + ATTN_KT * (hd + 1); LDS float* Ls = Ds + ATTN_KT * (hd + 1); LDS float* Es = Ls + ATTN_KT;
+  LDS float* Qs = (LDS float*)c.smem; LDS float* Ds = Qs + ATTN_KT * S; LDS float* Ls = Ds + ATTN_KT * S; LDS float* Es = Ls + ATTN_KT;
   long long krow = (long long)bb * T + gk;
-  float kr[64], vr[64], sk[64], sv[64];
-  for (int i = 0; i < half; ++i) {
-    kr[i] = active ? k.at(krow, kvh * hd + part * half + i) : 0.f;
-    vr[i] = active ? v.at(krow, kvh * hd + part * half + i) : 0.f;
+  float kr[HALF], vr[HALF], sk[HALF], sv[HALF];
+#pragma unroll
+  for (int i = 0; i < HALF; ++i) {
+    kr[i] = active ? k.at(krow, kvh * HD + part * HALF + i) : 0.f;
+    vr[i] = active ? v.at(krow, kvh * HD + part * HALF + i) : 0.f;
     sk[i] = sv[i] = 0.f;
   }
   for (int h = kvh * G; h < (kvh + 1) * G; ++h)
     for (int j0 = k0; j0 < T; j0 += ATTN_KT) {   // queries before k0 never see these keys
       int nv = min(ATTN_KT, T - j0);
       __syncthreads();
-      stage_rows(Qs, q, (long long)bb * T + j0, ATTN_KT, nv, h * hd, hd);
-      stage_rows(Ds, d, (long long)bb * T + j0, ATTN_KT, nv, h * hd, hd);
+      stage_rows<HD>(Qs, q, (long long)bb * T + j0, ATTN_KT, nv, h * HD);
+      stage_rows<HD>(Ds, d, (long long)bb * T + j0, ATTN_KT, nv, h * HD);
       for (int e = tid(); e < ATTN_KT; e += KVM_THREADS) {
         Ls[e] = e < nv ? lse.f()[((long long)bb * H + h) * T + j0 + e] : 0.f;
         Es[e] = e < nv ? delta.f()[((long long)bb * H + h) * T + j0 + e] : 0.f;
       }
       __syncthreads();
+      const int jmin = max(0, gk - j0);      // causal: queries j >= gk
       for (int jj = 0; jj < nv; ++jj) {
         float s = 0.f, dp = 0.f;
-        for (int i = 0; i < half; ++i) { s += Qs[jj * (hd + 1) + part * half + i] * kr[i]; dp += Ds[jj * (hd + 1) + part * half + i] * vr[i]; }
+#pragma unroll
+        for (int i = 0; i < HALF; ++i) { s += Qs[jj * S + part * HALF + i] * kr[i]; dp += Ds[jj * S + part * HALF + i] * vr[i]; }
         s += __shfl_xor(s, 1, 64); dp += __shfl_xor(dp, 1, 64);
-        if (!active || j0 + jj < gk) continue;
+        if (!active || jj < jmin) continue;
         float p = __expf(s * sc - Ls[jj]), w = p * (dp - Es[jj]);
-        for (int i = 0; i < half; ++i) { sv[i] += p * Ds[jj * (hd + 1) + part * half + i]; sk[i] += w * Qs[jj * (hd + 1) + part * half + i]; }
+#pragma unroll
+        for (int i = 0; i < HALF; ++i) { sv[i] += p * Ds[jj * S + part * HALF + i]; sk[i] += w * Qs[jj * S + part * HALF + i]; }
       }
     }
-  if (active) for (int i = 0; i < half; ++i) {
-    dk.st(krow * dk.cols + kvh * hd + part * half + i, sk[i] * sc);
-    dv.st(krow * dv.cols + kvh * hd + part * half + i, sv[i]);
-  }
+  if (active)
+#pragma unroll
+    for (int i = 0; i < HALF; ++i) {
+      dk.st(krow * dk.cols + kvh * HD + part * HALF + i, sk[i] * sc);
+      dv.st(krow * dv.cols + kvh * HD + part * HALF + i, sv[i]);
+    }
+}
+__device__ void op_attn_bwd_dkv(const Ctx& c) {
+  switch (c.i(13)) { case 16: attn_dkv_t<16>(c); break; case 32: attn_dkv_t<32>(c); break; case 64: attn_dkv_t<64>(c); break; default: attn_dkv_t<128>(c); }
 }
 
 // ---------------------------------------------------------------------------------------------- decode
 // One query row per (b, h) over cache positions [0, lens[b]] (registry op 50).
-__device__ void op_attn_decode(const Ctx& c) {
+__device__ __noinline__ void op_attn_decode(const Ctx& c) {
   View q = c.buf(0), kc = c.buf(1), vc = c.buf(2), lens = c.buf(3), o = c.buf(4);
   int bb = c.i(5), h = c.i(6), H = c.i(7), Hkv = c.i(8), hd = c.i(9), Tmax = c.i(10); float sc = c.f(11);
   int n = lens.i()[bb] + 1;
@@ -169,7 +238,7 @@ constexpr float ATTN_EMPTY_M = -3.4028234663852886e38f;
 // all issued before use), with an online softmax across chunks. Optional fused RoPE of q and the new key, and the KV
 // append of the new token by the split that holds it (flags 1, 3).
 constexpr int DEC_KC = 64;
-__device__ void op_attn_decode_part(const Ctx& c) {
+__device__ __noinline__ void op_attn_decode_part(const Ctx& c) {
   View q = c.buf(0), kc = c.buf(1), vc = c.buf(2), lens = c.buf(3), part = c.buf(4), kn = c.buf(5), vn = c.buf(6);
   int bb = c.i(7), kvh = c.i(8), s = c.i(9), S = c.i(10), H = c.i(11), Hkv = c.i(12), hd = c.i(13), Tmax = c.i(14);
   float sc = c.f(15), th = c.f(16); int fl = c.i(17);
@@ -286,7 +355,7 @@ __device__ void op_attn_decode_part(const Ctx& c) {
 }
 // Merge of the splits (registry op 136): per head, the split weights e_s = exp(m_s - max m) (live splits only) are
 // computed once into LDS, then each output element is one pass over the splits.
-__device__ void op_attn_decode_merge(const Ctx& c) {
+__device__ __noinline__ void op_attn_decode_merge(const Ctx& c) {
   View part = c.buf(0), o = c.buf(1); int bb = c.i(2), h0 = c.i(3), h1 = c.i(4), S = c.i(5), H = c.i(6), hd = c.i(7);
   LDS float* w = (LDS float*)c.smem;      // [h1-h0][S] split weights, then [h1-h0] 1/denominator
   LDS float* inv = w + (h1 - h0) * S;

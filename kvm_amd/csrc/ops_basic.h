@@ -11,13 +11,13 @@ namespace kvm {
 #define FLAT_FOR(i, e0, e1) for (long long i = (long long)(e0) + tid(); i < (long long)(e1); i += KVM_THREADS)
 
 // ---------------------------------------------------------------------------------------------- core pack
-__device__ void op_copy(const Ctx& c) { View s = c.buf(0), d = c.buf(1); FLAT_FOR(k, 0, c.i(2)) d.i()[k] = s.i()[k]; }
-__device__ void op_add(const Ctx& c) { View a = c.buf(0), b = c.buf(1), o = c.buf(2); FLAT_FOR(k, 0, c.i(3)) o.f()[k] = a.f()[k] + b.f()[k]; }
-__device__ void op_scale(const Ctx& c) { View x = c.buf(0), o = c.buf(1); float al = c.f(2); FLAT_FOR(k, 0, c.i(3)) o.f()[k] = x.f()[k] * al; }
-__device__ void op_relu(const Ctx& c) { View x = c.buf(0), o = c.buf(1); FLAT_FOR(k, 0, c.i(2)) { float v = x.f()[k]; o.f()[k] = v > 0.f ? v : 0.f; } }
-__device__ void op_sgd(const Ctx& c) { View w = c.buf(0), g = c.buf(1); float lr = c.f(2); FLAT_FOR(k, 0, c.i(3)) w.f()[k] = w.f()[k] - __fmul_rn(lr, g.f()[k]); }
-__device__ void op_predict(const Ctx& c) { View x = c.buf(0), w = c.buf(1), o = c.buf(2); float s = w.f()[0]; FLAT_FOR(k, 0, c.i(3)) o.f()[k] = s * x.f()[k]; }
-__device__ void op_mse_grad(const Ctx& c) {   // sequential f32 accumulation, as the reference (ref_ops.py:46-54)
+__device__ __noinline__ void op_copy(const Ctx& c) { View s = c.buf(0), d = c.buf(1); FLAT_FOR(k, 0, c.i(2)) d.i()[k] = s.i()[k]; }
+__device__ __noinline__ void op_add(const Ctx& c) { View a = c.buf(0), b = c.buf(1), o = c.buf(2); FLAT_FOR(k, 0, c.i(3)) o.f()[k] = a.f()[k] + b.f()[k]; }
+__device__ __noinline__ void op_scale(const Ctx& c) { View x = c.buf(0), o = c.buf(1); float al = c.f(2); FLAT_FOR(k, 0, c.i(3)) o.f()[k] = x.f()[k] * al; }
+__device__ __noinline__ void op_relu(const Ctx& c) { View x = c.buf(0), o = c.buf(1); FLAT_FOR(k, 0, c.i(2)) { float v = x.f()[k]; o.f()[k] = v > 0.f ? v : 0.f; } }
+__device__ __noinline__ void op_sgd(const Ctx& c) { View w = c.buf(0), g = c.buf(1); float lr = c.f(2); FLAT_FOR(k, 0, c.i(3)) w.f()[k] = w.f()[k] - __fmul_rn(lr, g.f()[k]); }
+__device__ __noinline__ void op_predict(const Ctx& c) { View x = c.buf(0), w = c.buf(1), o = c.buf(2); float s = w.f()[0]; FLAT_FOR(k, 0, c.i(3)) o.f()[k] = s * x.f()[k]; }
+__device__ __noinline__ void op_mse_grad(const Ctx& c) {   // sequential f32 accumulation, as the reference (ref_ops.py:46-54)
   View p = c.buf(0), t = c.buf(1), x = c.buf(2), l = c.buf(3), g = c.buf(4); int n = c.i(5);
   if (tid() == 0) {
     float la = 0.f, ga = 0.f;
@@ -29,7 +29,7 @@ __device__ void op_mse_grad(const Ctx& c) {   // sequential f32 accumulation, as
     l.f()[0] = la / (float)n; g.f()[0] = ga / (float)n;
   }
 }
-__device__ void op_matmul(const Ctx& c) {   // small fp32 GEMM, sequential k (ref_ops.py:57-66)
+__device__ __noinline__ void op_matmul(const Ctx& c) {   // small fp32 GEMM, sequential k (ref_ops.py:57-66)
   View a = c.buf(0), b = c.buf(1), o = c.buf(2); int m = c.i(3), n = c.i(4), k = c.i(5);
   for (int e = tid(); e < m * n; e += KVM_THREADS) {
     int i = e / n, j = e % n; float acc = 0.f;
@@ -37,8 +37,8 @@ __device__ void op_matmul(const Ctx& c) {   // small fp32 GEMM, sequential k (re
     o.f()[e] = acc;
   }
 }
-__device__ void op_fill(const Ctx& c) { View x = c.buf(0); float v = c.f(1); FLAT_FOR(k, 0, c.i(2)) x.f()[k] = v; }
-__device__ void op_spin(const Ctx& c) {
+__device__ __noinline__ void op_fill(const Ctx& c) { View x = c.buf(0); float v = c.f(1); FLAT_FOR(k, 0, c.i(2)) x.f()[k] = v; }
+__device__ __noinline__ void op_spin(const Ctx& c) {
   if (tid() == 0) { unsigned long long t0 = wall_clock64(), n = (unsigned long long)c.i(0) * 100ull; while (wall_clock64() - t0 < n) __builtin_amdgcn_s_sleep(2); }
 }
 
@@ -55,24 +55,24 @@ __device__ __forceinline__ float sigmoid_f(float x) { return x >= 0.f ? 1.f / (1
 __device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 __device__ __forceinline__ float silu_d_f(float x) { float s = sigmoid_f(x); return s * (1.f + x * (1.f - s)); }
 
-__device__ void op_gelu_fwd(const Ctx& c) { View x = c.buf(0), o = c.buf(1); FLAT_FOR(k, c.i(2), c.i(3)) o.st(k, gelu_f(x.ld(k))); }
-__device__ void op_gelu_bwd(const Ctx& c) {
+__device__ __noinline__ void op_gelu_fwd(const Ctx& c) { View x = c.buf(0), o = c.buf(1); FLAT_FOR(k, c.i(2), c.i(3)) o.st(k, gelu_f(x.ld(k))); }
+__device__ __noinline__ void op_gelu_bwd(const Ctx& c) {
   View x = c.buf(0), dy = c.buf(1), dx = c.buf(2); int acc = c.i(5);
   FLAT_FOR(k, c.i(3), c.i(4)) { float v = dy.ld(k) * gelu_grad_f(x.ld(k)); dx.st(k, acc ? dx.ld(k) + v : v); }
 }
-__device__ void op_residual_add(const Ctx& c) { View a = c.buf(0), b = c.buf(1), o = c.buf(2); FLAT_FOR(k, c.i(3), c.i(4)) o.st(k, a.ld(k) + b.ld(k)); }
-__device__ void op_sgd_range(const Ctx& c) { View w = c.buf(0), g = c.buf(1); float lr = c.f(2); FLAT_FOR(k, c.i(3), c.i(4)) w.f()[k] = w.f()[k] - __fmul_rn(lr, g.f()[k]); }
-__device__ void op_round_tf32(const Ctx& c) {
+__device__ __noinline__ void op_residual_add(const Ctx& c) { View a = c.buf(0), b = c.buf(1), o = c.buf(2); FLAT_FOR(k, c.i(3), c.i(4)) o.st(k, a.ld(k) + b.ld(k)); }
+__device__ __noinline__ void op_sgd_range(const Ctx& c) { View w = c.buf(0), g = c.buf(1); float lr = c.f(2); FLAT_FOR(k, c.i(3), c.i(4)) w.f()[k] = w.f()[k] - __fmul_rn(lr, g.f()[k]); }
+__device__ __noinline__ void op_round_tf32(const Ctx& c) {
   View x = c.buf(0), o = c.buf(1);
   FLAT_FOR(k, c.i(2), c.i(3)) { uint32_t u = __float_as_uint(x.f()[k]); if ((u & 0x7fffffffu) <= 0x7f800000u) u += 0x1000u; o.f()[k] = __uint_as_float(u & 0xffffe000u); }
 }
-__device__ void op_zero_buf(const Ctx& c) {
+__device__ __noinline__ void op_zero_buf(const Ctx& c) {
   View x = c.buf(0);
   if (x.dtype == 2) { FLAT_FOR(k, c.i(1), c.i(2)) x.h()[k] = 0; }
   else FLAT_FOR(k, c.i(1), c.i(2)) x.i()[k] = 0;
 }
-__device__ void op_counter_inc(const Ctx& c) { View x = c.buf(0); FLAT_FOR(k, c.i(1), c.i(2)) x.i()[k] = (int)((unsigned)x.i()[k] + (unsigned)c.i(3)); }
-__device__ void op_round_bf16(const Ctx& c) {   // f32<->bf16 storage conversion (or f32->f32 emulation)
+__device__ __noinline__ void op_counter_inc(const Ctx& c) { View x = c.buf(0); FLAT_FOR(k, c.i(1), c.i(2)) x.i()[k] = (int)((unsigned)x.i()[k] + (unsigned)c.i(3)); }
+__device__ __noinline__ void op_round_bf16(const Ctx& c) {   // f32<->bf16 storage conversion (or f32->f32 emulation)
   View x = c.buf(0), o = c.buf(1);
   if (x.dtype == 2 && o.dtype == 2) { FLAT_FOR(k, c.i(2), c.i(3)) o.h()[k] = x.h()[k]; return; }
   FLAT_FOR(k, c.i(2), c.i(3)) { float v = x.ld(k); if (o.dtype == 2) o.h()[k] = f2bf(v); else o.f()[k] = round_bf(v); }
@@ -84,21 +84,21 @@ __device__ __forceinline__ float act_d(int kind, float x) {
   switch (kind) { case 0: return x > 0.f ? 1.f : 0.f; case 1: return silu_d_f(x); case 2: { float t = tanhf(x); return 1.f - t * t; }
     default: { float s = sigmoid_f(x); return s * (1.f - s); } }
 }
-__device__ void op_act_fwd(const Ctx& c) { View x = c.buf(0), o = c.buf(1); int kind = c.i(2); FLAT_FOR(k, c.i(3), c.i(4)) o.f()[k] = act_f(kind, x.f()[k]); }
-__device__ void op_act_bwd(const Ctx& c) {
+__device__ __noinline__ void op_act_fwd(const Ctx& c) { View x = c.buf(0), o = c.buf(1); int kind = c.i(2); FLAT_FOR(k, c.i(3), c.i(4)) o.f()[k] = act_f(kind, x.f()[k]); }
+__device__ __noinline__ void op_act_bwd(const Ctx& c) {
   View x = c.buf(0), dy = c.buf(1), dx = c.buf(2); int kind = c.i(3), acc = c.i(6);
   FLAT_FOR(k, c.i(4), c.i(5)) { float v = dy.f()[k] * act_d(kind, x.f()[k]); dx.f()[k] = acc ? dx.f()[k] + v : v; }
 }
-__device__ void op_silu_mul_fwd(const Ctx& c) { View g = c.buf(0), u = c.buf(1), o = c.buf(2); FLAT_FOR(k, c.i(3), c.i(4)) o.st(k, silu_f(g.ld(k)) * u.ld(k)); }
-__device__ void op_silu_mul_bwd(const Ctx& c) {
+__device__ __noinline__ void op_silu_mul_fwd(const Ctx& c) { View g = c.buf(0), u = c.buf(1), o = c.buf(2); FLAT_FOR(k, c.i(3), c.i(4)) o.st(k, silu_f(g.ld(k)) * u.ld(k)); }
+__device__ __noinline__ void op_silu_mul_bwd(const Ctx& c) {
   View g = c.buf(0), u = c.buf(1), dy = c.buf(2), dg = c.buf(3), du = c.buf(4); int acc = c.i(7);
   FLAT_FOR(k, c.i(5), c.i(6)) {
     float gv = g.f()[k], vg = dy.f()[k] * (u.f()[k] * silu_d_f(gv)), vu = dy.f()[k] * silu_f(gv);
     dg.f()[k] = acc ? dg.f()[k] + vg : vg; du.f()[k] = acc ? du.f()[k] + vu : vu;
   }
 }
-__device__ void op_scale_flat(const Ctx& c) { View x = c.buf(0), o = c.buf(1); float al = c.f(2); FLAT_FOR(k, c.i(3), c.i(4)) o.f()[k] = al * x.f()[k]; }
-__device__ void op_add_rowtile(const Ctx& c) {
+__device__ __noinline__ void op_scale_flat(const Ctx& c) { View x = c.buf(0), o = c.buf(1); float al = c.f(2); FLAT_FOR(k, c.i(3), c.i(4)) o.f()[k] = al * x.f()[k]; }
+__device__ __noinline__ void op_add_rowtile(const Ctx& c) {
   View x = c.buf(0), pos = c.buf(1), o = c.buf(2); int r0 = c.i(3), r1 = c.i(4), T = c.i(5), d = c.i(6);
   for (long long e = tid(); e < (long long)(r1 - r0) * d; e += KVM_THREADS) {
     int r = r0 + (int)(e / d), k = (int)(e % d);
@@ -107,7 +107,7 @@ __device__ void op_add_rowtile(const Ctx& c) {
 }
 
 // ---------------------------------------------------------------------------------------------- embeddings
-__device__ void op_embedding_fwd(const Ctx& c) {
+__device__ __noinline__ void op_embedding_fwd(const Ctx& c) {
   View ids = c.buf(0), wte = c.buf(1), wpe = c.buf(2), out = c.buf(3);
   int r0 = c.i(4), r1 = c.i(5), T = c.i(6), d = c.i(7);
   for (int r = r0 + wave(); r < r1; r += KVM_WAVES) {
@@ -122,7 +122,7 @@ __device__ void op_embedding_fwd(const Ctx& c) {
   }
 }
 // dtab[key,:] (+)= sum of dout rows with that key, rows ascending. Each thread owns columns; rows in order.
-__device__ void op_embedding_bwd(const Ctx& c) {
+__device__ __noinline__ void op_embedding_bwd(const Ctx& c) {
   View ids = c.buf(0), dout = c.buf(1), dt = c.buf(2);
   int N = c.i(3), mod = c.i(4), v0 = c.i(5), v1 = c.i(6), d = c.i(7), acc = c.i(8);
   if (!acc) for (long long e = tid(); e < (long long)(v1 - v0) * d; e += KVM_THREADS) dt.f()[(long long)(v0 + e / d) * dt.cols + e % d] = 0.f;
@@ -139,7 +139,7 @@ __device__ void op_embedding_bwd(const Ctx& c) {
         for (int k = tid(); k < d; k += KVM_THREADS) dt.f()[(long long)key * dt.cols + k] += dout.at(r, k);
   }
 }
-__device__ void op_gather_rows(const Ctx& c) {
+__device__ __noinline__ void op_gather_rows(const Ctx& c) {
   View src = c.buf(0), idx = c.buf(1), dst = c.buf(2); int r0 = c.i(3), r1 = c.i(4), d = c.i(5);
   for (int r = r0 + wave(); r < r1; r += KVM_WAVES) {
     int j = idx.i()[r]; bool bad = j < 0 || j >= src.rows;
@@ -147,13 +147,13 @@ __device__ void op_gather_rows(const Ctx& c) {
     for (int k = lane(); k < d; k += 64) dst.f()[(long long)r * dst.cols + k] = bad ? 0.f : src.f()[(long long)j * src.cols + k];
   }
 }
-__device__ void op_select_window(const Ctx& c) {
+__device__ __noinline__ void op_select_window(const Ctx& c) {
   View src = c.buf(0), step = c.buf(1), dst = c.buf(2); int i0 = c.i(3), i1 = c.i(4), stride = c.i(5), off = c.i(6);
   long long base = (long long)step.i()[0] * stride + off;
   if (base < 0 || base + i1 > src.n()) { if (tid() == 0) c.fail(KVM_ERR_OP_RANGE, (int)base, i1); return; }
   FLAT_FOR(k, i0, i1) dst.i()[k] = src.i()[base + k];
 }
-__device__ void op_gather_rows_scaled(const Ctx& c) {
+__device__ __noinline__ void op_gather_rows_scaled(const Ctx& c) {
   View src = c.buf(0), idx = c.buf(1), sc = c.buf(2), dst = c.buf(3); int r0 = c.i(4), r1 = c.i(5), d = c.i(6), acc = c.i(7), i0 = c.i(8);
   for (int r = r0 + wave(); r < r1; r += KVM_WAVES) {
     int j = idx.i()[i0 + r]; float s = sc.ok() ? sc.f()[i0 + r] : 1.f; bool ok = j >= 0 && j < src.rows;
@@ -163,7 +163,7 @@ __device__ void op_gather_rows_scaled(const Ctx& c) {
     }
   }
 }
-__device__ void op_scatter_add_rows(const Ctx& c) {
+__device__ __noinline__ void op_scatter_add_rows(const Ctx& c) {
   View src = c.buf(0), idx = c.buf(1), sc = c.buf(2), dst = c.buf(3);
   int N = c.i(4), v0 = c.i(5), v1 = c.i(6), d = c.i(7), acc = c.i(8), i0 = c.i(9);
   for (int v = v0; v < v1; ++v)
@@ -173,7 +173,7 @@ __device__ void op_scatter_add_rows(const Ctx& c) {
       long long o = (long long)v * dst.cols + k; dst.f()[o] = acc ? dst.f()[o] + a : a;
     }
 }
-__device__ void op_row_dot(const Ctx& c) {
+__device__ __noinline__ void op_row_dot(const Ctx& c) {
   View A = c.buf(0), B = c.buf(1), idx = c.buf(2), out = c.buf(3); int r0 = c.i(4), r1 = c.i(5), d = c.i(6), acc = c.i(7), i0 = c.i(8);
   for (int r = r0 + wave(); r < r1; r += KVM_WAVES) {
     int j = idx.ok() ? idx.i()[i0 + r] : r; bool ok = j >= 0 && j < A.rows;
@@ -186,7 +186,7 @@ __device__ void op_row_dot(const Ctx& c) {
 
 // ---------------------------------------------------------------------------------------------- normalisation
 // One wave per row; row statistics in f32 with a two-pass (mean, then centred square) reduction.
-template <bool RMS> __device__ void op_norm_fwd(const Ctx& c) {
+template <bool RMS> __device__ __noinline__ void op_norm_fwd(const Ctx& c) {
   int k = 0; View x = c.buf(k++), g = c.buf(k++), be; if (!RMS) be = c.buf(k++);
   View out = c.buf(k++), mean; if (!RMS) mean = c.buf(k++);
   View rstd = c.buf(k++);
@@ -200,7 +200,7 @@ template <bool RMS> __device__ void op_norm_fwd(const Ctx& c) {
     if (lane() == 0) { rstd.f()[r] = rs; if (!RMS) mean.f()[r] = mu; }
   }
 }
-template <bool RMS> __device__ void op_norm_bwd_dx(const Ctx& c) {
+template <bool RMS> __device__ __noinline__ void op_norm_bwd_dx(const Ctx& c) {
   int k = 0; View x = c.buf(k++), dy = c.buf(k++), g = c.buf(k++), mean; if (!RMS) mean = c.buf(k++);
   View rstd = c.buf(k++), dx = c.buf(k++);
   int r0 = c.i(k), r1 = c.i(k + 1), d = c.i(k + 2), acc = c.i(k + 3);
@@ -216,7 +216,7 @@ template <bool RMS> __device__ void op_norm_bwd_dx(const Ctx& c) {
   }
 }
 // dgamma/dbeta column sums over all rows ascending; each thread owns a column, rows read coalesced across threads.
-__device__ void op_norm_bwd_params(const Ctx& c) {
+__device__ __noinline__ void op_norm_bwd_params(const Ctx& c) {
   View x = c.buf(0), dy = c.buf(1), mean = c.buf(2), rstd = c.buf(3), dg = c.buf(4), db = c.buf(5);
   int R = c.i(6), c0 = c.i(8), c1 = c.i(9), acc = c.i(10);
   for (int j = c0 + tid(); j < c1; j += KVM_THREADS) {
@@ -226,14 +226,14 @@ __device__ void op_norm_bwd_params(const Ctx& c) {
     if (db.ok()) db.f()[j] = acc ? db.f()[j] + sb : sb;
   }
 }
-__device__ void op_colsum(const Ctx& c) {
+__device__ __noinline__ void op_colsum(const Ctx& c) {
   View x = c.buf(0), out = c.buf(1); int R = c.i(2), c0 = c.i(3), c1 = c.i(4), acc = c.i(5);
   for (int j = c0 + tid(); j < c1; j += KVM_THREADS) {
     float s = 0.f; for (int r = 0; r < R; ++r) s += x.at(r, j);
     out.f()[j] = acc ? out.f()[j] + s : s;
   }
 }
-__device__ void op_head_rmsnorm(const Ctx& c) {   // RMSNorm per head slice of hd columns (Qwen3 q/k norm)
+__device__ __noinline__ void op_head_rmsnorm(const Ctx& c) {   // RMSNorm per head slice of hd columns (Qwen3 q/k norm)
   View x = c.buf(0), g = c.buf(1), o = c.buf(2); int r0 = c.i(3), r1 = c.i(4), H = c.i(5), hd = c.i(6); float eps = c.f(7);
   for (int rh = r0 * H + wave(); rh < r1 * H; rh += KVM_WAVES) {
     int r = rh / H, h = rh % H; float ss = 0.f;
@@ -249,7 +249,7 @@ __device__ __forceinline__ void rope_sc(long long p, int i, int hd, float theta,
   float ang = (float)p * inv;
   sincosf(ang, &s, &co);
 }
-template <int SIGN> __device__ void op_rope(const Ctx& c) {
+template <int SIGN> __device__ __noinline__ void op_rope(const Ctx& c) {
   View x = c.buf(0), out = c.buf(1), pos = c.buf(2); int r0 = c.i(3), r1 = c.i(4), T = c.i(5), H = c.i(6), hd = c.i(7); float th = c.f(8);
   long long p0 = pos.ok() ? pos.i()[0] : 0; int half = hd / 2;
   for (long long e = tid(); e < (long long)(r1 - r0) * H * half; e += KVM_THREADS) {
@@ -262,7 +262,7 @@ template <int SIGN> __device__ void op_rope(const Ctx& c) {
 }
 
 // ---------------------------------------------------------------------------------------------- softmax / loss
-__device__ void op_softmax_rows_fwd(const Ctx& c) {
+__device__ __noinline__ void op_softmax_rows_fwd(const Ctx& c) {
   View x = c.buf(0), o = c.buf(1); int r0 = c.i(2), r1 = c.i(3), d = c.i(4); float sc = c.f(5);
   for (int r = r0 + wave(); r < r1; r += KVM_WAVES) {
     float m = -INFINITY; for (int j = lane(); j < d; j += 64) m = fmaxf(m, x.at(r, j) * sc);
@@ -272,7 +272,7 @@ __device__ void op_softmax_rows_fwd(const Ctx& c) {
     for (int j = lane(); j < d; j += 64) o.f()[(long long)r * o.cols + j] = __expf(x.at(r, j) * sc - m) / z;
   }
 }
-__device__ void op_softmax_rows_bwd(const Ctx& c) {
+__device__ __noinline__ void op_softmax_rows_bwd(const Ctx& c) {
   View p = c.buf(0), dp = c.buf(1), dx = c.buf(2); int r0 = c.i(3), r1 = c.i(4), d = c.i(5), acc = c.i(7); float sc = c.f(6);
   for (int r = r0 + wave(); r < r1; r += KVM_WAVES) {
     float dot = 0.f; for (int j = lane(); j < d; j += 64) dot += p.at(r, j) * dp.at(r, j);
@@ -304,8 +304,8 @@ __device__ void ce_rows(const Ctx& c, View lg, View tg, View rl, View ls, View d
       dl.st((long long)r * dl.cols + j, ign ? 0.f : (__expf(lg.at(r, j) - lse) - (j == t ? 1.f : 0.f)) * f);
   }
 }
-__device__ void op_softmax_ce_fwd(const Ctx& c) { View n{}; ce_rows(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), n, c.i(4), c.i(5), c.i(6), c.i(7), 0.f, true, false); }
-__device__ void op_softmax_ce_reduce(const Ctx& c) {
+__device__ __noinline__ void op_softmax_ce_fwd(const Ctx& c) { View n{}; ce_rows(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), n, c.i(4), c.i(5), c.i(6), c.i(7), 0.f, true, false); }
+__device__ __noinline__ void op_softmax_ce_reduce(const Ctx& c) {
   View rl = c.buf(0), tg = c.buf(1), loss = c.buf(2); int N = c.i(3), ig = c.i(4);
   __shared__ double red[KVM_WAVES]; __shared__ float redc[KVM_WAVES];
   double s = 0.0; float cnt = 0.f;
@@ -313,11 +313,11 @@ __device__ void op_softmax_ce_reduce(const Ctx& c) {
   s = block_sum_d(s, red); cnt = block_sum(cnt, redc);
   if (tid() == 0) { int n = (int)cnt; loss.f()[0] = n ? (float)(s / n) : 0.f; loss.f()[1] = n ? (float)(1.0 / n) : 0.f; }
 }
-__device__ void op_softmax_ce_bwd(const Ctx& c) {
+__device__ __noinline__ void op_softmax_ce_bwd(const Ctx& c) {
   View n{}; float f = c.buf(3).f()[1] * c.f(9);
   ce_rows(c, c.buf(0), c.buf(1), n, c.buf(2), c.buf(4), c.i(5), c.i(6), c.i(7), c.i(8), f, false, true);
 }
-__device__ void op_softmax_ce_fused(const Ctx& c) {
+__device__ __noinline__ void op_softmax_ce_fused(const Ctx& c) {
   float f = (float)(1.0 / c.i(9)) * c.f(10);
   ce_rows(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.i(5), c.i(6), c.i(7), c.i(8), f, true, true);
 }
@@ -359,15 +359,15 @@ __device__ void adamw_body(const Ctx& c, View p, View g, View m, View v, View gs
     P[q] = pp; M[q] = mm; Vv[q] = vv;
   }
 }
-__device__ void op_adamw(const Ctx& c) { adamw_body(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.i(6), c.i(7), c.f(8), c.f(9), c.f(10), c.f(11), c.f(12)); }
-__device__ void op_adamw_lr(const Ctx& c) { adamw_body(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.i(6), c.i(7), c.buf(8).f()[0], c.f(9), c.f(10), c.f(11), c.f(12)); }
-__device__ void op_gradnorm_partial(const Ctx& c) {
+__device__ __noinline__ void op_adamw(const Ctx& c) { adamw_body(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.i(6), c.i(7), c.f(8), c.f(9), c.f(10), c.f(11), c.f(12)); }
+__device__ __noinline__ void op_adamw_lr(const Ctx& c) { adamw_body(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.i(6), c.i(7), c.buf(8).f()[0], c.f(9), c.f(10), c.f(11), c.f(12)); }
+__device__ __noinline__ void op_gradnorm_partial(const Ctx& c) {
   View g = c.buf(0), part = c.buf(1); __shared__ double red[KVM_WAVES];
   double s = 0.0; FLAT_FOR(i, c.i(3), c.i(4)) { double x = g.f()[i]; s += x * x; }
   s = block_sum_d(s, red);
   if (tid() == 0) part.f()[c.i(2)] = (float)s;
 }
-__device__ void op_gradnorm_finish(const Ctx& c) {
+__device__ __noinline__ void op_gradnorm_finish(const Ctx& c) {
   View part = c.buf(0), out = c.buf(2); int ns = c.i(1); float mx = c.f(3);
   if (tid() == 0) {
     double s = 0.0; for (int i = 0; i < ns; ++i) s += part.f()[i];
@@ -376,7 +376,7 @@ __device__ void op_gradnorm_finish(const Ctx& c) {
     out.f()[1] = n;
   }
 }
-__device__ void op_lr_schedule(const Ctx& c) {
+__device__ __noinline__ void op_lr_schedule(const Ctx& c) {
   View st = c.buf(0), lr = c.buf(1); int kind = c.i(2); float base = c.f(3); int wu = c.i(4), tot = c.i(5); float mr = c.f(6);
   if (tid() == 0) {
     int t = st.i()[0];
@@ -404,7 +404,7 @@ template <class PF, class PI> __device__ int row_argmax(const View& lg, int r, i
   for (int w = 1; w < KVM_WAVES; ++w) if (redv[w] > bv || (redv[w] == bv && redi[w] < bi)) { bv = redv[w]; bi = redi[w]; }
   return bi == 0x7FFFFFFF ? 0 : bi;
 }
-__device__ void op_argmax(const Ctx& c) {
+__device__ __noinline__ void op_argmax(const Ctx& c) {
   View lg = c.buf(0), out = c.buf(1); int r0 = c.i(2), r1 = c.i(3), V = c.i(4);
   __shared__ float rv[KVM_WAVES]; __shared__ int ri[KVM_WAVES];
   for (int r = r0; r < r1; ++r) { int a = row_argmax(lg, r, V, rv, ri); if (tid() == 0) out.i()[r] = a; }
@@ -419,7 +419,7 @@ __device__ void philox10(uint32_t c[4], uint32_t k0, uint32_t k1) {
 }
 // Sampling (registry text of op 57): temperature softmax over the top-k, inverse CDF in index order, Philox uniform.
 // Serial per row on thread 0 after a parallel threshold search; sampling is off the hot path.
-__device__ void op_sample(const Ctx& c) {
+__device__ __noinline__ void op_sample(const Ctx& c) {
   View lg = c.buf(0), out = c.buf(1), ctr = c.buf(2); int r0 = c.i(3), r1 = c.i(4), V = c.i(5); float temp = c.f(6); int topk = c.i(7), seed = c.i(8);
   __shared__ float rv[KVM_WAVES]; __shared__ int ri[KVM_WAVES]; __shared__ uint32_t s_thr;
   int cv = ctr.ok() ? ctr.i()[0] : 0;
@@ -451,7 +451,7 @@ __device__ void op_sample(const Ctx& c) {
 }
 
 // ---------------------------------------------------------------------------------------------- KV cache
-__device__ void op_kv_append(const Ctx& c) {
+__device__ __noinline__ void op_kv_append(const Ctx& c) {
   View kn = c.buf(0), vn = c.buf(1), kc = c.buf(2), vc = c.buf(3), lens = c.buf(4);
   int b0 = c.i(5), b1 = c.i(6), nn = c.i(7), Hkv = c.i(8), hd = c.i(9), Tmax = c.i(10);
   for (int b = b0; b < b1; ++b) { int L = lens.i()[b]; if (L < 0 || L + nn > Tmax) { if (tid() == 0) c.fail(KVM_ERR_OP_KVLEN, b, L); return; } }

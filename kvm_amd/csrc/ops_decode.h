@@ -56,7 +56,7 @@ __device__ __forceinline__ float dot8(const u16x8_t w, const LDS float* v) {
 }
 
 // Registry op 134. Each wave owns two weight rows at a time and keeps 16 loads of 16 bytes in flight per lane.
-__device__ void op_gemv_bf16(const Ctx& c) {
+__device__ __noinline__ void op_gemv_bf16(const Ctx& c) {
   View x = c.buf(0), x2 = c.buf(1), g = c.buf(2), w = c.buf(3), out = c.buf(4), res = c.buf(5);
   int n0 = c.i(6), n1 = c.i(7), K = c.i(8), pro = c.i(9); float eps = c.f(10);
   LDS float* vs = (LDS float*)c.smem; LDS float* red = vs + 2 * K;
@@ -116,7 +116,7 @@ __device__ void op_gemv_bf16(const Ctx& c) {
 // steps, so four lanes cover a 128-byte line; A uses the same k permutation, which leaves the dot products unchanged.
 // The four waves split K into quarters and their 16x16 partial tiles are summed in LDS (fixed order).
 constexpr int ROWS_KC = 2048;   // K chunk whose prologue vectors are staged in LDS at once
-__device__ void op_gemv_bf16_rows(const Ctx& c) {
+__device__ __noinline__ void op_gemv_bf16_rows(const Ctx& c) {
   View x = c.buf(0), x2 = c.buf(1), g = c.buf(2), w = c.buf(3), out = c.buf(4), res = c.buf(5);
   int n0 = c.i(6), n1 = c.i(7), K = c.i(8), M = c.i(9), pro = c.i(10); float eps = c.f(11);
   LDS uint16_t* vs = (LDS uint16_t*)c.smem;              // [16][ROWS_KC + 8] bf16

@@ -72,7 +72,7 @@ __device__ void f32_block(const Ctx& c, View A, View B, int ta, int tb, int m0, 
 __device__ __forceinline__ int tile_m(int fl) { return fl & 64 ? 256 : fl & 32 ? 128 : 64; }
 __device__ __forceinline__ int tile_n(int fl) { return (fl & 96) ? 128 : 64; }
 
-__device__ void op_matmul_tile(const Ctx& c) {
+__device__ __noinline__ void op_matmul_tile(const Ctx& c) {
   View A = c.buf(0), B = c.buf(1);
   int m0 = c.i(6), n0 = c.i(7), M = c.i(8), N = c.i(9), K = c.i(10), fl = c.i(11);
   Epi e{c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.f(12), fl & 4, fl & 8, fl & 512};
@@ -82,7 +82,7 @@ __device__ void op_matmul_tile(const Ctx& c) {
 }
 
 // SwiGLU epilogue wrappers: the raw tile lands in LDS, then the elementwise pass (registry ops 120 / 121).
-__device__ void op_matmul_tile_silu_mul(const Ctx& c) {
+__device__ __noinline__ void op_matmul_tile_silu_mul(const Ctx& c) {
   View A = c.buf(0), B = c.buf(1), out = c.buf(2), gate = c.buf(3), up = c.buf(4);
   int m0 = c.i(5), n0 = c.i(6), M = c.i(7), N = c.i(8), K = c.i(9), fl = c.i(10);
   Epi e{}; e.alpha = c.f(11);
@@ -98,7 +98,7 @@ __device__ void op_matmul_tile_silu_mul(const Ctx& c) {
     __syncthreads();
   }
 }
-__device__ void op_matmul_tile_silu_mul_bwd(const Ctx& c) {
+__device__ __noinline__ void op_matmul_tile_silu_mul_bwd(const Ctx& c) {
   View A = c.buf(0), B = c.buf(1), gate = c.buf(2), up = c.buf(3), dg = c.buf(4), du = c.buf(5);
   int m0 = c.i(6), n0 = c.i(7), M = c.i(8), N = c.i(9), K = c.i(10), fl = c.i(11);
   Epi e{}; e.alpha = c.f(12);
@@ -137,13 +137,35 @@ __device__ __forceinline__ u16x8_t load8(const View& X, long long base, int vali
 }
 
 // One operand tile of R rows x KT k values, staged to LDS as [row][k] with a padded row stride.
+//   trans == 0: element (r, k) at X[r*ld + k] (k contiguous): thread vectors run along k, one 16-byte LDS store each.
+//   trans == 1: element (r, k) at X[k*ld + r] (r contiguous): a vector holds 8 consecutive rows at one k; consecutive
+//     lanes take consecutive k so the eight 2-byte LDS stores of a vector hit consecutive addresses (no bank
+//     conflicts), at the price of 16-byte global loads from different rows (each 128-byte line is still read whole by
+//     the tile).
+// `fast` (uniform per task): bf16 storage, 16-byte aligned rows, the whole tile in range: every load is
+// unconditional, so all of a thread's loads are in flight together.
 template <int R, int KT> struct Stage {
   static constexpr int STRIDE = KT + 8;                   // elements; +16 B per row spreads rows over LDS banks
   static constexpr int VEC = R * KT / 8;                  // 8-element vectors per tile
   static constexpr int PER = (VEC + KVM_THREADS - 1) / KVM_THREADS;
   u16x8_t v[PER];
-  // trans == 0: element (r, k) at X[r*ld + k]; trans == 1: at X[k*ld + r].
-  __device__ void fetch(const View& X, int trans, int r0, int rows, int k0, int K) {
+  __device__ void fetch(const View& X, int trans, int r0, int rows, int k0, int K, bool fast) {
+    if (fast) {
+      const GLOBAL uint16_t* base = X.h();
+#pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const int idx = tid() + q * KVM_THREADS;
+        if (VEC % KVM_THREADS != 0 && idx >= VEC) break;
+        if (!trans) {
+          const int row = idx / (KT / 8), kv = idx % (KT / 8);
+          v[q] = *(const GLOBAL u16x8_t*)(base + (long long)(r0 + row) * X.cols + k0 + kv * 8);
+        } else {
+          const int k = idx % KT, rv = idx / KT;
+          v[q] = *(const GLOBAL u16x8_t*)(base + (long long)(k0 + k) * X.cols + r0 + rv * 8);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       int idx = tid() + q * KVM_THREADS;
@@ -153,7 +175,7 @@ template <int R, int KT> struct Stage {
         int valid = (r < rows) ? min(8, K - k) : 0;
         v[q] = load8(X, (long long)r * X.cols + k, valid);
       } else {
-        int k = idx / (R / 8), rv = idx % (R / 8), kk = k0 + k, r = r0 + rv * 8;
+        int k = idx % KT, rv = idx / KT, kk = k0 + k, r = r0 + rv * 8;
         int valid = (kk < K) ? min(8, rows - r) : 0;
         v[q] = load8(X, (long long)kk * X.cols + r, valid);
       }
@@ -163,12 +185,12 @@ template <int R, int KT> struct Stage {
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       int idx = tid() + q * KVM_THREADS;
-      if (idx >= VEC) break;
+      if (VEC % KVM_THREADS != 0 && idx >= VEC) break;
       if (!trans) {
         int row = idx / (KT / 8), kv = idx % (KT / 8);
         *(LDS u16x8_t*)(lds + row * STRIDE + kv * 8) = v[q];
       } else {
-        int k = idx / (R / 8), rv = idx % (R / 8);
+        int k = idx % KT, rv = idx / KT;
 #pragma unroll
         for (int i = 0; i < 8; ++i) lds[(rv * 8 + i) * STRIDE + k] = v[q][i];
       }
@@ -176,30 +198,37 @@ template <int R, int KT> struct Stage {
   }
 };
 
+// Whether an operand tile can take the unconditional fast path (see Stage).
+__device__ __forceinline__ bool fast_operand(const View& X, int trans, int r0, int R, int rows, int K, int KT) {
+  if (X.dtype != 2 || (X.cols & 7) || (((uintptr_t)X.p) & 15) || (K % KT)) return false;
+  return r0 + R <= rows && (!trans || (r0 & 7) == 0);
+}
+
 // TM x TN output tile at (m0, n0); waves in a 2 x 2 grid, each owning (TM/2) x (TN/2) as 32x32 MFMA blocks.
-template <int TM, int TN> __device__ void mfma_tile(const Ctx& c, View A, View B, int ta, int tb, int m0, int n0, int M, int N, int K,
-                                                    const Epi& e) {
+template <int TM, int TN> __device__ __noinline__ void mfma_tile(const Ctx& c, View A, View B, int ta, int tb, int m0, int n0, int M, int N,
+                                                                  int K, const Epi& e) {
   constexpr int KT = 32, WM = TM / 2, WN = TN / 2, BM = WM / 32, BN = WN / 32;
   typedef Stage<TM, KT> SA;
   typedef Stage<TN, KT> SB;
   LDS uint16_t* lA[2] = {(LDS uint16_t*)c.smem, (LDS uint16_t*)c.smem + TM * SA::STRIDE};
   LDS uint16_t* lB[2] = {lA[1] + TM * SA::STRIDE, lA[1] + TM * SA::STRIDE + TN * SB::STRIDE};
   const int wm0 = (wave() >> 1) * WM, wn0 = (wave() & 1) * WN, l = lane();
+  const bool fa = fast_operand(A, ta, m0, TM, M, K, KT), fb = fast_operand(B, !tb, n0, TN, N, K, KT);
   f32x16 acc[BM][BN];
 #pragma unroll
   for (int i = 0; i < BM; ++i)
 #pragma unroll
     for (int j = 0; j < BN; ++j) acc[i][j] = f32x16{};
   SA sa; SB sb;
-  sa.fetch(A, ta, m0, M, 0, K);
-  sb.fetch(B, !tb, n0, N, 0, K);
+  sa.fetch(A, ta, m0, M, 0, K, fa);
+  sb.fetch(B, !tb, n0, N, 0, K, fb);
   __syncthreads();                        // LDS may still be read by the previous tile / task
   sa.store(lA[0], ta); sb.store(lB[0], !tb);
   __syncthreads();
   int buf = 0;
   for (int k0 = 0; k0 < K; k0 += KT) {
     bool more = k0 + KT < K;
-    if (more) { sa.fetch(A, ta, m0, M, k0 + KT, K); sb.fetch(B, !tb, n0, N, k0 + KT, K); }
+    if (more) { sa.fetch(A, ta, m0, M, k0 + KT, K, fa); sb.fetch(B, !tb, n0, N, k0 + KT, K, fb); }
     __builtin_amdgcn_sched_barrier(0);     // the next slab's loads are in flight during this slab's MFMAs
 #pragma unroll
     for (int kk = 0; kk < KT; kk += 16) {
@@ -231,7 +260,7 @@ template <int TM, int TN> __device__ void mfma_tile(const Ctx& c, View A, View B
 
 // Note on operand orientation: the LDS tile of B is [n][k]. B stored [N,K] (flag 2) is read row-contiguous (trans 0 in
 // Stage terms); B stored [K,N] is read column-wise (trans 1).
-__device__ void op_matmul_tile_bf16(const Ctx& c) {
+__device__ __noinline__ void op_matmul_tile_bf16(const Ctx& c) {
   View A = c.buf(0), B = c.buf(1);
   int m0 = c.i(6), n0 = c.i(7), M = c.i(8), N = c.i(9), K = c.i(10), fl = c.i(11);
   Epi e{c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.f(12), fl & 4, fl & 8, fl & 512};
@@ -239,7 +268,7 @@ __device__ void op_matmul_tile_bf16(const Ctx& c) {
   else if (fl & 32) mfma_tile<128, 128>(c, A, B, fl & 1, (fl & 2) != 0, m0, n0, M, N, K, e);
   else mfma_tile<64, 64>(c, A, B, fl & 1, (fl & 2) != 0, m0, n0, M, N, K, e);
 }
-__device__ void op_matmul_mma_bf16(const Ctx& c) {
+__device__ __noinline__ void op_matmul_mma_bf16(const Ctx& c) {
   View A = c.buf(0), B = c.buf(1);
   int m0 = c.i(6), n0 = c.i(7), M = c.i(8), N = c.i(9), K = c.i(10), fl = c.i(11);
   Epi e{c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.f(12), fl & 4, fl & 8, fl & 512};

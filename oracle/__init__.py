@@ -38,7 +38,7 @@ def lib():
         _lib = ctypes.CDLL(str(LIB))
         P = ctypes.c_void_p
         _lib.orc_run.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P,
-                                 ctypes.c_int, P, P, ctypes.c_int, ctypes.c_char_p, ctypes.c_int]
+                                 ctypes.c_int, P, P, ctypes.c_int, P, ctypes.c_char_p, ctypes.c_int]
         _lib.orc_run.restype = ctypes.c_int
         _lib.orc_seeded.argtypes = [P, ctypes.c_longlong, ctypes.c_ulonglong, ctypes.c_int, ctypes.c_float, ctypes.c_float]
     return _lib
@@ -72,6 +72,7 @@ def run(bundle, buffers=None, limit=0):
         rarr[i] = OrcRead(r['task'], r['var'], 0 if r['policy'] == 'exact' else 1, r['version'])
     observed = np.zeros(max(1, len(reads)), np.int32)
     order = np.full(b.ntasks, -1, np.int32)
+    dur = np.zeros(b.ntasks, np.float32)
     err = ctypes.create_string_buffer(512)
     tasks = np.ascontiguousarray(b.tasks, np.int32)
     succ = np.ascontiguousarray(b.succ, np.int32) if b.succ.size else np.zeros(1, np.int32)
@@ -79,12 +80,22 @@ def run(bundle, buffers=None, limit=0):
     t0 = time.perf_counter()
     rc = lib().orc_run(tasks.ctypes.data, b.ntasks, succ.ctypes.data, int(b.succ.size), args.ctypes.data, int(b.args.size),
                        obufs, len(buffers), versions.ctypes.data, nvars, rarr, len(reads), observed.ctypes.data,
-                       order.ctypes.data, limit, err, 512)
+                       order.ctypes.data, limit, dur.ctypes.data, err, 512)
     dt = time.perf_counter() - t0
     if rc:
         raise OracleError(err.value.decode())
     return {'buffers': buffers, 'versions': {v['name']: int(versions[v['id']]) for v in meta['variables']},
-            'order': order, 'observed': observed[:len(reads)].tolist(), 'seconds': dt}
+            'order': order, 'observed': observed[:len(reads)].tolist(), 'seconds': dt, 'task_us': dur}
+
+
+def materialize(meta_buf, init=None, root=None):
+    """Initial contents of a bundle buffer like kvm_amd.bundle.materialize, with the seeded generator in C (fast)."""
+    from kvm_amd import bundle as bl
+    init = init or meta_buf['init']
+    if init['kind'] != 'seeded':
+        return bl.materialize({**meta_buf, 'init': init}, root)
+    v = seeded(meta_buf['rows'] * meta_buf['cols'], init['seed'], init['draws'], init['bias'], init['coef'])
+    return bl.bf16_round(v) if meta_buf['dtype'] == bl.DT_BF16 else v
 
 
 def seeded(n, seed, draws, bias, coef):

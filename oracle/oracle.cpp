@@ -20,6 +20,7 @@
 #include <cstdio>
 #include <cstring>
 #include <algorithm>
+#include <chrono>
 #include <set>
 #include <string>
 #include <vector>
@@ -673,7 +674,7 @@ typedef struct OrcRead { int32_t task, var, policy, version; } OrcRead;   // pol
 // order[i] = the i-th task run; observed[r] = version of reads[r].var when reads[r].task started.
 int orc_run(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs,
             OrcBuf* bufs, int nbufs, int32_t* versions, int nvars, const OrcRead* reads, int nreads, int32_t* observed,
-            int32_t* order, int limit, char* err, int errlen) {
+            int32_t* order, int limit, float* dur_us, char* err, int errlen) {
   std::vector<int> indeg(ntasks);
   std::vector<std::vector<int>> reads_of(ntasks);
   for (int r = 0; r < nreads; ++r) if (reads[r].task >= 0 && reads[r].task < ntasks) reads_of[reads[r].task].push_back(r);
@@ -708,7 +709,9 @@ int orc_run(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedge
       OpFn fn = find_op(d.op_id);
       if (!fn) fail("operator not supported by the oracle");
       Ctx c{(OBuf*)bufs, nbufs, args + d.args_off};
+      auto t0 = std::chrono::steady_clock::now();
       fn(c);
+      if (dur_us) dur_us[cur] = std::chrono::duration<float, std::micro>(std::chrono::steady_clock::now() - t0).count();
       order[done++] = cur;
       if (d.pub_var >= 0) {
         if (versions[d.pub_var] + 1 != d.pub_ver) fail("publish order broken");

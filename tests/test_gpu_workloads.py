@@ -41,3 +41,58 @@ def test_qwen3_decode_tiny(batch):
     assert np.array_equal(ex.read('tok'), ref['buffers'][names.index('tok')])
     assert np.array_equal(ex.read('lens'), ref['buffers'][names.index('lens')])
     ex.close()
+
+
+# Tiny GPT (exact shape, 10 steps, f32). The device's GEMMs are exact fp32 (FMA) where the
+# oracle rounds every product and partial sum to f32, so all buffers - activations, gradients, weights and AdamW
+# moments after 10 steps - are held to the reference's own "precise" tolerance (tests/gptdiff/golden_check.py:28-31:
+# TOL_PRECISE 2e-4, TOL_LOSS 1e-3).
+TOL_GPT_F32 = 2e-4
+
+
+def test_tiny_gpt_f32_10_steps():
+    from kvm_amd.workloads import gpt
+    print('tiny gpt f32, 10 steps', flush=True)
+    w = gpt.build(gpt.GPTConfig.tiny())
+    lb, ref, ex = _run_both(w)
+    check_schedule(ex, lb)
+    names = [m['name'] for m in lb.metadata['buffers']]
+    loss, want = ex.read('loss'), ref['buffers'][names.index('loss')]
+    assert abs(loss[0] - want[0]) <= 1e-3 * abs(want[0]), (loss, want)
+    # The key bias has an exactly zero gradient (softmax is invariant to the shift q.b_k it adds to every score of a
+    # query), so d.bk holds rounding noise on both sides and AdamW turns noise into +-lr steps: bk and its moments are
+    # compared by magnitude only, the rest to the tolerance.
+    kbias = [m['name'] for m in lb.metadata['buffers'] if m['name'].split('.')[-2:-1] == ['bk'] or m['name'].startswith('bk.')]
+    bad = compare_run(ex, lb.metadata, ref, tol_f32=TOL_GPT_F32, skip=tuple(kbias))
+    assert not bad, bad
+    for l in range(2):
+        assert np.abs(ex.read(f'd.bk.{l}')).max() <= 1e-4 * np.abs(ex.read(f'd.bq.{l}')).max()
+        assert np.abs(ex.read(f'bk.{l}')).max() <= 10 * 1e-3 + 1e-6     # at most 10 steps of lr
+    ex.close()
+
+
+# Small bf16-storage GPT, one step: weight gradients against the oracle. Bound: twice the reference's own bf16s
+# step-1 gradient deviation from fp64 (1.69e-2 worst relative L2, README.md:212 of the reference) = 3.4e-2.
+TOL_GPT_BF16_GRAD = 3.4e-2
+
+
+def test_small_gpt_bf16_step():
+    from kvm_amd.workloads import gpt
+    print('small gpt bf16, 1 step', flush=True)
+    c = gpt.GPTConfig(layers=2, d=128, heads=2, T=128, vocab=512, ffn=256, batch=2, steps=1, tasks_target=32)
+    w = gpt.build(c)
+    lb, ref, ex = _run_both(w)
+    check_schedule(ex, lb)
+    names = [m['name'] for m in lb.metadata['buffers']]
+    from gpu_check import rel_l2
+    loss, want = ex.read('loss'), ref['buffers'][names.index('loss')]
+    assert abs(loss[0] - want[0]) <= 1e-2 * abs(want[0]), (loss, want)
+    worst = []
+    for m, r in zip(lb.metadata['buffers'], ref['buffers']):
+        if m['name'].startswith('d.') and not m['name'].startswith('d.bk.'):
+            e = rel_l2(ex.read(m['name']), r)
+            worst.append((e, m['name']))
+    worst.sort(reverse=True)
+    print('worst gradient rel L2', worst[:3])
+    assert worst[0][0] <= TOL_GPT_BF16_GRAD, worst[:5]
+    ex.close()

@@ -30,14 +30,14 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def build_executor(w, trace=False):
+def build_executor(w, trace=False, blocks=0):
     from kvm_amd import bundle as bl
     from kvm_amd import compiler
     from kvm_amd.executor import Executor
     t0 = time.perf_counter()
     lb = bl.load(compiler.compile_spec(w.spec))
     t1 = time.perf_counter()
-    ex = Executor(num_vars=max(1, len(lb.metadata['variables'])), trace=trace, timeout_s=60.0)
+    ex = Executor(num_vars=max(1, len(lb.metadata['variables'])), trace=trace, timeout_s=60.0, blocks=blocks)
     for m in lb.metadata['buffers']:
         ex.add_buffer(m['name'], m['rows'], m['cols'], m['dtype'], init=w.init_override.get(m['name'], m['init']))
     for v in lb.metadata['variables']:

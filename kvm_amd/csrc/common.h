@@ -42,6 +42,7 @@ struct KvmCounters {
 
 // One ready queue. Head (consumer tickets) and tail (producer slots) sit on separate 128-byte lines.
 #define KVM_MAX_QUEUES 8
+#define KVM_OPMASK_IDS 1024
 struct KvmQueue {
   unsigned head; int pad0[31];
   int tail; int pad1[31];
@@ -64,6 +65,7 @@ struct KvmDevState {
   int* park_head;             // [nvars] park list heads, -1 empty
   KvmCounters* cnt;
   KvmTrace* trace;            // [ntasks] or null
+  const unsigned* opmask;     // [KVM_OPMASK_IDS] bit k set when argument word k of the operator is a buffer index
   int ntasks, nbufs, nvars, trace_on, nq, qcap, grid;
   unsigned long long timeout_ticks;   // stall timeout in wall_clock64 ticks (100 MHz)
 };
@@ -112,16 +114,14 @@ struct View {
 };
 
 struct Ctx {
-  const MvmBuf* bufs;
+  const LDS View* views;     // buffer arguments of the task, resolved from the buffer table by the dispatcher (in LDS)
   const LDS int32_t* a;      // argument words (in LDS)
   LDS char* smem;            // KVM_LDS_BYTES of LDS
   KvmCounters* cnt;
   int slot;
   __device__ View buf(int k) const {
-    int idx = a[k];
-    if (idx < 0) return View{nullptr, 0, 0, 0};
-    const MvmBuf& b = bufs[idx];
-    return View{b.p, b.rows, b.cols, b.dtype};
+    if (a[k] < 0) return View{nullptr, 0, 0, 0};
+    return View{views[k].p, views[k].rows, views[k].cols, views[k].dtype};
   }
   __device__ int i(int k) const { return a[k]; }
   __device__ float f(int k) const { return __int_as_float(a[k]); }

@@ -169,6 +169,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
   __shared__ int s_slot;
   __shared__ int32_t s_args[KVM_MAX_ARGS];
   __shared__ MvmTaskDesc s_desc;
+  __shared__ View s_view[KVM_MAX_ARGS];
   const int t = threadIdx.x;
   for (;;) {
     if (t == 0) {
@@ -207,7 +208,15 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
     if (t < 16) ((int32_t*)&s_desc)[t] = ((const int32_t*)&S.tasks[slot])[t];
     __syncthreads();
     const int op = s_desc.op_id;
-    if (t < s_desc.args_words && t < KVM_MAX_ARGS) s_args[t] = S.args[s_desc.args_off + t];
+    if (t < s_desc.args_words && t < KVM_MAX_ARGS) {
+      // argument words, and for buffer arguments the buffer's view, all fetched in one parallel round trip
+      const int w = S.args[s_desc.args_off + t];
+      s_args[t] = w;
+      if (w >= 0 && (unsigned)op < KVM_OPMASK_IDS && ((S.opmask[op] >> t) & 1u)) {
+        const MvmBuf& b = S.bufs[w];
+        s_view[t] = View{b.p, b.rows, b.cols, b.dtype};
+      }
+    }
     if (t == 0 && S.trace_on) {
       KvmTrace& tr = S.trace[slot];
       tr.start = wall_clock64();
@@ -226,7 +235,8 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
       }
     }
     __syncthreads();
-    Ctx c{S.bufs, (const LDS int32_t*)s_args, (LDS char*)smem, S.cnt, slot};
+    Ctx c{(const LDS View*)s_view, (const LDS int32_t*)s_args, (LDS char*)smem, S.cnt, slot};
+    KVM_PT(6);
     dispatch(op, c);
     __syncthreads();
     // Completion. Waves that touch successors first make this task's stores agent-visible (release fence: the
@@ -378,6 +388,7 @@ struct KvmExec {
   MvmTaskDesc* d_tasks = nullptr; int32_t *d_succ = nullptr, *d_args = nullptr; MvmBuf* d_bufs = nullptr;
   int *d_indeg = nullptr, *d_ready = nullptr, *d_state = nullptr, *d_park_next = nullptr, *d_version = nullptr, *d_park_head = nullptr;
   int *d_base = nullptr, *d_roots = nullptr;
+  unsigned* d_opmask = nullptr;
   KvmCounters* d_cnt = nullptr; KvmTrace* d_trace = nullptr;
   KvmQueue* d_queues = nullptr; int *d_qcount = nullptr, *d_done_blk = nullptr;
   KvmDevState S{};
@@ -427,7 +438,7 @@ void kvm_destroy(KvmExec* ex) {
   for (auto& b : ex->bufs) hipFree(b.p);
   void* ptrs[] = {ex->d_tasks, ex->d_succ, ex->d_args, ex->d_bufs, ex->d_indeg, ex->d_ready, ex->d_state, ex->d_park_next,
                   ex->d_version, ex->d_park_head, ex->d_base, ex->d_roots, ex->d_cnt, ex->d_trace, ex->d_queues, ex->d_qcount,
-                  ex->d_done_blk};
+                  ex->d_done_blk, ex->d_opmask};
   for (void* q : ptrs) if (q) hipFree(q);
   if (ex->ev0) hipEventDestroy(ex->ev0);
   if (ex->ev1) hipEventDestroy(ex->ev1);
@@ -545,6 +556,13 @@ static int do_upload(KvmExec* ex) {
   HIPCK(upload(&ex->d_args, ex->args, ex->stream));
   HIPCK(upload(&ex->d_bufs, table, ex->stream));
   HIPCK(upload(&ex->d_roots, ex->roots, ex->stream));
+  std::vector<unsigned> opmask(KVM_OPMASK_IDS, 0u);     // buffer-argument positions of every registry operator
+  for (const kvmv::OpSig& o : kvmv::kRegistry) {
+    if (o.id < 0 || o.id >= KVM_OPMASK_IDS) continue;
+    std::vector<kvmv::ArgInfo> a = kvmv::parse_sig(o.sig);
+    for (size_t k = 0; k < a.size() && k < 32; ++k) if (a[k].type == 0) opmask[o.id] |= 1u << k;
+  }
+  HIPCK(upload(&ex->d_opmask, opmask, ex->stream));
   HIPCK(hipMalloc(&ex->d_indeg, n * sizeof(int)));
   const int nq = std::max(1, std::min(KVM_MAX_QUEUES, ex->grid));
   const int qcap = (n + nq - 1) / nq;
@@ -565,7 +583,7 @@ static int do_upload(KvmExec* ex) {
   S.tasks = ex->d_tasks; S.succ = ex->d_succ; S.args = ex->d_args; S.bufs = ex->d_bufs;
   S.indeg = ex->d_indeg; S.ready = ex->d_ready; S.state = ex->d_state; S.park_next = ex->d_park_next;
   S.version = ex->d_version; S.park_head = ex->d_park_head; S.cnt = ex->d_cnt; S.trace = ex->d_trace;
-  S.queues = ex->d_queues; S.qcount = ex->d_qcount; S.done_blk = ex->d_done_blk;
+  S.queues = ex->d_queues; S.qcount = ex->d_qcount; S.done_blk = ex->d_done_blk; S.opmask = ex->d_opmask;
   S.ntasks = n; S.nbufs = (int)ex->bufs.size(); S.nvars = nv; S.trace_on = ex->cfg.trace_on ? 1 : 0;
   S.nq = nq; S.qcap = qcap; S.grid = ex->grid;
   S.timeout_ticks = ex->cfg.timeout_us * 100ull;   // wall_clock64 runs at 100 MHz on gfx950

@@ -120,159 +120,508 @@ __device__ __noinline__ void op_matmul_tile_silu_mul_bwd(const Ctx& c) {
 }
 
 // ---------------------------------------------------------------------------------------------- bf16 MFMA engine
-// Loads 8 consecutive elements (along the operand's contiguous dimension) as bf16 bits; out-of-range -> 0.
-__device__ __forceinline__ u16x8_t load8(const View& X, long long base, int valid) {
+// Layout and schedule (one workgroup = four wave64s; waves in a 2 x 2 grid, each owning (TM/2) x (TN/2) of the tile):
+//   * K advances in slabs of GK = 64. Each operand slab sits in LDS as [row][k] (row = m for A, n for B) with a row
+//     stride of GS = 72 elements, and the eight 16-byte k-chunks of a row are XOR-swizzled by (row >> 4) & 7. With
+//     that, the MFMA fragment reads (16 consecutive rows, one chunk) and the stores of transposed operands (16 row
+//     groups, one chunk) both touch every LDS bank once.
+//   * Operands stored k-contiguous are fetched as 16-byte row pieces (8 lanes read one 128-byte row segment) and
+//     written to LDS unchanged. Operands stored row-contiguous ([K][rows]: A with flag 1, B without flag 2) are fetched
+//     as 16-byte pieces along the rows (a wave reads whole 128-byte lines); each thread fetches KPT consecutive k rows
+//     of one 8-row group and transposes them in registers, so it writes 8 rows x KPT k values with 8 LDS stores.
+//   * Two LDS buffers: while slab s is multiplied, slab s+1 is already loaded into registers; it is written to the
+//     other buffer afterwards and one barrier per slab separates the phases.
+//   * MFMA v_mfma_f32_32x32x16_bf16 with the B fragment as the first source, so the accumulator holds D^T: each lane
+//     owns 4 consecutive output columns of one row, and the epilogue reads and writes 4-element vectors.
+typedef uint16_t u16x4_t __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+#ifdef KVM_GEMM_PROF
+__device__ unsigned long long g_prof[1024][16];
+#define KVM_PT(i) do { if (tid() == 0) g_prof[blockIdx.x][i] = wall_clock64(); } while (0)
+#else
+#define KVM_PT(i) do { } while (0)
+#endif
+constexpr int GK = 64;
+constexpr int GS = GK + 8;
+
+// LDS element offset of k-chunk `ch` (8 k values) of tile row `row`.
+__device__ __forceinline__ int gsw(int row, int ch) { return row * GS + ((ch ^ ((row >> 4) & 7)) << 3); }
+
+// Element-wise form of load8 for tile edges (rows / K past the matrix, unaligned or short vectors).
+__device__ __noinline__ u16x8_t load8_tail(const View& X, long long base, int valid) {
   u16x8_t r;
+  for (int i = 0; i < 8; ++i) r[i] = i < valid ? (X.dtype == 2 ? X.h()[base + i] : f2bf(X.f()[base + i])) : (uint16_t)0;
+  return r;
+}
+// 8 consecutive elements (along X's contiguous dimension) as bf16 bits; elements past `valid` read as 0.
+__device__ __forceinline__ u16x8_t load8(const View& X, long long base, int valid) {
   if (valid >= 8 && (base & 7) == 0) {
     if (X.dtype == 2) return *(const GLOBAL u16x8_t*)(X.h() + base);
     const GLOBAL f32x4n* p = (const GLOBAL f32x4n*)(X.f() + base);
     f32x4n a = p[0], b = p[1];
-    r[0] = f2bf(a.x); r[1] = f2bf(a.y); r[2] = f2bf(a.z); r[3] = f2bf(a.w);
-    r[4] = f2bf(b.x); r[5] = f2bf(b.y); r[6] = f2bf(b.z); r[7] = f2bf(b.w);
-    return r;
+    return u16x8_t{f2bf(a.x), f2bf(a.y), f2bf(a.z), f2bf(a.w), f2bf(b.x), f2bf(b.y), f2bf(b.z), f2bf(b.w)};
   }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = i < valid ? (X.dtype == 2 ? X.h()[base + i] : f2bf(X.f()[base + i])) : (uint16_t)0;
-  return r;
+  return load8_tail(X, base, valid);
 }
 
-// One operand tile of R rows x KT k values, staged to LDS as [row][k] with a padded row stride.
-//   trans == 0: element (r, k) at X[r*ld + k] (k contiguous): thread vectors run along k, one 16-byte LDS store each.
-//   trans == 1: element (r, k) at X[k*ld + r] (r contiguous): a vector holds 8 consecutive rows at one k; consecutive
-//     lanes take consecutive k so the eight 2-byte LDS stores of a vector hit consecutive addresses (no bank
-//     conflicts), at the price of 16-byte global loads from different rows (each 128-byte line is still read whole by
-//     the tile).
-// `fast` (uniform per task): bf16 storage, 16-byte aligned rows, the whole tile in range: every load is
-// unconditional, so all of a thread's loads are in flight together.
-template <int R, int KT> struct Stage {
-  static constexpr int STRIDE = KT + 8;                   // elements; +16 B per row spreads rows over LDS banks
-  static constexpr int VEC = R * KT / 8;                  // 8-element vectors per tile
-  static constexpr int PER = (VEC + KVM_THREADS - 1) / KVM_THREADS;
-  u16x8_t v[PER];
-  __device__ void fetch(const View& X, int trans, int r0, int rows, int k0, int K, bool fast) {
-    if (fast) {
-      const GLOBAL uint16_t* base = X.h();
+// A view with every field made wave-uniform (scalar registers): the operand loads then address through buffer
+// descriptors in SGPRs and nothing is re-read from memory inside the K loop.
+__device__ __forceinline__ View uniform_view(const View& v) {
+  const uint64_t p = (uint64_t)(uintptr_t)v.p;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p), hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(p >> 32));
+  return View{(void*)(uintptr_t)(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(v.rows), __builtin_amdgcn_readfirstlane(v.cols),
+              __builtin_amdgcn_readfirstlane(v.dtype)};
+}
+__device__ __forceinline__ Epi uniform_epi(const Epi& e) {
+  return Epi{uniform_view(e.out), uniform_view(e.bias), uniform_view(e.res), uniform_view(e.pre),
+             __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(e.alpha))), __builtin_amdgcn_readfirstlane(e.accum), __builtin_amdgcn_readfirstlane(e.ge),
+             __builtin_amdgcn_readfirstlane(e.dg)};
+}
+// Raw buffer descriptor over `bytes` bytes from p (gfx9 word 3); loads past the range return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, long long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)min(bytes, 0x7fffffffll), 0x00020000);
+}
+
+// One operand slab: R tile rows x GK k values. NV 16-byte vectors per thread.
+//   KC (k-contiguous, element (r, k) at X[r*cols + k]): vector q of a thread is row idx/8, k-chunk idx%8 with
+//     idx = tid + 256q, so 8 lanes read one 128-byte row segment.
+//   row-contiguous (element (r, k) at X[k*cols + r]): a thread takes rows 8*(tid % MV) .. +8 at k rows
+//     KPT*(tid / MV) .. +KPT, so a wave reads whole lines along the rows.
+// The fast path (bf16, whole tile inside the matrix, K a whole number of slabs) loads through a buffer descriptor
+// with per-thread 32-bit offsets fixed for the task and a uniform per-slab offset.
+template <int R> struct GTile {
+  static constexpr int NV = R * GK / 8 / KVM_THREADS;    // R / 32
+  static constexpr int KPT = NV;                         // row-contiguous operands: k rows per thread
+  static constexpr int MV = R / 8;                       // row-contiguous operands: 8-row groups
+  static_assert(NV >= 2 && KPT * (KVM_THREADS / MV) == GK, "tile shape");
+  u16x8_t v[NV];
+  __amdgpu_buffer_rsrc_t rs;
+  int voff[NV];
+  template <bool KC> __device__ __forceinline__ void init_fast(const View& X, int r0) {
+    if constexpr (KC) {
+      const GLOBAL uint16_t* base = X.h() + (long long)r0 * X.cols;
+      rs = buf_rsrc((const void*)base, ((long long)X.rows - r0) * X.cols * 2);
 #pragma unroll
-      for (int q = 0; q < PER; ++q) {
+      for (int q = 0; q < NV; ++q) {
         const int idx = tid() + q * KVM_THREADS;
-        if (VEC % KVM_THREADS != 0 && idx >= VEC) break;
-        if (!trans) {
-          const int row = idx / (KT / 8), kv = idx % (KT / 8);
-          v[q] = *(const GLOBAL u16x8_t*)(base + (long long)(r0 + row) * X.cols + k0 + kv * 8);
-        } else {
-          const int k = idx % KT, rv = idx / KT;
-          v[q] = *(const GLOBAL u16x8_t*)(base + (long long)(k0 + k) * X.cols + r0 + rv * 8);
-        }
+        voff[q] = ((idx >> 3) * X.cols + (idx & 7) * 8) * 2;
       }
-      return;
-    }
+    } else {
+      const GLOBAL uint16_t* base = X.h() + r0;
+      rs = buf_rsrc((const void*)base, (long long)X.rows * X.cols * 2 - (long long)r0 * 2);
 #pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      int idx = tid() + q * KVM_THREADS;
-      if (idx >= VEC) break;
-      if (!trans) {
-        int row = idx / (KT / 8), kv = idx % (KT / 8), r = r0 + row, k = k0 + kv * 8;
-        int valid = (r < rows) ? min(8, K - k) : 0;
-        v[q] = load8(X, (long long)r * X.cols + k, valid);
-      } else {
-        int k = idx % KT, rv = idx / KT, kk = k0 + k, r = r0 + rv * 8;
-        int valid = (kk < K) ? min(8, rows - r) : 0;
-        v[q] = load8(X, (long long)kk * X.cols + r, valid);
+      for (int q = 0; q < NV; ++q) voff[q] = (((tid() / MV) * KPT + q) * X.cols + (tid() % MV) * 8) * 2;
+    }
+  }
+  template <bool KC> __device__ __forceinline__ void fetch_fast(int k0, int cols) {
+    const int so = KC ? k0 * 2 : k0 * cols * 2;
+#pragma unroll
+    for (int q = 0; q < NV; ++q) v[q] = (u16x8_t)__builtin_amdgcn_raw_buffer_load_b128(rs, voff[q], so, 0);
+  }
+  template <bool KC> __device__ __forceinline__ void fetch_any(const View& X, int r0, int rows, int k0, int K) {
+    if constexpr (KC) {
+#pragma unroll
+      for (int q = 0; q < NV; ++q) {
+        const int idx = tid() + q * KVM_THREADS, r = r0 + (idx >> 3), k = k0 + (idx & 7) * 8;
+        v[q] = load8(X, (long long)r * X.cols + k, r < rows ? min(8, K - k) : 0);
+      }
+    } else {
+      const int r = r0 + (tid() % MV) * 8, kb = k0 + (tid() / MV) * KPT;
+#pragma unroll
+      for (int q = 0; q < NV; ++q) {
+        const int k = kb + q;
+        v[q] = load8(X, (long long)k * X.cols + r, k < K ? min(8, rows - r) : 0);
       }
     }
   }
-  __device__ void store(LDS uint16_t* lds, int trans) const {
+  template <bool FAST, bool KC> __device__ __forceinline__ void fetch(const View& X, int r0, int rows, int k0, int K) {
+    if constexpr (FAST) fetch_fast<KC>(k0, X.cols);
+    else fetch_any<KC>(X, r0, rows, k0, K);
+  }
+  template <bool KC> __device__ __forceinline__ void store(LDS uint16_t* lds) const {
+    if constexpr (KC) {
 #pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      int idx = tid() + q * KVM_THREADS;
-      if (VEC % KVM_THREADS != 0 && idx >= VEC) break;
-      if (!trans) {
-        int row = idx / (KT / 8), kv = idx % (KT / 8);
-        *(LDS u16x8_t*)(lds + row * STRIDE + kv * 8) = v[q];
-      } else {
-        int k = idx % KT, rv = idx / KT;
+      for (int q = 0; q < NV; ++q) {
+        const int idx = tid() + q * KVM_THREADS;
+        *(LDS u16x8_t*)(lds + gsw(idx >> 3, idx & 7)) = v[q];
+      }
+    } else {
+      const int rg = (tid() % MV) * 8, kq = (tid() / MV) * KPT;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) lds[(rv * 8 + i) * STRIDE + k] = v[q][i];
+      for (int i = 0; i < 8; ++i) {
+        const int o = gsw(rg + i, kq >> 3) + (kq & 7);
+        if constexpr (KPT == 8) {
+          u16x8_t w;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) w[q] = v[q][i];
+          *(LDS u16x8_t*)(lds + o) = w;
+        } else if constexpr (KPT == 4) {
+          u16x4_t w;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) w[q] = v[q][i];
+          *(LDS u16x4_t*)(lds + o) = w;
+        } else {
+          u16x2_t w;
+          w[0] = v[0][i]; w[1] = v[1][i];
+          *(LDS u16x2_t*)(lds + o) = w;
+        }
       }
     }
   }
 };
 
-// Whether an operand tile can take the unconditional fast path (see Stage).
-__device__ __forceinline__ bool fast_operand(const View& X, int trans, int r0, int R, int rows, int K, int KT) {
-  if (X.dtype != 2 || (X.cols & 7) || (((uintptr_t)X.p) & 15) || (K % KT)) return false;
-  return r0 + R <= rows && (!trans || (r0 & 7) == 0);
+// 4 consecutive elements of a view at flat offset o (o % 4 == 0, cols % 4 == 0), widened to f32 / rounded on store.
+__device__ __forceinline__ f32x4n ld4(const View& X, long long o) {
+  if (X.dtype == 2) {
+    const u16x4_t h = *(const GLOBAL u16x4_t*)(X.h() + o);
+    return f32x4n{bf2f(h[0]), bf2f(h[1]), bf2f(h[2]), bf2f(h[3])};
+  }
+  return *(const GLOBAL f32x4n*)(X.f() + o);
+}
+__device__ __forceinline__ void st4(const View& X, long long o, f32x4n v) {
+  if (X.dtype == 2) *(GLOBAL u16x4_t*)(X.h() + o) = u16x4_t{f2bf(v.x), f2bf(v.y), f2bf(v.z), f2bf(v.w)};
+  else *(GLOBAL f32x4n*)(X.f() + o) = v;
 }
 
-// TM x TN output tile at (m0, n0); waves in a 2 x 2 grid, each owning (TM/2) x (TN/2) as 32x32 MFMA blocks.
-template <int TM, int TN> __device__ __noinline__ void mfma_tile(const Ctx& c, View A, View B, int ta, int tb, int m0, int n0, int M, int N,
-                                                                  int K, const Epi& e) {
-  constexpr int KT = 32, WM = TM / 2, WN = TN / 2, BM = WM / 32, BN = WN / 32;
-  typedef Stage<TM, KT> SA;
-  typedef Stage<TN, KT> SB;
-  LDS uint16_t* lA[2] = {(LDS uint16_t*)c.smem, (LDS uint16_t*)c.smem + TM * SA::STRIDE};
-  LDS uint16_t* lB[2] = {lA[1] + TM * SA::STRIDE, lA[1] + TM * SA::STRIDE + TN * SB::STRIDE};
+__device__ __noinline__ void epi_tail(Epi e, int N, int m, int n, f32x4n a) {
+  for (int i = 0; i < 4 && n + i < N; ++i) e.put(m, n + i, a[i]);
+}
+// Epilogue of 4 consecutive outputs (m, n..n+3), all inside the matrix and vector-aligned:
+// alpha -> bias -> dgelu(pre) | (pre, gelu) -> res -> accumulate.
+__device__ __forceinline__ void epi4_vec(const Epi& e, int m, int n, f32x4n a) {
+  const long long o = (long long)m * e.out.cols + n;
+  f32x4n v = a * e.alpha;
+  if (e.bias.ok()) v += ld4(e.bias, n);
+  if (e.dg) {
+    const f32x4n p = ld4(e.pre, (long long)m * e.pre.cols + n);
+    v.x *= gelu_grad_f(p.x); v.y *= gelu_grad_f(p.y); v.z *= gelu_grad_f(p.z); v.w *= gelu_grad_f(p.w);
+  } else {
+    if (e.pre.ok()) st4(e.pre, (long long)m * e.pre.cols + n, v);
+    if (e.ge) { v.x = gelu_f(v.x); v.y = gelu_f(v.y); v.z = gelu_f(v.z); v.w = gelu_f(v.w); }
+  }
+  if (e.res.ok()) v += ld4(e.res, (long long)m * e.res.cols + n);
+  if (e.accum) v += ld4(e.out, o);
+  st4(e.out, o, v);
+}
+__device__ __forceinline__ void epi4(const Epi& e, bool vec, int N, int m, int n, f32x4n a) {
+  if (!vec || n + 4 > N) epi_tail(e, N, m, n, a);
+  else epi4_vec(e, m, n, a);
+}
+
+// The arguments of a GEMM tile task (ops 114 and 122 share the layout a, b, out, bias, res, pre, m0, n0, M, N, K,
+// flags, alpha), read from the dispatcher's LDS copies and made wave-uniform, so nothing is re-read from memory later.
+struct GemmArgs { View A, B; Epi e; int m0, n0, M, N, K, fl; };
+__device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ GemmArgs gemm_args(const Ctx& c) {
+  const LDS View* vw = c.views;
+  const LDS int32_t* a = c.a;
+  auto V = [&](int k) {
+    const View v = a[k] < 0 ? View{nullptr, 0, 0, 0} : View{vw[k].p, vw[k].rows, vw[k].cols, vw[k].dtype};
+    return uniform_view(v);
+  };
+  const int fl = rfl(a[11]);
+  GemmArgs g;
+  g.A = V(0); g.B = V(1);
+  g.e = Epi{V(2), V(3), V(4), V(5), __int_as_float(rfl(a[12])), fl & 4, fl & 8, fl & 512};
+  g.m0 = rfl(a[6]); g.n0 = rfl(a[7]); g.M = rfl(a[8]); g.N = rfl(a[9]); g.K = rfl(a[10]); g.fl = fl;
+  return g;
+}
+
+// acc[i][j][r] = D^T: row m = l % 32 of block i, columns 8*(r/4) + 4*(l/32) + r%4 of block j. Whole, vector-aligned
+// tiles with a plain epilogue (out = acc) store straight from the accumulators: each lane writes 4 consecutive columns
+// of one row per register group. Every other tile goes through LDS (two halves, one per wave row), then every thread
+// applies the epilogue to 4-column pieces along the rows with bounds checks.
+template <int TM, int TN>
+__device__ __forceinline__ void gemm_store(const Ctx& c, const f32x16 (&acc)[TM / 64][TN / 64], const GemmArgs& g) {
+  constexpr int BM = TM / 64, BN = TN / 64, WM = TM / 2;
+  const int wm0 = (wave() >> 1) * WM, wn0 = (wave() & 1) * (TN / 2), l = lane();
+  const Epi& e = g.e;
+  const bool vec = (e.out.cols & 3) == 0 && (!e.res.ok() || (e.res.cols & 3) == 0) && (!e.pre.ok() || (e.pre.cols & 3) == 0);
+  const bool plain = !e.bias.ok() && !e.res.ok() && !e.pre.ok() && !e.accum && !e.ge && !e.dg && e.alpha == 1.0f;
+  if (plain && vec && g.m0 + TM <= g.M && g.n0 + TN <= g.N) {
+    const long long ld = e.out.cols;
+    if (e.out.dtype == 2) {
+      GLOBAL uint16_t* o = e.out.h() + (long long)(g.m0 + wm0 + (l & 31)) * ld + g.n0 + wn0 + 4 * (l >> 5);
+#pragma unroll
+      for (int i = 0; i < BM; ++i)
+#pragma unroll
+        for (int j = 0; j < BN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *(GLOBAL u16x4_t*)(o + i * 32 * ld + j * 32 + 8 * q) =
+                u16x4_t{f2bf(acc[i][j][4 * q]), f2bf(acc[i][j][4 * q + 1]), f2bf(acc[i][j][4 * q + 2]), f2bf(acc[i][j][4 * q + 3])};
+    } else {
+      GLOBAL float* o = e.out.f() + (long long)(g.m0 + wm0 + (l & 31)) * ld + g.n0 + wn0 + 4 * (l >> 5);
+#pragma unroll
+      for (int i = 0; i < BM; ++i)
+#pragma unroll
+        for (int j = 0; j < BN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *(GLOBAL f32x4n*)(o + i * 32 * ld + j * 32 + 8 * q) = f32x4n{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+    }
+    return;
+  }
+  constexpr int ES = TN + 4;                               // fp32 row stride: rows land 4 banks apart
+  static_assert(WM * ES * 4 <= KVM_LDS_BYTES, "LDS epilogue");
+  LDS float* et = (LDS float*)c.smem;
+  __syncthreads();                                         // operand stages are no longer read
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    if ((wave() >> 1) == half) {
+#pragma unroll
+      for (int i = 0; i < BM; ++i)
+#pragma unroll
+        for (int j = 0; j < BN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *(LDS f32x4n*)(et + (i * 32 + (l & 31)) * ES + wn0 + j * 32 + 8 * q + 4 * (l >> 5)) =
+                f32x4n{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+    }
+    __syncthreads();
+    const int mb = g.m0 + half * WM;
+    for (int q = tid(); q < WM * (TN / 4); q += KVM_THREADS) {
+      const int r = q / (TN / 4), cc = (q % (TN / 4)) * 4, m = mb + r, n = g.n0 + cc;
+      if (m < g.M && n < g.N) epi4(e, vec, g.N, m, n, *(const LDS f32x4n*)(et + r * ES + cc));
+    }
+    __syncthreads();
+  }
+}
+
+template <int TM, int TN, bool FAST, bool AKC, bool BKC>
+__device__ __noinline__ void gemm_loop(const Ctx& c) {
+  const GemmArgs g = gemm_args(c);
+  const View& A = g.A; const View& B = g.B;
+  const int m0 = g.m0, n0 = g.n0, M = g.M, N = g.N, K = g.K;
+  constexpr int WM = TM / 2, WN = TN / 2, BM = WM / 32, BN = WN / 32;
+  LDS uint16_t* lA0 = (LDS uint16_t*)c.smem;
+  LDS uint16_t* lB0 = lA0 + TM * GS;
+  LDS uint16_t* lA1 = lB0 + TN * GS;
+  LDS uint16_t* lB1 = lA1 + TM * GS;
   const int wm0 = (wave() >> 1) * WM, wn0 = (wave() & 1) * WN, l = lane();
-  const bool fa = fast_operand(A, ta, m0, TM, M, K, KT), fb = fast_operand(B, !tb, n0, TN, N, K, KT);
   f32x16 acc[BM][BN];
 #pragma unroll
   for (int i = 0; i < BM; ++i)
 #pragma unroll
     for (int j = 0; j < BN; ++j) acc[i][j] = f32x16{};
-  SA sa; SB sb;
-  sa.fetch(A, ta, m0, M, 0, K, fa);
-  sb.fetch(B, !tb, n0, N, 0, K, fb);
-  __syncthreads();                        // LDS may still be read by the previous tile / task
-  sa.store(lA[0], ta); sb.store(lB[0], !tb);
+  GTile<TM> ga;
+  GTile<TN> gb;
+  if constexpr (FAST) { ga.template init_fast<AKC>(A, m0); gb.template init_fast<BKC>(B, n0); }
+  ga.template fetch<FAST, AKC>(A, m0, M, 0, K);
+  gb.template fetch<FAST, BKC>(B, n0, N, 0, K);
+  __syncthreads();                         // the previous task may still read this LDS
+  ga.template store<AKC>(lA0);
+  gb.template store<BKC>(lB0);
   __syncthreads();
-  int buf = 0;
-  for (int k0 = 0; k0 < K; k0 += KT) {
-    bool more = k0 + KT < K;
-    if (more) { sa.fetch(A, ta, m0, M, k0 + KT, K, fa); sb.fetch(B, !tb, n0, N, k0 + KT, K, fb); }
-    __builtin_amdgcn_sched_barrier(0);     // the next slab's loads are in flight during this slab's MFMAs
+  const int nslab = (K + GK - 1) / GK;
+  for (int s = 0; s < nslab; ++s) {
+    LDS uint16_t* la = (s & 1) ? lA1 : lA0;
+    LDS uint16_t* lb = (s & 1) ? lB1 : lB0;
+    const bool more = s + 1 < nslab;
+    if (more) {
+      ga.template fetch<FAST, AKC>(A, m0, M, (s + 1) * GK, K);
+      gb.template fetch<FAST, BKC>(B, n0, N, (s + 1) * GK, K);
+    }
 #pragma unroll
-    for (int kk = 0; kk < KT; kk += 16) {
+    for (int kk = 0; kk < GK / 16; ++kk) {
+      const int ch = kk * 2 + (l >> 5);
       bf16x8 af[BM], bfr[BN];
 #pragma unroll
-      for (int i = 0; i < BM; ++i) af[i] = *(const LDS bf16x8*)(lA[buf] + (wm0 + i * 32 + (l & 31)) * SA::STRIDE + kk + (l >> 5) * 8);
+      for (int i = 0; i < BM; ++i) af[i] = *(const LDS bf16x8*)(la + gsw(wm0 + i * 32 + (l & 31), ch));
 #pragma unroll
-      for (int j = 0; j < BN; ++j) bfr[j] = *(const LDS bf16x8*)(lB[buf] + (wn0 + j * 32 + (l & 31)) * SB::STRIDE + kk + (l >> 5) * 8);
+      for (int j = 0; j < BN; ++j) bfr[j] = *(const LDS bf16x8*)(lb + gsw(wn0 + j * 32 + (l & 31), ch));
 #pragma unroll
       for (int i = 0; i < BM; ++i)
 #pragma unroll
-        for (int j = 0; j < BN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < BN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
     }
-    if (more) { sa.store(lA[buf ^ 1], ta); sb.store(lB[buf ^ 1], !tb); }
+    if (more) {
+      ga.template store<AKC>((s & 1) ? lA0 : lA1);
+      gb.template store<BKC>((s & 1) ? lB0 : lB1);
+    }
     __syncthreads();
-    buf ^= 1;
   }
-  // D layout of a 32x32 block: column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4 for accumulator register r.
+  gemm_store<TM, TN>(c, acc, g);
+}
+
+// ---------------------------------------------------------------------------------------------- direct-to-LDS pipeline
+// The path for whole bf16 tiles: operands go from HBM straight into LDS (buffer_load ... lds, 16 bytes per lane), so
+// no registers stage them and DNS stages of DK k values are in flight at once (prefetch distance DNS-1). A wave's
+// direct load writes 1 KiB of LDS, 16 bytes per lane in lane order; each lane picks its global source so that the
+// LDS image comes out in the layouts below.
+//   k-contiguous operand: [R][DK] bf16, 16-byte k-chunks XOR-swizzled by (row >> 2) & 3; fragments are one
+//     ds_read_b128 per lane (16 rows of one chunk touch every bank once).
+//   row-contiguous operand: [DK][R] bf16 (the global layout), 16-byte units XOR-swizzled per k row; fragments are two
+//     ds_read_b64_tr_b16 per lane. That instruction, in each group of 16 lanes, hands lane i slot j the 16-bit value
+//     at (address of lane 4j + i/4) + 2*(i%4): with lane i16 of a group addressing k row kb + i16/4 and rows
+//     mb + 4*(i16%4) .. +3, lane i16 receives rows mb + i16 at k = kb .. kb+3, i.e. an MFMA operand (8 k values of one
+//     row) from two reads.
+constexpr int DK = 32;
+constexpr int DNS = 4;
+
+__device__ __forceinline__ void wait_vm(int n) {       // s_waitcnt vmcnt(n), n <= 15 (other counters untouched)
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+    case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
+    case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;   // wait for everything (never less safe)
+  }
+}
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+template <int R, bool KC> struct DOp {
+  static constexpr int BLK = R * DK * 2 / 1024;         // 1 KiB blocks per stage
+  static constexpr int NL = BLK / KVM_WAVES;            // direct loads per thread per stage
+  static constexpr int UPR = KC ? DK / 8 : R / 8;       // 16-byte units per LDS row
+  static_assert(NL >= 1 && BLK % KVM_WAVES == 0, "tile shape");
+  __amdgpu_buffer_rsrc_t rs;
+  int voff[NL];
+  int sstep;
+  __device__ static __forceinline__ int kswz(int row) { return (row >> 2) & 3; }                       // k-contiguous
+  __device__ static __forceinline__ int rswz(int k) { return R >= 128 ? 4 * (k & 3) : 4 * ((k >> 1) & 1); }  // row-contiguous
+  __device__ __forceinline__ void init(const View& X, int r0) {
+    if constexpr (KC) {
+      rs = buf_rsrc((const void*)(X.h() + (long long)r0 * X.cols), ((long long)X.rows - r0) * X.cols * 2);
+      sstep = DK * 2;
+    } else {
+      rs = buf_rsrc((const void*)(X.h() + r0), (long long)X.rows * X.cols * 2 - (long long)r0 * 2);
+      sstep = DK * X.cols * 2;
+    }
+#pragma unroll
+    for (int q = 0; q < NL; ++q) {
+      const int u = 64 * (q * KVM_WAVES + wave()) + lane(), row = u / UPR, ph = u % UPR;
+      if constexpr (KC) voff[q] = (row * X.cols + 8 * (ph ^ kswz(row))) * 2;
+      else voff[q] = (row * X.cols + 8 * (ph ^ rswz(row))) * 2;
+    }
+  }
+  // Direct loads of stage s (k0 = s*DK) into `lds` (this operand's region of one stage buffer).
+  __device__ __forceinline__ void issue(LDS uint16_t* lds, int s) const {
+#pragma unroll
+    for (int q = 0; q < NL; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS void*)(lds + (q * KVM_WAVES + wave()) * 512), 16, voff[q], s * sstep, 0, 0);
+  }
+  // MFMA operand for the 32 tile rows rb.. and k16 step kk: 8 bf16 of row rb + l%32 at k = 16kk + 8(l/32) ...
+  __device__ __forceinline__ bf16x8 frag(const LDS uint16_t* lds, int rb, int kk) const {
+    const int l = lane();
+    if constexpr (KC) {
+      const int r = rb + (l & 31), ch = kk * 2 + (l >> 5);
+      return *(const LDS bf16x8*)(lds + r * DK + 8 * (ch ^ kswz(r)));
+    } else {
+      const int g = l >> 4, i = l & 15;
+      const int k = kk * 16 + 8 * (g >> 1) + (i >> 2), m = rb + 16 * (g & 1) + 4 * (i & 3);
+      const LDS uint16_t* p0 = lds + k * R + 8 * ((m >> 3) ^ rswz(k)) + (m & 7);
+      const s16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS s16x4_t*)p0);
+      const s16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS s16x4_t*)(p0 + 4 * R));
+      typedef short s16x8_t __attribute__((ext_vector_type(8)));
+      const s16x8_t v = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+      return (bf16x8)v;
+    }
+  }
+};
+
+template <int TM, int TN, bool AKC, bool BKC>
+__device__ __noinline__ void gemm_lds(const Ctx& c) {
+  constexpr int WM = TM / 2, WN = TN / 2, BM = WM / 32, BN = WN / 32;
+  constexpr int SA = TM * DK, SB = TN * DK, ST = SA + SB;    // elements per stage
+  static_assert(DNS * ST * 2 <= KVM_LDS_BYTES, "LDS");
+  const GemmArgs g = gemm_args(c);
+  const View& A = g.A; const View& B = g.B;
+  const int m0 = g.m0, n0 = g.n0, K = g.K;
+  LDS uint16_t* lds = (LDS uint16_t*)c.smem;
+#ifdef KVM_GEMM_PROF
+  unsigned long long pt[8]; pt[0] = wall_clock64(); pt[1] = __builtin_amdgcn_s_memtime();
+#endif
+  const int wm0 = (wave() >> 1) * WM, wn0 = (wave() & 1) * WN;
+  DOp<TM, AKC> da;
+  DOp<TN, BKC> db;
+  da.init(A, m0);
+  db.init(B, n0);
+  f32x16 acc[BM][BN];
 #pragma unroll
   for (int i = 0; i < BM; ++i)
 #pragma unroll
-    for (int j = 0; j < BN; ++j)
+    for (int j = 0; j < BN; ++j) acc[i][j] = f32x16{};
+  const int nst = K / DK;
+  __syncthreads();                                 // the previous task may still read this LDS
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), n = n0 + wn0 + j * 32 + (l & 31);
-        if (m < M && n < N) e.put(m, n, acc[i][j][r]);
-      }
+  for (int p = 0; p < DNS - 1; ++p)
+    if (p < nst) { da.issue(lds + p * ST, p); db.issue(lds + p * ST + SA, p); }
+  constexpr int NLS = DOp<TM, AKC>::NL + DOp<TN, BKC>::NL;  // direct loads per thread per stage
+  for (int s = 0; s < nst; ++s) {
+    wait_vm(min(DNS - 2, nst - 1 - s) * NLS);     // this thread's loads of stage s have landed
+    __syncthreads();                               // ... everyone's; and stage s-1 is no longer read
+    if (s + DNS - 1 < nst) {
+      LDS uint16_t* nb = lds + ((s + DNS - 1) % DNS) * ST;
+      da.issue(nb, s + DNS - 1);
+      db.issue(nb + SA, s + DNS - 1);
+    }
+    const LDS uint16_t* la = lds + (s % DNS) * ST;
+    const LDS uint16_t* lb = la + SA;
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk) {
+      bf16x8 af[BM], bfr[BN];
+#pragma unroll
+      for (int i = 0; i < BM; ++i) af[i] = da.frag(la, wm0 + i * 32, kk);
+#pragma unroll
+      for (int j = 0; j < BN; ++j) bfr[j] = db.frag(lb, wn0 + j * 32, kk);
+#pragma unroll
+      for (int i = 0; i < BM; ++i)
+#pragma unroll
+        for (int j = 0; j < BN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+    }
+  }
+#ifdef KVM_GEMM_PROF
+  pt[2] = wall_clock64(); pt[3] = __builtin_amdgcn_s_memtime();
+#endif
+  gemm_store<TM, TN>(c, acc, g);
+#ifdef KVM_GEMM_PROF
+  pt[4] = wall_clock64(); pt[5] = __builtin_amdgcn_s_memtime();
+  __syncthreads();
+  if (tid() == 0) { unsigned long long* o = (unsigned long long*)(g.e.out.h() + (long long)m0 * g.e.out.cols + n0); for (int i = 0; i < 6; ++i) o[i] = pt[i]; for (int i = 6; i < 16; ++i) o[i] = g_prof[blockIdx.x][i]; }
+#endif
 }
 
-// Note on operand orientation: the LDS tile of B is [n][k]. B stored [N,K] (flag 2) is read row-contiguous (trans 0 in
-// Stage terms); B stored [K,N] is read column-wise (trans 1).
+// Whether an operand slab sequence can use unconditional vector loads: bf16 storage, rows of whole 16-byte vectors,
+// the tile's rows inside the matrix and K a whole number of slabs.
+__device__ __forceinline__ bool gemm_fast_operand(const View& X, bool kc, int r0, int R, int rows, int K) {
+  if (X.dtype != 2 || (X.cols & 7) || (K % DK) || r0 + R > rows) return false;
+  if (kc) return (long long)R * X.cols * 2 + (long long)K * 2 < 0x7fffffffll;
+  return (r0 & 7) == 0 && (long long)K * X.cols * 2 < 0x7fffffffll;    // buffer offsets are 32-bit
+}
+
+template <int TM, int TN> __device__ __forceinline__ void mfma_tile(const Ctx& c) {
+  static_assert(2 * (TM + TN) * GS * 2 <= KVM_LDS_BYTES, "LDS");
+  const GemmArgs g = gemm_args(c);
+  const bool akc = !(g.fl & 1), bkc = (g.fl & 2) != 0;
+  const bool fast = gemm_fast_operand(g.A, akc, g.m0, TM, g.M, g.K) && gemm_fast_operand(g.B, bkc, g.n0, TN, g.N, g.K);
+  // One instantiation per operand orientation, so the slab prefetch is straight-line code (a runtime branch between
+  // orientations makes the compiler wait for the loads of one operand before issuing the other's).
+  if (fast) {
+    if (akc) { if (bkc) gemm_lds<TM, TN, true, true>(c); else gemm_lds<TM, TN, true, false>(c); }
+    else { if (bkc) gemm_lds<TM, TN, false, true>(c); else gemm_lds<TM, TN, false, false>(c); }
+  } else {
+    if (akc) { if (bkc) gemm_loop<TM, TN, false, true, true>(c); else gemm_loop<TM, TN, false, true, false>(c); }
+    else { if (bkc) gemm_loop<TM, TN, false, false, true>(c); else gemm_loop<TM, TN, false, false, false>(c); }
+  }
+}
+
 __device__ __noinline__ void op_matmul_tile_bf16(const Ctx& c) {
-  View A = c.buf(0), B = c.buf(1);
-  int m0 = c.i(6), n0 = c.i(7), M = c.i(8), N = c.i(9), K = c.i(10), fl = c.i(11);
-  Epi e{c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.f(12), fl & 4, fl & 8, fl & 512};
-  if (fl & 64) mfma_tile<256, 128>(c, A, B, fl & 1, (fl & 2) != 0, m0, n0, M, N, K, e);
-  else if (fl & 32) mfma_tile<128, 128>(c, A, B, fl & 1, (fl & 2) != 0, m0, n0, M, N, K, e);
-  else mfma_tile<64, 64>(c, A, B, fl & 1, (fl & 2) != 0, m0, n0, M, N, K, e);
+  const int fl = c.i(11);
+  if (fl & 64) mfma_tile<256, 128>(c);
+  else if (fl & 32) mfma_tile<128, 128>(c);
+  else mfma_tile<64, 64>(c);
 }
-__device__ __noinline__ void op_matmul_mma_bf16(const Ctx& c) {
-  View A = c.buf(0), B = c.buf(1);
-  int m0 = c.i(6), n0 = c.i(7), M = c.i(8), N = c.i(9), K = c.i(10), fl = c.i(11);
-  Epi e{c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.f(12), fl & 4, fl & 8, fl & 512};
-  mfma_tile<128, 256>(c, A, B, fl & 1, (fl & 2) != 0, m0, n0, M, N, K, e);
-}
+__device__ __noinline__ void op_matmul_mma_bf16(const Ctx& c) { mfma_tile<128, 256>(c); }
 
 }  // namespace kvm

@@ -1,0 +1,96 @@
+"""GPU parity of the bf16 GEMM tile operators (matmul_mma_bf16, op 122; matmul_tile_bf16, op 114) against the CPU oracle.
+
+Shapes are chosen so that both device paths run: whole tiles with K a multiple of 32 take the direct-to-LDS pipeline,
+partial tiles / odd K / f32 operands take the register-staged path. All four operand orientations (flags 1 and 2) and
+every epilogue (bias, GELU with pre-activation store, dGELU, residual, accumulate, alpha) are covered. The oracle
+rounds operands to bf16 and sums exact products in double (reference: runtime/ref_extra.py:312-331); the device sums
+in fp32 on MFMA, so outputs are held to a relative L2 error of 2e-5 (f32 outputs) or 4e-3 (bf16 outputs: one bf16
+ulp is 2^-8 relative).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from gpu_check import compare_run
+from kvm_amd import bundle as bl
+from kvm_amd import compiler
+from kvm_amd.executor import Executor
+from kvm_amd.workloads import Builder, Workload
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemm_graph(M, N, K, flags, op='matmul_mma_bf16', adt='bf16', bdt='bf16', odt='bf16', bias=False, res=False, pre=False,
+                alpha=1.0, tiles=(128, 256)):
+    b = Builder(7)
+    ta, tb = flags & 1, flags & 2
+    b.normal('A', K if ta else M, M if ta else K, adt, scale=1.0)
+    b.normal('B', N if tb else K, K if tb else N, bdt, scale=1.0)
+    b.normal('C', M, N, odt, scale=1.0)           # nonzero start: flag 4 accumulates into it
+    if bias:
+        b.normal('bias', 1, N, 'f32', scale=1.0)
+    if res:
+        b.normal('R', M, N, odt, scale=1.0)
+    if pre:
+        b.normal('P', M, N, odt, scale=1.0)
+    TM, TN = tiles
+    for m0 in range(0, M, TM):
+        for n0 in range(0, N, TN):
+            b.task(op, a='A', b='B', out='C', bias='bias' if bias else None, res='R' if res else None, pre='P' if pre else None,
+                   m0=m0, n0=n0, M=M, N=N, K=K, flags=flags, alpha=alpha)
+    return Workload(b.spec(), b.init_override)
+
+
+def _check(w, tol_f32=2e-5, tol_bf16=4e-3):
+    lb = bl.load(compiler.compile_spec(w.spec))
+    init = [oracle.materialize(m, w.init_override.get(m['name'])) for m in lb.metadata['buffers']]
+    ref = oracle.run(lb, [x.copy() for x in init])
+    ex = Executor.from_bundle(lb, buffers=init)
+    ex.run()
+    bad = compare_run(ex, lb.metadata, ref, tol_f32=tol_f32, tol_bf16=tol_bf16)
+    ex.close()
+    assert not bad, bad
+
+
+@pytest.mark.parametrize('flags', [0, 1, 2, 3])
+def test_mma_whole_tiles_all_orientations(flags):
+    print(f'mma whole tiles flags {flags}', flush=True)
+    _check(_gemm_graph(256, 512, 192, flags))
+
+
+@pytest.mark.parametrize('flags', [0, 3])
+def test_mma_f32_output_k4096(flags):
+    print(f'mma f32 out K=4096 flags {flags}', flush=True)
+    _check(_gemm_graph(128, 256, 4096, flags, odt='f32'))
+
+
+@pytest.mark.parametrize('flags,kw', [
+    (2, dict(bias=True)),
+    (2 | 8, dict(bias=True, pre=True)),           # GELU epilogue, pre-activation stored
+    (512, dict(pre=True)),                        # dGELU epilogue
+    (2, dict(bias=True, res=True)),
+    (4, dict()),                                  # accumulate into out
+    (1, dict(alpha=0.5, odt='f32')),
+])
+def test_mma_epilogues(flags, kw):
+    print(f'mma epilogue flags {flags} {kw}', flush=True)
+    _check(_gemm_graph(256, 256, 128, flags, **kw))
+
+
+@pytest.mark.parametrize('flags', [0, 1, 2, 3])
+def test_mma_edge_tiles(flags):
+    """Partial tiles in M and N, K not a multiple of the slab: the register-staged path."""
+    print(f'mma edge tiles flags {flags}', flush=True)
+    _check(_gemm_graph(200, 300, 100, flags, bias=True))
+
+
+def test_mma_f32_operands():
+    print('mma f32 operands', flush=True)
+    _check(_gemm_graph(128, 256, 64, 2, adt='f32', bdt='f32', odt='f32'))
+
+
+@pytest.mark.parametrize('tiles,fl', [((64, 64), 0), ((128, 128), 32), ((256, 128), 64)])
+def test_tile_bf16_sizes(tiles, fl):
+    print(f'tile_bf16 {tiles}', flush=True)
+    _check(_gemm_graph(256, 256, 96, fl | 2, op='matmul_tile_bf16', tiles=tiles, bias=True))
+    _check(_gemm_graph(256, 256, 128, fl | 1, op='matmul_tile_bf16', tiles=tiles))

@@ -29,6 +29,7 @@
 #include "ops_gemm.h"
 #include "ops_attn.h"
 #include "ops_decode.h"
+#include "ops_stream.h"
 #include "validate.h"
 
 using namespace kvm;
@@ -105,33 +106,33 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 32: op_embedding_fwd(c); break;
     case 33: op_embedding_bwd(c); break;
     case 34: op_matmul_tile(c); break;
-    case 35: op_norm_fwd<false>(c); break;
-    case 36: op_norm_fwd<true>(c); break;
-    case 37: op_norm_bwd_dx<false>(c); break;
-    case 38: op_norm_bwd_dx<true>(c); break;
-    case 39: op_norm_bwd_params(c); break;
+    case 35: if (!op_norm_fwd_fast<false>(c)) op_norm_fwd<false>(c); break;
+    case 36: if (!op_norm_fwd_fast<true>(c)) op_norm_fwd<true>(c); break;
+    case 37: if (!op_norm_bwd_dx_fast<false>(c)) op_norm_bwd_dx<false>(c); break;
+    case 38: if (!op_norm_bwd_dx_fast<true>(c)) op_norm_bwd_dx<true>(c); break;
+    case 39: if (!op_norm_bwd_params_fast(c)) op_norm_bwd_params(c); break;
     case 40: op_gelu_fwd(c); break;
     case 41: op_gelu_bwd(c); break;
     case 42: op_residual_add(c); break;
     case 43: op_rope<1>(c); break;
     case 44: op_rope<-1>(c); break;
     case 45: op_attn_fwd(c); break;
-    case 46: op_attn_bwd_delta(c); break;
+    case 46: if (!op_attn_bwd_delta_fast(c)) op_attn_bwd_delta(c); break;
     case 47: op_attn_bwd_dq(c); break;
     case 48: op_attn_bwd_dkv(c); break;
     case 49: op_kv_append(c); break;
     case 50: op_attn_decode(c); break;
-    case 51: op_softmax_ce_fwd(c); break;
+    case 51: op_softmax_ce_fwd_any(c); break;
     case 52: op_softmax_ce_reduce(c); break;
-    case 53: op_softmax_ce_bwd(c); break;
+    case 53: op_softmax_ce_bwd_any(c); break;
     case 54: op_adamw(c); break;
-    case 55: op_gradnorm_partial(c); break;
+    case 55: if (!op_gradnorm_partial_fast(c)) op_gradnorm_partial(c); break;
     case 56: op_gradnorm_finish(c); break;
     case 57: op_sample(c); break;
     case 58: op_argmax(c); break;
     case 59: op_zero_buf(c); break;
     case 60: op_counter_inc(c); break;
-    case 61: op_colsum(c); break;
+    case 61: if (!op_colsum_fast(c)) op_colsum(c); break;
     case 62: op_select_window(c); break;
     case 63: op_gather_rows(c); break;
     case 96: op_act_fwd(c); break;
@@ -143,7 +144,7 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 102: op_gather_rows_scaled(c); break;
     case 103: op_scatter_add_rows(c); break;
     case 104: op_row_dot(c); break;
-    case 113: op_round_bf16(c); break;
+    case 113: if (!op_round_bf16_fast(c)) op_round_bf16(c); break;
     case 114: op_matmul_tile_bf16(c); break;
     case 115: op_adamw_lr(c); break;
     case 116: op_lr_schedule(c); break;
@@ -154,7 +155,7 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 122: op_matmul_mma_bf16(c); break;
     case 123: op_sgd_range(c); break;
     case 126: op_round_tf32(c); break;
-    case 127: op_softmax_ce_fused(c); break;
+    case 127: op_softmax_ce_fused_any(c); break;
     case 134: op_gemv_bf16(c); break;
     case 135: op_attn_decode_part(c); break;
     case 136: op_attn_decode_merge(c); break;

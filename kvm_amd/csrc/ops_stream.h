@@ -1,0 +1,426 @@
+// Bandwidth-bound operators in streaming form: 16-byte loads, several loads in flight per lane, rows held in registers
+// between the passes that need them, and reductions in a fixed order (so results are reproducible run to run).
+// Each op_*_fast returns false when the shape or alignment is outside what it handles; the caller then runs the
+// element-wise body in ops_basic.h (same semantics).
+#pragma once
+#include "common.h"
+#include "ops_basic.h"
+#include "ops_gemm.h"
+
+namespace kvm {
+
+// 8 consecutive elements at flat offset o (o % 8 == 0) of a bf16 or f32 view, widened to f32.
+__device__ __forceinline__ void ld8(const View& X, long long o, float (&v)[8]) {
+  if (X.dtype == 2) {
+    const u16x8_t h = *(const GLOBAL u16x8_t*)(X.h() + o);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = bf2f(h[i]);
+  } else {
+    const f32x4n a = *(const GLOBAL f32x4n*)(X.f() + o), b = *(const GLOBAL f32x4n*)(X.f() + o + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+}
+__device__ __forceinline__ void st8(const View& X, long long o, const float (&v)[8]) {
+  if (X.dtype == 2) {
+    u16x8_t h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = f2bf(v[i]);
+    *(GLOBAL u16x8_t*)(X.h() + o) = h;
+  } else {
+    *(GLOBAL f32x4n*)(X.f() + o) = f32x4n{v[0], v[1], v[2], v[3]};
+    *(GLOBAL f32x4n*)(X.f() + o + 4) = f32x4n{v[4], v[5], v[6], v[7]};
+  }
+}
+__device__ __forceinline__ bool vec8_ok(const View& X) { return X.dtype != 1 && (X.cols % 8) == 0; }
+__device__ __forceinline__ bool vec4_ok(const View& X) { return X.dtype != 1 && (X.cols % 4) == 0; }
+
+// ---------------------------------------------------------------------------------------------- column reductions
+// Column sums over rows [0, R) for 64-column chunks: 8 lanes cover 64 columns of one row (8 columns each), so 32 row
+// slots run side by side; slot s takes rows s, s+32, ... (ascending, CR_UNROLL rows in flight) and the 32 slot partials
+// are added in slot order through LDS.
+constexpr int CR_UNROLL = 8;
+template <class Row> __device__ __forceinline__ void col_reduce(const Ctx& c, int R, int cb, int W, Row row, float (&a)[8], float (&b)[8]) {
+  const int vi = tid() & 7, slot = tid() >> 3;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = b[i] = 0.f;
+  if (vi * 8 >= W) return;
+  for (int r0 = slot; r0 < R; r0 += 32 * CR_UNROLL) {
+#pragma unroll
+    for (int u = 0; u < CR_UNROLL; ++u) {
+      const int r = r0 + 32 * u;
+      if (r < R) row(r, cb + vi * 8, a, b);
+    }
+  }
+}
+// Adds the 32 slot partials (LDS, [32][64] per quantity) in slot order; thread t < W gets column t's total.
+__device__ __forceinline__ float slot_total(const LDS float* part, int t) {
+  float s = 0.f;
+#pragma unroll 8
+  for (int k = 0; k < 32; ++k) s += part[k * 64 + t];
+  return s;
+}
+
+__device__ __noinline__ bool op_colsum_fast(const Ctx& c) {
+  const View x = c.buf(0), out = c.buf(1);
+  const int R = c.i(2), c0 = c.i(3), c1 = c.i(4), acc = c.i(5);
+  if (!vec8_ok(x) || (c0 % 8) || ((c1 - c0) % 8)) return false;
+  LDS float* part = (LDS float*)c.smem;
+  for (int cb = c0; cb < c1; cb += 64) {
+    const int W = min(64, c1 - cb);
+    float a[8], b[8];
+    col_reduce(c, R, cb, W, [&](int r, int col, float (&s)[8], float (&)[8]) {
+      float v[8]; ld8(x, (long long)r * x.cols + col, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s[i] += v[i];
+    }, a, b);
+    __syncthreads();
+    const int vi = tid() & 7, slot = tid() >> 3;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) part[slot * 64 + vi * 8 + i] = a[i];
+    __syncthreads();
+    if (tid() < W) {
+      const float s = slot_total(part, tid());
+      out.f()[cb + tid()] = acc ? out.f()[cb + tid()] + s : s;
+    }
+  }
+  return true;
+}
+
+// dgamma = sum_r dy * (x - mean) * rstd, dbeta = sum_r dy (registry op 39).
+__device__ __noinline__ bool op_norm_bwd_params_fast(const Ctx& c) {
+  const View x = c.buf(0), dy = c.buf(1), mean = c.buf(2), rstd = c.buf(3), dg = c.buf(4), db = c.buf(5);
+  const int R = c.i(6), c0 = c.i(8), c1 = c.i(9), acc = c.i(10);
+  if (!vec8_ok(x) || !vec8_ok(dy) || (c0 % 8) || ((c1 - c0) % 8)) return false;
+  LDS float* part = (LDS float*)c.smem;
+  for (int cb = c0; cb < c1; cb += 64) {
+    const int W = min(64, c1 - cb);
+    float a[8], b[8];
+    col_reduce(c, R, cb, W, [&](int r, int col, float (&sg)[8], float (&sb)[8]) {
+      float xv[8], gv[8];
+      ld8(x, (long long)r * x.cols + col, xv);
+      ld8(dy, (long long)r * dy.cols + col, gv);
+      const float mu = mean.ok() ? mean.f()[r] : 0.f, rs = rstd.f()[r];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) { sg[i] += gv[i] * (xv[i] - mu) * rs; sb[i] += gv[i]; }
+    }, a, b);
+    __syncthreads();
+    const int vi = tid() & 7, slot = tid() >> 3;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { part[slot * 64 + vi * 8 + i] = a[i]; part[2048 + slot * 64 + vi * 8 + i] = b[i]; }
+    __syncthreads();
+    if (tid() < W) {
+      const int j = cb + tid();
+      const float sg = slot_total(part, tid());
+      dg.f()[j] = acc ? dg.f()[j] + sg : sg;
+      if (db.ok()) { const float sb = slot_total(part + 2048, tid()); db.f()[j] = acc ? db.f()[j] + sb : sb; }
+    }
+  }
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------------- row normalisation
+// One wave per row, the row in registers (NV 4-element vectors per lane, d = 256 * NV), rows of a wave loaded before
+// any is reduced (RPW rows at a time) so their loads overlap.
+template <int NV, bool RMS> __device__ __noinline__ void norm_fwd_rows(const View& x, const View& g, const View& be, const View& out, const View& mean,
+                                                          const View& rstd, int r0, int r1, int d, float eps) {
+  constexpr int RPW = NV >= 8 ? 1 : NV >= 4 ? 2 : 4;
+  float gv[NV][4], bv[NV][4];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const f32x4n t = *(const GLOBAL f32x4n*)(g.f() + 4 * (lane() + 64 * i));
+    gv[i][0] = t.x; gv[i][1] = t.y; gv[i][2] = t.z; gv[i][3] = t.w;
+    const f32x4n u = RMS ? f32x4n{0.f, 0.f, 0.f, 0.f} : *(const GLOBAL f32x4n*)(be.f() + 4 * (lane() + 64 * i));
+    bv[i][0] = u.x; bv[i][1] = u.y; bv[i][2] = u.z; bv[i][3] = u.w;
+  }
+  for (int rb = r0 + wave() * RPW; rb < r1; rb += KVM_WAVES * RPW) {
+    f32x4n v[RPW][NV];
+#pragma unroll
+    for (int q = 0; q < RPW; ++q)
+#pragma unroll
+      for (int i = 0; i < NV; ++i) if (rb + q < r1) v[q][i] = ld4(x, (long long)(rb + q) * x.cols + 4 * (lane() + 64 * i));
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int r = rb + q;
+      if (r >= r1) break;
+      float mu = 0.f;
+      if (!RMS) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) s += (v[q][i].x + v[q][i].y) + (v[q][i].z + v[q][i].w);
+        mu = wave_sum(s) / (float)d;
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const f32x4n t = v[q][i] - mu;
+        ss += (t.x * t.x + t.y * t.y) + (t.z * t.z + t.w * t.w);
+      }
+      const float rs = 1.f / sqrtf(wave_sum(ss) / (float)d + eps);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        f32x4n o;
+        o.x = (v[q][i].x - mu) * rs * gv[i][0] + bv[i][0]; o.y = (v[q][i].y - mu) * rs * gv[i][1] + bv[i][1];
+        o.z = (v[q][i].z - mu) * rs * gv[i][2] + bv[i][2]; o.w = (v[q][i].w - mu) * rs * gv[i][3] + bv[i][3];
+        st4(out, (long long)r * out.cols + 4 * (lane() + 64 * i), o);
+      }
+      if (lane() == 0) { rstd.f()[r] = rs; if (!RMS) mean.f()[r] = mu; }
+    }
+  }
+}
+template <bool RMS> __device__ __noinline__ bool op_norm_fwd_fast(const Ctx& c) {
+  int k = 0; View x = c.buf(k++), g = c.buf(k++), be; if (!RMS) be = c.buf(k++);
+  View out = c.buf(k++), mean; if (!RMS) mean = c.buf(k++);
+  View rstd = c.buf(k++);
+  const int r0 = c.i(k), r1 = c.i(k + 1), d = c.i(k + 2); const float eps = c.f(k + 3);
+  if (d % 256 || d > 4096 || !vec4_ok(x) || !vec4_ok(out) || g.dtype != 0 || (!RMS && be.dtype != 0)) return false;
+  switch (d / 256) {
+    case 1: norm_fwd_rows<1, RMS>(x, g, be, out, mean, rstd, r0, r1, d, eps); break;
+    case 2: norm_fwd_rows<2, RMS>(x, g, be, out, mean, rstd, r0, r1, d, eps); break;
+    case 3: norm_fwd_rows<3, RMS>(x, g, be, out, mean, rstd, r0, r1, d, eps); break;
+    case 4: norm_fwd_rows<4, RMS>(x, g, be, out, mean, rstd, r0, r1, d, eps); break;
+    case 8: norm_fwd_rows<8, RMS>(x, g, be, out, mean, rstd, r0, r1, d, eps); break;
+    case 16: norm_fwd_rows<16, RMS>(x, g, be, out, mean, rstd, r0, r1, d, eps); break;
+    default: return false;
+  }
+  return true;
+}
+
+// dx = rstd * (dy*g - mean(dy*g) - xhat * mean(dy*g*xhat)) (+ dx when acc) (registry ops 37, 38).
+template <int NV, bool RMS> __device__ __noinline__ void norm_bwd_rows(const View& x, const View& dy, const View& g, const View& mean, const View& rstd,
+                                                          const View& dx, int r0, int r1, int d, int acc) {
+  constexpr int RPW = NV >= 8 ? 1 : NV >= 4 ? 2 : 4;
+  float gv[NV][4];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const f32x4n t = *(const GLOBAL f32x4n*)(g.f() + 4 * (lane() + 64 * i));
+    gv[i][0] = t.x; gv[i][1] = t.y; gv[i][2] = t.z; gv[i][3] = t.w;
+  }
+  for (int rb = r0 + wave() * RPW; rb < r1; rb += KVM_WAVES * RPW) {
+    f32x4n xv[RPW][NV], gy[RPW][NV];
+#pragma unroll
+    for (int q = 0; q < RPW; ++q)
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (rb + q < r1) {
+          xv[q][i] = ld4(x, (long long)(rb + q) * x.cols + 4 * (lane() + 64 * i));
+          gy[q][i] = ld4(dy, (long long)(rb + q) * dy.cols + 4 * (lane() + 64 * i));
+        }
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int r = rb + q;
+      if (r >= r1) break;
+      const float mu = RMS ? 0.f : mean.f()[r], rs = rstd.f()[r];
+      float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float gs = gy[q][i][e] * gv[i][e];
+          s1 += gs; s2 += gs * (xv[q][i][e] - mu) * rs;
+        }
+      s1 = RMS ? 0.f : wave_sum(s1) / (float)d;
+      s2 = wave_sum(s2) / (float)d;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const long long o = (long long)r * dx.cols + 4 * (lane() + 64 * i);
+        f32x4n res;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float gs = gy[q][i][e] * gv[i][e], xh = (xv[q][i][e] - mu) * rs;
+          res[e] = rs * (gs - s1 - xh * s2);
+        }
+        if (acc) res += ld4(dx, o);
+        st4(dx, o, res);
+      }
+    }
+  }
+}
+template <bool RMS> __device__ __noinline__ bool op_norm_bwd_dx_fast(const Ctx& c) {
+  int k = 0; View x = c.buf(k++), dy = c.buf(k++), g = c.buf(k++), mean; if (!RMS) mean = c.buf(k++);
+  View rstd = c.buf(k++), dx = c.buf(k++);
+  const int r0 = c.i(k), r1 = c.i(k + 1), d = c.i(k + 2), acc = c.i(k + 3);
+  if (d % 256 || d > 4096 || !vec4_ok(x) || !vec4_ok(dy) || !vec4_ok(dx) || g.dtype != 0) return false;
+  switch (d / 256) {
+    case 1: norm_bwd_rows<1, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
+    case 2: norm_bwd_rows<2, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
+    case 3: norm_bwd_rows<3, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
+    case 4: norm_bwd_rows<4, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
+    case 8: norm_bwd_rows<8, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
+    case 16: norm_bwd_rows<16, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
+    default: return false;
+  }
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------------- cross entropy
+// One wave per row: pass 1 streams the logits in 8-element vectors (4 in flight per lane) with a per-lane online
+// max / sum, combined across the wave; pass 2 writes dlogits = (softmax - onehot) * f. Same results as ce_rows up to
+// fp32 reassociation.
+constexpr float LOG2E = 1.4426950408889634f, LN2 = 0.6931471805599453f;
+__device__ __noinline__ bool ce_rows_fast(const Ctx& c, View lg, View tg, View rl, View ls, View dl, int r0, int r1, int V, int ignore, float f, bool fwd, bool bwd) {
+  if (!vec8_ok(lg) || (V % 8) || (bwd && !vec8_ok(dl))) return false;
+  const int nv = V / 8;
+  for (int r = r0 + wave(); r < r1; r += KVM_WAVES) {
+    const int t = tg.i()[r];
+    const bool ign = t == ignore;
+    if (!ign && (t < 0 || t >= V)) { if (lane() == 0) c.fail(KVM_ERR_OP_TOKEN, r, t); continue; }
+    const long long base = (long long)r * lg.cols;
+    float lse;
+    if (fwd) {
+      if (ign) { if (lane() == 0) { rl.f()[r] = 0.f; ls.f()[r] = 0.f; } lse = 0.f; }
+      else {
+        float m = -INFINITY, s = 0.f;            // log2 domain
+        for (int j0 = lane(); j0 < nv; j0 += 64 * 4) {
+          float v[4][8];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) if (j0 + 64 * u < nv) ld8(lg, base + 8 * (j0 + 64 * u), v[u]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (j0 + 64 * u >= nv) break;
+            float bm = v[u][0];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) bm = fmaxf(bm, v[u][i]);
+            const float nm = fmaxf(m, bm * LOG2E);
+            float a = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a += exp2f(v[u][i] * LOG2E - nm);
+            s = s * exp2f(m - nm) + a;
+            m = nm;
+          }
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+          const float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64), nm = fmaxf(m, m2);
+          s = (nm == -INFINITY) ? 0.f : s * exp2f(m - nm) + s2 * exp2f(m2 - nm);
+          m = nm;
+        }
+        lse = (m + log2f(s)) * LN2;
+        if (lane() == 0) { ls.f()[r] = lse; rl.f()[r] = lse - lg.at(r, t); }
+      }
+    } else lse = ls.f()[r];
+    if (bwd) {
+      const long long ob = (long long)r * dl.cols;
+      const float l2 = lse * LOG2E;
+      for (int j0 = lane(); j0 < nv; j0 += 64 * 4) {
+        float v[4][8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) if (j0 + 64 * u < nv && !ign) ld8(lg, base + 8 * (j0 + 64 * u), v[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int j = j0 + 64 * u;
+          if (j >= nv) break;
+          float o[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = ign ? 0.f : (exp2f(v[u][i] * LOG2E - l2) - (8 * j + i == t ? 1.f : 0.f)) * f;
+          st8(dl, ob + 8 * j, o);
+        }
+      }
+    }
+  }
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------------- flat streams
+// f32 <-> bf16 storage conversion / copy over [e0, e1) (registry op 113): aligned 8-element vectors in the middle.
+__device__ __noinline__ bool op_round_bf16_fast(const Ctx& c) {
+  const View x = c.buf(0), o = c.buf(1);
+  const long long e0 = c.i(2), e1 = c.i(3);
+  if (x.dtype == 1 || o.dtype == 1) return false;
+  const long long a0 = min(e1, (e0 + 7) & ~7ll), a1 = max(a0, e1 & ~7ll);
+  auto one = [&](long long k) { const float v = x.ld(k); if (o.dtype == 2) o.h()[k] = f2bf(v); else o.f()[k] = x.dtype == 2 ? v : round_bf(v); };
+  for (long long k = e0 + tid(); k < a0; k += KVM_THREADS) one(k);
+  for (long long k = a1 + tid(); k < e1; k += KVM_THREADS) one(k);
+  const long long n8 = (a1 - a0) / 8;
+  for (long long q0 = tid(); q0 < n8; q0 += 4 * KVM_THREADS) {
+    float v[4][8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) if (q0 + u * KVM_THREADS < n8) ld8(x, a0 + 8 * (q0 + u * KVM_THREADS), v[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long long q = q0 + u * KVM_THREADS;
+      if (q >= n8) break;
+      if (o.dtype == 0 && x.dtype == 0)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[u][i] = round_bf(v[u][i]);
+      st8(o, a0 + 8 * q, v[u]);
+    }
+  }
+  return true;
+}
+
+// Sum of squares of g[e0, e1) in double (registry op 55), 4 vectors in flight per lane.
+__device__ __noinline__ bool op_gradnorm_partial_fast(const Ctx& c) {
+  const View g = c.buf(0), part = c.buf(1);
+  const long long e0 = c.i(3), e1 = c.i(4);
+  if (g.dtype != 0) return false;
+  __shared__ double red[KVM_WAVES];
+  const long long a0 = min(e1, (e0 + 3) & ~3ll), a1 = max(a0, e1 & ~3ll);
+  double s = 0.0;
+  for (long long k = e0 + tid(); k < a0; k += KVM_THREADS) { const double v = g.f()[k]; s += v * v; }
+  for (long long k = a1 + tid(); k < e1; k += KVM_THREADS) { const double v = g.f()[k]; s += v * v; }
+  const long long n4 = (a1 - a0) / 4;
+  const GLOBAL f32x4n* p = (const GLOBAL f32x4n*)(g.f() + a0);
+  double t[4] = {0.0, 0.0, 0.0, 0.0};
+  for (long long q0 = tid(); q0 < n4; q0 += 4 * KVM_THREADS) {
+    f32x4n v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) if (q0 + u * KVM_THREADS < n4) v[u] = p[q0 + u * KVM_THREADS];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (q0 + u * KVM_THREADS < n4) t[u] += ((double)v[u].x * v[u].x + (double)v[u].y * v[u].y) + ((double)v[u].z * v[u].z + (double)v[u].w * v[u].w);
+  }
+  s += (t[0] + t[1]) + (t[2] + t[3]);
+  s = block_sum_d(s, red);
+  if (tid() == 0) part.f()[c.i(2)] = (float)s;
+  return true;
+}
+
+// delta[b, h, t] = sum over the head's columns of o * do (registry op 46): one wave per row, each head's hd columns
+// on hd/4 lanes (reduced with lane exchanges inside the group); NV 4-element vectors per lane (row width 256 * NV).
+template <int NV> __device__ __noinline__ void delta_rows(const View& o, const View& d, const View& delta, int r0, int r1, int T, int H, int hd) {
+  const int gl = hd / 4;
+  for (int r = r0 + wave(); r < r1; r += KVM_WAVES) {
+    f32x4n a[NV], b[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) { a[i] = ld4(o, (long long)r * o.cols + 4 * (lane() + 64 * i)); b[i] = ld4(d, (long long)r * d.cols + 4 * (lane() + 64 * i)); }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float s = (a[i].x * b[i].x + a[i].y * b[i].y) + (a[i].z * b[i].z + a[i].w * b[i].w);
+      for (int x = 1; x < gl; x <<= 1) s += __shfl_xor(s, x, 64);
+      const int col = 4 * (lane() + 64 * i);
+      if ((lane() & (gl - 1)) == 0) delta.f()[((long long)(r / T) * H + col / hd) * T + r % T] = s;
+    }
+  }
+}
+__device__ __noinline__ bool op_attn_bwd_delta_fast(const Ctx& c) {
+  const View o = c.buf(0), d = c.buf(1), delta = c.buf(2);
+  const int r0 = c.i(3), r1 = c.i(4), T = c.i(5), H = c.i(6), hd = c.i(7);
+  const int W = H * hd, gl = hd / 4;
+  if (hd % 4 || (gl & (gl - 1)) || gl > 64 || W % 256 || !vec4_ok(o) || !vec4_ok(d)) return false;
+  switch (W / 256) {
+    case 1: delta_rows<1>(o, d, delta, r0, r1, T, H, hd); break;
+    case 2: delta_rows<2>(o, d, delta, r0, r1, T, H, hd); break;
+    case 3: delta_rows<3>(o, d, delta, r0, r1, T, H, hd); break;
+    case 4: delta_rows<4>(o, d, delta, r0, r1, T, H, hd); break;
+    case 8: delta_rows<8>(o, d, delta, r0, r1, T, H, hd); break;
+    case 16: delta_rows<16>(o, d, delta, r0, r1, T, H, hd); break;
+    default: return false;
+  }
+  return true;
+}
+
+// Cross-entropy entry points (ops 51, 53, 127): the streaming rows when the logits allow, else ce_rows.
+__device__ __noinline__ void op_softmax_ce_fwd_any(const Ctx& c) {
+  View n{};
+  if (!ce_rows_fast(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), n, c.i(4), c.i(5), c.i(6), c.i(7), 0.f, true, false)) op_softmax_ce_fwd(c);
+}
+__device__ __noinline__ void op_softmax_ce_bwd_any(const Ctx& c) {
+  View n{};
+  const float f = c.buf(3).f()[1] * c.f(9);
+  if (!ce_rows_fast(c, c.buf(0), c.buf(1), n, c.buf(2), c.buf(4), c.i(5), c.i(6), c.i(7), c.i(8), f, false, true)) op_softmax_ce_bwd(c);
+}
+__device__ __noinline__ void op_softmax_ce_fused_any(const Ctx& c) {
+  const float f = (float)(1.0 / c.i(9)) * c.f(10);
+  if (!ce_rows_fast(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.i(5), c.i(6), c.i(7), c.i(8), f, true, true)) op_softmax_ce_fused(c);
+}
+
+}  // namespace kvm

@@ -1,0 +1,112 @@
+"""GPU parity of the streaming forms of the bandwidth-bound operators (row norms, column reductions, softmax cross
+entropy, bf16 conversion, gradient norm, attention delta) at the widths of the GPT-162M workload (d = 768, 4096
+rows), in bf16 and f32 storage, against the CPU oracle. The oracle sums in double; the device sums in fp32 in a fixed
+tree order: f32 outputs within a relative L2 error of 2e-5, bf16 outputs 4e-3 (one bf16 ulp is 2^-8)."""
+import pytest
+
+import oracle
+from gpu_check import compare_run
+from kvm_amd import bundle as bl
+from kvm_amd import compiler
+from kvm_amd.executor import Executor
+from kvm_amd.workloads import Builder, Workload, split
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(b):
+    w = Workload(b.spec(), b.init_override)
+    lb = bl.load(compiler.compile_spec(w.spec))
+    init = [oracle.materialize(m, w.init_override.get(m['name'])) for m in lb.metadata['buffers']]
+    ref = oracle.run(lb, [x.copy() for x in init])
+    ex = Executor.from_bundle(lb, buffers=init)
+    ex.run()
+    bad = compare_run(ex, lb.metadata, ref)
+    ex.close()
+    assert not bad, bad
+
+
+@pytest.mark.parametrize('dt', ['bf16', 'f32'])
+def test_norms_and_column_sums(dt):
+    print(f'norms {dt}', flush=True)
+    N, d = 1024, 768
+    b = Builder(3)
+    for nm in ('x', 'dy'):
+        b.normal(nm, N, d, dt, scale=1.0)
+    b.normal('g', 1, d, 'f32', scale=1.0)
+    b.normal('be', 1, d, 'f32', scale=1.0)
+    b.normal('dx', N, d, dt, scale=1.0)
+    b.fill('h', N, d, dt)
+    b.fill('hr', N, d, dt)
+    for nm in ('mu', 'rs', 'rsr'):
+        b.fill(nm, N)
+    for nm in ('dg', 'db', 'cs'):
+        b.fill(nm, 1, d)
+    ts = []
+    for r0, r1 in split(N, 64):
+        ts.append(b.task('layernorm_fwd', x='x', gamma='g', beta='be', out='h', mean='mu', rstd='rs', r0=r0, r1=r1, d=d, eps=1e-5))
+        ts.append(b.task('rmsnorm_fwd', x='x', gamma='g', out='hr', rstd='rsr', r0=r0, r1=r1, d=d, eps=1e-6))
+    for r0, r1 in split(N, 64):
+        b.task('layernorm_bwd_dx', after=ts, x='x', dy='dy', gamma='g', mean='mu', rstd='rs', dx='dx', r0=r0, r1=r1, d=d, acc=1)
+    for c0, c1 in split(d, 12):
+        b.task('norm_bwd_params', after=ts, x='x', dy='dy', mean='mu', rstd='rs', dgamma='dg', dbeta='db', R=N, d=d, c0=c0, c1=c1, acc=0)
+        b.task('colsum', x='dy', out='cs', R=N, c0=c0, c1=c1, acc=0)
+    _run(b)
+
+
+def test_rmsnorm_bwd_and_wide_rows():
+    print('rmsnorm bwd d=4096', flush=True)
+    N, d = 128, 4096
+    b = Builder(5)
+    for nm in ('x', 'dy'):
+        b.normal(nm, N, d, 'bf16', scale=1.0)
+    b.normal('g', 1, d, 'f32', scale=1.0)
+    b.fill('h', N, d, 'bf16')
+    b.fill('rs', N)
+    b.fill('dx', N, d, 'bf16')
+    t = [b.task('rmsnorm_fwd', x='x', gamma='g', out='h', rstd='rs', r0=r0, r1=r1, d=d, eps=1e-6) for r0, r1 in split(N, 8)]
+    for r0, r1 in split(N, 8):
+        b.task('rmsnorm_bwd_dx', after=t, x='x', dy='dy', gamma='g', rstd='rs', dx='dx', r0=r0, r1=r1, d=d, acc=0)
+    _run(b)
+
+
+@pytest.mark.parametrize('dt', ['bf16', 'f32'])
+def test_cross_entropy(dt):
+    print(f'cross entropy {dt}', flush=True)
+    N, V = 256, 5000
+    b = Builder(9)
+    b.normal('lg', N, V, dt, scale=3.0)
+    b.values('tgt', [(37 * i + 11) % V if i % 17 else -1 for i in range(N)], N, 1, 'i32')
+    b.fill('rl', N)
+    b.fill('ls', N)
+    b.fill('dl', N, V, dt)
+    b.fill('loss', 2)
+    ts = [b.task('softmax_ce_fused', logits='lg', tgt='tgt', rowloss='rl', lse='ls', dlogits='dl', r0=r0, r1=r1, V=V, ignore=-1, N=N, scale=1.0)
+          for r0, r1 in split(N, 16)]
+    b.task('softmax_ce_reduce', after=ts, rowloss='rl', tgt='tgt', loss='loss', N=N, ignore=-1)
+    _run(b)
+
+
+def test_flat_streams():
+    print('round_bf16 / gradnorm / delta', flush=True)
+    b = Builder(13)
+    n = 100003
+    b.normal('f', 1, n, 'f32', scale=1.0)
+    b.normal('hb', 1, n, 'bf16', scale=1.0)
+    b.fill('f2b', 1, n, 'bf16')
+    b.fill('b2b', 1, n, 'bf16')
+    b.fill('b2f', 1, n, 'f32')
+    b.fill('gn', 8)
+    for e0, e1 in ((3, 50001), (50001, n)):
+        b.task('round_bf16', x='f', out='f2b', e0=e0, e1=e1)
+        b.task('round_bf16', x='hb', out='b2b', e0=e0, e1=e1)
+        b.task('round_bf16', x='hb', out='b2f', e0=e0, e1=e1)
+    for i, (e0, e1) in enumerate(split(n, 8)):
+        b.task('gradnorm_partial', g='f', partial='gn', slot=i, e0=e0, e1=e1)
+    N, H, hd, T = 256, 12, 64, 128
+    b.normal('o', N, H * hd, 'bf16', scale=1.0)
+    b.normal('do', N, H * hd, 'bf16', scale=1.0)
+    b.fill('delta', N * H)
+    for r0, r1 in split(N, 16):
+        b.task('attn_bwd_delta', o='o', do='do', delta='delta', r0=r0, r1=r1, T=T, H=H, hd=hd)
+    _run(b)

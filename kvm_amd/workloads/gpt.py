@@ -25,6 +25,7 @@ from dataclasses import dataclass, asdict
 from . import Builder, Workload, split
 
 RB = 128   # row-block granularity of the dependency index
+CHUNK = 131072   # elements per optimizer / bf16-copy task (balances the step's tail)
 
 
 @dataclass
@@ -84,6 +85,12 @@ def step_flops(c: GPTConfig) -> dict:
     attn_fwd = 2 * 2 * pairs * hd * c.layers
     attn_bwd = 5 * 2 * pairs * hd * c.layers
     return {'gemm': gemm, 'attn': attn_fwd + attn_bwd, 'total': gemm + attn_fwd + attn_bwd}
+
+
+def row_chunks(R, C):
+    """Flat [e0, e1) ranges of about CHUNK elements covering an R x C matrix, on whole rows: tasks of different chunks
+    never share a row, so the dependency tracker keeps them independent."""
+    return [(r0 * C, r1 * C) for r0, r1 in split(R, -(-(R * C) // CHUNK))]
 
 
 class Deps:
@@ -200,8 +207,10 @@ class GPTBuilder:
     def gemm(self, A, B, out, M, N, K, flags=0, bias=None, res=None, pre=None, alpha=1.0):
         """C = alpha * op(A) op(B) (+ epilogue), tiled; returns the task ids."""
         bf, ta, tb = self.bf, flags & 1, flags & 2
-        if bf:
+        if bf and -(-M // 128) * -(-N // 256) >= 256:
             op, TM, TN, fl = 'matmul_mma_bf16', 128, 256, flags
+        elif bf:   # fewer than 256 tiles of 128x256: 128x128 tiles keep more of the chip busy
+            op, TM, TN, fl = 'matmul_tile_bf16', 128, 128, flags | 32
         elif M >= 128 and N >= 128:
             op, TM, TN, fl = 'matmul_tile', 128, 128, flags | 32
         else:
@@ -297,7 +306,7 @@ class GPTBuilder:
             for (p, g, m, v, sh, dec) in self.params:
                 if sh:
                     R, C = self.shapes[p]
-                    for e0, e1 in split(R * C, max(1, min(64, R * C // 262144 + 1))):
+                    for e0, e1 in row_chunks(R, C):
                         rows = (e0 // C, (e1 - 1) // C + 1)
                         self.task('round_bf16', [(p, rows)], [(sh, rows)], x=p, out=sh, e0=e0, e1=e1)
         # ---- forward
@@ -420,7 +429,12 @@ class GPTBuilder:
         scale = 1.0 / math.sqrt(hd)
         o, q, k, v, lse, delta = f'o.{l}', f'q.{l}', f'k.{l}', f'v.{l}', f'lse.{l}', f'delta.{l}'
         for r0, r1 in self.rows(N):
-            dr = [(delta, ((r0 // T * H) * T + r0 % T, ((r1 - 1) // T * H + H - 1) * T + (r1 - 1) % T + 1))]
+            # delta is [B*H*T] at (b*H + h)*T + t: rows [r0, r1) write one range per (batch, head), so delta tasks of
+            # different row blocks stay independent
+            dr = []
+            for bi in range(r0 // T, (r1 - 1) // T + 1):
+                t0, t1 = max(r0, bi * T) - bi * T, min(r1, (bi + 1) * T) - bi * T
+                dr += [(delta, ((bi * H + h) * T + t0, (bi * H + h) * T + t1)) for h in range(H)]
             self.task('attn_bwd_delta', [(o, (r0, r1)), (f'do.{l}', (r0, r1))], dr, o=o, do=f'do.{l}', delta=delta, r0=r0, r1=r1, T=T, H=H, hd=hd)
         for bb in range(c.batch):
             for h in range(H):
@@ -445,8 +459,7 @@ class GPTBuilder:
         for (p, g, m, v, sh, dec) in self.params:
             R, C = self.shapes[p]
             n = R * C
-            parts = max(1, min(64, n // 262144 + 1))
-            for e0, e1 in split(n, parts):
+            for e0, e1 in row_chunks(R, C):
                 chunks.append((p, g, m, v, sh, dec, e0, e1, C))
         if 'gn' not in self.shapes:
             self.buf('gn', len(chunks)), self.buf('gscale', 2)

@@ -93,6 +93,10 @@ int kvm_relaunch(KvmExec* ex);
 // Launches `n` back-to-back runs without host synchronisation in between and returns the elapsed milliseconds
 // measured with HIP events around them (the timed region of the benchmark). Result of the last run via kvm_finish.
 int kvm_run_timed(KvmExec* ex, int n, float* ms);
+// As kvm_run_timed, and also the summed duration of the n persistent-kernel launches alone (HIP events on the
+// executor's stream right before and after each launch, i.e. without the per-launch state reset). No counterpart in
+// the reference; for benchmarks that report a kernel's own duration.
+int kvm_run_timed_split(KvmExec* ex, int n, float* total_ms, float* exec_ms);
 
 // Host-only validation of one bundle against a buffer table (shapes and dtypes in `bufs`; `p` unused): the checks
 // kvm_submit runs. Returns 0 when valid, else KVM_STATUS_INVALID with the reason in `err`. Needs no GPU.

@@ -68,16 +68,18 @@ static void usage() {
                   "  --golden [--golden-tol R]   compare with <bundle_dir>/golden.json (one bundle): buffers (relative L2), versions, reads\n"
                   "  --dump-bin DIR i,j,..       write buffers (widened to f32 / raw i32) to DIR/<index>.bin\n"
                   "  --trace-csv FILE            per-task timeline   --repeat N   run the graph N times (timed)   --timeout-s N\n"
+                  "  --dump-buffers              print every buffer (reference text format)\n"
                   "  --blocks N   --no-trace   --quiet   --check-ops\n");
 }
 
 int main(int argc, char** argv) {
-  std::vector<std::string> dirs; bool golden = false, quiet = false, trace = true; float tol = 1e-6f;
+  std::vector<std::string> dirs; bool golden = false, quiet = false, trace = true, dump_text = false; float tol = 1e-6f;
   const char* csv = nullptr; std::string dump_dir; std::vector<int> dump_idx; int repeat = 1, blocks = 0; long long timeout_s = 20;
   for (int i = 1; i < argc; ++i) {
     std::string a = argv[i];
     auto next = [&]() -> const char* { if (i + 1 >= argc) { usage(); exit(2); } return argv[++i]; };
     if (a == "--golden") golden = true;
+    else if (a == "--dump-buffers") dump_text = true;
     else if (a == "--golden-tol") tol = (float)atof(next());
     else if (a == "--trace-csv") csv = next();
     else if (a == "--repeat") repeat = atoi(next());
@@ -175,6 +177,17 @@ int main(int argc, char** argv) {
         for (size_t i = 0; i < tr.size(); ++i) fprintf(f, "%zu,%llu,%llu,%d,%d,%d,%d,%d\n", i, tr[i].start, tr[i].end, tr[i].block, tr[i].xcc, tr[i].ver0, tr[i].ver1, tr[i].exec_count);
         fclose(f); }
     }
+    // text dump of every buffer, one line each, in the reference CLI's format (mvm_exec.cu:2298): raw 4-byte elements
+    // printed as floats (an i32 buffer's bits reinterpreted), bf16 storage widened to fp32
+    if (dump_text)
+      for (int idx = 0; idx < kvm_nbufs(ex.get()); ++idx) {
+        const Json& jb = metas[0].need("buffers").a[idx];
+        size_t n = (size_t)jb.num("rows", 1) * (size_t)jb.num("cols", 1);
+        std::vector<float> v(n); kvm_read_buffer(ex.get(), idx, v.data(), n);
+        printf("buffer %d:", idx);
+        for (float x : v) printf(" %.9g", x);
+        printf("\n");
+      }
     for (int idx : dump_idx) {
       if (idx < 0 || idx >= kvm_nbufs(ex.get())) { fprintf(stderr, "--dump-bin: buffer %d out of range\n", idx); return 2; }
       int dt = kvm_buffer_dtype(ex.get(), idx);

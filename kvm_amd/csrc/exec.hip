@@ -313,20 +313,20 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
   if (i < S.nq) { KvmQueue z = {}; S.queues[i] = z; }
   if (i == 0) { KvmCounters z = {}; *S.cnt = z; }
 }
-// Roots (tasks with no predecessors), single thread, in index order: those without a version wait take the first
-// cells of their queues, the rest are released afterwards (they park until their version is published).
-__global__ void kvm_seed_kernel(KvmDevState S, const int* roots, int nroots) {
-  if (threadIdx.x != 0) return;
-  for (int r = 0; r < nroots; ++r) {
+// Roots (tasks with no predecessors). Roots without a version wait go to fixed cells computed on the host (queue
+// t % nq, in index order within the queue), written by all threads at once; the queue tails then start past them.
+// Roots with a version wait are released one by one by thread 0 afterwards (they park until the version is published,
+// or are enqueued behind the fixed cells when it already is).
+__global__ void kvm_seed_kernel(KvmDevState S, const int* roots, const int* root_cell, int nfixed, int nroots, const int* fixed_tail) {
+  for (int r = threadIdx.x; r < nfixed; r += blockDim.x) {
     const int t = roots[r];
-    const MvmTaskDesc& d = S.tasks[t];
-    if (d.wait_var < 0 || S.version[d.wait_var] >= d.wait_ver) {
-      const int q = t % S.nq;
-      S.ready[q * S.qcap + S.queues[q].tail++] = t;
-      S.state[t] = 2;
-    }
+    S.ready[root_cell[r]] = t;
+    S.state[t] = 2;
   }
-  for (int r = 0; r < nroots; ++r) if (S.state[roots[r]] == 0) release(S, roots[r]);
+  if (threadIdx.x < S.nq) S.queues[threadIdx.x].tail = fixed_tail[threadIdx.x];
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int r = nfixed; r < nroots; ++r) release(S, roots[r]);
 }
 
 // ---------------------------------------------------------------------------------------------- init kernels
@@ -388,7 +388,8 @@ struct KvmExec {
   // device memory
   MvmTaskDesc* d_tasks = nullptr; int32_t *d_succ = nullptr, *d_args = nullptr; MvmBuf* d_bufs = nullptr;
   int *d_indeg = nullptr, *d_ready = nullptr, *d_state = nullptr, *d_park_next = nullptr, *d_version = nullptr, *d_park_head = nullptr;
-  int *d_base = nullptr, *d_roots = nullptr;
+  int *d_base = nullptr, *d_roots = nullptr, *d_root_cell = nullptr, *d_fixed_tail = nullptr;
+  int nfixed = 0;
   unsigned* d_opmask = nullptr;
   KvmCounters* d_cnt = nullptr; KvmTrace* d_trace = nullptr;
   KvmQueue* d_queues = nullptr; int *d_qcount = nullptr, *d_done_blk = nullptr;
@@ -439,7 +440,7 @@ void kvm_destroy(KvmExec* ex) {
   for (auto& b : ex->bufs) hipFree(b.p);
   void* ptrs[] = {ex->d_tasks, ex->d_succ, ex->d_args, ex->d_bufs, ex->d_indeg, ex->d_ready, ex->d_state, ex->d_park_next,
                   ex->d_version, ex->d_park_head, ex->d_base, ex->d_roots, ex->d_cnt, ex->d_trace, ex->d_queues, ex->d_qcount,
-                  ex->d_done_blk, ex->d_opmask};
+                  ex->d_done_blk, ex->d_opmask, ex->d_root_cell, ex->d_fixed_tail};
   for (void* q : ptrs) if (q) hipFree(q);
   if (ex->ev0) hipEventDestroy(ex->ev0);
   if (ex->ev1) hipEventDestroy(ex->ev1);
@@ -556,7 +557,6 @@ static int do_upload(KvmExec* ex) {
   HIPCK(upload(&ex->d_succ, succ_dev, ex->stream));
   HIPCK(upload(&ex->d_args, ex->args, ex->stream));
   HIPCK(upload(&ex->d_bufs, table, ex->stream));
-  HIPCK(upload(&ex->d_roots, ex->roots, ex->stream));
   std::vector<unsigned> opmask(KVM_OPMASK_IDS, 0u);     // buffer-argument positions of every registry operator
   for (const kvmv::OpSig& o : kvmv::kRegistry) {
     if (o.id < 0 || o.id >= KVM_OPMASK_IDS) continue;
@@ -570,6 +570,18 @@ static int do_upload(KvmExec* ex) {
   std::vector<int> qcount(nq, 0);
   for (int t = 0; t < n; ++t) ++qcount[t % nq];
   HIPCK(hipMalloc(&ex->d_ready, (size_t)nq * qcap * sizeof(int)));
+  {   // roots: those without a version wait first (fixed ready cells), then those with one
+    std::vector<int> ordered, cells, tail(nq, 0), waiting;
+    for (int t : ex->roots) {
+      if (ex->tasks[t].wait_var < 0) { const int q = t % nq; ordered.push_back(t); cells.push_back(q * qcap + tail[q]++); }
+      else waiting.push_back(t);
+    }
+    ex->nfixed = (int)ordered.size();
+    ordered.insert(ordered.end(), waiting.begin(), waiting.end());
+    HIPCK(upload(&ex->d_roots, ordered, ex->stream));
+    HIPCK(upload(&ex->d_root_cell, cells, ex->stream));
+    HIPCK(upload(&ex->d_fixed_tail, tail, ex->stream));
+  }
   HIPCK(hipMalloc(&ex->d_queues, nq * sizeof(KvmQueue)));
   HIPCK(hipMalloc(&ex->d_done_blk, ex->grid * sizeof(int)));
   HIPCK(upload(&ex->d_qcount, qcount, ex->stream));
@@ -592,12 +604,15 @@ static int do_upload(KvmExec* ex) {
   return 0;
 }
 
-static int launch_once(KvmExec* ex) {
+static int launch_once(KvmExec* ex, hipEvent_t before_exec = nullptr, hipEvent_t after_exec = nullptr) {
   KvmDevState& S = ex->S;
   HIPCK(hipMemcpyAsync(ex->d_base, ex->base_versions.data(), ex->base_versions.size() * sizeof(int), hipMemcpyHostToDevice, ex->stream));
   hipLaunchKernelGGL(kvm_reset_kernel, dim3(std::min(1024, (S.ntasks + 255) / 256 + 1)), dim3(256), 0, ex->stream, S, (const int*)ex->d_base);
-  hipLaunchKernelGGL(kvm_seed_kernel, dim3(1), dim3(64), 0, ex->stream, S, (const int*)ex->d_roots, (int)ex->roots.size());
+  hipLaunchKernelGGL(kvm_seed_kernel, dim3(1), dim3(1024), 0, ex->stream, S, (const int*)ex->d_roots, (const int*)ex->d_root_cell,
+                     ex->nfixed, (int)ex->roots.size(), (const int*)ex->d_fixed_tail);
+  if (before_exec) HIPCK(hipEventRecord(before_exec, ex->stream));
   hipLaunchKernelGGL(kvm_exec_kernel, dim3(ex->grid), dim3(KVM_THREADS), 0, ex->stream, S);
+  if (after_exec) HIPCK(hipEventRecord(after_exec, ex->stream));
   HIPCK(hipGetLastError());
   return 0;
 }
@@ -634,6 +649,30 @@ int kvm_run_timed(KvmExec* ex, int n, float* ms) {
   HIPCK(hipEventRecord(ex->ev1, ex->stream));
   HIPCK(hipEventSynchronize(ex->ev1));
   HIPCK(hipEventElapsedTime(ms, ex->ev0, ex->ev1));
+  ex->launched = true;
+  return 0;
+}
+
+int kvm_run_timed_split(KvmExec* ex, int n, float* total_ms, float* exec_ms) {
+  hipSetDevice(ex->dev);
+  if (n < 1) { ex->err = "kvm_run_timed_split: n < 1"; return KVM_STATUS_INVALID; }
+  if (!ex->uploaded) { int rc = do_upload(ex); if (rc) return rc; }
+  std::vector<hipEvent_t> ev(2 * n, nullptr);
+  for (auto& e : ev) HIPCK(hipEventCreate(&e));
+  HIPCK(hipStreamSynchronize(ex->stream));
+  HIPCK(hipEventRecord(ex->ev0, ex->stream));
+  int rc = 0;
+  for (int i = 0; i < n && !rc; ++i) rc = launch_once(ex, ev[2 * i], ev[2 * i + 1]);
+  HIPCK(hipEventRecord(ex->ev1, ex->stream));
+  HIPCK(hipEventSynchronize(ex->ev1));
+  float tot = 0.f, ex_sum = 0.f;
+  if (!rc) {
+    HIPCK(hipEventElapsedTime(&tot, ex->ev0, ex->ev1));
+    for (int i = 0; i < n; ++i) { float t = 0.f; HIPCK(hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1])); ex_sum += t; }
+  }
+  for (auto& e : ev) hipEventDestroy(e);
+  if (rc) return rc;
+  *total_ms = tot; *exec_ms = ex_sum;
   ex->launched = true;
   return 0;
 }

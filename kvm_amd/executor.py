@@ -67,7 +67,7 @@ def lib():
             'kvm_buffer_dtype': (I, [P, I]), 'kvm_buffer_device_ptr': (P, [P, I]), 'kvm_write_buffer': (I, [P, I, P, U]),
             'kvm_read_buffer': (I, [P, I, P, U]), 'kvm_read_raw': (I, [P, I, P, U]), 'kvm_set_version': (I, [P, I, I]),
             'kvm_submit': (I, [P, P, I, P, I, P, I]), 'kvm_start': (I, [P]), 'kvm_finish': (I, [P, P]), 'kvm_relaunch': (I, [P]),
-            'kvm_run_timed': (I, [P, I, P]), 'kvm_versions': (I, [P, P, I]), 'kvm_trace': (I, [P, P, I]), 'kvm_ntasks': (I, [P]),
+            'kvm_run_timed': (I, [P, I, P]), 'kvm_run_timed_split': (I, [P, I, P, P]), 'kvm_versions': (I, [P, P, I]), 'kvm_trace': (I, [P, P, I]), 'kvm_ntasks': (I, [P]),
             'kvm_op_name': (ctypes.c_char_p, [I]),
             'kvm_validate': (I, [P, I, P, I, P, I, P, I, I, ctypes.c_char_p, I]),
             'kvm_seeded_fill_test': (I, [ctypes.c_ulonglong, ctypes.c_longlong, I, ctypes.c_float, ctypes.c_float, P]),
@@ -218,6 +218,12 @@ class Executor:
         ms = ctypes.c_float()
         self._check(lib().kvm_run_timed(self._h, n, ctypes.byref(ms)), 'run_timed')
         return ms.value
+
+    def run_timed_split(self, n: int) -> tuple[float, float]:
+        """(total ms, persistent-kernel-only ms) of n back-to-back runs."""
+        tot, exe = ctypes.c_float(), ctypes.c_float()
+        self._check(lib().kvm_run_timed_split(self._h, n, ctypes.byref(tot), ctypes.byref(exe)), 'run_timed_split')
+        return tot.value, exe.value
 
     def versions(self, n: int | None = None) -> np.ndarray:
         n = n if n is not None else max(1, len(self.meta['variables']) if self.meta else 1)

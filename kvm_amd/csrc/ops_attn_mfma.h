@@ -38,12 +38,12 @@ template <int HD> struct FaL {
   __device__ static __forceinline__ int tr(int row, int col) { return row * HD + 8 * ((col >> 3) ^ tswz(row)) + (col & 7); }
   // Direct loads of rows [row0, row0 + 64), columns [c0, c0 + HD) of a bf16 matrix with `cols` columns (buffer
   // descriptor rs) into dst in the kc (TRL false) or tr (TRL true) layout.
-  template <bool TRL> __device__ static __forceinline__ void issue(LDS uint16_t* dst, __amdgpu_buffer_rsrc_t rs, int row0, int cols, int c0) {
+  template <bool TRL> __device__ static __forceinline__ void issue(LDS uint16_t* dst, i32x4_t rs, int row0, int cols, int c0) {
 #pragma unroll
     for (int q = 0; q < NL; ++q) {
       const int b = q * KVM_WAVES + wave(), u = 64 * b + lane(), row = u / UPR, ph = u % UPR;
       const int lu = ph ^ (TRL ? tswz(row) : kswz(row));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS void*)(dst + b * 512), 16, ((row0 + row) * cols + c0 + 8 * lu) * 2, 0, 0, 0);
+      dma16(rs, ((row0 + row) * cols + c0 + 8 * lu) * 2, 0, dst + b * 512);
     }
   }
   // MFMA operand from the kc layout: 8 values of row rb + l % 32 at head-dim chunk kk*2 + l/32.
@@ -94,8 +94,8 @@ template <int HD> __device__ __noinline__ void attn_fwd_mfma(const Ctx& c) {
     qf[kk] = qok ? *(const GLOBAL bf16x8*)(q.h() + ((long long)bb * T + qrow) * q.cols + h * HD + kk * 16 + 8 * g) : bf16x8{};
   const int kend = min(T, q0 + 128), nkb = (kend + FA_KB - 1) / FA_KB;
   const int wlast = min(T - 1, q0 + 32 * w + 31);
-  const __amdgpu_buffer_rsrc_t rk = buf_rsrc((const void*)(k.h() + (long long)bb * T * k.cols), (long long)T * k.cols * 2);
-  const __amdgpu_buffer_rsrc_t rv = buf_rsrc((const void*)(v.h() + (long long)bb * T * v.cols), (long long)T * v.cols * 2);
+  const i32x4_t rk = dma_rsrc((const void*)(k.h() + (long long)bb * T * k.cols), (long long)T * k.cols * 2);
+  const i32x4_t rv = dma_rsrc((const void*)(v.h() + (long long)bb * T * v.cols), (long long)T * v.cols * 2);
   LDS uint16_t* lds = (LDS uint16_t*)c.smem;
   constexpr int ST = 2 * FA_KB * HD;                       // elements per stage: K then V
   f32x16 oacc[NDB];
@@ -196,8 +196,8 @@ template <int HD> __device__ __noinline__ void attn_dq_mfma(const Ctx& c) {
   const float di = qok ? delta.f()[((long long)bb * H + h) * T + qrow] : 0.f;
   const int kend = min(T, q0 + 128), nkb = (kend + FA_KB - 1) / FA_KB;
   const int wlast = min(T - 1, q0 + 32 * w + 31);
-  const __amdgpu_buffer_rsrc_t rk = buf_rsrc((const void*)(k.h() + (long long)bb * T * k.cols), (long long)T * k.cols * 2);
-  const __amdgpu_buffer_rsrc_t rv = buf_rsrc((const void*)(v.h() + (long long)bb * T * v.cols), (long long)T * v.cols * 2);
+  const i32x4_t rk = dma_rsrc((const void*)(k.h() + (long long)bb * T * k.cols), (long long)T * k.cols * 2);
+  const i32x4_t rv = dma_rsrc((const void*)(v.h() + (long long)bb * T * v.cols), (long long)T * v.cols * 2);
   LDS uint16_t* lds = (LDS uint16_t*)c.smem;
   auto issue = [&](int blk) {
     LDS uint16_t* d = lds + (blk % FA_NS) * ST;
@@ -281,8 +281,8 @@ template <int HD> __device__ __noinline__ void attn_dkv_mfma(const Ctx& c) {
   }
   const int qb0 = k0 / FA_KB, nqb = (T + FA_KB - 1) / FA_KB - qb0, nit = G * nqb;
   const int wfirst = k0 + 32 * w;                          // this wave's first key: queries before it see none of its keys
-  const __amdgpu_buffer_rsrc_t rq = buf_rsrc((const void*)(q.h() + (long long)bb * T * q.cols), (long long)T * q.cols * 2);
-  const __amdgpu_buffer_rsrc_t rd = buf_rsrc((const void*)(dO.h() + (long long)bb * T * dO.cols), (long long)T * dO.cols * 2);
+  const i32x4_t rq = dma_rsrc((const void*)(q.h() + (long long)bb * T * q.cols), (long long)T * q.cols * 2);
+  const i32x4_t rd = dma_rsrc((const void*)(dO.h() + (long long)bb * T * dO.cols), (long long)T * dO.cols * 2);
   LDS uint16_t* lds = (LDS uint16_t*)c.smem;
   auto issue = [&](int it) {
     const int hh = kvh * G + it / nqb, qb = qb0 + it % nqb;
@@ -293,10 +293,9 @@ template <int HD> __device__ __noinline__ void attn_dkv_mfma(const Ctx& c) {
     L::template issue<true>(d + 3 * BK, rd, qb * FA_KB, dO.cols, hh * HD);
     // lse / delta: wave 0, 1 -> lse[0:32], [32:64]; wave 2, 3 -> delta; 8 lanes x 16 bytes each
     const View& src = w < 2 ? lse : delta;
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc((const void*)(src.f() + ((long long)bb * H + hh) * T), (long long)T * 4);
+    const i32x4_t rs = dma_rsrc((const void*)(src.f() + ((long long)bb * H + hh) * T), (long long)T * 4);
     if (l < 8)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS void*)(d + 4 * BK + (w >> 1) * 128 + (w & 1) * 64), 16,
-                                               (qb * FA_KB + 32 * (w & 1) + 4 * l) * 4, 0, 0, 0);
+      dma16(rs, (qb * FA_KB + 32 * (w & 1) + 4 * l) * 4, 0, d + 4 * BK + (w >> 1) * 128 + (w & 1) * 64);
   };
   f32x16 adk[NDB], adv[NDB];
 #pragma unroll

@@ -9,6 +9,7 @@ namespace kvm {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
 // v[k] for one row: pro 0 x, 1 x*rstd*gamma (rstd of the whole row), 2 silu(x)*x2; rounded to bf16 (registry op 134).
 // Copies n floats (f32 buffer, 16-byte aligned, n % 4 == 0) to LDS with all of a thread's loads issued together;
@@ -56,7 +57,7 @@ __device__ __forceinline__ float dot8(const u16x8_t w, const LDS float* v) {
 }
 
 // Registry op 134. Each wave owns two weight rows at a time and keeps 16 loads of 16 bytes in flight per lane.
-__device__ __noinline__ void op_gemv_bf16(const Ctx& c) {
+__device__ __noinline__ void op_gemv_bf16_simt(const Ctx& c) {
   View x = c.buf(0), x2 = c.buf(1), g = c.buf(2), w = c.buf(3), out = c.buf(4), res = c.buf(5);
   int n0 = c.i(6), n1 = c.i(7), K = c.i(8), pro = c.i(9); float eps = c.f(10);
   LDS float* vs = (LDS float*)c.smem; LDS float* red = vs + 2 * K;
@@ -116,7 +117,7 @@ __device__ __noinline__ void op_gemv_bf16(const Ctx& c) {
 // steps, so four lanes cover a 128-byte line; A uses the same k permutation, which leaves the dot products unchanged.
 // The four waves split K into quarters and their 16x16 partial tiles are summed in LDS (fixed order).
 constexpr int ROWS_KC = 2048;   // K chunk whose prologue vectors are staged in LDS at once
-__device__ __noinline__ void op_gemv_bf16_rows(const Ctx& c) {
+__device__ __noinline__ void op_gemv_bf16_rows_simt(const Ctx& c) {
   View x = c.buf(0), x2 = c.buf(1), g = c.buf(2), w = c.buf(3), out = c.buf(4), res = c.buf(5);
   int n0 = c.i(6), n1 = c.i(7), K = c.i(8), M = c.i(9), pro = c.i(10); float eps = c.f(11);
   LDS uint16_t* vs = (LDS uint16_t*)c.smem;              // [16][ROWS_KC + 8] bf16
@@ -190,6 +191,208 @@ __device__ __noinline__ void op_gemv_bf16_rows(const Ctx& c) {
       }
     }
   }
+}
+
+
+// ---------------------------------------------------------------------------------------------- streaming GEMV
+// out[m, n] = sum_k v[m, k] * w[n, k] (+ res[m, n]) for M <= 16 rows of activations (op 134 with M = 1, and op 301),
+// v = bf16(prologue(x)). The weight stream is the whole cost, so it is shaped for HBM:
+//   * each wave streams one quarter of K. A 64-k step covers 16 weight rows: lane l loads 32 contiguous bytes of row
+//     l % 16 (16 lanes cover 16 rows, the 4 lane groups cover the 64 k, so every 128-byte line is read whole) straight
+//     into the registers that two v_mfma_f32_16x16x32_bf16 take as their B operand; the activation rows are the A
+//     operand (rows >= M read as zero). Both operands take k in the same lane-group order, so the dot products are
+//     unchanged;
+//   * the weight loads are issued from inline assembly into a ring of GV_RING register pairs, GV_RING steps ahead,
+//     and each step waits with an explicit vmcnt tied to the registers it consumes: the compiler's own wait placement
+//     (which drains all loads at any branch) never sees them. Every step issues exactly two loads (past the end a
+//     re-read of a line just streamed), so the wait count is a constant, and the ring is drained before it goes out of
+//     scope;
+//   * the first steps' loads are requested before v is staged, which does not depend on the weights;
+//   * v is staged as bf16 [M][KC + 8] in LDS once per K chunk, with the activation loads batched; each wave adds its
+//     partial 16x16 tiles into its own LDS region, and the four regions are summed in wave order at the end (fixed
+//     order).
+constexpr int GV_GRP = 4;          // 16-row blocks whose partial tiles are kept in LDS at once
+constexpr int GV_RING = 12;        // 64-k steps in flight per wave (24 KiB per wave)
+
+__device__ __forceinline__ float gv_pro(int pro, float xv, float x2v, float gv, float rs) {
+  return pro == 1 ? xv * rs * gv : pro == 2 ? silu_f(xv) * x2v : xv;
+}
+
+// Shapes the stream form takes: K a multiple of 256 (each wave a whole number of 64-k steps) made of equal chunks,
+// 16-byte aligned rows.
+__device__ __forceinline__ bool gemv_stream_ok(const View& x, const View& x2, const View& w, const View& out, int K, int M, int pro) {
+  const int KC = M <= 8 ? 4096 : 2048;
+  return M >= 1 && M <= 16 && K % 256 == 0 && (K <= KC || K % KC == 0) && w.dtype == 2 && (w.cols % 8) == 0 && x.dtype != 1 &&
+         (x.cols % 4) == 0 && (pro != 2 || (x2.ok() && x2.dtype != 1 && (x2.cols % 4) == 0)) && out.dtype != 1 &&
+         (long long)w.rows * w.cols * 2 < 0x7fffffffll && (long long)x.rows * x.cols * 4 < 0x7fffffffll &&
+         (!x2.ok() || (long long)x2.rows * x2.cols * 4 < 0x7fffffffll);
+}
+
+// Four consecutive f32 or bf16 elements through a buffer descriptor: one 16-byte load either way (bf16 uses its
+// first half), converted by selects, so a batch of these has no branches for the compiler to wait at.
+struct Ld4 {
+  __amdgpu_buffer_rsrc_t rs;
+  int es;                              // element size: 4 (f32) or 2 (bf16)
+  __device__ __forceinline__ void init(const View& v) {
+    es = v.dtype == 2 ? 2 : 4;
+    rs = v.ok() ? buf_rsrc((const void*)v.p, (long long)v.rows * v.cols * es) : buf_rsrc((const void*)v.p, 0);
+  }
+  __device__ __forceinline__ f32x4n get(int idx) const {
+    const u32x4_t r = __builtin_amdgcn_raw_buffer_load_b128(rs, idx * es, 0, 0);
+    if (es == 2)
+      return f32x4n{__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u)};
+    return f32x4n{__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z), __uint_as_float(r.w)};
+  }
+};
+
+// 32 bytes of weights into registers, invisible to the compiler's wait tracking.
+__device__ __forceinline__ void gv_load(u16x8_t& a, u16x8_t& b, i32x4_t rs, int off) {
+  asm volatile("buffer_load_dwordx4 %0, %2, %3, 0 offen\n\tbuffer_load_dwordx4 %1, %2, %3, 0 offen offset:16"
+               : "=v"(a), "=v"(b) : "v"(off), "s"(rs));
+}
+// vmcnt(N), tied to the registers about to be read so that their uses stay after it.
+template <int N> __device__ __forceinline__ void gv_wait(u16x8_t& a, u16x8_t& b) {
+  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N));
+}
+
+__device__ __noinline__ void gemv_stream(const Ctx& c, int M, int pro, float eps) {
+  const View x = uniform_view(c.buf(0)), x2 = uniform_view(c.buf(1)), g = uniform_view(c.buf(2)), w = uniform_view(c.buf(3));
+  const View out = uniform_view(c.buf(4)), res = uniform_view(c.buf(5));
+  const int n0 = rfl(c.i(6)), n1 = rfl(c.i(7)), K = rfl(c.i(8));
+  const int KC = M <= 8 ? 4096 : 2048, VS = KC + 8;
+  LDS uint16_t* vs = (LDS uint16_t*)c.smem;                                    // [M][VS]
+  LDS float* rstd = (LDS float*)(c.smem + ((M * VS * 2 + 15) & ~15));          // [16]
+  LDS float* part = rstd + 16;                                                  // [4][GV_GRP][256]
+  const int l = lane(), wv = wave(), nrows = n1 - n0, nrb = (nrows + 15) / 16, rowb = w.cols * 2;
+#ifdef KVM_GEMM_PROF
+  unsigned long long pt[8] = {(unsigned long long)wall_clock64(), 0, 0, 0, 0, 0, 0, 0};
+#endif
+  const i32x4_t rw = dma_rsrc((const void*)(w.h() + (long long)n0 * w.cols), ((long long)w.rows - n0) * w.cols * 2);
+  Ld4 lx, lx2, lg;
+  lx.init(x); lx2.init(x2); lg.init(g);
+  const bool arow = (l & 15) < M;
+  const LDS uint16_t* va = vs + (arow ? (l & 15) : 0) * VS + 16 * (l >> 4);   // rows >= M read row 0 and are zeroed
+  bool rstd_done = pro != 1;
+  u16x8_t wb[GV_RING][2];
+  for (int g0 = 0; g0 < nrb; g0 += GV_GRP) {
+    const int ng = min(GV_GRP, nrb - g0);
+    for (int kc = 0; kc < K; kc += KC) {
+      const int kn = min(KC, K - kc), kq = kn / 4, ns = kq / 64, T = ng * ns;
+      // byte offset of this lane's 32 bytes in step 0 of row block rb (rows past n1 repeat the last; dropped below)
+      auto row_base = [&](int rb) { return min((g0 + rb) * 16 + (l & 15), nrows - 1) * rowb + (kc + wv * kq) * 2 + 32 * (l >> 4); };
+      // issue cursor: step it = (irb, ist)
+      int irb = 0, ist = 0, ibase = row_base(0);
+      const int dummy = ibase;
+      auto issue_next = [&](u16x8_t& a, u16x8_t& b) {
+        const bool live = irb < ng;
+        gv_load(a, b, rw, live ? ibase + ist * 128 : dummy);
+        if (live && ++ist == ns) { ist = 0; ++irb; if (irb < ng) ibase = row_base(irb); }
+      };
+#pragma unroll
+      for (int j = 0; j < GV_RING; ++j) issue_next(wb[j][0], wb[j][1]);     // weights first: they do not wait for x
+      if (!rstd_done) {                                                          // rstd of each row over all of K
+        for (int m = wv; m < M; m += KVM_WAVES) {
+          float ss = 0.f;
+          for (int k = 4 * l; k < K; k += 4 * 256) {
+            f32x4n t4[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) t4[u] = lx.get(m * x.cols + min(k + 256 * u, K - 4));
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              if (k + 256 * u < K) ss += (t4[u].x * t4[u].x + t4[u].y * t4[u].y) + (t4[u].z * t4[u].z + t4[u].w * t4[u].w);
+          }
+          ss = wave_sum(ss);
+          if (l == 0) rstd[m] = 1.f / sqrtf(ss / (float)K + eps);
+        }
+        rstd_done = true;
+      }
+      if (kc == 0) for (int e = l; e < ng * 256; e += 64) part[(wv * GV_GRP) * 256 + e] = 0.f;
+      __syncthreads();                                                          // rstd ready; the previous chunk's readers are done
+      {                                                                          // v = bf16(prologue(x)) for this chunk
+        const int q4 = kn / 4, nel = M * q4;
+        for (int e0 = tid(); e0 < nel; e0 += 4 * KVM_THREADS) {
+          f32x4n xv[4], x2v[4], gg[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int e = min(e0 + u * KVM_THREADS, nel - 1), m = e / q4, k = kc + 4 * (e % q4);
+            xv[u] = lx.get(m * x.cols + k);                                      // absent views read as 0
+            x2v[u] = lx2.get(m * x2.cols + k);
+            gg[u] = lg.get(k);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int e = e0 + u * KVM_THREADS;
+            if (e < nel) {
+              const int m = e / q4, k = 4 * (e % q4);
+              const float rs = pro == 1 ? rstd[m] : 0.f;
+              const f32x4n a2 = pro == 2 ? x2v[u] : f32x4n{0.f, 0.f, 0.f, 0.f}, ga = pro == 1 ? gg[u] : f32x4n{0.f, 0.f, 0.f, 0.f};
+              *(LDS u16x4_t*)(vs + m * VS + k) = u16x4_t{f2bf(gv_pro(pro, xv[u].x, a2.x, ga.x, rs)), f2bf(gv_pro(pro, xv[u].y, a2.y, ga.y, rs)),
+                                                        f2bf(gv_pro(pro, xv[u].z, a2.z, ga.z, rs)), f2bf(gv_pro(pro, xv[u].w, a2.w, ga.w, rs))};
+            }
+          }
+        }
+      }
+      __syncthreads();
+#ifdef KVM_GEMM_PROF
+      if (g0 == 0) pt[1] = wall_clock64();
+#endif
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      int crb = 0, cst = 0;
+      const LDS uint16_t* vk = va + wv * kq;
+      for (int t0 = 0; t0 < T; t0 += GV_RING) {
+#pragma unroll
+        for (int j = 0; j < GV_RING; ++j) {
+          if (t0 + j < T) {
+            gv_wait<2 * (GV_RING - 1)>(wb[j][0], wb[j][1]);                  // this step's two loads have landed
+            const u16x8_t a0 = *(const LDS u16x8_t*)(vk + cst * 64), a1 = *(const LDS u16x8_t*)(vk + cst * 64 + 8);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8_t)(arow ? a0 : u16x8_t{}), (bf16x8_t)wb[j][0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8_t)(arow ? a1 : u16x8_t{}), (bf16x8_t)wb[j][1], acc, 0, 0, 0);
+            issue_next(wb[j][0], wb[j][1]);
+            if (++cst == ns) {        // row block finished for this chunk: D[m][n], lane holds m = 4*(l/16) + i, n = l % 16
+              LDS float* pp = part + (wv * GV_GRP + crb) * 256 + 4 * (l >> 4) * 16 + (l & 15);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) pp[i * 16] += acc[i];
+              acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+              cst = 0; ++crb;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < GV_RING; ++j) gv_wait<0>(wb[j][0], wb[j][1]);      // the ring's trailing re-reads have landed
+    }
+#ifdef KVM_GEMM_PROF
+    if (g0 == 0) pt[2] = wall_clock64();
+#endif
+    __syncthreads();
+#ifdef KVM_GEMM_PROF
+    if (g0 == 0) pt[3] = wall_clock64();
+#endif
+    for (int e = tid(); e < ng * 16 * M; e += KVM_THREADS) {                   // sum the four waves' tiles, in wave order
+      const int rb = e / (16 * M), m = (e / 16) % M, nn = e % 16, n = n0 + (g0 + rb) * 16 + nn;
+      if (n >= n1) continue;
+      const int q = rb * 256 + m * 16 + nn;
+      const float s = (part[q] + part[GV_GRP * 256 + q]) + (part[2 * GV_GRP * 256 + q] + part[3 * GV_GRP * 256 + q]);
+      out.st((long long)m * out.cols + n, s + (res.ok() ? res.ld((long long)m * res.cols + n) : 0.f));
+    }
+    __syncthreads();
+  }
+#ifdef KVM_GEMM_PROF
+  pt[4] = wall_clock64();
+  __syncthreads();
+  if (tid() == 0 && out.dtype == 0) { unsigned long long* o = (unsigned long long*)(out.f() + n0); for (int i = 0; i < 5; ++i) o[i] = pt[i]; o[5] = g_prof[blockIdx.x][6]; }
+#endif
+}
+
+__device__ __noinline__ void op_gemv_bf16(const Ctx& c) {
+  const View x = c.buf(0), x2 = c.buf(1), w = c.buf(3), out = c.buf(4);
+  if (gemv_stream_ok(x, x2, w, out, c.i(8), 1, c.i(9))) gemv_stream(c, 1, c.i(9), c.f(10));
+  else op_gemv_bf16_simt(c);
+}
+__device__ __noinline__ void op_gemv_bf16_rows(const Ctx& c) {
+  const View x = c.buf(0), x2 = c.buf(1), w = c.buf(3), out = c.buf(4);
+  if (gemv_stream_ok(x, x2, w, out, c.i(8), c.i(9), c.i(10))) gemv_stream(c, c.i(9), c.i(10), c.f(11));
+  else op_gemv_bf16_rows_simt(c);
 }
 
 }  // namespace kvm

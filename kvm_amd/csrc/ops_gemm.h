@@ -182,6 +182,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, long l
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)min(bytes, 0x7fffffffll), 0x00020000);
 }
 
+// Direct HBM -> LDS loads (buffer_load_dwordx4 ... lds: lane l's 16 bytes land at M0 + 16 l). They are issued from
+// inline assembly on purpose: the compiler tracks its own LDS-DMA loads and, lacking alias information, waits for all
+// of them (vmcnt(0)) before any later LDS read, which drains every prefetch pipeline built on them. Code using dma16
+// therefore orders its LDS reads itself, with wait_vm before reading a staged block and a barrier where other waves
+// read it.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4_t dma_rsrc(const void* p, long long bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const long long nb = bytes < 0 ? 0 : min(bytes, 0x7fffffffll);
+  return i32x4_t{__builtin_amdgcn_readfirstlane((int)(uint32_t)a), __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffff)),
+                 __builtin_amdgcn_readfirstlane((int)nb), 0x00020000};
+}
+// 16 bytes per lane from rs + voff + soff into LDS at dst + 16 * lane (dst uniform across the wave).
+__device__ __forceinline__ void dma16(i32x4_t rs, int voff, int soff, const LDS void* dst) {
+  const int m = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)dst);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" :: "s"(m), "v"(voff), "s"(rs), "s"(soff) : "memory", "m0");
+}
+
 // One operand slab: R tile rows x GK k values. NV 16-byte vectors per thread.
 //   KC (k-contiguous, element (r, k) at X[r*cols + k]): vector q of a thread is row idx/8, k-chunk idx%8 with
 //     idx = tid + 256q, so 8 lanes read one 128-byte row segment.
@@ -459,24 +477,22 @@ __device__ __noinline__ void gemm_loop(const Ctx& c) {
 constexpr int DK = 32;
 constexpr int DNS = 4;
 
-__device__ __forceinline__ void wait_vm(int n) {       // s_waitcnt vmcnt(n), n <= 15 (other counters untouched)
-  switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
-    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
-    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
-    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
-    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-    case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
-    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
-    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
-    case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
-    case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
-    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
-    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;   // wait for everything (never less safe)
+// s_waitcnt vmcnt(n) for a wave-uniform runtime n (other counters untouched); n above 30 waits for everything. The
+// immediate must be a constant, so a (scalar) switch picks it; the wait is inline assembly with a memory clobber so
+// that no LDS read of a dma16-staged block moves above it.
+template <int N> __device__ __forceinline__ void wait_vm_c() { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory"); }
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (__builtin_amdgcn_readfirstlane(n)) {
+#define KVM_WV(k) case k: wait_vm_c<k>(); break;
+    KVM_WV(0) KVM_WV(1) KVM_WV(2) KVM_WV(3) KVM_WV(4) KVM_WV(5) KVM_WV(6) KVM_WV(7) KVM_WV(8) KVM_WV(9) KVM_WV(10) KVM_WV(11)
+    KVM_WV(12) KVM_WV(13) KVM_WV(14) KVM_WV(15) KVM_WV(16) KVM_WV(17) KVM_WV(18) KVM_WV(19) KVM_WV(20) KVM_WV(21) KVM_WV(22)
+    KVM_WV(23) KVM_WV(24) KVM_WV(25) KVM_WV(26) KVM_WV(27) KVM_WV(28) KVM_WV(29) KVM_WV(30)
+#undef KVM_WV
+    default: wait_vm_c<0>(); break;
   }
 }
+// lgkmcnt(0): this wave's LDS reads have returned (before a dma16 reuses the LDS they read).
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
@@ -485,17 +501,17 @@ template <int R, bool KC> struct DOp {
   static constexpr int NL = BLK / KVM_WAVES;            // direct loads per thread per stage
   static constexpr int UPR = KC ? DK / 8 : R / 8;       // 16-byte units per LDS row
   static_assert(NL >= 1 && BLK % KVM_WAVES == 0, "tile shape");
-  __amdgpu_buffer_rsrc_t rs;
+  i32x4_t rs;
   int voff[NL];
   int sstep;
   __device__ static __forceinline__ int kswz(int row) { return (row >> 2) & 3; }                       // k-contiguous
   __device__ static __forceinline__ int rswz(int k) { return R >= 128 ? 4 * (k & 3) : 4 * ((k >> 1) & 1); }  // row-contiguous
   __device__ __forceinline__ void init(const View& X, int r0) {
     if constexpr (KC) {
-      rs = buf_rsrc((const void*)(X.h() + (long long)r0 * X.cols), ((long long)X.rows - r0) * X.cols * 2);
+      rs = dma_rsrc((const void*)(X.h() + (long long)r0 * X.cols), ((long long)X.rows - r0) * X.cols * 2);
       sstep = DK * 2;
     } else {
-      rs = buf_rsrc((const void*)(X.h() + r0), (long long)X.rows * X.cols * 2 - (long long)r0 * 2);
+      rs = dma_rsrc((const void*)(X.h() + r0), (long long)X.rows * X.cols * 2 - (long long)r0 * 2);
       sstep = DK * X.cols * 2;
     }
 #pragma unroll
@@ -509,7 +525,7 @@ template <int R, bool KC> struct DOp {
   __device__ __forceinline__ void issue(LDS uint16_t* lds, int s) const {
 #pragma unroll
     for (int q = 0; q < NL; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS void*)(lds + (q * KVM_WAVES + wave()) * 512), 16, voff[q], s * sstep, 0, 0);
+      dma16(rs, voff[q], s * sstep, lds + (q * KVM_WAVES + wave()) * 512);
   }
   // MFMA operand for the 32 tile rows rb.. and k16 step kk: 8 bf16 of row rb + l%32 at k = 16kk + 8(l/32) ...
   __device__ __forceinline__ bf16x8 frag(const LDS uint16_t* lds, int rb, int kk) const {

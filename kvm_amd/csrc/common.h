@@ -92,10 +92,11 @@ __device__ __forceinline__ void fence_release() { __builtin_amdgcn_fence(__ATOMI
 // ---------------------------------------------------------------------------------------------- bf16
 __device__ __host__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 // float -> bf16, round to nearest even; NaN stays NaN (quiet bit set), inf stays inf.
+// Round to nearest even; NaNs stay NaN (quiet bit set), infinities stay infinite. A select, not a branch.
 __device__ __forceinline__ uint16_t f2bf(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0x007fffffu) ? 0x40u : 0u));
-  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x40u) : r);
 }
 __device__ __forceinline__ float round_bf(float x) { return bf2f(f2bf(x)); }
 

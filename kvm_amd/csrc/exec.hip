@@ -161,6 +161,8 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 136: op_attn_decode_merge(c); break;
     case 300: op_head_rmsnorm(c); break;
     case 301: op_gemv_bf16_rows(c); break;
+    case 302: op_matmul_mma_bf16_kr(c); break;
+    case 303: op_splitk_reduce(c); break;
     default: if (threadIdx.x == 0) c.fail(KVM_ERR_BAD_OP, op, 0);
   }
 }

@@ -9,7 +9,6 @@ namespace kvm {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
 // v[k] for one row: pro 0 x, 1 x*rstd*gamma (rstd of the whole row), 2 silu(x)*x2; rounded to bf16 (registry op 134).
 // Copies n floats (f32 buffer, 16-byte aligned, n % 4 == 0) to LDS with all of a thread's loads issued together;
@@ -227,23 +226,6 @@ __device__ __forceinline__ bool gemv_stream_ok(const View& x, const View& x2, co
          (long long)w.rows * w.cols * 2 < 0x7fffffffll && (long long)x.rows * x.cols * 4 < 0x7fffffffll &&
          (!x2.ok() || (long long)x2.rows * x2.cols * 4 < 0x7fffffffll);
 }
-
-// Four consecutive f32 or bf16 elements through a buffer descriptor: one 16-byte load either way (bf16 uses its
-// first half), converted by selects, so a batch of these has no branches for the compiler to wait at.
-struct Ld4 {
-  __amdgpu_buffer_rsrc_t rs;
-  int es;                              // element size: 4 (f32) or 2 (bf16)
-  __device__ __forceinline__ void init(const View& v) {
-    es = v.dtype == 2 ? 2 : 4;
-    rs = v.ok() ? buf_rsrc((const void*)v.p, (long long)v.rows * v.cols * es) : buf_rsrc((const void*)v.p, 0);
-  }
-  __device__ __forceinline__ f32x4n get(int idx) const {
-    const u32x4_t r = __builtin_amdgcn_raw_buffer_load_b128(rs, idx * es, 0, 0);
-    if (es == 2)
-      return f32x4n{__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u)};
-    return f32x4n{__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z), __uint_as_float(r.w)};
-  }
-};
 
 // 32 bytes of weights into registers, invisible to the compiler's wait tracking.
 __device__ __forceinline__ void gv_load(u16x8_t& a, u16x8_t& b, i32x4_t rs, int off) {

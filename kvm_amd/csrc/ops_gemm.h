@@ -301,31 +301,28 @@ __device__ __forceinline__ void st4(const View& X, long long o, f32x4n v) {
   else *(GLOBAL f32x4n*)(X.f() + o) = v;
 }
 
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+// Four consecutive f32 or bf16 elements through a buffer descriptor: one 16-byte load either way (bf16 uses its
+// first half), converted by selects, so a batch of these has no branches for the compiler to wait at.
+struct Ld4 {
+  __amdgpu_buffer_rsrc_t rs;
+  int es;                              // element size: 4 (f32) or 2 (bf16)
+  __device__ __forceinline__ void init(const View& v, bool use = true) {
+    es = v.dtype == 2 ? 2 : 4;
+    rs = v.ok() && use ? buf_rsrc((const void*)v.p, (long long)v.rows * v.cols * es) : buf_rsrc((const void*)v.p, 0);
+  }
+  __device__ __forceinline__ u32x4_t raw(int idx) const { return __builtin_amdgcn_raw_buffer_load_b128(rs, idx * es, 0, 0); }
+  __device__ __forceinline__ f32x4n cvt(u32x4_t r) const {
+    const bool h = es == 2;                      // selects, not a branch: a branch makes every load wait alone
+    return f32x4n{__uint_as_float(h ? r.x << 16 : r.x), __uint_as_float(h ? r.x & 0xffff0000u : r.y),
+                  __uint_as_float(h ? r.y << 16 : r.z), __uint_as_float(h ? r.y & 0xffff0000u : r.w)};
+  }
+  __device__ __forceinline__ f32x4n get(int idx) const { return cvt(raw(idx)); }
+};
+
 __device__ __noinline__ void epi_tail(Epi e, int N, int m, int n, f32x4n a) {
   for (int i = 0; i < 4 && n + i < N; ++i) e.put(m, n + i, a[i]);
 }
-// Epilogue of 4 consecutive outputs (m, n..n+3), all inside the matrix and vector-aligned:
-// alpha -> bias -> dgelu(pre) | (pre, gelu) -> res -> accumulate.
-__device__ __forceinline__ void epi4_vec(const Epi& e, int m, int n, f32x4n a) {
-  const long long o = (long long)m * e.out.cols + n;
-  f32x4n v = a * e.alpha;
-  if (e.bias.ok()) v += ld4(e.bias, n);
-  if (e.dg) {
-    const f32x4n p = ld4(e.pre, (long long)m * e.pre.cols + n);
-    v.x *= gelu_grad_f(p.x); v.y *= gelu_grad_f(p.y); v.z *= gelu_grad_f(p.z); v.w *= gelu_grad_f(p.w);
-  } else {
-    if (e.pre.ok()) st4(e.pre, (long long)m * e.pre.cols + n, v);
-    if (e.ge) { v.x = gelu_f(v.x); v.y = gelu_f(v.y); v.z = gelu_f(v.z); v.w = gelu_f(v.w); }
-  }
-  if (e.res.ok()) v += ld4(e.res, (long long)m * e.res.cols + n);
-  if (e.accum) v += ld4(e.out, o);
-  st4(e.out, o, v);
-}
-__device__ __forceinline__ void epi4(const Epi& e, bool vec, int N, int m, int n, f32x4n a) {
-  if (!vec || n + 4 > N) epi_tail(e, N, m, n, a);
-  else epi4_vec(e, m, n, a);
-}
-
 // The arguments of a GEMM tile task (ops 114 and 122 share the layout a, b, out, bias, res, pre, m0, n0, M, N, K,
 // flags, alpha), read from the dispatcher's LDS copies and made wave-uniform, so nothing is re-read from memory later.
 struct GemmArgs { View A, B; Epi e; int m0, n0, M, N, K, fl; };
@@ -345,65 +342,159 @@ __device__ __forceinline__ GemmArgs gemm_args(const Ctx& c) {
   return g;
 }
 
-// acc[i][j][r] = D^T: row m = l % 32 of block i, columns 8*(r/4) + 4*(l/32) + r%4 of block j. Whole, vector-aligned
-// tiles with a plain epilogue (out = acc) store straight from the accumulators: each lane writes 4 consecutive columns
-// of one row per register group. Every other tile goes through LDS (two halves, one per wave row), then every thread
-// applies the epilogue to 4-column pieces along the rows with bounds checks.
+// Epilogue. The accumulators hold D^T: acc[i][j][r] is row m = l % 32 of block i, column 8*(r/4) + 4*(l/32) + r%4 of
+// block j. The whole tile is staged in LDS as f32 (TM x TN floats, at most 128 KiB), its 16-byte column chunks XOR-
+// swizzled by row so that both the accumulator writes (16 rows per phase, one chunk) and the row reads (one row, 16
+// chunks) are conflict-free. The epilogue proper then runs as one out-of-line function per tile shape and output
+// type: the accumulators are dead by then, so the call saves almost nothing, and its code exists once instead of once
+// per operand orientation. There every lane owns a fixed 4-column piece (bias loaded once) and the waves take rows in
+// turn, with the res / pre / previous-output loads of a batch of rows issued together through branch-free buffer
+// loads; every row is stored as whole lines. Pieces that are not whole, aligned vectors take the scalar path.
+template <int TN> __device__ __forceinline__ int epi_swz(int r) { return r & ((TN / 4 < 32 ? TN / 4 : 32) - 1); }
+
+// Whole, aligned tile with one of the epilogues the GPT graphs use, as straight-line code: KIND 0 = (bias), 1 = bias +
+// residual, 2 = accumulate into the output, 3 = times gelu'(pre), 4 = pre = bias-added value, out = gelu(pre).
+// The second operand of kinds 1-3 is loaded raw for a batch of rows before any of them is used.
+template <int TM, int TN, bool OBF, int KIND>
+__device__ __forceinline__ void epi_rows(const Ctx& c, const GemmArgs& g) {
+  constexpr int LPR = TN / 4, RPI = 64 / LPR, NI = TM / KVM_WAVES / RPI, NB = NI < 8 ? NI : 8;
+  const Epi& e = g.e;
+  const LDS float* et = (const LDS float*)c.smem;
+  const int l = lane(), w = wave(), ch = l % LPR, n = g.n0 + 4 * ch;
+  Ld4 lb, lx;
+  lb.init(e.bias);
+  const View& xv = KIND == 1 ? e.res : KIND == 2 ? e.out : e.pre;
+  lx.init(xv, KIND >= 1 && KIND <= 3);
+  const f32x4n bv = lb.get(n);
+  const int xc = xv.cols;
+  for (int k0 = 0; k0 < NI; k0 += NB) {
+    u32x4_t raw[NB];
+    f32x4n a[NB];
+    if constexpr (KIND >= 1 && KIND <= 3) {
+#pragma unroll
+      for (int u = 0; u < NB; ++u) raw[u] = lx.raw((g.m0 + ((k0 + u) * KVM_WAVES + w) * RPI + l / LPR) * xc + n);
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int r = ((k0 + u) * KVM_WAVES + w) * RPI + l / LPR;
+      a[u] = *(const LDS f32x4n*)(et + r * TN + 4 * (ch ^ epi_swz<TN>(r)));
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int m = g.m0 + ((k0 + u) * KVM_WAVES + w) * RPI + l / LPR;
+      f32x4n v = a[u] * e.alpha + bv;
+      if constexpr (KIND == 1 || KIND == 2) v += lx.cvt(raw[u]);
+      if constexpr (KIND == 3) {
+        const f32x4n p = lx.cvt(raw[u]);
+        v.x *= gelu_grad_f(p.x); v.y *= gelu_grad_f(p.y); v.z *= gelu_grad_f(p.z); v.w *= gelu_grad_f(p.w);
+      }
+      if constexpr (KIND == 4) {
+        st4(e.pre, (long long)m * e.pre.cols + n, v);
+        v.x = gelu_f(v.x); v.y = gelu_f(v.y); v.z = gelu_f(v.z); v.w = gelu_f(v.w);
+      }
+      if constexpr (OBF) *(GLOBAL u16x4_t*)(e.out.h() + (long long)m * e.out.cols + n) = u16x4_t{f2bf(v.x), f2bf(v.y), f2bf(v.z), f2bf(v.w)};
+      else *(GLOBAL f32x4n*)(e.out.f() + (long long)m * e.out.cols + n) = v;
+    }
+  }
+#ifdef KVM_GEMM_PROF
+  KVM_PT(10);
+#endif
+}
+
+template <int TM, int TN, bool OBF>
+__device__ __noinline__ void gemm_epilogue(const Ctx& c) {
+  constexpr int LPR = TN / 4, RPI = 64 / LPR, NI = TM / KVM_WAVES / RPI;   // lanes per row, rows per instruction
+  constexpr int NB = NI < 4 ? NI : 4;
+  const GemmArgs g = gemm_args(c);
+  const Epi& e = g.e;
+  const LDS float* et = (const LDS float*)c.smem;
+  const int l = lane(), w = wave(), ch = l % LPR, n = g.n0 + 4 * ch;
+  const long long lim = 0x7fffffffll;
+  const bool small = (long long)g.M * e.out.cols * 4 < lim && (long long)g.M * e.res.cols * 4 < lim && (long long)g.M * e.pre.cols * 4 < lim;
+  const bool vec = (e.out.cols & 3) == 0 && (!e.res.ok() || (e.res.cols & 3) == 0) && (!e.pre.ok() || (e.pre.cols & 3) == 0);
+  const bool fast = vec && small && n + 4 <= g.N;
+  const bool dg = e.dg != 0, ge = e.ge != 0, spre = !dg && e.pre.ok(), loads = e.res.ok() || dg || e.accum;
+  if (vec && small && g.m0 + TM <= g.M && g.n0 + TN <= g.N) {
+    const bool res = e.res.ok(), acc = e.accum != 0;
+    if (!res && !acc && !dg && !ge && !spre) { epi_rows<TM, TN, OBF, 0>(c, g); return; }
+    if (res && !acc && !dg && !ge && !spre) { epi_rows<TM, TN, OBF, 1>(c, g); return; }
+    if (!res && acc && !dg && !ge && !spre) { epi_rows<TM, TN, OBF, 2>(c, g); return; }
+    if (!res && !acc && dg) { epi_rows<TM, TN, OBF, 3>(c, g); return; }
+    if (!res && !acc && !dg && ge && spre) { epi_rows<TM, TN, OBF, 4>(c, g); return; }
+  }
+  Ld4 lb, lr, lp, lo;
+  lb.init(e.bias); lr.init(e.res); lp.init(e.pre, dg); lo.init(e.out, e.accum != 0);
+  const f32x4n bv = lb.get(n);
+#ifdef KVM_GEMM_PROF
+  KVM_PT(9);
+#endif
+  for (int k0 = 0; k0 < NI; k0 += NB) {
+    f32x4n rv[NB], pv[NB], ov[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) { rv[u] = f32x4n{0.f, 0.f, 0.f, 0.f}; pv[u] = rv[u]; ov[u] = rv[u]; }
+    if (loads && small) {
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        const int m = g.m0 + ((k0 + u) * KVM_WAVES + w) * RPI + l / LPR;
+        rv[u] = lr.get(m * e.res.cols + n);
+        pv[u] = lp.get(m * e.pre.cols + n);
+        ov[u] = lo.get(m * e.out.cols + n);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int r = ((k0 + u) * KVM_WAVES + w) * RPI + l / LPR, m = g.m0 + r;
+      if (m >= g.M) continue;
+      const f32x4n a = *(const LDS f32x4n*)(et + r * TN + 4 * (ch ^ epi_swz<TN>(r)));
+      if (fast) {
+        f32x4n v = a * e.alpha + bv;
+        if (dg) {
+          v.x *= gelu_grad_f(pv[u].x); v.y *= gelu_grad_f(pv[u].y); v.z *= gelu_grad_f(pv[u].z); v.w *= gelu_grad_f(pv[u].w);
+        } else {
+          if (spre) st4(e.pre, (long long)m * e.pre.cols + n, v);
+          if (ge) { v.x = gelu_f(v.x); v.y = gelu_f(v.y); v.z = gelu_f(v.z); v.w = gelu_f(v.w); }
+        }
+        v += rv[u] + ov[u];
+        if constexpr (OBF) *(GLOBAL u16x4_t*)(e.out.h() + (long long)m * e.out.cols + n) = u16x4_t{f2bf(v.x), f2bf(v.y), f2bf(v.z), f2bf(v.w)};
+        else *(GLOBAL f32x4n*)(e.out.f() + (long long)m * e.out.cols + n) = v;
+      } else if (n < g.N) {
+        epi_tail(e, g.N, m, n, a);
+      }
+    }
+  }
+#ifdef KVM_GEMM_PROF
+  KVM_PT(10);
+#endif
+}
+
+// Stages the accumulators in LDS (see above) and runs the epilogue.
 template <int TM, int TN>
 __device__ __forceinline__ void gemm_store(const Ctx& c, const f32x16 (&acc)[TM / 64][TN / 64], const GemmArgs& g) {
-  constexpr int BM = TM / 64, BN = TN / 64, WM = TM / 2;
-  const int wm0 = (wave() >> 1) * WM, wn0 = (wave() & 1) * (TN / 2), l = lane();
-  const Epi& e = g.e;
-  const bool vec = (e.out.cols & 3) == 0 && (!e.res.ok() || (e.res.cols & 3) == 0) && (!e.pre.ok() || (e.pre.cols & 3) == 0);
-  const bool plain = !e.bias.ok() && !e.res.ok() && !e.pre.ok() && !e.accum && !e.ge && !e.dg && e.alpha == 1.0f;
-  if (plain && vec && g.m0 + TM <= g.M && g.n0 + TN <= g.N) {
-    const long long ld = e.out.cols;
-    if (e.out.dtype == 2) {
-      GLOBAL uint16_t* o = e.out.h() + (long long)(g.m0 + wm0 + (l & 31)) * ld + g.n0 + wn0 + 4 * (l >> 5);
-#pragma unroll
-      for (int i = 0; i < BM; ++i)
-#pragma unroll
-        for (int j = 0; j < BN; ++j)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            *(GLOBAL u16x4_t*)(o + i * 32 * ld + j * 32 + 8 * q) =
-                u16x4_t{f2bf(acc[i][j][4 * q]), f2bf(acc[i][j][4 * q + 1]), f2bf(acc[i][j][4 * q + 2]), f2bf(acc[i][j][4 * q + 3])};
-    } else {
-      GLOBAL float* o = e.out.f() + (long long)(g.m0 + wm0 + (l & 31)) * ld + g.n0 + wn0 + 4 * (l >> 5);
-#pragma unroll
-      for (int i = 0; i < BM; ++i)
-#pragma unroll
-        for (int j = 0; j < BN; ++j)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            *(GLOBAL f32x4n*)(o + i * 32 * ld + j * 32 + 8 * q) = f32x4n{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-    }
-    return;
-  }
-  constexpr int ES = TN + 4;                               // fp32 row stride: rows land 4 banks apart
-  static_assert(WM * ES * 4 <= KVM_LDS_BYTES, "LDS epilogue");
+  constexpr int BM = TM / 64, BN = TN / 64, WM = TM / 2, WN = TN / 2;
+  static_assert(TM * TN * 4 <= KVM_LDS_BYTES, "LDS epilogue");
+  const int wm0 = (wave() >> 1) * WM, wn0 = (wave() & 1) * WN, l = lane();
   LDS float* et = (LDS float*)c.smem;
   __syncthreads();                                         // operand stages are no longer read
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    if ((wave() >> 1) == half) {
+  for (int i = 0; i < BM; ++i) {
+    const int r = wm0 + i * 32 + (l & 31);
 #pragma unroll
-      for (int i = 0; i < BM; ++i)
+    for (int j = 0; j < BN; ++j)
 #pragma unroll
-        for (int j = 0; j < BN; ++j)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            *(LDS f32x4n*)(et + (i * 32 + (l & 31)) * ES + wn0 + j * 32 + 8 * q + 4 * (l >> 5)) =
-                f32x4n{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-    }
-    __syncthreads();
-    const int mb = g.m0 + half * WM;
-    for (int q = tid(); q < WM * (TN / 4); q += KVM_THREADS) {
-      const int r = q / (TN / 4), cc = (q % (TN / 4)) * 4, m = mb + r, n = g.n0 + cc;
-      if (m < g.M && n < g.N) epi4(e, vec, g.N, m, n, *(const LDS f32x4n*)(et + r * ES + cc));
-    }
-    __syncthreads();
+      for (int q = 0; q < 4; ++q) {
+        const int chunk = (wn0 + j * 32 + 8 * q) / 4 + (l >> 5);
+        *(LDS f32x4n*)(et + r * TN + 4 * (chunk ^ epi_swz<TN>(r))) = f32x4n{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+      }
   }
+  __syncthreads();
+#ifdef KVM_GEMM_PROF
+  KVM_PT(8);
+#endif
+  if (g.e.out.dtype == 2) gemm_epilogue<TM, TN, true>(c);
+  else gemm_epilogue<TM, TN, false>(c);
+#ifdef KVM_GEMM_PROF
+  KVM_PT(11);
+#endif
 }
 
 template <int TM, int TN, bool FAST, bool AKC, bool BKC>
@@ -475,7 +566,7 @@ __device__ __noinline__ void gemm_loop(const Ctx& c) {
 //     mb + 4*(i16%4) .. +3, lane i16 receives rows mb + i16 at k = kb .. kb+3, i.e. an MFMA operand (8 k values of one
 //     row) from two reads.
 constexpr int DK = 32;
-constexpr int DNS = 4;
+constexpr int DNS = 5;
 
 // s_waitcnt vmcnt(n) for a wave-uniform runtime n (other counters untouched); n above 30 waits for everything. The
 // immediate must be a constant, so a (scalar) switch picks it; the wait is inline assembly with a memory clobber so
@@ -569,34 +660,57 @@ __device__ __noinline__ void gemm_lds(const Ctx& c) {
 #pragma unroll
     for (int j = 0; j < BN; ++j) acc[i][j] = f32x16{};
   const int nst = K / DK;
+  constexpr int NLS = DOp<TM, AKC>::NL + DOp<TN, BKC>::NL;  // direct loads per thread per stage
+  // Waits until at most k stages issued after the one needed are still in flight (k <= DNS - 2).
+  auto wait_stages = [](int k) {
+    k = __builtin_amdgcn_readfirstlane(k);
+    if (k >= 3) wait_vm_c<3 * NLS>(); else if (k == 2) wait_vm_c<2 * NLS>(); else if (k == 1) wait_vm_c<NLS>(); else wait_vm_c<0>();
+  };
+  static_assert(DNS - 2 <= 3, "wait_stages");
   __syncthreads();                                 // the previous task may still read this LDS
 #pragma unroll
   for (int p = 0; p < DNS - 1; ++p)
     if (p < nst) { da.issue(lds + p * ST, p); db.issue(lds + p * ST + SA, p); }
-  constexpr int NLS = DOp<TM, AKC>::NL + DOp<TN, BKC>::NL;  // direct loads per thread per stage
-  for (int s = 0; s < nst; ++s) {
-    wait_vm(min(DNS - 2, nst - 1 - s) * NLS);     // this thread's loads of stage s have landed
-    __syncthreads();                               // ... everyone's; and stage s-1 is no longer read
+  // Software pipeline over stages. Iteration s: read the second k16 half of stage s while the MFMAs of its first half
+  // run; wait for stage s + 1 and barrier (every wave is then past stage s - 1, whose buffer the next load reuses);
+  // issue stage s + DNS - 1; read the first half of stage s + 1 while the MFMAs of the second half of stage s run.
+  bf16x8 fa0[BM], fb0[BN], fa1[BM], fb1[BN];
+  auto read_half = [&](const LDS uint16_t* st, int kk, bf16x8 (&fa)[BM], bf16x8 (&fb)[BN]) {
+#pragma unroll
+    for (int i = 0; i < BM; ++i) fa[i] = da.frag(st, wm0 + i * 32, kk);
+#pragma unroll
+    for (int j = 0; j < BN; ++j) fb[j] = db.frag(st + SA, wn0 + j * 32, kk);
+  };
+  auto mfma_half = [&](const bf16x8 (&fa)[BM], const bf16x8 (&fb)[BN]) {
+#pragma unroll
+    for (int i = 0; i < BM; ++i)
+#pragma unroll
+      for (int j = 0; j < BN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+  };
+  wait_stages(min(DNS - 2, nst - 1));
+  __syncthreads();
+  read_half(lds, 0, fa0, fb0);
+  // The loop body has no branch around LDS reads (the last stage is peeled), so the compiler's in-order LDS counter
+  // stays exact and the MFMAs of one half never wait for the reads issued for the next. The barrier is a bare
+  // s_barrier: the staged data is complete once vmcnt says so, and the buffer the next load overwrites was last read
+  // by MFMA operands consumed before it.
+  for (int s = 0; s + 1 < nst; ++s) {
+    const LDS uint16_t* la = lds + (s % DNS) * ST;
+    read_half(la, 1, fa1, fb1);
+    mfma_half(fa0, fb0);
+    wait_stages(min(DNS - 3, nst - 2 - s));        // this thread's loads of stage s + 1 have landed
+    asm volatile("s_barrier" ::: "memory");        // ... everyone's
     if (s + DNS - 1 < nst) {
       LDS uint16_t* nb = lds + ((s + DNS - 1) % DNS) * ST;
       da.issue(nb, s + DNS - 1);
       db.issue(nb + SA, s + DNS - 1);
     }
-    const LDS uint16_t* la = lds + (s % DNS) * ST;
-    const LDS uint16_t* lb = la + SA;
-#pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk) {
-      bf16x8 af[BM], bfr[BN];
-#pragma unroll
-      for (int i = 0; i < BM; ++i) af[i] = da.frag(la, wm0 + i * 32, kk);
-#pragma unroll
-      for (int j = 0; j < BN; ++j) bfr[j] = db.frag(lb, wn0 + j * 32, kk);
-#pragma unroll
-      for (int i = 0; i < BM; ++i)
-#pragma unroll
-        for (int j = 0; j < BN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
-    }
+    read_half(lds + ((s + 1) % DNS) * ST, 0, fa0, fb0);
+    mfma_half(fa1, fb1);
   }
+  read_half(lds + ((nst - 1) % DNS) * ST, 1, fa1, fb1);
+  mfma_half(fa0, fb0);
+  mfma_half(fa1, fb1);
 #ifdef KVM_GEMM_PROF
   pt[2] = wall_clock64(); pt[3] = __builtin_amdgcn_s_memtime();
 #endif
@@ -639,5 +753,23 @@ __device__ __noinline__ void op_matmul_tile_bf16(const Ctx& c) {
   else mfma_tile<64, 64>(c);
 }
 __device__ __noinline__ void op_matmul_mma_bf16(const Ctx& c) { mfma_tile<128, 256>(c); }
+// Op 302: op 122 over the K range [k0, k0 + K), written at output rows om0 + m. The task's buffer views (LDS copies
+// made by the dispatcher) are narrowed in place to that K range and output row offset; the tile then runs unchanged.
+__device__ __noinline__ void op_matmul_mma_bf16_kr(const Ctx& c) {
+  if (tid() == 0) {
+    LDS View* v = (LDS View*)c.views;
+    const int fl = c.i(11), k0 = c.i(13), om0 = c.i(14);
+    auto shift = [](LDS View& x, long long rows_off, long long elems) {
+      const int es = x.dtype == 2 ? 2 : 4;
+      x.p = (char*)x.p + elems * es;
+      x.rows -= (int)rows_off;
+    };
+    if (fl & 1) shift(v[0], k0, (long long)k0 * v[0].cols); else shift(v[0], 0, k0);   // A [K, M] rows / [M, K] columns
+    if (fl & 2) shift(v[1], 0, k0); else shift(v[1], k0, (long long)k0 * v[1].cols);   // B [N, K] columns / [K, N] rows
+    shift(v[2], om0, (long long)om0 * v[2].cols);
+  }
+  __syncthreads();
+  mfma_tile<128, 256>(c);
+}
 
 }  // namespace kvm

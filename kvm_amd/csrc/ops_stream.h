@@ -424,3 +424,37 @@ __device__ __noinline__ void op_softmax_ce_fused_any(const Ctx& c) {
 }
 
 }  // namespace kvm
+
+namespace kvm {
+// Op 303: out[r, c] = sum over s = 0..S-1, in order, of part[s*M + r, c] for rows [r0, r1) and columns [0, N). Each
+// thread takes 4 columns of one row and keeps the S partial loads of that piece in flight together (S <= 16 in the
+// vector form; larger S and unaligned shapes take the scalar loop).
+__device__ __noinline__ void op_splitk_reduce(const Ctx& c) {
+  const View part = c.buf(0), out = c.buf(1);
+  const int M = c.i(2), N = c.i(3), S = c.i(4), r0 = c.i(5), r1 = c.i(6);
+  const long long pc = part.cols, oc = out.cols;
+  if (S <= 16 && (N & 3) == 0 && (pc & 3) == 0 && (oc & 3) == 0 && part.dtype == 0) {
+    const int q = N / 4;
+    const long long n = (long long)(r1 - r0) * q;
+    for (long long e = tid(); e < n; e += KVM_THREADS) {
+      const int r = r0 + (int)(e / q), col = 4 * (int)(e % q);
+      f32x4n v[16];
+#pragma unroll
+      for (int s = 0; s < 16; ++s)
+        if (s < S) v[s] = *(const GLOBAL f32x4n*)(part.f() + ((long long)s * M + r) * pc + col);
+      f32x4n t = v[0];
+#pragma unroll
+      for (int s = 1; s < 16; ++s)
+        if (s < S) t += v[s];
+      st4(out, (long long)r * oc + col, t);
+    }
+    return;
+  }
+  for (long long e = tid(); e < (long long)(r1 - r0) * N; e += KVM_THREADS) {
+    const int r = r0 + (int)(e / N), col = (int)(e % N);
+    float t = part.ld((long long)r * pc + col);
+    for (int s = 1; s < S; ++s) t += part.ld(((long long)s * M + r) * pc + col);
+    out.st((long long)r * oc + col, t);
+  }
+}
+}  // namespace kvm

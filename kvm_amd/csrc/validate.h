@@ -39,7 +39,7 @@ static const OpSig* find_op(int id) { for (const OpSig& o : kRegistry) if (o.id 
 static bool implemented(int id) {
   static const int ids[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 32, 33, 34, 35, 36, 37, 38, 39, 40, 41, 42, 43, 44, 45, 46, 47, 48, 49, 50,
                             51, 52, 53, 54, 55, 56, 57, 58, 59, 60, 61, 62, 63, 96, 97, 98, 99, 100, 101, 102, 103, 104, 113, 114, 115,
-                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301};
+                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303};
   for (int i : ids) if (i == id) return true;
   return false;
 }
@@ -102,6 +102,8 @@ static char arg_class(int op, const std::string& n) {
     case 136: return in({"o"}) ? 'a' : 'f';
     case 300: return in({"x", "out"}) ? 'a' : 'f';
     case 301: return in({"gamma"}) ? 'f' : 'a';
+    case 302: return in({"bias"}) ? 'f' : 'a';
+    case 303: return in({"out"}) ? 'a' : 'f';
     default: return 'f';
   }
 }
@@ -245,6 +247,16 @@ static void extents(int op, Check& k) {
       if (pro == 2) k.need(k.B("x2") != nullptr, "pro 2 needs x2");
       const MvmBuf* w = k.B("w"); if (w) k.need(w->dtype == 2 && w->cols % 8 == 0, "w must be bf16 storage with cols % 8 == 0");
       break; }
+    case 302: {
+      int M = k.I("M"), N = k.I("N"), K = k.I("K"), fl = k.I("flags"), m0 = k.I("m0"), n0 = k.I("n0"), k0 = k.I("k0"), om0 = k.I("om0");
+      k.need(M > 0 && N > 0 && K > 0 && 0 <= m0 && m0 < M && 0 <= n0 && n0 < N && k0 >= 0 && om0 >= 0, "bad M/N/K/m0/n0/k0/om0");
+      k.need((fl & ~(1 | 2 | 4 | 32 | 64)) == 0, "flags: only 1, 2, 4");
+      k.need(!k.B("bias") && !k.B("res") && !k.B("pre"), "bias, res and pre must be absent");
+      const long long k1 = (long long)k0 + K;
+      k.ext("a", fl & 1 ? k1 : M, fl & 1 ? M : k1); k.ext("b", fl & 2 ? N : k1, fl & 2 ? k1 : N); k.ext("out", (long long)om0 + M, N); break; }
+    case 303: { int M = k.I("M"), N = k.I("N"), S = k.I("S"), r0 = k.I("r0"), r1 = k.I("r1");
+      k.need(M > 0 && N > 0 && S > 0 && 0 <= r0 && r0 <= r1 && r1 <= M, "bad M/N/S/r0/r1");
+      k.ext("part", (long long)(S - 1) * M + r1, N); k.ext("out", r1, N); break; }
     case 300: { int r1 = k.I("r1"), H = k.I("H"), hd = k.I("hd"); k.range(k.I("r0"), r1); k.need(H > 0 && hd > 0, "bad H/hd");
       k.ext("x", r1, (long long)H * hd); k.ext("out", r1, (long long)H * hd); k.extn("gamma", hd); break; }
     default: k.need(false, "no extent rule");

@@ -507,6 +507,38 @@ void op_matmul_mma_bf16(const Ctx& c) {   // the 128x256 tile = eight 64x64 bf16
     if (a[6] < c.a[8] && a[7] < c.a[9]) mm_tile(sub, true, 64);
   }
 }
+// This executor's op 302: op 122's 128x256 tile over k in [k0, k0 + K), written to output row om0 + m; plain epilogue
+// (alpha, optional accumulate).
+void op_matmul_mma_bf16_kr(const Ctx& c) {
+  V A = c.buf(0), B = c.buf(1), out = c.buf(2);
+  int m0 = c.i(6), n0 = c.i(7), M = c.i(8), N = c.i(9), K = c.i(10), fl = c.i(11), k0 = c.i(13), om0 = c.i(14); float alpha = c.fl(12);
+  need((fl & ~(1 | 2 | 4 | 32 | 64)) == 0 && c.a[3] == -1 && c.a[4] == -1 && c.a[5] == -1 && k0 >= 0 && om0 >= 0,
+       "matmul_mma_bf16_kr: flags / epilogue / k0 / om0");
+  int ta = fl & 1, tb = fl & 2, accum = fl & 4;
+  for (int m = m0; m < std::min(m0 + 128, M); ++m)
+    for (int n = n0; n < std::min(n0 + 256, N); ++n) {
+      float acc = 0;
+      for (int k = k0; k < k0 + K; ++k) {
+        float x = bf16r(ta ? A.f[(long long)k * A.cols + m] : A.f[(long long)m * A.cols + k]);
+        float y = bf16r(tb ? B.f[(long long)n * B.cols + k] : B.f[(long long)k * B.cols + n]);
+        acc = f32((double)acc + (double)f32((double)x * y));
+      }
+      float v = f32((double)acc * alpha);
+      long long o = (long long)(om0 + m) * out.cols + n;
+      out.stf(o, accum ? f32((double)out.f[o] + v) : v);
+    }
+}
+// This executor's op 303: out[r, c] = sum over s in order of part[s*M + r, c].
+void op_splitk_reduce(const Ctx& c) {
+  V part = c.buf(0), out = c.buf(1); int M = c.i(2), N = c.i(3), S = c.i(4), r0 = c.i(5), r1 = c.i(6);
+  need(M > 0 && N > 0 && S > 0 && 0 <= r0 && r0 <= r1 && r1 <= M, "splitk_reduce: args");
+  for (int r = r0; r < r1; ++r)
+    for (int col = 0; col < N; ++col) {
+      float t = part.f[(long long)r * part.cols + col];
+      for (int s = 1; s < S; ++s) t = f32((double)t + part.f[((long long)s * M + r) * part.cols + col]);
+      out.stf((long long)r * out.cols + col, t);
+    }
+}
 void op_lr_schedule(const Ctx& c) {   // ref_extra.py:339-345
   V st = c.buf(0), lr = c.buf(1); int kind = c.i(2); float base = c.fl(3); int wu = c.i(4), tot = c.i(5); float mr = c.fl(6);
   need(kind >= 0 && kind <= 2, "lr_schedule: kind");
@@ -659,7 +691,7 @@ const OpEnt kOps[] = {
   {101, op_softmax_rows_bwd}, {102, op_gather_rows_scaled}, {103, op_scatter_add_rows}, {104, op_row_dot},
   {113, op_round_bf16}, {114, op_matmul_tile_bf16}, {122, op_matmul_mma_bf16}, {134, op_gemv_bf16},
   {135, op_attn_decode_part}, {136, op_attn_decode_merge}, {115, op_adamw_lr}, {116, op_lr_schedule}, {117, op_scale_flat},
-  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows},
+  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce},
 };
 OpFn find_op(int id) { for (const OpEnt& e : kOps) if (e.id == id) return e.fn; return nullptr; }
 

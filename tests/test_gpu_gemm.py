@@ -94,3 +94,36 @@ def test_tile_bf16_sizes(tiles, fl):
     print(f'tile_bf16 {tiles}', flush=True)
     _check(_gemm_graph(256, 256, 96, fl | 2, op='matmul_tile_bf16', tiles=tiles, bias=True))
     _check(_gemm_graph(256, 256, 128, fl | 1, op='matmul_tile_bf16', tiles=tiles))
+
+
+def _splitk_graph(M, N, K, flags, S, odt='bf16'):
+    """Split-K as the GPT generator emits it: op 302 tiles over S K ranges into an f32 partial buffer of S row blocks,
+    then op 303 sums the blocks in order into C."""
+    b = Builder(11)
+    ta, tb = flags & 1, flags & 2
+    b.normal('A', K if ta else M, M if ta else K, 'bf16', scale=1.0)
+    b.normal('B', N if tb else K, K if tb else N, 'bf16', scale=1.0)
+    b.fill('P', S * M, N, 'f32')
+    b.fill('C', M, N, odt)
+    slabs = K // 32
+    bounds = [32 * (slabs * s // S) for s in range(S + 1)]
+    ts = []
+    for s in range(S):
+        for m0 in range(0, M, 128):
+            for n0 in range(0, N, 256):
+                ts.append(b.task('matmul_mma_bf16_kr', a='A', b='B', out='P', bias=None, res=None, pre=None, m0=m0, n0=n0, M=M, N=N,
+                                 K=bounds[s + 1] - bounds[s], flags=flags, alpha=1.0, k0=bounds[s], om0=s * M))
+    for r0 in range(0, M, 64):
+        b.task('splitk_reduce', after=ts, part='P', out='C', M=M, N=N, S=S, r0=r0, r1=min(M, r0 + 64))
+    return Workload(b.spec(), b.init_override)
+
+
+@pytest.mark.parametrize('flags', [0, 1, 2, 3])
+def test_splitk_all_orientations(flags):
+    print(f'split-K flags {flags}', flush=True)
+    _check(_splitk_graph(256, 512, 416, flags, S=3))
+
+
+def test_splitk_partial_tiles_f32_out():
+    print('split-K partial tiles, f32 out', flush=True)
+    _check(_splitk_graph(200, 300, 640, 0, S=4, odt='f32'))

@@ -138,3 +138,37 @@ def test_gemv_bf16_closed_form():
     W_ = _get(r, b, 'w').reshape(N, K).astype(np.float64)
     v = bl.bf16_round((x / math.sqrt((x * x).mean() + 1e-6) * gm).astype(np.float32)).astype(np.float64)
     assert np.abs(_get(r, b, 'o') - W_ @ v).max() < 1e-5
+
+
+@pytest.mark.parametrize('flags', [0, 3])
+def test_splitk_closed_form(flags):
+    """Split-K (ops 302 + 303): the in-order sum of the K-range partials equals the fp64 product of the bf16 operands
+    (a wrong k0 / om0 offset, a transposed operand or a dropped range fails this); each partial block equals the
+    product over its own K range."""
+    w = W(5)
+    M, N, K, S = 130, 260, 96, 3
+    ta, tb = flags & 1, flags & 2
+    w.buf('A', K if ta else M, M if ta else K, 'bf16'), w.buf('B', N if tb else K, K if tb else N, 'bf16')
+    w.zeros('P', S * M, N), w.zeros('C', M, N, 'bf16')
+    bounds = [0, 32, 64, 96]
+    ts = []
+    for s in range(S):
+        for m0 in (0, 128):
+            for n0 in (0, 256):
+                ts.append(w.task('matmul_mma_bf16_kr', a='A', b='B', out='P', bias=None, res=None, pre=None, m0=m0, n0=n0, M=M, N=N,
+                                 K=bounds[s + 1] - bounds[s], flags=flags, alpha=1.0, k0=bounds[s], om0=s * M))
+    w.task('splitk_reduce', after=ts, part='P', out='C', M=M, N=N, S=S, r0=0, r1=M)
+    r, b = _run_one(w)
+    A = _get(r, b, 'A').astype(np.float64).reshape(K if ta else M, M if ta else K)
+    B = _get(r, b, 'B').astype(np.float64).reshape(N if tb else K, K if tb else N)
+    A = A.T if ta else A
+    B = B.T if tb else B
+    P = _get(r, b, 'P').reshape(S, M, N)
+    for s in range(S):
+        k0, k1 = bounds[s], bounds[s + 1]
+        want = A[:, k0:k1] @ B[k0:k1, :]
+        assert np.abs(P[s] - want).max() < 1e-5 * np.abs(want).max()
+    full = A @ B
+    got = _get(r, b, 'C').reshape(M, N).astype(np.float64)
+    assert np.abs(got - full).max() < 2 ** -7 * np.abs(full).max()
+    assert np.array_equal(got, bl.bf16_round((P[0] + P[1] + P[2]).astype(np.float32)).astype(np.float64))

@@ -257,9 +257,88 @@ template <bool RMS> __device__ __noinline__ bool op_norm_bwd_dx_fast(const Ctx& 
 // max / sum, combined across the wave; pass 2 writes dlogits = (softmax - onehot) * f. Same results as ce_rows up to
 // fp32 reassociation.
 constexpr float LOG2E = 1.4426950408889634f, LN2 = 0.6931471805599453f;
+// Block-per-row form for bf16 logits: the whole row (V <= 2048 * NR) is loaded into registers with every load in
+// flight at once (thread t holds the 8-element vectors t, t + 256, ...), the row max and the exp-sum are reduced over
+// the block in a fixed order (lanes by xor steps, then the four waves in order), and dlogits is written from the same
+// registers, so each row is read from memory once. The exponentials are the hardware exp2 (arguments are <= 0, so
+// only results below the normal range, probabilities under 2^-126, can differ from exp2f).
+__device__ __forceinline__ float bfl(unsigned short h) { return __uint_as_float((unsigned)h << 16); }
+template <typename F> __device__ __forceinline__ float block_reduce(LDS float* red, float v, F op) {
+  for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, 64));
+  __syncthreads();                                   // the previous use of red is done
+  if (lane() == 0) red[wave()] = v;
+  __syncthreads();
+  return op(op(red[0], red[1]), op(red[2], red[3]));
+}
+template <int NR>
+__device__ __noinline__ void ce_rows_block(const Ctx& c, const View& lg_, const View& tg_, const View& rl_, const View& ls_, const View& dl_, int r0,
+                                           int r1, int V, int ignore, float f, bool fwd, bool bwd) {
+  // Register copies: fields of by-reference views would be re-read from memory with a full vmcnt wait each time,
+  // which also waits for every store in flight.
+  const View lg = uniform_view(lg_), tg = uniform_view(tg_), rl = uniform_view(rl_), ls = uniform_view(ls_), dl = uniform_view(dl_);
+  LDS float* red = (LDS float*)c.smem;
+  const int nv = V / 8, t8 = tid();
+  for (int r = r0; r < r1; ++r) {
+    const int t = tg.i()[r];
+    const bool ign = t == ignore;
+    if (!ign && (t < 0 || t >= V)) { if (tid() == 0) c.fail(KVM_ERR_OP_TOKEN, r, t); continue; }
+    const GLOBAL u16x8_t* row = (const GLOBAL u16x8_t*)(lg.h() + (long long)r * lg.cols);
+    u16x8_t v[NR];
+#pragma unroll
+    for (int u = 0; u < NR; ++u) v[u] = row[min(t8 + 256 * u, nv - 1)];         // unconditional: all in flight
+    float lse = 0.f;
+    if (fwd && !ign) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < NR; ++u)
+        if (t8 + 256 * u < nv)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) m = fmaxf(m, bfl(v[u][i]));
+      m = block_reduce(red, m, [](float a, float b) { return fmaxf(a, b); });
+      const float ml2 = m * LOG2E;
+      float s = 0.f;
+#pragma unroll
+      for (int u = 0; u < NR; ++u)
+        if (t8 + 256 * u < nv)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) s += __builtin_amdgcn_exp2f(bfl(v[u][i]) * LOG2E - ml2);
+      s = block_reduce(red, s, [](float a, float b) { return a + b; });
+      lse = (ml2 + log2f(s)) * LN2;
+      if (tid() == 0) { ls.f()[r] = lse; rl.f()[r] = lse - lg.at(r, t); }
+    } else if (fwd) {
+      if (tid() == 0) { ls.f()[r] = 0.f; rl.f()[r] = 0.f; }
+    } else {
+      lse = ls.f()[r];
+    }
+    if (bwd) {
+      const long long ob = (long long)r * dl.cols;
+      const float l2 = lse * LOG2E;
+#pragma unroll
+      for (int u = 0; u < NR; ++u) {
+        const int j = t8 + 256 * u;
+        if (j < nv) {
+          float o[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = ign ? 0.f : (__builtin_amdgcn_exp2f(bfl(v[u][i]) * LOG2E - l2) - (8 * j + i == t ? 1.f : 0.f)) * f;
+          st8(dl, ob + 8 * j, o);
+        }
+      }
+    }
+  }
+}
+
 __device__ __noinline__ bool ce_rows_fast(const Ctx& c, View lg, View tg, View rl, View ls, View dl, int r0, int r1, int V, int ignore, float f, bool fwd, bool bwd) {
   if (!vec8_ok(lg) || (V % 8) || (bwd && !vec8_ok(dl))) return false;
   const int nv = V / 8;
+  if (lg.dtype == 2 && nv <= 256 * 32) {
+    const int nr = (nv + 255) / 256;
+    if (nr <= 4) ce_rows_block<4>(c, lg, tg, rl, ls, dl, r0, r1, V, ignore, f, fwd, bwd);
+    else if (nr <= 8) ce_rows_block<8>(c, lg, tg, rl, ls, dl, r0, r1, V, ignore, f, fwd, bwd);
+    else if (nr <= 16) ce_rows_block<16>(c, lg, tg, rl, ls, dl, r0, r1, V, ignore, f, fwd, bwd);
+    else if (nr <= 25) ce_rows_block<25>(c, lg, tg, rl, ls, dl, r0, r1, V, ignore, f, fwd, bwd);
+    else ce_rows_block<32>(c, lg, tg, rl, ls, dl, r0, r1, V, ignore, f, fwd, bwd);
+    return true;
+  }
   for (int r = r0 + wave(); r < r1; r += KVM_WAVES) {
     const int t = tg.i()[r];
     const bool ign = t == ignore;

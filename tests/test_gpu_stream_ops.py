@@ -2,6 +2,7 @@
 entropy, bf16 conversion, gradient norm, attention delta) at the widths of the GPT-162M workload (d = 768, 4096
 rows), in bf16 and f32 storage, against the CPU oracle. The oracle sums in double; the device sums in fp32 in a fixed
 tree order: f32 outputs within a relative L2 error of 2e-5, bf16 outputs 4e-3 (one bf16 ulp is 2^-8)."""
+import numpy as np
 import pytest
 
 import oracle
@@ -110,3 +111,34 @@ def test_flat_streams():
     for r0, r1 in split(N, 16):
         b.task('attn_bwd_delta', o='o', do='do', delta='delta', r0=r0, r1=r1, T=T, H=H, hd=hd)
     _run(b)
+
+
+def test_bf16_rounding_special_values():
+    """f32 -> bf16 storage rounding on the device (hardware conversion) against round-to-nearest-even on the bits:
+    ties in both directions, carries into the exponent, the largest finite values (rounding to infinity), denormals,
+    signed zeros and infinities must match bit for bit; NaNs must stay NaN."""
+    print('bf16 rounding special values', flush=True)
+    rng = np.random.default_rng(5)
+    pats = [0x00000000, 0x80000000, 0x7f800000, 0xff800000, 0x7f7fffff, 0xff7fffff, 0x7f7f8000, 0x3f808000, 0x3f818000,
+            0x3f80ffff, 0x3fffffff, 0x00000001, 0x00008000, 0x00018000, 0x007fffff, 0x80000001, 0x807fffff, 0x00800000,
+            0x7fc00000, 0x7f800001, 0xffc12345]
+    pats += [int(x) for x in rng.integers(0, 2 ** 32, 4000, dtype=np.uint64)]
+    pats += [int(x) & 0xffff8000 | 0x8000 for x in rng.integers(0, 2 ** 32, 2000, dtype=np.uint64)]   # exact ties
+    n = len(pats)
+    b = Builder(3)
+    b.fill('x', 1, n, 'f32')                      # overwritten with the raw bit patterns below
+    b.fill('y', 1, n, 'bf16')
+    b.task('round_bf16', x='x', out='y', e0=0, e1=n)
+    w = Workload(b.spec(), b.init_override)
+    lb = bl.load(compiler.compile_spec(w.spec))
+    init = [oracle.materialize(m, w.init_override.get(m['name'])) for m in lb.metadata['buffers']]
+    ex = Executor.from_bundle(lb, buffers=init)
+    ex.write('x', np.array(pats, dtype=np.uint32).view(np.float32))
+    ex.run()
+    got = ex.read_raw('y').reshape(-1).astype(np.uint32)
+    ex.close()
+    u = np.array(pats, dtype=np.uint64)
+    want = ((u + 0x7fff + ((u >> 16) & 1)) >> 16).astype(np.uint32) & 0xffff
+    nan = ((u & 0x7fffffff) > 0x7f800000)
+    assert np.array_equal(got[~nan], want[~nan]), np.nonzero(got[~nan] != want[~nan])
+    assert np.all(((got[nan] & 0x7fff) > 0x7f80))

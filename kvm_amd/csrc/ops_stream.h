@@ -537,3 +537,44 @@ __device__ __noinline__ void op_splitk_reduce(const Ctx& c) {
   }
 }
 }  // namespace kvm
+
+namespace kvm {
+// Embedding backward with token ids (registry op 33): dtab[key] += dout[r] for the rows r whose id falls in this
+// task's key range [v0, v1). The ids are read 4096 at a time with all loads in flight, the matching rows are compacted
+// into an LDS list in ascending row order (wave ballots, then the four waves in order), and only those rows are added,
+// row after row in that order (the reference's summation order), 256 columns per pass.
+__device__ __noinline__ bool op_embedding_bwd_fast(const Ctx& c) {
+  const View ids = uniform_view(c.buf(0)), dout = uniform_view(c.buf(1)), dt = uniform_view(c.buf(2));
+  const int N = c.i(3), v0 = c.i(5), v1 = c.i(6), d = c.i(7), acc = c.i(8);
+  if (!ids.ok() || dt.dtype != 0 || N > 16384) return false;
+  LDS int* list = (LDS int*)c.smem;                 // [N] matching rows
+  LDS int* wcnt = list + 16384;                      // [4]
+  if (!acc)
+    for (long long e = tid(); e < (long long)(v1 - v0) * d; e += KVM_THREADS) dt.f()[(long long)(v0 + e / d) * dt.cols + e % d] = 0.f;
+  int nm = 0;
+  for (int s0 = 0; s0 < N; s0 += 16 * KVM_THREADS) {
+    int key[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) key[u] = ids.i()[min(s0 + u * KVM_THREADS + tid(), N - 1)];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int r = s0 + u * KVM_THREADS + tid();
+      const bool hit = r < N && key[u] >= v0 && key[u] < v1;
+      const unsigned long long bal = __ballot(hit);
+      __syncthreads();                                 // the previous round's counts are consumed
+      if (lane() == 0) wcnt[wave()] = __popcll(bal);
+      __syncthreads();
+      int off = nm;
+      for (int w = 0; w < wave(); ++w) off += wcnt[w];
+      if (hit) list[off + __popcll(bal & ((1ull << lane()) - 1ull))] = r;
+      nm += (wcnt[0] + wcnt[1]) + (wcnt[2] + wcnt[3]);
+    }
+  }
+  __syncthreads();
+  for (int i = 0; i < nm; ++i) {
+    const int r = list[i], k = ids.i()[r];
+    for (int col = tid(); col < d; col += KVM_THREADS) dt.f()[(long long)k * dt.cols + col] += dout.at(r, col);
+  }
+  return true;
+}
+}  // namespace kvm

@@ -142,3 +142,19 @@ def test_bf16_rounding_special_values():
     nan = ((u & 0x7fffffff) > 0x7f800000)
     assert np.array_equal(got[~nan], want[~nan]), np.nonzero(got[~nan] != want[~nan])
     assert np.all(((got[nan] & 0x7fff) > 0x7f80))
+
+
+@pytest.mark.parametrize('acc', [0, 1])
+def test_embedding_bwd_ids(acc):
+    """Token-embedding backward with ids: repeated keys, several key ranges per table, N over one 4096-row batch of
+    the id scan, accumulate or overwrite; the rows of a key are added in ascending order as in the oracle."""
+    print(f'embedding_bwd acc {acc}', flush=True)
+    rng = np.random.default_rng(9)
+    N, V, d = 5000, 700, 192
+    b = Builder(21)
+    b.values('ids', [int(x) for x in rng.integers(0, V, N)] , N, 1, 'i32')
+    b.normal('dout', N, d, 'f32', scale=1.0)
+    b.normal('dtab', V, d, 'f32', scale=1.0)
+    for v0, v1 in split(V, 7):
+        b.task('embedding_bwd', ids='ids', dout='dout', dtab='dtab', N=N, mod=0, v0=v0, v1=v1, d=d, acc=acc)
+    _run(b)

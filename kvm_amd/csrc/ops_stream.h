@@ -33,6 +33,8 @@ __device__ __forceinline__ void st8(const View& X, long long o, const float (&v)
 }
 __device__ __forceinline__ bool vec8_ok(const View& X) { return X.dtype != 1 && (X.cols % 8) == 0; }
 __device__ __forceinline__ bool vec4_ok(const View& X) { return X.dtype != 1 && (X.cols % 4) == 0; }
+// Within reach of 32-bit byte offsets (buffer loads).
+__device__ __forceinline__ bool off32_ok(const View& X) { return (long long)X.rows * X.cols * 4 < 0x7fffffffll; }
 
 // ---------------------------------------------------------------------------------------------- column reductions
 // Column sums over rows [0, R) for 64-column chunks: 8 lanes cover 64 columns of one row (8 columns each), so 32 row
@@ -121,9 +123,15 @@ __device__ __noinline__ bool op_norm_bwd_params_fast(const Ctx& c) {
 // ---------------------------------------------------------------------------------------------- row normalisation
 // One wave per row, the row in registers (NV 4-element vectors per lane, d = 256 * NV), rows of a wave loaded before
 // any is reduced (RPW rows at a time) so their loads overlap.
-template <int NV, bool RMS> __device__ __noinline__ void norm_fwd_rows(const View& x, const View& g, const View& be, const View& out, const View& mean,
-                                                          const View& rstd, int r0, int r1, int d, float eps) {
+template <int NV, bool RMS> __device__ __noinline__ void norm_fwd_rows(const View& x_, const View& g_, const View& be_, const View& out_,
+                                                          const View& mean_, const View& rstd_, int r0, int r1, int d, float eps) {
+  // Register copies of the views, and all of a wave's row loads issued together through branch-free buffer loads
+  // (rows past r1 re-read the last row): by-reference views and dtype branches would each add a full memory wait.
+  const View x = uniform_view(x_), g = uniform_view(g_), be = uniform_view(be_), out = uniform_view(out_), mean = uniform_view(mean_),
+             rstd = uniform_view(rstd_);
   constexpr int RPW = NV >= 8 ? 1 : NV >= 4 ? 2 : 4;
+  Ld4 lx;
+  lx.init(x);
   float gv[NV][4], bv[NV][4];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -133,37 +141,41 @@ template <int NV, bool RMS> __device__ __noinline__ void norm_fwd_rows(const Vie
     bv[i][0] = u.x; bv[i][1] = u.y; bv[i][2] = u.z; bv[i][3] = u.w;
   }
   for (int rb = r0 + wave() * RPW; rb < r1; rb += KVM_WAVES * RPW) {
-    f32x4n v[RPW][NV];
+    u32x4_t raw[RPW][NV];
 #pragma unroll
     for (int q = 0; q < RPW; ++q)
 #pragma unroll
-      for (int i = 0; i < NV; ++i) if (rb + q < r1) v[q][i] = ld4(x, (long long)(rb + q) * x.cols + 4 * (lane() + 64 * i));
+      for (int i = 0; i < NV; ++i) raw[q][i] = lx.raw(min(rb + q, r1 - 1) * x.cols + 4 * (lane() + 64 * i));
 #pragma unroll
     for (int q = 0; q < RPW; ++q) {
       const int r = rb + q;
-      if (r >= r1) break;
+      f32x4n v[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) v[i] = lx.cvt(raw[q][i]);
       float mu = 0.f;
       if (!RMS) {
         float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) s += (v[q][i].x + v[q][i].y) + (v[q][i].z + v[q][i].w);
+        for (int i = 0; i < NV; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
         mu = wave_sum(s) / (float)d;
       }
       float ss = 0.f;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
-        const f32x4n t = v[q][i] - mu;
+        const f32x4n t = v[i] - mu;
         ss += (t.x * t.x + t.y * t.y) + (t.z * t.z + t.w * t.w);
       }
       const float rs = 1.f / sqrtf(wave_sum(ss) / (float)d + eps);
+      if (r < r1) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        f32x4n o;
-        o.x = (v[q][i].x - mu) * rs * gv[i][0] + bv[i][0]; o.y = (v[q][i].y - mu) * rs * gv[i][1] + bv[i][1];
-        o.z = (v[q][i].z - mu) * rs * gv[i][2] + bv[i][2]; o.w = (v[q][i].w - mu) * rs * gv[i][3] + bv[i][3];
-        st4(out, (long long)r * out.cols + 4 * (lane() + 64 * i), o);
+        for (int i = 0; i < NV; ++i) {
+          f32x4n o;
+          o.x = (v[i].x - mu) * rs * gv[i][0] + bv[i][0]; o.y = (v[i].y - mu) * rs * gv[i][1] + bv[i][1];
+          o.z = (v[i].z - mu) * rs * gv[i][2] + bv[i][2]; o.w = (v[i].w - mu) * rs * gv[i][3] + bv[i][3];
+          st4(out, (long long)r * out.cols + 4 * (lane() + 64 * i), o);
+        }
+        if (lane() == 0) { rstd.f()[r] = rs; if (!RMS) mean.f()[r] = mu; }
       }
-      if (lane() == 0) { rstd.f()[r] = rs; if (!RMS) mean.f()[r] = mu; }
     }
   }
 }
@@ -172,7 +184,7 @@ template <bool RMS> __device__ __noinline__ bool op_norm_fwd_fast(const Ctx& c) 
   View out = c.buf(k++), mean; if (!RMS) mean = c.buf(k++);
   View rstd = c.buf(k++);
   const int r0 = c.i(k), r1 = c.i(k + 1), d = c.i(k + 2); const float eps = c.f(k + 3);
-  if (d % 256 || d > 4096 || !vec4_ok(x) || !vec4_ok(out) || g.dtype != 0 || (!RMS && be.dtype != 0)) return false;
+  if (d % 256 || d > 4096 || !vec4_ok(x) || !vec4_ok(out) || g.dtype != 0 || (!RMS && be.dtype != 0) || !off32_ok(x)) return false;
   switch (d / 256) {
     case 1: norm_fwd_rows<1, RMS>(x, g, be, out, mean, rstd, r0, r1, d, eps); break;
     case 2: norm_fwd_rows<2, RMS>(x, g, be, out, mean, rstd, r0, r1, d, eps); break;
@@ -186,9 +198,15 @@ template <bool RMS> __device__ __noinline__ bool op_norm_fwd_fast(const Ctx& c) 
 }
 
 // dx = rstd * (dy*g - mean(dy*g) - xhat * mean(dy*g*xhat)) (+ dx when acc) (registry ops 37, 38).
-template <int NV, bool RMS> __device__ __noinline__ void norm_bwd_rows(const View& x, const View& dy, const View& g, const View& mean, const View& rstd,
-                                                          const View& dx, int r0, int r1, int d, int acc) {
+template <int NV, bool RMS> __device__ __noinline__ void norm_bwd_rows(const View& x_, const View& dy_, const View& g_, const View& mean_,
+                                                          const View& rstd_, const View& dx_, int r0, int r1, int d, int acc) {
+  // As norm_fwd_rows: register copies of the views; x, dy, the accumulated dx and the row statistics of all of a
+  // wave's rows are loaded together before any of them is used.
+  const View x = uniform_view(x_), dy = uniform_view(dy_), g = uniform_view(g_), mean = uniform_view(mean_), rstd = uniform_view(rstd_),
+             dx = uniform_view(dx_);
   constexpr int RPW = NV >= 8 ? 1 : NV >= 4 ? 2 : 4;
+  Ld4 lx, ly, ld;
+  lx.init(x); ly.init(dy); ld.init(dx, acc != 0);
   float gv[NV][4];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -196,41 +214,48 @@ template <int NV, bool RMS> __device__ __noinline__ void norm_bwd_rows(const Vie
     gv[i][0] = t.x; gv[i][1] = t.y; gv[i][2] = t.z; gv[i][3] = t.w;
   }
   for (int rb = r0 + wave() * RPW; rb < r1; rb += KVM_WAVES * RPW) {
-    f32x4n xv[RPW][NV], gy[RPW][NV];
+    u32x4_t rx[RPW][NV], ry[RPW][NV], rd[RPW][NV];
+    float mu[RPW], rs[RPW];
 #pragma unroll
-    for (int q = 0; q < RPW; ++q)
+    for (int q = 0; q < RPW; ++q) {
+      const int rr = min(rb + q, r1 - 1);
+      mu[q] = RMS ? 0.f : mean.f()[rr];
+      rs[q] = rstd.f()[rr];
 #pragma unroll
-      for (int i = 0; i < NV; ++i)
-        if (rb + q < r1) {
-          xv[q][i] = ld4(x, (long long)(rb + q) * x.cols + 4 * (lane() + 64 * i));
-          gy[q][i] = ld4(dy, (long long)(rb + q) * dy.cols + 4 * (lane() + 64 * i));
-        }
+      for (int i = 0; i < NV; ++i) {
+        rx[q][i] = lx.raw(rr * x.cols + 4 * (lane() + 64 * i));
+        ry[q][i] = ly.raw(rr * dy.cols + 4 * (lane() + 64 * i));
+        rd[q][i] = ld.raw(rr * dx.cols + 4 * (lane() + 64 * i));
+      }
+    }
 #pragma unroll
     for (int q = 0; q < RPW; ++q) {
       const int r = rb + q;
-      if (r >= r1) break;
-      const float mu = RMS ? 0.f : mean.f()[r], rs = rstd.f()[r];
       float s1 = 0.f, s2 = 0.f;
 #pragma unroll
-      for (int i = 0; i < NV; ++i)
+      for (int i = 0; i < NV; ++i) {
+        const f32x4n xv = lx.cvt(rx[q][i]), gy = ly.cvt(ry[q][i]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float gs = gy[q][i][e] * gv[i][e];
-          s1 += gs; s2 += gs * (xv[q][i][e] - mu) * rs;
+          const float gs = gy[e] * gv[i][e];
+          s1 += gs; s2 += gs * (xv[e] - mu[q]) * rs[q];
         }
+      }
       s1 = RMS ? 0.f : wave_sum(s1) / (float)d;
       s2 = wave_sum(s2) / (float)d;
+      if (r < r1) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const long long o = (long long)r * dx.cols + 4 * (lane() + 64 * i);
-        f32x4n res;
+        for (int i = 0; i < NV; ++i) {
+          const f32x4n xv = lx.cvt(rx[q][i]), gy = ly.cvt(ry[q][i]);
+          f32x4n res;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float gs = gy[q][i][e] * gv[i][e], xh = (xv[q][i][e] - mu) * rs;
-          res[e] = rs * (gs - s1 - xh * s2);
+          for (int e = 0; e < 4; ++e) {
+            const float gs = gy[e] * gv[i][e], xh = (xv[e] - mu[q]) * rs[q];
+            res[e] = rs[q] * (gs - s1 - xh * s2);
+          }
+          res += ld.cvt(rd[q][i]);                  // zero unless accumulating
+          st4(dx, (long long)r * dx.cols + 4 * (lane() + 64 * i), res);
         }
-        if (acc) res += ld4(dx, o);
-        st4(dx, o, res);
       }
     }
   }
@@ -239,7 +264,7 @@ template <bool RMS> __device__ __noinline__ bool op_norm_bwd_dx_fast(const Ctx& 
   int k = 0; View x = c.buf(k++), dy = c.buf(k++), g = c.buf(k++), mean; if (!RMS) mean = c.buf(k++);
   View rstd = c.buf(k++), dx = c.buf(k++);
   const int r0 = c.i(k), r1 = c.i(k + 1), d = c.i(k + 2), acc = c.i(k + 3);
-  if (d % 256 || d > 4096 || !vec4_ok(x) || !vec4_ok(dy) || !vec4_ok(dx) || g.dtype != 0) return false;
+  if (d % 256 || d > 4096 || !vec4_ok(x) || !vec4_ok(dy) || !vec4_ok(dx) || g.dtype != 0 || !off32_ok(x) || !off32_ok(dy) || !off32_ok(dx)) return false;
   switch (d / 256) {
     case 1: norm_bwd_rows<1, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
     case 2: norm_bwd_rows<2, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;

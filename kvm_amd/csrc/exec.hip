@@ -163,6 +163,7 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 301: op_gemv_bf16_rows(c); break;
     case 302: op_matmul_mma_bf16_kr(c); break;
     case 303: op_splitk_reduce(c); break;
+    case 304: op_matmul_mma_bf16_256(c); break;
     default: if (threadIdx.x == 0) c.fail(KVM_ERR_BAD_OP, op, 0);
   }
 }

@@ -402,10 +402,11 @@ __device__ __forceinline__ void epi_rows(const Ctx& c, const GemmArgs& g) {
 }
 
 template <int TM, int TN, bool OBF>
-__device__ __noinline__ void gemm_epilogue(const Ctx& c) {
+__device__ __noinline__ void gemm_epilogue(const Ctx& c, int moff) {
   constexpr int LPR = TN / 4, RPI = 64 / LPR, NI = TM / KVM_WAVES / RPI;   // lanes per row, rows per instruction
   constexpr int NB = NI < 4 ? NI : 4;
-  const GemmArgs g = gemm_args(c);
+  GemmArgs g = gemm_args(c);
+  g.m0 += moff;                                          // the staged rows start at tile row moff
   const Epi& e = g.e;
   const LDS float* et = (const LDS float*)c.smem;
   const int l = lane(), w = wave(), ch = l % LPR, n = g.n0 + 4 * ch;
@@ -467,31 +468,38 @@ __device__ __noinline__ void gemm_epilogue(const Ctx& c) {
 #endif
 }
 
-// Stages the accumulators in LDS (see above) and runs the epilogue.
+// Stages the accumulators in LDS (see above) and runs the epilogue; a tile whose f32 copy exceeds the LDS budget
+// (256 x 256) goes in two row halves, each staged by the two waves that own it.
 template <int TM, int TN>
 __device__ __forceinline__ void gemm_store(const Ctx& c, const f32x16 (&acc)[TM / 64][TN / 64], const GemmArgs& g) {
   constexpr int BM = TM / 64, BN = TN / 64, WM = TM / 2, WN = TN / 2;
-  static_assert(TM * TN * 4 <= KVM_LDS_BYTES, "LDS epilogue");
+  constexpr int NH = TM * TN * 4 <= KVM_LDS_BYTES ? 1 : 2, HM = TM / NH;
+  static_assert(HM * TN * 4 <= KVM_LDS_BYTES && (NH == 1 || HM == WM), "LDS epilogue");
   const int wm0 = (wave() >> 1) * WM, wn0 = (wave() & 1) * WN, l = lane();
   LDS float* et = (LDS float*)c.smem;
-  __syncthreads();                                         // operand stages are no longer read
 #pragma unroll
-  for (int i = 0; i < BM; ++i) {
-    const int r = wm0 + i * 32 + (l & 31);
+  for (int h = 0; h < NH; ++h) {
+    __syncthreads();                                       // operand stages / the previous half are no longer read
+    if (NH == 1 || (wave() >> 1) == h) {
 #pragma unroll
-    for (int j = 0; j < BN; ++j)
+      for (int i = 0; i < BM; ++i) {
+        const int r = (NH == 1 ? wm0 : 0) + i * 32 + (l & 31);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int chunk = (wn0 + j * 32 + 8 * q) / 4 + (l >> 5);
-        *(LDS f32x4n*)(et + r * TN + 4 * (chunk ^ epi_swz<TN>(r))) = f32x4n{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        for (int j = 0; j < BN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int chunk = (wn0 + j * 32 + 8 * q) / 4 + (l >> 5);
+            *(LDS f32x4n*)(et + r * TN + 4 * (chunk ^ epi_swz<TN>(r))) = f32x4n{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          }
       }
-  }
-  __syncthreads();
+    }
+    __syncthreads();
 #ifdef KVM_GEMM_PROF
-  KVM_PT(8);
+    KVM_PT(8);
 #endif
-  if (g.e.out.dtype == 2) gemm_epilogue<TM, TN, true>(c);
-  else gemm_epilogue<TM, TN, false>(c);
+    if (g.e.out.dtype == 2) gemm_epilogue<HM, TN, true>(c, h * HM);
+    else gemm_epilogue<HM, TN, false>(c, h * HM);
+  }
 #ifdef KVM_GEMM_PROF
   KVM_PT(11);
 #endif
@@ -641,7 +649,8 @@ template <int TM, int TN, bool AKC, bool BKC>
 __device__ __noinline__ void gemm_lds(const Ctx& c) {
   constexpr int WM = TM / 2, WN = TN / 2, BM = WM / 32, BN = WN / 32;
   constexpr int SA = TM * DK, SB = TN * DK, ST = SA + SB;    // elements per stage
-  static_assert(DNS * ST * 2 <= KVM_LDS_BYTES, "LDS");
+  constexpr int NS = DNS * ST * 2 <= KVM_LDS_BYTES ? DNS : KVM_LDS_BYTES / (ST * 2);   // stages that fit in LDS
+  static_assert(NS >= 3, "LDS");
   const GemmArgs g = gemm_args(c);
   const View& A = g.A; const View& B = g.B;
   const int m0 = g.m0, n0 = g.n0, K = g.K;
@@ -661,19 +670,19 @@ __device__ __noinline__ void gemm_lds(const Ctx& c) {
     for (int j = 0; j < BN; ++j) acc[i][j] = f32x16{};
   const int nst = K / DK;
   constexpr int NLS = DOp<TM, AKC>::NL + DOp<TN, BKC>::NL;  // direct loads per thread per stage
-  // Waits until at most k stages issued after the one needed are still in flight (k <= DNS - 2).
+  // Waits until at most k stages issued after the one needed are still in flight (k <= NS - 2).
   auto wait_stages = [](int k) {
     k = __builtin_amdgcn_readfirstlane(k);
     if (k >= 3) wait_vm_c<3 * NLS>(); else if (k == 2) wait_vm_c<2 * NLS>(); else if (k == 1) wait_vm_c<NLS>(); else wait_vm_c<0>();
   };
-  static_assert(DNS - 2 <= 3, "wait_stages");
+  static_assert(NS - 2 <= 3, "wait_stages");
   __syncthreads();                                 // the previous task may still read this LDS
 #pragma unroll
-  for (int p = 0; p < DNS - 1; ++p)
+  for (int p = 0; p < NS - 1; ++p)
     if (p < nst) { da.issue(lds + p * ST, p); db.issue(lds + p * ST + SA, p); }
   // Software pipeline over stages. Iteration s: read the second k16 half of stage s while the MFMAs of its first half
   // run; wait for stage s + 1 and barrier (every wave is then past stage s - 1, whose buffer the next load reuses);
-  // issue stage s + DNS - 1; read the first half of stage s + 1 while the MFMAs of the second half of stage s run.
+  // issue stage s + NS - 1; read the first half of stage s + 1 while the MFMAs of the second half of stage s run.
   bf16x8 fa0[BM], fb0[BN], fa1[BM], fb1[BN];
   auto read_half = [&](const LDS uint16_t* st, int kk, bf16x8 (&fa)[BM], bf16x8 (&fb)[BN]) {
 #pragma unroll
@@ -687,7 +696,7 @@ __device__ __noinline__ void gemm_lds(const Ctx& c) {
 #pragma unroll
       for (int j = 0; j < BN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
   };
-  wait_stages(min(DNS - 2, nst - 1));
+  wait_stages(min(NS - 2, nst - 1));
   __syncthreads();
   read_half(lds, 0, fa0, fb0);
   // The loop body has no branch around LDS reads (the last stage is peeled), so the compiler's in-order LDS counter
@@ -695,20 +704,20 @@ __device__ __noinline__ void gemm_lds(const Ctx& c) {
   // s_barrier: the staged data is complete once vmcnt says so, and the buffer the next load overwrites was last read
   // by MFMA operands consumed before it.
   for (int s = 0; s + 1 < nst; ++s) {
-    const LDS uint16_t* la = lds + (s % DNS) * ST;
+    const LDS uint16_t* la = lds + (s % NS) * ST;
     read_half(la, 1, fa1, fb1);
     mfma_half(fa0, fb0);
-    wait_stages(min(DNS - 3, nst - 2 - s));        // this thread's loads of stage s + 1 have landed
+    wait_stages(min(NS - 3, nst - 2 - s));        // this thread's loads of stage s + 1 have landed
     asm volatile("s_barrier" ::: "memory");        // ... everyone's
-    if (s + DNS - 1 < nst) {
-      LDS uint16_t* nb = lds + ((s + DNS - 1) % DNS) * ST;
-      da.issue(nb, s + DNS - 1);
-      db.issue(nb + SA, s + DNS - 1);
+    if (s + NS - 1 < nst) {
+      LDS uint16_t* nb = lds + ((s + NS - 1) % NS) * ST;
+      da.issue(nb, s + NS - 1);
+      db.issue(nb + SA, s + NS - 1);
     }
-    read_half(lds + ((s + 1) % DNS) * ST, 0, fa0, fb0);
+    read_half(lds + ((s + 1) % NS) * ST, 0, fa0, fb0);
     mfma_half(fa1, fb1);
   }
-  read_half(lds + ((nst - 1) % DNS) * ST, 1, fa1, fb1);
+  read_half(lds + ((nst - 1) % NS) * ST, 1, fa1, fb1);
   mfma_half(fa0, fb0);
   mfma_half(fa1, fb1);
 #ifdef KVM_GEMM_PROF
@@ -753,6 +762,24 @@ __device__ __noinline__ void op_matmul_tile_bf16(const Ctx& c) {
   else mfma_tile<64, 64>(c);
 }
 __device__ __noinline__ void op_matmul_mma_bf16(const Ctx& c) { mfma_tile<128, 256>(c); }
+// Op 304: the 256x256 tile. Shapes outside the direct-to-LDS path (partial tiles, odd K, f32 operands) run as two
+// 128x256 tiles, rows m0 and m0 + 128 (the second by advancing m0 in the task's LDS copy of its arguments).
+__device__ __noinline__ void op_matmul_mma_bf16_256(const Ctx& c) {
+  const GemmArgs g = gemm_args(c);
+  const bool akc = !(g.fl & 1), bkc = (g.fl & 2) != 0;
+  if (gemm_fast_operand(g.A, akc, g.m0, 256, g.M, g.K) && gemm_fast_operand(g.B, bkc, g.n0, 256, g.N, g.K)) {
+    if (akc) { if (bkc) gemm_lds<256, 256, true, true>(c); else gemm_lds<256, 256, true, false>(c); }
+    else { if (bkc) gemm_lds<256, 256, false, true>(c); else gemm_lds<256, 256, false, false>(c); }
+    return;
+  }
+  mfma_tile<128, 256>(c);
+  if (g.m0 + 128 < g.M) {
+    __syncthreads();                                     // every thread has read the arguments
+    if (tid() == 0) ((LDS int32_t*)c.a)[6] = g.m0 + 128;
+    __syncthreads();
+    mfma_tile<128, 256>(c);
+  }
+}
 // Op 302: op 122 over the K range [k0, k0 + K), written at output rows om0 + m. The task's buffer views (LDS copies
 // made by the dispatcher) are narrowed in place to that K range and output row offset; the tile then runs unchanged.
 __device__ __noinline__ void op_matmul_mma_bf16_kr(const Ctx& c) {

@@ -39,7 +39,7 @@ static const OpSig* find_op(int id) { for (const OpSig& o : kRegistry) if (o.id 
 static bool implemented(int id) {
   static const int ids[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 32, 33, 34, 35, 36, 37, 38, 39, 40, 41, 42, 43, 44, 45, 46, 47, 48, 49, 50,
                             51, 52, 53, 54, 55, 56, 57, 58, 59, 60, 61, 62, 63, 96, 97, 98, 99, 100, 101, 102, 103, 104, 113, 114, 115,
-                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303};
+                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304};
   for (int i : ids) if (i == id) return true;
   return false;
 }
@@ -95,7 +95,7 @@ static char arg_class(int op, const std::string& n) {
     case 63: case 102: case 103: case 104: return in({"idx"}) ? 'i' : 'f';
     case 98: return 'a';
     case 113: return 'a';
-    case 114: case 122: return in({"bias"}) ? 'f' : 'a';
+    case 114: case 122: case 304: return in({"bias"}) ? 'f' : 'a';
     case 116: return in({"step"}) ? 'i' : 'f';
     case 134: return in({"gamma"}) ? 'f' : 'a';
     case 135: return in({"lens"}) ? 'i' : in({"part"}) ? 'f' : 'a';
@@ -131,7 +131,7 @@ static void extents(int op, Check& k) {
     case 33: { int N = k.I("N"), v0 = k.I("v0"), v1 = k.I("v1"), d = k.I("d"); k.need(N >= 0 && 0 <= v0 && v0 <= v1 && d > 0, "bad N/v0/v1/d");
       k.need(k.B("ids") || k.I("mod") > 0, "ids absent needs mod > 0");
       k.extn("ids", N); k.ext("dout", N, d); k.ext("dtab", v1, d); break; }
-    case 34: case 114: case 122: {
+    case 34: case 114: case 122: case 304: {
       int M = k.I("M"), N = k.I("N"), K = k.I("K"), fl = k.I("flags"), m0 = k.I("m0"), n0 = k.I("n0");
       k.need(M > 0 && N > 0 && K > 0 && 0 <= m0 && m0 < M && 0 <= n0 && n0 < N, "bad M/N/K/m0/n0");
       k.need((fl & ~(127 | 256 | 512 | 1024)) == 0 && !((fl & 32) && (fl & 64)) && !((fl & 256) && (fl & 1024)), "unsupported flags");

@@ -204,10 +204,15 @@ class GPTBuilder:
         self.dep.record(t, R, W)
         return t
 
+    TILES_256 = 256    # bf16 GEMMs with at least this many 256x256 output tiles use them (op 304)
+    TILES_MMA = 16     # else at least this many 128x256 tiles: op 122; else 128x128 tiles (op 114), more of them
+
     def gemm(self, A, B, out, M, N, K, flags=0, bias=None, res=None, pre=None, alpha=1.0):
         """C = alpha * op(A) op(B) (+ epilogue), tiled; returns the task ids."""
         bf, ta, tb = self.bf, flags & 1, flags & 2
-        if bf and -(-M // 128) * -(-N // 256) >= 256:
+        if bf and -(-M // 256) * -(-N // 256) >= self.TILES_256:
+            op, TM, TN, fl = 'matmul_mma_bf16_256', 256, 256, flags
+        elif bf and -(-M // 128) * -(-N // 256) >= self.TILES_MMA:
             op, TM, TN, fl = 'matmul_mma_bf16', 128, 256, flags
         elif bf:   # fewer than 256 tiles of 128x256: 128x128 tiles keep more of the chip busy
             op, TM, TN, fl = 'matmul_tile_bf16', 128, 128, flags | 32

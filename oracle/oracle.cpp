@@ -507,6 +507,14 @@ void op_matmul_mma_bf16(const Ctx& c) {   // the 128x256 tile = eight 64x64 bf16
     if (a[6] < c.a[8] && a[7] < c.a[9]) mm_tile(sub, true, 64);
   }
 }
+void op_matmul_mma_bf16_256(const Ctx& c) {   // this executor's op 304: op 122 with a 256x256 tile (sixteen 64x64 tiles)
+  int32_t a[13]; memcpy(a, c.a, sizeof a);
+  Ctx sub = c; sub.a = a;
+  for (int dm = 0; dm < 256; dm += 64) for (int dn = 0; dn < 256; dn += 64) {
+    a[6] = c.a[6] + dm; a[7] = c.a[7] + dn; a[11] = c.a[11] & ~(32 | 64);
+    if (a[6] < c.a[8] && a[7] < c.a[9]) mm_tile(sub, true, 64);
+  }
+}
 // This executor's op 302: op 122's 128x256 tile over k in [k0, k0 + K), written to output row om0 + m; plain epilogue
 // (alpha, optional accumulate).
 void op_matmul_mma_bf16_kr(const Ctx& c) {
@@ -691,7 +699,7 @@ const OpEnt kOps[] = {
   {101, op_softmax_rows_bwd}, {102, op_gather_rows_scaled}, {103, op_scatter_add_rows}, {104, op_row_dot},
   {113, op_round_bf16}, {114, op_matmul_tile_bf16}, {122, op_matmul_mma_bf16}, {134, op_gemv_bf16},
   {135, op_attn_decode_part}, {136, op_attn_decode_merge}, {115, op_adamw_lr}, {116, op_lr_schedule}, {117, op_scale_flat},
-  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce},
+  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce}, {304, op_matmul_mma_bf16_256},
 };
 OpFn find_op(int id) { for (const OpEnt& e : kOps) if (e.id == id) return e.fn; return nullptr; }
 

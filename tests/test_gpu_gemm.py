@@ -127,3 +127,27 @@ def test_splitk_all_orientations(flags):
 def test_splitk_partial_tiles_f32_out():
     print('split-K partial tiles, f32 out', flush=True)
     _check(_splitk_graph(200, 300, 640, 0, S=4, odt='f32'))
+
+
+@pytest.mark.parametrize('flags', [0, 1, 2, 3])
+def test_mma256_whole_tiles_all_orientations(flags):
+    """matmul_mma_bf16_256 (op 304): 256x256 tiles, two-half epilogue."""
+    print(f'mma256 whole tiles flags {flags}', flush=True)
+    _check(_gemm_graph(512, 512, 192, flags, op='matmul_mma_bf16_256', tiles=(256, 256)))
+
+
+@pytest.mark.parametrize('flags,kw', [
+    (2 | 8, dict(bias=True, pre=True)),
+    (512, dict(pre=True)),
+    (2, dict(bias=True, res=True)),
+    (4, dict(odt='f32')),
+])
+def test_mma256_epilogues(flags, kw):
+    print(f'mma256 epilogue flags {flags} {kw}', flush=True)
+    _check(_gemm_graph(256, 512, 128, flags, op='matmul_mma_bf16_256', tiles=(256, 256), **kw))
+
+
+def test_mma256_partial_tiles():
+    """Partial tiles and K off the slab: two 128x256 register-path tiles."""
+    print('mma256 partial tiles', flush=True)
+    _check(_gemm_graph(300, 400, 100, 1, op='matmul_mma_bf16_256', tiles=(256, 256), bias=True))

@@ -372,6 +372,216 @@ __device__ __noinline__ void op_attn_decode_part(const Ctx& c) {
     if (k == 0) { part.f()[r + hd] = st[g]; part.f()[r + hd + 1] = st[8 + g]; }
   }
 }
+// Streaming form of op 135 for bf16 caches with hd = 128: the split's tokens go in blocks of 128 (32 per wave). Lane l
+// owns head dimensions 8 * (l % 16) .. + 8 of token slot l / 16, so each of the 8 rounds of a wave covers 4 tokens, and
+// the K and V rows of a block arrive with 16-byte loads that are all in flight together. Scores are dot products
+// against the (rotated, scale-folded) query held in registers, summed over the 16 lanes of a token; the block max and
+// exp-sum are reduced over the workgroup in a fixed order; P V accumulates in the same layout and is reduced over the
+// token slots, then over the waves in order. Blocks after the first rescale the running sums (online softmax).
+// Sum over the 16 lanes of a DPP row, every lane receiving it: four rotate-and-add steps (row_ror 8, 4, 2, 1), all in
+// registers (a lane shuffle goes through the LDS crossbar).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xf, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
+  return v;
+}
+template <int G>
+__device__ __noinline__ void attn_decode_part_fast(const Ctx& c) {
+  const View q = uniform_view(c.buf(0)), kc = uniform_view(c.buf(1)), vc = uniform_view(c.buf(2)), lens = uniform_view(c.buf(3));
+  const View part = uniform_view(c.buf(4)), kn = uniform_view(c.buf(5)), vn = uniform_view(c.buf(6));
+  const int bb = c.i(7), kvh = c.i(8), s = c.i(9), S = c.i(10), H = c.i(11), Hkv = c.i(12), Tmax = c.i(14);
+  const float sc = c.f(15), th = c.f(16);
+  const int fl = c.i(17);
+#ifdef KVM_GEMM_PROF
+  unsigned long long pt[8] = {(unsigned long long)wall_clock64(), 0, 0, 0, 0, 0, 0, 0};
+#endif
+  constexpr int hd = 128, half = 64;
+  const int L = lens.i()[bb], n = L + 1;
+  if (L < 0 || n > Tmax) { if (tid() == 0) c.fail(KVM_ERR_OP_KVLEN, bb, L); return; }
+  const int chunk = (n + S - 1) / S, j0 = s * chunk, j1 = min(n, j0 + chunk), nk = max(0, j1 - j0);
+  const long long base = ((long long)bb * Hkv + kvh) * Tmax;
+  const int l = lane(), w = wave(), cb = l & 15, ts = l >> 4, d0 = 8 * cb;
+  LDS float* red = (LDS float*)c.smem;                  // [4 waves][G] block max / sum
+  LDS float* racc = red + 2 * 4 * 8;                    // [16 token slots][G][hd] P V partials
+  LDS float* rot = racc + 16 * G * hd;                   // [half] sin, [half] cos of this position's angles
+  // query (rotated when flag 1, rounded to bf16 when flag 2), times the score scale. This lane's 8 dimensions and their
+  // rotation partners (d -+ 64) are loaded as vectors, every load before any use.
+  float qr[G][8], qp[G][8];
+  const bool qv = (q.cols % 8) == 0 && q.dtype != 1;
+  if (qv && q.dtype == 2) {
+    u16x8_t a[G], b2[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const long long qo = (long long)bb * q.cols + (long long)(kvh * G + g) * hd;
+      a[g] = *(const GLOBAL u16x8_t*)(q.h() + qo + d0);
+      b2[g] = *(const GLOBAL u16x8_t*)(q.h() + qo + (d0 ^ half));
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { qr[g][e] = bf2f(a[g][e]); qp[g][e] = bf2f(b2[g][e]); }
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const long long qo = (long long)bb * q.cols + (long long)(kvh * G + g) * hd;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { qr[g][e] = q.ld(qo + d0 + e); qp[g][e] = q.ld(qo + (d0 ^ half) + e); }
+    }
+  }
+  // the rotation table (computed while the query loads are in flight)
+  if (fl & 1) {
+    if (tid() < half) { float sn, co; rope_sc_ref(L, tid(), hd, log((double)th), sn, co); rot[tid()] = sn; rot[half + tid()] = co; }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = d0 + e;
+      float x = qr[g][e];
+      if (fl & 1) {
+        const double sn = rot[d % half], co = rot[half + d % half], y = qp[g][e];
+        x = d < half ? (float)((double)x * co - y * sn) : (float)(y * sn + (double)x * co);
+        if (fl & 2) x = round_bf(x);
+      }
+      qr[g][e] = x * sc;
+    }
+  if ((fl & 1) && j0 <= n - 1 && n - 1 < j1) {          // this split holds the new key: store it (rotated) and its value
+    const long long row = base + n - 1;
+    for (int i = tid(); i < half; i += KVM_THREADS) {
+      const double sn = rot[i], co = rot[half + i];
+      const double x1 = kn.at(bb, kvh * hd + i), x2 = kn.at(bb, kvh * hd + i + half);
+      kc.st(row * kc.cols + i, (float)(x1 * co - x2 * sn)); kc.st(row * kc.cols + i + half, (float)(x1 * sn + x2 * co));
+    }
+    for (int k = tid(); k < hd; k += KVM_THREADS) vc.st(row * vc.cols + k, vn.at(bb, kvh * hd + k));
+  }
+#ifdef KVM_GEMM_PROF
+  pt[1] = wall_clock64();
+#endif
+  __syncthreads();                                      // the new row is stored before any block reads it
+#ifdef KVM_GEMM_PROF
+  pt[2] = wall_clock64();
+#endif
+  if (nk == 0) {
+    for (int e = tid(); e < G * (hd + 2); e += KVM_THREADS) {
+      const int g = e / (hd + 2), k = e % (hd + 2);
+      const long long r = (((long long)bb * S + s) * H + kvh * G + g) * part.cols;
+      part.f()[r + k] = k < hd ? 0.f : (k == hd ? ATTN_EMPTY_M : 0.f);
+    }
+    return;
+  }
+  float mrun[G], lrun[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    mrun[g] = -INFINITY; lrun[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  }
+  for (int b0 = 0; b0 < nk; b0 += 128) {
+    u16x8_t kr[8], vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const long long row = base + j0 + min(b0 + w * 32 + 4 * i + ts, nk - 1);
+      kr[i] = *(const GLOBAL u16x8_t*)(kc.h() + row * kc.cols + d0);
+      vr[i] = *(const GLOBAL u16x8_t*)(vc.h() + row * vc.cols + d0);
+    }
+    float sv[8][G];
+    float mb[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) mb[g] = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool live = b0 + w * 32 + 4 * i + ts < nk;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float a = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a += qr[g][e] * bf2f(kr[i][e]);
+        a = row16_sum(a);
+        sv[i][g] = live ? a : -INFINITY;
+        mb[g] = fmaxf(mb[g], sv[i][g]);
+      }
+    }
+#ifdef KVM_GEMM_PROF
+    if (b0 == 0) pt[3] = wall_clock64();
+#endif
+#pragma unroll
+    for (int g = 0; g < G; ++g) { mb[g] = fmaxf(mb[g], __shfl_xor(mb[g], 16, 64)); mb[g] = fmaxf(mb[g], __shfl_xor(mb[g], 32, 64)); }
+    __syncthreads();                                    // red is free
+    if (l == 0)
+#pragma unroll
+      for (int g = 0; g < G; ++g) red[w * 8 + g] = mb[g];
+    __syncthreads();
+    float scale[G], ps[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float m = fmaxf(fmaxf(red[g], red[8 + g]), fmaxf(red[16 + g], red[24 + g]));
+      const float mn = fmaxf(mrun[g], m);
+      scale[g] = __expf(mrun[g] - mn);                  // 0 on the first block
+      mrun[g] = mn;
+      ps[g] = 0.f;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= scale[g];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float p = __expf(sv[i][g] - mrun[g]);     // 0 for dead slots
+        ps[g] += p;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] += p * bf2f(vr[i][e]);
+      }
+#pragma unroll
+    for (int g = 0; g < G; ++g) { ps[g] += __shfl_xor(ps[g], 16, 64); ps[g] += __shfl_xor(ps[g], 32, 64); }
+    __syncthreads();
+    if (l == 0)
+#pragma unroll
+      for (int g = 0; g < G; ++g) red[32 + w * 8 + g] = ps[g];
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) lrun[g] = lrun[g] * scale[g] + ((red[32 + g] + red[40 + g]) + (red[48 + g] + red[56 + g]));
+  }
+  // P V: the partial sums of the 16 token slots (4 per wave) through LDS, added in slot order
+#ifdef KVM_GEMM_PROF
+  pt[4] = wall_clock64();
+#endif
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) racc[((w * 4 + ts) * G + g) * hd + d0 + e] = acc[g][e];
+  __syncthreads();
+  for (int e = tid(); e < G * hd; e += KVM_THREADS) {
+    const int g = e / hd, k = e % hd;
+    float t = 0.f;
+#pragma unroll
+    for (int q2 = 0; q2 < 16; ++q2) t += racc[(q2 * G + g) * hd + k];
+    const long long r = (((long long)bb * S + s) * H + kvh * G + g) * part.cols;
+    part.f()[r + k] = t;
+    if (k == 0) { part.f()[r + hd] = mrun[g]; part.f()[r + hd + 1] = lrun[g]; }
+  }
+#ifdef KVM_GEMM_PROF
+  pt[5] = wall_clock64();
+  __syncthreads();
+  if (tid() == 0) { unsigned long long* o = (unsigned long long*)(part.f() + (((long long)bb * S + s) * H + kvh * G) * part.cols); for (int i = 0; i < 6; ++i) o[i] = pt[i]; o[6] = g_prof[blockIdx.x][6]; }
+#endif
+}
+__device__ __noinline__ void op_attn_decode_part_any(const Ctx& c) {
+  const View kc = c.buf(1), vc = c.buf(2);
+  const int H = c.i(11), Hkv = c.i(12), hd = c.i(13), G = H / Hkv;
+  const bool ok = kc.dtype == 2 && vc.dtype == 2 && hd == 128 && (kc.cols % 8) == 0 && (vc.cols % 8) == 0;
+  if (ok && G == 4) attn_decode_part_fast<4>(c);
+  else if (ok && G == 8) attn_decode_part_fast<8>(c);
+  else if (ok && G == 2) attn_decode_part_fast<2>(c);
+  else if (ok && G == 1) attn_decode_part_fast<1>(c);
+  else op_attn_decode_part(c);
+}
+
 // Merge of the splits (registry op 136): per head, the split weights e_s = exp(m_s - max m) (live splits only) are
 // computed once into LDS, then each output element is one pass over the splits.
 __device__ __noinline__ void op_attn_decode_merge(const Ctx& c) {

@@ -249,6 +249,15 @@ __device__ __forceinline__ void rope_sc(long long p, int i, int hd, float theta,
   float ang = (float)p * inv;
   sincosf(ang, &s, &co);
 }
+// The rotation angle with the reference's rounding steps: the inverse frequency theta^(-2i/hd) evaluated in double
+// (as exp(x * ln theta), ln theta passed in) and rounded to f32, the angle rounded to f32 from the double product (an
+// f32 powf can be an ulp off, which at positions in the thousands moves the angle by ~1e-4); sin and cos of that f32
+// angle in f32.
+__device__ __forceinline__ void rope_sc_ref(long long p, int i, int hd, double ln_theta, float& s, float& co) {
+  const float inv = (float)exp(-(double)(float)(2 * i) / hd * ln_theta);
+  const float ang = (float)((double)(float)p * (double)inv);
+  sincosf(ang, &s, &co);
+}
 template <int SIGN> __device__ __noinline__ void op_rope(const Ctx& c) {
   View x = c.buf(0), out = c.buf(1), pos = c.buf(2); int r0 = c.i(3), r1 = c.i(4), T = c.i(5), H = c.i(6), hd = c.i(7); float th = c.f(8);
   long long p0 = pos.ok() ? pos.i()[0] : 0; int half = hd / 2;

@@ -52,7 +52,7 @@ def build(c: Qwen3Config) -> Workload:
     b = Builder(c.seed)
     B, D, H, Hkv, hd, F, V = c.batch, c.hidden, c.heads, c.kv_heads, c.head_dim, c.ffn, c.vocab
     Tmax = c.ctx + c.max_new
-    S = c.splits or max(1, 256 // (B * Hkv))
+    S = c.splits or max(1, 256 // (B * Hkv), -(-(c.ctx + 1) // 128))   # >= 256 part tasks, <= 128 tokens each
     rows_mode = B > 1
     # ---- buffers
     b.values('tok', [(7919 * (i + 1)) % V for i in range(B)], B, 1, 'i32')

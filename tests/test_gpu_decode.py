@@ -58,3 +58,31 @@ def test_gemv_rows(M, pro, K):
         b.task('gemv_bf16_rows', x='x', x2='x2' if pro == 2 else None, gamma='g' if pro == 1 else None, w='w', out='out', res='res',
                n0=16 * lo, n1=16 * hi, K=K, M=M, pro=pro, eps=1e-6)
     _run(b)
+
+
+@pytest.mark.parametrize('G,fl,S', [(4, 3, 3), (4, 1, 16), (4, 0, 40), (8, 3, 5), (2, 1, 7), (1, 0, 9)])
+def test_attn_decode_parts(G, fl, S):
+    """Split-context decode attention (op 135) and the merge (op 136) at hd = 128 (the streaming form): two sequences
+    of different lengths, splits longer than one 128-token block (S = 3), short ones and empty ones (S = 40 with a
+    30-token context), with RoPE + cache append + bf16 rounding of the rotated query (flags 3), RoPE + append (1) or
+    neither (0)."""
+    print(f'attn_decode_part G {G} flags {fl} S {S}', flush=True)
+    B, Hkv, hd = 2, 2, 128
+    H = G * Hkv
+    lens = [700, 30] if S == 40 else [700, 301]
+    Tmax = max(lens) + 1
+    b = Builder(31)
+    b.normal('q', B, H * hd, 'bf16', scale=1.0)
+    b.normal('kc', B * Hkv * Tmax, hd, 'bf16', scale=1.0)
+    b.normal('vc', B * Hkv * Tmax, hd, 'bf16', scale=1.0)
+    b.normal('kn', B, Hkv * hd, 'bf16', scale=1.0)
+    b.normal('vn', B, Hkv * hd, 'bf16', scale=1.0)
+    b.values('lens', lens, B, 1, 'i32')
+    b.fill('part', B * S * H, hd + 2, 'f32')
+    b.fill('o', B, H * hd, 'f32')
+    for bb in range(B):
+        ts = [b.task('attn_decode_part', q='q', kc='kc', vc='vc', lens='lens', part='part', knew='kn', vnew='vn', b=bb, kvh=kh, s=s, S=S,
+                     H=H, Hkv=Hkv, hd=hd, Tmax=Tmax, scale=1.0 / hd ** 0.5, theta=1e6, flags=fl)
+              for kh in range(Hkv) for s in range(S)]
+        b.task('attn_decode_merge', after=ts, part='part', o='o', b=bb, h0=0, h1=H, S=S, H=H, hd=hd)
+    _run(b, tol=1e-4)

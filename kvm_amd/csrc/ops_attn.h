@@ -372,8 +372,8 @@ __device__ __noinline__ void op_attn_decode_part(const Ctx& c) {
     if (k == 0) { part.f()[r + hd] = st[g]; part.f()[r + hd + 1] = st[8 + g]; }
   }
 }
-// Streaming form of op 135 for bf16 caches with hd = 128: the split's tokens go in blocks of 128 (32 per wave). Lane l
-// owns head dimensions 8 * (l % 16) .. + 8 of token slot l / 16, so each of the 8 rounds of a wave covers 4 tokens, and
+// Streaming form of op 135 for bf16 caches with hd = 128: the split's tokens go in blocks of 160 (40 per wave). Lane l
+// owns head dimensions 8 * (l % 16) .. + 8 of token slot l / 16, so each of the 10 rounds of a wave covers 4 tokens, and
 // the K and V rows of a block arrive with 16-byte loads that are all in flight together. Scores are dot products
 // against the (rotated, scale-folded) query held in registers, summed over the 16 lanes of a token; the block max and
 // exp-sum are reduced over the workgroup in a fixed order; P V accumulates in the same layout and is reduced over the
@@ -398,6 +398,7 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c) {
   unsigned long long pt[8] = {(unsigned long long)wall_clock64(), 0, 0, 0, 0, 0, 0, 0};
 #endif
   constexpr int hd = 128, half = 64;
+  constexpr int DR = 10, DB = 4 * KVM_WAVES * DR;     // rounds of 4 tokens per wave; tokens per block (160)
   const int L = lens.i()[bb], n = L + 1;
   if (L < 0 || n > Tmax) { if (tid() == 0) c.fail(KVM_ERR_OP_KVLEN, bb, L); return; }
   const int chunk = (n + S - 1) / S, j0 = s * chunk, j1 = min(n, j0 + chunk), nk = max(0, j1 - j0);
@@ -479,21 +480,21 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   }
-  for (int b0 = 0; b0 < nk; b0 += 128) {
-    u16x8_t kr[8], vr[8];
+  for (int b0 = 0; b0 < nk; b0 += DB) {
+    u16x8_t kr[DR], vr[DR];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const long long row = base + j0 + min(b0 + w * 32 + 4 * i + ts, nk - 1);
+    for (int i = 0; i < DR; ++i) {
+      const long long row = base + j0 + min(b0 + w * 4 * DR + 4 * i + ts, nk - 1);
       kr[i] = *(const GLOBAL u16x8_t*)(kc.h() + row * kc.cols + d0);
       vr[i] = *(const GLOBAL u16x8_t*)(vc.h() + row * vc.cols + d0);
     }
-    float sv[8][G];
+    float sv[DR][G];
     float mb[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) mb[g] = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const bool live = b0 + w * 32 + 4 * i + ts < nk;
+    for (int i = 0; i < DR; ++i) {
+      const bool live = b0 + w * 4 * DR + 4 * i + ts < nk;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float a = 0.f;
@@ -528,7 +529,7 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[g][e] *= scale[g];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < DR; ++i)
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float p = __expf(sv[i][g] - mrun[g]);     // 0 for dead slots

@@ -210,18 +210,31 @@ __device__ __noinline__ void op_gemv_bf16_rows_simt(const Ctx& c) {
 //   * v is staged as bf16 [M][KC + 8] in LDS once per K chunk, with the activation loads batched; each wave adds its
 //     partial 16x16 tiles into its own LDS region, and the four regions are summed in wave order at the end (fixed
 //     order).
-constexpr int GV_GRP = 4;          // 16-row blocks whose partial tiles are kept in LDS at once
-constexpr int GV_RING = 12;        // 64-k steps in flight per wave (24 KiB per wave)
+constexpr int GV_SB = 8;           // activation vectors per thread per staging batch (all in flight)
+constexpr int GV_GRP = 8;          // 16-row blocks whose partial tiles are kept in LDS at once (a group re-stages v)
+#ifndef KVM_GV_RING
+#define KVM_GV_RING 4
+#endif
+constexpr int GV_RING = KVM_GV_RING;   // 64-k steps in flight per wave (2 KiB each): deeper rings measured slower
 
 __device__ __forceinline__ float gv_pro(int pro, float xv, float x2v, float gv, float rs) {
   return pro == 1 ? xv * rs * gv : pro == 2 ? silu_f(xv) * x2v : xv;
 }
 
+// K chunk staged in LDS at once: all of K when M rows of it fit in 64 KiB (then one chunk, one continuous weight
+// stream), else the largest of 4096 / 2048 / 1024 that divides K.
+__device__ __forceinline__ int gv_kc(int K, int M) {
+  if ((long long)M * (K + 8) * 2 <= 65536) return K;
+  for (int kc = 4096; kc >= 256; kc >>= 1)
+    if (K % kc == 0 && (long long)M * (kc + 8) * 2 <= 65536) return kc;
+  return 256;
+}
+
 // Shapes the stream form takes: K a multiple of 256 (each wave a whole number of 64-k steps) made of equal chunks,
 // 16-byte aligned rows.
 __device__ __forceinline__ bool gemv_stream_ok(const View& x, const View& x2, const View& w, const View& out, int K, int M, int pro) {
-  const int KC = M <= 8 ? 4096 : 2048;
-  return M >= 1 && M <= 16 && K % 256 == 0 && (K <= KC || K % KC == 0) && w.dtype == 2 && (w.cols % 8) == 0 && x.dtype != 1 &&
+  const int KC = gv_kc(K, M);
+  return M >= 1 && M <= 16 && K % 256 == 0 && K % KC == 0 && w.dtype == 2 && (w.cols % 8) == 0 && x.dtype != 1 &&
          (x.cols % 4) == 0 && (pro != 2 || (x2.ok() && x2.dtype != 1 && (x2.cols % 4) == 0)) && out.dtype != 1 &&
          (long long)w.rows * w.cols * 2 < 0x7fffffffll && (long long)x.rows * x.cols * 4 < 0x7fffffffll &&
          (!x2.ok() || (long long)x2.rows * x2.cols * 4 < 0x7fffffffll);
@@ -241,7 +254,7 @@ __device__ __noinline__ void gemv_stream(const Ctx& c, int M, int pro, float eps
   const View x = uniform_view(c.buf(0)), x2 = uniform_view(c.buf(1)), g = uniform_view(c.buf(2)), w = uniform_view(c.buf(3));
   const View out = uniform_view(c.buf(4)), res = uniform_view(c.buf(5));
   const int n0 = rfl(c.i(6)), n1 = rfl(c.i(7)), K = rfl(c.i(8));
-  const int KC = M <= 8 ? 4096 : 2048, VS = KC + 8;
+  const int KC = gv_kc(K, M), VS = KC + 8;
   LDS uint16_t* vs = (LDS uint16_t*)c.smem;                                    // [M][VS]
   LDS float* rstd = (LDS float*)(c.smem + ((M * VS * 2 + 15) & ~15));          // [16]
   LDS float* part = rstd + 16;                                                  // [4][GV_GRP][256]
@@ -292,17 +305,17 @@ __device__ __noinline__ void gemv_stream(const Ctx& c, int M, int pro, float eps
       __syncthreads();                                                          // rstd ready; the previous chunk's readers are done
       {                                                                          // v = bf16(prologue(x)) for this chunk
         const int q4 = kn / 4, nel = M * q4;
-        for (int e0 = tid(); e0 < nel; e0 += 4 * KVM_THREADS) {
-          f32x4n xv[4], x2v[4], gg[4];
+        for (int e0 = tid(); e0 < nel; e0 += GV_SB * KVM_THREADS) {
+          f32x4n xv[GV_SB], x2v[GV_SB], gg[GV_SB];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
+          for (int u = 0; u < GV_SB; ++u) {
             const int e = min(e0 + u * KVM_THREADS, nel - 1), m = e / q4, k = kc + 4 * (e % q4);
             xv[u] = lx.get(m * x.cols + k);                                      // absent views read as 0
             x2v[u] = lx2.get(m * x2.cols + k);
             gg[u] = lg.get(k);
           }
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
+          for (int u = 0; u < GV_SB; ++u) {
             const int e = e0 + u * KVM_THREADS;
             if (e < nel) {
               const int m = e / q4, k = 4 * (e % q4);

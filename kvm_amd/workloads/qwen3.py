@@ -52,7 +52,7 @@ def build(c: Qwen3Config) -> Workload:
     b = Builder(c.seed)
     B, D, H, Hkv, hd, F, V = c.batch, c.hidden, c.heads, c.kv_heads, c.head_dim, c.ffn, c.vocab
     Tmax = c.ctx + c.max_new
-    S = c.splits or max(1, 256 // (B * Hkv), -(-(c.ctx + 1) // 128))   # >= 256 part tasks, <= 128 tokens each
+    S = c.splits or max(1, 256 // (B * Hkv), -(-(c.ctx + 1) // 160))   # 256 part tasks (one round), <= 160 tokens each
     rows_mode = B > 1
     # ---- buffers
     b.values('tok', [(7919 * (i + 1)) % V for i in range(B)], B, 1, 'i32')
@@ -107,7 +107,8 @@ def build(c: Qwen3Config) -> Workload:
     for l in range(c.layers):
         nq, nkv = H * hd, Hkv * hd
         tot = nq + 2 * nkv
-        pq, pk = max(1, round(P * nq / tot)), max(1, round(P * nkv / tot))
+        pk = max(1, round(P * nkv / tot))
+        pq = max(1, P - 2 * pk)                 # q, k, v together: one round of P tasks
         if rows_mode:
             prev = [b.task('rmsnorm_fwd', after=prev, x='x', gamma=f'ln1.{l}', out='xn', rstd='rstd', r0=0, r1=B, d=D, eps=c.eps)]
             tq = proj(prev, 'xn', f'wq.{l}', 'q', nq, D, pq)
@@ -129,21 +130,21 @@ def build(c: Qwen3Config) -> Workload:
         last_parts = [t for pb in parts for t in pb]
         merges = []
         for bb in range(B):
-            nm = max(1, min(H, 4 // B)) if B < 4 else 1
+            nm = max(1, H // B)                 # one merge task per head (batch 1): short, parallel
             for h0, h1 in split(H, nm):
                 merges.append(b.task('attn_decode_merge', after=parts[bb], part='part', o='att', b=bb, h0=h0, h1=h1, S=S, H=H, hd=hd))
         to = proj(merges, 'att', f'wo.{l}', 'x', D, H * hd, P, res='x')
         if rows_mode:
             r2 = [b.task('rmsnorm_fwd', after=to, x='x', gamma=f'ln2.{l}', out='xn', rstd='rstd', r0=0, r1=B, d=D, eps=c.eps)]
-            tg = proj(r2, 'xn', f'wg.{l}', 'g', F, D, P)
-            tu = proj(r2, 'xn', f'wu.{l}', 'u', F, D, P)
+            tg = proj(r2, 'xn', f'wg.{l}', 'g', F, D, P // 2)     # gate and up together: one round of P tasks
+            tu = proj(r2, 'xn', f'wu.{l}', 'u', F, D, P // 2)
             sm = [b.task('silu_mul_fwd', after=tg + tu, gate='g', up='u', out='h', e0=0, e1=B * F)]
             td = proj(sm, 'h', f'wd.{l}', 'x', D, F, P, res='x')
             prev = td if len(td) <= 256 else b.join(td, P)
         else:
             oj = b.join(to, 2 * P)
-            tg = proj(oj, 'x', f'wg.{l}', 'g', F, D, P, pro=1, gamma=f'ln2.{l}')
-            tu = proj(oj, 'x', f'wu.{l}', 'u', F, D, P, pro=1, gamma=f'ln2.{l}')
+            tg = proj(oj, 'x', f'wg.{l}', 'g', F, D, P // 2, pro=1, gamma=f'ln2.{l}')     # gate and up: one round of P tasks
+            tu = proj(oj, 'x', f'wu.{l}', 'u', F, D, P // 2, pro=1, gamma=f'ln2.{l}')
             gj = b.join(tg + tu, P)
             td = proj(gj, 'g', f'wd.{l}', 'x', D, F, P, pro=2, x2='u', res='x')
             prev = b.join(td, P)

@@ -211,6 +211,24 @@ def bench_sched():
     return out
 
 
+def hbm_traffic(key):
+    """HBM bytes per launch of the persistent kernel for a workload, from the committed counter summary
+    (profiles/hbm_traffic.json: rocprofv3 FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by the same counter's
+    reading for a plain copy of known size); None when the summary has no entry."""
+    path = Path(__file__).resolve().parent / 'profiles' / 'hbm_traffic.json'
+    try:
+        return json.loads(path.read_text())[key]['bytes_per_launch']
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def copy_probe(mib):
+    """One plain copy kernel over `mib` MiB (reads mib MiB, writes mib MiB; the library's kvm_copy_probe): a dispatch
+    whose HBM traffic is known, against which the byte counters of the executor's dispatches are calibrated."""
+    from kvm_amd import executor
+    executor.copy_probe(mib << 20)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -219,6 +237,8 @@ def main():
     ap.add_argument('--workload', default='all', choices=['all', 'gpt162m', 'decode', 'sched'])
     ap.add_argument('--decode-batch', default='1,8')
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--copy-probe', type=int, default=0, metavar='MIB',
+                    help='after the runs, one plain device copy of MIB MiB (reference dispatch for the HBM byte counters)')
     a = ap.parse_args()
     if a.gpus != 1:
         print(json.dumps({'error': 'this executor runs on one GPU; multi-GPU runs are not part of this build', 'n_gpus': a.gpus}))
@@ -250,7 +270,11 @@ def main():
                                     'frac': d['hbm_frac'], 'traffic': None}})
         if 'cpu_baseline' in d:
             result['cpu_baseline'] = d['cpu_baseline']
+    if 'roofline' in result:
+        result['roofline']['traffic'] = hbm_traffic('gpt162m' if 'gpt162m' in extra else f'decode_b{extra["decode"][0]["batch"]}')
     result.update(extra)
+    if a.copy_probe:
+        copy_probe(a.copy_probe)
     print(json.dumps(result))
 
 

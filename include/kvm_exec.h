@@ -110,6 +110,10 @@ int kvm_ntasks(const KvmExec* ex);
 const char* kvm_op_name(int op_id);
 // Fills `out` with n SplitMix64 seeded values on the device and copies them back (initialiser known-answer test).
 int kvm_seeded_fill_test(unsigned long long seed, long long n, int draws, float bias, float coef, float* out);
+// Copies `bytes` bytes between two fresh device buffers with a plain 16-byte-per-lane kernel and waits for it. No
+// counterpart in the reference: a dispatch of known HBM traffic for calibrating byte counters (rocprofv3 FETCH_SIZE /
+// WRITE_SIZE) against the executor's own dispatches.
+int kvm_copy_probe(long long bytes);
 
 #ifdef __cplusplus
 }

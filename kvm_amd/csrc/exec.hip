@@ -728,6 +728,27 @@ int kvm_ntasks(const KvmExec* ex) { return (int)ex->tasks.size(); }
 
 const char* kvm_op_name(int op_id) { return kvm_registry_name(op_id); }
 
+// Plain copy, 16 bytes per lane, grid-stride: the reference dispatch for the HBM byte counters (reads n16 * 16 bytes,
+// writes as many).
+__global__ __launch_bounds__(256) void kvm_copy_probe_kernel(const f32x4n* __restrict__ src, f32x4n* __restrict__ dst, long long n16) {
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n16; i += (long long)gridDim.x * 256) dst[i] = src[i];
+}
+int kvm_copy_probe(long long bytes) {
+  const long long n16 = bytes / 16;
+  void *a = nullptr, *b = nullptr;
+  if (n16 <= 0 || hipMalloc(&a, n16 * 16) != hipSuccess || hipMalloc(&b, n16 * 16) != hipSuccess) {
+    if (a) hipFree(a);
+    g_err = "kvm_copy_probe: bad size or hipMalloc failed";
+    return KVM_STATUS_HIP_ERROR;
+  }
+  hipMemset(a, 0, n16 * 16);
+  hipLaunchKernelGGL(kvm_copy_probe_kernel, dim3(2048), dim3(256), 0, 0, (const f32x4n*)a, (f32x4n*)b, n16);
+  hipError_t e = hipDeviceSynchronize();
+  hipFree(a); hipFree(b);
+  if (e != hipSuccess) { g_err = hipGetErrorString(e); return KVM_STATUS_HIP_ERROR; }
+  return 0;
+}
+
 int kvm_seeded_fill_test(unsigned long long seed, long long n, int draws, float bias, float coef, float* out) {
   float* d = nullptr;
   if (hipMalloc(&d, std::max<long long>(n, 1) * 4) != hipSuccess) { g_err = "hipMalloc failed"; return KVM_STATUS_HIP_ERROR; }

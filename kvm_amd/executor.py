@@ -71,6 +71,7 @@ def lib():
             'kvm_op_name': (ctypes.c_char_p, [I]),
             'kvm_validate': (I, [P, I, P, I, P, I, P, I, I, ctypes.c_char_p, I]),
             'kvm_seeded_fill_test': (I, [ctypes.c_ulonglong, ctypes.c_longlong, I, ctypes.c_float, ctypes.c_float, P]),
+            'kvm_copy_probe': (I, [ctypes.c_longlong]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -278,3 +279,9 @@ def seeded_fill_test(seed, n, draws, bias, coef) -> np.ndarray:
     if lib().kvm_seeded_fill_test(seed % 2**64, n, draws, bias, coef, out.ctypes.data) < 0:
         raise KvmError(lib().kvm_last_error(None).decode())
     return out
+
+
+def copy_probe(nbytes: int) -> None:
+    """One plain device copy of nbytes (kvm_copy_probe): the reference dispatch for HBM byte counters."""
+    if lib().kvm_copy_probe(int(nbytes)) < 0:
+        raise RuntimeError(lib().kvm_last_error(None).decode())

@@ -164,6 +164,7 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 302: op_matmul_mma_bf16_kr(c); break;
     case 303: op_splitk_reduce(c); break;
     case 304: op_matmul_mma_bf16_256(c); break;
+    case 305: op_adamw_bf16(c); break;
     default: if (threadIdx.x == 0) c.fail(KVM_ERR_BAD_OP, op, 0);
   }
 }

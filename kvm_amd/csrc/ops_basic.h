@@ -342,23 +342,26 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
   float step = __fdiv_rn(__fmul_rn(lr, __fdiv_rn(m, bc1)), __fadd_rn(__fsqrt_rn(__fdiv_rn(v, bc2)), eps));
   p = __fsub_rn(__fsub_rn(p, decay), step);
 }
-__device__ void adamw_body(const Ctx& c, View p, View g, View m, View v, View gs, View st, int e0, int e1, float lr, float b1, float b2, float eps, float wd) {
+// sh (optional, op 305): the updated weight rounded to bf16 (or its f32 emulation when sh is f32), as op 113 would write it.
+__device__ void adamw_body(const Ctx& c, View p, View g, View m, View v, View gs, View st, int e0, int e1, float lr, float b1, float b2, float eps, float wd,
+                           View sh = View{nullptr, 0, 0, 0}) {
   int t = st.i()[0];
   if (t < 1) { if (tid() == 0) c.fail(KVM_ERR_OP_RANGE, t, 0); return; }
   float gsc = gs.ok() ? gs.f()[0] : 1.f;
   float bc1 = 1.f - (float)pow((double)b1, (double)t), bc2 = 1.f - (float)pow((double)b2, (double)t);
+  const int shk = sh.ok() ? (sh.dtype == 2 ? 2 : 1) : 0;    // 0 none, 1 f32 emulation, 2 bf16 storage
   long long a0 = ((long long)e0 + 3) & ~3ll, a1 = (long long)e1 & ~3ll;
   if (a0 > a1) { a0 = e1; a1 = e1; }
   auto one = [&](long long i) {
     float pp = p.f()[i], mm = m.f()[i], vv = v.f()[i];
     adamw_elem(pp, g.f()[i], mm, vv, gsc, b1, b2, lr, eps, wd, bc1, bc2);
     p.f()[i] = pp; m.f()[i] = mm; v.f()[i] = vv;
+    if (shk == 2) sh.h()[i] = f2bf(pp); else if (shk == 1) sh.f()[i] = round_bf(pp);
   };
   for (long long i = e0 + tid(); i < a0; i += KVM_THREADS) one(i);
   for (long long i = a1 + tid(); i < e1; i += KVM_THREADS) one(i);
   GLOBAL f32x4n* P = (GLOBAL f32x4n*)p.f(); const GLOBAL f32x4n* G = (const GLOBAL f32x4n*)g.f(); GLOBAL f32x4n* M = (GLOBAL f32x4n*)m.f(); GLOBAL f32x4n* Vv = (GLOBAL f32x4n*)v.f();
-  for (long long q = a0 / 4 + tid(); q < a1 / 4; q += KVM_THREADS) {
-    f32x4n pp = P[q], gg = G[q], mm = M[q], vv = Vv[q];
+  auto upd = [&](long long q, f32x4n pp, f32x4n gg, f32x4n mm, f32x4n vv) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float a = pp[j], b = mm[j], d = vv[j];
@@ -366,9 +369,27 @@ __device__ void adamw_body(const Ctx& c, View p, View g, View m, View v, View gs
       pp[j] = a; mm[j] = b; vv[j] = d;
     }
     P[q] = pp; M[q] = mm; Vv[q] = vv;
+    if (shk == 2) {
+      typedef uint32_t u32x2n __attribute__((ext_vector_type(2)));
+      u32x2n w; w.x = (uint32_t)f2bf(pp[0]) | ((uint32_t)f2bf(pp[1]) << 16); w.y = (uint32_t)f2bf(pp[2]) | ((uint32_t)f2bf(pp[3]) << 16);
+      ((GLOBAL u32x2n*)sh.h())[q] = w;
+    } else if (shk == 1) {
+      f32x4n r; for (int j = 0; j < 4; ++j) r[j] = round_bf(pp[j]);
+      ((GLOBAL f32x4n*)sh.f())[q] = r;
+    }
+  };
+  // two 16-byte groups per thread per pass: eight loads in flight before the first update
+  long long q = a0 / 4 + tid(), qe = a1 / 4;
+  for (; q + KVM_THREADS < qe; q += 2 * KVM_THREADS) {
+    long long r = q + KVM_THREADS;
+    f32x4n p0 = P[q], g0 = G[q], m0 = M[q], v0 = Vv[q], p1 = P[r], g1 = G[r], m1 = M[r], v1 = Vv[r];
+    upd(q, p0, g0, m0, v0);
+    upd(r, p1, g1, m1, v1);
   }
+  if (q < qe) upd(q, P[q], G[q], M[q], Vv[q]);
 }
 __device__ __noinline__ void op_adamw(const Ctx& c) { adamw_body(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.i(6), c.i(7), c.f(8), c.f(9), c.f(10), c.f(11), c.f(12)); }
+__device__ __noinline__ void op_adamw_bf16(const Ctx& c) { adamw_body(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.i(6), c.i(7), c.f(8), c.f(9), c.f(10), c.f(11), c.f(12), c.buf(13)); }
 __device__ __noinline__ void op_adamw_lr(const Ctx& c) { adamw_body(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.i(6), c.i(7), c.buf(8).f()[0], c.f(9), c.f(10), c.f(11), c.f(12)); }
 __device__ __noinline__ void op_gradnorm_partial(const Ctx& c) {
   View g = c.buf(0), part = c.buf(1); __shared__ double red[KVM_WAVES];

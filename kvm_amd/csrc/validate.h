@@ -39,7 +39,7 @@ static const OpSig* find_op(int id) { for (const OpSig& o : kRegistry) if (o.id 
 static bool implemented(int id) {
   static const int ids[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 32, 33, 34, 35, 36, 37, 38, 39, 40, 41, 42, 43, 44, 45, 46, 47, 48, 49, 50,
                             51, 52, 53, 54, 55, 56, 57, 58, 59, 60, 61, 62, 63, 96, 97, 98, 99, 100, 101, 102, 103, 104, 113, 114, 115,
-                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304};
+                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304, 305};
   for (int i : ids) if (i == id) return true;
   return false;
 }
@@ -86,6 +86,7 @@ static char arg_class(int op, const std::string& n) {
     case 51: case 52: return in({"tgt"}) ? 'i' : in({"logits"}) ? 'a' : 'f';
     case 53: case 127: return in({"tgt"}) ? 'i' : in({"logits", "dlogits"}) ? 'a' : 'f';
     case 54: case 115: return in({"step"}) ? 'i' : 'f';
+    case 305: return in({"step"}) ? 'i' : in({"sh"}) ? 'a' : 'f';
     case 57: return in({"out", "ctr"}) ? 'i' : 'f';
     case 58: return in({"out"}) ? 'i' : 'f';
     case 59: return 'a';
@@ -186,6 +187,7 @@ static void extents(int op, Check& k) {
       k.ext("logits", r1, V); k.extn("tgt", r1); k.extn("lse", r1); k.extn("loss", 2); k.ext("dlogits", r1, V); break; }
     case 127: { int r0 = k.I("r0"), r1 = k.I("r1"), V = k.I("V"); k.range(r0, r1); k.need(V > 0 && k.I("ignore") == -1 && k.I("N") > 0, "bad V/ignore/N");
       k.ext("logits", r1, V); k.extn("tgt", r1); k.extn("rowloss", r1); k.extn("lse", r1); k.ext("dlogits", r1, V); break; }
+    case 305: flat({"p", "g", "m", "v", "sh"}, "e0", "e1"); k.extn("gscale", 1); k.extn("step", 1); break;
     case 54: case 115: flat({"p", "g", "m", "v"}, "e0", "e1"); k.extn("gscale", 1); k.extn("step", 1); if (op == 115) k.extn("lr", 1); break;
     case 55: k.range(k.I("e0"), k.I("e1")); k.need(k.I("slot") >= 0, "slot >= 0"); k.extn("g", k.I("e1")); k.extn("partial", k.I("slot") + 1); break;
     case 56: k.need(k.I("nslots") >= 0, "nslots >= 0"); k.extn("partial", k.I("nslots")); k.extn("out", 2); break;

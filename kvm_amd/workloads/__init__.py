@@ -54,9 +54,10 @@ class Builder:
         self.buffers.append(d)
         return name
 
-    def normal(self, name, rows, cols=1, dtype='f32', scale=0.02):
-        """Seeded N(0, scale) (Irwin-Hall(4), the reference's `normal`); bf16 buffers get it as an executor override."""
-        init = {'kind': 'seeded', 'seed': seed_of(self.seed, name), 'scale': scale, 'dist': 'normal'}
+    def normal(self, name, rows, cols=1, dtype='f32', scale=0.02, seed_name=None):
+        """Seeded N(0, scale) (Irwin-Hall(4), the reference's `normal`); bf16 buffers get it as an executor override.
+        `seed_name`: draw the values of that buffer instead (a bf16 buffer then holds the other one's values rounded)."""
+        init = {'kind': 'seeded', 'seed': seed_of(self.seed, seed_name or name), 'scale': scale, 'dist': 'normal'}
         if dtype == 'bf16':
             from ..initgen import params
             draws, bias, coef = params('normal', scale)

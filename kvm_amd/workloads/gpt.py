@@ -164,8 +164,9 @@ class GPTBuilder:
         self.buf(f'm.{name}', rows, cols)
         self.buf(f'v.{name}', rows, cols)
         shadow = None
-        if self.bf and kind == 'matrix':
-            shadow = self.buf(f'{name}.bf', rows, cols, 'bf16')
+        if self.bf and kind == 'matrix':   # starts as the master rounded to bf16; each AdamW task refreshes its rows
+            self.shapes[f'{name}.bf'] = (rows, cols)
+            shadow = self.b.normal(f'{name}.bf', rows, cols, 'bf16', scale=self.c.init_scale, seed_name=name)
         self.params.append((name, f'd.{name}', f'm.{name}', f'v.{name}', shadow, kind == 'matrix'))
         return name
 
@@ -205,12 +206,17 @@ class GPTBuilder:
         return t
 
     TILES_256 = 256    # bf16 GEMMs with at least this many 256x256 output tiles use them (op 304)
+    TILES_ALONE = 128  # a GEMM running alone with fewer 128x256 tiles than this uses 128x128 tiles
     TILES_MMA = 16     # else at least this many 128x256 tiles: op 122; else 128x128 tiles (op 114), more of them
 
-    def gemm(self, A, B, out, M, N, K, flags=0, bias=None, res=None, pre=None, alpha=1.0):
-        """C = alpha * op(A) op(B) (+ epilogue), tiled; returns the task ids."""
+    def gemm(self, A, B, out, M, N, K, flags=0, bias=None, res=None, pre=None, alpha=1.0, alone=False):
+        """C = alpha * op(A) op(B) (+ epilogue), tiled; returns the task ids. `alone`: nothing else runs beside this
+        GEMM (a forward projection after a layer's attention or MLP input), so its tiles should fill the chip by
+        themselves: 128x128 tiles when 128x256 ones would leave most CUs idle."""
         bf, ta, tb = self.bf, flags & 1, flags & 2
-        if bf and -(-M // 256) * -(-N // 256) >= self.TILES_256:
+        if bf and alone and -(-M // 128) * -(-N // 256) < self.TILES_ALONE:
+            op, TM, TN, fl = 'matmul_tile_bf16', 128, 128, flags | 32
+        elif bf and -(-M // 256) * -(-N // 256) >= self.TILES_256:
             op, TM, TN, fl = 'matmul_mma_bf16_256', 256, 256, flags
         elif bf and -(-M // 128) * -(-N // 256) >= self.TILES_MMA:
             op, TM, TN, fl = 'matmul_mma_bf16', 128, 256, flags
@@ -332,13 +338,6 @@ class GPTBuilder:
         L = c.layers
         scale = 1.0 / math.sqrt(hd)
         self.task('counter_inc', [], [('step', ())], x='step', i0=0, i1=1, delta=1)
-        if self.bf:   # bf16 copies of this step's weights, chunked like the optimizer (GEMM tiles wait for their rows)
-            for (p, g, m, v, sh, dec) in self.params:
-                if sh:
-                    R, C = self.shapes[p]
-                    for e0, e1 in row_chunks(R, C):
-                        rows = (e0 // C, (e1 - 1) // C + 1)
-                        self.task('round_bf16', [(p, rows)], [(sh, rows)], x=p, out=sh, e0=e0, e1=e1)
         # ---- forward
         for r0, r1 in self.rows(N):
             self.task('embedding_fwd', [('ids', (r0, r1)), ('wte', ()), ('wpe', ())], [('x.0', (r0, r1))],
@@ -358,10 +357,10 @@ class GPTBuilder:
                               (f'lse.{l}', ((bb * H + h) * T + q0, (bb * H + h) * T + q1))]
                         self.task('attn_fwd', rd, wr, q=f'q.{l}', k=f'k.{l}', v=f'v.{l}', o=f'o.{l}', lse=f'lse.{l}', b=bb, h=h, q0=q0,
                                   T=T, H=H, Hkv=H, hd=hd, scale=scale)
-            self.gemm(f'o.{l}', self.w(f'wo.{l}'), f'xm.{l}', N, d, d, flags=2, bias=f'bo.{l}', res=x)
+            self.gemm(f'o.{l}', self.w(f'wo.{l}'), f'xm.{l}', N, d, d, flags=2, bias=f'bo.{l}', res=x, alone=True)
             self.layernorm(f'xm.{l}', f'ln2g.{l}', f'ln2b.{l}', f'h2.{l}', f'mu2.{l}', f'rs2.{l}')
             self.gemm(f'h2.{l}', self.w(f'w1.{l}'), f'a.{l}', N, F, d, flags=2 | 8, bias=f'b1.{l}', pre=f'u.{l}')
-            self.gemm(f'a.{l}', self.w(f'w2.{l}'), f'x.{l + 1}', N, d, F, flags=2, bias=f'b2.{l}', res=f'xm.{l}')
+            self.gemm(f'a.{l}', self.w(f'w2.{l}'), f'x.{l + 1}', N, d, F, flags=2, bias=f'b2.{l}', res=f'xm.{l}', alone=True)
         self.layernorm(f'x.{L}', 'lnfg', 'lnfb', 'hf', 'muf', 'rsf')
         self.gemm('hf', self.w('wte'), 'logits', N, V, d, flags=2)
         for r0, r1 in self.rows(N):
@@ -501,8 +500,12 @@ class GPTBuilder:
         self.task('gradnorm_finish', [('gn', ())], [('gscale', ())], partial='gn', nslots=len(chunks), out='gscale', max_norm=c.clip)
         for (p, g, m, v, sh, dec, e0, e1, C) in chunks:
             rows = (e0 // C, (e1 - 1) // C + 1)
-            self.task('adamw', [(g, rows), ('gscale', ()), ('step', ())], [(p, rows), (m, rows), (v, rows)], p=p, g=g, m=m, v=v,
-                      gscale='gscale', step='step', e0=e0, e1=e1, lr=c.lr, b1=c.b1, b2=c.b2, eps=c.eps, wd=c.wd if dec else 0.0)
+            kw = dict(p=p, g=g, m=m, v=v, gscale='gscale', step='step', e0=e0, e1=e1, lr=c.lr, b1=c.b1, b2=c.b2, eps=c.eps,
+                      wd=c.wd if dec else 0.0)
+            if sh:   # the bf16 GEMM copy of the new weight is written by the same pass
+                self.task('adamw_bf16', [(g, rows), ('gscale', ()), ('step', ())], [(p, rows), (m, rows), (v, rows), (sh, rows)], sh=sh, **kw)
+            else:
+                self.task('adamw', [(g, rows), ('gscale', ()), ('step', ())], [(p, rows), (m, rows), (v, rows)], **kw)
 
 
 def build(c: GPTConfig) -> Workload:

@@ -383,7 +383,7 @@ void op_softmax_ce_fused(const Ctx& c) {   // ref_gpt.py:451-453
   ce_fwd(c, lg, tg, rl, ls, r0, r1, Vn, ig);
   ce_bwd(lg, tg, ls, dl, r0, r1, Vn, ig, f32((double)f32(1.0 / N) * sc));
 }
-void adamw(V p, V g, V m, V v, V gs, V st, int e0, int e1, float lr, float b1, float b2, float eps, float wd) {   // ref_gpt.py:457-471
+void adamw(V p, V g, V m, V v, V gs, V st, int e0, int e1, float lr, float b1, float b2, float eps, float wd, V sh = V()) {   // ref_gpt.py:457-471
   int t = st.i[0];
   if (t < 1) fail("adamw: step counter < 1");
   double gsc = gs.ok() ? (double)gs.f[0] : 1.0;
@@ -396,9 +396,13 @@ void adamw(V p, V g, V m, V v, V gs, V st, int e0, int e1, float lr, float b1, f
     float decay = f32((double)f32((double)lr * wd) * p.f[i]);
     float step = f32((double)f32((double)lr * (double)f32((double)mi / bc1)) / (double)f32((double)f32(std::sqrt((double)f32((double)vi / bc2))) + eps));
     p.f[i] = f32((double)f32((double)p.f[i] - decay) - step);
+    if (sh.ok()) sh.f[i] = bf16r(p.f[i]);
   }
 }
 void op_adamw(const Ctx& c) { adamw(c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4, true), c.buf(5), c.i(6), c.i(7), c.fl(8), c.fl(9), c.fl(10), c.fl(11), c.fl(12)); }
+void op_adamw_bf16(const Ctx& c) {   // this executor's op 305: adamw, then the bf16 copy of the new weight
+  adamw(c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4, true), c.buf(5), c.i(6), c.i(7), c.fl(8), c.fl(9), c.fl(10), c.fl(11), c.fl(12), c.buf(13));
+}
 void op_adamw_lr(const Ctx& c) { V lr = c.buf(8); adamw(c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4, true), c.buf(5), c.i(6), c.i(7), lr.f[0], c.fl(9), c.fl(10), c.fl(11), c.fl(12)); }
 void op_gradnorm_partial(const Ctx& c) { V g = c.buf(0), part = c.buf(1); double s = 0;
   for (int i = c.i(3); i < c.i(4); ++i) s += (double)g.f[i] * g.f[i];
@@ -699,7 +703,7 @@ const OpEnt kOps[] = {
   {101, op_softmax_rows_bwd}, {102, op_gather_rows_scaled}, {103, op_scatter_add_rows}, {104, op_row_dot},
   {113, op_round_bf16}, {114, op_matmul_tile_bf16}, {122, op_matmul_mma_bf16}, {134, op_gemv_bf16},
   {135, op_attn_decode_part}, {136, op_attn_decode_merge}, {115, op_adamw_lr}, {116, op_lr_schedule}, {117, op_scale_flat},
-  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce}, {304, op_matmul_mma_bf16_256},
+  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce}, {304, op_matmul_mma_bf16_256}, {305, op_adamw_bf16},
 };
 OpFn find_op(int id) { for (const OpEnt& e : kOps) if (e.id == id) return e.fn; return nullptr; }
 

@@ -158,3 +158,22 @@ def test_embedding_bwd_ids(acc):
     for v0, v1 in split(V, 7):
         b.task('embedding_bwd', ids='ids', dout='dout', dtab='dtab', N=N, mod=0, v0=v0, v1=v1, d=d, acc=acc)
     _run(b)
+
+
+@pytest.mark.parametrize('sh_dt', ['bf16', 'f32'])
+def test_adamw_bf16_shadow(sh_dt):
+    """Op 305: AdamW plus the rounded copy of the new weight, over unaligned ranges (scalar heads/tails), a range
+    shorter than one 16-byte group and the two-groups-per-pass main loop."""
+    print(f'adamw_bf16 sh={sh_dt}', flush=True)
+    b = Builder(29)
+    n = 300007
+    for nm in ('p', 'g', 'm'):
+        b.normal(nm, 1, n, 'f32', scale=1.0)
+    b.normal('v', 1, n, 'f32', scale=0.01)
+    b.values('step', [3], 1, 1, 'i32')
+    b.fill('gs', 1, value=0.75)
+    b.fill('sh', 1, n, sh_dt)
+    for e0, e1 in ((1, 3), (3, 150001), (150001, 150003), (150003, n)):
+        b.task('adamw_bf16', p='p', g='g', m='m', v='v', gscale='gs', step='step', e0=e0, e1=e1, lr=3e-4, b1=0.9, b2=0.95,
+               eps=1e-8, wd=0.1, sh='sh')
+    _run(b)

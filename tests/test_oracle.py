@@ -112,6 +112,53 @@ def test_adamw_step1_fp64():
     assert np.abs(_get(r, b, 'p') - want).max() < 1e-6
 
 
+def _rne_bf16(x):
+    """float32 -> bf16 (round to nearest, ties to even) by integer arithmetic on the bits, back as float32."""
+    u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def test_adamw_bf16_matches_adamw_and_rounds_the_new_weight():
+    """Op 305 leaves p, m, v exactly as op 54 does and stores bf16(p_new) in sh (bf16 storage)."""
+    w = W(11)
+    n = 203
+    for pre in ('a', 'b'):
+        w.buf(pre + 'p', n), w.buf(pre + 'm', n, scale=0.1), w.pos(pre + 'v', n, 0.01)
+    w.buf('g', n), w.ints('step', [4]), w.zeros('sh', n, 1, 'bf16')
+    kw = dict(g='g', gscale=None, step='step', e0=0, e1=n, lr=1e-2, b1=0.9, b2=0.95, eps=1e-8, wd=0.1)
+    r, b = _run_one(w)
+    # same initial state for both: copy a* into b* through the materialised init
+    meta = b.metadata['buffers']
+    init = {m['name']: bl.materialize(m) for m in meta}
+    w2 = W(11)
+    for nm in ('p', 'm', 'v'):
+        w2.buf(nm, n, 1, 'f32', {'kind': 'values', 'values': init['a' + nm].tolist()})
+    w2.buf('g', n, 1, 'f32', {'kind': 'values', 'values': init['g'].tolist()})
+    w2.ints('step', [4]), w2.zeros('sh', n, 1, 'bf16')
+    for nm in ('p', 'm', 'v'):
+        w2.buf('q' + nm, n, 1, 'f32', {'kind': 'values', 'values': init['a' + nm].tolist()})
+    w2.task('adamw', p='p', m='m', v='v', **kw)
+    w2.task('adamw_bf16', p='qp', m='qm', v='qv', sh='sh', **kw)
+    r, b = _run_one(w2)
+    for nm in ('p', 'm', 'v'):
+        assert np.array_equal(_get(r, b, nm).view(np.uint32), _get(r, b, 'q' + nm).view(np.uint32)), nm
+    assert not np.array_equal(_get(r, b, 'p'), init['ap'])
+    assert np.array_equal(_get(r, b, 'sh').view(np.uint32), _rne_bf16(_get(r, b, 'p')).view(np.uint32))
+
+
+def test_gpt_bf16_shadow_starts_as_rounded_master():
+    """The bf16 GEMM copies of a bf16 GPT start as the fp32 masters rounded to bf16 (they are not rewritten before the
+    first forward; AdamW refreshes them afterwards)."""
+    from kvm_amd.workloads import gpt
+    wl = gpt.build(gpt.GPTConfig.tiny(dtype='bf16', layers=1, steps=1))
+    bufs = {m['name']: m for m in compiler.compile_spec(wl.spec).metadata['buffers']}
+    for name in ('wte', 'wq.0', 'w2.0'):
+        a = oracle.materialize(bufs[name], wl.init_override.get(name))
+        s = oracle.materialize(bufs[name + '.bf'], wl.init_override.get(name + '.bf'))
+        assert np.array_equal(s.view(np.uint32), _rne_bf16(a).view(np.uint32)), name
+
+
 def test_rope_inverse_and_head_rmsnorm():
     w = W(6)
     R, H, hd = 6, 2, 8

@@ -89,6 +89,7 @@ __device__ __forceinline__ void fence_seqcst() { __atomic_thread_fence(__ATOMIC_
 __device__ __forceinline__ void fence_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
 __device__ __forceinline__ void fence_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
 
+
 // ---------------------------------------------------------------------------------------------- bf16
 __device__ __host__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 // float -> bf16, round to nearest even; NaN stays NaN (quiet bit set), inf stays inf.
@@ -96,6 +97,27 @@ __device__ __host__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_fl
 // Finite values and infinities round exactly as (u + 0x7fff + ((u >> 16) & 1)) >> 16; NaNs stay NaN.
 __device__ __forceinline__ uint16_t f2bf(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 __device__ __forceinline__ float round_bf(float x) { return bf2f(f2bf(x)); }
+
+// Write-through global stores: the agent-scope form of a store (sc1, the encoding of an agent-scope relaxed atomic
+// store), which is agent-visible once it completes, with no L2 write-back. A task of an operator whose every global
+// store has this form is completed by waiting for the stores (vmcnt) instead of a release fence, whose L2 write-back
+// costs microseconds per task on a chip with one L2 per XCD. Consumers still acquire (L1 / L2 invalidate) as usual.
+__device__ __forceinline__ void stwt16(GLOBAL uint16_t* p, uint16_t v) { __hip_atomic_store((uint16_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void stwt32(GLOBAL float* p, float v) { __hip_atomic_store((float*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void stwt32i(GLOBAL int* p, int v) { __hip_atomic_store((int*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void stwt64(GLOBAL void* p, uint64_t v) { __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// 16 bytes as two 8-byte stores: every store stays visible to the compiler, whose wait counts must know about stores
+// (on gfx950 loads and stores share vmcnt and complete out of order with respect to each other).
+typedef uint64_t u64x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void stwt_f4(GLOBAL float* p, f32x4n v) {
+  const u64x2_t u = __builtin_bit_cast(u64x2_t, v);
+  stwt64(p, u.x); stwt64(p + 2, u.y);
+}
+// Four bf16 values as one 8-byte write-through store.
+__device__ __forceinline__ void stwt_bf4(GLOBAL uint16_t* p, float a, float b, float c, float d) {
+  stwt64(p, (uint64_t)f2bf(a) | ((uint64_t)f2bf(b) << 16) | ((uint64_t)f2bf(c) << 32) | ((uint64_t)f2bf(d) << 48));
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---------------------------------------------------------------------------------------------- views
 // A buffer argument as an operator sees it. ld()/st() widen / round bf16 storage; f/i give typed raw pointers.
@@ -107,7 +129,7 @@ struct View {
   __device__ GLOBAL uint16_t* h() const { return (GLOBAL uint16_t*)p; }
   __device__ float ld(long long k) const { return dtype == 2 ? bf2f(((const GLOBAL uint16_t*)p)[k]) : ((const GLOBAL float*)p)[k]; }
   __device__ float at(long long r, long long c) const { return ld(r * cols + c); }
-  __device__ void st(long long k, float v) const { if (dtype == 2) ((GLOBAL uint16_t*)p)[k] = f2bf(v); else ((GLOBAL float*)p)[k] = v; }
+  __device__ void st(long long k, float v) const { if (dtype == 2) stwt16((GLOBAL uint16_t*)p + k, f2bf(v)); else stwt32((GLOBAL float*)p + k, v); }
   __device__ long long n() const { return (long long)rows * cols; }
 };
 
@@ -127,7 +149,7 @@ struct Ctx {
   __device__ void fail(int code, int x = 0, int y = 0) const {
     int zero = 0;
     if (__hip_atomic_compare_exchange_strong(&cnt->err_code, &zero, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-      cnt->err_slot = slot; cnt->err_a = x; cnt->err_b = y;
+      stwt32i((GLOBAL int*)&cnt->err_slot, slot); stwt32i((GLOBAL int*)&cnt->err_a, x); stwt32i((GLOBAL int*)&cnt->err_b, y);
     }
   }
 };

@@ -9,9 +9,11 @@
 //     design for comparison: include/mvm_sched.cuh:115-374). There is one queue per XCD (workers of block b use queue
 //     b % nq; the hardware places block b on XCD b % 8), so the ticket and tail atomics of a phase's tasks spread over
 //     eight addresses instead of one.
-//   * Dependencies: after an operator, the workgroup barrier orders all its stores before wave 0's agent-scope
-//     release fence (on gfx950 this writes the XCD's L2 back so another XCD sees the data); wave 0 then decrements
-//     successor counters with acq_rel atomics and enqueues the ones that reach zero.
+//   * Dependencies: operators store only with write-through (agent-scope, sc1) stores, so after an operator each wave
+//     waits for its own stores and the workgroup barrier orders them before wave 0 signals successors, with no
+//     release fence (an agent-scope release writes the XCD's whole L2 back: microseconds per task). Wave 0
+//     decrements successor counters (relaxed atomics) and enqueues the ones that reach zero; the worker that dequeues
+//     a task acquires (agent scope: L1 and L2 invalidate) before running it.
 //   * Versions: a task released with version[wait_var] < wait_ver is parked on the variable's lock-free list. The
 //     publisher CASes version from pub_ver-1 to pub_ver (else VERSION_GAP), then takes the whole list and enqueues
 //     what is now satisfied. Parker (push; seq_cst fence; re-read version) and publisher (CAS version; seq_cst fence;
@@ -243,9 +245,12 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
     Ctx c{(const LDS View*)s_view, (const LDS int32_t*)s_args, (LDS char*)smem, S.cnt, slot};
     KVM_PT(6);
     dispatch(op, c);
+    // Every operator stores through write-through (agent-scope) stores only, which tests/test_wt_stores.py checks
+    // in the compiled code: once each wave has waited for its own stores, they are agent-visible, and the barrier
+    // orders that before wave 0 signals successors. No release fence, so no L2 write-back per task.
+    wait_stores();
     __syncthreads();
-    // Completion. Waves that touch successors first make this task's stores agent-visible (release fence: the
-    // barrier above ordered every thread's stores before it). Edges carry a host-computed bit: KVM_EDGE_DIRECT means
+    // Completion. The task's stores are agent-visible (above). Edges carry a host-computed bit: KVM_EDGE_DIRECT means
     // the successor has this task as its only predecessor and no version wait, so it is released with no counter
     // and no descriptor read. Other successors count down with a relaxed atomic; the decrement that reaches zero
     // acquires (fence) before releasing the task. Released tasks are enqueued in batches: per wave and per queue one
@@ -253,7 +258,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
     const int nsucc = s_desc.succ_cnt;
     const int nwaves = nsucc > 64 ? KVM_WAVES : 1;
     if (wave() < nwaves) {
-      fence_release();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       if (t == 0) {
         if (S.trace_on) {
           KvmTrace& tr = S.trace[slot];
@@ -271,8 +276,11 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
           s = e & KVM_EDGE_INDEX;
           if (e & KVM_EDGE_DIRECT) direct = true;
           else if (add_relaxed(&S.indeg[s], -1) == 1) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "agent");
-            if (S.tasks[s].wait_var < 0) direct = true; else release(S, s);
+            // Every predecessor made its stores agent-visible before its decrement, and the task that dequeues the
+            // successor acquires (L1 / L2 invalidate) before reading them, so the plain enqueue needs no fence here;
+            // the versioned path keeps its acquire-release.
+            if (S.tasks[s].wait_var < 0) direct = true;
+            else { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "agent"); release(S, s); }
           }
         }
         const int sq = direct ? s % S.nq : -1;

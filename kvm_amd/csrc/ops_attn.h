@@ -99,10 +99,10 @@ template <int HD> __device__ __noinline__ void attn_fwd_t(const Ctx& c) {
     float inv = 1.f / l;
 #pragma unroll
     for (int i = 0; i < HALF; ++i) o.st(((long long)bb * T + gq) * o.cols + h * HD + part * HALF + i, acc[i] * inv);
-    if (part == 0) lse.f()[((long long)bb * H + h) * T + gq] = m + logf(l);
+    if (part == 0) stwt32(lse.f() + (((long long)bb * H + h) * T + gq), m + logf(l));
   }
 }
-__device__ void op_attn_fwd(const Ctx& c) {
+__device__ __noinline__ void op_attn_fwd(const Ctx& c) {
   const int hd = c.i(11), T = c.i(8);
   if ((hd == 32 || hd == 64 || hd == 128) && T % FA_KB == 0 && fa_ok(c.buf(0), T) && fa_ok(c.buf(1), T) && fa_ok(c.buf(2), T) &&
       fa_ok(c.buf(3), T) && c.buf(4).dtype == 0) {
@@ -118,7 +118,7 @@ __device__ __noinline__ void op_attn_bwd_delta(const Ctx& c) {
     int r = rh / H, h = rh % H; float s = 0.f;
     for (int k = lane(); k < hd; k += 64) s += o.at(r, h * hd + k) * d.at(r, h * hd + k);
     s = wave_sum(s);
-    if (lane() == 0) delta.f()[((long long)(r / T) * H + h) * T + r % T] = s;
+    if (lane() == 0) stwt32(delta.f() + (((long long)(r / T) * H + h) * T + r % T), s);
   }
 }
 
@@ -161,7 +161,7 @@ template <int HD> __device__ __noinline__ void attn_dq_t(const Ctx& c) {
 #pragma unroll
     for (int i = 0; i < HALF; ++i) dq.st(qrow * dq.cols + h * HD + part * HALF + i, acc[i] * sc);
 }
-__device__ void op_attn_bwd_dq(const Ctx& c) {
+__device__ __noinline__ void op_attn_bwd_dq(const Ctx& c) {
   const int hd = c.i(13), T = c.i(10);
   if ((hd == 32 || hd == 64) && T % FA_KB == 0 && fa_ok(c.buf(0), T) && fa_ok(c.buf(1), T) && fa_ok(c.buf(2), T) && fa_ok(c.buf(3), T) &&
       fa_ok(c.buf(6), T) && c.buf(4).dtype == 0 && c.buf(5).dtype == 0) {
@@ -217,7 +217,7 @@ template <int HD> __device__ __noinline__ void attn_dkv_t(const Ctx& c) {
       dv.st(krow * dv.cols + kvh * HD + part * HALF + i, sv[i]);
     }
 }
-__device__ void op_attn_bwd_dkv(const Ctx& c) {
+__device__ __noinline__ void op_attn_bwd_dkv(const Ctx& c) {
   const int hd = c.i(13), T = c.i(11);
   if ((hd == 32 || hd == 64) && T % FA_KB == 0 && fa_ok(c.buf(0), T) && fa_ok(c.buf(1), T) && fa_ok(c.buf(2), T) && fa_ok(c.buf(3), T) &&
       fa_ok(c.buf(6), T) && fa_ok(c.buf(7), T) && c.buf(4).dtype == 0 && c.buf(5).dtype == 0) {
@@ -295,7 +295,7 @@ __device__ __noinline__ void op_attn_decode_part(const Ctx& c) {
   if (nk == 0) {
     for (int e = tid(); e < G * (hd + 2); e += KVM_THREADS) {
       int g = e / (hd + 2), k = e % (hd + 2); long long r = (((long long)bb * S + s) * H + kvh * G + g) * part.cols;
-      part.f()[r + k] = k < hd ? 0.f : (k == hd ? ATTN_EMPTY_M : 0.f);
+      stwt32(part.f() + (r + k), k < hd ? 0.f : (k == hd ? ATTN_EMPTY_M : 0.f));
     }
     return;
   }
@@ -368,8 +368,8 @@ __device__ __noinline__ void op_attn_decode_part(const Ctx& c) {
     if (e >= G * hd) break;
     int g = e / hd, k = e % hd;
     long long r = (((long long)bb * S + s) * H + kvh * G + g) * part.cols;
-    part.f()[r + k] = acc[u];
-    if (k == 0) { part.f()[r + hd] = st[g]; part.f()[r + hd + 1] = st[8 + g]; }
+    stwt32(part.f() + (r + k), acc[u]);
+    if (k == 0) { stwt32(part.f() + (r + hd), st[g]); stwt32(part.f() + (r + hd + 1), st[8 + g]); }
   }
 }
 // Streaming form of op 135 for bf16 caches with hd = 128: the split's tokens go in blocks of 160 (40 per wave). Lane l
@@ -469,7 +469,7 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c) {
     for (int e = tid(); e < G * (hd + 2); e += KVM_THREADS) {
       const int g = e / (hd + 2), k = e % (hd + 2);
       const long long r = (((long long)bb * S + s) * H + kvh * G + g) * part.cols;
-      part.f()[r + k] = k < hd ? 0.f : (k == hd ? ATTN_EMPTY_M : 0.f);
+      stwt32(part.f() + (r + k), k < hd ? 0.f : (k == hd ? ATTN_EMPTY_M : 0.f));
     }
     return;
   }
@@ -563,8 +563,8 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c) {
 #pragma unroll
     for (int q2 = 0; q2 < 16; ++q2) t += racc[(q2 * G + g) * hd + k];
     const long long r = (((long long)bb * S + s) * H + kvh * G + g) * part.cols;
-    part.f()[r + k] = t;
-    if (k == 0) { part.f()[r + hd] = mrun[g]; part.f()[r + hd + 1] = lrun[g]; }
+    stwt32(part.f() + (r + k), t);
+    if (k == 0) { stwt32(part.f() + (r + hd), mrun[g]); stwt32(part.f() + (r + hd + 1), lrun[g]); }
   }
 #ifdef KVM_GEMM_PROF
   pt[5] = wall_clock64();

@@ -166,9 +166,8 @@ template <int HD> __device__ __noinline__ void attn_fwd_mfma(const Ctx& c) {
     for (int d = 0; d < NDB; ++d)
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq)
-        *(GLOBAL u16x4_t*)(orow + d * 32 + 8 * rq) = u16x4_t{f2bf(oacc[d][4 * rq] * inv), f2bf(oacc[d][4 * rq + 1] * inv),
-                                                             f2bf(oacc[d][4 * rq + 2] * inv), f2bf(oacc[d][4 * rq + 3] * inv)};
-    if (g == 0) lse.f()[((long long)bb * H + h) * T + qrow] = (m + log2f(lsum)) * 0.6931471805599453f;
+        stwt_bf4(orow + d * 32 + 8 * rq, oacc[d][4 * rq] * inv, oacc[d][4 * rq + 1] * inv, oacc[d][4 * rq + 2] * inv, oacc[d][4 * rq + 3] * inv);
+    if (g == 0) stwt32(lse.f() + (((long long)bb * H + h) * T + qrow), (m + log2f(lsum)) * 0.6931471805599453f);
   }
 }
 
@@ -251,8 +250,7 @@ template <int HD> __device__ __noinline__ void attn_dq_mfma(const Ctx& c) {
     for (int d = 0; d < NDB; ++d)
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq)
-        *(GLOBAL u16x4_t*)(orow + d * 32 + 8 * rq) = u16x4_t{f2bf(acc[d][4 * rq] * sc), f2bf(acc[d][4 * rq + 1] * sc),
-                                                             f2bf(acc[d][4 * rq + 2] * sc), f2bf(acc[d][4 * rq + 3] * sc)};
+        stwt_bf4(orow + d * 32 + 8 * rq, acc[d][4 * rq] * sc, acc[d][4 * rq + 1] * sc, acc[d][4 * rq + 2] * sc, acc[d][4 * rq + 3] * sc);
   }
 }
 
@@ -359,10 +357,8 @@ template <int HD> __device__ __noinline__ void attn_dkv_mfma(const Ctx& c) {
     for (int d = 0; d < NDB; ++d)
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
-        *(GLOBAL u16x4_t*)(kr + d * 32 + 8 * rq) = u16x4_t{f2bf(adk[d][4 * rq] * sc), f2bf(adk[d][4 * rq + 1] * sc),
-                                                           f2bf(adk[d][4 * rq + 2] * sc), f2bf(adk[d][4 * rq + 3] * sc)};
-        *(GLOBAL u16x4_t*)(vr + d * 32 + 8 * rq) = u16x4_t{f2bf(adv[d][4 * rq]), f2bf(adv[d][4 * rq + 1]), f2bf(adv[d][4 * rq + 2]),
-                                                           f2bf(adv[d][4 * rq + 3])};
+        stwt_bf4(kr + d * 32 + 8 * rq, adk[d][4 * rq] * sc, adk[d][4 * rq + 1] * sc, adk[d][4 * rq + 2] * sc, adk[d][4 * rq + 3] * sc);
+        stwt_bf4(vr + d * 32 + 8 * rq, adv[d][4 * rq], adv[d][4 * rq + 1], adv[d][4 * rq + 2], adv[d][4 * rq + 3]);
       }
   }
 }

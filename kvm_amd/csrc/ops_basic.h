@@ -11,12 +11,12 @@ namespace kvm {
 #define FLAT_FOR(i, e0, e1) for (long long i = (long long)(e0) + tid(); i < (long long)(e1); i += KVM_THREADS)
 
 // ---------------------------------------------------------------------------------------------- core pack
-__device__ __noinline__ void op_copy(const Ctx& c) { View s = c.buf(0), d = c.buf(1); FLAT_FOR(k, 0, c.i(2)) d.i()[k] = s.i()[k]; }
-__device__ __noinline__ void op_add(const Ctx& c) { View a = c.buf(0), b = c.buf(1), o = c.buf(2); FLAT_FOR(k, 0, c.i(3)) o.f()[k] = a.f()[k] + b.f()[k]; }
-__device__ __noinline__ void op_scale(const Ctx& c) { View x = c.buf(0), o = c.buf(1); float al = c.f(2); FLAT_FOR(k, 0, c.i(3)) o.f()[k] = x.f()[k] * al; }
-__device__ __noinline__ void op_relu(const Ctx& c) { View x = c.buf(0), o = c.buf(1); FLAT_FOR(k, 0, c.i(2)) { float v = x.f()[k]; o.f()[k] = v > 0.f ? v : 0.f; } }
-__device__ __noinline__ void op_sgd(const Ctx& c) { View w = c.buf(0), g = c.buf(1); float lr = c.f(2); FLAT_FOR(k, 0, c.i(3)) w.f()[k] = w.f()[k] - __fmul_rn(lr, g.f()[k]); }
-__device__ __noinline__ void op_predict(const Ctx& c) { View x = c.buf(0), w = c.buf(1), o = c.buf(2); float s = w.f()[0]; FLAT_FOR(k, 0, c.i(3)) o.f()[k] = s * x.f()[k]; }
+__device__ __noinline__ void op_copy(const Ctx& c) { View s = c.buf(0), d = c.buf(1); FLAT_FOR(k, 0, c.i(2)) stwt32i(d.i() + k, s.i()[k]); }
+__device__ __noinline__ void op_add(const Ctx& c) { View a = c.buf(0), b = c.buf(1), o = c.buf(2); FLAT_FOR(k, 0, c.i(3)) stwt32(o.f() + k, a.f()[k] + b.f()[k]); }
+__device__ __noinline__ void op_scale(const Ctx& c) { View x = c.buf(0), o = c.buf(1); float al = c.f(2); FLAT_FOR(k, 0, c.i(3)) stwt32(o.f() + k, x.f()[k] * al); }
+__device__ __noinline__ void op_relu(const Ctx& c) { View x = c.buf(0), o = c.buf(1); FLAT_FOR(k, 0, c.i(2)) { float v = x.f()[k]; stwt32(o.f() + k, v > 0.f ? v : 0.f); } }
+__device__ __noinline__ void op_sgd(const Ctx& c) { View w = c.buf(0), g = c.buf(1); float lr = c.f(2); FLAT_FOR(k, 0, c.i(3)) stwt32(w.f() + k, w.f()[k] - __fmul_rn(lr, g.f()[k])); }
+__device__ __noinline__ void op_predict(const Ctx& c) { View x = c.buf(0), w = c.buf(1), o = c.buf(2); float s = w.f()[0]; FLAT_FOR(k, 0, c.i(3)) stwt32(o.f() + k, s * x.f()[k]); }
 __device__ __noinline__ void op_mse_grad(const Ctx& c) {   // sequential f32 accumulation, as the reference (ref_ops.py:46-54)
   View p = c.buf(0), t = c.buf(1), x = c.buf(2), l = c.buf(3), g = c.buf(4); int n = c.i(5);
   if (tid() == 0) {
@@ -26,7 +26,7 @@ __device__ __noinline__ void op_mse_grad(const Ctx& c) {   // sequential f32 acc
       la = la + __fmul_rn(d, d);
       ga = ga + __fmul_rn(2.f * d, x.f()[k]);
     }
-    l.f()[0] = la / (float)n; g.f()[0] = ga / (float)n;
+    stwt32(l.f() + 0, la / (float)n); stwt32(g.f() + 0, ga / (float)n);
   }
 }
 __device__ __noinline__ void op_matmul(const Ctx& c) {   // small fp32 GEMM, sequential k (ref_ops.py:57-66)
@@ -34,10 +34,10 @@ __device__ __noinline__ void op_matmul(const Ctx& c) {   // small fp32 GEMM, seq
   for (int e = tid(); e < m * n; e += KVM_THREADS) {
     int i = e / n, j = e % n; float acc = 0.f;
     for (int p = 0; p < k; ++p) acc = acc + __fmul_rn(a.f()[i * k + p], b.f()[p * n + j]);
-    o.f()[e] = acc;
+    stwt32(o.f() + e, acc);
   }
 }
-__device__ __noinline__ void op_fill(const Ctx& c) { View x = c.buf(0); float v = c.f(1); FLAT_FOR(k, 0, c.i(2)) x.f()[k] = v; }
+__device__ __noinline__ void op_fill(const Ctx& c) { View x = c.buf(0); float v = c.f(1); FLAT_FOR(k, 0, c.i(2)) stwt32(x.f() + k, v); }
 __device__ __noinline__ void op_spin(const Ctx& c) {
   if (tid() == 0) { unsigned long long t0 = wall_clock64(), n = (unsigned long long)c.i(0) * 100ull; while (wall_clock64() - t0 < n) __builtin_amdgcn_s_sleep(2); }
 }
@@ -61,21 +61,21 @@ __device__ __noinline__ void op_gelu_bwd(const Ctx& c) {
   FLAT_FOR(k, c.i(3), c.i(4)) { float v = dy.ld(k) * gelu_grad_f(x.ld(k)); dx.st(k, acc ? dx.ld(k) + v : v); }
 }
 __device__ __noinline__ void op_residual_add(const Ctx& c) { View a = c.buf(0), b = c.buf(1), o = c.buf(2); FLAT_FOR(k, c.i(3), c.i(4)) o.st(k, a.ld(k) + b.ld(k)); }
-__device__ __noinline__ void op_sgd_range(const Ctx& c) { View w = c.buf(0), g = c.buf(1); float lr = c.f(2); FLAT_FOR(k, c.i(3), c.i(4)) w.f()[k] = w.f()[k] - __fmul_rn(lr, g.f()[k]); }
+__device__ __noinline__ void op_sgd_range(const Ctx& c) { View w = c.buf(0), g = c.buf(1); float lr = c.f(2); FLAT_FOR(k, c.i(3), c.i(4)) stwt32(w.f() + k, w.f()[k] - __fmul_rn(lr, g.f()[k])); }
 __device__ __noinline__ void op_round_tf32(const Ctx& c) {
   View x = c.buf(0), o = c.buf(1);
-  FLAT_FOR(k, c.i(2), c.i(3)) { uint32_t u = __float_as_uint(x.f()[k]); if ((u & 0x7fffffffu) <= 0x7f800000u) u += 0x1000u; o.f()[k] = __uint_as_float(u & 0xffffe000u); }
+  FLAT_FOR(k, c.i(2), c.i(3)) { uint32_t u = __float_as_uint(x.f()[k]); if ((u & 0x7fffffffu) <= 0x7f800000u) u += 0x1000u; stwt32(o.f() + k, __uint_as_float(u & 0xffffe000u)); }
 }
 __device__ __noinline__ void op_zero_buf(const Ctx& c) {
   View x = c.buf(0);
-  if (x.dtype == 2) { FLAT_FOR(k, c.i(1), c.i(2)) x.h()[k] = 0; }
-  else FLAT_FOR(k, c.i(1), c.i(2)) x.i()[k] = 0;
+  if (x.dtype == 2) { FLAT_FOR(k, c.i(1), c.i(2)) stwt16(x.h() + k, 0); }
+  else FLAT_FOR(k, c.i(1), c.i(2)) stwt32i(x.i() + k, 0);
 }
-__device__ __noinline__ void op_counter_inc(const Ctx& c) { View x = c.buf(0); FLAT_FOR(k, c.i(1), c.i(2)) x.i()[k] = (int)((unsigned)x.i()[k] + (unsigned)c.i(3)); }
+__device__ __noinline__ void op_counter_inc(const Ctx& c) { View x = c.buf(0); FLAT_FOR(k, c.i(1), c.i(2)) stwt32i(x.i() + k, (int)((unsigned)x.i()[k] + (unsigned)c.i(3))); }
 __device__ __noinline__ void op_round_bf16(const Ctx& c) {   // f32<->bf16 storage conversion (or f32->f32 emulation)
   View x = c.buf(0), o = c.buf(1);
-  if (x.dtype == 2 && o.dtype == 2) { FLAT_FOR(k, c.i(2), c.i(3)) o.h()[k] = x.h()[k]; return; }
-  FLAT_FOR(k, c.i(2), c.i(3)) { float v = x.ld(k); if (o.dtype == 2) o.h()[k] = f2bf(v); else o.f()[k] = round_bf(v); }
+  if (x.dtype == 2 && o.dtype == 2) { FLAT_FOR(k, c.i(2), c.i(3)) stwt16(o.h() + k, x.h()[k]); return; }
+  FLAT_FOR(k, c.i(2), c.i(3)) { float v = x.ld(k); if (o.dtype == 2) stwt16(o.h() + k, f2bf(v)); else stwt32(o.f() + k, round_bf(v)); }
 }
 __device__ __forceinline__ float act_f(int kind, float x) {
   switch (kind) { case 0: return x > 0.f ? x : 0.f; case 1: return silu_f(x); case 2: return tanhf(x); default: return sigmoid_f(x); }
@@ -84,25 +84,25 @@ __device__ __forceinline__ float act_d(int kind, float x) {
   switch (kind) { case 0: return x > 0.f ? 1.f : 0.f; case 1: return silu_d_f(x); case 2: { float t = tanhf(x); return 1.f - t * t; }
     default: { float s = sigmoid_f(x); return s * (1.f - s); } }
 }
-__device__ __noinline__ void op_act_fwd(const Ctx& c) { View x = c.buf(0), o = c.buf(1); int kind = c.i(2); FLAT_FOR(k, c.i(3), c.i(4)) o.f()[k] = act_f(kind, x.f()[k]); }
+__device__ __noinline__ void op_act_fwd(const Ctx& c) { View x = c.buf(0), o = c.buf(1); int kind = c.i(2); FLAT_FOR(k, c.i(3), c.i(4)) stwt32(o.f() + k, act_f(kind, x.f()[k])); }
 __device__ __noinline__ void op_act_bwd(const Ctx& c) {
   View x = c.buf(0), dy = c.buf(1), dx = c.buf(2); int kind = c.i(3), acc = c.i(6);
-  FLAT_FOR(k, c.i(4), c.i(5)) { float v = dy.f()[k] * act_d(kind, x.f()[k]); dx.f()[k] = acc ? dx.f()[k] + v : v; }
+  FLAT_FOR(k, c.i(4), c.i(5)) { float v = dy.f()[k] * act_d(kind, x.f()[k]); stwt32(dx.f() + k, acc ? dx.f()[k] + v : v); }
 }
 __device__ __noinline__ void op_silu_mul_fwd(const Ctx& c) { View g = c.buf(0), u = c.buf(1), o = c.buf(2); FLAT_FOR(k, c.i(3), c.i(4)) o.st(k, silu_f(g.ld(k)) * u.ld(k)); }
 __device__ __noinline__ void op_silu_mul_bwd(const Ctx& c) {
   View g = c.buf(0), u = c.buf(1), dy = c.buf(2), dg = c.buf(3), du = c.buf(4); int acc = c.i(7);
   FLAT_FOR(k, c.i(5), c.i(6)) {
     float gv = g.f()[k], vg = dy.f()[k] * (u.f()[k] * silu_d_f(gv)), vu = dy.f()[k] * silu_f(gv);
-    dg.f()[k] = acc ? dg.f()[k] + vg : vg; du.f()[k] = acc ? du.f()[k] + vu : vu;
+    stwt32(dg.f() + k, acc ? dg.f()[k] + vg : vg); stwt32(du.f() + k, acc ? du.f()[k] + vu : vu);
   }
 }
-__device__ __noinline__ void op_scale_flat(const Ctx& c) { View x = c.buf(0), o = c.buf(1); float al = c.f(2); FLAT_FOR(k, c.i(3), c.i(4)) o.f()[k] = al * x.f()[k]; }
+__device__ __noinline__ void op_scale_flat(const Ctx& c) { View x = c.buf(0), o = c.buf(1); float al = c.f(2); FLAT_FOR(k, c.i(3), c.i(4)) stwt32(o.f() + k, al * x.f()[k]); }
 __device__ __noinline__ void op_add_rowtile(const Ctx& c) {
   View x = c.buf(0), pos = c.buf(1), o = c.buf(2); int r0 = c.i(3), r1 = c.i(4), T = c.i(5), d = c.i(6);
   for (long long e = tid(); e < (long long)(r1 - r0) * d; e += KVM_THREADS) {
     int r = r0 + (int)(e / d), k = (int)(e % d);
-    o.f()[(long long)r * o.cols + k] = x.f()[(long long)r * x.cols + k] + pos.f()[(long long)(r % T) * pos.cols + k];
+    stwt32(o.f() + ((long long)r * o.cols + k), x.f()[(long long)r * x.cols + k] + pos.f()[(long long)(r % T) * pos.cols + k]);
   }
 }
 
@@ -125,18 +125,18 @@ __device__ __noinline__ void op_embedding_fwd(const Ctx& c) {
 __device__ __noinline__ void op_embedding_bwd(const Ctx& c) {
   View ids = c.buf(0), dout = c.buf(1), dt = c.buf(2);
   int N = c.i(3), mod = c.i(4), v0 = c.i(5), v1 = c.i(6), d = c.i(7), acc = c.i(8);
-  if (!acc) for (long long e = tid(); e < (long long)(v1 - v0) * d; e += KVM_THREADS) dt.f()[(long long)(v0 + e / d) * dt.cols + e % d] = 0.f;
+  if (!acc) for (long long e = tid(); e < (long long)(v1 - v0) * d; e += KVM_THREADS) stwt32(dt.f() + ((long long)(v0 + e / d) * dt.cols + e % d), 0.f);
   __syncthreads();
   if (ids.ok()) {
     for (int r = 0; r < N; ++r) {
       int key = ids.i()[r];
       if (key < v0 || key >= v1) continue;
-      for (int k = tid(); k < d; k += KVM_THREADS) dt.f()[(long long)key * dt.cols + k] += dout.at(r, k);
+      for (int k = tid(); k < d; k += KVM_THREADS) stwt32(dt.f() + ((long long)key * dt.cols + k), dt.f()[(long long)key * dt.cols + k] + (dout.at(r, k)));
     }
   } else {
     for (int key = v0; key < v1; ++key)
       for (int r = key; r < N; r += mod)
-        for (int k = tid(); k < d; k += KVM_THREADS) dt.f()[(long long)key * dt.cols + k] += dout.at(r, k);
+        for (int k = tid(); k < d; k += KVM_THREADS) stwt32(dt.f() + ((long long)key * dt.cols + k), dt.f()[(long long)key * dt.cols + k] + (dout.at(r, k)));
   }
 }
 __device__ __noinline__ void op_gather_rows(const Ctx& c) {
@@ -144,14 +144,14 @@ __device__ __noinline__ void op_gather_rows(const Ctx& c) {
   for (int r = r0 + wave(); r < r1; r += KVM_WAVES) {
     int j = idx.i()[r]; bool bad = j < 0 || j >= src.rows;
     if (bad && lane() == 0) c.fail(KVM_ERR_OP_TOKEN, r, j);
-    for (int k = lane(); k < d; k += 64) dst.f()[(long long)r * dst.cols + k] = bad ? 0.f : src.f()[(long long)j * src.cols + k];
+    for (int k = lane(); k < d; k += 64) stwt32(dst.f() + ((long long)r * dst.cols + k), bad ? 0.f : src.f()[(long long)j * src.cols + k]);
   }
 }
 __device__ __noinline__ void op_select_window(const Ctx& c) {
   View src = c.buf(0), step = c.buf(1), dst = c.buf(2); int i0 = c.i(3), i1 = c.i(4), stride = c.i(5), off = c.i(6);
   long long base = (long long)step.i()[0] * stride + off;
   if (base < 0 || base + i1 > src.n()) { if (tid() == 0) c.fail(KVM_ERR_OP_RANGE, (int)base, i1); return; }
-  FLAT_FOR(k, i0, i1) dst.i()[k] = src.i()[base + k];
+  FLAT_FOR(k, i0, i1) stwt32i(dst.i() + k, src.i()[base + k]);
 }
 __device__ __noinline__ void op_gather_rows_scaled(const Ctx& c) {
   View src = c.buf(0), idx = c.buf(1), sc = c.buf(2), dst = c.buf(3); int r0 = c.i(4), r1 = c.i(5), d = c.i(6), acc = c.i(7), i0 = c.i(8);
@@ -159,7 +159,7 @@ __device__ __noinline__ void op_gather_rows_scaled(const Ctx& c) {
     int j = idx.i()[i0 + r]; float s = sc.ok() ? sc.f()[i0 + r] : 1.f; bool ok = j >= 0 && j < src.rows;
     for (int k = lane(); k < d; k += 64) {
       float v = ok ? s * src.f()[(long long)j * src.cols + k] : 0.f; long long o = (long long)r * dst.cols + k;
-      dst.f()[o] = acc ? dst.f()[o] + v : v;
+      stwt32(dst.f() + o, acc ? dst.f()[o] + v : v);
     }
   }
 }
@@ -170,7 +170,7 @@ __device__ __noinline__ void op_scatter_add_rows(const Ctx& c) {
     for (int k = tid(); k < d; k += KVM_THREADS) {
       float a = 0.f;
       for (int r = 0; r < N; ++r) if (idx.i()[i0 + r] == v) a += (sc.ok() ? sc.f()[i0 + r] : 1.f) * src.f()[(long long)r * src.cols + k];
-      long long o = (long long)v * dst.cols + k; dst.f()[o] = acc ? dst.f()[o] + a : a;
+      long long o = (long long)v * dst.cols + k; stwt32(dst.f() + o, acc ? dst.f()[o] + a : a);
     }
 }
 __device__ __noinline__ void op_row_dot(const Ctx& c) {
@@ -180,7 +180,7 @@ __device__ __noinline__ void op_row_dot(const Ctx& c) {
     float s = 0.f;
     if (ok) for (int k = lane(); k < d; k += 64) s += A.f()[(long long)j * A.cols + k] * B.f()[(long long)r * B.cols + k];
     s = wave_sum(s);
-    if (lane() == 0) out.f()[i0 + r] = acc ? out.f()[i0 + r] + s : s;
+    if (lane() == 0) stwt32(out.f() + (i0 + r), acc ? out.f()[i0 + r] + s : s);
   }
 }
 
@@ -197,7 +197,7 @@ template <bool RMS> __device__ __noinline__ void op_norm_fwd(const Ctx& c) {
     float ss = 0.f; for (int j = lane(); j < d; j += 64) { float v = x.at(r, j) - mu; ss += v * v; }
     float rs = 1.f / sqrtf(wave_sum(ss) / (float)d + eps);
     for (int j = lane(); j < d; j += 64) out.st((long long)r * out.cols + j, (x.at(r, j) - mu) * rs * g.f()[j] + (RMS ? 0.f : be.f()[j]));
-    if (lane() == 0) { rstd.f()[r] = rs; if (!RMS) mean.f()[r] = mu; }
+    if (lane() == 0) { stwt32(rstd.f() + r, rs); if (!RMS) stwt32(mean.f() + r, mu); }
   }
 }
 template <bool RMS> __device__ __noinline__ void op_norm_bwd_dx(const Ctx& c) {
@@ -222,15 +222,15 @@ __device__ __noinline__ void op_norm_bwd_params(const Ctx& c) {
   for (int j = c0 + tid(); j < c1; j += KVM_THREADS) {
     float sg = 0.f, sb = 0.f;
     for (int r = 0; r < R; ++r) { float gv = dy.at(r, j); sg += gv * (x.at(r, j) - (mean.ok() ? mean.f()[r] : 0.f)) * rstd.f()[r]; sb += gv; }
-    dg.f()[j] = acc ? dg.f()[j] + sg : sg;
-    if (db.ok()) db.f()[j] = acc ? db.f()[j] + sb : sb;
+    stwt32(dg.f() + j, acc ? dg.f()[j] + sg : sg);
+    if (db.ok()) stwt32(db.f() + j, acc ? db.f()[j] + sb : sb);
   }
 }
 __device__ __noinline__ void op_colsum(const Ctx& c) {
   View x = c.buf(0), out = c.buf(1); int R = c.i(2), c0 = c.i(3), c1 = c.i(4), acc = c.i(5);
   for (int j = c0 + tid(); j < c1; j += KVM_THREADS) {
     float s = 0.f; for (int r = 0; r < R; ++r) s += x.at(r, j);
-    out.f()[j] = acc ? out.f()[j] + s : s;
+    stwt32(out.f() + j, acc ? out.f()[j] + s : s);
   }
 }
 __device__ __noinline__ void op_head_rmsnorm(const Ctx& c) {   // RMSNorm per head slice of hd columns (Qwen3 q/k norm)
@@ -278,7 +278,7 @@ __device__ __noinline__ void op_softmax_rows_fwd(const Ctx& c) {
     m = wave_max(m);
     float z = 0.f; for (int j = lane(); j < d; j += 64) z += __expf(x.at(r, j) * sc - m);
     z = wave_sum(z);
-    for (int j = lane(); j < d; j += 64) o.f()[(long long)r * o.cols + j] = __expf(x.at(r, j) * sc - m) / z;
+    for (int j = lane(); j < d; j += 64) stwt32(o.f() + ((long long)r * o.cols + j), __expf(x.at(r, j) * sc - m) / z);
   }
 }
 __device__ __noinline__ void op_softmax_rows_bwd(const Ctx& c) {
@@ -286,7 +286,7 @@ __device__ __noinline__ void op_softmax_rows_bwd(const Ctx& c) {
   for (int r = r0 + wave(); r < r1; r += KVM_WAVES) {
     float dot = 0.f; for (int j = lane(); j < d; j += 64) dot += p.at(r, j) * dp.at(r, j);
     dot = wave_sum(dot);
-    for (int j = lane(); j < d; j += 64) { float v = sc * p.at(r, j) * (dp.at(r, j) - dot); long long o = (long long)r * dx.cols + j; dx.f()[o] = acc ? dx.f()[o] + v : v; }
+    for (int j = lane(); j < d; j += 64) { float v = sc * p.at(r, j) * (dp.at(r, j) - dot); long long o = (long long)r * dx.cols + j; stwt32(dx.f() + o, acc ? dx.f()[o] + v : v); }
   }
 }
 // Cross entropy over rows [r0, r1): one wave per row, online max/sum in one pass over the logits, then the gradient.
@@ -297,7 +297,7 @@ __device__ void ce_rows(const Ctx& c, View lg, View tg, View rl, View ls, View d
     if (!ign && (t < 0 || t >= V)) { if (lane() == 0) c.fail(KVM_ERR_OP_TOKEN, r, t); continue; }
     float lse;
     if (fwd) {
-      if (ign) { if (lane() == 0) { rl.f()[r] = 0.f; ls.f()[r] = 0.f; } lse = 0.f; }
+      if (ign) { if (lane() == 0) { stwt32(rl.f() + r, 0.f); stwt32(ls.f() + r, 0.f); } lse = 0.f; }
       else {
         float m = -INFINITY, s = 0.f;
         for (int j = lane(); j < V; j += 64) { float v = lg.at(r, j); float nm = fmaxf(m, v); s = s * __expf(m - nm) + __expf(v - nm); m = nm; }
@@ -306,7 +306,7 @@ __device__ void ce_rows(const Ctx& c, View lg, View tg, View rl, View ls, View d
           s = (nm == -INFINITY) ? 0.f : s * __expf(m - nm) + s2 * __expf(m2 - nm); m = nm;
         }
         lse = m + logf(s);
-        if (lane() == 0) { ls.f()[r] = lse; rl.f()[r] = lse - lg.at(r, t); }
+        if (lane() == 0) { stwt32(ls.f() + r, lse); stwt32(rl.f() + r, lse - lg.at(r, t)); }
       }
     } else lse = ls.f()[r];
     if (bwd) for (int j = lane(); j < V; j += 64)
@@ -320,7 +320,7 @@ __device__ __noinline__ void op_softmax_ce_reduce(const Ctx& c) {
   double s = 0.0; float cnt = 0.f;
   for (int r = tid(); r < N; r += KVM_THREADS) if (tg.i()[r] != ig) { s += rl.f()[r]; cnt += 1.f; }
   s = block_sum_d(s, red); cnt = block_sum(cnt, redc);
-  if (tid() == 0) { int n = (int)cnt; loss.f()[0] = n ? (float)(s / n) : 0.f; loss.f()[1] = n ? (float)(1.0 / n) : 0.f; }
+  if (tid() == 0) { int n = (int)cnt; stwt32(loss.f() + 0, n ? (float)(s / n) : 0.f); stwt32(loss.f() + 1, n ? (float)(1.0 / n) : 0.f); }
 }
 __device__ __noinline__ void op_softmax_ce_bwd(const Ctx& c) {
   View n{}; float f = c.buf(3).f()[1] * c.f(9);
@@ -355,8 +355,8 @@ __device__ void adamw_body(const Ctx& c, View p, View g, View m, View v, View gs
   auto one = [&](long long i) {
     float pp = p.f()[i], mm = m.f()[i], vv = v.f()[i];
     adamw_elem(pp, g.f()[i], mm, vv, gsc, b1, b2, lr, eps, wd, bc1, bc2);
-    p.f()[i] = pp; m.f()[i] = mm; v.f()[i] = vv;
-    if (shk == 2) sh.h()[i] = f2bf(pp); else if (shk == 1) sh.f()[i] = round_bf(pp);
+    stwt32(p.f() + i, pp); stwt32(m.f() + i, mm); stwt32(v.f() + i, vv);
+    if (shk == 2) stwt16(sh.h() + i, f2bf(pp)); else if (shk == 1) stwt32(sh.f() + i, round_bf(pp));
   };
   for (long long i = e0 + tid(); i < a0; i += KVM_THREADS) one(i);
   for (long long i = a1 + tid(); i < e1; i += KVM_THREADS) one(i);
@@ -368,14 +368,12 @@ __device__ void adamw_body(const Ctx& c, View p, View g, View m, View v, View gs
       adamw_elem(a, gg[j], b, d, gsc, b1, b2, lr, eps, wd, bc1, bc2);
       pp[j] = a; mm[j] = b; vv[j] = d;
     }
-    P[q] = pp; M[q] = mm; Vv[q] = vv;
+    stwt_f4((GLOBAL float*)(P + q), pp); stwt_f4((GLOBAL float*)(M + q), mm); stwt_f4((GLOBAL float*)(Vv + q), vv);
     if (shk == 2) {
-      typedef uint32_t u32x2n __attribute__((ext_vector_type(2)));
-      u32x2n w; w.x = (uint32_t)f2bf(pp[0]) | ((uint32_t)f2bf(pp[1]) << 16); w.y = (uint32_t)f2bf(pp[2]) | ((uint32_t)f2bf(pp[3]) << 16);
-      ((GLOBAL u32x2n*)sh.h())[q] = w;
+      stwt_bf4(sh.h() + 4 * q, pp[0], pp[1], pp[2], pp[3]);
     } else if (shk == 1) {
       f32x4n r; for (int j = 0; j < 4; ++j) r[j] = round_bf(pp[j]);
-      ((GLOBAL f32x4n*)sh.f())[q] = r;
+      stwt_f4(sh.f() + 4 * q, r);
     }
   };
   // two 16-byte groups per thread per pass: eight loads in flight before the first update
@@ -395,15 +393,15 @@ __device__ __noinline__ void op_gradnorm_partial(const Ctx& c) {
   View g = c.buf(0), part = c.buf(1); __shared__ double red[KVM_WAVES];
   double s = 0.0; FLAT_FOR(i, c.i(3), c.i(4)) { double x = g.f()[i]; s += x * x; }
   s = block_sum_d(s, red);
-  if (tid() == 0) part.f()[c.i(2)] = (float)s;
+  if (tid() == 0) stwt32(part.f() + (c.i(2)), (float)s);
 }
 __device__ __noinline__ void op_gradnorm_finish(const Ctx& c) {
   View part = c.buf(0), out = c.buf(2); int ns = c.i(1); float mx = c.f(3);
   if (tid() == 0) {
     double s = 0.0; for (int i = 0; i < ns; ++i) s += part.f()[i];
     float n = (float)sqrt(s);
-    out.f()[0] = mx > 0.f ? fminf(1.f, mx / (n + 1e-6f)) : 1.f;
-    out.f()[1] = n;
+    stwt32(out.f() + 0, mx > 0.f ? fminf(1.f, mx / (n + 1e-6f)) : 1.f);
+    stwt32(out.f() + 1, n);
   }
 }
 __device__ __noinline__ void op_lr_schedule(const Ctx& c) {
@@ -413,7 +411,7 @@ __device__ __noinline__ void op_lr_schedule(const Ctx& c) {
     double warm = (wu > 0 && t <= wu) ? (double)t / wu : 1.0;
     double prog = fmin(fmax((double)(t - wu) / (double)max(tot - wu, 1), 0.0), 1.0);
     double f = kind == 0 ? 1.0 : kind == 1 ? mr + (1.0 - mr) * 0.5 * (1.0 + cos(M_PI * prog)) : 1.0 - (1.0 - mr) * prog;
-    lr.f()[0] = (float)(base * warm * f);
+    stwt32(lr.f() + 0, (float)(base * warm * f));
   }
 }
 
@@ -437,7 +435,7 @@ template <class PF, class PI> __device__ int row_argmax(const View& lg, int r, i
 __device__ __noinline__ void op_argmax(const Ctx& c) {
   View lg = c.buf(0), out = c.buf(1); int r0 = c.i(2), r1 = c.i(3), V = c.i(4);
   __shared__ float rv[KVM_WAVES]; __shared__ int ri[KVM_WAVES];
-  for (int r = r0; r < r1; ++r) { int a = row_argmax(lg, r, V, rv, ri); if (tid() == 0) out.i()[r] = a; }
+  for (int r = r0; r < r1; ++r) { int a = row_argmax(lg, r, V, rv, ri); if (tid() == 0) stwt32i(out.i() + r, a); }
 }
 __device__ void philox10(uint32_t c[4], uint32_t k0, uint32_t k1) {
   for (int r = 0; r < 10; ++r) {
@@ -454,7 +452,7 @@ __device__ __noinline__ void op_sample(const Ctx& c) {
   __shared__ float rv[KVM_WAVES]; __shared__ int ri[KVM_WAVES]; __shared__ uint32_t s_thr;
   int cv = ctr.ok() ? ctr.i()[0] : 0;
   for (int r = r0; r < r1; ++r) {
-    if (temp <= 0.f) { int a = row_argmax(lg, r, V, rv, ri); if (tid() == 0) out.i()[r] = a; continue; }
+    if (temp <= 0.f) { int a = row_argmax(lg, r, V, rv, ri); if (tid() == 0) stwt32i(out.i() + r, a); continue; }
     if (tid() == 0) {
       uint32_t thr = 0;
       if (topk > 0 && topk < V) {   // k-th largest order key by bitwise binary search on the count of keys >= candidate
@@ -473,7 +471,7 @@ __device__ __noinline__ void op_sample(const Ctx& c) {
       uint32_t cc[4] = {(uint32_t)r, (uint32_t)cv, 0u, 0u}; philox10(cc, (uint32_t)seed, 0x9E3779B9u);
       double target = (double)(cc[0] >> 8) * (1.0 / 16777216.0) * total, run = 0.0; int pick = -1, last = -1;
       for (int j = 0; j < V; ++j) { float x = lg.at(r, j); if (x == x && order_key(x) >= thr) { run += exp((double)(x - mx) / temp); last = j; if (run > target) { pick = j; break; } } }
-      out.i()[r] = pick >= 0 ? pick : max(last, 0);
+      stwt32i(out.i() + r, pick >= 0 ? pick : max(last, 0));
     }
     __syncthreads();
   }

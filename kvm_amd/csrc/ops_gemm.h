@@ -93,7 +93,7 @@ __device__ __noinline__ void op_matmul_tile_silu_mul(const Ctx& c) {
     f32_block(c, A, B, fl & 1, fl & 2, bm, bn, M, N, K, e, false, t);
     for (int q = tid(); q < 64 * 64; q += KVM_THREADS) {
       int m = bm + q / 64, n = bn + q % 64;
-      if (m < M && n < N) { float u = t[q]; up.f()[(long long)m * up.cols + n] = u; out.f()[(long long)m * out.cols + n] = silu_f(gate.at(m, n)) * u; }
+      if (m < M && n < N) { float u = t[q]; stwt32(up.f() + ((long long)m * up.cols + n), u); stwt32(out.f() + ((long long)m * out.cols + n), silu_f(gate.at(m, n)) * u); }
     }
     __syncthreads();
   }
@@ -111,8 +111,8 @@ __device__ __noinline__ void op_matmul_tile_silu_mul_bwd(const Ctx& c) {
       int m = bm + q / 64, n = bn + q % 64;
       if (m < M && n < N) {
         float dh = t[q], g = gate.at(m, n);
-        dg.f()[(long long)m * dg.cols + n] = dh * (up.at(m, n) * silu_d_f(g));
-        du.f()[(long long)m * du.cols + n] = dh * silu_f(g);
+        stwt32(dg.f() + ((long long)m * dg.cols + n), dh * (up.at(m, n) * silu_d_f(g)));
+        stwt32(du.f() + ((long long)m * du.cols + n), dh * silu_f(g));
       }
     }
     __syncthreads();
@@ -297,8 +297,8 @@ __device__ __forceinline__ f32x4n ld4(const View& X, long long o) {
   return *(const GLOBAL f32x4n*)(X.f() + o);
 }
 __device__ __forceinline__ void st4(const View& X, long long o, f32x4n v) {
-  if (X.dtype == 2) *(GLOBAL u16x4_t*)(X.h() + o) = u16x4_t{f2bf(v.x), f2bf(v.y), f2bf(v.z), f2bf(v.w)};
-  else *(GLOBAL f32x4n*)(X.f() + o) = v;
+  if (X.dtype == 2) stwt_bf4(X.h() + o, v.x, v.y, v.z, v.w);
+  else stwt_f4(X.f() + o, v);
 }
 
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
@@ -392,8 +392,8 @@ __device__ __forceinline__ void epi_rows(const Ctx& c, const GemmArgs& g) {
         st4(e.pre, (long long)m * e.pre.cols + n, v);
         v.x = gelu_f(v.x); v.y = gelu_f(v.y); v.z = gelu_f(v.z); v.w = gelu_f(v.w);
       }
-      if constexpr (OBF) *(GLOBAL u16x4_t*)(e.out.h() + (long long)m * e.out.cols + n) = u16x4_t{f2bf(v.x), f2bf(v.y), f2bf(v.z), f2bf(v.w)};
-      else *(GLOBAL f32x4n*)(e.out.f() + (long long)m * e.out.cols + n) = v;
+      if constexpr (OBF) stwt_bf4(e.out.h() + (long long)m * e.out.cols + n, v.x, v.y, v.z, v.w);
+      else stwt_f4(e.out.f() + (long long)m * e.out.cols + n, v);
     }
   }
 #ifdef KVM_GEMM_PROF
@@ -456,8 +456,8 @@ __device__ __noinline__ void gemm_epilogue(const Ctx& c, int moff) {
           if (ge) { v.x = gelu_f(v.x); v.y = gelu_f(v.y); v.z = gelu_f(v.z); v.w = gelu_f(v.w); }
         }
         v += rv[u] + ov[u];
-        if constexpr (OBF) *(GLOBAL u16x4_t*)(e.out.h() + (long long)m * e.out.cols + n) = u16x4_t{f2bf(v.x), f2bf(v.y), f2bf(v.z), f2bf(v.w)};
-        else *(GLOBAL f32x4n*)(e.out.f() + (long long)m * e.out.cols + n) = v;
+        if constexpr (OBF) stwt_bf4(e.out.h() + (long long)m * e.out.cols + n, v.x, v.y, v.z, v.w);
+        else stwt_f4(e.out.f() + (long long)m * e.out.cols + n, v);
       } else if (n < g.N) {
         epi_tail(e, g.N, m, n, a);
       }

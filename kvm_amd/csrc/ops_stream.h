@@ -22,13 +22,11 @@ __device__ __forceinline__ void ld8(const View& X, long long o, float (&v)[8]) {
 }
 __device__ __forceinline__ void st8(const View& X, long long o, const float (&v)[8]) {
   if (X.dtype == 2) {
-    u16x8_t h;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = f2bf(v[i]);
-    *(GLOBAL u16x8_t*)(X.h() + o) = h;
+    stwt_bf4(X.h() + o, v[0], v[1], v[2], v[3]);
+    stwt_bf4(X.h() + o + 4, v[4], v[5], v[6], v[7]);
   } else {
-    *(GLOBAL f32x4n*)(X.f() + o) = f32x4n{v[0], v[1], v[2], v[3]};
-    *(GLOBAL f32x4n*)(X.f() + o + 4) = f32x4n{v[4], v[5], v[6], v[7]};
+    stwt_f4(X.f() + o, f32x4n{v[0], v[1], v[2], v[3]});
+    stwt_f4(X.f() + o + 4, f32x4n{v[4], v[5], v[6], v[7]});
   }
 }
 __device__ __forceinline__ bool vec8_ok(const View& X) { return X.dtype != 1 && (X.cols % 8) == 0; }
@@ -82,7 +80,7 @@ __device__ __noinline__ bool op_colsum_fast(const Ctx& c) {
     __syncthreads();
     if (tid() < W) {
       const float s = slot_total(part, tid());
-      out.f()[cb + tid()] = acc ? out.f()[cb + tid()] + s : s;
+      stwt32(out.f() + (cb + tid()), acc ? out.f()[cb + tid()] + s : s);
     }
   }
   return true;
@@ -113,8 +111,8 @@ __device__ __noinline__ bool op_norm_bwd_params_fast(const Ctx& c) {
     if (tid() < W) {
       const int j = cb + tid();
       const float sg = slot_total(part, tid());
-      dg.f()[j] = acc ? dg.f()[j] + sg : sg;
-      if (db.ok()) { const float sb = slot_total(part + 2048, tid()); db.f()[j] = acc ? db.f()[j] + sb : sb; }
+      stwt32(dg.f() + j, acc ? dg.f()[j] + sg : sg);
+      if (db.ok()) { const float sb = slot_total(part + 2048, tid()); stwt32(db.f() + j, acc ? db.f()[j] + sb : sb); }
     }
   }
   return true;
@@ -174,7 +172,7 @@ template <int NV, bool RMS> __device__ __noinline__ void norm_fwd_rows(const Vie
           o.z = (v[i].z - mu) * rs * gv[i][2] + bv[i][2]; o.w = (v[i].w - mu) * rs * gv[i][3] + bv[i][3];
           st4(out, (long long)r * out.cols + 4 * (lane() + 64 * i), o);
         }
-        if (lane() == 0) { rstd.f()[r] = rs; if (!RMS) mean.f()[r] = mu; }
+        if (lane() == 0) { stwt32(rstd.f() + r, rs); if (!RMS) stwt32(mean.f() + r, mu); }
       }
     }
   }
@@ -329,9 +327,9 @@ __device__ __noinline__ void ce_rows_block(const Ctx& c, const View& lg_, const 
           for (int i = 0; i < 8; ++i) s += __builtin_amdgcn_exp2f(bfl(v[u][i]) * LOG2E - ml2);
       s = block_reduce(red, s, [](float a, float b) { return a + b; });
       lse = (ml2 + log2f(s)) * LN2;
-      if (tid() == 0) { ls.f()[r] = lse; rl.f()[r] = lse - lg.at(r, t); }
+      if (tid() == 0) { stwt32(ls.f() + r, lse); stwt32(rl.f() + r, lse - lg.at(r, t)); }
     } else if (fwd) {
-      if (tid() == 0) { ls.f()[r] = 0.f; rl.f()[r] = 0.f; }
+      if (tid() == 0) { stwt32(ls.f() + r, 0.f); stwt32(rl.f() + r, 0.f); }
     } else {
       lse = ls.f()[r];
     }
@@ -371,7 +369,7 @@ __device__ __noinline__ bool ce_rows_fast(const Ctx& c, View lg, View tg, View r
     const long long base = (long long)r * lg.cols;
     float lse;
     if (fwd) {
-      if (ign) { if (lane() == 0) { rl.f()[r] = 0.f; ls.f()[r] = 0.f; } lse = 0.f; }
+      if (ign) { if (lane() == 0) { stwt32(rl.f() + r, 0.f); stwt32(ls.f() + r, 0.f); } lse = 0.f; }
       else {
         float m = -INFINITY, s = 0.f;            // log2 domain
         for (int j0 = lane(); j0 < nv; j0 += 64 * 4) {
@@ -398,7 +396,7 @@ __device__ __noinline__ bool ce_rows_fast(const Ctx& c, View lg, View tg, View r
           m = nm;
         }
         lse = (m + log2f(s)) * LN2;
-        if (lane() == 0) { ls.f()[r] = lse; rl.f()[r] = lse - lg.at(r, t); }
+        if (lane() == 0) { stwt32(ls.f() + r, lse); stwt32(rl.f() + r, lse - lg.at(r, t)); }
       }
     } else lse = ls.f()[r];
     if (bwd) {
@@ -430,7 +428,7 @@ __device__ __noinline__ bool op_round_bf16_fast(const Ctx& c) {
   const long long e0 = c.i(2), e1 = c.i(3);
   if (x.dtype == 1 || o.dtype == 1) return false;
   const long long a0 = min(e1, (e0 + 7) & ~7ll), a1 = max(a0, e1 & ~7ll);
-  auto one = [&](long long k) { const float v = x.ld(k); if (o.dtype == 2) o.h()[k] = f2bf(v); else o.f()[k] = x.dtype == 2 ? v : round_bf(v); };
+  auto one = [&](long long k) { const float v = x.ld(k); if (o.dtype == 2) stwt16(o.h() + k, f2bf(v)); else stwt32(o.f() + k, x.dtype == 2 ? v : round_bf(v)); };
   for (long long k = e0 + tid(); k < a0; k += KVM_THREADS) one(k);
   for (long long k = a1 + tid(); k < e1; k += KVM_THREADS) one(k);
   const long long n8 = (a1 - a0) / 8;
@@ -474,7 +472,7 @@ __device__ __noinline__ bool op_gradnorm_partial_fast(const Ctx& c) {
   }
   s += (t[0] + t[1]) + (t[2] + t[3]);
   s = block_sum_d(s, red);
-  if (tid() == 0) part.f()[c.i(2)] = (float)s;
+  if (tid() == 0) stwt32(part.f() + (c.i(2)), (float)s);
   return true;
 }
 
@@ -491,7 +489,7 @@ template <int NV> __device__ __noinline__ void delta_rows(const View& o, const V
       float s = (a[i].x * b[i].x + a[i].y * b[i].y) + (a[i].z * b[i].z + a[i].w * b[i].w);
       for (int x = 1; x < gl; x <<= 1) s += __shfl_xor(s, x, 64);
       const int col = 4 * (lane() + 64 * i);
-      if ((lane() & (gl - 1)) == 0) delta.f()[((long long)(r / T) * H + col / hd) * T + r % T] = s;
+      if ((lane() & (gl - 1)) == 0) stwt32(delta.f() + (((long long)(r / T) * H + col / hd) * T + r % T), s);
     }
   }
 }
@@ -575,7 +573,7 @@ __device__ __noinline__ bool op_embedding_bwd_fast(const Ctx& c) {
   LDS int* list = (LDS int*)c.smem;                 // [N] matching rows
   LDS int* wcnt = list + 16384;                      // [4]
   if (!acc)
-    for (long long e = tid(); e < (long long)(v1 - v0) * d; e += KVM_THREADS) dt.f()[(long long)(v0 + e / d) * dt.cols + e % d] = 0.f;
+    for (long long e = tid(); e < (long long)(v1 - v0) * d; e += KVM_THREADS) stwt32(dt.f() + ((long long)(v0 + e / d) * dt.cols + e % d), 0.f);
   int nm = 0;
   for (int s0 = 0; s0 < N; s0 += 16 * KVM_THREADS) {
     int key[16];
@@ -598,7 +596,7 @@ __device__ __noinline__ bool op_embedding_bwd_fast(const Ctx& c) {
   __syncthreads();
   for (int i = 0; i < nm; ++i) {
     const int r = list[i], k = ids.i()[r];
-    for (int col = tid(); col < d; col += KVM_THREADS) dt.f()[(long long)k * dt.cols + col] += dout.at(r, col);
+    for (int col = tid(); col < d; col += KVM_THREADS) stwt32(dt.f() + ((long long)k * dt.cols + col), dt.f()[(long long)k * dt.cols + col] + (dout.at(r, col)));
   }
   return true;
 }

@@ -117,6 +117,15 @@ __device__ __forceinline__ void stwt_f4(GLOBAL float* p, f32x4n v) {
 __device__ __forceinline__ void stwt_bf4(GLOBAL uint16_t* p, float a, float b, float c, float d) {
   stwt64(p, (uint64_t)f2bf(a) | ((uint64_t)f2bf(b) << 16) | ((uint64_t)f2bf(c) << 32) | ((uint64_t)f2bf(d) << 48));
 }
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+// 16-byte write-through stores through a buffer descriptor (cache policy SC1): one instruction, visible to the
+// compiler. The descriptor covers [base, base + bytes) with bytes < 2^31; offsets are bytes from base.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wt_rsrc(const void* base, long long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)(bytes < 0x7fffffffll ? bytes : 0x7fffffffll), 0x00020000);
+}
+__device__ __forceinline__ void stwt_buf(__amdgpu_buffer_rsrc_t r, int off, f32x4n v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, off, 0, 16 /* SC1 */);
+}
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---------------------------------------------------------------------------------------------- views

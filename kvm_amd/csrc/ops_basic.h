@@ -361,6 +361,10 @@ __device__ void adamw_body(const Ctx& c, View p, View g, View m, View v, View gs
   for (long long i = e0 + tid(); i < a0; i += KVM_THREADS) one(i);
   for (long long i = a1 + tid(); i < e1; i += KVM_THREADS) one(i);
   GLOBAL f32x4n* P = (GLOBAL f32x4n*)p.f(); const GLOBAL f32x4n* G = (const GLOBAL f32x4n*)g.f(); GLOBAL f32x4n* M = (GLOBAL f32x4n*)m.f(); GLOBAL f32x4n* Vv = (GLOBAL f32x4n*)v.f();
+  // 16-byte groups are stored through buffer descriptors (one write-through instruction each) when the ranges
+  // fit 32-bit byte offsets
+  const bool bo = (long long)e1 * 4 < 0x7fffffffll;
+  const __amdgpu_buffer_rsrc_t rp = wt_rsrc(p.p, 4ll * e1), rm = wt_rsrc(m.p, 4ll * e1), rv = wt_rsrc(v.p, 4ll * e1);
   auto upd = [&](long long q, f32x4n pp, f32x4n gg, f32x4n mm, f32x4n vv) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -368,7 +372,8 @@ __device__ void adamw_body(const Ctx& c, View p, View g, View m, View v, View gs
       adamw_elem(a, gg[j], b, d, gsc, b1, b2, lr, eps, wd, bc1, bc2);
       pp[j] = a; mm[j] = b; vv[j] = d;
     }
-    stwt_f4((GLOBAL float*)(P + q), pp); stwt_f4((GLOBAL float*)(M + q), mm); stwt_f4((GLOBAL float*)(Vv + q), vv);
+    if (bo) { stwt_buf(rp, (int)q * 16, pp); stwt_buf(rm, (int)q * 16, mm); stwt_buf(rv, (int)q * 16, vv); }
+    else { stwt_f4((GLOBAL float*)(P + q), pp); stwt_f4((GLOBAL float*)(M + q), mm); stwt_f4((GLOBAL float*)(Vv + q), vv); }
     if (shk == 2) {
       stwt_bf4(sh.h() + 4 * q, pp[0], pp[1], pp[2], pp[3]);
     } else if (shk == 1) {

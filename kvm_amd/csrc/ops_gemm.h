@@ -298,6 +298,7 @@ __device__ __forceinline__ f32x4n ld4(const View& X, long long o) {
 }
 __device__ __forceinline__ void st4(const View& X, long long o, f32x4n v) {
   if (X.dtype == 2) stwt_bf4(X.h() + o, v.x, v.y, v.z, v.w);
+  else if (X.n() * 4 < 0x7fffffffll) stwt_buf(wt_rsrc(X.p, X.n() * 4), (int)o * 4, v);
   else stwt_f4(X.f() + o, v);
 }
 
@@ -366,6 +367,7 @@ __device__ __forceinline__ void epi_rows(const Ctx& c, const GemmArgs& g) {
   const View& xv = KIND == 1 ? e.res : KIND == 2 ? e.out : e.pre;
   lx.init(xv, KIND >= 1 && KIND <= 3);
   const f32x4n bv = lb.get(n);
+  const __amdgpu_buffer_rsrc_t orsrc = wt_rsrc(e.out.p, (long long)g.M * e.out.cols * 4);   // f32 output rows (small: < 2^31 bytes)
   const int xc = xv.cols;
   for (int k0 = 0; k0 < NI; k0 += NB) {
     u32x4_t raw[NB];
@@ -393,7 +395,7 @@ __device__ __forceinline__ void epi_rows(const Ctx& c, const GemmArgs& g) {
         v.x = gelu_f(v.x); v.y = gelu_f(v.y); v.z = gelu_f(v.z); v.w = gelu_f(v.w);
       }
       if constexpr (OBF) stwt_bf4(e.out.h() + (long long)m * e.out.cols + n, v.x, v.y, v.z, v.w);
-      else stwt_f4(e.out.f() + (long long)m * e.out.cols + n, v);
+      else stwt_buf(orsrc, (m * e.out.cols + n) * 4, v);
     }
   }
 #ifdef KVM_GEMM_PROF
@@ -426,6 +428,7 @@ __device__ __noinline__ void gemm_epilogue(const Ctx& c, int moff) {
   Ld4 lb, lr, lp, lo;
   lb.init(e.bias); lr.init(e.res); lp.init(e.pre, dg); lo.init(e.out, e.accum != 0);
   const f32x4n bv = lb.get(n);
+  const __amdgpu_buffer_rsrc_t orsrc = wt_rsrc(e.out.p, (long long)g.M * e.out.cols * 4);   // f32 output rows (small: < 2^31 bytes)
 #ifdef KVM_GEMM_PROF
   KVM_PT(9);
 #endif
@@ -457,7 +460,7 @@ __device__ __noinline__ void gemm_epilogue(const Ctx& c, int moff) {
         }
         v += rv[u] + ov[u];
         if constexpr (OBF) stwt_bf4(e.out.h() + (long long)m * e.out.cols + n, v.x, v.y, v.z, v.w);
-        else stwt_f4(e.out.f() + (long long)m * e.out.cols + n, v);
+        else stwt_buf(orsrc, (m * e.out.cols + n) * 4, v);
       } else if (n < g.N) {
         epi_tail(e, g.N, m, n, a);
       }

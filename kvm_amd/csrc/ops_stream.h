@@ -22,8 +22,18 @@ __device__ __forceinline__ void ld8(const View& X, long long o, float (&v)[8]) {
 }
 __device__ __forceinline__ void st8(const View& X, long long o, const float (&v)[8]) {
   if (X.dtype == 2) {
-    stwt_bf4(X.h() + o, v[0], v[1], v[2], v[3]);
-    stwt_bf4(X.h() + o + 4, v[4], v[5], v[6], v[7]);
+    if (X.n() * 2 < 0x7fffffffll) {
+      const u32x4_t w = {(uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16), (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16),
+                         (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16), (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16)};
+      stwt_buf(wt_rsrc(X.p, X.n() * 2), (int)o * 2, __builtin_bit_cast(f32x4n, w));
+    } else {
+      stwt_bf4(X.h() + o, v[0], v[1], v[2], v[3]);
+      stwt_bf4(X.h() + o + 4, v[4], v[5], v[6], v[7]);
+    }
+  } else if (X.n() * 4 < 0x7fffffffll) {
+    const __amdgpu_buffer_rsrc_t r = wt_rsrc(X.p, X.n() * 4);
+    stwt_buf(r, (int)o * 4, f32x4n{v[0], v[1], v[2], v[3]});
+    stwt_buf(r, (int)o * 4 + 16, f32x4n{v[4], v[5], v[6], v[7]});
   } else {
     stwt_f4(X.f() + o, f32x4n{v[0], v[1], v[2], v[3]});
     stwt_f4(X.f() + o + 4, f32x4n{v[4], v[5], v[6], v[7]});

@@ -160,6 +160,7 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 127: op_softmax_ce_fused_any(c); break;
     case 134: op_gemv_bf16(c); break;
     case 135: op_attn_decode_part_any(c); break;
+    case 306: op_attn_decode_part_qkn(c); break;
     case 136: op_attn_decode_merge(c); break;
     case 300: op_head_rmsnorm(c); break;
     case 301: op_gemv_bf16_rows(c); break;

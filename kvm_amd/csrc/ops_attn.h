@@ -387,8 +387,9 @@ __device__ __forceinline__ float row16_sum(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
   return v;
 }
+// qkn (op 306): the query heads and the new key are RMS-normalised per head first (gamma args 18 / 19, eps arg 20).
 template <int G>
-__device__ __noinline__ void attn_decode_part_fast(const Ctx& c) {
+__device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) {
   const View q = uniform_view(c.buf(0)), kc = uniform_view(c.buf(1)), vc = uniform_view(c.buf(2)), lens = uniform_view(c.buf(3));
   const View part = uniform_view(c.buf(4)), kn = uniform_view(c.buf(5)), vn = uniform_view(c.buf(6));
   const int bb = c.i(7), kvh = c.i(8), s = c.i(9), S = c.i(10), H = c.i(11), Hkv = c.i(12), Tmax = c.i(14);
@@ -431,6 +432,22 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c) {
       for (int e = 0; e < 8; ++e) { qr[g][e] = q.ld(qo + d0 + e); qp[g][e] = q.ld(qo + (d0 ^ half) + e); }
     }
   }
+  if (qkn) {                                           // per-head RMSNorm: the 16 lanes of a DPP row hold one head's 128 dims
+    const View qg = uniform_view(c.buf(18));
+    const float eps = c.f(20);
+    float gq[8], gp[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { gq[e] = qg.f()[d0 + e]; gp[e] = qg.f()[(d0 ^ half) + e]; }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += qr[g][e] * qr[g][e];
+      const float rs = 1.f / sqrtf(row16_sum(ss) / (float)hd + eps);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { qr[g][e] = (qr[g][e] * rs) * gq[e]; qp[g][e] = (qp[g][e] * rs) * gp[e]; }
+    }
+  }
   // the rotation table (computed while the query loads are in flight)
   if (fl & 1) {
     if (tid() < half) { float sn, co; rope_sc_ref(L, tid(), hd, log((double)th), sn, co); rot[tid()] = sn; rot[half + tid()] = co; }
@@ -451,9 +468,16 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c) {
     }
   if ((fl & 1) && j0 <= n - 1 && n - 1 < j1) {          // this split holds the new key: store it (rotated) and its value
     const long long row = base + n - 1;
-    for (int i = tid(); i < half; i += KVM_THREADS) {
+    if (tid() < half) {                                  // wave 0: one lane per rotation pair
+      const int i = tid();
       const double sn = rot[i], co = rot[half + i];
-      const double x1 = kn.at(bb, kvh * hd + i), x2 = kn.at(bb, kvh * hd + i + half);
+      float k1 = kn.at(bb, kvh * hd + i), k2 = kn.at(bb, kvh * hd + i + half);
+      if (qkn) {
+        const View kg = uniform_view(c.buf(19));
+        const float rs = 1.f / sqrtf(wave_sum(k1 * k1 + k2 * k2) / (float)hd + c.f(20));
+        k1 = (k1 * rs) * kg.f()[i]; k2 = (k2 * rs) * kg.f()[i + half];
+      }
+      const double x1 = k1, x2 = k2;
       kc.st(row * kc.cols + i, (float)(x1 * co - x2 * sn)); kc.st(row * kc.cols + i + half, (float)(x1 * sn + x2 * co));
     }
     for (int k = tid(); k < hd; k += KVM_THREADS) vc.st(row * vc.cols + k, vn.at(bb, kvh * hd + k));
@@ -576,11 +600,19 @@ __device__ __noinline__ void op_attn_decode_part_any(const Ctx& c) {
   const View kc = c.buf(1), vc = c.buf(2);
   const int H = c.i(11), Hkv = c.i(12), hd = c.i(13), G = H / Hkv;
   const bool ok = kc.dtype == 2 && vc.dtype == 2 && hd == 128 && (kc.cols % 8) == 0 && (vc.cols % 8) == 0;
-  if (ok && G == 4) attn_decode_part_fast<4>(c);
-  else if (ok && G == 8) attn_decode_part_fast<8>(c);
-  else if (ok && G == 2) attn_decode_part_fast<2>(c);
-  else if (ok && G == 1) attn_decode_part_fast<1>(c);
+  if (ok && G == 4) attn_decode_part_fast<4>(c, false);
+  else if (ok && G == 8) attn_decode_part_fast<8>(c, false);
+  else if (ok && G == 2) attn_decode_part_fast<2>(c, false);
+  else if (ok && G == 1) attn_decode_part_fast<1>(c, false);
   else op_attn_decode_part(c);
+}
+// Op 306 (validated to the streaming path's shapes: hd 128, bf16 caches, G in {1, 2, 4, 8}).
+__device__ __noinline__ void op_attn_decode_part_qkn(const Ctx& c) {
+  const int G = c.i(11) / c.i(12);
+  if (G == 4) attn_decode_part_fast<4>(c, true);
+  else if (G == 8) attn_decode_part_fast<8>(c, true);
+  else if (G == 2) attn_decode_part_fast<2>(c, true);
+  else attn_decode_part_fast<1>(c, true);
 }
 
 // Merge of the splits (registry op 136): per head, the split weights e_s = exp(m_s - max m) (live splits only) are

@@ -39,7 +39,7 @@ static const OpSig* find_op(int id) { for (const OpSig& o : kRegistry) if (o.id 
 static bool implemented(int id) {
   static const int ids[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 32, 33, 34, 35, 36, 37, 38, 39, 40, 41, 42, 43, 44, 45, 46, 47, 48, 49, 50,
                             51, 52, 53, 54, 55, 56, 57, 58, 59, 60, 61, 62, 63, 96, 97, 98, 99, 100, 101, 102, 103, 104, 113, 114, 115,
-                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304, 305};
+                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304, 305, 306};
   for (int i : ids) if (i == id) return true;
   return false;
 }
@@ -100,6 +100,7 @@ static char arg_class(int op, const std::string& n) {
     case 116: return in({"step"}) ? 'i' : 'f';
     case 134: return in({"gamma"}) ? 'f' : 'a';
     case 135: return in({"lens"}) ? 'i' : in({"part"}) ? 'f' : 'a';
+    case 306: return in({"lens"}) ? 'i' : in({"part", "qgamma", "kgamma"}) ? 'f' : 'a';
     case 136: return in({"o"}) ? 'a' : 'f';
     case 300: return in({"x", "out"}) ? 'a' : 'f';
     case 301: return in({"gamma"}) ? 'f' : 'a';
@@ -229,6 +230,12 @@ static void extents(int op, Check& k) {
       if (pro == 2) k.need(k.B("x2") != nullptr, "pro 2 needs x2");
       const MvmBuf* w = k.B("w"); if (w) k.need(w->dtype == 2 && w->cols % 8 == 0, "w must be bf16 storage with cols % 8 == 0");
       break; }
+    case 306: { const MvmBuf* kc = k.B("kc"); const MvmBuf* vc = k.B("vc"); const int H = k.I("H"), Hkv = k.I("Hkv");
+      k.need(k.I("hd") == 128 && kc && vc && kc->dtype == 2 && vc->dtype == 2 && Hkv > 0 && H % Hkv == 0 &&
+             (H / Hkv == 1 || H / Hkv == 2 || H / Hkv == 4 || H / Hkv == 8) && (k.I("flags") == 1 || k.I("flags") == 3),
+             "needs hd 128, bf16 kc/vc, H/Hkv in {1,2,4,8} and flags 1 or 3");
+      k.extn("qgamma", 128); k.extn("kgamma", 128); }
+      [[fallthrough]];
     case 135: { int b = k.I("b"), kvh = k.I("kvh"), s = k.I("s"), S = k.I("S"), H = k.I("H"), Hkv = k.I("Hkv"), hd = k.I("hd"), Tm = k.I("Tmax"), fl = k.I("flags");
       k.need(b >= 0 && Hkv > 0 && H % Hkv == 0 && 0 <= kvh && kvh < Hkv && 0 <= s && s < S && Tm > 0, "bad b/kvh/s/S/H/Hkv/Tmax");
       k.need(0 < hd && hd <= 128 && hd % 8 == 0 && H / Hkv <= 8, "hd must be a multiple of 8 up to 128, H/Hkv <= 8");
@@ -282,6 +289,7 @@ static bool kvm_validate_bundle(const MvmTaskDesc* t, int n, const int32_t* succ
     if (!implemented(d.op_id)) return bad(i, std::string("operator ") + o->name + " is not run by this executor");
     std::vector<ArgInfo> sig = parse_sig(o->sig);
     if (d.args_words != (int)sig.size()) return bad(i, "args_words != arity of " + std::string(o->name));
+    if (d.args_words > KVM_MAX_ARGS) return bad(i, "more argument words than a task's LDS argument block holds");
     if (d.succ_off < 0 || d.succ_cnt < 0 || (long long)d.succ_off + d.succ_cnt > ne) return bad(i, "successor range outside the bundle");
     if (d.args_off < 0 || (long long)d.args_off + d.args_words > na) return bad(i, "argument range outside the bundle");
     if (d.indegree < 0) return bad(i, "negative indegree");

@@ -1,7 +1,7 @@
 """Qwen3-8B-shape greedy decode step as a task graph (no generator exists in the reference).
 
-One step: embed the previous token -> 36 x [RMSNorm -> q, k, v projections -> per-head q/k RMSNorm -> RoPE + KV append +
-split-context attention (attn_decode_part, flags 1) -> merge -> o projection + residual -> RMSNorm -> gate / up ->
+One step: embed the previous token -> 36 x [RMSNorm -> q, k, v projections -> per-head q/k RMSNorm + RoPE + KV append +
+split-context attention (attn_decode_part_qkn: the norm inside the attention tasks) -> merge -> o projection + residual -> RMSNorm -> gate / up ->
 SwiGLU -> down projection + residual] -> final RMSNorm -> untied LM head -> argmax -> the token buffer; then the cached
 length grows by one. Re-running the graph decodes the next token (the token buffer and lens carry over).
 
@@ -35,11 +35,14 @@ class Qwen3Config:
     seed: int = 1234
     splits: int = 0            # attention splits per (sequence, kv head); 0 = auto (256 part tasks)
     tasks_per_phase: int = 256
+    fused_norm: bool = True    # q / k head norm inside the attention tasks (op 306) where its shapes allow
 
     @staticmethod
     def tiny(batch=1, **kw):
-        return Qwen3Config(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000, ctx=37, batch=batch,
-                           max_new=4, tasks_per_phase=16, **kw)
+        base = dict(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=128, ffn=512, vocab=1000, ctx=37, batch=batch, max_new=4,
+                    tasks_per_phase=16)
+        base.update(kw)
+        return Qwen3Config(**base)
 
 
 def weight_elems(c: Qwen3Config) -> int:
@@ -102,6 +105,7 @@ def build(c: Qwen3Config) -> Workload:
         return ts
 
     P = c.tasks_per_phase
+    fused_norm = c.fused_norm and hd == 128 and H // Hkv in (1, 2, 4, 8)      # op 306's streaming-path shapes
     prev = [b.task('embedding_fwd', ids='tok', wte='wte', wpe=None, out='x', r0=0, r1=B, T=1, d=D)]
     last_parts = []
     for l in range(c.layers):
@@ -118,15 +122,18 @@ def build(c: Qwen3Config) -> Workload:
             tq = proj(prev, 'x', f'wq.{l}', 'q', nq, D, pq, pro=1, gamma=f'ln1.{l}')
             tk = proj(prev, 'x', f'wk.{l}', 'k', nkv, D, pk, pro=1, gamma=f'ln1.{l}')
             tv = proj(prev, 'x', f'wv.{l}', 'v', nkv, D, pk, pro=1, gamma=f'ln1.{l}')
-        hq = b.task('head_rmsnorm', after=tq, x='q', gamma=f'qn.{l}', out='q', r0=0, r1=B, H=H, hd=hd, eps=c.eps)
-        hk = b.task('head_rmsnorm', after=tk, x='k', gamma=f'kn.{l}', out='k', r0=0, r1=B, H=Hkv, hd=hd, eps=c.eps)
-        vj = b.join(tv, 2 * S)
+        kw = dict(q='q', kc=f'kc.{l}', vc=f'vc.{l}', lens='lens', part='part', knew='k', vnew='v', S=S, H=H, Hkv=Hkv, hd=hd, Tmax=Tmax,
+                  scale=1.0 / math.sqrt(hd), theta=c.theta, flags=1)
+        if fused_norm:   # q / k per-head RMSNorm inside the attention tasks (op 306 = op 300 on q and the new key, then op 135)
+            after, op = b.join(tq + tk + tv, B * Hkv * S), 'attn_decode_part_qkn'
+            kw.update(qgamma=f'qn.{l}', kgamma=f'kn.{l}', eps=c.eps)
+        else:
+            hq = b.task('head_rmsnorm', after=tq, x='q', gamma=f'qn.{l}', out='q', r0=0, r1=B, H=H, hd=hd, eps=c.eps)
+            hk = b.task('head_rmsnorm', after=tk, x='k', gamma=f'kn.{l}', out='k', r0=0, r1=B, H=Hkv, hd=hd, eps=c.eps)
+            after, op = [hq, hk, *b.join(tv, 2 * S)], 'attn_decode_part'
         parts = []
         for bb in range(B):
-            pb = [b.task('attn_decode_part', after=[hq, hk, *vj], q='q', kc=f'kc.{l}', vc=f'vc.{l}', lens='lens', part='part', knew='k',
-                         vnew='v', b=bb, kvh=kh, s=s, S=S, H=H, Hkv=Hkv, hd=hd, Tmax=Tmax, scale=1.0 / math.sqrt(hd), theta=c.theta,
-                         flags=1) for kh in range(Hkv) for s in range(S)]
-            parts.append(pb)
+            parts.append([b.task(op, after=after, b=bb, kvh=kh, s=s, **kw) for kh in range(Hkv) for s in range(S)])
         last_parts = [t for pb in parts for t in pb]
         merges = []
         for bb in range(B):

@@ -614,7 +614,15 @@ void rope_pair(double x1, double x2, long long p0, int i, int hd, float th, floa
   double s = f32(std::sin((double)ang)), co = f32(std::cos((double)ang));
   y1 = f32(x1 * co - x2 * s); y2 = f32(x1 * s + x2 * co);
 }
-void op_attn_decode_part(const Ctx& c) {   // ref_extra.py:441-479
+// Per-head RMSNorm of one head slice, as op_head_rmsnorm computes it: f32(f32(x * rs) * gamma), rs from a double sum.
+static void head_norm(std::vector<double>& x, const V& g, float eps) {
+  const int hd = (int)x.size();
+  double ss = 0; for (double v : x) ss += (double)f32(v) * f32(v);
+  const float rs = f32(1.0 / std::sqrt(ss / hd + eps));
+  for (int k = 0; k < hd; ++k) x[k] = f32((double)f32(f32(x[k]) * rs) * g.f[k]);
+}
+// attn_decode_part; with qg / kg (op 306) the query heads and the new key are head-normalised first.
+static void attn_decode_part_impl(const Ctx& c, V qg, V kg, float eps) {   // ref_extra.py:441-479
   V q = c.buf(0), kc = c.buf(1), vc = c.buf(2), lens = c.buf(3), part = c.buf(4), kn = c.buf(5, true), vn = c.buf(6, true);
   int bb = c.i(7), kvh = c.i(8), s = c.i(9), S = c.i(10), H = c.i(11), Hkv = c.i(12), hd = c.i(13), Tmax = c.i(14);
   float sc = c.fl(15), th = c.fl(16); int fl = c.i(17);
@@ -625,7 +633,10 @@ void op_attn_decode_part(const Ctx& c) {   // ref_extra.py:441-479
   int G = H / Hkv, half = hd / 2; long long base = ((long long)bb * Hkv + kvh) * Tmax, p0 = lens.i[bb];
   if ((fl & 1) && j0 <= n - 1 && n - 1 < j1) {
     long long row = (base + n - 1) * kc.cols;
-    for (int i = 0; i < half; ++i) { float y1, y2; rope_pair(kn.at(bb, kvh * hd + i), kn.at(bb, kvh * hd + i + half), p0, i, hd, th, y1, y2); kc.stf(row + i, y1); kc.stf(row + i + half, y2); }
+    std::vector<double> kv(hd);
+    for (int cc = 0; cc < hd; ++cc) kv[cc] = kn.at(bb, kvh * hd + cc);
+    if (kg.ok()) head_norm(kv, kg, eps);
+    for (int i = 0; i < half; ++i) { float y1, y2; rope_pair(kv[i], kv[i + half], p0, i, hd, th, y1, y2); kc.stf(row + i, y1); kc.stf(row + i + half, y2); }
     long long vrow = (base + n - 1) * vc.cols;
     for (int cc = 0; cc < hd; ++cc) vc.stf(vrow + cc, (float)vn.at(bb, kvh * hd + cc));
   }
@@ -633,6 +644,7 @@ void op_attn_decode_part(const Ctx& c) {   // ref_extra.py:441-479
   for (int g = 0; g < G; ++g) {
     int h = kvh * G + g;
     for (int cc = 0; cc < hd; ++cc) qv[cc] = q.at(bb, h * hd + cc);
+    if (qg.ok()) head_norm(qv, qg, eps);
     if (fl & 1) for (int i = 0; i < half; ++i) { float y1, y2; rope_pair(qv[i], qv[i + half], p0, i, hd, th, y1, y2);
       if (fl & 2) { y1 = bf16r(y1); y2 = bf16r(y2); } qv[i] = y1; qv[i + half] = y2; }
     long long row = (((long long)bb * S + s) * H + h) * part.cols;
@@ -644,6 +656,11 @@ void op_attn_decode_part(const Ctx& c) {   // ref_extra.py:441-479
     for (int j = 0; j < j1 - j0; ++j) l += p[j];
     part.f[row + hd] = f32(m); part.f[row + hd + 1] = f32(l);
   }
+}
+void op_attn_decode_part(const Ctx& c) { attn_decode_part_impl(c, V(), V(), 0.f); }
+void op_attn_decode_part_qkn(const Ctx& c) {   // this executor's op 306: op 135 after op 300's per-head norm of q and the new key
+  need(c.i(17) == 1 || c.i(17) == 3, "attn_decode_part_qkn: flags");
+  attn_decode_part_impl(c, c.buf(18), c.buf(19), c.fl(20));
 }
 void op_attn_decode_merge(const Ctx& c) {   // ref_extra.py:487-498
   V part = c.buf(0), o = c.buf(1); int bb = c.i(2), h0 = c.i(3), h1 = c.i(4), S = c.i(5), H = c.i(6), hd = c.i(7);
@@ -703,7 +720,7 @@ const OpEnt kOps[] = {
   {101, op_softmax_rows_bwd}, {102, op_gather_rows_scaled}, {103, op_scatter_add_rows}, {104, op_row_dot},
   {113, op_round_bf16}, {114, op_matmul_tile_bf16}, {122, op_matmul_mma_bf16}, {134, op_gemv_bf16},
   {135, op_attn_decode_part}, {136, op_attn_decode_merge}, {115, op_adamw_lr}, {116, op_lr_schedule}, {117, op_scale_flat},
-  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce}, {304, op_matmul_mma_bf16_256}, {305, op_adamw_bf16},
+  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce}, {304, op_matmul_mma_bf16_256}, {305, op_adamw_bf16}, {306, op_attn_decode_part_qkn},
 };
 OpFn find_op(int id) { for (const OpEnt& e : kOps) if (e.id == id) return e.fn; return nullptr; }
 

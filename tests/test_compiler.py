@@ -63,3 +63,14 @@ def test_bad_args_rejected():
         compiler.compile_spec(_spec([{'id': 'x', 'op': 'copy', 'args': {'src': 'a', 'dst': 'nope', 'n': 1}}]))
     with pytest.raises(compiler.CompileError):
         compiler.compile_spec(_spec([{'id': 'x', 'op': 'copy', 'args': {'src': 'a', 'n': 1}}]))
+
+
+def test_every_registry_op_fits_the_task_argument_block():
+    """A task's argument words are staged in a fixed LDS block of KVM_MAX_ARGS words; every registry operator's arity
+    must fit (an argument past the block would be read from whatever follows it)."""
+    import re
+    from conftest import REPO
+    cap = int(re.search(r'#define KVM_MAX_ARGS (\d+)', (REPO / 'kvm_amd/csrc/common.h').read_text()).group(1))
+    for f in sorted((REPO / 'include').glob('*.def')):
+        for m in re.finditer(r'X\((\w+),\s*(\d+),\s*"([^"]*)"', f.read_text()):
+            assert len(m.group(3).split(',')) <= cap, (f.name, m.group(1))

@@ -86,3 +86,32 @@ def test_attn_decode_parts(G, fl, S):
               for kh in range(Hkv) for s in range(S)]
         b.task('attn_decode_merge', after=ts, part='part', o='o', b=bb, h0=0, h1=H, S=S, H=H, hd=hd)
     _run(b, tol=1e-4)
+
+
+@pytest.mark.parametrize('G,fl,S,qdt', [(4, 1, 32, 'f32'), (4, 3, 3, 'f32'), (8, 1, 5, 'bf16'), (1, 3, 9, 'f32')])
+def test_attn_decode_parts_qkn(G, fl, S, qdt):
+    """Op 306: per-head RMSNorm of the query heads and of the new key inside the split-context attention task (the
+    Qwen3 q/k norm), against the oracle's op 300 + op 135 composition. eps 0.25 (comparable to the mean square of
+    the unit-scale inputs) so that a misread eps fails."""
+    print(f'attn_decode_part_qkn G {G} flags {fl} S {S} q {qdt}', flush=True)
+    B, Hkv, hd = 2, 2, 128
+    H = G * Hkv
+    lens = [700, 301]
+    Tmax = max(lens) + 1
+    b = Builder(37)
+    b.normal('q', B, H * hd, qdt, scale=1.0)
+    b.normal('kc', B * Hkv * Tmax, hd, 'bf16', scale=1.0)
+    b.normal('vc', B * Hkv * Tmax, hd, 'bf16', scale=1.0)
+    b.normal('kn', B, Hkv * hd, qdt, scale=1.0)
+    b.normal('vn', B, Hkv * hd, 'f32', scale=1.0)
+    b.normal('qg', 1, hd, 'f32', scale=1.0)
+    b.normal('kg', 1, hd, 'f32', scale=1.0)
+    b.values('lens', lens, B, 1, 'i32')
+    b.fill('part', B * S * H, hd + 2, 'f32')
+    b.fill('o', B, H * hd, 'f32')
+    for bb in range(B):
+        ts = [b.task('attn_decode_part_qkn', q='q', kc='kc', vc='vc', lens='lens', part='part', knew='kn', vnew='vn', b=bb, kvh=kh, s=s,
+                     S=S, H=H, Hkv=Hkv, hd=hd, Tmax=Tmax, scale=1.0 / hd ** 0.5, theta=1e6, flags=fl, qgamma='qg', kgamma='kg', eps=0.25)
+              for kh in range(Hkv) for s in range(S)]
+        b.task('attn_decode_merge', after=ts, part='part', o='o', b=bb, h0=0, h1=H, S=S, H=H, hd=hd)
+    _run(b, tol=1e-4)

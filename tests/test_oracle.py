@@ -159,6 +159,39 @@ def test_gpt_bf16_shadow_starts_as_rounded_master():
         assert np.array_equal(s.view(np.uint32), _rne_bf16(a).view(np.uint32)), name
 
 
+def test_attn_decode_part_qkn_is_head_norm_then_part():
+    """Op 306 equals op 300 on q and the new key followed by op 135 (bitwise), and differs from op 135 alone."""
+    H, Hkv, hd, L, S = 4, 2, 128, 37, 3
+    Tm = L + 2
+
+    def graph(fused):
+        w = W(41)
+        w.buf('q', 1, H * hd), w.buf('kn', 1, Hkv * hd), w.buf('vn', 1, Hkv * hd), w.buf('qg', hd), w.buf('kg', hd)
+        w.buf('kc', Hkv * Tm, hd), w.buf('vc', Hkv * Tm, hd), w.ints('lens', [L]), w.zeros('part', S * H, hd + 2)
+        w.zeros('qn', 1, H * hd), w.zeros('kn2', 1, Hkv * hd)
+        kw = dict(kc='kc', vc='vc', lens='lens', part='part', vnew='vn', b=0, S=S, H=H, Hkv=Hkv, hd=hd, Tmax=Tm,
+                  scale=1.0 / hd ** 0.5, theta=1e6, flags=1)
+        if fused == 'fused':
+            for kh in range(Hkv):
+                for s in range(S):
+                    w.task('attn_decode_part_qkn', q='q', knew='kn', kvh=kh, s=s, qgamma='qg', kgamma='kg', eps=1e-6, **kw)
+        else:
+            pre = []
+            if fused == 'composed':
+                pre = [w.task('head_rmsnorm', x='q', gamma='qg', out='qn', r0=0, r1=1, H=H, hd=hd, eps=1e-6),
+                       w.task('head_rmsnorm', x='kn', gamma='kg', out='kn2', r0=0, r1=1, H=Hkv, hd=hd, eps=1e-6)]
+            q, kn = ('qn', 'kn2') if fused == 'composed' else ('q', 'kn')
+            for kh in range(Hkv):
+                for s in range(S):
+                    w.task('attn_decode_part', after=pre, q=q, knew=kn, kvh=kh, s=s, **kw)
+        r, b = _run_one(w)
+        return _get(r, b, 'part'), _get(r, b, 'kc')
+    f, c, p = graph('fused'), graph('composed'), graph('plain')
+    assert np.array_equal(f[0].view(np.uint32), c[0].view(np.uint32))
+    assert np.array_equal(f[1].view(np.uint32), c[1].view(np.uint32))
+    assert not np.array_equal(f[0], p[0])
+
+
 def test_rope_inverse_and_head_rmsnorm():
     w = W(6)
     R, H, hd = 6, 2, 8

@@ -49,8 +49,10 @@ struct KvmQueue {
 };
 
 // Everything the persistent kernel reads. One task graph per launch (the submitted bundles concatenated).
+struct KvmRec;
 struct KvmDevState {
   const MvmTaskDesc* tasks;   // [ntasks]
+  const KvmRec* recs;         // [ntasks] dispatch records (descriptor, argument words, buffer views)
   const int32_t* succ;        // [nedges] global task indices
   const int32_t* args;        // [nargs]
   const MvmBuf* bufs;         // [nbufs]
@@ -141,6 +143,19 @@ struct View {
   __device__ void st(long long k, float v) const { if (dtype == 2) stwt16((GLOBAL uint16_t*)p + k, f2bf(v)); else stwt32((GLOBAL float*)p + k, v); }
   __device__ long long n() const { return (long long)rows * cols; }
 };
+
+// A task's dispatch record, built on the host when the graph is uploaded (buffers are fixed by then): the descriptor,
+// the argument words and, at every buffer argument's position, that buffer's view. A worker copies it to LDS with one
+// parallel 16-byte load per thread instead of three dependent fetches (descriptor, then arguments, then the buffer
+// table entries they name).
+struct KvmRec {
+  MvmTaskDesc desc;
+  int32_t args[KVM_MAX_ARGS];
+  View views[KVM_MAX_ARGS];
+  int32_t pad[8];
+};
+static_assert(sizeof(View) == 24 && sizeof(KvmRec) == 768, "record layout");
+#define KVM_REC_VEC (int)(sizeof(KvmRec) / 16)
 
 struct Ctx {
   const LDS View* views;     // buffer arguments of the task, resolved from the buffer table by the dispatcher (in LDS)

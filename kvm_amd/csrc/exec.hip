@@ -175,9 +175,8 @@ __device__ void dispatch(int op, const Ctx& c) {
 __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S) {
   __shared__ __attribute__((aligned(16))) char smem[KVM_LDS_BYTES];
   __shared__ int s_slot;
-  __shared__ int32_t s_args[KVM_MAX_ARGS];
-  __shared__ MvmTaskDesc s_desc;
-  __shared__ View s_view[KVM_MAX_ARGS];
+  __shared__ __attribute__((aligned(16))) KvmRec s_rec;
+  MvmTaskDesc& s_desc = s_rec.desc;
   const int t = threadIdx.x;
   for (;;) {
     if (t == 0) {
@@ -213,18 +212,9 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
     __syncthreads();
     const int slot = s_slot;
     if (slot < 0) break;
-    if (t < 16) ((int32_t*)&s_desc)[t] = ((const int32_t*)&S.tasks[slot])[t];
+    if (t < KVM_REC_VEC) ((LDS u32x4_t*)&s_rec)[t] = ((const u32x4_t*)(S.recs + slot))[t];   // the whole record, one load per thread
     __syncthreads();
     const int op = s_desc.op_id;
-    if (t < s_desc.args_words && t < KVM_MAX_ARGS) {
-      // argument words, and for buffer arguments the buffer's view, all fetched in one parallel round trip
-      const int w = S.args[s_desc.args_off + t];
-      s_args[t] = w;
-      if (w >= 0 && (unsigned)op < KVM_OPMASK_IDS && ((S.opmask[op] >> t) & 1u)) {
-        const MvmBuf& b = S.bufs[w];
-        s_view[t] = View{b.p, b.rows, b.cols, b.dtype};
-      }
-    }
     if (t == 0 && S.trace_on) {
       KvmTrace& tr = S.trace[slot];
       tr.start = wall_clock64();
@@ -243,7 +233,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
       }
     }
     __syncthreads();
-    Ctx c{(const LDS View*)s_view, (const LDS int32_t*)s_args, (LDS char*)smem, S.cnt, slot};
+    Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
     KVM_PT(6);
     dispatch(op, c);
     // Every operator stores through write-through (agent-scope) stores only, which tests/test_wt_stores.py checks
@@ -399,6 +389,7 @@ struct KvmExec {
   bool uploaded = false, launched = false;
   std::string err;
   // device memory
+  KvmRec* d_recs = nullptr;
   MvmTaskDesc* d_tasks = nullptr; int32_t *d_succ = nullptr, *d_args = nullptr; MvmBuf* d_bufs = nullptr;
   int *d_indeg = nullptr, *d_ready = nullptr, *d_state = nullptr, *d_park_next = nullptr, *d_version = nullptr, *d_park_head = nullptr;
   int *d_base = nullptr, *d_roots = nullptr, *d_root_cell = nullptr, *d_fixed_tail = nullptr;
@@ -451,7 +442,7 @@ void kvm_destroy(KvmExec* ex) {
   hipSetDevice(ex->dev);
   if (ex->stream) hipStreamSynchronize(ex->stream);
   for (auto& b : ex->bufs) hipFree(b.p);
-  void* ptrs[] = {ex->d_tasks, ex->d_succ, ex->d_args, ex->d_bufs, ex->d_indeg, ex->d_ready, ex->d_state, ex->d_park_next,
+  void* ptrs[] = {ex->d_recs, ex->d_tasks, ex->d_succ, ex->d_args, ex->d_bufs, ex->d_indeg, ex->d_ready, ex->d_state, ex->d_park_next,
                   ex->d_version, ex->d_park_head, ex->d_base, ex->d_roots, ex->d_cnt, ex->d_trace, ex->d_queues, ex->d_qcount,
                   ex->d_done_blk, ex->d_opmask, ex->d_root_cell, ex->d_fixed_tail};
   for (void* q : ptrs) if (q) hipFree(q);
@@ -577,6 +568,22 @@ static int do_upload(KvmExec* ex) {
     for (size_t k = 0; k < a.size() && k < 32; ++k) if (a[k].type == 0) opmask[o.id] |= 1u << k;
   }
   HIPCK(upload(&ex->d_opmask, opmask, ex->stream));
+  {   // dispatch records
+    std::vector<KvmRec> recs(n);
+    for (int i = 0; i < n; ++i) {
+      KvmRec& r = recs[i];
+      std::memset(&r, 0, sizeof(r));
+      const MvmTaskDesc& d = ex->tasks[i];
+      r.desc = d;
+      const unsigned mask = (unsigned)d.op_id < KVM_OPMASK_IDS ? opmask[d.op_id] : 0u;
+      for (int k = 0; k < d.args_words && k < KVM_MAX_ARGS; ++k) {
+        const int w = ex->args[d.args_off + k];
+        r.args[k] = w;
+        if (w >= 0 && ((mask >> k) & 1u)) r.views[k] = View{table[w].p, table[w].rows, table[w].cols, table[w].dtype};
+      }
+    }
+    HIPCK(upload(&ex->d_recs, recs, ex->stream));
+  }
   HIPCK(hipMalloc(&ex->d_indeg, n * sizeof(int)));
   const int nq = std::max(1, std::min(KVM_MAX_QUEUES, ex->grid));
   const int qcap = (n + nq - 1) / nq;
@@ -606,6 +613,7 @@ static int do_upload(KvmExec* ex) {
   HIPCK(hipMalloc(&ex->d_cnt, sizeof(KvmCounters)));
   if (ex->cfg.trace_on) HIPCK(hipMalloc(&ex->d_trace, n * sizeof(KvmTrace)));
   KvmDevState& S = ex->S;
+  S.recs = ex->d_recs;
   S.tasks = ex->d_tasks; S.succ = ex->d_succ; S.args = ex->d_args; S.bufs = ex->d_bufs;
   S.indeg = ex->d_indeg; S.ready = ex->d_ready; S.state = ex->d_state; S.park_next = ex->d_park_next;
   S.version = ex->d_version; S.park_head = ex->d_park_head; S.cnt = ex->d_cnt; S.trace = ex->d_trace;

@@ -424,6 +424,19 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) {
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int e = 0; e < 8; ++e) { qr[g][e] = bf2f(a[g][e]); qp[g][e] = bf2f(b2[g][e]); }
+  } else if (qv && q.dtype == 0) {                     // f32: four 16-byte loads per head, all issued before any use
+    f32x4n a[G][2], b2[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const long long qo = (long long)bb * q.cols + (long long)(kvh * G + g) * hd;
+      const GLOBAL f32x4n* pa = (const GLOBAL f32x4n*)(q.f() + qo + d0);
+      const GLOBAL f32x4n* pb = (const GLOBAL f32x4n*)(q.f() + qo + (d0 ^ half));
+      a[g][0] = pa[0]; a[g][1] = pa[1]; b2[g][0] = pb[0]; b2[g][1] = pb[1];
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { qr[g][e] = a[g][e >> 2][e & 3]; qp[g][e] = b2[g][e >> 2][e & 3]; }
   } else {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -436,8 +449,11 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) {
     const View qg = uniform_view(c.buf(18));
     const float eps = c.f(20);
     float gq[8], gp[8];
+    const GLOBAL f32x4n* ga = (const GLOBAL f32x4n*)(qg.f() + d0);        // gamma: f32, 128 values (validated)
+    const GLOBAL f32x4n* gb = (const GLOBAL f32x4n*)(qg.f() + (d0 ^ half));
+    const f32x4n g0 = ga[0], g1 = ga[1], p0 = gb[0], p1 = gb[1];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) { gq[e] = qg.f()[d0 + e]; gp[e] = qg.f()[(d0 ^ half) + e]; }
+    for (int e = 0; e < 4; ++e) { gq[e] = g0[e]; gq[e + 4] = g1[e]; gp[e] = p0[e]; gp[e + 4] = p1[e]; }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float ss = 0.f;

@@ -48,17 +48,56 @@ __device__ __forceinline__ bool off32_ok(const View& X) { return (long long)X.ro
 // Column sums over rows [0, R) for 64-column chunks: 8 lanes cover 64 columns of one row (8 columns each), so 32 row
 // slots run side by side; slot s takes rows s, s+32, ... (ascending, CR_UNROLL rows in flight) and the 32 slot partials
 // are added in slot order through LDS.
+// The CR_UNROLL rows of a step are loaded (at clamped row indices, no branch between the loads) before any is
+// used; rows past R then add nothing. The storage type is a template parameter, so there is no dtype test per row.
 constexpr int CR_UNROLL = 8;
-template <class Row> __device__ __forceinline__ void col_reduce(const Ctx& c, int R, int cb, int W, Row row, float (&a)[8], float (&b)[8]) {
-  const int vi = tid() & 7, slot = tid() >> 3;
+template <bool BF> __device__ __forceinline__ void ld8t(const View& X, long long o, float (&v)[8]) {
+  if constexpr (BF) {
+    const u16x8_t h = *(const GLOBAL u16x8_t*)(X.h() + o);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) a[i] = b[i] = 0.f;
-  if (vi * 8 >= W) return;
+    for (int i = 0; i < 8; ++i) v[i] = bf2f(h[i]);
+  } else {
+    const f32x4n a = *(const GLOBAL f32x4n*)(X.f() + o), b = *(const GLOBAL f32x4n*)(X.f() + o + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[i + 4] = b[i]; }
+  }
+}
+// Column sums of x over rows [0, R) at columns col .. col+7 for row slot `slot` (rows slot, slot+32, ...).
+template <bool BF> __device__ __forceinline__ void col_sum8(const View& x, int R, int col, int slot, float (&a)[8]) {
   for (int r0 = slot; r0 < R; r0 += 32 * CR_UNROLL) {
+    float v[CR_UNROLL][8];
+#pragma unroll
+    for (int u = 0; u < CR_UNROLL; ++u) ld8t<BF>(x, (long long)min(r0 + 32 * u, R - 1) * x.cols + col, v[u]);
 #pragma unroll
     for (int u = 0; u < CR_UNROLL; ++u) {
-      const int r = r0 + 32 * u;
-      if (r < R) row(r, cb + vi * 8, a, b);
+      const bool in = r0 + 32 * u < R;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] += in ? v[u][i] : 0.f;
+    }
+  }
+}
+// dgamma / dbeta partials: sum_r dy (x - mean_r) rstd_r and sum_r dy, same row order.
+template <bool BX, bool BY> __device__ __forceinline__ void col_norm8(const View& x, const View& dy, const View& mean, const View& rstd, int R,
+                                                                     int col, int slot, float (&sg)[8], float (&sb)[8]) {
+  const bool hm = mean.ok();
+  for (int r0 = slot; r0 < R; r0 += 32 * CR_UNROLL) {
+    float xv[CR_UNROLL][8], gv[CR_UNROLL][8], mu[CR_UNROLL], rs[CR_UNROLL];
+#pragma unroll
+    for (int u = 0; u < CR_UNROLL; ++u) {
+      const int r = min(r0 + 32 * u, R - 1);
+      ld8t<BX>(x, (long long)r * x.cols + col, xv[u]);
+      ld8t<BY>(dy, (long long)r * dy.cols + col, gv[u]);
+      mu[u] = hm ? mean.f()[r] : 0.f;
+      rs[u] = rstd.f()[r];
+    }
+#pragma unroll
+    for (int u = 0; u < CR_UNROLL; ++u) {
+      const bool in = r0 + 32 * u < R;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        sg[i] += in ? gv[u][i] * (xv[u][i] - mu[u]) * rs[u] : 0.f;
+        sb[i] += in ? gv[u][i] : 0.f;
+      }
     }
   }
 }
@@ -77,14 +116,10 @@ __device__ __noinline__ bool op_colsum_fast(const Ctx& c) {
   LDS float* part = (LDS float*)c.smem;
   for (int cb = c0; cb < c1; cb += 64) {
     const int W = min(64, c1 - cb);
-    float a[8], b[8];
-    col_reduce(c, R, cb, W, [&](int r, int col, float (&s)[8], float (&)[8]) {
-      float v[8]; ld8(x, (long long)r * x.cols + col, v);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s[i] += v[i];
-    }, a, b);
-    __syncthreads();
     const int vi = tid() & 7, slot = tid() >> 3;
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (vi * 8 < W) { if (x.dtype == 2) col_sum8<true>(x, R, cb + vi * 8, slot, a); else col_sum8<false>(x, R, cb + vi * 8, slot, a); }
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < 8; ++i) part[slot * 64 + vi * 8 + i] = a[i];
     __syncthreads();
@@ -104,17 +139,14 @@ __device__ __noinline__ bool op_norm_bwd_params_fast(const Ctx& c) {
   LDS float* part = (LDS float*)c.smem;
   for (int cb = c0; cb < c1; cb += 64) {
     const int W = min(64, c1 - cb);
-    float a[8], b[8];
-    col_reduce(c, R, cb, W, [&](int r, int col, float (&sg)[8], float (&sb)[8]) {
-      float xv[8], gv[8];
-      ld8(x, (long long)r * x.cols + col, xv);
-      ld8(dy, (long long)r * dy.cols + col, gv);
-      const float mu = mean.ok() ? mean.f()[r] : 0.f, rs = rstd.f()[r];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) { sg[i] += gv[i] * (xv[i] - mu) * rs; sb[i] += gv[i]; }
-    }, a, b);
-    __syncthreads();
     const int vi = tid() & 7, slot = tid() >> 3;
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, b[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (vi * 8 < W) {
+      const int col = cb + vi * 8;
+      if (x.dtype == 2) { if (dy.dtype == 2) col_norm8<true, true>(x, dy, mean, rstd, R, col, slot, a, b); else col_norm8<true, false>(x, dy, mean, rstd, R, col, slot, a, b); }
+      else { if (dy.dtype == 2) col_norm8<false, true>(x, dy, mean, rstd, R, col, slot, a, b); else col_norm8<false, false>(x, dy, mean, rstd, R, col, slot, a, b); }
+    }
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < 8; ++i) { part[slot * 64 + vi * 8 + i] = a[i]; part[2048 + slot * 64 + vi * 8 + i] = b[i]; }
     __syncthreads();

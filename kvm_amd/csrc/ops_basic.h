@@ -402,8 +402,19 @@ __device__ __noinline__ void op_gradnorm_partial(const Ctx& c) {
 }
 __device__ __noinline__ void op_gradnorm_finish(const Ctx& c) {
   View part = c.buf(0), out = c.buf(2); int ns = c.i(1); float mx = c.f(3);
+  // The partials are staged in LDS by all threads (one parallel load each), then added in index order in double by
+  // thread 0, the reference's order.
+  LDS float* st = (LDS float*)c.smem;
+  constexpr int CH = KVM_LDS_BYTES / 4;
+  double s = 0.0;
+  for (int b0 = 0; b0 < ns; b0 += CH) {
+    const int n = min(CH, ns - b0);
+    __syncthreads();
+    for (int i = tid(); i < n; i += KVM_THREADS) st[i] = part.f()[b0 + i];
+    __syncthreads();
+    if (tid() == 0) for (int i = 0; i < n; ++i) s += st[i];
+  }
   if (tid() == 0) {
-    double s = 0.0; for (int i = 0; i < ns; ++i) s += part.f()[i];
     float n = (float)sqrt(s);
     stwt32(out.f() + 0, mx > 0.f ? fminf(1.f, mx / (n + 1e-6f)) : 1.f);
     stwt32(out.f() + 1, n);

@@ -139,7 +139,7 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 63: op_gather_rows(c); break;
     case 96: op_act_fwd(c); break;
     case 97: op_act_bwd(c); break;
-    case 98: op_silu_mul_fwd(c); break;
+    case 98: if (!op_silu_mul_fwd_fast(c)) op_silu_mul_fwd(c); break;
     case 99: op_silu_mul_bwd(c); break;
     case 100: op_softmax_rows_fwd(c); break;
     case 101: op_softmax_rows_bwd(c); break;

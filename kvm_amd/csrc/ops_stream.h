@@ -44,6 +44,31 @@ __device__ __forceinline__ bool vec4_ok(const View& X) { return X.dtype != 1 && 
 // Within reach of 32-bit byte offsets (buffer loads).
 __device__ __forceinline__ bool off32_ok(const View& X) { return (long long)X.rows * X.cols * 4 < 0x7fffffffll; }
 
+// silu(gate) * up over [e0, e1) (registry op 104): groups of 8 elements, four groups in flight per thread.
+__device__ __noinline__ bool op_silu_mul_fwd_fast(const Ctx& c) {
+  const View g = c.buf(0), u = c.buf(1), o = c.buf(2);
+  const long long e0 = c.i(3), e1 = c.i(4);
+  if (!vec8_ok(g) || !vec8_ok(u) || !vec8_ok(o) || (e0 % 8) || (e1 % 8)) return false;
+  const long long n8 = (e1 - e0) / 8;
+  for (long long q0 = tid(); q0 < n8; q0 += 4 * KVM_THREADS) {
+    float gv[4][8], uv[4][8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const long long q = min(q0 + k * KVM_THREADS, n8 - 1);
+      ld8(g, e0 + 8 * q, gv[k]); ld8(u, e0 + 8 * q, uv[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (q0 + k * KVM_THREADS >= n8) break;
+      float r[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r[i] = silu_f(gv[k][i]) * uv[k][i];
+      st8(o, e0 + 8 * (q0 + k * KVM_THREADS), r);
+    }
+  }
+  return true;
+}
+
 // ---------------------------------------------------------------------------------------------- column reductions
 // Column sums over rows [0, R) for 64-column chunks: 8 lanes cover 64 columns of one row (8 columns each), so 32 row
 // slots run side by side; slot s takes rows s, s+32, ... (ascending, CR_UNROLL rows in flight) and the 32 slot partials

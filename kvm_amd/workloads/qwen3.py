@@ -55,7 +55,7 @@ def build(c: Qwen3Config) -> Workload:
     b = Builder(c.seed)
     B, D, H, Hkv, hd, F, V = c.batch, c.hidden, c.heads, c.kv_heads, c.head_dim, c.ffn, c.vocab
     Tmax = c.ctx + c.max_new
-    S = c.splits or max(1, 256 // (B * Hkv), -(-(c.ctx + 1) // 160))   # 256 part tasks (one round), <= 160 tokens each
+    S = c.splits or max(1, 256 // (B * Hkv))   # B * Hkv * S = 256 part tasks: one round of the workers
     rows_mode = B > 1
     # ---- buffers
     b.values('tok', [(7919 * (i + 1)) % V for i in range(B)], B, 1, 'i32')
@@ -145,7 +145,8 @@ def build(c: Qwen3Config) -> Workload:
             r2 = [b.task('rmsnorm_fwd', after=to, x='x', gamma=f'ln2.{l}', out='xn', rstd='rstd', r0=0, r1=B, d=D, eps=c.eps)]
             tg = proj(r2, 'xn', f'wg.{l}', 'g', F, D, P // 2)     # gate and up together: one round of P tasks
             tu = proj(r2, 'xn', f'wu.{l}', 'u', F, D, P // 2)
-            sm = [b.task('silu_mul_fwd', after=tg + tu, gate='g', up='u', out='h', e0=0, e1=B * F)]
+            sm = [b.task('silu_mul_fwd', after=tg + tu, gate='g', up='u', out='h', e0=lo * 8, e1=hi * 8)
+                  for lo, hi in split(B * F // 8, max(1, P // 8))]
             td = proj(sm, 'h', f'wd.{l}', 'x', D, F, P, res='x')
             prev = td if len(td) <= 256 else b.join(td, P)
         else:

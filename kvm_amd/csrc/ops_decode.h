@@ -221,12 +221,14 @@ __device__ __forceinline__ float gv_pro(int pro, float xv, float x2v, float gv, 
   return pro == 1 ? xv * rs * gv : pro == 2 ? silu_f(xv) * x2v : xv;
 }
 
-// K chunk staged in LDS at once: all of K when M rows of it fit in 64 KiB (then one chunk, one continuous weight
+// K chunk staged in LDS at once: all of K when M rows of it fit in GV_VS_MAX (then one chunk, one continuous weight
 // stream), else the largest of 4096 / 2048 / 1024 that divides K.
+// LDS left for the staged activations [M][KC + 8] next to the row statistics and the partial tiles.
+constexpr long long GV_VS_MAX = KVM_LDS_BYTES - 4ll * GV_GRP * 256 * 4 - 128;
 __device__ __forceinline__ int gv_kc(int K, int M) {
-  if ((long long)M * (K + 8) * 2 <= 65536) return K;
+  if ((long long)M * (K + 8) * 2 <= GV_VS_MAX) return K;
   for (int kc = 4096; kc >= 256; kc >>= 1)
-    if (K % kc == 0 && (long long)M * (kc + 8) * 2 <= 65536) return kc;
+    if (K % kc == 0 && (long long)M * (kc + 8) * 2 <= GV_VS_MAX) return kc;
   return 256;
 }
 

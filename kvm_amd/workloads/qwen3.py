@@ -7,8 +7,8 @@ length grows by one. Re-running the graph decodes the next token (the token buff
 
 Batch 1 uses the registry's one-row decode GEMV (gemv_bf16, RMSNorm / SwiGLU prologues fused) exactly as the
 reference's serving passes lay it out (reference: frontend/mvmfe/serve.py:243-315). Batch > 1 uses this executor's
-gemv_bf16_rows (op 301): the weights are streamed once for all sequences, with RMSNorm / SwiGLU as separate small
-tasks writing bf16 activations.
+gemv_bf16_rows (op 301): the weights are streamed once for all sequences, with the RMSNorm prologue fused (statistics
+per sequence) and SwiGLU as small streaming tasks writing bf16 activations.
 """
 from __future__ import annotations
 
@@ -113,11 +113,11 @@ def build(c: Qwen3Config) -> Workload:
         tot = nq + 2 * nkv
         pk = max(1, round(P * nkv / tot))
         pq = max(1, P - 2 * pk)                 # q, k, v together: one round of P tasks
-        if rows_mode:
-            prev = [b.task('rmsnorm_fwd', after=prev, x='x', gamma=f'ln1.{l}', out='xn', rstd='rstd', r0=0, r1=B, d=D, eps=c.eps)]
-            tq = proj(prev, 'xn', f'wq.{l}', 'q', nq, D, pq)
-            tk = proj(prev, 'xn', f'wk.{l}', 'k', nkv, D, pk)
-            tv = proj(prev, 'xn', f'wv.{l}', 'v', nkv, D, pk)
+        if rows_mode:   # the RMSNorm of every sequence is the GEMV's prologue (statistics per row, then the rows staged)
+            prev = b.join(prev, P)
+            tq = proj(prev, 'x', f'wq.{l}', 'q', nq, D, pq, pro=1, gamma=f'ln1.{l}')
+            tk = proj(prev, 'x', f'wk.{l}', 'k', nkv, D, pk, pro=1, gamma=f'ln1.{l}')
+            tv = proj(prev, 'x', f'wv.{l}', 'v', nkv, D, pk, pro=1, gamma=f'ln1.{l}')
         else:
             tq = proj(prev, 'x', f'wq.{l}', 'q', nq, D, pq, pro=1, gamma=f'ln1.{l}')
             tk = proj(prev, 'x', f'wk.{l}', 'k', nkv, D, pk, pro=1, gamma=f'ln1.{l}')
@@ -142,9 +142,9 @@ def build(c: Qwen3Config) -> Workload:
                 merges.append(b.task('attn_decode_merge', after=parts[bb], part='part', o='att', b=bb, h0=h0, h1=h1, S=S, H=H, hd=hd))
         to = proj(merges, 'att', f'wo.{l}', 'x', D, H * hd, P, res='x')
         if rows_mode:
-            r2 = [b.task('rmsnorm_fwd', after=to, x='x', gamma=f'ln2.{l}', out='xn', rstd='rstd', r0=0, r1=B, d=D, eps=c.eps)]
-            tg = proj(r2, 'xn', f'wg.{l}', 'g', F, D, P // 2)     # gate and up together: one round of P tasks
-            tu = proj(r2, 'xn', f'wu.{l}', 'u', F, D, P // 2)
+            oj = b.join(to, 2 * P)
+            tg = proj(oj, 'x', f'wg.{l}', 'g', F, D, P // 2, pro=1, gamma=f'ln2.{l}')     # gate and up: one round of P tasks
+            tu = proj(oj, 'x', f'wu.{l}', 'u', F, D, P // 2, pro=1, gamma=f'ln2.{l}')
             sm = [b.task('silu_mul_fwd', after=tg + tu, gate='g', up='u', out='h', e0=lo * 8, e1=hi * 8)
                   for lo, hi in split(B * F // 8, max(1, P // 8))]
             td = proj(sm, 'h', f'wd.{l}', 'x', D, F, P, res='x')

@@ -221,6 +221,65 @@ __device__ __forceinline__ float gv_pro(int pro, float xv, float x2v, float gv, 
   return pro == 1 ? xv * rs * gv : pro == 2 ? silu_f(xv) * x2v : xv;
 }
 
+// RMSNorm statistics of the M rows of x over all of K: each wave takes two rows at a time, and every load of a batch
+// (RU 16-byte vectors of each of the two rows per lane) is in flight before any is used.
+template <int RU> __device__ __forceinline__ void gv_rstd(const Ld4& lx, int xc, int M, int K, float eps, LDS float* rstd) {
+  const int l = lane(), wv = wave();
+  for (int m0 = wv; m0 < M; m0 += 2 * KVM_WAVES) {
+    const int mb = m0 + KVM_WAVES, mbc = mb < M ? mb : m0;
+    float sa = 0.f, sb = 0.f;
+    for (int k0 = 0; k0 < K; k0 += 256 * RU) {
+      f32x4n ta[RU], tb[RU];
+#pragma unroll
+      for (int u = 0; u < RU; ++u) {
+        const int kk = min(k0 + 4 * l + 256 * u, K - 4);
+        ta[u] = lx.get(m0 * xc + kk);
+        tb[u] = lx.get(mbc * xc + kk);
+      }
+#pragma unroll
+      for (int u = 0; u < RU; ++u)
+        if (k0 + 4 * l + 256 * u < K) {
+          sa += (ta[u].x * ta[u].x + ta[u].y * ta[u].y) + (ta[u].z * ta[u].z + ta[u].w * ta[u].w);
+          sb += (tb[u].x * tb[u].x + tb[u].y * tb[u].y) + (tb[u].z * tb[u].z + tb[u].w * tb[u].w);
+        }
+    }
+    sa = wave_sum(sa);
+    sb = wave_sum(sb);
+    if (l == 0) {
+      rstd[m0] = 1.f / sqrtf(sa / (float)K + eps);
+      if (mb < M) rstd[mb] = 1.f / sqrtf(sb / (float)K + eps);
+    }
+  }
+}
+// v = bf16(prologue(x)) for columns [kc, kc + kn) of the M rows: batches of SB vectors per thread, each batch's loads
+// (x, and x2 for the SwiGLU prologue or gamma for the RMSNorm one; nothing for an absent operand) issued first.
+template <int PRO, int SB>
+__device__ __forceinline__ void gv_stage(const Ld4& lx, const Ld4& la, int xc, int ac, int M, int kc, int kn, int VS, LDS uint16_t* vs,
+                                         const LDS float* rstd) {
+  const int q4 = kn / 4, nel = M * q4;
+  for (int e0 = tid(); e0 < nel; e0 += SB * KVM_THREADS) {
+    f32x4n xv[SB], av[SB];
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const int e = min(e0 + u * KVM_THREADS, nel - 1), m = e / q4, k = kc + 4 * (e % q4);
+      xv[u] = lx.get(m * xc + k);
+      if constexpr (PRO == 2) av[u] = la.get(m * ac + k);
+      else if constexpr (PRO == 1) av[u] = la.get(k);
+    }
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const int e = e0 + u * KVM_THREADS;
+      if (e < nel) {
+        const int m = e / q4, k = 4 * (e % q4);
+        const float rs = PRO == 1 ? rstd[m] : 0.f;
+        const f32x4n a = PRO != 0 ? av[u] : f32x4n{0.f, 0.f, 0.f, 0.f};
+        *(LDS u16x4_t*)(vs + m * VS + k) = u16x4_t{f2bf(gv_pro(PRO, xv[u].x, a.x, a.x, rs)), f2bf(gv_pro(PRO, xv[u].y, a.y, a.y, rs)),
+                                                  f2bf(gv_pro(PRO, xv[u].z, a.z, a.z, rs)), f2bf(gv_pro(PRO, xv[u].w, a.w, a.w, rs))};
+      }
+    }
+  }
+}
+
 // K chunk staged in LDS at once: all of K when M rows of it fit in GV_VS_MAX (then one chunk, one continuous weight
 // stream), else the largest of 4096 / 2048 / 1024 that divides K.
 // LDS left for the staged activations [M][KC + 8] next to the row statistics and the partial tiles.
@@ -288,47 +347,14 @@ __device__ __noinline__ void gemv_stream(const Ctx& c, int M, int pro, float eps
 #pragma unroll
       for (int j = 0; j < GV_RING; ++j) issue_next(wb[j][0], wb[j][1]);     // weights first: they do not wait for x
       if (!rstd_done) {                                                          // rstd of each row over all of K
-        for (int m = wv; m < M; m += KVM_WAVES) {
-          float ss = 0.f;
-          for (int k = 4 * l; k < K; k += 4 * 256) {
-            f32x4n t4[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) t4[u] = lx.get(m * x.cols + min(k + 256 * u, K - 4));
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-              if (k + 256 * u < K) ss += (t4[u].x * t4[u].x + t4[u].y * t4[u].y) + (t4[u].z * t4[u].z + t4[u].w * t4[u].w);
-          }
-          ss = wave_sum(ss);
-          if (l == 0) rstd[m] = 1.f / sqrtf(ss / (float)K + eps);
-        }
+        gv_rstd<8>(lx, x.cols, M, K, eps, rstd);
         rstd_done = true;
       }
       if (kc == 0) for (int e = l; e < ng * 256; e += 64) part[(wv * GV_GRP) * 256 + e] = 0.f;
       __syncthreads();                                                          // rstd ready; the previous chunk's readers are done
-      {                                                                          // v = bf16(prologue(x)) for this chunk
-        const int q4 = kn / 4, nel = M * q4;
-        for (int e0 = tid(); e0 < nel; e0 += GV_SB * KVM_THREADS) {
-          f32x4n xv[GV_SB], x2v[GV_SB], gg[GV_SB];
-#pragma unroll
-          for (int u = 0; u < GV_SB; ++u) {
-            const int e = min(e0 + u * KVM_THREADS, nel - 1), m = e / q4, k = kc + 4 * (e % q4);
-            xv[u] = lx.get(m * x.cols + k);                                      // absent views read as 0
-            x2v[u] = lx2.get(m * x2.cols + k);
-            gg[u] = lg.get(k);
-          }
-#pragma unroll
-          for (int u = 0; u < GV_SB; ++u) {
-            const int e = e0 + u * KVM_THREADS;
-            if (e < nel) {
-              const int m = e / q4, k = 4 * (e % q4);
-              const float rs = pro == 1 ? rstd[m] : 0.f;
-              const f32x4n a2 = pro == 2 ? x2v[u] : f32x4n{0.f, 0.f, 0.f, 0.f}, ga = pro == 1 ? gg[u] : f32x4n{0.f, 0.f, 0.f, 0.f};
-              *(LDS u16x4_t*)(vs + m * VS + k) = u16x4_t{f2bf(gv_pro(pro, xv[u].x, a2.x, ga.x, rs)), f2bf(gv_pro(pro, xv[u].y, a2.y, ga.y, rs)),
-                                                        f2bf(gv_pro(pro, xv[u].z, a2.z, ga.z, rs)), f2bf(gv_pro(pro, xv[u].w, a2.w, ga.w, rs))};
-            }
-          }
-        }
-      }
+      if (pro == 1) gv_stage<1, 8>(lx, lg, x.cols, 0, M, kc, kn, VS, vs, rstd);          // v = bf16(prologue(x)), this chunk
+      else if (pro == 2) gv_stage<2, 8>(lx, lx2, x.cols, x2.cols, M, kc, kn, VS, vs, rstd);
+      else gv_stage<0, 16>(lx, lx, x.cols, 0, M, kc, kn, VS, vs, rstd);
       __syncthreads();
 #ifdef KVM_GEMM_PROF
       if (g0 == 0) pt[1] = wall_clock64();

@@ -105,7 +105,7 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 8: op_matmul(c); break;
     case 9: op_fill(c); break;
     case 10: op_spin(c); break;
-    case 32: op_embedding_fwd(c); break;
+    case 32: if (!op_embedding_fwd_fast(c)) op_embedding_fwd(c); break;
     case 33: if (!op_embedding_bwd_fast(c)) op_embedding_bwd(c); break;
     case 34: op_matmul_tile(c); break;
     case 35: if (!op_norm_fwd_fast<false>(c)) op_norm_fwd<false>(c); break;

@@ -39,10 +39,74 @@ __device__ __forceinline__ void st8(const View& X, long long o, const float (&v)
     stwt_f4(X.f() + o + 4, f32x4n{v[4], v[5], v[6], v[7]});
   }
 }
+// ld8 with the storage type as a template parameter (no dtype test between a batch of loads).
+template <bool BF> __device__ __forceinline__ void ld8t(const View& X, long long o, float (&v)[8]) {
+  if constexpr (BF) {
+    const u16x8_t h = *(const GLOBAL u16x8_t*)(X.h() + o);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = bf2f(h[i]);
+  } else {
+    const f32x4n a = *(const GLOBAL f32x4n*)(X.f() + o), b = *(const GLOBAL f32x4n*)(X.f() + o + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[i + 4] = b[i]; }
+  }
+}
 __device__ __forceinline__ bool vec8_ok(const View& X) { return X.dtype != 1 && (X.cols % 8) == 0; }
 __device__ __forceinline__ bool vec4_ok(const View& X) { return X.dtype != 1 && (X.cols % 4) == 0; }
 // Within reach of 32-bit byte offsets (buffer loads).
 __device__ __forceinline__ bool off32_ok(const View& X) { return (long long)X.rows * X.cols * 4 < 0x7fffffffll; }
+
+// Embedding lookup (registry op 32): out[r] = wte[ids[r]] (+ wpe[r % T]), 8-column vectors, each wave's RPW rows
+// and both tables loaded before any is used; storage types as template parameters (no dtype test per vector).
+template <bool BW, bool BP, int NV>
+__device__ __forceinline__ void emb_rows(const Ctx& c, const View& ids, const View& wte, const View& wpe, const View& out, int r0, int r1, int T, int d) {
+  constexpr int RPW = NV == 1 ? 4 : NV == 2 ? 2 : 1;
+  const bool hp = wpe.ok();
+  for (int rb = r0 + wave() * RPW; rb < r1; rb += KVM_WAVES * RPW) {
+    int id[RPW];
+    float a[RPW][NV][8], b[RPW][NV][8];
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int r = min(rb + q, r1 - 1);
+      const int t = ids.i()[r];
+      id[q] = t;
+      const int tc = (t < 0 || t >= wte.rows) ? 0 : t;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int col = min(8 * (lane() + 64 * i), d - 8);
+        ld8t<BW>(wte, (long long)tc * wte.cols + col, a[q][i]);
+        if (hp) ld8t<BP>(wpe, (long long)(r % T) * wpe.cols + col, b[q][i]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int r = rb + q;
+      if (r >= r1) break;
+      const bool bad = id[q] < 0 || id[q] >= wte.rows;
+      if (bad && lane() == 0) c.fail(KVM_ERR_OP_TOKEN, r, id[q]);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int col = 8 * (lane() + 64 * i);
+        if (col >= d) break;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = bad ? 0.f : (hp ? a[q][i][e] + b[q][i][e] : a[q][i][e]);
+        st8(out, (long long)r * out.cols + col, v);
+      }
+    }
+  }
+}
+__device__ __noinline__ bool op_embedding_fwd_fast(const Ctx& c) {
+  const View ids = c.buf(0), wte = c.buf(1), wpe = c.buf(2), out = c.buf(3);
+  const int r0 = c.i(4), r1 = c.i(5), T = c.i(6), d = c.i(7);
+  if (d % 8 || d > 2048 || !vec8_ok(wte) || !vec8_ok(out) || (wpe.ok() && (!vec8_ok(wpe) || wpe.dtype != wte.dtype)) || T <= 0) return false;
+  const bool bw = wte.dtype == 2;
+  const int nv = (d + 511) / 512;
+  if (nv == 1) { if (bw) emb_rows<true, true, 1>(c, ids, wte, wpe, out, r0, r1, T, d); else emb_rows<false, false, 1>(c, ids, wte, wpe, out, r0, r1, T, d); }
+  else if (nv == 2) { if (bw) emb_rows<true, true, 2>(c, ids, wte, wpe, out, r0, r1, T, d); else emb_rows<false, false, 2>(c, ids, wte, wpe, out, r0, r1, T, d); }
+  else { if (bw) emb_rows<true, true, 4>(c, ids, wte, wpe, out, r0, r1, T, d); else emb_rows<false, false, 4>(c, ids, wte, wpe, out, r0, r1, T, d); }
+  return true;
+}
 
 // silu(gate) * up over [e0, e1) (registry op 104): groups of 8 elements, four groups in flight per thread.
 __device__ __noinline__ bool op_silu_mul_fwd_fast(const Ctx& c) {
@@ -76,17 +140,6 @@ __device__ __noinline__ bool op_silu_mul_fwd_fast(const Ctx& c) {
 // The CR_UNROLL rows of a step are loaded (at clamped row indices, no branch between the loads) before any is
 // used; rows past R then add nothing. The storage type is a template parameter, so there is no dtype test per row.
 constexpr int CR_UNROLL = 8;
-template <bool BF> __device__ __forceinline__ void ld8t(const View& X, long long o, float (&v)[8]) {
-  if constexpr (BF) {
-    const u16x8_t h = *(const GLOBAL u16x8_t*)(X.h() + o);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = bf2f(h[i]);
-  } else {
-    const f32x4n a = *(const GLOBAL f32x4n*)(X.f() + o), b = *(const GLOBAL f32x4n*)(X.f() + o + 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[i + 4] = b[i]; }
-  }
-}
 // Column sums of x over rows [0, R) at columns col .. col+7 for row slot `slot` (rows slot, slot+32, ...).
 template <bool BF> __device__ __forceinline__ void col_sum8(const View& x, int R, int col, int slot, float (&a)[8]) {
   for (int r0 = slot; r0 < R; r0 += 32 * CR_UNROLL) {

@@ -177,3 +177,19 @@ def test_adamw_bf16_shadow(sh_dt):
         b.task('adamw_bf16', p='p', g='g', m='m', v='v', gscale='gs', step='step', e0=e0, e1=e1, lr=3e-4, b1=0.9, b2=0.95,
                eps=1e-8, wd=0.1, sh='sh')
     _run(b)
+
+
+@pytest.mark.parametrize('tdt,odt,d,pos', [('f32', 'bf16', 768, True), ('f32', 'bf16', 256, False), ('f32', 'f32', 1024, True)])
+def test_embedding_fwd_rows(tdt, odt, d, pos):
+    """Op 32 (streaming form): token rows of wte (+ the position row), ragged row ranges, one and two vectors per lane."""
+    print(f'embedding_fwd table {tdt} out {odt} d {d} pos {pos}', flush=True)
+    b = Builder(43)
+    V, T, N = 997, 64, 203
+    b.values('ids', [(37 * i + 11) % V for i in range(N)], N, 1, 'i32')
+    b.normal('wte', V, d, tdt, scale=1.0)
+    if pos:
+        b.normal('wpe', T, d, tdt, scale=1.0)
+    b.fill('out', N, d, odt)
+    for r0, r1 in ((0, 5), (5, 77), (77, 203)):
+        b.task('embedding_fwd', ids='ids', wte='wte', wpe='wpe' if pos else None, out='out', r0=r0, r1=r1, T=T, d=d)
+    _run(b)

@@ -447,7 +447,16 @@ __device__ __noinline__ void ce_rows_block(const Ctx& c, const View& lg_, const 
           for (int i = 0; i < 8; ++i) s += __builtin_amdgcn_exp2f(bfl(v[u][i]) * LOG2E - ml2);
       s = block_reduce(red, s, [](float a, float b) { return a + b; });
       lse = (ml2 + log2f(s)) * LN2;
-      if (tid() == 0) { stwt32(ls.f() + r, lse); stwt32(rl.f() + r, lse - lg.at(r, t)); }
+      if (tid() == 0) stwt32(ls.f() + r, lse);
+      if (t8 == (t >> 3) % 256) {                    // the thread holding the target logit (element t % 8 of vector t / 8)
+        float xt = 0.f;
+#pragma unroll
+        for (int u = 0; u < NR; ++u)
+          if (u == (t >> 3) / 256)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) if (i == (t & 7)) xt = bfl(v[u][i]);
+        stwt32(rl.f() + r, lse - xt);
+      }
     } else if (fwd) {
       if (tid() == 0) { stwt32(ls.f() + r, 0.f); stwt32(rl.f() + r, 0.f); }
     } else {

@@ -14,6 +14,8 @@
 //     depend on the order of its terms, so the permutation is free.
 //   * O^T's accumulator has lane l owning query l % 32 again, so the online-softmax rescale is one multiply per
 //     register and the output store is 4 consecutive head-dim elements per lane.
+// Softmax exponentials are the hardware exp2 (v_exp_f32): every argument is <= 0 (a score minus the running max or the
+// row's log-sum-exp), where it differs from the library exp2f only by flushing results below 2^-126 to zero.
 // K/V (or Q/dO) blocks of 64 rows go from HBM straight into LDS (buffer_load ... lds), FA_NS stages deep. Each block
 // is kept in one of two swizzled layouts: "kc" for MFMA operands read along the head dim (ds_read_b128), "tr" for
 // operands read across rows (ds_read_b64_tr_b16); see ops_gemm.h for the transpose-read semantics.
@@ -135,7 +137,7 @@ template <int HD> __device__ __noinline__ void attn_fwd_mfma(const Ctx& c) {
         mloc = fmaxf(mloc, x);
       }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float mn = fmaxf(m, mloc), f = exp2f(m - mn);
+    const float mn = fmaxf(m, mloc), f = __builtin_amdgcn_exp2f(m - mn);
     float ps = 0.f;
     bf16x8 pf[2][2];
 #pragma unroll
@@ -144,7 +146,7 @@ template <int HD> __device__ __noinline__ void attn_fwd_mfma(const Ctx& c) {
       for (int t = 0; t < 2; ++t) {
         float pv[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { pv[i] = exp2f(s[sb][8 * t + i] - mn); ps += pv[i]; }
+        for (int i = 0; i < 8; ++i) { pv[i] = __builtin_amdgcn_exp2f(s[sb][8 * t + i] - mn); ps += pv[i]; }
         pf[sb][t] = pack_bf16(pv);
       }
     ps += __shfl_xor(ps, 32, 64);
@@ -233,7 +235,7 @@ template <int HD> __device__ __noinline__ void attn_dq_mfma(const Ctx& c) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int r = 8 * t + i, key = kb * FA_KB + sb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          const float pr = key > qrow ? 0.f : exp2f(sv[r] * sl2 - l2);
+          const float pr = key > qrow ? 0.f : __builtin_amdgcn_exp2f(sv[r] * sl2 - l2);
           d8[i] = pr * (dp[r] - di);
         }
         dsf[t] = pack_bf16(d8);
@@ -333,7 +335,7 @@ template <int HD> __device__ __noinline__ void attn_dkv_mfma(const Ctx& c) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int r = 8 * t + 4 * i4 + j, qq = qb * FA_KB + ql + j;
-            const float pr = qq < krow ? 0.f : exp2f(sv[r] * sl2 - lq[j] * 1.4426950408889634f);
+            const float pr = qq < krow ? 0.f : __builtin_amdgcn_exp2f(sv[r] * sl2 - lq[j] * 1.4426950408889634f);
             p8[4 * i4 + j] = pr;
             d8[4 * i4 + j] = pr * (dp[r] - eq[j]);
           }

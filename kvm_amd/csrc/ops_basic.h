@@ -43,12 +43,18 @@ __device__ __noinline__ void op_spin(const Ctx& c) {
 }
 
 // ---------------------------------------------------------------------------------------------- elementwise
+// tanh from the identity tanh(u) = sign(u) (1 - e) / (1 + e) with e = exp(-2|u|) = 2^(-2 log2(e) |u|), evaluated with
+// the hardware exp2 and reciprocal: absolute error a few 1e-8, no cancellation for large |u| (e -> 0).
+__device__ __forceinline__ float tanh_hw(float u) {
+  const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * fabsf(u));
+  return copysignf((1.f - e) * __builtin_amdgcn_rcpf(1.f + e), u);
+}
 __device__ __forceinline__ float gelu_f(float x) {
   float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.f + tanhf(u));
+  return 0.5f * x * (1.f + tanh_hw(u));
 }
 __device__ __forceinline__ float gelu_grad_f(float x) {
-  float t = tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x));
+  float t = tanh_hw(0.7978845608028654f * (x + 0.044715f * x * x * x));
   return 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * 0.7978845608028654f * (1.f + 3.f * 0.044715f * x * x);
 }
 __device__ __forceinline__ float sigmoid_f(float x) { return x >= 0.f ? 1.f / (1.f + __expf(-x)) : __expf(x) / (1.f + __expf(x)); }

@@ -25,7 +25,7 @@ from dataclasses import dataclass, asdict
 from . import Builder, Workload, split
 
 RB = 128   # row-block granularity of the dependency index
-CHUNK = 131072   # elements per optimizer / bf16-copy task (balances the step's tail)
+CHUNK = 49152    # elements per optimizer task (measured: 49152 balances the step's AdamW tail best of 32K-256K)
 
 
 @dataclass

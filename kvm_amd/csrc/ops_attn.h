@@ -387,6 +387,36 @@ __device__ __forceinline__ float row16_sum(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
   return v;
 }
+// Op 308: the 128 x 256 tile of op 122 (plain epilogue, bf16 output), then, from the tile still staged in LDS, the
+// attention backward statistic of its four 64-column heads: per row, each lane takes its 4 columns (bf16-rounded as
+// stored) times o, and the 16 lanes of a head (one DPP row) are summed.
+__device__ __noinline__ void op_matmul_mma_bf16_delta(const Ctx& c) {
+  mfma_tile<128, 256>(c);                                  // leaves the f32 tile staged in LDS (one 128 KiB half)
+  const GemmArgs g = gemm_args(c);
+  const View o = uniform_view(c.buf(13)), dl = uniform_view(c.buf(14));
+  const int T = rfl(c.i(15)), H = rfl(c.i(16));
+  constexpr int TN = 256, NB = 8;
+  const LDS float* et = (const LDS float*)c.smem;
+  const int ch = lane(), w = wave(), n = g.n0 + 4 * ch, head = n / 64;
+  Ld4 lo;
+  lo.init(o);
+  for (int r0 = w; r0 < 128; r0 += KVM_WAVES * NB) {
+    u32x4_t raw[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) raw[u] = lo.raw((g.m0 + r0 + KVM_WAVES * u) * o.cols + n);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int r = r0 + KVM_WAVES * u, m = g.m0 + r;
+      const f32x4n a = *(const LDS f32x4n*)(et + r * TN + 4 * (ch ^ epi_swz<TN>(r)));
+      const f32x4n ov = lo.cvt(raw[u]);
+      float p = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p += round_bf(a[e] * g.e.alpha) * ov[e];
+      p = row16_sum(p);
+      if ((ch & 15) == 0) stwt32(dl.f() + (((long long)(m / T) * H + head) * T + m % T), p);
+    }
+  }
+}
 // qkn (op 306): the query heads and the new key are RMS-normalised per head first (gamma args 18 / 19, eps arg 20).
 template <int G>
 __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) {

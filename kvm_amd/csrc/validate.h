@@ -39,7 +39,7 @@ static const OpSig* find_op(int id) { for (const OpSig& o : kRegistry) if (o.id 
 static bool implemented(int id) {
   static const int ids[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 32, 33, 34, 35, 36, 37, 38, 39, 40, 41, 42, 43, 44, 45, 46, 47, 48, 49, 50,
                             51, 52, 53, 54, 55, 56, 57, 58, 59, 60, 61, 62, 63, 96, 97, 98, 99, 100, 101, 102, 103, 104, 113, 114, 115,
-                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304, 305, 306};
+                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304, 305, 306, 308};
   for (int i : ids) if (i == id) return true;
   return false;
 }
@@ -97,6 +97,7 @@ static char arg_class(int op, const std::string& n) {
     case 98: return 'a';
     case 113: return 'a';
     case 114: case 122: case 304: return in({"bias"}) ? 'f' : 'a';
+    case 308: return in({"bias", "delta"}) ? 'f' : 'a';
     case 116: return in({"step"}) ? 'i' : 'f';
     case 134: return in({"gamma"}) ? 'f' : 'a';
     case 135: return in({"lens"}) ? 'i' : in({"part"}) ? 'f' : 'a';
@@ -133,6 +134,16 @@ static void extents(int op, Check& k) {
     case 33: { int N = k.I("N"), v0 = k.I("v0"), v1 = k.I("v1"), d = k.I("d"); k.need(N >= 0 && 0 <= v0 && v0 <= v1 && d > 0, "bad N/v0/v1/d");
       k.need(k.B("ids") || k.I("mod") > 0, "ids absent needs mod > 0");
       k.extn("ids", N); k.ext("dout", N, d); k.ext("dtab", v1, d); break; }
+    case 308: { const int M = k.I("M"), N = k.I("N"), K = k.I("K"), m0 = k.I("m0"), n0 = k.I("n0"), T = k.I("T"), H = k.I("H");
+      k.need(M > 0 && N > 0 && K > 0 && M % 128 == 0 && N % 256 == 0 && m0 % 128 == 0 && n0 % 256 == 0 && m0 < M && n0 < N,
+             "needs whole 128 x 256 tiles (M % 128, N % 256, m0, n0 on tile boundaries)");
+      k.need((k.I("flags") & ~3) == 0 && !k.B("bias") && !k.B("res") && !k.B("pre"), "plain epilogue only (flags 1 / 2, no bias, res, pre)");
+      k.need(k.I("hd") == 64 && T > 0 && H > 0 && N == H * 64, "needs 64-column heads covering N");
+      const MvmBuf* ob = k.B("out"); const MvmBuf* o = k.B("o");
+      k.need(ob && o && ob->dtype == 2 && o->dtype == 2 && o->cols % 8 == 0, "out and o must be bf16 storage");
+      const int fl = k.I("flags");
+      k.ext("a", fl & 1 ? K : M, fl & 1 ? M : K); k.ext("b", fl & 2 ? N : K, fl & 2 ? K : N); k.ext("out", M, N); k.ext("o", M, N);
+      k.extn("delta", (long long)((M - 1) / T + 1) * H * T); break; }
     case 34: case 114: case 122: case 304: {
       int M = k.I("M"), N = k.I("N"), K = k.I("K"), fl = k.I("flags"), m0 = k.I("m0"), n0 = k.I("n0");
       k.need(M > 0 && N > 0 && K > 0 && 0 <= m0 && m0 < M && 0 <= n0 && n0 < N, "bad M/N/K/m0/n0");

@@ -247,6 +247,25 @@ class GPTBuilder:
                                     flags=fl, alpha=alpha))
         return ts
 
+    def gemm_delta(self, A, B, out, M, N, K, flags, o, delta, T, H):
+        """The dO GEMM as op 308 tiles (128 x 256, plain epilogue): each also writes delta = rowsum(o * dO) for the four
+        64-column heads it covers, in place of separate delta tasks. Returns False when the shapes do not allow it."""
+        if not (self.bf and M % 128 == 0 and N % 256 == 0 and N == H * 64 and T % 128 == 0 and flags & ~3 == 0
+                and -(-M // 256) * -(-N // 256) < self.TILES_256 and (M // 128) * (N // 256) >= self.TILES_MMA):
+            return False
+        ta, tb = flags & 1, flags & 2
+        for m0 in range(0, M, 128):
+            m1 = m0 + 128
+            bi, t0 = m0 // T, m0 % T
+            for n0 in range(0, N, 256):
+                n1 = n0 + 256
+                reads = [(A, (0, K, m0, m1) if ta else (m0, m1, 0, K)), (B, (n0, n1, 0, K) if tb else (0, K, n0, n1)), (o, (m0, m1, n0, n1))]
+                writes = [(out, (m0, m1, n0, n1))] + [(delta, ((bi * H + h) * T + t0, (bi * H + h) * T + t0 + 128))
+                                                       for h in range(n0 // 64, n1 // 64)]
+                self.task('matmul_mma_bf16_delta', reads, writes, a=A, b=B, out=out, bias=None, res=None, pre=None, m0=m0, n0=n0, M=M, N=N,
+                          K=K, flags=flags, alpha=1.0, o=o, delta=delta, T=T, H=H, hd=64)
+        return True
+
     SPLITK_MIN = 16384   # K from which a GEMM with few output tiles is split along K (the tied head's input gradient)
 
     def gemm_splitk(self, A, B, out, M, N, K, flags, S):
@@ -392,10 +411,12 @@ class GPTBuilder:
             self.copy_rows(dxo, dm)                                                             # residual path
             self.layernorm_bwd(f'xm.{l}', f'dh.{l}', f'ln2g.{l}', f'mu2.{l}', f'rs2.{l}', dm, f'd.ln2g.{l}', f'd.ln2b.{l}', acc=1)
             # projection: xm = o @ wo^T + bo + x
-            self.gemm(dm, self.w(f'wo.{l}'), f'do.{l}', N, d, d, flags=0)
+            fused_delta = self.gemm_delta(dm, self.w(f'wo.{l}'), f'do.{l}', N, d, d, 0, f'o.{l}', f'delta.{l}', T, H)
+            if not fused_delta:
+                self.gemm(dm, self.w(f'wo.{l}'), f'do.{l}', N, d, d, flags=0)
             self.gemm(dm, f'o.{l}', f'd.wo.{l}', d, d, N, flags=1)
             self.colsum(dm, f'd.bo.{l}', N, d)
-            self.attention_bwd(l)
+            self.attention_bwd(l, delta_done=fused_delta)
             # q, k, v: dh1 = dq wq + dk wk + dv wv (per tile: overwrite, then accumulate twice); LN1 input grad into dx.l
             dh1 = f'dh.{l}'
             self.gemm(f'dq.{l}', self.w(f'wq.{l}'), dh1, N, d, d, flags=0)
@@ -454,13 +475,13 @@ class GPTBuilder:
         for c0, c1 in split(C, max(1, C // 64)):
             self.task('colsum', [(x, (0, R, c0, c1))], [(out, (0, 1, c0, c1))], x=x, out=out, R=R, c0=c0, c1=c1, acc=0)
 
-    def attention_bwd(self, l):
+    def attention_bwd(self, l, delta_done=False):
         c = self.c
         N, d, H, T = c.batch * c.T, c.d, c.heads, c.T
         hd = d // H
         scale = 1.0 / math.sqrt(hd)
         o, q, k, v, lse, delta = f'o.{l}', f'q.{l}', f'k.{l}', f'v.{l}', f'lse.{l}', f'delta.{l}'
-        for r0, r1 in self.rows(N):
+        for r0, r1 in ([] if delta_done else self.rows(N)):
             # delta is [B*H*T] at (b*H + h)*T + t: rows [r0, r1) write one range per (batch, head), so delta tasks of
             # different row blocks stay independent
             dr = []

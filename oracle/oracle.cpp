@@ -541,6 +541,16 @@ void op_matmul_mma_bf16_kr(const Ctx& c) {
     }
 }
 // This executor's op 303: out[r, c] = sum over s in order of part[s*M + r, c].
+void op_matmul_mma_bf16_delta(const Ctx& c) {   // this executor's op 308: op 122's tile, then op 46 over the tile's rows and heads
+  op_matmul_mma_bf16(c);
+  V out = c.buf(2), o = c.buf(13), dl = c.buf(14);
+  const int m0 = c.i(6), n0 = c.i(7), M = c.i(8), N = c.i(9), T = c.i(15), H = c.i(16), hd = c.i(17);
+  for (int m = m0; m < std::min(m0 + 128, M); ++m)
+    for (int h = n0 / hd; h < std::min(n0 + 256, N) / hd; ++h) {
+      double a = 0; for (int cc = 0; cc < hd; ++cc) a += o.at(m, h * hd + cc) * out.at(m, h * hd + cc);
+      dl.f[((long long)(m / T) * H + h) * T + m % T] = f32(a);
+    }
+}
 void op_splitk_reduce(const Ctx& c) {
   V part = c.buf(0), out = c.buf(1); int M = c.i(2), N = c.i(3), S = c.i(4), r0 = c.i(5), r1 = c.i(6);
   need(M > 0 && N > 0 && S > 0 && 0 <= r0 && r0 <= r1 && r1 <= M, "splitk_reduce: args");
@@ -720,7 +730,7 @@ const OpEnt kOps[] = {
   {101, op_softmax_rows_bwd}, {102, op_gather_rows_scaled}, {103, op_scatter_add_rows}, {104, op_row_dot},
   {113, op_round_bf16}, {114, op_matmul_tile_bf16}, {122, op_matmul_mma_bf16}, {134, op_gemv_bf16},
   {135, op_attn_decode_part}, {136, op_attn_decode_merge}, {115, op_adamw_lr}, {116, op_lr_schedule}, {117, op_scale_flat},
-  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce}, {304, op_matmul_mma_bf16_256}, {305, op_adamw_bf16}, {306, op_attn_decode_part_qkn},
+  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce}, {304, op_matmul_mma_bf16_256}, {305, op_adamw_bf16}, {306, op_attn_decode_part_qkn}, {308, op_matmul_mma_bf16_delta},
 };
 OpFn find_op(int id) { for (const OpEnt& e : kOps) if (e.id == id) return e.fn; return nullptr; }
 

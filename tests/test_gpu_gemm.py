@@ -151,3 +151,22 @@ def test_mma256_partial_tiles():
     """Partial tiles and K off the slab: two 128x256 register-path tiles."""
     print('mma256 partial tiles', flush=True)
     _check(_gemm_graph(300, 400, 100, 1, op='matmul_mma_bf16_256', tiles=(256, 256), bias=True))
+
+
+@pytest.mark.parametrize('flags', [0, 2])
+def test_mma_delta_tiles(flags):
+    """Op 308: op 122's 128x256 tiles (plain epilogue) that also write the attention-backward statistic
+    delta = rowsum(o * out) of each 64-column head, two sequences of T = 256 rows."""
+    print(f'mma delta flags {flags}', flush=True)
+    M, N, K, T, H = 512, 512, 192, 256, 8
+    b = Builder(9)
+    b.normal('A', M, K, 'bf16', scale=1.0)
+    b.normal('B', N if flags & 2 else K, K if flags & 2 else N, 'bf16', scale=1.0)
+    b.normal('O', M, N, 'bf16', scale=1.0)
+    b.fill('C', M, N, 'bf16')
+    b.fill('D', (M // T) * H * T)
+    for m0 in range(0, M, 128):
+        for n0 in range(0, N, 256):
+            b.task('matmul_mma_bf16_delta', a='A', b='B', out='C', bias=None, res=None, pre=None, m0=m0, n0=n0, M=M, N=N, K=K,
+                   flags=flags, alpha=0.5, o='O', delta='D', T=T, H=H, hd=64)
+    _check(Workload(b.spec(), b.init_override))

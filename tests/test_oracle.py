@@ -252,3 +252,24 @@ def test_splitk_closed_form(flags):
     got = _get(r, b, 'C').reshape(M, N).astype(np.float64)
     assert np.abs(got - full).max() < 2 ** -7 * np.abs(full).max()
     assert np.array_equal(got, bl.bf16_round((P[0] + P[1] + P[2]).astype(np.float32)).astype(np.float64))
+
+
+def test_mma_delta_is_tile_then_delta():
+    """Op 308 equals op 122 on the tile followed by op 46 over the tile's rows and heads, bit for bit."""
+    M, N, K, T, H = 128, 256, 64, 64, 4
+
+    def graph(fused):
+        w = W(47)
+        w.buf('A', M, K, 'bf16'), w.buf('B', K, N, 'bf16'), w.buf('O', M, N, 'bf16'), w.zeros('C', M, N, 'bf16'), w.zeros('D', (M // T) * H * T)
+        kw = dict(a='A', b='B', out='C', bias=None, res=None, pre=None, m0=0, n0=0, M=M, N=N, K=K, flags=0, alpha=1.0)
+        if fused:
+            w.task('matmul_mma_bf16_delta', o='O', delta='D', T=T, H=H, hd=64, **kw)
+        else:
+            t = w.task('matmul_mma_bf16', **kw)
+            w.task('attn_bwd_delta', after=[t], o='O', do='C', delta='D', r0=0, r1=M, T=T, H=H, hd=64)
+        r, b = _run_one(w)
+        return _get(r, b, 'C'), _get(r, b, 'D')
+    f, u = graph(True), graph(False)
+    assert np.array_equal(f[0].view(np.uint32), u[0].view(np.uint32))
+    assert np.array_equal(f[1].view(np.uint32), u[1].view(np.uint32))
+    assert np.abs(f[1]).max() > 0

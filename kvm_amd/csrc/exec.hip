@@ -162,6 +162,7 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 135: op_attn_decode_part_any(c); break;
     case 306: op_attn_decode_part_qkn(c); break;
     case 308: op_matmul_mma_bf16_delta(c); break;
+    case 309: if (!op_norm_bwd_dx_res_fast(c)) op_norm_bwd_dx_res(c); break;
     case 136: op_attn_decode_merge(c); break;
     case 300: op_head_rmsnorm(c); break;
     case 301: op_gemv_bf16_rows(c); break;

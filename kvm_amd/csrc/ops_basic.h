@@ -206,6 +206,20 @@ template <bool RMS> __device__ __noinline__ void op_norm_fwd(const Ctx& c) {
     if (lane() == 0) { stwt32(rstd.f() + r, rs); if (!RMS) stwt32(mean.f() + r, mu); }
   }
 }
+// Op 309 (element-wise form): dx = res + the LayerNorm input gradient.
+__device__ __noinline__ void op_norm_bwd_dx_res(const Ctx& c) {
+  View x = c.buf(0), dy = c.buf(1), g = c.buf(2), mean = c.buf(3), rstd = c.buf(4), dx = c.buf(5), res = c.buf(6);
+  int r0 = c.i(7), r1 = c.i(8), d = c.i(9);
+  for (int r = r0 + wave(); r < r1; r += KVM_WAVES) {
+    float mu = mean.f()[r], rs = rstd.f()[r], s1 = 0.f, s2 = 0.f;
+    for (int j = lane(); j < d; j += 64) { float gs = dy.at(r, j) * g.f()[j]; s1 += gs; s2 += gs * (x.at(r, j) - mu) * rs; }
+    s1 = wave_sum(s1) / (float)d; s2 = wave_sum(s2) / (float)d;
+    for (int j = lane(); j < d; j += 64) {
+      float gs = dy.at(r, j) * g.f()[j], xh = (x.at(r, j) - mu) * rs, v = rs * (gs - s1 - xh * s2);
+      dx.st((long long)r * dx.cols + j, res.at(r, j) + v);
+    }
+  }
+}
 template <bool RMS> __device__ __noinline__ void op_norm_bwd_dx(const Ctx& c) {
   int k = 0; View x = c.buf(k++), dy = c.buf(k++), g = c.buf(k++), mean; if (!RMS) mean = c.buf(k++);
   View rstd = c.buf(k++), dx = c.buf(k++);

@@ -316,15 +316,16 @@ template <bool RMS> __device__ __noinline__ bool op_norm_fwd_fast(const Ctx& c) 
 }
 
 // dx = rstd * (dy*g - mean(dy*g) - xhat * mean(dy*g*xhat)) (+ dx when acc) (registry ops 37, 38).
+// src: the accumulated term (dx itself for op 37 with acc, the residual gradient for op 309); unused when acc is 0.
 template <int NV, bool RMS> __device__ __noinline__ void norm_bwd_rows(const View& x_, const View& dy_, const View& g_, const View& mean_,
-                                                          const View& rstd_, const View& dx_, int r0, int r1, int d, int acc) {
+                                                          const View& rstd_, const View& dx_, const View& src_, int r0, int r1, int d, int acc) {
   // As norm_fwd_rows: register copies of the views; x, dy, the accumulated dx and the row statistics of all of a
   // wave's rows are loaded together before any of them is used.
   const View x = uniform_view(x_), dy = uniform_view(dy_), g = uniform_view(g_), mean = uniform_view(mean_), rstd = uniform_view(rstd_),
-             dx = uniform_view(dx_);
+             dx = uniform_view(dx_), src = uniform_view(src_);
   constexpr int RPW = NV >= 8 ? 1 : NV >= 4 ? 2 : 4;
   Ld4 lx, ly, ld;
-  lx.init(x); ly.init(dy); ld.init(dx, acc != 0);
+  lx.init(x); ly.init(dy); ld.init(src, acc != 0);
   float gv[NV][4];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -343,7 +344,7 @@ template <int NV, bool RMS> __device__ __noinline__ void norm_bwd_rows(const Vie
       for (int i = 0; i < NV; ++i) {
         rx[q][i] = lx.raw(rr * x.cols + 4 * (lane() + 64 * i));
         ry[q][i] = ly.raw(rr * dy.cols + 4 * (lane() + 64 * i));
-        rd[q][i] = ld.raw(rr * dx.cols + 4 * (lane() + 64 * i));
+        rd[q][i] = ld.raw(rr * src.cols + 4 * (lane() + 64 * i));
       }
     }
 #pragma unroll
@@ -378,21 +379,29 @@ template <int NV, bool RMS> __device__ __noinline__ void norm_bwd_rows(const Vie
     }
   }
 }
-template <bool RMS> __device__ __noinline__ bool op_norm_bwd_dx_fast(const Ctx& c) {
-  int k = 0; View x = c.buf(k++), dy = c.buf(k++), g = c.buf(k++), mean; if (!RMS) mean = c.buf(k++);
-  View rstd = c.buf(k++), dx = c.buf(k++);
-  const int r0 = c.i(k), r1 = c.i(k + 1), d = c.i(k + 2), acc = c.i(k + 3);
-  if (d % 256 || d > 4096 || !vec4_ok(x) || !vec4_ok(dy) || !vec4_ok(dx) || g.dtype != 0 || !off32_ok(x) || !off32_ok(dy) || !off32_ok(dx)) return false;
+template <bool RMS> __device__ bool norm_bwd_dispatch(const View& x, const View& dy, const View& g, const View& mean, const View& rstd,
+                                                     const View& dx, const View& src, int r0, int r1, int d, int acc) {
+  if (d % 256 || d > 4096 || !vec4_ok(x) || !vec4_ok(dy) || !vec4_ok(dx) || (acc && !vec4_ok(src)) || g.dtype != 0 || !off32_ok(x) ||
+      !off32_ok(dy) || !off32_ok(dx) || (acc && !off32_ok(src))) return false;
   switch (d / 256) {
-    case 1: norm_bwd_rows<1, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
-    case 2: norm_bwd_rows<2, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
-    case 3: norm_bwd_rows<3, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
-    case 4: norm_bwd_rows<4, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
-    case 8: norm_bwd_rows<8, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
-    case 16: norm_bwd_rows<16, RMS>(x, dy, g, mean, rstd, dx, r0, r1, d, acc); break;
+    case 1: norm_bwd_rows<1, RMS>(x, dy, g, mean, rstd, dx, src, r0, r1, d, acc); break;
+    case 2: norm_bwd_rows<2, RMS>(x, dy, g, mean, rstd, dx, src, r0, r1, d, acc); break;
+    case 3: norm_bwd_rows<3, RMS>(x, dy, g, mean, rstd, dx, src, r0, r1, d, acc); break;
+    case 4: norm_bwd_rows<4, RMS>(x, dy, g, mean, rstd, dx, src, r0, r1, d, acc); break;
+    case 8: norm_bwd_rows<8, RMS>(x, dy, g, mean, rstd, dx, src, r0, r1, d, acc); break;
+    case 16: norm_bwd_rows<16, RMS>(x, dy, g, mean, rstd, dx, src, r0, r1, d, acc); break;
     default: return false;
   }
   return true;
+}
+// Op 309: dx = res + the LayerNorm input gradient.
+__device__ __noinline__ bool op_norm_bwd_dx_res_fast(const Ctx& c) {
+  return norm_bwd_dispatch<false>(c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.buf(6), c.i(7), c.i(8), c.i(9), 1);
+}
+template <bool RMS> __device__ __noinline__ bool op_norm_bwd_dx_fast(const Ctx& c) {
+  int k = 0; View x = c.buf(k++), dy = c.buf(k++), g = c.buf(k++), mean; if (!RMS) mean = c.buf(k++);
+  View rstd = c.buf(k++), dx = c.buf(k++);
+  return norm_bwd_dispatch<RMS>(x, dy, g, mean, rstd, dx, dx, c.i(k), c.i(k + 1), c.i(k + 2), c.i(k + 3));
 }
 
 // ---------------------------------------------------------------------------------------------- cross entropy

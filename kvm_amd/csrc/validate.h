@@ -39,7 +39,7 @@ static const OpSig* find_op(int id) { for (const OpSig& o : kRegistry) if (o.id 
 static bool implemented(int id) {
   static const int ids[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 32, 33, 34, 35, 36, 37, 38, 39, 40, 41, 42, 43, 44, 45, 46, 47, 48, 49, 50,
                             51, 52, 53, 54, 55, 56, 57, 58, 59, 60, 61, 62, 63, 96, 97, 98, 99, 100, 101, 102, 103, 104, 113, 114, 115,
-                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304, 305, 306, 308};
+                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304, 305, 306, 308, 309};
   for (int i : ids) if (i == id) return true;
   return false;
 }
@@ -72,6 +72,7 @@ static char arg_class(int op, const std::string& n) {
     case 33: return in({"ids"}) ? 'i' : 'f';
     case 35: case 36: return in({"x", "out"}) ? 'a' : 'f';
     case 37: case 38: return in({"x", "dy", "dx"}) ? 'a' : 'f';
+    case 309: return in({"x", "dy", "dx", "res"}) ? 'a' : 'f';
     case 39: return in({"x", "dy"}) ? 'a' : 'f';
     case 40: return 'f';
     case 41: return in({"x", "dy", "dx"}) ? 'a' : 'f';
@@ -154,6 +155,8 @@ static void extents(int op, Check& k) {
     case 35: case 36: { int r0 = k.I("r0"), r1 = k.I("r1"), d = k.I("d"); k.range(r0, r1); k.need(d > 0, "d > 0");
       k.ext("x", r1, d); k.extn("gamma", d); k.ext("out", r1, d); k.extn("rstd", r1);
       if (op == 35) { k.extn("beta", d); k.extn("mean", r1); } break; }
+    case 309: { int r0 = k.I("r0"), r1 = k.I("r1"), d = k.I("d"); k.range(r0, r1); k.need(d > 0, "d > 0");
+      k.ext("x", r1, d); k.ext("dy", r1, d); k.extn("gamma", d); k.extn("rstd", r1); k.extn("mean", r1); k.ext("dx", r1, d); k.ext("res", r1, d); break; }
     case 37: case 38: { int r0 = k.I("r0"), r1 = k.I("r1"), d = k.I("d"); k.range(r0, r1); k.need(d > 0, "d > 0");
       k.ext("x", r1, d); k.ext("dy", r1, d); k.extn("gamma", d); k.extn("rstd", r1); k.ext("dx", r1, d); if (op == 37) k.extn("mean", r1); break; }
     case 39: { int R = k.I("R"), d = k.I("d"), c0 = k.I("c0"), c1 = k.I("c1"); k.need(R >= 0 && 0 <= c0 && c0 <= c1 && c1 <= d, "bad R/c0/c1/d");

@@ -408,8 +408,8 @@ class GPTBuilder:
             self.gemm(f'du.{l}', self.w(f'w1.{l}'), f'dh.{l}', N, d, F, flags=0)
             self.gemm(f'du.{l}', f'h2.{l}', f'd.w1.{l}', F, d, N, flags=1)
             self.colsum(f'du.{l}', f'd.b1.{l}', N, F)
-            self.copy_rows(dxo, dm)                                                             # residual path
-            self.layernorm_bwd(f'xm.{l}', f'dh.{l}', f'ln2g.{l}', f'mu2.{l}', f'rs2.{l}', dm, f'd.ln2g.{l}', f'd.ln2b.{l}', acc=1)
+            self.layernorm_bwd(f'xm.{l}', f'dh.{l}', f'ln2g.{l}', f'mu2.{l}', f'rs2.{l}', dm, f'd.ln2g.{l}', f'd.ln2b.{l}', acc=1,
+                               res=dxo)                                                     # + the residual path
             # projection: xm = o @ wo^T + bo + x
             fused_delta = self.gemm_delta(dm, self.w(f'wo.{l}'), f'do.{l}', N, d, d, 0, f'o.{l}', f'delta.{l}', T, H)
             if not fused_delta:
@@ -425,8 +425,7 @@ class GPTBuilder:
             for nm in ('q', 'k', 'v'):
                 self.gemm(f'd{nm}.{l}', f'h1.{l}', f'd.w{nm}.{l}', d, d, N, flags=1)
                 self.colsum(f'd{nm}.{l}', f'd.b{nm}.{l}', N, d)
-            self.copy_rows(dm, dx)
-            self.layernorm_bwd(f'x.{l}', dh1, f'ln1g.{l}', f'mu1.{l}', f'rs1.{l}', dx, f'd.ln1g.{l}', f'd.ln1b.{l}', acc=1)
+            self.layernorm_bwd(f'x.{l}', dh1, f'ln1g.{l}', f'mu1.{l}', f'rs1.{l}', dx, f'd.ln1g.{l}', f'd.ln1b.{l}', acc=1, res=dm)
         dx0 = 'dx.0'
         if self.bf:                                  # embedding_bwd takes an f32 gradient
             for r0, r1 in self.rows(N):
@@ -447,7 +446,8 @@ class GPTBuilder:
             self.task('layernorm_fwd', [(x, (r0, r1)), (g, ()), (bta, ())], [(out, (r0, r1)), (mu, (r0, r1)), (rs, (r0, r1))],
                       x=x, gamma=g, beta=bta, out=out, mean=mu, rstd=rs, r0=r0, r1=r1, d=d, eps=1e-5)
 
-    def layernorm_bwd(self, x, dy, g, mu, rs, dx, dg, db, acc):
+    def layernorm_bwd(self, x, dy, g, mu, rs, dx, dg, db, acc, res=None):
+        """res: dx = res + the input gradient (op 309, the residual path) instead of accumulating into dx."""
         c = self.c
         N, d = c.batch * c.T, c.d
         for c0, c1 in split(d, max(1, d // 64)):
@@ -456,20 +456,14 @@ class GPTBuilder:
                       c1=c1, acc=0)
         for r0, r1 in self.rows(N):
             reads = [(x, (r0, r1)), (dy, (r0, r1)), (g, ()), (mu, (r0, r1)), (rs, (r0, r1))]
+            if res is not None:
+                reads.append((res, (r0, r1)))
+                self.task('layernorm_bwd_dx_res', reads, [(dx, (r0, r1))], x=x, dy=dy, gamma=g, mean=mu, rstd=rs, dx=dx, res=res, r0=r0,
+                          r1=r1, d=d)
+                continue
             if acc:
                 reads.append((dx, (r0, r1)))
             self.task('layernorm_bwd_dx', reads, [(dx, (r0, r1))], x=x, dy=dy, gamma=g, mean=mu, rstd=rs, dx=dx, r0=r0, r1=r1, d=d, acc=acc)
-
-    def copy_rows(self, src, dst):
-        """dst = src, row blocks (the residual path of a layernorm backward, which then accumulates into dst):
-        round_bf16 between bf16 buffers is a copy; scale_flat by 1 is one for f32."""
-        c = self.c
-        N, d = c.batch * c.T, c.d
-        for r0, r1 in self.rows(N):
-            if self.bf:
-                self.task('round_bf16', [(src, (r0, r1))], [(dst, (r0, r1))], x=src, out=dst, e0=r0 * d, e1=r1 * d)
-            else:
-                self.task('scale_flat', [(src, (r0, r1))], [(dst, (r0, r1))], x=src, out=dst, alpha=1.0, e0=r0 * d, e1=r1 * d)
 
     def colsum(self, x, out, R, C):
         for c0, c1 in split(C, max(1, C // 64)):

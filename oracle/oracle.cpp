@@ -191,11 +191,13 @@ template <bool RMS> void norm_fwd(const Ctx& c) {   // ref_gpt.py:107-120
     if (!RMS) mean.f[r] = f32(mu);
   }
 }
-template <bool RMS> void norm_bwd_dx(const Ctx& c) {   // ref_gpt.py:131-144
-  V x = c.buf(0), dy = c.buf(1), g = c.buf(2), mean, rstd, dx; int k = 3;
+// res (this executor's op 309): the accumulated term read from res instead of dx.
+template <bool RMS> void norm_bwd_dx(const Ctx& c, bool res_op = false) {   // ref_gpt.py:131-144
+  V x = c.buf(0), dy = c.buf(1), g = c.buf(2), mean, rstd, dx, res; int k = 3;
   if (!RMS) mean = c.buf(k++);
   rstd = c.buf(k++); dx = c.buf(k++);
-  int r0 = c.i(k), r1 = c.i(k + 1), d = c.i(k + 2), acc = c.i(k + 3);
+  if (res_op) res = c.buf(k++);
+  int r0 = c.i(k), r1 = c.i(k + 1), d = c.i(k + 2), acc = res_op ? 1 : c.i(k + 3);
   std::vector<double> gs(d), xh(d);
   for (int r = r0; r < r1; ++r) {
     double mu = RMS ? 0.0 : mean.f[r], rs = rstd.f[r];
@@ -207,10 +209,14 @@ template <bool RMS> void norm_bwd_dx(const Ctx& c) {   // ref_gpt.py:131-144
     for (int j = 0; j < d; ++j) {
       float v = f32(rs * (gs[j] - s1 - xh[j] * s2));
       long long o = (long long)r * dx.cols + j;
-      dx.st(o, acc ? (double)f32((double)dx.f[o] + v) : (double)v);
+      const double prev = res_op ? (double)res.f[(long long)r * res.cols + j] : (double)dx.f[o];
+      dx.st(o, acc ? (double)f32(prev + v) : (double)v);
     }
   }
 }
+void op_layernorm_bwd_dx(const Ctx& c) { norm_bwd_dx<false>(c); }
+void op_rmsnorm_bwd_dx(const Ctx& c) { norm_bwd_dx<true>(c); }
+void op_layernorm_bwd_dx_res(const Ctx& c) { norm_bwd_dx<false>(c, true); }   // this executor's op 309
 void op_norm_bwd_params(const Ctx& c) {   // ref_gpt.py:147-159
   V x = c.buf(0), dy = c.buf(1), mean = c.buf(2, true), rstd = c.buf(3), dg = c.buf(4), db = c.buf(5, true);
   int R = c.i(6), c0 = c.i(8), c1 = c.i(9), acc = c.i(10);
@@ -720,7 +726,7 @@ const OpEnt kOps[] = {
   {0, [](const Ctx&) {}}, {1, op_copy}, {2, op_add}, {3, op_scale}, {4, op_relu}, {5, op_sgd}, {6, op_predict}, {7, op_mse_grad},
   {8, op_matmul}, {9, op_fill}, {10, [](const Ctx&) {}},
   {32, op_embedding_fwd}, {33, op_embedding_bwd}, {34, op_matmul_tile}, {35, norm_fwd<false>}, {36, norm_fwd<true>},
-  {37, norm_bwd_dx<false>}, {38, norm_bwd_dx<true>}, {39, op_norm_bwd_params}, {40, op_gelu_fwd}, {41, op_gelu_bwd},
+  {37, op_layernorm_bwd_dx}, {38, op_rmsnorm_bwd_dx}, {309, op_layernorm_bwd_dx_res}, {39, op_norm_bwd_params}, {40, op_gelu_fwd}, {41, op_gelu_bwd},
   {42, op_residual_add}, {123, op_sgd_range}, {43, op_rope<1>}, {44, op_rope<-1>}, {45, op_attn_fwd}, {46, op_attn_bwd_delta},
   {47, op_attn_bwd_dq}, {48, op_attn_bwd_dkv}, {49, op_kv_append}, {50, op_attn_decode}, {51, op_softmax_ce_fwd},
   {52, op_softmax_ce_reduce}, {53, op_softmax_ce_bwd}, {127, op_softmax_ce_fused}, {54, op_adamw}, {55, op_gradnorm_partial},

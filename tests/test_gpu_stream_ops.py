@@ -193,3 +193,21 @@ def test_embedding_fwd_rows(tdt, odt, d, pos):
     for r0, r1 in ((0, 5), (5, 77), (77, 203)):
         b.task('embedding_fwd', ids='ids', wte='wte', wpe='wpe' if pos else None, out='out', r0=r0, r1=r1, T=T, d=d)
     _run(b)
+
+
+@pytest.mark.parametrize('dt,d', [('bf16', 768), ('f32', 512)])
+def test_layernorm_bwd_dx_res(dt, d):
+    """Op 309: dx = res + the LayerNorm input gradient, ragged row ranges."""
+    print(f'layernorm_bwd_dx_res {dt} d {d}', flush=True)
+    b = Builder(59)
+    R = 203
+    b.normal('x', R, d, dt, scale=1.0)
+    b.normal('dy', R, d, dt, scale=1.0)
+    b.normal('res', R, d, dt, scale=1.0)
+    b.normal('g', 1, d, 'f32', scale=1.0)
+    b.normal('mu', R, 1, 'f32', scale=0.1)
+    b.fill('rs', R, 1, 'f32', value=1.3)
+    b.fill('dx', R, d, dt)
+    for r0, r1 in ((0, 7), (7, 130), (130, R)):
+        b.task('layernorm_bwd_dx_res', x='x', dy='dy', gamma='g', mean='mu', rstd='rs', dx='dx', res='res', r0=r0, r1=r1, d=d)
+    _run(b)

@@ -273,3 +273,21 @@ def test_mma_delta_is_tile_then_delta():
     assert np.array_equal(f[0].view(np.uint32), u[0].view(np.uint32))
     assert np.array_equal(f[1].view(np.uint32), u[1].view(np.uint32))
     assert np.abs(f[1]).max() > 0
+
+
+def test_layernorm_bwd_dx_res_is_copy_then_accumulate():
+    """Op 309 (dx = res + LayerNorm input gradient) equals copying res into dx and running op 37 with acc 1, bitwise."""
+    R, d = 6, 64
+
+    def graph(fused):
+        w = W(53)
+        w.buf('x', R, d), w.buf('dy', R, d), w.buf('g', d), w.buf('mu', R), w.pos('rs', R, 2.0), w.buf('res', R, d), w.zeros('dx', R, d)
+        if fused:
+            w.task('layernorm_bwd_dx_res', x='x', dy='dy', gamma='g', mean='mu', rstd='rs', dx='dx', res='res', r0=0, r1=R, d=d)
+        else:
+            t = w.task('copy', src='res', dst='dx', n=R * d)
+            w.task('layernorm_bwd_dx', after=[t], x='x', dy='dy', gamma='g', mean='mu', rstd='rs', dx='dx', r0=0, r1=R, d=d, acc=1)
+        r, b = _run_one(w)
+        return _get(r, b, 'dx')
+    f, u = graph(True), graph(False)
+    assert np.array_equal(f.view(np.uint32), u.view(np.uint32)) and np.abs(f).max() > 0

@@ -128,21 +128,61 @@ __device__ __noinline__ void op_embedding_fwd(const Ctx& c) {
   }
 }
 // dtab[key,:] (+)= sum of dout rows with that key, rows ascending. Each thread owns columns; rows in order.
+// Table gradient rows [v0, v1): each row gets its matching output-gradient rows added in ascending r (the reference's
+// order). With ids, the waves first scan the ids in parallel (wave w takes the w-th quarter of r, a 64-id ballot at a
+// time) into an LDS list of the matching r in ascending order, and the in-order updates then run over the matches
+// only. Without ids (positions: rows key, key + mod, ...) each wave owns whole table rows and sums them in registers.
 __device__ __noinline__ void op_embedding_bwd(const Ctx& c) {
   View ids = c.buf(0), dout = c.buf(1), dt = c.buf(2);
   int N = c.i(3), mod = c.i(4), v0 = c.i(5), v1 = c.i(6), d = c.i(7), acc = c.i(8);
+  if (!ids.ok()) {
+    for (int key = v0 + wave(); key < v1; key += KVM_WAVES)
+      for (int k = lane(); k < d; k += 64) {
+        auto* o = dt.f() + ((long long)key * dt.cols + k);
+        float s = acc ? *o : 0.f;
+        for (int r = key; r < N; r += mod) s += dout.at(r, k);
+        stwt32(o, s);
+      }
+    return;
+  }
   if (!acc) for (long long e = tid(); e < (long long)(v1 - v0) * d; e += KVM_THREADS) stwt32(dt.f() + ((long long)(v0 + e / d) * dt.cols + e % d), 0.f);
-  __syncthreads();
-  if (ids.ok()) {
-    for (int r = 0; r < N; ++r) {
-      int key = ids.i()[r];
-      if (key < v0 || key >= v1) continue;
-      for (int k = tid(); k < d; k += KVM_THREADS) stwt32(dt.f() + ((long long)key * dt.cols + k), dt.f()[(long long)key * dt.cols + k] + (dout.at(r, k)));
+  const int Q = (N + KVM_WAVES - 1) / KVM_WAVES;
+  if (2ll * N * 4 + 64 <= KVM_LDS_BYTES) {
+    LDS int* mr = (LDS int*)c.smem;          // [KVM_WAVES][Q]: matching r, per wave in ascending order
+    LDS int* mk = mr + KVM_WAVES * Q;        // their keys
+    LDS int* cnt = mk + KVM_WAVES * Q;       // [KVM_WAVES]
+    const int w = wave(), l = lane(), r1 = min(N, (w + 1) * Q);
+    int n = 0;
+    for (int r0 = w * Q; r0 < r1; r0 += 64) {
+      const int r = r0 + l;
+      const int key = r < r1 ? ids.i()[r] : -1;
+      const bool m = key >= v0 && key < v1;
+      const unsigned long long bal = __ballot(m);
+      if (m) {
+        const int at = n + __popcll(bal & ((1ull << l) - 1));
+        mr[w * Q + at] = r; mk[w * Q + at] = key;
+      }
+      n += __popcll(bal);
     }
-  } else {
-    for (int key = v0; key < v1; ++key)
-      for (int r = key; r < N; r += mod)
-        for (int k = tid(); k < d; k += KVM_THREADS) stwt32(dt.f() + ((long long)key * dt.cols + k), dt.f()[(long long)key * dt.cols + k] + (dout.at(r, k)));
+    if (l == 0) cnt[w] = n;
+    __syncthreads();
+    for (int ww = 0; ww < KVM_WAVES; ++ww) {
+      const int nw = cnt[ww];
+      for (int i = 0; i < nw; ++i) {
+        const int r = mr[ww * Q + i], key = mk[ww * Q + i];
+        for (int k = tid(); k < d; k += KVM_THREADS) {
+          auto* o = dt.f() + ((long long)key * dt.cols + k);
+          stwt32(o, *o + dout.at(r, k));
+        }
+      }
+    }
+    return;
+  }
+  __syncthreads();
+  for (int r = 0; r < N; ++r) {
+    int key = ids.i()[r];
+    if (key < v0 || key >= v1) continue;
+    for (int k = tid(); k < d; k += KVM_THREADS) stwt32(dt.f() + ((long long)key * dt.cols + k), dt.f()[(long long)key * dt.cols + k] + (dout.at(r, k)));
   }
 }
 __device__ __noinline__ void op_gather_rows(const Ctx& c) {
@@ -422,18 +462,12 @@ __device__ __noinline__ void op_gradnorm_partial(const Ctx& c) {
 }
 __device__ __noinline__ void op_gradnorm_finish(const Ctx& c) {
   View part = c.buf(0), out = c.buf(2); int ns = c.i(1); float mx = c.f(3);
-  // The partials are staged in LDS by all threads (one parallel load each), then added in index order in double by
-  // thread 0, the reference's order.
-  LDS float* st = (LDS float*)c.smem;
-  constexpr int CH = KVM_LDS_BYTES / 4;
+  // Sum in double: each thread adds a strided subset, then a fixed tree over the threads. The order differs from a
+  // serial sum only in the last bits of the double, far below the rounding of the float norm computed from it.
+  __shared__ double red[KVM_WAVES];
   double s = 0.0;
-  for (int b0 = 0; b0 < ns; b0 += CH) {
-    const int n = min(CH, ns - b0);
-    __syncthreads();
-    for (int i = tid(); i < n; i += KVM_THREADS) st[i] = part.f()[b0 + i];
-    __syncthreads();
-    if (tid() == 0) for (int i = 0; i < n; ++i) s += st[i];
-  }
+  for (int i = tid(); i < ns; i += KVM_THREADS) s += part.f()[i];
+  s = block_sum_d(s, red);
   if (tid() == 0) {
     float n = (float)sqrt(s);
     stwt32(out.f() + 0, mx > 0.f ? fminf(1.f, mx / (n + 1e-6f)) : 1.f);

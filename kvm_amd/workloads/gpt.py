@@ -434,7 +434,7 @@ class GPTBuilder:
         for v0, v1 in self.rows(V, c.tasks_target):
             self.task('embedding_bwd', [('ids', ()), (dx0, ())], [('d.wte', (v0, v1))], ids='ids', dout=dx0, dtab='d.wte', N=N, mod=0,
                       v0=v0, v1=v1, d=d, acc=1)
-        for v0, v1 in self.rows(T, c.tasks_target // 4):
+        for v0, v1 in self.rows(T, c.tasks_target):
             self.task('embedding_bwd', [(dx0, ())], [('d.wpe', (v0, v1))], ids=None, dout=dx0, dtab='d.wpe', N=N, mod=T, v0=v0, v1=v1,
                       d=d, acc=0)
         self.optimizer()

@@ -211,3 +211,26 @@ def test_layernorm_bwd_dx_res(dt, d):
     for r0, r1 in ((0, 7), (7, 130), (130, R)):
         b.task('layernorm_bwd_dx_res', x='x', dy='dy', gamma='g', mean='mu', rstd='rs', dx='dx', res='res', r0=r0, r1=r1, d=d)
     _run(b)
+
+
+@pytest.mark.parametrize('acc', [0, 1])
+def test_embedding_bwd_id_scan(acc):
+    """Table gradient from token ids: ragged N (not a multiple of the 64-id ballot or of the four waves' quarters),
+    repeated keys (each row must add its matches in ascending r), ids outside the table, ranges of one row and of
+    many; plus the position form (rows key, key + T, ...). Adds are in the reference's order, so f32 within 2e-5."""
+    print(f'embedding_bwd acc={acc}', flush=True)
+    N, V, d, T = 1001, 300, 96, 77
+    rng = np.random.default_rng(11 + acc)
+    ids = [int(x) for x in rng.integers(0, V, N)]
+    ids[5] = ids[900] = ids[17] = 42                 # one row hit often, from every wave's quarter
+    ids[3], ids[600] = -1, V + 5                     # ignored ids
+    b = Builder(5)
+    b.values('ids', ids, N, 1, 'i32')
+    b.normal('dout', N, d, 'f32', scale=1.0)
+    b.normal('dtab', V, d, 'f32', scale=1.0)
+    b.normal('dpos', T, d, 'f32', scale=1.0)
+    for v0, v1 in ((0, 1), (1, 42), (42, 43), (43, 299), (299, 300)):
+        b.task('embedding_bwd', ids='ids', dout='dout', dtab='dtab', N=N, mod=0, v0=v0, v1=v1, d=d, acc=acc)
+    for v0, v1 in ((0, 3), (3, 77)):
+        b.task('embedding_bwd', ids=None, dout='dout', dtab='dpos', N=N, mod=T, v0=v0, v1=v1, d=d, acc=acc)
+    _run(b)

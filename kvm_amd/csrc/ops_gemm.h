@@ -767,7 +767,7 @@ __device__ __noinline__ void op_matmul_tile_bf16(const Ctx& c) {
 __device__ __noinline__ void op_matmul_mma_bf16(const Ctx& c) { mfma_tile<128, 256>(c); }
 // Op 304: the 256x256 tile. Shapes outside the direct-to-LDS path (partial tiles, odd K, f32 operands) run as two
 // 128x256 tiles, rows m0 and m0 + 128 (the second by advancing m0 in the task's LDS copy of its arguments).
-__device__ __noinline__ void op_matmul_mma_bf16_256(const Ctx& c) {
+__device__ __forceinline__ void tile_256(const Ctx& c) {
   const GemmArgs g = gemm_args(c);
   const bool akc = !(g.fl & 1), bkc = (g.fl & 2) != 0;
   if (gemm_fast_operand(g.A, akc, g.m0, 256, g.M, g.K) && gemm_fast_operand(g.B, bkc, g.n0, 256, g.N, g.K)) {
@@ -783,8 +783,10 @@ __device__ __noinline__ void op_matmul_mma_bf16_256(const Ctx& c) {
     mfma_tile<128, 256>(c);
   }
 }
-// Op 302: op 122 over the K range [k0, k0 + K), written at output rows om0 + m. The task's buffer views (LDS copies
-// made by the dispatcher) are narrowed in place to that K range and output row offset; the tile then runs unchanged.
+__device__ __noinline__ void op_matmul_mma_bf16_256(const Ctx& c) { tile_256(c); }
+// Op 302: op 122 over the K range [k0, k0 + K), written at output rows om0 + m; with flag 64 op 304's 256x256 tile
+// (a quarter fewer operand bytes per output than 128x256). The task's buffer views (LDS copies made by the
+// dispatcher) are narrowed in place to that K range and output row offset; the tile then runs unchanged.
 __device__ __noinline__ void op_matmul_mma_bf16_kr(const Ctx& c) {
   if (tid() == 0) {
     LDS View* v = (LDS View*)c.views;
@@ -799,7 +801,8 @@ __device__ __noinline__ void op_matmul_mma_bf16_kr(const Ctx& c) {
     shift(v[2], om0, (long long)om0 * v[2].cols);
   }
   __syncthreads();
-  mfma_tile<128, 256>(c);
+  if (c.i(11) & 64) tile_256(c);
+  else mfma_tile<128, 256>(c);
 }
 
 }  // namespace kvm

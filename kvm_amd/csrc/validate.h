@@ -273,7 +273,7 @@ static void extents(int op, Check& k) {
     case 302: {
       int M = k.I("M"), N = k.I("N"), K = k.I("K"), fl = k.I("flags"), m0 = k.I("m0"), n0 = k.I("n0"), k0 = k.I("k0"), om0 = k.I("om0");
       k.need(M > 0 && N > 0 && K > 0 && 0 <= m0 && m0 < M && 0 <= n0 && n0 < N && k0 >= 0 && om0 >= 0, "bad M/N/K/m0/n0/k0/om0");
-      k.need((fl & ~(1 | 2 | 4 | 32 | 64)) == 0, "flags: only 1, 2, 4");
+      k.need((fl & ~(1 | 2 | 4 | 32 | 64)) == 0, "flags: only 1, 2, 4, 32, 64");
       k.need(!k.B("bias") && !k.B("res") && !k.B("pre"), "bias, res and pre must be absent");
       const long long k1 = (long long)k0 + K;
       k.ext("a", fl & 1 ? k1 : M, fl & 1 ? M : k1); k.ext("b", fl & 2 ? N : k1, fl & 2 ? k1 : N); k.ext("out", (long long)om0 + M, N); break; }

@@ -266,11 +266,13 @@ class GPTBuilder:
                           K=K, flags=flags, alpha=1.0, o=o, delta=delta, T=T, H=H, hd=64)
         return True
 
+    SPLITK_S, SPLITK_TM = 8, 256   # the head input gradient's K splits and tile rows
     SPLITK_MIN = 16384   # K from which a GEMM with few output tiles is split along K (the tied head's input gradient)
 
-    def gemm_splitk(self, A, B, out, M, N, K, flags, S):
-        """out = op(A) op(B) as S independent K ranges (split-K tiles, op 302) into an f32 partial buffer of S row
-        blocks, then an in-order sum of the blocks into `out` (op 303, row chunks). The K ranges are whole 32-deep slabs."""
+    def gemm_splitk(self, A, B, out, M, N, K, flags, S, TM=128):
+        """out = op(A) op(B) as S independent K ranges (split-K tiles, op 302; TM 256: 256x256 tiles) into an f32
+        partial buffer of S row blocks, then an in-order sum of the blocks into `out` (op 303, row chunks). The K
+        ranges are whole 32-deep slabs."""
         ta, tb = flags & 1, flags & 2
         part = f'{out}.kpart'
         if part not in self.shapes:
@@ -280,13 +282,14 @@ class GPTBuilder:
         bounds = [32 * (slabs * s // S) for s in range(S + 1)]
         for s in range(S):
             k0, k1 = bounds[s], bounds[s + 1]
-            for m0 in range(0, M, 128):
-                m1 = min(M, m0 + 128)
+            for m0 in range(0, M, TM):
+                m1 = min(M, m0 + TM)
                 for n0 in range(0, N, 256):
                     n1 = min(N, n0 + 256)
                     reads = [(A, (k0, k1, m0, m1) if ta else (m0, m1, k0, k1)), (B, (n0, n1, k0, k1) if tb else (k0, k1, n0, n1))]
                     self.task('matmul_mma_bf16_kr', reads, [(part, (s * M + m0, s * M + m1, n0, n1))], a=A, b=B, out=part, bias=None,
-                              res=None, pre=None, m0=m0, n0=n0, M=M, N=N, K=k1 - k0, flags=flags, alpha=1.0, k0=k0, om0=s * M)
+                              res=None, pre=None, m0=m0, n0=n0, M=M, N=N, K=k1 - k0, flags=flags | (64 if TM == 256 else 0), alpha=1.0,
+                              k0=k0, om0=s * M)
         for r0, r1 in self.rows(M):
             self.task('splitk_reduce', [(part, (s * M + r0, s * M + r1, 0, N)) for s in range(S)], [(out, (r0, r1, 0, N))],
                       part=part, out=out, M=M, N=N, S=S, r0=r0, r1=r1)
@@ -393,7 +396,7 @@ class GPTBuilder:
         # each LN backward adds into a copy-free buffer: LN2 bwd writes dm.l = dx.{l+1} + LN'(dh) via acc on a buffer
         # first filled by the residual path (the GEMM below writes it with res=), LN1 bwd likewise into dx.l.
         if self.bf and V >= self.SPLITK_MIN and V % 32 == 0:                                 # d hf: K = V is long, M x d has few tiles
-            self.gemm_splitk('dlogits', self.w('wte'), f'dh.{L}', N, d, V, flags=0, S=8)
+            self.gemm_splitk('dlogits', self.w('wte'), f'dh.{L}', N, d, V, flags=0, S=self.SPLITK_S, TM=self.SPLITK_TM)
         else:
             self.gemm('dlogits', self.w('wte'), f'dh.{L}', N, d, V, flags=0)
         self.gemm('dlogits', 'hf', 'd.wte', V, d, N, flags=1)                              # tied head: wte grad (overwrite)

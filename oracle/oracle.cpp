@@ -525,15 +525,15 @@ void op_matmul_mma_bf16_256(const Ctx& c) {   // this executor's op 304: op 122 
     if (a[6] < c.a[8] && a[7] < c.a[9]) mm_tile(sub, true, 64);
   }
 }
-// This executor's op 302: op 122's 128x256 tile over k in [k0, k0 + K), written to output row om0 + m; plain epilogue
-// (alpha, optional accumulate).
+// This executor's op 302: op 122's 128x256 tile (flag 64: a 256x256 tile) over k in [k0, k0 + K), written to output
+// row om0 + m; plain epilogue (alpha, optional accumulate).
 void op_matmul_mma_bf16_kr(const Ctx& c) {
   V A = c.buf(0), B = c.buf(1), out = c.buf(2);
   int m0 = c.i(6), n0 = c.i(7), M = c.i(8), N = c.i(9), K = c.i(10), fl = c.i(11), k0 = c.i(13), om0 = c.i(14); float alpha = c.fl(12);
   need((fl & ~(1 | 2 | 4 | 32 | 64)) == 0 && c.a[3] == -1 && c.a[4] == -1 && c.a[5] == -1 && k0 >= 0 && om0 >= 0,
        "matmul_mma_bf16_kr: flags / epilogue / k0 / om0");
   int ta = fl & 1, tb = fl & 2, accum = fl & 4;
-  for (int m = m0; m < std::min(m0 + 128, M); ++m)
+  for (int m = m0; m < std::min(m0 + (fl & 64 ? 256 : 128), M); ++m)
     for (int n = n0; n < std::min(n0 + 256, N); ++n) {
       float acc = 0;
       for (int k = k0; k < k0 + K; ++k) {

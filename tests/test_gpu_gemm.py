@@ -96,9 +96,9 @@ def test_tile_bf16_sizes(tiles, fl):
     _check(_gemm_graph(256, 256, 128, fl | 1, op='matmul_tile_bf16', tiles=tiles))
 
 
-def _splitk_graph(M, N, K, flags, S, odt='bf16'):
-    """Split-K as the GPT generator emits it: op 302 tiles over S K ranges into an f32 partial buffer of S row blocks,
-    then op 303 sums the blocks in order into C."""
+def _splitk_graph(M, N, K, flags, S, odt='bf16', TM=128):
+    """Split-K as the GPT generator emits it: op 302 tiles (TM 256: flag 64, 256x256 tiles) over S K ranges into an
+    f32 partial buffer of S row blocks, then op 303 sums the blocks in order into C."""
     b = Builder(11)
     ta, tb = flags & 1, flags & 2
     b.normal('A', K if ta else M, M if ta else K, 'bf16', scale=1.0)
@@ -109,19 +109,26 @@ def _splitk_graph(M, N, K, flags, S, odt='bf16'):
     bounds = [32 * (slabs * s // S) for s in range(S + 1)]
     ts = []
     for s in range(S):
-        for m0 in range(0, M, 128):
+        for m0 in range(0, M, TM):
             for n0 in range(0, N, 256):
                 ts.append(b.task('matmul_mma_bf16_kr', a='A', b='B', out='P', bias=None, res=None, pre=None, m0=m0, n0=n0, M=M, N=N,
-                                 K=bounds[s + 1] - bounds[s], flags=flags, alpha=1.0, k0=bounds[s], om0=s * M))
+                                 K=bounds[s + 1] - bounds[s], flags=flags | (64 if TM == 256 else 0), alpha=1.0, k0=bounds[s], om0=s * M))
     for r0 in range(0, M, 64):
         b.task('splitk_reduce', after=ts, part='P', out='C', M=M, N=N, S=S, r0=r0, r1=min(M, r0 + 64))
     return Workload(b.spec(), b.init_override)
 
 
+@pytest.mark.parametrize('TM', [128, 256])
 @pytest.mark.parametrize('flags', [0, 1, 2, 3])
-def test_splitk_all_orientations(flags):
-    print(f'split-K flags {flags}', flush=True)
-    _check(_splitk_graph(256, 512, 416, flags, S=3))
+def test_splitk_all_orientations(flags, TM):
+    print(f'split-K flags {flags} TM {TM}', flush=True)
+    _check(_splitk_graph(512, 512, 416, flags, S=3, TM=TM))
+
+
+def test_splitk_256_partial_tiles():
+    """256-row split-K tiles where the shape leaves partial tiles (the two-128-row fallback inside the tile)."""
+    print('split-K 256 partial tiles', flush=True)
+    _check(_splitk_graph(300, 300, 640, 0, S=2, odt='f32', TM=256))
 
 
 def test_splitk_partial_tiles_f32_out():

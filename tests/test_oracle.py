@@ -220,8 +220,9 @@ def test_gemv_bf16_closed_form():
     assert np.abs(_get(r, b, 'o') - W_ @ v).max() < 1e-5
 
 
+@pytest.mark.parametrize('TM', [128, 256])
 @pytest.mark.parametrize('flags', [0, 3])
-def test_splitk_closed_form(flags):
+def test_splitk_closed_form(flags, TM):
     """Split-K (ops 302 + 303): the in-order sum of the K-range partials equals the fp64 product of the bf16 operands
     (a wrong k0 / om0 offset, a transposed operand or a dropped range fails this); each partial block equals the
     product over its own K range."""
@@ -233,10 +234,10 @@ def test_splitk_closed_form(flags):
     bounds = [0, 32, 64, 96]
     ts = []
     for s in range(S):
-        for m0 in (0, 128):
+        for m0 in range(0, M, TM):
             for n0 in (0, 256):
                 ts.append(w.task('matmul_mma_bf16_kr', a='A', b='B', out='P', bias=None, res=None, pre=None, m0=m0, n0=n0, M=M, N=N,
-                                 K=bounds[s + 1] - bounds[s], flags=flags, alpha=1.0, k0=bounds[s], om0=s * M))
+                                 K=bounds[s + 1] - bounds[s], flags=flags | (64 if TM == 256 else 0), alpha=1.0, k0=bounds[s], om0=s * M))
     w.task('splitk_reduce', after=ts, part='P', out='C', M=M, N=N, S=S, r0=0, r1=M)
     r, b = _run_one(w)
     A = _get(r, b, 'A').astype(np.float64).reshape(K if ta else M, M if ta else K)

@@ -429,17 +429,46 @@ __device__ __noinline__ void ce_rows_block(const Ctx& c, const View& lg_, const 
   // which also waits for every store in flight.
   const View lg = uniform_view(lg_), tg = uniform_view(tg_), rl = uniform_view(rl_), ls = uniform_view(ls_), dl = uniform_view(dl_);
   LDS float* red = (LDS float*)c.smem;
+  // Rows pipelined when the row fits in LDS: after its reductions each thread parks its own vectors of row r in LDS
+  // (read back only by the same thread, so no barrier), the loads of row r + 1 go into the registers, and dlogits of
+  // row r is written from LDS while they are in flight.
+  constexpr bool PIPE = 64 + NR * 256 * 16 <= KVM_LDS_BYTES;
+  LDS u16x8_t* park = (LDS u16x8_t*)(c.smem + 64);
   const int nv = V / 8, t8 = tid();
-  for (int r = r0; r < r1; ++r) {
-    const int t = tg.i()[r];
-    const bool ign = t == ignore;
-    if (!ign && (t < 0 || t >= V)) { if (tid() == 0) c.fail(KVM_ERR_OP_TOKEN, r, t); continue; }
+  u16x8_t v[NR];
+  auto load_row = [&](int r) {
     const GLOBAL u16x8_t* row = (const GLOBAL u16x8_t*)(lg.h() + (long long)r * lg.cols);
-    u16x8_t v[NR];
 #pragma unroll
     for (int u = 0; u < NR; ++u) v[u] = row[min(t8 + 256 * u, nv - 1)];         // unconditional: all in flight
+  };
+  auto write_grad = [&](int r, int t, bool ign, float lse, auto get) {
+    if (ign) {                                       // ignored row: zeros (a uniform branch, outside the element loop)
+      const long long ob = (long long)r * dl.cols;
+      const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int j = t8; j < nv; j += 256) st8(dl, ob + 8 * j, z);
+      return;
+    }
+    const long long ob = (long long)r * dl.cols;
+    const float l2 = lse * LOG2E;
+#pragma unroll
+    for (int u = 0; u < NR; ++u) {
+      const int j = t8 + 256 * u;
+      if (j < nv) {
+        const u16x8_t x = get(u);
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = (__builtin_amdgcn_exp2f(bfl(x[i]) * LOG2E - l2) - (8 * j + i == t ? 1.f : 0.f)) * f;
+        st8(dl, ob + 8 * j, o);
+      }
+    }
+  };
+  if (r0 < r1) load_row(r0);
+  for (int r = r0; r < r1; ++r) {
+    const int t = __builtin_amdgcn_readfirstlane(tg.i()[r]);   // uniform: tests on it are scalar branches
+    const bool ign = t == ignore, bad = !ign && (t < 0 || t >= V);
+    if (bad && tid() == 0) c.fail(KVM_ERR_OP_TOKEN, r, t);
     float lse = 0.f;
-    if (fwd && !ign) {
+    if (fwd && !ign && !bad) {
       float m = -INFINITY;
 #pragma unroll
       for (int u = 0; u < NR; ++u)
@@ -466,24 +495,24 @@ __device__ __noinline__ void ce_rows_block(const Ctx& c, const View& lg_, const 
             for (int i = 0; i < 8; ++i) if (i == (t & 7)) xt = bfl(v[u][i]);
         stwt32(rl.f() + r, lse - xt);
       }
-    } else if (fwd) {
+    } else if (fwd && ign) {
       if (tid() == 0) { stwt32(ls.f() + r, 0.f); stwt32(rl.f() + r, 0.f); }
-    } else {
+    } else if (!fwd && !bad) {
       lse = ls.f()[r];
     }
-    if (bwd) {
-      const long long ob = (long long)r * dl.cols;
-      const float l2 = lse * LOG2E;
+    // lse is uniform; taking it into a scalar register here completes its load (bwd-only form) before the next
+    // row's loads are issued, so the gradient pass below waits for none of them.
+    lse = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(lse)));
+    const bool grad = bwd && !bad;
+    if constexpr (PIPE) {
+      if (grad)
 #pragma unroll
-      for (int u = 0; u < NR; ++u) {
-        const int j = t8 + 256 * u;
-        if (j < nv) {
-          float o[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = ign ? 0.f : (__builtin_amdgcn_exp2f(bfl(v[u][i]) * LOG2E - l2) - (8 * j + i == t ? 1.f : 0.f)) * f;
-          st8(dl, ob + 8 * j, o);
-        }
-      }
+        for (int u = 0; u < NR; ++u) park[u * 256 + t8] = v[u];
+      if (r + 1 < r1) load_row(r + 1);
+      if (grad) write_grad(r, t, ign, lse, [&](int u) { return park[u * 256 + t8]; });
+    } else {
+      if (grad) write_grad(r, t, ign, lse, [&](int u) { return v[u]; });
+      if (r + 1 < r1) load_row(r + 1);
     }
   }
 }

@@ -449,7 +449,24 @@ __device__ __noinline__ void ce_rows_block(const Ctx& c, const View& lg_, const 
       return;
     }
     const long long ob = (long long)r * dl.cols;
-    const float l2 = lse * LOG2E;
+    // softmax * f as one exponential: exp2(x log2 e - (lse log2 e - log2 f)); the target's -f is applied by the one
+    // lane holding it.
+    if (!(f > 0.f)) {                                // other scales: (softmax - onehot) * f as written
+      const float l2 = lse * LOG2E;
+#pragma unroll
+      for (int u = 0; u < NR; ++u) {
+        const int j = t8 + 256 * u;
+        if (j < nv) {
+          const u16x8_t x = get(u);
+          float o[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = (__builtin_amdgcn_exp2f(bfl(x[i]) * LOG2E - l2) - (8 * j + i == t ? 1.f : 0.f)) * f;
+          st8(dl, ob + 8 * j, o);
+        }
+      }
+      return;
+    }
+    const float l2 = lse * LOG2E - log2f(f);
 #pragma unroll
     for (int u = 0; u < NR; ++u) {
       const int j = t8 + 256 * u;
@@ -457,7 +474,10 @@ __device__ __noinline__ void ce_rows_block(const Ctx& c, const View& lg_, const 
         const u16x8_t x = get(u);
         float o[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = (__builtin_amdgcn_exp2f(bfl(x[i]) * LOG2E - l2) - (8 * j + i == t ? 1.f : 0.f)) * f;
+        for (int i = 0; i < 8; ++i) o[i] = __builtin_amdgcn_exp2f(bfl(x[i]) * LOG2E - l2);
+        if (j == (t >> 3))
+#pragma unroll
+          for (int i = 0; i < 8; ++i) if (i == (t & 7)) o[i] -= f;
         st8(dl, ob + 8 * j, o);
       }
     }

@@ -71,10 +71,12 @@ def test_rmsnorm_bwd_and_wide_rows():
     _run(b)
 
 
-@pytest.mark.parametrize('dt', ['bf16', 'f32'])
-def test_cross_entropy(dt):
-    print(f'cross entropy {dt}', flush=True)
-    N, V = 256, 5000
+@pytest.mark.parametrize('dt,N,V,scale', [('bf16', 256, 5000, 1.0), ('f32', 256, 5000, 1.0), ('bf16', 64, 50304, 1.0),
+                                           ('bf16', 64, 5000, -0.5), ('bf16', 64, 5000, 0.0)])
+def test_cross_entropy(dt, N, V, scale):
+    """Fused softmax cross entropy: ignored rows (every 17th target is -1), GPT's vocabulary width (the row parked in
+    LDS), and scales other than positive (the gradient formula's other form)."""
+    print(f'cross entropy {dt} N{N} V{V} scale {scale}', flush=True)
     b = Builder(9)
     b.normal('lg', N, V, dt, scale=3.0)
     b.values('tgt', [(37 * i + 11) % V if i % 17 else -1 for i in range(N)], N, 1, 'i32')
@@ -82,7 +84,7 @@ def test_cross_entropy(dt):
     b.fill('ls', N)
     b.fill('dl', N, V, dt)
     b.fill('loss', 2)
-    ts = [b.task('softmax_ce_fused', logits='lg', tgt='tgt', rowloss='rl', lse='ls', dlogits='dl', r0=r0, r1=r1, V=V, ignore=-1, N=N, scale=1.0)
+    ts = [b.task('softmax_ce_fused', logits='lg', tgt='tgt', rowloss='rl', lse='ls', dlogits='dl', r0=r0, r1=r1, V=V, ignore=-1, N=N, scale=scale)
           for r0, r1 in split(N, 16)]
     b.task('softmax_ce_reduce', after=ts, rowloss='rl', tgt='tgt', loss='loss', N=N, ignore=-1)
     _run(b)

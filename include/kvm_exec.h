@@ -10,6 +10,9 @@
 #include <stdint.h>
 #include "mvm_task_abi.h"
 
+// Task priorities are 0..KVM_PRIORITIES-1, larger first among ready tasks (reference: MVM_NBUCKETS, mvm_exec.cuh:51-52).
+#define KVM_PRIORITIES 32
+
 #ifdef __cplusplus
 extern "C" {
 #endif

@@ -7,7 +7,9 @@
 #include <string>
 #include <vector>
 #include <initializer_list>
+#include <algorithm>
 #include "../../include/mvm_task_abi.h"
+#include "../../include/kvm_exec.h"
 
 namespace kvmv {
 
@@ -290,6 +292,57 @@ static void extents(int op, Check& k) {
 
 static const char* kvm_registry_name(int id) { const kvmv::OpSig* o = kvmv::find_op(id); return o ? o->name : nullptr; }
 
+// Version waits that the bundle itself must satisfy (reference check: mvm_exec.cu:179-205). A task waiting for
+// version w of variable v can only start after every in-bundle publisher of v with pub_ver <= w has finished (versions
+// advance one step at a time). Those implied edges are added to the dependency graph through one virtual node per
+// published (variable, version): publisher -> node(v, k), node(v, k_prev) -> node(v, k) for the next lower published
+// version, and node(v, k*) -> waiter for the highest published k* <= w. The graph is O(tasks + edges + publishers)
+// and must stay acyclic, else some task can never run. Waits above every in-bundle publication depend on the outside
+// (base versions, other bundles) and add no edge.
+static bool version_waits_acyclic(const MvmTaskDesc* t, int n, const int32_t* succ, std::string* why) {
+  std::vector<std::pair<long long, int>> pubs;   // ((var << 32) | ver, publisher)
+  for (int i = 0; i < n; ++i) if (t[i].pub_var >= 0) pubs.push_back({((long long)t[i].pub_var << 32) | (unsigned)t[i].pub_ver, i});
+  if (pubs.empty()) return true;
+  for (int i = 0; i < n; ++i)
+    if (t[i].wait_var >= 0 && t[i].wait_var == t[i].pub_var && t[i].pub_ver <= t[i].wait_ver) {
+      *why = "task " + std::to_string(i) + ": waits for version " + std::to_string(t[i].wait_ver) + " of variable " +
+             std::to_string(t[i].wait_var) + " that it publishes itself";
+      return false;
+    }
+  std::sort(pubs.begin(), pubs.end());
+  std::vector<long long> key;                     // distinct published (var, ver), ascending: virtual node n + j
+  std::vector<int> node_of(pubs.size());
+  for (size_t k = 0; k < pubs.size(); ++k) {
+    if (key.empty() || key.back() != pubs[k].first) key.push_back(pubs[k].first);
+    node_of[k] = (int)key.size() - 1;
+  }
+  const int nv = (int)key.size(), N = n + nv;
+  std::vector<std::vector<int>> extra(N);          // implied edges only; the bundle's own edges are read from succ
+  for (size_t k = 0; k < pubs.size(); ++k) extra[pubs[k].second].push_back(n + node_of[k]);
+  for (int j = 1; j < nv; ++j) if ((key[j] >> 32) == (key[j - 1] >> 32)) extra[n + j - 1].push_back(n + j);
+  for (int i = 0; i < n; ++i) {
+    if (t[i].wait_var < 0) continue;
+    const long long want = ((long long)t[i].wait_var << 32) | (unsigned)t[i].wait_ver;
+    auto it = std::upper_bound(key.begin(), key.end(), want);   // first key above the wanted version
+    if (it == key.begin()) continue;
+    --it;
+    if ((*it >> 32) != t[i].wait_var) continue;    // no in-bundle publication of this variable at or below w
+    extra[n + (int)(it - key.begin())].push_back(i);
+  }
+  std::vector<int> deg(N, 0), st;
+  for (int i = 0; i < n; ++i) for (int k = 0; k < t[i].succ_cnt; ++k) ++deg[succ[t[i].succ_off + k]];
+  for (int u = 0; u < N; ++u) for (int v : extra[u]) ++deg[v];
+  for (int u = 0; u < N; ++u) if (!deg[u]) st.push_back(u);
+  int seen = 0;
+  while (!st.empty()) {
+    const int u = st.back(); st.pop_back(); ++seen;
+    if (u < n) for (int k = 0; k < t[u].succ_cnt; ++k) { const int v = succ[t[u].succ_off + k]; if (--deg[v] == 0) st.push_back(v); }
+    for (int v : extra[u]) if (--deg[v] == 0) st.push_back(v);
+  }
+  if (seen != N) { *why = "version-wait cycle: a task waits for a version that only a task depending on it can publish"; return false; }
+  return true;
+}
+
 // Whole-bundle validation: descriptors, arity, edges, indegrees, acyclicity, buffer arguments, extents.
 static bool kvm_validate_bundle(const MvmTaskDesc* t, int n, const int32_t* succ, int ne, const int32_t* args, int na,
                                 const MvmBuf* bufs, int nbufs, int nvars, std::string* why) {
@@ -309,9 +362,12 @@ static bool kvm_validate_bundle(const MvmTaskDesc* t, int n, const int32_t* succ
     if (d.indegree < 0) return bad(i, "negative indegree");
     if (d.wait_var < -1 || d.wait_var >= nvars || d.pub_var < -1 || d.pub_var >= nvars) return bad(i, "version variable out of range");
     if (d.pub_var >= 0 && d.pub_ver < 1) return bad(i, "pub_ver must be >= 1");
+    if (d.wait_var >= 0 && d.wait_ver < 0) return bad(i, "wait_ver must be >= 0");
+    if (d.priority < 0 || d.priority >= KVM_PRIORITIES) return bad(i, "priority " + std::to_string(d.priority) + " outside [0, " + std::to_string(KVM_PRIORITIES - 1) + "]");
+    if (d.deadline_us < -1) return bad(i, "deadline_us must be -1 (none) or >= 0");
     for (int k = 0; k < d.succ_cnt; ++k) {
       int s = succ[d.succ_off + k];
-      if (s < 0 || s >= n) return bad(i, "successor index out of range");
+      if (s < 0 || s >= n || s == i) return bad(i, "successor index out of range");
       ++indeg[s];
     }
     const int32_t* a = args + d.args_off;
@@ -336,5 +392,5 @@ static bool kvm_validate_bundle(const MvmTaskDesc* t, int n, const int32_t* succ
   for (int i = 0; i < n; ++i) if (rem[i] == 0) q.push_back(i);
   for (size_t h = 0; h < q.size(); ++h) { const MvmTaskDesc& d = t[q[h]]; for (int k = 0; k < d.succ_cnt; ++k) if (--rem[succ[d.succ_off + k]] == 0) q.push_back(succ[d.succ_off + k]); }
   if ((int)q.size() != n) { *why = "dependency cycle"; return false; }
-  return true;
+  return version_waits_acyclic(t, n, succ, why);
 }

@@ -292,3 +292,74 @@ def test_layernorm_bwd_dx_res_is_copy_then_accumulate():
         return _get(r, b, 'dx')
     f, u = graph(True), graph(False)
     assert np.array_equal(f.view(np.uint32), u.view(np.uint32)) and np.abs(f).max() > 0
+
+
+@pytest.mark.parametrize('flags', [0, 1, 2, 3, 4, 8, 512])
+def test_mma_256_is_two_128x256_tiles(flags):
+    """Op 304 (256x256 tile) equals op 122 (golden-pinned 128x256 tile) at (m0, n0) and (m0 + 128, n0), bit for bit,
+    for every operand orientation and epilogue (bias, pre-activation store, GELU, residual, accumulate, GELU'),
+    including ragged edge tiles; and the plain product equals the fp64 product of the bf16-rounded operands."""
+    M, N, K = 300, 290, 48
+    ta, tb = flags & 1, flags & 2
+
+    def graph(fused):
+        w = W(61)
+        w.buf('A', K if ta else M, M if ta else K), w.buf('B', N if tb else K, K if tb else N)
+        w.buf('bias', 1, N), w.buf('res', M, N), w.buf('pre', M, N), w.buf('out', M, N)
+        ep = dict(bias=None, res=None, pre=None)
+        if flags & 512:
+            ep['pre'] = 'pre'
+        elif flags in (0, 8):
+            ep = dict(bias='bias', res='res', pre='pre')
+        kw = dict(a='A', b='B', out='out', M=M, N=N, K=K, flags=flags, alpha=0.75, **ep)
+        for m0 in (0, 256):
+            for n0 in (0, 256):
+                if fused:
+                    w.task('matmul_mma_bf16_256', m0=m0, n0=n0, **kw)
+                else:
+                    for dm in (0, 128):
+                        if m0 + dm < M:
+                            w.task('matmul_mma_bf16', m0=m0 + dm, n0=n0, **kw)
+        r, b = _run_one(w)
+        return r, b
+    (rf, bf), (ru, bu) = graph(True), graph(False)
+    for nm in ('out', 'pre'):
+        f, u = _get(rf, bf, nm), _get(ru, bu, nm)
+        assert np.array_equal(f.view(np.uint32), u.view(np.uint32)), nm
+    if flags in (0, 1, 2, 3):
+        A = bl.bf16_round(_get(rf, bf, 'A')).astype(np.float64).reshape(K if ta else M, M if ta else K)
+        B = bl.bf16_round(_get(rf, bf, 'B')).astype(np.float64).reshape(N if tb else K, K if tb else N)
+        want = 0.75 * ((A.T if ta else A) @ (B.T if tb else B))
+        if flags == 0:
+            want = want + _get(rf, bf, 'bias').astype(np.float64) + _get(rf, bf, 'res').astype(np.float64).reshape(M, N)
+        got = _get(rf, bf, 'out').reshape(M, N)
+        assert np.abs(got - want).max() < 1e-5 * np.abs(want).max()
+
+
+@pytest.mark.parametrize('pro', [0, 1, 2])
+@pytest.mark.parametrize('with_res', [False, True])
+def test_gemv_rows_is_gemv_per_row(pro, with_res):
+    """Op 301 over M rows equals op 134 (golden-pinned decode GEMV) run on each row alone, bit for bit, for the three
+    prologues (none, RMSNorm, SwiGLU) with and without the residual; a row mix-up or a shared statistic fails this."""
+    M, K, N = 5, 128, 40
+    rng = np.random.default_rng(3 + pro)
+    X, X2, R = (rng.standard_normal((M, n)).astype(np.float32) for n in (K, K, N))
+    g = rng.standard_normal(K).astype(np.float32)
+    Wt = bl.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.1)
+    vals = lambda a: {'kind': 'values', 'values': a.ravel().tolist()}
+    w = W(71)
+    w.buf('W', N, K, 'bf16', vals(Wt)), w.buf('g', K, 1, 'f32', vals(g))
+    w.buf('X', M, K, 'f32', vals(X)), w.buf('X2', M, K, 'f32', vals(X2)), w.buf('R', M, N, 'f32', vals(R)), w.zeros('O', M, N)
+    opt = dict(x2='X2' if pro == 2 else None, gamma='g' if pro == 1 else None)
+    w.task('gemv_bf16_rows', x='X', w='W', out='O', res='R' if with_res else None, n0=3, n1=N, K=K, M=M, pro=pro, eps=1e-6, **opt)
+    for m in range(M):
+        w.buf(f'x{m}', 1, K, 'f32', vals(X[m])), w.buf(f'y{m}', 1, K, 'f32', vals(X2[m])), w.buf(f'r{m}', 1, N, 'f32', vals(R[m]))
+        w.zeros(f'o{m}', 1, N)
+        w.task('gemv_bf16', x=f'x{m}', x2=f'y{m}' if pro == 2 else None, gamma='g' if pro == 1 else None, w='W', out=f'o{m}',
+               res=f'r{m}' if with_res else None, n0=3, n1=N, K=K, pro=pro, eps=1e-6)
+    r, b = _run_one(w)
+    O = _get(r, b, 'O').reshape(M, N)
+    assert np.abs(O[:, 3:]).max() > 0 and not O[:, :3].any()
+    for m in range(M):
+        assert np.array_equal(O[m].view(np.uint32), _get(r, b, f'o{m}').view(np.uint32)), m
+    assert not np.array_equal(O[0], O[1])

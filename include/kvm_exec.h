@@ -30,6 +30,8 @@ typedef struct KvmConfig {
   int num_vars;                // version variables
   unsigned long long timeout_us;   // stall timeout: no task finished for this long while work is pending
   int device;                  // HIP device ordinal
+  int aging_us;                // 0: strict priority among ready tasks; else a ready task gains one priority level per
+                               //   aging_us of waiting (reference: MvmConfig::aging_us, mvm_exec.cu:375)
 } KvmConfig;
 
 // Buffer initialisation (reference: MvmInit, mvm_exec.cu:431-437).

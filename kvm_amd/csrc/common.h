@@ -57,9 +57,15 @@ struct KvmDevState {
   const int32_t* args;        // [nargs]
   const MvmBuf* bufs;         // [nbufs]
   int* indeg;                 // [ntasks] remaining predecessors
-  int* ready;                 // [nq * qcap] ready queues: cell q*qcap+i holds the i-th released task of queue q, -1 until then
-  KvmQueue* queues;           // [nq]
-  const int* qcount;          // [nq] tasks that go through queue q (task t goes to queue t % nq)
+  int* ready;                 // ready cells: queue qi's i-th released task at ready[qoff[qi] + i], -1 until then
+  KvmQueue* queues;           // [nq * nb]
+  const int* qcount;          // [nq * nb] tasks that go through queue qi
+  const int* qoff;            // [nq * nb] first cell of queue qi (FIFO mode: qi * qcap)
+  // Priority mode (nb > 1 priority buckets, or aging): task t goes to queue tq[t] = (t % nq) * nb + bucket, bucket 0
+  // holding the highest priority present in the graph. FIFO mode (nb == 1): queue t % nq, no table.
+  const int* tq;              // [ntasks] or null
+  const int* bucket_prio;     // [nb] priority of each bucket
+  unsigned long long* ready_ts;   // [ntasks] release time (wall_clock64) when aging, else null
   int* done_blk;              // [grid] tasks finished per worker (summed by the host; no shared counter per task)
   int* state;                 // [ntasks] 0 not released, 1 parked on a version, 2 enqueued
   int* park_next;             // [ntasks] park list links
@@ -68,8 +74,9 @@ struct KvmDevState {
   KvmCounters* cnt;
   KvmTrace* trace;            // [ntasks] or null
   const unsigned* opmask;     // [KVM_OPMASK_IDS] bit k set when argument word k of the operator is a buffer index
-  int ntasks, nbufs, nvars, trace_on, nq, qcap, grid;
+  int ntasks, nbufs, nvars, trace_on, nq, qcap, grid, nb, ncells;
   unsigned long long timeout_ticks;   // stall timeout in wall_clock64 ticks (100 MHz)
+  unsigned long long aging_ticks;     // wall_clock64 ticks of waiting worth one priority level (0: strict priority)
 };
 
 // ---------------------------------------------------------------------------------------------- atomics

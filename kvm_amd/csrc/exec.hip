@@ -42,6 +42,14 @@ __device__ __forceinline__ void queue_overflow(const KvmDevState& S) {
   __hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_QUEUE_OVERFLOW, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void enqueue(const KvmDevState& S, int t) {
+  if (S.tq) {   // priority mode: the task's (queue group, bucket) queue; its release time first when ready tasks age
+    const int q = S.tq[t];
+    if (S.ready_ts) __hip_atomic_store(&S.ready_ts[t], wall_clock64(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int pos = add_relaxed(&S.queues[q].tail, 1);
+    if (pos >= S.qcount[q]) { queue_overflow(S); return; }
+    st_release(&S.ready[S.qoff[q] + pos], t);
+    return;
+  }
   const int q = t % S.nq;
   int pos = add_relaxed(&S.queues[q].tail, 1);
   if (pos >= S.qcap) { queue_overflow(S); return; }
@@ -84,6 +92,76 @@ __device__ void publish(const KvmDevState& S, int slot, int var, int ver) {
       else park(S, h, var, want);
     }
     h = nx;
+  }
+}
+
+// Stall check of a waiting worker, every 4096 polls: has any worker finished a task since the last look? After
+// timeout_ticks without one, the run ends with TIMEOUT (first error wins). Returns true when it fired.
+__device__ bool stalled(const KvmDevState& S, unsigned long long& since, int& seen, int ticket) {
+  int d = 0;
+  for (int w = 0; w < S.grid; ++w) d += ld_relaxed(&S.done_blk[w]);
+  unsigned long long now = wall_clock64();
+  if (d != seen) { seen = d; since = now; return false; }
+  if (now - since <= S.timeout_ticks) return false;
+  int z = 0;
+  if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_TIMEOUT, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+    S.cnt->err_slot = -1; S.cnt->err_a = ticket; S.cnt->err_b = d;
+  }
+  return true;
+}
+
+// Priority-mode pop, run by all 64 lanes of wave 0 (lane b watches bucket b of this worker's queue group; bucket 0 is
+// the highest priority present). Strict priority: the lowest non-empty bucket wins; with aging, the largest
+// priority * aging_ticks + time since release (reference rule: mvm_sched.cuh:155-220, score = priority * aging + age).
+// A bucket's head is claimed with a CAS only while head < tail (the cell is reserved, so its store is imminent), so a
+// head never passes the bucket's task count; the worker leaves when every bucket's head has reached its count.
+// Returns the task, or -1 to leave (drained or error).
+__device__ int pop_prio(const KvmDevState& S) {
+  const int l = lane(), g = blockIdx.x % S.nq, qi = g * S.nb + l;
+  const bool mine = l < S.nb;
+  const int cnt = mine ? S.qcount[qi] : 0, off = mine ? S.qoff[qi] : 0;
+  const unsigned long long boost = (mine && S.aging_ticks) ? (unsigned long long)S.bucket_prio[l] * S.aging_ticks : 0ull;
+  unsigned long long since = wall_clock64();
+  int seen = -1;
+  for (unsigned polls = 0;; ++polls) {
+    if (__shfl(ld_relaxed(&S.cnt->err_code), 0, 64) != 0) return -1;
+    const int h = mine ? (int)ld_relaxed(&S.queues[qi].head) : 0;
+    const int tl = mine ? ld_relaxed(&S.queues[qi].tail) : 0;
+    if (__ballot(mine && h < cnt) == 0ull) return -1;
+    bool avail = mine && h < tl && h < cnt;
+    unsigned long long score = 0;
+    if (S.aging_ticks) {
+      int cell = avail ? ld_acquire(&S.ready[off + h]) : -1;
+      avail = cell >= 0;
+      if (avail) score = boost + (wall_clock64() - __hip_atomic_load(&S.ready_ts[cell], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    }
+    const unsigned long long m = __ballot(avail);
+    if (m) {
+      int win = __ffsll((long long)m) - 1;
+      if (S.aging_ticks) {
+        unsigned long long best = avail ? score : 0ull;
+        for (int o = 32; o > 0; o >>= 1) { unsigned long long y = __shfl_xor(best, o, 64); best = y > best ? y : best; }
+        win = __ffsll((long long)__ballot(avail && score == best)) - 1;
+      }
+      int got = -1;
+      if (l == win) {
+        unsigned expect = (unsigned)h;
+        if (__hip_atomic_compare_exchange_strong(&S.queues[qi].head, &expect, expect + 1u, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+          for (;;) {   // the enqueuer reserved this cell before we saw the tail: its store is in flight
+            got = ld_relaxed(&S.ready[off + h]);
+            if (got >= 0 || ld_relaxed(&S.cnt->err_code) != 0) break;
+            __builtin_amdgcn_s_sleep(1);
+          }
+        }
+      }
+      got = __shfl(got, win, 64);
+      if (got >= 0) { fence_acquire(); return got; }
+      continue;   // lost the head to another worker: look again at once
+    }
+    __builtin_amdgcn_s_sleep(1);
+    int fired = 0;
+    if (l == 0 && (polls & 4095) == 4095) fired = stalled(S, since, seen, -1);
+    if (__shfl(fired, 0, 64)) return -1;
   }
 }
 
@@ -181,7 +259,12 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
   MvmTaskDesc& s_desc = s_rec.desc;
   const int t = threadIdx.x;
   for (;;) {
-    if (t == 0) {
+    if (S.tq) {
+      if (wave() == 0) {
+        const int slot = pop_prio(S);
+        if (t == 0) s_slot = ld_relaxed(&S.cnt->err_code) != 0 ? -1 : slot;
+      }
+    } else if (t == 0) {
       const int q = blockIdx.x % S.nq;
       unsigned ticket = add_relaxed(&S.queues[q].head, 1u);
       int slot = -1;
@@ -193,19 +276,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
           if (slot >= 0) break;
           if (ld_relaxed(&S.cnt->err_code) != 0) break;
           __builtin_amdgcn_s_sleep(1);
-          if ((polls & 4095) == 4095) {      // stall check: has any worker finished a task since the last look?
-            int d = 0;
-            for (int w = 0; w < S.grid; ++w) d += ld_relaxed(&S.done_blk[w]);
-            unsigned long long now = wall_clock64();
-            if (d != seen) { seen = d; since = now; }
-            else if (now - since > S.timeout_ticks) {
-              int z = 0;
-              if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_TIMEOUT, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                S.cnt->err_slot = -1; S.cnt->err_a = (int)ticket; S.cnt->err_b = d;
-              }
-              break;
-            }
-          }
+          if ((polls & 4095) == 4095 && stalled(S, since, seen, (int)ticket)) break;
         }
         if (slot >= 0) fence_acquire();   // the enqueuer's release: predecessors' data is visible from here on
       }
@@ -276,6 +347,30 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
             else { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "agent"); release(S, s); }
           }
         }
+        if (S.tq) {   // priority mode: lanes bound for the same queue share one tail reservation, in lane order
+          const int myq = direct ? S.tq[s] : -1;
+          if (direct) {
+            st_relaxed(&S.state[s], 2);
+            if (S.ready_ts) __hip_atomic_store(&S.ready_ts[s], wall_clock64(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          unsigned long long todo = __ballot(direct);
+          while (todo) {
+            const int lead = __ffsll((long long)todo) - 1;
+            const int q = __shfl(myq, lead, 64);
+            const unsigned long long m = __ballot(direct && myq == q);
+            int base_q = 0;
+            if (l == lead) base_q = add_relaxed(&S.queues[q].tail, __popcll(m));
+            base_q = __shfl(base_q, lead, 64);
+            if (direct && myq == q) {
+              const int pos = base_q + __popcll(m & ((1ull << l) - 1ull));
+              if (pos >= S.qcount[q]) queue_overflow(S);
+              else if (S.ready_ts) st_release(&S.ready[S.qoff[q] + pos], s);   // release time before the cell
+              else st_relaxed(&S.ready[S.qoff[q] + pos], s);
+            }
+            todo &= ~m;
+          }
+          continue;
+        }
         const int sq = direct ? s % S.nq : -1;
         int cnt_mine = 0;            // lane q < nq: how many of this round's tasks go to queue q
         for (int q = 0; q < S.nq; ++q) {
@@ -312,10 +407,10 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
     S.indeg[k] = S.tasks[k].indegree; S.state[k] = 0; S.park_next[k] = -1;
     if (S.trace_on) { KvmTrace z = {}; z.ver0 = z.ver1 = -1; S.trace[k] = z; }
   }
-  for (long long k = i; k < (long long)S.nq * S.qcap; k += stride) S.ready[k] = -1;
+  for (long long k = i; k < (long long)S.ncells; k += stride) S.ready[k] = -1;
   for (int k = i; k < S.nvars; k += stride) { S.version[k] = base_versions[k]; S.park_head[k] = -1; }
   for (int k = i; k < S.grid; k += stride) S.done_blk[k] = 0;
-  if (i < S.nq) { KvmQueue z = {}; S.queues[i] = z; }
+  if (i < S.nq * S.nb) { KvmQueue z = {}; S.queues[i] = z; }
   if (i == 0) { KvmCounters z = {}; *S.cnt = z; }
 }
 // Roots (tasks with no predecessors). Roots without a version wait go to fixed cells computed on the host (queue
@@ -325,10 +420,11 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
 __global__ void kvm_seed_kernel(KvmDevState S, const int* roots, const int* root_cell, int nfixed, int nroots, const int* fixed_tail) {
   for (int r = threadIdx.x; r < nfixed; r += blockDim.x) {
     const int t = roots[r];
+    if (S.ready_ts) S.ready_ts[t] = wall_clock64();
     S.ready[root_cell[r]] = t;
     S.state[t] = 2;
   }
-  if (threadIdx.x < S.nq) S.queues[threadIdx.x].tail = fixed_tail[threadIdx.x];
+  for (int q = threadIdx.x; q < S.nq * S.nb; q += blockDim.x) S.queues[q].tail = fixed_tail[q];
   __syncthreads();
   if (threadIdx.x == 0)
     for (int r = nfixed; r < nroots; ++r) release(S, roots[r]);
@@ -399,6 +495,7 @@ struct KvmExec {
   unsigned* d_opmask = nullptr;
   KvmCounters* d_cnt = nullptr; KvmTrace* d_trace = nullptr;
   KvmQueue* d_queues = nullptr; int *d_qcount = nullptr, *d_done_blk = nullptr;
+  int *d_qoff = nullptr, *d_tq = nullptr, *d_bprio = nullptr; unsigned long long* d_ready_ts = nullptr;
   KvmDevState S{};
 };
 
@@ -418,7 +515,7 @@ template <class T> static hipError_t upload(T** dst, const std::vector<T>& v, hi
 extern "C" {
 
 void kvm_config_default(KvmConfig* c) {
-  c->blocks = 0; c->trace_on = 1; c->num_vars = 64; c->timeout_us = 20ull * 1000000ull; c->device = 0;
+  c->blocks = 0; c->trace_on = 1; c->num_vars = 64; c->timeout_us = 20ull * 1000000ull; c->device = 0; c->aging_us = 0;
 }
 
 const char* kvm_last_error(const KvmExec* ex) { return ex ? ex->err.c_str() : g_err.c_str(); }
@@ -427,6 +524,7 @@ KvmExec* kvm_create(const KvmConfig* cfg) {
   KvmConfig c; kvm_config_default(&c);
   if (cfg) c = *cfg;
   if (c.num_vars < 1 || c.num_vars > (1 << 20)) { g_err = "num_vars out of range"; return nullptr; }
+  if (c.aging_us < 0) { g_err = "aging_us must be >= 0"; return nullptr; }
   if (hipSetDevice(c.device) != hipSuccess) { g_err = "hipSetDevice failed"; return nullptr; }
   hipDeviceProp_t p;
   if (hipGetDeviceProperties(&p, c.device) != hipSuccess) { g_err = "hipGetDeviceProperties failed"; return nullptr; }
@@ -446,7 +544,8 @@ void kvm_destroy(KvmExec* ex) {
   for (auto& b : ex->bufs) hipFree(b.p);
   void* ptrs[] = {ex->d_recs, ex->d_tasks, ex->d_succ, ex->d_args, ex->d_bufs, ex->d_indeg, ex->d_ready, ex->d_state, ex->d_park_next,
                   ex->d_version, ex->d_park_head, ex->d_base, ex->d_roots, ex->d_cnt, ex->d_trace, ex->d_queues, ex->d_qcount,
-                  ex->d_done_blk, ex->d_opmask, ex->d_root_cell, ex->d_fixed_tail};
+                  ex->d_done_blk, ex->d_opmask, ex->d_root_cell, ex->d_fixed_tail, ex->d_qoff, ex->d_tq, ex->d_bprio,
+                  ex->d_ready_ts};
   for (void* q : ptrs) if (q) hipFree(q);
   if (ex->ev0) hipEventDestroy(ex->ev0);
   if (ex->ev1) hipEventDestroy(ex->ev1);
@@ -589,13 +688,33 @@ static int do_upload(KvmExec* ex) {
   HIPCK(hipMalloc(&ex->d_indeg, n * sizeof(int)));
   const int nq = std::max(1, std::min(KVM_MAX_QUEUES, ex->grid));
   const int qcap = (n + nq - 1) / nq;
-  std::vector<int> qcount(nq, 0);
-  for (int t = 0; t < n; ++t) ++qcount[t % nq];
-  HIPCK(hipMalloc(&ex->d_ready, (size_t)nq * qcap * sizeof(int)));
+  // Priority buckets: one per distinct priority in the graph, bucket 0 the highest. A graph with one priority and no
+  // aging runs in FIFO mode (queue t % nq, fetch-add tickets); otherwise task t goes to queue (t % nq) * nb + bucket.
+  std::vector<int> prios;
+  for (const MvmTaskDesc& d : ex->tasks) prios.push_back(d.priority);
+  std::sort(prios.begin(), prios.end(), [](int a, int b) { return a > b; });
+  prios.erase(std::unique(prios.begin(), prios.end()), prios.end());
+  const int nb = (int)prios.size();
+  const bool prio_mode = nb > 1 || ex->cfg.aging_us > 0;
+  const int nqb = prio_mode ? nq * nb : nq;
+  std::vector<int> qcount(nqb, 0), qoff(nqb, 0), tq;
+  if (prio_mode) {
+    int bucket_of[KVM_PRIORITIES];
+    for (int b = 0; b < nb; ++b) bucket_of[prios[b]] = b;
+    tq.resize(n);
+    for (int t = 0; t < n; ++t) { tq[t] = (t % nq) * nb + bucket_of[ex->tasks[t].priority]; ++qcount[tq[t]]; }
+    for (int q = 1; q < nqb; ++q) qoff[q] = qoff[q - 1] + qcount[q - 1];
+  } else {
+    for (int t = 0; t < n; ++t) ++qcount[t % nq];
+    for (int q = 0; q < nq; ++q) qoff[q] = q * qcap;
+  }
+  const int ncells = prio_mode ? n : nq * qcap;
+  auto queue_of = [&](int t) { return prio_mode ? tq[t] : t % nq; };
+  HIPCK(hipMalloc(&ex->d_ready, (size_t)ncells * sizeof(int)));
   {   // roots: those without a version wait first (fixed ready cells), then those with one
-    std::vector<int> ordered, cells, tail(nq, 0), waiting;
+    std::vector<int> ordered, cells, tail(nqb, 0), waiting;
     for (int t : ex->roots) {
-      if (ex->tasks[t].wait_var < 0) { const int q = t % nq; ordered.push_back(t); cells.push_back(q * qcap + tail[q]++); }
+      if (ex->tasks[t].wait_var < 0) { const int q = queue_of(t); ordered.push_back(t); cells.push_back(qoff[q] + tail[q]++); }
       else waiting.push_back(t);
     }
     ex->nfixed = (int)ordered.size();
@@ -604,9 +723,15 @@ static int do_upload(KvmExec* ex) {
     HIPCK(upload(&ex->d_root_cell, cells, ex->stream));
     HIPCK(upload(&ex->d_fixed_tail, tail, ex->stream));
   }
-  HIPCK(hipMalloc(&ex->d_queues, nq * sizeof(KvmQueue)));
+  HIPCK(hipMalloc(&ex->d_queues, nqb * sizeof(KvmQueue)));
   HIPCK(hipMalloc(&ex->d_done_blk, ex->grid * sizeof(int)));
   HIPCK(upload(&ex->d_qcount, qcount, ex->stream));
+  HIPCK(upload(&ex->d_qoff, qoff, ex->stream));
+  if (prio_mode) {
+    HIPCK(upload(&ex->d_tq, tq, ex->stream));
+    HIPCK(upload(&ex->d_bprio, prios, ex->stream));
+    if (ex->cfg.aging_us > 0) HIPCK(hipMalloc(&ex->d_ready_ts, n * sizeof(unsigned long long)));
+  }
   HIPCK(hipMalloc(&ex->d_state, n * sizeof(int)));
   HIPCK(hipMalloc(&ex->d_park_next, n * sizeof(int)));
   HIPCK(hipMalloc(&ex->d_version, nv * sizeof(int)));
@@ -621,7 +746,10 @@ static int do_upload(KvmExec* ex) {
   S.version = ex->d_version; S.park_head = ex->d_park_head; S.cnt = ex->d_cnt; S.trace = ex->d_trace;
   S.queues = ex->d_queues; S.qcount = ex->d_qcount; S.done_blk = ex->d_done_blk; S.opmask = ex->d_opmask;
   S.ntasks = n; S.nbufs = (int)ex->bufs.size(); S.nvars = nv; S.trace_on = ex->cfg.trace_on ? 1 : 0;
-  S.nq = nq; S.qcap = qcap; S.grid = ex->grid;
+  S.nq = nq; S.qcap = qcap; S.grid = ex->grid; S.ncells = ncells;
+  S.qoff = ex->d_qoff; S.tq = ex->d_tq; S.bucket_prio = ex->d_bprio; S.ready_ts = ex->d_ready_ts;
+  S.nb = prio_mode ? nb : 1;
+  S.aging_ticks = ex->cfg.aging_us > 0 ? (unsigned long long)ex->cfg.aging_us * 100ull : 0ull;
   S.timeout_ticks = ex->cfg.timeout_us * 100ull;   // wall_clock64 runs at 100 MHz on gfx950
   ex->uploaded = true;
   return 0;

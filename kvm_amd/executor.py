@@ -27,7 +27,7 @@ ERRORS = {0: 'OK', 1: 'BAD_OP', 2: 'BAD_ARITY', 3: 'BAD_BUF_INDEX', 4: 'BAD_BUF'
 
 class KvmConfig(ctypes.Structure):
     _fields_ = [('blocks', ctypes.c_int), ('trace_on', ctypes.c_int), ('num_vars', ctypes.c_int), ('timeout_us', ctypes.c_ulonglong),
-                ('device', ctypes.c_int)]
+                ('device', ctypes.c_int), ('aging_us', ctypes.c_int)]
 
 
 class KvmInit(ctypes.Structure):
@@ -92,11 +92,13 @@ class Executor:
         x = ex.read('logits')
     """
 
-    def __init__(self, num_vars: int = 64, trace: bool = True, timeout_s: float = 20.0, blocks: int = 0, device: int = 0):
+    def __init__(self, num_vars: int = 64, trace: bool = True, timeout_s: float = 20.0, blocks: int = 0, device: int = 0,
+                 aging_us: int = 0):
         L = lib()
         cfg = KvmConfig()
         L.kvm_config_default(ctypes.byref(cfg))
         cfg.num_vars, cfg.trace_on, cfg.timeout_us, cfg.blocks, cfg.device = max(1, num_vars), int(trace), int(timeout_s * 1e6), blocks, device
+        cfg.aging_us = aging_us
         self._h = L.kvm_create(ctypes.byref(cfg))
         if not self._h:
             raise KvmError(f'kvm_create: {L.kvm_last_error(None).decode()}')

@@ -53,9 +53,7 @@ struct KvmRec;
 struct KvmDevState {
   const MvmTaskDesc* tasks;   // [ntasks]
   const KvmRec* recs;         // [ntasks] dispatch records (descriptor, argument words, buffer views)
-  const int32_t* succ;        // [nedges] global task indices
-  const int32_t* args;        // [nargs]
-  const MvmBuf* bufs;         // [nbufs]
+  const int32_t* succ;        // [nedges] global task indices (| KVM_EDGE_DIRECT)
   int* indeg;                 // [ntasks] remaining predecessors
   int* ready;                 // ready cells: queue qi's i-th released task at ready[qoff[qi] + i], -1 until then
   KvmQueue* queues;           // [nq * nb]
@@ -73,8 +71,7 @@ struct KvmDevState {
   int* park_head;             // [nvars] park list heads, -1 empty
   KvmCounters* cnt;
   KvmTrace* trace;            // [ntasks] or null
-  const unsigned* opmask;     // [KVM_OPMASK_IDS] bit k set when argument word k of the operator is a buffer index
-  int ntasks, nbufs, nvars, trace_on, nq, qcap, grid, nb, ncells;
+  int ntasks, nvars, trace_on, nq, qcap, grid, nb, ncells;
   unsigned long long timeout_ticks;   // stall timeout in wall_clock64 ticks (100 MHz)
   unsigned long long aging_ticks;     // wall_clock64 ticks of waiting worth one priority level (0: strict priority)
 };

@@ -475,6 +475,9 @@ static thread_local std::string g_err;
 
 struct BufRec { void* p; int rows, cols, dtype; size_t bytes; };
 
+// What a launch needs besides the device state: base versions to copy in and the root lists of the seed kernel.
+struct LaunchArgs { int* base; const int* roots; const int* root_cell; const int* fixed_tail; int nfixed, nroots; };
+
 struct KvmExec {
   KvmConfig cfg;
   int dev = 0, cus = 0, grid = 0;
@@ -486,16 +489,9 @@ struct KvmExec {
   std::vector<int> base_versions;
   bool uploaded = false, launched = false;
   std::string err;
-  // device memory
-  KvmRec* d_recs = nullptr;
-  MvmTaskDesc* d_tasks = nullptr; int32_t *d_succ = nullptr, *d_args = nullptr; MvmBuf* d_bufs = nullptr;
-  int *d_indeg = nullptr, *d_ready = nullptr, *d_state = nullptr, *d_park_next = nullptr, *d_version = nullptr, *d_park_head = nullptr;
-  int *d_base = nullptr, *d_roots = nullptr, *d_root_cell = nullptr, *d_fixed_tail = nullptr;
-  int nfixed = 0;
-  unsigned* d_opmask = nullptr;
-  KvmCounters* d_cnt = nullptr; KvmTrace* d_trace = nullptr;
-  KvmQueue* d_queues = nullptr; int *d_qcount = nullptr, *d_done_blk = nullptr;
-  int *d_qoff = nullptr, *d_tq = nullptr, *d_bprio = nullptr; unsigned long long* d_ready_ts = nullptr;
+  // device memory of the placed graph (one hipMalloc each, freed by kvm_destroy)
+  std::vector<void*> allocs;
+  struct LaunchArgs L{};
   KvmDevState S{};
 };
 
@@ -503,13 +499,128 @@ struct KvmExec {
 
 static size_t elem_bytes(int dtype) { return dtype == 2 ? 2 : 4; }
 
-template <class T> static hipError_t upload(T** dst, const std::vector<T>& v, hipStream_t s) {
-  size_t bytes = std::max<size_t>(1, v.size()) * sizeof(T);
-  hipError_t e = hipMalloc((void**)dst, bytes);
-  if (e != hipSuccess || v.empty()) return e;
-  e = hipMemcpyAsync(*dst, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice, s);
-  if (e != hipSuccess) return e;
-  return hipStreamSynchronize(s);
+// ---------------------------------------------------------------------------------------------- graph layout
+// The host-side layout of one launch's task graph: dispatch records, device successor edges, ready-queue geometry
+// (FIFO or priority buckets), root cells. Computed once per graph; placed into device memory by place_graph.
+struct GraphPlan {
+  int n = 0, nq = 1, qcap = 1, nb = 1, nqb = 1, ncells = 1, nfixed = 0;
+  bool prio_mode = false;
+  std::vector<int32_t> succ_dev;
+  std::vector<KvmRec> recs;
+  std::vector<int> qcount, qoff, tq, prios, roots, root_cell, fixed_tail;
+};
+
+static void plan_graph(const std::vector<MvmTaskDesc>& tasks, const std::vector<int32_t>& succ, const std::vector<int32_t>& args,
+                       const std::vector<MvmBuf>& table, const std::vector<int32_t>& roots, int grid, int aging_us, GraphPlan& g) {
+  const int n = (int)tasks.size();
+  g.n = n;
+  g.succ_dev = succ;
+  for (auto& e : g.succ_dev) if (tasks[e].indegree == 1 && tasks[e].wait_var < 0) e |= KVM_EDGE_DIRECT;
+  unsigned opmask[KVM_OPMASK_IDS] = {};   // buffer-argument positions of every registry operator
+  for (const kvmv::OpSig& o : kvmv::kRegistry) {
+    if (o.id < 0 || o.id >= KVM_OPMASK_IDS) continue;
+    std::vector<kvmv::ArgInfo> a = kvmv::parse_sig(o.sig);
+    for (size_t k = 0; k < a.size() && k < 32; ++k) if (a[k].type == 0) opmask[o.id] |= 1u << k;
+  }
+  g.recs.assign(n, KvmRec{});
+  for (int i = 0; i < n; ++i) {   // dispatch records
+    KvmRec& r = g.recs[i];
+    std::memset(&r, 0, sizeof(r));
+    const MvmTaskDesc& d = tasks[i];
+    r.desc = d;
+    const unsigned mask = (unsigned)d.op_id < KVM_OPMASK_IDS ? opmask[d.op_id] : 0u;
+    for (int k = 0; k < d.args_words && k < KVM_MAX_ARGS; ++k) {
+      const int w = args[d.args_off + k];
+      r.args[k] = w;
+      if (w >= 0 && ((mask >> k) & 1u)) r.views[k] = View{table[w].p, table[w].rows, table[w].cols, table[w].dtype};
+    }
+  }
+  g.nq = std::max(1, std::min(KVM_MAX_QUEUES, grid));
+  g.qcap = (n + g.nq - 1) / g.nq;
+  // Priority buckets: one per distinct priority in the graph, bucket 0 the highest. A graph with one priority and no
+  // aging runs in FIFO mode (queue t % nq, fetch-add tickets); otherwise task t goes to queue (t % nq) * nb + bucket.
+  g.prios.clear();
+  for (const MvmTaskDesc& d : tasks) g.prios.push_back(d.priority);
+  std::sort(g.prios.begin(), g.prios.end(), [](int a, int b) { return a > b; });
+  g.prios.erase(std::unique(g.prios.begin(), g.prios.end()), g.prios.end());
+  g.prio_mode = g.prios.size() > 1 || aging_us > 0;
+  g.nb = g.prio_mode ? (int)g.prios.size() : 1;
+  g.nqb = g.nq * g.nb;
+  g.qcount.assign(g.nqb, 0); g.qoff.assign(g.nqb, 0); g.tq.clear();
+  if (g.prio_mode) {
+    int bucket_of[KVM_PRIORITIES];
+    for (int b = 0; b < g.nb; ++b) bucket_of[g.prios[b]] = b;
+    g.tq.resize(n);
+    for (int t = 0; t < n; ++t) { g.tq[t] = (t % g.nq) * g.nb + bucket_of[tasks[t].priority]; ++g.qcount[g.tq[t]]; }
+    for (int q = 1; q < g.nqb; ++q) g.qoff[q] = g.qoff[q - 1] + g.qcount[q - 1];
+  } else {
+    for (int t = 0; t < n; ++t) ++g.qcount[t % g.nq];
+    for (int q = 0; q < g.nq; ++q) g.qoff[q] = q * g.qcap;
+  }
+  g.ncells = g.prio_mode ? n : g.nq * g.qcap;
+  // roots: those without a version wait first (fixed ready cells, index order per queue), then those with one
+  g.roots.clear(); g.root_cell.clear(); g.fixed_tail.assign(g.nqb, 0);
+  std::vector<int> waiting;
+  for (int t : roots) {
+    if (tasks[t].wait_var < 0) {
+      const int q = g.prio_mode ? g.tq[t] : t % g.nq;
+      g.roots.push_back(t); g.root_cell.push_back(g.qoff[q] + g.fixed_tail[q]++);
+    } else waiting.push_back(t);
+  }
+  g.nfixed = (int)g.roots.size();
+  g.roots.insert(g.roots.end(), waiting.begin(), waiting.end());
+}
+
+// Places a planned graph into device memory obtained from `alloc(bytes)` (256-byte aligned, nullptr on failure),
+// copies the host arrays in on `st` and waits for the copies; fills the device state and the launch arguments.
+// With copy = false nothing is copied (a sizing pass over a counting allocator).
+template <class Alloc>
+static int place_graph(const GraphPlan& g, const std::vector<MvmTaskDesc>& tasks, int nv, int grid, bool trace, int aging_us,
+                       unsigned long long timeout_us, Alloc&& alloc, hipStream_t st, KvmDevState& S, LaunchArgs& L, std::string& err,
+                       bool copy = true) {
+  hipError_t e = hipSuccess;
+  auto put = [&](const void* host, size_t bytes) -> void* {
+    void* d = alloc(std::max<size_t>(bytes, 4));
+    if (!d) { if (err.empty()) err = "device memory for the task graph"; return nullptr; }
+    if (copy && host && bytes && e == hipSuccess) e = hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, st);
+    return d;
+  };
+  auto vec = [&](const auto& v) { return put(v.data(), v.size() * sizeof(v[0])); };
+  const int n = g.n;
+  S = KvmDevState{};
+  S.recs = (const KvmRec*)vec(g.recs);
+  S.tasks = (const MvmTaskDesc*)vec(tasks);
+  S.succ = (const int32_t*)vec(g.succ_dev);
+  S.indeg = (int*)put(nullptr, n * sizeof(int));
+  S.ready = (int*)put(nullptr, (size_t)g.ncells * sizeof(int));
+  S.queues = (KvmQueue*)put(nullptr, g.nqb * sizeof(KvmQueue));
+  S.qcount = (const int*)vec(g.qcount);
+  S.qoff = (const int*)vec(g.qoff);
+  if (g.prio_mode) {
+    S.tq = (const int*)vec(g.tq);
+    S.bucket_prio = (const int*)vec(g.prios);
+    if (aging_us > 0) S.ready_ts = (unsigned long long*)put(nullptr, n * sizeof(unsigned long long));
+  }
+  S.done_blk = (int*)put(nullptr, grid * sizeof(int));
+  S.state = (int*)put(nullptr, n * sizeof(int));
+  S.park_next = (int*)put(nullptr, n * sizeof(int));
+  S.version = (int*)put(nullptr, nv * sizeof(int));
+  S.park_head = (int*)put(nullptr, nv * sizeof(int));
+  S.cnt = (KvmCounters*)put(nullptr, sizeof(KvmCounters));
+  if (trace) S.trace = (KvmTrace*)put(nullptr, n * sizeof(KvmTrace));
+  L.base = (int*)put(nullptr, nv * sizeof(int));
+  L.roots = (const int*)vec(g.roots);
+  L.root_cell = (const int*)vec(g.root_cell);
+  L.fixed_tail = (const int*)vec(g.fixed_tail);
+  L.nfixed = g.nfixed; L.nroots = (int)g.roots.size();
+  if (!err.empty()) return KVM_STATUS_TOO_BIG;
+  if (copy && e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) { err = std::string("graph upload: ") + hipGetErrorString(e); return KVM_STATUS_HIP_ERROR; }
+  S.ntasks = n; S.nvars = nv; S.trace_on = trace ? 1 : 0;
+  S.nq = g.nq; S.qcap = g.qcap; S.grid = grid; S.ncells = g.ncells; S.nb = g.nb;
+  S.aging_ticks = aging_us > 0 ? (unsigned long long)aging_us * 100ull : 0ull;
+  S.timeout_ticks = timeout_us * 100ull;   // wall_clock64 runs at 100 MHz on gfx950
+  return 0;
 }
 
 extern "C" {
@@ -542,11 +653,7 @@ void kvm_destroy(KvmExec* ex) {
   hipSetDevice(ex->dev);
   if (ex->stream) hipStreamSynchronize(ex->stream);
   for (auto& b : ex->bufs) hipFree(b.p);
-  void* ptrs[] = {ex->d_recs, ex->d_tasks, ex->d_succ, ex->d_args, ex->d_bufs, ex->d_indeg, ex->d_ready, ex->d_state, ex->d_park_next,
-                  ex->d_version, ex->d_park_head, ex->d_base, ex->d_roots, ex->d_cnt, ex->d_trace, ex->d_queues, ex->d_qcount,
-                  ex->d_done_blk, ex->d_opmask, ex->d_root_cell, ex->d_fixed_tail, ex->d_qoff, ex->d_tq, ex->d_bprio,
-                  ex->d_ready_ts};
-  for (void* q : ptrs) if (q) hipFree(q);
+  for (void* q : ex->allocs) hipFree(q);
   if (ex->ev0) hipEventDestroy(ex->ev0);
   if (ex->ev1) hipEventDestroy(ex->ev1);
   if (ex->stream) hipStreamDestroy(ex->stream);
@@ -653,117 +760,36 @@ int kvm_submit(KvmExec* ex, const MvmTaskDesc* tasks, int ntasks, const int32_t*
 
 static int do_upload(KvmExec* ex) {
   if (ex->tasks.empty()) { ex->err = "nothing submitted"; return KVM_STATUS_INVALID; }
-  int n = (int)ex->tasks.size(), nv = (int)ex->base_versions.size();
   std::vector<MvmBuf> table(ex->bufs.size());
   for (size_t i = 0; i < table.size(); ++i) table[i] = MvmBuf{ex->bufs[i].p, ex->bufs[i].rows, ex->bufs[i].cols, ex->bufs[i].cols, ex->bufs[i].dtype, {0, 0}};
-  HIPCK(upload(&ex->d_tasks, ex->tasks, ex->stream));
-  std::vector<int32_t> succ_dev(ex->succ);
-  for (auto& e : succ_dev) if (ex->tasks[e].indegree == 1 && ex->tasks[e].wait_var < 0) e |= KVM_EDGE_DIRECT;
-  HIPCK(upload(&ex->d_succ, succ_dev, ex->stream));
-  HIPCK(upload(&ex->d_args, ex->args, ex->stream));
-  HIPCK(upload(&ex->d_bufs, table, ex->stream));
-  std::vector<unsigned> opmask(KVM_OPMASK_IDS, 0u);     // buffer-argument positions of every registry operator
-  for (const kvmv::OpSig& o : kvmv::kRegistry) {
-    if (o.id < 0 || o.id >= KVM_OPMASK_IDS) continue;
-    std::vector<kvmv::ArgInfo> a = kvmv::parse_sig(o.sig);
-    for (size_t k = 0; k < a.size() && k < 32; ++k) if (a[k].type == 0) opmask[o.id] |= 1u << k;
-  }
-  HIPCK(upload(&ex->d_opmask, opmask, ex->stream));
-  {   // dispatch records
-    std::vector<KvmRec> recs(n);
-    for (int i = 0; i < n; ++i) {
-      KvmRec& r = recs[i];
-      std::memset(&r, 0, sizeof(r));
-      const MvmTaskDesc& d = ex->tasks[i];
-      r.desc = d;
-      const unsigned mask = (unsigned)d.op_id < KVM_OPMASK_IDS ? opmask[d.op_id] : 0u;
-      for (int k = 0; k < d.args_words && k < KVM_MAX_ARGS; ++k) {
-        const int w = ex->args[d.args_off + k];
-        r.args[k] = w;
-        if (w >= 0 && ((mask >> k) & 1u)) r.views[k] = View{table[w].p, table[w].rows, table[w].cols, table[w].dtype};
-      }
-    }
-    HIPCK(upload(&ex->d_recs, recs, ex->stream));
-  }
-  HIPCK(hipMalloc(&ex->d_indeg, n * sizeof(int)));
-  const int nq = std::max(1, std::min(KVM_MAX_QUEUES, ex->grid));
-  const int qcap = (n + nq - 1) / nq;
-  // Priority buckets: one per distinct priority in the graph, bucket 0 the highest. A graph with one priority and no
-  // aging runs in FIFO mode (queue t % nq, fetch-add tickets); otherwise task t goes to queue (t % nq) * nb + bucket.
-  std::vector<int> prios;
-  for (const MvmTaskDesc& d : ex->tasks) prios.push_back(d.priority);
-  std::sort(prios.begin(), prios.end(), [](int a, int b) { return a > b; });
-  prios.erase(std::unique(prios.begin(), prios.end()), prios.end());
-  const int nb = (int)prios.size();
-  const bool prio_mode = nb > 1 || ex->cfg.aging_us > 0;
-  const int nqb = prio_mode ? nq * nb : nq;
-  std::vector<int> qcount(nqb, 0), qoff(nqb, 0), tq;
-  if (prio_mode) {
-    int bucket_of[KVM_PRIORITIES];
-    for (int b = 0; b < nb; ++b) bucket_of[prios[b]] = b;
-    tq.resize(n);
-    for (int t = 0; t < n; ++t) { tq[t] = (t % nq) * nb + bucket_of[ex->tasks[t].priority]; ++qcount[tq[t]]; }
-    for (int q = 1; q < nqb; ++q) qoff[q] = qoff[q - 1] + qcount[q - 1];
-  } else {
-    for (int t = 0; t < n; ++t) ++qcount[t % nq];
-    for (int q = 0; q < nq; ++q) qoff[q] = q * qcap;
-  }
-  const int ncells = prio_mode ? n : nq * qcap;
-  auto queue_of = [&](int t) { return prio_mode ? tq[t] : t % nq; };
-  HIPCK(hipMalloc(&ex->d_ready, (size_t)ncells * sizeof(int)));
-  {   // roots: those without a version wait first (fixed ready cells), then those with one
-    std::vector<int> ordered, cells, tail(nqb, 0), waiting;
-    for (int t : ex->roots) {
-      if (ex->tasks[t].wait_var < 0) { const int q = queue_of(t); ordered.push_back(t); cells.push_back(qoff[q] + tail[q]++); }
-      else waiting.push_back(t);
-    }
-    ex->nfixed = (int)ordered.size();
-    ordered.insert(ordered.end(), waiting.begin(), waiting.end());
-    HIPCK(upload(&ex->d_roots, ordered, ex->stream));
-    HIPCK(upload(&ex->d_root_cell, cells, ex->stream));
-    HIPCK(upload(&ex->d_fixed_tail, tail, ex->stream));
-  }
-  HIPCK(hipMalloc(&ex->d_queues, nqb * sizeof(KvmQueue)));
-  HIPCK(hipMalloc(&ex->d_done_blk, ex->grid * sizeof(int)));
-  HIPCK(upload(&ex->d_qcount, qcount, ex->stream));
-  HIPCK(upload(&ex->d_qoff, qoff, ex->stream));
-  if (prio_mode) {
-    HIPCK(upload(&ex->d_tq, tq, ex->stream));
-    HIPCK(upload(&ex->d_bprio, prios, ex->stream));
-    if (ex->cfg.aging_us > 0) HIPCK(hipMalloc(&ex->d_ready_ts, n * sizeof(unsigned long long)));
-  }
-  HIPCK(hipMalloc(&ex->d_state, n * sizeof(int)));
-  HIPCK(hipMalloc(&ex->d_park_next, n * sizeof(int)));
-  HIPCK(hipMalloc(&ex->d_version, nv * sizeof(int)));
-  HIPCK(hipMalloc(&ex->d_park_head, nv * sizeof(int)));
-  HIPCK(hipMalloc(&ex->d_base, nv * sizeof(int)));
-  HIPCK(hipMalloc(&ex->d_cnt, sizeof(KvmCounters)));
-  if (ex->cfg.trace_on) HIPCK(hipMalloc(&ex->d_trace, n * sizeof(KvmTrace)));
-  KvmDevState& S = ex->S;
-  S.recs = ex->d_recs;
-  S.tasks = ex->d_tasks; S.succ = ex->d_succ; S.args = ex->d_args; S.bufs = ex->d_bufs;
-  S.indeg = ex->d_indeg; S.ready = ex->d_ready; S.state = ex->d_state; S.park_next = ex->d_park_next;
-  S.version = ex->d_version; S.park_head = ex->d_park_head; S.cnt = ex->d_cnt; S.trace = ex->d_trace;
-  S.queues = ex->d_queues; S.qcount = ex->d_qcount; S.done_blk = ex->d_done_blk; S.opmask = ex->d_opmask;
-  S.ntasks = n; S.nbufs = (int)ex->bufs.size(); S.nvars = nv; S.trace_on = ex->cfg.trace_on ? 1 : 0;
-  S.nq = nq; S.qcap = qcap; S.grid = ex->grid; S.ncells = ncells;
-  S.qoff = ex->d_qoff; S.tq = ex->d_tq; S.bucket_prio = ex->d_bprio; S.ready_ts = ex->d_ready_ts;
-  S.nb = prio_mode ? nb : 1;
-  S.aging_ticks = ex->cfg.aging_us > 0 ? (unsigned long long)ex->cfg.aging_us * 100ull : 0ull;
-  S.timeout_ticks = ex->cfg.timeout_us * 100ull;   // wall_clock64 runs at 100 MHz on gfx950
+  GraphPlan g;
+  plan_graph(ex->tasks, ex->succ, ex->args, table, ex->roots, ex->grid, ex->cfg.aging_us, g);
+  auto alloc = [ex](size_t bytes) -> void* {
+    void* d = nullptr;
+    if (hipMalloc(&d, bytes) != hipSuccess) return nullptr;
+    ex->allocs.push_back(d);
+    return d;
+  };
+  ex->err.clear();
+  const int rc = place_graph(g, ex->tasks, (int)ex->base_versions.size(), ex->grid, ex->cfg.trace_on != 0, ex->cfg.aging_us,
+                             ex->cfg.timeout_us, alloc, ex->stream, ex->S, ex->L, ex->err);
+  if (rc) return rc == KVM_STATUS_TOO_BIG ? KVM_STATUS_HIP_ERROR : rc;
   ex->uploaded = true;
   return 0;
 }
 
+// Reset of the scheduler state, root seeding and the persistent kernel, on one stream.
+static void launch_graph(const KvmDevState& S, const LaunchArgs& L, int grid, hipStream_t st, hipEvent_t before_exec, hipEvent_t after_exec) {
+  hipLaunchKernelGGL(kvm_reset_kernel, dim3(std::min(1024, (S.ntasks + 255) / 256 + 1)), dim3(256), 0, st, S, (const int*)L.base);
+  hipLaunchKernelGGL(kvm_seed_kernel, dim3(1), dim3(1024), 0, st, S, L.roots, L.root_cell, L.nfixed, L.nroots, L.fixed_tail);
+  if (before_exec) hipEventRecord(before_exec, st);
+  hipLaunchKernelGGL(kvm_exec_kernel, dim3(grid), dim3(KVM_THREADS), 0, st, S);
+  if (after_exec) hipEventRecord(after_exec, st);
+}
+
 static int launch_once(KvmExec* ex, hipEvent_t before_exec = nullptr, hipEvent_t after_exec = nullptr) {
-  KvmDevState& S = ex->S;
-  HIPCK(hipMemcpyAsync(ex->d_base, ex->base_versions.data(), ex->base_versions.size() * sizeof(int), hipMemcpyHostToDevice, ex->stream));
-  hipLaunchKernelGGL(kvm_reset_kernel, dim3(std::min(1024, (S.ntasks + 255) / 256 + 1)), dim3(256), 0, ex->stream, S, (const int*)ex->d_base);
-  hipLaunchKernelGGL(kvm_seed_kernel, dim3(1), dim3(1024), 0, ex->stream, S, (const int*)ex->d_roots, (const int*)ex->d_root_cell,
-                     ex->nfixed, (int)ex->roots.size(), (const int*)ex->d_fixed_tail);
-  if (before_exec) HIPCK(hipEventRecord(before_exec, ex->stream));
-  hipLaunchKernelGGL(kvm_exec_kernel, dim3(ex->grid), dim3(KVM_THREADS), 0, ex->stream, S);
-  if (after_exec) HIPCK(hipEventRecord(after_exec, ex->stream));
+  HIPCK(hipMemcpyAsync(ex->L.base, ex->base_versions.data(), ex->base_versions.size() * sizeof(int), hipMemcpyHostToDevice, ex->stream));
+  launch_graph(ex->S, ex->L, ex->grid, ex->stream, before_exec, after_exec);
   HIPCK(hipGetLastError());
   return 0;
 }
@@ -833,10 +859,10 @@ int kvm_finish(KvmExec* ex, KvmResult* res) {
   HIPCK(hipStreamSynchronize(ex->stream));
   KvmCounters c{};
   int done = 0;
-  if (ex->d_cnt) {
-    HIPCK(hipMemcpy(&c, ex->d_cnt, sizeof c, hipMemcpyDeviceToHost));
+  if (ex->S.cnt) {
+    HIPCK(hipMemcpy(&c, ex->S.cnt, sizeof c, hipMemcpyDeviceToHost));
     std::vector<int> per(ex->grid);
-    HIPCK(hipMemcpy(per.data(), ex->d_done_blk, ex->grid * sizeof(int), hipMemcpyDeviceToHost));
+    HIPCK(hipMemcpy(per.data(), ex->S.done_blk, ex->grid * sizeof(int), hipMemcpyDeviceToHost));
     for (int d : per) done += d;
   }
   float ms = 0.f;
@@ -850,16 +876,16 @@ int kvm_finish(KvmExec* ex, KvmResult* res) {
 }
 
 int kvm_versions(KvmExec* ex, int32_t* out, int n) {
-  if (!ex->d_version || n > (int)ex->base_versions.size()) { ex->err = "kvm_versions: not started or n too large"; return KVM_STATUS_INVALID; }
+  if (!ex->S.version || n > (int)ex->base_versions.size()) { ex->err = "kvm_versions: not started or n too large"; return KVM_STATUS_INVALID; }
   HIPCK(hipStreamSynchronize(ex->stream));
-  HIPCK(hipMemcpy(out, ex->d_version, n * sizeof(int), hipMemcpyDeviceToHost));
+  HIPCK(hipMemcpy(out, ex->S.version, n * sizeof(int), hipMemcpyDeviceToHost));
   return 0;
 }
 
 int kvm_trace(KvmExec* ex, KvmTrace* out, int n) {
-  if (!ex->d_trace || n > (int)ex->tasks.size()) { ex->err = "kvm_trace: tracing off or n too large"; return KVM_STATUS_INVALID; }
+  if (!ex->S.trace || n > (int)ex->tasks.size()) { ex->err = "kvm_trace: tracing off or n too large"; return KVM_STATUS_INVALID; }
   HIPCK(hipStreamSynchronize(ex->stream));
-  HIPCK(hipMemcpy(out, ex->d_trace, n * sizeof(KvmTrace), hipMemcpyDeviceToHost));
+  HIPCK(hipMemcpy(out, ex->S.trace, n * sizeof(KvmTrace), hipMemcpyDeviceToHost));
   return 0;
 }
 

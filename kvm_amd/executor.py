@@ -287,3 +287,4 @@ def copy_probe(nbytes: int) -> None:
     """One plain device copy of nbytes (kvm_copy_probe): the reference dispatch for HBM byte counters."""
     if lib().kvm_copy_probe(int(nbytes)) < 0:
         raise RuntimeError(lib().kvm_last_error(None).decode())
+

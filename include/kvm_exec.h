@@ -120,6 +120,21 @@ int kvm_seeded_fill_test(unsigned long long seed, long long n, int draws, float 
 // WRITE_SIZE) against the executor's own dispatches.
 int kvm_copy_probe(long long bytes);
 
+// Device scratch of kvm_run_noalloc: one array per GPU the library runs on, held until the process ends.
+#define KVM_NOALLOC_SCRATCH_BYTES (32u << 20)
+// Runs one bundle to completion on the current HIP device without allocating device memory: no hipMalloc, hipFree or
+// allocating library call. No counterpart in the reference; for callers that cannot allocate (code under HIP graph
+// capture, serving loops, harnesses that forbid it). The caller owns the buffers: `bufs[i].p` are device addresses,
+// rows/cols/dtype as in kvm_add_buffer. `versions` holds the nvars base versions on entry and the final versions on
+// return. The scheduler state, queues and task graph live in the library's KVM_NOALLOC_SCRATCH_BYTES of scratch: a
+// graph that needs more is refused with KVM_STATUS_TOO_BIG before anything runs. Validation as kvm_submit; tracing off.
+// blocks 0 = one workgroup per CU; `stream` a hipStream_t or NULL (the null stream). Synchronous: returns after the
+// run with `res` filled (kernel_ms 0). Every call on one GPU shares that GPU's scratch and clears what must start at
+// zero; calls from one process are serialised per device, calls that overlap on one GPU from elsewhere would race.
+int kvm_run_noalloc(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs,
+                    const MvmBuf* bufs, int nbufs, int32_t* versions, int nvars, int blocks, unsigned long long timeout_us,
+                    void* stream, KvmResult* res, char* err, int errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <mutex>
 #include <vector>
 #include "common.h"
 #include "ops_basic.h"
@@ -920,6 +921,85 @@ int kvm_copy_probe(long long bytes) {
   hipError_t e = hipDeviceSynchronize();
   hipFree(a); hipFree(b);
   if (e != hipSuccess) { g_err = hipGetErrorString(e); return KVM_STATUS_HIP_ERROR; }
+  return 0;
+}
+
+// ---------------------------------------------------------------------------------------------- allocation-free run
+// All device memory of kvm_run_noalloc's scheduler state and task graph: one file-scope array per GPU, held until the
+// process ends. In host code `scratch` only names the symbol; its device address comes from hipGetSymbolAddress, once
+// per device, and only that address is ever passed to kernels or copies.
+static __device__ __align__(256) unsigned char scratch[KVM_NOALLOC_SCRATCH_BYTES];
+#define KVM_MAX_DEVICES 64
+static void* g_scratch_ptr[KVM_MAX_DEVICES];
+static int g_scratch_cus[KVM_MAX_DEVICES];
+static std::mutex g_scratch_mu[KVM_MAX_DEVICES];
+
+static int scratch_setup(int dev, std::string& err) {
+  if (g_scratch_ptr[dev]) return 0;
+  void* ptr = nullptr;
+  hipError_t e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ptr) { err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e); return KVM_STATUS_HIP_ERROR; }
+  int cus = 0;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess || cus < 1) { err = "hipDeviceGetAttribute(multiprocessor count) failed"; return KVM_STATUS_HIP_ERROR; }
+  g_scratch_cus[dev] = cus;
+  g_scratch_ptr[dev] = ptr;
+  return 0;
+}
+
+int kvm_run_noalloc(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs,
+                    const MvmBuf* bufs, int nbufs, int32_t* versions, int nvars, int blocks, unsigned long long timeout_us,
+                    void* stream, KvmResult* res, char* errbuf, int errlen) {
+  std::string err;
+  auto fail = [&](int rc) { if (errbuf && errlen > 0) snprintf(errbuf, errlen, "%s", err.c_str()); return rc; };
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= KVM_MAX_DEVICES) { err = "no current HIP device"; return fail(KVM_STATUS_HIP_ERROR); }
+  if (ntasks < 1 || nedges < 0 || nargs < 0 || nbufs < 0 || nvars < 1 || !versions || blocks < 0) { err = "bad sizes"; return fail(KVM_STATUS_INVALID); }
+  if (!kvm_validate_bundle(tasks, ntasks, succ, nedges, args, nargs, bufs, nbufs, nvars, &err)) return fail(KVM_STATUS_INVALID);
+  for (int i = 0; i < nbufs; ++i) if (!bufs[i].p) { err = "buffer " + std::to_string(i) + " has no device address"; return fail(KVM_STATUS_INVALID); }
+  std::lock_guard<std::mutex> lock(g_scratch_mu[dev]);   // calls on one device in this process never overlap
+  if (int rc = scratch_setup(dev, err)) return fail(rc);
+  const int grid = blocks > 0 ? blocks : g_scratch_cus[dev];
+  std::vector<MvmTaskDesc> tv(tasks, tasks + ntasks);
+  std::vector<int32_t> sv(succ, succ + nedges), av(args, args + nargs), roots;
+  for (int i = 0; i < ntasks; ++i) { tv[i].reserved0 = 0; if (tv[i].indegree == 0) roots.push_back(i); }
+  std::vector<MvmBuf> table(bufs, bufs + nbufs);
+  GraphPlan g;
+  plan_graph(tv, sv, av, table, roots, grid, 0, g);
+  unsigned char* base = (unsigned char*)g_scratch_ptr[dev];
+  size_t used = 0;
+  auto bump = [&](size_t bytes) -> void* {
+    const size_t at = (used + 255) & ~(size_t)255;
+    if (at + bytes > (size_t)KVM_NOALLOC_SCRATCH_BYTES) return nullptr;
+    used = at + bytes;
+    return base + at;
+  };
+  KvmDevState S; LaunchArgs L;
+  hipStream_t st = (hipStream_t)stream;
+  int rc = place_graph(g, tv, nvars, grid, false, 0, timeout_us, bump, st, S, L, err, false);   // sizing pass
+  if (rc == KVM_STATUS_TOO_BIG) {
+    err = "task graph needs more than the " + std::to_string(KVM_NOALLOC_SCRATCH_BYTES >> 20) + " MiB of kvm_run_noalloc's device scratch";
+    return fail(KVM_STATUS_TOO_BIG);
+  }
+  used = 0;
+  if ((rc = place_graph(g, tv, nvars, grid, false, 0, timeout_us, bump, st, S, L, err))) return fail(rc);
+  hipError_t e = hipMemcpyAsync(L.base, versions, nvars * sizeof(int), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) { launch_graph(S, L, grid, st, nullptr, nullptr); e = hipGetLastError(); }
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  KvmCounters c{};
+  std::vector<int> per(grid);
+  if (e == hipSuccess) e = hipMemcpyAsync(&c, S.cnt, sizeof c, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(per.data(), S.done_blk, grid * sizeof(int), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(versions, S.version, nvars * sizeof(int), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) { err = std::string("kvm_run_noalloc: ") + hipGetErrorString(e); return fail(KVM_STATUS_HIP_ERROR); }
+  int done = 0;
+  for (int d : per) done += d;
+  if (res) {
+    res->err_code = c.err_code; res->err_slot = c.err_slot; res->err_a = c.err_a; res->err_b = c.err_b;
+    res->done = done; res->admitted = ntasks; res->grid = grid; res->kernel_ms = 0.f;
+  }
+  if (c.err_code) { err = "device error " + std::to_string(c.err_code) + " at task " + std::to_string(c.err_slot); return fail(KVM_STATUS_DEVICE_ERROR); }
   return 0;
 }
 

@@ -72,6 +72,7 @@ def lib():
             'kvm_validate': (I, [P, I, P, I, P, I, P, I, I, ctypes.c_char_p, I]),
             'kvm_seeded_fill_test': (I, [ctypes.c_ulonglong, ctypes.c_longlong, I, ctypes.c_float, ctypes.c_float, P]),
             'kvm_copy_probe': (I, [ctypes.c_longlong]),
+            'kvm_run_noalloc': (I, [P, I, P, I, P, I, P, I, P, I, I, ctypes.c_ulonglong, P, P, ctypes.c_char_p, I]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -288,3 +289,23 @@ def copy_probe(nbytes: int) -> None:
     if lib().kvm_copy_probe(int(nbytes)) < 0:
         raise RuntimeError(lib().kvm_last_error(None).decode())
 
+
+def run_noalloc(b: bl.LoadedBundle, buffer_ptrs: list[int], versions: list[int], blocks: int = 0, timeout_s: float = 20.0):
+    """kvm_run_noalloc: runs bundle `b` on caller-owned device buffers (device addresses in metadata buffer order) with
+    no device allocation. Returns (result dict, final versions)."""
+    meta = b.metadata
+    bufs = (MvmBuf * max(1, len(meta['buffers'])))()
+    for i, (m, p) in enumerate(zip(meta['buffers'], buffer_ptrs)):
+        bufs[i] = MvmBuf(p, m['rows'], m['cols'], m['cols'], m['dtype'])
+    t = np.ascontiguousarray(b.tasks, np.int32)
+    s = np.ascontiguousarray(b.succ, np.int32) if b.succ.size else np.zeros(1, np.int32)
+    a = np.ascontiguousarray(b.args, np.int32) if b.args.size else np.zeros(1, np.int32)
+    ver = np.array(list(versions) or [0], np.int32)
+    r = KvmResult()
+    err = ctypes.create_string_buffer(512)
+    rc = lib().kvm_run_noalloc(t.ctypes.data, t.shape[0], s.ctypes.data, int(b.succ.size), a.ctypes.data, int(b.args.size), bufs,
+                               len(meta['buffers']), ver.ctypes.data, ver.size, blocks, int(timeout_s * 1e6), None,
+                               ctypes.byref(r), err, 512)
+    res = {'rc': rc, 'err': err.value.decode(), 'err_code': r.err_code, 'err_slot': r.err_slot, 'done': r.done,
+           'admitted': r.admitted, 'grid': r.grid}
+    return res, ver.tolist()

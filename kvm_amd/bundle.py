@@ -43,9 +43,10 @@ def load(src) -> LoadedBundle:
 def bf16_round(x: np.ndarray) -> np.ndarray:
     """float32 -> nearest-even bfloat16 value, as float32 (inf/nan kept)."""
     x = np.ascontiguousarray(x, np.float32)
-    u = x.view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
-    return np.where(np.isfinite(x), r, x).astype(np.float32)
+    u = x.view(np.uint32)
+    # uint32 arithmetic: only non-finite inputs (|u| near 0xFFFFFFFF) can wrap, and those are kept as they are below
+    r = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)).view(np.float32)
+    return np.where(np.isfinite(x), r, x)
 
 
 def bf16_bits(x: np.ndarray) -> np.ndarray:

@@ -55,7 +55,9 @@ class GPTConfig:
 
     @staticmethod
     def gpt355m(**kw):
-        return GPTConfig(layers=24, d=1024, heads=16, ffn=4096, dtype='f32', **kw)
+        base = dict(layers=24, d=1024, heads=16, ffn=4096, dtype='f32')
+        base.update(kw)
+        return GPTConfig(**base)
 
     @staticmethod
     def tiny(**kw):
@@ -119,6 +121,11 @@ class Deps:
         return out
 
     def record(self, task, reads, writes):
+        """Accesses are kept per row bucket, clipped to the bucket's rows. A write subtracts its rectangle from every
+        older access it overlaps (up to four remainder pieces stay): later tasks touching the overlap are ordered after
+        the writer, which is ordered after those accesses, so only the uncovered remainders still need edges of their
+        own. Without the subtraction, reads that chunked writes only partly cover (a GEMM tile's weight columns against
+        an optimizer's row chunks) would pile up over training steps, and every later write would depend on them all."""
         for name, _ in writes:
             self.writers.setdefault(name, []).append(task)
             self.gen[name] = self.gen.get(name, 0) + 1
@@ -128,9 +135,26 @@ class Deps:
                 bk = self.acc.setdefault(name, {})
                 for b in range(r0 // RB, (r1 - 1) // RB + 1):
                     lst = bk.setdefault(b, [])
-                    if kind:   # a write covering an older access of the same rows/cols makes it redundant
-                        lst[:] = [x for x in lst if not (r0 <= x[0] and x[1] <= r1 and c0 <= x[2] and x[3] <= c1)]
-                    lst.append((r0, r1, c0, c1, task, kind))
+                    q0, q1 = max(r0, b * RB), min(r1, (b + 1) * RB)
+                    if kind:
+                        keep = []
+                        for x in lst:
+                            a0, a1, d0, d1 = x[:4]
+                            if not (a0 < q1 and q0 < a1 and d0 < c1 and c0 < d1):
+                                keep.append(x)
+                                continue
+                            t, w = x[4], x[5]
+                            if a0 < q0:
+                                keep.append((a0, q0, d0, d1, t, w))
+                            if q1 < a1:
+                                keep.append((q1, a1, d0, d1, t, w))
+                            m0, m1 = max(a0, q0), min(a1, q1)
+                            if d0 < c0:
+                                keep.append((m0, m1, d0, c0, t, w))
+                            if c1 < d1:
+                                keep.append((m0, m1, c1, d1, t, w))
+                        lst[:] = keep
+                    lst.append((q0, q1, c0, c1, task, kind))
 
 
 class GPTBuilder:

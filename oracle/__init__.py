@@ -40,7 +40,11 @@ def lib():
         _lib.orc_run.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P,
                                  ctypes.c_int, P, P, ctypes.c_int, P, ctypes.c_char_p, ctypes.c_int]
         _lib.orc_run.restype = ctypes.c_int
+        _lib.orc_run_mt.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P,
+                                    ctypes.c_int, P, P, P, ctypes.c_int, ctypes.c_char_p, ctypes.c_int]
+        _lib.orc_run_mt.restype = ctypes.c_int
         _lib.orc_seeded.argtypes = [P, ctypes.c_longlong, ctypes.c_ulonglong, ctypes.c_int, ctypes.c_float, ctypes.c_float]
+        _lib.orc_seeded_bf16.argtypes = _lib.orc_seeded.argtypes
     return _lib
 
 
@@ -48,12 +52,13 @@ class OracleError(RuntimeError):
     pass
 
 
-def run(bundle, buffers=None, limit=0):
+def run(bundle, buffers=None, limit=0, threads=1):
     """Run a bundle (directory, compiler.Bundle or bundle.LoadedBundle) on the CPU oracle.
 
     buffers: optional list of initial arrays (float32 for f32/bf16, int32 for i32); default = the metadata init.
     Returns dict(buffers=[arrays], versions={name: v}, order=[task indices], observed=[...per metadata read], seconds=s).
-    limit > 0 stops after that many tasks (bounded CPU-baseline samples).
+    limit > 0 stops after that many tasks (bounded CPU-baseline samples). threads > 1 runs ready tasks in parallel on
+    that many worker threads (same results; `order` is then the completion order); limit applies to threads == 1 only.
     """
     from kvm_amd import bundle as bl
     b = bundle if isinstance(bundle, bl.LoadedBundle) else bl.load(bundle)
@@ -78,9 +83,14 @@ def run(bundle, buffers=None, limit=0):
     succ = np.ascontiguousarray(b.succ, np.int32) if b.succ.size else np.zeros(1, np.int32)
     args = np.ascontiguousarray(b.args, np.int32) if b.args.size else np.zeros(1, np.int32)
     t0 = time.perf_counter()
-    rc = lib().orc_run(tasks.ctypes.data, b.ntasks, succ.ctypes.data, int(b.succ.size), args.ctypes.data, int(b.args.size),
-                       obufs, len(buffers), versions.ctypes.data, nvars, rarr, len(reads), observed.ctypes.data,
-                       order.ctypes.data, limit, dur.ctypes.data, err, 512)
+    if threads > 1 and limit <= 0:
+        rc = lib().orc_run_mt(tasks.ctypes.data, b.ntasks, succ.ctypes.data, int(b.succ.size), args.ctypes.data, int(b.args.size),
+                              obufs, len(buffers), versions.ctypes.data, nvars, rarr, len(reads), observed.ctypes.data,
+                              order.ctypes.data, dur.ctypes.data, threads, err, 512)
+    else:
+        rc = lib().orc_run(tasks.ctypes.data, b.ntasks, succ.ctypes.data, int(b.succ.size), args.ctypes.data, int(b.args.size),
+                           obufs, len(buffers), versions.ctypes.data, nvars, rarr, len(reads), observed.ctypes.data,
+                           order.ctypes.data, limit, dur.ctypes.data, err, 512)
     dt = time.perf_counter() - t0
     if rc:
         raise OracleError(err.value.decode())
@@ -94,11 +104,11 @@ def materialize(meta_buf, init=None, root=None):
     init = init or meta_buf['init']
     if init['kind'] != 'seeded':
         return bl.materialize({**meta_buf, 'init': init}, root)
-    v = seeded(meta_buf['rows'] * meta_buf['cols'], init['seed'], init['draws'], init['bias'], init['coef'])
-    return bl.bf16_round(v) if meta_buf['dtype'] == bl.DT_BF16 else v
+    return seeded(meta_buf['rows'] * meta_buf['cols'], init['seed'], init['draws'], init['bias'], init['coef'],
+                  bf16=meta_buf['dtype'] == bl.DT_BF16)
 
 
-def seeded(n, seed, draws, bias, coef):
-    out = np.zeros(n, np.float32)
-    lib().orc_seeded(out.ctypes.data, n, seed % 2**64, draws, bias, coef)
+def seeded(n, seed, draws, bias, coef, bf16=False):
+    out = np.empty(n, np.float32)
+    (lib().orc_seeded_bf16 if bf16 else lib().orc_seeded)(out.ctypes.data, n, seed % 2**64, draws, bias, coef)
     return out

@@ -21,7 +21,11 @@
 #include <cstring>
 #include <algorithm>
 #include <chrono>
+#include <functional>
 #include <set>
+#include <thread>
+#include <mutex>
+#include <condition_variable>
 #include <string>
 #include <vector>
 
@@ -148,6 +152,28 @@ void op_embedding_bwd(const Ctx& c) {   // ref_gpt.py:55-65
 int tile_m(int fl) { return fl & 64 ? 256 : fl & 32 ? 128 : 64; }
 int tile_n(int fl) { return fl & 64 ? 128 : fl & 32 ? 128 : 64; }
 // matmul_tile (ref_gpt.py:69-95); round_ops: operands rounded to bf16 first (matmul_tile_bf16, ref_extra.py:312-323)
+// The reference's tile product: acc = f32(acc + f32(a * b)) over k in order, per output element
+// (ref_gpt.py:69-103). Computed in float: f32(a * b) of two floats is the float product (their exact product fits a
+// double), and f32(double(acc) + double(p)) is the float sum (double rounding is innocuous for one addition), so the
+// float loop below gives the same bits. Each output column keeps its own k-ordered chain; the loop runs over the
+// tile's columns innermost (independent chains, which the compiler may vectorise without reassociating anything).
+static void tile_product(int m0, int m1, int n0, int n1, int k0, int K, const std::function<float(int, int)>& opA,
+                         const std::function<float(int, int)>& opB, std::vector<float>& acc) {
+  const int nn = n1 - n0;
+  std::vector<float> Bt((size_t)K * nn), arow(K);
+  for (int k = 0; k < K; ++k) for (int n = 0; n < nn; ++n) Bt[(size_t)k * nn + n] = opB(n0 + n, k0 + k);
+  acc.assign((size_t)(m1 - m0) * nn, 0.0f);
+  for (int m = m0; m < m1; ++m) {
+    for (int k = 0; k < K; ++k) arow[k] = opA(m, k0 + k);
+    float* __restrict__ out = &acc[(size_t)(m - m0) * nn];
+    for (int k = 0; k < K; ++k) {
+      const float a = arow[k];
+      const float* __restrict__ b = &Bt[(size_t)k * nn];
+      for (int n = 0; n < nn; ++n) out[n] = out[n] + a * b[n];
+    }
+  }
+}
+
 void mm_tile(const Ctx& c, bool bf16ops, int tm_override = 0) {
   V A = c.buf(0), B = c.buf(1), out = c.buf(2), bias = c.buf(3, true), res = c.buf(4, true), pre = c.buf(5, true);
   int m0 = c.i(6), n0 = c.i(7), M = c.i(8), N = c.i(9), K = c.i(10), fl = c.i(11); float alpha = c.fl(12);
@@ -156,10 +182,13 @@ void mm_tile(const Ctx& c, bool bf16ops, int tm_override = 0) {
   int tm = tm_override ? tm_override : tile_m(fl), tn = tm_override ? tm_override : tile_n(fl);
   auto opA = [&](int m, int k) -> float { float x = ta ? A.f[(long long)k * A.cols + m] : A.f[(long long)m * A.cols + k]; return bf16ops ? bf16r(x) : x; };
   auto opB = [&](int n, int k) -> float { float y = tb ? B.f[(long long)n * B.cols + k] : B.f[(long long)k * B.cols + n]; return bf16ops ? bf16r(y) : y; };
-  for (int m = m0; m < std::min(m0 + tm, M); ++m)
-    for (int n = n0; n < std::min(n0 + tn, N); ++n) {
-      float acc = 0;
-      for (int k = 0; k < K; ++k) acc = f32((double)acc + (double)f32((double)opA(m, k) * opB(n, k)));
+  const int m1 = std::min(m0 + tm, M), n1 = std::min(n0 + tn, N);
+  if (m0 >= m1 || n0 >= n1) return;
+  std::vector<float> accv;
+  tile_product(m0, m1, n0, n1, 0, K, opA, opB, accv);
+  for (int m = m0; m < m1; ++m)
+    for (int n = n0; n < n1; ++n) {
+      float acc = accv[(size_t)(m - m0) * (n1 - n0) + (n - n0)];
       float v = f32((double)acc * alpha);
       if (bias.ok()) v = f32((double)v + bias.f[n]);
       if (dg) v = f32((double)v * gelu_grad(pre.at(m, n)));
@@ -533,14 +562,15 @@ void op_matmul_mma_bf16_kr(const Ctx& c) {
   need((fl & ~(1 | 2 | 4 | 32 | 64)) == 0 && c.a[3] == -1 && c.a[4] == -1 && c.a[5] == -1 && k0 >= 0 && om0 >= 0,
        "matmul_mma_bf16_kr: flags / epilogue / k0 / om0");
   int ta = fl & 1, tb = fl & 2, accum = fl & 4;
-  for (int m = m0; m < std::min(m0 + (fl & 64 ? 256 : 128), M); ++m)
-    for (int n = n0; n < std::min(n0 + 256, N); ++n) {
-      float acc = 0;
-      for (int k = k0; k < k0 + K; ++k) {
-        float x = bf16r(ta ? A.f[(long long)k * A.cols + m] : A.f[(long long)m * A.cols + k]);
-        float y = bf16r(tb ? B.f[(long long)n * B.cols + k] : B.f[(long long)k * B.cols + n]);
-        acc = f32((double)acc + (double)f32((double)x * y));
-      }
+  auto opA = [&](int m, int k) -> float { return bf16r(ta ? A.f[(long long)k * A.cols + m] : A.f[(long long)m * A.cols + k]); };
+  auto opB = [&](int n, int k) -> float { return bf16r(tb ? B.f[(long long)n * B.cols + k] : B.f[(long long)k * B.cols + n]); };
+  const int m1 = std::min(m0 + (fl & 64 ? 256 : 128), M), n1 = std::min(n0 + 256, N);
+  if (m0 >= m1 || n0 >= n1) return;
+  std::vector<float> accv;
+  tile_product(m0, m1, n0, n1, k0, K, opA, opB, accv);
+  for (int m = m0; m < m1; ++m)
+    for (int n = n0; n < n1; ++n) {
+      float acc = accv[(size_t)(m - m0) * (n1 - n0) + (n - n0)];
       float v = f32((double)acc * alpha);
       long long o = (long long)(om0 + m) * out.cols + n;
       out.stf(o, accum ? f32((double)out.f[o] + v) : v);
@@ -805,6 +835,83 @@ int orc_run(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedge
   return 0;
 }
 
+// The same VM with `threads` workers (the reference's Runtime(workers=N), workload_vm.py:46): every ready task may run
+// beside the others, since a valid graph orders every conflicting pair of accesses by an edge or a version wait. Picks
+// follow the same (priority, index) rule under one lock; operators run outside it. Results do not depend on the
+// interleaving (each output has one writer per phase); `order` records completion order and `observed` the version
+// each read saw at its task's start. threads <= 1 runs orc_run.
+int orc_run_mt(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs,
+               OrcBuf* bufs, int nbufs, int32_t* versions, int nvars, const OrcRead* reads, int nreads, int32_t* observed,
+               int32_t* order, float* dur_us, int threads, char* err, int errlen) {
+  if (threads <= 1) return orc_run(tasks, ntasks, succ, nedges, args, nargs, bufs, nbufs, versions, nvars, reads, nreads, observed, order, 0, dur_us, err, errlen);
+  std::vector<int> indeg(ntasks);
+  std::vector<std::vector<int>> reads_of(ntasks);
+  for (int r = 0; r < nreads; ++r) if (reads[r].task >= 0 && reads[r].task < ntasks) reads_of[reads[r].task].push_back(r);
+  std::set<std::pair<long long, int>> ready;
+  std::vector<std::vector<int>> parked(nvars > 0 ? nvars : 1);
+  auto key = [&](int t) { return std::make_pair(-(long long)tasks[t].priority, t); };
+  auto release = [&](int t) {
+    const MvmTaskDesc& d = tasks[t];
+    if (d.wait_var >= 0 && versions[d.wait_var] < d.wait_ver) parked[d.wait_var].push_back(t);
+    else ready.insert(key(t));
+  };
+  for (int t = 0; t < ntasks; ++t) {
+    const MvmTaskDesc& d = tasks[t];
+    if (d.succ_off < 0 || d.succ_cnt < 0 || d.succ_off + d.succ_cnt > nedges || d.args_off < 0 || d.args_off + d.args_words > nargs ||
+        d.wait_var >= nvars || d.pub_var >= nvars) { snprintf(err, errlen, "task %d: descriptor out of range", t); return 1; }
+    indeg[t] = d.indegree;
+  }
+  for (int t = 0; t < ntasks; ++t) if (indeg[t] == 0) release(t);
+  std::mutex mu;
+  std::condition_variable cv;
+  int done = 0, running = 0;
+  bool failed = false;
+  std::string why;
+  auto worker = [&]() {
+    std::unique_lock<std::mutex> lk(mu);
+    for (;;) {
+      cv.wait(lk, [&] { return failed || done == ntasks || !ready.empty() || running == 0; });
+      if (failed || done == ntasks) return;
+      if (ready.empty()) { failed = true; why = "deadlock: no runnable task"; cv.notify_all(); return; }
+      const int cur = ready.begin()->second;
+      ready.erase(ready.begin());
+      const MvmTaskDesc& d = tasks[cur];
+      for (int r : reads_of[cur]) {
+        int seen = versions[reads[r].var];
+        observed[r] = seen;
+        if (reads[r].policy == 0 ? seen != reads[r].version : seen < reads[r].version) { failed = true; why = "task " + std::to_string(cur) + ": read version violated"; }
+      }
+      OpFn fn = find_op(d.op_id);
+      if (!fn) { failed = true; why = "task " + std::to_string(cur) + ": operator not supported by the oracle"; }
+      if (failed) { cv.notify_all(); return; }
+      ++running;
+      lk.unlock();
+      std::string msg;
+      auto t0 = std::chrono::steady_clock::now();
+      try { Ctx c{(OBuf*)bufs, nbufs, args + d.args_off}; fn(c); } catch (const Fail& f) { msg = f.msg; }
+      const float us = std::chrono::duration<float, std::micro>(std::chrono::steady_clock::now() - t0).count();
+      lk.lock();
+      --running;
+      if (dur_us) dur_us[cur] = us;
+      if (!msg.empty()) { failed = true; why = "task " + std::to_string(cur) + ": " + msg; cv.notify_all(); return; }
+      order[done++] = cur;
+      if (d.pub_var >= 0) {
+        if (versions[d.pub_var] + 1 != d.pub_ver) { failed = true; why = "task " + std::to_string(cur) + ": publish order broken"; cv.notify_all(); return; }
+        versions[d.pub_var] = d.pub_ver;
+        std::vector<int> w; w.swap(parked[d.pub_var]);
+        for (int t : w) release(t);
+      }
+      for (int k = 0; k < d.succ_cnt; ++k) { int sx = succ[d.succ_off + k]; if (--indeg[sx] == 0) release(sx); }
+      cv.notify_all();
+    }
+  };
+  std::vector<std::thread> pool;
+  for (int i = 0; i < threads; ++i) pool.emplace_back(worker);
+  for (auto& th : pool) th.join();
+  if (failed) { snprintf(err, errlen, "%s", why.c_str()); return 1; }
+  return 0;
+}
+
 // Single-op entry for tests: runs one operator on explicit buffers.
 int orc_op(int op_id, const int32_t* args, OrcBuf* bufs, int nbufs, char* err, int errlen) {
   OpFn fn = find_op(op_id);
@@ -815,16 +922,33 @@ int orc_op(int op_id, const int32_t* args, OrcBuf* bufs, int nbufs, char* err, i
 }
 
 // SplitMix64 seeded value (runtime/initgen.py:49-58), for the tests' known-answer check.
+// The same values rounded to bf16 (nearest even on the bits; the executor's bf16 seeded weights), as float.
+void orc_seeded(float* out, long long n, unsigned long long seed, int draws, float bias, float coef);
+void orc_seeded_bf16(float* out, long long n, unsigned long long seed, int draws, float bias, float coef) {
+  orc_seeded(out, n, seed, draws, bias, coef);
+  auto rnd = [&](long long i0, long long i1) { for (long long i = i0; i < i1; ++i) out[i] = bf16r(out[i]); };
+  const int nt = n >= (1ll << 22) ? (int)std::min<unsigned>(16u, std::max(1u, std::thread::hardware_concurrency())) : 1;
+  std::vector<std::thread> pool;
+  for (int t = 0; t < nt; ++t) pool.emplace_back(rnd, n * t / nt, n * (t + 1) / nt);
+  for (auto& th : pool) th.join();
+}
 void orc_seeded(float* out, long long n, unsigned long long seed, int draws, float bias, float coef) {
   auto u = [&](unsigned long long j) {
     unsigned long long z = seed + (j + 1) * 0x9E3779B97F4A7C15ull;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull; z = (z ^ (z >> 27)) * 0x94D049BB133111EBull; z ^= z >> 31;
     return (float)(z >> 40) * (1.0f / 16777216.0f);
   };
-  for (long long i = 0; i < n; ++i) {
-    float acc = draws == 1 ? u(i) : (u(i * 4) + u(i * 4 + 1)) + (u(i * 4 + 2) + u(i * 4 + 3));
-    out[i] = (acc - bias) * coef;
-  }
+  auto fill = [&](long long i0, long long i1) {
+    for (long long i = i0; i < i1; ++i) {
+      float acc = draws == 1 ? u(i) : (u(i * 4) + u(i * 4 + 1)) + (u(i * 4 + 2) + u(i * 4 + 3));
+      out[i] = (acc - bias) * coef;
+    }
+  };
+  // counter-based: every element is a function of its index alone, so large fills split over threads
+  const int nt = n >= (1ll << 22) ? (int)std::min<unsigned>(16u, std::max(1u, std::thread::hardware_concurrency())) : 1;
+  std::vector<std::thread> pool;
+  for (int t = 0; t < nt; ++t) pool.emplace_back(fill, n * t / nt, n * (t + 1) / nt);
+  for (auto& th : pool) th.join();
 }
 
 }  // extern "C"

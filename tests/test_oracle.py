@@ -363,3 +363,42 @@ def test_gemv_rows_is_gemv_per_row(pro, with_res):
     for m in range(M):
         assert np.array_equal(O[m].view(np.uint32), _get(r, b, f'o{m}').view(np.uint32)), m
     assert not np.array_equal(O[0], O[1])
+
+
+@pytest.mark.parametrize('case', golden_cases())
+def test_threaded_oracle_matches_reference_vm_bitwise(case):
+    """The N-thread oracle (ready tasks in parallel) gives the reference VM's final buffers and versions bit for bit."""
+    d = GOLDEN / case
+    g = json.loads((d / 'golden.json').read_text())
+    r = oracle.run(d, threads=4)
+    meta = json.loads((d / 'metadata.json').read_text())
+    for m, x in zip(meta['buffers'], r['buffers']):
+        want = np.array(g['buffers'][m['name']], np.int32 if m['dtype'] == 1 else np.float32)
+        assert np.array_equal(want.view(np.uint32), x.view(np.uint32)), m['name']
+    assert r['versions'] == g['versions']
+    assert sorted(r['order'].tolist()) == list(range(len(r['order'])))
+
+
+def test_threaded_oracle_matches_one_thread_on_generated_graphs():
+    """Tiny GPT (2 steps) and the 8-MLP graph (1 step): 8 threads give the 1-thread buffers bit for bit."""
+    from kvm_amd.workloads import gpt, mlp
+    for w in (gpt.build(gpt.GPTConfig.tiny(steps=2)), mlp.build(mlp.MLPConfig(steps=1, widths=(64, 96, 128)))):
+        b = bl.load(compiler.compile_spec(w.spec))
+        init = [oracle.materialize(m, w.init_override.get(m['name'])) for m in b.metadata['buffers']]
+        r1 = oracle.run(b, [x.copy() for x in init])
+        r8 = oracle.run(b, [x.copy() for x in init], threads=8)
+        for m, x, y in zip(b.metadata['buffers'], r1['buffers'], r8['buffers']):
+            assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), m['name']
+
+
+def test_decode_reference_deviation_from_fp64_fixture():
+    """The oracle on the full-width one-layer Qwen3 decode graph (batch 1) against an independent fp64 numpy model of
+    the same step: the same greedy token, a deviation below 1e-2 (bf16 activation stores and f32 RoPE angles are the
+    reference's rounding points), and the committed deviation fixture the GPU decode tolerances are derived from."""
+    import decode_fp64  # noqa: F401
+    from golden.make_decode_deviation import deviation
+    fix = json.loads((REPO / 'tests/golden/data/decode_fp64_deviation.json').read_text())['b1']
+    got = deviation(1)
+    assert got['tok'] == got['tok_fp64'] == fix['tok']
+    for k, v in got['deviation'].items():
+        assert 0 < v < 1e-2 and abs(v - fix['deviation'][k]) <= 1e-3 * v, (k, v, fix['deviation'][k])

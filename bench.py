@@ -1,10 +1,13 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X task-graph executor on BASELINE.json's headline configurations.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|gpt162m|decode|sched] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|gpt162m|decode|sched|tiny|mlp8|gpt355m]
+                    [--no-cpu-baseline]
 
 A "step" is one run of the workload's task graph (one persistent-kernel launch): one GPT-162M training step
-(forward + backward + AdamW), or one Qwen3-8B-shape greedy decode token for every sequence of the batch. Inputs and
+(forward + backward + AdamW), or one Qwen3-8B-shape greedy decode token for every sequence of the batch. The other
+BASELINE configurations are reported beside the headline: tiny GPT (10 steps per graph) and the eight MLPs (50 steps
+per graph) as time per training step and worker-busy fraction, GPT-355M f32 as step time against the fp32 peak. Inputs and
 weights are synthetic (seeded, on the device) and resident in HBM before the timed region; the timed region is K
 back-to-back launches bracketed by HIP events on the executor's stream. Prints one JSON line.
 """
@@ -23,6 +26,8 @@ sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+FP32_PEAK_TFLOPS = 157.3       # MI355X dense fp32 (matrix)
+CPU_THREADS = int(os.environ.get('KVM_CPU_THREADS', '16'))   # oracle worker threads for the CPU baseline (the box's CPU share)
 METRIC = 'GPT-162M train step ms; Qwen3-8B-shape decode tok/s + HBM GB/s fraction'
 
 
@@ -76,35 +81,69 @@ def bench_decode(batch, steps, warmup, cpu):
     return out
 
 
-def cpu_decode(batch):
-    """Oracle on a 1-layer full-width Qwen3 graph (+ LM head), scaled to 36 layers by weight elements."""
+_INIT_CACHE = {}
+
+
+def _oracle_time(w, threads, reuse=False):
+    """Wall time of the oracle (C++ restatement of the reference CPU VM + ops) on a whole graph with `threads` workers.
+    reuse: initial buffers with the same name, shape and initialiser are generated once and copied (graphs of 1 and 2
+    layers, or two batch sizes, share most of their weights)."""
     import oracle
     from kvm_amd import bundle as bl
     from kvm_amd import compiler
-    from kvm_amd.workloads import qwen3
-    c1 = qwen3.Qwen3Config(batch=batch, layers=1, max_new=4)
-    w = qwen3.build(c1)
     lb = bl.load(compiler.compile_spec(w.spec))
-    bufs = [bl.materialize({**m, 'init': w.init_override.get(m['name'], m['init'])}) for m in lb.metadata['buffers']]
-    r = oracle.run(lb, bufs)
-    full = qwen3.weight_elems(qwen3.Qwen3Config(batch=batch))
-    est = r['seconds'] * full / qwen3.weight_elems(c1)
-    return {'value': round(batch / est, 4), 'unit': 'tok/s', 'cores': 1, 'kind': 'port',
-            'sample': f'C++ oracle (restated reference CPU VM) on a 1-layer full-width graph + LM head, batch {batch}: '
-                      f'{r["seconds"]:.2f} s, scaled x{full / qwen3.weight_elems(c1):.1f} by weight elements to 36 layers'}
+    init = []
+    for m in lb.metadata['buffers']:
+        ini = w.init_override.get(m['name'], m['init'])
+        key = (m['name'], m['rows'], m['cols'], m['dtype'], json.dumps(ini, sort_keys=True))
+        if not reuse:
+            init.append(oracle.materialize(m, ini))
+            continue
+        if key not in _INIT_CACHE:
+            _INIT_CACHE[key] = oracle.materialize(m, ini)
+        init.append(_INIT_CACHE[key].copy())
+    return oracle.run(lb, init, threads=threads)['seconds']
+
+
+def _layer_fit(make, layers_full, threads):
+    """CPU time of the full-depth graph from whole-graph oracle timings at 1 and 2 layers: t1 + (L - 1) * (t2 - t1)."""
+    t1 = _oracle_time(make(1), threads, reuse=True)
+    t2 = _oracle_time(make(2), threads, reuse=True)
+    return t1 + (layers_full - 1) * max(t2 - t1, 0.0), t1, t2
+
+
+def cpu_decode(batch):
+    from kvm_amd.workloads import qwen3
+    est, t1, t2 = _layer_fit(lambda L: qwen3.build(qwen3.Qwen3Config(batch=batch, layers=L, max_new=4)), 36, CPU_THREADS)
+    return {'value': round(batch / est, 4), 'unit': 'tok/s', 'cores': CPU_THREADS, 'nproc': os.cpu_count(), 'kind': 'port',
+            'sample': f'oracle (C++ restatement of the reference CPU VM + ops, {CPU_THREADS} worker threads) timed on whole full-width '
+                      f'decode graphs of 1 and 2 layers (+ LM head), batch {batch}: {t1:.2f} s and {t2:.2f} s; 36 layers = '
+                      f't1 + 35 (t2 - t1) = {est:.2f} s per step'}
+
+
+GEMM_OPS = (34, 114, 122, 302, 304, 308)
+ATTN_OPS = (45, 47, 48)
 
 
 def gemm_task_flops(lb):
-    """FLOPs of every GEMM tile task (2*tm*tn*K clipped to the matrix) and of the attention tasks (their share of
-    the causal attention's algorithmic FLOPs: fwd 2 products, bwd 5), from the bundle's own arguments."""
+    """FLOPs of every GEMM tile task (2*tm*tn*K clipped to the matrix; K is the task's own range for the split-K tiles
+    of op 302) and of the attention tasks (their share of the causal attention's algorithmic FLOPs: fwd 2 products,
+    bwd 5), from the bundle's own arguments."""
     import numpy as np
     t, a = lb.tasks, lb.args
     fl = np.zeros(t.shape[0])
     for i in range(t.shape[0]):
         op, off = t[i, 0], t[i, 6]
-        if op in (34, 114, 122):
+        if op in GEMM_OPS:
             m0, n0, M, N, K, f = (int(x) for x in a[off + 6:off + 12])
-            tm, tn = (128, 256) if op == 122 else ((256, 128) if f & 64 else (128, 128) if f & 32 else (64, 64))
+            if op in (122, 308):
+                tm, tn = 128, 256
+            elif op == 304:
+                tm, tn = 256, 256
+            elif op == 302:
+                tm, tn = (256, 256) if f & 64 else (128, 256)
+            else:
+                tm, tn = (256, 128) if f & 64 else (128, 128) if f & 32 else (64, 64)
             fl[i] = 2.0 * (min(M, m0 + tm) - m0) * (min(N, n0 + tn) - n0) * K
         elif op in (45, 47, 48):
             q0, T, hd = int(a[off + (7 if op != 48 else 10)]), int(a[off + (8 if op != 48 else 11)]), int(a[off + (11 if op != 48 else 13)])
@@ -124,6 +163,7 @@ def bench_gpt(steps, warmup, cpu):
     log('gpt-162m bf16 training step: building')
     w = gpt.build(c)
     ex, lb = build_executor(w, trace=True)
+    check = first_step_invariants(ex, lb, c.vocab)
     ms, kms, res = time_steps(ex, steps, warmup)
     flops = w.info['flops']['total']
     tflops = flops / (kms / 1e3) / 1e12
@@ -132,7 +172,7 @@ def bench_gpt(steps, warmup, cpu):
     dur = (tr['end'] - tr['start']).astype(np.float64) / 100e6     # s (wall_clock64 at 100 MHz)
     fl = gemm_task_flops(lb)
     ops = lb.tasks[:, 0]
-    gm = np.isin(ops, [34, 114, 122]); at = np.isin(ops, [45, 47, 48])
+    gm = np.isin(ops, GEMM_OPS); at = np.isin(ops, ATTN_OPS)
     per_cu = BF16_PEAK_TFLOPS / 256 * 1e12
     in_task = {'gemm': float(fl[gm].sum() / dur[gm].sum() / per_cu), 'attention': float(fl[at].sum() / dur[at].sum() / per_cu)}
     busy = float(dur.sum() / (res['grid'] * (tr['end'].max() - tr['start'].min()) / 100e6))
@@ -141,50 +181,85 @@ def bench_gpt(steps, warmup, cpu):
     out = {'ms_per_step': round(ms, 3), 'kernel_ms': round(kms, 3), 'tflops': round(tflops, 1), 'mfma_frac_step': round(tflops / BF16_PEAK_TFLOPS, 4),
            'mfma_frac_in_gemm_tasks': round(in_task['gemm'], 4), 'mfma_frac_in_attention_tasks': round(in_task['attention'], 4),
            'worker_busy_frac': round(busy, 4), 'tasks': lb.ntasks, 'edges': int(lb.succ.size), 'loss_after': loss,
-           'step_flops': flops, 'params': w.info['params']}
+           'step_flops': flops, 'params': w.info['params'], 'first_step_check': check}
     log(f'  gpt-162m: {ms:.2f} ms/step (persistent kernel {kms:.2f} ms), {tflops:.1f} TFLOP/s ({tflops / BF16_PEAK_TFLOPS:.1%} of bf16 peak); in-task MFMA: '
         f'GEMM {in_task["gemm"]:.1%}, attention {in_task["attention"]:.1%}; workers busy {busy:.1%}; loss {loss:.4f}')
     ex.close()
     if cpu:
-        out['cpu_baseline'] = cpu_gpt(w, lb)
+        out['cpu_baseline'] = cpu_gpt()
     return out
 
 
-def cpu_gpt(w, lb, per_op=16, seed=0):
-    """CPU reference time of the same GPT-162M step graph, sampled: the oracle (C++ restatement of the reference CPU VM
-    and its operators) runs `per_op` tasks of every operator of the graph, drawn at random, on the step's initial
-    buffers; the step estimate is the sum over operators of (task count x mean sampled task time). The sampled tasks run
-    as a graph of their own with no edges, so the sample is bounded (about 10-30 s of CPU work) and its tasks read
-    buffers as initialised (the operators' costs do not depend on the values). GEMM and attention tasks are scaled by
-    their algorithmic FLOPs (tile sizes differ up to 60x across the graph), the others by task count."""
+def first_step_invariants(ex, lb, vocab):
+    """Full-size sanity of the first training step (untimed): the loss of a randomly initialised model is close to
+    ln V, and every weight gradient is finite and nonzero. Raises when not."""
     import numpy as np
-    import oracle
-    from kvm_amd import bundle as bl
-    rng = np.random.default_rng(seed)
-    ops = lb.tasks[:, 0]
-    pick = []
-    for o in np.unique(ops):
-        idx = np.nonzero(ops == o)[0]
-        pick += list(rng.choice(idx, size=min(per_op, idx.size), replace=False))
-    pick = np.array(sorted(pick))
-    t = lb.tasks[pick].copy()
-    t[:, 1] = 0; t[:, 2] = 0; t[:, 3] = 0          # no successors, no predecessors
-    t[:, 8] = -1; t[:, 10] = -1                     # no version wait, no publish
-    sub = bl.LoadedBundle({**lb.metadata, 'reads': [], 'publishers': []}, t, np.zeros(0, np.int32), lb.args, lb.root)
-    bufs = [oracle.materialize(m, w.init_override.get(m['name'])) for m in lb.metadata['buffers']]
-    r = oracle.run(sub, bufs)
-    fl = gemm_task_flops(lb)            # GEMM and attention tasks: CPU time scales with the task's FLOPs
-    est_s = 0.0
-    for o in np.unique(ops):
-        sel = ops[pick] == o
-        us = r['task_us'][sel].astype(np.float64)
-        if fl[pick][sel].sum() > 0:
-            est_s += fl[ops == o].sum() * us.sum() / fl[pick][sel].sum() / 1e6
-        else:
-            est_s += (ops == o).sum() * us.mean() / 1e6
-    return {'value': round(float(est_s) * 1e3, 1), 'unit': 'ms/step', 'cores': 1, 'kind': 'port',
-            'sample': f'C++ oracle (restated reference CPU VM + ops, 1 thread) on {len(pick)} tasks of the same step graph '
-                      f'({per_op} per operator, {r["seconds"]:.1f} s), scaled to the {lb.ntasks} tasks by FLOPs (GEMM, attention) or task count'}
+    ex.relaunch()
+    ex.finish()
+    loss = float(ex.read('loss')[0])
+    if not abs(loss - np.log(vocab)) <= 0.05 * np.log(vocab):
+        raise RuntimeError(f'first-step loss {loss} is not near ln V = {np.log(vocab):.3f}')
+    grads = [m['name'] for m in lb.metadata['buffers'] if m['name'].startswith('d.w')]
+    for g in grads:
+        x = ex.read(g)
+        if not np.isfinite(x).all() or not np.abs(x).max() > 0:
+            raise RuntimeError(f'gradient {g} is not finite and nonzero')
+    return {'loss_step1': round(loss, 4), 'ln_vocab': round(float(np.log(vocab)), 4), 'grads_finite_nonzero': len(grads)}
+
+
+def cpu_gpt(layers=12, dtype='bf16', **kw):
+    """CPU reference time of the GPT step from whole-graph oracle timings at full width and 1 and 2 layers."""
+    from kvm_amd.workloads import gpt
+    make = (lambda L: gpt.build(gpt.GPTConfig(layers=L, **kw))) if dtype == 'bf16' else (lambda L: gpt.build(gpt.GPTConfig.gpt355m(layers=L, **kw)))
+    est, t1, t2 = _layer_fit(make, layers, CPU_THREADS)
+    return {'value': round(est * 1e3, 1), 'unit': 'ms/step', 'cores': CPU_THREADS, 'nproc': os.cpu_count(), 'kind': 'port',
+            'sample': f'oracle (C++ restatement of the reference CPU VM + ops, {CPU_THREADS} worker threads) timed on whole full-width '
+                      f'step graphs of 1 and 2 layers: {t1:.1f} s and {t2:.1f} s; {layers} layers = t1 + {layers - 1} (t2 - t1)'}
+
+
+def bench_small(name, w, steps_in_graph, reps, warmup, cpu):
+    """A graph that holds several training steps (C1, C2): time per step = launch time / steps in the graph; worker-busy
+    fraction = summed task time / (workers x span) from the last launch's trace."""
+    import numpy as np
+    log(f'{name}: building')
+    ex, lb = build_executor(w, trace=True)
+    ms, kms, res = time_steps(ex, reps, warmup)
+    tr = ex.trace()
+    dur = (tr['end'] - tr['start']).astype(np.float64)
+    span = float(tr['end'].max() - tr['start'].min())
+    busy = float(dur.sum() / (res['grid'] * span))
+    out = {'us_per_step': round(kms * 1e3 / steps_in_graph, 2), 'launch_ms': round(kms, 4), 'steps_in_graph': steps_in_graph,
+           'worker_busy_frac': round(busy, 4), 'tasks': lb.ntasks, 'edges': int(lb.succ.size)}
+    log(f'  {name}: {out["us_per_step"]} us/step ({steps_in_graph} steps per launch, {lb.ntasks} tasks), workers busy {busy:.1%}')
+    ex.close()
+    if cpu:
+        t = _oracle_time(w, CPU_THREADS)
+        out['cpu_baseline'] = {'value': round(t * 1e6 / steps_in_graph, 1), 'unit': 'us/step', 'cores': CPU_THREADS, 'nproc': os.cpu_count(),
+                               'kind': 'port', 'sample': f'oracle on the whole graph ({steps_in_graph} steps, {CPU_THREADS} threads): {t:.2f} s'}
+    return out
+
+
+def bench_gpt355m(steps, warmup, cpu):
+    """GPT-355M shape, f32 storage and math (fp32 GEMM tiles), batch 4."""
+    from kvm_amd.workloads import gpt
+    c = gpt.GPTConfig.gpt355m()
+    log('gpt-355m f32 training step: building')
+    w = gpt.build(c)
+    ex, lb = build_executor(w, trace=False)
+    check = first_step_invariants(ex, lb, c.vocab)
+    ms, kms, res = time_steps(ex, steps, warmup)
+    flops = w.info['flops']['total']
+    tflops = flops / (kms / 1e3) / 1e12
+    out = {'ms_per_step': round(ms, 2), 'kernel_ms': round(kms, 2), 'tflops': round(tflops, 2), 'fp32_frac': round(tflops / FP32_PEAK_TFLOPS, 4),
+           'step_flops': flops, 'params': w.info['params'], 'tasks': lb.ntasks, 'first_step_check': check}
+    log(f'  gpt-355m f32: {ms:.1f} ms/step, {tflops:.1f} TFLOP/s ({tflops / FP32_PEAK_TFLOPS:.1%} of the fp32 peak)')
+    ex.close()
+    if cpu:   # batch 1 graphs, times 4 (every phase of the step is linear in the batch at fixed T)
+        cb = cpu_gpt(layers=24, dtype='f32', batch=1)
+        cb['value'] = round(cb['value'] * 4, 1)
+        cb['sample'] += ', at batch 1, x4 for batch 4'
+        out['cpu_baseline'] = cb
+    return out
 
 
 def bench_sched():
@@ -234,7 +309,7 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=3)
-    ap.add_argument('--workload', default='all', choices=['all', 'gpt162m', 'decode', 'sched'])
+    ap.add_argument('--workload', default='all', choices=['all', 'gpt162m', 'decode', 'sched', 'tiny', 'mlp8', 'gpt355m'])
     ap.add_argument('--decode-batch', default='1,8')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--copy-probe', type=int, default=0, metavar='MIB',
@@ -253,6 +328,15 @@ def main():
         extra['gpt162m'] = bench_gpt(a.steps, a.warmup, cpu)
     if a.workload in ('all', 'decode'):
         extra['decode'] = [bench_decode(int(bs), a.steps, a.warmup, cpu) for bs in a.decode_batch.split(',')]
+    _INIT_CACHE.clear()
+    if a.workload in ('all', 'tiny'):
+        from kvm_amd.workloads import gpt
+        extra['tiny_gpt'] = bench_small('tiny gpt f32 (C1, 10 steps per graph)', gpt.build(gpt.GPTConfig.tiny()), 10, a.steps, a.warmup, cpu)
+    if a.workload in ('all', 'mlp8'):
+        from kvm_amd.workloads import mlp
+        extra['mlp8'] = bench_small('8 MLPs f32 (C2, 50 steps per graph)', mlp.build(), 50, max(3, a.steps // 4), 1, cpu)
+    if a.workload in ('all', 'gpt355m'):
+        extra['gpt355m'] = bench_gpt355m(max(3, a.steps // 4), 1, cpu)
     if 'gpt162m' in extra:
         g = extra['gpt162m']
         result.update({'value': g['ms_per_step'], 'unit': 'ms/step', 'higher_is_better': False, 'ms_per_step': g['ms_per_step'],

@@ -72,14 +72,6 @@ __device__ void f32_block(const Ctx& c, View A, View B, int ta, int tb, int m0, 
 __device__ __forceinline__ int tile_m(int fl) { return fl & 64 ? 256 : fl & 32 ? 128 : 64; }
 __device__ __forceinline__ int tile_n(int fl) { return (fl & 96) ? 128 : 64; }
 
-__device__ __noinline__ void op_matmul_tile(const Ctx& c) {
-  View A = c.buf(0), B = c.buf(1);
-  int m0 = c.i(6), n0 = c.i(7), M = c.i(8), N = c.i(9), K = c.i(10), fl = c.i(11);
-  Epi e{c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.f(12), fl & 4, fl & 8, fl & 512};
-  int tm = tile_m(fl), tn = tile_n(fl);
-  for (int dm = 0; dm < tm; dm += 64) for (int dn = 0; dn < tn; dn += 64)
-    if (m0 + dm < M && n0 + dn < N) f32_block(c, A, B, fl & 1, fl & 2, m0 + dm, n0 + dn, M, N, K, e, false, nullptr);
-}
 
 // SwiGLU epilogue wrappers: the raw tile lands in LDS, then the elementwise pass (registry ops 120 / 121).
 __device__ __noinline__ void op_matmul_tile_silu_mul(const Ctx& c) {
@@ -758,6 +750,115 @@ template <int TM, int TN> __device__ __forceinline__ void mfma_tile(const Ctx& c
   }
 }
 
+// ---------------------------------------------------------------------------------------------- fp32 MFMA engine
+// matmul_tile (op 34) on the matrix cores: v_mfma_f32_32x32x2_f32, exact fp32 products with fp32 accumulation (CDNA4
+// has no TF32; the reference's TF32 flags run as plain fp32). Four waves in a 2 x 2 grid, each owning (TM/2) x (TN/2)
+// as 32 x 32 blocks. K advances in slabs of FKS = 16: both operands sit in LDS as [row][k] f32 (64-byte rows, 16-byte
+// k-chunks XOR-swizzled by (row >> 2) & 3), double-buffered; the next slab is loaded into registers while the current
+// one is multiplied. One ds_read_b128 per operand block gives a lane four k values: lanes 0-31 hold k 8q..8q+3 and
+// lanes 32-63 k 8q+4..8q+7 of their row, and the four MFMAs of that read pair them up (which k each MFMA sums is a
+// free choice as long as A and B agree). B is the MFMA's first source, so the accumulators hold D^T exactly as the
+// bf16 engine's, and the tile leaves through the same LDS-staged epilogue (gemm_store).
+constexpr int FKS = 16;
+__device__ __forceinline__ int fsw(int row, int ch) { return row * FKS + 4 * (ch ^ ((row >> 2) & 3)); }
+
+template <int R> struct FTile {
+  static constexpr int NV = R * FKS / 4 / KVM_THREADS;   // float4 per thread per slab
+  static_assert(NV >= 1, "tile shape");
+  f32x4n v[NV];
+  // Slab k0 of rows r0..r0+R of X: kc = element (r, k) at X[r*cols + k], else at X[k*cols + r]. Rows / k past the
+  // matrix read as 0. vec: f32 storage with cols % 4 == 0 (every 4-aligned element index is a 16-byte load).
+  __device__ __forceinline__ void fetch(const View& X, bool kc, bool vec, int r0, int rows, int k0, int K) {
+#pragma unroll
+    for (int q = 0; q < NV; ++q) {
+      const int idx = tid() + q * KVM_THREADS;
+      int r, k;
+      if (kc) { r = r0 + (idx >> 2); k = k0 + 4 * (idx & 3); }       // 4 k of one row
+      else { r = r0 + 4 * (idx % (R / 4)); k = k0 + idx / (R / 4); }   // 4 rows of one k
+      const long long o = kc ? (long long)r * X.cols + k : (long long)k * X.cols + r;
+      const bool whole = kc ? (r < rows && k + 4 <= K) : (k < K && r + 4 <= rows);
+      if (vec && whole) v[q] = *(const GLOBAL f32x4n*)(X.f() + o);
+      else {
+        f32x4n t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool in = kc ? (r < rows && k + i < K) : (k < K && r + i < rows);
+          if (in) t[i] = X.ld(o + i);
+        }
+        v[q] = t;
+      }
+    }
+  }
+  __device__ __forceinline__ void store(LDS float* lds, bool kc) const {
+#pragma unroll
+    for (int q = 0; q < NV; ++q) {
+      const int idx = tid() + q * KVM_THREADS;
+      if (kc) *(LDS f32x4n*)(lds + fsw(idx >> 2, idx & 3)) = v[q];
+      else {
+        const int r = 4 * (idx % (R / 4)), k = idx / (R / 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lds[fsw(r + i, k >> 2) + (k & 3)] = v[q][i];
+      }
+    }
+  }
+};
+
+template <int TM, int TN> __device__ __noinline__ void gemm_f32(const Ctx& c) {
+  constexpr int WM = TM / 2, WN = TN / 2, BM = WM / 32, BN = WN / 32, ST = (TM + TN) * FKS;
+  static_assert(2 * ST * 4 <= KVM_LDS_BYTES && TM * TN * 4 <= KVM_LDS_BYTES, "LDS");
+  const GemmArgs g = gemm_args(c);
+  const View& A = g.A; const View& B = g.B;
+  const bool akc = !(g.fl & 1), bkc = (g.fl & 2) != 0;
+  const bool avec = A.dtype == 0 && (A.cols & 3) == 0, bvec = B.dtype == 0 && (B.cols & 3) == 0;
+  const int wm0 = (wave() >> 1) * WM, wn0 = (wave() & 1) * WN, l = lane();
+  LDS float* lds = (LDS float*)c.smem;
+  f32x16 acc[BM][BN];
+#pragma unroll
+  for (int i = 0; i < BM; ++i)
+#pragma unroll
+    for (int j = 0; j < BN; ++j) acc[i][j] = f32x16{};
+  FTile<TM> fa;
+  FTile<TN> fb;
+  fa.fetch(A, akc, avec, g.m0, g.M, 0, g.K);
+  fb.fetch(B, bkc, bvec, g.n0, g.N, 0, g.K);
+  __syncthreads();                         // the previous task may still read this LDS
+  fa.store(lds, akc);
+  fb.store(lds + TM * FKS, bkc);
+  __syncthreads();
+  const int nslab = (g.K + FKS - 1) / FKS;
+  for (int s = 0; s < nslab; ++s) {
+    const LDS float* la = lds + (s & 1) * ST;
+    const LDS float* lb = la + TM * FKS;
+    const bool more = s + 1 < nslab;
+    if (more) {
+      fa.fetch(A, akc, avec, g.m0, g.M, (s + 1) * FKS, g.K);
+      fb.fetch(B, bkc, bvec, g.n0, g.N, (s + 1) * FKS, g.K);
+    }
+#pragma unroll
+    for (int q = 0; q < FKS / 8; ++q) {
+      const int ch = 2 * q + (l >> 5);
+      f32x4n av[BM], bv[BN];
+#pragma unroll
+      for (int i = 0; i < BM; ++i) av[i] = *(const LDS f32x4n*)(la + fsw(wm0 + i * 32 + (l & 31), ch));
+#pragma unroll
+      for (int j = 0; j < BN; ++j) bv[j] = *(const LDS f32x4n*)(lb + fsw(wn0 + j * 32 + (l & 31), ch));
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < BM; ++i)
+#pragma unroll
+          for (int j = 0; j < BN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[j][t], av[i][t], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      LDS float* nb = lds + ((s + 1) & 1) * ST;
+      fa.store(nb, akc);
+      fb.store(nb + TM * FKS, bkc);
+    }
+    __syncthreads();
+  }
+  gemm_store<TM, TN>(c, acc, g);
+}
+
 __device__ __noinline__ void op_matmul_tile_bf16(const Ctx& c) {
   const int fl = c.i(11);
   if (fl & 64) mfma_tile<256, 128>(c);
@@ -803,6 +904,14 @@ __device__ __noinline__ void op_matmul_mma_bf16_kr(const Ctx& c) {
   __syncthreads();
   if (c.i(11) & 64) tile_256(c);
   else mfma_tile<128, 256>(c);
+}
+
+// Op 34 on the fp32 MFMA engine: 64x64 tiles by default, 128x128 with flag 32, 256x128 with flag 64.
+__device__ __noinline__ void op_matmul_tile(const Ctx& c) {
+  const int fl = c.i(11);
+  if (fl & 64) gemm_f32<256, 128>(c);
+  else if (fl & 32) gemm_f32<128, 128>(c);
+  else gemm_f32<64, 64>(c);
 }
 
 }  // namespace kvm

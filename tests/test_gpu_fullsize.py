@@ -103,9 +103,18 @@ def test_gpt355m_shape_f32_two_layers_step():
     ex = _device(w, lb)
     check_schedule(ex, lb)
     r = oracle.run(lb, init, threads=THREADS)
-    kbias = tuple(n for n in names if n.startswith(('bk.', 'd.bk.', 'm.bk.', 'v.bk.')))   # zero gradient: noise on both sides
-    bad = compare_run(ex, lb.metadata, r, tol_f32=TOL_PRECISE, skip=kbias)
+    # Vectors that start at zero (biases, LayerNorm shifts) hold -lr * g / (|g| + eps) after the first AdamW step: an
+    # element whose gradient is near zero takes either sign under any change of summation order, so these are held
+    # elementwise to the size of one update instead; their gradients and moments are compared like everything else.
+    # The key bias has an exactly zero gradient (softmax is shift-invariant): noise on both sides, skipped.
+    zero_init = [m['name'] for m in lb.metadata['buffers'] if m['init'].get('kind') == 'fill' and m['init'].get('value') == 0
+                 and f'd.{m["name"]}' in names]
+    skip = tuple(zero_init) + tuple(n for n in names if n.startswith(('d.bk.', 'm.bk.', 'v.bk.')))
+    bad = compare_run(ex, lb.metadata, r, tol_f32=TOL_PRECISE, skip=skip)
     assert not bad, bad
+    lr = w.info['config']['lr']
+    for n in zero_init:
+        assert np.abs(ex.read(n) - r['buffers'][names.index(n)]).max() <= 2.0 * lr + 1e-7, n
     ex.close()
 
 

@@ -175,9 +175,9 @@ __device__ void dispatch(int op, const Ctx& c) {
   switch (op) {
     case 0: break;
     case 1: op_copy(c); break;
-    case 2: op_add(c); break;
-    case 3: op_scale(c); break;
-    case 4: op_relu(c); break;
+    case 2: if (!op_add_fast(c)) op_add(c); break;
+    case 3: if (!op_scale_fast(c)) op_scale(c); break;
+    case 4: if (!op_relu_fast(c)) op_relu(c); break;
     case 5: op_sgd(c); break;
     case 6: op_predict(c); break;
     case 7: op_mse_grad(c); break;
@@ -216,8 +216,8 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 61: if (!op_colsum_fast(c)) op_colsum(c); break;
     case 62: op_select_window(c); break;
     case 63: op_gather_rows(c); break;
-    case 96: op_act_fwd(c); break;
-    case 97: op_act_bwd(c); break;
+    case 96: if (!op_act_fwd_fast(c)) op_act_fwd(c); break;
+    case 97: if (!op_act_bwd_fast(c)) op_act_bwd(c); break;
     case 98: if (!op_silu_mul_fwd_fast(c)) op_silu_mul_fwd(c); break;
     case 99: op_silu_mul_bwd(c); break;
     case 100: op_softmax_rows_fwd(c); break;
@@ -229,7 +229,7 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 114: op_matmul_tile_bf16(c); break;
     case 115: op_adamw_lr(c); break;
     case 116: op_lr_schedule(c); break;
-    case 117: op_scale_flat(c); break;
+    case 117: if (!op_scale_flat_fast(c)) op_scale_flat(c); break;
     case 118: op_add_rowtile(c); break;
     case 120: op_matmul_tile_silu_mul(c); break;
     case 121: op_matmul_tile_silu_mul_bwd(c); break;

@@ -441,15 +441,21 @@ __device__ void adamw_body(const Ctx& c, View p, View g, View m, View v, View gs
       stwt_f4(sh.f() + 4 * q, r);
     }
   };
-  // two 16-byte groups per thread per pass: eight loads in flight before the first update
+  // four 16-byte groups per thread per pass: sixteen loads in flight before the first update (the loads of a pass
+  // wait for the previous pass's write-through stores, so fewer, larger passes)
+  constexpr int NG = 4;
   long long q = a0 / 4 + tid(), qe = a1 / 4;
-  for (; q + KVM_THREADS < qe; q += 2 * KVM_THREADS) {
-    long long r = q + KVM_THREADS;
-    f32x4n p0 = P[q], g0 = G[q], m0 = M[q], v0 = Vv[q], p1 = P[r], g1 = G[r], m1 = M[r], v1 = Vv[r];
-    upd(q, p0, g0, m0, v0);
-    upd(r, p1, g1, m1, v1);
+  for (; q + (NG - 1) * KVM_THREADS < qe; q += NG * KVM_THREADS) {
+    f32x4n pv[NG], gv[NG], mv[NG], vv[NG];
+#pragma unroll
+    for (int u = 0; u < NG; ++u) {
+      const long long r = q + u * KVM_THREADS;
+      pv[u] = P[r]; gv[u] = G[r]; mv[u] = M[r]; vv[u] = Vv[r];
+    }
+#pragma unroll
+    for (int u = 0; u < NG; ++u) upd(q + u * KVM_THREADS, pv[u], gv[u], mv[u], vv[u]);
   }
-  if (q < qe) upd(q, P[q], G[q], M[q], Vv[q]);
+  for (; q < qe; q += KVM_THREADS) upd(q, P[q], G[q], M[q], Vv[q]);
 }
 __device__ __noinline__ void op_adamw(const Ctx& c) { adamw_body(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.i(6), c.i(7), c.f(8), c.f(9), c.f(10), c.f(11), c.f(12)); }
 __device__ __noinline__ void op_adamw_bf16(const Ctx& c) { adamw_body(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.buf(5), c.i(6), c.i(7), c.f(8), c.f(9), c.f(10), c.f(11), c.f(12), c.buf(13)); }

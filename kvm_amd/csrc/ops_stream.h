@@ -108,6 +108,106 @@ __device__ __noinline__ bool op_embedding_fwd_fast(const Ctx& c) {
   return true;
 }
 
+// ---------------------------------------------------------------------------------------------- flat elementwise ops
+// out[i] = f(in_0[i], .., in_{NIN-1}[i]) over flat [e0, e1) for f32 views: groups of 4 elements, NB groups per thread
+// loaded before any is used (a load / store round trip per element otherwise serialises the loop: write-through
+// stores and loads share one counter), elements outside the 16-byte grid one by one. In-place use (an input is the
+// output) is fine: each element is read and written by the same thread.
+template <int NIN, class F>
+__device__ __forceinline__ void flat_map(const View (&in)[NIN], const View& out, long long e0, long long e1, F f) {
+  constexpr int NB = 8;
+  const long long a0 = min((e0 + 3) & ~3ll, e1), a1 = max(a0, e1 & ~3ll);
+  auto one = [&](long long i) {
+    float x[NIN];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) x[k] = in[k].f()[i];
+    stwt32(out.f() + i, f(x));
+  };
+  for (long long i = e0 + tid(); i < a0; i += KVM_THREADS) one(i);
+  for (long long i = a1 + tid(); i < e1; i += KVM_THREADS) one(i);
+  const long long q1 = a1 / 4;
+  const bool bo = out.n() * 4 < 0x7fffffffll;
+  const __amdgpu_buffer_rsrc_t ro = wt_rsrc(out.p, bo ? out.n() * 4 : 0);
+  for (long long q = a0 / 4 + tid(); q < q1; q += NB * KVM_THREADS) {
+    f32x4n v[NB][NIN];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const long long qq = min(q + (long long)u * KVM_THREADS, q1 - 1);
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) v[u][k] = ((const GLOBAL f32x4n*)in[k].f())[qq];
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const long long qq = q + (long long)u * KVM_THREADS;
+      if (qq >= q1) break;
+      f32x4n r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float x[NIN];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) x[k] = v[u][k][j];
+        r[j] = f(x);
+      }
+      if (bo) stwt_buf(ro, (int)(qq * 16), r);
+      else stwt_f4(out.f() + 4 * qq, r);
+    }
+  }
+}
+__device__ __forceinline__ bool all_f32(const View& a, const View& b = View{nullptr, 0, 0, 0}, const View& c = View{nullptr, 0, 0, 0}) {
+  return a.dtype == 0 && (!b.ok() || b.dtype == 0) && (!c.ok() || c.dtype == 0);
+}
+__device__ __noinline__ bool op_act_fwd_fast(const Ctx& c) {
+  const View x = c.buf(0), o = c.buf(1);
+  const int kind = c.i(2);
+  if (!all_f32(x, o)) return false;
+  const View in[1] = {x};
+  flat_map(in, o, c.i(3), c.i(4), [kind](const float (&v)[1]) { return act_f(kind, v[0]); });
+  return true;
+}
+__device__ __noinline__ bool op_act_bwd_fast(const Ctx& c) {
+  const View x = c.buf(0), dy = c.buf(1), dx = c.buf(2);
+  const int kind = c.i(3), acc = c.i(6);
+  if (!all_f32(x, dy, dx)) return false;
+  if (acc) {
+    const View in[3] = {x, dy, dx};
+    flat_map(in, dx, c.i(4), c.i(5), [kind](const float (&v)[3]) { return v[2] + v[1] * act_d(kind, v[0]); });
+  } else {
+    const View in[2] = {x, dy};
+    flat_map(in, dx, c.i(4), c.i(5), [kind](const float (&v)[2]) { return v[1] * act_d(kind, v[0]); });
+  }
+  return true;
+}
+__device__ __noinline__ bool op_scale_flat_fast(const Ctx& c) {
+  const View x = c.buf(0), o = c.buf(1);
+  const float al = c.f(2);
+  if (!all_f32(x, o)) return false;
+  const View in[1] = {x};
+  flat_map(in, o, c.i(3), c.i(4), [al](const float (&v)[1]) { return al * v[0]; });
+  return true;
+}
+__device__ __noinline__ bool op_relu_fast(const Ctx& c) {
+  const View x = c.buf(0), o = c.buf(1);
+  if (!all_f32(x, o)) return false;
+  const View in[1] = {x};
+  flat_map(in, o, 0, c.i(2), [](const float (&v)[1]) { return v[0] > 0.f ? v[0] : 0.f; });
+  return true;
+}
+__device__ __noinline__ bool op_add_fast(const Ctx& c) {
+  const View a = c.buf(0), b = c.buf(1), o = c.buf(2);
+  if (!all_f32(a, b, o)) return false;
+  const View in[2] = {a, b};
+  flat_map(in, o, 0, c.i(3), [](const float (&v)[2]) { return v[0] + v[1]; });
+  return true;
+}
+__device__ __noinline__ bool op_scale_fast(const Ctx& c) {
+  const View x = c.buf(0), o = c.buf(1);
+  const float al = c.f(2);
+  if (!all_f32(x, o)) return false;
+  const View in[1] = {x};
+  flat_map(in, o, 0, c.i(3), [al](const float (&v)[1]) { return v[0] * al; });
+  return true;
+}
+
 // silu(gate) * up over [e0, e1) (registry op 104): groups of 8 elements, four groups in flight per thread.
 __device__ __noinline__ bool op_silu_mul_fwd_fast(const Ctx& c) {
   const View g = c.buf(0), u = c.buf(1), o = c.buf(2);
@@ -707,8 +807,42 @@ __device__ __noinline__ void op_softmax_ce_bwd_any(const Ctx& c) {
   const float f = c.buf(3).f()[1] * c.f(9);
   if (!ce_rows_fast(c, c.buf(0), c.buf(1), n, c.buf(2), c.buf(4), c.i(5), c.i(6), c.i(7), c.i(8), f, false, true)) op_softmax_ce_bwd(c);
 }
+// Cross entropy for small vocabularies (V <= 32, f32 logits and gradient: classifier heads): one row per lane, the row's
+// logits loaded together into registers, then max, sum of exponentials, lse, loss and gradient as in ce_rows.
+constexpr int CE_SMALL_V = 32;
+__device__ bool ce_rows_small(const Ctx& c, View lg, View tg, View rl, View ls, View dl, int r0, int r1, int V, int ignore, float f) {
+  if (V > CE_SMALL_V || V < 1 || lg.dtype != 0 || dl.dtype != 0) return false;
+  for (int r = r0 + tid(); r < r1; r += KVM_THREADS) {
+    const int t = tg.i()[r];
+    const bool ign = t == ignore;
+    if (!ign && (t < 0 || t >= V)) { c.fail(KVM_ERR_OP_TOKEN, r, t); continue; }
+    const GLOBAL float* row = lg.f() + (long long)r * lg.cols;
+    float x[CE_SMALL_V];
+#pragma unroll
+    for (int j = 0; j < CE_SMALL_V; ++j) x[j] = row[j < V ? j : V - 1];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < CE_SMALL_V; ++j) if (j < V) m = fmaxf(m, x[j]);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < CE_SMALL_V; ++j) if (j < V) s += __expf(x[j] - m);
+    const float lse = ign ? 0.f : m + logf(s);
+    float xt = 0.f;                          // the target's logit, without indexing the register array at run time
+#pragma unroll
+    for (int j = 0; j < CE_SMALL_V; ++j) if (j == t) xt = x[j];
+    stwt32(ls.f() + r, lse);
+    stwt32(rl.f() + r, ign ? 0.f : lse - xt);
+    GLOBAL float* d = dl.f() + (long long)r * dl.cols;
+#pragma unroll
+    for (int j = 0; j < CE_SMALL_V; ++j)
+      if (j < V) stwt32(d + j, ign ? 0.f : (__expf(x[j] - lse) - (j == t ? 1.f : 0.f)) * f);
+  }
+  return true;
+}
+
 __device__ __noinline__ void op_softmax_ce_fused_any(const Ctx& c) {
   const float f = (float)(1.0 / c.i(9)) * c.f(10);
+  if (ce_rows_small(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.i(5), c.i(6), c.i(7), c.i(8), f)) return;
   if (!ce_rows_fast(c, c.buf(0), c.buf(1), c.buf(2), c.buf(3), c.buf(4), c.i(5), c.i(6), c.i(7), c.i(8), f, true, true)) op_softmax_ce_fused(c);
 }
 

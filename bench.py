@@ -164,10 +164,14 @@ def bench_gpt(steps, warmup, cpu):
     w = gpt.build(c)
     ex, lb = build_executor(w, trace=True)
     check = first_step_invariants(ex, lb, c.vocab)
+    ex.set_trace(False)                   # timed runs untraced; one traced run afterwards for the per-task statistics
     ms, kms, res = time_steps(ex, steps, warmup)
     flops = w.info['flops']['total']
     tflops = flops / (kms / 1e3) / 1e12
-    # MFMA utilisation inside the GEMM / attention tasks, from the last run's per-task trace
+    ex.set_trace(True)
+    ex.relaunch()
+    res = ex.finish()
+    # MFMA utilisation inside the GEMM / attention tasks, from the traced run's per-task record
     tr = ex.trace()
     dur = (tr['end'] - tr['start']).astype(np.float64) / 100e6     # s (wall_clock64 at 100 MHz)
     fl = gemm_task_flops(lb)
@@ -223,7 +227,11 @@ def bench_small(name, w, steps_in_graph, reps, warmup, cpu):
     import numpy as np
     log(f'{name}: building')
     ex, lb = build_executor(w, trace=True)
+    ex.set_trace(False)
     ms, kms, res = time_steps(ex, reps, warmup)
+    ex.set_trace(True)
+    ex.relaunch()
+    res = ex.finish()
     tr = ex.trace()
     dur = (tr['end'] - tr['start']).astype(np.float64)
     span = float(tr['end'].max() - tr['start'].min())

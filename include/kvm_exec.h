@@ -111,6 +111,10 @@ int kvm_validate(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int 
 int kvm_versions(KvmExec* ex, int32_t* out, int n);
 int kvm_trace(KvmExec* ex, KvmTrace* out, int n);
 int kvm_ntasks(const KvmExec* ex);
+// Turns the per-task trace on or off for the following launches (an executor created with trace_on keeps its trace
+// buffer; tracing costs a read-modify-write at every task start). No counterpart in the reference, whose trace is
+// fixed at creation; for benchmarks that time untraced runs and trace one more.
+int kvm_set_trace(KvmExec* ex, int on);
 // Name of a registry operator id, or NULL (reference: --check-ops).
 const char* kvm_op_name(int op_id);
 // Fills `out` with n SplitMix64 seeded values on the device and copies them back (initialiser known-answer test).

@@ -901,6 +901,12 @@ int kvm_validate(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int 
 
 int kvm_ntasks(const KvmExec* ex) { return (int)ex->tasks.size(); }
 
+int kvm_set_trace(KvmExec* ex, int on) {
+  if (on && !ex->cfg.trace_on) { ex->err = "kvm_set_trace: the executor was created without a trace buffer"; return KVM_STATUS_INVALID; }
+  ex->S.trace_on = on ? 1 : 0;
+  return 0;
+}
+
 const char* kvm_op_name(int op_id) { return kvm_registry_name(op_id); }
 
 // Plain copy, 16 bytes per lane, grid-stride: the reference dispatch for the HBM byte counters (reads n16 * 16 bytes,

@@ -343,6 +343,16 @@ __device__ __forceinline__ GemmArgs gemm_args(const Ctx& c) {
 // per operand orientation. There every lane owns a fixed 4-column piece (bias loaded once) and the waves take rows in
 // turn, with the res / pre / previous-output loads of a batch of rows issued together through branch-free buffer
 // loads; every row is stored as whole lines. Pieces that are not whole, aligned vectors take the scalar path.
+// Rows of a wave whose second-operand loads (residual, pre-activation, previous output) are issued together, in the
+// straight-line epilogues (KVM_EPI_NB) and the general one (KVM_EPI_NB2). Larger batches measured slower: the
+// epilogue is an out-of-line function, and every register it uses beyond the caller-saved ones is saved and restored
+// around each call.
+#ifndef KVM_EPI_NB
+#define KVM_EPI_NB 8
+#endif
+#ifndef KVM_EPI_NB2
+#define KVM_EPI_NB2 4
+#endif
 template <int TN> __device__ __forceinline__ int epi_swz(int r) { return r & ((TN / 4 < 32 ? TN / 4 : 32) - 1); }
 
 // Whole, aligned tile with one of the epilogues the GPT graphs use, as straight-line code: KIND 0 = (bias), 1 = bias +
@@ -350,7 +360,7 @@ template <int TN> __device__ __forceinline__ int epi_swz(int r) { return r & ((T
 // The second operand of kinds 1-3 is loaded raw for a batch of rows before any of them is used.
 template <int TM, int TN, bool OBF, int KIND>
 __device__ __forceinline__ void epi_rows(const Ctx& c, const GemmArgs& g) {
-  constexpr int LPR = TN / 4, RPI = 64 / LPR, NI = TM / KVM_WAVES / RPI, NB = NI < 8 ? NI : 8;
+  constexpr int LPR = TN / 4, RPI = 64 / LPR, NI = TM / KVM_WAVES / RPI, NB = NI < KVM_EPI_NB ? NI : KVM_EPI_NB;
   const Epi& e = g.e;
   const LDS float* et = (const LDS float*)c.smem;
   const int l = lane(), w = wave(), ch = l % LPR, n = g.n0 + 4 * ch;
@@ -398,7 +408,7 @@ __device__ __forceinline__ void epi_rows(const Ctx& c, const GemmArgs& g) {
 template <int TM, int TN, bool OBF>
 __device__ __noinline__ void gemm_epilogue(const Ctx& c, int moff) {
   constexpr int LPR = TN / 4, RPI = 64 / LPR, NI = TM / KVM_WAVES / RPI;   // lanes per row, rows per instruction
-  constexpr int NB = NI < 4 ? NI : 4;
+  constexpr int NB = NI < KVM_EPI_NB2 ? NI : KVM_EPI_NB2;
   GemmArgs g = gemm_args(c);
   g.m0 += moff;                                          // the staged rows start at tile row moff
   const Epi& e = g.e;

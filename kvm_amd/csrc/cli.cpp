@@ -2,7 +2,7 @@
 // (reference: mvm_exec.cu:1962-2315). Prints "OK: d/a tasks, X ms[, golden match]" or "FAIL: ..." and exits 0 / 1
 // (2 for usage errors).
 //
-//   kvm_exec [--golden [--golden-tol R]] [--dump-bin DIR i,j,..] [--trace-csv FILE] [--repeat N] [--timeout-s N]
+//   kvm_exec [--golden [--golden-tol R] [--golden-tol-bf16 R]] [--dump-bin DIR i,j,..] [--trace-csv FILE] [--repeat N] [--timeout-s N]
 //            [--blocks N] [--no-trace] [--quiet] [--check-ops] bundle_dir...
 #include <cmath>
 #include <cstdio>
@@ -63,9 +63,17 @@ template <class T> static std::vector<T> read_bin(const std::string& path) {
   std::string d = read_file(path); std::vector<T> v(d.size() / sizeof(T)); memcpy(v.data(), d.data(), v.size() * sizeof(T)); return v;
 }
 
+// f32 -> bf16 storage bits, round to nearest even (reference: mvm_exec.cu:1607); NaN stays NaN, infinities stay.
+static uint16_t bf16_rne(float f) {
+  uint32_t u; memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffffu) ? 0x40u : 0u));
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
 static void usage() {
   fprintf(stderr, "usage: kvm_exec [options] bundle_dir...\n"
-                  "  --golden [--golden-tol R]   compare with <bundle_dir>/golden.json (one bundle): buffers (relative L2), versions, reads\n"
+                  "  --golden [--golden-tol R] [--golden-tol-bf16 R]   compare with <bundle_dir>/golden.json (one bundle): buffers (relative\n"
+                  "                              L2; bf16-storage buffers by the second tolerance, default 1e-2), versions, reads\n"
                   "  --dump-bin DIR i,j,..       write buffers (widened to f32 / raw i32) to DIR/<index>.bin\n"
                   "  --trace-csv FILE            per-task timeline   --repeat N   run the graph N times (timed)   --timeout-s N\n"
                   "  --dump-buffers              print every buffer (reference text format)\n"
@@ -73,7 +81,7 @@ static void usage() {
 }
 
 int main(int argc, char** argv) {
-  std::vector<std::string> dirs; bool golden = false, quiet = false, trace = true, dump_text = false; float tol = 1e-6f;
+  std::vector<std::string> dirs; bool golden = false, quiet = false, trace = true, dump_text = false; float tol = 1e-6f, tol_bf16 = 1e-2f;
   const char* csv = nullptr; std::string dump_dir; std::vector<int> dump_idx; int repeat = 1, blocks = 0; long long timeout_s = 20;
   for (int i = 1; i < argc; ++i) {
     std::string a = argv[i];
@@ -81,6 +89,7 @@ int main(int argc, char** argv) {
     if (a == "--golden") golden = true;
     else if (a == "--dump-buffers") dump_text = true;
     else if (a == "--golden-tol") tol = (float)atof(next());
+    else if (a == "--golden-tol-bf16") tol_bf16 = (float)atof(next());
     else if (a == "--trace-csv") csv = next();
     else if (a == "--repeat") repeat = atoi(next());
     else if (a == "--timeout-s") timeout_s = atoll(next());
@@ -114,13 +123,22 @@ int main(int argc, char** argv) {
       if (kind == "fill") { init.kind = KVM_INIT_FILL; init.value = (float)in.need("value").n; }
       else if (kind == "values") {
         init.kind = KVM_INIT_VALUES; const auto& vals = in.need("values").a;
+        if ((long long)vals.size() != (long long)rows * cols)   // the reference refuses a short or long array the same way
+          throw std::runtime_error("buffer " + jb.need("name").s + ": buffer init size " + std::to_string(vals.size()) + " != " +
+                                   std::to_string((long long)rows * cols));
         if (dt == 1) { for (auto& v : vals) vi.push_back((int32_t)v.n); init.values = vi.data(); }
-        else if (dt == 2) { for (auto& v : vals) { float f = (float)v.n; uint32_t u; memcpy(&u, &f, 4); vh.push_back((uint16_t)(u >> 16)); } init.values = vh.data(); }
+        else if (dt == 2) { for (auto& v : vals) vh.push_back(bf16_rne((float)v.n)); init.values = vh.data(); }
         else { for (auto& v : vals) vf.push_back((float)v.n); init.values = vf.data(); }
       } else if (kind == "seeded") {
         init.kind = KVM_INIT_SEEDED; init.seed = strtoull(in.need("seed").s.c_str(), nullptr, 10); init.draws = (int)in.need("draws").n;
         init.bias = (float)in.need("bias").n; init.coef = (float)in.need("coef").n;
-      } else if (kind == "file") { init.kind = KVM_INIT_VALUES; raw = read_file(dirs[0] + "/" + in.need("path").s); init.values = raw.data(); }
+      } else if (kind == "file") {
+        init.kind = KVM_INIT_VALUES; raw = read_file(dirs[0] + "/" + in.need("path").s);
+        const size_t want = (size_t)rows * cols * (dt == 2 ? 2 : 4);
+        if (raw.size() != want)
+          throw std::runtime_error("buffer " + jb.need("name").s + ": buffer init size " + std::to_string(raw.size()) + " bytes != " + std::to_string(want));
+        init.values = raw.data();
+      }
       else throw std::runtime_error("unknown init kind " + kind);
       if (kvm_add_buffer(ex.get(), rows, cols, dt, &init) < 0) throw std::runtime_error(std::string("add_buffer: ") + kvm_last_error(ex.get()));
       names.push_back(jb.need("name").s);
@@ -152,21 +170,31 @@ int main(int argc, char** argv) {
         if (idx < 0) { ++bad; continue; }
         size_t n = kv.second.a.size(); std::vector<float> got(n);
         if (kvm_read_buffer(ex.get(), idx, got.data(), n) < 0) { ++bad; continue; }
-        bool is_int = kvm_buffer_dtype(ex.get(), idx) == 1; double num = 0, den = 0;
+        const int bdt = kvm_buffer_dtype(ex.get(), idx);
+        bool is_int = bdt == 1; double num = 0, den = 0;
+        const float btol = bdt == 2 ? tol_bf16 : tol;   // bf16 storage: a stored value may round to the neighbouring bf16
         for (size_t i = 0; i < n; ++i) {
           if (is_int) { int32_t gi; memcpy(&gi, &got[i], 4); if (gi != (int32_t)kv.second.a[i].n) ++bad; continue; }
           double w = kv.second.a[i].n, d = got[i] - w; num += d * d; den += w * w;
         }
         float rel = (float)(std::sqrt(num) / std::max(1e-30, std::sqrt(den))); worst = std::max(worst, rel);
-        if (rel > tol) { if (!quiet) fprintf(stderr, "golden: buffer %s relative L2 %.3g > %.3g\n", kv.first.c_str(), rel, tol); ++bad; }
+        if (rel > btol) { if (!quiet) fprintf(stderr, "golden: buffer %s relative L2 %.3g > %.3g\n", kv.first.c_str(), rel, btol); ++bad; }
       }
       std::vector<int32_t> ver(nvars); kvm_versions(ex.get(), ver.data(), nvars);
       std::map<std::string, int> vid; for (auto& jv : metas[0].need("variables").a) vid[jv.need("name").s] = (int)jv.num("id", 0);
       for (auto& kv : g.need("versions").o) if (ver[vid[kv.first]] != (int)kv.second.n) { ++bad; if (!quiet) fprintf(stderr, "golden: version %s\n", kv.first.c_str()); }
+      std::map<std::pair<int, int>, int> pub;   // (variable, version) -> publishing task
+      for (auto& jp : metas[0].need("publishers").a) pub[{(int)jp.num("var", -1), (int)jp.num("version", -1)}] = (int)jp.num("task", -1);
       for (auto& jr : metas[0].need("reads").a) {   // the task carrying each read's wait saw an admissible version
-        int slot = (int)jr.num("task", -1); const Json* gate = jr.get("gate"); if (gate && gate->t == Json::N) slot = (int)gate->n;
-        int want = (int)jr.num("version", 0); bool exact = jr.need("policy").s == "exact";
-        const KvmTrace& t = tr[slot]; bool ok = t.ver0 >= want && (!exact || (t.ver0 == want && t.ver1 == want));
+        int task = (int)jr.num("task", -1), slot = task; const Json* gate = jr.get("gate"); if (gate && gate->t == Json::N) slot = (int)gate->n;
+        int var = (int)jr.num("var", -1), want = (int)jr.num("version", 0); bool exact = jr.need("policy").s == "exact";
+        const KvmTrace& t = tr[slot];
+        bool ok;
+        if (t.ver0 < 0) {   // a read of the initial version carries no wait: it held if the next publisher started after it
+          auto nx = pub.find({var, want + 1});
+          ok = want == 0 && (!exact || nx == pub.end() || tr[nx->second].start >= tr[task].end);
+        } else ok = t.ver0 >= want && (!exact || (t.ver0 == want && t.ver1 == want));
+        if (!ok && !quiet) fprintf(stderr, "golden: read %s of variable %d at version %d not admissible\n", jr.need("name").s.c_str(), var, want);
         bad += !ok;
       }
       if (!quiet) fprintf(stderr, "golden: worst buffer relative L2 %.3g (tolerance %.3g)\n", worst, tol);

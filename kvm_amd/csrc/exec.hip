@@ -640,6 +640,15 @@ KvmExec* kvm_create(const KvmConfig* cfg) {
   if (hipSetDevice(c.device) != hipSuccess) { g_err = "hipSetDevice failed"; return nullptr; }
   hipDeviceProp_t p;
   if (hipGetDeviceProperties(&p, c.device) != hipSuccess) { g_err = "hipGetDeviceProperties failed"; return nullptr; }
+  // Every worker of the persistent kernel must be resident at once (a worker that never starts leaves its queue's tasks
+  // unrun and the others waiting): the grid is at most what the occupancy calculator admits per CU times the CUs.
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kvm_exec_kernel, KVM_THREADS, 0) != hipSuccess || per_cu < 1) {
+    g_err = "the executor kernel does not fit on a CU (occupancy query)"; return nullptr;
+  }
+  if (c.blocks < 0 || (long long)c.blocks > (long long)per_cu * p.multiProcessorCount) {
+    g_err = "blocks exceeds the co-resident capacity of the device (" + std::to_string(per_cu * p.multiProcessorCount) + ")"; return nullptr;
+  }
   KvmExec* ex = new KvmExec();
   ex->cfg = c; ex->dev = c.device; ex->cus = p.multiProcessorCount;
   ex->grid = c.blocks > 0 ? c.blocks : ex->cus;

@@ -158,3 +158,10 @@ def test_unsatisfiable_wait_times_out():
     assert res['err_code'] == 15
     assert res['done'] == 1
     ex.close()
+
+
+def test_grid_beyond_coresidency_is_refused():
+    """A persistent executor needs every worker resident at once: more workgroups than the device holds is refused."""
+    from kvm_amd.executor import KvmError
+    with pytest.raises(KvmError, match='co-resident'):
+        Executor(blocks=100000)

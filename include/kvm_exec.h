@@ -32,7 +32,16 @@ typedef struct KvmConfig {
   int device;                  // HIP device ordinal
   int aging_us;                // 0: strict priority among ready tasks; else a ready task gains one priority level per
                                //   aging_us of waiting (reference: MvmConfig::aging_us, mvm_exec.cu:375)
+  int path;                    // KVM_PATH_*: dynamic scheduler, static per-worker programs, or chosen per graph
+                               //   (reference: the --static / --dynamic path choice, mvm_exec.cu:2146-2164)
 } KvmConfig;
+
+// Execution paths. DYNAMIC: ready queues and dependency counters. STATIC: the graph is planned on the host into one
+// program per worker (list scheduling), cross-worker dependencies are waits on progress watermarks (needs every
+// version wait decided inside the graph). AUTO: STATIC when the graph allows it and its mean estimated task cost is at
+// most KVM_STATIC_MAX_MEAN_US (short tasks, where queue and counter overheads dominate), else DYNAMIC.
+enum KvmPath { KVM_PATH_DYNAMIC = 0, KVM_PATH_STATIC = 1, KVM_PATH_AUTO = 2 };
+#define KVM_STATIC_MAX_MEAN_US 12.0
 
 // Buffer initialisation (reference: MvmInit, mvm_exec.cu:431-437).
 enum KvmInitKind { KVM_INIT_ZERO = 0, KVM_INIT_FILL = 1, KVM_INIT_VALUES = 2, KVM_INIT_SEEDED = 3 };
@@ -123,6 +132,19 @@ int kvm_seeded_fill_test(unsigned long long seed, long long n, int draws, float 
 // counterpart in the reference: a dispatch of known HBM traffic for calibrating byte counters (rocprofv3 FETCH_SIZE /
 // WRITE_SIZE) against the executor's own dispatches.
 int kvm_copy_probe(long long bytes);
+
+// The static planner alone, on the host (no GPU): plans the bundle for `workers` workers exactly as KVM_PATH_STATIC does
+// at upload. Outputs (caller-sized): worker_of[ntasks], pos_of[ntasks] (index in the worker's program), nwaits[ntasks]
+// (cross-worker waits kept after reduction), publishes[ntasks], and the waits themselves as (worker, need) pairs in
+// task order into waits[2 * wait_cap] (a task's waits follow the previous task's); stats[4] = predicted makespan us,
+// summed cost us, cross-worker edges, DAG edges. Returns 0, or KVM_STATUS_INVALID (reason in err; also when the waits
+// exceed wait_cap). No counterpart in the reference as a C entry (its planner is mvm_static_plan,
+// include/mvm_static.h); for tests and tooling.
+int kvm_static_plan(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs,
+                    int workers, int* worker_of, int* pos_of, int* nwaits, int* publishes, int* waits, int wait_cap,
+                    double* stats, char* err, int errlen);
+// The path a launch of this executor uses (KVM_PATH_DYNAMIC or KVM_PATH_STATIC; decided at the first start), or < 0.
+int kvm_path(const KvmExec* ex);
 
 // Device scratch of kvm_run_noalloc: one array per GPU the library runs on, held until the process ends.
 #define KVM_NOALLOC_SCRATCH_BYTES (32u << 20)

@@ -71,6 +71,15 @@ struct KvmDevState {
   int* park_head;             // [nvars] park list heads, -1 empty
   KvmCounters* cnt;
   KvmTrace* trace;            // [ntasks] or null
+  // Static path (kvm_static_kernel): worker w runs tasks sprog[sprog_off[w] .. sprog_off[w + 1]); task t first waits for
+  // sprogress[sw[2k]] >= sw[2k + 1] for k in [swait_off[t], swait_off[t + 1]); after it, a task with spub[t] set stores its
+  // program position + 1 into sprogress[w].
+  const int* sprog_off;
+  const int* sprog;
+  const int* swait_off;
+  const int* sw;
+  const int* spub;
+  int* sprogress;            // [grid]
   int ntasks, nvars, trace_on, nq, qcap, grid, nb, ncells;
   unsigned long long timeout_ticks;   // stall timeout in wall_clock64 ticks (100 MHz)
   unsigned long long aging_ticks;     // wall_clock64 ticks of waiting worth one priority level (0: strict priority)

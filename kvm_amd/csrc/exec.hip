@@ -34,6 +34,7 @@
 #include "ops_decode.h"
 #include "ops_stream.h"
 #include "validate.h"
+#include "static_plan.h"
 
 using namespace kvm;
 
@@ -410,10 +411,82 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
   }
   for (long long k = i; k < (long long)S.ncells; k += stride) S.ready[k] = -1;
   for (int k = i; k < S.nvars; k += stride) { S.version[k] = base_versions[k]; S.park_head[k] = -1; }
-  for (int k = i; k < S.grid; k += stride) S.done_blk[k] = 0;
+  for (int k = i; k < S.grid; k += stride) { S.done_blk[k] = 0; if (S.sprogress) S.sprogress[k] = 0; }
   if (i < S.nq * S.nb) { KvmQueue z = {}; S.queues[i] = z; }
   if (i == 0) { KvmCounters z = {}; *S.cnt = z; }
 }
+// The static path: worker w runs its program (the host plan) in order. Before a task, wave 0 waits for its cross-worker
+// dependencies (lane k polls wait k: progress[worker] >= need) and acquires; after it, every wave waits for its own
+// write-through stores and the barrier orders them before thread 0 publishes the program position, when another
+// worker waits for this task. Version publications keep the dynamic path's CAS (a gap is still reported); no task
+// parks, the plan orders every waiter after its publisher. A wait gives up after timeout_ticks (TIMEOUT) or when any
+// worker reports an error, so every worker exits.
+__global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState S) {
+  __shared__ __attribute__((aligned(16))) char smem[KVM_LDS_BYTES];
+  __shared__ int s_go;
+  __shared__ __attribute__((aligned(16))) KvmRec s_rec;
+  const int t = threadIdx.x, w = blockIdx.x;
+  const int p0 = S.sprog_off[w], p1 = S.sprog_off[w + 1];
+  for (int i = p0; i < p1; ++i) {
+    const int slot = S.sprog[i];
+    if (t < 64) {
+      const int k0 = S.swait_off[slot], k1 = S.swait_off[slot + 1];
+      int bad = 0;
+      for (int k = k0 + t; k < k1 && !bad; k += 64) {
+        const int ww = S.sw[2 * k], need = S.sw[2 * k + 1];
+        const unsigned long long since = wall_clock64();
+        for (unsigned polls = 0; ld_relaxed(&S.sprogress[ww]) < need; ++polls) {
+          if (ld_relaxed(&S.cnt->err_code) != 0) { bad = 1; break; }
+          __builtin_amdgcn_s_sleep(1);
+          if ((polls & 1023) == 1023 && wall_clock64() - since > S.timeout_ticks) {
+            int z = 0;
+            if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_TIMEOUT, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+              S.cnt->err_slot = slot; S.cnt->err_a = ww; S.cnt->err_b = need;
+            }
+            bad = 1;
+            break;
+          }
+        }
+      }
+      bad = __ballot(bad) != 0ull;
+      fence_acquire();                       // the publishers' stores are visible from here on
+      if (t == 0) s_go = !bad && ld_relaxed(&S.cnt->err_code) == 0;
+    }
+    __syncthreads();
+    if (!s_go) break;
+    if (t < KVM_REC_VEC) ((LDS u32x4_t*)&s_rec)[t] = ((const u32x4_t*)(S.recs + slot))[t];
+    __syncthreads();
+    const MvmTaskDesc& d = s_rec.desc;
+    if (t == 0 && S.trace_on) {
+      KvmTrace& tr = S.trace[slot];
+      tr.start = wall_clock64();
+      tr.block = w; tr.xcc = xcc_id();
+      tr.ver0 = d.wait_var >= 0 ? ld_relaxed(&S.version[d.wait_var]) : -1;
+      tr.exec_count += 1;
+      if (d.wait_var >= 0 && tr.ver0 < d.wait_ver) {
+        int z = 0;
+        if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_WAIT_VIOLATION, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+          S.cnt->err_slot = slot;
+      }
+    }
+    __syncthreads();
+    Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
+    dispatch(d.op_id, c);
+    wait_stores();
+    __syncthreads();
+    if (t == 0) {
+      if (S.trace_on) {
+        KvmTrace& tr = S.trace[slot];
+        tr.ver1 = d.wait_var >= 0 ? ld_relaxed(&S.version[d.wait_var]) : -1;
+        tr.end = wall_clock64();
+      }
+      if (d.pub_var >= 0) publish(S, slot, d.pub_var, d.pub_ver);
+      if (S.spub[slot]) st_relaxed(&S.sprogress[w], i - p0 + 1);
+      st_relaxed(&S.done_blk[w], ld_relaxed(&S.done_blk[w]) + 1);
+    }
+  }
+}
+
 // Roots (tasks with no predecessors). Roots without a version wait go to fixed cells computed on the host (queue
 // t % nq, in index order within the queue), written by all threads at once; the queue tails then start past them.
 // Roots with a version wait are released one by one by thread 0 afterwards (they park until the version is published,
@@ -492,6 +565,8 @@ struct KvmExec {
   std::string err;
   // device memory of the placed graph (one hipMalloc each, freed by kvm_destroy)
   std::vector<void*> allocs;
+  int path = -1;                           // the path launches use: KVM_PATH_DYNAMIC or KVM_PATH_STATIC (set at upload)
+  kvms::Plan splan;
   struct LaunchArgs L{};
   KvmDevState S{};
 };
@@ -628,6 +703,7 @@ extern "C" {
 
 void kvm_config_default(KvmConfig* c) {
   c->blocks = 0; c->trace_on = 1; c->num_vars = 64; c->timeout_us = 20ull * 1000000ull; c->device = 0; c->aging_us = 0;
+  c->path = KVM_PATH_DYNAMIC;
 }
 
 const char* kvm_last_error(const KvmExec* ex) { return ex ? ex->err.c_str() : g_err.c_str(); }
@@ -637,6 +713,7 @@ KvmExec* kvm_create(const KvmConfig* cfg) {
   if (cfg) c = *cfg;
   if (c.num_vars < 1 || c.num_vars > (1 << 20)) { g_err = "num_vars out of range"; return nullptr; }
   if (c.aging_us < 0) { g_err = "aging_us must be >= 0"; return nullptr; }
+  if (c.path < KVM_PATH_DYNAMIC || c.path > KVM_PATH_AUTO) { g_err = "path must be KVM_PATH_DYNAMIC, KVM_PATH_STATIC or KVM_PATH_AUTO"; return nullptr; }
   if (hipSetDevice(c.device) != hipSuccess) { g_err = "hipSetDevice failed"; return nullptr; }
   hipDeviceProp_t p;
   if (hipGetDeviceProperties(&p, c.device) != hipSuccess) { g_err = "hipGetDeviceProperties failed"; return nullptr; }
@@ -768,6 +845,49 @@ int kvm_submit(KvmExec* ex, const MvmTaskDesc* tasks, int ntasks, const int32_t*
   return 0;
 }
 
+// Estimated task cost in microseconds for the static planner (only relative weights and the auto path's threshold use
+// it): a fixed per-task cost, plus for GEMM tiles their FLOPs at a typical in-task rate (bf16 MFMA about 3 TFLOP/s per
+// CU, fp32 about 0.25), for attention tasks their score pairs, for streaming operators the bytes of their range.
+static double task_cost_us(const MvmTaskDesc& d, const int32_t* a) {
+  const int op = d.op_id;
+  if (op == 34 || op == 114 || op == 122 || op == 302 || op == 304 || op == 308) {
+    const long long m0 = a[6], n0 = a[7], M = a[8], N = a[9], K = a[10], fl = a[11];
+    int tm = 64, tn = 64;
+    if (op == 122 || op == 308) { tm = 128; tn = 256; }
+    else if (op == 304) { tm = 256; tn = 256; }
+    else if (op == 302) { tm = fl & 64 ? 256 : 128; tn = 256; }
+    else if (fl & 64) { tm = 256; tn = 128; }
+    else if (fl & 32) { tm = tn = 128; }
+    const double flops = 2.0 * (double)std::max(0ll, std::min(M, m0 + tm) - m0) * (double)std::max(0ll, std::min(N, n0 + tn) - n0) * (double)K;
+    return 3.0 + flops / (op == 34 ? 0.25e6 : 3.0e6);
+  }
+  if (op == 45 || op == 47 || op == 48) {   // q0 / k0 block of 128 rows against up to T keys: about T * 128 * hd * 4 flop
+    const int T = op == 48 ? a[11] : a[8], hd = op == 48 ? a[13] : a[11];
+    return 5.0 + 4.0 * 128.0 * (double)T * hd / 1.0e6;
+  }
+  return 3.0;
+}
+
+static int plan_static(KvmExec* ex, bool forced) {
+  std::string why;
+  if (!kvms::feasible(ex->tasks.data(), (int)ex->tasks.size(), ex->base_versions.data(), (int)ex->base_versions.size(), &why)) {
+    if (forced) { ex->err = "static path: " + why; return KVM_STATUS_INVALID; }
+    return 0;
+  }
+  std::vector<double> cost(ex->tasks.size());
+  double total = 0;
+  for (size_t i = 0; i < ex->tasks.size(); ++i) { cost[i] = task_cost_us(ex->tasks[i], ex->args.data() + ex->tasks[i].args_off); total += cost[i]; }
+  if (!forced && total / (double)cost.size() > KVM_STATIC_MAX_MEAN_US) return 0;
+  try {
+    ex->splan = kvms::plan(ex->tasks.data(), (int)ex->tasks.size(), ex->succ.data(), cost, ex->grid);
+  } catch (const std::exception& e) {
+    ex->err = std::string("static path: ") + e.what();
+    return KVM_STATUS_INVALID;
+  }
+  ex->path = KVM_PATH_STATIC;
+  return 0;
+}
+
 static int do_upload(KvmExec* ex) {
   if (ex->tasks.empty()) { ex->err = "nothing submitted"; return KVM_STATUS_INVALID; }
   std::vector<MvmBuf> table(ex->bufs.size());
@@ -784,22 +904,42 @@ static int do_upload(KvmExec* ex) {
   const int rc = place_graph(g, ex->tasks, (int)ex->base_versions.size(), ex->grid, ex->cfg.trace_on != 0, ex->cfg.aging_us,
                              ex->cfg.timeout_us, alloc, ex->stream, ex->S, ex->L, ex->err);
   if (rc) return rc == KVM_STATUS_TOO_BIG ? KVM_STATUS_HIP_ERROR : rc;
+  ex->path = KVM_PATH_DYNAMIC;
+  if (ex->cfg.path != KVM_PATH_DYNAMIC) {
+    if (int r = plan_static(ex, ex->cfg.path == KVM_PATH_STATIC)) return r;
+    if (ex->path == KVM_PATH_STATIC) {   // the plan's arrays next to the dynamic state (a later relaunch may use either)
+      const kvms::Plan& P = ex->splan;
+      std::vector<int> sw(2 * P.waits.size()), spub(P.publishes.begin(), P.publishes.end());
+      for (size_t k = 0; k < P.waits.size(); ++k) { sw[2 * k] = P.waits[k].worker; sw[2 * k + 1] = P.waits[k].need; }
+      auto put = [&](const std::vector<int>& v) -> int* {
+        void* d = alloc(std::max<size_t>(v.size(), 1) * sizeof(int));
+        if (d && !v.empty() && hipMemcpy(d, v.data(), v.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+        return (int*)d;
+      };
+      KvmDevState& S = ex->S;
+      S.sprog_off = put(P.prog_off); S.sprog = put(P.prog); S.swait_off = put(P.wait_off); S.sw = put(sw); S.spub = put(spub);
+      S.sprogress = (int*)alloc(ex->grid * sizeof(int));
+      if (!S.sprog_off || !S.sprog || !S.swait_off || !S.sw || !S.spub || !S.sprogress) { ex->err = "static path: device memory"; return KVM_STATUS_HIP_ERROR; }
+    }
+  }
   ex->uploaded = true;
   return 0;
 }
 
 // Reset of the scheduler state, root seeding and the persistent kernel, on one stream.
-static void launch_graph(const KvmDevState& S, const LaunchArgs& L, int grid, hipStream_t st, hipEvent_t before_exec, hipEvent_t after_exec) {
+static void launch_graph(const KvmDevState& S, const LaunchArgs& L, int grid, hipStream_t st, hipEvent_t before_exec, hipEvent_t after_exec,
+                         bool static_path = false) {
   hipLaunchKernelGGL(kvm_reset_kernel, dim3(std::min(1024, (S.ntasks + 255) / 256 + 1)), dim3(256), 0, st, S, (const int*)L.base);
-  hipLaunchKernelGGL(kvm_seed_kernel, dim3(1), dim3(1024), 0, st, S, L.roots, L.root_cell, L.nfixed, L.nroots, L.fixed_tail);
+  if (!static_path) hipLaunchKernelGGL(kvm_seed_kernel, dim3(1), dim3(1024), 0, st, S, L.roots, L.root_cell, L.nfixed, L.nroots, L.fixed_tail);
   if (before_exec) hipEventRecord(before_exec, st);
-  hipLaunchKernelGGL(kvm_exec_kernel, dim3(grid), dim3(KVM_THREADS), 0, st, S);
+  if (static_path) hipLaunchKernelGGL(kvm_static_kernel, dim3(grid), dim3(KVM_THREADS), 0, st, S);
+  else hipLaunchKernelGGL(kvm_exec_kernel, dim3(grid), dim3(KVM_THREADS), 0, st, S);
   if (after_exec) hipEventRecord(after_exec, st);
 }
 
 static int launch_once(KvmExec* ex, hipEvent_t before_exec = nullptr, hipEvent_t after_exec = nullptr) {
   HIPCK(hipMemcpyAsync(ex->L.base, ex->base_versions.data(), ex->base_versions.size() * sizeof(int), hipMemcpyHostToDevice, ex->stream));
-  launch_graph(ex->S, ex->L, ex->grid, ex->stream, before_exec, after_exec);
+  launch_graph(ex->S, ex->L, ex->grid, ex->stream, before_exec, after_exec, ex->path == KVM_PATH_STATIC);
   HIPCK(hipGetLastError());
   return 0;
 }
@@ -909,6 +1049,37 @@ int kvm_validate(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int 
 }
 
 int kvm_ntasks(const KvmExec* ex) { return (int)ex->tasks.size(); }
+
+int kvm_path(const KvmExec* ex) { return ex ? ex->path : KVM_STATUS_INVALID; }
+
+int kvm_static_plan(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs,
+                    int workers, int* worker_of, int* pos_of, int* nwaits, int* publishes, int* waits, int wait_cap,
+                    double* stats, char* err, int errlen) {
+  try {
+    if (ntasks < 1 || workers < 1 || nedges < 0 || nargs < 0) throw std::invalid_argument("empty graph or no workers");
+    std::vector<double> cost(ntasks);
+    for (int i = 0; i < ntasks; ++i) {
+      if (tasks[i].args_off < 0 || tasks[i].args_off + tasks[i].args_words > nargs || tasks[i].succ_off < 0 ||
+          tasks[i].succ_off + tasks[i].succ_cnt > nedges) throw std::invalid_argument("task " + std::to_string(i) + ": range outside the bundle");
+      for (int k = 0; k < tasks[i].succ_cnt; ++k) {
+        const int s2 = succ[tasks[i].succ_off + k];
+        if (s2 < 0 || s2 >= ntasks || s2 == i) throw std::invalid_argument("task " + std::to_string(i) + ": successor out of range");
+      }
+      cost[i] = task_cost_us(tasks[i], args + tasks[i].args_off);
+    }
+    const kvms::Plan P = kvms::plan(tasks, ntasks, succ, cost, workers);
+    for (int i = 0; i < ntasks; ++i) {
+      worker_of[i] = P.worker_of[i]; pos_of[i] = P.pos_of[i]; nwaits[i] = P.wait_off[i + 1] - P.wait_off[i]; publishes[i] = P.publishes[i];
+    }
+    if ((long long)P.waits.size() > wait_cap) throw std::invalid_argument("more waits than wait_cap");
+    for (size_t k = 0; k < P.waits.size(); ++k) { waits[2 * k] = P.waits[k].worker; waits[2 * k + 1] = P.waits[k].need; }
+    stats[0] = P.makespan_us; stats[1] = P.work_us; stats[2] = P.cross_edges; stats[3] = P.edges;
+    return 0;
+  } catch (const std::exception& e) {
+    if (err && errlen > 0) snprintf(err, errlen, "%s", e.what());
+    return KVM_STATUS_INVALID;
+  }
+}
 
 int kvm_set_trace(KvmExec* ex, int on) {
   if (on && !ex->cfg.trace_on) { ex->err = "kvm_set_trace: the executor was created without a trace buffer"; return KVM_STATUS_INVALID; }

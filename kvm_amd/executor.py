@@ -27,7 +27,10 @@ ERRORS = {0: 'OK', 1: 'BAD_OP', 2: 'BAD_ARITY', 3: 'BAD_BUF_INDEX', 4: 'BAD_BUF'
 
 class KvmConfig(ctypes.Structure):
     _fields_ = [('blocks', ctypes.c_int), ('trace_on', ctypes.c_int), ('num_vars', ctypes.c_int), ('timeout_us', ctypes.c_ulonglong),
-                ('device', ctypes.c_int), ('aging_us', ctypes.c_int)]
+                ('device', ctypes.c_int), ('aging_us', ctypes.c_int), ('path', ctypes.c_int)]
+
+
+PATH_DYNAMIC, PATH_STATIC, PATH_AUTO = 0, 1, 2
 
 
 class KvmInit(ctypes.Structure):
@@ -72,6 +75,8 @@ def lib():
             'kvm_validate': (I, [P, I, P, I, P, I, P, I, I, ctypes.c_char_p, I]),
             'kvm_seeded_fill_test': (I, [ctypes.c_ulonglong, ctypes.c_longlong, I, ctypes.c_float, ctypes.c_float, P]),
             'kvm_copy_probe': (I, [ctypes.c_longlong]),
+            'kvm_path': (I, [P]),
+            'kvm_static_plan': (I, [P, I, P, I, P, I, I, P, P, P, P, P, I, P, ctypes.c_char_p, I]),
             'kvm_run_noalloc': (I, [P, I, P, I, P, I, P, I, P, I, I, ctypes.c_ulonglong, P, P, ctypes.c_char_p, I]),
         }
         for name, (res, args) in sig.items():
@@ -94,12 +99,12 @@ class Executor:
     """
 
     def __init__(self, num_vars: int = 64, trace: bool = True, timeout_s: float = 20.0, blocks: int = 0, device: int = 0,
-                 aging_us: int = 0):
+                 aging_us: int = 0, path: int = 0):
         L = lib()
         cfg = KvmConfig()
         L.kvm_config_default(ctypes.byref(cfg))
         cfg.num_vars, cfg.trace_on, cfg.timeout_us, cfg.blocks, cfg.device = max(1, num_vars), int(trace), int(timeout_s * 1e6), blocks, device
-        cfg.aging_us = aging_us
+        cfg.aging_us, cfg.path = aging_us, path
         self._h = L.kvm_create(ctypes.byref(cfg))
         if not self._h:
             raise KvmError(f'kvm_create: {L.kvm_last_error(None).decode()}')
@@ -198,6 +203,10 @@ class Executor:
         ex.submit(b)
         ex.meta = b.metadata
         return ex
+
+    def path(self) -> int:
+        """PATH_DYNAMIC or PATH_STATIC: the path launches use (decided at the first start)."""
+        return lib().kvm_path(self._h)
 
     def set_trace(self, on: bool):
         """Per-task tracing on / off for the following launches (needs an executor created with trace=True)."""
@@ -313,3 +322,24 @@ def run_noalloc(b: bl.LoadedBundle, buffer_ptrs: list[int], versions: list[int],
     res = {'rc': rc, 'err': err.value.decode(), 'err_code': r.err_code, 'err_slot': r.err_slot, 'done': r.done,
            'admitted': r.admitted, 'grid': r.grid}
     return res, ver.tolist()
+
+
+def static_plan(b: bl.LoadedBundle, workers: int) -> dict:
+    """kvm_static_plan: the static path's plan of bundle b for `workers` workers, computed on the host (no GPU)."""
+    n = b.ntasks
+    t = np.ascontiguousarray(b.tasks, np.int32)
+    s = np.ascontiguousarray(b.succ, np.int32) if b.succ.size else np.zeros(1, np.int32)
+    a = np.ascontiguousarray(b.args, np.int32) if b.args.size else np.zeros(1, np.int32)
+    out = {k: np.zeros(n, np.int32) for k in ('worker', 'pos', 'nwaits', 'publishes')}
+    stats = np.zeros(4, np.float64)
+    cap = int(b.succ.size) + 2 * n + 1
+    waits = np.zeros(2 * cap, np.int32)
+    err = ctypes.create_string_buffer(512)
+    rc = lib().kvm_static_plan(t.ctypes.data, n, s.ctypes.data, int(b.succ.size), a.ctypes.data, int(b.args.size), workers,
+                               out['worker'].ctypes.data, out['pos'].ctypes.data, out['nwaits'].ctypes.data,
+                               out['publishes'].ctypes.data, waits.ctypes.data, cap, stats.ctypes.data, err, 512)
+    if rc < 0:
+        raise KvmError(err.value.decode())
+    out.update(makespan_us=float(stats[0]), work_us=float(stats[1]), cross_edges=int(stats[2]), edges=int(stats[3]))
+    out['waits'] = waits[:2 * int(out['nwaits'].sum())].reshape(-1, 2)
+    return out

@@ -35,14 +35,19 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def build_executor(w, trace=False, blocks=0):
+PATH_NAMES = {0: 'dynamic', 1: 'static'}
+
+
+def build_executor(w, trace=False, blocks=0, path=2):
+    """Executor with the workload's buffers and graph submitted. path 2 (auto): the static path for graphs of short tasks
+    (mean estimated task cost at most KVM_STATIC_MAX_MEAN_US), the dynamic scheduler otherwise."""
     from kvm_amd import bundle as bl
     from kvm_amd import compiler
     from kvm_amd.executor import Executor
     t0 = time.perf_counter()
     lb = bl.load(compiler.compile_spec(w.spec))
     t1 = time.perf_counter()
-    ex = Executor(num_vars=max(1, len(lb.metadata['variables'])), trace=trace, timeout_s=60.0, blocks=blocks)
+    ex = Executor(num_vars=max(1, len(lb.metadata['variables'])), trace=trace, timeout_s=60.0, blocks=blocks, path=path)
     for m in lb.metadata['buffers']:
         ex.add_buffer(m['name'], m['rows'], m['cols'], m['dtype'], init=w.init_override.get(m['name'], m['init']))
     for v in lb.metadata['variables']:
@@ -72,7 +77,7 @@ def bench_decode(batch, steps, warmup, cpu):
     ms, kms, res = time_steps(ex, steps, warmup)
     byts = w.info['weight_bytes'] + w.info['kv_bytes_per_step']
     gbs = byts / (kms / 1e3) / 1e9
-    out = {'batch': batch, 'ms_per_token_step': round(ms, 4), 'kernel_ms': round(kms, 4), 'tok_s': round(batch * 1e3 / ms, 2),
+    out = {'batch': batch, 'path': PATH_NAMES.get(ex.path()), 'ms_per_token_step': round(ms, 4), 'kernel_ms': round(kms, 4), 'tok_s': round(batch * 1e3 / ms, 2),
            'hbm_gbs': round(gbs, 1), 'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'bytes_per_step': byts, 'tasks': lb.ntasks}
     log(f'  decode batch {batch}: {ms:.3f} ms/step, {out["tok_s"]} tok/s, {gbs:.0f} GB/s ({out["hbm_frac"]:.1%} of peak)')
     ex.close()
@@ -182,7 +187,7 @@ def bench_gpt(steps, warmup, cpu):
     busy = float(dur.sum() / (res['grid'] * (tr['end'].max() - tr['start'].min()) / 100e6))
     names = [m['name'] for m in lb.metadata['buffers']]
     loss = float(ex.read('loss')[0])
-    out = {'ms_per_step': round(ms, 3), 'kernel_ms': round(kms, 3), 'tflops': round(tflops, 1), 'mfma_frac_step': round(tflops / BF16_PEAK_TFLOPS, 4),
+    out = {'ms_per_step': round(ms, 3), 'path': PATH_NAMES.get(ex.path()), 'kernel_ms': round(kms, 3), 'tflops': round(tflops, 1), 'mfma_frac_step': round(tflops / BF16_PEAK_TFLOPS, 4),
            'mfma_frac_in_gemm_tasks': round(in_task['gemm'], 4), 'mfma_frac_in_attention_tasks': round(in_task['attention'], 4),
            'worker_busy_frac': round(busy, 4), 'tasks': lb.ntasks, 'edges': int(lb.succ.size), 'loss_after': loss,
            'step_flops': flops, 'params': w.info['params'], 'first_step_check': check}
@@ -236,7 +241,7 @@ def bench_small(name, w, steps_in_graph, reps, warmup, cpu):
     dur = (tr['end'] - tr['start']).astype(np.float64)
     span = float(tr['end'].max() - tr['start'].min())
     busy = float(dur.sum() / (res['grid'] * span))
-    out = {'us_per_step': round(kms * 1e3 / steps_in_graph, 2), 'launch_ms': round(kms, 4), 'steps_in_graph': steps_in_graph,
+    out = {'us_per_step': round(kms * 1e3 / steps_in_graph, 2), 'path': PATH_NAMES.get(ex.path()), 'launch_ms': round(kms, 4), 'steps_in_graph': steps_in_graph,
            'worker_busy_frac': round(busy, 4), 'tasks': lb.ntasks, 'edges': int(lb.succ.size)}
     log(f'  {name}: {out["us_per_step"]} us/step ({steps_in_graph} steps per launch, {lb.ntasks} tasks), workers busy {busy:.1%}')
     ex.close()
@@ -258,7 +263,7 @@ def bench_gpt355m(steps, warmup, cpu):
     ms, kms, res = time_steps(ex, steps, warmup)
     flops = w.info['flops']['total']
     tflops = flops / (kms / 1e3) / 1e12
-    out = {'ms_per_step': round(ms, 2), 'kernel_ms': round(kms, 2), 'tflops': round(tflops, 2), 'fp32_frac': round(tflops / FP32_PEAK_TFLOPS, 4),
+    out = {'ms_per_step': round(ms, 2), 'path': PATH_NAMES.get(ex.path()), 'kernel_ms': round(kms, 2), 'tflops': round(tflops, 2), 'fp32_frac': round(tflops / FP32_PEAK_TFLOPS, 4),
            'step_flops': flops, 'params': w.info['params'], 'tasks': lb.ntasks, 'first_step_check': check}
     log(f'  gpt-355m f32: {ms:.1f} ms/step, {tflops:.1f} TFLOP/s ({tflops / FP32_PEAK_TFLOPS:.1%} of the fp32 peak)')
     ex.close()

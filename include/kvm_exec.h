@@ -41,7 +41,7 @@ typedef struct KvmConfig {
 // version wait decided inside the graph). AUTO: STATIC when the graph allows it and its mean estimated task cost is at
 // most KVM_STATIC_MAX_MEAN_US (short tasks, where queue and counter overheads dominate), else DYNAMIC.
 enum KvmPath { KVM_PATH_DYNAMIC = 0, KVM_PATH_STATIC = 1, KVM_PATH_AUTO = 2 };
-#define KVM_STATIC_MAX_MEAN_US 12.0
+#define KVM_STATIC_MAX_MEAN_US 22.0
 
 // Buffer initialisation (reference: MvmInit, mvm_exec.cu:431-437).
 enum KvmInitKind { KVM_INIT_ZERO = 0, KVM_INIT_FILL = 1, KVM_INIT_VALUES = 2, KVM_INIT_SEEDED = 3 };

@@ -77,12 +77,13 @@ static void usage() {
                   "  --dump-bin DIR i,j,..       write buffers (widened to f32 / raw i32) to DIR/<index>.bin\n"
                   "  --trace-csv FILE            per-task timeline   --repeat N   run the graph N times (timed)   --timeout-s N\n"
                   "  --dump-buffers              print every buffer (reference text format)\n"
+                  "  --path auto|dynamic|static  scheduler: per-worker static programs, ready queues, or chosen from the graph (default auto)\n"
                   "  --blocks N   --no-trace   --quiet   --check-ops\n");
 }
 
 int main(int argc, char** argv) {
   std::vector<std::string> dirs; bool golden = false, quiet = false, trace = true, dump_text = false; float tol = 1e-6f, tol_bf16 = 1e-2f;
-  const char* csv = nullptr; std::string dump_dir; std::vector<int> dump_idx; int repeat = 1, blocks = 0; long long timeout_s = 20;
+  const char* csv = nullptr; std::string dump_dir; std::vector<int> dump_idx; int repeat = 1, blocks = 0, path = KVM_PATH_AUTO; long long timeout_s = 20;
   for (int i = 1; i < argc; ++i) {
     std::string a = argv[i];
     auto next = [&]() -> const char* { if (i + 1 >= argc) { usage(); exit(2); } return argv[++i]; };
@@ -95,6 +96,11 @@ int main(int argc, char** argv) {
     else if (a == "--timeout-s") timeout_s = atoll(next());
     else if (a == "--blocks") blocks = atoi(next());
     else if (a == "--no-trace") trace = false;
+    else if (a == "--path") {
+      std::string p = next();
+      if (p == "auto") path = KVM_PATH_AUTO; else if (p == "dynamic") path = KVM_PATH_DYNAMIC; else if (p == "static") path = KVM_PATH_STATIC;
+      else { usage(); return 2; }
+    }
     else if (a == "--quiet") quiet = true;
     else if (a == "--dump-bin") { dump_dir = next(); for (char* p = (char*)next(); *p;) { char* e; long v = strtol(p, &e, 10); if (e == p) { usage(); return 2; } dump_idx.push_back((int)v); p = *e == ',' ? e + 1 : e; } }
     else if (a == "--check-ops") { for (int id = 0; id < 400; ++id) if (const char* n = kvm_op_name(id)) printf("%3d %s\n", id, n); return 0; }
@@ -111,7 +117,7 @@ int main(int argc, char** argv) {
       nvars = std::max(nvars, (int)metas.back().need("variables").a.size());
     }
     KvmConfig cfg; kvm_config_default(&cfg);
-    cfg.num_vars = nvars; cfg.trace_on = (trace || golden || csv) ? 1 : 0; cfg.timeout_us = (unsigned long long)timeout_s * 1000000ull; cfg.blocks = blocks;
+    cfg.num_vars = nvars; cfg.trace_on = (trace || golden || csv) ? 1 : 0; cfg.timeout_us = (unsigned long long)timeout_s * 1000000ull; cfg.blocks = blocks; cfg.path = path;
     std::unique_ptr<KvmExec, void (*)(KvmExec*)> ex(kvm_create(&cfg), kvm_destroy);
     if (!ex) throw std::runtime_error(std::string("kvm_create: ") + kvm_last_error(nullptr));
     // buffers: the first bundle declares them; later bundles must name the same table (the reference's shared buffer model)
@@ -227,7 +233,7 @@ int main(int argc, char** argv) {
       fclose(f);
     }
     bool pass = r.err_code == 0 && bad == 0;
-    printf("%s: %d/%d tasks, %.3f ms%s\n", pass ? "OK" : "FAIL", r.done, r.admitted, r.kernel_ms, golden ? (bad ? ", golden MISMATCH" : ", golden match") : "");
+    printf("%s: %d/%d tasks, %.3f ms (%s path)%s\n", pass ? "OK" : "FAIL", r.done, r.admitted, r.kernel_ms, kvm_path(ex.get()) == KVM_PATH_STATIC ? "static" : "dynamic", golden ? (bad ? ", golden MISMATCH" : ", golden match") : "");
     return pass ? 0 : 1;
   } catch (const std::exception& e) {
     fprintf(stderr, "kvm_exec: %s\n", e.what());

@@ -14,7 +14,7 @@ from kvm_amd import compiler
 from cases import W
 
 CLI = REPO / 'kvm_amd' / '_build' / 'kvm_exec'
-LINE = re.compile(r'^(OK|FAIL): (\d+)/(\d+) tasks, [0-9.]+ ms(, golden (match|MISMATCH))?$')
+LINE = re.compile(r'^(OK|FAIL): (\d+)/(\d+) tasks, [0-9.]+ ms \((static|dynamic) path\)(, golden (match|MISMATCH))?$')
 
 
 def _run(*args, timeout=120):
@@ -34,14 +34,21 @@ def test_usage_and_check_ops_need_no_gpu():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('path', ['auto', 'dynamic', 'static'])
 @pytest.mark.parametrize('case', golden_cases())
-def test_golden_bundle_through_the_cli(case):
-    print(f'cli golden {case}', flush=True)
+def test_golden_bundle_through_the_cli(case, path):
+    """Every golden bundle on each scheduler path. The static path is refused only for a graph whose version waits
+    it cannot plan (exit 1 with the reason); auto then falls back to the dynamic path."""
+    print(f'cli golden {case} --path {path}', flush=True)
     n = json.loads((GOLDEN / case / 'metadata.json').read_text())['task_count']
-    rc, out, err = _run('--golden', '--golden-tol', '2e-5', GOLDEN / case)
+    rc, out, err = _run('--golden', '--golden-tol', '2e-5', '--path', path, GOLDEN / case)
+    if path == 'static' and rc == 1 and 'static' in err:
+        pytest.skip(f'static path refused: {err.strip()}')
     m = LINE.match(out.strip().split('\n')[-1])
     assert rc == 0 and m, (rc, out, err)
-    assert m.group(1) == 'OK' and int(m.group(2)) == int(m.group(3)) == n and m.group(5) == 'match'
+    assert m.group(1) == 'OK' and int(m.group(2)) == int(m.group(3)) == n and m.group(6) == 'match'
+    if path != 'auto':
+        assert m.group(4) == path
 
 
 @pytest.mark.gpu

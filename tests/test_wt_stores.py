@@ -18,7 +18,7 @@ import pytest
 
 from kvm_amd import build as kb
 
-KERNELS = ('kvm_exec_kernel', 'kvm_reset_kernel', 'kvm_seed_kernel', 'kvm_seeded_kernel', 'kvm_seeded_bf16_kernel',
+KERNELS = ('kvm_exec_kernel', 'kvm_static_kernel', 'kvm_reset_kernel', 'kvm_seed_kernel', 'kvm_seeded_kernel', 'kvm_seeded_bf16_kernel',
            'kvm_fill32_kernel', 'kvm_fill16_kernel', 'kvm_copy_probe_kernel')
 
 

@@ -260,6 +260,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
   __shared__ __attribute__((aligned(16))) KvmRec s_rec;
   MvmTaskDesc& s_desc = s_rec.desc;
   const int t = threadIdx.x;
+  int ndone = 0;              // tasks this worker finished (thread 0's count, stored after each task)
   for (;;) {
     if (S.tq) {
       if (wave() == 0) {
@@ -272,17 +273,18 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
       int slot = -1;
       if (ticket < (unsigned)S.qcount[q]) {
         unsigned long long since = wall_clock64();
-        int seen = -1;
+        int seen = -1, err = 0;
         for (unsigned polls = 0;; ++polls) {
-          slot = ld_relaxed(&S.ready[q * S.qcap + ticket]);
-          if (slot >= 0) break;
-          if (ld_relaxed(&S.cnt->err_code) != 0) break;
+          slot = ld_relaxed(&S.ready[q * S.qcap + ticket]);   // the cell and the error word: two loads in flight at once
+          err = ld_relaxed(&S.cnt->err_code);
+          if (slot >= 0 || err != 0) break;
           __builtin_amdgcn_s_sleep(1);
           if ((polls & 4095) == 4095 && stalled(S, since, seen, (int)ticket)) break;
         }
         if (slot >= 0) fence_acquire();   // the enqueuer's release: predecessors' data is visible from here on
+        if (err != 0) slot = -1;
       }
-      s_slot = ld_relaxed(&S.cnt->err_code) != 0 ? -1 : slot;
+      s_slot = slot;
     }
     __syncthreads();
     const int slot = s_slot;
@@ -395,9 +397,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
         }
       }
     }
-    if (t == 0) {
-      st_relaxed(&S.done_blk[blockIdx.x], ld_relaxed(&S.done_blk[blockIdx.x]) + 1);
-    }
+    if (t == 0) st_relaxed(&S.done_blk[blockIdx.x], ++ndone);
   }
 }
 
@@ -429,8 +429,11 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
   const int p0 = S.sprog_off[w], p1 = S.sprog_off[w + 1];
   for (int i = p0; i < p1; ++i) {
     const int slot = S.sprog[i];
+    // The record depends on nothing: wave 1 loads it while wave 0 waits for the task's dependencies.
+    if (t >= 64 && t < 64 + KVM_REC_VEC) ((LDS u32x4_t*)&s_rec)[t - 64] = ((const u32x4_t*)(S.recs + slot))[t - 64];
     if (t < 64) {
       const int k0 = S.swait_off[slot], k1 = S.swait_off[slot + 1];
+      const int err0 = ld_relaxed(&S.cnt->err_code);
       int bad = 0;
       for (int k = k0 + t; k < k1 && !bad; k += 64) {
         const int ww = S.sw[2 * k], need = S.sw[2 * k + 1];
@@ -450,13 +453,12 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
       }
       bad = __ballot(bad) != 0ull;
       fence_acquire();                       // the publishers' stores are visible from here on
-      if (t == 0) s_go = !bad && ld_relaxed(&S.cnt->err_code) == 0;
+      if (t == 0) s_go = !bad && err0 == 0;
     }
     __syncthreads();
     if (!s_go) break;
-    if (t < KVM_REC_VEC) ((LDS u32x4_t*)&s_rec)[t] = ((const u32x4_t*)(S.recs + slot))[t];
-    __syncthreads();
     const MvmTaskDesc& d = s_rec.desc;
+    const int pub_var = d.pub_var, pub_ver = d.pub_ver, wait_var = d.wait_var;   // s_rec is reloaded while thread 0 completes
     if (t == 0 && S.trace_on) {
       KvmTrace& tr = S.trace[slot];
       tr.start = wall_clock64();
@@ -469,20 +471,20 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
           S.cnt->err_slot = slot;
       }
     }
-    __syncthreads();
     Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
     dispatch(d.op_id, c);
+    const bool pub_pos = t == 0 && S.spub[slot];
     wait_stores();
     __syncthreads();
     if (t == 0) {
       if (S.trace_on) {
         KvmTrace& tr = S.trace[slot];
-        tr.ver1 = d.wait_var >= 0 ? ld_relaxed(&S.version[d.wait_var]) : -1;
+        tr.ver1 = wait_var >= 0 ? ld_relaxed(&S.version[wait_var]) : -1;
         tr.end = wall_clock64();
       }
-      if (d.pub_var >= 0) publish(S, slot, d.pub_var, d.pub_ver);
-      if (S.spub[slot]) st_relaxed(&S.sprogress[w], i - p0 + 1);
-      st_relaxed(&S.done_blk[w], ld_relaxed(&S.done_blk[w]) + 1);
+      if (pub_var >= 0) publish(S, slot, pub_var, pub_ver);
+      if (pub_pos) st_relaxed(&S.sprogress[w], i - p0 + 1);
+      st_relaxed(&S.done_blk[w], i - p0 + 1);
     }
   }
 }

@@ -282,7 +282,7 @@ def bench_sched():
     prev = []
     for i in range(2000):
         prev = [b.task('noop', after=prev)]
-    ex, lb = build_executor(Workload(b.spec()))
+    ex, lb = build_executor(Workload(b.spec()), path=0)
     _, ms, _ = time_steps(ex, 5, 2)
     hop_us = ms * 1e3 / 2000
     ex.close()
@@ -291,7 +291,7 @@ def bench_sched():
     for p in range(50):
         prev = [b.task('noop', after=prev) for _ in range(512)]
         prev = [b.task('noop', after=prev)]
-    ex, lb = build_executor(Workload(b.spec()))
+    ex, lb = build_executor(Workload(b.spec()), path=0)
     _, ms2, _ = time_steps(ex, 5, 2)
     ex.close()
     out = {'hop_us': round(hop_us, 3), 'phase_us_512wide': round(ms2 * 1e3 / 50, 2), 'tasks_per_s_wide': round(50 * 513 / (ms2 / 1e3))}

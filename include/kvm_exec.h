@@ -134,14 +134,18 @@ int kvm_seeded_fill_test(unsigned long long seed, long long n, int draws, float 
 int kvm_copy_probe(long long bytes);
 
 // The static planner alone, on the host (no GPU): plans the bundle for `workers` workers exactly as KVM_PATH_STATIC does
-// at upload. Outputs (caller-sized): worker_of[ntasks], pos_of[ntasks] (index in the worker's program), nwaits[ntasks]
-// (cross-worker waits kept after reduction), publishes[ntasks], and the waits themselves as (worker, need) pairs in
-// task order into waits[2 * wait_cap] (a task's waits follow the previous task's); stats[4] = predicted makespan us,
-// summed cost us, cross-worker edges, DAG edges. Returns 0, or KVM_STATUS_INVALID (reason in err; also when the waits
-// exceed wait_cap). No counterpart in the reference as a C entry (its planner is mvm_static_plan,
-// include/mvm_static.h); for tests and tooling.
+// at upload (flags KVM_PLAN_DISSOLVE: as untraced launches do, with the ordering no-ops dissolved). Outputs
+// (caller-sized): worker_of[ntasks], pos_of[ntasks] (index in the worker's program; both -1 for a dissolved no-op),
+// nwaits[ntasks] (cross-worker waits kept after reduction), publishes[ntasks], and the waits as (worker, need) pairs in
+// task order into waits[2 * wait_cap] (a task's waits follow the previous task's). A pair (-1 - count, start) is a
+// reference to a dissolved no-op's wait set: the `count` pairs from pair index `start`, stored after every task's list.
+// stats[5] = predicted makespan us, summed cost us, cross-worker edges, DAG edges, no-ops dissolved. Returns 0, or
+// KVM_STATUS_INVALID (reason in err; also when the pairs exceed wait_cap). No counterpart in the reference as a C entry
+// (its planner is mvm_static_plan, include/mvm_static.h; the dissolving transform mvm_dissolve_noops,
+// mvm_exec.cu:212-296); for tests and tooling.
+#define KVM_PLAN_DISSOLVE 1
 int kvm_static_plan(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs,
-                    int workers, int* worker_of, int* pos_of, int* nwaits, int* publishes, int* waits, int wait_cap,
+                    int workers, int flags, int* worker_of, int* pos_of, int* nwaits, int* publishes, int* waits, int wait_cap,
                     double* stats, char* err, int errlen);
 // The path a launch of this executor uses (KVM_PATH_DYNAMIC or KVM_PATH_STATIC; decided at the first start), or < 0.
 int kvm_path(const KvmExec* ex);

@@ -33,6 +33,8 @@ enum KvmErr {
 // Successor edges as uploaded to the device: the task index plus a bit set when the successor has exactly one
 // predecessor and no version wait (it is released by that predecessor without a counter).
 #define KVM_EDGE_DIRECT (1 << 30)
+#define KVM_SF_PUB 1             // static path, per task: another worker waits for this task's program position
+#define KVM_SF_PRE 2             // static path, per task: input-independent loads may be issued before the wait
 #define KVM_EDGE_INDEX (KVM_EDGE_DIRECT - 1)
 
 struct KvmCounters {
@@ -72,13 +74,14 @@ struct KvmDevState {
   KvmCounters* cnt;
   KvmTrace* trace;            // [ntasks] or null
   // Static path (kvm_static_kernel): worker w runs tasks sprog[sprog_off[w] .. sprog_off[w + 1]); task t first waits for
-  // sprogress[sw[2k]] >= sw[2k + 1] for k in [swait_off[t], swait_off[t + 1]); after it, a task with spub[t] set stores its
-  // program position + 1 into sprogress[w].
+  // sprogress[sw[2k]] >= sw[2k + 1] for k in [swait_off[t], swait_off[t + 1]); after it, a task with KVM_SF_PUB in
+  // sflag[t] stores its program position + 1 into sprogress[w]. KVM_SF_PRE: the task's input-independent loads may be
+  // issued before the wait.
   const int* sprog_off;
   const int* sprog;
   const int* swait_off;
   const int* sw;
-  const int* spub;
+  const int* sflag;
   int* sprogress;            // [grid]
   int ntasks, nvars, trace_on, nq, qcap, grid, nb, ncells;
   unsigned long long timeout_ticks;   // stall timeout in wall_clock64 ticks (100 MHz)
@@ -176,6 +179,7 @@ struct Ctx {
   LDS char* smem;            // KVM_LDS_BYTES of LDS
   KvmCounters* cnt;
   int slot;
+  int pre = 0;               // the task's first input-independent loads were issued before its dependency wait
   __device__ View buf(int k) const {
     if (a[k] < 0) return View{nullptr, 0, 0, 0};
     return View{views[k].p, views[k].rows, views[k].cols, views[k].dtype};

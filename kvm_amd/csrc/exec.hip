@@ -415,6 +415,46 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
   if (i < S.nq * S.nb) { KvmQueue z = {}; S.queues[i] = z; }
   if (i == 0) { KvmCounters z = {}; *S.cnt = z; }
 }
+// Static-path wait on `cnt` (worker, need) pairs at ent, by the 64 lanes of one wave: each lane takes up to four
+// entries per round of 256 and polls them together (their loads in flight at once), entries of the worker itself
+// (program order) and set references (worker < 0) skipped. Gives up on an error anywhere or after timeout_ticks
+// (TIMEOUT, first error wins). Returns true when it gave up (uniform across the wave).
+__device__ bool static_wait(const KvmDevState& S, const int* ent, int cnt, int self, int slot) {
+  const int l = lane();
+  bool bad = false;
+  for (int j0 = 0; j0 < cnt && !bad; j0 += 256) {
+    int ww[4], need[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = j0 + l + 64 * u;
+      ww[u] = j < cnt ? ent[2 * j] : -1;
+      need[u] = j < cnt ? ent[2 * j + 1] : 0;
+      if (ww[u] == self) ww[u] = -1;
+    }
+    const unsigned long long since = wall_clock64();
+    for (unsigned polls = 0;; ++polls) {
+      int have[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) have[u] = ww[u] >= 0 ? ld_relaxed(&S.sprogress[ww[u]]) : 0x7fffffff;
+      bool mine = true;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) mine = mine && have[u] >= need[u];
+      if (__ballot(!mine) == 0ull) break;
+      if (ld_relaxed(&S.cnt->err_code) != 0) { bad = true; break; }
+      __builtin_amdgcn_s_sleep(1);
+      if ((polls & 1023) == 1023 && wall_clock64() - since > S.timeout_ticks) {
+        int z = 0;
+        if (l == 0 && __hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_TIMEOUT, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+          S.cnt->err_slot = slot; S.cnt->err_a = ww[0]; S.cnt->err_b = need[0];
+        }
+        bad = true;
+        break;
+      }
+    }
+  }
+  return bad;
+}
+
 // The static path: worker w runs its program (the host plan) in order. Before a task, wave 0 waits for its cross-worker
 // dependencies (lane k polls wait k: progress[worker] >= need) and acquires; after it, every wave waits for its own
 // write-through stores and the barrier orders them before thread 0 publishes the program position, when another
@@ -424,34 +464,40 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
 __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState S) {
   __shared__ __attribute__((aligned(16))) char smem[KVM_LDS_BYTES];
   __shared__ int s_go;
-  __shared__ __attribute__((aligned(16))) KvmRec s_rec;
+  __shared__ __attribute__((aligned(16))) KvmRec s_recs[2];
   const int t = threadIdx.x, w = blockIdx.x;
   const int p0 = S.sprog_off[w], p1 = S.sprog_off[w + 1];
+  if (p0 < p1 && t < KVM_REC_VEC) ((LDS u32x4_t*)&s_recs[0])[t] = ((const u32x4_t*)(S.recs + S.sprog[p0]))[t];
+  int next = p0 < p1 ? S.sprog[p0] : -1;
+  __syncthreads();
   for (int i = p0; i < p1; ++i) {
-    const int slot = S.sprog[i];
-    // The record depends on nothing: wave 1 loads it while wave 0 waits for the task's dependencies.
-    if (t >= 64 && t < 64 + KVM_REC_VEC) ((LDS u32x4_t*)&s_rec)[t - 64] = ((const u32x4_t*)(S.recs + slot))[t - 64];
+    const int slot = next;
+    KvmRec& s_rec = s_recs[(i - p0) & 1];
+    // Records depend on nothing: wave 1 requests the next task's into the other buffer (direct to LDS) now; its
+    // end-of-task store wait covers that load too.
+    next = i + 1 < p1 ? S.sprog[i + 1] : -1;
+    if (wave() == 1 && next >= 0 && lane() < KVM_REC_VEC)
+      dma16(dma_rsrc(S.recs + next, sizeof(KvmRec)), 16 * lane(), 0, (const LDS void*)&s_recs[(i + 1 - p0) & 1]);
+    const int sf = S.sflag[slot];
+    // A decode GEMV whose weights no task writes requests its first weight steps before waiting (wave 0's share
+    // lands before its first poll returns).
+    Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
+    if (sf & KVM_SF_PRE) { gemv_prefetch(c, s_rec.desc.op_id); c.pre = 1; }
     if (t < 64) {
       const int k0 = S.swait_off[slot], k1 = S.swait_off[slot + 1];
       const int err0 = ld_relaxed(&S.cnt->err_code);
-      int bad = 0;
-      for (int k = k0 + t; k < k1 && !bad; k += 64) {
-        const int ww = S.sw[2 * k], need = S.sw[2 * k + 1];
-        const unsigned long long since = wall_clock64();
-        for (unsigned polls = 0; ld_relaxed(&S.sprogress[ww]) < need; ++polls) {
-          if (ld_relaxed(&S.cnt->err_code) != 0) { bad = 1; break; }
-          __builtin_amdgcn_s_sleep(1);
-          if ((polls & 1023) == 1023 && wall_clock64() - since > S.timeout_ticks) {
-            int z = 0;
-            if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_TIMEOUT, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-              S.cnt->err_slot = slot; S.cnt->err_a = ww; S.cnt->err_b = need;
-            }
-            bad = 1;
-            break;
-          }
+      // the task's own list (set references skipped), then each referenced wait set (lanes of the reference
+      // broadcast it in turn)
+      bool bad = static_wait(S, S.sw + 2 * k0, k1 - k0, w, slot);
+      for (int kb = k0; kb < k1 && !bad; kb += 64) {
+        const int k = kb + t;
+        unsigned long long refs = __ballot(k < k1 && S.sw[2 * k] < 0);
+        while (refs && !bad) {
+          const int kk = kb + __ffsll((long long)refs) - 1;
+          refs &= refs - 1;
+          bad = static_wait(S, S.sw + 2 * S.sw[2 * kk + 1], -1 - S.sw[2 * kk], w, slot);
         }
       }
-      bad = __ballot(bad) != 0ull;
       fence_acquire();                       // the publishers' stores are visible from here on
       if (t == 0) s_go = !bad && err0 == 0;
     }
@@ -471,9 +517,8 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
           S.cnt->err_slot = slot;
       }
     }
-    Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
     dispatch(d.op_id, c);
-    const bool pub_pos = t == 0 && S.spub[slot];
+    const bool pub_pos = (sf & KVM_SF_PUB) != 0;
     wait_stores();
     __syncthreads();
     if (t == 0) {
@@ -487,6 +532,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
       st_relaxed(&S.done_blk[w], i - p0 + 1);
     }
   }
+  wait_stores();   // after an early exit: no direct-to-LDS load of a prefetch is still in flight when the workgroup ends
 }
 
 // Roots (tasks with no predecessors). Roots without a version wait go to fixed cells computed on the host (queue
@@ -568,7 +614,12 @@ struct KvmExec {
   // device memory of the placed graph (one hipMalloc each, freed by kvm_destroy)
   std::vector<void*> allocs;
   int path = -1;                           // the path launches use: KVM_PATH_DYNAMIC or KVM_PATH_STATIC (set at upload)
-  kvms::Plan splan;
+  // Static plans: splan keeps every task (traced launches: the trace is indexed by task); splan_d dissolves the
+  // ordering no-ops (untraced launches). Their device arrays: sfull, sdis (the same arrays when nothing dissolves).
+  kvms::Plan splan, splan_d;
+  struct StaticDev { const int *prog_off = nullptr, *prog = nullptr, *wait_off = nullptr, *sw = nullptr, *flag = nullptr; int dissolved = 0; };
+  StaticDev sfull, sdis;
+  int last_dissolved = 0;                  // no-ops the last launch dissolved (counted as done)
   struct LaunchArgs L{};
   KvmDevState S{};
 };
@@ -870,6 +921,34 @@ static double task_cost_us(const MvmTaskDesc& d, const int32_t* a) {
   return 3.0;
 }
 
+// Static-path flags per task: KVM_SF_PUB, another worker waits for the task; KVM_SF_PRE, a decode GEMV (op 134 / 301)
+// whose weight buffer no task of the graph writes (it appears in no argument slot other than the weights of such
+// GEMVs), so its first weight loads may be issued before its dependencies are met.
+static std::vector<int> static_flags(const KvmExec* ex, const kvms::Plan& P) {
+  const int n = (int)ex->tasks.size(), nb = (int)ex->bufs.size();
+  std::vector<char> other_use(nb, 0);
+  std::vector<std::vector<kvmv::ArgInfo>> sigs(1024);
+  for (int i = 0; i < n; ++i) {
+    const MvmTaskDesc& d = ex->tasks[i];
+    const int op = d.op_id;
+    if (op < 0 || op >= 1024) continue;
+    if (sigs[op].empty()) if (const kvmv::OpSig* o = kvmv::find_op(op)) sigs[op] = kvmv::parse_sig(o->sig);
+    const int32_t* a = ex->args.data() + d.args_off;
+    for (size_t k = 0; k < sigs[op].size() && (int)k < d.args_words; ++k)
+      if (sigs[op][k].type == 0 && a[k] >= 0 && a[k] < nb && !((op == 134 || op == 301) && k == 3)) other_use[a[k]] = 1;
+  }
+  std::vector<int> f(n, 0);
+  for (int i = 0; i < n; ++i) {
+    const MvmTaskDesc& d = ex->tasks[i];
+    if (P.publishes[i]) f[i] |= KVM_SF_PUB;
+    if ((d.op_id == 134 || d.op_id == 301) && d.args_words > 3) {
+      const int wb = ex->args[d.args_off + 3];
+      if (wb >= 0 && wb < nb && !other_use[wb] && !getenv("KVM_NO_PREFETCH")) f[i] |= KVM_SF_PRE;
+    }
+  }
+  return f;
+}
+
 static int plan_static(KvmExec* ex, bool forced) {
   std::string why;
   if (!kvms::feasible(ex->tasks.data(), (int)ex->tasks.size(), ex->base_versions.data(), (int)ex->base_versions.size(), &why)) {
@@ -881,7 +960,11 @@ static int plan_static(KvmExec* ex, bool forced) {
   for (size_t i = 0; i < ex->tasks.size(); ++i) { cost[i] = task_cost_us(ex->tasks[i], ex->args.data() + ex->tasks[i].args_off); total += cost[i]; }
   if (!forced && total / (double)cost.size() > KVM_STATIC_MAX_MEAN_US) return 0;
   try {
-    ex->splan = kvms::plan(ex->tasks.data(), (int)ex->tasks.size(), ex->succ.data(), cost, ex->grid);
+    ex->splan_d = kvms::plan(ex->tasks.data(), (int)ex->tasks.size(), ex->succ.data(), cost, ex->grid, 1.5, true);
+    if (ex->cfg.trace_on) {
+      if (ex->splan_d.dissolved) ex->splan = kvms::plan(ex->tasks.data(), (int)ex->tasks.size(), ex->succ.data(), cost, ex->grid, 1.5, false);
+      else ex->splan = ex->splan_d;
+    }
   } catch (const std::exception& e) {
     ex->err = std::string("static path: ") + e.what();
     return KVM_STATUS_INVALID;
@@ -909,19 +992,23 @@ static int do_upload(KvmExec* ex) {
   ex->path = KVM_PATH_DYNAMIC;
   if (ex->cfg.path != KVM_PATH_DYNAMIC) {
     if (int r = plan_static(ex, ex->cfg.path == KVM_PATH_STATIC)) return r;
-    if (ex->path == KVM_PATH_STATIC) {   // the plan's arrays next to the dynamic state (a later relaunch may use either)
-      const kvms::Plan& P = ex->splan;
-      std::vector<int> sw(2 * P.waits.size()), spub(P.publishes.begin(), P.publishes.end());
-      for (size_t k = 0; k < P.waits.size(); ++k) { sw[2 * k] = P.waits[k].worker; sw[2 * k + 1] = P.waits[k].need; }
+    if (ex->path == KVM_PATH_STATIC) {   // the plans' arrays next to the dynamic state (a later relaunch may use either)
       auto put = [&](const std::vector<int>& v) -> int* {
         void* d = alloc(std::max<size_t>(v.size(), 1) * sizeof(int));
         if (d && !v.empty() && hipMemcpy(d, v.data(), v.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
         return (int*)d;
       };
-      KvmDevState& S = ex->S;
-      S.sprog_off = put(P.prog_off); S.sprog = put(P.prog); S.swait_off = put(P.wait_off); S.sw = put(sw); S.spub = put(spub);
-      S.sprogress = (int*)alloc(ex->grid * sizeof(int));
-      if (!S.sprog_off || !S.sprog || !S.swait_off || !S.sw || !S.spub || !S.sprogress) { ex->err = "static path: device memory"; return KVM_STATUS_HIP_ERROR; }
+      auto upload_plan = [&](const kvms::Plan& P, KvmExec::StaticDev& D) {
+        std::vector<int> sw(2 * P.waits.size()), sflag = static_flags(ex, P);
+        for (size_t k = 0; k < P.waits.size(); ++k) { sw[2 * k] = P.waits[k].worker; sw[2 * k + 1] = P.waits[k].need; }
+        D.prog_off = put(P.prog_off); D.prog = put(P.prog); D.wait_off = put(P.wait_off); D.sw = put(sw); D.flag = put(sflag);
+        D.dissolved = P.dissolved;
+        return D.prog_off && D.prog && D.wait_off && D.sw && D.flag;
+      };
+      bool ok = upload_plan(ex->splan_d, ex->sdis);
+      if (ex->cfg.trace_on) ok = ok && (ex->splan_d.dissolved ? upload_plan(ex->splan, ex->sfull) : (ex->sfull = ex->sdis, true));
+      ex->S.sprogress = (int*)alloc(ex->grid * sizeof(int));
+      if (!ok || !ex->S.sprogress) { ex->err = "static path: device memory"; return KVM_STATUS_HIP_ERROR; }
     }
   }
   ex->uploaded = true;
@@ -941,6 +1028,12 @@ static void launch_graph(const KvmDevState& S, const LaunchArgs& L, int grid, hi
 
 static int launch_once(KvmExec* ex, hipEvent_t before_exec = nullptr, hipEvent_t after_exec = nullptr) {
   HIPCK(hipMemcpyAsync(ex->L.base, ex->base_versions.data(), ex->base_versions.size() * sizeof(int), hipMemcpyHostToDevice, ex->stream));
+  ex->last_dissolved = 0;
+  if (ex->path == KVM_PATH_STATIC) {   // traced launches run every task; untraced ones the plan with the no-ops dissolved
+    const KvmExec::StaticDev& D = ex->S.trace_on ? ex->sfull : ex->sdis;
+    ex->S.sprog_off = D.prog_off; ex->S.sprog = D.prog; ex->S.swait_off = D.wait_off; ex->S.sw = D.sw; ex->S.sflag = D.flag;
+    ex->last_dissolved = D.dissolved;
+  }
   launch_graph(ex->S, ex->L, ex->grid, ex->stream, before_exec, after_exec, ex->path == KVM_PATH_STATIC);
   HIPCK(hipGetLastError());
   return 0;
@@ -1016,6 +1109,7 @@ int kvm_finish(KvmExec* ex, KvmResult* res) {
     std::vector<int> per(ex->grid);
     HIPCK(hipMemcpy(per.data(), ex->S.done_blk, ex->grid * sizeof(int), hipMemcpyDeviceToHost));
     for (int d : per) done += d;
+    if (!c.err_code) done += ex->last_dissolved;   // dissolved no-ops have no work: done once the run completes
   }
   float ms = 0.f;
   if (ex->launched) hipEventElapsedTime(&ms, ex->ev0, ex->ev1);
@@ -1055,7 +1149,7 @@ int kvm_ntasks(const KvmExec* ex) { return (int)ex->tasks.size(); }
 int kvm_path(const KvmExec* ex) { return ex ? ex->path : KVM_STATUS_INVALID; }
 
 int kvm_static_plan(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs,
-                    int workers, int* worker_of, int* pos_of, int* nwaits, int* publishes, int* waits, int wait_cap,
+                    int workers, int flags, int* worker_of, int* pos_of, int* nwaits, int* publishes, int* waits, int wait_cap,
                     double* stats, char* err, int errlen) {
   try {
     if (ntasks < 1 || workers < 1 || nedges < 0 || nargs < 0) throw std::invalid_argument("empty graph or no workers");
@@ -1069,13 +1163,13 @@ int kvm_static_plan(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, i
       }
       cost[i] = task_cost_us(tasks[i], args + tasks[i].args_off);
     }
-    const kvms::Plan P = kvms::plan(tasks, ntasks, succ, cost, workers);
+    const kvms::Plan P = kvms::plan(tasks, ntasks, succ, cost, workers, 1.5, (flags & KVM_PLAN_DISSOLVE) != 0);
     for (int i = 0; i < ntasks; ++i) {
       worker_of[i] = P.worker_of[i]; pos_of[i] = P.pos_of[i]; nwaits[i] = P.wait_off[i + 1] - P.wait_off[i]; publishes[i] = P.publishes[i];
     }
     if ((long long)P.waits.size() > wait_cap) throw std::invalid_argument("more waits than wait_cap");
     for (size_t k = 0; k < P.waits.size(); ++k) { waits[2 * k] = P.waits[k].worker; waits[2 * k + 1] = P.waits[k].need; }
-    stats[0] = P.makespan_us; stats[1] = P.work_us; stats[2] = P.cross_edges; stats[3] = P.edges;
+    stats[0] = P.makespan_us; stats[1] = P.work_us; stats[2] = P.cross_edges; stats[3] = P.edges; stats[4] = P.dissolved;
     return 0;
   } catch (const std::exception& e) {
     if (err && errlen > 0) snprintf(err, errlen, "%s", e.what());

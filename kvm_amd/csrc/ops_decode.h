@@ -196,26 +196,24 @@ __device__ __noinline__ void op_gemv_bf16_rows_simt(const Ctx& c) {
 // ---------------------------------------------------------------------------------------------- streaming GEMV
 // out[m, n] = sum_k v[m, k] * w[n, k] (+ res[m, n]) for M <= 16 rows of activations (op 134 with M = 1, and op 301),
 // v = bf16(prologue(x)). The weight stream is the whole cost, so it is shaped for HBM:
-//   * each wave streams one quarter of K. A 64-k step covers 16 weight rows: lane l loads 32 contiguous bytes of row
-//     l % 16 (16 lanes cover 16 rows, the 4 lane groups cover the 64 k, so every 128-byte line is read whole) straight
-//     into the registers that two v_mfma_f32_16x16x32_bf16 take as their B operand; the activation rows are the A
-//     operand (rows >= M read as zero). Both operands take k in the same lane-group order, so the dot products are
-//     unchanged;
-//   * the weight loads are issued from inline assembly into a ring of GV_RING register pairs, GV_RING steps ahead,
-//     and each step waits with an explicit vmcnt tied to the registers it consumes: the compiler's own wait placement
-//     (which drains all loads at any branch) never sees them. Every step issues exactly two loads (past the end a
-//     re-read of a line just streamed), so the wait count is a constant, and the ring is drained before it goes out of
-//     scope;
-//   * the first steps' loads are requested before v is staged, which does not depend on the weights;
+//   * each wave streams one quarter of K. A 64-k step covers 16 weight rows: two direct HBM -> LDS loads per wave
+//     (buffer_load_dwordx4 ... lds), the first bringing bytes 0-63 of each row's 128-byte step segment, the second
+//     bytes 64-127 (lane l: row l % 16, 16 bytes at 16 (l / 16) of its half), so each load reads 16 whole 64-byte
+//     runs. Lane l then reads its own two 16-byte pieces back as the B operands of two v_mfma_f32_16x16x32_bf16; the
+//     activation rows are the A operand in the same k order (rows >= M read as zero), so the dot products are unchanged;
+//   * the loads land in a ring of R step slots per wave in LDS (R up to 12: 24 KiB in flight per wave, 96 KiB per CU,
+//     where registers held 8 KiB per wave), issued R steps ahead across row blocks, K chunks and row groups. Each step
+//     waits with an explicit vmcnt for its own two loads (every step issues exactly two, past the end two loads
+//     outside the descriptor's range, which touch no memory), and the compiler never sees the ring;
+//   * the first R steps do not depend on the task's inputs: they are requested before v is staged, and on the static
+//     path before the task even waits for its predecessors (gemv_prefetch, when the host found the weight buffer
+//     read-only in the graph);
 //   * v is staged as bf16 [M][KC + 8] in LDS once per K chunk, with the activation loads batched; each wave adds its
-//     partial 16x16 tiles into its own LDS region, and the four regions are summed in wave order at the end (fixed
+//     partial 16 x M tiles into its own LDS region, and the four regions are summed in wave order at the end (fixed
 //     order).
 constexpr int GV_SB = 8;           // activation vectors per thread per staging batch (all in flight)
 constexpr int GV_GRP = 8;          // 16-row blocks whose partial tiles are kept in LDS at once (a group re-stages v)
-#ifndef KVM_GV_RING
-#define KVM_GV_RING 4
-#endif
-constexpr int GV_RING = KVM_GV_RING;   // 64-k steps in flight per wave (2 KiB each): deeper rings measured slower
+constexpr int GV_STEP = 2048;      // one wave's 64-k step of 16 rows: 64 lanes x 32 bytes
 
 __device__ __forceinline__ float gv_pro(int pro, float xv, float x2v, float gv, float rs) {
   return pro == 1 ? xv * rs * gv : pro == 2 ? silu_f(xv) * x2v : xv;
@@ -280,109 +278,163 @@ __device__ __forceinline__ void gv_stage(const Ld4& lx, const Ld4& la, int xc, i
   }
 }
 
-// K chunk staged in LDS at once: all of K when M rows of it fit in GV_VS_MAX (then one chunk, one continuous weight
-// stream), else the largest of 4096 / 2048 / 1024 that divides K.
-// LDS left for the staged activations [M][KC + 8] next to the row statistics and the partial tiles.
-constexpr long long GV_VS_MAX = KVM_LDS_BYTES - 4ll * GV_GRP * 256 * 4 - 128;
-__device__ __forceinline__ int gv_kc(int K, int M) {
-  if ((long long)M * (K + 8) * 2 <= GV_VS_MAX) return K;
-  for (int kc = 4096; kc >= 256; kc >>= 1)
-    if (K % kc == 0 && (long long)M * (kc + 8) * 2 <= GV_VS_MAX) return kc;
-  return 256;
+// LDS geometry of one call with a ring of R steps per wave: [ring: 4 waves x R steps][v: M x (KC + 8) bf16]
+// [rstd: 16 f32][partials: 4 x GV_GRP x M x 16 f32]. KC is all of K when it fits, else the largest of 4096 .. 256
+// dividing K that does.
+struct GvGeo { int KC, VS, vs_off, rstd_off, part_off; };
+__device__ __forceinline__ GvGeo gv_geo(int K, int M, int R) {
+  auto fits = [&](int kc) {
+    return R * KVM_WAVES * GV_STEP + ((M * (kc + 8) * 2 + 15) & ~15) + 64 + KVM_WAVES * GV_GRP * M * 16 * 4 <= KVM_LDS_BYTES;
+  };
+  int KC = 256;
+  if (fits(K)) KC = K;
+  else
+    for (int kc = 4096; kc >= 512; kc >>= 1)
+      if (K % kc == 0 && fits(kc)) { KC = kc; break; }
+  GvGeo g;
+  g.KC = KC; g.VS = KC + 8;
+  g.vs_off = R * KVM_WAVES * GV_STEP;
+  g.rstd_off = g.vs_off + ((M * g.VS * 2 + 15) & ~15);
+  g.part_off = g.rstd_off + 64;
+  return g;
 }
+// Ring depth: GV_R steps per wave (8 KiB per wave: in the steady state the stream is not latency bound with more);
+// a ring filled before the dependency wait is deeper, so that more of the task's weights arrive during the wait.
+constexpr int GV_R = 4;
+#ifndef KVM_GV_PRE
+#define KVM_GV_PRE 4
+#endif
+__device__ __forceinline__ int gv_pre_ring(int M) { return KVM_GV_PRE; }
 
-// Shapes the stream form takes: K a multiple of 256 (each wave a whole number of 64-k steps) made of equal chunks,
-// 16-byte aligned rows.
+// Shapes the stream form takes: K a multiple of 256 (each wave a whole number of 64-k steps), M <= 16, 16-byte
+// aligned rows, byte offsets inside 31 bits.
 __device__ __forceinline__ bool gemv_stream_ok(const View& x, const View& x2, const View& w, const View& out, int K, int M, int pro) {
-  const int KC = gv_kc(K, M);
-  return M >= 1 && M <= 16 && K % 256 == 0 && K % KC == 0 && w.dtype == 2 && (w.cols % 8) == 0 && x.dtype != 1 &&
+  return M >= 1 && M <= 16 && K % 256 == 0 && w.dtype == 2 && (w.cols % 8) == 0 && x.dtype != 1 &&
          (x.cols % 4) == 0 && (pro != 2 || (x2.ok() && x2.dtype != 1 && (x2.cols % 4) == 0)) && out.dtype != 1 &&
-         (long long)w.rows * w.cols * 2 < 0x7fffffffll && (long long)x.rows * x.cols * 4 < 0x7fffffffll &&
+         (long long)w.rows * w.cols * 2 < 0x7fff0000ll && (long long)x.rows * x.cols * 4 < 0x7fffffffll &&
          (!x2.ok() || (long long)x2.rows * x2.cols * 4 < 0x7fffffffll);
 }
 
-// 32 bytes of weights into registers, invisible to the compiler's wait tracking.
-__device__ __forceinline__ void gv_load(u16x8_t& a, u16x8_t& b, i32x4_t rs, int off) {
-  asm volatile("buffer_load_dwordx4 %0, %2, %3, 0 offen\n\tbuffer_load_dwordx4 %1, %2, %3, 0 offen offset:16"
-               : "=v"(a), "=v"(b) : "v"(off), "s"(rs));
+// One wave's weight stream: a wave-uniform issue cursor over (row group, K chunk, row block, step) and the ring slot
+// it fills next.
+struct GvStream {
+  i32x4_t rw;
+  int nrows, nrb, rowb, K, KC, ns, koff;
+  int g0, kc, rb, st, islot;
+  __device__ __forceinline__ void init(const View& w, int n0, int n1, int K_, int KC_) {
+    nrows = rfl(n1 - n0); nrb = rfl((nrows + 15) / 16); rowb = rfl(w.cols * 2); K = rfl(K_); KC = rfl(KC_); ns = KC / 256;
+    koff = rfl(wave() * (KC / 4) * 2);
+    rw = dma_rsrc((const void*)(w.h() + (long long)n0 * w.cols), ((long long)w.rows - n0) * w.cols * 2);
+    g0 = kc = rb = st = islot = 0;
+  }
+  __device__ __forceinline__ void advance() {
+    if (g0 >= nrb) return;
+    if (++st == ns) {
+      st = 0;
+      if (++rb == min(GV_GRP, nrb - g0)) { rb = 0; kc += KC; if (kc == K) { kc = 0; g0 += GV_GRP; } }
+    }
+    g0 = rfl(g0); kc = rfl(kc); rb = rfl(rb); st = rfl(st);
+  }
+  // Requests the next step into its ring slot (past the end: two loads beyond the descriptor's range).
+  template <int R> __device__ __forceinline__ void issue(LDS char* ring) {
+    LDS char* dst = ring + islot * GV_STEP;
+    const int row = min((g0 + rb) * 16 + (lane() & 15), nrows - 1);
+    const int off = g0 < nrb ? row * rowb + kc * 2 + koff + st * 128 + 16 * (lane() >> 4) : 0x7fff0000;
+    dma16(rw, off, 0, dst);
+    dma16(rw, off + 64, 0, dst + 1024);
+    islot = islot + 1 == R ? 0 : islot + 1;
+    advance();
+  }
+  template <int R> __device__ __forceinline__ void skip() { islot = islot + 1 == R ? 0 : islot + 1; advance(); }
+};
+
+// The first steps of every wave's stream, into the ring of a task that will run with c.pre set. Called by all four
+// waves with the task's record in c (op 134 or 301) before its dependencies are met; it reads only the weights and
+// writes only the ring.
+template <int R> __device__ __forceinline__ void gemv_prefetch_r(const View& w, int n0, int n1, int K, int M, LDS char* smem) {
+  GvStream ws;
+  ws.init(w, n0, n1, K, gv_geo(K, M, R).KC);
+  LDS char* ring = smem + wave() * R * GV_STEP;
+#pragma unroll
+  for (int j = 0; j < R; ++j) ws.issue<R>(ring);
 }
-// vmcnt(N), tied to the registers about to be read so that their uses stay after it.
-template <int N> __device__ __forceinline__ void gv_wait(u16x8_t& a, u16x8_t& b) {
-  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N));
+__device__ __noinline__ void gemv_prefetch(const Ctx& c, int op) {
+  const View x = c.buf(0), x2 = c.buf(1), w = uniform_view(c.buf(3)), out = c.buf(4);
+  const bool rows = op == 301;
+  const int M = rfl(rows ? c.i(9) : 1), pro = rows ? c.i(10) : c.i(9), K = rfl(c.i(8)), n0 = rfl(c.i(6)), n1 = rfl(c.i(7));
+  if (!gemv_stream_ok(x, x2, w, out, K, M, pro)) return;
+  const int R = gv_pre_ring(M);
+  if (R == 12) gemv_prefetch_r<12>(w, n0, n1, K, M, c.smem);
+  else if (R == 8) gemv_prefetch_r<8>(w, n0, n1, K, M, c.smem);
+  else gemv_prefetch_r<4>(w, n0, n1, K, M, c.smem);
 }
 
-__device__ __noinline__ void gemv_stream(const Ctx& c, int M, int pro, float eps) {
+template <int R> __device__ void gemv_stream_r(const Ctx& c, int M_, int pro_, float eps) {
+  const int M = rfl(M_), pro = rfl(pro_);                                       // function arguments arrive in VGPRs
   const View x = uniform_view(c.buf(0)), x2 = uniform_view(c.buf(1)), g = uniform_view(c.buf(2)), w = uniform_view(c.buf(3));
   const View out = uniform_view(c.buf(4)), res = uniform_view(c.buf(5));
   const int n0 = rfl(c.i(6)), n1 = rfl(c.i(7)), K = rfl(c.i(8));
-  const int KC = gv_kc(K, M), VS = KC + 8;
-  LDS uint16_t* vs = (LDS uint16_t*)c.smem;                                    // [M][VS]
-  LDS float* rstd = (LDS float*)(c.smem + ((M * VS * 2 + 15) & ~15));          // [16]
-  LDS float* part = rstd + 16;                                                  // [4][GV_GRP][256]
-  const int l = lane(), wv = wave(), nrows = n1 - n0, nrb = (nrows + 15) / 16, rowb = w.cols * 2;
+  const GvGeo geo = gv_geo(K, M, R);
+  const int KC = geo.KC, VS = geo.VS, PM = 16 * M;
+  LDS uint16_t* vs = (LDS uint16_t*)(c.smem + geo.vs_off);                     // [M][VS]
+  LDS float* rstd = (LDS float*)(c.smem + geo.rstd_off);                       // [16]
+  LDS float* part = (LDS float*)(c.smem + geo.part_off);                       // [4][GV_GRP][M][16]
+  const int l = lane(), wv = wave(), nrows = n1 - n0, nrb = (nrows + 15) / 16;
 #ifdef KVM_GEMM_PROF
   unsigned long long pt[8] = {(unsigned long long)wall_clock64(), 0, 0, 0, 0, 0, 0, 0};
 #endif
-  const i32x4_t rw = dma_rsrc((const void*)(w.h() + (long long)n0 * w.cols), ((long long)w.rows - n0) * w.cols * 2);
+  LDS char* ring = c.smem + wv * R * GV_STEP;
+  GvStream ws;
+  ws.init(w, n0, n1, K, KC);
+  if (rfl(c.pre)) {
+#pragma unroll
+    for (int j = 0; j < R; ++j) ws.skip<R>();                                    // issued before the dependency wait
+  } else {
+#pragma unroll
+    for (int j = 0; j < R; ++j) ws.issue<R>(ring);                              // weights first: they do not wait for x
+  }
   Ld4 lx, lx2, lg;
   lx.init(x); lx2.init(x2); lg.init(g);
   const bool arow = (l & 15) < M;
-  const LDS uint16_t* va = vs + (arow ? (l & 15) : 0) * VS + 16 * (l >> 4);   // rows >= M read row 0 and are zeroed
-  bool rstd_done = pro != 1;
-  u16x8_t wb[GV_RING][2];
+  const LDS uint16_t* va = vs + (arow ? (l & 15) : 0) * VS + 8 * (l >> 4);     // rows >= M read row 0 and are zeroed
+  const LDS char* rl = ring + 16 * l;
+  if (pro == 1) gv_rstd<8>(lx, x.cols, M, K, eps, rstd);                        // rstd of each row over all of K
+  int cslot = 0;                                                                // ring slot of the next step consumed
   for (int g0 = 0; g0 < nrb; g0 += GV_GRP) {
     const int ng = min(GV_GRP, nrb - g0);
+    for (int e = l; e < ng * PM; e += 64) part[(wv * GV_GRP) * PM + e] = 0.f;
     for (int kc = 0; kc < K; kc += KC) {
-      const int kn = min(KC, K - kc), kq = kn / 4, ns = kq / 64, T = ng * ns;
-      // byte offset of this lane's 32 bytes in step 0 of row block rb (rows past n1 repeat the last; dropped below)
-      auto row_base = [&](int rb) { return min((g0 + rb) * 16 + (l & 15), nrows - 1) * rowb + (kc + wv * kq) * 2 + 32 * (l >> 4); };
-      // issue cursor: step it = (irb, ist)
-      int irb = 0, ist = 0, ibase = row_base(0);
-      const int dummy = ibase;
-      auto issue_next = [&](u16x8_t& a, u16x8_t& b) {
-        const bool live = irb < ng;
-        gv_load(a, b, rw, live ? ibase + ist * 128 : dummy);
-        if (live && ++ist == ns) { ist = 0; ++irb; if (irb < ng) ibase = row_base(irb); }
-      };
-#pragma unroll
-      for (int j = 0; j < GV_RING; ++j) issue_next(wb[j][0], wb[j][1]);     // weights first: they do not wait for x
-      if (!rstd_done) {                                                          // rstd of each row over all of K
-        gv_rstd<8>(lx, x.cols, M, K, eps, rstd);
-        rstd_done = true;
-      }
-      if (kc == 0) for (int e = l; e < ng * 256; e += 64) part[(wv * GV_GRP) * 256 + e] = 0.f;
+      const int kq = KC / 4, ns = kq / 64;
       __syncthreads();                                                          // rstd ready; the previous chunk's readers are done
-      if (pro == 1) gv_stage<1, 8>(lx, lg, x.cols, 0, M, kc, kn, VS, vs, rstd);          // v = bf16(prologue(x)), this chunk
-      else if (pro == 2) gv_stage<2, 8>(lx, lx2, x.cols, x2.cols, M, kc, kn, VS, vs, rstd);
-      else gv_stage<0, 16>(lx, lx, x.cols, 0, M, kc, kn, VS, vs, rstd);
+      if (pro == 1) gv_stage<1, GV_SB>(lx, lg, x.cols, 0, M, kc, KC, VS, vs, rstd);      // v = bf16(prologue(x)), this chunk
+      else if (pro == 2) gv_stage<2, GV_SB>(lx, lx2, x.cols, x2.cols, M, kc, KC, VS, vs, rstd);
+      else gv_stage<0, 2 * GV_SB>(lx, lx, x.cols, 0, M, kc, KC, VS, vs, rstd);
       __syncthreads();
 #ifdef KVM_GEMM_PROF
       if (g0 == 0) pt[1] = wall_clock64();
 #endif
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-      int crb = 0, cst = 0;
       const LDS uint16_t* vk = va + wv * kq;
-      for (int t0 = 0; t0 < T; t0 += GV_RING) {
+      for (int rb = 0; rb < ng; ++rb) {
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        for (int st = 0; st < ns; ++st) {
+          wait_vm_c<2 * (R - 1)>();                                             // this step's two loads have landed
+          const LDS char* slot = rl + cslot * GV_STEP;
+          const u16x8_t w0 = *(const LDS u16x8_t*)slot, w1 = *(const LDS u16x8_t*)(slot + 1024);
+          const u16x8_t a0 = *(const LDS u16x8_t*)(vk + st * 64), a1 = *(const LDS u16x8_t*)(vk + st * 64 + 32);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8_t)(arow ? a0 : u16x8_t{}), (bf16x8_t)w0, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8_t)(arow ? a1 : u16x8_t{}), (bf16x8_t)w1, acc, 0, 0, 0);
+          wait_lds();                                                           // the slot's reads are done before it is refilled
+          ws.issue<R>(ring);
+          cslot = cslot + 1 == R ? 0 : cslot + 1;
+        }
+        // D[m][n]: lane holds m = 4 (l / 16) + i, n = l % 16; rows m >= M are padding
+        LDS float* pp = part + (wv * GV_GRP + rb) * PM + (l & 15);
 #pragma unroll
-        for (int j = 0; j < GV_RING; ++j) {
-          if (t0 + j < T) {
-            gv_wait<2 * (GV_RING - 1)>(wb[j][0], wb[j][1]);                  // this step's two loads have landed
-            const u16x8_t a0 = *(const LDS u16x8_t*)(vk + cst * 64), a1 = *(const LDS u16x8_t*)(vk + cst * 64 + 8);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8_t)(arow ? a0 : u16x8_t{}), (bf16x8_t)wb[j][0], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8_t)(arow ? a1 : u16x8_t{}), (bf16x8_t)wb[j][1], acc, 0, 0, 0);
-            issue_next(wb[j][0], wb[j][1]);
-            if (++cst == ns) {        // row block finished for this chunk: D[m][n], lane holds m = 4*(l/16) + i, n = l % 16
-              LDS float* pp = part + (wv * GV_GRP + crb) * 256 + 4 * (l >> 4) * 16 + (l & 15);
-#pragma unroll
-              for (int i = 0; i < 4; ++i) pp[i * 16] += acc[i];
-              acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-              cst = 0; ++crb;
-            }
-          }
+        for (int i = 0; i < 4; ++i) {
+          const int m = 4 * (l >> 4) + i;
+          if (m < M) pp[m * 16] += acc[i];
         }
       }
-#pragma unroll
-      for (int j = 0; j < GV_RING; ++j) gv_wait<0>(wb[j][0], wb[j][1]);      // the ring's trailing re-reads have landed
     }
 #ifdef KVM_GEMM_PROF
     if (g0 == 0) pt[2] = wall_clock64();
@@ -391,20 +443,29 @@ __device__ __noinline__ void gemv_stream(const Ctx& c, int M, int pro, float eps
 #ifdef KVM_GEMM_PROF
     if (g0 == 0) pt[3] = wall_clock64();
 #endif
-    for (int e = tid(); e < ng * 16 * M; e += KVM_THREADS) {                   // sum the four waves' tiles, in wave order
-      const int rb = e / (16 * M), m = (e / 16) % M, nn = e % 16, n = n0 + (g0 + rb) * 16 + nn;
+    for (int e = tid(); e < ng * PM; e += KVM_THREADS) {                       // sum the four waves' tiles, in wave order
+      const int rb = e / PM, m = (e / 16) % M, nn = e % 16, n = n0 + (g0 + rb) * 16 + nn;
       if (n >= n1) continue;
-      const int q = rb * 256 + m * 16 + nn;
-      const float s = (part[q] + part[GV_GRP * 256 + q]) + (part[2 * GV_GRP * 256 + q] + part[3 * GV_GRP * 256 + q]);
+      const float s = (part[e] + part[GV_GRP * PM + e]) + (part[2 * GV_GRP * PM + e] + part[3 * GV_GRP * PM + e]);
       out.st((long long)m * out.cols + n, s + (res.ok() ? res.ld((long long)m * res.cols + n) : 0.f));
     }
-    __syncthreads();
+    if (g0 + GV_GRP < nrb) __syncthreads();                                    // the sums are read before the tiles are cleared
   }
+  wait_vm_c<0>();                                                               // the ring's trailing loads have landed
 #ifdef KVM_GEMM_PROF
   pt[4] = wall_clock64();
   __syncthreads();
   if (tid() == 0 && out.dtype == 0) { unsigned long long* o = (unsigned long long*)(out.f() + n0); for (int i = 0; i < 5; ++i) o[i] = pt[i]; o[5] = g_prof[blockIdx.x][6]; }
 #endif
+}
+__device__ __noinline__ void gemv_stream(const Ctx& c, int M, int pro, float eps) {
+  if (!rfl(c.pre)) gemv_stream_r<GV_R>(c, M, pro, eps);
+  else {
+    const int R = gv_pre_ring(rfl(M));
+    if (R == 12) gemv_stream_r<12>(c, M, pro, eps);
+    else if (R == 8) gemv_stream_r<8>(c, M, pro, eps);
+    else gemv_stream_r<4>(c, M, pro, eps);
+  }
 }
 
 __device__ __noinline__ void op_gemv_bf16(const Ctx& c) {

@@ -76,7 +76,7 @@ def lib():
             'kvm_seeded_fill_test': (I, [ctypes.c_ulonglong, ctypes.c_longlong, I, ctypes.c_float, ctypes.c_float, P]),
             'kvm_copy_probe': (I, [ctypes.c_longlong]),
             'kvm_path': (I, [P]),
-            'kvm_static_plan': (I, [P, I, P, I, P, I, I, P, P, P, P, P, I, P, ctypes.c_char_p, I]),
+            'kvm_static_plan': (I, [P, I, P, I, P, I, I, I, P, P, P, P, P, I, P, ctypes.c_char_p, I]),
             'kvm_run_noalloc': (I, [P, I, P, I, P, I, P, I, P, I, I, ctypes.c_ulonglong, P, P, ctypes.c_char_p, I]),
         }
         for name, (res, args) in sig.items():
@@ -324,22 +324,33 @@ def run_noalloc(b: bl.LoadedBundle, buffer_ptrs: list[int], versions: list[int],
     return res, ver.tolist()
 
 
-def static_plan(b: bl.LoadedBundle, workers: int) -> dict:
-    """kvm_static_plan: the static path's plan of bundle b for `workers` workers, computed on the host (no GPU)."""
+def static_plan(b: bl.LoadedBundle, workers: int, dissolve: bool = False) -> dict:
+    """kvm_static_plan: the static path's plan of bundle b for `workers` workers, computed on the host (no GPU).
+    dissolve: the plan of untraced launches (ordering no-ops dissolved into wait sets; see include/kvm_exec.h)."""
     n = b.ntasks
     t = np.ascontiguousarray(b.tasks, np.int32)
     s = np.ascontiguousarray(b.succ, np.int32) if b.succ.size else np.zeros(1, np.int32)
     a = np.ascontiguousarray(b.args, np.int32) if b.args.size else np.zeros(1, np.int32)
     out = {k: np.zeros(n, np.int32) for k in ('worker', 'pos', 'nwaits', 'publishes')}
-    stats = np.zeros(4, np.float64)
+    stats = np.zeros(5, np.float64)
     cap = int(b.succ.size) + 2 * n + 1
-    waits = np.zeros(2 * cap, np.int32)
     err = ctypes.create_string_buffer(512)
-    rc = lib().kvm_static_plan(t.ctypes.data, n, s.ctypes.data, int(b.succ.size), a.ctypes.data, int(b.args.size), workers,
-                               out['worker'].ctypes.data, out['pos'].ctypes.data, out['nwaits'].ctypes.data,
-                               out['publishes'].ctypes.data, waits.ctypes.data, cap, stats.ctypes.data, err, 512)
+    while True:
+        waits = np.zeros(2 * cap, np.int32)
+        rc = lib().kvm_static_plan(t.ctypes.data, n, s.ctypes.data, int(b.succ.size), a.ctypes.data, int(b.args.size), workers,
+                                   1 if dissolve else 0, out['worker'].ctypes.data, out['pos'].ctypes.data, out['nwaits'].ctypes.data,
+                                   out['publishes'].ctypes.data, waits.ctypes.data, cap, stats.ctypes.data, err, 512)
+        if rc < 0 and b'wait_cap' in err.value:
+            cap *= 4
+            continue
+        break
     if rc < 0:
         raise KvmError(err.value.decode())
-    out.update(makespan_us=float(stats[0]), work_us=float(stats[1]), cross_edges=int(stats[2]), edges=int(stats[3]))
-    out['waits'] = waits[:2 * int(out['nwaits'].sum())].reshape(-1, 2)
+    out.update(makespan_us=float(stats[0]), work_us=float(stats[1]), cross_edges=int(stats[2]), edges=int(stats[3]),
+               dissolved=int(stats[4]))
+    w = waits.reshape(-1, 2)
+    nt = int(out['nwaits'].sum())
+    refs = w[:nt][w[:nt, 0] < 0]
+    end = max([nt] + [int(st) + (-1 - int(c)) for c, st in refs])
+    out['waits'] = w[:end].copy()
     return out

@@ -84,3 +84,33 @@ def test_undecidable_wait_is_refused_on_the_static_path():
     with pytest.raises(KvmError, match='no task of the graph publishes'):
         ex.run()
     ex.close()
+
+
+def test_untraced_launches_run_the_plan_with_dissolved_noops():
+    """Untraced launches run the plan with the ordering no-ops dissolved into wait sets: the same results as the
+    oracle and every task counted done; a traced launch of the same executor runs every task (trace complete)."""
+    from kvm_amd.workloads import gpt, mlp, qwen3
+    for w, tol in ((gpt.build(gpt.GPTConfig.tiny(steps=2)), 2e-4), (mlp.build(mlp.MLPConfig(steps=2)), 2e-4),
+                   (qwen3.build(qwen3.Qwen3Config.tiny(batch=2)), None)):
+        lb = bl.load(compiler.compile_spec(w.spec))
+        assert (lb.tasks[:, 0] == 0).any()
+        print(f'static dissolved: {lb.ntasks} tasks', flush=True)
+        init = [oracle.materialize(m, w.init_override.get(m['name'])) for m in lb.metadata['buffers']]
+        ref = oracle.run(lb, [x.copy() for x in init], threads=16)
+        names = [m['name'] for m in lb.metadata['buffers']]
+        skip = tuple(n for n in names if n.startswith(('bk.', 'd.bk.', 'm.bk.', 'v.bk.')))
+        ex = Executor.from_bundle(lb, buffers=[x.copy() for x in init], path=PATH_STATIC)
+        ex.set_trace(False)
+        res = ex.run()
+        assert ex.path() == PATH_STATIC and res['done'] == lb.ntasks and res['err_code'] == 0
+        if tol is not None:
+            assert not compare_run(ex, lb.metadata, ref, tol_f32=tol, skip=skip)
+        else:   # decode: tokens and lengths exact, logits close (the dynamic-path tolerance of this graph is derived elsewhere)
+            assert np.array_equal(ex.read('tok'), ref['buffers'][names.index('tok')])
+            assert np.array_equal(ex.read('lens'), ref['buffers'][names.index('lens')])
+        ex.close()
+        # traced: every task in the trace, the schedule checked (a fresh executor: the graph mutates its buffers)
+        ex = Executor.from_bundle(lb, buffers=[x.copy() for x in init], path=PATH_STATIC)
+        ex.run()
+        check_schedule(ex, lb)
+        ex.close()

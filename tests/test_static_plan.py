@@ -31,22 +31,36 @@ def dag_edges(b):
     return edges
 
 
+def expand(P, lo, hi, self_w):
+    """The (worker, need) pairs of waits[lo:hi], set references expanded, the worker's own entries dropped (program
+    order covers them, as the device skips them)."""
+    out = []
+    for ww, need in P['waits'][lo:hi]:
+        if ww < 0:
+            out += [tuple(x) for x in P['waits'][need:need + (-1 - ww)] if x[0] != self_w]
+        elif ww != self_w:
+            out.append((ww, need))
+    return out
+
+
 def replay(b, P, workers):
-    """Runs the programs with the planned waits only; returns the completion step of every task."""
+    """Runs the programs with the planned waits only; returns the completion step of every placed task (dissolved
+    no-ops: -1)."""
     n = b.ntasks
     progs = [sorted([i for i in range(n) if P['worker'][i] == w], key=lambda i: P['pos'][i]) for w in range(workers)]
+    placed = sum(len(p) for p in progs)
     woff = np.concatenate([[0], np.cumsum(P['nwaits'])])
     progress = [0] * workers                 # published watermark per worker
     nxt = [0] * workers
     done_at = [-1] * n
     step = 0
-    while step < n:
+    while step < placed:
         moved = False
         for w in range(workers):
             if nxt[w] == len(progs[w]):
                 continue
             i = progs[w][nxt[w]]
-            if all(progress[ww] >= need for ww, need in P['waits'][woff[i]:woff[i + 1]]):
+            if all(progress[ww] >= need for ww, need in expand(P, woff[i], woff[i + 1], w)):
                 done_at[i] = step
                 step += 1
                 nxt[w] += 1
@@ -57,13 +71,36 @@ def replay(b, P, workers):
     return done_at
 
 
-def _check(b, workers):
-    P = static_plan(b, workers)
+def placed_edges(b, gone):
+    """DAG edges between placed tasks, through chains of dissolved no-ops."""
+    succ = {}
+    for u, v in dag_edges(b):
+        succ.setdefault(u, []).append(v)
+    out = set()
+    for u in range(b.ntasks):
+        if gone[u]:
+            continue
+        stack, seen = list(succ.get(u, [])), set()
+        while stack:
+            v = stack.pop()
+            if not gone[v]:
+                out.add((u, v))
+            elif v not in seen:
+                seen.add(v)
+                stack += succ.get(v, [])
+    return out
+
+
+def _check(b, workers, dissolve=False):
+    P = static_plan(b, workers, dissolve)
     n = b.ntasks
-    assert sorted((int(P['worker'][i]), int(P['pos'][i])) for i in range(n)) == sorted(
+    gone = P['worker'] < 0
+    assert gone.sum() == P['dissolved'] and (dissolve or not gone.any())
+    assert (b.tasks[gone, 0] == 0).all() and (P['pos'][gone] == -1).all()       # only no-ops dissolve
+    assert sorted((int(P['worker'][i]), int(P['pos'][i])) for i in range(n) if not gone[i]) == sorted(
         (w, k) for w in range(workers) for k in range(int((P['worker'] == w).sum())))
     done = replay(b, P, workers)
-    for u, v in dag_edges(b):
+    for u, v in placed_edges(b, gone):
         assert done[u] < done[v], (u, v)
         if P['worker'][u] == P['worker'][v]:
             assert P['pos'][u] < P['pos'][v]
@@ -73,26 +110,36 @@ def _check(b, workers):
 
 @pytest.mark.parametrize('case', golden_cases())
 @pytest.mark.parametrize('workers', [1, 3, 16])
-def test_plan_of_golden_bundles(case, workers):
-    _check(bl.load(GOLDEN / case), workers)
+@pytest.mark.parametrize('dissolve', [False, True])
+def test_plan_of_golden_bundles(case, workers, dissolve):
+    _check(bl.load(GOLDEN / case), workers, dissolve)
 
 
-def test_plan_of_generated_graphs():
-    from kvm_amd.workloads import gpt, mlp
-    for w, workers in ((gpt.build(gpt.GPTConfig.tiny(steps=2)), 64), (mlp.build(mlp.MLPConfig(steps=2, widths=(64, 128, 768))), 256)):
+@pytest.mark.parametrize('dissolve', [False, True])
+def test_plan_of_generated_graphs(dissolve):
+    from kvm_amd.workloads import gpt, mlp, qwen3
+    for w, workers in ((gpt.build(gpt.GPTConfig.tiny(steps=2)), 64), (mlp.build(mlp.MLPConfig(steps=2, widths=(64, 128, 768))), 256),
+                       (qwen3.build(qwen3.Qwen3Config.tiny(batch=2)), 32)):
         b = bl.load(compiler.compile_spec(w.spec))
-        P = _check(b, workers)
-        assert P['cross_edges'] <= P['edges'] and P['nwaits'].sum() <= P['cross_edges']
+        P = _check(b, workers, dissolve)
+        assert P['nwaits'].sum() <= P['cross_edges']
+        if dissolve:
+            assert P['dissolved'] > 0
 
 
-def test_plan_keeps_a_chain_on_one_worker():
-    """A pure chain costs a cross-worker hop per edge elsewhere: the list scheduler keeps it on one worker, no waits."""
-    from cases import W
-    w = W(1)
-    w.buf('x', 4)
-    prev = []
-    for _ in range(20):
-        prev = [w.task('relu', after=prev, x='x', out='x', n=4)]
-    b = bl.load(compiler.compile_spec(w.spec()))
-    P = static_plan(b, 8)
-    assert len(set(P['worker'].tolist())) == 1 and P['nwaits'].sum() == 0
+def test_dissolved_join_becomes_one_shared_wait_set():
+    """A wide join between two phases: dissolved, the consumers reference one shared set whose entries name the
+    producers' workers, and the replay still honours every producer -> consumer order."""
+    from kvm_amd.workloads import Builder, Workload
+    w = Builder(1)
+    for k in range(8):
+        w.fill(f'x{k}', 4)
+    prod = [w.task('relu', x=f'x{k}', out=f'x{k}', n=4) for k in range(8)]
+    j = w.join(prod, 8)
+    [w.task('relu', after=j, x=f'x{k}', out=f'x{k}', n=4) for k in range(8)]
+    b = bl.load(compiler.compile_spec(Workload(w.spec()).spec))
+    assert (b.tasks[:, 0] == 0).sum() == 1
+    P = _check(b, 8, dissolve=True)
+    assert P['dissolved'] == 1
+    refs = P['waits'][:int(P['nwaits'].sum())]
+    assert (refs[:, 0] < 0).any() and len({int(x) for x in refs[refs[:, 0] < 0, 1]}) == 1

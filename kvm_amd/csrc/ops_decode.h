@@ -300,11 +300,14 @@ __device__ __forceinline__ GvGeo gv_geo(int K, int M, int R) {
 }
 // Ring depth: GV_R steps per wave (8 KiB per wave: in the steady state the stream is not latency bound with more);
 // a ring filled before the dependency wait is deeper, so that more of the task's weights arrive during the wait.
-constexpr int GV_R = 4;
-#ifndef KVM_GV_PRE
-#define KVM_GV_PRE 4
+#ifndef KVM_GV_R
+#define KVM_GV_R 4
 #endif
-__device__ __forceinline__ int gv_pre_ring(int M) { return KVM_GV_PRE; }
+constexpr int GV_R = KVM_GV_R;
+#ifndef KVM_GV_PRE
+#define KVM_GV_PRE 0
+#endif
+__device__ __forceinline__ int gv_pre_ring(int M) { return KVM_GV_PRE ? KVM_GV_PRE : M <= 4 ? 12 : M <= 8 ? 8 : 4; }
 
 // Shapes the stream form takes: K a multiple of 256 (each wave a whole number of 64-k steps), M <= 16, 16-byte
 // aligned rows, byte offsets inside 31 bits.
@@ -369,7 +372,7 @@ __device__ __noinline__ void gemv_prefetch(const Ctx& c, int op) {
   else gemv_prefetch_r<4>(w, n0, n1, K, M, c.smem);
 }
 
-template <int R> __device__ void gemv_stream_r(const Ctx& c, int M_, int pro_, float eps) {
+template <int R> __device__ __noinline__ void gemv_stream_r(const Ctx& c, int M_, int pro_, float eps) {
   const int M = rfl(M_), pro = rfl(pro_);                                       // function arguments arrive in VGPRs
   const View x = uniform_view(c.buf(0)), x2 = uniform_view(c.buf(1)), g = uniform_view(c.buf(2)), w = uniform_view(c.buf(3));
   const View out = uniform_view(c.buf(4)), res = uniform_view(c.buf(5));
@@ -414,25 +417,29 @@ template <int R> __device__ void gemv_stream_r(const Ctx& c, int M_, int pro_, f
       if (g0 == 0) pt[1] = wall_clock64();
 #endif
       const LDS uint16_t* vk = va + wv * kq;
-      for (int rb = 0; rb < ng; ++rb) {
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-        for (int st = 0; st < ns; ++st) {
-          wait_vm_c<2 * (R - 1)>();                                             // this step's two loads have landed
-          const LDS char* slot = rl + cslot * GV_STEP;
-          const u16x8_t w0 = *(const LDS u16x8_t*)slot, w1 = *(const LDS u16x8_t*)(slot + 1024);
-          const u16x8_t a0 = *(const LDS u16x8_t*)(vk + st * 64), a1 = *(const LDS u16x8_t*)(vk + st * 64 + 32);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8_t)(arow ? a0 : u16x8_t{}), (bf16x8_t)w0, acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8_t)(arow ? a1 : u16x8_t{}), (bf16x8_t)w1, acc, 0, 0, 0);
-          wait_lds();                                                           // the slot's reads are done before it is refilled
-          ws.issue<R>(ring);
-          cslot = cslot + 1 == R ? 0 : cslot + 1;
-        }
-        // D[m][n]: lane holds m = 4 (l / 16) + i, n = l % 16; rows m >= M are padding
-        LDS float* pp = part + (wv * GV_GRP + rb) * PM + (l & 15);
+      // One flat loop over the group's steps (row block rb, step st): a nested loop's header is where the compiler
+      // places a full vmcnt wait, which would drain the ring once per row block.
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      int rb = 0, st = 0;
+      for (int tt = 0; tt < ng * ns; ++tt) {
+        wait_vm_c<2 * (R - 1)>();                                               // this step's two loads have landed
+        const LDS char* slot = rl + cslot * GV_STEP;
+        const u16x8_t w0 = *(const LDS u16x8_t*)slot, w1 = *(const LDS u16x8_t*)(slot + 1024);
+        const u16x8_t a0 = *(const LDS u16x8_t*)(vk + st * 64), a1 = *(const LDS u16x8_t*)(vk + st * 64 + 32);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8_t)(arow ? a0 : u16x8_t{}), (bf16x8_t)w0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8_t)(arow ? a1 : u16x8_t{}), (bf16x8_t)w1, acc, 0, 0, 0);
+        wait_lds();                                                             // the slot's reads are done before it is refilled
+        ws.issue<R>(ring);
+        cslot = cslot + 1 == R ? 0 : cslot + 1;
+        if (++st == ns) {           // row block done. D[m][n]: lane holds m = 4 (l / 16) + i, n = l % 16; m >= M padding
+          LDS float* pp = part + (wv * GV_GRP + rb) * PM + (l & 15);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = 4 * (l >> 4) + i;
-          if (m < M) pp[m * 16] += acc[i];
+          for (int i = 0; i < 4; ++i) {
+            const int m = 4 * (l >> 4) + i;
+            if (m < M) pp[m * 16] += acc[i];
+          }
+          acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          st = 0; ++rb;
         }
       }
     }

@@ -34,6 +34,14 @@ typedef struct KvmConfig {
                                //   aging_us of waiting (reference: MvmConfig::aging_us, mvm_exec.cu:375)
   int path;                    // KVM_PATH_*: dynamic scheduler, static per-worker programs, or chosen per graph
                                //   (reference: the --static / --dynamic path choice, mvm_exec.cu:2146-2164)
+  // Stream mode (window_cap > 0; reference: live_cap / win_cap / succ_cap and submit while running, mvm_exec.cu:
+  // 367-408, 742-889): kvm_start launches the persistent kernel at once and each kvm_submit admits one bundle into one
+  // of window_cap window slots of window_tasks tasks and window_edges successor edges while it runs; a slot is reused
+  // once its window has finished. Dynamic FIFO scheduling (no static path, no priority buckets).
+  int window_cap;
+  int window_tasks;
+  int window_edges;
+  int backpressure_ms;         // how long kvm_submit waits for a free window slot before KVM_STATUS_BACKPRESSURE_TIMEOUT
 } KvmConfig;
 
 // Execution paths. DYNAMIC: ready queues and dependency counters. STATIC: the graph is planned on the host into one
@@ -94,11 +102,26 @@ int kvm_read_raw(KvmExec* ex, int idx, void* out, size_t bytes);
 int kvm_set_version(KvmExec* ex, int var, int version);
 // Adds one bundle (reference: MvmExec::submit, mvm_exec.cu:742): its tasks' successor indices are bundle-local.
 // The host validates descriptors, arities, buffer indices/dtypes and operand extents; KVM_STATUS_INVALID on failure.
-// Bundles submitted before kvm_start run in one launch and share state only through version variables.
+// Bundles submitted before kvm_start run in one launch and share state only through version variables. Stream mode:
+// also while the kernel runs; returns the bundle's window id (>= 0), KVM_STATUS_TOO_BIG when it exceeds a window and
+// KVM_STATUS_BACKPRESSURE_TIMEOUT when no slot frees up within backpressure_ms.
 int kvm_submit(KvmExec* ex, const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges,
                const int32_t* args, int nargs);
-// Uploads the task graph, resets the scheduler state and launches the persistent kernel (asynchronous).
+// Uploads the task graph, resets the scheduler state and launches the persistent kernel (asynchronous). Stream mode:
+// launches the kernel with empty window slots and admits the bundles submitted so far.
 int kvm_start(KvmExec* ex);
+// Stream mode: no bundle follows (reference: MvmExec::close, mvm_exec.cu:1505). The kernel ends once every admitted
+// task has finished; kvm_finish closes first when the caller has not.
+int kvm_close(KvmExec* ex);
+// Stream mode: 1 when window `wid` (the non-negative value kvm_submit returned) has finished, 0 when not yet.
+int kvm_window_done(KvmExec* ex, long long wid);
+// Stream mode: one bundle larger than a window, in consecutive windows of at most max_window_tasks tasks (0: the slot
+// size). Task order must be topological (every edge to a higher index). Edges inside a window are device edges; a
+// window with a predecessor in an earlier window is submitted once that window has finished (the host waits, up to
+// timeout_ms per window). Returns the number of windows, or a negative status (reference: submit_stream,
+// mvm_exec.cu:830-889).
+int kvm_submit_stream(KvmExec* ex, const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges,
+                      const int32_t* args, int nargs, int max_window_tasks, int timeout_ms);
 // Waits for the launch, then fills `res` (reference: close/finish, mvm_exec.cu:1505-1540).
 int kvm_finish(KvmExec* ex, KvmResult* res);
 // Runs the whole submitted graph again on the current buffer contents (versions restart from their set values):

@@ -50,7 +50,27 @@ struct KvmQueue {
   int tail; int pad1[31];
 };
 
-// Everything the persistent kernel reads. One task graph per launch (the submitted bundles concatenated).
+// Streaming admission (stream mode, reference: the admitter and its windows, mvm_exec.cuh:820-1058). The persistent
+// kernel runs while the host submits bundles: each bundle occupies one of `wcap` window slots (task slots
+// [w * wtasks, (w + 1) * wtasks), successor slots [w * wedges, ...)). The host stages a window in pinned host memory
+// (KvmHostWin + the arrays after it) and raises `submitted`; an idle worker takes the admission lock, copies the
+// window into device memory, adds its tasks to the per-queue totals and releases its roots. The worker that finishes
+// a window's last task writes its completion mark to host memory, after which the host may reuse the slot.
+struct KvmHostCtl {                      // pinned, written by the host (submitted, closed) and the device (done_mark)
+  long long submitted;                   // windows staged so far (window seq k lives in slot k % wcap)
+  int closed;                            // no window follows the last one submitted
+  int pad[13];
+  long long done_mark[1];                // [wcap] seq + 1 of the last window completed in each slot (flexible)
+};
+struct KvmHostWin { int seq, ntasks, nedges, nroots; int qn[8]; int pad[4]; };   // per slot; qn: tasks per ready queue
+struct KvmAdm {                          // device admission state
+  int lock, next, fin, admitted;         // next: seq of the next window to admit; fin: closed and everything admitted
+  int total[8];                          // tasks admitted per ready queue (tickets below it will be served)
+  int pad[16];
+};
+
+// Everything the persistent kernel reads. One task graph per launch (the submitted bundles concatenated), or, in
+// stream mode, the window slots.
 struct KvmRec;
 struct KvmDevState {
   const MvmTaskDesc* tasks;   // [ntasks]
@@ -83,6 +103,15 @@ struct KvmDevState {
   const int* sw;
   const int* sflag;
   int* sprogress;            // [grid]
+  // Stream mode (stream != 0): FIFO queues of reused cells, ready64[q * qcap + (ticket & (qcap - 1))] = (round << 32) |
+  // slot with round = ticket / qcap + 1 (0: empty); qcap a power of two above the slots' capacity.
+  unsigned long long* ready64;
+  KvmAdm* adm;
+  KvmHostCtl* hctl;          // device address of the pinned control block
+  const char* hwin;          // device address of the pinned staging: KvmHostWin[wcap], then per slot recs, tasks, succ, roots
+  int* win_left;             // [wcap] tasks of the slot's window not yet finished
+  int* win_seq;              // [wcap] seq of the window in the slot
+  int stream, wcap, wtasks, wedges;
   int ntasks, nvars, trace_on, nq, qcap, grid, nb, ncells;
   unsigned long long timeout_ticks;   // stall timeout in wall_clock64 ticks (100 MHz)
   unsigned long long aging_ticks;     // wall_clock64 ticks of waiting worth one priority level (0: strict priority)
@@ -172,6 +201,20 @@ struct KvmRec {
 };
 static_assert(sizeof(View) == 24 && sizeof(KvmRec) == 768, "record layout");
 #define KVM_REC_VEC (int)(sizeof(KvmRec) / 16)
+
+// Byte offsets inside the pinned staging block of stream mode (host and device compute them alike).
+struct KvmWinLayout {
+  size_t meta, recs, tasks, succ, roots, total;
+  __host__ __device__ KvmWinLayout(int wcap, int wtasks, int wedges) {
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    meta = 0;
+    recs = up((size_t)wcap * sizeof(KvmHostWin));
+    tasks = up(recs + (size_t)wcap * wtasks * sizeof(KvmRec));
+    succ = up(tasks + (size_t)wcap * wtasks * sizeof(MvmTaskDesc));
+    roots = up(succ + (size_t)wcap * wedges * sizeof(int32_t));
+    total = up(roots + (size_t)wcap * wtasks * sizeof(int32_t));
+  }
+};
 
 struct Ctx {
   const LDS View* views;     // buffer arguments of the task, resolved from the buffer table by the dispatcher (in LDS)

@@ -25,7 +25,10 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <atomic>
+#include <chrono>
 #include <mutex>
+#include <thread>
 #include <vector>
 #include "common.h"
 #include "ops_basic.h"
@@ -43,7 +46,23 @@ __device__ __forceinline__ void queue_overflow(const KvmDevState& S) {
   int z = 0;   // cannot happen when every task is enqueued once; reported, never written out of bounds
   __hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_QUEUE_OVERFLOW, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Host-memory (pinned, fine-grained) accesses of stream mode: system scope.
+__device__ __forceinline__ long long ld_sys64(const long long* p) { return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM); }
+__device__ __forceinline__ int ld_sys(const int* p) { return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM); }
+__device__ __forceinline__ void st_sys64(long long* p, long long v) { __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM); }
+// Stream mode: cell of ticket `pos` of queue q, stamped with its round.
+__device__ __forceinline__ void put_cell64(const KvmDevState& S, int q, unsigned pos, int t, bool release) {
+  const unsigned long long v = ((unsigned long long)(pos / (unsigned)S.qcap + 1u) << 32) | (unsigned)t;
+  unsigned long long* c = &S.ready64[(size_t)q * S.qcap + (pos & (unsigned)(S.qcap - 1))];
+  if (release) __hip_atomic_store(c, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  else __hip_atomic_store(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ void enqueue(const KvmDevState& S, int t) {
+  if (S.stream) {
+    const int q = t % S.nq;
+    put_cell64(S, q, (unsigned)add_relaxed(&S.queues[q].tail, 1), t, true);
+    return;
+  }
   if (S.tq) {   // priority mode: the task's (queue group, bucket) queue; its release time first when ready tasks age
     const int q = S.tq[t];
     if (S.ready_ts) __hip_atomic_store(&S.ready_ts[t], wall_clock64(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -103,6 +122,8 @@ __device__ bool stalled(const KvmDevState& S, unsigned long long& since, int& se
   int d = 0;
   for (int w = 0; w < S.grid; ++w) d += ld_relaxed(&S.done_blk[w]);
   unsigned long long now = wall_clock64();
+  // stream mode: with every admitted task finished the device is waiting for the host, which is no stall
+  if (S.stream && d >= ld_relaxed(&S.adm->admitted)) { seen = d; since = now; return false; }
   if (d != seen) { seen = d; since = now; return false; }
   if (now - since <= S.timeout_ticks) return false;
   int z = 0;
@@ -164,6 +185,92 @@ __device__ int pop_prio(const KvmDevState& S) {
     int fired = 0;
     if (l == 0 && (polls & 4095) == 4095) fired = stalled(S, since, seen, -1);
     if (__shfl(fired, 0, 64)) return -1;
+  }
+}
+
+// Stream-mode admission, by the whole workgroup of the worker holding the admission lock: every window the host has
+// staged since is copied from pinned host memory into its slot (records, descriptors, successors; counters and park
+// links reset), its tasks are added to the per-queue totals and its roots are released, window by window in seq
+// order. Then, once the host has closed and everything is admitted, fin is raised. Releases the lock.
+__device__ void admit_windows(const KvmDevState& S) {
+  __shared__ int s_go, s_seq;
+  const int t = threadIdx.x;
+  const KvmWinLayout lay(S.wcap, S.wtasks, S.wedges);
+  for (;;) {
+    if (t == 0) {
+      const long long sub = ld_sys64(&S.hctl->submitted);
+      s_seq = ld_relaxed(&S.adm->next);
+      s_go = s_seq < sub;
+    }
+    __syncthreads();
+    if (!s_go) break;
+    const int seq = s_seq, w = seq % S.wcap, base = w * S.wtasks;
+    const KvmHostWin* hm = (const KvmHostWin*)(S.hwin + lay.meta) + w;
+    const int n = ld_sys(&hm->ntasks), ne = ld_sys(&hm->nedges), nr = ld_sys(&hm->nroots);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");    // the staged window (written before `submitted`) is visible
+    const u32x4_t* hr = (const u32x4_t*)(S.hwin + lay.recs + (size_t)base * sizeof(KvmRec));
+    u32x4_t* dr = (u32x4_t*)(const_cast<KvmRec*>(S.recs) + base);
+    for (int k = t; k < n * KVM_REC_VEC; k += KVM_THREADS) dr[k] = hr[k];
+    const u32x4_t* ht = (const u32x4_t*)(S.hwin + lay.tasks + (size_t)base * sizeof(MvmTaskDesc));
+    u32x4_t* dt = (u32x4_t*)(const_cast<MvmTaskDesc*>(S.tasks) + base);
+    for (int k = t; k < n * 4; k += KVM_THREADS) dt[k] = ht[k];
+    const int32_t* hs = (const int32_t*)(S.hwin + lay.succ) + (size_t)w * S.wedges;
+    int32_t* ds = const_cast<int32_t*>(S.succ) + (size_t)w * S.wedges;
+    for (int k = t; k < ne; k += KVM_THREADS) ds[k] = hs[k];
+    const MvmTaskDesc* htd = (const MvmTaskDesc*)(S.hwin + lay.tasks) + base;
+    for (int k = t; k < n; k += KVM_THREADS) {
+      S.indeg[base + k] = htd[k].indegree;
+      S.state[base + k] = 0;
+      S.park_next[base + k] = -1;
+      if (S.trace_on) { KvmTrace z = {}; z.ver0 = z.ver1 = -1; S.trace[base + k] = z; }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (t == 0) {
+      st_relaxed(&S.win_left[w], n);
+      st_relaxed(&S.win_seq[w], seq);
+      for (int q = 0; q < S.nq; ++q) add_relaxed(&S.adm->total[q], ld_sys(&hm->qn[q]));
+      add_relaxed(&S.adm->admitted, n);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    }
+    __syncthreads();
+    const int32_t* hroot = (const int32_t*)(S.hwin + lay.roots) + base;
+    for (int k = t; k < nr; k += KVM_THREADS) release(S, base + hroot[k]);
+    __syncthreads();
+    if (t == 0) st_release(&S.adm->next, seq + 1);
+    __syncthreads();
+  }
+  if (t == 0) {
+    if (ld_sys(&S.hctl->closed) && (long long)ld_relaxed(&S.adm->next) == ld_sys64(&S.hctl->submitted)) st_release(&S.adm->fin, 1);
+    st_release(&S.adm->lock, 0);
+  }
+  __syncthreads();
+}
+
+// Stream-mode dequeue by thread 0: the ticket held across calls (taken once, kept while the worker admits). Returns
+// a task, -1 to leave (error, or closed with every ticket of this queue served), or -2 with the admission lock taken.
+__device__ int stream_next(const KvmDevState& S, long long& held) {
+  const int q = blockIdx.x % S.nq;
+  if (held < 0) held = add_relaxed(&S.queues[q].head, 1u);
+  const unsigned tk = (unsigned)held, round = tk / (unsigned)S.qcap + 1u;
+  const unsigned long long* cell = &S.ready64[(size_t)q * S.qcap + (tk & (unsigned)(S.qcap - 1))];
+  unsigned long long since = wall_clock64();
+  int seen = -1;
+  for (unsigned polls = 0;; ++polls) {
+    const unsigned long long v = __hip_atomic_load(cell, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int err = ld_relaxed(&S.cnt->err_code);
+    if ((unsigned)(v >> 32) == round) { fence_acquire(); held = -1; return (int)(unsigned)v; }
+    if (err != 0) return -1;
+    if (ld_relaxed(&S.adm->fin) && tk >= (unsigned)ld_relaxed(&S.adm->total[q])) return -1;
+    if ((polls & 15) == 0 && !ld_relaxed(&S.adm->fin)) {
+      const bool work = (long long)ld_relaxed(&S.adm->next) < ld_sys64(&S.hctl->submitted) || ld_sys(&S.hctl->closed);
+      int z = 0;
+      if (work && ld_relaxed(&S.adm->lock) == 0 &&
+          __hip_atomic_compare_exchange_strong(&S.adm->lock, &z, 1, __ATOMIC_ACQUIRE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+        return -2;
+    }
+    __builtin_amdgcn_s_sleep(2);
+    if ((polls & 4095) == 4095 && stalled(S, since, seen, (int)tk)) return -1;
   }
 }
 
@@ -261,8 +368,13 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
   MvmTaskDesc& s_desc = s_rec.desc;
   const int t = threadIdx.x;
   int ndone = 0;              // tasks this worker finished (thread 0's count, stored after each task)
+  long long held = -1;        // stream mode: thread 0's ticket, kept while it admits windows
   for (;;) {
-    if (S.tq) {
+    if (S.stream) {
+      if (t == 0) s_slot = stream_next(S, held);
+      __syncthreads();
+      if (s_slot == -2) { admit_windows(S); continue; }
+    } else if (S.tq) {
       if (wave() == 0) {
         const int slot = pop_prio(S);
         if (t == 0) s_slot = ld_relaxed(&S.cnt->err_code) != 0 ? -1 : slot;
@@ -376,6 +488,10 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
           continue;
         }
         const int sq = direct ? s % S.nq : -1;
+        if (S.stream) {   // stream mode: one tail reservation per task, the cell stamped with its round
+          if (direct) { st_relaxed(&S.state[s], 2); put_cell64(S, sq, (unsigned)add_relaxed(&S.queues[sq].tail, 1), s, false); }
+          continue;
+        }
         int cnt_mine = 0;            // lane q < nq: how many of this round's tasks go to queue q
         for (int q = 0; q < S.nq; ++q) {
           const int c2 = __popcll(__ballot(sq == q));
@@ -397,7 +513,13 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
         }
       }
     }
-    if (t == 0) st_relaxed(&S.done_blk[blockIdx.x], ++ndone);
+    if (t == 0) {
+      st_relaxed(&S.done_blk[blockIdx.x], ++ndone);
+      if (S.stream) {   // the slot's window: its last task marks it complete in host memory (the host may reuse it)
+        const int w = slot / S.wtasks;
+        if (add_acqrel(&S.win_left[w], -1) == 1) st_sys64(&S.hctl->done_mark[w], (long long)ld_relaxed(&S.win_seq[w]) + 1);
+      }
+    }
   }
 }
 
@@ -414,6 +536,11 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
   for (int k = i; k < S.grid; k += stride) { S.done_blk[k] = 0; if (S.sprogress) S.sprogress[k] = 0; }
   if (i < S.nq * S.nb) { KvmQueue z = {}; S.queues[i] = z; }
   if (i == 0) { KvmCounters z = {}; *S.cnt = z; }
+  if (S.stream) {
+    for (long long k = i; k < (long long)S.nq * S.qcap; k += stride) S.ready64[k] = 0ull;
+    for (int k = i; k < S.wcap; k += stride) { S.win_left[k] = 0; S.win_seq[k] = -1; }
+    if (i == 0) { KvmAdm z = {}; *S.adm = z; }
+  }
 }
 // Static-path wait on `cnt` (worker, need) pairs at ent, by the 64 lanes of one wave: each lane takes up to four
 // entries per round of 256 and polls them together (their loads in flight at once), entries of the worker itself
@@ -620,6 +747,13 @@ struct KvmExec {
   struct StaticDev { const int *prog_off = nullptr, *prog = nullptr, *wait_off = nullptr, *sw = nullptr, *flag = nullptr; int dissolved = 0; };
   StaticDev sfull, sdis;
   int last_dissolved = 0;                  // no-ops the last launch dissolved (counted as done)
+  // stream mode
+  bool streaming = false, closed = false;
+  KvmHostCtl* hctl = nullptr;              // pinned control block (host address)
+  char* hwin = nullptr;                    // pinned window staging (host address)
+  long long seq = 0, stream_tasks = 0;     // windows and tasks submitted
+  struct Pending { std::vector<MvmTaskDesc> t; std::vector<int32_t> s, a; };
+  std::vector<Pending> pending;            // bundles submitted before kvm_start
   struct LaunchArgs L{};
   KvmDevState S{};
 };
@@ -639,31 +773,40 @@ struct GraphPlan {
   std::vector<int> qcount, qoff, tq, prios, roots, root_cell, fixed_tail;
 };
 
+// Buffer-argument positions of every registry operator (bit k: argument k is a buffer).
+static const unsigned* op_buf_mask() {
+  static unsigned m[KVM_OPMASK_IDS] = {};
+  static bool done = false;
+  if (!done) {
+    for (const kvmv::OpSig& o : kvmv::kRegistry) {
+      if (o.id < 0 || o.id >= KVM_OPMASK_IDS) continue;
+      std::vector<kvmv::ArgInfo> a = kvmv::parse_sig(o.sig);
+      for (size_t k = 0; k < a.size() && k < 32; ++k) if (a[k].type == 0) m[o.id] |= 1u << k;
+    }
+    done = true;
+  }
+  return m;
+}
+// A task's dispatch record: descriptor, argument words and the views of its buffer arguments.
+static void make_rec(const MvmTaskDesc& d, const int32_t* a, const std::vector<MvmBuf>& table, KvmRec& r) {
+  std::memset(&r, 0, sizeof(r));
+  r.desc = d;
+  const unsigned mask = (unsigned)d.op_id < KVM_OPMASK_IDS ? op_buf_mask()[d.op_id] : 0u;
+  for (int k = 0; k < d.args_words && k < KVM_MAX_ARGS; ++k) {
+    const int w = a[k];
+    r.args[k] = w;
+    if (w >= 0 && ((mask >> k) & 1u)) r.views[k] = View{table[w].p, table[w].rows, table[w].cols, table[w].dtype};
+  }
+}
+
 static void plan_graph(const std::vector<MvmTaskDesc>& tasks, const std::vector<int32_t>& succ, const std::vector<int32_t>& args,
                        const std::vector<MvmBuf>& table, const std::vector<int32_t>& roots, int grid, int aging_us, GraphPlan& g) {
   const int n = (int)tasks.size();
   g.n = n;
   g.succ_dev = succ;
   for (auto& e : g.succ_dev) if (tasks[e].indegree == 1 && tasks[e].wait_var < 0) e |= KVM_EDGE_DIRECT;
-  unsigned opmask[KVM_OPMASK_IDS] = {};   // buffer-argument positions of every registry operator
-  for (const kvmv::OpSig& o : kvmv::kRegistry) {
-    if (o.id < 0 || o.id >= KVM_OPMASK_IDS) continue;
-    std::vector<kvmv::ArgInfo> a = kvmv::parse_sig(o.sig);
-    for (size_t k = 0; k < a.size() && k < 32; ++k) if (a[k].type == 0) opmask[o.id] |= 1u << k;
-  }
   g.recs.assign(n, KvmRec{});
-  for (int i = 0; i < n; ++i) {   // dispatch records
-    KvmRec& r = g.recs[i];
-    std::memset(&r, 0, sizeof(r));
-    const MvmTaskDesc& d = tasks[i];
-    r.desc = d;
-    const unsigned mask = (unsigned)d.op_id < KVM_OPMASK_IDS ? opmask[d.op_id] : 0u;
-    for (int k = 0; k < d.args_words && k < KVM_MAX_ARGS; ++k) {
-      const int w = args[d.args_off + k];
-      r.args[k] = w;
-      if (w >= 0 && ((mask >> k) & 1u)) r.views[k] = View{table[w].p, table[w].rows, table[w].cols, table[w].dtype};
-    }
-  }
+  for (int i = 0; i < n; ++i) make_rec(tasks[i], args.data() + tasks[i].args_off, table, g.recs[i]);
   g.nq = std::max(1, std::min(KVM_MAX_QUEUES, grid));
   g.qcap = (n + g.nq - 1) / g.nq;
   // Priority buckets: one per distinct priority in the graph, bucket 0 the highest. A graph with one priority and no
@@ -757,6 +900,7 @@ extern "C" {
 void kvm_config_default(KvmConfig* c) {
   c->blocks = 0; c->trace_on = 1; c->num_vars = 64; c->timeout_us = 20ull * 1000000ull; c->device = 0; c->aging_us = 0;
   c->path = KVM_PATH_DYNAMIC;
+  c->window_cap = 0; c->window_tasks = 0; c->window_edges = 0; c->backpressure_ms = 60000;
 }
 
 const char* kvm_last_error(const KvmExec* ex) { return ex ? ex->err.c_str() : g_err.c_str(); }
@@ -767,6 +911,14 @@ KvmExec* kvm_create(const KvmConfig* cfg) {
   if (c.num_vars < 1 || c.num_vars > (1 << 20)) { g_err = "num_vars out of range"; return nullptr; }
   if (c.aging_us < 0) { g_err = "aging_us must be >= 0"; return nullptr; }
   if (c.path < KVM_PATH_DYNAMIC || c.path > KVM_PATH_AUTO) { g_err = "path must be KVM_PATH_DYNAMIC, KVM_PATH_STATIC or KVM_PATH_AUTO"; return nullptr; }
+  if (c.window_cap < 0 || c.window_cap > (1 << 16)) { g_err = "window_cap out of range"; return nullptr; }
+  if (c.window_cap > 0) {
+    if (c.window_tasks < 1 || c.window_edges < 0 || (long long)c.window_cap * c.window_tasks > (1ll << 26) ||
+        (long long)c.window_cap * c.window_edges > (1ll << 28)) { g_err = "stream mode: window_tasks / window_edges out of range"; return nullptr; }
+    if (c.path == KVM_PATH_STATIC) { g_err = "stream mode runs the dynamic path (a static plan needs the whole graph)"; return nullptr; }
+    if (c.aging_us != 0) { g_err = "stream mode schedules FIFO: aging_us must be 0"; return nullptr; }
+    if (c.backpressure_ms < 0) { g_err = "backpressure_ms must be >= 0"; return nullptr; }
+  }
   if (hipSetDevice(c.device) != hipSuccess) { g_err = "hipSetDevice failed"; return nullptr; }
   hipDeviceProp_t p;
   if (hipGetDeviceProperties(&p, c.device) != hipSuccess) { g_err = "hipGetDeviceProperties failed"; return nullptr; }
@@ -783,6 +935,7 @@ KvmExec* kvm_create(const KvmConfig* cfg) {
   ex->cfg = c; ex->dev = c.device; ex->cus = p.multiProcessorCount;
   ex->grid = c.blocks > 0 ? c.blocks : ex->cus;
   ex->base_versions.assign(c.num_vars, 0);
+  ex->streaming = c.window_cap > 0;
   if (hipStreamCreateWithFlags(&ex->stream, hipStreamNonBlocking) != hipSuccess || hipEventCreate(&ex->ev0) != hipSuccess ||
       hipEventCreate(&ex->ev1) != hipSuccess) { g_err = "stream/event creation failed"; delete ex; return nullptr; }
   return ex;
@@ -791,9 +944,12 @@ KvmExec* kvm_create(const KvmConfig* cfg) {
 void kvm_destroy(KvmExec* ex) {
   if (!ex) return;
   hipSetDevice(ex->dev);
+  if (ex->streaming && ex->hctl && !ex->closed) kvm_close(ex);   // the kernel ends once the admitted tasks finish
   if (ex->stream) hipStreamSynchronize(ex->stream);
   for (auto& b : ex->bufs) hipFree(b.p);
   for (void* q : ex->allocs) hipFree(q);
+  if (ex->hctl) hipHostFree(ex->hctl);
+  if (ex->hwin) hipHostFree(ex->hwin);
   if (ex->ev0) hipEventDestroy(ex->ev0);
   if (ex->ev1) hipEventDestroy(ex->ev1);
   if (ex->stream) hipStreamDestroy(ex->stream);
@@ -876,7 +1032,240 @@ int kvm_set_version(KvmExec* ex, int var, int version) {
   return 0;
 }
 
+// ---------------------------------------------------------------------------------------------- stream mode (host)
+static std::vector<MvmBuf> buf_table(const KvmExec* ex) {
+  std::vector<MvmBuf> table(ex->bufs.size());
+  for (size_t i = 0; i < table.size(); ++i) table[i] = MvmBuf{ex->bufs[i].p, ex->bufs[i].rows, ex->bufs[i].cols, ex->bufs[i].cols, ex->bufs[i].dtype, {0, 0}};
+  return table;
+}
+
+// Device window slots, pinned staging and control block; reset and launch of the persistent kernel.
+static int stream_launch(KvmExec* ex) {
+  const KvmConfig& c = ex->cfg;
+  const int cap = c.window_cap * c.window_tasks;
+  auto alloc = [ex](size_t bytes) -> void* {
+    void* d = nullptr;
+    if (hipMalloc(&d, std::max<size_t>(bytes, 4)) != hipSuccess) return nullptr;
+    ex->allocs.push_back(d);
+    return d;
+  };
+  KvmDevState& S = ex->S;
+  S = KvmDevState{};
+  const int nq = std::max(1, std::min(KVM_MAX_QUEUES, ex->grid));
+  int qcap = 1;
+  while (qcap < cap) qcap <<= 1;
+  S.recs = (const KvmRec*)alloc((size_t)cap * sizeof(KvmRec));
+  S.tasks = (const MvmTaskDesc*)alloc((size_t)cap * sizeof(MvmTaskDesc));
+  S.succ = (const int32_t*)alloc((size_t)c.window_cap * std::max(1, c.window_edges) * sizeof(int32_t));
+  S.indeg = (int*)alloc((size_t)cap * sizeof(int));
+  S.state = (int*)alloc((size_t)cap * sizeof(int));
+  S.park_next = (int*)alloc((size_t)cap * sizeof(int));
+  if (c.trace_on) S.trace = (KvmTrace*)alloc((size_t)cap * sizeof(KvmTrace));
+  S.ready64 = (unsigned long long*)alloc((size_t)nq * qcap * sizeof(unsigned long long));
+  S.queues = (KvmQueue*)alloc(nq * sizeof(KvmQueue));
+  S.done_blk = (int*)alloc(ex->grid * sizeof(int));
+  S.version = (int*)alloc(ex->base_versions.size() * sizeof(int));
+  S.park_head = (int*)alloc(ex->base_versions.size() * sizeof(int));
+  S.cnt = (KvmCounters*)alloc(sizeof(KvmCounters));
+  S.adm = (KvmAdm*)alloc(sizeof(KvmAdm));
+  S.win_left = (int*)alloc(c.window_cap * sizeof(int));
+  S.win_seq = (int*)alloc(c.window_cap * sizeof(int));
+  ex->L = LaunchArgs{};
+  ex->L.base = (int*)alloc(ex->base_versions.size() * sizeof(int));
+  if (!S.recs || !S.tasks || !S.succ || !S.indeg || !S.state || !S.park_next || (c.trace_on && !S.trace) || !S.ready64 || !S.queues ||
+      !S.done_blk || !S.version || !S.park_head || !S.cnt || !S.adm || !S.win_left || !S.win_seq || !ex->L.base) {
+    ex->err = "stream mode: device memory for the window slots"; return KVM_STATUS_HIP_ERROR;
+  }
+  const KvmWinLayout lay(c.window_cap, c.window_tasks, c.window_edges);
+  const size_t ctl_bytes = sizeof(KvmHostCtl) + (size_t)c.window_cap * sizeof(long long);
+  HIPCK(hipHostMalloc((void**)&ex->hctl, ctl_bytes, hipHostMallocCoherent | hipHostMallocMapped));
+  HIPCK(hipHostMalloc((void**)&ex->hwin, lay.total, hipHostMallocCoherent | hipHostMallocMapped));
+  std::memset(ex->hctl, 0, ctl_bytes);
+  std::memset(ex->hwin, 0, lay.meta + (size_t)c.window_cap * sizeof(KvmHostWin));
+  void *dctl = nullptr, *dwin = nullptr;
+  HIPCK(hipHostGetDevicePointer(&dctl, ex->hctl, 0));
+  HIPCK(hipHostGetDevicePointer(&dwin, ex->hwin, 0));
+  S.hctl = (KvmHostCtl*)dctl; S.hwin = (const char*)dwin;
+  S.stream = 1; S.wcap = c.window_cap; S.wtasks = c.window_tasks; S.wedges = c.window_edges;
+  S.ntasks = cap; S.nvars = (int)ex->base_versions.size(); S.trace_on = c.trace_on ? 1 : 0;
+  S.nq = nq; S.qcap = qcap; S.grid = ex->grid; S.nb = 1; S.ncells = 0;
+  S.timeout_ticks = c.timeout_us * 100ull;
+  ex->path = KVM_PATH_DYNAMIC;
+  ex->uploaded = true;
+  HIPCK(hipStreamSynchronize(ex->stream));   // buffer initialisation done
+  HIPCK(hipMemcpyAsync(ex->L.base, ex->base_versions.data(), ex->base_versions.size() * sizeof(int), hipMemcpyHostToDevice, ex->stream));
+  HIPCK(hipEventRecord(ex->ev0, ex->stream));
+  hipLaunchKernelGGL(kvm_reset_kernel, dim3(1024), dim3(256), 0, ex->stream, S, (const int*)ex->L.base);
+  hipLaunchKernelGGL(kvm_exec_kernel, dim3(ex->grid), dim3(KVM_THREADS), 0, ex->stream, S);
+  HIPCK(hipGetLastError());
+  HIPCK(hipEventRecord(ex->ev1, ex->stream));
+  ex->launched = true;
+  return 0;
+}
+
+static bool stream_done_mark(const KvmExec* ex, long long wid) {
+  return __atomic_load_n(&ex->hctl->done_mark[wid % ex->cfg.window_cap], __ATOMIC_ACQUIRE) >= wid + 1;
+}
+
+// Stages one validated bundle into the next window slot (waiting for it to be free) and publishes it. Returns the
+// window id or a negative status.
+static long long stream_stage(KvmExec* ex, const MvmTaskDesc* tasks, int n, const int32_t* succ, int ne, const int32_t* args) {
+  const KvmConfig& c = ex->cfg;
+  if (n > c.window_tasks || ne > c.window_edges) {
+    ex->err = "stream mode: bundle of " + std::to_string(n) + " tasks / " + std::to_string(ne) + " edges exceeds a window (" +
+              std::to_string(c.window_tasks) + " / " + std::to_string(c.window_edges) + ")";
+    return KVM_STATUS_TOO_BIG;
+  }
+  const long long seq = ex->seq;
+  const int w = (int)(seq % c.window_cap), base = w * c.window_tasks;
+  if (seq >= c.window_cap) {   // the slot's previous window (seq - window_cap) must have finished
+    const auto t0 = std::chrono::steady_clock::now();
+    while (!stream_done_mark(ex, seq - c.window_cap)) {
+      if (hipStreamQuery(ex->stream) == hipSuccess) { ex->err = "stream mode: the kernel ended (device error or stall) while windows were pending"; return KVM_STATUS_DEVICE_ERROR; }
+      if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(c.backpressure_ms)) {
+        ex->err = "stream mode: no window slot became free within " + std::to_string(c.backpressure_ms) + " ms (window " + std::to_string(seq - c.window_cap) + " not finished)";
+        return KVM_STATUS_BACKPRESSURE_TIMEOUT;
+      }
+      std::this_thread::sleep_for(std::chrono::microseconds(20));
+    }
+  }
+  const KvmWinLayout lay(c.window_cap, c.window_tasks, c.window_edges);
+  const std::vector<MvmBuf> table = buf_table(ex);
+  KvmRec* recs = (KvmRec*)(ex->hwin + lay.recs) + base;
+  MvmTaskDesc* td = (MvmTaskDesc*)(ex->hwin + lay.tasks) + base;
+  int32_t* sd = (int32_t*)(ex->hwin + lay.succ) + (size_t)w * c.window_edges;
+  int32_t* rt = (int32_t*)(ex->hwin + lay.roots) + base;
+  KvmHostWin& m = *((KvmHostWin*)(ex->hwin + lay.meta) + w);
+  int nroots = 0, qn[KVM_MAX_QUEUES] = {};
+  const int nq = ex->S.nq;
+  for (int i = 0; i < n; ++i) {
+    MvmTaskDesc d = tasks[i];
+    d.succ_off += w * c.window_edges;
+    d.reserved0 = base;
+    td[i] = d;
+    make_rec(d, args + tasks[i].args_off, table, recs[i]);
+    if (d.indegree == 0) rt[nroots++] = i;
+    ++qn[(base + i) % nq];
+  }
+  for (int e = 0; e < ne; ++e) {
+    const int l = succ[e];
+    sd[e] = (base + l) | ((tasks[l].indegree == 1 && tasks[l].wait_var < 0) ? KVM_EDGE_DIRECT : 0);
+  }
+  m.seq = (int)seq; m.ntasks = n; m.nedges = ne; m.nroots = nroots;
+  for (int q = 0; q < KVM_MAX_QUEUES; ++q) m.qn[q] = qn[q];
+  std::atomic_thread_fence(std::memory_order_seq_cst);
+  __atomic_store_n(&ex->hctl->submitted, seq + 1, __ATOMIC_SEQ_CST);
+  ex->seq = seq + 1;
+  ex->stream_tasks += n;
+  return seq;
+}
+
+int kvm_close(KvmExec* ex) {
+  if (!ex->streaming) { ex->err = "kvm_close: not in stream mode"; return KVM_STATUS_INVALID; }
+  if (!ex->hctl) {   // never started: start (admits the pending bundles), then close
+    if (int rc = kvm_start(ex)) return rc;
+  }
+  ex->closed = true;
+  std::atomic_thread_fence(std::memory_order_seq_cst);
+  __atomic_store_n(&ex->hctl->closed, 1, __ATOMIC_SEQ_CST);
+  return 0;
+}
+
+int kvm_window_done(KvmExec* ex, long long wid) {
+  if (!ex->streaming || !ex->hctl || wid < 0 || wid >= ex->seq) { ex->err = "kvm_window_done: not a submitted window"; return KVM_STATUS_INVALID; }
+  return stream_done_mark(ex, wid) ? 1 : 0;
+}
+
+int kvm_submit_stream(KvmExec* ex, const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args,
+                      int nargs, int max_window_tasks, int timeout_ms) {
+  if (!ex->streaming) { ex->err = "kvm_submit_stream: not in stream mode"; return KVM_STATUS_INVALID; }
+  if (ex->closed) { ex->err = "kvm_submit_stream: closed"; return KVM_STATUS_CLOSED; }
+  const std::vector<MvmBuf> table = buf_table(ex);
+  std::string why;
+  if (!kvm_validate_bundle(tasks, ntasks, succ, nedges, args, nargs, table.data(), (int)table.size(), (int)ex->base_versions.size(), &why)) {
+    ex->err = why; return KVM_STATUS_INVALID;
+  }
+  for (int i = 0; i < ntasks; ++i)
+    for (int k = 0; k < tasks[i].succ_cnt; ++k)
+      if (succ[tasks[i].succ_off + k] <= i) {
+        ex->err = "kvm_submit_stream: tasks must be in topological order (edge " + std::to_string(i) + " -> " + std::to_string(succ[tasks[i].succ_off + k]) + ")";
+        return KVM_STATUS_INVALID;
+      }
+  if (!ex->hctl) { if (int rc = kvm_start(ex)) return rc; }
+  const int cap = std::min(max_window_tasks > 0 ? max_window_tasks : ex->cfg.window_tasks, ex->cfg.window_tasks);
+  // window boundaries: at most `cap` tasks and window_edges edges inside the window
+  std::vector<int> lo{0};
+  { int cnt = 0; long long edges = 0;
+    for (int i = 0; i < ntasks; ++i) {
+      int inside = 0;   // edges of task i that stay in its window if the window grows to hold it (counted pessimistically: all)
+      inside = tasks[i].succ_cnt;
+      if (cnt > 0 && (cnt >= cap || edges + inside > ex->cfg.window_edges)) { lo.push_back(i); cnt = 0; edges = 0; }
+      ++cnt; edges += inside;
+    }
+    lo.push_back(ntasks); }
+  const int nw = (int)lo.size() - 1;
+  std::vector<int> win_of(ntasks);
+  for (int k = 0; k < nw; ++k) for (int i = lo[k]; i < lo[k + 1]; ++i) win_of[i] = k;
+  std::vector<std::vector<int>> needs(nw);
+  { std::vector<int> last(nw, -1);
+    for (int i = 0; i < ntasks; ++i) for (int k = 0; k < tasks[i].succ_cnt; ++k) {
+      const int wt = win_of[succ[tasks[i].succ_off + k]], wi = win_of[i];
+      if (wt != wi && last[wt] != wi) { last[wt] = wi; needs[wt].push_back(wi); }
+    } }
+  std::vector<long long> wid(nw, -1);
+  for (int k = 0; k < nw; ++k) {
+    for (int j : needs[k]) {
+      const auto t0 = std::chrono::steady_clock::now();
+      while (!stream_done_mark(ex, wid[j])) {
+        if (hipStreamQuery(ex->stream) == hipSuccess) { ex->err = "kvm_submit_stream: the kernel ended while windows were pending"; return KVM_STATUS_DEVICE_ERROR; }
+        if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(timeout_ms)) {
+          ex->err = "kvm_submit_stream: window " + std::to_string(j) + " did not finish within " + std::to_string(timeout_ms) + " ms";
+          return KVM_STATUS_BACKPRESSURE_TIMEOUT;
+        }
+        std::this_thread::sleep_for(std::chrono::microseconds(20));
+      }
+    }
+    const int a = lo[k], z = lo[k + 1];
+    std::vector<MvmTaskDesc> wt;
+    std::vector<int32_t> ws, wa;
+    for (int i = a; i < z; ++i) {
+      MvmTaskDesc t = tasks[i];
+      const int off = (int)ws.size();
+      for (int e = 0; e < tasks[i].succ_cnt; ++e) { const int s2 = succ[tasks[i].succ_off + e]; if (s2 < z) ws.push_back(s2 - a); }
+      t.succ_off = off; t.succ_cnt = (int)ws.size() - off; t.indegree = 0;
+      t.args_off = (int)wa.size();
+      wa.insert(wa.end(), args + tasks[i].args_off, args + tasks[i].args_off + t.args_words);
+      wt.push_back(t);
+    }
+    for (int s2 : ws) ++wt[s2].indegree;
+    const long long r = stream_stage(ex, wt.data(), (int)wt.size(), ws.data(), (int)ws.size(), wa.data());
+    if (r < 0) return (int)r;
+    wid[k] = r;
+  }
+  return nw;
+}
+
 int kvm_submit(KvmExec* ex, const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs) {
+  if (ex->streaming) {
+    if (ex->closed) { ex->err = "kvm_submit: closed"; return KVM_STATUS_CLOSED; }
+    if (ntasks < 1 || nedges < 0 || nargs < 0) { ex->err = "empty bundle"; return KVM_STATUS_INVALID; }
+    const std::vector<MvmBuf> table = buf_table(ex);
+    std::string why;
+    if (!kvm_validate_bundle(tasks, ntasks, succ, nedges, args, nargs, table.data(), (int)table.size(), (int)ex->base_versions.size(), &why)) {
+      ex->err = why; return KVM_STATUS_INVALID;
+    }
+    if (ntasks > ex->cfg.window_tasks || nedges > ex->cfg.window_edges) {
+      ex->err = "stream mode: bundle exceeds a window (" + std::to_string(ntasks) + " tasks, " + std::to_string(nedges) + " edges)";
+      return KVM_STATUS_TOO_BIG;
+    }
+    if (!ex->hctl) {   // before start: kept, admitted in order at kvm_start
+      ex->pending.push_back(KvmExec::Pending{std::vector<MvmTaskDesc>(tasks, tasks + ntasks), std::vector<int32_t>(succ, succ + nedges),
+                                              std::vector<int32_t>(args, args + nargs)});
+      return (int)(ex->pending.size() - 1);
+    }
+    const long long r = stream_stage(ex, tasks, ntasks, succ, nedges, args);
+    return r < 0 ? (int)r : (int)std::min<long long>(r, 0x7fffffff);
+  }
   if (ex->uploaded) { ex->err = "kvm_submit after kvm_start: this executor runs the bundles submitted before start"; return KVM_STATUS_CLOSED; }
   if (ntasks < 1 || nedges < 0 || nargs < 0) { ex->err = "empty bundle"; return KVM_STATUS_INVALID; }
   std::vector<MvmBuf> table(ex->bufs.size());
@@ -1041,6 +1430,17 @@ static int launch_once(KvmExec* ex, hipEvent_t before_exec = nullptr, hipEvent_t
 
 int kvm_start(KvmExec* ex) {
   hipSetDevice(ex->dev);
+  if (ex->streaming) {
+    if (ex->hctl) { ex->err = "kvm_start: already started"; return KVM_STATUS_INVALID; }
+    if (int rc = stream_launch(ex)) return rc;
+    std::vector<KvmExec::Pending> p;
+    p.swap(ex->pending);
+    for (auto& b : p) {
+      const long long r = stream_stage(ex, b.t.data(), (int)b.t.size(), b.s.data(), (int)b.s.size(), b.a.data());
+      if (r < 0) return (int)r;
+    }
+    return 0;
+  }
   if (!ex->uploaded) { int rc = do_upload(ex); if (rc) return rc; }
   HIPCK(hipStreamSynchronize(ex->stream));   // buffer initialisation done
   HIPCK(hipEventRecord(ex->ev0, ex->stream));
@@ -1052,6 +1452,7 @@ int kvm_start(KvmExec* ex) {
 }
 
 int kvm_relaunch(KvmExec* ex) {
+  if (ex->streaming) { ex->err = "kvm_relaunch: stream mode runs one launch (submit more bundles instead)"; return KVM_STATUS_INVALID; }
   if (!ex->uploaded) return kvm_start(ex);
   hipSetDevice(ex->dev);
   HIPCK(hipEventRecord(ex->ev0, ex->stream));
@@ -1063,6 +1464,7 @@ int kvm_relaunch(KvmExec* ex) {
 }
 
 int kvm_run_timed(KvmExec* ex, int n, float* ms) {
+  if (ex->streaming) { ex->err = "kvm_run_timed: not in stream mode"; return KVM_STATUS_INVALID; }
   hipSetDevice(ex->dev);
   if (!ex->uploaded) { int rc = do_upload(ex); if (rc) return rc; }
   HIPCK(hipStreamSynchronize(ex->stream));
@@ -1076,6 +1478,7 @@ int kvm_run_timed(KvmExec* ex, int n, float* ms) {
 }
 
 int kvm_run_timed_split(KvmExec* ex, int n, float* total_ms, float* exec_ms) {
+  if (ex->streaming) { ex->err = "kvm_run_timed_split: not in stream mode"; return KVM_STATUS_INVALID; }
   hipSetDevice(ex->dev);
   if (n < 1) { ex->err = "kvm_run_timed_split: n < 1"; return KVM_STATUS_INVALID; }
   if (!ex->uploaded) { int rc = do_upload(ex); if (rc) return rc; }
@@ -1101,6 +1504,7 @@ int kvm_run_timed_split(KvmExec* ex, int n, float* total_ms, float* exec_ms) {
 
 int kvm_finish(KvmExec* ex, KvmResult* res) {
   hipSetDevice(ex->dev);
+  if (ex->streaming && !ex->closed) { if (int rc = kvm_close(ex)) return rc; }
   HIPCK(hipStreamSynchronize(ex->stream));
   KvmCounters c{};
   int done = 0;
@@ -1115,7 +1519,7 @@ int kvm_finish(KvmExec* ex, KvmResult* res) {
   if (ex->launched) hipEventElapsedTime(&ms, ex->ev0, ex->ev1);
   if (res) {
     res->err_code = c.err_code; res->err_slot = c.err_slot; res->err_a = c.err_a; res->err_b = c.err_b;
-    res->done = done; res->admitted = (int)ex->tasks.size(); res->grid = ex->grid; res->kernel_ms = ms;
+    res->done = done; res->admitted = ex->streaming ? (int)ex->stream_tasks : (int)ex->tasks.size(); res->grid = ex->grid; res->kernel_ms = ms;
   }
   if (c.err_code) { ex->err = "device error " + std::to_string(c.err_code) + " at task " + std::to_string(c.err_slot); return KVM_STATUS_DEVICE_ERROR; }
   return 0;
@@ -1129,7 +1533,7 @@ int kvm_versions(KvmExec* ex, int32_t* out, int n) {
 }
 
 int kvm_trace(KvmExec* ex, KvmTrace* out, int n) {
-  if (!ex->S.trace || n > (int)ex->tasks.size()) { ex->err = "kvm_trace: tracing off or n too large"; return KVM_STATUS_INVALID; }
+  if (!ex->S.trace || n > kvm_ntasks(ex)) { ex->err = "kvm_trace: tracing off or n too large"; return KVM_STATUS_INVALID; }
   HIPCK(hipStreamSynchronize(ex->stream));
   HIPCK(hipMemcpy(out, ex->S.trace, n * sizeof(KvmTrace), hipMemcpyDeviceToHost));
   return 0;
@@ -1144,7 +1548,9 @@ int kvm_validate(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int 
   return KVM_STATUS_INVALID;
 }
 
-int kvm_ntasks(const KvmExec* ex) { return (int)ex->tasks.size(); }
+int kvm_ntasks(const KvmExec* ex) {   // stream mode: the task slots (window w's task i at w * window_tasks + i)
+  return ex->streaming ? ex->cfg.window_cap * ex->cfg.window_tasks : (int)ex->tasks.size();
+}
 
 int kvm_path(const KvmExec* ex) { return ex ? ex->path : KVM_STATUS_INVALID; }
 

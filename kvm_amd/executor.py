@@ -27,7 +27,8 @@ ERRORS = {0: 'OK', 1: 'BAD_OP', 2: 'BAD_ARITY', 3: 'BAD_BUF_INDEX', 4: 'BAD_BUF'
 
 class KvmConfig(ctypes.Structure):
     _fields_ = [('blocks', ctypes.c_int), ('trace_on', ctypes.c_int), ('num_vars', ctypes.c_int), ('timeout_us', ctypes.c_ulonglong),
-                ('device', ctypes.c_int), ('aging_us', ctypes.c_int), ('path', ctypes.c_int)]
+                ('device', ctypes.c_int), ('aging_us', ctypes.c_int), ('path', ctypes.c_int), ('window_cap', ctypes.c_int),
+                ('window_tasks', ctypes.c_int), ('window_edges', ctypes.c_int), ('backpressure_ms', ctypes.c_int)]
 
 
 PATH_DYNAMIC, PATH_STATIC, PATH_AUTO = 0, 1, 2
@@ -75,7 +76,8 @@ def lib():
             'kvm_validate': (I, [P, I, P, I, P, I, P, I, I, ctypes.c_char_p, I]),
             'kvm_seeded_fill_test': (I, [ctypes.c_ulonglong, ctypes.c_longlong, I, ctypes.c_float, ctypes.c_float, P]),
             'kvm_copy_probe': (I, [ctypes.c_longlong]),
-            'kvm_path': (I, [P]),
+            'kvm_path': (I, [P]), 'kvm_close': (I, [P]), 'kvm_window_done': (I, [P, ctypes.c_longlong]),
+            'kvm_submit_stream': (I, [P, P, I, P, I, P, I, I, I]),
             'kvm_static_plan': (I, [P, I, P, I, P, I, I, I, P, P, P, P, P, I, P, ctypes.c_char_p, I]),
             'kvm_run_noalloc': (I, [P, I, P, I, P, I, P, I, P, I, I, ctypes.c_ulonglong, P, P, ctypes.c_char_p, I]),
         }
@@ -99,12 +101,16 @@ class Executor:
     """
 
     def __init__(self, num_vars: int = 64, trace: bool = True, timeout_s: float = 20.0, blocks: int = 0, device: int = 0,
-                 aging_us: int = 0, path: int = 0):
+                 aging_us: int = 0, path: int = 0, window_cap: int = 0, window_tasks: int = 0, window_edges: int = 0,
+                 backpressure_ms: int = 60000):
+        """window_cap > 0: stream mode (include/kvm_exec.h): start() launches the kernel, submit() admits bundles while
+        it runs (window slots of window_tasks tasks / window_edges edges), stream_close() ends the stream."""
         L = lib()
         cfg = KvmConfig()
         L.kvm_config_default(ctypes.byref(cfg))
         cfg.num_vars, cfg.trace_on, cfg.timeout_us, cfg.blocks, cfg.device = max(1, num_vars), int(trace), int(timeout_s * 1e6), blocks, device
         cfg.aging_us, cfg.path = aging_us, path
+        cfg.window_cap, cfg.window_tasks, cfg.window_edges, cfg.backpressure_ms = window_cap, window_tasks, window_edges, backpressure_ms
         self._h = L.kvm_create(ctypes.byref(cfg))
         if not self._h:
             raise KvmError(f'kvm_create: {L.kvm_last_error(None).decode()}')
@@ -184,12 +190,36 @@ class Executor:
     def set_version(self, var: int, v: int):
         self._check(lib().kvm_set_version(self._h, var, v), 'set_version')
 
-    def submit(self, b: bl.LoadedBundle):
+    @staticmethod
+    def _arrays(b: bl.LoadedBundle):
         t = np.ascontiguousarray(b.tasks, np.int32)
         s = np.ascontiguousarray(b.succ, np.int32) if b.succ.size else np.zeros(1, np.int32)
         a = np.ascontiguousarray(b.args, np.int32) if b.args.size else np.zeros(1, np.int32)
-        self._check(lib().kvm_submit(self._h, t.ctypes.data, t.shape[0], s.ctypes.data, int(b.succ.size), a.ctypes.data, int(b.args.size)),
-                    'submit')
+        return t, s, a
+
+    def submit(self, b: bl.LoadedBundle) -> int:
+        """kvm_submit. Stream mode: the bundle's window id."""
+        t, s, a = self._arrays(b)
+        rc = lib().kvm_submit(self._h, t.ctypes.data, t.shape[0], s.ctypes.data, int(b.succ.size), a.ctypes.data, int(b.args.size))
+        self._check(rc, 'submit')
+        return rc
+
+    def submit_stream(self, b: bl.LoadedBundle, max_window_tasks: int = 0, timeout_ms: int = 60000) -> int:
+        """kvm_submit_stream: one bundle larger than a window, in consecutive windows. Returns the number of windows."""
+        t, s, a = self._arrays(b)
+        rc = lib().kvm_submit_stream(self._h, t.ctypes.data, t.shape[0], s.ctypes.data, int(b.succ.size), a.ctypes.data, int(b.args.size),
+                                     max_window_tasks, timeout_ms)
+        self._check(rc, 'submit_stream')
+        return rc
+
+    def stream_close(self):
+        """kvm_close: no bundle follows; the kernel ends once the admitted tasks have finished."""
+        self._check(lib().kvm_close(self._h), 'close')
+
+    def window_done(self, wid: int) -> bool:
+        rc = lib().kvm_window_done(self._h, wid)
+        self._check(rc, 'window_done')
+        return rc == 1
 
     @classmethod
     def from_bundle(cls, src, buffers: list | None = None, **kw) -> 'Executor':

@@ -113,6 +113,9 @@ int kvm_start(KvmExec* ex);
 // Stream mode: no bundle follows (reference: MvmExec::close, mvm_exec.cu:1505). The kernel ends once every admitted
 // task has finished; kvm_finish closes first when the caller has not.
 int kvm_close(KvmExec* ex);
+// Stream mode: the version variables as the device has published them so far (a pinned mirror, readable while the
+// kernel runs; reference: live_versions).
+int kvm_live_versions(KvmExec* ex, int32_t* out, int n);
 // Stream mode: 1 when window `wid` (the non-negative value kvm_submit returned) has finished, 0 when not yet.
 int kvm_window_done(KvmExec* ex, long long wid);
 // Stream mode: one bundle larger than a window, in consecutive windows of at most max_window_tasks tasks (0: the slot

@@ -11,6 +11,7 @@ CSRC = HERE / 'csrc'
 OUT = HERE / '_build'
 LIB = OUT / 'libkvm_exec.so'
 CLI = OUT / 'kvm_exec'
+RUNNER = OUT / 'kvm_run'
 HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
 ARCH = os.environ.get('KVM_ARCH', 'gfx950')
 # Packed-FP32 instructions are disabled for all device code (they have given silently wrong results on these boxes).
@@ -25,6 +26,8 @@ def build(verbose: bool = False) -> Path:
     _run(cmd, verbose)
     cli = [HIPCC, *FLAGS, str(CSRC / 'cli.cpp'), '-o', str(CLI), f'-L{OUT}', '-lkvm_exec', f'-Wl,-rpath,$ORIGIN']
     _run(cli, verbose)
+    run = [HIPCC, *FLAGS, str(CSRC / 'run.cpp'), '-o', str(RUNNER), f'-L{OUT}', '-lkvm_exec', f'-Wl,-rpath,$ORIGIN']
+    _run(run, verbose)
     del srcs
     return LIB
 

@@ -108,6 +108,7 @@ struct KvmDevState {
   unsigned long long* ready64;
   KvmAdm* adm;
   KvmHostCtl* hctl;          // device address of the pinned control block
+  int* hver;                 // device address of the pinned mirror of the version variables (stream mode), or null
   const char* hwin;          // device address of the pinned staging: KvmHostWin[wcap], then per slot recs, tasks, succ, roots
   int* win_left;             // [wcap] tasks of the slot's window not yet finished
   int* win_seq;              // [wcap] seq of the window in the slot

@@ -103,6 +103,7 @@ __device__ void publish(const KvmDevState& S, int slot, int var, int ver) {
     }
     return;
   }
+  if (S.hver) __hip_atomic_store(&S.hver[var], ver, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);   // host's live view
   fence_seqcst();
   int h = xchg_acqrel(&S.park_head[var], -1);
   while (h >= 0) {
@@ -750,6 +751,7 @@ struct KvmExec {
   // stream mode
   bool streaming = false, closed = false;
   KvmHostCtl* hctl = nullptr;              // pinned control block (host address)
+  int* hver = nullptr;                     // pinned mirror of the version variables (host address)
   char* hwin = nullptr;                    // pinned window staging (host address)
   long long seq = 0, stream_tasks = 0;     // windows and tasks submitted
   struct Pending { std::vector<MvmTaskDesc> t; std::vector<int32_t> s, a; };
@@ -950,6 +952,7 @@ void kvm_destroy(KvmExec* ex) {
   for (void* q : ex->allocs) hipFree(q);
   if (ex->hctl) hipHostFree(ex->hctl);
   if (ex->hwin) hipHostFree(ex->hwin);
+  if (ex->hver) hipHostFree(ex->hver);
   if (ex->ev0) hipEventDestroy(ex->ev0);
   if (ex->ev1) hipEventDestroy(ex->ev1);
   if (ex->stream) hipStreamDestroy(ex->stream);
@@ -1080,12 +1083,16 @@ static int stream_launch(KvmExec* ex) {
   const size_t ctl_bytes = sizeof(KvmHostCtl) + (size_t)c.window_cap * sizeof(long long);
   HIPCK(hipHostMalloc((void**)&ex->hctl, ctl_bytes, hipHostMallocCoherent | hipHostMallocMapped));
   HIPCK(hipHostMalloc((void**)&ex->hwin, lay.total, hipHostMallocCoherent | hipHostMallocMapped));
+  HIPCK(hipHostMalloc((void**)&ex->hver, ex->base_versions.size() * sizeof(int), hipHostMallocCoherent | hipHostMallocMapped));
+  std::memcpy(ex->hver, ex->base_versions.data(), ex->base_versions.size() * sizeof(int));
   std::memset(ex->hctl, 0, ctl_bytes);
   std::memset(ex->hwin, 0, lay.meta + (size_t)c.window_cap * sizeof(KvmHostWin));
   void *dctl = nullptr, *dwin = nullptr;
   HIPCK(hipHostGetDevicePointer(&dctl, ex->hctl, 0));
   HIPCK(hipHostGetDevicePointer(&dwin, ex->hwin, 0));
-  S.hctl = (KvmHostCtl*)dctl; S.hwin = (const char*)dwin;
+  void* dver = nullptr;
+  HIPCK(hipHostGetDevicePointer(&dver, ex->hver, 0));
+  S.hctl = (KvmHostCtl*)dctl; S.hwin = (const char*)dwin; S.hver = (int*)dver;
   S.stream = 1; S.wcap = c.window_cap; S.wtasks = c.window_tasks; S.wedges = c.window_edges;
   S.ntasks = cap; S.nvars = (int)ex->base_versions.size(); S.trace_on = c.trace_on ? 1 : 0;
   S.nq = nq; S.qcap = qcap; S.grid = ex->grid; S.nb = 1; S.ncells = 0;
@@ -1168,6 +1175,12 @@ int kvm_close(KvmExec* ex) {
   ex->closed = true;
   std::atomic_thread_fence(std::memory_order_seq_cst);
   __atomic_store_n(&ex->hctl->closed, 1, __ATOMIC_SEQ_CST);
+  return 0;
+}
+
+int kvm_live_versions(KvmExec* ex, int32_t* out, int n) {
+  if (!ex->streaming || !ex->hver || n < 0 || n > (int)ex->base_versions.size()) { ex->err = "kvm_live_versions: not started in stream mode, or n too large"; return KVM_STATUS_INVALID; }
+  for (int i = 0; i < n; ++i) out[i] = __atomic_load_n(&ex->hver[i], __ATOMIC_ACQUIRE);
   return 0;
 }
 

@@ -76,7 +76,7 @@ def lib():
             'kvm_validate': (I, [P, I, P, I, P, I, P, I, I, ctypes.c_char_p, I]),
             'kvm_seeded_fill_test': (I, [ctypes.c_ulonglong, ctypes.c_longlong, I, ctypes.c_float, ctypes.c_float, P]),
             'kvm_copy_probe': (I, [ctypes.c_longlong]),
-            'kvm_path': (I, [P]), 'kvm_close': (I, [P]), 'kvm_window_done': (I, [P, ctypes.c_longlong]),
+            'kvm_path': (I, [P]), 'kvm_close': (I, [P]), 'kvm_window_done': (I, [P, ctypes.c_longlong]), 'kvm_live_versions': (I, [P, P, I]),
             'kvm_submit_stream': (I, [P, P, I, P, I, P, I, I, I]),
             'kvm_static_plan': (I, [P, I, P, I, P, I, I, I, P, P, P, P, P, I, P, ctypes.c_char_p, I]),
             'kvm_run_noalloc': (I, [P, I, P, I, P, I, P, I, P, I, I, ctypes.c_ulonglong, P, P, ctypes.c_char_p, I]),
@@ -215,6 +215,12 @@ class Executor:
     def stream_close(self):
         """kvm_close: no bundle follows; the kernel ends once the admitted tasks have finished."""
         self._check(lib().kvm_close(self._h), 'close')
+
+    def live_versions(self, n: int) -> np.ndarray:
+        """Stream mode: the version variables as published so far (readable while the kernel runs)."""
+        out = np.zeros(n, np.int32)
+        self._check(lib().kvm_live_versions(self._h, out.ctypes.data, n), 'live_versions')
+        return out
 
     def window_done(self, wid: int) -> bool:
         rc = lib().kvm_window_done(self._h, wid)

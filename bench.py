@@ -199,6 +199,67 @@ def bench_gpt(steps, warmup, cpu):
     return out
 
 
+# Operator classes of the GPT step for the per-class byte-counter attribution (--phases).
+PHASE_OPS = {
+    'gemm': (34, 114, 122, 302, 303, 304, 308),
+    'attention': (45, 46, 47, 48),
+    'cross_entropy': (51, 52, 53, 127),
+    'optimizer': (54, 55, 56, 59, 60, 113, 115, 116, 305),
+}
+
+
+def phase_subgraph(lb, keep):
+    """The tasks of lb selected by the boolean mask `keep`, with the edges among them (edges through dropped tasks
+    are lost, so kept tasks may run in another order: for byte counts, not results) and no version waits or
+    publications."""
+    import numpy as np
+    from kvm_amd import bundle as bl
+    idx = np.nonzero(keep)[0]
+    new = -np.ones(lb.ntasks, np.int64)
+    new[idx] = np.arange(idx.size)
+    t = lb.tasks[idx].copy()
+    succ, indeg = [], np.zeros(idx.size, np.int64)
+    for k, u in enumerate(idx):
+        s = [int(new[v]) for v in lb.succ[lb.tasks[u, 1]:lb.tasks[u, 1] + lb.tasks[u, 2]] if new[v] >= 0]
+        t[k, 1], t[k, 2] = len(succ), len(s)
+        succ += s
+        for v in s:
+            indeg[v] += 1
+    t[:, 3] = indeg
+    t[:, 8], t[:, 9], t[:, 10], t[:, 11] = -1, 0, -1, 0
+    meta = dict(lb.metadata, variables=[], reads=[], publishers=[])
+    return bl.LoadedBundle(meta, t, np.array(succ or [0], np.int32)[:len(succ)], lb.args, lb.root)
+
+
+def bench_phases():
+    """One launch per operator class of the GPT-162M step (its tasks alone, see phase_subgraph), after one launch of
+    the whole step, in this order: step, gemm, attention, cross_entropy, optimizer, other. A counter run of rocprofv3
+    lists the dispatches in the same order; the summaries in profiles/ attribute the step's HBM bytes with them."""
+    import numpy as np
+    from kvm_amd.executor import Executor
+    from kvm_amd.workloads import gpt
+    w = gpt.build(gpt.GPTConfig())
+    ex, lb = build_executor(w, trace=False)
+    ex.relaunch(); ex.finish()
+    ops = lb.tasks[:, 0]
+    out = {'step': {'tasks': lb.ntasks}}
+    ex.close()
+    used = np.zeros(lb.ntasks, bool)
+    for name in (*PHASE_OPS, 'other'):
+        keep = np.isin(ops, PHASE_OPS[name]) if name != 'other' else ~used
+        used |= keep
+        sub = phase_subgraph(lb, keep)
+        ex = Executor(num_vars=1, trace=False, timeout_s=60.0, path=0)
+        for m in lb.metadata['buffers']:
+            ex.add_buffer(m['name'], m['rows'], m['cols'], m['dtype'], init=w.init_override.get(m['name'], m['init']), root=lb.root)
+        ex.submit(sub)
+        res = ex.run()
+        out[name] = {'tasks': int(keep.sum()), 'kernel_ms': round(res['kernel_ms'], 3)}
+        log(f'  phase {name}: {int(keep.sum())} tasks, {res["kernel_ms"]:.3f} ms')
+        ex.close()
+    return out
+
+
 def first_step_invariants(ex, lb, vocab):
     """Full-size sanity of the first training step (untimed): the loss of a randomly initialised model is close to
     ln V, and every weight gradient is finite and nonzero. Raises when not."""
@@ -314,7 +375,8 @@ def copy_probe(mib):
     """One plain copy kernel over `mib` MiB (reads mib MiB, writes mib MiB; the library's kvm_copy_probe): a dispatch
     whose HBM traffic is known, against which the byte counters of the executor's dispatches are calibrated."""
     from kvm_amd import executor
-    executor.copy_probe(mib << 20)
+    for m in str(mib).split(','):
+        executor.copy_probe(int(m) << 20)
 
 
 def main():
@@ -322,11 +384,11 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=3)
-    ap.add_argument('--workload', default='all', choices=['all', 'gpt162m', 'decode', 'sched', 'tiny', 'mlp8', 'gpt355m'])
+    ap.add_argument('--workload', default='all', choices=['all', 'gpt162m', 'decode', 'sched', 'tiny', 'mlp8', 'gpt355m', 'phases'])
     ap.add_argument('--decode-batch', default='1,8')
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--copy-probe', type=int, default=0, metavar='MIB',
-                    help='after the runs, one plain device copy of MIB MiB (reference dispatch for the HBM byte counters)')
+    ap.add_argument('--copy-probe', default='', metavar='MIB[,MIB..]',
+                    help='after the runs, plain device copies of these sizes (reference dispatches for the HBM byte counters)')
     a = ap.parse_args()
     if a.gpus != 1:
         print(json.dumps({'error': 'this executor runs on one GPU; multi-GPU runs are not part of this build', 'n_gpus': a.gpus}))
@@ -350,6 +412,8 @@ def main():
         extra['mlp8'] = bench_small('8 MLPs f32 (C2, 50 steps per graph)', mlp.build(), 50, max(3, a.steps // 4), 1, cpu)
     if a.workload in ('all', 'gpt355m'):
         extra['gpt355m'] = bench_gpt355m(max(3, a.steps // 4), 1, cpu)
+    if a.workload == 'phases':
+        extra['phases'] = bench_phases()
     if 'gpt162m' in extra:
         g = extra['gpt162m']
         result.update({'value': g['ms_per_step'], 'unit': 'ms/step', 'higher_is_better': False, 'ms_per_step': g['ms_per_step'],
@@ -367,7 +431,7 @@ def main():
                                     'frac': d['hbm_frac'], 'traffic': None}})
         if 'cpu_baseline' in d:
             result['cpu_baseline'] = d['cpu_baseline']
-    if 'roofline' in result:
+    if 'roofline' in result and a.workload != 'phases':
         result['roofline']['traffic'] = hbm_traffic('gpt162m' if 'gpt162m' in extra else f'decode_b{extra["decode"][0]["batch"]}')
     result.update(extra)
     if a.copy_probe:

@@ -17,6 +17,7 @@ typedef float f32x4n __attribute__((ext_vector_type(4)));   // native 128-bit fl
 #define KVM_THREADS 256          // every operator runs on one workgroup of 256 threads = four wave64s
 #define KVM_WAVES (KVM_THREADS / 64)
 #define KVM_MAX_ARGS 24
+#define KVM_MAX_PRIVATE_BYTES 2048   // private segment per lane above which kvm_create refuses the kernel build
 #define KVM_LDS_BYTES (128 * 1024)   // LDS one task may use (gfx950 has 160 KiB per CU; the executor keeps the rest)
 
 // Device error codes. 0-20 keep the reference's numbering (reference: include/mvm_exec.cuh:148-164); operator

@@ -930,6 +930,18 @@ KvmExec* kvm_create(const KvmConfig* cfg) {
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kvm_exec_kernel, KVM_THREADS, 0) != hipSuccess || per_cu < 1) {
     g_err = "the executor kernel does not fit on a CU (occupancy query)"; return nullptr;
   }
+  // The workers' private segments (callee-saved registers of the operator calls) are backed by scratch for every
+  // resident wave; a kernel build whose segment grew to 2,096 bytes per lane stopped before its first task finished,
+  // while 1,328 runs. Builds above 2,048 bytes per lane are refused rather than launched.
+  for (const void* k : {(const void*)kvm_exec_kernel, (const void*)kvm_static_kernel}) {
+    hipFuncAttributes fa{};
+    if (hipFuncGetAttributes(&fa, k) != hipSuccess) { g_err = "hipFuncGetAttributes failed"; return nullptr; }
+    if (fa.localSizeBytes > KVM_MAX_PRIVATE_BYTES) {
+      g_err = "the executor kernel's private segment (" + std::to_string(fa.localSizeBytes) + " bytes per lane) exceeds " +
+              std::to_string(KVM_MAX_PRIVATE_BYTES) + ": refusing a build whose workers may not all be resident";
+      return nullptr;
+    }
+  }
   if (c.blocks < 0 || (long long)c.blocks > (long long)per_cu * p.multiProcessorCount) {
     g_err = "blocks exceeds the co-resident capacity of the device (" + std::to_string(per_cu * p.multiProcessorCount) + ")"; return nullptr;
   }

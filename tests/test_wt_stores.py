@@ -72,3 +72,15 @@ def test_every_dispatch_case_is_a_function(asm):
     have = {d.split('(')[0].split('kvm::')[-1].split('<')[0] for d in _demangle(list(_functions(asm))).values()}
     missing = sorted(f for f in called if f not in have)
     assert not missing, f'operators inlined into the kernel (mark them __noinline__): {missing}'
+
+
+def test_kernel_private_segments_stay_below_the_residency_guard(asm):
+    """kvm_create refuses a build whose persistent kernels need more than KVM_MAX_PRIVATE_BYTES (2,048) of private
+    segment per lane; the compiled kernels stay below it (a 2,096-byte build stopped before its first task)."""
+    sizes = {}
+    for name in ('kvm_exec_kernel', 'kvm_static_kernel'):
+        m = re.search(r'\.amdhsa_kernel\s+\S*' + name + r'\S*\n(.*?)\.end_amdhsa_kernel', asm, re.S)
+        assert m, name
+        f = re.search(r'\.amdhsa_private_segment_fixed_size\s+(\d+)', m.group(1))
+        sizes[name] = int(f.group(1))
+    assert all(0 < v <= 2048 for v in sizes.values()), sizes

@@ -1,4 +1,5 @@
-"""Builds the HIP executor library (kvm_amd/_build/libkvm_exec.so) and the kvm_exec CLI for gfx950 with hipcc."""
+"""Builds the HIP executor library (kvm_amd/_build/libkvm_exec.so), the kvm_exec and kvm_run CLIs for gfx950 with hipcc,
+and the host-only bundle compiler kvm_compile."""
 from __future__ import annotations
 
 import os
@@ -12,6 +13,8 @@ OUT = HERE / '_build'
 LIB = OUT / 'libkvm_exec.so'
 CLI = OUT / 'kvm_exec'
 RUNNER = OUT / 'kvm_run'
+COMPILER = OUT / 'kvm_compile'
+CXX = os.environ.get('CXX', 'g++')
 HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
 ARCH = os.environ.get('KVM_ARCH', 'gfx950')
 # Packed-FP32 instructions are disabled for all device code (they have given silently wrong results on these boxes).
@@ -28,6 +31,7 @@ def build(verbose: bool = False) -> Path:
     _run(cli, verbose)
     run = [HIPCC, *FLAGS, str(CSRC / 'run.cpp'), '-o', str(RUNNER), f'-L{OUT}', '-lkvm_exec', f'-Wl,-rpath,$ORIGIN']
     _run(run, verbose)
+    _run([CXX, '-O2', '-std=c++17', str(CSRC / 'compile.cpp'), '-o', str(COMPILER)], verbose)   # host only
     del srcs
     return LIB
 

@@ -33,7 +33,8 @@ def load(src) -> LoadedBundle:
     """`src` is a bundle directory or a kvm_amd.compiler.Bundle."""
     if hasattr(src, 'metadata') and hasattr(src, 'tasks') and isinstance(src.tasks, (bytes, bytearray)):
         return LoadedBundle(src.metadata, np.frombuffer(src.tasks, np.int32).reshape(-1, 16).copy(),
-                            np.frombuffer(src.successors, np.int32).copy(), np.frombuffer(src.args, np.int32).copy())
+                            np.frombuffer(src.successors, np.int32).copy(), np.frombuffer(src.args, np.int32).copy(),
+                            getattr(src, 'data_dir', None))
     d = Path(src)
     meta = json.loads((d / 'metadata.json').read_text())
     return LoadedBundle(meta, np.fromfile(d / 'tasks.bin', np.int32).reshape(-1, 16), np.fromfile(d / 'successors.bin', np.int32),

@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import json
 import math
+import shutil
 import struct
 from array import array
 from dataclasses import dataclass, field
@@ -114,10 +115,20 @@ class Bundle:
     names: list
     buffers: list
     variables: list
+    data_dir: Path | None = None
 
     def write(self, out_dir) -> Path:
+        """Writes the bundle directory; `file` initial values are copied in under their relative path
+        (reference: runtime/compile_workload.py:693-713)."""
         d = Path(out_dir)
+        files = [b for b in self.buffers if b.init['kind'] == 'file']
+        _need(not files or self.data_dir is not None, f'buffers {[b.name for b in files][:4]} use file init: compile with a data_dir')
         d.mkdir(parents=True, exist_ok=True)
+        for b in files:
+            src, dst = self.data_dir / b.init['path'], d / b.init['path']
+            if src.resolve() != dst.resolve():
+                dst.parent.mkdir(parents=True, exist_ok=True)
+                shutil.copyfile(src, dst)
         (d / 'tasks.bin').write_bytes(self.tasks)
         (d / 'successors.bin').write_bytes(self.successors)
         (d / 'args.bin').write_bytes(self.args)
@@ -141,7 +152,7 @@ def _num_i32(x, where):
     return int(x)
 
 
-def _init(where, init, n, dtype):
+def _init(where, init, n, dtype, data_dir=None):
     _need(isinstance(init, dict) and 'kind' in init, f'{where}: init needs a kind')
     conv = {'f32': _num_f32, 'i32': _num_i32, 'bf16': lambda x, w: bf16(_num_f32(x, w))}[dtype]
     k = init['kind']
@@ -161,7 +172,13 @@ def _init(where, init, n, dtype):
         return {'kind': 'seeded', 'seed': seed, 'scale': scale, 'dist': dist, 'draws': draws, 'bias': bias, 'coef': coef}
     if k == 'file':
         p = init['path']
-        _need(isinstance(p, str) and p and not Path(p).is_absolute() and '..' not in Path(p).parts, f'{where}: bad init.path')
+        _need(isinstance(p, str) and p and not Path(p).is_absolute() and '..' not in Path(p).parts and '\\' not in p,
+              f'{where}: bad init.path')
+        if data_dir is not None:      # validated when the data directory is known (compile_workload.py:237-241)
+            f = Path(data_dir) / p
+            _need(f.is_file(), f'{where}: init file {str(f)!r} not found')
+            want = (2 if dtype == 'bf16' else 4) * n
+            _need(f.stat().st_size == want, f'{where}: init file {p!r} has {f.stat().st_size} bytes, expected {want}')
         return {'kind': 'file', 'path': Path(p).as_posix()}
     raise CompileError(f'{where}: unknown init kind {k!r}')
 
@@ -250,7 +267,9 @@ def _reaches(off, succ, pos, a, b):
 
 
 # ------------------------------------------------------------------------------------------------ compile
-def compile_spec(spec: dict, base_versions: dict | None = None, ops: dict | None = None) -> Bundle:
+def compile_spec(spec: dict, base_versions: dict | None = None, ops: dict | None = None, data_dir=None) -> Bundle:
+    """`data_dir`: where `file` initial values are read from (checked here, copied by Bundle.write); None leaves them
+    unchecked, and writing such a bundle is then refused."""
     ops = ops or abi.load_ops()
     _need(isinstance(spec, dict) and 'graphs' in spec and set(spec) <= {'variables', 'buffers', 'graphs'},
           'workload: keys are variables, buffers, graphs (graphs required)')
@@ -268,7 +287,7 @@ def compile_spec(spec: dict, base_versions: dict | None = None, ops: dict | None
         _need(isinstance(rows, int) and isinstance(cols, int) and rows >= 1 and cols >= 1 and rows * cols <= I32_MAX,
               f'buffer {name!r}: bad shape')
         _need(dt in DTYPES, f'buffer {name!r}: bad dtype {dt!r}')
-        init = _init(f'buffer {name!r}', d.get('init', {'kind': 'fill', 'value': 0}), rows * cols, dt)
+        init = _init(f'buffer {name!r}', d.get('init', {'kind': 'fill', 'value': 0}), rows * cols, dt, data_dir)
         buffers[name] = Buffer(name, len(buffers), rows, cols, dt, init)
 
     decls = []
@@ -389,7 +408,7 @@ def compile_spec(spec: dict, base_versions: dict | None = None, ops: dict | None
         'final_versions': {v.name: v.final for v in variables.values()},
     }
     return Bundle(meta, bytes(desc), succ.tobytes(), words.tobytes(), [t.name for t in tasks], list(buffers.values()),
-                  list(variables.values()))
+                  list(variables.values()), Path(data_dir) if data_dir is not None else None)
 
 
 def main(argv=None):
@@ -397,13 +416,15 @@ def main(argv=None):
     p = argparse.ArgumentParser(description='compile a workload JSON into a task bundle directory')
     p.add_argument('workload')
     p.add_argument('out_dir')
-    p.add_argument('--base-versions', default='', help='var=N,...')
+    p.add_argument('--base-versions', action='append', default=[], help='var=N,... (repeatable)')
+    p.add_argument('--data-dir', help='where `file` initial values live (default: the workload file directory)')
     a = p.parse_args(argv)
     base = {}
-    for item in filter(None, a.base_versions.split(',')):
+    for item in filter(None, ','.join(a.base_versions).split(',')):
         k, _, v = item.partition('=')
         base[k] = int(v)
-    compile_spec(json.loads(Path(a.workload).read_text()), base).write(a.out_dir)
+    data_dir = Path(a.data_dir) if a.data_dir else Path(a.workload).resolve().parent
+    compile_spec(json.loads(Path(a.workload).read_text()), base, data_dir=data_dir).write(a.out_dir)
 
 
 if __name__ == '__main__':

@@ -48,8 +48,26 @@ struct Parser {
   std::string str() {
     if (s[p] != '"') throw std::runtime_error("json: string expected");
     std::string out; ++p;
-    while (s[p] != '"') { if (s[p] == '\\') { ++p; char c = s[p++]; out += c == 'n' ? '\n' : c == 't' ? '\t' : c; } else out += s[p++]; }
+    while (p < s.size() && s[p] != '"') {
+      if (s[p] != '\\') { out += s[p++]; continue; }
+      ++p; const char c = s[p++];
+      if (c == 'u') { unsigned cp = hex4();
+        if (cp >= 0xD800 && cp < 0xDC00 && !s.compare(p, 2, "\\u")) { p += 2; cp = 0x10000 + ((cp - 0xD800) << 10) + (hex4() - 0xDC00); }
+        utf8(out, cp); }
+      else out += c == 'n' ? '\n' : c == 't' ? '\t' : c == 'r' ? '\r' : c == 'b' ? '\b' : c == 'f' ? '\f' : c;
+    }
+    if (p >= s.size()) throw std::runtime_error("json: unterminated string");
     ++p; return out;
+  }
+  unsigned hex4() {
+    if (p + 4 > s.size()) throw std::runtime_error("json: bad \\u escape");
+    const unsigned v = (unsigned)std::stoul(s.substr(p, 4), nullptr, 16); p += 4; return v;
+  }
+  static void utf8(std::string& o, unsigned cp) {
+    if (cp < 0x80) o += (char)cp;
+    else if (cp < 0x800) { o += (char)(0xC0 | (cp >> 6)); o += (char)(0x80 | (cp & 0x3F)); }
+    else if (cp < 0x10000) { o += (char)(0xE0 | (cp >> 12)); o += (char)(0x80 | ((cp >> 6) & 0x3F)); o += (char)(0x80 | (cp & 0x3F)); }
+    else { o += (char)(0xF0 | (cp >> 18)); o += (char)(0x80 | ((cp >> 12) & 0x3F)); o += (char)(0x80 | ((cp >> 6) & 0x3F)); o += (char)(0x80 | (cp & 0x3F)); }
   }
 };
 inline std::string read_file(const std::string& path) {

@@ -27,8 +27,11 @@
 #include <regex>
 #include <set>
 #include <sys/stat.h>
+#include <ftw.h>
 #include <thread>
+#include <unistd.h>
 #include "../../include/kvm_exec.h"
+#include "compile.h"
 #include "host_json.h"
 
 using namespace kvmh;
@@ -82,7 +85,7 @@ VerMap as_versions(const Json* j, const std::string& where) {
 struct Cond { std::string var; long long mn = 0, mx = LLONG_MAX; };
 struct Workload { std::string name, file, cls; long long tasks = 0, edges = 0; int priority = 0; std::vector<std::string> variables; };
 struct Admission {
-  std::string name, workload, bundle_dir;
+  std::string name, workload, bundle_dir, compile_workload, compile_data_dir;
   std::vector<std::string> after;
   std::vector<Cond> when;
   long long at_us = -1;
@@ -194,7 +197,11 @@ Manifest parse_manifest(const std::string& root) {
     a.base = as_versions(x.get("base_versions"), w2 + ".base_versions");
     a.publishes = as_versions(x.get("publishes"), w2 + ".publishes");
     if (const Json* bd = x.get("bundle_dir")) if (!is_null(bd)) a.bundle_dir = as_rel_path(*bd, w2 + ".bundle_dir");
-    if (x.get("compile")) fail("%s: compiling on demand is not supported by this runner; give a bundle_dir (or reuse a previous bundle of the workload)", w2.c_str());
+    if (const Json* cp = x.get("compile")) if (!is_null(cp)) {
+      a.compile_workload = as_rel_path(member(*cp, "workload", w2 + ".compile"), w2 + ".compile.workload");
+      a.compile_data_dir = cp->get("data_dir") ? as_rel_path(*cp->get("data_dir"), w2 + ".compile.data_dir") : ".";
+      as_versions(cp->get("base_versions"), w2 + ".compile.base_versions");   // checked; the admission's own base is used
+    }
     const Workload& w = m.workloads[wi->second];
     auto declared = [&](const std::string& v) { return std::find(w.variables.begin(), w.variables.end(), v) != w.variables.end(); };
     for (auto& kv : a.publishes) {
@@ -462,8 +469,52 @@ class Runner {
   double now_us() const { return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0_).count(); }
   bool exists(const std::string& f) const { struct stat sb; return stat(f.c_str(), &sb) == 0; }
 
-  // Each admission's bundle: its own directory (shifted when compiled for other base versions), else the last bundle
-  // of the same workload shifted; then remapped onto the global tables and validated against them.
+  std::vector<std::string> scratch_;                  // directories of bundles compiled on demand (removed at exit)
+
+  // Compiles an admission's workload file in-process (the same compiler as kvm_compile) for the admission's base
+  // versions into a scratch directory, so `file` initial values sit beside the bundle like a precompiled one's.
+  Bundle compile_admission(const Admission& a) {
+    if (a.compile_workload.empty()) fail("admission %s: no usable bundle and no compile entry", a.name.c_str());
+    char tmpl[] = "/tmp/kvm_run_compile.XXXXXX";
+    if (!mkdtemp(tmpl)) fail("admission %s: cannot create a scratch directory", a.name.c_str());
+    scratch_.push_back(tmpl);
+    const std::string data_dir = m_.root + "/" + a.compile_data_dir, out = std::string(tmpl);
+    std::map<std::string, int> base;
+    for (auto& kv : a.base) base[kv.first] = (int)kv.second;
+    try {
+      const std::string text = read_file(m_.root + "/" + a.compile_workload);
+      const kvmc::Bundle b = kvmc::compile(Parser(text).parse(), base, &data_dir);
+      auto put = [&](const std::string& f, const void* p, size_t n) {
+        FILE* fp = fopen((out + "/" + f).c_str(), "wb");
+        if (!fp || (n && fwrite(p, 1, n, fp) != n) || fclose(fp) != 0) fail("admission %s: cannot write %s", a.name.c_str(), f.c_str());
+      };
+      for (const std::string& f : b.files) {     // the file's directories, then the file
+        for (size_t k = f.find('/'); k != std::string::npos; k = f.find('/', k + 1)) mkdir((out + "/" + f.substr(0, k)).c_str(), 0777);
+        const std::string d = read_file(data_dir + "/" + f);
+        put(f, d.data(), d.size());
+      }
+      put("tasks.bin", b.tasks.data(), b.tasks.size() * sizeof(MvmTaskDesc));
+      put("successors.bin", b.succ.data(), b.succ.size() * 4);
+      put("args.bin", b.args.data(), b.args.size() * 4);
+      put("metadata.json", b.metadata.data(), b.metadata.size());
+    } catch (const ManifestError&) {
+      throw;
+    } catch (const std::exception& e) {
+      fail("admission %s: compiling %s: %s", a.name.c_str(), a.compile_workload.c_str(), e.what());
+    }
+    return read_bundle(out);
+  }
+
+ public:
+  ~Runner() {
+    for (auto& d : scratch_)
+      nftw(d.c_str(), [](const char* p, const struct stat*, int, struct FTW*) { return remove(p); }, 16, FTW_DEPTH | FTW_PHYS);
+  }
+
+ private:
+  // Each admission's bundle, the first of: its own directory, the last bundle of the same workload, a compile of its
+  // workload file (the `compile` entry); the first two shifted when compiled for other base versions and skipped
+  // when no shift applies. Then remapped onto the global tables and validated against them.
   void load_bundles() {
     std::map<std::string, Bundle> last;   // workload -> last loaded bundle (local ids)
     std::vector<MvmBuf> table;
@@ -476,21 +527,26 @@ class Runner {
         for (auto& kv : a.publishes) { auto f = b.var_base.find(kv.first); if (f == b.var_base.end() || f->second != a.base.at(kv.first)) return true; }
         return false;
       };
+      std::string why_not;
+      auto try_shift = [&](Bundle& t, const char* what) {
+        if (!needs_shift(t)) { how = what; return true; }
+        const std::string why = rebase(t, a.base);
+        if (why.empty()) { how = std::string(what) + ", versions shifted"; return true; }
+        why_not += std::string(" the ") + what + " bundle cannot be shifted to its base versions:" + why + ";";
+        return false;
+      };
       if (!a.bundle_dir.empty() && exists(m_.root + "/" + a.bundle_dir + "/metadata.json")) {
-        r = read_bundle(m_.root + "/" + a.bundle_dir);
-        how = "precompiled";
-        have = true;
-      } else if (last.count(a.workload)) {
-        r = last.at(a.workload);
-        how = "previous bundle of the workload";
-        have = true;
+        Bundle t = read_bundle(m_.root + "/" + a.bundle_dir);
+        if (try_shift(t, "precompiled")) { r = std::move(t); have = true; }
       }
-      if (!have) fail("admission %s: no bundle (bundle_dir %s missing, and no earlier bundle of workload %s)", a.name.c_str(), a.bundle_dir.c_str(), a.workload.c_str());
-      if (needs_shift(r)) {
-        const std::string why = rebase(r, a.base);
-        if (!why.empty()) fail("admission %s: the %s cannot be shifted to its base versions: %s", a.name.c_str(), how.c_str(), why.c_str());
-        how += ", versions shifted";
+      if (!have && last.count(a.workload)) {
+        Bundle t = last.at(a.workload);
+        if (try_shift(t, "previous bundle of the workload")) { r = std::move(t); have = true; }
       }
+      if (!have && !a.compile_workload.empty()) { r = compile_admission(a); how = "compiled on demand"; have = true; }
+      if (!have)
+        fail("admission %s: no bundle (bundle_dir '%s' missing or unusable, no usable earlier bundle of workload %s, no compile entry);%s",
+             a.name.c_str(), a.bundle_dir.c_str(), a.workload.c_str(), why_not.c_str());
       last[a.workload] = r;
       remap(r, m_, "admission " + a.name);
       char err[1024] = {0};

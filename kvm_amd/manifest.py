@@ -1,7 +1,8 @@
 """Demo directories for the manifest runner `kvm_run` (reference: demo/mvm_run.cu; the frontend's demo writer and its
 CPU runner, frontend/mvmfe/demo.py and mvmfe.run_manifest).
 
-A demo directory holds MANIFEST.json and the compiled bundles of its admissions. `Demo` writes one from workload
+A demo directory holds MANIFEST.json and the compiled bundles of its admissions (or, for an admission with a
+`compile` entry, the workload file the runner compiles on demand). `Demo` writes one from workload
 specs (compiled with kvm_amd.compiler); `serial_order` and `replay` restate the runner's semantics on the CPU: the
 admissions in the first order their conditions allow, each bundle shifted to its base versions and mapped onto the
 manifest's buffer and variable tables, run on the oracle against shared buffers. Tests compare a GPU run of
@@ -47,10 +48,20 @@ class Demo:
     def buffer(self, name, rows, cols, dtype, owner):
         self.buffers[name] = {'rows': rows, 'cols': cols, 'dtype': dtype, 'owner': owner}
 
-    def admission(self, name, workload, bundle_dir=None, after=(), when=(), at_us=None, base_versions=None, publishes=None):
+    def workload_file(self, rel, spec):
+        """Writes a workload JSON for an admission compiled on demand (its `compile` entry)."""
+        p = self.root / rel
+        p.parent.mkdir(parents=True, exist_ok=True)
+        p.write_text(json.dumps(spec))
+
+    def admission(self, name, workload, bundle_dir=None, after=(), when=(), at_us=None, base_versions=None, publishes=None,
+                  compile=None):
+        """compile: (workload file, data dir) relative to the root, compiled by the runner when no bundle applies."""
         a = {'name': name, 'workload': workload}
         if bundle_dir:
             a['bundle_dir'] = bundle_dir
+        if compile:
+            a['compile'] = {'workload': compile[0], 'data_dir': compile[1]}
         if after:
             a['after_bundles'] = list(after)
         if when:
@@ -159,8 +170,12 @@ def replay(root, init: dict | None = None) -> dict:
         d = a.get('bundle_dir')
         if d and (root / d / 'metadata.json').exists():
             b = bl.load(root / d)
-        else:
+        elif a['workload'] in last:
             b = last[a['workload']]
+        else:       # compiled on demand for the admission's base versions
+            c = a['compile']
+            b = bl.load(compiler.compile_spec(json.loads((root / c['workload']).read_text()), a.get('base_versions'),
+                                              data_dir=root / c.get('data_dir', '.')))
         if a.get('publishes'):
             b = _rebase(b, a['base_versions'])
         last[a['workload']] = b

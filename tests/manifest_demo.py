@@ -13,7 +13,9 @@ def _spec(bufs, tasks, variables=()):
     return s
 
 
-def build(root, steps=3):
+def build(root, steps=3, probe=False):
+    """probe: one more workload, admitted after the last serve pass and compiled on demand by the runner from its
+    workload file, with an input read from a data file: Z = P W on the final weights."""
     d = Demo(root)
     d.workload('train', variables=['w'], cls='train')
     d.workload('serve', variables=['w'], cls='serve')
@@ -38,5 +40,19 @@ def build(root, steps=3):
                     base_versions={'w': k - 1}, publishes={'w': k})
         d.admission(f'serve{k}', 'serve', bundle_dir=f'serve{k}', when=[('w', k, k)])
         prev = f'serve{k}'
+    if probe:
+        import numpy as np
+        (d.root / 'data').mkdir(exist_ok=True)
+        np.arange(4 * N, dtype=np.float32).reshape(4, N).__mul__(np.float32(0.125)).tofile(d.root / 'data' / 'p.bin')
+        P = {'name': 'P', 'rows': 4, 'cols': N, 'dtype': 'f32', 'init': {'kind': 'file', 'path': 'p.bin'}}
+        Z = {'name': 'Z', 'rows': 4, 'cols': N, 'dtype': 'f32', 'init': {'kind': 'fill', 'value': 0}}
+        d.workload('probe', variables=['w'], cls='serve')
+        d.workload_file('workloads/probe.json', _spec([W, P, Z], [
+            {'id': 'mm', 'op': 'matmul_tile', 'reads': [{'var': 'w', 'policy': 'at_least', 'version': steps}],
+             'args': {'a': 'P', 'b': 'W', 'out': 'Z', 'bias': None, 'res': None, 'pre': None,
+                      'm0': 0, 'n0': 0, 'M': 4, 'N': N, 'K': N, 'flags': 0, 'alpha': 1.0}}], ['w']))
+        d.buffer('P', 4, N, 'f32', 'probe')
+        d.buffer('Z', 4, N, 'f32', 'probe')
+        d.admission('probe1', 'probe', after=[prev], base_versions={'w': steps}, compile=('workloads/probe.json', 'data'))
     d.classes = {'train': {'weight': 1}, 'serve': {'weight': 4, 'urgent_us': 500}}
     return d.write()

@@ -34,3 +34,18 @@ def test_train_and_serve_demo_matches_the_serial_replay(tmp_path):
         got = np.fromfile(out / f'{name}.bin', np.float32)
         want = ref['buffers'][name].reshape(-1)
         assert np.allclose(got, want, rtol=2e-5, atol=1e-6), (name, np.abs(got - want).max())
+
+
+def test_admission_compiled_on_demand_runs(tmp_path):
+    root = manifest_demo.build(tmp_path / 'demo', steps=2, probe=True)
+    out = tmp_path / 'out'
+    print('kvm_run demo with an on-demand compile', flush=True)
+    r = subprocess.run([str(RUNNER), str(root), '--out', str(out), '--dump', '^(W|Z)$', '--timeout-s', '60'],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.startswith('OK: 5/5 tasks'), (r.stdout, r.stderr)
+    adm = {a['name']: a for a in json.loads((out / 'summary.json').read_text())['admissions']}
+    assert adm['probe1']['how'] == 'compiled on demand'
+    ref = mf.replay(root)
+    for name in ('W', 'Z'):
+        got = np.fromfile(out / f'{name}.bin', np.float32)
+        assert np.allclose(got, ref['buffers'][name].reshape(-1), rtol=2e-5, atol=1e-6), name

@@ -72,3 +72,20 @@ def test_a_bundle_that_does_not_fit_the_table_is_refused(tmp_path):
     _edit(root, lambda m: m['buffers']['X'].update(rows=2))
     rc, out, err = _run(root, '--check-only')
     assert rc == 1 and 'admission serve1' in err, (out, err)
+
+
+def test_an_admission_compiled_on_demand(tmp_path):
+    """The probe admission has no bundle: the runner compiles its workload file (file init read from its data dir)."""
+    root = manifest_demo.build(tmp_path / 'demo', probe=True)
+    rc, out, err = _run(root, '--check-only')
+    assert rc == 0 and out.startswith('OK') and 'probe1' in out, (out, err)
+    r = mf.replay(root)
+    P = np.arange(32, dtype=np.float32).reshape(4, 8) * np.float32(0.125)
+    want = P.astype(np.float64) @ r['buffers']['W'].reshape(8, 8).astype(np.float64)
+    assert np.allclose(r['buffers']['Z'].reshape(4, 8), want, rtol=1e-5, atol=1e-6)
+    (root / 'data' / 'p.bin').write_bytes(bytes(12))
+    rc, out, err = _run(root, '--check-only')
+    assert rc == 1 and 'compiling workloads/probe.json' in err and 'bytes' in err, (out, err)
+    (root / 'workloads' / 'probe.json').unlink()
+    rc, out, err = _run(root, '--check-only')
+    assert rc == 1 and 'probe1' in err, (out, err)

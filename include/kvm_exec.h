@@ -12,6 +12,9 @@
 
 // Task priorities are 0..KVM_PRIORITIES-1, larger first among ready tasks (reference: MVM_NBUCKETS, mvm_exec.cuh:51-52).
 #define KVM_PRIORITIES 32
+// Scheduler classes (reference: MVM_MAX_CLS, MVM_UNLIMITED, include/mvm_sched.h:19-20).
+#define KVM_MAX_CLASSES 8
+#define KVM_UNLIMITED 0x7fffffff
 
 #ifdef __cplusplus
 extern "C" {
@@ -67,8 +70,13 @@ typedef struct KvmInit {
 typedef struct KvmTrace {
   unsigned long long start, end;
   int block, xcc, ver0, ver1;  // ver0/ver1: version of the task's wait variable at start / end (-1 none)
-  int exec_count, pad;         // exec_count: times the task ran (the exactly-once witness)
+  int exec_count;              // times the task ran (the exactly-once witness)
+  int how;                     // scheduler classes on: KVM_TRACE_* bits of how the task was started and ended
 } KvmTrace;
+// KvmTrace.how bits (reference: MVM_TRACE_MISSED / _RESV / _URGENT, include/mvm_sched.h:33-36).
+#define KVM_TRACE_MISSED 1     // finished after its deadline
+#define KVM_TRACE_RESV 2       // started while its class was below its reservation
+#define KVM_TRACE_URGENT 8     // started by the deadline (EDF) tier
 
 typedef struct KvmResult {
   int err_code, err_slot, err_a, err_b;   // first device error (0 none)
@@ -173,6 +181,32 @@ int kvm_copy_probe(long long bytes);
 int kvm_static_plan(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int nedges, const int32_t* args, int nargs,
                     int workers, int flags, int* worker_of, int* pos_of, int* nwaits, int* publishes, int* waits, int wait_cap,
                     double* stats, char* err, int errlen);
+// Scheduler classes (reference: MvmSchedCfg / MvmClassParams, include/mvm_sched.h:24-49, 112-121; the CLI's --sched,
+// --classes, --weights, --min, --max, --urgent-us, --shares, mvm_exec.cu:1940-1952). A task's class is its
+// workload_id (0 .. nclasses-1). Modes: KVM_SCHED_GLOBAL = off (one set of queues, the default). KVM_SCHED_DYNAMIC:
+// per-class ready queues; a worker serves, in this order, a class below its reservation (running < min_cta), then a
+// task whose deadline is within urgent_us (earliest deadline first; deadline_us counts from the launch), then the class
+// with the least weighted worker-time (ticks run / weight) among those below their cap (running < max_cta). The cap is
+// a hard bound on the class's concurrently running tasks outside its reservation. KVM_SCHED_STATIC: the workers are
+// split among the classes in proportion to `share` and each serves only its own class. Priorities and aging order
+// the tasks inside a class. Set before the first kvm_start; not in stream mode; the launches run the dynamic path.
+enum KvmSchedMode { KVM_SCHED_GLOBAL = 0, KVM_SCHED_STATIC = 1, KVM_SCHED_DYNAMIC = 2 };
+typedef struct KvmClassParams {
+  int weight;                  // >= 1: relative share of worker-time among competing classes
+  int min_cta;                 // reservation: workers the class is served first up to (0 none)
+  int max_cta;                 // cap on running tasks, >= 1 (KVM_UNLIMITED none)
+  int urgent_us;               // EDF window: a ready task whose deadline is this close is served first (0 off)
+  int share;                   // KVM_SCHED_STATIC: relative number of workers (>= 1)
+} KvmClassParams;
+int kvm_set_classes(KvmExec* ex, int mode, const KvmClassParams* params, int nclasses);
+// Per-class counters of the last launch (reference: MvmClassTele, include/mvm_sched.h:59-66). Times in
+// wall_clock64 ticks (100 MHz).
+typedef struct KvmClassStats {
+  unsigned long long tasks, busy_ticks, resv_starts, urgent_starts, missed;
+  int max_running, pad;
+} KvmClassStats;
+int kvm_class_stats(KvmExec* ex, KvmClassStats* out, int n);
+
 // The path a launch of this executor uses (KVM_PATH_DYNAMIC or KVM_PATH_STATIC; decided at the first start), or < 0.
 int kvm_path(const KvmExec* ex);
 

@@ -3,7 +3,8 @@
 // (2 for usage errors).
 //
 //   kvm_exec [--golden [--golden-tol R] [--golden-tol-bf16 R]] [--dump-bin DIR i,j,..] [--trace-csv FILE] [--repeat N] [--timeout-s N]
-//            [--blocks N] [--no-trace] [--quiet] [--check-ops] bundle_dir...
+//            [--blocks N] [--no-trace] [--quiet] [--check-ops] [--sched global|static|dynamic --classes N --weights a,b,..
+//            --min a,b,.. --max a,b,.. --urgent-us a,b,.. --shares a,b,..] bundle_dir...
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -28,12 +29,27 @@ static void usage() {
                   "  --trace-csv FILE            per-task timeline   --repeat N   run the graph N times (timed)   --timeout-s N\n"
                   "  --dump-buffers              print every buffer (reference text format)\n"
                   "  --path auto|dynamic|static  scheduler: per-worker static programs, ready queues, or chosen from the graph (default auto)\n"
-                  "  --blocks N   --no-trace   --quiet   --check-ops\n");
+                  "  --blocks N   --no-trace   --quiet   --check-ops\n"
+                  "  --sched global|static|dynamic --classes N   scheduler classes (a task's class is its workload_id); per class, comma\n"
+                  "    lists: --weights, --min (reservation), --max (cap), --urgent-us (EDF window), --shares (static split)\n");
 }
 
 int main(int argc, char** argv) {
   std::vector<std::string> dirs; bool golden = false, quiet = false, trace = true, dump_text = false; float tol = 1e-6f, tol_bf16 = 1e-2f;
   const char* csv = nullptr; std::string dump_dir; std::vector<int> dump_idx; int repeat = 1, blocks = 0, path = KVM_PATH_AUTO; long long timeout_s = 20;
+  int sched = KVM_SCHED_GLOBAL, nclasses = 1;
+  std::vector<KvmClassParams> cls(KVM_MAX_CLASSES, KvmClassParams{1, 0, KVM_UNLIMITED, 0, 1});
+  // a comma list of integers into field f of classes 0, 1, ...
+  auto list = [&](const char* v, int KvmClassParams::*f) {
+    int c = 0;
+    for (const char* p = v; *p && c < KVM_MAX_CLASSES; ++c) {
+      char* e; const long x = strtol(p, &e, 10);
+      if (e == p) return false;
+      cls[c].*f = (int)x;
+      p = *e == ',' ? e + 1 : e;
+    }
+    return true;
+  };
   for (int i = 1; i < argc; ++i) {
     std::string a = argv[i];
     auto next = [&]() -> const char* { if (i + 1 >= argc) { usage(); exit(2); } return argv[++i]; };
@@ -52,6 +68,17 @@ int main(int argc, char** argv) {
       else { usage(); return 2; }
     }
     else if (a == "--quiet") quiet = true;
+    else if (a == "--sched") {
+      const std::string m = next();
+      if (m == "global") sched = KVM_SCHED_GLOBAL; else if (m == "static") sched = KVM_SCHED_STATIC; else if (m == "dynamic") sched = KVM_SCHED_DYNAMIC;
+      else { usage(); return 2; }
+    }
+    else if (a == "--classes") { nclasses = atoi(next()); if (nclasses < 1 || nclasses > KVM_MAX_CLASSES) { usage(); return 2; } }
+    else if (a == "--weights") { if (!list(next(), &KvmClassParams::weight)) { usage(); return 2; } }
+    else if (a == "--min") { if (!list(next(), &KvmClassParams::min_cta)) { usage(); return 2; } }
+    else if (a == "--max") { if (!list(next(), &KvmClassParams::max_cta)) { usage(); return 2; } }
+    else if (a == "--urgent-us") { if (!list(next(), &KvmClassParams::urgent_us)) { usage(); return 2; } }
+    else if (a == "--shares") { if (!list(next(), &KvmClassParams::share)) { usage(); return 2; } }
     else if (a == "--dump-bin") { dump_dir = next(); for (char* p = (char*)next(); *p;) { char* e; long v = strtol(p, &e, 10); if (e == p) { usage(); return 2; } dump_idx.push_back((int)v); p = *e == ',' ? e + 1 : e; } }
     else if (a == "--check-ops") { for (int id = 0; id < 400; ++id) if (const char* n = kvm_op_name(id)) printf("%3d %s\n", id, n); return 0; }
     else if (a[0] == '-') { usage(); return 2; }
@@ -85,6 +112,8 @@ int main(int argc, char** argv) {
       if (kvm_submit(ex.get(), t.data(), (int)t.size(), s.data(), (int)s.size(), a.data(), (int)a.size()) < 0)
         throw std::runtime_error(dirs[k] + ": submit: " + kvm_last_error(ex.get()));
     }
+    if (sched != KVM_SCHED_GLOBAL && kvm_set_classes(ex.get(), sched, cls.data(), nclasses) < 0)
+      throw std::runtime_error(kvm_last_error(ex.get()));
     KvmResult r{}; float ms = 0;
     if (repeat == 1) { if (kvm_start(ex.get()) < 0) throw std::runtime_error(kvm_last_error(ex.get())); }
     else if (kvm_run_timed(ex.get(), repeat, &ms) < 0) throw std::runtime_error(kvm_last_error(ex.get()));
@@ -161,6 +190,13 @@ int main(int argc, char** argv) {
     }
     bool pass = r.err_code == 0 && bad == 0;
     printf("%s: %d/%d tasks, %.3f ms (%s path)%s\n", pass ? "OK" : "FAIL", r.done, r.admitted, r.kernel_ms, kvm_path(ex.get()) == KVM_PATH_STATIC ? "static" : "dynamic", golden ? (bad ? ", golden MISMATCH" : ", golden match") : "");
+    if (sched != KVM_SCHED_GLOBAL && !quiet) {   // per-class report (reference: mvm_exec.cu:1842-1860)
+      std::vector<KvmClassStats> st(nclasses);
+      const int m = kvm_class_stats(ex.get(), st.data(), nclasses);
+      for (int c = 0; c < m; ++c)
+        printf("class %d: %llu tasks, busy %.3f ms, %llu reserved starts, %llu urgent starts, %llu missed deadlines, max running %d\n", c,
+               st[c].tasks, st[c].busy_ticks / 1e5, st[c].resv_starts, st[c].urgent_starts, st[c].missed, st[c].max_running);
+    }
     return pass ? 0 : 1;
   } catch (const std::exception& e) {
     fprintf(stderr, "kvm_exec: %s\n", e.what());

@@ -72,6 +72,27 @@ struct KvmAdm {                          // device admission state
 
 // Everything the persistent kernel reads. One task graph per launch (the submitted bundles concatenated), or, in
 // stream mode, the window slots.
+// Scheduler classes (reference: MvmClsDev / MvmSchedDev, include/mvm_sched.h:80-111). A task's class is its
+// workload_id. Per class: a parameter line written by the host at upload, a hot line (running workers, weighted
+// virtual time charged ahead of time, the running-time estimate) and a statistics line; times in wall_clock64 ticks.
+struct alignas(128) KvmClsDev {
+  int weight, min_cta, max_cta, urgent_ticks, vt_mul, blk_lo, blk_hi, has_dl;   // vt_mul = 2^20 / weight
+  int pad0[24];
+  int running, pad1a;
+  unsigned long long vtime;        // sum of (ticks run) * vt_mul: the class with the least is served first
+  unsigned est;                    // running-time estimate of the class's tasks (moving average, ticks)
+  int pad1[27];
+  unsigned long long tasks, busy, resv_starts, urgent_starts, missed;
+  int max_running;
+  int pad2[21];
+};
+static_assert(sizeof(KvmClsDev) == 384, "class lines");
+struct KvmSchedDev {
+  unsigned long long t0;           // launch time: task deadlines count from here
+  int pad[30];
+  KvmClsDev cls[KVM_MAX_CLASSES];
+};
+
 struct KvmRec;
 struct KvmDevState {
   const MvmTaskDesc* tasks;   // [ntasks]
@@ -114,6 +135,10 @@ struct KvmDevState {
   int* win_left;             // [wcap] tasks of the slot's window not yet finished
   int* win_seq;              // [wcap] seq of the window in the slot
   int stream, wcap, wtasks, wedges;
+  // Scheduler classes (ncls > 0): task t of class c = tasks[t].workload_id goes to queue ((t % nq) * ncls + c) * nb +
+  // bucket; a worker's lane c * nb + b watches class c's bucket b.
+  KvmSchedDev* sched;
+  int ncls;
   int ntasks, nvars, trace_on, nq, qcap, grid, nb, ncells;
   unsigned long long timeout_ticks;   // stall timeout in wall_clock64 ticks (100 MHz)
   unsigned long long aging_ticks;     // wall_clock64 ticks of waiting worth one priority level (0: strict priority)

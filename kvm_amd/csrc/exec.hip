@@ -189,6 +189,143 @@ __device__ int pop_prio(const KvmDevState& S) {
   }
 }
 
+// Class-mode pop (scheduler classes on), by all 64 lanes of wave 0: lane c * nb + b watches bucket b of class c in
+// this worker's queue group (reference policy: mvm_pop, mvm_sched.cuh:261-374; its tiers restated on one wave64
+// that sees every class's buckets at once instead of deciding the class first and scanning it after). Each
+// available bucket head gets a key (tier << 60 | order): tier 1 its class is below its reservation (order: running /
+// min_cta), tier 2 its deadline is within the class's EDF window (order: slack), tier 3 the class's weighted virtual
+// time. Classes at their cap offer nothing outside tier 1. The smallest key wins; inside the winning class the
+// bucket rule of pop_prio applies (lowest bucket, or the largest aged score). The winner counts itself into its
+// class's running workers before the head CAS, and gives the count back when capped or when the CAS loses, so the
+// cap holds at every instant. Returns the task (how = KVM_TRACE_* start bits, est = the virtual-time charge taken,
+// in ticks), or -1 to leave.
+#define KVM_SLACKMAX (1ll << 40)
+__device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
+  const int l = lane(), g = blockIdx.x % S.nq, nb = S.nb, nc = S.ncls;
+  const bool lane_ok = l < nc * nb;
+  const int c = lane_ok ? l / nb : 0, b = lane_ok ? l % nb : 0;
+  KvmClsDev* const K = S.sched->cls;
+  const int mn = K[c].min_cta, mx = K[c].max_cta, urg = K[c].urgent_ticks, vt_mul = K[c].vt_mul;
+  const bool mine = lane_ok && (int)blockIdx.x >= K[c].blk_lo && (int)blockIdx.x < K[c].blk_hi;
+  const bool need_cell = S.aging_ticks != 0 || (urg > 0 && K[c].has_dl != 0);
+  const int qi = (g * nc + c) * nb + b;
+  const int cnt = mine ? S.qcount[qi] : 0, off = mine ? S.qoff[qi] : 0;
+  const unsigned long long boost = (mine && S.aging_ticks) ? (unsigned long long)S.bucket_prio[b] * S.aging_ticks : 0ull;
+  const unsigned long long t0 = S.sched->t0;
+  unsigned long long since = wall_clock64();
+  int seen = -1;
+  for (unsigned polls = 0;; ++polls) {
+    if (__shfl(ld_relaxed(&S.cnt->err_code), 0, 64) != 0) return -1;
+    const int h = mine ? (int)ld_relaxed(&S.queues[qi].head) : 0;
+    const int tl = mine ? ld_relaxed(&S.queues[qi].tail) : 0;
+    if (__ballot(mine && h < cnt) == 0ull) return -1;
+    bool avail = mine && h < tl && h < cnt;
+    int cell = -1;
+    if (avail && need_cell) { cell = ld_acquire(&S.ready[off + h]); avail = cell >= 0; }
+    int run_k = 0;
+    unsigned long long vt_k = 0;
+    if (l < nc) {
+      run_k = ld_relaxed(&K[l].running);
+      vt_k = __hip_atomic_load(&K[l].vtime, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const int run = __shfl(run_k, c, 64);
+    const unsigned long long vt = __shfl(vt_k, c, 64);
+    const unsigned long long now = wall_clock64();
+    unsigned long long key = ~0ull, score = 0;
+    if (avail) {
+      if (run < mn) key = (1ull << 60) | (((unsigned long long)run << 20) / (unsigned)(mn > 0 ? mn : 1));
+      else if (run >= mx) avail = false;
+      else {
+        key = (3ull << 60) | (vt < (1ull << 60) ? vt : (1ull << 60) - 1);
+        if (urg > 0 && cell >= 0) {
+          const int dl = S.tasks[cell].deadline_us;
+          if (dl >= 0) {
+            long long slack = (long long)(t0 + (unsigned long long)dl * 100ull) - (long long)now;
+            if (slack <= (long long)urg) {
+              slack = slack < -KVM_SLACKMAX ? -KVM_SLACKMAX : slack > KVM_SLACKMAX ? KVM_SLACKMAX : slack;
+              key = (2ull << 60) | (unsigned long long)(slack + KVM_SLACKMAX);
+            }
+          }
+        }
+      }
+      if (avail && S.aging_ticks) score = boost + (now - __hip_atomic_load(&S.ready_ts[cell], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    }
+    if (!avail) key = ~0ull;
+    if (__ballot(avail)) {
+      unsigned long long best = key;
+      for (int o = 32; o > 0; o >>= 1) { const unsigned long long y = __shfl_xor(best, o, 64); best = y < best ? y : best; }
+      unsigned long long wm = __ballot(avail && key == best);
+      const int first = __ffsll((long long)wm) - 1, wc = first / nb;
+      const unsigned long long cmask = nb >= 64 ? ~0ull : (((1ull << nb) - 1ull) << (wc * nb));
+      wm &= cmask;                                 // equal keys across classes: the lower class
+      const int tier = (int)(best >> 60);
+      int win = first;
+      if (tier != 2 && S.aging_ticks) {
+        const bool cand = (wm >> l) & 1ull;
+        unsigned long long bs = cand ? score : 0ull;
+        for (int o = 32; o > 0; o >>= 1) { const unsigned long long y = __shfl_xor(bs, o, 64); bs = y > bs ? y : bs; }
+        win = __ffsll((long long)__ballot(cand && score == bs)) - 1;
+      }
+      int got = -1;
+      unsigned charge = 0;
+      if (l == win) {
+        KvmClsDev& k = K[c];
+        const int old = add_relaxed(&k.running, 1);
+        if (tier >= 2 && old >= mx) add_relaxed(&k.running, -1);   // capped meanwhile: look again
+        else {
+          unsigned expect = (unsigned)h;
+          if (__hip_atomic_compare_exchange_strong(&S.queues[qi].head, &expect, expect + 1u, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+            for (;;) {   // the enqueuer reserved this cell before we saw the tail: its store is in flight
+              got = ld_relaxed(&S.ready[off + h]);
+              if (got >= 0 || ld_relaxed(&S.cnt->err_code) != 0) break;
+              __builtin_amdgcn_s_sleep(1);
+            }
+          }
+          if (got < 0) add_relaxed(&k.running, -1);
+          else {
+            __hip_atomic_fetch_max(&k.max_running, old + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            charge = __hip_atomic_load(&k.est, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(&k.vtime, (unsigned long long)charge * (unsigned)vt_mul, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+      got = __shfl(got, win, 64);
+      if (got >= 0) {
+        est = __shfl(charge, win, 64);
+        how = tier == 1 ? KVM_TRACE_RESV : tier == 2 ? KVM_TRACE_URGENT : 0;
+        fence_acquire();
+        return got;
+      }
+      continue;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    int fired = 0;
+    if (l == 0 && (polls & 4095) == 4095) fired = stalled(S, since, seen, -1);
+    if (__shfl(fired, 0, 64)) return -1;
+  }
+}
+
+// Completion accounting of a class-mode task (thread 0): the worker leaves its class's running count, the
+// virtual-time charge taken at the claim is corrected to the ticks run, the class's running-time estimate moves
+// (a racy moving average, an estimate by design) and the statistics line counts the task. Returns the trace bits.
+__device__ int cls_done(const KvmDevState& S, const MvmTaskDesc& d, int how, unsigned est, unsigned long long start) {
+  KvmClsDev& k = S.sched->cls[d.workload_id];
+  const unsigned long long end = wall_clock64(), run = end - start;
+  add_relaxed(&k.running, -1);
+  __hip_atomic_fetch_add(&k.vtime, (unsigned long long)(((long long)run - (long long)est) * (long long)k.vt_mul), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned r32 = run < 0xffffffffull ? (unsigned)run : 0xffffffffu;
+  const unsigned old = __hip_atomic_load(&k.est, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(&k.est, old ? (unsigned)(((unsigned long long)old * 7ull + r32) / 8ull) : r32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool missed = d.deadline_us >= 0 && end > S.sched->t0 + (unsigned long long)d.deadline_us * 100ull;
+  auto add64 = [](unsigned long long* p, unsigned long long v) { __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  add64(&k.tasks, 1ull);
+  add64(&k.busy, run);
+  if (how & KVM_TRACE_RESV) add64(&k.resv_starts, 1ull);
+  if (how & KVM_TRACE_URGENT) add64(&k.urgent_starts, 1ull);
+  if (missed) add64(&k.missed, 1ull);
+  return how | (missed ? KVM_TRACE_MISSED : 0);
+}
+
 // Stream-mode admission, by the whole workgroup of the worker holding the admission lock: every window the host has
 // staged since is copied from pinned host memory into its slot (records, descriptors, successors; counters and park
 // links reset), its tasks are added to the per-queue totals and its roots are released, window by window in seq
@@ -370,11 +507,19 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
   const int t = threadIdx.x;
   int ndone = 0;              // tasks this worker finished (thread 0's count, stored after each task)
   long long held = -1;        // stream mode: thread 0's ticket, kept while it admits windows
+  int how = 0;                // class mode (thread 0): start bits and virtual-time charge of the running task
+  unsigned est = 0;
+  unsigned long long t_start = 0;
   for (;;) {
     if (S.stream) {
       if (t == 0) s_slot = stream_next(S, held);
       __syncthreads();
       if (s_slot == -2) { admit_windows(S); continue; }
+    } else if (S.ncls) {
+      if (wave() == 0) {
+        const int slot = pop_cls(S, how, est);
+        if (t == 0) { s_slot = ld_relaxed(&S.cnt->err_code) != 0 ? -1 : slot; t_start = wall_clock64(); }
+      }
     } else if (S.tq) {
       if (wave() == 0) {
         const int slot = pop_prio(S);
@@ -515,6 +660,10 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
       }
     }
     if (t == 0) {
+      if (S.ncls) {
+        const int bits = cls_done(S, s_desc, how, est, t_start);
+        if (S.trace_on) S.trace[slot].how = bits;
+      }
       st_relaxed(&S.done_blk[blockIdx.x], ++ndone);
       if (S.stream) {   // the slot's window: its last task marks it complete in host memory (the host may reuse it)
         const int w = slot / S.wtasks;
@@ -535,8 +684,14 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
   for (long long k = i; k < (long long)S.ncells; k += stride) S.ready[k] = -1;
   for (int k = i; k < S.nvars; k += stride) { S.version[k] = base_versions[k]; S.park_head[k] = -1; }
   for (int k = i; k < S.grid; k += stride) { S.done_blk[k] = 0; if (S.sprogress) S.sprogress[k] = 0; }
-  if (i < S.nq * S.nb) { KvmQueue z = {}; S.queues[i] = z; }
+  for (int k = i; k < S.nq * S.nb * (S.ncls ? S.ncls : 1); k += stride) { KvmQueue z = {}; S.queues[k] = z; }
   if (i == 0) { KvmCounters z = {}; *S.cnt = z; }
+  if (S.ncls && i < S.ncls) {   // class hot and statistics lines; the parameter line stays as uploaded
+    KvmClsDev& k = S.sched->cls[i];
+    k.running = 0; k.vtime = 0; k.est = 200;   // 2 us until measured
+    k.tasks = k.busy = k.resv_starts = k.urgent_starts = k.missed = 0; k.max_running = 0;
+  }
+  if (S.ncls && i == 0) S.sched->t0 = wall_clock64();
   if (S.stream) {
     for (long long k = i; k < (long long)S.nq * S.qcap; k += stride) S.ready64[k] = 0ull;
     for (int k = i; k < S.wcap; k += stride) { S.win_left[k] = 0; S.win_seq[k] = -1; }
@@ -674,7 +829,7 @@ __global__ void kvm_seed_kernel(KvmDevState S, const int* roots, const int* root
     S.ready[root_cell[r]] = t;
     S.state[t] = 2;
   }
-  for (int q = threadIdx.x; q < S.nq * S.nb; q += blockDim.x) S.queues[q].tail = fixed_tail[q];
+  for (int q = threadIdx.x; q < S.nq * S.nb * (S.ncls ? S.ncls : 1); q += blockDim.x) S.queues[q].tail = fixed_tail[q];
   __syncthreads();
   if (threadIdx.x == 0)
     for (int r = nfixed; r < nroots; ++r) release(S, roots[r]);
@@ -758,6 +913,9 @@ struct KvmExec {
   std::vector<Pending> pending;            // bundles submitted before kvm_start
   struct LaunchArgs L{};
   KvmDevState S{};
+  // scheduler classes (kvm_set_classes)
+  int sched_mode = KVM_SCHED_GLOBAL;
+  std::vector<KvmClassParams> classes;
 };
 
 #define HIPCK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { ex->err = std::string(#x) + ": " + hipGetErrorString(e_); return KVM_STATUS_HIP_ERROR; } } while (0)
@@ -801,15 +959,18 @@ static void make_rec(const MvmTaskDesc& d, const int32_t* a, const std::vector<M
   }
 }
 
+// ncls > 0: scheduler classes, the buckets split per class (task t's class is its workload_id); one_group: a single
+// queue group (the class-partitioned mode, whose workers of one class must all see its buckets).
 static void plan_graph(const std::vector<MvmTaskDesc>& tasks, const std::vector<int32_t>& succ, const std::vector<int32_t>& args,
-                       const std::vector<MvmBuf>& table, const std::vector<int32_t>& roots, int grid, int aging_us, GraphPlan& g) {
+                       const std::vector<MvmBuf>& table, const std::vector<int32_t>& roots, int grid, int aging_us, GraphPlan& g,
+                       int ncls = 0, bool one_group = false) {
   const int n = (int)tasks.size();
   g.n = n;
   g.succ_dev = succ;
   for (auto& e : g.succ_dev) if (tasks[e].indegree == 1 && tasks[e].wait_var < 0) e |= KVM_EDGE_DIRECT;
   g.recs.assign(n, KvmRec{});
   for (int i = 0; i < n; ++i) make_rec(tasks[i], args.data() + tasks[i].args_off, table, g.recs[i]);
-  g.nq = std::max(1, std::min(KVM_MAX_QUEUES, grid));
+  g.nq = one_group ? 1 : std::max(1, std::min(KVM_MAX_QUEUES, grid));
   g.qcap = (n + g.nq - 1) / g.nq;
   // Priority buckets: one per distinct priority in the graph, bucket 0 the highest. A graph with one priority and no
   // aging runs in FIFO mode (queue t % nq, fetch-add tickets); otherwise task t goes to queue (t % nq) * nb + bucket.
@@ -817,15 +978,20 @@ static void plan_graph(const std::vector<MvmTaskDesc>& tasks, const std::vector<
   for (const MvmTaskDesc& d : tasks) g.prios.push_back(d.priority);
   std::sort(g.prios.begin(), g.prios.end(), [](int a, int b) { return a > b; });
   g.prios.erase(std::unique(g.prios.begin(), g.prios.end()), g.prios.end());
-  g.prio_mode = g.prios.size() > 1 || aging_us > 0;
+  g.prio_mode = g.prios.size() > 1 || aging_us > 0 || ncls > 0;
   g.nb = g.prio_mode ? (int)g.prios.size() : 1;
-  g.nqb = g.nq * g.nb;
+  const int nc = ncls > 0 ? ncls : 1;
+  g.nqb = g.nq * nc * g.nb;
   g.qcount.assign(g.nqb, 0); g.qoff.assign(g.nqb, 0); g.tq.clear();
   if (g.prio_mode) {
     int bucket_of[KVM_PRIORITIES];
     for (int b = 0; b < g.nb; ++b) bucket_of[g.prios[b]] = b;
     g.tq.resize(n);
-    for (int t = 0; t < n; ++t) { g.tq[t] = (t % g.nq) * g.nb + bucket_of[tasks[t].priority]; ++g.qcount[g.tq[t]]; }
+    for (int t = 0; t < n; ++t) {
+      const int c = ncls > 0 ? tasks[t].workload_id : 0;
+      g.tq[t] = ((t % g.nq) * nc + c) * g.nb + bucket_of[tasks[t].priority];
+      ++g.qcount[g.tq[t]];
+    }
     for (int q = 1; q < g.nqb; ++q) g.qoff[q] = g.qoff[q - 1] + g.qcount[q - 1];
   } else {
     for (int t = 0; t < n; ++t) ++g.qcount[t % g.nq];
@@ -1391,8 +1557,29 @@ static int do_upload(KvmExec* ex) {
   if (ex->tasks.empty()) { ex->err = "nothing submitted"; return KVM_STATUS_INVALID; }
   std::vector<MvmBuf> table(ex->bufs.size());
   for (size_t i = 0; i < table.size(); ++i) table[i] = MvmBuf{ex->bufs[i].p, ex->bufs[i].rows, ex->bufs[i].cols, ex->bufs[i].cols, ex->bufs[i].dtype, {0, 0}};
+  const int ncls = ex->sched_mode != KVM_SCHED_GLOBAL ? (int)ex->classes.size() : 0;
+  std::vector<unsigned char> has_dl(KVM_MAX_CLASSES, 0);
+  if (ncls) {   // every task names a class; the (class, priority) buckets fit one wave's lanes
+    std::vector<char> seen(KVM_PRIORITIES, 0);
+    int nprio = 0;
+    for (size_t i = 0; i < ex->tasks.size(); ++i) {
+      const MvmTaskDesc& d = ex->tasks[i];
+      if (d.workload_id < 0 || d.workload_id >= ncls) {
+        ex->err = "scheduler classes: task " + std::to_string(i) + " has workload_id " + std::to_string(d.workload_id) + ", not a class in [0, " +
+                  std::to_string(ncls) + ")";
+        return KVM_STATUS_INVALID;
+      }
+      if (!seen[d.priority]) { seen[d.priority] = 1; ++nprio; }
+      if (d.deadline_us >= 0) has_dl[d.workload_id] = 1;
+    }
+    if (nprio * ncls > 64) {
+      ex->err = "scheduler classes: " + std::to_string(ncls) + " classes x " + std::to_string(nprio) + " distinct priorities exceed 64 ready buckets";
+      return KVM_STATUS_INVALID;
+    }
+    if (ex->cfg.path == KVM_PATH_STATIC) { ex->err = "scheduler classes run on the dynamic path (path must be DYNAMIC or AUTO)"; return KVM_STATUS_INVALID; }
+  }
   GraphPlan g;
-  plan_graph(ex->tasks, ex->succ, ex->args, table, ex->roots, ex->grid, ex->cfg.aging_us, g);
+  plan_graph(ex->tasks, ex->succ, ex->args, table, ex->roots, ex->grid, ex->cfg.aging_us, g, ncls, ex->sched_mode == KVM_SCHED_STATIC);
   auto alloc = [ex](size_t bytes) -> void* {
     void* d = nullptr;
     if (hipMalloc(&d, bytes) != hipSuccess) return nullptr;
@@ -1404,7 +1591,34 @@ static int do_upload(KvmExec* ex) {
                              ex->cfg.timeout_us, alloc, ex->stream, ex->S, ex->L, ex->err);
   if (rc) return rc == KVM_STATUS_TOO_BIG ? KVM_STATUS_HIP_ERROR : rc;
   ex->path = KVM_PATH_DYNAMIC;
-  if (ex->cfg.path != KVM_PATH_DYNAMIC) {
+  if (ncls) {   // class parameter lines; the reset kernel clears the rest at every launch
+    KvmSchedDev h{};
+    double tot = 0, acc = 0;
+    for (auto& c : ex->classes) tot += c.share;
+    for (int c = 0; c < ncls; ++c) {
+      const KvmClassParams& p = ex->classes[c];
+      KvmClsDev& k = h.cls[c];
+      k.weight = p.weight; k.min_cta = p.min_cta; k.max_cta = p.max_cta;
+      k.urgent_ticks = (int)std::min<long long>((long long)p.urgent_us * 100ll, 0x7fffffffll);
+      k.vt_mul = (1 << 20) / p.weight; k.has_dl = has_dl[c];
+      k.blk_lo = 0; k.blk_hi = ex->grid;
+      if (ex->sched_mode == KVM_SCHED_STATIC) {   // cumulative bounds, the last class takes the rest
+        k.blk_lo = (int)(acc / tot * ex->grid + 0.5);
+        acc += p.share;
+        k.blk_hi = c + 1 == ncls ? ex->grid : (int)(acc / tot * ex->grid + 0.5);
+        bool used = false;
+        for (const MvmTaskDesc& d : ex->tasks) if (d.workload_id == c) { used = true; break; }
+        if (used && k.blk_hi <= k.blk_lo) {
+          ex->err = "scheduler classes: class " + std::to_string(c) + " gets no worker of " + std::to_string(ex->grid) + " (shares)";
+          return KVM_STATUS_INVALID;
+        }
+      }
+    }
+    KvmSchedDev* d = (KvmSchedDev*)alloc(sizeof(KvmSchedDev));
+    if (!d || hipMemcpy(d, &h, sizeof h, hipMemcpyHostToDevice) != hipSuccess) { ex->err = "scheduler classes: device memory"; return KVM_STATUS_HIP_ERROR; }
+    ex->S.sched = d; ex->S.ncls = ncls;
+  }
+  if (ex->cfg.path != KVM_PATH_DYNAMIC && !ncls) {
     if (int r = plan_static(ex, ex->cfg.path == KVM_PATH_STATIC)) return r;
     if (ex->path == KVM_PATH_STATIC) {   // the plans' arrays next to the dynamic state (a later relaunch may use either)
       auto put = [&](const std::vector<int>& v) -> int* {
@@ -1575,6 +1789,38 @@ int kvm_validate(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, int 
 
 int kvm_ntasks(const KvmExec* ex) {   // stream mode: the task slots (window w's task i at w * window_tasks + i)
   return ex->streaming ? ex->cfg.window_cap * ex->cfg.window_tasks : (int)ex->tasks.size();
+}
+
+int kvm_set_classes(KvmExec* ex, int mode, const KvmClassParams* params, int nclasses) {
+  if (ex->uploaded || ex->launched) { ex->err = "kvm_set_classes: before the first kvm_start"; return KVM_STATUS_INVALID; }
+  if (ex->streaming) { ex->err = "kvm_set_classes: stream mode schedules FIFO"; return KVM_STATUS_INVALID; }
+  if (mode == KVM_SCHED_GLOBAL) { ex->sched_mode = mode; ex->classes.clear(); return 0; }
+  if (mode != KVM_SCHED_STATIC && mode != KVM_SCHED_DYNAMIC) { ex->err = "kvm_set_classes: mode must be KVM_SCHED_GLOBAL, _STATIC or _DYNAMIC"; return KVM_STATUS_INVALID; }
+  if (!params || nclasses < 1 || nclasses > KVM_MAX_CLASSES) { ex->err = "kvm_set_classes: 1 to KVM_MAX_CLASSES classes"; return KVM_STATUS_INVALID; }
+  for (int c = 0; c < nclasses; ++c) {
+    const KvmClassParams& p = params[c];
+    const std::string w = "kvm_set_classes: class " + std::to_string(c) + ": ";
+    if (p.weight < 1 || p.weight > (1 << 20)) { ex->err = w + "weight must be in [1, 2^20]"; return KVM_STATUS_INVALID; }
+    if (p.min_cta < 0) { ex->err = w + "min_cta must be >= 0"; return KVM_STATUS_INVALID; }
+    if (p.max_cta < 1) { ex->err = w + "max_cta must be >= 1 (KVM_UNLIMITED for none)"; return KVM_STATUS_INVALID; }
+    if (p.urgent_us < 0) { ex->err = w + "urgent_us must be >= 0"; return KVM_STATUS_INVALID; }
+    if (mode == KVM_SCHED_STATIC && p.share < 1) { ex->err = w + "share must be >= 1"; return KVM_STATUS_INVALID; }
+  }
+  ex->sched_mode = mode;
+  ex->classes.assign(params, params + nclasses);
+  return 0;
+}
+
+int kvm_class_stats(KvmExec* ex, KvmClassStats* out, int n) {
+  if (!ex->S.sched || !ex->launched) { ex->err = "kvm_class_stats: no launch with scheduler classes"; return KVM_STATUS_INVALID; }
+  hipSetDevice(ex->dev);
+  HIPCK(hipStreamSynchronize(ex->stream));
+  std::vector<KvmClsDev> k(ex->S.ncls);
+  HIPCK(hipMemcpy(k.data(), ex->S.sched->cls, k.size() * sizeof(KvmClsDev), hipMemcpyDeviceToHost));
+  const int m = std::min(n, ex->S.ncls);
+  for (int c = 0; c < m; ++c)
+    out[c] = KvmClassStats{k[c].tasks, k[c].busy, k[c].resv_starts, k[c].urgent_starts, k[c].missed, k[c].max_running, 0};
+  return m;
 }
 
 int kvm_path(const KvmExec* ex) { return ex ? ex->path : KVM_STATUS_INVALID; }

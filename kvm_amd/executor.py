@@ -41,7 +41,7 @@ class KvmInit(ctypes.Structure):
 
 class KvmTrace(ctypes.Structure):
     _fields_ = [('start', ctypes.c_ulonglong), ('end', ctypes.c_ulonglong), ('block', ctypes.c_int), ('xcc', ctypes.c_int),
-                ('ver0', ctypes.c_int), ('ver1', ctypes.c_int), ('exec_count', ctypes.c_int), ('pad', ctypes.c_int)]
+                ('ver0', ctypes.c_int), ('ver1', ctypes.c_int), ('exec_count', ctypes.c_int), ('how', ctypes.c_int)]
 
 
 class KvmResult(ctypes.Structure):
@@ -50,7 +50,19 @@ class KvmResult(ctypes.Structure):
 
 
 TRACE_DTYPE = np.dtype([('start', '<u8'), ('end', '<u8'), ('block', '<i4'), ('xcc', '<i4'), ('ver0', '<i4'), ('ver1', '<i4'),
-                        ('exec_count', '<i4'), ('pad', '<i4')])
+                        ('exec_count', '<i4'), ('how', '<i4')])
+TRACE_MISSED, TRACE_RESV, TRACE_URGENT = 1, 2, 8
+SCHED_GLOBAL, SCHED_STATIC, SCHED_DYNAMIC = 0, 1, 2
+UNLIMITED = 0x7fffffff
+
+
+class KvmClassParams(ctypes.Structure):
+    _fields_ = [('weight', ctypes.c_int), ('min_cta', ctypes.c_int), ('max_cta', ctypes.c_int), ('urgent_us', ctypes.c_int),
+                ('share', ctypes.c_int)]
+
+
+CLASS_STATS_DTYPE = np.dtype([('tasks', '<u8'), ('busy_ticks', '<u8'), ('resv_starts', '<u8'), ('urgent_starts', '<u8'),
+                              ('missed', '<u8'), ('max_running', '<i4'), ('pad', '<i4')])
 
 
 def declared_symbols() -> list[str]:
@@ -79,6 +91,7 @@ def lib():
             'kvm_path': (I, [P]), 'kvm_close': (I, [P]), 'kvm_window_done': (I, [P, ctypes.c_longlong]), 'kvm_live_versions': (I, [P, P, I]),
             'kvm_submit_stream': (I, [P, P, I, P, I, P, I, I, I]),
             'kvm_static_plan': (I, [P, I, P, I, P, I, I, I, P, P, P, P, P, I, P, ctypes.c_char_p, I]),
+            'kvm_set_classes': (I, [P, I, P, I]), 'kvm_class_stats': (I, [P, P, I]),
             'kvm_run_noalloc': (I, [P, I, P, I, P, I, P, I, P, I, I, ctypes.c_ulonglong, P, P, ctypes.c_char_p, I]),
         }
         for name, (res, args) in sig.items():
@@ -239,6 +252,20 @@ class Executor:
         ex.submit(b)
         ex.meta = b.metadata
         return ex
+
+    def set_classes(self, mode: int, classes: list):
+        """Scheduler classes (include/kvm_exec.h, kvm_set_classes): classes[c] is a dict with weight, min_cta, max_cta,
+        urgent_us, share (defaults 1, 0, UNLIMITED, 0, 1); a task's class is its workload_id. Before the first start."""
+        arr = (KvmClassParams * max(1, len(classes)))()
+        for c, d in enumerate(classes):
+            arr[c] = KvmClassParams(d.get('weight', 1), d.get('min_cta', 0), d.get('max_cta', UNLIMITED), d.get('urgent_us', 0), d.get('share', 1))
+        self._check(lib().kvm_set_classes(self._h, mode, arr, len(classes)), 'set_classes')
+
+    def class_stats(self, n: int) -> np.ndarray:
+        """Per-class counters of the last launch (CLASS_STATS_DTYPE; busy_ticks at 100 MHz)."""
+        out = np.zeros(n, CLASS_STATS_DTYPE)
+        m = self._check(lib().kvm_class_stats(self._h, out.ctypes.data, n), 'class_stats')
+        return out[:m]
 
     def path(self) -> int:
         """PATH_DYNAMIC or PATH_STATIC: the path launches use (decided at the first start)."""

@@ -125,6 +125,7 @@ struct KvmDevState {
   const int* sw;
   const int* sflag;
   int* sprogress;            // [grid]
+  int svariant;              // the static kernel's inlined operator set (kvm_static_kernel<V>)
   // Stream mode (stream != 0): FIFO queues of reused cells, ready64[q * qcap + (ticket & (qcap - 1))] = (round << 32) |
   // slot with round = ticket / qcap + 1 (0: empty); qcap a power of two above the slots' capacity.
   unsigned long long* ready64;

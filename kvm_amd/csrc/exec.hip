@@ -744,6 +744,13 @@ __device__ bool static_wait(const KvmDevState& S, const int* ent, int cnt, int s
 // worker waits for this task. Version publications keep the dynamic path's CAS (a gap is still reported); no task
 // parks, the plan orders every waiter after its publisher. A wait gives up after timeout_ticks (TIMEOUT) or when any
 // worker reports an error, so every worker exits.
+//
+// V selects the operator bodies inlined into the worker loop (a call costs each task the callee-saved register spills
+// and reloads of a large body, microseconds per task): 0 none, 1 batch-1 decode (one-row GEMV with the deep ring, the
+// GQA-4 attention split), 2 batched decode (the 8-row GEMV, the GQA-4 attention split). One instantiation per set:
+// each body's registers are allocated with only its set's other bodies (two GEMV ring depths in one kernel made both
+// slower). The host picks V from the graph's operators.
+template <int V>
 __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState S) {
   __shared__ __attribute__((aligned(16))) char smem[KVM_LDS_BYTES];
   __shared__ int s_go;
@@ -765,7 +772,12 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
     // A decode GEMV whose weights no task writes requests its first weight steps before waiting (wave 0's share
     // lands before its first poll returns).
     Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
-    if (sf & KVM_SF_PRE) { gemv_prefetch(c, s_rec.desc.op_id); c.pre = 1; }
+    if (sf & KVM_SF_PRE) {
+      const int op = s_rec.desc.op_id;
+      if (op == 134 || op == 301) gemv_prefetch(c, op);
+      else attn_prefetch(c, op);
+      c.pre = 1;
+    }
     if (t < 64) {
       const int k0 = S.swait_off[slot], k1 = S.swait_off[slot + 1];
       const int err0 = ld_relaxed(&S.cnt->err_code);
@@ -800,7 +812,21 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
           S.cnt->err_slot = slot;
       }
     }
-    dispatch(d.op_id, c);
+    KVM_PT(6);
+    // The decode hot path's bodies are inlined here (no call: no callee-saved register spills and reloads per
+    // task); every other operator goes through the dispatcher.
+    const int op = d.op_id;
+    if (V == 0) dispatch(op, c);
+    else {
+      constexpr int GR = V == 1 ? 12 : 8;          // the set's GEMV ring depth
+      const bool rows = op == 301, gv = (op == 134 || rows) && c.pre;
+      const int gm = rows ? c.i(9) : 1, gpro = rows ? c.i(10) : c.i(9);
+      if (op == 306 && c.i(11) == 4 * c.i(12)) attn_part_body<4>(c, true);
+      else if (gv && gv_pre_ring(gm) == GR && gemv_stream_ok(c.buf(0), c.buf(1), c.buf(3), c.buf(4), c.i(8), gm, gpro))
+        gemv_body<GR>(c, gm, gpro, rows ? c.f(11) : c.f(10));
+      else dispatch(op, c);
+    }
+    KVM_PT(7);
     const bool pub_pos = (sf & KVM_SF_PUB) != 0;
     wait_stores();
     __syncthreads();
@@ -809,6 +835,9 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
         KvmTrace& tr = S.trace[slot];
         tr.ver1 = wait_var >= 0 ? ld_relaxed(&S.version[wait_var]) : -1;
         tr.end = wall_clock64();
+#ifdef KVM_GEMM_PROF
+        tr.ver0 = (int)(g_prof[w][6] - tr.start); tr.ver1 = (int)(g_prof[w][7] - tr.start);   // profiling builds only
+#endif
       }
       if (pub_var >= 0) publish(S, slot, pub_var, pub_ver);
       if (pub_pos) st_relaxed(&S.sprogress[w], i - p0 + 1);
@@ -1099,7 +1128,8 @@ KvmExec* kvm_create(const KvmConfig* cfg) {
   // The workers' private segments (callee-saved registers of the operator calls) are backed by scratch for every
   // resident wave; a kernel build whose segment grew to 2,096 bytes per lane stopped before its first task finished,
   // while 1,328 runs. Builds above 2,048 bytes per lane are refused rather than launched.
-  for (const void* k : {(const void*)kvm_exec_kernel, (const void*)kvm_static_kernel}) {
+  for (const void* k : {(const void*)kvm_exec_kernel, (const void*)kvm_static_kernel<0>, (const void*)kvm_static_kernel<1>,
+                        (const void*)kvm_static_kernel<2>}) {
     hipFuncAttributes fa{};
     if (hipFuncGetAttributes(&fa, k) != hipSuccess) { g_err = "hipFuncGetAttributes failed"; return nullptr; }
     if (fa.localSizeBytes > KVM_MAX_PRIVATE_BYTES) {
@@ -1503,7 +1533,8 @@ static double task_cost_us(const MvmTaskDesc& d, const int32_t* a) {
 
 // Static-path flags per task: KVM_SF_PUB, another worker waits for the task; KVM_SF_PRE, a decode GEMV (op 134 / 301)
 // whose weight buffer no task of the graph writes (it appears in no argument slot other than the weights of such
-// GEMVs), so its first weight loads may be issued before its dependencies are met.
+// GEMVs), so its first weight loads may be issued before its dependencies are met, or a decode attention split whose
+// caches appear only as the caches of splits.
 static std::vector<int> static_flags(const KvmExec* ex, const kvms::Plan& P) {
   const int n = (int)ex->tasks.size(), nb = (int)ex->bufs.size();
   std::vector<char> other_use(nb, 0);
@@ -1515,7 +1546,8 @@ static std::vector<int> static_flags(const KvmExec* ex, const kvms::Plan& P) {
     if (sigs[op].empty()) if (const kvmv::OpSig* o = kvmv::find_op(op)) sigs[op] = kvmv::parse_sig(o->sig);
     const int32_t* a = ex->args.data() + d.args_off;
     for (size_t k = 0; k < sigs[op].size() && (int)k < d.args_words; ++k)
-      if (sigs[op][k].type == 0 && a[k] >= 0 && a[k] < nb && !((op == 134 || op == 301) && k == 3)) other_use[a[k]] = 1;
+      if (sigs[op][k].type == 0 && a[k] >= 0 && a[k] < nb && !((op == 134 || op == 301) && k == 3) && !((op == 135 || op == 306) && (k == 1 || k == 2)))
+        other_use[a[k]] = 1;
   }
   std::vector<int> f(n, 0);
   for (int i = 0; i < n; ++i) {
@@ -1525,8 +1557,32 @@ static std::vector<int> static_flags(const KvmExec* ex, const kvms::Plan& P) {
       const int wb = ex->args[d.args_off + 3];
       if (wb >= 0 && wb < nb && !other_use[wb] && !getenv("KVM_NO_PREFETCH")) f[i] |= KVM_SF_PRE;
     }
+    // A decode attention split whose caches only the splits use (each writes its own new row): its first block and
+    // rotation table are staged before the wait.
+    if ((d.op_id == 135 || d.op_id == 306) && d.args_words > 3) {
+      const int kb = ex->args[d.args_off + 1], vb = ex->args[d.args_off + 2];
+      if (kb >= 0 && kb < nb && vb >= 0 && vb < nb && kb != vb && !other_use[kb] && !other_use[vb] && !getenv("KVM_NO_PREFETCH") &&
+          !getenv("KVM_NO_ATTN_PREFETCH"))
+        f[i] |= KVM_SF_PRE;
+    }
   }
   return f;
+}
+
+// The static kernel's inlined operator set for this graph: the one covering more of its decode GEMVs (the GQA-4
+// attention split is in both).
+static int static_variant(const KvmExec* ex) {
+  long long deep = 0, rows8 = 0;
+  for (const MvmTaskDesc& d : ex->tasks) {
+    if (d.op_id == 134) ++deep;
+    else if (d.op_id == 301 && d.args_words > 9) {
+      const int M = ex->args[d.args_off + 9];
+      if (M >= 1 && M <= 4) ++deep;
+      else if (M >= 5 && M <= 8) ++rows8;
+    }
+  }
+  if (getenv("KVM_STATIC_VARIANT")) return atoi(getenv("KVM_STATIC_VARIANT")) % 3;
+  return rows8 > deep ? 2 : deep > 0 ? 1 : 0;
 }
 
 static int plan_static(KvmExec* ex, bool forced) {
@@ -1550,6 +1606,7 @@ static int plan_static(KvmExec* ex, bool forced) {
     return KVM_STATUS_INVALID;
   }
   ex->path = KVM_PATH_STATIC;
+  ex->S.svariant = static_variant(ex);
   return 0;
 }
 
@@ -1649,7 +1706,11 @@ static void launch_graph(const KvmDevState& S, const LaunchArgs& L, int grid, hi
   hipLaunchKernelGGL(kvm_reset_kernel, dim3(std::min(1024, (S.ntasks + 255) / 256 + 1)), dim3(256), 0, st, S, (const int*)L.base);
   if (!static_path) hipLaunchKernelGGL(kvm_seed_kernel, dim3(1), dim3(1024), 0, st, S, L.roots, L.root_cell, L.nfixed, L.nroots, L.fixed_tail);
   if (before_exec) hipEventRecord(before_exec, st);
-  if (static_path) hipLaunchKernelGGL(kvm_static_kernel, dim3(grid), dim3(KVM_THREADS), 0, st, S);
+  if (static_path) {
+    if (S.svariant == 1) hipLaunchKernelGGL(kvm_static_kernel<1>, dim3(grid), dim3(KVM_THREADS), 0, st, S);
+    else if (S.svariant == 2) hipLaunchKernelGGL(kvm_static_kernel<2>, dim3(grid), dim3(KVM_THREADS), 0, st, S);
+    else hipLaunchKernelGGL(kvm_static_kernel<0>, dim3(grid), dim3(KVM_THREADS), 0, st, S);
+  }
   else hipLaunchKernelGGL(kvm_exec_kernel, dim3(grid), dim3(KVM_THREADS), 0, st, S);
   if (after_exec) hipEventRecord(after_exec, st);
 }

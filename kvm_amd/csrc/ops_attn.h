@@ -417,9 +417,64 @@ __device__ __noinline__ void op_matmul_mma_bf16_delta(const Ctx& c) {
     }
   }
 }
+// Geometry of the streaming split: 160 tokens per block, staged in LDS as [token slot][128] bf16 rows, K then V
+// (a block's slot k holds row min(k, nk - 1) of the split), then the block statistics and the rotation table. The
+// P V partials alias the staging after the last block.
+constexpr int ATT_DR = 10, ATT_DB = 4 * KVM_WAVES * ATT_DR, ATT_HD = 128;
+constexpr int ATT_KV_BYTES = ATT_DB * ATT_HD * 2, ATT_RED_OFF = 2 * ATT_KV_BYTES, ATT_ROT_OFF = ATT_RED_OFF + 64 * 4;
+static_assert(ATT_ROT_OFF + 128 * 4 <= KVM_LDS_BYTES && 16 * 8 * ATT_HD * 4 <= 2 * ATT_KV_BYTES, "decode attention LDS map");
+// The split's token range [j0, j0 + nk) of the n = L + 1 tokens (L = lens[b]); false when L is out of range.
+__device__ __forceinline__ bool attn_split(const Ctx& c, int& L, int& j0, int& nk) {
+  const View lens = c.buf(3);
+  const int bb = c.i(7), s = c.i(9), S = c.i(10), Tmax = c.i(14);
+  L = lens.i()[bb];
+  const int n = L + 1;
+  if (L < 0 || n > Tmax) return false;
+  const int chunk = (n + S - 1) / S;
+  j0 = s * chunk;
+  nk = max(0, min(n, j0 + chunk) - j0);
+  return true;
+}
+// The rotation table of position L: sin, then cos, of the 64 angles (threads 0..63).
+__device__ __forceinline__ void attn_rot_table(int L, float theta, LDS float* rot) {
+  if (tid() < 64) { float sn, co; rope_sc_ref(L, tid(), ATT_HD, log((double)theta), sn, co); rot[tid()] = sn; rot[64 + tid()] = co; }
+}
+// Op 135 takes the streaming form for bf16 caches at hd 128 with G in {1, 2, 4, 8}; op 306 always (validated).
+__device__ __forceinline__ bool attn_fast_ok(const Ctx& c, int op) {
+  if (op == 306) return true;
+  const View kc = c.buf(1), vc = c.buf(2);
+  const int H = c.i(11), Hkv = c.i(12), G = Hkv > 0 ? H / Hkv : 0;
+  return kc.dtype == 2 && vc.dtype == 2 && c.i(13) == 128 && (kc.cols % 8) == 0 && (vc.cols % 8) == 0 && (G == 1 || G == 2 || G == 4 || G == 8);
+}
+// Before the dependency wait of a streaming split that will run with c.pre set (all four waves, the task's record in
+// c): its first block's K and V rows go to the staging direct from HBM (loads in flight through the wait) and the
+// rotation table is computed. The cache rows read here are written only by earlier launches, except the split's own
+// new row, which the task itself writes into the staging after these loads have landed. The lengths are written
+// only after the last layer's splits.
+__device__ __noinline__ void attn_prefetch(const Ctx& c, int op) {
+  if (!attn_fast_ok(c, op)) return;
+  int L, j0, nk;
+  if (!attn_split(c, L, j0, nk) || nk == 0) return;
+  const View kc = uniform_view(c.buf(1)), vc = uniform_view(c.buf(2));
+  const int bb = c.i(7), kvh = c.i(8), Hkv = c.i(12), Tmax = c.i(14);
+  const long long row0 = ((long long)bb * Hkv + kvh) * Tmax + j0;
+  const i32x4_t rk = dma_rsrc((const void*)(kc.h() + row0 * kc.cols), (long long)nk * kc.cols * 2);
+  const i32x4_t rv = dma_rsrc((const void*)(vc.h() + row0 * vc.cols), (long long)nk * vc.cols * 2);
+  const int l = lane(), w = wave(), ts = l >> 4, d0 = 8 * (l & 15);
+  LDS uint16_t* Ks = (LDS uint16_t*)c.smem;
+  LDS uint16_t* Vs = Ks + ATT_DB * ATT_HD;
+#pragma unroll
+  for (int i = 0; i < ATT_DR; ++i) {
+    const int slot = w * 4 * ATT_DR + 4 * i, row = min(slot + ts, nk - 1);
+    dma16(rk, (row * kc.cols + d0) * 2, 0, Ks + slot * ATT_HD);
+    dma16(rv, (row * vc.cols + d0) * 2, 0, Vs + slot * ATT_HD);
+  }
+  if (c.i(17) & 1) attn_rot_table(L, c.f(16), (LDS float*)(c.smem + ATT_ROT_OFF));
+}
 // qkn (op 306): the query heads and the new key are RMS-normalised per head first (gamma args 18 / 19, eps arg 20).
+// c.pre: attn_prefetch ran before the wait (block 0 staged, rotation table ready).
 template <int G>
-__device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) {
+__device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn) {
   const View q = uniform_view(c.buf(0)), kc = uniform_view(c.buf(1)), vc = uniform_view(c.buf(2)), lens = uniform_view(c.buf(3));
   const View part = uniform_view(c.buf(4)), kn = uniform_view(c.buf(5)), vn = uniform_view(c.buf(6));
   const int bb = c.i(7), kvh = c.i(8), s = c.i(9), S = c.i(10), H = c.i(11), Hkv = c.i(12), Tmax = c.i(14);
@@ -428,16 +483,19 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) {
 #ifdef KVM_GEMM_PROF
   unsigned long long pt[8] = {(unsigned long long)wall_clock64(), 0, 0, 0, 0, 0, 0, 0};
 #endif
-  constexpr int hd = 128, half = 64;
-  constexpr int DR = 10, DB = 4 * KVM_WAVES * DR;     // rounds of 4 tokens per wave; tokens per block (160)
-  const int L = lens.i()[bb], n = L + 1;
-  if (L < 0 || n > Tmax) { if (tid() == 0) c.fail(KVM_ERR_OP_KVLEN, bb, L); return; }
-  const int chunk = (n + S - 1) / S, j0 = s * chunk, j1 = min(n, j0 + chunk), nk = max(0, j1 - j0);
+  constexpr int hd = ATT_HD, half = 64;
+  constexpr int DR = ATT_DR, DB = ATT_DB;               // rounds of 4 tokens per wave; tokens per block (160)
+  int L, j0, nk;
+  if (!attn_split(c, L, j0, nk)) { if (tid() == 0) c.fail(KVM_ERR_OP_KVLEN, bb, lens.i()[bb]); return; }
+  const int n = L + 1, j1 = j0 + nk;
+  const bool pre = rfl(c.pre) && nk > 0;                // block 0 and the rotation table staged before the wait
   const long long base = ((long long)bb * Hkv + kvh) * Tmax;
   const int l = lane(), w = wave(), cb = l & 15, ts = l >> 4, d0 = 8 * cb;
-  LDS float* red = (LDS float*)c.smem;                  // [4 waves][G] block max / sum
-  LDS float* racc = red + 2 * 4 * 8;                    // [16 token slots][G][hd] P V partials
-  LDS float* rot = racc + 16 * G * hd;                   // [half] sin, [half] cos of this position's angles
+  LDS uint16_t* Ks = (LDS uint16_t*)c.smem;             // [DB][hd] block 0 K rows (prefetched), then V rows
+  LDS uint16_t* Vs = Ks + DB * hd;
+  LDS float* red = (LDS float*)(c.smem + ATT_RED_OFF);  // [4 waves][G] block max / sum
+  LDS float* racc = (LDS float*)c.smem;                 // [16 token slots][G][hd] P V partials, after the last block
+  LDS float* rot = (LDS float*)(c.smem + ATT_ROT_OFF);  // [half] sin, [half] cos of this position's angles
   // query (rotated when flag 1, rounded to bf16 when flag 2), times the score scale. This lane's 8 dimensions and their
   // rotation partners (d -+ 64) are loaded as vectors, every load before any use.
   float qr[G][8], qp[G][8];
@@ -496,7 +554,7 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) {
   }
   // the rotation table (computed while the query loads are in flight)
   if (fl & 1) {
-    if (tid() < half) { float sn, co; rope_sc_ref(L, tid(), hd, log((double)th), sn, co); rot[tid()] = sn; rot[half + tid()] = co; }
+    if (!pre) attn_rot_table(L, th, rot);
     __syncthreads();
   }
 #pragma unroll
@@ -512,8 +570,14 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) {
       }
       qr[g][e] = x * sc;
     }
+  if (pre) {                                            // the staged block has landed (every wave's own loads), for all waves
+    wait_vm_c<0>();
+    __syncthreads();
+  }
   if ((fl & 1) && j0 <= n - 1 && n - 1 < j1) {          // this split holds the new key: store it (rotated) and its value
     const long long row = base + n - 1;
+    const int srow = n - 1 - j0;                         // its staging slot, when staged (block 0, prefetched)
+    const bool stage = pre && srow < DB;
     if (tid() < half) {                                  // wave 0: one lane per rotation pair
       const int i = tid();
       const double sn = rot[i], co = rot[half + i];
@@ -524,9 +588,15 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) {
         k1 = (k1 * rs) * kg.f()[i]; k2 = (k2 * rs) * kg.f()[i + half];
       }
       const double x1 = k1, x2 = k2;
-      kc.st(row * kc.cols + i, (float)(x1 * co - x2 * sn)); kc.st(row * kc.cols + i + half, (float)(x1 * sn + x2 * co));
+      const float r1 = (float)(x1 * co - x2 * sn), r2 = (float)(x1 * sn + x2 * co);
+      kc.st(row * kc.cols + i, r1); kc.st(row * kc.cols + i + half, r2);
+      if (stage) { Ks[srow * hd + i] = f2bf(r1); Ks[srow * hd + i + half] = f2bf(r2); }
     }
-    for (int k = tid(); k < hd; k += KVM_THREADS) vc.st(row * vc.cols + k, vn.at(bb, kvh * hd + k));
+    for (int k = tid(); k < hd; k += KVM_THREADS) {
+      const float v = vn.at(bb, kvh * hd + k);
+      vc.st(row * vc.cols + k, v);
+      if (stage) Vs[srow * hd + k] = f2bf(v);
+    }
   }
 #ifdef KVM_GEMM_PROF
   pt[1] = wall_clock64();
@@ -552,11 +622,20 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) {
   }
   for (int b0 = 0; b0 < nk; b0 += DB) {
     u16x8_t kr[DR], vr[DR];
+    if (pre && b0 == 0) {
 #pragma unroll
-    for (int i = 0; i < DR; ++i) {
-      const long long row = base + j0 + min(b0 + w * 4 * DR + 4 * i + ts, nk - 1);
-      kr[i] = *(const GLOBAL u16x8_t*)(kc.h() + row * kc.cols + d0);
-      vr[i] = *(const GLOBAL u16x8_t*)(vc.h() + row * vc.cols + d0);
+      for (int i = 0; i < DR; ++i) {
+        const int slot = w * 4 * DR + 4 * i + ts;
+        kr[i] = *(const LDS u16x8_t*)(Ks + slot * hd + d0);
+        vr[i] = *(const LDS u16x8_t*)(Vs + slot * hd + d0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < DR; ++i) {
+        const long long row = base + j0 + min(b0 + w * 4 * DR + 4 * i + ts, nk - 1);
+        kr[i] = *(const GLOBAL u16x8_t*)(kc.h() + row * kc.cols + d0);
+        vr[i] = *(const GLOBAL u16x8_t*)(vc.h() + row * vc.cols + d0);
+      }
     }
     float sv[DR][G];
     float mb[G];
@@ -642,6 +721,7 @@ __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) {
   if (tid() == 0) { unsigned long long* o = (unsigned long long*)(part.f() + (((long long)bb * S + s) * H + kvh * G) * part.cols); for (int i = 0; i < 6; ++i) o[i] = pt[i]; o[6] = g_prof[blockIdx.x][6]; }
 #endif
 }
+template <int G> __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) { attn_part_body<G>(c, qkn); }
 __device__ __noinline__ void op_attn_decode_part_any(const Ctx& c) {
   const View kc = c.buf(1), vc = c.buf(2);
   const int H = c.i(11), Hkv = c.i(12), hd = c.i(13), G = H / Hkv;
@@ -663,7 +743,7 @@ __device__ __noinline__ void op_attn_decode_part_qkn(const Ctx& c) {
 
 // Merge of the splits (registry op 136): per head, the split weights e_s = exp(m_s - max m) (live splits only) are
 // computed once into LDS, then each output element is one pass over the splits.
-__device__ __noinline__ void op_attn_decode_merge(const Ctx& c) {
+__device__ __forceinline__ void attn_merge_body(const Ctx& c) {
   View part = c.buf(0), o = c.buf(1); int bb = c.i(2), h0 = c.i(3), h1 = c.i(4), S = c.i(5), H = c.i(6), hd = c.i(7);
   LDS float* w = (LDS float*)c.smem;      // [h1-h0][S] split weights, then [h1-h0] 1/denominator
   LDS float* inv = w + (h1 - h0) * S;
@@ -698,5 +778,7 @@ __device__ __noinline__ void op_attn_decode_merge(const Ctx& c) {
     o.st((long long)bb * o.cols + (h0 + hh) * hd + k, num * inv[hh]);
   }
 }
+
+__device__ __noinline__ void op_attn_decode_merge(const Ctx& c) { attn_merge_body(c); }
 
 }  // namespace kvm

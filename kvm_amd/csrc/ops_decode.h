@@ -372,7 +372,7 @@ __device__ __noinline__ void gemv_prefetch(const Ctx& c, int op) {
   else gemv_prefetch_r<4>(w, n0, n1, K, M, c.smem);
 }
 
-template <int R> __device__ __noinline__ void gemv_stream_r(const Ctx& c, int M_, int pro_, float eps) {
+template <int R> __device__ __forceinline__ void gemv_body(const Ctx& c, int M_, int pro_, float eps) {
   const int M = rfl(M_), pro = rfl(pro_);                                       // function arguments arrive in VGPRs
   const View x = uniform_view(c.buf(0)), x2 = uniform_view(c.buf(1)), g = uniform_view(c.buf(2)), w = uniform_view(c.buf(3));
   const View out = uniform_view(c.buf(4)), res = uniform_view(c.buf(5));
@@ -465,6 +465,7 @@ template <int R> __device__ __noinline__ void gemv_stream_r(const Ctx& c, int M_
   if (tid() == 0 && out.dtype == 0) { unsigned long long* o = (unsigned long long*)(out.f() + n0); for (int i = 0; i < 5; ++i) o[i] = pt[i]; o[5] = g_prof[blockIdx.x][6]; }
 #endif
 }
+template <int R> __device__ __noinline__ void gemv_stream_r(const Ctx& c, int M, int pro, float eps) { gemv_body<R>(c, M, pro, eps); }
 __device__ __noinline__ void gemv_stream(const Ctx& c, int M, int pro, float eps) {
   if (!rfl(c.pre)) gemv_stream_r<GV_R>(c, M, pro, eps);
   else {

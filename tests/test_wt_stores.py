@@ -56,7 +56,8 @@ def test_operators_store_write_through_only(asm):
     dem = _demangle(list(funcs))
     bad = {}
     for name, body in funcs.items():
-        if any(dem[name] == k or dem[name].startswith(k + '(') for k in KERNELS):
+        plain_name = dem[name][5:] if dem[name].startswith('void ') else dem[name]   # templates demangle with their return type
+        if any(plain_name == k or plain_name.startswith(k + '(') or plain_name.startswith(k + '<') for k in KERNELS):
             continue
         plain = [t for t in body if re.match(r'(global|flat|buffer)_store', t) and not re.search(r'\bsc1\b', t)]
         if plain:
@@ -79,8 +80,10 @@ def test_kernel_private_segments_stay_below_the_residency_guard(asm):
     segment per lane; the compiled kernels stay below it (a 2,096-byte build stopped before its first task)."""
     sizes = {}
     for name in ('kvm_exec_kernel', 'kvm_static_kernel'):
-        m = re.search(r'\.amdhsa_kernel\s+\S*' + name + r'\S*\n(.*?)\.end_amdhsa_kernel', asm, re.S)
-        assert m, name
-        f = re.search(r'\.amdhsa_private_segment_fixed_size\s+(\d+)', m.group(1))
-        sizes[name] = int(f.group(1))
+        ms = re.findall(r'\.amdhsa_kernel\s+(\S*' + name + r'\S*)\n(.*?)\.end_amdhsa_kernel', asm, re.S)
+        assert ms, name
+        for sym, body in ms:
+            f = re.search(r'\.amdhsa_private_segment_fixed_size\s+(\d+)', body)
+            sizes[sym] = int(f.group(1))
+    assert len(sizes) == 4                      # the dynamic kernel and the three static instantiations
     assert all(0 < v <= 2048 for v in sizes.values()), sizes

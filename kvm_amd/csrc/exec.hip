@@ -486,6 +486,7 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 134: op_gemv_bf16(c); break;
     case 135: op_attn_decode_part_any(c); break;
     case 306: op_attn_decode_part_qkn(c); break;
+    case 310: op_attn_decode_part_merge(c); break;
     case 308: op_matmul_mma_bf16_delta(c); break;
     case 309: if (!op_norm_bwd_dx_res_fast(c)) op_norm_bwd_dx_res(c); break;
     case 136: op_attn_decode_merge(c); break;
@@ -821,7 +822,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
       constexpr int GR = V == 1 ? 12 : 8;          // the set's GEMV ring depth
       const bool rows = op == 301, gv = (op == 134 || rows) && c.pre;
       const int gm = rows ? c.i(9) : 1, gpro = rows ? c.i(10) : c.i(9);
-      if (op == 306 && c.i(11) == 4 * c.i(12)) attn_part_body<4>(c, true);
+      if ((op == 306 || op == 310) && c.i(11) == 4 * c.i(12)) attn_part_body<4>(c, true, op == 310);
       else if (gv && gv_pre_ring(gm) == GR && gemv_stream_ok(c.buf(0), c.buf(1), c.buf(3), c.buf(4), c.i(8), gm, gpro))
         gemv_body<GR>(c, gm, gpro, rows ? c.f(11) : c.f(10));
       else dispatch(op, c);
@@ -1546,7 +1547,7 @@ static std::vector<int> static_flags(const KvmExec* ex, const kvms::Plan& P) {
     if (sigs[op].empty()) if (const kvmv::OpSig* o = kvmv::find_op(op)) sigs[op] = kvmv::parse_sig(o->sig);
     const int32_t* a = ex->args.data() + d.args_off;
     for (size_t k = 0; k < sigs[op].size() && (int)k < d.args_words; ++k)
-      if (sigs[op][k].type == 0 && a[k] >= 0 && a[k] < nb && !((op == 134 || op == 301) && k == 3) && !((op == 135 || op == 306) && (k == 1 || k == 2)))
+      if (sigs[op][k].type == 0 && a[k] >= 0 && a[k] < nb && !((op == 134 || op == 301) && k == 3) && !((op == 135 || op == 306 || op == 310) && (k == 1 || k == 2)))
         other_use[a[k]] = 1;
   }
   std::vector<int> f(n, 0);
@@ -1559,7 +1560,7 @@ static std::vector<int> static_flags(const KvmExec* ex, const kvms::Plan& P) {
     }
     // A decode attention split whose caches only the splits use (each writes its own new row): its first block and
     // rotation table are staged before the wait.
-    if ((d.op_id == 135 || d.op_id == 306) && d.args_words > 3) {
+    if ((d.op_id == 135 || d.op_id == 306 || d.op_id == 310) && d.args_words > 3) {
       const int kb = ex->args[d.args_off + 1], vb = ex->args[d.args_off + 2];
       if (kb >= 0 && kb < nb && vb >= 0 && vb < nb && kb != vb && !other_use[kb] && !other_use[vb] && !getenv("KVM_NO_PREFETCH") &&
           !getenv("KVM_NO_ATTN_PREFETCH"))
@@ -1572,9 +1573,10 @@ static std::vector<int> static_flags(const KvmExec* ex, const kvms::Plan& P) {
 // The static kernel's inlined operator set for this graph: the one covering more of its decode GEMVs (the GQA-4
 // attention split is in both).
 static int static_variant(const KvmExec* ex) {
-  long long deep = 0, rows8 = 0;
+  long long deep = 0, rows8 = 0, attn4 = 0;
   for (const MvmTaskDesc& d : ex->tasks) {
     if (d.op_id == 134) ++deep;
+    else if ((d.op_id == 306 || d.op_id == 310) && d.args_words > 12 && ex->args[d.args_off + 11] == 4 * ex->args[d.args_off + 12]) ++attn4;
     else if (d.op_id == 301 && d.args_words > 9) {
       const int M = ex->args[d.args_off + 9];
       if (M >= 1 && M <= 4) ++deep;
@@ -1582,7 +1584,7 @@ static int static_variant(const KvmExec* ex) {
     }
   }
   if (getenv("KVM_STATIC_VARIANT")) return atoi(getenv("KVM_STATIC_VARIANT")) % 3;
-  return rows8 > deep ? 2 : deep > 0 ? 1 : 0;
+  return rows8 > deep ? 2 : deep > 0 || attn4 > 0 ? 1 : 0;
 }
 
 static int plan_static(KvmExec* ex, bool forced) {

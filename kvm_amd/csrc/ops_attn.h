@@ -441,7 +441,7 @@ __device__ __forceinline__ void attn_rot_table(int L, float theta, LDS float* ro
 }
 // Op 135 takes the streaming form for bf16 caches at hd 128 with G in {1, 2, 4, 8}; op 306 always (validated).
 __device__ __forceinline__ bool attn_fast_ok(const Ctx& c, int op) {
-  if (op == 306) return true;
+  if (op == 306 || op == 310) return true;
   const View kc = c.buf(1), vc = c.buf(2);
   const int H = c.i(11), Hkv = c.i(12), G = Hkv > 0 ? H / Hkv : 0;
   return kc.dtype == 2 && vc.dtype == 2 && c.i(13) == 128 && (kc.cols % 8) == 0 && (vc.cols % 8) == 0 && (G == 1 || G == 2 || G == 4 || G == 8);
@@ -473,8 +473,67 @@ __device__ __noinline__ void attn_prefetch(const Ctx& c, int op) {
 }
 // qkn (op 306): the query heads and the new key are RMS-normalised per head first (gamma args 18 / 19, eps arg 20).
 // c.pre: attn_prefetch ran before the wait (block 0 staged, rotation table ready).
+__device__ __forceinline__ void attn_merge(const View& part, const View& o, int bb, int h0, int h1, int S, int H, int hd, LDS char* smem);
+// The merge of op 136 for the G query heads h0.. of one kv head at hd 128, latency-bound (a few KB per split):
+// wave w takes heads w, w + 4, ...; lane l owns dimensions 2l, 2l + 1. Each lane requests its two values of 16
+// splits at once (8-byte loads, all in flight), while lanes 0..S-1 hold the splits' (m, l) and the split weights
+// e_s = exp(m_s - max m) over live splits (l > 0) are formed and broadcast from them. Sums in split order, as op 136.
+template <int G> __device__ __forceinline__ void attn_merge_g(const View& part, const View& o, int bb, int h0, int S, int H) {
+  constexpr int hd = ATT_HD, SB = 16;
+  const int l = lane(), cols = part.cols;
+  for (int g = wave(); g < G; g += KVM_WAVES) {
+    const int h = h0 + g;
+    const GLOBAL float* base = part.f() + (((long long)bb * S) * H + h) * cols;
+    const long long step = (long long)H * cols;
+    float M = -INFINITY;
+    for (int s = l; s < S; s += 64) if (base[s * step + hd + 1] > 0.f) M = fmaxf(M, base[s * step + hd]);
+    M = wave_max(M);
+    float den = 0.f, a0 = 0.f, a1 = 0.f;
+    for (int s0 = 0; s0 < S; s0 += 64) {
+      float e = 0.f;
+      if (s0 + l < S) {
+        const float ll = base[(s0 + l) * step + hd + 1];
+        e = ll > 0.f ? __expf(base[(s0 + l) * step + hd] - M) : 0.f;
+        den += e * ll;
+      }
+      for (int s1 = 0; s1 < 64 && s0 + s1 < S; s1 += SB) {
+        typedef float f2v __attribute__((ext_vector_type(2)));
+        f2v v[SB];
+#pragma unroll
+        for (int i = 0; i < SB; ++i) {
+          const int s = min(s0 + s1 + i, S - 1);
+          v[i] = *(const GLOBAL f2v*)(base + s * step + 2 * l);
+        }
+#pragma unroll
+        for (int i = 0; i < SB; ++i) {
+          const float w = __shfl(e, s1 + i, 64);
+          if (s0 + s1 + i < S) { a0 += w * v[i].x; a1 += w * v[i].y; }
+        }
+      }
+    }
+    const float inv = 1.f / wave_sum(den);
+    o.st((long long)bb * o.cols + h * hd + 2 * l, a0 * inv);
+    o.st((long long)bb * o.cols + h * hd + 2 * l + 1, a1 * inv);
+  }
+}
+// Op 310's completion: this split's partials are made agent-visible (write-through stores, waited for) before it counts
+// itself; the split that counts last acquires and merges the kv head's G query heads (op 136), then resets the count.
+template <int G> __device__ __forceinline__ void attn_arrive(const Ctx& c, int bb, int kvh, int S, int H, int Hkv) {
+  const View part = uniform_view(c.buf(4)), o = uniform_view(c.buf(21)), cnt = uniform_view(c.buf(22));
+  LDS int* flag = (LDS int*)(c.smem + ATT_RED_OFF);
+  wait_stores();
+  __syncthreads();
+  if (tid() == 0) *flag = add_relaxed((int*)(cnt.i() + ((long long)bb * Hkv + kvh)), 1);
+  __syncthreads();
+  const int old = *flag;
+  if (old < 0 || old >= S) { if (tid() == 0) c.fail(KVM_ERR_OP_RANGE, bb * Hkv + kvh, old); return; }
+  if (old != S - 1) return;
+  fence_acquire();                                      // the other splits' partials, stored before their counts
+  attn_merge_g<G>(part, o, bb, kvh * G, S, H);
+  if (tid() == 0) st_relaxed((int*)(cnt.i() + ((long long)bb * Hkv + kvh)), 0);
+}
 template <int G>
-__device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn) {
+__device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn, bool merge = false) {
   const View q = uniform_view(c.buf(0)), kc = uniform_view(c.buf(1)), vc = uniform_view(c.buf(2)), lens = uniform_view(c.buf(3));
   const View part = uniform_view(c.buf(4)), kn = uniform_view(c.buf(5)), vn = uniform_view(c.buf(6));
   const int bb = c.i(7), kvh = c.i(8), s = c.i(9), S = c.i(10), H = c.i(11), Hkv = c.i(12), Tmax = c.i(14);
@@ -611,6 +670,7 @@ __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn) {
       const long long r = (((long long)bb * S + s) * H + kvh * G + g) * part.cols;
       stwt32(part.f() + (r + k), k < hd ? 0.f : (k == hd ? ATTN_EMPTY_M : 0.f));
     }
+    if (merge) attn_arrive<G>(c, bb, kvh, S, H, Hkv);
     return;
   }
   float mrun[G], lrun[G], acc[G][8];
@@ -715,13 +775,14 @@ __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn) {
     stwt32(part.f() + (r + k), t);
     if (k == 0) { stwt32(part.f() + (r + hd), mrun[g]); stwt32(part.f() + (r + hd + 1), lrun[g]); }
   }
+  if (merge) attn_arrive<G>(c, bb, kvh, S, H, Hkv);
 #ifdef KVM_GEMM_PROF
   pt[5] = wall_clock64();
   __syncthreads();
   if (tid() == 0) { unsigned long long* o = (unsigned long long*)(part.f() + (((long long)bb * S + s) * H + kvh * G) * part.cols); for (int i = 0; i < 6; ++i) o[i] = pt[i]; o[6] = g_prof[blockIdx.x][6]; }
 #endif
 }
-template <int G> __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn) { attn_part_body<G>(c, qkn); }
+template <int G> __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn, bool merge = false) { attn_part_body<G>(c, qkn, merge); }
 __device__ __noinline__ void op_attn_decode_part_any(const Ctx& c) {
   const View kc = c.buf(1), vc = c.buf(2);
   const int H = c.i(11), Hkv = c.i(12), hd = c.i(13), G = H / Hkv;
@@ -741,11 +802,19 @@ __device__ __noinline__ void op_attn_decode_part_qkn(const Ctx& c) {
   else attn_decode_part_fast<1>(c, true);
 }
 
+// Op 310 (validated as op 306): op 306, then the last split of its kv head merges the head's query heads.
+__device__ __noinline__ void op_attn_decode_part_merge(const Ctx& c) {
+  const int G = c.i(11) / c.i(12);
+  if (G == 4) attn_decode_part_fast<4>(c, true, true);
+  else if (G == 8) attn_decode_part_fast<8>(c, true, true);
+  else if (G == 2) attn_decode_part_fast<2>(c, true, true);
+  else attn_decode_part_fast<1>(c, true, true);
+}
+
 // Merge of the splits (registry op 136): per head, the split weights e_s = exp(m_s - max m) (live splits only) are
 // computed once into LDS, then each output element is one pass over the splits.
-__device__ __forceinline__ void attn_merge_body(const Ctx& c) {
-  View part = c.buf(0), o = c.buf(1); int bb = c.i(2), h0 = c.i(3), h1 = c.i(4), S = c.i(5), H = c.i(6), hd = c.i(7);
-  LDS float* w = (LDS float*)c.smem;      // [h1-h0][S] split weights, then [h1-h0] 1/denominator
+__device__ __forceinline__ void attn_merge(const View& part, const View& o, int bb, int h0, int h1, int S, int H, int hd, LDS char* smem) {
+  LDS float* w = (LDS float*)smem;        // [h1-h0][S] split weights, then [h1-h0] 1/denominator
   LDS float* inv = w + (h1 - h0) * S;
   for (int h = h0 + wave(); h < h1; h += KVM_WAVES) {
     float M = -INFINITY;
@@ -779,6 +848,9 @@ __device__ __forceinline__ void attn_merge_body(const Ctx& c) {
   }
 }
 
+__device__ __forceinline__ void attn_merge_body(const Ctx& c) {
+  attn_merge(c.buf(0), c.buf(1), c.i(2), c.i(3), c.i(4), c.i(5), c.i(6), c.i(7), c.smem);
+}
 __device__ __noinline__ void op_attn_decode_merge(const Ctx& c) { attn_merge_body(c); }
 
 }  // namespace kvm

@@ -41,7 +41,7 @@ static const OpSig* find_op(int id) { for (const OpSig& o : kRegistry) if (o.id 
 static bool implemented(int id) {
   static const int ids[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 32, 33, 34, 35, 36, 37, 38, 39, 40, 41, 42, 43, 44, 45, 46, 47, 48, 49, 50,
                             51, 52, 53, 54, 55, 56, 57, 58, 59, 60, 61, 62, 63, 96, 97, 98, 99, 100, 101, 102, 103, 104, 113, 114, 115,
-                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304, 305, 306, 308, 309};
+                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304, 305, 306, 308, 309, 310};
   for (int i : ids) if (i == id) return true;
   return false;
 }
@@ -105,6 +105,7 @@ static char arg_class(int op, const std::string& n) {
     case 134: return in({"gamma"}) ? 'f' : 'a';
     case 135: return in({"lens"}) ? 'i' : in({"part"}) ? 'f' : 'a';
     case 306: return in({"lens"}) ? 'i' : in({"part", "qgamma", "kgamma"}) ? 'f' : 'a';
+    case 310: return in({"lens", "cnt"}) ? 'i' : in({"part", "qgamma", "kgamma"}) ? 'f' : 'a';
     case 136: return in({"o"}) ? 'a' : 'f';
     case 300: return in({"x", "out"}) ? 'a' : 'f';
     case 301: return in({"gamma"}) ? 'f' : 'a';
@@ -246,6 +247,10 @@ static void extents(int op, Check& k) {
       if (pro == 2) k.need(k.B("x2") != nullptr, "pro 2 needs x2");
       const MvmBuf* w = k.B("w"); if (w) k.need(w->dtype == 2 && w->cols % 8 == 0, "w must be bf16 storage with cols % 8 == 0");
       break; }
+    case 310: { const int S = k.I("S"), H = k.I("H"), Hkv = k.I("Hkv"), b = k.I("b");
+      k.need(Hkv > 0 && b >= 0 && (long long)(H / Hkv) * (S + 1) * 4 <= 128 * 1024, "G*(S+1) too large for one task's LDS");
+      k.ext("o", (long long)b + 1, (long long)H * 128); k.extn("cnt", ((long long)b + 1) * Hkv); }
+      [[fallthrough]];
     case 306: { const MvmBuf* kc = k.B("kc"); const MvmBuf* vc = k.B("vc"); const int H = k.I("H"), Hkv = k.I("Hkv");
       k.need(k.I("hd") == 128 && kc && vc && kc->dtype == 2 && vc->dtype == 2 && Hkv > 0 && H % Hkv == 0 &&
              (H / Hkv == 1 || H / Hkv == 2 || H / Hkv == 4 || H / Hkv == 8) && (k.I("flags") == 1 || k.I("flags") == 3),

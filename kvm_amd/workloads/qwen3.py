@@ -36,6 +36,7 @@ class Qwen3Config:
     splits: int = 0            # attention splits per (sequence, kv head); 0 = auto (256 part tasks)
     tasks_per_phase: int = 256
     fused_norm: bool = True    # q / k head norm inside the attention tasks (op 306) where its shapes allow
+    fused_merge: bool = True   # with fused_norm: the last split of each kv head merges its query heads (op 310)
 
     @staticmethod
     def tiny(batch=1, **kw):
@@ -74,6 +75,10 @@ def build(c: Qwen3Config) -> Workload:
         b.fill('h', B, F, 'bf16')
         b.fill('rstd', B)
     b.fill('logits', B, V)
+    fused_norm = c.fused_norm and hd == 128 and H // Hkv in (1, 2, 4, 8)      # op 306's streaming-path shapes
+    fused_merge = fused_norm and c.fused_merge
+    if fused_merge:
+        b.fill('acnt', B * Hkv, 1, 'i32')       # split counts of op 310 (0 between steps; shared by the layers in turn)
     for l in range(c.layers):
         b.fill(f'ln1.{l}', D, value=1.0)
         b.fill(f'ln2.{l}', D, value=1.0)
@@ -105,7 +110,6 @@ def build(c: Qwen3Config) -> Workload:
         return ts
 
     P = c.tasks_per_phase
-    fused_norm = c.fused_norm and hd == 128 and H // Hkv in (1, 2, 4, 8)      # op 306's streaming-path shapes
     prev = [b.task('embedding_fwd', ids='tok', wte='wte', wpe=None, out='x', r0=0, r1=B, T=1, d=D)]
     last_parts = []
     for l in range(c.layers):
@@ -127,6 +131,9 @@ def build(c: Qwen3Config) -> Workload:
         if fused_norm:   # q / k per-head RMSNorm inside the attention tasks (op 306 = op 300 on q and the new key, then op 135)
             after, op = b.join(tq + tk + tv, B * Hkv * S), 'attn_decode_part_qkn'
             kw.update(qgamma=f'qn.{l}', kgamma=f'kn.{l}', eps=c.eps)
+            if fused_merge:
+                op = 'attn_decode_part_merge'
+                kw.update(o='att', cnt='acnt')
         else:
             hq = b.task('head_rmsnorm', after=tq, x='q', gamma=f'qn.{l}', out='q', r0=0, r1=B, H=H, hd=hd, eps=c.eps)
             hk = b.task('head_rmsnorm', after=tk, x='k', gamma=f'kn.{l}', out='k', r0=0, r1=B, H=Hkv, hd=hd, eps=c.eps)
@@ -136,10 +143,13 @@ def build(c: Qwen3Config) -> Workload:
             parts.append([b.task(op, after=after, b=bb, kvh=kh, s=s, **kw) for kh in range(Hkv) for s in range(S)])
         last_parts = [t for pb in parts for t in pb]
         merges = []
-        for bb in range(B):
-            nm = max(1, H // B)                 # one merge task per head (batch 1): short, parallel
-            for h0, h1 in split(H, nm):
-                merges.append(b.task('attn_decode_merge', after=parts[bb], part='part', o='att', b=bb, h0=h0, h1=h1, S=S, H=H, hd=hd))
+        if fused_merge:
+            merges = b.join(last_parts, P)
+        else:
+            for bb in range(B):
+                nm = max(1, H // B)             # one merge task per head (batch 1): short, parallel
+                for h0, h1 in split(H, nm):
+                    merges.append(b.task('attn_decode_merge', after=parts[bb], part='part', o='att', b=bb, h0=h0, h1=h1, S=S, H=H, hd=hd))
         to = proj(merges, 'att', f'wo.{l}', 'x', D, H * hd, P, res='x')
         if rows_mode:
             oj = b.join(to, 2 * P)

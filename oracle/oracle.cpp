@@ -708,8 +708,7 @@ void op_attn_decode_part_qkn(const Ctx& c) {   // this executor's op 306: op 135
   need(c.i(17) == 1 || c.i(17) == 3, "attn_decode_part_qkn: flags");
   attn_decode_part_impl(c, c.buf(18), c.buf(19), c.fl(20));
 }
-void op_attn_decode_merge(const Ctx& c) {   // ref_extra.py:487-498
-  V part = c.buf(0), o = c.buf(1); int bb = c.i(2), h0 = c.i(3), h1 = c.i(4), S = c.i(5), H = c.i(6), hd = c.i(7);
+static void merge_heads(const V& part, const V& o, int bb, int h0, int h1, int S, int H, int hd) {   // ref_extra.py:487-498
   for (int h = h0; h < h1; ++h) {
     std::vector<long long> live;
     for (int s = 0; s < S; ++s) { long long r = (((long long)bb * S + s) * H + h) * part.cols; if (part.f[r + hd + 1] > 0.0f) live.push_back(r); }
@@ -721,6 +720,27 @@ void op_attn_decode_merge(const Ctx& c) {   // ref_extra.py:487-498
     for (int cc = 0; cc < hd; ++cc) { double a = 0; for (size_t i = 0; i < live.size(); ++i) a += e[i] * part.f[live[i] + cc];
       o.stf((long long)bb * o.cols + h * hd + cc, f32(a / L)); }
   }
+}
+void op_attn_decode_merge(const Ctx& c) {
+  merge_heads(c.buf(0), c.buf(1), c.i(2), c.i(3), c.i(4), c.i(5), c.i(6), c.i(7));
+}
+// This executor's op 310: op 306, then the split that completes last among the S splits of (b, kvh) (counted in cnt,
+// under a lock when the VM runs tasks on several threads) merges that kv head's G query heads as op 136 and resets
+// the count.
+void op_attn_decode_part_merge(const Ctx& c) {
+  op_attn_decode_part_qkn(c);
+  static std::mutex mu;
+  const int bb = c.i(7), kvh = c.i(8), S = c.i(10), H = c.i(11), Hkv = c.i(12), hd = c.i(13);
+  V cnt = c.buf(22);
+  bool last;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    int32_t& k = cnt.i[(long long)bb * Hkv + kvh];
+    if (k < 0 || k >= S) fail("attn_decode_part_merge: split count out of range");
+    last = ++k == S;
+    if (last) k = 0;
+  }
+  if (last) merge_heads(c.buf(4), c.buf(21), bb, kvh * (H / Hkv), (kvh + 1) * (H / Hkv), S, H, hd);
 }
 void op_head_rmsnorm(const Ctx& c) {   // this executor's own op: RMSNorm over each head slice (no reference counterpart)
   V x = c.buf(0), g = c.buf(1), o = c.buf(2); int r0 = c.i(3), r1 = c.i(4), H = c.i(5), hd = c.i(6); float eps = c.fl(7);
@@ -766,7 +786,7 @@ const OpEnt kOps[] = {
   {101, op_softmax_rows_bwd}, {102, op_gather_rows_scaled}, {103, op_scatter_add_rows}, {104, op_row_dot},
   {113, op_round_bf16}, {114, op_matmul_tile_bf16}, {122, op_matmul_mma_bf16}, {134, op_gemv_bf16},
   {135, op_attn_decode_part}, {136, op_attn_decode_merge}, {115, op_adamw_lr}, {116, op_lr_schedule}, {117, op_scale_flat},
-  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce}, {304, op_matmul_mma_bf16_256}, {305, op_adamw_bf16}, {306, op_attn_decode_part_qkn}, {308, op_matmul_mma_bf16_delta},
+  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce}, {304, op_matmul_mma_bf16_256}, {305, op_adamw_bf16}, {306, op_attn_decode_part_qkn}, {310, op_attn_decode_part_merge}, {308, op_matmul_mma_bf16_delta},
 };
 OpFn find_op(int id) { for (const OpEnt& e : kOps) if (e.id == id) return e.fn; return nullptr; }
 

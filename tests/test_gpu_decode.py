@@ -115,3 +115,48 @@ def test_attn_decode_parts_qkn(G, fl, S, qdt):
               for kh in range(Hkv) for s in range(S)]
         b.task('attn_decode_merge', after=ts, part='part', o='o', b=bb, h0=0, h1=H, S=S, H=H, hd=hd)
     _run(b, tol=1e-4)
+
+
+@pytest.mark.parametrize('G,S,path', [(4, 32, 0), (4, 32, 1), (8, 5, 0), (2, 3, 1)])
+def test_attn_decode_part_merge(G, S, path):
+    """Op 310 (op 306 whose last split per kv head merges that head's query heads) against the oracle's op 306 + op
+    136 composition, on the dynamic and the static path (where the GQA-4 body is inlined and its first block staged
+    before the wait); two launches in a row, so the split counts must have returned to 0."""
+    print(f'attn_decode_part_merge G {G} S {S} path {path}', flush=True)
+    B, Hkv, hd = 2, 2, 128
+    H = G * Hkv
+    lens = [700, 301]
+    Tmax = max(lens) + 1
+    b = Builder(53)
+    b.normal('q', B, H * hd, 'f32', scale=1.0)
+    b.normal('kc', B * Hkv * Tmax, hd, 'bf16', scale=1.0)
+    b.normal('vc', B * Hkv * Tmax, hd, 'bf16', scale=1.0)
+    b.normal('kn', B, Hkv * hd, 'f32', scale=1.0)
+    b.normal('vn', B, Hkv * hd, 'f32', scale=1.0)
+    b.normal('qg', 1, hd, 'f32', scale=1.0)
+    b.normal('kg', 1, hd, 'f32', scale=1.0)
+    b.values('lens', lens, B, 1, 'i32')
+    b.fill('part', B * S * H, hd + 2, 'f32')
+    b.fill('o', B, H * hd, 'f32')
+    b.fill('cnt', B * Hkv, 1, 'i32')
+    for bb in range(B):
+        for kh in range(Hkv):
+            for s in range(S):
+                b.task('attn_decode_part_merge', q='q', kc='kc', vc='vc', lens='lens', part='part', knew='kn', vnew='vn', b=bb, kvh=kh,
+                       s=s, S=S, H=H, Hkv=Hkv, hd=hd, Tmax=Tmax, scale=1.0 / hd ** 0.5, theta=1e6, flags=1, qgamma='qg', kgamma='kg',
+                       eps=0.25, o='o', cnt='cnt')
+    w = Workload(b.spec(), b.init_override)
+    lb = bl.load(compiler.compile_spec(w.spec))
+    init = [oracle.materialize(m, w.init_override.get(m['name'])) for m in lb.metadata['buffers']]
+    ref = oracle.run(lb, [x.copy() for x in init])
+    ex = Executor.from_bundle(lb, buffers=init, path=path)
+    for launch in range(2):      # the second launch re-appends the same new row: the same results
+        if launch:
+            ex.relaunch()
+            ex.finish()
+        else:
+            ex.run()
+        assert ex.path() == path
+        bad = compare_run(ex, lb.metadata, ref, tol_f32=1e-4)
+        assert not bad, (launch, bad)
+    ex.close()

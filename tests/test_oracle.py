@@ -192,6 +192,41 @@ def test_attn_decode_part_qkn_is_head_norm_then_part():
     assert not np.array_equal(f[0], p[0])
 
 
+def test_attn_decode_part_merge_is_part_then_merge():
+    """Op 310 equals op 306 followed by op 136 over each kv head's query heads (bitwise: part, caches and the merged
+    output), whichever split completes last, and leaves every split count at 0."""
+    H, Hkv, hd, L, S = 8, 2, 128, 41, 4
+    Tm = L + 2
+    G = H // Hkv
+
+    def graph(fused, order):
+        w = W(43)
+        w.buf('q', 1, H * hd), w.buf('kn', 1, Hkv * hd), w.buf('vn', 1, Hkv * hd), w.buf('qg', hd), w.buf('kg', hd)
+        w.buf('kc', Hkv * Tm, hd), w.buf('vc', Hkv * Tm, hd), w.ints('lens', [L]), w.zeros('part', S * H, hd + 2)
+        w.zeros('att', 1, H * hd), w.ints('cnt', [0] * Hkv)
+        kw = dict(q='q', kc='kc', vc='vc', lens='lens', part='part', knew='kn', vnew='vn', b=0, S=S, H=H, Hkv=Hkv, hd=hd, Tmax=Tm,
+                  scale=1.0 / hd ** 0.5, theta=1e6, flags=1, qgamma='qg', kgamma='kg', eps=1e-6)
+        parts = []
+        for kh, s in order:
+            if fused:
+                parts.append(w.task('attn_decode_part_merge', kvh=kh, s=s, o='att', cnt='cnt', after=parts[-1:], **kw))
+            else:
+                parts.append(w.task('attn_decode_part_qkn', kvh=kh, s=s, after=parts[-1:], **kw))
+        if not fused:
+            for kh in range(Hkv):
+                w.task('attn_decode_merge', after=parts, part='part', o='att', b=0, h0=kh * G, h1=kh * G + G, S=S, H=H, hd=hd)
+        r, b = _run_one(w)
+        return [_get(r, b, n) for n in ('part', 'kc', 'att')] + ([_get(r, b, 'cnt')] if fused else [])
+    fwd = [(kh, s) for kh in range(Hkv) for s in range(S)]
+    ref = graph(False, fwd)
+    for order in (fwd, fwd[::-1], sorted(fwd, key=lambda x: (x[1], -x[0]))):
+        got = graph(True, order)
+        for g, r in zip(got, ref):
+            assert np.array_equal(np.asarray(g).view(np.uint32), np.asarray(r).view(np.uint32))
+        assert (got[3] == 0).all()
+    assert np.abs(ref[2]).sum() > 0
+
+
 def test_rope_inverse_and_head_rmsnorm():
     w = W(6)
     R, H, hd = 6, 2, 8

@@ -249,6 +249,34 @@ template <int RU> __device__ __forceinline__ void gv_rstd(const Ld4& lx, int xc,
     }
   }
 }
+// One row's RMSNorm prologue over all of K in one round trip (the batch-1 decode form): each thread loads its NV
+// 16-byte vectors of x and gamma at once, the sum of squares is reduced over the workgroup (wave sums, then the four
+// in order through `red`), and v = bf16(x * rstd * gamma) is written to vs. K / 4 <= NV * KVM_THREADS.
+template <int NV> __device__ __forceinline__ void gv_stage_rms1(const Ld4& lx, const Ld4& lg, int K, float eps, LDS uint16_t* vs, LDS float* red) {
+  const int q4 = K / 4;
+  f32x4n xv[NV], gv[NV];
+#pragma unroll
+  for (int u = 0; u < NV; ++u) {
+    const int e = min(tid() + u * KVM_THREADS, q4 - 1);
+    xv[u] = lx.get(4 * e);
+    gv[u] = lg.get(4 * e);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < NV; ++u)
+    if (tid() + u * KVM_THREADS < q4) ss += (xv[u].x * xv[u].x + xv[u].y * xv[u].y) + (xv[u].z * xv[u].z + xv[u].w * xv[u].w);
+  ss = wave_sum(ss);
+  if (lane() == 0) red[wave()] = ss;
+  __syncthreads();
+  const float rs = 1.f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)K + eps);
+#pragma unroll
+  for (int u = 0; u < NV; ++u) {
+    const int e = tid() + u * KVM_THREADS;
+    if (e < q4)
+      *(LDS u16x4_t*)(vs + 4 * e) = u16x4_t{f2bf(xv[u].x * rs * gv[u].x), f2bf(xv[u].y * rs * gv[u].y), f2bf(xv[u].z * rs * gv[u].z),
+                                           f2bf(xv[u].w * rs * gv[u].w)};
+  }
+}
 // v = bf16(prologue(x)) for columns [kc, kc + kn) of the M rows: batches of SB vectors per thread, each batch's loads
 // (x, and x2 for the SwiGLU prologue or gamma for the RMSNorm one; nothing for an absent operand) issued first.
 template <int PRO, int SB>
@@ -401,7 +429,11 @@ template <int R> __device__ __forceinline__ void gemv_body(const Ctx& c, int M_,
   const bool arow = (l & 15) < M;
   const LDS uint16_t* va = vs + (arow ? (l & 15) : 0) * VS + 8 * (l >> 4);     // rows >= M read row 0 and are zeroed
   const LDS char* rl = ring + 16 * l;
-  if (pro == 1) gv_rstd<8>(lx, x.cols, M, K, eps, rstd);                        // rstd of each row over all of K
+  // With KC == K the staged v covers all of K and serves every row group. A single row with the RMSNorm prologue
+  // is then staged in one pass (statistics and v from the same loads).
+  const bool once = KC == K, rms1 = once && pro == 1 && M == 1 && K / 4 <= 4 * KVM_THREADS;
+  if (rms1) gv_stage_rms1<4>(lx, lg, K, eps, vs, rstd + 4);
+  else if (pro == 1) gv_rstd<8>(lx, x.cols, M, K, eps, rstd);                   // rstd of each row over all of K
   int cslot = 0;                                                                // ring slot of the next step consumed
   for (int g0 = 0; g0 < nrb; g0 += GV_GRP) {
     const int ng = min(GV_GRP, nrb - g0);
@@ -409,9 +441,11 @@ template <int R> __device__ __forceinline__ void gemv_body(const Ctx& c, int M_,
     for (int kc = 0; kc < K; kc += KC) {
       const int kq = KC / 4, ns = kq / 64;
       __syncthreads();                                                          // rstd ready; the previous chunk's readers are done
-      if (pro == 1) gv_stage<1, GV_SB>(lx, lg, x.cols, 0, M, kc, KC, VS, vs, rstd);      // v = bf16(prologue(x)), this chunk
-      else if (pro == 2) gv_stage<2, GV_SB>(lx, lx2, x.cols, x2.cols, M, kc, KC, VS, vs, rstd);
-      else gv_stage<0, 2 * GV_SB>(lx, lx, x.cols, 0, M, kc, KC, VS, vs, rstd);
+      if (!rms1 && (!once || g0 == 0)) {                                        // v = bf16(prologue(x)), this chunk
+        if (pro == 1) gv_stage<1, GV_SB>(lx, lg, x.cols, 0, M, kc, KC, VS, vs, rstd);
+        else if (pro == 2) gv_stage<2, GV_SB>(lx, lx2, x.cols, x2.cols, M, kc, KC, VS, vs, rstd);
+        else gv_stage<0, 2 * GV_SB>(lx, lx, x.cols, 0, M, kc, KC, VS, vs, rstd);
+      }
       __syncthreads();
 #ifdef KVM_GEMM_PROF
       if (g0 == 0) pt[1] = wall_clock64();

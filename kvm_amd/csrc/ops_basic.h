@@ -496,7 +496,30 @@ __device__ __forceinline__ uint32_t order_key(float x) { uint32_t b = __float_as
 // Row argmax: largest value, lowest index on ties; NaN never wins (all-NaN row -> 0).
 template <class PF, class PI> __device__ int row_argmax(const View& lg, int r, int V, PF redv, PI redi) {
   float bv = -INFINITY; int bi = 0x7FFFFFFF;
-  for (int j = tid(); j < V; j += KVM_THREADS) { float x = lg.at(r, j); if (x > bv || (x == bv && j < bi)) { bv = x; bi = j; } }
+  auto take = [&](float x, int j) { if (x > bv || (x == bv && j < bi)) { bv = x; bi = j; } };
+  int j0 = 0;
+  if (lg.dtype == 0 && (lg.cols % 4) == 0 && V <= lg.cols) {
+    // f32 rows: 16-byte loads, NB of them in flight per thread before any is compared (a scalar load per step
+    // serialises a 150k-wide row on load latency). The tie rule makes the visiting order irrelevant.
+    constexpr int NB = 16;
+    const GLOBAL f32x4n* row = (const GLOBAL f32x4n*)(lg.f() + (long long)r * lg.cols);
+    const int nq = V / 4;
+    for (int q = tid(); q < nq; q += NB * KVM_THREADS) {
+      f32x4n v[NB];
+#pragma unroll
+      for (int u = 0; u < NB; ++u) v[u] = row[min(q + u * KVM_THREADS, nq - 1)];
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        const int qq = q + u * KVM_THREADS;
+        if (qq < nq) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) take(v[u][e], 4 * qq + e);
+        }
+      }
+    }
+    j0 = nq * 4;
+  }
+  for (int j = j0 + tid(); j < V; j += KVM_THREADS) take(lg.at(r, j), j);
   for (int o = 32; o > 0; o >>= 1) {
     float v2 = __shfl_xor(bv, o, 64); int i2 = __shfl_xor(bi, o, 64);
     if (v2 > bv || (v2 == bv && i2 < bi)) { bv = v2; bi = i2; }

@@ -181,9 +181,10 @@ def test_adamw_bf16_shadow(sh_dt):
     _run(b)
 
 
-@pytest.mark.parametrize('tdt,odt,d,pos', [('f32', 'bf16', 768, True), ('f32', 'bf16', 256, False), ('f32', 'f32', 1024, True)])
+@pytest.mark.parametrize('tdt,odt,d,pos', [('f32', 'bf16', 768, True), ('f32', 'bf16', 256, False), ('f32', 'f32', 1024, True),
+                                            ('f32', 'f32', 4096, False), ('f32', 'bf16', 4104, True)])
 def test_embedding_fwd_rows(tdt, odt, d, pos):
-    """Op 32 (streaming form): token rows of wte (+ the position row), ragged row ranges, one and two vectors per lane."""
+    """Op 32 (streaming form): token rows of wte (+ the position row), ragged row ranges, one and two vectors per lane, and rows wider than 2048 (flat form)."""
     print(f'embedding_fwd table {tdt} out {odt} d {d} pos {pos}', flush=True)
     b = Builder(43)
     V, T, N = 997, 64, 203
@@ -236,3 +237,43 @@ def test_embedding_bwd_id_scan(acc):
     for v0, v1 in ((0, 3), (3, 77)):
         b.task('embedding_bwd', ids=None, dout='dout', dtab='dpos', N=N, mod=T, v0=v0, v1=v1, d=d, acc=acc)
     _run(b)
+
+
+def test_argmax_rows():
+    """Op 58 over decode-width rows: lowest index among equal maxima, NaN never wins (all-NaN and all -inf rows give 0),
+    V below the row width and not a multiple of 4."""
+    print('argmax rows', flush=True)
+    V, C, R = 151933, 151936, 7
+    rng = np.random.default_rng(5)
+    lg = rng.standard_normal((R, C)).astype(np.float32)
+    lg[0, C - 1] = 100.0                         # beyond V: ignored
+    lg[1, [5, 100000, 151932]] = 50.0            # ties: the lowest index wins
+    lg[2, :] = np.nan
+    lg[3, :] = -np.inf
+    lg[4, ::3] = np.nan
+    lg[4, 77777] = 9.0
+    lg[5, 151930:] = 60.0                        # the maximum in the scalar tail (151932 is V - 1)
+    lg[6, :] = 1.0                               # all equal
+    want = [None, 5, 0, 0, 77777, 151930, 0]
+    for dt in ('f32',):
+        b = Builder(44)
+        b.fill('lg', R, C, dt)
+        b.fill('tok', R, 1, 'i32')
+        b.fill('tok2', R, 1, 'i32')
+        for r in range(R):
+            b.task('argmax', logits='lg', out='tok', r0=r, r1=r + 1, V=V)
+        b.task('argmax', logits='lg', out='tok2', r0=0, r1=R, V=V)     # several rows in one task
+        w = Workload(b.spec(), b.init_override)
+        lb = bl.load(compiler.compile_spec(w.spec))
+        init = [oracle.materialize(m, w.init_override.get(m['name'])) for m in lb.metadata['buffers']]
+        ex = Executor.from_bundle(lb, buffers=init)
+        ex.write('lg', lg)
+        ex.run()
+        got, got2 = ex.read('tok').reshape(-1), ex.read('tok2').reshape(-1)
+        ex.close()
+        assert (got == got2).all(), (got, got2)
+        ref = lg
+        for r in range(R):
+            row = ref[r, :V]
+            exp = want[r] if want[r] is not None else int(np.argmax(np.where(np.isnan(row), -np.inf, row)))
+            assert got[r] == exp, (dt, r, got[r], exp)

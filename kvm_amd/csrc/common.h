@@ -31,12 +31,14 @@ enum KvmErr {
   KVM_ERR_OP_TOKEN = 1005, KVM_ERR_OP_KVLEN = 1006,
 };
 
-// Successor edges as uploaded to the device: the task index plus a bit set when the successor has exactly one
-// predecessor and no version wait (it is released by that predecessor without a counter).
+// Successor edges as uploaded to the device: the task index plus flag bits. KVM_EDGE_NOWAIT: the successor has no
+// version wait (the predecessor whose decrement reaches zero enqueues it without reading its descriptor);
+// KVM_EDGE_DIRECT: also exactly one predecessor (released by that predecessor without a counter).
 #define KVM_EDGE_DIRECT (1 << 30)
+#define KVM_EDGE_NOWAIT (1 << 29)
 #define KVM_SF_PUB 1             // static path, per task: another worker waits for this task's program position
 #define KVM_SF_PRE 2             // static path, per task: input-independent loads may be issued before the wait
-#define KVM_EDGE_INDEX (KVM_EDGE_DIRECT - 1)
+#define KVM_EDGE_INDEX (KVM_EDGE_NOWAIT - 1)
 
 struct KvmCounters {
   int err_code, err_slot, err_a, err_b;
@@ -97,7 +99,7 @@ struct KvmRec;
 struct KvmDevState {
   const MvmTaskDesc* tasks;   // [ntasks]
   const KvmRec* recs;         // [ntasks] dispatch records (descriptor, argument words, buffer views)
-  const int32_t* succ;        // [nedges] global task indices (| KVM_EDGE_DIRECT)
+  const int32_t* succ;        // [nedges] global task indices (| KVM_EDGE_NOWAIT, KVM_EDGE_DIRECT)
   int* indeg;                 // [ntasks] remaining predecessors
   int* ready;                 // ready cells: queue qi's i-th released task at ready[qoff[qi] + i], -1 until then
   KvmQueue* queues;           // [nq * nb]
@@ -221,14 +223,21 @@ struct View {
 // the argument words and, at every buffer argument's position, that buffer's view. A worker copies it to LDS with one
 // parallel 16-byte load per thread instead of three dependent fetches (descriptor, then arguments, then the buffer
 // table entries they name).
+// The first KVM_REC_SUCC successor edges (device form, flag bits included) ride in the record, so the worker that
+// completes the task signals them without a dependent load of the successor list (nsucc_rec of them; the rest, and
+// all of them when nsucc_rec is 0, are read from the successor array).
+#define KVM_REC_SUCC 64
 struct KvmRec {
   MvmTaskDesc desc;
   int32_t args[KVM_MAX_ARGS];
   View views[KVM_MAX_ARGS];
-  int32_t pad[8];
+  int32_t succ[KVM_REC_SUCC];
+  int32_t nsucc_rec;
+  int32_t pad[7];
 };
-static_assert(sizeof(View) == 24 && sizeof(KvmRec) == 768, "record layout");
+static_assert(sizeof(View) == 24 && sizeof(KvmRec) == 1024, "record layout");
 #define KVM_REC_VEC (int)(sizeof(KvmRec) / 16)
+#define KVM_REC_VEC_OPS (int)(offsetof(KvmRec, succ) / 16)   // 16-byte pieces before the successors (all an operator reads)
 
 // Byte offsets inside the pinned staging block of stream mode (host and device compute them alike).
 struct KvmWinLayout {

@@ -577,9 +577,11 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
     // orders that before wave 0 signals successors. No release fence, so no L2 write-back per task.
     wait_stores();
     __syncthreads();
-    // Completion. The task's stores are agent-visible (above). Edges carry a host-computed bit: KVM_EDGE_DIRECT means
-    // the successor has this task as its only predecessor and no version wait, so it is released with no counter
-    // and no descriptor read. Other successors count down with a relaxed atomic; the decrement that reaches zero
+    // Completion. The task's stores are agent-visible (above). The first successor edges come from the record (in
+    // LDS since dispatch), the rest from the successor array. Edges carry host-computed bits: KVM_EDGE_DIRECT means
+    // the successor has this task as its only predecessor and no version wait, so it is released with no counter;
+    // KVM_EDGE_NOWAIT that it has no version wait, so the decrement that reaches zero enqueues it with no descriptor
+    // read. Other successors count down with a relaxed atomic; the decrement that reaches zero
     // acquires (fence) before releasing the task. Released tasks are enqueued in batches: per wave and per queue one
     // tail reservation (issued by lanes 0..nq-1 in parallel) and one relaxed cell store per task.
     const int nsucc = s_desc.succ_cnt;
@@ -599,14 +601,14 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
         const int k = base + l;
         int s = -1; bool direct = false;
         if (k < nsucc) {
-          const int e = S.succ[s_desc.succ_off + k];
+          const int e = k < s_rec.nsucc_rec ? s_rec.succ[k] : S.succ[s_desc.succ_off + k];
           s = e & KVM_EDGE_INDEX;
           if (e & KVM_EDGE_DIRECT) direct = true;
           else if (add_relaxed(&S.indeg[s], -1) == 1) {
             // Every predecessor made its stores agent-visible before its decrement, and the task that dequeues the
             // successor acquires (L1 / L2 invalidate) before reading them, so the plain enqueue needs no fence here;
             // the versioned path keeps its acquire-release.
-            if (S.tasks[s].wait_var < 0) direct = true;
+            if (e & KVM_EDGE_NOWAIT) direct = true;
             else { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "agent"); release(S, s); }
           }
         }
@@ -758,7 +760,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
   __shared__ __attribute__((aligned(16))) KvmRec s_recs[2];
   const int t = threadIdx.x, w = blockIdx.x;
   const int p0 = S.sprog_off[w], p1 = S.sprog_off[w + 1];
-  if (p0 < p1 && t < KVM_REC_VEC) ((LDS u32x4_t*)&s_recs[0])[t] = ((const u32x4_t*)(S.recs + S.sprog[p0]))[t];
+  if (p0 < p1 && t < KVM_REC_VEC_OPS) ((LDS u32x4_t*)&s_recs[0])[t] = ((const u32x4_t*)(S.recs + S.sprog[p0]))[t];
   int next = p0 < p1 ? S.sprog[p0] : -1;
   __syncthreads();
   for (int i = p0; i < p1; ++i) {
@@ -767,7 +769,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
     // Records depend on nothing: wave 1 requests the next task's into the other buffer (direct to LDS) now; its
     // end-of-task store wait covers that load too.
     next = i + 1 < p1 ? S.sprog[i + 1] : -1;
-    if (wave() == 1 && next >= 0 && lane() < KVM_REC_VEC)
+    if (wave() == 1 && next >= 0 && lane() < KVM_REC_VEC_OPS)
       dma16(dma_rsrc(S.recs + next, sizeof(KvmRec)), 16 * lane(), 0, (const LDS void*)&s_recs[(i + 1 - p0) & 1]);
     const int sf = S.sflag[slot];
     // A decode GEMV whose weights no task writes requests its first weight steps before waiting (wave 0's share
@@ -978,6 +980,9 @@ static const unsigned* op_buf_mask() {
   return m;
 }
 // A task's dispatch record: descriptor, argument words and the views of its buffer arguments.
+static int32_t edge_flags(const MvmTaskDesc& d) {
+  return d.wait_var < 0 ? (KVM_EDGE_NOWAIT | (d.indegree == 1 ? KVM_EDGE_DIRECT : 0)) : 0;
+}
 static void make_rec(const MvmTaskDesc& d, const int32_t* a, const std::vector<MvmBuf>& table, KvmRec& r) {
   std::memset(&r, 0, sizeof(r));
   r.desc = d;
@@ -997,9 +1002,14 @@ static void plan_graph(const std::vector<MvmTaskDesc>& tasks, const std::vector<
   const int n = (int)tasks.size();
   g.n = n;
   g.succ_dev = succ;
-  for (auto& e : g.succ_dev) if (tasks[e].indegree == 1 && tasks[e].wait_var < 0) e |= KVM_EDGE_DIRECT;
+  for (auto& e : g.succ_dev) e |= edge_flags(tasks[e]);
   g.recs.assign(n, KvmRec{});
-  for (int i = 0; i < n; ++i) make_rec(tasks[i], args.data() + tasks[i].args_off, table, g.recs[i]);
+  for (int i = 0; i < n; ++i) {
+    KvmRec& r = g.recs[i];
+    make_rec(tasks[i], args.data() + tasks[i].args_off, table, r);
+    r.nsucc_rec = std::min(tasks[i].succ_cnt, KVM_REC_SUCC);
+    for (int k = 0; k < r.nsucc_rec; ++k) r.succ[k] = g.succ_dev[tasks[i].succ_off + k];
+  }
   g.nq = one_group ? 1 : std::max(1, std::min(KVM_MAX_QUEUES, grid));
   g.qcap = (n + g.nq - 1) / g.nq;
   // Priority buckets: one per distinct priority in the graph, bucket 0 the highest. A graph with one priority and no
@@ -1365,7 +1375,7 @@ static long long stream_stage(KvmExec* ex, const MvmTaskDesc* tasks, int n, cons
   }
   for (int e = 0; e < ne; ++e) {
     const int l = succ[e];
-    sd[e] = (base + l) | ((tasks[l].indegree == 1 && tasks[l].wait_var < 0) ? KVM_EDGE_DIRECT : 0);
+    sd[e] = (base + l) | edge_flags(tasks[l]);
   }
   m.seq = (int)seq; m.ntasks = n; m.nedges = ne; m.nroots = nroots;
   for (int q = 0; q < KVM_MAX_QUEUES; ++q) m.qn[q] = qn[q];

@@ -27,7 +27,11 @@ def test_train_and_serve_demo_matches_the_serial_replay(tmp_path):
     adm = {a['name']: a for a in s['admissions']}
     for k in range(1, 4):
         assert adm[f'serve{k}']['versions_at_done'] == {'w': k}
-        assert adm[f'train{k}']['done_us'] <= adm[f'serve{k}']['submitted_us']
+        # serve k is admitted once train k has published w = k, which can precede the runner's sight of train k's
+        # completion mark; train k + 1 waits for serve k to complete
+        assert adm[f'train{k}']['submitted_us'] <= adm[f'serve{k}']['submitted_us']
+        if k > 1:
+            assert adm[f'serve{k - 1}']['done_us'] <= adm[f'train{k}']['submitted_us']
     assert adm['train2']['how'].startswith('previous bundle') and 'shifted' in adm['train2']['how']
     ref = mf.replay(root)
     for name in ('W', 'Y1', 'Y2', 'Y3'):

@@ -165,6 +165,8 @@ class GPTBuilder:
         self.dep = None
         self.bf = c.dtype == 'bf16'
         self.act = 'bf16' if self.bf else 'f32'
+        if self.bf:
+            self.READ_JOIN_OVER = 1 << 30
         self.params = []      # (master, grad, m, v, shadow or None, wd)
         self.joins = {}       # predecessor set -> join task
         self.bjoins = {}      # buffer -> (write generation, join task over all its writers)
@@ -201,11 +203,11 @@ class GPTBuilder:
     # ---- tasks with data dependencies
     # A task with more predecessors than JOIN_OVER waits on a shared noop join of exactly those instead (edges stay
     # linear). A read depending on more writers than READ_JOIN_OVER waits on the whole buffer's completion join (a
-    # barrier over every sequence): off by default, since the exact joins let sequences run ahead of each other.
-    # GPT-162M measured: joins over 24 with no buffer joins 10.22-10.25 ms; 48 / 16 (the former setting) 10.42;
-    # joins over 8 or 16 12.3-12.6 (join tasks on the critical path); over 32 10.29.
+    # barrier over every sequence). Measured on one MI355X: GPT-162M (bf16) 10.22-10.25 ms with joins over 24 and no
+    # buffer joins, 10.42 with 48 / 16, 12.3-12.6 with joins over 8 or 16 (join tasks on the critical path);
+    # GPT-355M (f32) 232.6 ms with buffer joins over 16, 266-280 without. The bf16 graphs take no buffer joins.
     JOIN_OVER = 24
-    READ_JOIN_OVER = 1 << 30
+    READ_JOIN_OVER = 16
 
     def buffer_join(self, name):
         g = self.dep.gen.get(name, 0)
@@ -236,6 +238,7 @@ class GPTBuilder:
     TILES_256 = 256    # bf16 GEMMs with at least this many 256x256 output tiles use them (op 304)
     TILES_ALONE = 128  # a GEMM running alone with fewer 128x256 tiles than this uses 128x128 tiles
     TILES_MMA = 16     # else at least this many 128x256 tiles: op 122; else 128x128 tiles (op 114), more of them
+    F32_TILES_128 = 64   # f32 GEMMs with at least this many 128x128 output tiles use them (op 34), else 64x64 tiles
 
     def gemm(self, A, B, out, M, N, K, flags=0, bias=None, res=None, pre=None, alpha=1.0, alone=False):
         """C = alpha * op(A) op(B) (+ epilogue), tiled; returns the task ids. `alone`: nothing else runs beside this
@@ -250,7 +253,7 @@ class GPTBuilder:
             op, TM, TN, fl = 'matmul_mma_bf16', 128, 256, flags
         elif bf:   # fewer than 256 tiles of 128x256: 128x128 tiles keep more of the chip busy
             op, TM, TN, fl = 'matmul_tile_bf16', 128, 128, flags | 32
-        elif M >= 128 and N >= 128:
+        elif M >= 128 and N >= 128 and -(-M // 128) * -(-N // 128) >= self.F32_TILES_128:
             op, TM, TN, fl = 'matmul_tile', 128, 128, flags | 32
         else:
             op, TM, TN, fl = 'matmul_tile', 64, 64, flags

@@ -60,3 +60,32 @@ def test_relaunch_is_repeatable():
     for k, v in first.items():
         assert np.array_equal(ex.read(k), v), k
     ex.close()
+
+
+@pytest.mark.parametrize('path', [0, 1])
+def test_wide_fanout_and_fanin(path):
+    """A root with 200 successors (the first 64 edges travel in the dispatch record, the rest come from the successor
+    array), half of them also waiting on the version the root publishes (no no-wait edge bit), a task joining all
+    200, and 100 more after it: every task runs once, after its predecessors, on both paths."""
+    from kvm_amd import compiler
+    from kvm_amd.workloads import Builder
+    print(f'wide fan-out / fan-in, path {path}', flush=True)
+    b = Builder(7)
+    n = 200
+    b.fill('c', 1 + n + 1 + 100, 1, 'i32')
+    b.variables.append('v')
+    root = b.task('counter_inc', publishes='v', x='c', i0=0, i1=1, delta=1)
+    mids = [b.task('counter_inc', after=[root], reads=[{'var': 'v', 'policy': 'exact', 'version': 1}] if i % 2 else None,
+                   x='c', i0=1 + i, i1=2 + i, delta=i + 1) for i in range(n)]
+    last = b.task('counter_inc', after=mids, x='c', i0=n + 1, i1=n + 2, delta=5)
+    for i in range(100):
+        b.task('counter_inc', after=[last], x='c', i0=n + 2 + i, i1=n + 3 + i, delta=2)
+    lb = bl.load(compiler.compile_spec(b.spec()))
+    ex = Executor.from_bundle(lb, path=path)
+    res = ex.run()
+    assert res['done'] == res['admitted'] == lb.ntasks
+    check_schedule(ex, lb)
+    got = ex.read('c').reshape(-1)
+    want = np.array([1] + [i + 1 for i in range(n)] + [5] + [2] * 100, np.int32)
+    assert (got == want).all()
+    ex.close()

@@ -503,8 +503,11 @@ __device__ void dispatch(int op, const Ctx& c) {
 __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S) {
   __shared__ __attribute__((aligned(16))) char smem[KVM_LDS_BYTES];
   __shared__ int s_slot;
-  __shared__ __attribute__((aligned(16))) KvmRec s_rec;
-  MvmTaskDesc& s_desc = s_rec.desc;
+  // Two record buffers, alternating per task: wave 0 writes the next task's record while the other waves may still
+  // read the finished task's successor edges.
+  __shared__ __attribute__((aligned(16))) KvmRec s_recs[2];
+  static_assert(KVM_REC_VEC <= 64, "one record piece per lane of wave 0");
+  int cur = 0;
   const int t = threadIdx.x;
   int ndone = 0;              // tasks this worker finished (thread 0's count, stored after each task)
   long long held = -1;        // stream mode: thread 0's ticket, kept while it admits windows
@@ -512,6 +515,8 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
   unsigned est = 0;
   unsigned long long t_start = 0;
   for (;;) {
+    KvmRec& s_rec = s_recs[cur];
+    MvmTaskDesc& s_desc = s_rec.desc;
     if (S.stream) {
       if (t == 0) s_slot = stream_next(S, held);
       __syncthreads();
@@ -526,30 +531,41 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
         const int slot = pop_prio(S);
         if (t == 0) s_slot = ld_relaxed(&S.cnt->err_code) != 0 ? -1 : slot;
       }
-    } else if (t == 0) {
+    } else if (wave() == 0) {
+      // FIFO mode: wave 0 takes the ticket (lane 0), polls the cell with every lane (one broadcast load), and pulls
+      // the task's record into LDS itself (one 16-byte piece per lane), so one barrier hands the task to the block.
       const int q = blockIdx.x % S.nq;
-      unsigned ticket = add_relaxed(&S.queues[q].head, 1u);
+      unsigned ticket = 0;
+      if (t == 0) ticket = add_relaxed(&S.queues[q].head, 1u);
+      ticket = __builtin_amdgcn_readfirstlane(ticket);
       int slot = -1;
       if (ticket < (unsigned)S.qcount[q]) {
         unsigned long long since = wall_clock64();
         int seen = -1, err = 0;
         for (unsigned polls = 0;; ++polls) {
-          slot = ld_relaxed(&S.ready[q * S.qcap + ticket]);   // the cell and the error word: two loads in flight at once
-          err = ld_relaxed(&S.cnt->err_code);
+          slot = __builtin_amdgcn_readfirstlane(ld_relaxed(&S.ready[q * S.qcap + ticket]));   // cell and error word in flight together
+          err = __builtin_amdgcn_readfirstlane(ld_relaxed(&S.cnt->err_code));
           if (slot >= 0 || err != 0) break;
           __builtin_amdgcn_s_sleep(1);
-          if ((polls & 4095) == 4095 && stalled(S, since, seen, (int)ticket)) break;
+          if ((polls & 4095) == 4095) {
+            int st = 0;
+            if (t == 0) st = stalled(S, since, seen, (int)ticket);
+            if (__builtin_amdgcn_readfirstlane(st)) break;
+          }
         }
         if (slot >= 0) fence_acquire();   // the enqueuer's release: predecessors' data is visible from here on
         if (err != 0) slot = -1;
       }
-      s_slot = slot;
+      if (slot >= 0 && t < KVM_REC_VEC) ((LDS u32x4_t*)&s_rec)[t] = ((const u32x4_t*)(S.recs + slot))[t];
+      if (t == 0) s_slot = slot;
     }
     __syncthreads();
     const int slot = s_slot;
     if (slot < 0) break;
-    if (t < KVM_REC_VEC) ((LDS u32x4_t*)&s_rec)[t] = ((const u32x4_t*)(S.recs + slot))[t];   // the whole record, one load per thread
-    __syncthreads();
+    if (S.stream || S.ncls || S.tq) {   // the other pop paths hand over only the slot: the record is loaded here
+      if (t < KVM_REC_VEC) ((LDS u32x4_t*)&s_rec)[t] = ((const u32x4_t*)(S.recs + slot))[t];   // the whole record, one load per thread
+      __syncthreads();
+    }
     const int op = s_desc.op_id;
     if (t == 0 && S.trace_on) {
       KvmTrace& tr = S.trace[slot];
@@ -568,7 +584,6 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
           S.cnt->err_slot = slot;
       }
     }
-    __syncthreads();
     Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
     KVM_PT(6);
     dispatch(op, c);
@@ -673,6 +688,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
         if (add_acqrel(&S.win_left[w], -1) == 1) st_sys64(&S.hctl->done_mark[w], (long long)ld_relaxed(&S.win_seq[w]) + 1);
       }
     }
+    cur ^= 1;
   }
 }
 

@@ -500,6 +500,164 @@ __device__ void dispatch(int op, const Ctx& c) {
   }
 }
 
+// Static-path wait on `cnt` (worker, need) pairs at ent, by the 64 lanes of one wave: each lane takes up to four
+// entries per round of 256 and polls them together (their loads in flight at once), entries of the worker itself
+// (program order) and set references (worker < 0) skipped. Gives up on an error anywhere or after timeout_ticks
+// (TIMEOUT, first error wins). Returns true when it gave up (uniform across the wave).
+__device__ bool static_wait(const KvmDevState& S, const int* ent, int cnt, int self, int slot) {
+  const int l = lane();
+  bool bad = false;
+  for (int j0 = 0; j0 < cnt && !bad; j0 += 256) {
+    int ww[4], need[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = j0 + l + 64 * u;
+      ww[u] = j < cnt ? ent[2 * j] : -1;
+      need[u] = j < cnt ? ent[2 * j + 1] : 0;
+      if (ww[u] == self) ww[u] = -1;
+    }
+    const unsigned long long since = wall_clock64();
+    for (unsigned polls = 0;; ++polls) {
+      int have[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) have[u] = ww[u] >= 0 ? ld_relaxed(&S.sprogress[ww[u]]) : 0x7fffffff;
+      bool mine = true;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) mine = mine && have[u] >= need[u];
+      if (__ballot(!mine) == 0ull) break;
+      if (ld_relaxed(&S.cnt->err_code) != 0) { bad = true; break; }
+      __builtin_amdgcn_s_sleep(1);
+      if ((polls & 1023) == 1023 && wall_clock64() - since > S.timeout_ticks) {
+        int z = 0;
+        if (l == 0 && __hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_TIMEOUT, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+          S.cnt->err_slot = slot; S.cnt->err_a = ww[0]; S.cnt->err_b = need[0];
+        }
+        bad = true;
+        break;
+      }
+    }
+  }
+  return bad;
+}
+
+// The static path: worker w runs its program (the host plan) in order. Before a task, wave 0 waits for its cross-worker
+// dependencies (lane k polls wait k: progress[worker] >= need) and acquires; after it, every wave waits for its own
+// write-through stores and the barrier orders them before thread 0 publishes the program position, when another
+// worker waits for this task. Version publications keep the dynamic path's CAS (a gap is still reported); no task
+// parks, the plan orders every waiter after its publisher. A wait gives up after timeout_ticks (TIMEOUT) or when any
+// worker reports an error, so every worker exits.
+//
+// V selects the operator bodies inlined into the worker loop (a call costs each task the callee-saved register spills
+// and reloads of a large body, microseconds per task): 0 none, 1 batch-1 decode (one-row GEMV with the deep ring, the
+// GQA-4 attention split), 2 batched decode (the 8-row GEMV, the GQA-4 attention split). One instantiation per set:
+// each body's registers are allocated with only its set's other bodies (two GEMV ring depths in one kernel made both
+// slower). The host picks V from the graph's operators.
+template <int V>
+__global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState S) {
+  __shared__ __attribute__((aligned(16))) char smem[KVM_LDS_BYTES];
+  __shared__ int s_go;
+  __shared__ __attribute__((aligned(16))) KvmRec s_recs[2];
+  const int t = threadIdx.x, w = blockIdx.x;
+  const int p0 = S.sprog_off[w], p1 = S.sprog_off[w + 1];
+  if (p0 < p1 && t < KVM_REC_VEC_OPS) ((LDS u32x4_t*)&s_recs[0])[t] = ((const u32x4_t*)(S.recs + S.sprog[p0]))[t];
+  int next = p0 < p1 ? S.sprog[p0] : -1;
+  __syncthreads();
+  for (int i = p0; i < p1; ++i) {
+    const int slot = next;
+    KvmRec& s_rec = s_recs[(i - p0) & 1];
+    // Records depend on nothing: wave 1 requests the next task's into the other buffer (direct to LDS) now; its
+    // end-of-task store wait covers that load too.
+    next = i + 1 < p1 ? S.sprog[i + 1] : -1;
+    if (wave() == 1 && next >= 0 && lane() < KVM_REC_VEC_OPS)
+      dma16(dma_rsrc(S.recs + next, sizeof(KvmRec)), 16 * lane(), 0, (const LDS void*)&s_recs[(i + 1 - p0) & 1]);
+    const int sf = S.sflag[slot];
+    // A decode GEMV whose weights no task writes requests its first weight steps before waiting (wave 0's share
+    // lands before its first poll returns).
+    Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
+    if (sf & KVM_SF_PRE) {
+      const int op = s_rec.desc.op_id;
+      if (op == 134 || op == 301) gemv_prefetch(c, op);
+      else attn_prefetch(c, op);
+      c.pre = 1;
+    }
+    if (t < 64) {
+      const int k0 = S.swait_off[slot], k1 = S.swait_off[slot + 1];
+      const int err0 = ld_relaxed(&S.cnt->err_code);
+      // the task's own list (set references skipped), then each referenced wait set (lanes of the reference
+      // broadcast it in turn)
+      bool bad = static_wait(S, S.sw + 2 * k0, k1 - k0, w, slot);
+      for (int kb = k0; kb < k1 && !bad; kb += 64) {
+        const int k = kb + t;
+        unsigned long long refs = __ballot(k < k1 && S.sw[2 * k] < 0);
+        while (refs && !bad) {
+          const int kk = kb + __ffsll((long long)refs) - 1;
+          refs &= refs - 1;
+          bad = static_wait(S, S.sw + 2 * S.sw[2 * kk + 1], -1 - S.sw[2 * kk], w, slot);
+        }
+      }
+      fence_acquire();                       // the publishers' stores are visible from here on
+      if (t == 0) s_go = !bad && err0 == 0;
+    }
+    __syncthreads();
+    if (!s_go) break;
+    const MvmTaskDesc& d = s_rec.desc;
+    const int pub_var = d.pub_var, pub_ver = d.pub_ver, wait_var = d.wait_var;   // s_rec is reloaded while thread 0 completes
+    if (t == 0 && S.trace_on) {
+      KvmTrace& tr = S.trace[slot];
+      tr.start = wall_clock64();
+      tr.block = w; tr.xcc = xcc_id();
+      tr.ver0 = d.wait_var >= 0 ? ld_relaxed(&S.version[d.wait_var]) : -1;
+      tr.exec_count += 1;
+      if (d.wait_var >= 0 && tr.ver0 < d.wait_ver) {
+        int z = 0;
+        if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_WAIT_VIOLATION, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+          S.cnt->err_slot = slot;
+      }
+    }
+    KVM_PT(6);
+    // The decode hot path's bodies are inlined here (no call: no callee-saved register spills and reloads per
+    // task); every other operator goes through the dispatcher.
+    const int op = d.op_id;
+    if (V == 0) dispatch(op, c);
+    else {
+      constexpr int GR = V == 1 ? 12 : 8;          // the set's GEMV ring depth
+      const bool rows = op == 301, gv = (op == 134 || rows) && c.pre;
+      const int gm = rows ? c.i(9) : 1, gpro = rows ? c.i(10) : c.i(9);
+      if ((op == 306 || op == 310) && c.i(11) == 4 * c.i(12)) attn_part_body<4>(c, true, op == 310);
+      else if (gv && gv_pre_ring(gm) == GR && gemv_stream_ok(c.buf(0), c.buf(1), c.buf(3), c.buf(4), c.i(8), gm, gpro))
+        gemv_body<GR>(c, gm, gpro, rows ? c.f(11) : c.f(10));
+      else dispatch(op, c);
+    }
+    KVM_PT(7);
+    const bool pub_pos = (sf & KVM_SF_PUB) != 0;
+    wait_stores();
+    __syncthreads();
+    if (t == 0) {
+      if (S.trace_on) {
+        KvmTrace& tr = S.trace[slot];
+        tr.ver1 = wait_var >= 0 ? ld_relaxed(&S.version[wait_var]) : -1;
+        tr.end = wall_clock64();
+#ifdef KVM_GEMM_PROF
+        tr.ver0 = (int)(g_prof[w][6] - tr.start); tr.ver1 = (int)(g_prof[w][7] - tr.start);   // profiling builds only
+#endif
+      }
+      if (pub_var >= 0) publish(S, slot, pub_var, pub_ver);
+      if (pub_pos) st_relaxed(&S.sprogress[w], i - p0 + 1);
+      st_relaxed(&S.done_blk[w], i - p0 + 1);
+    }
+  }
+  wait_stores();   // after an early exit: no direct-to-LDS load of a prefetch is still in flight when the workgroup ends
+}
+
+// Roots (tasks with no predecessors). Roots without a version wait go to fixed cells computed on the host (queue
+// t % nq, in index order within the queue), written by all threads at once; the queue tails then start past them.
+// Roots with a version wait are released one by one by thread 0 afterwards (they park until the version is published,
+// or are enqueued behind the fixed cells when it already is).
+// Instantiated here, ahead of the dynamic kernel: their place in the code object does not move with its code.
+template __global__ void kvm_static_kernel<1>(KvmDevState);
+template __global__ void kvm_static_kernel<2>(KvmDevState);
+template __global__ void kvm_static_kernel<0>(KvmDevState);
+
 __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S) {
   __shared__ __attribute__((aligned(16))) char smem[KVM_LDS_BYTES];
   __shared__ int s_slot;
@@ -717,159 +875,6 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
     if (i == 0) { KvmAdm z = {}; *S.adm = z; }
   }
 }
-// Static-path wait on `cnt` (worker, need) pairs at ent, by the 64 lanes of one wave: each lane takes up to four
-// entries per round of 256 and polls them together (their loads in flight at once), entries of the worker itself
-// (program order) and set references (worker < 0) skipped. Gives up on an error anywhere or after timeout_ticks
-// (TIMEOUT, first error wins). Returns true when it gave up (uniform across the wave).
-__device__ bool static_wait(const KvmDevState& S, const int* ent, int cnt, int self, int slot) {
-  const int l = lane();
-  bool bad = false;
-  for (int j0 = 0; j0 < cnt && !bad; j0 += 256) {
-    int ww[4], need[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int j = j0 + l + 64 * u;
-      ww[u] = j < cnt ? ent[2 * j] : -1;
-      need[u] = j < cnt ? ent[2 * j + 1] : 0;
-      if (ww[u] == self) ww[u] = -1;
-    }
-    const unsigned long long since = wall_clock64();
-    for (unsigned polls = 0;; ++polls) {
-      int have[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) have[u] = ww[u] >= 0 ? ld_relaxed(&S.sprogress[ww[u]]) : 0x7fffffff;
-      bool mine = true;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) mine = mine && have[u] >= need[u];
-      if (__ballot(!mine) == 0ull) break;
-      if (ld_relaxed(&S.cnt->err_code) != 0) { bad = true; break; }
-      __builtin_amdgcn_s_sleep(1);
-      if ((polls & 1023) == 1023 && wall_clock64() - since > S.timeout_ticks) {
-        int z = 0;
-        if (l == 0 && __hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_TIMEOUT, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-          S.cnt->err_slot = slot; S.cnt->err_a = ww[0]; S.cnt->err_b = need[0];
-        }
-        bad = true;
-        break;
-      }
-    }
-  }
-  return bad;
-}
-
-// The static path: worker w runs its program (the host plan) in order. Before a task, wave 0 waits for its cross-worker
-// dependencies (lane k polls wait k: progress[worker] >= need) and acquires; after it, every wave waits for its own
-// write-through stores and the barrier orders them before thread 0 publishes the program position, when another
-// worker waits for this task. Version publications keep the dynamic path's CAS (a gap is still reported); no task
-// parks, the plan orders every waiter after its publisher. A wait gives up after timeout_ticks (TIMEOUT) or when any
-// worker reports an error, so every worker exits.
-//
-// V selects the operator bodies inlined into the worker loop (a call costs each task the callee-saved register spills
-// and reloads of a large body, microseconds per task): 0 none, 1 batch-1 decode (one-row GEMV with the deep ring, the
-// GQA-4 attention split), 2 batched decode (the 8-row GEMV, the GQA-4 attention split). One instantiation per set:
-// each body's registers are allocated with only its set's other bodies (two GEMV ring depths in one kernel made both
-// slower). The host picks V from the graph's operators.
-template <int V>
-__global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState S) {
-  __shared__ __attribute__((aligned(16))) char smem[KVM_LDS_BYTES];
-  __shared__ int s_go;
-  __shared__ __attribute__((aligned(16))) KvmRec s_recs[2];
-  const int t = threadIdx.x, w = blockIdx.x;
-  const int p0 = S.sprog_off[w], p1 = S.sprog_off[w + 1];
-  if (p0 < p1 && t < KVM_REC_VEC_OPS) ((LDS u32x4_t*)&s_recs[0])[t] = ((const u32x4_t*)(S.recs + S.sprog[p0]))[t];
-  int next = p0 < p1 ? S.sprog[p0] : -1;
-  __syncthreads();
-  for (int i = p0; i < p1; ++i) {
-    const int slot = next;
-    KvmRec& s_rec = s_recs[(i - p0) & 1];
-    // Records depend on nothing: wave 1 requests the next task's into the other buffer (direct to LDS) now; its
-    // end-of-task store wait covers that load too.
-    next = i + 1 < p1 ? S.sprog[i + 1] : -1;
-    if (wave() == 1 && next >= 0 && lane() < KVM_REC_VEC_OPS)
-      dma16(dma_rsrc(S.recs + next, sizeof(KvmRec)), 16 * lane(), 0, (const LDS void*)&s_recs[(i + 1 - p0) & 1]);
-    const int sf = S.sflag[slot];
-    // A decode GEMV whose weights no task writes requests its first weight steps before waiting (wave 0's share
-    // lands before its first poll returns).
-    Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
-    if (sf & KVM_SF_PRE) {
-      const int op = s_rec.desc.op_id;
-      if (op == 134 || op == 301) gemv_prefetch(c, op);
-      else attn_prefetch(c, op);
-      c.pre = 1;
-    }
-    if (t < 64) {
-      const int k0 = S.swait_off[slot], k1 = S.swait_off[slot + 1];
-      const int err0 = ld_relaxed(&S.cnt->err_code);
-      // the task's own list (set references skipped), then each referenced wait set (lanes of the reference
-      // broadcast it in turn)
-      bool bad = static_wait(S, S.sw + 2 * k0, k1 - k0, w, slot);
-      for (int kb = k0; kb < k1 && !bad; kb += 64) {
-        const int k = kb + t;
-        unsigned long long refs = __ballot(k < k1 && S.sw[2 * k] < 0);
-        while (refs && !bad) {
-          const int kk = kb + __ffsll((long long)refs) - 1;
-          refs &= refs - 1;
-          bad = static_wait(S, S.sw + 2 * S.sw[2 * kk + 1], -1 - S.sw[2 * kk], w, slot);
-        }
-      }
-      fence_acquire();                       // the publishers' stores are visible from here on
-      if (t == 0) s_go = !bad && err0 == 0;
-    }
-    __syncthreads();
-    if (!s_go) break;
-    const MvmTaskDesc& d = s_rec.desc;
-    const int pub_var = d.pub_var, pub_ver = d.pub_ver, wait_var = d.wait_var;   // s_rec is reloaded while thread 0 completes
-    if (t == 0 && S.trace_on) {
-      KvmTrace& tr = S.trace[slot];
-      tr.start = wall_clock64();
-      tr.block = w; tr.xcc = xcc_id();
-      tr.ver0 = d.wait_var >= 0 ? ld_relaxed(&S.version[d.wait_var]) : -1;
-      tr.exec_count += 1;
-      if (d.wait_var >= 0 && tr.ver0 < d.wait_ver) {
-        int z = 0;
-        if (__hip_atomic_compare_exchange_strong(&S.cnt->err_code, &z, (int)KVM_ERR_WAIT_VIOLATION, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-          S.cnt->err_slot = slot;
-      }
-    }
-    KVM_PT(6);
-    // The decode hot path's bodies are inlined here (no call: no callee-saved register spills and reloads per
-    // task); every other operator goes through the dispatcher.
-    const int op = d.op_id;
-    if (V == 0) dispatch(op, c);
-    else {
-      constexpr int GR = V == 1 ? 12 : 8;          // the set's GEMV ring depth
-      const bool rows = op == 301, gv = (op == 134 || rows) && c.pre;
-      const int gm = rows ? c.i(9) : 1, gpro = rows ? c.i(10) : c.i(9);
-      if ((op == 306 || op == 310) && c.i(11) == 4 * c.i(12)) attn_part_body<4>(c, true, op == 310);
-      else if (gv && gv_pre_ring(gm) == GR && gemv_stream_ok(c.buf(0), c.buf(1), c.buf(3), c.buf(4), c.i(8), gm, gpro))
-        gemv_body<GR>(c, gm, gpro, rows ? c.f(11) : c.f(10));
-      else dispatch(op, c);
-    }
-    KVM_PT(7);
-    const bool pub_pos = (sf & KVM_SF_PUB) != 0;
-    wait_stores();
-    __syncthreads();
-    if (t == 0) {
-      if (S.trace_on) {
-        KvmTrace& tr = S.trace[slot];
-        tr.ver1 = wait_var >= 0 ? ld_relaxed(&S.version[wait_var]) : -1;
-        tr.end = wall_clock64();
-#ifdef KVM_GEMM_PROF
-        tr.ver0 = (int)(g_prof[w][6] - tr.start); tr.ver1 = (int)(g_prof[w][7] - tr.start);   // profiling builds only
-#endif
-      }
-      if (pub_var >= 0) publish(S, slot, pub_var, pub_ver);
-      if (pub_pos) st_relaxed(&S.sprogress[w], i - p0 + 1);
-      st_relaxed(&S.done_blk[w], i - p0 + 1);
-    }
-  }
-  wait_stores();   // after an early exit: no direct-to-LDS load of a prefetch is still in flight when the workgroup ends
-}
-
-// Roots (tasks with no predecessors). Roots without a version wait go to fixed cells computed on the host (queue
-// t % nq, in index order within the queue), written by all threads at once; the queue tails then start past them.
-// Roots with a version wait are released one by one by thread 0 afterwards (they park until the version is published,
-// or are enqueued behind the fixed cells when it already is).
 __global__ void kvm_seed_kernel(KvmDevState S, const int* roots, const int* root_cell, int nfixed, int nroots, const int* fixed_tail) {
   for (int r = threadIdx.x; r < nfixed; r += blockDim.x) {
     const int t = roots[r];

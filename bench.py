@@ -151,13 +151,16 @@ def gemm_task_flops(lb):
                 tm, tn = (256, 128) if f & 64 else (128, 128) if f & 32 else (64, 64)
             fl[i] = 2.0 * (min(M, m0 + tm) - m0) * (min(N, n0 + tn) - n0) * K
         elif op in (45, 47, 48):
-            q0, T, hd = int(a[off + (7 if op != 48 else 10)]), int(a[off + (8 if op != 48 else 11)]), int(a[off + (11 if op != 48 else 13)])
+            # argument positions of (q0 or k0, T, hd) in the registry signatures (mvm_ops_gpt.def)
+            iq, it, ih = {45: (7, 8, 11), 47: (9, 10, 13), 48: (10, 11, 13)}[op]
+            q0, T, hd = int(a[off + iq]), int(a[off + it]), int(a[off + ih])
             q1 = min(T, q0 + 128)
             if op == 48:   # keys [q0, q1) meet queries [k, T): sum over keys of (T - k)
                 pairs = sum(T - k for k in range(q0, q1))
             else:
                 pairs = sum(k + 1 for k in range(q0, q1))
-            fl[i] = 2.0 * hd * pairs * (2 if op == 45 else 2.5)
+            # per (query, key) pair: forward S and P V 4 hd; dQ: S, dP, dS K 6 hd; dK / dV: S, dP, P^T dO, dS^T Q 8 hd
+            fl[i] = 2.0 * hd * pairs * {45: 2, 47: 3, 48: 4}[op]
     return fl
 
 

@@ -25,7 +25,11 @@ FLAGS = ['-O3', '-std=c++17', f'--offload-arch={ARCH}', '-Xclang', '-target-feat
 def build(verbose: bool = False) -> Path:
     OUT.mkdir(exist_ok=True)
     srcs = sorted(CSRC.glob('*.h')) + sorted(CSRC.glob('*.hip')) + sorted((HERE.parent / 'include').glob('*'))
-    cmd = [HIPCC, *FLAGS, '-fPIC', '-shared', str(CSRC / 'exec.hip'), '-o', str(LIB)]
+    # The decode-specialised static kernels and their pre-wait loaders are placed first in the device code object
+    # (device_order.txt): measured decode times moved by up to 2% with their placement alone (identical kernel code),
+    # and a fixed order keeps edits elsewhere in the library from moving them.
+    order = ['-ffunction-sections', '-Xoffload-linker', f'--symbol-ordering-file={CSRC / "device_order.txt"}']
+    cmd = [HIPCC, *FLAGS, *order, '-fPIC', '-shared', str(CSRC / 'exec.hip'), '-o', str(LIB)]
     _run(cmd, verbose)
     cli = [HIPCC, *FLAGS, str(CSRC / 'cli.cpp'), '-o', str(CLI), f'-L{OUT}', '-lkvm_exec', f'-Wl,-rpath,$ORIGIN']
     _run(cli, verbose)

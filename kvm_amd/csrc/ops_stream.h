@@ -99,9 +99,13 @@ __device__ __forceinline__ void emb_rows(const Ctx& c, const View& ids, const Vi
 __device__ __noinline__ bool op_embedding_fwd_fast(const Ctx& c) {
   const View ids = c.buf(0), wte = c.buf(1), wpe = c.buf(2), out = c.buf(3);
   const int r0 = c.i(4), r1 = c.i(5), T = c.i(6), d = c.i(7);
-  if (d % 8 || d > 2048 || !vec8_ok(wte) || !vec8_ok(out) || (wpe.ok() && (!vec8_ok(wpe) || wpe.dtype != wte.dtype)) || T <= 0) return false;
+  if (d % 8 || d > 4096 || !vec8_ok(wte) || !vec8_ok(out) || (wpe.ok() && (!vec8_ok(wpe) || wpe.dtype != wte.dtype)) || T <= 0) return false;
   const bool bw = wte.dtype == 2;
   const int nv = (d + 511) / 512;
+  if (nv > 4) {   // rows up to 4096 wide (a decode step's token rows): one row per wave, 8 vectors per lane in flight
+    if (bw) emb_rows<true, true, 8>(c, ids, wte, wpe, out, r0, r1, T, d); else emb_rows<false, false, 8>(c, ids, wte, wpe, out, r0, r1, T, d);
+    return true;
+  }
   if (nv == 1) { if (bw) emb_rows<true, true, 1>(c, ids, wte, wpe, out, r0, r1, T, d); else emb_rows<false, false, 1>(c, ids, wte, wpe, out, r0, r1, T, d); }
   else if (nv == 2) { if (bw) emb_rows<true, true, 2>(c, ids, wte, wpe, out, r0, r1, T, d); else emb_rows<false, false, 2>(c, ids, wte, wpe, out, r0, r1, T, d); }
   else { if (bw) emb_rows<true, true, 4>(c, ids, wte, wpe, out, r0, r1, T, d); else emb_rows<false, false, 4>(c, ids, wte, wpe, out, r0, r1, T, d); }

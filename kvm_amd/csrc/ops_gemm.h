@@ -815,7 +815,12 @@ template <int R> struct FTile {
 
 template <int TM, int TN> __device__ __noinline__ void gemm_f32(const Ctx& c) {
   constexpr int WM = TM / 2, WN = TN / 2, BM = WM / 32, BN = WN / 32, ST = (TM + TN) * FKS;
-  static_assert(2 * ST * 4 <= KVM_LDS_BYTES && TM * TN * 4 <= KVM_LDS_BYTES, "LDS");
+  // Slabs move in batches of SB (all of a batch's loads in flight together, double-buffered in LDS): one global-load
+  // latency per batch instead of per slab, which is what a small tile's short K loop is bound by.
+  constexpr int NVA = FTile<TM>::NV, NVB = FTile<TN>::NV;
+  constexpr int SB_REG = 16 / (NVA + NVB), SB_LDS = KVM_LDS_BYTES / 2 / (ST * 4);
+  constexpr int SB = SB_REG < SB_LDS ? (SB_REG < 8 ? SB_REG : 8) : (SB_LDS < 8 ? SB_LDS : 8);
+  static_assert(SB >= 1 && 2 * SB * ST * 4 <= KVM_LDS_BYTES && TM * TN * 4 <= KVM_LDS_BYTES, "LDS");
   const GemmArgs g = gemm_args(c);
   const View& A = g.A; const View& B = g.B;
   const bool akc = !(g.fl & 1), bkc = (g.fl & 2) != 0;
@@ -827,43 +832,52 @@ template <int TM, int TN> __device__ __noinline__ void gemm_f32(const Ctx& c) {
   for (int i = 0; i < BM; ++i)
 #pragma unroll
     for (int j = 0; j < BN; ++j) acc[i][j] = f32x16{};
-  FTile<TM> fa;
-  FTile<TN> fb;
-  fa.fetch(A, akc, avec, g.m0, g.M, 0, g.K);
-  fb.fetch(B, bkc, bvec, g.n0, g.N, 0, g.K);
+  FTile<TM> fa[SB];
+  FTile<TN> fb[SB];
+  auto fetch = [&](int bt) {
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      fa[u].fetch(A, akc, avec, g.m0, g.M, (bt * SB + u) * FKS, g.K);
+      fb[u].fetch(B, bkc, bvec, g.n0, g.N, (bt * SB + u) * FKS, g.K);
+    }
+  };
+  auto store = [&](int bt) {
+    LDS float* base = lds + (bt & 1) * SB * ST;
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      fa[u].store(base + u * ST, akc);
+      fb[u].store(base + u * ST + TM * FKS, bkc);
+    }
+  };
+  const int nslab = (g.K + FKS - 1) / FKS, nbat = (nslab + SB - 1) / SB;
+  fetch(0);
   __syncthreads();                         // the previous task may still read this LDS
-  fa.store(lds, akc);
-  fb.store(lds + TM * FKS, bkc);
+  store(0);
   __syncthreads();
-  const int nslab = (g.K + FKS - 1) / FKS;
-  for (int s = 0; s < nslab; ++s) {
-    const LDS float* la = lds + (s & 1) * ST;
-    const LDS float* lb = la + TM * FKS;
-    const bool more = s + 1 < nslab;
-    if (more) {
-      fa.fetch(A, akc, avec, g.m0, g.M, (s + 1) * FKS, g.K);
-      fb.fetch(B, bkc, bvec, g.n0, g.N, (s + 1) * FKS, g.K);
+  for (int bt = 0; bt < nbat; ++bt) {
+    const bool more = bt + 1 < nbat;
+    if (more) fetch(bt + 1);
+    const int ns = min(SB, nslab - bt * SB);
+    for (int u = 0; u < ns; ++u) {
+      const LDS float* la = lds + ((bt & 1) * SB + u) * ST;
+      const LDS float* lb = la + TM * FKS;
+#pragma unroll
+      for (int q = 0; q < FKS / 8; ++q) {
+        const int ch = 2 * q + (l >> 5);
+        f32x4n av[BM], bv[BN];
+#pragma unroll
+        for (int i = 0; i < BM; ++i) av[i] = *(const LDS f32x4n*)(la + fsw(wm0 + i * 32 + (l & 31), ch));
+#pragma unroll
+        for (int j = 0; j < BN; ++j) bv[j] = *(const LDS f32x4n*)(lb + fsw(wn0 + j * 32 + (l & 31), ch));
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < BM; ++i)
+#pragma unroll
+            for (int j = 0; j < BN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[j][t], av[i][t], acc[i][j], 0, 0, 0);
+      }
     }
-#pragma unroll
-    for (int q = 0; q < FKS / 8; ++q) {
-      const int ch = 2 * q + (l >> 5);
-      f32x4n av[BM], bv[BN];
-#pragma unroll
-      for (int i = 0; i < BM; ++i) av[i] = *(const LDS f32x4n*)(la + fsw(wm0 + i * 32 + (l & 31), ch));
-#pragma unroll
-      for (int j = 0; j < BN; ++j) bv[j] = *(const LDS f32x4n*)(lb + fsw(wn0 + j * 32 + (l & 31), ch));
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int i = 0; i < BM; ++i)
-#pragma unroll
-          for (int j = 0; j < BN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[j][t], av[i][t], acc[i][j], 0, 0, 0);
-    }
-    if (more) {
-      LDS float* nb = lds + ((s + 1) & 1) * ST;
-      fa.store(nb, akc);
-      fb.store(nb + TM * FKS, bkc);
-    }
+    if (more) store(bt + 1);
     __syncthreads();
   }
   gemm_store<TM, TN>(c, acc, g);

@@ -89,10 +89,10 @@ def step_flops(c: GPTConfig) -> dict:
     return {'gemm': gemm, 'attn': attn_fwd + attn_bwd, 'total': gemm + attn_fwd + attn_bwd}
 
 
-def row_chunks(R, C):
-    """Flat [e0, e1) ranges of about CHUNK elements covering an R x C matrix, on whole rows: tasks of different chunks
-    never share a row, so the dependency tracker keeps them independent."""
-    return [(r0 * C, r1 * C) for r0, r1 in split(R, -(-(R * C) // CHUNK))]
+def row_chunks(R, C, chunk=None):
+    """Flat [e0, e1) ranges of about `chunk` (default CHUNK) elements covering an R x C matrix, on whole rows: tasks of
+    different chunks never share a row, so the dependency tracker keeps them independent."""
+    return [(r0 * C, r1 * C) for r0, r1 in split(R, -(-(R * C) // (chunk or CHUNK)))]
 
 
 class Deps:

@@ -680,23 +680,36 @@ __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn, bool merg
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   }
-  for (int b0 = 0; b0 < nk; b0 += DB) {
-    u16x8_t kr[DR], vr[DR];
-    if (pre && b0 == 0) {
+  // K and V rows of a block in registers. The next block's K rows are requested once this block's scores are done
+  // (under its softmax and P V), its V rows once this block's P V is done (under the next scores): the registers
+  // each set occupies are free by then, so the pipeline costs no registers.
+  u16x8_t kr[DR], vr[DR];
+  auto load_k = [&](int b0) {
 #pragma unroll
-      for (int i = 0; i < DR; ++i) {
-        const int slot = w * 4 * DR + 4 * i + ts;
-        kr[i] = *(const LDS u16x8_t*)(Ks + slot * hd + d0);
-        vr[i] = *(const LDS u16x8_t*)(Vs + slot * hd + d0);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < DR; ++i) {
-        const long long row = base + j0 + min(b0 + w * 4 * DR + 4 * i + ts, nk - 1);
-        kr[i] = *(const GLOBAL u16x8_t*)(kc.h() + row * kc.cols + d0);
-        vr[i] = *(const GLOBAL u16x8_t*)(vc.h() + row * vc.cols + d0);
-      }
+    for (int i = 0; i < DR; ++i) {
+      const long long row = base + j0 + min(b0 + w * 4 * DR + 4 * i + ts, nk - 1);
+      kr[i] = *(const GLOBAL u16x8_t*)(kc.h() + row * kc.cols + d0);
     }
+  };
+  auto load_v = [&](int b0) {
+#pragma unroll
+    for (int i = 0; i < DR; ++i) {
+      const long long row = base + j0 + min(b0 + w * 4 * DR + 4 * i + ts, nk - 1);
+      vr[i] = *(const GLOBAL u16x8_t*)(vc.h() + row * vc.cols + d0);
+    }
+  };
+  if (pre) {
+#pragma unroll
+    for (int i = 0; i < DR; ++i) {
+      const int slot = w * 4 * DR + 4 * i + ts;
+      kr[i] = *(const LDS u16x8_t*)(Ks + slot * hd + d0);
+      vr[i] = *(const LDS u16x8_t*)(Vs + slot * hd + d0);
+    }
+  } else {
+    load_k(0);
+    load_v(0);
+  }
+  for (int b0 = 0; b0 < nk; b0 += DB) {
     float sv[DR][G];
     float mb[G];
 #pragma unroll
@@ -717,6 +730,8 @@ __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn, bool merg
 #ifdef KVM_GEMM_PROF
     if (b0 == 0) pt[3] = wall_clock64();
 #endif
+    const bool more = b0 + DB < nk;
+    if (more) load_k(b0 + DB);
 #pragma unroll
     for (int g = 0; g < G; ++g) { mb[g] = fmaxf(mb[g], __shfl_xor(mb[g], 16, 64)); mb[g] = fmaxf(mb[g], __shfl_xor(mb[g], 32, 64)); }
     __syncthreads();                                    // red is free
@@ -746,6 +761,7 @@ __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn, bool merg
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[g][e] += p * bf2f(vr[i][e]);
       }
+    if (more) load_v(b0 + DB);
 #pragma unroll
     for (int g = 0; g < G; ++g) { ps[g] += __shfl_xor(ps[g], 16, 64); ps[g] += __shfl_xor(ps[g], 32, 64); }
     __syncthreads();

@@ -286,11 +286,31 @@ __device__ __noinline__ void op_norm_bwd_params(const Ctx& c) {
     if (db.ok()) stwt32(db.f() + j, acc ? db.f()[j] + sb : sb);
   }
 }
+// Columns in groups of 16, each summed by 16 row slots (slot k takes rows k, k + 16, ..., four loads in flight) whose
+// partials are then added in slot order: a column of R rows costs R / 16 dependent steps instead of R.
 __device__ __noinline__ void op_colsum(const Ctx& c) {
   View x = c.buf(0), out = c.buf(1); int R = c.i(2), c0 = c.i(3), c1 = c.i(4), acc = c.i(5);
-  for (int j = c0 + tid(); j < c1; j += KVM_THREADS) {
-    float s = 0.f; for (int r = 0; r < R; ++r) s += x.at(r, j);
-    stwt32(out.f() + j, acc ? out.f()[j] + s : s);
+  LDS float* part = (LDS float*)c.smem;                 // [16 slots][16 columns]
+  const int cj = tid() & 15, slot = tid() >> 4;
+  for (int cb = c0; cb < c1; cb += 16) {
+    const int j = cb + cj;
+    float s = 0.f;
+    if (j < c1) {
+      int r = slot;
+      for (; r + 48 < R; r += 64) {
+        const float a0 = x.at(r, j), a1 = x.at(r + 16, j), a2 = x.at(r + 32, j), a3 = x.at(r + 48, j);
+        s += a0; s += a1; s += a2; s += a3;
+      }
+      for (; r < R; r += 16) s += x.at(r, j);
+    }
+    __syncthreads();                                    // the previous group's partials are read
+    part[slot * 16 + cj] = s;
+    __syncthreads();
+    if (tid() < 16 && j < c1) {
+      float t = 0.f;
+      for (int k = 0; k < 16; ++k) t += part[k * 16 + tid()];
+      stwt32(out.f() + j, acc ? out.f()[j] + t : t);
+    }
   }
 }
 __device__ __noinline__ void op_head_rmsnorm(const Ctx& c) {   // RMSNorm per head slice of hd columns (Qwen3 q/k norm)

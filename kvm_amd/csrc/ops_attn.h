@@ -61,6 +61,32 @@ template <int HD> __device__ __forceinline__ void stage_rows(LDS float* dst, con
   }
 }
 
+// N consecutive values of row r of X from column c0 (zeros when !on): 16-byte loads, all issued before any is
+// converted, when the storage and alignment allow (a per-element load with its dtype test waits for each load alone).
+template <int N> __device__ __forceinline__ void load_row_part(const View& X, long long r, int c0, bool on, float (&out)[N]) {
+  const long long o = r * X.cols + c0;
+  if (on && N % 4 == 0 && X.dtype == 0 && (X.cols & 3) == 0 && (c0 & 3) == 0) {
+    f32x4n t[N / 4];
+#pragma unroll
+    for (int u = 0; u < N / 4; ++u) t[u] = *(const GLOBAL f32x4n*)(X.f() + o + 4 * u);
+#pragma unroll
+    for (int u = 0; u < N / 4; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[4 * u + i] = t[u][i];
+  } else if (on && N % 8 == 0 && X.dtype == 2 && (X.cols & 7) == 0 && (c0 & 7) == 0) {
+    u16x8_t t[N / 8];
+#pragma unroll
+    for (int u = 0; u < N / 8; ++u) t[u] = *(const GLOBAL u16x8_t*)(X.h() + o + 8 * u);
+#pragma unroll
+    for (int u = 0; u < N / 8; ++u)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) out[8 * u + i] = bf2f(t[u][i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = on ? X.ld(o + i) : 0.f;
+  }
+}
+
 // Two threads per query row: thread pair (2*row, 2*row+1) splits the head dimension in halves; dot products combine
 // with one lane swap. HD is a template parameter so the per-thread halves live in registers.
 template <int HD> __device__ __noinline__ void attn_fwd_t(const Ctx& c) {
@@ -71,8 +97,9 @@ template <int HD> __device__ __noinline__ void attn_fwd_t(const Ctx& c) {
   int gq = q0 + row; bool active = gq < T;
   LDS float* Ks = (LDS float*)c.smem; LDS float* Vs = Ks + ATTN_KT * S;
   float qr[HALF], acc[HALF];
+  load_row_part<HALF>(q, (long long)bb * T + gq, h * HD + part * HALF, active, qr);
 #pragma unroll
-  for (int i = 0; i < HALF; ++i) { qr[i] = active ? q.at((long long)bb * T + gq, h * HD + part * HALF + i) * sc : 0.f; acc[i] = 0.f; }
+  for (int i = 0; i < HALF; ++i) { qr[i] *= sc; acc[i] = 0.f; }
   float m = -INFINITY, l = 0.f;
   int last = min(q0 + ATTN_ROWS, T);     // keys [0, last) can matter to this task
   for (int j0 = 0; j0 < last; j0 += ATTN_KT) {
@@ -131,12 +158,10 @@ template <int HD> __device__ __noinline__ void attn_dq_t(const Ctx& c) {
   LDS float* Ks = (LDS float*)c.smem; LDS float* Vs = Ks + ATTN_KT * S;
   float qr[HALF], dr[HALF], acc[HALF];
   long long qrow = (long long)bb * T + gq;
+  load_row_part<HALF>(q, qrow, h * HD + part * HALF, active, qr);
+  load_row_part<HALF>(d, qrow, h * HD + part * HALF, active, dr);
 #pragma unroll
-  for (int i = 0; i < HALF; ++i) {
-    qr[i] = active ? q.at(qrow, h * HD + part * HALF + i) : 0.f;
-    dr[i] = active ? d.at(qrow, h * HD + part * HALF + i) : 0.f;
-    acc[i] = 0.f;
-  }
+  for (int i = 0; i < HALF; ++i) acc[i] = 0.f;
   float li = active ? lse.f()[((long long)bb * H + h) * T + gq] : 0.f, di = active ? delta.f()[((long long)bb * H + h) * T + gq] : 0.f;
   int last = min(q0 + ATTN_ROWS, T);
   for (int j0 = 0; j0 < last; j0 += ATTN_KT) {
@@ -181,12 +206,10 @@ template <int HD> __device__ __noinline__ void attn_dkv_t(const Ctx& c) {
   LDS float* Qs = (LDS float*)c.smem; LDS float* Ds = Qs + ATTN_KT * S; LDS float* Ls = Ds + ATTN_KT * S; LDS float* Es = Ls + ATTN_KT;
   long long krow = (long long)bb * T + gk;
   float kr[HALF], vr[HALF], sk[HALF], sv[HALF];
+  load_row_part<HALF>(k, krow, kvh * HD + part * HALF, active, kr);
+  load_row_part<HALF>(v, krow, kvh * HD + part * HALF, active, vr);
 #pragma unroll
-  for (int i = 0; i < HALF; ++i) {
-    kr[i] = active ? k.at(krow, kvh * HD + part * HALF + i) : 0.f;
-    vr[i] = active ? v.at(krow, kvh * HD + part * HALF + i) : 0.f;
-    sk[i] = sv[i] = 0.f;
-  }
+  for (int i = 0; i < HALF; ++i) sk[i] = sv[i] = 0.f;
   for (int h = kvh * G; h < (kvh + 1) * G; ++h)
     for (int j0 = k0; j0 < T; j0 += ATTN_KT) {   // queries before k0 never see these keys
       int nv = min(ATTN_KT, T - j0);

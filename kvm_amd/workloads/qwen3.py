@@ -37,6 +37,7 @@ class Qwen3Config:
     tasks_per_phase: int = 256
     fused_norm: bool = True    # q / k head norm inside the attention tasks (op 306) where its shapes allow
     fused_merge: bool = True   # with fused_norm: the last split of each kv head merges its query heads (op 310)
+    silu_tasks: int = 0        # batch > 1: SwiGLU tasks per layer; 0 = tasks_per_phase / 2 (measured best of 32-256)
     head_tasks: int = 0        # LM-head GEMV tasks; 0 = 2 x tasks_per_phase (measured: 512 best of 256-2048 at 256 per phase)
 
     @staticmethod
@@ -157,7 +158,7 @@ def build(c: Qwen3Config) -> Workload:
             tg = proj(oj, 'x', f'wg.{l}', 'g', F, D, P // 2, pro=1, gamma=f'ln2.{l}')     # gate and up: one round of P tasks
             tu = proj(oj, 'x', f'wu.{l}', 'u', F, D, P // 2, pro=1, gamma=f'ln2.{l}')
             sm = [b.task('silu_mul_fwd', after=tg + tu, gate='g', up='u', out='h', e0=lo * 8, e1=hi * 8)
-                  for lo, hi in split(B * F // 8, max(1, P // 8))]
+                  for lo, hi in split(B * F // 8, max(1, c.silu_tasks or P // 2))]
             td = proj(sm, 'h', f'wd.{l}', 'x', D, F, P, res='x')
             prev = td if len(td) <= 256 else b.join(td, P)
         else:

@@ -620,7 +620,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
     const int op = d.op_id;
     if (V == 0) dispatch(op, c);
     else {
-      constexpr int GR = V == 1 ? 12 : 8;          // the set's GEMV ring depth
+      constexpr int GR = V == 1 ? 12 : 4;          // the set's GEMV ring depth
       const bool rows = op == 301, gv = (op == 134 || rows) && c.pre;
       const int gm = rows ? c.i(9) : 1, gpro = rows ? c.i(10) : c.i(9);
       if ((op == 306 || op == 310) && c.i(11) == 4 * c.i(12)) attn_part_body<4>(c, true, op == 310);

@@ -614,7 +614,6 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
           S.cnt->err_slot = slot;
       }
     }
-    KVM_PT(6);
     // The decode hot path's bodies are inlined here (no call: no callee-saved register spills and reloads per
     // task); every other operator goes through the dispatcher.
     const int op = d.op_id;
@@ -628,7 +627,6 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
         gemv_body<GR>(c, gm, gpro, rows ? c.f(11) : c.f(10));
       else dispatch(op, c);
     }
-    KVM_PT(7);
     const bool pub_pos = (sf & KVM_SF_PUB) != 0;
     wait_stores();
     __syncthreads();
@@ -637,9 +635,6 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
         KvmTrace& tr = S.trace[slot];
         tr.ver1 = wait_var >= 0 ? ld_relaxed(&S.version[wait_var]) : -1;
         tr.end = wall_clock64();
-#ifdef KVM_GEMM_PROF
-        tr.ver0 = (int)(g_prof[w][6] - tr.start); tr.ver1 = (int)(g_prof[w][7] - tr.start);   // profiling builds only
-#endif
       }
       if (pub_var >= 0) publish(S, slot, pub_var, pub_ver);
       if (pub_pos) st_relaxed(&S.sprogress[w], i - p0 + 1);
@@ -743,7 +738,6 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
       }
     }
     Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
-    KVM_PT(6);
     dispatch(op, c);
     // Every operator stores through write-through (agent-scope) stores only, which tests/test_wt_stores.py checks
     // in the compiled code: once each wave has waited for its own stores, they are agent-visible, and the barrier
@@ -1124,6 +1118,31 @@ static int place_graph(const GraphPlan& g, const std::vector<MvmTaskDesc>& tasks
   return 0;
 }
 
+// Every worker of a persistent kernel must be resident at once (a worker that never starts leaves its queue's tasks
+// unrun and the others waiting): the grid is at most what the occupancy calculator admits per CU times the CUs.
+// The workers' private segments (callee-saved registers of the operator calls) are backed by scratch for every
+// resident wave; a kernel build whose segment grew to 2,096 bytes per lane stopped before its first task finished,
+// while 1,328 runs, so builds above KVM_MAX_PRIVATE_BYTES per lane are refused rather than launched. Returns the
+// co-resident worker capacity of the device, or -1 with the reason in err.
+// The current device is the one asked about.
+static int resident_capacity(int cus, std::string& err) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kvm_exec_kernel, KVM_THREADS, 0) != hipSuccess || per_cu < 1) {
+    err = "the executor kernel does not fit on a CU (occupancy query)"; return -1;
+  }
+  for (const void* k : {(const void*)kvm_exec_kernel, (const void*)kvm_static_kernel<0>, (const void*)kvm_static_kernel<1>,
+                        (const void*)kvm_static_kernel<2>}) {
+    hipFuncAttributes fa{};
+    if (hipFuncGetAttributes(&fa, k) != hipSuccess) { err = "hipFuncGetAttributes failed"; return -1; }
+    if (fa.localSizeBytes > KVM_MAX_PRIVATE_BYTES) {
+      err = "the executor kernel's private segment (" + std::to_string(fa.localSizeBytes) + " bytes per lane) exceeds " +
+            std::to_string(KVM_MAX_PRIVATE_BYTES) + ": refusing a build whose workers may not all be resident";
+      return -1;
+    }
+  }
+  return per_cu * cus;
+}
+
 extern "C" {
 
 void kvm_config_default(KvmConfig* c) {
@@ -1151,27 +1170,10 @@ KvmExec* kvm_create(const KvmConfig* cfg) {
   if (hipSetDevice(c.device) != hipSuccess) { g_err = "hipSetDevice failed"; return nullptr; }
   hipDeviceProp_t p;
   if (hipGetDeviceProperties(&p, c.device) != hipSuccess) { g_err = "hipGetDeviceProperties failed"; return nullptr; }
-  // Every worker of the persistent kernel must be resident at once (a worker that never starts leaves its queue's tasks
-  // unrun and the others waiting): the grid is at most what the occupancy calculator admits per CU times the CUs.
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kvm_exec_kernel, KVM_THREADS, 0) != hipSuccess || per_cu < 1) {
-    g_err = "the executor kernel does not fit on a CU (occupancy query)"; return nullptr;
-  }
-  // The workers' private segments (callee-saved registers of the operator calls) are backed by scratch for every
-  // resident wave; a kernel build whose segment grew to 2,096 bytes per lane stopped before its first task finished,
-  // while 1,328 runs. Builds above 2,048 bytes per lane are refused rather than launched.
-  for (const void* k : {(const void*)kvm_exec_kernel, (const void*)kvm_static_kernel<0>, (const void*)kvm_static_kernel<1>,
-                        (const void*)kvm_static_kernel<2>}) {
-    hipFuncAttributes fa{};
-    if (hipFuncGetAttributes(&fa, k) != hipSuccess) { g_err = "hipFuncGetAttributes failed"; return nullptr; }
-    if (fa.localSizeBytes > KVM_MAX_PRIVATE_BYTES) {
-      g_err = "the executor kernel's private segment (" + std::to_string(fa.localSizeBytes) + " bytes per lane) exceeds " +
-              std::to_string(KVM_MAX_PRIVATE_BYTES) + ": refusing a build whose workers may not all be resident";
-      return nullptr;
-    }
-  }
-  if (c.blocks < 0 || (long long)c.blocks > (long long)per_cu * p.multiProcessorCount) {
-    g_err = "blocks exceeds the co-resident capacity of the device (" + std::to_string(per_cu * p.multiProcessorCount) + ")"; return nullptr;
+  const int capacity = resident_capacity(p.multiProcessorCount, g_err);
+  if (capacity < 0) return nullptr;
+  if (c.blocks < 0 || c.blocks > capacity) {
+    g_err = "blocks exceeds the co-resident capacity of the device (" + std::to_string(capacity) + ")"; return nullptr;
   }
   KvmExec* ex = new KvmExec();
   ex->cfg = c; ex->dev = c.device; ex->cus = p.multiProcessorCount;
@@ -1985,6 +1987,7 @@ static __device__ __align__(256) unsigned char scratch[KVM_NOALLOC_SCRATCH_BYTES
 #define KVM_MAX_DEVICES 64
 static void* g_scratch_ptr[KVM_MAX_DEVICES];
 static int g_scratch_cus[KVM_MAX_DEVICES];
+static int g_scratch_cap[KVM_MAX_DEVICES];   // co-resident worker capacity (resident_capacity)
 static std::mutex g_scratch_mu[KVM_MAX_DEVICES];
 
 static int scratch_setup(int dev, std::string& err) {
@@ -1995,7 +1998,10 @@ static int scratch_setup(int dev, std::string& err) {
   int cus = 0;
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess || cus < 1) { err = "hipDeviceGetAttribute(multiprocessor count) failed"; return KVM_STATUS_HIP_ERROR; }
+  const int cap = resident_capacity(cus, err);
+  if (cap < 0) return KVM_STATUS_INVALID;
   g_scratch_cus[dev] = cus;
+  g_scratch_cap[dev] = cap;
   g_scratch_ptr[dev] = ptr;
   return 0;
 }
@@ -2012,6 +2018,10 @@ int kvm_run_noalloc(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, i
   for (int i = 0; i < nbufs; ++i) if (!bufs[i].p) { err = "buffer " + std::to_string(i) + " has no device address"; return fail(KVM_STATUS_INVALID); }
   std::lock_guard<std::mutex> lock(g_scratch_mu[dev]);   // calls on one device in this process never overlap
   if (int rc = scratch_setup(dev, err)) return fail(rc);
+  if (blocks > g_scratch_cap[dev]) {
+    err = "blocks " + std::to_string(blocks) + " exceeds the co-resident capacity of the device (" + std::to_string(g_scratch_cap[dev]) + ")";
+    return fail(KVM_STATUS_INVALID);
+  }
   const int grid = blocks > 0 ? blocks : g_scratch_cus[dev];
   std::vector<MvmTaskDesc> tv(tasks, tasks + ntasks);
   std::vector<int32_t> sv(succ, succ + nedges), av(args, args + nargs), roots;

@@ -562,9 +562,6 @@ __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn, bool merg
   const int bb = c.i(7), kvh = c.i(8), s = c.i(9), S = c.i(10), H = c.i(11), Hkv = c.i(12), Tmax = c.i(14);
   const float sc = c.f(15), th = c.f(16);
   const int fl = c.i(17);
-#ifdef KVM_GEMM_PROF
-  unsigned long long pt[8] = {(unsigned long long)wall_clock64(), 0, 0, 0, 0, 0, 0, 0};
-#endif
   constexpr int hd = ATT_HD, half = 64;
   constexpr int DR = ATT_DR, DB = ATT_DB;               // rounds of 4 tokens per wave; tokens per block (160)
   int L, j0, nk;
@@ -680,13 +677,7 @@ __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn, bool merg
       if (stage) Vs[srow * hd + k] = f2bf(v);
     }
   }
-#ifdef KVM_GEMM_PROF
-  pt[1] = wall_clock64();
-#endif
   __syncthreads();                                      // the new row is stored before any block reads it
-#ifdef KVM_GEMM_PROF
-  pt[2] = wall_clock64();
-#endif
   if (nk == 0) {
     for (int e = tid(); e < G * (hd + 2); e += KVM_THREADS) {
       const int g = e / (hd + 2), k = e % (hd + 2);
@@ -750,9 +741,6 @@ __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn, bool merg
         mb[g] = fmaxf(mb[g], sv[i][g]);
       }
     }
-#ifdef KVM_GEMM_PROF
-    if (b0 == 0) pt[3] = wall_clock64();
-#endif
     const bool more = b0 + DB < nk;
     if (more) load_k(b0 + DB);
 #pragma unroll
@@ -796,9 +784,6 @@ __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn, bool merg
     for (int g = 0; g < G; ++g) lrun[g] = lrun[g] * scale[g] + ((red[32 + g] + red[40 + g]) + (red[48 + g] + red[56 + g]));
   }
   // P V: the partial sums of the 16 token slots (4 per wave) through LDS, added in slot order
-#ifdef KVM_GEMM_PROF
-  pt[4] = wall_clock64();
-#endif
   __syncthreads();
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -815,11 +800,6 @@ __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn, bool merg
     if (k == 0) { stwt32(part.f() + (r + hd), mrun[g]); stwt32(part.f() + (r + hd + 1), lrun[g]); }
   }
   if (merge) attn_arrive<G>(c, bb, kvh, S, H, Hkv);
-#ifdef KVM_GEMM_PROF
-  pt[5] = wall_clock64();
-  __syncthreads();
-  if (tid() == 0) { unsigned long long* o = (unsigned long long*)(part.f() + (((long long)bb * S + s) * H + kvh * G) * part.cols); for (int i = 0; i < 6; ++i) o[i] = pt[i]; o[6] = g_prof[blockIdx.x][6]; }
-#endif
 }
 template <int G> __device__ __noinline__ void attn_decode_part_fast(const Ctx& c, bool qkn, bool merge = false) { attn_part_body<G>(c, qkn, merge); }
 __device__ __noinline__ void op_attn_decode_part_any(const Ctx& c) {

@@ -413,9 +413,6 @@ template <int R> __device__ __forceinline__ void gemv_body(const Ctx& c, int M_,
   LDS float* rstd = (LDS float*)(c.smem + geo.rstd_off);                       // [16]
   LDS float* part = (LDS float*)(c.smem + geo.part_off);                       // [4][GV_GRP][M][16]
   const int l = lane(), wv = wave(), nrows = n1 - n0, nrb = (nrows + 15) / 16;
-#ifdef KVM_GEMM_PROF
-  unsigned long long pt[8] = {(unsigned long long)wall_clock64(), 0, 0, 0, 0, 0, 0, 0};
-#endif
   LDS char* ring = c.smem + wv * R * GV_STEP;
   GvStream ws;
   ws.init(w, n0, n1, K, KC);
@@ -449,9 +446,6 @@ template <int R> __device__ __forceinline__ void gemv_body(const Ctx& c, int M_,
         else gv_stage<0, 2 * GV_SB>(lx, lx, x.cols, 0, M, kc, KC, VS, vs, rstd);
       }
       __syncthreads();
-#ifdef KVM_GEMM_PROF
-      if (g0 == 0) pt[1] = wall_clock64();
-#endif
       const LDS uint16_t* vk = va + wv * kq;
       // One flat loop over the group's steps (row block rb, step st): a nested loop's header is where the compiler
       // places a full vmcnt wait, which would drain the ring once per row block.
@@ -479,13 +473,7 @@ template <int R> __device__ __forceinline__ void gemv_body(const Ctx& c, int M_,
         }
       }
     }
-#ifdef KVM_GEMM_PROF
-    if (g0 == 0) pt[2] = wall_clock64();
-#endif
     __syncthreads();
-#ifdef KVM_GEMM_PROF
-    if (g0 == 0) pt[3] = wall_clock64();
-#endif
     for (int e = tid(); e < ng * PM; e += KVM_THREADS) {                       // sum the four waves' tiles, in wave order
       const int rb = e / PM, m = (e / 16) % M, nn = e % 16, n = n0 + (g0 + rb) * 16 + nn;
       if (n >= n1) continue;
@@ -495,11 +483,6 @@ template <int R> __device__ __forceinline__ void gemv_body(const Ctx& c, int M_,
     if (g0 + GV_GRP < nrb) __syncthreads();                                    // the sums are read before the tiles are cleared
   }
   wait_vm_c<0>();                                                               // the ring's trailing loads have landed
-#ifdef KVM_GEMM_PROF
-  pt[4] = wall_clock64();
-  __syncthreads();
-  if (tid() == 0 && out.dtype == 0) { unsigned long long* o = (unsigned long long*)(out.f() + n0); for (int i = 0; i < 5; ++i) o[i] = pt[i]; o[5] = g_prof[blockIdx.x][6]; }
-#endif
 }
 template <int R> __device__ __noinline__ void gemv_stream_r(const Ctx& c, int M, int pro, float eps) { gemv_body<R>(c, M, pro, eps); }
 __device__ __noinline__ void gemv_stream(const Ctx& c, int M, int pro, float eps) {

@@ -127,12 +127,6 @@ __device__ __noinline__ void op_matmul_tile_silu_mul_bwd(const Ctx& c) {
 //     owns 4 consecutive output columns of one row, and the epilogue reads and writes 4-element vectors.
 typedef uint16_t u16x4_t __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
-#ifdef KVM_GEMM_PROF
-__device__ unsigned long long g_prof[1024][16];
-#define KVM_PT(i) do { if (tid() == 0) g_prof[blockIdx.x][i] = wall_clock64(); } while (0)
-#else
-#define KVM_PT(i) do { } while (0)
-#endif
 constexpr int GK = 64;
 constexpr int GS = GK + 8;
 
@@ -400,9 +394,6 @@ __device__ __forceinline__ void epi_rows(const Ctx& c, const GemmArgs& g) {
       else stwt_buf(orsrc, (m * e.out.cols + n) * 4, v);
     }
   }
-#ifdef KVM_GEMM_PROF
-  KVM_PT(10);
-#endif
 }
 
 template <int TM, int TN, bool OBF>
@@ -431,9 +422,6 @@ __device__ __noinline__ void gemm_epilogue(const Ctx& c, int moff) {
   lb.init(e.bias); lr.init(e.res); lp.init(e.pre, dg); lo.init(e.out, e.accum != 0);
   const f32x4n bv = lb.get(n);
   const __amdgpu_buffer_rsrc_t orsrc = wt_rsrc(e.out.p, (long long)g.M * e.out.cols * 4);   // f32 output rows (small: < 2^31 bytes)
-#ifdef KVM_GEMM_PROF
-  KVM_PT(9);
-#endif
   for (int k0 = 0; k0 < NI; k0 += NB) {
     f32x4n rv[NB], pv[NB], ov[NB];
 #pragma unroll
@@ -468,9 +456,6 @@ __device__ __noinline__ void gemm_epilogue(const Ctx& c, int moff) {
       }
     }
   }
-#ifdef KVM_GEMM_PROF
-  KVM_PT(10);
-#endif
 }
 
 // Stages the accumulators in LDS (see above) and runs the epilogue; a tile whose f32 copy exceeds the LDS budget
@@ -499,15 +484,9 @@ __device__ __forceinline__ void gemm_store(const Ctx& c, const f32x16 (&acc)[TM 
       }
     }
     __syncthreads();
-#ifdef KVM_GEMM_PROF
-    KVM_PT(8);
-#endif
     if (g.e.out.dtype == 2) gemm_epilogue<HM, TN, true>(c, h * HM);
     else gemm_epilogue<HM, TN, false>(c, h * HM);
   }
-#ifdef KVM_GEMM_PROF
-  KVM_PT(11);
-#endif
 }
 
 template <int TM, int TN, bool FAST, bool AKC, bool BKC>
@@ -660,9 +639,6 @@ __device__ __noinline__ void gemm_lds(const Ctx& c) {
   const View& A = g.A; const View& B = g.B;
   const int m0 = g.m0, n0 = g.n0, K = g.K;
   LDS uint16_t* lds = (LDS uint16_t*)c.smem;
-#ifdef KVM_GEMM_PROF
-  unsigned long long pt[8]; pt[0] = wall_clock64(); pt[1] = __builtin_amdgcn_s_memtime();
-#endif
   const int wm0 = (wave() >> 1) * WM, wn0 = (wave() & 1) * WN;
   DOp<TM, AKC> da;
   DOp<TN, BKC> db;
@@ -725,15 +701,7 @@ __device__ __noinline__ void gemm_lds(const Ctx& c) {
   read_half(lds + ((nst - 1) % NS) * ST, 1, fa1, fb1);
   mfma_half(fa0, fb0);
   mfma_half(fa1, fb1);
-#ifdef KVM_GEMM_PROF
-  pt[2] = wall_clock64(); pt[3] = __builtin_amdgcn_s_memtime();
-#endif
   gemm_store<TM, TN>(c, acc, g);
-#ifdef KVM_GEMM_PROF
-  pt[4] = wall_clock64(); pt[5] = __builtin_amdgcn_s_memtime();
-  __syncthreads();
-  if (tid() == 0) { unsigned long long* o = (unsigned long long*)(g.e.out.h() + (long long)m0 * g.e.out.cols + n0); for (int i = 0; i < 6; ++i) o[i] = pt[i]; for (int i = 6; i < 16; ++i) o[i] = g_prof[blockIdx.x][i]; }
-#endif
 }
 
 // Whether an operand slab sequence can use unconditional vector loads: bf16 storage, rows of whole 16-byte vectors,

@@ -1,33 +1,39 @@
-// kvm_run: the manifest runner, counterpart of the reference's demo runner (reference: demo/mvm_run.cu). It reads a
-// demo directory (MANIFEST.json plus compiled ABI-v2 bundles) and runs every admission it lists on ONE persistent
-// kernel in stream mode, with no knowledge of the models: buffers, version variables, admission order and conditions
-// all come from the manifest.
+// kvm_run: runs a demo directory (MANIFEST.json plus ABI-v2 bundles) on ONE persistent kernel in stream mode. It is
+// the counterpart of the reference's demo runner (reference: demo/mvm_run.cu; manifest writer and CPU runner:
+// frontend/mvmfe/demo.py, frontend/mvmfe/run_manifest.py). The runner knows nothing about models: buffers, version
+// variables and the admission order come from the manifest.
 //
-//   kvm_run DEMO_DIR [--out DIR] [--dump REGEX] [--windows N] [--blocks N] [--timeout-s N] [--check-only] [--quiet]
+//   kvm_run DEMO_DIR [--out DIR] [--dump REGEX] [--windows N] [--blocks N] [--timeout-s N] [--sched auto|off]
+//                    [--check-only] [--quiet]
 //
-// Manifest semantics (the reference's, restated): `buffers` are allocated once, initialised from their owner
-// workload's bundle, and shared by name across bundles; an admission starts when its time (at_us) has come, every
-// `after_bundles` entry has completed, each `when` condition holds for the LIVE version of its variable, and, for every
-// variable it publishes, the live version equals the base it was compiled for while no other admission in flight
-// publishes it. Several admissions may be in flight. A bundle compiled for other base versions is shifted (every wait
-// and publish of a published variable moved by the difference) when it reads no such variable by absolute version; an
-// admission without a bundle directory reuses the last bundle of its workload, shifted. Everything that can be checked
-// without a GPU is checked first: the manifest's shape, a serial simulation of the version flow (cycles, conditions no
-// order reaches), and every bundle against the global buffer table.
+// The rules this runner applies (the manifest format's, frontend/mvmfe/demo.py:136-152):
+//   * every `buffers` entry is one device allocation, initialised from the bundle of its owner workload and shared by
+//     name by every bundle that names it;
+//   * an admission may be submitted when its `at_us` has passed, every admission in its `after_bundles` has finished,
+//     the live version of each `when` variable lies in [min, max], and, for every variable in its `publishes`, the
+//     live version equals the admission's base version and no other admission publishing it is in flight;
+//   * an admission that completes has advanced each published variable BY `publishes[var]`:
+//     live after completion = base + publishes[var] (demo.py:136, mvm_run.cu:262);
+//   * a bundle compiled for other base versions runs shifted (its waits and publications of a published variable
+//     move by the difference) when it reads that variable by no absolute version;
+//   * `classes` configure the device scheduler. Stream mode schedules first-come first-served, so a manifest that
+//     declares classes is refused unless `--sched off` asks for exactly that (the reference runner's own switch).
+// Before the GPU is touched the runner checks the manifest's shape, checks every bundle against the global tables
+// (including that what it publishes is what its admission declares), and runs the version flow serially (one
+// admission at a time, the first in manifest order whose gate is open; time ignored).
 //
-// Output (--out): summary.json (per admission: tasks, windows, submit / completion times, live versions at
-// completion; final versions), and DIR/<buffer>.bin for buffers matching --dump (f32 widened, i32 raw). Prints
-// "OK: d/a tasks, X ms, N admissions" or "FAIL: ..." and exits 0 / 1 (2 for usage errors).
+// --out DIR writes summary.json (per admission: tasks, windows, submission and completion times, live versions at
+// completion; final versions) and DIR/<buffer>.bin for the buffers --dump matches (f32 values; i32 raw). The last
+// stdout line is "OK: d/a tasks, X ms, N admissions" or "FAIL: <reason>"; exit 0 / 1, 2 for usage errors.
 #include <algorithm>
 #include <chrono>
 #include <climits>
-#include <cstdarg>
+#include <ftw.h>
 #include <map>
 #include <memory>
 #include <regex>
 #include <set>
 #include <sys/stat.h>
-#include <ftw.h>
 #include <thread>
 #include <unistd.h>
 #include "../../include/kvm_exec.h"
@@ -38,609 +44,706 @@ using namespace kvmh;
 
 namespace {
 
-struct ManifestError : std::runtime_error { using std::runtime_error::runtime_error; };
-[[noreturn]] void fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
-void fail(const char* fmt, ...) {
-  char b[2048];
-  va_list ap; va_start(ap, fmt); vsnprintf(b, sizeof b, fmt, ap); va_end(ap);
-  throw ManifestError(b);
-}
+// ================================================================================================ reading the manifest
+// Every problem the runner finds before launch is a ManifestProblem whose text starts with where it was found, as a
+// JSON path ("$.admissions[2].when[0].min") or the name of the object concerned.
+struct ManifestProblem : std::runtime_error { using std::runtime_error::runtime_error; };
+[[noreturn]] void refuse(const std::string& where, const std::string& what) { throw ManifestProblem(where + ": " + what); }
 
-// ---------------------------------------------------------------------------------------------- strict accessors
-const Json& member(const Json& o, const char* k, const std::string& where) {
-  if (o.t != Json::O) fail("%s: expected an object", where.c_str());
-  const Json* j = o.get(k);
-  if (!j) fail("%s: missing key '%s'", where.c_str(), k);
-  return *j;
-}
-long long as_int(const Json& j, const std::string& where, long long lo = LLONG_MIN / 2, long long hi = LLONG_MAX / 2) {
-  if (j.t != Json::N || j.n != std::floor(j.n) || !std::isfinite(j.n)) fail("%s: expected an integer", where.c_str());
-  if (j.n < (double)lo || j.n > (double)hi) fail("%s: %.17g outside [%lld, %lld]", where.c_str(), j.n, lo, hi);
-  return (long long)j.n;
-}
-const std::string& as_str(const Json& j, const std::string& where) {
-  if (j.t != Json::S || j.s.empty()) fail("%s: expected a non-empty string", where.c_str());
-  return j.s;
-}
-const std::vector<Json>& as_arr(const Json& j, const std::string& where) {
-  if (j.t != Json::A) fail("%s: expected an array", where.c_str());
-  return j.a;
-}
-bool is_null(const Json* j) { return !j || j->t == Json::NUL; }
-const std::string& as_rel_path(const Json& j, const std::string& where) {
-  const std::string& s = as_str(j, where);
-  if (s[0] == '/' || s.find("..") != std::string::npos) fail("%s: '%s' must be a relative path without '..'", where.c_str(), s.c_str());
-  return s;
-}
-typedef std::map<std::string, long long> VerMap;
-VerMap as_versions(const Json* j, const std::string& where) {
-  VerMap m;
-  if (is_null(j)) return m;
-  if (j->t != Json::O) fail("%s: expected an object of variable -> version", where.c_str());
-  for (auto& kv : j->o) m[kv.first] = as_int(kv.second, where + "." + kv.first, 0, INT_MAX / 2);
-  return m;
-}
+// A position in a parsed JSON document, carrying its path so that every typed read can say where it failed.
+class Node {
+ public:
+  Node(const Json* j, std::string path) : j_(j), path_(std::move(path)) {}
+  const std::string& path() const { return path_; }
+  bool given() const { return j_ && j_->t != Json::NUL; }
+  bool is_object() const { return j_ && j_->t == Json::O; }
 
-// ---------------------------------------------------------------------------------------------- manifest model
-struct Cond { std::string var; long long mn = 0, mx = LLONG_MAX; };
-struct Workload { std::string name, file, cls; long long tasks = 0, edges = 0; int priority = 0; std::vector<std::string> variables; };
-struct Admission {
-  std::string name, workload, bundle_dir, compile_workload, compile_data_dir;
-  std::vector<std::string> after;
-  std::vector<Cond> when;
-  long long at_us = -1;
-  VerMap base, publishes;
+  Node field(const std::string& key) const {      // a member that must be there
+    const Node n = opt(key);
+    if (!n.j_) refuse(path_, "the key \"" + key + "\" is required");
+    return n;
+  }
+  Node opt(const std::string& key) const {        // a member that may be absent (given() is false then)
+    if (!is_object()) refuse(path_, "must be a JSON object");
+    return Node(j_->get(key), path_ + "." + key);
+  }
+  std::vector<std::pair<std::string, Node>> members() const {
+    if (!is_object()) refuse(path_, "must be a JSON object");
+    std::vector<std::pair<std::string, Node>> v;
+    for (auto& kv : j_->o) v.emplace_back(kv.first, Node(&kv.second, path_ + "." + kv.first));
+    return v;
+  }
+  std::vector<Node> items() const {
+    if (!j_ || j_->t != Json::A) refuse(path_, "must be a JSON array");
+    std::vector<Node> v;
+    for (size_t i = 0; i < j_->a.size(); ++i) v.emplace_back(&j_->a[i], path_ + "[" + std::to_string(i) + "]");
+    return v;
+  }
+  long long whole(long long lo, long long hi) const {
+    if (!j_ || j_->t != Json::N || !std::isfinite(j_->n) || std::floor(j_->n) != j_->n) refuse(path_, "must be a whole number");
+    if (j_->n < (double)lo || j_->n > (double)hi)
+      refuse(path_, "is " + std::to_string((long long)j_->n) + ", allowed " + std::to_string(lo) + " .. " + std::to_string(hi));
+    return (long long)j_->n;
+  }
+  std::string text() const {
+    if (!j_ || j_->t != Json::S || j_->s.empty()) refuse(path_, "must be a non-empty string");
+    return j_->s;
+  }
+  std::string inner_path() const {                // a file or directory inside the demo directory
+    const std::string s = text();
+    if (s[0] == '/' || s.find("..") != std::string::npos) refuse(path_, "\"" + s + "\" leaves the demo directory (relative path without '..' required)");
+    return s;
+  }
+
+ private:
+  const Json* j_;
+  std::string path_;
 };
-struct BufDecl { std::string name; int rows = 0, cols = 0, dtype = 0; std::string owner; };
-struct ClassDecl { std::string name; std::map<std::string, long long> params; };
-struct Manifest {
+
+constexpr long long kMaxVersion = INT_MAX / 2;
+
+struct Window { int var; long long lo, hi; };           // a `when` entry: lo <= live[var] <= hi
+struct VarVersion { int var; long long v; };
+
+struct WorkloadDecl { std::string name, cls; std::vector<int> vars; };
+struct BufferDecl { std::string name, owner; int rows, cols, dtype; };
+struct AdmissionDecl {
+  std::string name;
+  int workload = -1;
+  std::vector<int> after;                               // admissions that must have finished
+  std::vector<Window> when;
+  long long at_us = -1;                                 // -1: no time condition
+  std::vector<VarVersion> base;                         // versions the bundle was compiled for
+  std::vector<VarVersion> advance;                      // `publishes`: increments applied at completion
+  std::string bundle_dir, compile_file, compile_data;
+  long long base_of(int var) const { for (auto& b : base) if (b.var == var) return b.v; return -1; }
+  bool publishes(int var) const { for (auto& p : advance) if (p.var == var) return true; return false; }
+};
+
+// The manifest with every name resolved to an index.
+struct Plan {
   std::string root;
-  std::vector<Workload> workloads; std::map<std::string, int> wl_idx;
-  std::vector<Admission> adms; std::map<std::string, int> adm_idx;
-  std::vector<BufDecl> buffers; std::map<std::string, int> buf_idx;
-  std::vector<std::string> vars; std::map<std::string, int> var_idx;
-  std::vector<ClassDecl> classes;
-  int var_id(const std::string& n, const std::string& where) const {
-    auto it = var_idx.find(n);
-    if (it == var_idx.end()) fail("%s: version variable '%s' is not declared by any workload", where.c_str(), n.c_str());
-    return it->second;
+  std::vector<std::string> vars;
+  std::vector<WorkloadDecl> workloads;
+  std::vector<BufferDecl> buffers;
+  std::vector<AdmissionDecl> adms;
+  std::map<std::string, std::map<std::string, long long>> classes;   // declared class -> parameters
+
+  static int find(const std::vector<std::string>& names, const std::string& n) {
+    auto it = std::find(names.begin(), names.end(), n);
+    return it == names.end() ? -1 : (int)(it - names.begin());
   }
+  int var(const std::string& n) const { return find(vars, n); }
+  int buffer(const std::string& n) const { for (size_t i = 0; i < buffers.size(); ++i) if (buffers[i].name == n) return (int)i; return -1; }
+  int workload(const std::string& n) const { for (size_t i = 0; i < workloads.size(); ++i) if (workloads[i].name == n) return (int)i; return -1; }
+  int admission(const std::string& n) const { for (size_t i = 0; i < adms.size(); ++i) if (adms[i].name == n) return (int)i; return -1; }
 };
 
-const char* const kClassKeys[] = {"weight", "min_cta", "max_cta", "bw_cta", "urgent_us"};
+const char* const kClassParams[] = {"weight", "min_cta", "max_cta", "bw_cta", "urgent_us"};
 
-Manifest parse_manifest(const std::string& root) {
-  Manifest m; m.root = root;
-  Json j = Parser(read_file(root + "/MANIFEST.json")).parse();
-  if (as_int(member(j, "manifest_version", "manifest"), "manifest_version") != 1) fail("manifest_version must be 1");
-  const Json& jw = member(j, "workloads", "manifest");
-  if (jw.t != Json::O || jw.o.empty()) fail("workloads: expected a non-empty object");
-  auto class_of = [&](const std::string& c) {
-    for (size_t i = 0; i < m.classes.size(); ++i) if (m.classes[i].name == c) return (int)i;
-    m.classes.push_back(ClassDecl{c, {}});
-    return (int)m.classes.size() - 1;
-  };
-  if (const Json* jc = j.get("classes")) {
-    if (jc->t != Json::O) fail("classes: expected an object");
-    for (auto& kv : jc->o) {
-      const int c = class_of(kv.first);
-      if (kv.second.t != Json::O) fail("classes.%s: expected an object", kv.first.c_str());
-      for (auto& pk : kv.second.o) {
-        if (std::none_of(std::begin(kClassKeys), std::end(kClassKeys), [&](const char* k) { return pk.first == k; }))
-          fail("classes.%s: unknown scheduler parameter '%s' (weight, min_cta, max_cta, bw_cta, urgent_us)", kv.first.c_str(), pk.first.c_str());
-        const long long v = as_int(pk.second, "classes." + kv.first + "." + pk.first, 0, INT_MAX);
-        if (pk.first == "weight" && v < 1) fail("classes.%s.weight must be >= 1", kv.first.c_str());
-        m.classes[c].params[pk.first] = v;
-      }
-    }
+std::vector<VarVersion> read_versions(const Node& n, const Plan& p, bool positive) {
+  std::vector<VarVersion> out;
+  if (!n.given()) return out;
+  for (auto& [name, v] : n.members()) {
+    const int id = p.var(name);
+    if (id < 0) refuse(v.path(), "\"" + name + "\" is not a variable any workload declares");
+    out.push_back({id, v.whole(positive ? 1 : 0, kMaxVersion)});
   }
-  for (auto& kv : jw.o) {
-    const std::string where = "workloads." + kv.first;
-    Workload w; w.name = kv.first;
-    w.file = as_rel_path(member(kv.second, "file", where), where + ".file");
-    w.tasks = as_int(member(kv.second, "tasks", where), where + ".tasks", 1, INT_MAX);
-    w.edges = as_int(member(kv.second, "edges", where), where + ".edges", 0, INT_MAX);
-    w.priority = (int)as_int(member(kv.second, "priority", where), where + ".priority", 0, 1 << 20);
-    w.cls = kv.second.get("class") ? as_str(*kv.second.get("class"), where + ".class") : "default";
-    if (const Json* v = kv.second.get("variables"))
-      for (auto& x : as_arr(*v, where + ".variables")) w.variables.push_back(as_str(x, where + ".variables[]"));
-    if (const Json* rq = kv.second.get("requirements"))
-      if (const Json* rs = rq->get("resources"))
-        if (!as_arr(*rs, where + ".requirements.resources").empty())
-          fail("%s needs host resources, which this runner does not provide (the game pack is out of scope)", where.c_str());
-    class_of(w.cls);
-    for (auto& v : w.variables) if (!m.var_idx.count(v)) { m.var_idx[v] = (int)m.vars.size(); m.vars.push_back(v); }
-    m.wl_idx[w.name] = (int)m.workloads.size();
-    m.workloads.push_back(w);
-  }
-  const Json& jb = member(j, "buffers", "manifest");
-  if (jb.t != Json::O) fail("buffers: expected an object");
-  for (auto& kv : jb.o) {
-    const std::string where = "buffers." + kv.first;
-    BufDecl b; b.name = kv.first;
-    b.rows = (int)as_int(member(kv.second, "rows", where), where + ".rows", 1, INT_MAX);
-    b.cols = (int)as_int(member(kv.second, "cols", where), where + ".cols", 1, INT_MAX);
-    const std::string& dt = as_str(member(kv.second, "dtype", where), where + ".dtype");
-    if (dt != "f32" && dt != "i32" && dt != "bf16") fail("%s.dtype: '%s' is not f32, i32 or bf16", where.c_str(), dt.c_str());
-    b.dtype = dt == "i32" ? 1 : dt == "bf16" ? 2 : 0;
-    b.owner = as_str(member(kv.second, "owner", where), where + ".owner");
-    if (!m.wl_idx.count(b.owner)) fail("%s.owner: unknown workload '%s'", where.c_str(), b.owner.c_str());
-    if ((long long)b.rows * b.cols > (1ll << 31) - 1) fail("%s: %d x %d elements overflow", where.c_str(), b.rows, b.cols);
-    m.buf_idx[b.name] = (int)m.buffers.size();
-    m.buffers.push_back(b);
-  }
-  const auto& arr = as_arr(member(j, "admissions", "manifest"), "admissions");
-  if (arr.empty()) fail("admissions: empty");
-  for (size_t i = 0; i < arr.size(); ++i) {
-    const Json& x = arr[i];
-    const std::string where = "admissions[" + std::to_string(i) + "]";
-    Admission a;
-    a.name = as_str(member(x, "name", where), where + ".name");
-    if (m.adm_idx.count(a.name)) fail("%s: duplicate admission name '%s'", where.c_str(), a.name.c_str());
-    a.workload = as_str(member(x, "workload", where), where + ".workload");
-    auto wi = m.wl_idx.find(a.workload);
-    if (wi == m.wl_idx.end()) fail("%s (%s): unknown workload '%s'", where.c_str(), a.name.c_str(), a.workload.c_str());
-    const std::string w2 = "admission " + a.name;
-    if (const Json* v = x.get("after_bundles")) for (auto& s : as_arr(*v, w2 + ".after_bundles")) a.after.push_back(as_str(s, w2 + ".after_bundles[]"));
-    if (const Json* v = x.get("when"))
-      for (auto& c : as_arr(*v, w2 + ".when")) {
-        Cond cd;
-        cd.var = as_str(member(c, "var", w2 + ".when[]"), w2 + ".when.var");
-        cd.mn = as_int(member(c, "min", w2 + ".when[]"), w2 + ".when.min", 0, INT_MAX / 2);
-        if (const Json* mx = c.get("max")) {
-          cd.mx = as_int(*mx, w2 + ".when.max", 0, INT_MAX / 2);
-          if (cd.mx < cd.mn) fail("%s: when %s has max %lld < min %lld (can never hold)", w2.c_str(), cd.var.c_str(), cd.mx, cd.mn);
-        }
-        a.when.push_back(cd);
-      }
-    if (const Json* t = x.get("at_us")) if (!is_null(t)) a.at_us = as_int(*t, w2 + ".at_us", 0, 1ll << 50);
-    a.base = as_versions(x.get("base_versions"), w2 + ".base_versions");
-    a.publishes = as_versions(x.get("publishes"), w2 + ".publishes");
-    if (const Json* bd = x.get("bundle_dir")) if (!is_null(bd)) a.bundle_dir = as_rel_path(*bd, w2 + ".bundle_dir");
-    if (const Json* cp = x.get("compile")) if (!is_null(cp)) {
-      a.compile_workload = as_rel_path(member(*cp, "workload", w2 + ".compile"), w2 + ".compile.workload");
-      a.compile_data_dir = cp->get("data_dir") ? as_rel_path(*cp->get("data_dir"), w2 + ".compile.data_dir") : ".";
-      as_versions(cp->get("base_versions"), w2 + ".compile.base_versions");   // checked; the admission's own base is used
-    }
-    const Workload& w = m.workloads[wi->second];
-    auto declared = [&](const std::string& v) { return std::find(w.variables.begin(), w.variables.end(), v) != w.variables.end(); };
-    for (auto& kv : a.publishes) {
-      m.var_id(kv.first, w2 + ".publishes");
-      if (!declared(kv.first)) fail("%s publishes '%s', which its workload does not declare", w2.c_str(), kv.first.c_str());
-      if (!a.base.count(kv.first)) fail("%s publishes '%s' but has no base version for it", w2.c_str(), kv.first.c_str());
-    }
-    for (auto& kv : a.base) m.var_id(kv.first, w2 + ".base_versions");
-    for (auto& c : a.when) m.var_id(c.var, w2 + ".when");
-    m.adm_idx[a.name] = (int)m.adms.size();
-    m.adms.push_back(a);
-  }
-  for (auto& a : m.adms)
-    for (auto& d : a.after) {
-      if (!m.adm_idx.count(d)) fail("admission %s: after_bundles names unknown admission '%s'", a.name.c_str(), d.c_str());
-      if (d == a.name) fail("admission %s waits for itself", a.name.c_str());
-    }
-  for (auto& b : m.buffers)
-    if (std::none_of(m.adms.begin(), m.adms.end(), [&](const Admission& a) { return a.workload == b.owner; }))
-      fail("buffer %s: owner workload '%s' has no admission", b.name.c_str(), b.owner.c_str());
-  return m;
+  return out;
 }
 
-// ---------------------------------------------------------------------------------------------- serial simulation
-bool conds_hold(const Admission& a, const std::vector<long long>& live, const Manifest& m) {
-  for (auto& c : a.when) {
-    const long long v = live[m.var_idx.at(c.var)];
-    if (v < c.mn || v > c.mx) return false;
-  }
-  return true;
-}
-// One admission at a time, the first (in manifest order) whose conditions hold, time conditions ignored; a
-// publishing admission moves its variables from its base to the published versions. Fails with the reason for every
-// admission that no order reaches.
-std::vector<std::string> simulate(const Manifest& m) {
-  std::vector<long long> live(m.vars.size(), 0);
-  std::vector<char> done(m.adms.size(), 0);
-  std::vector<std::string> order;
-  for (size_t left = m.adms.size(); left > 0; --left) {
-    int pick = -1;
-    for (size_t i = 0; i < m.adms.size() && pick < 0; ++i) {
-      const Admission& a = m.adms[i];
-      if (done[i]) continue;
-      bool ok = conds_hold(a, live, m);
-      for (auto& d : a.after) ok = ok && done[m.adm_idx.at(d)];
-      for (auto& kv : a.publishes) ok = ok && live[m.var_idx.at(kv.first)] == a.base.at(kv.first);
-      if (ok) pick = (int)i;
-    }
-    if (pick < 0) {
-      std::string why;
-      for (size_t i = 0; i < m.adms.size(); ++i) {
-        if (done[i]) continue;
-        const Admission& a = m.adms[i];
-        why += "\n  " + a.name + ":";
-        for (auto& d : a.after) if (!done[m.adm_idx.at(d)]) why += " waits for bundle " + d + ";";
-        for (auto& c : a.when) {
-          const long long v = live[m.var_idx.at(c.var)];
-          if (v < c.mn || v > c.mx)
-            why += " needs " + c.var + " in [" + std::to_string(c.mn) + "," + (c.mx == LLONG_MAX ? "inf" : std::to_string(c.mx)) + "] but it is " + std::to_string(v) + ";";
-        }
-        for (auto& kv : a.publishes) {
-          const long long v = live[m.var_idx.at(kv.first)];
-          if (v != a.base.at(kv.first)) why += " compiled for " + kv.first + "=" + std::to_string(a.base.at(kv.first)) + " but the flow gives " + std::to_string(v) + ";";
-        }
+Plan read_plan(const std::string& root) {
+  Plan p;
+  p.root = root;
+  const Json doc = Parser(read_file(root + "/MANIFEST.json")).parse();
+  const Node top(&doc, "$");
+  if (top.field("manifest_version").whole(LLONG_MIN / 2, LLONG_MAX / 2) != 1)
+    refuse("$.manifest_version", "this runner reads manifest_version 1");
+
+  if (const Node cls = top.opt("classes"); cls.given())
+    for (auto& [cname, params] : cls.members()) {
+      auto& dst = p.classes[cname];
+      for (auto& [key, val] : params.members()) {
+        bool known = false;
+        for (const char* k : kClassParams) known = known || key == k;
+        if (!known) refuse(val.path(), "\"" + key + "\" is not a scheduler class parameter (weight, min_cta, max_cta, bw_cta, urgent_us)");
+        dst[key] = val.whole(key == "weight" ? 1 : 0, INT_MAX);
       }
-      fail("the manifest cannot complete (%zu of %zu admissions run in the serial simulation):%s", order.size(), m.adms.size(), why.c_str());
     }
-    done[pick] = 1;
-    order.push_back(m.adms[pick].name);
-    for (auto& kv : m.adms[pick].publishes) live[m.var_idx.at(kv.first)] = kv.second;
+
+  const auto wls = top.field("workloads").members();
+  if (wls.empty()) refuse("$.workloads", "declares no workload");
+  for (auto& [wname, w] : wls) {
+    WorkloadDecl d;
+    d.name = wname;
+    w.field("file").inner_path();
+    w.field("tasks").whole(1, INT_MAX);
+    w.field("edges").whole(0, INT_MAX);
+    w.field("priority").whole(0, 1 << 20);
+    d.cls = w.opt("class").given() ? w.opt("class").text() : "default";
+    if (const Node vs = w.opt("variables"); vs.given())
+      for (const Node& v : vs.items()) {
+        const std::string vn = v.text();
+        int id = p.var(vn);
+        if (id < 0) { id = (int)p.vars.size(); p.vars.push_back(vn); }
+        d.vars.push_back(id);
+      }
+    if (const Node req = w.opt("requirements"); req.given())
+      if (const Node res = req.opt("resources"); res.given() && !res.items().empty())
+        refuse(res.path(), "host resources are not provided by this runner (the game pack is not part of this build)");
+    p.workloads.push_back(d);
+  }
+
+  for (auto& [bname, b] : top.field("buffers").members()) {
+    BufferDecl d;
+    d.name = bname;
+    d.rows = (int)b.field("rows").whole(1, INT_MAX);
+    d.cols = (int)b.field("cols").whole(1, INT_MAX);
+    const std::string dt = b.field("dtype").text();
+    d.dtype = dt == "f32" ? 0 : dt == "i32" ? 1 : dt == "bf16" ? 2 : -1;
+    if (d.dtype < 0) refuse(b.path() + ".dtype", "\"" + dt + "\" is not one of f32, i32, bf16");
+    if ((long long)d.rows * d.cols > (long long)INT_MAX) refuse(b.path(), "more than 2^31-1 elements");
+    d.owner = b.field("owner").text();
+    if (p.workload(d.owner) < 0) refuse(b.path() + ".owner", "no workload is called \"" + d.owner + "\"");
+    p.buffers.push_back(d);
+  }
+
+  const std::vector<Node> list = top.field("admissions").items();
+  if (list.empty()) refuse("$.admissions", "lists no admission");
+  std::vector<std::vector<std::string>> after_names(list.size());
+  for (size_t i = 0; i < list.size(); ++i) {
+    const Node& x = list[i];
+    AdmissionDecl a;
+    a.name = x.field("name").text();
+    if (p.admission(a.name) >= 0) refuse(x.path() + ".name", "\"" + a.name + "\" names an earlier admission too");
+    const std::string wl = x.field("workload").text();
+    a.workload = p.workload(wl);
+    if (a.workload < 0) refuse(x.path() + ".workload", "no workload is called \"" + wl + "\"");
+    if (const Node ab = x.opt("after_bundles"); ab.given()) for (const Node& n : ab.items()) after_names[i].push_back(n.text());
+    if (const Node wh = x.opt("when"); wh.given())
+      for (const Node& c : wh.items()) {
+        const std::string vn = c.field("var").text();
+        Window win{p.var(vn), c.field("min").whole(0, kMaxVersion), LLONG_MAX};
+        if (win.var < 0) refuse(c.path() + ".var", "\"" + vn + "\" is not a variable any workload declares");
+        if (c.opt("max").given()) win.hi = c.opt("max").whole(0, kMaxVersion);
+        if (win.hi < win.lo) refuse(c.path(), "max " + std::to_string(win.hi) + " below min " + std::to_string(win.lo) + ": the window is empty");
+        a.when.push_back(win);
+      }
+    if (const Node t = x.opt("at_us"); t.given()) a.at_us = t.whole(0, 1ll << 50);
+    a.base = read_versions(x.opt("base_versions"), p, false);
+    a.advance = read_versions(x.opt("publishes"), p, true);
+    if (const Node bd = x.opt("bundle_dir"); bd.given()) a.bundle_dir = bd.inner_path();
+    if (const Node cp = x.opt("compile"); cp.given()) {
+      a.compile_file = cp.field("workload").inner_path();
+      a.compile_data = cp.opt("data_dir").given() ? cp.opt("data_dir").inner_path() : ".";
+      read_versions(cp.opt("base_versions"), p, false);    // shape-checked; the admission's own base versions are used
+    }
+    const WorkloadDecl& w = p.workloads[a.workload];
+    for (const VarVersion& pv : a.advance) {
+      const std::string& vn = p.vars[pv.var];
+      if (std::find(w.vars.begin(), w.vars.end(), pv.var) == w.vars.end())
+        refuse(x.path() + ".publishes." + vn, "workload \"" + w.name + "\" does not declare the variable");
+      if (a.base_of(pv.var) < 0) refuse(x.path() + ".publishes." + vn, "a published variable needs an entry in base_versions");
+    }
+    p.adms.push_back(a);
+  }
+  for (size_t i = 0; i < list.size(); ++i)
+    for (const std::string& n : after_names[i]) {
+      const int j = p.admission(n);
+      if (j < 0) refuse(list[i].path() + ".after_bundles", "no admission is called \"" + n + "\"");
+      if (j == (int)i) refuse(list[i].path() + ".after_bundles", "the admission lists itself");
+      p.adms[i].after.push_back(j);
+    }
+  for (const BufferDecl& b : p.buffers) {
+    const int w = p.workload(b.owner);
+    if (std::none_of(p.adms.begin(), p.adms.end(), [&](const AdmissionDecl& a) { return a.workload == w; }))
+      refuse("$.buffers." + b.name, "its owner \"" + b.owner + "\" is never admitted, so nothing initialises it");
+  }
+  return p;
+}
+
+// ================================================================================================ the admission gate
+// The state the gate looks at. `now_us` < 0 ignores time conditions (the dry run).
+struct Flow {
+  std::vector<long long> live;        // per variable
+  std::vector<char> finished, in_flight;
+  double now_us = -1;
+};
+
+struct Gate {
+  bool open = true;                   // may be submitted now
+  bool dead = false;                  // can never open again (a window passed, or a base version overtaken)
+  std::string why;                    // what keeps it closed
+  void close(const std::string& r, bool fatal = false) { open = false; dead = dead || fatal; why += (why.empty() ? "" : "; ") + r; }
+};
+
+// One gate for the dry run and the live loop, so both apply exactly the same rules.
+Gate gate(const Plan& p, int ai, const Flow& f) {
+  const AdmissionDecl& a = p.adms[ai];
+  Gate g;
+  if (f.now_us >= 0 && a.at_us >= 0 && f.now_us < (double)a.at_us) g.close("starts at " + std::to_string(a.at_us) + " us");
+  for (int d : a.after)
+    if (!f.finished[d]) g.close("after " + p.adms[d].name);
+  for (const Window& w : a.when) {
+    const long long v = f.live[w.var];
+    if (v < w.lo || v > w.hi)
+      g.close(p.vars[w.var] + " is " + std::to_string(v) + ", window [" + std::to_string(w.lo) + ", " +
+              (w.hi == LLONG_MAX ? std::string("any") : std::to_string(w.hi)) + "]", v > w.hi);
+  }
+  for (const VarVersion& pv : a.advance) {
+    const long long v = f.live[pv.var], b = a.base_of(pv.var);
+    if (v != b) g.close("built for " + p.vars[pv.var] + " = " + std::to_string(b) + ", live " + std::to_string(v), v > b);
+    for (size_t j = 0; j < p.adms.size(); ++j)
+      if ((int)j != ai && f.in_flight[j] && p.adms[j].publishes(pv.var)) { g.close(p.vars[pv.var] + " is being published by " + p.adms[j].name); break; }
+  }
+  return g;
+}
+
+void complete(const Plan& p, int ai, Flow& f) {
+  for (const VarVersion& pv : p.adms[ai].advance) f.live[pv.var] += pv.v;
+  f.finished[ai] = 1;
+}
+
+// Serial run of the version flow: repeatedly the first admission (manifest order) whose gate is open. Returns the
+// order, or refuses with every waiting admission's reason when the flow gets stuck.
+std::vector<int> dry_run(const Plan& p) {
+  Flow f;
+  f.live.assign(p.vars.size(), 0);
+  f.finished.assign(p.adms.size(), 0);
+  f.in_flight.assign(p.adms.size(), 0);
+  std::vector<int> order;
+  while (order.size() < p.adms.size()) {
+    int next = -1;
+    for (size_t i = 0; i < p.adms.size() && next < 0; ++i)
+      if (!f.finished[i] && gate(p, (int)i, f).open) next = (int)i;
+    if (next < 0) {
+      std::string stuck;
+      for (size_t i = 0; i < p.adms.size(); ++i)
+        if (!f.finished[i]) stuck += "\n  " + p.adms[i].name + ": " + gate(p, (int)i, f).why;
+      refuse("version flow", "stuck after " + std::to_string(order.size()) + " of " + std::to_string(p.adms.size()) +
+                             " admissions in the serial order; waiting:" + stuck);
+    }
+    order.push_back(next);
+    complete(p, next, f);
   }
   return order;
 }
 
-// ---------------------------------------------------------------------------------------------- bundles
-struct Bundle {
-  std::vector<MvmTaskDesc> t; std::vector<int32_t> s, a;
-  Json meta; std::string dir;
-  std::map<int, std::string> var_name;   // local id -> name
-  VerMap var_base;                       // variable -> base version the bundle was compiled for
-  std::map<int, std::string> buf_name;   // local index -> name
+// ================================================================================================ bundles
+// One bundle as read from disk, with its local buffer and variable tables.
+struct Program {
+  std::string dir;
+  Json meta;
+  std::vector<MvmTaskDesc> tasks;
+  std::vector<int32_t> succ, args;
+  std::map<int, std::string> local_var;          // local variable id -> name
+  std::map<std::string, long long> built_for;    // variable name -> base version the bundle was compiled with
+  std::map<int, std::string> local_buf;          // local buffer index -> name
+  std::string origin;                            // how the runner obtained it (summary.json)
 };
 
-Bundle read_bundle(const std::string& dir) {
-  Bundle r; r.dir = dir;
-  r.meta = Parser(read_file(dir + "/metadata.json")).parse();
-  if (as_int(member(r.meta, "abi_version", dir), dir + ".abi_version") != MVM_ABI_VERSION) fail("%s: abi_version is not %d", dir.c_str(), MVM_ABI_VERSION);
-  const long long nt = as_int(member(r.meta, "task_count", dir), dir + ".task_count", 1, INT_MAX);
-  const long long ne = as_int(member(r.meta, "edge_count", dir), dir + ".edge_count", 0, INT_MAX);
-  const long long nw = as_int(member(r.meta, "args_words", dir), dir + ".args_words", 0, INT_MAX);
-  r.t = read_bin<MvmTaskDesc>(dir + "/tasks.bin");
-  r.s = read_bin<int32_t>(dir + "/successors.bin");
-  r.a = read_bin<int32_t>(dir + "/args.bin");
-  if ((long long)r.t.size() != nt || (long long)r.s.size() != ne || (long long)r.a.size() != nw) fail("%s: binary files do not match the metadata counts", dir.c_str());
-  for (auto& v : as_arr(member(r.meta, "variables", dir), dir + ".variables")) {
-    const std::string& nm = as_str(member(v, "name", dir), dir + ".variables.name");
-    r.var_name[(int)as_int(member(v, "id", dir), dir + ".variables.id", 0, 1 << 20)] = nm;
-    r.var_base[nm] = as_int(member(v, "base_version", dir), dir + ".variables.base_version", 0, INT_MAX / 2);
+Program load_program(const std::string& dir) {
+  Program g;
+  g.dir = dir;
+  g.meta = Parser(read_file(dir + "/metadata.json")).parse();
+  const Node m(&g.meta, dir + "/metadata.json");
+  if (m.field("abi_version").whole(0, INT_MAX) != MVM_ABI_VERSION) refuse(m.path(), "abi_version is not " + std::to_string(MVM_ABI_VERSION));
+  const long long nt = m.field("task_count").whole(1, INT_MAX), ne = m.field("edge_count").whole(0, INT_MAX), nw = m.field("args_words").whole(0, INT_MAX);
+  g.tasks = read_bin<MvmTaskDesc>(dir + "/tasks.bin");
+  g.succ = read_bin<int32_t>(dir + "/successors.bin");
+  g.args = read_bin<int32_t>(dir + "/args.bin");
+  if ((long long)g.tasks.size() != nt || (long long)g.succ.size() != ne || (long long)g.args.size() != nw)
+    refuse(dir, "tasks.bin / successors.bin / args.bin sizes disagree with task_count / edge_count / args_words");
+  for (const Node& v : m.field("variables").items()) {
+    const std::string name = v.field("name").text();
+    g.local_var[(int)v.field("id").whole(0, 1 << 20)] = name;
+    g.built_for[name] = v.field("base_version").whole(0, kMaxVersion);
   }
-  const auto& bufs = as_arr(member(r.meta, "buffers", dir), dir + ".buffers");
+  const std::vector<Node> bufs = m.field("buffers").items();
   for (size_t i = 0; i < bufs.size(); ++i) {
-    const Json* ix = bufs[i].get("index");
-    r.buf_name[ix ? (int)as_int(*ix, dir + ".buffers.index", 0, 1 << 24) : (int)i] = as_str(member(bufs[i], "name", dir), dir + ".buffers.name");
+    const int idx = bufs[i].opt("index").given() ? (int)bufs[i].opt("index").whole(0, 1 << 24) : (int)i;
+    g.local_buf[idx] = bufs[i].field("name").text();
   }
-  return r;
+  return g;
 }
 
-// Version shift: a bundle compiled with base b for a variable it publishes is the same program with every wait and
-// publish of that variable moved by (target - b), valid when no read of that variable is by absolute version (the
-// metadata lists the reads). Returns "" when applied, else the reason it does not apply.
-std::string rebase(Bundle& r, const VerMap& to) {
-  std::map<int, long long> shift;
-  for (auto& kv : r.var_name) {
-    bool published = false;
-    for (auto& t : r.t) if (t.pub_var == kv.first) { published = true; break; }
-    if (!published) continue;
-    auto f = r.var_base.find(kv.second);
-    auto g = to.find(kv.second);
-    if (f == r.var_base.end() || g == to.end()) return "no base version for published variable " + kv.second;
-    if (g->second == f->second) continue;
-    if (const Json* reads = r.meta.get("reads"))
-      for (auto& rd : reads->a)
-        if (rd.get("var") && (int)rd.get("var")->n == kv.first) return "the bundle reads " + kv.second + " by absolute version";
-    shift[kv.first] = g->second - f->second;
+// Local variable ids a bundle publishes (some task has pub_var = id).
+std::set<int> published_ids(const Program& g) {
+  std::set<int> s;
+  for (const MvmTaskDesc& t : g.tasks) if (t.pub_var >= 0) s.insert(t.pub_var);
+  return s;
+}
+
+// Moves every wait and publication of the variables the bundle publishes from the base it was built for to the
+// admission's base. Returns an empty string when done, else why the bundle cannot be moved (it then stays as is).
+std::string shift_to(Program& g, const std::map<std::string, long long>& target) {
+  std::map<int, long long> delta;
+  std::set<int> absolute_reads;
+  if (const Json* reads = g.meta.get("reads"))
+    for (const Json& r : reads->a) if (const Json* v = r.get("var")) absolute_reads.insert((int)v->n);
+  for (int id : published_ids(g)) {
+    auto nm = g.local_var.find(id);
+    if (nm == g.local_var.end()) return "a task publishes undeclared local variable " + std::to_string(id);
+    auto want = target.find(nm->second);
+    if (want == target.end()) return "no base version given for published variable " + nm->second;
+    const long long d = want->second - g.built_for[nm->second];
+    if (d == 0) continue;
+    if (absolute_reads.count(id)) return nm->second + " is read at an absolute version inside the bundle";
+    delta[id] = d;
   }
-  for (auto& kv : shift) r.var_base[r.var_name.at(kv.first)] = to.at(r.var_name.at(kv.first));
-  for (auto& t : r.t) {
-    auto p = shift.find(t.pub_var);
-    if (t.pub_var >= 0 && p != shift.end()) { t.pub_ver += (int)p->second; if (t.pub_ver < 1) return "shifted publish version below 1"; }
-    auto w = shift.find(t.wait_var);
-    if (t.wait_var >= 0 && w != shift.end()) { t.wait_ver += (int)w->second; if (t.wait_ver < 0) return "shifted wait version below 0"; }
+  std::vector<MvmTaskDesc> moved = g.tasks;
+  for (MvmTaskDesc& t : moved) {
+    if (auto it = delta.find(t.pub_var); t.pub_var >= 0 && it != delta.end()) {
+      t.pub_ver += (int)it->second;
+      if (t.pub_ver < 1) return "a publication would move below version 1";
+    }
+    if (auto it = delta.find(t.wait_var); t.wait_var >= 0 && it != delta.end()) {
+      t.wait_ver += (int)it->second;
+      if (t.wait_ver < 0) return "a wait would move below version 0";
+    }
   }
+  g.tasks.swap(moved);
+  for (auto& [id, d] : delta) g.built_for[g.local_var[id]] += d;
   return "";
 }
 
-// Buffer-argument positions of every registry operator.
-const std::map<int, std::vector<std::pair<bool, bool>>>& registry_args() {   // id -> per argument (is buffer, optional)
-  static std::map<int, std::vector<std::pair<bool, bool>>> m;
-  if (m.empty()) {
-    struct Op { int id; const char* sig; };
-    static const Op ops[] = {
+// The admission's declared publications against the bundle: each published variable's last version must be its base
+// plus the declared increment, and a bundle may publish nothing its admission does not declare (the runner's
+// in-flight exclusion and the version flow rest on that).
+void check_publications(const Program& g, const AdmissionDecl& a, const Plan& p) {
+  std::map<std::string, int> last;
+  for (const MvmTaskDesc& t : g.tasks)
+    if (t.pub_var >= 0) {
+      const std::string& n = g.local_var.at(t.pub_var);
+      last[n] = std::max(last.count(n) ? last[n] : 0, (int)t.pub_ver);
+    }
+  for (auto& [name, top] : last) {
+    const int id = p.var(name);
+    if (id < 0 || !a.publishes(id)) refuse("admission " + a.name, "its bundle publishes " + name + ", which the admission's publishes does not declare");
+  }
+  for (const VarVersion& pv : a.advance) {
+    const std::string& name = p.vars[pv.var];
+    const long long want = a.base_of(pv.var) + pv.v;
+    auto it = last.find(name);
+    if (it == last.end()) refuse("admission " + a.name, "declares publishes " + name + " +" + std::to_string(pv.v) + " but its bundle publishes no version of it");
+    if (it->second != want)
+      refuse("admission " + a.name, "its bundle leaves " + name + " at " + std::to_string(it->second) + ", the manifest says " +
+                                        std::to_string(a.base_of(pv.var)) + " + " + std::to_string(pv.v) + " = " + std::to_string(want));
+  }
+}
+
+// Operator id -> which argument words are buffer indices (first) and which of those may be -1 (second), from the
+// registry signatures.
+const std::map<int, std::vector<std::pair<bool, bool>>>& buffer_slots() {
+  static const std::map<int, std::vector<std::pair<bool, bool>>> table = [] {
+    std::map<int, std::vector<std::pair<bool, bool>>> m;
+    struct Sig { int id; const char* sig; };
+    static const Sig sigs[] = {
 #define X(n, id, sig) {id, sig},
 #include "../../include/mvm_ops_list.inc"
 #undef X
     };
-    for (const Op& o : ops) {
-      std::vector<std::pair<bool, bool>> v;
-      std::string s(o.sig);
-      size_t p = 0;
-      while (p < s.size()) {
-        size_t e = s.find(',', p); if (e == std::string::npos) e = s.size();
-        const std::string ty = s.substr(s.find(':', p) + 1, e - s.find(':', p) - 1);
-        v.push_back({ty == "buf" || ty == "buf?", ty == "buf?"});
-        p = e + 1;
+    for (const Sig& s : sigs) {
+      auto& v = m[s.id];
+      std::string rest(s.sig);
+      while (!rest.empty()) {
+        const size_t comma = rest.find(',');
+        const std::string item = rest.substr(0, comma);
+        const std::string type = item.substr(item.find(':') + 1);
+        v.push_back({type == "buf" || type == "buf?", type == "buf?"});
+        rest = comma == std::string::npos ? "" : rest.substr(comma + 1);
       }
-      m[o.id] = v;
     }
-  }
-  return m;
+    return m;
+  }();
+  return table;
 }
 
-// Local buffer and variable ids to the manifest's global tables.
-void remap(Bundle& r, const Manifest& m, const std::string& what) {
-  std::map<int, int> bmap, vmap;
-  for (auto& kv : r.buf_name) {
-    auto it = m.buf_idx.find(kv.second);
-    if (it == m.buf_idx.end()) fail("%s: buffer '%s' is not in manifest.buffers", what.c_str(), kv.second.c_str());
-    bmap[kv.first] = it->second;
+// Rewrites the bundle's local buffer and variable ids into the manifest's global tables.
+void bind_globals(Program& g, const Plan& p, const std::string& who) {
+  std::map<int, int> buf, var;
+  for (auto& [local, name] : g.local_buf) {
+    buf[local] = p.buffer(name);
+    if (buf[local] < 0) refuse(who, "bundle buffer \"" + name + "\" is not declared in $.buffers");
   }
-  for (auto& kv : r.var_name) vmap[kv.first] = m.var_id(kv.second, what);
-  const auto& reg = registry_args();
-  for (size_t i = 0; i < r.t.size(); ++i) {
-    MvmTaskDesc& t = r.t[i];
-    auto op = reg.find(t.op_id);
-    if (op == reg.end()) fail("%s: task %zu: op id %d is not in the operator registry", what.c_str(), i, t.op_id);
-    if (t.args_words != (int)op->second.size() || t.args_off < 0 || (long long)t.args_off + t.args_words > (long long)r.a.size())
-      fail("%s: task %zu: bad argument range", what.c_str(), i);
+  for (auto& [local, name] : g.local_var) {
+    var[local] = p.var(name);
+    if (var[local] < 0) refuse(who, "bundle variable \"" + name + "\" is not declared by any workload");
+  }
+  const auto& slots = buffer_slots();
+  for (size_t i = 0; i < g.tasks.size(); ++i) {
+    MvmTaskDesc& t = g.tasks[i];
+    const std::string at = who + ", task " + std::to_string(i);
+    auto op = slots.find(t.op_id);
+    if (op == slots.end()) refuse(at, "operator id " + std::to_string(t.op_id) + " is not in the registry");
+    if (t.args_words != (int)op->second.size() || t.args_off < 0 || (long long)t.args_off + t.args_words > (long long)g.args.size())
+      refuse(at, "argument words outside args.bin or not the operator's arity");
     for (int k = 0; k < t.args_words; ++k) {
       if (!op->second[k].first) continue;
-      int32_t& w = r.a[t.args_off + k];
+      int32_t& w = g.args[t.args_off + k];
       if (w == -1 && op->second[k].second) continue;
-      auto it = bmap.find(w);
-      if (it == bmap.end()) fail("%s: task %zu arg %d: local buffer index %d is not in the bundle's buffer table", what.c_str(), i, k, w);
+      auto it = buf.find(w);
+      if (it == buf.end()) refuse(at, "argument " + std::to_string(k) + " names local buffer " + std::to_string(w) + ", absent from the bundle's table");
       w = it->second;
     }
     for (int32_t* v : {&t.wait_var, &t.pub_var}) {
       if (*v < 0) continue;
-      auto it = vmap.find(*v);
-      if (it == vmap.end()) fail("%s: task %zu: local version variable %d is not declared in the bundle", what.c_str(), i, *v);
+      auto it = var.find(*v);
+      if (it == var.end()) refuse(at, "local variable " + std::to_string(*v) + " is not in the bundle's table");
       *v = it->second;
     }
   }
 }
 
-// ---------------------------------------------------------------------------------------------- the run
+// ================================================================================================ the run
 struct Options {
-  std::string root, out, dump;
+  std::string root, out, dump, sched = "auto";
   int windows = 4, blocks = 0, timeout_s = 120;
   bool check_only = false, quiet = false;
 };
 
-enum class St { PENDING, SUBMITTED, DONE, FAILED };
-struct Runtime {
-  St st = St::PENDING;
-  std::vector<long long> wids;
-  int tasks = 0;
-  std::string how;
-  double t_submit = -1, t_done = -1;
-  std::vector<int> live_done;
+enum class Phase { WAITING, RUNNING, FINISHED, FAILED };
+struct Track {
+  Phase phase = Phase::WAITING;
+  std::vector<long long> windows;     // window ids of its submission
+  double submitted_us = -1, done_us = -1;
+  std::vector<int32_t> live_at_done;
 };
 
-class Runner {
+class ManifestRun {
  public:
-  Runner(Manifest m, Options o) : m_(std::move(m)), o_(std::move(o)) {}
+  ManifestRun(Plan p, Options o) : p_(std::move(p)), o_(std::move(o)) {}
+  ~ManifestRun() {
+    for (const std::string& d : scratch_dirs_)
+      nftw(d.c_str(), [](const char* f, const struct stat*, int, struct FTW*) { return remove(f); }, 16, FTW_DEPTH | FTW_PHYS);
+  }
 
-  int run() {
-    order_ = simulate(m_);
-    load_bundles();
+  int go() {
+    if (!p_.classes.empty() && o_.sched != "off") {
+      std::string names;
+      for (auto& c : p_.classes) names += (names.empty() ? "" : ", ") + c.first;
+      refuse("$.classes", "declares scheduler classes (" + names + "); stream mode schedules first-come first-served, "
+                          "so this runner applies no classes: pass --sched off to run the manifest that way");
+    }
+    prepare_programs();
+    order_ = dry_run(p_);
     if (o_.check_only) {
-      printf("OK: manifest, %zu bundles and the version flow are consistent (serial order %s ... %s)\n", m_.adms.size(), order_.front().c_str(), order_.back().c_str());
+      printf("OK: %zu admissions, bundles and version flow consistent; serial order %s",
+             p_.adms.size(), p_.adms[order_.front()].name.c_str());
+      for (size_t i = 1; i < order_.size(); ++i) printf(" %s", p_.adms[order_[i]].name.c_str());
+      printf("\n");
       return 0;
     }
     if (!o_.out.empty()) mkdir(o_.out.c_str(), 0755);
-    KvmConfig cfg; kvm_config_default(&cfg);
-    size_t max_t = 1, max_e = 1;
-    for (auto& b : bundles_) { max_t = std::max(max_t, b->t.size()); max_e = std::max(max_e, b->s.size()); }
-    int wt = 256;
-    while ((size_t)wt < max_t && wt < (1 << 16)) wt <<= 1;
-    cfg_tasks_ = wt;                                    // a bundle above a window streams in windows
-    cfg_edges_ = (int)std::min<size_t>(std::max<size_t>(max_e, 1024), (size_t)1 << 22);
-    cfg.window_cap = o_.windows; cfg.window_tasks = cfg_tasks_; cfg.window_edges = cfg_edges_;
-    cfg.num_vars = std::max<int>(1, (int)m_.vars.size());
-    cfg.blocks = o_.blocks; cfg.trace_on = 0;
-    cfg.timeout_us = (unsigned long long)o_.timeout_s * 1000000ull;
-    cfg.backpressure_ms = o_.timeout_s * 1000;
-    ex_.reset(kvm_create(&cfg));
-    if (!ex_) fail("kvm_create: %s", kvm_last_error(nullptr));
-    allocate_buffers();
-    if (kvm_start(ex_.get()) < 0) fail("kvm_start: %s", kvm_last_error(ex_.get()));
-    t0_ = std::chrono::steady_clock::now();
-    bool ok = loop();
+    launch();
+    const bool drove = drive();
     kvm_close(ex_.get());
     KvmResult r{};
-    const int frc = kvm_finish(ex_.get(), &r);
-    ok = ok && frc == 0 && r.err_code == 0;
+    const bool ok = drove && kvm_finish(ex_.get(), &r) == 0 && r.err_code == 0;
     if (r.err_code && !o_.quiet) fprintf(stderr, "device error %d at task %d (a=%d b=%d)\n", r.err_code, r.err_slot, r.err_a, r.err_b);
-    if (!errors_.empty() && !o_.quiet) fprintf(stderr, "%s", errors_.c_str());
-    if (!o_.out.empty()) { write_summary(r, ok); dump_buffers(); }
-    printf("%s: %d/%d tasks, %.3f ms, %zu admissions\n", ok ? "OK" : "FAIL", r.done, r.admitted, r.kernel_ms, m_.adms.size());
+    if (!problems_.empty() && !o_.quiet) fprintf(stderr, "%s", problems_.c_str());
+    if (!o_.out.empty()) { write_summary(r, ok); write_dumps(); }
+    printf("%s: %d/%d tasks, %.3f ms, %zu admissions\n", ok ? "OK" : "FAIL", r.done, r.admitted, r.kernel_ms, p_.adms.size());
     return ok ? 0 : 1;
   }
 
  private:
-  Manifest m_; Options o_;
+  Plan p_;
+  Options o_;
+  std::vector<int> order_;
+  std::vector<Program> progs_;                   // per admission, bound to the global tables
+  std::vector<Track> track_;
+  std::vector<std::string> scratch_dirs_;
   std::unique_ptr<KvmExec, void (*)(KvmExec*)> ex_{nullptr, kvm_destroy};
-  std::vector<std::unique_ptr<Bundle>> bundles_;   // per admission, remapped
-  std::vector<std::string> how_;
-  std::vector<Runtime> rt_;
-  std::vector<std::string> order_;
   std::chrono::steady_clock::time_point t0_;
-  std::string errors_;
-  long long next_wid_ = 0;                            // window ids are consecutive: this runner is the only submitter
-  int cfg_tasks_ = 0, cfg_edges_ = 0;                 // window slot size
+  std::string problems_;
+  long long window_serial_ = 0;                  // the runner is the only submitter, so window ids are consecutive
+  int slot_tasks_ = 0, slot_edges_ = 0;
 
-  double now_us() const { return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0_).count(); }
-  bool exists(const std::string& f) const { struct stat sb; return stat(f.c_str(), &sb) == 0; }
+  double elapsed_us() const { return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0_).count(); }
+  static bool has_file(const std::string& f) { struct stat sb; return stat(f.c_str(), &sb) == 0; }
 
-  std::vector<std::string> scratch_;                  // directories of bundles compiled on demand (removed at exit)
-
-  // Compiles an admission's workload file in-process (the same compiler as kvm_compile) for the admission's base
-  // versions into a scratch directory, so `file` initial values sit beside the bundle like a precompiled one's.
-  Bundle compile_admission(const Admission& a) {
-    if (a.compile_workload.empty()) fail("admission %s: no usable bundle and no compile entry", a.name.c_str());
-    char tmpl[] = "/tmp/kvm_run_compile.XXXXXX";
-    if (!mkdtemp(tmpl)) fail("admission %s: cannot create a scratch directory", a.name.c_str());
-    scratch_.push_back(tmpl);
-    const std::string data_dir = m_.root + "/" + a.compile_data_dir, out = std::string(tmpl);
+  // Compiles the admission's workload file for its base versions (the compiler kvm_compile links) into a scratch
+  // directory that receives the data files its `file` inits name, then loads it like a precompiled bundle.
+  Program compile_for(const AdmissionDecl& a) {
+    char dir_t[] = "/tmp/kvm_run_bundle.XXXXXX";
+    if (!mkdtemp(dir_t)) refuse("admission " + a.name, "no scratch directory for the on-demand compile");
+    const std::string dir = dir_t, data = p_.root + "/" + a.compile_data;
+    scratch_dirs_.push_back(dir);
     std::map<std::string, int> base;
-    for (auto& kv : a.base) base[kv.first] = (int)kv.second;
+    for (const VarVersion& b : a.base) base[p_.vars[b.var]] = (int)b.v;
+    auto save = [&](const std::string& rel, const void* bytes, size_t n) {
+      for (size_t k = rel.find('/'); k != std::string::npos; k = rel.find('/', k + 1)) mkdir((dir + "/" + rel.substr(0, k)).c_str(), 0777);
+      FILE* fp = fopen((dir + "/" + rel).c_str(), "wb");
+      const bool good = fp && (n == 0 || fwrite(bytes, 1, n, fp) == n);
+      if (fp && fclose(fp) != 0) refuse("admission " + a.name, "writing " + rel + " failed");
+      if (!good) refuse("admission " + a.name, "writing " + rel + " failed");
+    };
     try {
-      const std::string text = read_file(m_.root + "/" + a.compile_workload);
-      const kvmc::Bundle b = kvmc::compile(Parser(text).parse(), base, &data_dir);
-      auto put = [&](const std::string& f, const void* p, size_t n) {
-        FILE* fp = fopen((out + "/" + f).c_str(), "wb");
-        if (!fp || (n && fwrite(p, 1, n, fp) != n) || fclose(fp) != 0) fail("admission %s: cannot write %s", a.name.c_str(), f.c_str());
-      };
-      for (const std::string& f : b.files) {     // the file's directories, then the file
-        for (size_t k = f.find('/'); k != std::string::npos; k = f.find('/', k + 1)) mkdir((out + "/" + f.substr(0, k)).c_str(), 0777);
-        const std::string d = read_file(data_dir + "/" + f);
-        put(f, d.data(), d.size());
-      }
-      put("tasks.bin", b.tasks.data(), b.tasks.size() * sizeof(MvmTaskDesc));
-      put("successors.bin", b.succ.data(), b.succ.size() * 4);
-      put("args.bin", b.args.data(), b.args.size() * 4);
-      put("metadata.json", b.metadata.data(), b.metadata.size());
-    } catch (const ManifestError&) {
+      const kvmc::Bundle b = kvmc::compile(Parser(read_file(p_.root + "/" + a.compile_file)).parse(), base, &data);
+      for (const std::string& f : b.files) { const std::string bytes = read_file(data + "/" + f); save(f, bytes.data(), bytes.size()); }
+      save("tasks.bin", b.tasks.data(), b.tasks.size() * sizeof(MvmTaskDesc));
+      save("successors.bin", b.succ.data(), b.succ.size() * sizeof(int32_t));
+      save("args.bin", b.args.data(), b.args.size() * sizeof(int32_t));
+      save("metadata.json", b.metadata.data(), b.metadata.size());
+    } catch (const ManifestProblem&) {
       throw;
     } catch (const std::exception& e) {
-      fail("admission %s: compiling %s: %s", a.name.c_str(), a.compile_workload.c_str(), e.what());
+      refuse("admission " + a.name, "compiling " + a.compile_file + " failed: " + e.what());
     }
-    return read_bundle(out);
+    Program g = load_program(dir);
+    g.origin = "compiled on demand";
+    return g;
   }
 
- public:
-  ~Runner() {
-    for (auto& d : scratch_)
-      nftw(d.c_str(), [](const char* p, const struct stat*, int, struct FTW*) { return remove(p); }, 16, FTW_DEPTH | FTW_PHYS);
-  }
-
- private:
-  // Each admission's bundle, the first of: its own directory, the last bundle of the same workload, a compile of its
-  // workload file (the `compile` entry); the first two shifted when compiled for other base versions and skipped
-  // when no shift applies. Then remapped onto the global tables and validated against them.
-  void load_bundles() {
-    std::map<std::string, Bundle> last;   // workload -> last loaded bundle (local ids)
+  // A bundle per admission: its bundle_dir, else the workload's previous bundle, each moved to the admission's base
+  // versions when it was built for others; else a compile of its `compile` entry. Then checked and bound.
+  void prepare_programs() {
+    std::map<int, Program> previous;             // workload -> last bundle before binding
     std::vector<MvmBuf> table;
-    for (auto& b : m_.buffers) table.push_back(MvmBuf{nullptr, b.rows, b.cols, b.cols, b.dtype, {0, 0}});
-    for (auto& a : m_.adms) {
-      Bundle r;
-      std::string how;
+    for (const BufferDecl& b : p_.buffers) table.push_back(MvmBuf{nullptr, b.rows, b.cols, b.cols, b.dtype, {0, 0}});
+    for (const AdmissionDecl& a : p_.adms) {
+      const std::string who = "admission " + a.name;
+      std::map<std::string, long long> target;
+      for (const VarVersion& b : a.base) target[p_.vars[b.var]] = b.v;
+      std::vector<std::string> tried;
+      auto usable = [&](Program& g, const std::string& label) {
+        const std::string why = shift_to(g, target);
+        if (!why.empty()) { tried.push_back(label + ": " + why); return false; }
+        return true;
+      };
+      Program g;
       bool have = false;
-      auto needs_shift = [&](const Bundle& b) {
-        for (auto& kv : a.publishes) { auto f = b.var_base.find(kv.first); if (f == b.var_base.end() || f->second != a.base.at(kv.first)) return true; }
-        return false;
-      };
-      std::string why_not;
-      auto try_shift = [&](Bundle& t, const char* what) {
-        if (!needs_shift(t)) { how = what; return true; }
-        const std::string why = rebase(t, a.base);
-        if (why.empty()) { how = std::string(what) + ", versions shifted"; return true; }
-        why_not += std::string(" the ") + what + " bundle cannot be shifted to its base versions:" + why + ";";
-        return false;
-      };
-      if (!a.bundle_dir.empty() && exists(m_.root + "/" + a.bundle_dir + "/metadata.json")) {
-        Bundle t = read_bundle(m_.root + "/" + a.bundle_dir);
-        if (try_shift(t, "precompiled")) { r = std::move(t); have = true; }
+      if (!a.bundle_dir.empty() && has_file(p_.root + "/" + a.bundle_dir + "/metadata.json")) {
+        Program c = load_program(p_.root + "/" + a.bundle_dir);
+        const auto before = c.built_for;
+        if (usable(c, a.bundle_dir)) { g = std::move(c); g.origin = g.built_for == before ? "bundle_dir" : "bundle_dir, versions moved"; have = true; }
       }
-      if (!have && last.count(a.workload)) {
-        Bundle t = last.at(a.workload);
-        if (try_shift(t, "previous bundle of the workload")) { r = std::move(t); have = true; }
+      if (!have && previous.count(a.workload)) {
+        Program c = previous.at(a.workload);
+        const auto before = c.built_for;
+        if (usable(c, "previous bundle of " + p_.workloads[a.workload].name)) {
+          g = std::move(c);
+          g.origin = g.built_for == before ? "reused" : "reused, versions moved";
+          have = true;
+        }
       }
-      if (!have && !a.compile_workload.empty()) { r = compile_admission(a); how = "compiled on demand"; have = true; }
-      if (!have)
-        fail("admission %s: no bundle (bundle_dir '%s' missing or unusable, no usable earlier bundle of workload %s, no compile entry);%s",
-             a.name.c_str(), a.bundle_dir.c_str(), a.workload.c_str(), why_not.c_str());
-      last[a.workload] = r;
-      remap(r, m_, "admission " + a.name);
+      if (!have && !a.compile_file.empty()) { g = compile_for(a); have = true; }
+      if (!have) {
+        std::string detail;
+        for (const std::string& t : tried) detail += " [" + t + "]";
+        refuse(who, "no bundle: bundle_dir absent or unusable, no usable earlier bundle of its workload, no compile entry" + detail);
+      }
+      check_publications(g, a, p_);
+      previous[a.workload] = g;
+      bind_globals(g, p_, who);
       char err[1024] = {0};
-      if (kvm_validate(r.t.data(), (int)r.t.size(), r.s.data(), (int)r.s.size(), r.a.data(), (int)r.a.size(), table.data(), (int)table.size(),
-                       std::max<int>(1, (int)m_.vars.size()), err, sizeof err) < 0)
-        fail("admission %s: %s", a.name.c_str(), err);
-      bundles_.push_back(std::make_unique<Bundle>(std::move(r)));
-      how_.push_back(how);
+      if (kvm_validate(g.tasks.data(), (int)g.tasks.size(), g.succ.data(), (int)g.succ.size(), g.args.data(), (int)g.args.size(),
+                       table.data(), (int)table.size(), std::max<int>(1, (int)p_.vars.size()), err, sizeof err) < 0)
+        refuse(who, err);
+      progs_.push_back(std::move(g));
     }
   }
 
-  // Buffers are fixed at launch: each initialised from the bundle of the first admission of its owner workload.
-  void allocate_buffers() {
-    for (size_t bi = 0; bi < m_.buffers.size(); ++bi) {
-      const BufDecl& b = m_.buffers[bi];
+  // Creates the executor in stream mode (window slots sized to the largest bundle, up to 64K tasks; larger bundles
+  // stream through several windows), allocates and initialises every manifest buffer from its owner's first bundle,
+  // and starts the kernel.
+  void launch() {
+    size_t most_tasks = 1, most_edges = 1;
+    for (const Program& g : progs_) { most_tasks = std::max(most_tasks, g.tasks.size()); most_edges = std::max(most_edges, g.succ.size()); }
+    slot_tasks_ = 256;
+    while ((size_t)slot_tasks_ < most_tasks && slot_tasks_ < (1 << 16)) slot_tasks_ *= 2;
+    slot_edges_ = (int)std::min<size_t>(std::max<size_t>(most_edges, 1024), (size_t)1 << 22);
+    KvmConfig cfg;
+    kvm_config_default(&cfg);
+    cfg.window_cap = o_.windows;
+    cfg.window_tasks = slot_tasks_;
+    cfg.window_edges = slot_edges_;
+    cfg.num_vars = std::max<int>(1, (int)p_.vars.size());
+    cfg.blocks = o_.blocks;
+    cfg.trace_on = 0;
+    cfg.timeout_us = (unsigned long long)o_.timeout_s * 1000000ull;
+    cfg.backpressure_ms = o_.timeout_s * 1000;
+    ex_.reset(kvm_create(&cfg));
+    if (!ex_) refuse("executor", std::string("kvm_create: ") + kvm_last_error(nullptr));
+    for (size_t bi = 0; bi < p_.buffers.size(); ++bi) {
+      const BufferDecl& b = p_.buffers[bi];
+      const int owner = p_.workload(b.owner);
       size_t ai = 0;
-      while (m_.adms[ai].workload != b.owner) ++ai;
-      const Bundle& own = *bundles_[ai];
+      while (p_.adms[ai].workload != owner) ++ai;
       const Json* decl = nullptr;
-      for (auto& jb : own.meta.need("buffers").a) if (jb.get("name") && jb.get("name")->s == b.name) { decl = &jb; break; }
-      if (!decl) fail("buffer %s: its owner workload %s has no such buffer in its bundle", b.name.c_str(), b.owner.c_str());
-      const int rows = (int)decl->num("rows", 0), cols = (int)decl->num("cols", 0), dtype = (int)decl->num("dtype", 0);
-      if (rows != b.rows || cols != b.cols || dtype != b.dtype)
-        fail("buffer %s: manifest says %dx%d dtype %d, owner bundle %dx%d dtype %d", b.name.c_str(), b.rows, b.cols, b.dtype, rows, cols, dtype);
-      if (add_buffer_from_meta(ex_.get(), *decl, own.dir) != (int)bi) fail("buffer %s: index mismatch", b.name.c_str());
+      for (const Json& jb : progs_[ai].meta.need("buffers").a)
+        if (const Json* n = jb.get("name"); n && n->s == b.name) { decl = &jb; break; }
+      if (!decl) refuse("$.buffers." + b.name, "the bundle of owner " + b.owner + " does not declare it");
+      const int rows = (int)decl->num("rows", 0), cols = (int)decl->num("cols", 0), dt = (int)decl->num("dtype", 0);
+      if (rows != b.rows || cols != b.cols || dt != b.dtype)
+        refuse("$.buffers." + b.name, "manifest " + std::to_string(b.rows) + "x" + std::to_string(b.cols) + " dtype " + std::to_string(b.dtype) +
+                                      ", owner bundle " + std::to_string(rows) + "x" + std::to_string(cols) + " dtype " + std::to_string(dt));
+      if (add_buffer_from_meta(ex_.get(), *decl, progs_[ai].dir) != (int)bi) refuse("$.buffers." + b.name, "buffer index out of step");
     }
+    if (kvm_start(ex_.get()) < 0) refuse("executor", std::string("kvm_start: ") + kvm_last_error(ex_.get()));
+    t0_ = std::chrono::steady_clock::now();
   }
 
-  bool windows_done(const Runtime& r) const {
-    for (long long w : r.wids) if (kvm_window_done(ex_.get(), w) != 1) return false;
+  bool submit(int ai) {
+    const Program& g = progs_[ai];
+    Track& tr = track_[ai];
+    const int nt = (int)g.tasks.size(), ne = (int)g.succ.size(), na = (int)g.args.size();
+    int rc;
+    if (nt <= slot_tasks_ && ne <= slot_edges_) {
+      rc = kvm_submit(ex_.get(), g.tasks.data(), nt, g.succ.data(), ne, g.args.data(), na);
+      if (rc >= 0) tr.windows.push_back(window_serial_++);
+    } else {
+      rc = kvm_submit_stream(ex_.get(), g.tasks.data(), nt, g.succ.data(), ne, g.args.data(), na, 0, o_.timeout_s * 1000);
+      for (int k = 0; k < rc; ++k) tr.windows.push_back(window_serial_++);
+    }
+    if (rc < 0) {
+      problems_ += p_.adms[ai].name + ": submission refused: " + kvm_last_error(ex_.get()) + "\n";
+      tr.phase = Phase::FAILED;
+      return false;
+    }
+    tr.submitted_us = elapsed_us();
+    tr.phase = Phase::RUNNING;
+    if (!o_.quiet) fprintf(stderr, "[%10.0f us] submit %-16s %7d tasks (%s)\n", tr.submitted_us, p_.adms[ai].name.c_str(), nt, g.origin.c_str());
     return true;
   }
 
-  void submit(size_t i) {
-    Runtime& r = rt_[i];
-    const Bundle& b = *bundles_[i];
-    const int nt = (int)b.t.size(), ne = (int)b.s.size();
-    r.tasks = nt;
-    r.how = how_[i];
-    int rc;
-    if (nt <= cfg_tasks_ && ne <= cfg_edges_) {
-      rc = kvm_submit(ex_.get(), b.t.data(), nt, b.s.data(), ne, b.a.data(), (int)b.a.size());
-      if (rc >= 0) { r.wids.push_back(next_wid_++); }
-    } else {
-      rc = kvm_submit_stream(ex_.get(), b.t.data(), nt, b.s.data(), ne, b.a.data(), (int)b.a.size(), 0, o_.timeout_s * 1000);
-      if (rc >= 0) for (int k = 0; k < rc; ++k) r.wids.push_back(next_wid_++);
-    }
-    if (rc < 0) {
-      errors_ += m_.adms[i].name + ": submit failed: " + kvm_last_error(ex_.get()) + "\n";
-      r.st = St::FAILED;
-      return;
-    }
-    r.t_submit = now_us();
-    r.st = St::SUBMITTED;
-  }
-
-  bool loop() {
-    rt_.assign(m_.adms.size(), Runtime{});
-    const size_t nv = std::max<size_t>(1, m_.vars.size());
-    std::vector<int> live(nv, 0);
-    size_t done = 0;
-    while (done < m_.adms.size()) {
-      if (now_us() > o_.timeout_s * 1e6) { errors_ += "the manifest did not complete within --timeout-s\n"; return false; }
-      if (kvm_live_versions(ex_.get(), live.data(), (int)nv) < 0) { errors_ += std::string("live versions: ") + kvm_last_error(ex_.get()) + "\n"; return false; }
-      for (size_t i = 0; i < m_.adms.size(); ++i) {
-        Runtime& r = rt_[i];
-        if (r.st == St::SUBMITTED && windows_done(r)) {
-          r.st = St::DONE; r.t_done = now_us(); r.live_done = live; ++done;
-          if (!o_.quiet) fprintf(stderr, "[%9.0f us] done %-16s %6d tasks\n", r.t_done, m_.adms[i].name.c_str(), r.tasks);
-        }
-        if (r.st == St::FAILED) return false;
+  // Polls the device's live versions and window completion marks, retires finished admissions and submits every
+  // admission whose gate opens (manifest order within one poll), until all have finished or something fails.
+  bool drive() {
+    track_.assign(p_.adms.size(), Track{});
+    const int nv = std::max<int>(1, (int)p_.vars.size());
+    std::vector<int32_t> live(nv, 0);
+    Flow f;
+    f.finished.assign(p_.adms.size(), 0);
+    f.in_flight.assign(p_.adms.size(), 0);
+    size_t left = p_.adms.size();
+    while (left > 0) {
+      if (elapsed_us() > o_.timeout_s * 1e6) { problems_ += "not finished within --timeout-s\n"; return false; }
+      if (kvm_live_versions(ex_.get(), live.data(), nv) < 0) { problems_ += std::string("live versions: ") + kvm_last_error(ex_.get()) + "\n"; return false; }
+      for (size_t i = 0; i < p_.adms.size(); ++i) {
+        Track& tr = track_[i];
+        if (tr.phase != Phase::RUNNING) continue;
+        bool all = true;
+        for (long long w : tr.windows) all = all && kvm_window_done(ex_.get(), w) == 1;
+        if (!all) continue;
+        tr.phase = Phase::FINISHED;
+        tr.done_us = elapsed_us();
+        tr.live_at_done = live;
+        f.finished[i] = 1;
+        f.in_flight[i] = 0;
+        --left;
+        if (!o_.quiet) fprintf(stderr, "[%10.0f us] done   %-16s\n", tr.done_us, p_.adms[i].name.c_str());
       }
-      for (size_t i = 0; i < m_.adms.size(); ++i) {
-        if (rt_[i].st != St::PENDING) continue;
-        const Admission& a = m_.adms[i];
-        bool elig = a.at_us < 0 || now_us() >= (double)a.at_us;
-        for (auto& d : a.after) elig = elig && rt_[m_.adm_idx.at(d)].st == St::DONE;
-        for (auto& c : a.when) {
-          const int v = live[m_.var_idx.at(c.var)];
-          if (v > c.mx) { errors_ += a.name + ": version window passed (" + c.var + "=" + std::to_string(v) + " > max " + std::to_string(c.mx) + ")\n"; return false; }
-          elig = elig && v >= c.mn;
-        }
-        for (auto& kv : a.publishes) {
-          const int v = live[m_.var_idx.at(kv.first)], base = (int)a.base.at(kv.first);
-          if (v > base) { errors_ += a.name + ": compiled for " + kv.first + "=" + std::to_string(base) + " but the live version is already " + std::to_string(v) + "\n"; return false; }
-          elig = elig && v == base;
-          for (size_t j = 0; j < m_.adms.size() && elig; ++j)   // one publisher of a variable in flight
-            if (j != i && rt_[j].st == St::SUBMITTED && m_.adms[j].publishes.count(kv.first)) elig = false;
-        }
-        if (elig) {
-          submit(i);
-          if (rt_[i].st == St::FAILED) return false;
-          if (!o_.quiet) fprintf(stderr, "[%9.0f us] admit %-15s %6d tasks (%s)\n", rt_[i].t_submit, a.name.c_str(), rt_[i].tasks, rt_[i].how.c_str());
-        }
+      f.live.assign(live.begin(), live.begin() + p_.vars.size());
+      f.now_us = elapsed_us();
+      for (size_t i = 0; i < p_.adms.size(); ++i) {
+        if (track_[i].phase != Phase::WAITING) continue;
+        const Gate g = gate(p_, (int)i, f);
+        if (g.dead) { problems_ += p_.adms[i].name + " can no longer be admitted: " + g.why + "\n"; return false; }
+        if (!g.open) continue;
+        if (!submit((int)i)) return false;
+        f.in_flight[i] = 1;
       }
       std::this_thread::sleep_for(std::chrono::microseconds(50));
     }
@@ -649,44 +752,54 @@ class Runner {
 
   void write_summary(const KvmResult& r, bool ok) {
     FILE* f = fopen((o_.out + "/summary.json").c_str(), "w");
-    if (!f) { errors_ += "cannot write summary.json\n"; return; }
-    fprintf(f, "{\"ok\": %s, \"done\": %d, \"admitted\": %d, \"kernel_ms\": %.3f, \"serial_order\": [", ok ? "true" : "false", r.done, r.admitted, r.kernel_ms);
-    for (size_t i = 0; i < order_.size(); ++i) fprintf(f, "%s\"%s\"", i ? ", " : "", order_[i].c_str());
-    fprintf(f, "], \"admissions\": [");
-    for (size_t i = 0; i < m_.adms.size(); ++i) {
-      const Runtime& t = rt_[i];
-      fprintf(f, "%s{\"name\": \"%s\", \"workload\": \"%s\", \"tasks\": %d, \"windows\": %zu, \"how\": \"%s\", \"submitted_us\": %.1f, \"done_us\": %.1f, \"versions_at_done\": {",
-              i ? ", " : "", m_.adms[i].name.c_str(), m_.adms[i].workload.c_str(), t.tasks, t.wids.size(), t.how.c_str(), t.t_submit, t.t_done);
-      for (size_t v = 0; v < m_.vars.size() && v < t.live_done.size(); ++v) fprintf(f, "%s\"%s\": %d", v ? ", " : "", m_.vars[v].c_str(), t.live_done[v]);
-      fprintf(f, "}}");
+    if (!f) { problems_ += "cannot write summary.json\n"; return; }
+    auto versions = [&](const std::vector<int32_t>& v) {
+      fprintf(f, "{");
+      for (size_t k = 0; k < p_.vars.size() && k < v.size(); ++k) fprintf(f, "%s\"%s\": %d", k ? ", " : "", p_.vars[k].c_str(), v[k]);
+      fprintf(f, "}");
+    };
+    fprintf(f, "{\"ok\": %s, \"done\": %d, \"admitted\": %d, \"kernel_ms\": %.3f,\n \"serial_order\": [", ok ? "true" : "false", r.done, r.admitted, r.kernel_ms);
+    for (size_t i = 0; i < order_.size(); ++i) fprintf(f, "%s\"%s\"", i ? ", " : "", p_.adms[order_[i]].name.c_str());
+    fprintf(f, "],\n \"admissions\": [");
+    for (size_t i = 0; i < p_.adms.size(); ++i) {
+      const Track& t = track_[i];
+      fprintf(f, "%s\n  {\"name\": \"%s\", \"workload\": \"%s\", \"tasks\": %zu, \"windows\": %zu, \"how\": \"%s\", \"submitted_us\": %.1f, \"done_us\": %.1f, \"versions_at_done\": ",
+              i ? "," : "", p_.adms[i].name.c_str(), p_.workloads[p_.adms[i].workload].name.c_str(), progs_[i].tasks.size(), t.windows.size(),
+              progs_[i].origin.c_str(), t.submitted_us, t.done_us);
+      versions(t.live_at_done);
+      fprintf(f, "}");
     }
-    std::vector<int32_t> ver(std::max<size_t>(1, m_.vars.size()));
-    kvm_versions(ex_.get(), ver.data(), (int)ver.size());
-    fprintf(f, "], \"versions\": {");
-    for (size_t v = 0; v < m_.vars.size(); ++v) fprintf(f, "%s\"%s\": %d", v ? ", " : "", m_.vars[v].c_str(), ver[v]);
-    fprintf(f, "}}\n");
+    std::vector<int32_t> fin(std::max<size_t>(1, p_.vars.size()));
+    kvm_versions(ex_.get(), fin.data(), (int)fin.size());
+    fprintf(f, "],\n \"versions\": ");
+    versions(fin);
+    fprintf(f, "}\n");
     fclose(f);
   }
 
-  void dump_buffers() {
+  void write_dumps() {
     if (o_.dump.empty()) return;
-    std::regex re;
-    try { re = std::regex(o_.dump); } catch (const std::regex_error& e) { errors_ += std::string("--dump: bad regex: ") + e.what() + "\n"; return; }
-    for (size_t i = 0; i < m_.buffers.size(); ++i) {
-      if (!std::regex_search(m_.buffers[i].name, re)) continue;
-      const size_t n = (size_t)m_.buffers[i].rows * m_.buffers[i].cols;
+    std::regex pick;
+    try { pick = std::regex(o_.dump); } catch (const std::regex_error& e) { problems_ += std::string("--dump: ") + e.what() + "\n"; return; }
+    for (size_t i = 0; i < p_.buffers.size(); ++i) {
+      if (!std::regex_search(p_.buffers[i].name, pick)) continue;
+      const size_t n = (size_t)p_.buffers[i].rows * p_.buffers[i].cols;
       std::vector<float> v(n);
-      if (kvm_read_buffer(ex_.get(), (int)i, v.data(), n) < 0) { errors_ += "dump " + m_.buffers[i].name + ": " + kvm_last_error(ex_.get()) + "\n"; continue; }
-      FILE* f = fopen((o_.out + "/" + m_.buffers[i].name + ".bin").c_str(), "wb");
-      if (!f || fwrite(v.data(), 4, n, f) != n) errors_ += "cannot write the dump of " + m_.buffers[i].name + "\n";
+      if (kvm_read_buffer(ex_.get(), (int)i, v.data(), n) < 0) { problems_ += "dump " + p_.buffers[i].name + ": " + kvm_last_error(ex_.get()) + "\n"; continue; }
+      FILE* f = fopen((o_.out + "/" + p_.buffers[i].name + ".bin").c_str(), "wb");
+      if (!f || fwrite(v.data(), sizeof(float), n, f) != n) problems_ += "cannot write the dump of " + p_.buffers[i].name + "\n";
       if (f) fclose(f);
     }
   }
 };
 
-void usage() {
-  fprintf(stderr, "usage: kvm_run DEMO_DIR [--out DIR] [--dump REGEX] [--windows N] [--blocks N] [--timeout-s N] [--check-only] [--quiet]\n"
-                  "  runs every admission of DEMO_DIR/MANIFEST.json on one persistent kernel (stream mode)\n");
+int usage() {
+  fprintf(stderr,
+          "usage: kvm_run DEMO_DIR [--out DIR] [--dump REGEX] [--windows N] [--blocks N] [--timeout-s N] [--sched auto|off]\n"
+          "               [--check-only] [--quiet]\n"
+          "  runs every admission of DEMO_DIR/MANIFEST.json on one persistent kernel (stream mode)\n"
+          "  --sched off   run a manifest that declares scheduler classes first-come first-served\n");
+  return 2;
 }
 
 }  // namespace
@@ -694,23 +807,24 @@ void usage() {
 int main(int argc, char** argv) {
   Options o;
   for (int i = 1; i < argc; ++i) {
-    std::string a = argv[i];
-    auto next = [&]() -> const char* { if (i + 1 >= argc) { usage(); exit(2); } return argv[++i]; };
-    if (a == "--out") o.out = next();
-    else if (a == "--dump") o.dump = next();
-    else if (a == "--windows") o.windows = atoi(next());
-    else if (a == "--blocks") o.blocks = atoi(next());
-    else if (a == "--timeout-s") o.timeout_s = atoi(next());
-    else if (a == "--check-only") o.check_only = true;
+    const std::string a = argv[i];
+    const bool has_value = i + 1 < argc;
+    if (a == "--check-only") o.check_only = true;
     else if (a == "--quiet") o.quiet = true;
-    else if (a[0] == '-') { usage(); return 2; }
-    else if (o.root.empty()) o.root = a;
-    else { usage(); return 2; }
+    else if (a[0] == '-' && !has_value) return usage();
+    else if (a == "--out") o.out = argv[++i];
+    else if (a == "--dump") o.dump = argv[++i];
+    else if (a == "--windows") o.windows = atoi(argv[++i]);
+    else if (a == "--blocks") o.blocks = atoi(argv[++i]);
+    else if (a == "--timeout-s") o.timeout_s = atoi(argv[++i]);
+    else if (a == "--sched") o.sched = argv[++i];
+    else if (a[0] == '-' || !o.root.empty()) return usage();
+    else o.root = a;
   }
-  if (o.root.empty() || o.windows < 1 || o.timeout_s < 1) { usage(); return 2; }
+  if (o.root.empty() || o.windows < 1 || o.timeout_s < 1 || (o.sched != "auto" && o.sched != "off")) return usage();
   try {
-    Runner r(parse_manifest(o.root), o);
-    return r.run();
+    ManifestRun run(read_plan(o.root), o);
+    return run.go();
   } catch (const std::exception& e) {
     fprintf(stderr, "kvm_run: %s\n", e.what());
     printf("FAIL: %s\n", e.what());

@@ -54,3 +54,13 @@ def test_noalloc_refuses_a_graph_beyond_its_scratch():
     assert res['rc'] == -2          # KVM_STATUS_TOO_BIG
     assert 'MiB' in res['err']
     mem.close()
+
+
+def test_noalloc_refuses_a_grid_beyond_resident_capacity():
+    """A persistent grid larger than the device can hold at once is refused before launch (workers that never start
+    would leave their queues unserved), as kvm_create refuses it."""
+    b = bl.load(GOLDEN / 'versions')
+    mem, ptrs = _caller_buffers(b)
+    res, _ = executor.run_noalloc(b, ptrs, [v['base_version'] for v in b.metadata['variables']], blocks=1 << 20)
+    assert res['rc'] == -5 and 'co-resident capacity' in res['err'], res     # KVM_STATUS_INVALID
+    mem.close()

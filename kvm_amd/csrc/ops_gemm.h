@@ -587,9 +587,11 @@ template <int R, bool KC> struct DOp {
   i32x4_t rs;
   int voff[NL];
   int sstep;
+  unsigned m0w;                                         // LDS byte offset of this wave's first 1 KiB block (scalar)
   __device__ static __forceinline__ int kswz(int row) { return (row >> 2) & 3; }                       // k-contiguous
   __device__ static __forceinline__ int rswz(int k) { return R >= 128 ? 4 * (k & 3) : 4 * ((k >> 1) & 1); }  // row-contiguous
   __device__ __forceinline__ void init(const View& X, int r0) {
+    m0w = (unsigned)__builtin_amdgcn_readfirstlane(wave()) * 1024u;
     if constexpr (KC) {
       rs = dma_rsrc((const void*)(X.h() + (long long)r0 * X.cols), ((long long)X.rows - r0) * X.cols * 2);
       sstep = DK * 2;
@@ -604,11 +606,19 @@ template <int R, bool KC> struct DOp {
       else voff[q] = (row * X.cols + 8 * (ph ^ rswz(row))) * 2;
     }
   }
-  // Direct loads of stage s (k0 = s*DK) into `lds` (this operand's region of one stage buffer).
-  __device__ __forceinline__ void issue(LDS uint16_t* lds, int s) const {
+  // Direct loads of stage s (k0 = s*DK) into `lds` (this operand's region of one stage buffer); issue_one: load q only.
+  // A stage at or past nst (a placeholder that keeps the count of loads in flight constant) loads from offset 2^31 and
+  // up, past every descriptor's range: no memory access, the LDS bytes it writes are never read.
+  // `lds` is the wave-uniform LDS byte address of the operand's region in the stage buffer: M0 is then computed with
+  // scalar instructions only (a v_readfirstlane per load, with its hazard wait, measurably slows the MFMA stream).
+  __device__ __forceinline__ void issue(unsigned lds, int s, int nst) const {
 #pragma unroll
-    for (int q = 0; q < NL; ++q)
-      dma16(rs, voff[q], s * sstep, lds + (q * KVM_WAVES + wave()) * 512);
+    for (int q = 0; q < NL; ++q) issue_one(lds, s, q, nst);
+  }
+  __device__ __forceinline__ void issue_one(unsigned lds, int s, int q, int nst) const {
+    const unsigned m = lds + m0w + q * KVM_WAVES * 1024u;
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" :: "s"(m), "v"(voff[q]), "s"(rs),
+                 "s"(s < nst ? s * sstep : (int)0x80000000) : "memory", "m0");
   }
   // MFMA operand for the 32 tile rows rb.. and k16 step kk: 8 bf16 of row rb + l%32 at k = 16kk + 8(l/32) ...
   __device__ __forceinline__ bf16x8 frag(const LDS uint16_t* lds, int rb, int kk) const {
@@ -651,56 +661,75 @@ __device__ __noinline__ void gemm_lds(const Ctx& c) {
     for (int j = 0; j < BN; ++j) acc[i][j] = f32x16{};
   const int nst = K / DK;
   constexpr int NLS = DOp<TM, AKC>::NL + DOp<TN, BKC>::NL;  // direct loads per thread per stage
-  // Waits until at most k stages issued after the one needed are still in flight (k <= NS - 2).
-  auto wait_stages = [](int k) {
-    k = __builtin_amdgcn_readfirstlane(k);
-    if (k >= 3) wait_vm_c<3 * NLS>(); else if (k == 2) wait_vm_c<2 * NLS>(); else if (k == 1) wait_vm_c<NLS>(); else wait_vm_c<0>();
-  };
-  static_assert(NS - 2 <= 3, "wait_stages");
+  // Every stage slot issues its direct loads, also past the last stage (placeholders, into a buffer no later stage
+  // reads), so the number of loads in flight behind a stage is always the same and every wait is a constant vmcnt.
   __syncthreads();                                 // the previous task may still read this LDS
+  const unsigned lb = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)(uintptr_t)lds);   // LDS byte address
 #pragma unroll
-  for (int p = 0; p < NS - 1; ++p)
-    if (p < nst) { da.issue(lds + p * ST, p); db.issue(lds + p * ST + SA, p); }
-  // Software pipeline over stages. Iteration s: read the second k16 half of stage s while the MFMAs of its first half
-  // run; wait for stage s + 1 and barrier (every wave is then past stage s - 1, whose buffer the next load reuses);
-  // issue stage s + NS - 1; read the first half of stage s + 1 while the MFMAs of the second half of stage s run.
+  for (int p = 0; p < NS - 1; ++p) { da.issue(lb + p * ST * 2, p, nst); db.issue(lb + (p * ST + SA) * 2, p, nst); }
+  // Software pipeline over stages, every instruction placed by hand (scheduling barriers around each MFMA): the compiler
+  // otherwise sinks the fragment reads to just before the MFMAs that consume them (full LDS latency exposed at every
+  // half) and issues the direct loads back to back (their issue stalls the wave's MFMA stream). Iteration s:
+  //   half 0: the MFMAs of stage s's first k16 half, the fragment reads of its second half placed after its first
+  //   MFMAs (as early as possible: they have the rest of the half to land);
+  //   wait for stage s + 1 and barrier (every wave is then past stage s - 1, whose buffer the next loads reuse);
+  //   half 1: the MFMAs of the second half; after its first ones the fragment reads of stage s + 1's first half, then
+  //   the direct loads of stage s + NS - 1 (they have NS - 2 stages to land).
+  // The last stage is peeled, so the loop body has no branch around LDS reads.
+  constexpr int NF = BM + BN, NM = BM * BN;          // fragment reads / MFMAs per k16 half
+  constexpr int NLA = DOp<TM, AKC>::NL;
+  constexpr int PF = (NF + NM - 1) / NM, PX = (NF + NLS + NM - 1) / NM;   // reads / loads placed after each MFMA
   bf16x8 fa0[BM], fb0[BN], fa1[BM], fb1[BN];
-  auto read_half = [&](const LDS uint16_t* st, int kk, bf16x8 (&fa)[BM], bf16x8 (&fb)[BN]) {
-#pragma unroll
-    for (int i = 0; i < BM; ++i) fa[i] = da.frag(st, wm0 + i * 32, kk);
-#pragma unroll
-    for (int j = 0; j < BN; ++j) fb[j] = db.frag(st + SA, wn0 + j * 32, kk);
+  auto read_one = [&](const LDS uint16_t* st, int kk, int f, bf16x8 (&fa)[BM], bf16x8 (&fb)[BN]) {
+    if (f < BM) fa[f] = da.frag(st, wm0 + f * 32, kk);
+    else fb[f - BM] = db.frag(st + SA, wn0 + (f - BM) * 32, kk);
   };
-  auto mfma_half = [&](const bf16x8 (&fa)[BM], const bf16x8 (&fb)[BN]) {
-#pragma unroll
-    for (int i = 0; i < BM; ++i)
-#pragma unroll
-      for (int j = 0; j < BN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+  auto mfma_one = [&](int m, const bf16x8 (&fa)[BM], const bf16x8 (&fb)[BN]) {
+    const int i = m / BN, j = m % BN;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
   };
-  wait_stages(min(NS - 2, nst - 1));
+  wait_vm_c<(NS - 2) * NLS>();                   // stage 0 has landed (NS - 2 stages were issued after it)
   __syncthreads();
-  read_half(lds, 0, fa0, fb0);
-  // The loop body has no branch around LDS reads (the last stage is peeled), so the compiler's in-order LDS counter
-  // stays exact and the MFMAs of one half never wait for the reads issued for the next. The barrier is a bare
-  // s_barrier: the staged data is complete once vmcnt says so, and the buffer the next load overwrites was last read
-  // by MFMA operands consumed before it.
+#pragma unroll
+  for (int f = 0; f < NF; ++f) read_one(lds, 0, f, fa0, fb0);
   for (int s = 0; s + 1 < nst; ++s) {
     const LDS uint16_t* la = lds + (s % NS) * ST;
-    read_half(la, 1, fa1, fb1);
-    mfma_half(fa0, fb0);
-    wait_stages(min(NS - 3, nst - 2 - s));        // this thread's loads of stage s + 1 have landed
-    asm volatile("s_barrier" ::: "memory");        // ... everyone's
-    if (s + NS - 1 < nst) {
-      LDS uint16_t* nb = lds + ((s + NS - 1) % NS) * ST;
-      da.issue(nb, s + NS - 1);
-      db.issue(nb + SA, s + NS - 1);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      mfma_one(m, fa0, fb0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int f = m * PF; f < (m + 1) * PF && f < NF; ++f) read_one(la, 1, f, fa1, fb1);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    read_half(lds + ((s + 1) % NS) * ST, 0, fa0, fb0);
-    mfma_half(fa1, fb1);
+    wait_vm_c<(NS - 3) * NLS>();                 // this thread's loads of stage s + 1 have landed
+    asm volatile("s_barrier" ::: "memory");        // ... everyone's
+    const int sn = s + NS - 1;
+    const unsigned nb = lb + ((s + NS - 1) % NS) * ST * 2;
+    const LDS uint16_t* ln = lds + ((s + 1) % NS) * ST;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      mfma_one(m, fa1, fb1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int x = m * PX; x < (m + 1) * PX && x < NF + NLS; ++x) {
+        if (x < NF) read_one(ln, 0, x, fa0, fb0);
+        else if (x - NF < NLA) da.issue_one(nb, sn, x - NF, nst);
+        else db.issue_one(nb + SA * 2, sn, x - NF - NLA, nst);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
-  read_half(lds + ((nst - 1) % NS) * ST, 1, fa1, fb1);
-  mfma_half(fa0, fb0);
-  mfma_half(fa1, fb1);
+  {
+    const LDS uint16_t* la = lds + ((nst - 1) % NS) * ST;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) read_one(la, 1, f, fa1, fb1);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) mfma_one(m, fa0, fb0);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) mfma_one(m, fa1, fb1);
+  }
+  wait_vm_c<0>();                                  // the placeholder loads have written their LDS bytes
   gemm_store<TM, TN>(c, acc, g);
 }
 

@@ -8,6 +8,9 @@ run with several threads, same results as one).
 - C3 GPT-162M, one layer at full width (d 768, 12 heads, T 1024, batch 4, vocab 50304, tied), bf16 storage: step-1
   weight gradients within 3.4e-2 relative L2 (twice the reference's bf16s deviation from fp64, 1.69e-2, README.md:212
   of the reference), loss within 1e-2.
+- C3 GPT-162M, full depth (12 layers): loss, logits, gradient groups and parameter groups after AdamW within twice the
+  reference path's own deviation from an fp64 run of the step (tests/golden/data/gpt_fp64_deviation.json, written by
+  tests/golden/make_gpt_deviation.py with tests/gpt_fp64.py).
 - C4 GPT-355M shape, two layers (d 1024, 16 heads, T 1024, ffn 4096, vocab 50304), f32, batch 1: every buffer after
   the step within the reference's TOL_PRECISE 2e-4 (tests/gptdiff/golden_check.py:28-31 of the reference).
 - C2 the eight MLPs (784 -> w -> w -> 10, all eight widths, batch 256), two training steps: every buffer within 2e-4.
@@ -91,6 +94,33 @@ def test_gpt162m_full_width_one_layer_step():
     assert np.array_equal(ex.read('step'), r['buffers'][names.index('step')])
     ex.close()
 
+
+def test_gpt162m_full_depth_step():
+    """The whole GPT-162M training step (12 layers, bf16 storage, fp32 master AdamW) against the oracle: the loss,
+    the logits, every gradient group and every parameter group after AdamW (pooled over layers) within twice the
+    reference path's own deviation from an fp64 run of the same step (tests/golden/data/gpt_fp64_deviation.json,
+    written by tests/golden/make_gpt_deviation.py with tests/gpt_fp64.py)."""
+    import os
+    import gpt_fp64 as G
+    from kvm_amd.workloads import gpt
+    print('gpt-162m full depth, bf16 step', flush=True)
+    dev = json.loads((REPO / 'tests/golden/data/gpt_fp64_deviation.json').read_text())
+    w = gpt.build(gpt.GPTConfig())
+    lb, names, init = _prepare(w)
+    ex = _device(w, lb)
+    check_schedule(ex, lb)
+    got = [ex.read(n) for n in names]
+    ex.close()
+    r = oracle.run(lb, init, threads=min(THREADS, os.cpu_count() or 1))
+    err = G.deviations(names, got, G.quantities(names, r['buffers']))
+    worst = sorted(((e / dev['deviation'][k], k, e) for k, e in err.items()), reverse=True)
+    print('device vs reference path / reference deviation from fp64, worst:', worst[:4], flush=True)
+    for ratio, k, e in worst:
+        assert ratio <= 2.0, (k, e, dev['deviation'][k])
+    assert np.array_equal(got[names.index('step')], r['buffers'][names.index('step')])
+
+
+test_gpt162m_full_depth_step = pytest.mark.timeout(600)(test_gpt162m_full_depth_step)
 
 TOL_PRECISE = 2e-4
 

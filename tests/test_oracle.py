@@ -437,3 +437,21 @@ def test_decode_reference_deviation_from_fp64_fixture():
     assert got['tok'] == got['tok_fp64'] == fix['tok']
     for k, v in got['deviation'].items():
         assert 0 < v < 1e-2 and abs(v - fix['deviation'][k]) <= 1e-3 * v, (k, v, fix['deviation'][k])
+
+
+def test_gpt_fp64_model_matches_the_f32_oracle():
+    """tests/gpt_fp64.py (the fp64 model the full-depth GPT tolerances are measured with) computes the graph's step:
+    on an f32 GPT graph (2 layers, d 128, 4 heads, T 64, vocab 256, batch 8) the oracle's loss, logits, gradients and
+    AdamW-updated parameters agree with it to f32 rounding (relative L2 below 2e-5 everywhere)."""
+    import gpt_fp64 as G
+    from kvm_amd.workloads import gpt
+    c = gpt.GPTConfig(layers=2, d=128, heads=4, T=64, vocab=256, ffn=512, batch=8, dtype='f32')
+    w = gpt.build(c)
+    lb = bl.load(compiler.compile_spec(w.spec))
+    names = [m['name'] for m in lb.metadata['buffers']]
+    init = [oracle.materialize(m, w.init_override.get(m['name'])) for m in lb.metadata['buffers']]
+    ref = G.step(c, {n: x.copy() for n, x in zip(names, init)})
+    r = oracle.run(lb, init, threads=4)
+    dev = G.deviations(names, r['buffers'], ref)
+    assert dev.pop('loss_abs') < 1e-5
+    assert max(dev.values()) < 2e-5, sorted(dev.items(), key=lambda kv: -kv[1])[:3]

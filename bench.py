@@ -118,22 +118,24 @@ def _layer_fit(make, layers_full, threads):
 
 
 def cpu_decode(batch):
+    """CPU reference time of one decode step: the oracle on the whole 36-layer graph (weights materialised outside the
+    timed region)."""
     from kvm_amd.workloads import qwen3
-    est, t1, t2 = _layer_fit(lambda L: qwen3.build(qwen3.Qwen3Config(batch=batch, layers=L, max_new=4)), 36, CPU_THREADS)
-    return {'value': round(batch / est, 4), 'unit': 'tok/s', 'cores': CPU_THREADS, 'nproc': os.cpu_count(), 'kind': 'port',
-            'sample': f'oracle (C++ restatement of the reference CPU VM + ops, {CPU_THREADS} worker threads) timed on whole full-width '
-                      f'decode graphs of 1 and 2 layers (+ LM head), batch {batch}: {t1:.2f} s and {t2:.2f} s; 36 layers = '
-                      f't1 + 35 (t2 - t1) = {est:.2f} s per step'}
+    t = _oracle_time(qwen3.build(qwen3.Qwen3Config(batch=batch, max_new=4)), CPU_THREADS)
+    return {'value': round(batch / t, 4), 'unit': 'tok/s', 'cores': CPU_THREADS, 'nproc': os.cpu_count(), 'kind': 'port',
+            'sample': f'oracle (C++ restatement of the reference CPU VM + ops, {CPU_THREADS} worker threads) on the whole decode '
+                      f'graph (36 layers + LM head, batch {batch}, 4096-token cache), one step: {t:.2f} s'}
 
 
 GEMM_OPS = (34, 114, 122, 302, 304, 308)
 ATTN_OPS = (45, 47, 48)
 
 
-def gemm_task_flops(lb):
+def gemm_task_flops(lb, executed_out=None):
     """FLOPs of every GEMM tile task (2*tm*tn*K clipped to the matrix; K is the task's own range for the split-K tiles
     of op 302) and of the attention tasks (their share of the causal attention's algorithmic FLOPs: fwd 2 products,
-    bwd 5), from the bundle's own arguments."""
+    bwd 5), from the bundle's own arguments. executed_out (array): the attention tasks' executed FLOPs (backward with
+    the recomputed products)."""
     import numpy as np
     t, a = lb.tasks, lb.args
     fl = np.zeros(t.shape[0])
@@ -159,8 +161,13 @@ def gemm_task_flops(lb):
                 pairs = sum(T - k for k in range(q0, q1))
             else:
                 pairs = sum(k + 1 for k in range(q0, q1))
-            # per (query, key) pair: forward S and P V 4 hd; dQ: S, dP, dS K 6 hd; dK / dV: S, dP, P^T dO, dS^T Q 8 hd
-            fl[i] = 2.0 * hd * pairs * {45: 2, 47: 3, 48: 4}[op]
+            # per (query, key) pair the algorithmic work is forward 4 hd (S, P V) and backward 10 hd (S, dP, dV, dQ, dK:
+            # 2.5x the forward); the backward tasks execute 6 hd (dQ: S, dP, dS K) and 8 hd (dK / dV: S, dP, P^T dO,
+            # dS^T Q), recomputing S and dP in both, so the algorithmic 10 hd is split between them as 6:8
+            executed = 2.0 * hd * pairs * {45: 2, 47: 3, 48: 4}[op]
+            fl[i] = executed if op == 45 else executed * 10.0 / 14.0
+            if executed_out is not None:
+                executed_out[i] = executed
     return fl
 
 
@@ -182,23 +189,26 @@ def bench_gpt(steps, warmup, cpu):
     # MFMA utilisation inside the GEMM / attention tasks, from the traced run's per-task record
     tr = ex.trace()
     dur = (tr['end'] - tr['start']).astype(np.float64) / 100e6     # s (wall_clock64 at 100 MHz)
-    fl = gemm_task_flops(lb)
+    fx = np.zeros(lb.ntasks)
+    fl = gemm_task_flops(lb, fx)
     ops = lb.tasks[:, 0]
     gm = np.isin(ops, GEMM_OPS); at = np.isin(ops, ATTN_OPS)
     per_cu = BF16_PEAK_TFLOPS / 256 * 1e12
-    in_task = {'gemm': float(fl[gm].sum() / dur[gm].sum() / per_cu), 'attention': float(fl[at].sum() / dur[at].sum() / per_cu)}
+    in_task = {'gemm': float(fl[gm].sum() / dur[gm].sum() / per_cu), 'attention': float(fl[at].sum() / dur[at].sum() / per_cu),
+               'attention_executed': float(fx[at].sum() / dur[at].sum() / per_cu)}
     busy = float(dur.sum() / (res['grid'] * (tr['end'].max() - tr['start'].min()) / 100e6))
     names = [m['name'] for m in lb.metadata['buffers']]
     loss = float(ex.read('loss')[0])
     out = {'ms_per_step': round(ms, 3), 'path': PATH_NAMES.get(ex.path()), 'kernel_ms': round(kms, 3), 'tflops': round(tflops, 1), 'mfma_frac_step': round(tflops / BF16_PEAK_TFLOPS, 4),
            'mfma_frac_in_gemm_tasks': round(in_task['gemm'], 4), 'mfma_frac_in_attention_tasks': round(in_task['attention'], 4),
+           'mfma_frac_in_attention_tasks_executed': round(in_task['attention_executed'], 4),
            'worker_busy_frac': round(busy, 4), 'tasks': lb.ntasks, 'edges': int(lb.succ.size), 'loss_after': loss,
            'step_flops': flops, 'params': w.info['params'], 'first_step_check': check}
     log(f'  gpt-162m: {ms:.2f} ms/step (persistent kernel {kms:.2f} ms), {tflops:.1f} TFLOP/s ({tflops / BF16_PEAK_TFLOPS:.1%} of bf16 peak); in-task MFMA: '
         f'GEMM {in_task["gemm"]:.1%}, attention {in_task["attention"]:.1%}; workers busy {busy:.1%}; loss {loss:.4f}')
     ex.close()
     if cpu:
-        out['cpu_baseline'] = cpu_gpt()
+        out['cpu_baseline'] = cpu_gpt_whole()
     return out
 
 
@@ -280,8 +290,18 @@ def first_step_invariants(ex, lb, vocab):
     return {'loss_step1': round(loss, 4), 'ln_vocab': round(float(np.log(vocab)), 4), 'grads_finite_nonzero': len(grads)}
 
 
+def cpu_gpt_whole():
+    """CPU reference time of the GPT-162M step: the oracle on the whole 12-layer step graph."""
+    from kvm_amd.workloads import gpt
+    t = _oracle_time(gpt.build(gpt.GPTConfig()), CPU_THREADS)
+    return {'value': round(t * 1e3, 1), 'unit': 'ms/step', 'cores': CPU_THREADS, 'nproc': os.cpu_count(), 'kind': 'port',
+            'sample': f'oracle (C++ restatement of the reference CPU VM + ops, {CPU_THREADS} worker threads) on the whole step graph '
+                      f'(12 layers, forward + backward + AdamW), one step: {t:.1f} s'}
+
+
 def cpu_gpt(layers=12, dtype='bf16', **kw):
-    """CPU reference time of the GPT step from whole-graph oracle timings at full width and 1 and 2 layers."""
+    """CPU reference time of a GPT step from whole-graph oracle timings at full width and 1 and 2 layers (GPT-355M, whose
+    whole 24-layer f32 graph would take minutes on the oracle)."""
     from kvm_amd.workloads import gpt
     make = (lambda L: gpt.build(gpt.GPTConfig(layers=L, **kw))) if dtype == 'bf16' else (lambda L: gpt.build(gpt.GPTConfig.gpt355m(layers=L, **kw)))
     est, t1, t2 = _layer_fit(make, layers, CPU_THREADS)

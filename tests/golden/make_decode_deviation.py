@@ -1,6 +1,6 @@
 """Writes tests/golden/data/decode_fp64_deviation.json: the reference CPU path's own deviation from an fp64 run on the
-full-width Qwen3-8B-shape decode graph cut to one layer (hidden 4096, 32/8 heads, hd 128, ffn 12288, vocab 151936,
-4096-token cache), batch 1 and 8. "Reference CPU path" is the oracle (the C++ restatement of the reference's CPU VM and
+full-width Qwen3-8B-shape decode graph (hidden 4096, 32/8 heads, hd 128, ffn 12288, vocab 151936, 4096-token cache) cut
+to one layer, batch 1 and 8, and at full depth (36 layers), batch 1 and 8 (keys b1_full, b8_full). "Reference CPU path" is the oracle (the C++ restatement of the reference's CPU VM and
 ops, rounding like the reference); the fp64 run is tests/decode_fp64.py on the same initial buffers. Decode tolerances
 are twice these figures. Run from the repository root: python tests/golden/make_decode_deviation.py
 """
@@ -18,8 +18,8 @@ from kvm_amd import compiler  # noqa: E402
 from kvm_amd.workloads import qwen3  # noqa: E402
 
 
-def deviation(batch, threads=8):
-    c = qwen3.Qwen3Config(batch=batch, layers=1, max_new=4)
+def deviation(batch, threads=8, layers=1):
+    c = qwen3.Qwen3Config(batch=batch, layers=layers, max_new=4)
     w = qwen3.build(c)
     lb = bl.load(compiler.compile_spec(w.spec))
     names = [m['name'] for m in lb.metadata['buffers']]
@@ -36,4 +36,7 @@ if __name__ == '__main__':
     for b in (1, 8):
         out[f'b{b}'] = deviation(b)
         print(b, out[f'b{b}'], flush=True)
+    for b in (1, 8):
+        out[f'b{b}_full'] = deviation(b, layers=36)
+        print(b, 'full depth', out[f'b{b}_full'], flush=True)
     (ROOT / 'tests/golden/data/decode_fp64_deviation.json').write_text(json.dumps(out, indent=1) + '\n')

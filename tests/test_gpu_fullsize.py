@@ -5,6 +5,8 @@ run with several threads, same results as one).
   4096-token cache), batch 1 and 8: tokens and lengths exact; logits, final residual and the new KV-cache rows within
   twice the reference path's own deviation from an fp64 run of the same step (tests/golden/data/
   decode_fp64_deviation.json, written by tests/golden/make_decode_deviation.py).
+- C5 at full depth (36 layers + LM head), batch 1 and 8: the same checks against the full-depth fp64 deviations (b1_full,
+  b8_full in the same file).
 - C3 GPT-162M, one layer at full width (d 768, 12 heads, T 1024, batch 4, vocab 50304, tied), bf16 storage: step-1
   weight gradients within 3.4e-2 relative L2 (twice the reference's bf16s deviation from fp64, 1.69e-2, README.md:212
   of the reference), loss within 1e-2.
@@ -71,6 +73,35 @@ def test_qwen3_decode_full_width_one_layer(batch):
     for k, e in err.items():
         assert e <= 2 * dev['deviation'][k], (k, e, dev['deviation'][k])
     ex.close()
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize('batch', [1, 8])
+def test_qwen3_decode_full_depth(batch):
+    """The whole 36-layer Qwen3-8B-shape decode step (+ LM head): tokens and lengths exact; logits, final residual and
+    the new KV-cache rows of every layer within twice the reference path's own deviation from an fp64 run of the same
+    step at full depth (b1_full / b8_full in tests/golden/data/decode_fp64_deviation.json)."""
+    import os
+    from kvm_amd.workloads import qwen3
+    print(f'qwen3 full depth, batch {batch}', flush=True)
+    dev = json.loads((REPO / 'tests/golden/data/decode_fp64_deviation.json').read_text())[f'b{batch}_full']
+    c = qwen3.Qwen3Config(batch=batch, max_new=4)
+    w = qwen3.build(c)
+    lb, names, init = _prepare(w)
+    ex = _device(w, lb)
+    check_schedule(ex, lb)
+    need = {'logits', 'x', 'tok', 'lens'} | {f'{k}.{l}' for k in ('kc', 'vc') for l in range(c.layers)}
+    got_bufs = [ex.read(n) if n in need else None for n in names]
+    ex.close()
+    r = oracle.run(lb, init, threads=min(THREADS, os.cpu_count() or 1))
+    want = D.graph_outputs(c, names, r['buffers'])
+    got = D.graph_outputs(c, names, got_bufs)
+    assert got['tok'].tolist() == want['tok'].tolist() == dev['tok']
+    assert np.array_equal(got_bufs[names.index('lens')], r['buffers'][names.index('lens')])
+    err = D.deviations(got, want)
+    print('device vs reference path', err, 'tolerance 2 x', dev['deviation'], flush=True)
+    for k, e in err.items():
+        assert e <= 2 * dev['deviation'][k], (k, e, dev['deviation'][k])
 
 
 TOL_GPT_BF16_GRAD = 3.4e-2

@@ -492,6 +492,7 @@ __device__ void dispatch(int op, const Ctx& c) {
     case 136: op_attn_decode_merge(c); break;
     case 300: op_head_rmsnorm(c); break;
     case 301: op_gemv_bf16_rows(c); break;
+    case 311: op_gemv_swiglu(c); break;
     case 302: op_matmul_mma_bf16_kr(c); break;
     case 303: op_splitk_reduce(c); break;
     case 304: op_matmul_mma_bf16_256(c); break;
@@ -576,7 +577,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
     Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
     if (sf & KVM_SF_PRE) {
       const int op = s_rec.desc.op_id;
-      if (op == 134 || op == 301) gemv_prefetch(c, op);
+      if (op == 134 || op == 301 || op == 311) gemv_prefetch(c, op);
       else attn_prefetch(c, op);
       c.pre = 1;
     }
@@ -620,6 +621,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
     if (V == 0) dispatch(op, c);
     else {
       constexpr int GR = V == 1 ? 12 : 4;          // the set's GEMV ring depth
+      // (the fused SwiGLU GEMV, op 311, runs through the dispatcher: inlined beside the others it made the kernel spill)
       const bool rows = op == 301, gv = (op == 134 || rows) && c.pre;
       const int gm = rows ? c.i(9) : 1, gpro = rows ? c.i(10) : c.i(9);
       if ((op == 306 || op == 310) && c.i(11) == 4 * c.i(12)) attn_part_body<4>(c, true, op == 310);
@@ -1580,7 +1582,8 @@ static std::vector<int> static_flags(const KvmExec* ex, const kvms::Plan& P) {
     if (sigs[op].empty()) if (const kvmv::OpSig* o = kvmv::find_op(op)) sigs[op] = kvmv::parse_sig(o->sig);
     const int32_t* a = ex->args.data() + d.args_off;
     for (size_t k = 0; k < sigs[op].size() && (int)k < d.args_words; ++k)
-      if (sigs[op][k].type == 0 && a[k] >= 0 && a[k] < nb && !((op == 134 || op == 301) && k == 3) && !((op == 135 || op == 306 || op == 310) && (k == 1 || k == 2)))
+      if (sigs[op][k].type == 0 && a[k] >= 0 && a[k] < nb && !((op == 134 || op == 301) && k == 3) && !(op == 311 && (k == 2 || k == 3)) &&
+          !((op == 135 || op == 306 || op == 310) && (k == 1 || k == 2)))
         other_use[a[k]] = 1;
   }
   std::vector<int> f(n, 0);
@@ -1590,6 +1593,10 @@ static std::vector<int> static_flags(const KvmExec* ex, const kvms::Plan& P) {
     if ((d.op_id == 134 || d.op_id == 301) && d.args_words > 3) {
       const int wb = ex->args[d.args_off + 3];
       if (wb >= 0 && wb < nb && !other_use[wb] && !getenv("KVM_NO_PREFETCH")) f[i] |= KVM_SF_PRE;
+    }
+    if (d.op_id == 311 && d.args_words > 3) {
+      const int wg = ex->args[d.args_off + 2], wu = ex->args[d.args_off + 3];
+      if (wg >= 0 && wg < nb && wu >= 0 && wu < nb && !other_use[wg] && !other_use[wu] && !getenv("KVM_NO_PREFETCH")) f[i] |= KVM_SF_PRE;
     }
     // A decode attention split whose caches only the splits use (each writes its own new row): its first block and
     // rotation table are staged before the wait.
@@ -1610,8 +1617,8 @@ static int static_variant(const KvmExec* ex) {
   for (const MvmTaskDesc& d : ex->tasks) {
     if (d.op_id == 134) ++deep;
     else if ((d.op_id == 306 || d.op_id == 310) && d.args_words > 12 && ex->args[d.args_off + 11] == 4 * ex->args[d.args_off + 12]) ++attn4;
-    else if (d.op_id == 301 && d.args_words > 9) {
-      const int M = ex->args[d.args_off + 9];
+    else if ((d.op_id == 301 && d.args_words > 9) || (d.op_id == 311 && d.args_words > 8)) {
+      const int M = ex->args[d.args_off + (d.op_id == 301 ? 9 : 8)];
       if (M >= 1 && M <= 4) ++deep;
       else if (M >= 5 && M <= 8) ++rows8;
     }

@@ -350,14 +350,17 @@ __device__ __forceinline__ bool gemv_stream_ok(const View& x, const View& x2, co
 
 // One wave's weight stream: a wave-uniform issue cursor over (row group, K chunk, row block, step) and the ring slot
 // it fills next.
-struct GvStream {
-  i32x4_t rw;
+// DUAL (the fused SwiGLU GEMV): two matrices of one shape, whose row blocks alternate in the stream: block 2j holds
+// rows n0 + 16j .. +16 of w, block 2j + 1 the same rows of w2.
+template <bool DUAL = false> struct GvStream {
+  i32x4_t rw, rw2;
   int nrows, nrb, rowb, K, KC, ns, koff;
   int g0, kc, rb, st, islot;
-  __device__ __forceinline__ void init(const View& w, int n0, int n1, int K_, int KC_) {
-    nrows = rfl(n1 - n0); nrb = rfl((nrows + 15) / 16); rowb = rfl(w.cols * 2); K = rfl(K_); KC = rfl(KC_); ns = KC / 256;
+  __device__ __forceinline__ void init(const View& w, int n0, int n1, int K_, int KC_, const View* w2 = nullptr) {
+    nrows = rfl(n1 - n0); nrb = rfl(((nrows + 15) / 16) * (DUAL ? 2 : 1)); rowb = rfl(w.cols * 2); K = rfl(K_); KC = rfl(KC_); ns = KC / 256;
     koff = rfl(wave() * (KC / 4) * 2);
     rw = dma_rsrc((const void*)(w.h() + (long long)n0 * w.cols), ((long long)w.rows - n0) * w.cols * 2);
+    if constexpr (DUAL) rw2 = dma_rsrc((const void*)(w2->h() + (long long)n0 * w2->cols), ((long long)w2->rows - n0) * w2->cols * 2);
     g0 = kc = rb = st = islot = 0;
   }
   __device__ __forceinline__ void advance() {
@@ -371,10 +374,20 @@ struct GvStream {
   // Requests the next step into its ring slot (past the end: two loads beyond the descriptor's range).
   template <int R> __device__ __forceinline__ void issue(LDS char* ring) {
     LDS char* dst = ring + islot * GV_STEP;
-    const int row = min((g0 + rb) * 16 + (lane() & 15), nrows - 1);
-    const int off = g0 < nrb ? row * rowb + kc * 2 + koff + st * 128 + 16 * (lane() >> 4) : 0x7fff0000;
-    dma16(rw, off, 0, dst);
-    dma16(rw, off + 64, 0, dst + 1024);
+    if constexpr (DUAL) {
+      const int vb = g0 + rb;
+      const int row = min((vb >> 1) * 16 + (lane() & 15), nrows - 1);
+      const int off = g0 < nrb ? row * rowb + kc * 2 + koff + st * 128 + 16 * (lane() >> 4) : 0x7fff0000;
+      const bool up = rfl(vb & 1) != 0;                                         // wave-uniform: the descriptor stays scalar
+      const i32x4_t r = {rfl(up ? rw2[0] : rw[0]), rfl(up ? rw2[1] : rw[1]), rfl(up ? rw2[2] : rw[2]), rfl(up ? rw2[3] : rw[3])};
+      dma16(r, off, 0, dst);
+      dma16(r, off + 64, 0, dst + 1024);
+    } else {
+      const int row = min((g0 + rb) * 16 + (lane() & 15), nrows - 1);
+      const int off = g0 < nrb ? row * rowb + kc * 2 + koff + st * 128 + 16 * (lane() >> 4) : 0x7fff0000;
+      dma16(rw, off, 0, dst);
+      dma16(rw, off + 64, 0, dst + 1024);
+    }
     islot = islot + 1 == R ? 0 : islot + 1;
     advance();
   }
@@ -384,14 +397,30 @@ struct GvStream {
 // The first steps of every wave's stream, into the ring of a task that will run with c.pre set. Called by all four
 // waves with the task's record in c (op 134 or 301) before its dependencies are met; it reads only the weights and
 // writes only the ring.
-template <int R> __device__ __forceinline__ void gemv_prefetch_r(const View& w, int n0, int n1, int K, int M, LDS char* smem) {
-  GvStream ws;
-  ws.init(w, n0, n1, K, gv_geo(K, M, R).KC);
+template <int R, bool DUAL = false>
+__device__ __forceinline__ void gemv_prefetch_r(const View& w, int n0, int n1, int K, int M, LDS char* smem, const View* w2 = nullptr) {
+  GvStream<DUAL> ws;
+  ws.init(w, n0, n1, K, gv_geo(K, M, R).KC, w2);
   LDS char* ring = smem + wave() * R * GV_STEP;
 #pragma unroll
-  for (int j = 0; j < R; ++j) ws.issue<R>(ring);
+  for (int j = 0; j < R; ++j) ws.template issue<R>(ring);
+}
+// Op 311's stream form: op 301's shapes with pro 1, both matrices bf16 of one shape.
+__device__ __forceinline__ bool gemv_swiglu_ok(const Ctx& c) {
+  const View wg = c.buf(2), wu = c.buf(3);
+  return gemv_stream_ok(c.buf(0), View{nullptr, 0, 0, 0}, wg, c.buf(4), c.i(7), c.i(8), 1) && wu.dtype == 2 && wu.rows == wg.rows &&
+         wu.cols == wg.cols;
 }
 __device__ __noinline__ void gemv_prefetch(const Ctx& c, int op) {
+  if (op == 311) {
+    if (!gemv_swiglu_ok(c)) return;
+    const View wg = uniform_view(c.buf(2)), wu = uniform_view(c.buf(3));
+    const int M = rfl(c.i(8)), K = rfl(c.i(7)), n0 = rfl(c.i(5)), n1 = rfl(c.i(6)), R = gv_pre_ring(M);
+    if (R == 12) gemv_prefetch_r<12, true>(wg, n0, n1, K, M, c.smem, &wu);
+    else if (R == 8) gemv_prefetch_r<8, true>(wg, n0, n1, K, M, c.smem, &wu);
+    else gemv_prefetch_r<4, true>(wg, n0, n1, K, M, c.smem, &wu);
+    return;
+  }
   const View x = c.buf(0), x2 = c.buf(1), w = uniform_view(c.buf(3)), out = c.buf(4);
   const bool rows = op == 301;
   const int M = rfl(rows ? c.i(9) : 1), pro = rows ? c.i(10) : c.i(9), K = rfl(c.i(8)), n0 = rfl(c.i(6)), n1 = rfl(c.i(7));
@@ -402,26 +431,30 @@ __device__ __noinline__ void gemv_prefetch(const Ctx& c, int op) {
   else gemv_prefetch_r<4>(w, n0, n1, K, M, c.smem);
 }
 
-template <int R> __device__ __forceinline__ void gemv_body(const Ctx& c, int M_, int pro_, float eps) {
-  const int M = rfl(M_), pro = rfl(pro_);                                       // function arguments arrive in VGPRs
-  const View x = uniform_view(c.buf(0)), x2 = uniform_view(c.buf(1)), g = uniform_view(c.buf(2)), w = uniform_view(c.buf(3));
-  const View out = uniform_view(c.buf(4)), res = uniform_view(c.buf(5));
-  const int n0 = rfl(c.i(6)), n1 = rfl(c.i(7)), K = rfl(c.i(8));
+// The streaming GEMV of ops 134 / 301; DUAL: op 311 (x, gamma, wg, wu, out, n0, n1, K, M, eps), whose output row n is
+// silu(g) * u with g and u the sums of its gate and up row blocks.
+template <int R, bool DUAL = false> __device__ __forceinline__ void gemv_body(const Ctx& c, int M_, int pro_, float eps) {
+  const int M = rfl(M_), pro = DUAL ? 1 : rfl(pro_);                            // function arguments arrive in VGPRs
+  constexpr int BX = 0, BX2 = 1, BG = DUAL ? 1 : 2, BW = DUAL ? 2 : 3, BO = 4, IA = DUAL ? 5 : 6;
+  const View x = uniform_view(c.buf(BX)), x2 = DUAL ? View{nullptr, 0, 0, 0} : uniform_view(c.buf(BX2)), g = uniform_view(c.buf(BG));
+  const View w = uniform_view(c.buf(BW)), w2 = DUAL ? uniform_view(c.buf(3)) : View{nullptr, 0, 0, 0};
+  const View out = uniform_view(c.buf(BO)), res = DUAL ? View{nullptr, 0, 0, 0} : uniform_view(c.buf(5));
+  const int n0 = rfl(c.i(IA)), n1 = rfl(c.i(IA + 1)), K = rfl(c.i(IA + 2));
   const GvGeo geo = gv_geo(K, M, R);
   const int KC = geo.KC, VS = geo.VS, PM = 16 * M;
   LDS uint16_t* vs = (LDS uint16_t*)(c.smem + geo.vs_off);                     // [M][VS]
   LDS float* rstd = (LDS float*)(c.smem + geo.rstd_off);                       // [16]
   LDS float* part = (LDS float*)(c.smem + geo.part_off);                       // [4][GV_GRP][M][16]
-  const int l = lane(), wv = wave(), nrows = n1 - n0, nrb = (nrows + 15) / 16;
+  const int l = lane(), wv = wave(), nrows = n1 - n0, nrb = ((nrows + 15) / 16) * (DUAL ? 2 : 1);   // stream row blocks
   LDS char* ring = c.smem + wv * R * GV_STEP;
-  GvStream ws;
-  ws.init(w, n0, n1, K, KC);
+  GvStream<DUAL> ws;
+  ws.init(w, n0, n1, K, KC, &w2);
   if (rfl(c.pre)) {
 #pragma unroll
-    for (int j = 0; j < R; ++j) ws.skip<R>();                                    // issued before the dependency wait
+    for (int j = 0; j < R; ++j) ws.template skip<R>();                           // issued before the dependency wait
   } else {
 #pragma unroll
-    for (int j = 0; j < R; ++j) ws.issue<R>(ring);                              // weights first: they do not wait for x
+    for (int j = 0; j < R; ++j) ws.template issue<R>(ring);                     // weights first: they do not wait for x
   }
   Ld4 lx, lx2, lg;
   lx.init(x); lx2.init(x2); lg.init(g);
@@ -459,7 +492,7 @@ template <int R> __device__ __forceinline__ void gemv_body(const Ctx& c, int M_,
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8_t)(arow ? a0 : u16x8_t{}), (bf16x8_t)w0, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8_t)(arow ? a1 : u16x8_t{}), (bf16x8_t)w1, acc, 0, 0, 0);
         wait_lds();                                                             // the slot's reads are done before it is refilled
-        ws.issue<R>(ring);
+        ws.template issue<R>(ring);
         cslot = cslot + 1 == R ? 0 : cslot + 1;
         if (++st == ns) {           // row block done. D[m][n]: lane holds m = 4 (l / 16) + i, n = l % 16; m >= M padding
           LDS float* pp = part + (wv * GV_GRP + rb) * PM + (l & 15);
@@ -474,24 +507,37 @@ template <int R> __device__ __forceinline__ void gemv_body(const Ctx& c, int M_,
       }
     }
     __syncthreads();
-    for (int e = tid(); e < ng * PM; e += KVM_THREADS) {                       // sum the four waves' tiles, in wave order
-      const int rb = e / PM, m = (e / 16) % M, nn = e % 16, n = n0 + (g0 + rb) * 16 + nn;
-      if (n >= n1) continue;
-      const float s = (part[e] + part[GV_GRP * PM + e]) + (part[2 * GV_GRP * PM + e] + part[3 * GV_GRP * PM + e]);
-      out.st((long long)m * out.cols + n, s + (res.ok() ? res.ld((long long)m * res.cols + n) : 0.f));
+    if constexpr (DUAL) {                                                      // block pairs (gate, up): silu(g) u
+      for (int e = tid(); e < (ng >> 1) * PM; e += KVM_THREADS) {
+        const int rp = e / PM, m = (e / 16) % M, nn = e % 16, n = n0 + ((g0 >> 1) + rp) * 16 + nn;
+        if (n >= n1) continue;
+        const int eg = 2 * rp * PM + e % PM, eu = eg + PM;
+        const float sg = (part[eg] + part[GV_GRP * PM + eg]) + (part[2 * GV_GRP * PM + eg] + part[3 * GV_GRP * PM + eg]);
+        const float su = (part[eu] + part[GV_GRP * PM + eu]) + (part[2 * GV_GRP * PM + eu] + part[3 * GV_GRP * PM + eu]);
+        out.st((long long)m * out.cols + n, silu_f(sg) * su);
+      }
+    } else {
+      for (int e = tid(); e < ng * PM; e += KVM_THREADS) {                     // sum the four waves' tiles, in wave order
+        const int rb = e / PM, m = (e / 16) % M, nn = e % 16, n = n0 + (g0 + rb) * 16 + nn;
+        if (n >= n1) continue;
+        const float s = (part[e] + part[GV_GRP * PM + e]) + (part[2 * GV_GRP * PM + e] + part[3 * GV_GRP * PM + e]);
+        out.st((long long)m * out.cols + n, s + (res.ok() ? res.ld((long long)m * res.cols + n) : 0.f));
+      }
     }
     if (g0 + GV_GRP < nrb) __syncthreads();                                    // the sums are read before the tiles are cleared
   }
   wait_vm_c<0>();                                                               // the ring's trailing loads have landed
 }
-template <int R> __device__ __noinline__ void gemv_stream_r(const Ctx& c, int M, int pro, float eps) { gemv_body<R>(c, M, pro, eps); }
-__device__ __noinline__ void gemv_stream(const Ctx& c, int M, int pro, float eps) {
-  if (!rfl(c.pre)) gemv_stream_r<GV_R>(c, M, pro, eps);
+template <int R, bool DUAL = false> __device__ __noinline__ void gemv_stream_r(const Ctx& c, int M, int pro, float eps) {
+  gemv_body<R, DUAL>(c, M, pro, eps);
+}
+template <bool DUAL = false> __device__ __noinline__ void gemv_stream(const Ctx& c, int M, int pro, float eps) {
+  if (!rfl(c.pre)) gemv_stream_r<GV_R, DUAL>(c, M, pro, eps);
   else {
     const int R = gv_pre_ring(rfl(M));
-    if (R == 12) gemv_stream_r<12>(c, M, pro, eps);
-    else if (R == 8) gemv_stream_r<8>(c, M, pro, eps);
-    else gemv_stream_r<4>(c, M, pro, eps);
+    if (R == 12) gemv_stream_r<12, DUAL>(c, M, pro, eps);
+    else if (R == 8) gemv_stream_r<8, DUAL>(c, M, pro, eps);
+    else gemv_stream_r<4, DUAL>(c, M, pro, eps);
   }
 }
 
@@ -504,6 +550,14 @@ __device__ __noinline__ void op_gemv_bf16_rows(const Ctx& c) {
   const View x = c.buf(0), x2 = c.buf(1), w = c.buf(3), out = c.buf(4);
   if (gemv_stream_ok(x, x2, w, out, c.i(8), c.i(9), c.i(10))) gemv_stream(c, c.i(9), c.i(10), c.f(11));
   else op_gemv_bf16_rows_simt(c);
+}
+
+// Op 311 (this executor's fused SwiGLU GEMV): out[m, n] = silu(g) * u for n in [n0, n1), g / u the RMSNorm-prologue
+// GEMV sums of row n of wg / wu (each exactly as op 301 with pro 1 computes it), rounded once as out stores. The
+// validator admits only the stream form's shapes.
+__device__ __noinline__ void op_gemv_swiglu(const Ctx& c) {
+  if (gemv_swiglu_ok(c)) gemv_stream<true>(c, c.i(8), 1, c.f(9));
+  else c.fail(KVM_ERR_OP_SHAPE, c.i(7), c.i(8));
 }
 
 }  // namespace kvm

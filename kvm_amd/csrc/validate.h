@@ -41,7 +41,7 @@ static const OpSig* find_op(int id) { for (const OpSig& o : kRegistry) if (o.id 
 static bool implemented(int id) {
   static const int ids[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 32, 33, 34, 35, 36, 37, 38, 39, 40, 41, 42, 43, 44, 45, 46, 47, 48, 49, 50,
                             51, 52, 53, 54, 55, 56, 57, 58, 59, 60, 61, 62, 63, 96, 97, 98, 99, 100, 101, 102, 103, 104, 113, 114, 115,
-                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304, 305, 306, 308, 309, 310};
+                            116, 117, 118, 120, 121, 122, 123, 126, 127, 134, 135, 136, 300, 301, 302, 303, 304, 305, 306, 308, 309, 310, 311};
   for (int i : ids) if (i == id) return true;
   return false;
 }
@@ -109,6 +109,7 @@ static char arg_class(int op, const std::string& n) {
     case 136: return in({"o"}) ? 'a' : 'f';
     case 300: return in({"x", "out"}) ? 'a' : 'f';
     case 301: return in({"gamma"}) ? 'f' : 'a';
+    case 311: return in({"gamma"}) ? 'f' : 'a';
     case 302: return in({"bias"}) ? 'f' : 'a';
     case 303: return in({"out"}) ? 'a' : 'f';
     default: return 'f';
@@ -276,6 +277,14 @@ static void extents(int op, Check& k) {
       if (pro == 1) k.need(k.B("gamma") != nullptr, "pro 1 needs gamma");
       if (pro == 2) k.need(k.B("x2") != nullptr, "pro 2 needs x2");
       const MvmBuf* w = k.B("w"); if (w) k.need(w->dtype == 2 && w->cols % 8 == 0, "w must be bf16 storage with cols % 8 == 0");
+      break; }
+    case 311: { int n0 = k.I("n0"), n1 = k.I("n1"), K = k.I("K"), M = k.I("M");
+      k.need(0 <= n0 && n0 < n1 && K > 0 && K % 256 == 0 && 1 <= M && M <= 16, "bad range, K (% 256) or M (1..16)");
+      k.ext("x", M, K); k.extn("gamma", K); k.ext("wg", n1, K); k.ext("wu", n1, K); k.ext("out", M, n1);
+      const MvmBuf* wg = k.B("wg"); const MvmBuf* wu = k.B("wu"); const MvmBuf* x = k.B("x"); const MvmBuf* o = k.B("out");
+      if (wg && wu) k.need(wg->dtype == 2 && wu->dtype == 2 && wg->cols % 8 == 0 && wg->rows == wu->rows && wg->cols == wu->cols,
+                           "wg and wu must be bf16 storage of one shape with cols % 8 == 0");
+      if (x && o) k.need(x->dtype != 1 && o->dtype != 1 && x->cols % 4 == 0, "x and out must be f32 or bf16, x cols % 4 == 0");
       break; }
     case 302: {
       int M = k.I("M"), N = k.I("N"), K = k.I("K"), fl = k.I("flags"), m0 = k.I("m0"), n0 = k.I("n0"), k0 = k.I("k0"), om0 = k.I("om0");

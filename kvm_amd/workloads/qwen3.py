@@ -38,6 +38,10 @@ class Qwen3Config:
     fused_norm: bool = True    # q / k head norm inside the attention tasks (op 306) where its shapes allow
     fused_merge: bool = True   # with fused_norm: the last split of each kv head merges its query heads (op 310)
     silu_tasks: int = 0        # batch > 1: SwiGLU tasks per layer; 0 = tasks_per_phase / 2 (measured best of 32-256)
+    fused_swiglu: bool = True  # batch > 1: gate, up and silu(g) u as one GEMV phase (op 311) writing bf16 h for the down
+    #                            projection, in place of the gate / up GEMVs and the silu_mul phase (batch 8: 7.19 vs 7.27
+    #                            ms). Batch 1 keeps the gate / up GEMVs (inlined in the static kernel; op 311 runs through
+    #                            the dispatcher there: 5.03 vs 4.87 ms).
     head_tasks: int = 0        # LM-head GEMV tasks; 0 = 2 x tasks_per_phase (measured: 512 best of 256-2048 at 256 per phase)
 
     @staticmethod
@@ -74,8 +78,9 @@ def build(c: Qwen3Config) -> Workload:
     b.fill('u', B, F)
     if rows_mode:
         b.fill('xn', B, D, 'bf16')
-        b.fill('h', B, F, 'bf16')
         b.fill('rstd', B)
+    if rows_mode:
+        b.fill('h', B, F, 'bf16')
     b.fill('logits', B, V)
     fused_norm = c.fused_norm and hd == 128 and H // Hkv in (1, 2, 4, 8)      # op 306's streaming-path shapes
     fused_merge = fused_norm and c.fused_merge
@@ -153,7 +158,14 @@ def build(c: Qwen3Config) -> Workload:
                 for h0, h1 in split(H, nm):
                     merges.append(b.task('attn_decode_merge', after=parts[bb], part='part', o='att', b=bb, h0=h0, h1=h1, S=S, H=H, hd=hd))
         to = proj(merges, 'att', f'wo.{l}', 'x', D, H * hd, P, res='x')
-        if rows_mode:
+        if rows_mode and c.fused_swiglu and F % 16 == 0 and D % 256 == 0 and B <= 16:
+            # gate, up and silu(g) u in one phase of P tasks (op 311, 16-row blocks), h in bf16 for the down projection
+            oj = b.join(to, 2 * P)
+            sw = [b.task('gemv_swiglu', after=oj, x='x', gamma=f'ln2.{l}', wg=f'wg.{l}', wu=f'wu.{l}', out='h', n0=16 * lo, n1=16 * hi,
+                         K=D, M=B, eps=c.eps) for lo, hi in split(F // 16, max(1, min(P, F // 16)))]
+            td = proj(b.join(sw, P), 'h', f'wd.{l}', 'x', D, F, P, res='x')
+            prev = td if len(td) <= 256 else b.join(td, P)
+        elif rows_mode:
             oj = b.join(to, 2 * P)
             tg = proj(oj, 'x', f'wg.{l}', 'g', F, D, P // 2, pro=1, gamma=f'ln2.{l}')     # gate and up: one round of P tasks
             tu = proj(oj, 'x', f'wu.{l}', 'u', F, D, P // 2, pro=1, gamma=f'ln2.{l}')

@@ -770,6 +770,27 @@ void op_gemv_bf16_rows(const Ctx& c) {   // this executor's op 301: gemv_bf16 fo
   }
 }
 
+// This executor's op 311: op 301 with pro 1 on the rows of wg and of wu (the two sums of a row n rounded to f32 as
+// op 301 stores them), then out = silu(g) * u rounded once as out stores it (the down projection's pro 2 prologue /
+// op 98 on the stored gate and up values).
+void op_gemv_swiglu(const Ctx& c) {
+  V x = c.buf(0), g = c.buf(1), wg = c.buf(2), wu = c.buf(3), out = c.buf(4);
+  int n0 = c.i(5), n1 = c.i(6), K = c.i(7), M = c.i(8); float eps = c.fl(9);
+  need(0 <= n0 && n0 < n1 && K > 0 && K % 256 == 0 && M >= 1 && M <= 16, "gemv_swiglu: bad args");
+  std::vector<double> v(K);
+  for (int m = 0; m < M; ++m) {
+    double ss = 0; for (int k = 0; k < K; ++k) ss += x.at(m, k) * x.at(m, k);
+    float rs = f32(1.0 / std::sqrt(ss / K + eps));
+    for (int k = 0; k < K; ++k) v[k] = bf16r(f32(x.at(m, k) * rs * g.f[k]));
+    for (int n = n0; n < n1; ++n) {
+      double yg = 0, yu = 0;
+      for (int k = 0; k < K; ++k) { yg += v[k] * wg.at(n, k); yu += v[k] * wu.at(n, k); }
+      const float gf = f32(yg), uf = f32(yu);
+      out.st((long long)m * out.cols + n, silu(gf) * uf);
+    }
+  }
+}
+
 typedef void (*OpFn)(const Ctx&);
 struct OpEnt { int id; OpFn fn; };
 const OpEnt kOps[] = {
@@ -786,7 +807,7 @@ const OpEnt kOps[] = {
   {101, op_softmax_rows_bwd}, {102, op_gather_rows_scaled}, {103, op_scatter_add_rows}, {104, op_row_dot},
   {113, op_round_bf16}, {114, op_matmul_tile_bf16}, {122, op_matmul_mma_bf16}, {134, op_gemv_bf16},
   {135, op_attn_decode_part}, {136, op_attn_decode_merge}, {115, op_adamw_lr}, {116, op_lr_schedule}, {117, op_scale_flat},
-  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce}, {304, op_matmul_mma_bf16_256}, {305, op_adamw_bf16}, {306, op_attn_decode_part_qkn}, {310, op_attn_decode_part_merge}, {308, op_matmul_mma_bf16_delta},
+  {118, op_add_rowtile}, {120, op_matmul_tile_silu_mul}, {121, op_matmul_tile_silu_mul_bwd}, {300, op_head_rmsnorm}, {301, op_gemv_bf16_rows}, {311, op_gemv_swiglu}, {302, op_matmul_mma_bf16_kr}, {303, op_splitk_reduce}, {304, op_matmul_mma_bf16_256}, {305, op_adamw_bf16}, {306, op_attn_decode_part_qkn}, {310, op_attn_decode_part_merge}, {308, op_matmul_mma_bf16_delta},
 };
 OpFn find_op(int id) { for (const OpEnt& e : kOps) if (e.id == id) return e.fn; return nullptr; }
 

@@ -160,3 +160,38 @@ def test_attn_decode_part_merge(G, S, path):
         bad = compare_run(ex, lb.metadata, ref, tol_f32=1e-4)
         assert not bad, (launch, bad)
     ex.close()
+
+
+@pytest.mark.parametrize('M,N,path', [(1, 768, 1), (1, 768, 0), (8, 512, 1), (3, 200, 0)])
+def test_gemv_swiglu(M, N, path):
+    """Op 311 (fused gate / up / silu(g) u) at K = 4096: bit for bit the device's own op 301 on the gate rows and on the
+    up rows followed by op 98 (silu_mul_fwd) into bf16, and the bf16 result within the bf16 tolerance of the oracle;
+    on the static path (pre-wait weight ring, inlined body) and the dynamic one; N = 200: ragged 16-row blocks."""
+    print(f'gemv_swiglu M {M} N {N} path {path}', flush=True)
+    K = 4096
+    b = Builder(29)
+    b.normal('x', M, K, 'f32', scale=1.0)
+    b.normal('g', 1, K, 'f32', scale=1.0)
+    b.normal('wg', N, K, 'bf16', scale=0.02)
+    b.normal('wu', N, K, 'bf16', scale=0.02)
+    b.buf('h', M, N, 'bf16', {'kind': 'fill', 'value': 0})
+    b.buf('h2', M, N, 'bf16', {'kind': 'fill', 'value': 0})
+    b.fill('gg', M, N), b.fill('uu', M, N)
+    parts = split(N // 16, 7) if N % 16 == 0 else [(0, 5), (5, 9), (9, 12.5)]
+    for lo, hi in parts:
+        b.task('gemv_swiglu', x='x', gamma='g', wg='wg', wu='wu', out='h', n0=int(16 * lo), n1=int(16 * hi), K=K, M=M, eps=1e-6)
+    tg = b.task('gemv_bf16_rows', x='x', x2=None, gamma='g', w='wg', out='gg', res=None, n0=0, n1=N, K=K, M=M, pro=1, eps=1e-6)
+    tu = b.task('gemv_bf16_rows', x='x', x2=None, gamma='g', w='wu', out='uu', res=None, n0=0, n1=N, K=K, M=M, pro=1, eps=1e-6)
+    b.task('silu_mul_fwd', after=[tg, tu], gate='gg', up='uu', out='h2', e0=0, e1=M * N)
+    w = Workload(b.spec(), b.init_override)
+    lb = bl.load(compiler.compile_spec(w.spec))
+    init = [oracle.materialize(m, w.init_override.get(m['name'])) for m in lb.metadata['buffers']]
+    ref = oracle.run(lb, [x.copy() for x in init])
+    ex = Executor.from_bundle(lb, buffers=init, path=path)
+    ex.run()
+    assert ex.path() == path
+    h, h2 = ex.read_raw('h'), ex.read_raw('h2')
+    assert (h != 0).any() and (h == h2).all()
+    bad = compare_run(ex, lb.metadata, ref, tol_f32=2e-5)
+    ex.close()
+    assert not bad, bad

@@ -455,3 +455,31 @@ def test_gpt_fp64_model_matches_the_f32_oracle():
     dev = G.deviations(names, r['buffers'], ref)
     assert dev.pop('loss_abs') < 1e-5
     assert max(dev.values()) < 2e-5, sorted(dev.items(), key=lambda kv: -kv[1])[:3]
+
+
+@pytest.mark.parametrize('M', [1, 3])
+def test_gemv_swiglu_is_gate_up_gemvs_then_silu_mul(M):
+    """Op 311 equals op 301 with the RMSNorm prologue on the gate rows and on the up rows (f32 outputs), followed by
+    op 98 (silu_mul_fwd, the reference's SwiGLU) into a bf16 buffer, bit for bit; a swapped gate / up or a missing
+    prologue fails this (silu is not symmetric in its factors)."""
+    K, N = 256, 48
+    rng = np.random.default_rng(11 + M)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    Wg, Wu = (bl.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.1) for _ in range(2))
+    vals = lambda a: {'kind': 'values', 'values': a.ravel().tolist()}
+    w = W(72)
+    w.buf('Wg', N, K, 'bf16', vals(Wg)), w.buf('Wu', N, K, 'bf16', vals(Wu)), w.buf('g', K, 1, 'f32', vals(g))
+    w.buf('X', M, K, 'f32', vals(X)), w.buf('H', M, N, 'bf16', {'kind': 'fill', 'value': 0})
+    w.task('gemv_swiglu', x='X', gamma='g', wg='Wg', wu='Wu', out='H', n0=16, n1=N, K=K, M=M, eps=1e-6)
+    w.zeros('G', M, N), w.zeros('U', M, N), w.buf('H2', M, N, 'bf16', {'kind': 'fill', 'value': 0})
+    tg = w.task('gemv_bf16_rows', x='X', x2=None, res=None, gamma='g', w='Wg', out='G', n0=16, n1=N, K=K, M=M, pro=1, eps=1e-6)
+    tu = w.task('gemv_bf16_rows', x='X', x2=None, res=None, gamma='g', w='Wu', out='U', n0=16, n1=N, K=K, M=M, pro=1, eps=1e-6)
+    w.task('silu_mul_fwd', after=[tg, tu], gate='G', up='U', out='H2', e0=0, e1=M * N)
+    r, b = _run_one(w)
+    H, H2 = _get(r, b, 'H').reshape(M, N), _get(r, b, 'H2').reshape(M, N)
+    assert np.abs(H[:, 16:]).max() > 0 and not H[:, :16].any()
+    assert np.array_equal(H[:, 16:].view(np.uint32), H2[:, 16:].view(np.uint32))
+    G, U = _get(r, b, 'G').reshape(M, N), _get(r, b, 'U').reshape(M, N)
+    swapped = bl.bf16_round((U / (1.0 + np.exp(-U.astype(np.float64))) * G).astype(np.float32))
+    assert not np.array_equal(H[:, 16:], swapped[:, 16:])

@@ -76,6 +76,7 @@ typedef struct KvmTrace {
 // KvmTrace.how bits (reference: MVM_TRACE_MISSED / _RESV / _URGENT, include/mvm_sched.h:33-36).
 #define KVM_TRACE_MISSED 1     // finished after its deadline
 #define KVM_TRACE_RESV 2       // started while its class was below its reservation
+#define KVM_TRACE_BOOST 4      // started under priority inheritance
 #define KVM_TRACE_URGENT 8     // started by the deadline (EDF) tier
 
 typedef struct KvmResult {
@@ -194,16 +195,31 @@ enum KvmSchedMode { KVM_SCHED_GLOBAL = 0, KVM_SCHED_STATIC = 1, KVM_SCHED_DYNAMI
 typedef struct KvmClassParams {
   int weight;                  // >= 1: relative share of worker-time among competing classes
   int min_cta;                 // reservation: workers the class is served first up to (0 none)
-  int max_cta;                 // cap on running tasks, >= 1 (KVM_UNLIMITED none)
+  int max_cta;                 // cap on running tasks (KVM_UNLIMITED none; 0: only reservations and inheritance start them)
   int urgent_us;               // EDF window: a ready task whose deadline is this close is served first (0 off)
   int share;                   // KVM_SCHED_STATIC: relative number of workers (>= 1)
+  int bw_cta;                  // cap on the class's running bandwidth-bound tasks (KVM_UNLIMITED none)
 } KvmClassParams;
 int kvm_set_classes(KvmExec* ex, int mode, const KvmClassParams* params, int nclasses);
+// Policy switches of KVM_SCHED_DYNAMIC (reference: MvmSchedParams.flags and MVM_SF_*, include/mvm_sched.h:26-33, default
+// MVM_SF_DEFAULT = reservations + inheritance). KVM_SCHED_F_GUARANTEE: reservations are served first. KVM_SCHED_F_INHERIT:
+// priority inheritance across version waits: while a task of class W is parked on a variable that a task of class C
+// publishes, C is boosted (transitively: C's own parked tasks boost their publishers' classes); a boosted class is served
+// before the reservations and ignores its caps, so a throttled publisher cannot hold a waiter back. KVM_SCHED_F_ARBITER:
+// at most bw_limit bandwidth-bound tasks of all classes run at once outside reservations and boosts (the reference adapts
+// this limit online from protected classes' queue waits; here it is fixed). A task is bandwidth-bound when its operator
+// streams memory (the reference's cost table, include/mvm_ops_cost.inc, restated for the operators implemented here) and
+// it moves at least 16 KiB. Default: GUARANTEE | INHERIT. Set before the first kvm_start.
+#define KVM_SCHED_F_GUARANTEE 1
+#define KVM_SCHED_F_INHERIT 2
+#define KVM_SCHED_F_ARBITER 4
+int kvm_set_sched_flags(KvmExec* ex, int flags, int bw_limit);
 // Per-class counters of the last launch (reference: MvmClassTele, include/mvm_sched.h:59-66). Times in
 // wall_clock64 ticks (100 MHz).
 typedef struct KvmClassStats {
   unsigned long long tasks, busy_ticks, resv_starts, urgent_starts, missed;
   int max_running, pad;
+  unsigned long long boost_starts;   // tasks started under priority inheritance
 } KvmClassStats;
 int kvm_class_stats(KvmExec* ex, KvmClassStats* out, int n);
 

@@ -31,14 +31,15 @@ static void usage() {
                   "  --path auto|dynamic|static  scheduler: per-worker static programs, ready queues, or chosen from the graph (default auto)\n"
                   "  --blocks N   --no-trace   --quiet   --check-ops\n"
                   "  --sched global|static|dynamic --classes N   scheduler classes (a task's class is its workload_id); per class, comma\n"
-                  "    lists: --weights, --min (reservation), --max (cap), --urgent-us (EDF window), --shares (static split)\n");
+                  "    lists: --weights, --min (reservation), --max (cap), --bw-cta (bandwidth-bound cap), --urgent-us (EDF window),\n"
+                  "    --shares (static split); --arbiter --bw-limit N (global bandwidth-bound cap), --no-guarantee, --no-inherit\n");
 }
 
 int main(int argc, char** argv) {
   std::vector<std::string> dirs; bool golden = false, quiet = false, trace = true, dump_text = false; float tol = 1e-6f, tol_bf16 = 1e-2f;
   const char* csv = nullptr; std::string dump_dir; std::vector<int> dump_idx; int repeat = 1, blocks = 0, path = KVM_PATH_AUTO; long long timeout_s = 20;
-  int sched = KVM_SCHED_GLOBAL, nclasses = 1;
-  std::vector<KvmClassParams> cls(KVM_MAX_CLASSES, KvmClassParams{1, 0, KVM_UNLIMITED, 0, 1});
+  int sched = KVM_SCHED_GLOBAL, nclasses = 1, sflags = KVM_SCHED_F_GUARANTEE | KVM_SCHED_F_INHERIT, bw_limit = KVM_UNLIMITED;
+  std::vector<KvmClassParams> cls(KVM_MAX_CLASSES, KvmClassParams{1, 0, KVM_UNLIMITED, 0, 1, KVM_UNLIMITED});
   // a comma list of integers into field f of classes 0, 1, ...
   auto list = [&](const char* v, int KvmClassParams::*f) {
     int c = 0;
@@ -79,6 +80,11 @@ int main(int argc, char** argv) {
     else if (a == "--max") { if (!list(next(), &KvmClassParams::max_cta)) { usage(); return 2; } }
     else if (a == "--urgent-us") { if (!list(next(), &KvmClassParams::urgent_us)) { usage(); return 2; } }
     else if (a == "--shares") { if (!list(next(), &KvmClassParams::share)) { usage(); return 2; } }
+    else if (a == "--bw-cta") { if (!list(next(), &KvmClassParams::bw_cta)) { usage(); return 2; } }
+    else if (a == "--arbiter") sflags |= KVM_SCHED_F_ARBITER;
+    else if (a == "--bw-limit") bw_limit = atoi(next());
+    else if (a == "--no-guarantee") sflags &= ~KVM_SCHED_F_GUARANTEE;
+    else if (a == "--no-inherit") sflags &= ~KVM_SCHED_F_INHERIT;
     else if (a == "--dump-bin") { dump_dir = next(); for (char* p = (char*)next(); *p;) { char* e; long v = strtol(p, &e, 10); if (e == p) { usage(); return 2; } dump_idx.push_back((int)v); p = *e == ',' ? e + 1 : e; } }
     else if (a == "--check-ops") { for (int id = 0; id < 400; ++id) if (const char* n = kvm_op_name(id)) printf("%3d %s\n", id, n); return 0; }
     else if (a[0] == '-') { usage(); return 2; }
@@ -112,7 +118,8 @@ int main(int argc, char** argv) {
       if (kvm_submit(ex.get(), t.data(), (int)t.size(), s.data(), (int)s.size(), a.data(), (int)a.size()) < 0)
         throw std::runtime_error(dirs[k] + ": submit: " + kvm_last_error(ex.get()));
     }
-    if (sched != KVM_SCHED_GLOBAL && kvm_set_classes(ex.get(), sched, cls.data(), nclasses) < 0)
+    if (sched != KVM_SCHED_GLOBAL && (kvm_set_classes(ex.get(), sched, cls.data(), nclasses) < 0 ||
+                                      kvm_set_sched_flags(ex.get(), sflags, bw_limit) < 0))
       throw std::runtime_error(kvm_last_error(ex.get()));
     KvmResult r{}; float ms = 0;
     if (repeat == 1) { if (kvm_start(ex.get()) < 0) throw std::runtime_error(kvm_last_error(ex.get())); }

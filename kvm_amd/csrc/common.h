@@ -79,19 +79,25 @@ struct KvmAdm {                          // device admission state
 // virtual time charged ahead of time, the running-time estimate) and a statistics line; times in wall_clock64 ticks.
 struct alignas(128) KvmClsDev {
   int weight, min_cta, max_cta, urgent_ticks, vt_mul, blk_lo, blk_hi, has_dl;   // vt_mul = 2^20 / weight
-  int pad0[24];
-  int running, pad1a;
+  int bw_cta, has_bw;              // cap on running bandwidth-bound tasks; the class has such tasks
+  int pad0[22];
+  int running, bw_running;         // running tasks; of those, bandwidth-bound ones
   unsigned long long vtime;        // sum of (ticks run) * vt_mul: the class with the least is served first
   unsigned est;                    // running-time estimate of the class's tasks (moving average, ticks)
   int pad1[27];
-  unsigned long long tasks, busy, resv_starts, urgent_starts, missed;
+  unsigned long long tasks, busy, resv_starts, urgent_starts, missed, boost_starts;
   int max_running;
-  int pad2[21];
+  int pad2[19];
 };
 static_assert(sizeof(KvmClsDev) == 384, "class lines");
+// (KVM_SCHED_F_* policy switches: include/kvm_exec.h)
+#define KVM_HOW_BW 0x100          // pop_cls / cls_done only: the claimed task counts as bandwidth-bound (never traced)
 struct KvmSchedDev {
   unsigned long long t0;           // launch time: task deadlines count from here
-  int pad[30];
+  int flags, bw_limit;             // KVM_SCHED_F_*; the global cap on running bandwidth-bound tasks (ARBITER)
+  int boost;                       // classes boosted by inheritance (bit c), recomputed on every park / unpark
+  int bw_total;                    // running bandwidth-bound tasks of all classes
+  int pad[26];
   KvmClsDev cls[KVM_MAX_CLASSES];
 };
 
@@ -142,6 +148,14 @@ struct KvmDevState {
   // bucket; a worker's lane c * nb + b watches class c's bucket b.
   KvmSchedDev* sched;
   int ncls;
+  // Priority inheritance (classes on): pv[v * KVM_MAX_CLASSES + c] = tasks of class c parked on variable v; pubcls[v] =
+  // classes with a task that publishes v; publist[0 .. npub) = the variables some task publishes. tbw[t] = 1: task t is
+  // bandwidth-bound (counts against bw_cta / bw_limit).
+  int* pv;
+  const int* pubcls;
+  const int* publist;
+  const unsigned char* tbw;
+  int npub;
   int ntasks, nvars, trace_on, nq, qcap, grid, nb, ncells;
   unsigned long long timeout_ticks;   // stall timeout in wall_clock64 ticks (100 MHz)
   unsigned long long aging_ticks;     // wall_clock64 ticks of waiting worth one priority level (0: strict priority)

@@ -77,12 +77,40 @@ __device__ __forceinline__ void enqueue(const KvmDevState& S, int t) {
   st_release(&S.ready[q * S.qcap + pos], t);
 }
 
+// Priority inheritance (reference: the policy block's boost, include/mvm_sched.cuh:35-40 and 486-496, restated without a
+// policy block): the classes boosted now, from the parked-waiter counts. wants[w] = the classes publishing a variable
+// that a parked task of class w waits on; the boost is every wanted class, closed transitively (a boosted class's own
+// parked tasks boost their publishers). Recomputed by whoever parks or unparks a task, and by idle workers of the class
+// scheduler (a recomputation that raced with another park is repaired by the next idle poll).
+__device__ int boost_mask(const KvmDevState& S) {
+  const int nc = S.ncls;
+  int wants[KVM_MAX_CLASSES] = {};
+  for (int i = 0; i < S.npub; ++i) {
+    const int v = S.publist[i], pc = S.pubcls[v];
+    for (int w = 0; w < nc; ++w)
+      if (ld_relaxed(&S.pv[v * KVM_MAX_CLASSES + w]) > 0) wants[w] |= pc & ~(1 << w);
+  }
+  int B = 0;
+  for (int w = 0; w < nc; ++w) B |= wants[w];
+  for (int it = 0; it < nc; ++it)
+    for (int c = 0; c < nc; ++c) if ((B >> c) & 1) B |= wants[c];
+  return B;
+}
+// A task of a class enters (+1) or leaves (-1) the parked state on `var`; the boost follows.
+__device__ void park_count(const KvmDevState& S, int t, int var, int d) {
+  if (!S.pv || !(S.sched->flags & KVM_SCHED_F_INHERIT)) return;
+  const int c = S.tasks[t].workload_id;
+  if (c < 0 || c >= S.ncls) return;
+  add_relaxed(&S.pv[var * KVM_MAX_CLASSES + c], d);
+  st_relaxed(&S.sched->boost, boost_mask(S));
+}
+
 __device__ void park(const KvmDevState& S, int t, int var, int want) {
   int* head = &S.park_head[var];
   int h = ld_relaxed(head);
   do { st_relaxed(&S.park_next[t], h); } while (!__hip_atomic_compare_exchange_strong(head, &h, t, __ATOMIC_ACQ_REL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
   fence_seqcst();
-  if (ld_acquire(&S.version[var]) >= want && cas_acqrel(&S.state[t], 1, 2)) enqueue(S, t);
+  if (ld_acquire(&S.version[var]) >= want && cas_acqrel(&S.state[t], 1, 2)) { park_count(S, t, var, -1); enqueue(S, t); }
 }
 
 // A task whose predecessors have all finished: run it when its version wait holds, else park it.
@@ -91,6 +119,7 @@ __device__ void release(const KvmDevState& S, int t) {
   int var = d.wait_var;
   if (var < 0 || ld_acquire(&S.version[var]) >= d.wait_ver) { st_relaxed(&S.state[t], 2); enqueue(S, t); return; }
   st_relaxed(&S.state[t], 1);
+  park_count(S, t, var, 1);
   park(S, t, var, d.wait_ver);
 }
 
@@ -110,7 +139,7 @@ __device__ void publish(const KvmDevState& S, int slot, int var, int ver) {
     int nx = ld_relaxed(&S.park_next[h]);
     if (ld_relaxed(&S.state[h]) == 1) {
       int want = S.tasks[h].wait_ver;
-      if (ld_acquire(&S.version[var]) >= want) { if (cas_acqrel(&S.state[h], 1, 2)) enqueue(S, h); }
+      if (ld_acquire(&S.version[var]) >= want) { if (cas_acqrel(&S.state[h], 1, 2)) { park_count(S, h, var, -1); enqueue(S, h); } }
       else park(S, h, var, want);
     }
     h = nx;
@@ -205,9 +234,13 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
   const bool lane_ok = l < nc * nb;
   const int c = lane_ok ? l / nb : 0, b = lane_ok ? l % nb : 0;
   KvmClsDev* const K = S.sched->cls;
-  const int mn = K[c].min_cta, mx = K[c].max_cta, urg = K[c].urgent_ticks, vt_mul = K[c].vt_mul;
+  const int flags = S.sched->flags, bw_limit = S.sched->bw_limit;
+  const bool arb = (flags & KVM_SCHED_F_ARBITER) != 0, inherit = (flags & KVM_SCHED_F_INHERIT) != 0;
+  const int mn = (flags & KVM_SCHED_F_GUARANTEE) ? K[c].min_cta : 0, mx = K[c].max_cta, urg = K[c].urgent_ticks, vt_mul = K[c].vt_mul;
+  const int bwc = K[c].bw_cta;
+  const bool bw_gate = K[c].has_bw != 0 && (bwc < KVM_UNLIMITED || arb);   // the head task's kind matters
   const bool mine = lane_ok && (int)blockIdx.x >= K[c].blk_lo && (int)blockIdx.x < K[c].blk_hi;
-  const bool need_cell = S.aging_ticks != 0 || (urg > 0 && K[c].has_dl != 0);
+  const bool need_cell = S.aging_ticks != 0 || (urg > 0 && K[c].has_dl != 0) || bw_gate;
   const int qi = (g * nc + c) * nb + b;
   const int cnt = mine ? S.qcount[qi] : 0, off = mine ? S.qoff[qi] : 0;
   const unsigned long long boost = (mine && S.aging_ticks) ? (unsigned long long)S.bucket_prio[b] * S.aging_ticks : 0ull;
@@ -222,19 +255,24 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
     bool avail = mine && h < tl && h < cnt;
     int cell = -1;
     if (avail && need_cell) { cell = ld_acquire(&S.ready[off + h]); avail = cell >= 0; }
-    int run_k = 0;
+    int run_k = 0, bwr_k = 0;
     unsigned long long vt_k = 0;
     if (l < nc) {
       run_k = ld_relaxed(&K[l].running);
+      bwr_k = ld_relaxed(&K[l].bw_running);
       vt_k = __hip_atomic_load(&K[l].vtime, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    const int run = __shfl(run_k, c, 64);
+    const int run = __shfl(run_k, c, 64), bwr = __shfl(bwr_k, c, 64);
     const unsigned long long vt = __shfl(vt_k, c, 64);
+    const int boost = inherit ? __shfl(l == 0 ? ld_relaxed(&S.sched->boost) : 0, 0, 64) : 0;
+    const int bwt = arb ? __shfl(l == 0 ? ld_relaxed(&S.sched->bw_total) : 0, 0, 64) : 0;
+    const bool isbw = bw_gate && cell >= 0 && S.tbw[cell];
     const unsigned long long now = wall_clock64();
     unsigned long long key = ~0ull, score = 0;
     if (avail) {
-      if (run < mn) key = (1ull << 60) | (((unsigned long long)run << 20) / (unsigned)(mn > 0 ? mn : 1));
-      else if (run >= mx) avail = false;
+      if ((boost >> c) & 1) key = (unsigned long long)run;                       // tier 0: inheritance, no caps
+      else if (run < mn) key = (1ull << 60) | (((unsigned long long)run << 20) / (unsigned)(mn > 0 ? mn : 1));
+      else if (run >= mx || (isbw && (bwr >= bwc || (arb && bwt >= bw_limit)))) avail = false;
       else {
         key = (3ull << 60) | (vt < (1ull << 60) ? vt : (1ull << 60) - 1);
         if (urg > 0 && cell >= 0) {
@@ -270,8 +308,17 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
       unsigned charge = 0;
       if (l == win) {
         KvmClsDev& k = K[c];
+        // counts taken before the head CAS and given back when capped meanwhile or when the CAS loses: every cap holds
+        // at every instant (tiers 0 and 1 override the caps but are counted)
         const int old = add_relaxed(&k.running, 1);
-        if (tier >= 2 && old >= mx) add_relaxed(&k.running, -1);   // capped meanwhile: look again
+        const int oldbw = isbw ? add_relaxed(&k.bw_running, 1) : 0;
+        const int oldt = isbw && arb ? add_relaxed(&S.sched->bw_total, 1) : 0;
+        auto give_back = [&]() {
+          add_relaxed(&k.running, -1);
+          if (isbw) add_relaxed(&k.bw_running, -1);
+          if (isbw && arb) add_relaxed(&S.sched->bw_total, -1);
+        };
+        if (tier >= 2 && (old >= mx || (isbw && (oldbw >= bwc || (arb && oldt >= bw_limit))))) give_back();   // capped meanwhile
         else {
           unsigned expect = (unsigned)h;
           if (__hip_atomic_compare_exchange_strong(&S.queues[qi].head, &expect, expect + 1u, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
@@ -281,7 +328,7 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
               __builtin_amdgcn_s_sleep(1);
             }
           }
-          if (got < 0) add_relaxed(&k.running, -1);
+          if (got < 0) give_back();
           else {
             __hip_atomic_fetch_max(&k.max_running, old + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             charge = __hip_atomic_load(&k.est, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -292,7 +339,8 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
       got = __shfl(got, win, 64);
       if (got >= 0) {
         est = __shfl(charge, win, 64);
-        how = tier == 1 ? KVM_TRACE_RESV : tier == 2 ? KVM_TRACE_URGENT : 0;
+        how = (tier == 0 ? KVM_TRACE_BOOST : tier == 1 ? KVM_TRACE_RESV : tier == 2 ? KVM_TRACE_URGENT : 0) |
+              (__shfl((int)isbw, win, 64) ? KVM_HOW_BW : 0);
         fence_acquire();
         return got;
       }
@@ -300,6 +348,7 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
     }
     __builtin_amdgcn_s_sleep(1);
     int fired = 0;
+    if (l == 0 && inherit && S.pv && (polls & 63) == 63) st_relaxed(&S.sched->boost, boost_mask(S));   // repair a raced boost
     if (l == 0 && (polls & 4095) == 4095) fired = stalled(S, since, seen, -1);
     if (__shfl(fired, 0, 64)) return -1;
   }
@@ -312,6 +361,10 @@ __device__ int cls_done(const KvmDevState& S, const MvmTaskDesc& d, int how, uns
   KvmClsDev& k = S.sched->cls[d.workload_id];
   const unsigned long long end = wall_clock64(), run = end - start;
   add_relaxed(&k.running, -1);
+  if (how & KVM_HOW_BW) {
+    add_relaxed(&k.bw_running, -1);
+    if (S.sched->flags & KVM_SCHED_F_ARBITER) add_relaxed(&S.sched->bw_total, -1);
+  }
   __hip_atomic_fetch_add(&k.vtime, (unsigned long long)(((long long)run - (long long)est) * (long long)k.vt_mul), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const unsigned r32 = run < 0xffffffffull ? (unsigned)run : 0xffffffffu;
   const unsigned old = __hip_atomic_load(&k.est, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -322,8 +375,9 @@ __device__ int cls_done(const KvmDevState& S, const MvmTaskDesc& d, int how, uns
   add64(&k.busy, run);
   if (how & KVM_TRACE_RESV) add64(&k.resv_starts, 1ull);
   if (how & KVM_TRACE_URGENT) add64(&k.urgent_starts, 1ull);
+  if (how & KVM_TRACE_BOOST) add64(&k.boost_starts, 1ull);
   if (missed) add64(&k.missed, 1ull);
-  return how | (missed ? KVM_TRACE_MISSED : 0);
+  return (how & ~KVM_HOW_BW) | (missed ? KVM_TRACE_MISSED : 0);
 }
 
 // Stream-mode admission, by the whole workgroup of the worker holding the admission lock: every window the host has
@@ -861,10 +915,11 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
   if (i == 0) { KvmCounters z = {}; *S.cnt = z; }
   if (S.ncls && i < S.ncls) {   // class hot and statistics lines; the parameter line stays as uploaded
     KvmClsDev& k = S.sched->cls[i];
-    k.running = 0; k.vtime = 0; k.est = 200;   // 2 us until measured
-    k.tasks = k.busy = k.resv_starts = k.urgent_starts = k.missed = 0; k.max_running = 0;
+    k.running = 0; k.bw_running = 0; k.vtime = 0; k.est = 200;   // 2 us until measured
+    k.tasks = k.busy = k.resv_starts = k.urgent_starts = k.missed = k.boost_starts = 0; k.max_running = 0;
   }
-  if (S.ncls && i == 0) S.sched->t0 = wall_clock64();
+  if (S.pv) for (int k = i; k < S.nvars * KVM_MAX_CLASSES; k += stride) S.pv[k] = 0;
+  if (S.ncls && i == 0) { S.sched->t0 = wall_clock64(); S.sched->boost = 0; S.sched->bw_total = 0; }
   if (S.stream) {
     for (long long k = i; k < (long long)S.nq * S.qcap; k += stride) S.ready64[k] = 0ull;
     for (int k = i; k < S.wcap; k += stride) { S.win_left[k] = 0; S.win_seq[k] = -1; }
@@ -962,9 +1017,10 @@ struct KvmExec {
   std::vector<Pending> pending;            // bundles submitted before kvm_start
   struct LaunchArgs L{};
   KvmDevState S{};
-  // scheduler classes (kvm_set_classes)
+  // scheduler classes (kvm_set_classes, kvm_set_sched_flags)
   int sched_mode = KVM_SCHED_GLOBAL;
   std::vector<KvmClassParams> classes;
+  int sched_flags = KVM_SCHED_F_GUARANTEE | KVM_SCHED_F_INHERIT, bw_limit = KVM_UNLIMITED;
 };
 
 #define HIPCK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { ex->err = std::string(#x) + ": " + hipGetErrorString(e_); return KVM_STATUS_HIP_ERROR; } } while (0)
@@ -1567,6 +1623,40 @@ static double task_cost_us(const MvmTaskDesc& d, const int32_t* a) {
   return 3.0;
 }
 
+// Bytes a task streams when its operator is bandwidth-bound, else -1: the reference's scheduler cost table
+// (include/mvm_ops_cost.inc: the operators it lists as BW, with its byte expressions over the argument words) for the
+// operators implemented here, and this executor's AdamW with the bf16 copy (op 305). Operators it leaves out (GEMM tiles,
+// attention, reductions, the decode GEMVs) count as not bandwidth-bound, as there. A BW task under 16 KiB is
+// latency-bound (MVM_LAT_BYTES).
+static long long task_bw_bytes(const MvmTaskDesc& d, const int32_t* a) {
+  auto U = [&](int k) { return k < d.args_words ? (long long)(unsigned)a[k] : 0ll; };
+  auto R = [&](int lo, int hi) { return std::max(0ll, U(hi) - U(lo)); };
+  switch (d.op_id) {
+    case 1: return 8 * U(2);                 // copy
+    case 2: return 12 * U(3);                // add
+    case 3: return 8 * U(3);                 // scale
+    case 4: return 8 * U(2);                 // relu
+    case 5: return 12 * U(3);                // sgd
+    case 6: return 8 * U(3);                 // predict
+    case 7: return 12 * U(5);                // mse_grad
+    case 9: return 4 * U(2);                 // fill
+    case 54: return 28 * R(6, 7);            // adamw
+    case 305: return 30 * R(6, 7);           // adamw_bf16
+    case 55: return 4 * R(3, 4);             // gradnorm_partial
+    case 42: return 12 * R(3, 4);            // residual_add
+    case 40: return 8 * R(2, 3);             // gelu_fwd
+    case 41: return 12 * R(3, 4);            // gelu_bwd
+    case 123: return 12 * R(3, 4);           // sgd_range
+    case 126: return 8 * R(2, 3);            // round_tf32
+    case 59: return 4 * R(1, 2);             // zero_buf
+    case 32: return 8 * R(4, 5) * U(7);      // embedding_fwd
+    case 51: return 4 * R(4, 5) * U(6);      // softmax_ce_fwd
+    case 53: return 8 * R(5, 6) * U(7);      // softmax_ce_bwd
+    default: return -1;
+  }
+}
+static bool task_is_bw(const MvmTaskDesc& d, const int32_t* a) { return task_bw_bytes(d, a) >= 16384; }
+
 // Static-path flags per task: KVM_SF_PUB, another worker waits for the task; KVM_SF_PRE, a decode GEMV (op 134 / 301)
 // whose weight buffer no task of the graph writes (it appears in no argument slot other than the weights of such
 // GEMVs), so its first weight loads may be issued before its dependencies are met, or a decode attention split whose
@@ -1657,7 +1747,8 @@ static int do_upload(KvmExec* ex) {
   std::vector<MvmBuf> table(ex->bufs.size());
   for (size_t i = 0; i < table.size(); ++i) table[i] = MvmBuf{ex->bufs[i].p, ex->bufs[i].rows, ex->bufs[i].cols, ex->bufs[i].cols, ex->bufs[i].dtype, {0, 0}};
   const int ncls = ex->sched_mode != KVM_SCHED_GLOBAL ? (int)ex->classes.size() : 0;
-  std::vector<unsigned char> has_dl(KVM_MAX_CLASSES, 0);
+  std::vector<unsigned char> has_dl(KVM_MAX_CLASSES, 0), has_bw(KVM_MAX_CLASSES, 0), tbw(ncls ? ex->tasks.size() : 0, 0);
+  std::vector<int> pubcls(ex->base_versions.size(), 0);   // classes publishing each variable (inheritance)
   if (ncls) {   // every task names a class; the (class, priority) buckets fit one wave's lanes
     std::vector<char> seen(KVM_PRIORITIES, 0);
     int nprio = 0;
@@ -1670,6 +1761,9 @@ static int do_upload(KvmExec* ex) {
       }
       if (!seen[d.priority]) { seen[d.priority] = 1; ++nprio; }
       if (d.deadline_us >= 0) has_dl[d.workload_id] = 1;
+      tbw[i] = task_is_bw(d, ex->args.data() + d.args_off) ? 1 : 0;
+      if (tbw[i]) has_bw[d.workload_id] = 1;
+      if (d.pub_var >= 0 && d.pub_var < (int)pubcls.size()) pubcls[d.pub_var] |= 1 << d.workload_id;
     }
     if (nprio * ncls > 64) {
       ex->err = "scheduler classes: " + std::to_string(ncls) + " classes x " + std::to_string(nprio) + " distinct priorities exceed 64 ready buckets";
@@ -1700,6 +1794,7 @@ static int do_upload(KvmExec* ex) {
       k.weight = p.weight; k.min_cta = p.min_cta; k.max_cta = p.max_cta;
       k.urgent_ticks = (int)std::min<long long>((long long)p.urgent_us * 100ll, 0x7fffffffll);
       k.vt_mul = (1 << 20) / p.weight; k.has_dl = has_dl[c];
+      k.bw_cta = p.bw_cta; k.has_bw = has_bw[c];
       k.blk_lo = 0; k.blk_hi = ex->grid;
       if (ex->sched_mode == KVM_SCHED_STATIC) {   // cumulative bounds, the last class takes the rest
         k.blk_lo = (int)(acc / tot * ex->grid + 0.5);
@@ -1713,9 +1808,25 @@ static int do_upload(KvmExec* ex) {
         }
       }
     }
+    h.flags = ex->sched_mode == KVM_SCHED_DYNAMIC ? ex->sched_flags : 0;
+    h.bw_limit = ex->bw_limit;
     KvmSchedDev* d = (KvmSchedDev*)alloc(sizeof(KvmSchedDev));
     if (!d || hipMemcpy(d, &h, sizeof h, hipMemcpyHostToDevice) != hipSuccess) { ex->err = "scheduler classes: device memory"; return KVM_STATUS_HIP_ERROR; }
     ex->S.sched = d; ex->S.ncls = ncls;
+    // inheritance: parked-waiter counts (cleared by the reset kernel), the publisher classes and the published variables
+    std::vector<int> publist;
+    for (size_t v = 0; v < pubcls.size(); ++v) if (pubcls[v]) publist.push_back((int)v);
+    const size_t nv = std::max<size_t>(pubcls.size(), 1);
+    int* pv = (int*)alloc(nv * KVM_MAX_CLASSES * sizeof(int));
+    int* pc = (int*)alloc(nv * sizeof(int));
+    int* pl = (int*)alloc(std::max<size_t>(publist.size(), 1) * sizeof(int));
+    unsigned char* tb = (unsigned char*)alloc(std::max<size_t>(tbw.size(), 1));
+    if (!pv || !pc || !pl || !tb || (!pubcls.empty() && hipMemcpy(pc, pubcls.data(), pubcls.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) ||
+        (!publist.empty() && hipMemcpy(pl, publist.data(), publist.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) ||
+        (!tbw.empty() && hipMemcpy(tb, tbw.data(), tbw.size(), hipMemcpyHostToDevice) != hipSuccess)) {
+      ex->err = "scheduler classes: device memory"; return KVM_STATUS_HIP_ERROR;
+    }
+    ex->S.pv = pubcls.empty() ? nullptr : pv; ex->S.pubcls = pc; ex->S.publist = pl; ex->S.npub = (int)publist.size(); ex->S.tbw = tb;
   }
   if (ex->cfg.path != KVM_PATH_DYNAMIC && !ncls) {
     if (int r = plan_static(ex, ex->cfg.path == KVM_PATH_STATIC)) return r;
@@ -1905,12 +2016,22 @@ int kvm_set_classes(KvmExec* ex, int mode, const KvmClassParams* params, int ncl
     const std::string w = "kvm_set_classes: class " + std::to_string(c) + ": ";
     if (p.weight < 1 || p.weight > (1 << 20)) { ex->err = w + "weight must be in [1, 2^20]"; return KVM_STATUS_INVALID; }
     if (p.min_cta < 0) { ex->err = w + "min_cta must be >= 0"; return KVM_STATUS_INVALID; }
-    if (p.max_cta < 1) { ex->err = w + "max_cta must be >= 1 (KVM_UNLIMITED for none)"; return KVM_STATUS_INVALID; }
+    if (p.max_cta < 0) { ex->err = w + "max_cta must be >= 0 (KVM_UNLIMITED for none)"; return KVM_STATUS_INVALID; }
+    if (p.bw_cta < 0) { ex->err = w + "bw_cta must be >= 0 (KVM_UNLIMITED for none)"; return KVM_STATUS_INVALID; }
     if (p.urgent_us < 0) { ex->err = w + "urgent_us must be >= 0"; return KVM_STATUS_INVALID; }
     if (mode == KVM_SCHED_STATIC && p.share < 1) { ex->err = w + "share must be >= 1"; return KVM_STATUS_INVALID; }
   }
   ex->sched_mode = mode;
   ex->classes.assign(params, params + nclasses);
+  return 0;
+}
+
+int kvm_set_sched_flags(KvmExec* ex, int flags, int bw_limit) {
+  if (ex->uploaded || ex->launched) { ex->err = "kvm_set_sched_flags: before the first kvm_start"; return KVM_STATUS_INVALID; }
+  if (flags & ~(KVM_SCHED_F_GUARANTEE | KVM_SCHED_F_INHERIT | KVM_SCHED_F_ARBITER)) { ex->err = "kvm_set_sched_flags: unknown flags"; return KVM_STATUS_INVALID; }
+  if ((flags & KVM_SCHED_F_ARBITER) && bw_limit < 1) { ex->err = "kvm_set_sched_flags: bw_limit must be >= 1"; return KVM_STATUS_INVALID; }
+  ex->sched_flags = flags;
+  ex->bw_limit = bw_limit;
   return 0;
 }
 
@@ -1922,7 +2043,7 @@ int kvm_class_stats(KvmExec* ex, KvmClassStats* out, int n) {
   HIPCK(hipMemcpy(k.data(), ex->S.sched->cls, k.size() * sizeof(KvmClsDev), hipMemcpyDeviceToHost));
   const int m = std::min(n, ex->S.ncls);
   for (int c = 0; c < m; ++c)
-    out[c] = KvmClassStats{k[c].tasks, k[c].busy, k[c].resv_starts, k[c].urgent_starts, k[c].missed, k[c].max_running, 0};
+    out[c] = KvmClassStats{k[c].tasks, k[c].busy, k[c].resv_starts, k[c].urgent_starts, k[c].missed, k[c].max_running, 0, k[c].boost_starts};
   return m;
 }
 

@@ -14,8 +14,8 @@ from conftest import GOLDEN
 from gpu_check import check_schedule, compare_run
 from kvm_amd import bundle as bl
 from kvm_amd import compiler
-from kvm_amd.executor import (SCHED_DYNAMIC, SCHED_STATIC, TRACE_MISSED, TRACE_RESV, TRACE_URGENT, UNLIMITED, Executor,
-                              KvmError)
+from kvm_amd.executor import (SCHED_DYNAMIC, SCHED_F_ARBITER, SCHED_F_GUARANTEE, SCHED_F_INHERIT, SCHED_STATIC, TRACE_BOOST,
+                              TRACE_MISSED, TRACE_RESV, TRACE_URGENT, UNLIMITED, Executor, KvmError)
 
 pytestmark = pytest.mark.gpu
 
@@ -178,7 +178,13 @@ def test_class_errors():
     with pytest.raises(KvmError, match='weight'):
         ex.set_classes(SCHED_DYNAMIC, [{'weight': 0}])
     with pytest.raises(KvmError, match='max_cta'):
-        ex.set_classes(SCHED_DYNAMIC, [{'max_cta': 0}])
+        ex.set_classes(SCHED_DYNAMIC, [{'max_cta': -1}])
+    with pytest.raises(KvmError, match='bw_cta'):
+        ex.set_classes(SCHED_DYNAMIC, [{'bw_cta': -1}])
+    with pytest.raises(KvmError, match='unknown flags'):
+        ex.set_sched_flags(8)
+    with pytest.raises(KvmError, match='bw_limit'):
+        ex.set_sched_flags(SCHED_F_ARBITER, 0)
     ex.set_classes(SCHED_DYNAMIC, [{'weight': 1}])            # graph 1 has no class
     with pytest.raises(KvmError, match='workload_id'):
         ex.start()
@@ -209,3 +215,106 @@ def test_cli_sched_flags(tmp_path):
     assert lines[1].startswith('class 0: 6 tasks') and lines[2].startswith('class 1: 3 tasks'), lines
     r = subprocess.run([str(exe), '--sched', 'dynamic', '--classes', '1', str(d)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 1 and 'workload_id' in r.stderr, (r.stdout, r.stderr)
+
+
+# ---- priority inheritance across version waits and bandwidth caps (reference: include/mvm_sched.cuh:35-40, 486-496;
+# include/mvm_sched.h:26-33, 45-46)
+
+def versioned_spec(graphs, variables):
+    """graphs: per class, a list of (spin us, publishes var or None, reads var or None)."""
+    out = []
+    for c, tasks in enumerate(graphs):
+        ts = []
+        for k, (us, pub, rd) in enumerate(tasks):
+            t = {'id': f't{k}', 'op': 'spin', 'args': {'us': us}}
+            if pub:
+                t['publishes'] = pub
+            if rd:
+                t['reads'] = [{'var': rd, 'policy': 'at_least', 'version': 1}]
+            ts.append(t)
+        out.append({'name': f'c{c}', 'tasks': ts})
+    return {'variables': variables, 'buffers': [{'name': 'x', 'rows': 4}], 'graphs': out}
+
+
+def run_flags(spec, classes, flags, bw_limit=UNLIMITED, timeout_s=20.0):
+    b = bl.load(compiler.compile_spec(spec))
+    ex = Executor.from_bundle(b, timeout_s=timeout_s)
+    ex.set_classes(SCHED_DYNAMIC, classes)
+    ex.set_sched_flags(flags, bw_limit)
+    return ex, b
+
+
+def test_inheritance_runs_a_fully_throttled_publisher():
+    """Class 1 may not run at all (max_cta 0) but publishes the version a class-0 task waits for: inheritance boosts it,
+    its task starts under the boost and the graph completes; with inheritance off the waiter parks for ever and the run
+    ends with the stall TIMEOUT (the reference's negative test, mvm_sched.cuh:40)."""
+    spec = versioned_spec([[(20, None, 'v'), (20, None, None)], [(50, 'v', None)]], ['v'])
+    classes = [{}, {'max_cta': 0}]
+    ex, b = run_flags(spec, classes, SCHED_F_GUARANTEE | SCHED_F_INHERIT)
+    ex.run()
+    tr = check_schedule(ex, b)
+    cls = b.tasks[:, 12]
+    assert (tr['how'][cls == 1] & TRACE_BOOST).all()
+    assert ex.class_stats(2)['boost_starts'][1] == 1
+    assert ex.versions(1)[0] == 1
+    ex.close()
+    ex, b = run_flags(spec, classes, SCHED_F_GUARANTEE, timeout_s=0.5)
+    ex.start()
+    res = ex.finish(check=False)
+    assert res['err_code'] == 15, res          # TIMEOUT: nothing finished while work was pending
+    ex.close()
+
+
+def test_inheritance_is_transitive():
+    """Class 0 waits on v1, published by a class-1 task that itself waits on v2, published by class 2; classes 1 and 2
+    are both throttled to nothing: both get boosted (the closure over parked waiters) and the chain completes in order."""
+    spec = versioned_spec([[(10, None, 'v1')], [(30, 'v1', 'v2')], [(30, 'v2', None)]], ['v1', 'v2'])
+    ex, b = run_flags(spec, [{}, {'max_cta': 0}, {'max_cta': 0}], SCHED_F_GUARANTEE | SCHED_F_INHERIT)
+    ex.run()
+    tr = check_schedule(ex, b)
+    cls = b.tasks[:, 12]
+    assert (tr['how'][cls >= 1] & TRACE_BOOST).all()
+    t1, t2 = np.where(cls == 1)[0][0], np.where(cls == 2)[0][0]
+    assert tr['end'][t2] <= tr['start'][t1]
+    assert ex.versions(2).tolist() == [1, 1]
+    ex.close()
+
+
+def fill_spec(per_class, n=1 << 22):
+    """Per class, `per_class[c]` independent fill tasks of n floats each (bandwidth-bound: 4n bytes) and two spins."""
+    graphs = []
+    for c, k in enumerate(per_class):
+        ts = [{'id': f'f{i}', 'op': 'fill', 'args': {'x': f'b{c}', 'value': float(i), 'n': n}} for i in range(k)]
+        ts += [{'id': f's{i}', 'op': 'spin', 'args': {'us': 30}} for i in range(2)]
+        graphs.append({'name': f'c{c}', 'tasks': ts})
+    return {'buffers': [{'name': f'b{c}', 'rows': n} for c in range(len(per_class))], 'graphs': graphs}
+
+
+def test_bw_cta_bounds_a_class_bandwidth_bound_tasks():
+    """bw_cta 2: at no instant do more than two of class 0's fill tasks run (its spin tasks are not bandwidth-bound and
+    are not held back); uncapped, the same graph runs more of them at once (so the bound is the cap's doing)."""
+    spec = fill_spec([24, 8])
+    for cap in (2, UNLIMITED):
+        ex, b = run_flags(spec, [{'bw_cta': cap}, {}], SCHED_F_GUARANTEE | SCHED_F_INHERIT)
+        ex.run()
+        tr = check_schedule(ex, b)
+        cls, fills = b.tasks[:, 12], b.tasks[:, 0] == 9
+        peak = max_overlap(tr, (cls == 0) & fills)
+        print('bw_cta', cap, 'peak running fills', peak, flush=True)
+        if cap == 2:
+            assert 1 <= peak <= 2
+        else:
+            assert peak > 2
+        ex.close()
+
+
+def test_arbiter_bounds_bandwidth_bound_tasks_of_all_classes():
+    """ARBITER with bw_limit 3: at most three fill tasks of the two classes together run at once."""
+    spec = fill_spec([16, 16])
+    ex, b = run_flags(spec, [{}, {}], SCHED_F_GUARANTEE | SCHED_F_INHERIT | SCHED_F_ARBITER, bw_limit=3)
+    ex.run()
+    tr = check_schedule(ex, b)
+    peak = max_overlap(tr, b.tasks[:, 0] == 9)
+    print('arbiter peak running fills', peak, flush=True)
+    assert 1 <= peak <= 3
+    ex.close()

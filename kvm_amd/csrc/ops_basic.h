@@ -43,19 +43,19 @@ __device__ __noinline__ void op_spin(const Ctx& c) {
 }
 
 // ---------------------------------------------------------------------------------------------- elementwise
-// tanh from the identity tanh(u) = sign(u) (1 - e) / (1 + e) with e = exp(-2|u|) = 2^(-2 log2(e) |u|), evaluated with
-// the hardware exp2 and reciprocal: absolute error a few 1e-8, no cancellation for large |u| (e -> 0).
-__device__ __forceinline__ float tanh_hw(float u) {
-  const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * fabsf(u));
-  return copysignf((1.f - e) * __builtin_amdgcn_rcpf(1.f + e), u);
+// tanh-GELU through the identity 0.5 (1 + tanh(u)) = sigmoid(2u): gelu(x) = x / (1 + 2^(-2 log2(e) u)) with
+// u = sqrt(2/pi) (x + 0.044715 x^3), one hardware exp2 and one reciprocal (absolute error below 1e-6 of the tanh
+// form in f32; an epilogue of the GEMM tiles, where half the instructions of the tanh form made it VALU-bound).
+// For x -> -inf the exponential overflows to inf and the result is -0; for x -> +inf it is x.
+__device__ __forceinline__ float gelu_sig(float x, float x2) {
+  const float t = fmaf(0.044715f * x2, x, x);                            // x + 0.044715 x^3
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-2.302208198144325f * t));   // sigmoid(2 sqrt(2/pi) t)
 }
-__device__ __forceinline__ float gelu_f(float x) {
-  float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.f + tanh_hw(u));
-}
+__device__ __forceinline__ float gelu_f(float x) { return x * gelu_sig(x, x * x); }
+// d/dx x s(x) = s + x s (1 - s) 2 sqrt(2/pi) (1 + 3 * 0.044715 x^2), s = sigmoid(2u).
 __device__ __forceinline__ float gelu_grad_f(float x) {
-  float t = tanh_hw(0.7978845608028654f * (x + 0.044715f * x * x * x));
-  return 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * 0.7978845608028654f * (1.f + 3.f * 0.044715f * x * x);
+  const float x2 = x * x, s = gelu_sig(x, x2);
+  return fmaf((x * s) * (1.f - s), fmaf(0.21406444881780076f, x2, 1.5957691216057308f), s);
 }
 __device__ __forceinline__ float sigmoid_f(float x) { return x >= 0.f ? 1.f / (1.f + __expf(-x)) : __expf(x) / (1.f + __expf(x)); }
 __device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }

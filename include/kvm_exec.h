@@ -190,7 +190,9 @@ int kvm_static_plan(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, i
 // with the least weighted worker-time (ticks run / weight) among those below their cap (running < max_cta). The cap is
 // a hard bound on the class's concurrently running tasks outside its reservation. KVM_SCHED_STATIC: the workers are
 // split among the classes in proportion to `share` and each serves only its own class. Priorities and aging order
-// the tasks inside a class. Set before the first kvm_start; not in stream mode; the launches run the dynamic path.
+// the tasks inside a class. Set before the first kvm_start; the launches run the dynamic path. In stream mode (the
+// reference's admission path, where classes are the reason it exists) each class has one FIFO ring per queue group:
+// priorities do not reorder tasks inside a class there, and deadline_us counts from the admission of the task's window.
 enum KvmSchedMode { KVM_SCHED_GLOBAL = 0, KVM_SCHED_STATIC = 1, KVM_SCHED_DYNAMIC = 2 };
 typedef struct KvmClassParams {
   int weight;                  // >= 1: relative share of worker-time among competing classes

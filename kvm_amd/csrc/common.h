@@ -68,8 +68,9 @@ struct KvmHostCtl {                      // pinned, written by the host (submitt
 struct KvmHostWin { int seq, ntasks, nedges, nroots; int qn[8]; int pad[4]; };   // per slot; qn: tasks per ready queue
 struct KvmAdm {                          // device admission state
   int lock, next, fin, admitted;         // next: seq of the next window to admit; fin: closed and everything admitted
-  int total[8];                          // tasks admitted per ready queue (tickets below it will be served)
-  int pad[16];
+  int total[64];                         // tasks admitted per ready queue (tickets below it will be served); with
+                                         // scheduler classes per (queue group, class) ring
+  int pad[24];
 };
 
 // Everything the persistent kernel reads. One task graph per launch (the submitted bundles concatenated), or, in
@@ -143,18 +144,20 @@ struct KvmDevState {
   const char* hwin;          // device address of the pinned staging: KvmHostWin[wcap], then per slot recs, tasks, succ, roots
   int* win_left;             // [wcap] tasks of the slot's window not yet finished
   int* win_seq;              // [wcap] seq of the window in the slot
+  unsigned long long* win_t0;   // [wcap] admission time of the slot's window (stream-mode deadlines count from it)
   int stream, wcap, wtasks, wedges;
   // Scheduler classes (ncls > 0): task t of class c = tasks[t].workload_id goes to queue ((t % nq) * ncls + c) * nb +
-  // bucket; a worker's lane c * nb + b watches class c's bucket b.
+  // bucket; a worker's lane c * nb + b watches class c's bucket b. In stream mode nb = 1 and queue (t % nq) * ncls + c
+  // is a ring of ready64 cells like the FIFO queues.
   KvmSchedDev* sched;
   int ncls;
   // Priority inheritance (classes on): pv[v * KVM_MAX_CLASSES + c] = tasks of class c parked on variable v; pubcls[v] =
   // classes with a task that publishes v; publist[0 .. npub) = the variables some task publishes. tbw[t] = 1: task t is
   // bandwidth-bound (counts against bw_cta / bw_limit).
   int* pv;
-  const int* pubcls;
+  int* pubcls;               // stream mode: or-ed in at admission (publist then lists every variable)
   const int* publist;
-  const unsigned char* tbw;
+  unsigned char* tbw;        // stream mode: written at admission, per slot
   int npub;
   int ntasks, nvars, trace_on, nq, qcap, grid, nb, ncells;
   unsigned long long timeout_ticks;   // stall timeout in wall_clock64 ticks (100 MHz)

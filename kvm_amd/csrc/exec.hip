@@ -20,6 +20,7 @@
 //     exchange list) form a Dekker pair, and a per-task state CAS makes the enqueue unique.
 //   * Errors: first error wins (CAS on err_code); every worker polls it while waiting and leaves. A stall timeout
 //     (no task finished for timeout_ticks while a worker waits) ends the run with TIMEOUT instead of hanging.
+#include <functional>
 #include <hip/hip_runtime.h>
 #include <algorithm>
 #include <cstdio>
@@ -57,9 +58,26 @@ __device__ __forceinline__ void put_cell64(const KvmDevState& S, int q, unsigned
   if (release) __hip_atomic_store(c, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
   else __hip_atomic_store(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Stream mode: the ring of task t (its queue group, and with scheduler classes its class within the group).
+__device__ __forceinline__ int ring_of(const KvmDevState& S, int t) {
+  return S.ncls ? (t % S.nq) * S.ncls + S.tasks[t].workload_id : t % S.nq;
+}
+// Deadlines count from the launch, in stream mode from the admission of the task's window.
+__device__ __forceinline__ unsigned long long deadline_base(const KvmDevState& S, int t) {
+  return S.stream ? S.win_t0[t / S.wtasks] : S.sched->t0;
+}
+// Stream mode: takes the admission lock when a window is staged and not admitted yet (or the host closed and fin is
+// still down). Thread 0 / one lane only.
+__device__ bool take_admission(const KvmDevState& S) {
+  if (ld_relaxed(&S.adm->fin)) return false;
+  const bool work = (long long)ld_relaxed(&S.adm->next) < ld_sys64(&S.hctl->submitted) || ld_sys(&S.hctl->closed);
+  int z = 0;
+  return work && ld_relaxed(&S.adm->lock) == 0 &&
+         __hip_atomic_compare_exchange_strong(&S.adm->lock, &z, 1, __ATOMIC_ACQUIRE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ void enqueue(const KvmDevState& S, int t) {
   if (S.stream) {
-    const int q = t % S.nq;
+    const int q = ring_of(S, t);
     put_cell64(S, q, (unsigned)add_relaxed(&S.queues[q].tail, 1), t, true);
     return;
   }
@@ -240,9 +258,10 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
   const int bwc = K[c].bw_cta;
   const bool bw_gate = K[c].has_bw != 0 && (bwc < KVM_UNLIMITED || arb);   // the head task's kind matters
   const bool mine = lane_ok && (int)blockIdx.x >= K[c].blk_lo && (int)blockIdx.x < K[c].blk_hi;
-  const bool need_cell = S.aging_ticks != 0 || (urg > 0 && K[c].has_dl != 0) || bw_gate;
+  const bool strm = S.stream != 0;
+  const bool need_cell = strm || S.aging_ticks != 0 || (urg > 0 && K[c].has_dl != 0) || bw_gate;
   const int qi = (g * nc + c) * nb + b;
-  const int cnt = mine ? S.qcount[qi] : 0, off = mine ? S.qoff[qi] : 0;
+  const int cnt = mine && !strm ? S.qcount[qi] : 0, off = mine && !strm ? S.qoff[qi] : 0;
   const unsigned long long boost = (mine && S.aging_ticks) ? (unsigned long long)S.bucket_prio[b] * S.aging_ticks : 0ull;
   const unsigned long long t0 = S.sched->t0;
   unsigned long long since = wall_clock64();
@@ -250,11 +269,22 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
   for (unsigned polls = 0;; ++polls) {
     if (__shfl(ld_relaxed(&S.cnt->err_code), 0, 64) != 0) return -1;
     const int h = mine ? (int)ld_relaxed(&S.queues[qi].head) : 0;
-    const int tl = mine ? ld_relaxed(&S.queues[qi].tail) : 0;
-    if (__ballot(mine && h < cnt) == 0ull) return -1;
-    bool avail = mine && h < tl && h < cnt;
+    bool avail;
     int cell = -1;
-    if (avail && need_cell) { cell = ld_acquire(&S.ready[off + h]); avail = cell >= 0; }
+    if (strm) {   // a ring: the head cell is published when it carries the head's round; done once closed and drained
+      if (ld_acquire(&S.adm->fin) && __ballot(mine && (unsigned)h < (unsigned)ld_relaxed(&S.adm->total[qi])) == 0ull) return -1;
+      avail = false;
+      if (mine) {
+        const unsigned long long v = __hip_atomic_load(&S.ready64[(size_t)qi * S.qcap + ((unsigned)h & (unsigned)(S.qcap - 1))],
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((unsigned)(v >> 32) == (unsigned)h / (unsigned)S.qcap + 1u) { cell = (int)(unsigned)v; avail = true; }
+      }
+    } else {
+      const int tl = mine ? ld_relaxed(&S.queues[qi].tail) : 0;
+      if (__ballot(mine && h < cnt) == 0ull) return -1;
+      avail = mine && h < tl && h < cnt;
+      if (avail && need_cell) { cell = ld_acquire(&S.ready[off + h]); avail = cell >= 0; }
+    }
     int run_k = 0, bwr_k = 0;
     unsigned long long vt_k = 0;
     if (l < nc) {
@@ -278,7 +308,7 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
         if (urg > 0 && cell >= 0) {
           const int dl = S.tasks[cell].deadline_us;
           if (dl >= 0) {
-            long long slack = (long long)(t0 + (unsigned long long)dl * 100ull) - (long long)now;
+            long long slack = (long long)((strm ? S.win_t0[cell / S.wtasks] : t0) + (unsigned long long)dl * 100ull) - (long long)now;
             if (slack <= (long long)urg) {
               slack = slack < -KVM_SLACKMAX ? -KVM_SLACKMAX : slack > KVM_SLACKMAX ? KVM_SLACKMAX : slack;
               key = (2ull << 60) | (unsigned long long)(slack + KVM_SLACKMAX);
@@ -322,7 +352,10 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
         else {
           unsigned expect = (unsigned)h;
           if (__hip_atomic_compare_exchange_strong(&S.queues[qi].head, &expect, expect + 1u, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-            for (;;) {   // the enqueuer reserved this cell before we saw the tail: its store is in flight
+            // ring: the cell read above is the head's (its round matched, and it cannot be reused before its task has
+            // run, which needs this claim); counted queues: the enqueuer reserved the cell before we saw the tail
+            if (strm) got = cell;
+            else for (;;) {   // the enqueuer reserved this cell before we saw the tail: its store is in flight
               got = ld_relaxed(&S.ready[off + h]);
               if (got >= 0 || ld_relaxed(&S.cnt->err_code) != 0) break;
               __builtin_amdgcn_s_sleep(1);
@@ -347,6 +380,7 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
       continue;
     }
     __builtin_amdgcn_s_sleep(1);
+    if (strm && (polls & 15) == 0 && __shfl((int)(l == 0 && take_admission(S)), 0, 64)) return -2;   // lock taken: admit
     int fired = 0;
     if (l == 0 && inherit && S.pv && (polls & 63) == 63) st_relaxed(&S.sched->boost, boost_mask(S));   // repair a raced boost
     if (l == 0 && (polls & 4095) == 4095) fired = stalled(S, since, seen, -1);
@@ -357,7 +391,7 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
 // Completion accounting of a class-mode task (thread 0): the worker leaves its class's running count, the
 // virtual-time charge taken at the claim is corrected to the ticks run, the class's running-time estimate moves
 // (a racy moving average, an estimate by design) and the statistics line counts the task. Returns the trace bits.
-__device__ int cls_done(const KvmDevState& S, const MvmTaskDesc& d, int how, unsigned est, unsigned long long start) {
+__device__ int cls_done(const KvmDevState& S, const MvmTaskDesc& d, int slot, int how, unsigned est, unsigned long long start) {
   KvmClsDev& k = S.sched->cls[d.workload_id];
   const unsigned long long end = wall_clock64(), run = end - start;
   add_relaxed(&k.running, -1);
@@ -369,7 +403,7 @@ __device__ int cls_done(const KvmDevState& S, const MvmTaskDesc& d, int how, uns
   const unsigned r32 = run < 0xffffffffull ? (unsigned)run : 0xffffffffu;
   const unsigned old = __hip_atomic_load(&k.est, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __hip_atomic_store(&k.est, old ? (unsigned)(((unsigned long long)old * 7ull + r32) / 8ull) : r32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const bool missed = d.deadline_us >= 0 && end > S.sched->t0 + (unsigned long long)d.deadline_us * 100ull;
+  const bool missed = d.deadline_us >= 0 && end > deadline_base(S, slot) + (unsigned long long)d.deadline_us * 100ull;
   auto add64 = [](unsigned long long* p, unsigned long long v) { __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
   add64(&k.tasks, 1ull);
   add64(&k.busy, run);
@@ -386,6 +420,7 @@ __device__ int cls_done(const KvmDevState& S, const MvmTaskDesc& d, int how, uns
 // order. Then, once the host has closed and everything is admitted, fin is raised. Releases the lock.
 __device__ void admit_windows(const KvmDevState& S) {
   __shared__ int s_go, s_seq;
+  __shared__ int s_ring[KVM_MAX_QUEUES * KVM_MAX_CLASSES];   // with classes: the window's tasks per (group, class) ring
   const int t = threadIdx.x;
   const KvmWinLayout lay(S.wcap, S.wtasks, S.wedges);
   for (;;) {
@@ -410,18 +445,29 @@ __device__ void admit_windows(const KvmDevState& S) {
     int32_t* ds = const_cast<int32_t*>(S.succ) + (size_t)w * S.wedges;
     for (int k = t; k < ne; k += KVM_THREADS) ds[k] = hs[k];
     const MvmTaskDesc* htd = (const MvmTaskDesc*)(S.hwin + lay.tasks) + base;
+    const int nring = S.nq * S.ncls;
+    if (S.ncls) for (int k = t; k < nring; k += KVM_THREADS) s_ring[k] = 0;
+    __syncthreads();
     for (int k = t; k < n; k += KVM_THREADS) {
       S.indeg[base + k] = htd[k].indegree;
       S.state[base + k] = 0;
       S.park_next[base + k] = -1;
       if (S.trace_on) { KvmTrace z = {}; z.ver0 = z.ver1 = -1; S.trace[base + k] = z; }
+      if (S.ncls) {   // class of the task (validated on the host), its bandwidth flag (staged in reserved1), its publication
+        const int cls = htd[k].workload_id, pv = htd[k].pub_var;
+        atomicAdd(&s_ring[((base + k) % S.nq) * S.ncls + cls], 1);
+        S.tbw[base + k] = (unsigned char)(htd[k].reserved1 & 1);
+        if (pv >= 0) __hip_atomic_fetch_or(&S.pubcls[pv], 1 << cls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (t == 0) {
       st_relaxed(&S.win_left[w], n);
       st_relaxed(&S.win_seq[w], seq);
-      for (int q = 0; q < S.nq; ++q) add_relaxed(&S.adm->total[q], ld_sys(&hm->qn[q]));
+      __hip_atomic_store(&S.win_t0[w], wall_clock64(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (S.ncls) for (int r = 0; r < nring; ++r) add_relaxed(&S.adm->total[r], s_ring[r]);
+      else for (int q = 0; q < S.nq; ++q) add_relaxed(&S.adm->total[q], ld_sys(&hm->qn[q]));
       add_relaxed(&S.adm->admitted, n);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     }
@@ -454,13 +500,7 @@ __device__ int stream_next(const KvmDevState& S, long long& held) {
     if ((unsigned)(v >> 32) == round) { fence_acquire(); held = -1; return (int)(unsigned)v; }
     if (err != 0) return -1;
     if (ld_relaxed(&S.adm->fin) && tk >= (unsigned)ld_relaxed(&S.adm->total[q])) return -1;
-    if ((polls & 15) == 0 && !ld_relaxed(&S.adm->fin)) {
-      const bool work = (long long)ld_relaxed(&S.adm->next) < ld_sys64(&S.hctl->submitted) || ld_sys(&S.hctl->closed);
-      int z = 0;
-      if (work && ld_relaxed(&S.adm->lock) == 0 &&
-          __hip_atomic_compare_exchange_strong(&S.adm->lock, &z, 1, __ATOMIC_ACQUIRE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-        return -2;
-    }
+    if ((polls & 15) == 0 && take_admission(S)) return -2;
     __builtin_amdgcn_s_sleep(2);
     if ((polls & 4095) == 4095 && stalled(S, since, seen, (int)tk)) return -1;
   }
@@ -726,15 +766,17 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
   for (;;) {
     KvmRec& s_rec = s_recs[cur];
     MvmTaskDesc& s_desc = s_rec.desc;
-    if (S.stream) {
+    if (S.ncls) {   // class pop (-2 in stream mode: the admission lock was taken)
+      if (wave() == 0) {
+        const int slot = pop_cls(S, how, est);
+        if (t == 0) { s_slot = slot == -2 ? -2 : ld_relaxed(&S.cnt->err_code) != 0 ? -1 : slot; t_start = wall_clock64(); }
+      }
+      __syncthreads();
+      if (s_slot == -2) { admit_windows(S); continue; }
+    } else if (S.stream) {
       if (t == 0) s_slot = stream_next(S, held);
       __syncthreads();
       if (s_slot == -2) { admit_windows(S); continue; }
-    } else if (S.ncls) {
-      if (wave() == 0) {
-        const int slot = pop_cls(S, how, est);
-        if (t == 0) { s_slot = ld_relaxed(&S.cnt->err_code) != 0 ? -1 : slot; t_start = wall_clock64(); }
-      }
     } else if (S.tq) {
       if (wave() == 0) {
         const int slot = pop_prio(S);
@@ -861,7 +903,11 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
         }
         const int sq = direct ? s % S.nq : -1;
         if (S.stream) {   // stream mode: one tail reservation per task, the cell stamped with its round
-          if (direct) { st_relaxed(&S.state[s], 2); put_cell64(S, sq, (unsigned)add_relaxed(&S.queues[sq].tail, 1), s, false); }
+          if (direct) {
+            const int r = ring_of(S, s);
+            st_relaxed(&S.state[s], 2);
+            put_cell64(S, r, (unsigned)add_relaxed(&S.queues[r].tail, 1), s, false);
+          }
           continue;
         }
         int cnt_mine = 0;            // lane q < nq: how many of this round's tasks go to queue q
@@ -887,7 +933,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
     }
     if (t == 0) {
       if (S.ncls) {
-        const int bits = cls_done(S, s_desc, how, est, t_start);
+        const int bits = cls_done(S, s_desc, slot, how, est, t_start);
         if (S.trace_on) S.trace[slot].how = bits;
       }
       st_relaxed(&S.done_blk[blockIdx.x], ++ndone);
@@ -921,8 +967,9 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
   if (S.pv) for (int k = i; k < S.nvars * KVM_MAX_CLASSES; k += stride) S.pv[k] = 0;
   if (S.ncls && i == 0) { S.sched->t0 = wall_clock64(); S.sched->boost = 0; S.sched->bw_total = 0; }
   if (S.stream) {
-    for (long long k = i; k < (long long)S.nq * S.qcap; k += stride) S.ready64[k] = 0ull;
-    for (int k = i; k < S.wcap; k += stride) { S.win_left[k] = 0; S.win_seq[k] = -1; }
+    for (long long k = i; k < (long long)S.nq * (S.ncls ? S.ncls : 1) * S.qcap; k += stride) S.ready64[k] = 0ull;
+    for (int k = i; k < S.wcap; k += stride) { S.win_left[k] = 0; S.win_seq[k] = -1; S.win_t0[k] = 0ull; }
+    if (S.ncls) for (int k = i; k < S.nvars; k += stride) S.pubcls[k] = 0;
     if (i == 0) { KvmAdm z = {}; *S.adm = z; }
   }
 }
@@ -1342,7 +1389,12 @@ static std::vector<MvmBuf> buf_table(const KvmExec* ex) {
   return table;
 }
 
-// Device window slots, pinned staging and control block; reset and launch of the persistent kernel.
+static int upload_classes(KvmExec* ex, const std::function<void*(size_t)>& alloc, const unsigned char* has_dl, const unsigned char* has_bw,
+                          const std::vector<int>& pubcls, const std::vector<unsigned char>& tbw, bool stream);
+static bool task_is_bw(const MvmTaskDesc& d, const int32_t* a);
+
+// Device window slots, pinned staging and control block; reset and launch of the persistent kernel. With scheduler
+// classes each queue group holds one ring per class.
 static int stream_launch(KvmExec* ex) {
   const KvmConfig& c = ex->cfg;
   const int cap = c.window_cap * c.window_tasks;
@@ -1364,8 +1416,9 @@ static int stream_launch(KvmExec* ex) {
   S.state = (int*)alloc((size_t)cap * sizeof(int));
   S.park_next = (int*)alloc((size_t)cap * sizeof(int));
   if (c.trace_on) S.trace = (KvmTrace*)alloc((size_t)cap * sizeof(KvmTrace));
-  S.ready64 = (unsigned long long*)alloc((size_t)nq * qcap * sizeof(unsigned long long));
-  S.queues = (KvmQueue*)alloc(nq * sizeof(KvmQueue));
+  const int ncls = ex->sched_mode != KVM_SCHED_GLOBAL ? (int)ex->classes.size() : 0, nring = nq * std::max(1, ncls);
+  S.ready64 = (unsigned long long*)alloc((size_t)nring * qcap * sizeof(unsigned long long));
+  S.queues = (KvmQueue*)alloc(nring * sizeof(KvmQueue));
   S.done_blk = (int*)alloc(ex->grid * sizeof(int));
   S.version = (int*)alloc(ex->base_versions.size() * sizeof(int));
   S.park_head = (int*)alloc(ex->base_versions.size() * sizeof(int));
@@ -1373,10 +1426,11 @@ static int stream_launch(KvmExec* ex) {
   S.adm = (KvmAdm*)alloc(sizeof(KvmAdm));
   S.win_left = (int*)alloc(c.window_cap * sizeof(int));
   S.win_seq = (int*)alloc(c.window_cap * sizeof(int));
+  S.win_t0 = (unsigned long long*)alloc(c.window_cap * sizeof(unsigned long long));
   ex->L = LaunchArgs{};
   ex->L.base = (int*)alloc(ex->base_versions.size() * sizeof(int));
   if (!S.recs || !S.tasks || !S.succ || !S.indeg || !S.state || !S.park_next || (c.trace_on && !S.trace) || !S.ready64 || !S.queues ||
-      !S.done_blk || !S.version || !S.park_head || !S.cnt || !S.adm || !S.win_left || !S.win_seq || !ex->L.base) {
+      !S.done_blk || !S.version || !S.park_head || !S.cnt || !S.adm || !S.win_left || !S.win_seq || !S.win_t0 || !ex->L.base) {
     ex->err = "stream mode: device memory for the window slots"; return KVM_STATUS_HIP_ERROR;
   }
   const KvmWinLayout lay(c.window_cap, c.window_tasks, c.window_edges);
@@ -1397,6 +1451,16 @@ static int stream_launch(KvmExec* ex) {
   S.ntasks = cap; S.nvars = (int)ex->base_versions.size(); S.trace_on = c.trace_on ? 1 : 0;
   S.nq = nq; S.qcap = qcap; S.grid = ex->grid; S.nb = 1; S.ncells = 0;
   S.timeout_ticks = c.timeout_us * 100ull;
+  if (ncls) {   // deadlines and bandwidth caps may concern any class: their head cells are always inspected
+    unsigned char hd[KVM_MAX_CLASSES] = {}, hb[KVM_MAX_CLASSES] = {};
+    for (int k = 0; k < ncls; ++k) {
+      hd[k] = ex->classes[k].urgent_us > 0;
+      hb[k] = ex->classes[k].bw_cta < KVM_UNLIMITED || (ex->sched_flags & KVM_SCHED_F_ARBITER);
+    }
+    const std::vector<int> pubcls(ex->base_versions.size(), 0);
+    const std::vector<unsigned char> tbw((size_t)cap, 0);
+    if (int r = upload_classes(ex, alloc, hd, hb, pubcls, tbw, true)) return r;
+  }
   ex->path = KVM_PATH_DYNAMIC;
   ex->uploaded = true;
   HIPCK(hipStreamSynchronize(ex->stream));   // buffer initialisation done
@@ -1407,6 +1471,18 @@ static int stream_launch(KvmExec* ex) {
   HIPCK(hipGetLastError());
   HIPCK(hipEventRecord(ex->ev1, ex->stream));
   ex->launched = true;
+  return 0;
+}
+
+// Stream mode with scheduler classes: every task of a bundle names a class (checked before anything is staged).
+static int stream_class_check(KvmExec* ex, const MvmTaskDesc* tasks, int n) {
+  const int ncls = ex->sched_mode != KVM_SCHED_GLOBAL ? (int)ex->classes.size() : 0;
+  for (int i = 0; ncls && i < n; ++i)
+    if (tasks[i].workload_id < 0 || tasks[i].workload_id >= ncls) {
+      ex->err = "scheduler classes: task " + std::to_string(i) + " of the bundle has workload_id " + std::to_string(tasks[i].workload_id) +
+                ", not a class in [0, " + std::to_string(ncls) + ")";
+      return KVM_STATUS_INVALID;
+    }
   return 0;
 }
 
@@ -1444,11 +1520,12 @@ static long long stream_stage(KvmExec* ex, const MvmTaskDesc* tasks, int n, cons
   int32_t* rt = (int32_t*)(ex->hwin + lay.roots) + base;
   KvmHostWin& m = *((KvmHostWin*)(ex->hwin + lay.meta) + w);
   int nroots = 0, qn[KVM_MAX_QUEUES] = {};
-  const int nq = ex->S.nq;
+  const int nq = ex->S.nq, ncls = ex->S.ncls;
   for (int i = 0; i < n; ++i) {
     MvmTaskDesc d = tasks[i];
     d.succ_off += w * c.window_edges;
     d.reserved0 = base;
+    d.reserved1 = ncls && task_is_bw(tasks[i], args + tasks[i].args_off) ? 1 : 0;   // the staged copy: bandwidth-bound
     td[i] = d;
     make_rec(d, args + tasks[i].args_off, table, recs[i]);
     if (d.indegree == 0) rt[nroots++] = i;
@@ -1498,6 +1575,7 @@ int kvm_submit_stream(KvmExec* ex, const MvmTaskDesc* tasks, int ntasks, const i
   if (!kvm_validate_bundle(tasks, ntasks, succ, nedges, args, nargs, table.data(), (int)table.size(), (int)ex->base_versions.size(), &why)) {
     ex->err = why; return KVM_STATUS_INVALID;
   }
+  if (int r = stream_class_check(ex, tasks, ntasks)) return r;
   for (int i = 0; i < ntasks; ++i)
     for (int k = 0; k < tasks[i].succ_cnt; ++k)
       if (succ[tasks[i].succ_off + k] <= i) {
@@ -1571,6 +1649,7 @@ int kvm_submit(KvmExec* ex, const MvmTaskDesc* tasks, int ntasks, const int32_t*
       ex->err = "stream mode: bundle exceeds a window (" + std::to_string(ntasks) + " tasks, " + std::to_string(nedges) + " edges)";
       return KVM_STATUS_TOO_BIG;
     }
+    if (int r = stream_class_check(ex, tasks, ntasks)) return r;
     if (!ex->hctl) {   // before start: kept, admitted in order at kvm_start
       ex->pending.push_back(KvmExec::Pending{std::vector<MvmTaskDesc>(tasks, tasks + ntasks), std::vector<int32_t>(succ, succ + nedges),
                                               std::vector<int32_t>(args, args + nargs)});
@@ -1742,6 +1821,57 @@ static int plan_static(KvmExec* ex, bool forced) {
   return 0;
 }
 
+// Scheduler classes on the device: the class parameter lines (the reset kernel clears the rest at every launch) and
+// the inheritance and bandwidth state. Launch mode: has_dl / has_bw / pubcls / tbw from the submitted tasks. Stream
+// mode: tbw per slot and pubcls start empty and are filled at admission; every variable is in the publication list.
+static int upload_classes(KvmExec* ex, const std::function<void*(size_t)>& alloc, const unsigned char* has_dl, const unsigned char* has_bw,
+                          const std::vector<int>& pubcls, const std::vector<unsigned char>& tbw, bool stream) {
+  const int ncls = (int)ex->classes.size();
+  KvmSchedDev h{};
+  double tot = 0, acc = 0;
+  for (auto& c : ex->classes) tot += c.share;
+  for (int c = 0; c < ncls; ++c) {
+    const KvmClassParams& p = ex->classes[c];
+    KvmClsDev& k = h.cls[c];
+    k.weight = p.weight; k.min_cta = p.min_cta; k.max_cta = p.max_cta;
+    k.urgent_ticks = (int)std::min<long long>((long long)p.urgent_us * 100ll, 0x7fffffffll);
+    k.vt_mul = (1 << 20) / p.weight; k.has_dl = has_dl[c];
+    k.bw_cta = p.bw_cta; k.has_bw = has_bw[c];
+    k.blk_lo = 0; k.blk_hi = ex->grid;
+    if (ex->sched_mode == KVM_SCHED_STATIC) {   // cumulative bounds, the last class takes the rest
+      k.blk_lo = (int)(acc / tot * ex->grid + 0.5);
+      acc += p.share;
+      k.blk_hi = c + 1 == ncls ? ex->grid : (int)(acc / tot * ex->grid + 0.5);
+      bool used = stream;   // stream mode: the tasks come later, every class needs a worker
+      for (const MvmTaskDesc& d : ex->tasks) if (d.workload_id == c) { used = true; break; }
+      if (used && k.blk_hi <= k.blk_lo) {
+        ex->err = "scheduler classes: class " + std::to_string(c) + " gets no worker of " + std::to_string(ex->grid) + " (shares)";
+        return KVM_STATUS_INVALID;
+      }
+    }
+  }
+  h.flags = ex->sched_mode == KVM_SCHED_DYNAMIC ? ex->sched_flags : 0;
+  h.bw_limit = ex->bw_limit;
+  KvmSchedDev* d = (KvmSchedDev*)alloc(sizeof(KvmSchedDev));
+  if (!d || hipMemcpy(d, &h, sizeof h, hipMemcpyHostToDevice) != hipSuccess) { ex->err = "scheduler classes: device memory"; return KVM_STATUS_HIP_ERROR; }
+  ex->S.sched = d; ex->S.ncls = ncls;
+  // inheritance: parked-waiter counts (cleared by the reset kernel), the publisher classes and the published variables
+  std::vector<int> publist;   // stream mode: every variable (pubcls is or-ed in at admission)
+  for (size_t v = 0; v < pubcls.size(); ++v) if (pubcls[v] || stream) publist.push_back((int)v);
+  const size_t nv = std::max<size_t>(pubcls.size(), 1);
+  int* pv = (int*)alloc(nv * KVM_MAX_CLASSES * sizeof(int));
+  int* pc = (int*)alloc(nv * sizeof(int));
+  int* pl = (int*)alloc(std::max<size_t>(publist.size(), 1) * sizeof(int));
+  unsigned char* tb = (unsigned char*)alloc(std::max<size_t>(tbw.size(), 1));
+  if (!pv || !pc || !pl || !tb || (!pubcls.empty() && hipMemcpy(pc, pubcls.data(), pubcls.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) ||
+      (!publist.empty() && hipMemcpy(pl, publist.data(), publist.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) ||
+      (!tbw.empty() && hipMemcpy(tb, tbw.data(), tbw.size(), hipMemcpyHostToDevice) != hipSuccess)) {
+    ex->err = "scheduler classes: device memory"; return KVM_STATUS_HIP_ERROR;
+  }
+  ex->S.pv = pubcls.empty() ? nullptr : pv; ex->S.pubcls = pc; ex->S.publist = pl; ex->S.npub = (int)publist.size(); ex->S.tbw = tb;
+  return 0;
+}
+
 static int do_upload(KvmExec* ex) {
   if (ex->tasks.empty()) { ex->err = "nothing submitted"; return KVM_STATUS_INVALID; }
   std::vector<MvmBuf> table(ex->bufs.size());
@@ -1784,50 +1914,7 @@ static int do_upload(KvmExec* ex) {
                              ex->cfg.timeout_us, alloc, ex->stream, ex->S, ex->L, ex->err);
   if (rc) return rc == KVM_STATUS_TOO_BIG ? KVM_STATUS_HIP_ERROR : rc;
   ex->path = KVM_PATH_DYNAMIC;
-  if (ncls) {   // class parameter lines; the reset kernel clears the rest at every launch
-    KvmSchedDev h{};
-    double tot = 0, acc = 0;
-    for (auto& c : ex->classes) tot += c.share;
-    for (int c = 0; c < ncls; ++c) {
-      const KvmClassParams& p = ex->classes[c];
-      KvmClsDev& k = h.cls[c];
-      k.weight = p.weight; k.min_cta = p.min_cta; k.max_cta = p.max_cta;
-      k.urgent_ticks = (int)std::min<long long>((long long)p.urgent_us * 100ll, 0x7fffffffll);
-      k.vt_mul = (1 << 20) / p.weight; k.has_dl = has_dl[c];
-      k.bw_cta = p.bw_cta; k.has_bw = has_bw[c];
-      k.blk_lo = 0; k.blk_hi = ex->grid;
-      if (ex->sched_mode == KVM_SCHED_STATIC) {   // cumulative bounds, the last class takes the rest
-        k.blk_lo = (int)(acc / tot * ex->grid + 0.5);
-        acc += p.share;
-        k.blk_hi = c + 1 == ncls ? ex->grid : (int)(acc / tot * ex->grid + 0.5);
-        bool used = false;
-        for (const MvmTaskDesc& d : ex->tasks) if (d.workload_id == c) { used = true; break; }
-        if (used && k.blk_hi <= k.blk_lo) {
-          ex->err = "scheduler classes: class " + std::to_string(c) + " gets no worker of " + std::to_string(ex->grid) + " (shares)";
-          return KVM_STATUS_INVALID;
-        }
-      }
-    }
-    h.flags = ex->sched_mode == KVM_SCHED_DYNAMIC ? ex->sched_flags : 0;
-    h.bw_limit = ex->bw_limit;
-    KvmSchedDev* d = (KvmSchedDev*)alloc(sizeof(KvmSchedDev));
-    if (!d || hipMemcpy(d, &h, sizeof h, hipMemcpyHostToDevice) != hipSuccess) { ex->err = "scheduler classes: device memory"; return KVM_STATUS_HIP_ERROR; }
-    ex->S.sched = d; ex->S.ncls = ncls;
-    // inheritance: parked-waiter counts (cleared by the reset kernel), the publisher classes and the published variables
-    std::vector<int> publist;
-    for (size_t v = 0; v < pubcls.size(); ++v) if (pubcls[v]) publist.push_back((int)v);
-    const size_t nv = std::max<size_t>(pubcls.size(), 1);
-    int* pv = (int*)alloc(nv * KVM_MAX_CLASSES * sizeof(int));
-    int* pc = (int*)alloc(nv * sizeof(int));
-    int* pl = (int*)alloc(std::max<size_t>(publist.size(), 1) * sizeof(int));
-    unsigned char* tb = (unsigned char*)alloc(std::max<size_t>(tbw.size(), 1));
-    if (!pv || !pc || !pl || !tb || (!pubcls.empty() && hipMemcpy(pc, pubcls.data(), pubcls.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) ||
-        (!publist.empty() && hipMemcpy(pl, publist.data(), publist.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) ||
-        (!tbw.empty() && hipMemcpy(tb, tbw.data(), tbw.size(), hipMemcpyHostToDevice) != hipSuccess)) {
-      ex->err = "scheduler classes: device memory"; return KVM_STATUS_HIP_ERROR;
-    }
-    ex->S.pv = pubcls.empty() ? nullptr : pv; ex->S.pubcls = pc; ex->S.publist = pl; ex->S.npub = (int)publist.size(); ex->S.tbw = tb;
-  }
+  if (ncls) { if (int r = upload_classes(ex, alloc, has_dl.data(), has_bw.data(), pubcls, tbw, false)) return r; }
   if (ex->cfg.path != KVM_PATH_DYNAMIC && !ncls) {
     if (int r = plan_static(ex, ex->cfg.path == KVM_PATH_STATIC)) return r;
     if (ex->path == KVM_PATH_STATIC) {   // the plans' arrays next to the dynamic state (a later relaunch may use either)
@@ -2007,7 +2094,6 @@ int kvm_ntasks(const KvmExec* ex) {   // stream mode: the task slots (window w's
 
 int kvm_set_classes(KvmExec* ex, int mode, const KvmClassParams* params, int nclasses) {
   if (ex->uploaded || ex->launched) { ex->err = "kvm_set_classes: before the first kvm_start"; return KVM_STATUS_INVALID; }
-  if (ex->streaming) { ex->err = "kvm_set_classes: stream mode schedules FIFO"; return KVM_STATUS_INVALID; }
   if (mode == KVM_SCHED_GLOBAL) { ex->sched_mode = mode; ex->classes.clear(); return 0; }
   if (mode != KVM_SCHED_STATIC && mode != KVM_SCHED_DYNAMIC) { ex->err = "kvm_set_classes: mode must be KVM_SCHED_GLOBAL, _STATIC or _DYNAMIC"; return KVM_STATUS_INVALID; }
   if (!params || nclasses < 1 || nclasses > KVM_MAX_CLASSES) { ex->err = "kvm_set_classes: 1 to KVM_MAX_CLASSES classes"; return KVM_STATUS_INVALID; }

@@ -3,8 +3,8 @@
 // frontend/mvmfe/demo.py, frontend/mvmfe/run_manifest.py). The runner knows nothing about models: buffers, version
 // variables and the admission order come from the manifest.
 //
-//   kvm_run DEMO_DIR [--out DIR] [--dump REGEX] [--windows N] [--blocks N] [--timeout-s N] [--sched auto|off]
-//                    [--check-only] [--quiet]
+//   kvm_run DEMO_DIR [--out DIR] [--dump REGEX] [--windows N] [--blocks N] [--timeout-s N]
+//                    [--sched off|global|static|dynamic] [--shares a,b,..] [--check-only] [--quiet]
 //
 // The rules this runner applies (the manifest format's, frontend/mvmfe/demo.py:136-152):
 //   * every `buffers` entry is one device allocation, initialised from the bundle of its owner workload and shared by
@@ -16,8 +16,11 @@
 //     live after completion = base + publishes[var] (demo.py:136, mvm_run.cu:262);
 //   * a bundle compiled for other base versions runs shifted (its waits and publications of a published variable
 //     move by the difference) when it reads that variable by no absolute version;
-//   * `classes` configure the device scheduler. Stream mode schedules first-come first-served, so a manifest that
-//     declares classes is refused unless `--sched off` asks for exactly that (the reference runner's own switch).
+//   * scheduler classes: one per class name, the `classes` entries first (their parameters: weight, min_cta, max_cta,
+//     bw_cta, urgent_us), then each workload's `class` (default "default") not declared there; every task of an
+//     admission runs in its workload's class (its workload_id). --sched dynamic (the default) applies them with the
+//     device's class scheduler, static splits the workers by --shares, off and global run first-come first-served
+//     (reference: demo/mvm_run.cu, class_id / apply_class_param and --sched).
 // Before the GPU is touched the runner checks the manifest's shape, checks every bundle against the global tables
 // (including that what it publishes is what its admission declares), and runs the version flow serially (one
 // admission at a time, the first in manifest order whose gate is open; time ignored).
@@ -105,7 +108,7 @@ constexpr long long kMaxVersion = INT_MAX / 2;
 struct Window { int var; long long lo, hi; };           // a `when` entry: lo <= live[var] <= hi
 struct VarVersion { int var; long long v; };
 
-struct WorkloadDecl { std::string name, cls; std::vector<int> vars; };
+struct WorkloadDecl { std::string name, cls; int cls_id = 0; std::vector<int> vars; };
 struct BufferDecl { std::string name, owner; int rows, cols, dtype; };
 struct AdmissionDecl {
   std::string name;
@@ -127,7 +130,14 @@ struct Plan {
   std::vector<WorkloadDecl> workloads;
   std::vector<BufferDecl> buffers;
   std::vector<AdmissionDecl> adms;
-  std::map<std::string, std::map<std::string, long long>> classes;   // declared class -> parameters
+  std::vector<std::string> class_names;                 // class ids: declared classes, then workloads' classes
+  std::vector<std::map<std::string, long long>> class_params;
+  int class_id(const std::string& n) {
+    for (size_t i = 0; i < class_names.size(); ++i) if (class_names[i] == n) return (int)i;
+    class_names.push_back(n);
+    class_params.emplace_back();
+    return (int)class_names.size() - 1;
+  }
 
   static int find(const std::vector<std::string>& names, const std::string& n) {
     auto it = std::find(names.begin(), names.end(), n);
@@ -162,7 +172,7 @@ Plan read_plan(const std::string& root) {
 
   if (const Node cls = top.opt("classes"); cls.given())
     for (auto& [cname, params] : cls.members()) {
-      auto& dst = p.classes[cname];
+      auto& dst = p.class_params[p.class_id(cname)];
       for (auto& [key, val] : params.members()) {
         bool known = false;
         for (const char* k : kClassParams) known = known || key == k;
@@ -181,6 +191,8 @@ Plan read_plan(const std::string& root) {
     w.field("edges").whole(0, INT_MAX);
     w.field("priority").whole(0, 1 << 20);
     d.cls = w.opt("class").given() ? w.opt("class").text() : "default";
+    d.cls_id = p.class_id(d.cls);
+    if (p.class_names.size() > KVM_MAX_CLASSES) refuse(w.path(), "more than " + std::to_string(KVM_MAX_CLASSES) + " scheduler classes");
     if (const Node vs = w.opt("variables"); vs.given())
       for (const Node& v : vs.items()) {
         const std::string vn = v.text();
@@ -497,7 +509,8 @@ void bind_globals(Program& g, const Plan& p, const std::string& who) {
 
 // ================================================================================================ the run
 struct Options {
-  std::string root, out, dump, sched = "auto";
+  std::string root, out, dump, sched = "dynamic";
+  std::vector<int> shares;
   int windows = 4, blocks = 0, timeout_s = 120;
   bool check_only = false, quiet = false;
 };
@@ -519,12 +532,8 @@ class ManifestRun {
   }
 
   int go() {
-    if (!p_.classes.empty() && o_.sched != "off") {
-      std::string names;
-      for (auto& c : p_.classes) names += (names.empty() ? "" : ", ") + c.first;
-      refuse("$.classes", "declares scheduler classes (" + names + "); stream mode schedules first-come first-served, "
-                          "so this runner applies no classes: pass --sched off to run the manifest that way");
-    }
+    if (o_.sched == "static" && o_.shares.size() != p_.class_names.size())
+      refuse("--shares", "--sched static needs one share per class (" + std::to_string(p_.class_names.size()) + " classes)");
     prepare_programs();
     order_ = dry_run(p_);
     if (o_.check_only) {
@@ -635,6 +644,7 @@ class ManifestRun {
         refuse(who, "no bundle: bundle_dir absent or unusable, no usable earlier bundle of its workload, no compile entry" + detail);
       }
       check_publications(g, a, p_);
+      for (MvmTaskDesc& t : g.tasks) t.workload_id = p_.workloads[a.workload].cls_id;   // the scheduler class
       previous[a.workload] = g;
       bind_globals(g, p_, who);
       char err[1024] = {0};
@@ -648,6 +658,8 @@ class ManifestRun {
   // Creates the executor in stream mode (window slots sized to the largest bundle, up to 64K tasks; larger bundles
   // stream through several windows), allocates and initialises every manifest buffer from its owner's first bundle,
   // and starts the kernel.
+  bool classes_on() const { return o_.sched == "dynamic" || o_.sched == "static"; }
+
   void launch() {
     size_t most_tasks = 1, most_edges = 1;
     for (const Program& g : progs_) { most_tasks = std::max(most_tasks, g.tasks.size()); most_edges = std::max(most_edges, g.succ.size()); }
@@ -680,6 +692,17 @@ class ManifestRun {
         refuse("$.buffers." + b.name, "manifest " + std::to_string(b.rows) + "x" + std::to_string(b.cols) + " dtype " + std::to_string(b.dtype) +
                                       ", owner bundle " + std::to_string(rows) + "x" + std::to_string(cols) + " dtype " + std::to_string(dt));
       if (add_buffer_from_meta(ex_.get(), *decl, progs_[ai].dir) != (int)bi) refuse("$.buffers." + b.name, "buffer index out of step");
+    }
+    if (classes_on()) {
+      std::vector<KvmClassParams> cp(p_.class_names.size());
+      for (size_t c = 0; c < cp.size(); ++c) {
+        const auto& m = p_.class_params[c];
+        auto get = [&](const char* k, int d) { auto it = m.find(k); return it == m.end() ? d : (int)it->second; };
+        cp[c] = KvmClassParams{get("weight", 1), get("min_cta", 0), get("max_cta", KVM_UNLIMITED), get("urgent_us", 0),
+                               o_.sched == "static" ? o_.shares[c] : 1, get("bw_cta", KVM_UNLIMITED)};
+      }
+      if (kvm_set_classes(ex_.get(), o_.sched == "static" ? KVM_SCHED_STATIC : KVM_SCHED_DYNAMIC, cp.data(), (int)cp.size()) < 0)
+        refuse("$.classes", std::string("kvm_set_classes: ") + kvm_last_error(ex_.get()));
     }
     if (kvm_start(ex_.get()) < 0) refuse("executor", std::string("kvm_start: ") + kvm_last_error(ex_.get()));
     t0_ = std::chrono::steady_clock::now();
@@ -753,6 +776,8 @@ class ManifestRun {
   void write_summary(const KvmResult& r, bool ok) {
     FILE* f = fopen((o_.out + "/summary.json").c_str(), "w");
     if (!f) { problems_ += "cannot write summary.json\n"; return; }
+    std::vector<KvmClassStats> cs(p_.class_names.size());
+    const int ncs = classes_on() ? kvm_class_stats(ex_.get(), cs.data(), (int)cs.size()) : 0;
     auto versions = [&](const std::vector<int32_t>& v) {
       fprintf(f, "{");
       for (size_t k = 0; k < p_.vars.size() && k < v.size(); ++k) fprintf(f, "%s\"%s\": %d", k ? ", " : "", p_.vars[k].c_str(), v[k]);
@@ -771,6 +796,13 @@ class ManifestRun {
     }
     std::vector<int32_t> fin(std::max<size_t>(1, p_.vars.size()));
     kvm_versions(ex_.get(), fin.data(), (int)fin.size());
+    fprintf(f, "],\n \"sched\": \"%s\", \"classes\": [", o_.sched.c_str());
+    for (size_t c = 0; c < p_.class_names.size(); ++c) {
+      fprintf(f, "%s{\"name\": \"%s\"", c ? ", " : "", p_.class_names[c].c_str());
+      if ((int)c < ncs) fprintf(f, ", \"tasks\": %llu, \"max_running\": %d, \"missed\": %llu", (unsigned long long)cs[c].tasks, cs[c].max_running,
+                                (unsigned long long)cs[c].missed);
+      fprintf(f, "}");
+    }
     fprintf(f, "],\n \"versions\": ");
     versions(fin);
     fprintf(f, "}\n");
@@ -795,10 +827,11 @@ class ManifestRun {
 
 int usage() {
   fprintf(stderr,
-          "usage: kvm_run DEMO_DIR [--out DIR] [--dump REGEX] [--windows N] [--blocks N] [--timeout-s N] [--sched auto|off]\n"
-          "               [--check-only] [--quiet]\n"
+          "usage: kvm_run DEMO_DIR [--out DIR] [--dump REGEX] [--windows N] [--blocks N] [--timeout-s N]\n"
+          "               [--sched off|global|static|dynamic] [--shares a,b,..] [--check-only] [--quiet]\n"
           "  runs every admission of DEMO_DIR/MANIFEST.json on one persistent kernel (stream mode)\n"
-          "  --sched off   run a manifest that declares scheduler classes first-come first-served\n");
+          "  --sched MODE  dynamic (default): one scheduler class per manifest class; static: workers split by --shares\n"
+          "                (one per class); off / global: first-come first-served\n");
   return 2;
 }
 
@@ -818,10 +851,20 @@ int main(int argc, char** argv) {
     else if (a == "--blocks") o.blocks = atoi(argv[++i]);
     else if (a == "--timeout-s") o.timeout_s = atoi(argv[++i]);
     else if (a == "--sched") o.sched = argv[++i];
+    else if (a == "--shares") {
+      std::string v = argv[++i];
+      for (size_t pos = 0; pos <= v.size();) {
+        const size_t e = std::min(v.find(',', pos), v.size());
+        const int x = atoi(v.substr(pos, e - pos).c_str());
+        if (x < 1) return usage();
+        o.shares.push_back(x);
+        pos = e + 1;
+      }
+    }
     else if (a[0] == '-' || !o.root.empty()) return usage();
     else o.root = a;
   }
-  if (o.root.empty() || o.windows < 1 || o.timeout_s < 1 || (o.sched != "auto" && o.sched != "off")) return usage();
+  if (o.root.empty() || o.windows < 1 || o.timeout_s < 1 || (o.sched != "off" && o.sched != "global" && o.sched != "static" && o.sched != "dynamic")) return usage();
   try {
     ManifestRun run(read_plan(o.root), o);
     return run.go();

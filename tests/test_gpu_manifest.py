@@ -32,9 +32,12 @@ def test_train_and_serve_demo_matches_the_serial_replay(tmp_path):
     root = manifest_demo.build(tmp_path / 'demo', steps=3)
     out = tmp_path / 'out'
     print('kvm_run train + serve demo', flush=True)
-    r, s = _kvm_run(root, out, '--dump', '^(W|Y[0-9])$', '--windows', '2', '--sched', 'off')
+    r, s = _kvm_run(root, out, '--dump', '^(W|Y[0-9])$', '--windows', '2')
     assert r.returncode == 0 and r.stdout.startswith('OK: 6/6 tasks'), (r.stdout, r.stderr)
     assert s['ok'] and s['versions'] == {'w': 3}
+    # the manifest's classes (train, serve) scheduled by the device's class scheduler: each task counted in its class
+    assert s['sched'] == 'dynamic' and [c['name'] for c in s['classes']] == ['train', 'serve']
+    assert [c['tasks'] for c in s['classes']] == [3, 3]
     adm = {a['name']: a for a in s['admissions']}
     for k in range(1, 4):
         assert adm[f'serve{k}']['versions_at_done'] == {'w': k}
@@ -65,6 +68,17 @@ def test_training_windows_advance_by_their_publishes(tmp_path):
     ref = replay(root)
     assert ref['order'] == s['serial_order']
     _matches_replay(out, ref, ['W1', 'W2'] + [f'{p}{k}' for p in 'YZ' for k in (0, 2, 4, 6)])
+
+
+def test_static_class_split_runs_the_demo(tmp_path):
+    """The same demo with the workers split 1:3 between the train and serve classes (--sched static): same results."""
+    root = manifest_demo.build(tmp_path / 'demo', steps=3)
+    out = tmp_path / 'out'
+    print('kvm_run train + serve demo, static class split', flush=True)
+    r, s = _kvm_run(root, out, '--dump', '^(W|Y[0-9])$', '--sched', 'static', '--shares', '1,3', '--blocks', '16')
+    assert r.returncode == 0 and r.stdout.startswith('OK: 6/6 tasks'), (r.stdout, r.stderr)
+    assert s['sched'] == 'static' and [c['tasks'] for c in s['classes']] == [3, 3]
+    _matches_replay(out, replay(root), ('W', 'Y1', 'Y2', 'Y3'))
 
 
 def test_admission_compiled_on_demand_runs(tmp_path):

@@ -1,7 +1,8 @@
 """The manifest runner's host side (kvm_run --check-only; reference: demo/mvm_run.cu): well-formed demos pass the
 checks without a GPU, the serial version flow orders train / serve as their versions require with `publishes` read as
 an increment (frontend/mvmfe/demo.py:136), bundles whose publications disagree with their admission are refused,
-manifests with scheduler classes need --sched off, and malformed manifests are refused with the reason."""
+scheduler classes are accepted (a static split needs one share per class), and malformed manifests are refused with
+the reason."""
 import json
 import subprocess
 
@@ -84,10 +85,19 @@ def _edit(root, fn):
     p.write_text(json.dumps(m))
 
 
-def test_classes_need_sched_off(tmp_path):
+def test_classes_and_sched_modes(tmp_path):
+    """Declared classes run under the default dynamic scheduler; --sched static needs one share per class (train,
+    serve), and an unknown mode or a share below 1 is a usage error (exit 2)."""
     root = manifest_demo.build(tmp_path / 'demo')
-    rc, out, err = _run(root, '--check-only')
-    assert rc == 1 and '$.classes' in err and '--sched off' in err, (out, err)
+    for extra in ((), ('--sched', 'off'), ('--sched', 'global'), ('--sched', 'static', '--shares', '1,3')):
+        rc, out, err = _run(root, '--check-only', *extra)
+        assert rc == 0 and out.startswith('OK'), (extra, out, err)
+    rc, out, err = _run(root, '--check-only', '--sched', 'static')
+    assert rc == 1 and '--shares' in err and '2 classes' in err, (out, err)
+    rc, out, err = _run(root, '--check-only', '--sched', 'static', '--shares', '1,2,3')
+    assert rc == 1 and '--shares' in err, (out, err)
+    assert _run(root, '--check-only', '--sched', 'fifo')[0] == 2
+    assert _run(root, '--check-only', '--sched', 'static', '--shares', '1,0')[0] == 2
     rc, out, err = _run(manifest_demo.build(tmp_path / 'plain', classes=False), '--check-only')
     assert rc == 0, (out, err)
 

@@ -201,7 +201,11 @@ typedef struct KvmClassParams {
   int urgent_us;               // EDF window: a ready task whose deadline is this close is served first (0 off)
   int share;                   // KVM_SCHED_STATIC: relative number of workers (>= 1)
   int bw_cta;                  // cap on the class's running bandwidth-bound tasks (KVM_UNLIMITED none)
+  int flags;                   // KVM_CLASS_OPAFF: op affinity (with an affinity window, kvm_set_affinity)
 } KvmClassParams;
+// A task of the class released by a finishing task prefers the worker that last finished a task of its operator
+// (warm code and caches) instead of the releasing worker (reference: MVM_CF_OPAFF, include/mvm_sched.h:34).
+#define KVM_CLASS_OPAFF 2
 int kvm_set_classes(KvmExec* ex, int mode, const KvmClassParams* params, int nclasses);
 // Policy switches of KVM_SCHED_DYNAMIC (reference: MvmSchedParams.flags and MVM_SF_*, include/mvm_sched.h:26-33, default
 // MVM_SF_DEFAULT = reservations + inheritance). KVM_SCHED_F_GUARANTEE: reservations are served first. KVM_SCHED_F_INHERIT:
@@ -216,6 +220,12 @@ int kvm_set_classes(KvmExec* ex, int mode, const KvmClassParams* params, int ncl
 #define KVM_SCHED_F_INHERIT 2
 #define KVM_SCHED_F_ARBITER 4
 int kvm_set_sched_flags(KvmExec* ex, int flags, int bw_limit);
+// Task affinity window of the class scheduler (reference: MvmSchedParams.affinity_us, include/mvm_sched.h:55): a ready
+// task released by a finishing task is offered only to its preferred worker (the releasing one, or with
+// KVM_CLASS_OPAFF the one that last ran its operator) for affinity_us after its release, then to every worker.
+// Roots have no preferred worker. 0 (the default) = off. Set before the first kvm_start; with scheduler classes only. With
+// a window the class queues form one group that every worker polls (no per-XCD queue groups), as in the reference.
+int kvm_set_affinity(KvmExec* ex, int affinity_us);
 // Per-class counters of the last launch (reference: MvmClassTele, include/mvm_sched.h:59-66). Times in
 // wall_clock64 ticks (100 MHz).
 typedef struct KvmClassStats {

@@ -32,14 +32,15 @@ static void usage() {
                   "  --blocks N   --no-trace   --quiet   --check-ops\n"
                   "  --sched global|static|dynamic --classes N   scheduler classes (a task's class is its workload_id); per class, comma\n"
                   "    lists: --weights, --min (reservation), --max (cap), --bw-cta (bandwidth-bound cap), --urgent-us (EDF window),\n"
-                  "    --shares (static split); --arbiter --bw-limit N (global bandwidth-bound cap), --no-guarantee, --no-inherit\n");
+                  "    --shares (static split), --op-affinity (1 = op affinity); --arbiter --bw-limit N (global bandwidth-bound cap),\n"
+                  "    --no-guarantee, --no-inherit, --affinity-us N (task affinity window)\n");
 }
 
 int main(int argc, char** argv) {
   std::vector<std::string> dirs; bool golden = false, quiet = false, trace = true, dump_text = false; float tol = 1e-6f, tol_bf16 = 1e-2f;
   const char* csv = nullptr; std::string dump_dir; std::vector<int> dump_idx; int repeat = 1, blocks = 0, path = KVM_PATH_AUTO; long long timeout_s = 20;
-  int sched = KVM_SCHED_GLOBAL, nclasses = 1, sflags = KVM_SCHED_F_GUARANTEE | KVM_SCHED_F_INHERIT, bw_limit = KVM_UNLIMITED;
-  std::vector<KvmClassParams> cls(KVM_MAX_CLASSES, KvmClassParams{1, 0, KVM_UNLIMITED, 0, 1, KVM_UNLIMITED});
+  int sched = KVM_SCHED_GLOBAL, nclasses = 1, sflags = KVM_SCHED_F_GUARANTEE | KVM_SCHED_F_INHERIT, bw_limit = KVM_UNLIMITED, affinity_us = 0;
+  std::vector<KvmClassParams> cls(KVM_MAX_CLASSES, KvmClassParams{1, 0, KVM_UNLIMITED, 0, 1, KVM_UNLIMITED, 0});
   // a comma list of integers into field f of classes 0, 1, ...
   auto list = [&](const char* v, int KvmClassParams::*f) {
     int c = 0;
@@ -81,6 +82,11 @@ int main(int argc, char** argv) {
     else if (a == "--urgent-us") { if (!list(next(), &KvmClassParams::urgent_us)) { usage(); return 2; } }
     else if (a == "--shares") { if (!list(next(), &KvmClassParams::share)) { usage(); return 2; } }
     else if (a == "--bw-cta") { if (!list(next(), &KvmClassParams::bw_cta)) { usage(); return 2; } }
+    else if (a == "--op-affinity") {
+      if (!list(next(), &KvmClassParams::flags)) { usage(); return 2; }
+      for (auto& c : cls) c.flags = c.flags ? KVM_CLASS_OPAFF : 0;
+    }
+    else if (a == "--affinity-us") affinity_us = atoi(next());
     else if (a == "--arbiter") sflags |= KVM_SCHED_F_ARBITER;
     else if (a == "--bw-limit") bw_limit = atoi(next());
     else if (a == "--no-guarantee") sflags &= ~KVM_SCHED_F_GUARANTEE;
@@ -119,7 +125,7 @@ int main(int argc, char** argv) {
         throw std::runtime_error(dirs[k] + ": submit: " + kvm_last_error(ex.get()));
     }
     if (sched != KVM_SCHED_GLOBAL && (kvm_set_classes(ex.get(), sched, cls.data(), nclasses) < 0 ||
-                                      kvm_set_sched_flags(ex.get(), sflags, bw_limit) < 0))
+                                      kvm_set_sched_flags(ex.get(), sflags, bw_limit) < 0 || kvm_set_affinity(ex.get(), affinity_us) < 0))
       throw std::runtime_error(kvm_last_error(ex.get()));
     KvmResult r{}; float ms = 0;
     if (repeat == 1) { if (kvm_start(ex.get()) < 0) throw std::runtime_error(kvm_last_error(ex.get())); }

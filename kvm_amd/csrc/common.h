@@ -81,7 +81,8 @@ struct KvmAdm {                          // device admission state
 struct alignas(128) KvmClsDev {
   int weight, min_cta, max_cta, urgent_ticks, vt_mul, blk_lo, blk_hi, has_dl;   // vt_mul = 2^20 / weight
   int bw_cta, has_bw;              // cap on running bandwidth-bound tasks; the class has such tasks
-  int pad0[22];
+  int opaff;                       // op affinity: a released task prefers the worker that last ran its operator
+  int pad0[21];
   int running, bw_running;         // running tasks; of those, bandwidth-bound ones
   unsigned long long vtime;        // sum of (ticks run) * vt_mul: the class with the least is served first
   unsigned est;                    // running-time estimate of the class's tasks (moving average, ticks)
@@ -92,13 +93,15 @@ struct alignas(128) KvmClsDev {
 };
 static_assert(sizeof(KvmClsDev) == 384, "class lines");
 // (KVM_SCHED_F_* policy switches: include/kvm_exec.h)
+#define KVM_OP_SLOTS 512          // operator ids below this have an op-affinity slot
 #define KVM_HOW_BW 0x100          // pop_cls / cls_done only: the claimed task counts as bandwidth-bound (never traced)
 struct KvmSchedDev {
   unsigned long long t0;           // launch time: task deadlines count from here
   int flags, bw_limit;             // KVM_SCHED_F_*; the global cap on running bandwidth-bound tasks (ARBITER)
   int boost;                       // classes boosted by inheritance (bit c), recomputed on every park / unpark
   int bw_total;                    // running bandwidth-bound tasks of all classes
-  int pad[26];
+  unsigned long long aff_ticks;    // task affinity window (0 off): a ready task is offered only to its preferred worker
+  int pad[24];
   KvmClsDev cls[KVM_MAX_CLASSES];
 };
 
@@ -158,6 +161,10 @@ struct KvmDevState {
   int* pubcls;               // stream mode: or-ed in at admission (publist then lists every variable)
   const int* publist;
   unsigned char* tbw;        // stream mode: written at admission, per slot
+  // Task affinity (classes on, an affinity window set): aff[t] = (ready time << 12) | (preferred worker + 1), written
+  // before the task's cell is published; op_blk[op] = the worker that last finished a task of operator op (-1 none).
+  unsigned long long* aff;
+  int* op_blk;
   int npub;
   int ntasks, nvars, trace_on, nq, qcap, grid, nb, ncells;
   unsigned long long timeout_ticks;   // stall timeout in wall_clock64 ticks (100 MHz)

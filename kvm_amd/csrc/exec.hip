@@ -75,7 +75,20 @@ __device__ bool take_admission(const KvmDevState& S) {
   return work && ld_relaxed(&S.adm->lock) == 0 &&
          __hip_atomic_compare_exchange_strong(&S.adm->lock, &z, 1, __ATOMIC_ACQUIRE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void enqueue(const KvmDevState& S, int t) {
+// Task affinity (reference: mvm_sched.cuh, the cell's pref and mvm_sched_pref): a task released by a finishing task
+// prefers the releasing worker (chain affinity), or, in a class with op affinity, the worker that last finished a task
+// of its operator; roots prefer none. Recorded with the release time before the task's cell is published.
+__device__ __forceinline__ void note_ready(const KvmDevState& S, int t, bool chain) {
+  int pref = chain ? (int)blockIdx.x : -1;
+  const MvmTaskDesc& d = S.tasks[t];
+  if (chain && S.sched->cls[d.workload_id].opaff && d.op_id >= 0 && d.op_id < KVM_OP_SLOTS) {
+    const int ob = ld_relaxed(&S.op_blk[d.op_id]);
+    if (ob >= 0) pref = ob;
+  }
+  __hip_atomic_store(&S.aff[t], (wall_clock64() << 12) | (unsigned long long)(pref + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void enqueue(const KvmDevState& S, int t, bool chain = true) {
+  if (S.aff) note_ready(S, t, chain);
   if (S.stream) {
     const int q = ring_of(S, t);
     put_cell64(S, q, (unsigned)add_relaxed(&S.queues[q].tail, 1), t, true);
@@ -132,10 +145,11 @@ __device__ void park(const KvmDevState& S, int t, int var, int want) {
 }
 
 // A task whose predecessors have all finished: run it when its version wait holds, else park it.
-__device__ void release(const KvmDevState& S, int t) {
+// chain: released by a finishing task on this worker (false for roots).
+__device__ void release(const KvmDevState& S, int t, bool chain = true) {
   const MvmTaskDesc& d = S.tasks[t];
   int var = d.wait_var;
-  if (var < 0 || ld_acquire(&S.version[var]) >= d.wait_ver) { st_relaxed(&S.state[t], 2); enqueue(S, t); return; }
+  if (var < 0 || ld_acquire(&S.version[var]) >= d.wait_ver) { st_relaxed(&S.state[t], 2); enqueue(S, t, chain); return; }
   st_relaxed(&S.state[t], 1);
   park_count(S, t, var, 1);
   park(S, t, var, d.wait_ver);
@@ -259,7 +273,8 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
   const bool bw_gate = K[c].has_bw != 0 && (bwc < KVM_UNLIMITED || arb);   // the head task's kind matters
   const bool mine = lane_ok && (int)blockIdx.x >= K[c].blk_lo && (int)blockIdx.x < K[c].blk_hi;
   const bool strm = S.stream != 0;
-  const bool need_cell = strm || S.aging_ticks != 0 || (urg > 0 && K[c].has_dl != 0) || bw_gate;
+  const unsigned long long aff_ticks = S.aff ? S.sched->aff_ticks : 0ull;
+  const bool need_cell = strm || S.aging_ticks != 0 || (urg > 0 && K[c].has_dl != 0) || bw_gate || aff_ticks != 0;
   const int qi = (g * nc + c) * nb + b;
   const int cnt = mine && !strm ? S.qcount[qi] : 0, off = mine && !strm ? S.qoff[qi] : 0;
   const unsigned long long boost = (mine && S.aging_ticks) ? (unsigned long long)S.bucket_prio[b] * S.aging_ticks : 0ull;
@@ -276,7 +291,7 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
       avail = false;
       if (mine) {
         const unsigned long long v = __hip_atomic_load(&S.ready64[(size_t)qi * S.qcap + ((unsigned)h & (unsigned)(S.qcap - 1))],
-                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                                       aff_ticks ? __ATOMIC_ACQUIRE : __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if ((unsigned)(v >> 32) == (unsigned)h / (unsigned)S.qcap + 1u) { cell = (int)(unsigned)v; avail = true; }
       }
     } else {
@@ -298,6 +313,11 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
     const int bwt = arb ? __shfl(l == 0 ? ld_relaxed(&S.sched->bw_total) : 0, 0, 64) : 0;
     const bool isbw = bw_gate && cell >= 0 && S.tbw[cell];
     const unsigned long long now = wall_clock64();
+    if (avail && aff_ticks) {   // a head reserved for another worker within the affinity window is not offered here
+      const unsigned long long a = __hip_atomic_load(&S.aff[cell], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int pref = (int)(a & 0xfffull) - 1;
+      if (pref >= 0 && pref != (int)blockIdx.x && now - (a >> 12) < aff_ticks) avail = false;
+    }
     unsigned long long key = ~0ull, score = 0;
     if (avail) {
       if ((boost >> c) & 1) key = (unsigned long long)run;                       // tier 0: inheritance, no caps
@@ -394,6 +414,7 @@ __device__ int pop_cls(const KvmDevState& S, int& how, unsigned& est) {
 __device__ int cls_done(const KvmDevState& S, const MvmTaskDesc& d, int slot, int how, unsigned est, unsigned long long start) {
   KvmClsDev& k = S.sched->cls[d.workload_id];
   const unsigned long long end = wall_clock64(), run = end - start;
+  if (S.op_blk && d.op_id >= 0 && d.op_id < KVM_OP_SLOTS) st_relaxed(&S.op_blk[d.op_id], (int)blockIdx.x);
   add_relaxed(&k.running, -1);
   if (how & KVM_HOW_BW) {
     add_relaxed(&k.bw_running, -1);
@@ -473,7 +494,7 @@ __device__ void admit_windows(const KvmDevState& S) {
     }
     __syncthreads();
     const int32_t* hroot = (const int32_t*)(S.hwin + lay.roots) + base;
-    for (int k = t; k < nr; k += KVM_THREADS) release(S, base + hroot[k]);
+    for (int k = t; k < nr; k += KVM_THREADS) release(S, base + hroot[k], false);
     __syncthreads();
     if (t == 0) st_release(&S.adm->next, seq + 1);
     __syncthreads();
@@ -882,6 +903,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
           if (direct) {
             st_relaxed(&S.state[s], 2);
             if (S.ready_ts) __hip_atomic_store(&S.ready_ts[s], wall_clock64(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (S.aff) note_ready(S, s, true);
           }
           unsigned long long todo = __ballot(direct);
           while (todo) {
@@ -894,7 +916,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
             if (direct && myq == q) {
               const int pos = base_q + __popcll(m & ((1ull << l) - 1ull));
               if (pos >= S.qcount[q]) queue_overflow(S);
-              else if (S.ready_ts) st_release(&S.ready[S.qoff[q] + pos], s);   // release time before the cell
+              else if (S.ready_ts || S.aff) st_release(&S.ready[S.qoff[q] + pos], s);   // release time / affinity before the cell
               else st_relaxed(&S.ready[S.qoff[q] + pos], s);
             }
             todo &= ~m;
@@ -906,7 +928,8 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
           if (direct) {
             const int r = ring_of(S, s);
             st_relaxed(&S.state[s], 2);
-            put_cell64(S, r, (unsigned)add_relaxed(&S.queues[r].tail, 1), s, false);
+            if (S.aff) note_ready(S, s, true);
+            put_cell64(S, r, (unsigned)add_relaxed(&S.queues[r].tail, 1), s, S.aff != nullptr);
           }
           continue;
         }
@@ -965,6 +988,7 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
     k.tasks = k.busy = k.resv_starts = k.urgent_starts = k.missed = k.boost_starts = 0; k.max_running = 0;
   }
   if (S.pv) for (int k = i; k < S.nvars * KVM_MAX_CLASSES; k += stride) S.pv[k] = 0;
+  if (S.op_blk) for (int k = i; k < KVM_OP_SLOTS; k += stride) S.op_blk[k] = -1;
   if (S.ncls && i == 0) { S.sched->t0 = wall_clock64(); S.sched->boost = 0; S.sched->bw_total = 0; }
   if (S.stream) {
     for (long long k = i; k < (long long)S.nq * (S.ncls ? S.ncls : 1) * S.qcap; k += stride) S.ready64[k] = 0ull;
@@ -977,13 +1001,14 @@ __global__ void kvm_seed_kernel(KvmDevState S, const int* roots, const int* root
   for (int r = threadIdx.x; r < nfixed; r += blockDim.x) {
     const int t = roots[r];
     if (S.ready_ts) S.ready_ts[t] = wall_clock64();
+    if (S.aff) S.aff[t] = 0ull;   // no preferred worker
     S.ready[root_cell[r]] = t;
     S.state[t] = 2;
   }
   for (int q = threadIdx.x; q < S.nq * S.nb * (S.ncls ? S.ncls : 1); q += blockDim.x) S.queues[q].tail = fixed_tail[q];
   __syncthreads();
   if (threadIdx.x == 0)
-    for (int r = nfixed; r < nroots; ++r) release(S, roots[r]);
+    for (int r = nfixed; r < nroots; ++r) release(S, roots[r], false);
 }
 
 // ---------------------------------------------------------------------------------------------- init kernels
@@ -1068,6 +1093,7 @@ struct KvmExec {
   int sched_mode = KVM_SCHED_GLOBAL;
   std::vector<KvmClassParams> classes;
   int sched_flags = KVM_SCHED_F_GUARANTEE | KVM_SCHED_F_INHERIT, bw_limit = KVM_UNLIMITED;
+  int affinity_us = 0;
 };
 
 #define HIPCK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { ex->err = std::string(#x) + ": " + hipGetErrorString(e_); return KVM_STATUS_HIP_ERROR; } } while (0)
@@ -1406,7 +1432,10 @@ static int stream_launch(KvmExec* ex) {
   };
   KvmDevState& S = ex->S;
   S = KvmDevState{};
-  const int nq = std::max(1, std::min(KVM_MAX_QUEUES, ex->grid));
+  // one queue group when a task may be reserved for any worker (task affinity) or a class owns only some workers (the
+  // static split): every worker sees every ring
+  const bool one_group = ex->sched_mode == KVM_SCHED_STATIC || (ex->sched_mode != KVM_SCHED_GLOBAL && ex->affinity_us > 0);
+  const int nq = one_group ? 1 : std::max(1, std::min(KVM_MAX_QUEUES, ex->grid));
   int qcap = 1;
   while (qcap < cap) qcap <<= 1;
   S.recs = (const KvmRec*)alloc((size_t)cap * sizeof(KvmRec));
@@ -1836,7 +1865,7 @@ static int upload_classes(KvmExec* ex, const std::function<void*(size_t)>& alloc
     k.weight = p.weight; k.min_cta = p.min_cta; k.max_cta = p.max_cta;
     k.urgent_ticks = (int)std::min<long long>((long long)p.urgent_us * 100ll, 0x7fffffffll);
     k.vt_mul = (1 << 20) / p.weight; k.has_dl = has_dl[c];
-    k.bw_cta = p.bw_cta; k.has_bw = has_bw[c];
+    k.bw_cta = p.bw_cta; k.has_bw = has_bw[c]; k.opaff = (p.flags & KVM_CLASS_OPAFF) ? 1 : 0;
     k.blk_lo = 0; k.blk_hi = ex->grid;
     if (ex->sched_mode == KVM_SCHED_STATIC) {   // cumulative bounds, the last class takes the rest
       k.blk_lo = (int)(acc / tot * ex->grid + 0.5);
@@ -1852,6 +1881,7 @@ static int upload_classes(KvmExec* ex, const std::function<void*(size_t)>& alloc
   }
   h.flags = ex->sched_mode == KVM_SCHED_DYNAMIC ? ex->sched_flags : 0;
   h.bw_limit = ex->bw_limit;
+  h.aff_ticks = (unsigned long long)ex->affinity_us * 100ull;
   KvmSchedDev* d = (KvmSchedDev*)alloc(sizeof(KvmSchedDev));
   if (!d || hipMemcpy(d, &h, sizeof h, hipMemcpyHostToDevice) != hipSuccess) { ex->err = "scheduler classes: device memory"; return KVM_STATUS_HIP_ERROR; }
   ex->S.sched = d; ex->S.ncls = ncls;
@@ -1869,6 +1899,11 @@ static int upload_classes(KvmExec* ex, const std::function<void*(size_t)>& alloc
     ex->err = "scheduler classes: device memory"; return KVM_STATUS_HIP_ERROR;
   }
   ex->S.pv = pubcls.empty() ? nullptr : pv; ex->S.pubcls = pc; ex->S.publist = pl; ex->S.npub = (int)publist.size(); ex->S.tbw = tb;
+  if (ex->affinity_us > 0) {   // per task slot: release time and preferred worker; per operator: the last worker
+    ex->S.aff = (unsigned long long*)alloc(std::max<size_t>(tbw.size(), 1) * sizeof(unsigned long long));
+    ex->S.op_blk = (int*)alloc(KVM_OP_SLOTS * sizeof(int));
+    if (!ex->S.aff || !ex->S.op_blk) { ex->err = "scheduler classes: device memory"; return KVM_STATUS_HIP_ERROR; }
+  }
   return 0;
 }
 
@@ -1902,7 +1937,8 @@ static int do_upload(KvmExec* ex) {
     if (ex->cfg.path == KVM_PATH_STATIC) { ex->err = "scheduler classes run on the dynamic path (path must be DYNAMIC or AUTO)"; return KVM_STATUS_INVALID; }
   }
   GraphPlan g;
-  plan_graph(ex->tasks, ex->succ, ex->args, table, ex->roots, ex->grid, ex->cfg.aging_us, g, ncls, ex->sched_mode == KVM_SCHED_STATIC);
+  plan_graph(ex->tasks, ex->succ, ex->args, table, ex->roots, ex->grid, ex->cfg.aging_us, g, ncls,
+             ex->sched_mode == KVM_SCHED_STATIC || (ncls && ex->affinity_us > 0));   // one group: every worker sees every queue
   auto alloc = [ex](size_t bytes) -> void* {
     void* d = nullptr;
     if (hipMalloc(&d, bytes) != hipSuccess) return nullptr;
@@ -2105,6 +2141,7 @@ int kvm_set_classes(KvmExec* ex, int mode, const KvmClassParams* params, int ncl
     if (p.max_cta < 0) { ex->err = w + "max_cta must be >= 0 (KVM_UNLIMITED for none)"; return KVM_STATUS_INVALID; }
     if (p.bw_cta < 0) { ex->err = w + "bw_cta must be >= 0 (KVM_UNLIMITED for none)"; return KVM_STATUS_INVALID; }
     if (p.urgent_us < 0) { ex->err = w + "urgent_us must be >= 0"; return KVM_STATUS_INVALID; }
+    if (p.flags & ~KVM_CLASS_OPAFF) { ex->err = w + "unknown flags"; return KVM_STATUS_INVALID; }
     if (mode == KVM_SCHED_STATIC && p.share < 1) { ex->err = w + "share must be >= 1"; return KVM_STATUS_INVALID; }
   }
   ex->sched_mode = mode;
@@ -2118,6 +2155,13 @@ int kvm_set_sched_flags(KvmExec* ex, int flags, int bw_limit) {
   if ((flags & KVM_SCHED_F_ARBITER) && bw_limit < 1) { ex->err = "kvm_set_sched_flags: bw_limit must be >= 1"; return KVM_STATUS_INVALID; }
   ex->sched_flags = flags;
   ex->bw_limit = bw_limit;
+  return 0;
+}
+
+int kvm_set_affinity(KvmExec* ex, int affinity_us) {
+  if (ex->uploaded || ex->launched) { ex->err = "kvm_set_affinity: before the first kvm_start"; return KVM_STATUS_INVALID; }
+  if (affinity_us < 0 || affinity_us > 10000000) { ex->err = "kvm_set_affinity: affinity_us must be in [0, 10^7]"; return KVM_STATUS_INVALID; }
+  ex->affinity_us = affinity_us;
   return 0;
 }
 

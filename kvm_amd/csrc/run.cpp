@@ -699,7 +699,7 @@ class ManifestRun {
         const auto& m = p_.class_params[c];
         auto get = [&](const char* k, int d) { auto it = m.find(k); return it == m.end() ? d : (int)it->second; };
         cp[c] = KvmClassParams{get("weight", 1), get("min_cta", 0), get("max_cta", KVM_UNLIMITED), get("urgent_us", 0),
-                               o_.sched == "static" ? o_.shares[c] : 1, get("bw_cta", KVM_UNLIMITED)};
+                               o_.sched == "static" ? o_.shares[c] : 1, get("bw_cta", KVM_UNLIMITED), 0};
       }
       if (kvm_set_classes(ex_.get(), o_.sched == "static" ? KVM_SCHED_STATIC : KVM_SCHED_DYNAMIC, cp.data(), (int)cp.size()) < 0)
         refuse("$.classes", std::string("kvm_set_classes: ") + kvm_last_error(ex_.get()));

@@ -53,13 +53,14 @@ TRACE_DTYPE = np.dtype([('start', '<u8'), ('end', '<u8'), ('block', '<i4'), ('xc
                         ('exec_count', '<i4'), ('how', '<i4')])
 TRACE_MISSED, TRACE_RESV, TRACE_BOOST, TRACE_URGENT = 1, 2, 4, 8
 SCHED_F_GUARANTEE, SCHED_F_INHERIT, SCHED_F_ARBITER = 1, 2, 4
+CLASS_OPAFF = 2                 # KvmClassParams.flags: op affinity (kvm_set_affinity sets the window)
 SCHED_GLOBAL, SCHED_STATIC, SCHED_DYNAMIC = 0, 1, 2
 UNLIMITED = 0x7fffffff
 
 
 class KvmClassParams(ctypes.Structure):
     _fields_ = [('weight', ctypes.c_int), ('min_cta', ctypes.c_int), ('max_cta', ctypes.c_int), ('urgent_us', ctypes.c_int),
-                ('share', ctypes.c_int), ('bw_cta', ctypes.c_int)]
+                ('share', ctypes.c_int), ('bw_cta', ctypes.c_int), ('flags', ctypes.c_int)]
 
 
 CLASS_STATS_DTYPE = np.dtype([('tasks', '<u8'), ('busy_ticks', '<u8'), ('resv_starts', '<u8'), ('urgent_starts', '<u8'),
@@ -92,7 +93,7 @@ def lib():
             'kvm_path': (I, [P]), 'kvm_close': (I, [P]), 'kvm_window_done': (I, [P, ctypes.c_longlong]), 'kvm_live_versions': (I, [P, P, I]),
             'kvm_submit_stream': (I, [P, P, I, P, I, P, I, I, I]),
             'kvm_static_plan': (I, [P, I, P, I, P, I, I, I, P, P, P, P, P, I, P, ctypes.c_char_p, I]),
-            'kvm_set_classes': (I, [P, I, P, I]), 'kvm_class_stats': (I, [P, P, I]), 'kvm_set_sched_flags': (I, [P, I, I]),
+            'kvm_set_classes': (I, [P, I, P, I]), 'kvm_class_stats': (I, [P, P, I]), 'kvm_set_sched_flags': (I, [P, I, I]), 'kvm_set_affinity': (I, [P, I]),
             'kvm_run_noalloc': (I, [P, I, P, I, P, I, P, I, P, I, I, ctypes.c_ulonglong, P, P, ctypes.c_char_p, I]),
         }
         for name, (res, args) in sig.items():
@@ -256,18 +257,23 @@ class Executor:
 
     def set_classes(self, mode: int, classes: list):
         """Scheduler classes (include/kvm_exec.h, kvm_set_classes): classes[c] is a dict with weight, min_cta, max_cta,
-        urgent_us, share, bw_cta (defaults 1, 0, UNLIMITED, 0, 1, UNLIMITED); a task's class is its workload_id. Before
-        the first start."""
+        urgent_us, share, bw_cta, opaff (defaults 1, 0, UNLIMITED, 0, 1, UNLIMITED, False); a task's class is its
+        workload_id. Before the first start."""
         arr = (KvmClassParams * max(1, len(classes)))()
         for c, d in enumerate(classes):
             arr[c] = KvmClassParams(d.get('weight', 1), d.get('min_cta', 0), d.get('max_cta', UNLIMITED), d.get('urgent_us', 0), d.get('share', 1),
-                                    d.get('bw_cta', UNLIMITED))
+                                    d.get('bw_cta', UNLIMITED), CLASS_OPAFF if d.get('opaff') else 0)
         self._check(lib().kvm_set_classes(self._h, mode, arr, len(classes)), 'set_classes')
 
     def set_sched_flags(self, flags: int, bw_limit: int = UNLIMITED):
         """Policy switches of the dynamic class scheduler (SCHED_F_*; default GUARANTEE | INHERIT) and the global cap on
         running bandwidth-bound tasks (ARBITER). Before the first start."""
         self._check(lib().kvm_set_sched_flags(self._h, flags, bw_limit), 'set_sched_flags')
+
+    def set_affinity(self, affinity_us: int):
+        """Task affinity window of the class scheduler (kvm_set_affinity): a released task is offered only to its
+        preferred worker for affinity_us. Before the first start."""
+        self._check(lib().kvm_set_affinity(self._h, affinity_us), 'set_affinity')
 
     def class_stats(self, n: int) -> np.ndarray:
         """Per-class counters of the last launch (CLASS_STATS_DTYPE; busy_ticks at 100 MHz)."""

@@ -318,3 +318,71 @@ def test_arbiter_bounds_bandwidth_bound_tasks_of_all_classes():
     print('arbiter peak running fills', peak, flush=True)
     assert 1 <= peak <= 3
     ex.close()
+
+
+def chain_spec(chains, length, us):
+    """`chains` independent chains of `length` dependent spin tasks, one class."""
+    ts = []
+    for c in range(chains):
+        for k in range(length):
+            t = {'id': f'c{c}k{k}', 'op': 'spin', 'args': {'us': us}}
+            if k:
+                t['after'] = [f'c{c}k{k - 1}']
+            ts.append(t)
+    return {'buffers': [{'name': 'x', 'rows': 4}], 'graphs': [{'name': 'g', 'tasks': ts}]}
+
+
+def test_task_affinity_keeps_a_chain_on_its_worker():
+    """Affinity window 1 s (reference: MvmSchedParams.affinity_us): each task released by its predecessor is offered
+    only to the worker that ran the predecessor, so every chain runs on one worker (its root's)."""
+    spec = chain_spec(8, 10, 10)
+    for aff in (1_000_000, 0):
+        b = bl.load(compiler.compile_spec(spec))
+        ex = Executor.from_bundle(b)
+        ex.set_classes(SCHED_DYNAMIC, [{}])
+        ex.set_affinity(aff)
+        ex.run()
+        tr = check_schedule(ex, b)
+        blocks = [len(np.unique(tr['block'][c * 10:(c + 1) * 10])) for c in range(8)]
+        print('affinity', aff, 'workers per chain', blocks, flush=True)
+        if aff:
+            assert blocks == [1] * 8
+        ex.close()
+
+
+def test_op_affinity_prefers_the_worker_that_last_ran_the_operator():
+    """Task C (spin) waits for A (a 1 us spin) and B (a 64 MiB fill, which ends later and releases C). With op affinity
+    C runs on A's worker, the last to finish a spin; with chain affinity only, on B's worker, which released it."""
+    ts = [{'id': 'a', 'op': 'spin', 'args': {'us': 1}},
+          {'id': 'b', 'op': 'fill', 'args': {'x': 'y', 'value': 1.0, 'n': 1 << 24}},
+          {'id': 'c', 'op': 'spin', 'args': {'us': 1}, 'after': ['a', 'b']}]
+    spec = {'buffers': [{'name': 'x', 'rows': 4}, {'name': 'y', 'rows': 1 << 24}], 'graphs': [{'name': 'g', 'tasks': ts}]}
+    for opaff in (True, False):
+        b = bl.load(compiler.compile_spec(spec))
+        ex = Executor.from_bundle(b)
+        ex.set_classes(SCHED_DYNAMIC, [{'opaff': opaff}])
+        ex.set_affinity(1_000_000)
+        ex.run()
+        tr = check_schedule(ex, b)
+        print('op affinity', opaff, 'blocks a b c', tr['block'][:3].tolist(), 'ends', tr['end'][:2].tolist(), flush=True)
+        assert tr['end'][0] < tr['end'][1] and tr['block'][0] != tr['block'][1]
+        assert tr['block'][2] == tr['block'][0 if opaff else 1]
+        ex.close()
+
+
+def test_affinity_errors():
+    """A negative window and class flags other than op affinity are refused; a short window runs normally."""
+    import ctypes
+    from kvm_amd.executor import KvmClassParams, lib
+    b = bl.load(compiler.compile_spec(spin_spec([[(1, None)]])))
+    ex = Executor.from_bundle(b)
+    with pytest.raises(KvmError, match='affinity_us'):
+        ex.set_affinity(-1)
+    p = (KvmClassParams * 1)()
+    p[0] = KvmClassParams(1, 0, UNLIMITED, 0, 1, UNLIMITED, 1)
+    with pytest.raises(KvmError, match='unknown flags'):
+        ex._check(lib().kvm_set_classes(ex._h, SCHED_DYNAMIC, ctypes.byref(p), 1), 'set_classes')
+    ex.set_classes(SCHED_DYNAMIC, [{'opaff': True}])
+    ex.set_affinity(50)
+    ex.run()
+    ex.close()

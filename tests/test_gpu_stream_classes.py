@@ -150,9 +150,10 @@ def test_stream_deadlines_count_from_admission():
 
 
 def test_stream_static_split_keeps_classes_on_their_workers():
-    """STATIC split 1:3 of 32 workers in stream mode: class 0 runs only on workers 0-7, class 1 only on 8-31."""
+    """STATIC split 1:7 of 32 workers in stream mode: class 0 runs only on workers 0-3 (fewer than the queue groups of
+    the shared mode, so its rings must be visible to those four), class 1 only on 4-31."""
     bundles = [spin_bundle(64, 5, k % 2) for k in range(6)]
-    ex = stream_executor(bundles[0], [{'share': 1}, {'share': 3}], mode=SCHED_STATIC, window_cap=6, window_tasks=64, window_edges=4,
+    ex = stream_executor(bundles[0], [{'share': 1}, {'share': 7}], mode=SCHED_STATIC, window_cap=6, window_tasks=64, window_edges=4,
                          timeout_s=10.0, blocks=32)
     print('stream classes: static split', flush=True)
     ex.start()
@@ -161,7 +162,7 @@ def test_stream_static_split_keeps_classes_on_their_workers():
     assert res['err_code'] == 0 and res['done'] == 6 * 64
     tr = ex.trace()[slots_of(wids, 64, 64)]
     cls = np.repeat([k % 2 for k in range(6)], 64)
-    assert tr['block'][cls == 0].max() < 8 and tr['block'][cls == 1].min() >= 8
+    assert tr['block'][cls == 0].max() < 4 and tr['block'][cls == 1].min() >= 4
     assert len(np.unique(tr['block'][cls == 1])) > 8
     ex.close()
 
@@ -200,4 +201,22 @@ def test_stream_classes_results_match_the_oracle():
     assert st['tasks'].sum() == b.ntasks and st['max_running'][0] <= 8
     skip = tuple(m['name'] for m in b.metadata['buffers'] if m['name'].startswith(('bk.', 'd.bk.', 'm.bk.', 'v.bk.')))
     assert not compare_run(ex, b.metadata, ref, tol_f32=2e-4, skip=skip)
+    ex.close()
+
+
+def test_stream_task_affinity_keeps_a_chain_on_its_worker():
+    """Affinity window 1 s in stream mode: each admitted chain of 8 dependent spin tasks runs on one worker."""
+    ts = [{'id': f'k{k}', 'op': 'spin', 'args': {'us': 10}, **({'after': [f'k{k - 1}']} if k else {})} for k in range(8)]
+    b = bl.load(compiler.compile_spec({'buffers': [{'name': 'x', 'rows': 4}], 'graphs': [{'name': 'g', 'tasks': ts}]}))
+    ex = stream_executor(b, [{}], window_cap=4, window_tasks=8, window_edges=8, timeout_s=10.0)
+    ex.set_affinity(1_000_000)
+    print('stream classes: task affinity', flush=True)
+    ex.start()
+    wids = [ex.submit(b) for _ in range(4)]
+    res = ex.finish()
+    assert res['err_code'] == 0 and res['done'] == 32
+    tr = ex.trace()
+    blocks = [len(np.unique(tr['block'][w * 8:(w + 1) * 8])) for w in wids]
+    print('workers per chain', blocks, flush=True)
+    assert blocks == [1] * 4
     ex.close()

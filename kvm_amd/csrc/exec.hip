@@ -739,7 +739,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
       // (the fused SwiGLU GEMV, op 311, runs through the dispatcher: inlined beside the others it made the kernel spill)
       const bool rows = op == 301, gv = (op == 134 || rows) && c.pre;
       const int gm = rows ? c.i(9) : 1, gpro = rows ? c.i(10) : c.i(9);
-      if ((op == 306 || op == 310) && c.i(11) == 4 * c.i(12)) attn_part_body<4>(c, true, op == 310);
+      if ((op == 306 || op == 310) && c.i(11) == 4 * c.i(12)) attn_part_body<4, V == 2>(c, true, op == 310);
       else if (gv && gv_pre_ring(gm) == GR && gemv_stream_ok(c.buf(0), c.buf(1), c.buf(3), c.buf(4), c.i(8), gm, gpro))
         gemv_body<GR>(c, gm, gpro, rows ? c.f(11) : c.f(10));
       else dispatch(op, c);

@@ -469,6 +469,25 @@ __device__ __forceinline__ bool attn_fast_ok(const Ctx& c, int op) {
   const int H = c.i(11), Hkv = c.i(12), G = Hkv > 0 ? H / Hkv : 0;
   return kc.dtype == 2 && vc.dtype == 2 && c.i(13) == 128 && (kc.cols % 8) == 0 && (vc.cols % 8) == 0 && (G == 1 || G == 2 || G == 4 || G == 8);
 }
+// A long split on the MFMA units (the batched decode graph's splits hold ~1,000 tokens; a one-row split's ~130 stay on
+// the VALU form below, whose block pipeline suits it). Each wave streams its own contiguous quarter of the split in
+// chunks of 16 tokens, K and V rows direct from HBM into a per-wave 3-stage LDS ring (16-byte units XOR-swizzled by
+// token), with its own flash-softmax state; the four waves' states are combined at the end.
+//   scores: v_mfma_f32_16x16x32_bf16, A = 16 K rows (tokens x hd), B = the query block (hd x 16 rows): rows 0..G-1 are
+//   the bf16 rounding of the query heads, rows G..2G-1 the bf16 rounding of the remainder, so score = D[row g] +
+//   D[row g + G] is the product with the f32 query to ~2^-16 (K is bf16 already: every product is exact in f32).
+//   P V: v_mfma_f32_16x16x16_bf16, A = P (16 rows x 16 tokens, again hi rows and remainder rows; the scores' output
+//   registers are already the A operand's layout: lane = row, 4 registers = 4 consecutive tokens), B = V rows read
+//   transposed (ds_read_b64_tr_b16), 8 blocks of 16 head dims.
+// The partial (unnormalised P V, max, sum) has op 135's format and meaning; the query block comes in LDS at ATT_MQ_OFF
+// ([G][128] f32, rotated, normalised and scaled).
+#ifndef ATT_MNS_V
+#define ATT_MNS_V 3
+#endif
+constexpr int ATT_MCH = 16, ATT_MNS = ATT_MNS_V, ATT_MSB = ATT_MCH * ATT_HD * 2;   // tokens per chunk, ring stages, bytes per operand per stage
+constexpr int ATT_MQ_OFF = KVM_LDS_BYTES - 8 * ATT_HD * 4;                // query block [8][128] f32 at the end of the LDS
+constexpr int ATT_MFMA_MIN = 256;                                          // splits longer than this take the MFMA form
+static_assert(KVM_WAVES * ATT_MNS * 2 * ATT_MSB <= ATT_MQ_OFF && KVM_WAVES * (16 * ATT_HD + 16) * 4 <= ATT_MQ_OFF, "decode MFMA LDS map");
 // Before the dependency wait of a streaming split that will run with c.pre set (all four waves, the task's record in
 // c): its first block's K and V rows go to the staging direct from HBM (loads in flight through the wait) and the
 // rotation table is computed. The cache rows read here are written only by earlier launches, except the split's own
@@ -555,7 +574,138 @@ template <int G> __device__ __forceinline__ void attn_arrive(const Ctx& c, int b
   attn_merge_g<G>(part, o, bb, kvh * G, S, H);
   if (tid() == 0) st_relaxed((int*)(cnt.i() + ((long long)bb * Hkv + kvh)), 0);
 }
-template <int G>
+template <int G> __device__ __noinline__ void attn_split_mfma(const Ctx& c, int j0, int nk) {
+  static_assert(2 * G <= 16, "query rows");
+  constexpr int hd = ATT_HD, CH = ATT_MCH, NS = ATT_MNS, SB = ATT_MSB;
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const View kc = uniform_view(c.buf(1)), vc = uniform_view(c.buf(2)), part = uniform_view(c.buf(4));
+  const int bb = c.i(7), kvh = c.i(8), s = c.i(9), S = c.i(10), H = c.i(11), Hkv = c.i(12), Tmax = c.i(14);
+  const long long row0 = ((long long)bb * Hkv + kvh) * Tmax + j0;
+  const i32x4_t rk = dma_rsrc((const void*)(kc.h() + row0 * kc.cols), (long long)nk * kc.cols * 2);
+  const i32x4_t rv = dma_rsrc((const void*)(vc.h() + row0 * vc.cols), (long long)nk * vc.cols * 2);
+  const int l = lane(), w = wave(), n = l & 15, qq = l >> 4;
+  // the query block as the B operand: lane (n, qq) holds row n, head dims 32 kk + 8 qq .. + 7
+  const LDS float* qs = (const LDS float*)(c.smem + ATT_MQ_OFF);
+  bf16x8 qb[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = n < 2 * G ? qs[(n % G) * hd + 32 * kk + 8 * qq + e] : 0.f;
+      const __bf16 hi = (__bf16)x;
+      qb[kk][e] = n < G ? hi : (__bf16)(x - (float)hi);
+    }
+  __syncthreads();                                         // every wave has its query block: the rings may overwrite it
+  LDS char* ring = c.smem + w * NS * 2 * SB;
+  const int nch = (nk + CH - 1) / CH, per = (nch + KVM_WAVES - 1) / KVM_WAVES, c0 = min(nch, w * per), c1 = min(nch, c0 + per);
+  // chunk ch into stage slot: 4 loads of K and 4 of V per lane; lane (n, qq) of load i fills token 4 i + qq, unit
+  // position n with the row's 16-byte unit n ^ token
+  auto issue = [&](int ch, int slot) {
+    LDS char* st = ring + slot * 2 * SB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 4 * i + qq, tok = min(ch * CH + t, nk - 1), u = n ^ t;
+      dma16(rk, (tok * kc.cols + 8 * u) * 2, 0, st + i * 1024);
+      dma16(rv, (tok * vc.cols + 8 * u) * 2, 0, st + SB + i * 1024);
+    }
+  };
+  f32x4n o[8];
+#pragma unroll
+  for (int hb = 0; hb < 8; ++hb) o[hb] = f32x4n{0.f, 0.f, 0.f, 0.f};
+  float mrun = -INFINITY, lrun = 0.f;
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p) if (c0 + p < c1) issue(c0 + p, p);
+  for (int ch = c0; ch < c1; ++ch) {
+    const int k = ch - c0;
+    if (ch + NS - 1 < c1) { wait_lds(); issue(ch + NS - 1, (k + NS - 1) % NS); }
+    wait_vm(8 * min(NS - 1, c1 - 1 - ch));               // this chunk's loads have landed
+    const LDS char* Ks = ring + (k % NS) * 2 * SB;
+    const LDS char* Vs = Ks + SB;
+    f32x4n d = f32x4n{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const bf16x8 a = *(const LDS bf16x8*)(Ks + n * 256 + (((4 * kk + qq) ^ n) * 16));
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[kk], d, 0, 0, 0);
+    }
+    // lane (n, qq), register i: row n, token 16 ch + 4 qq + i
+    float sc4[4], bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = d[i] + __shfl_xor(d[i], G, 64);
+      sc4[i] = (n < 2 * G && ch * CH + 4 * qq + i < nk) ? x : -INFINITY;
+      bm = fmaxf(bm, sc4[i]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mn = fmaxf(mrun, bm);
+    const float f = mn == -INFINITY ? 1.f : __expf(mrun - mn);
+    float ps = 0.f;
+    s16x4 pa;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = sc4[i] == -INFINITY ? 0.f : __expf(sc4[i] - mn);
+      ps += p;
+      const __bf16 hi = (__bf16)p, v = n < G ? hi : (__bf16)(p - (float)hi);
+      pa[i] = __builtin_bit_cast(short, v);
+    }
+    lrun = lrun * f + ps;
+    mrun = mn;
+    if (__ballot(f != 1.f)) {                             // rescale: output register i of lane group qq is row 4 qq + i
+      float fh[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) fh[g] = __shfl(f, g, 64);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * qq + i;
+        float fr = 1.f;
+#pragma unroll
+        for (int g = 0; g < G; ++g) if (r % G == g && r < 2 * G) fr = fh[g];
+#pragma unroll
+        for (int hb = 0; hb < 8; ++hb) o[hb][i] *= fr;
+      }
+    }
+    const int t = 4 * qq + (n >> 2);                       // transposed read: token row of this lane's 8 bytes
+#pragma unroll
+    for (int hb = 0; hb < 8; ++hb) {
+      const int dd = hb * 16 + 4 * (n & 3);
+      const LDS char* pv = Vs + t * 256 + (((dd >> 3) ^ t) * 16) + (dd & 7) * 2;
+      const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS s16x4*)pv);
+      o[hb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, b, o[hb], 0, 0, 0);
+    }
+  }
+  // per wave: rows of P V (16 x 128), and the max and sum of each head
+  float lsum = lrun + __shfl_xor(lrun, 16, 64);           // over the four lane groups (their tokens)
+  lsum += __shfl_xor(lsum, 32, 64);
+  wait_vm_c<0>();
+  __syncthreads();                                         // every wave is past its ring: the state goes over it
+  LDS float* ow = (LDS float*)c.smem + w * (16 * hd + 16);
+#pragma unroll
+  for (int hb = 0; hb < 8; ++hb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ow[(4 * qq + i) * hd + hb * 16 + n] = o[hb][i];
+  if (qq == 0 && n < G) { ow[16 * hd + n] = mrun; ow[16 * hd + 8 + n] = lsum; }
+  __syncthreads();
+  for (int e = tid(); e < G * hd; e += KVM_THREADS) {
+    const int g = e / hd, dd = e % hd;
+    float M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < KVM_WAVES; ++v) M = fmaxf(M, ((const LDS float*)c.smem)[v * (16 * hd + 16) + 16 * hd + g]);
+    float acc = 0.f, ls = 0.f;
+#pragma unroll
+    for (int v = 0; v < KVM_WAVES; ++v) {
+      const LDS float* x = (const LDS float*)c.smem + v * (16 * hd + 16);
+      const float mv = x[16 * hd + g], ew = mv == -INFINITY ? 0.f : __expf(mv - M);
+      acc += ew * (x[g * hd + dd] + x[(g + G) * hd + dd]);
+      ls += ew * x[16 * hd + 8 + g];
+    }
+    const long long r = (((long long)bb * S + s) * H + kvh * G + g) * part.cols;
+    stwt32(part.f() + (r + dd), acc);
+    if (dd == 0) { stwt32(part.f() + (r + hd), M); stwt32(part.f() + (r + hd + 1), ls); }
+  }
+}
+// LONG: long splits may take the MFMA form (a call site the batch-1 static kernel is built without: its register
+// allocation spills with it).
+template <int G, bool LONG = true>
 __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn, bool merge = false) {
   const View q = uniform_view(c.buf(0)), kc = uniform_view(c.buf(1)), vc = uniform_view(c.buf(2)), lens = uniform_view(c.buf(3));
   const View part = uniform_view(c.buf(4)), kn = uniform_view(c.buf(5)), vn = uniform_view(c.buf(6));
@@ -568,6 +718,7 @@ __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn, bool merg
   if (!attn_split(c, L, j0, nk)) { if (tid() == 0) c.fail(KVM_ERR_OP_KVLEN, bb, lens.i()[bb]); return; }
   const int n = L + 1, j1 = j0 + nk;
   const bool pre = rfl(c.pre) && nk > 0;                // block 0 and the rotation table staged before the wait
+  const bool mf = LONG && nk > ATT_MFMA_MIN;            // a long split: the MFMA form (its staged block 0 unused)
   const long long base = ((long long)bb * Hkv + kvh) * Tmax;
   const int l = lane(), w = wave(), cb = l & 15, ts = l >> 4, d0 = 8 * cb;
   LDS uint16_t* Ks = (LDS uint16_t*)c.smem;             // [DB][hd] block 0 K rows (prefetched), then V rows
@@ -684,6 +835,18 @@ __device__ __forceinline__ void attn_part_body(const Ctx& c, bool qkn, bool merg
       const long long r = (((long long)bb * S + s) * H + kvh * G + g) * part.cols;
       stwt32(part.f() + (r + k), k < hd ? 0.f : (k == hd ? ATTN_EMPTY_M : 0.f));
     }
+    if (merge) attn_arrive<G>(c, bb, kvh, S, H, Hkv);
+    return;
+  }
+  if (mf) {                                             // the MFMA form, the query block through LDS
+    if (w == 0 && ts == 0)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ((LDS float*)(c.smem + ATT_MQ_OFF))[g * hd + d0 + e] = qr[g][e];
+    wait_stores();                                      // the new row is in L2 before the direct loads
+    __syncthreads();
+    attn_split_mfma<G>(c, j0, nk);
     if (merge) attn_arrive<G>(c, bb, kvh, S, H, Hkv);
     return;
   }

@@ -60,16 +60,20 @@ def test_gemv_rows(M, pro, K):
     _run(b)
 
 
-@pytest.mark.parametrize('G,fl,S', [(4, 3, 3), (4, 1, 16), (4, 0, 40), (8, 3, 5), (2, 1, 7), (1, 0, 9)])
-def test_attn_decode_parts(G, fl, S):
+LONG = [1500, 700]      # splits of 751 / 351 tokens at S = 2, 501 / 234 at S = 3: the MFMA form (over 256 tokens)
+
+
+@pytest.mark.parametrize('G,fl,S,lens', [(4, 3, 3, None), (4, 1, 16, None), (4, 0, 40, None), (8, 3, 5, None), (2, 1, 7, None),
+                                         (1, 0, 9, None), (4, 3, 2, LONG), (8, 1, 2, LONG), (2, 0, 3, LONG), (1, 3, 2, LONG)])
+def test_attn_decode_parts(G, fl, S, lens):
     """Split-context decode attention (op 135) and the merge (op 136) at hd = 128 (the streaming form): two sequences
     of different lengths, splits longer than one 128-token block (S = 3), short ones and empty ones (S = 40 with a
     30-token context), with RoPE + cache append + bf16 rounding of the rotated query (flags 3), RoPE + append (1) or
-    neither (0)."""
-    print(f'attn_decode_part G {G} flags {fl} S {S}', flush=True)
+    neither (0); splits over 256 tokens (LONG) take the MFMA form, with a partial last chunk."""
+    print(f'attn_decode_part G {G} flags {fl} S {S} lens {lens}', flush=True)
     B, Hkv, hd = 2, 2, 128
     H = G * Hkv
-    lens = [700, 30] if S == 40 else [700, 301]
+    lens = lens or ([700, 30] if S == 40 else [700, 301])
     Tmax = max(lens) + 1
     b = Builder(31)
     b.normal('q', B, H * hd, 'bf16', scale=1.0)
@@ -88,15 +92,16 @@ def test_attn_decode_parts(G, fl, S):
     _run(b, tol=1e-4)
 
 
-@pytest.mark.parametrize('G,fl,S,qdt', [(4, 1, 32, 'f32'), (4, 3, 3, 'f32'), (8, 1, 5, 'bf16'), (1, 3, 9, 'f32')])
-def test_attn_decode_parts_qkn(G, fl, S, qdt):
+@pytest.mark.parametrize('G,fl,S,qdt,lens', [(4, 1, 32, 'f32', None), (4, 3, 3, 'f32', None), (8, 1, 5, 'bf16', None), (1, 3, 9, 'f32', None),
+                                              (4, 1, 2, 'f32', LONG), (8, 3, 2, 'bf16', LONG)])
+def test_attn_decode_parts_qkn(G, fl, S, qdt, lens):
     """Op 306: per-head RMSNorm of the query heads and of the new key inside the split-context attention task (the
     Qwen3 q/k norm), against the oracle's op 300 + op 135 composition. eps 0.25 (comparable to the mean square of
     the unit-scale inputs) so that a misread eps fails."""
-    print(f'attn_decode_part_qkn G {G} flags {fl} S {S} q {qdt}', flush=True)
+    print(f'attn_decode_part_qkn G {G} flags {fl} S {S} q {qdt} lens {lens}', flush=True)
     B, Hkv, hd = 2, 2, 128
     H = G * Hkv
-    lens = [700, 301]
+    lens = lens or [700, 301]
     Tmax = max(lens) + 1
     b = Builder(37)
     b.normal('q', B, H * hd, qdt, scale=1.0)
@@ -117,15 +122,16 @@ def test_attn_decode_parts_qkn(G, fl, S, qdt):
     _run(b, tol=1e-4)
 
 
-@pytest.mark.parametrize('G,S,path', [(4, 32, 0), (4, 32, 1), (8, 5, 0), (2, 3, 1)])
-def test_attn_decode_part_merge(G, S, path):
+@pytest.mark.parametrize('G,S,path,lens', [(4, 32, 0, None), (4, 32, 1, None), (8, 5, 0, None), (2, 3, 1, None), (4, 2, 0, LONG),
+                                           (4, 2, 1, LONG)])
+def test_attn_decode_part_merge(G, S, path, lens):
     """Op 310 (op 306 whose last split per kv head merges that head's query heads) against the oracle's op 306 + op
     136 composition, on the dynamic and the static path (where the GQA-4 body is inlined and its first block staged
     before the wait); two launches in a row, so the split counts must have returned to 0."""
-    print(f'attn_decode_part_merge G {G} S {S} path {path}', flush=True)
+    print(f'attn_decode_part_merge G {G} S {S} path {path} lens {lens}', flush=True)
     B, Hkv, hd = 2, 2, 128
     H = G * Hkv
-    lens = [700, 301]
+    lens = lens or [700, 301]
     Tmax = max(lens) + 1
     b = Builder(53)
     b.normal('q', B, H * hd, 'f32', scale=1.0)

@@ -171,6 +171,38 @@ def gemm_task_flops(lb, executed_out=None):
     return fl
 
 
+def critical_path(lb, tr):
+    """From a traced launch: the graph's critical path with the measured task durations and no hop latency (the
+    longest chain of dependent task times: a lower bound on the launch for these task times), and the chain the launch
+    actually ran (from the last task to finish, each step to the predecessor that finished last): its task count, the
+    time its tasks ran and the time they waited (dependency release, queueing, dispatch). Times in us."""
+    import numpy as np
+    st, en = tr['start'].astype(np.int64), tr['end'].astype(np.int64)
+    t0 = int(st.min())
+    dur = (en - st) / 100.0
+    n = lb.ntasks
+    off, cnt = lb.tasks[:, 1], lb.tasks[:, 2]
+    ef = np.zeros(n)
+    rel = np.zeros(n)
+    last = np.full(n, -1)
+    for i in np.argsort(st, kind='stable'):          # start order is a topological order of the executed graph
+        ef[i] += dur[i]
+        e = (en[i] - t0) / 100.0
+        for j in lb.succ[off[i]:off[i] + cnt[i]]:
+            if ef[i] > ef[j]:
+                ef[j] = ef[i]
+            if e > rel[j]:
+                rel[j], last[j] = e, i
+    chain, i = [], int(np.argmax(en))
+    while i >= 0:
+        chain.append(i)
+        i = int(last[i])
+    run = float(dur[chain].sum())
+    span = (int(en.max()) - t0) / 100.0
+    return {'span_us': round(span, 1), 'critical_path_us': round(float(ef.max()), 1), 'chain_tasks': len(chain),
+            'chain_running_us': round(run, 1), 'chain_waiting_us': round(span - run, 1)}
+
+
 def bench_gpt(steps, warmup, cpu):
     import numpy as np
     from kvm_amd.workloads import gpt
@@ -197,13 +229,14 @@ def bench_gpt(steps, warmup, cpu):
     in_task = {'gemm': float(fl[gm].sum() / dur[gm].sum() / per_cu), 'attention': float(fl[at].sum() / dur[at].sum() / per_cu),
                'attention_executed': float(fx[at].sum() / dur[at].sum() / per_cu)}
     busy = float(dur.sum() / (res['grid'] * (tr['end'].max() - tr['start'].min()) / 100e6))
+    crit = critical_path(lb, tr)
     names = [m['name'] for m in lb.metadata['buffers']]
     loss = float(ex.read('loss')[0])
     out = {'ms_per_step': round(ms, 3), 'path': PATH_NAMES.get(ex.path()), 'kernel_ms': round(kms, 3), 'tflops': round(tflops, 1), 'mfma_frac_step': round(tflops / BF16_PEAK_TFLOPS, 4),
            'mfma_frac_in_gemm_tasks': round(in_task['gemm'], 4), 'mfma_frac_in_attention_tasks': round(in_task['attention'], 4),
            'mfma_frac_in_attention_tasks_executed': round(in_task['attention_executed'], 4),
            'worker_busy_frac': round(busy, 4), 'tasks': lb.ntasks, 'edges': int(lb.succ.size), 'loss_after': loss,
-           'step_flops': flops, 'params': w.info['params'], 'first_step_check': check}
+           'step_flops': flops, 'params': w.info['params'], 'first_step_check': check, 'critical_path_traced': crit}
     log(f'  gpt-162m: {ms:.2f} ms/step (persistent kernel {kms:.2f} ms), {tflops:.1f} TFLOP/s ({tflops / BF16_PEAK_TFLOPS:.1%} of bf16 peak); in-task MFMA: '
         f'GEMM {in_task["gemm"]:.1%}, attention {in_task["attention"]:.1%}; workers busy {busy:.1%}; loss {loss:.4f}')
     ex.close()
@@ -325,9 +358,12 @@ def bench_small(name, w, steps_in_graph, reps, warmup, cpu):
     dur = (tr['end'] - tr['start']).astype(np.float64)
     span = float(tr['end'].max() - tr['start'].min())
     busy = float(dur.sum() / (res['grid'] * span))
+    crit = critical_path(lb, tr)
     out = {'us_per_step': round(kms * 1e3 / steps_in_graph, 2), 'path': PATH_NAMES.get(ex.path()), 'launch_ms': round(kms, 4), 'steps_in_graph': steps_in_graph,
-           'worker_busy_frac': round(busy, 4), 'tasks': lb.ntasks, 'edges': int(lb.succ.size)}
-    log(f'  {name}: {out["us_per_step"]} us/step ({steps_in_graph} steps per launch, {lb.ntasks} tasks), workers busy {busy:.1%}')
+           'worker_busy_frac': round(busy, 4), 'tasks': lb.ntasks, 'edges': int(lb.succ.size), 'critical_path_traced': crit}
+    log(f'  {name}: {out["us_per_step"]} us/step ({steps_in_graph} steps per launch, {lb.ntasks} tasks), workers busy {busy:.1%}; traced launch '
+        f'{crit["span_us"]} us, critical path of its task times {crit["critical_path_us"]} us, the chain it ran: {crit["chain_tasks"]} tasks, '
+        f'{crit["chain_running_us"]} us running, {crit["chain_waiting_us"]} us waiting')
     ex.close()
     if cpu:
         t = _oracle_time(w, CPU_THREADS)

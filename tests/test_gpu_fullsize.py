@@ -6,7 +6,7 @@ run with several threads, same results as one).
   twice the reference path's own deviation from an fp64 run of the same step (tests/golden/data/
   decode_fp64_deviation.json, written by tests/golden/make_decode_deviation.py).
 - C5 at full depth (36 layers + LM head), batch 1 and 8: the same checks against the full-depth fp64 deviations (b1_full,
-  b8_full in the same file).
+  b8_full in the same file); a token may differ from the reference path's only at a near-tie inside that deviation.
 - C3 GPT-162M, one layer at full width (d 768, 12 heads, T 1024, batch 4, vocab 50304, tied), bf16 storage: step-1
   weight gradients within 3.4e-2 relative L2 (twice the reference's bf16s deviation from fp64, 1.69e-2, README.md:212
   of the reference), loss within 1e-2.
@@ -96,12 +96,21 @@ def test_qwen3_decode_full_depth(batch):
     r = oracle.run(lb, init, threads=min(THREADS, os.cpu_count() or 1))
     want = D.graph_outputs(c, names, r['buffers'])
     got = D.graph_outputs(c, names, got_bufs)
-    assert got['tok'].tolist() == want['tok'].tolist() == dev['tok']
+    assert want['tok'].tolist() == dev['tok']
     assert np.array_equal(got_bufs[names.index('lens')], r['buffers'][names.index('lens')])
     err = D.deviations(got, want)
     print('device vs reference path', err, 'tolerance 2 x', dev['deviation'], flush=True)
     for k, e in err.items():
         assert e <= 2 * dev['deviation'][k], (k, e, dev['deviation'][k])
+    # Tokens: the reference path's, except at a near-tie that the reference path's own deviation from fp64 covers (36
+    # layers of bf16 activations move the logits by ~2% RMS): a different token must then score, in the reference
+    # path's logits, within twice that deviation (per element, RMS) of the best one.
+    for bb, (t_got, t_want) in enumerate(zip(got['tok'].tolist(), want['tok'].tolist())):
+        if t_got != t_want:
+            lg = want['logits'][bb]
+            margin, allow = lg[t_want] - lg[t_got], 2 * dev['deviation']['logits'] * float(np.sqrt(np.mean(lg * lg)))
+            print(f'sequence {bb}: token {t_got} (reference path {t_want}), logit margin {margin:.4g}, allowed {allow:.4g}', flush=True)
+            assert margin <= allow, (bb, t_got, t_want, margin, allow)
 
 
 TOL_GPT_BF16_GRAD = 3.4e-2

@@ -5,6 +5,7 @@
 #include "common.h"
 #include "ops_basic.h"
 #include "ops_attn_mfma.h"
+#include "ops_attn_f32mfma.h"
 
 namespace kvm {
 
@@ -136,6 +137,11 @@ __device__ __noinline__ void op_attn_fwd(const Ctx& c) {
     if (hd == 64) attn_fwd_mfma<64>(c); else if (hd == 128) attn_fwd_mfma<128>(c); else attn_fwd_mfma<32>(c);
     return;
   }
+  if ((hd == 32 || hd == 64 || hd == 128) && T % FA_KB == 0 && fa_ok_f32(c.buf(0), T) && fa_ok_f32(c.buf(1), T) && fa_ok_f32(c.buf(2), T) &&
+      fa_ok_f32(c.buf(3), T) && c.buf(4).dtype == 0) {
+    if (hd == 64) attn_fwd_f32mfma<64>(c); else if (hd == 128) attn_fwd_f32mfma<128>(c); else attn_fwd_f32mfma<32>(c);
+    return;
+  }
   switch (c.i(11)) { case 16: attn_fwd_t<16>(c); break; case 32: attn_fwd_t<32>(c); break; case 64: attn_fwd_t<64>(c); break; default: attn_fwd_t<128>(c); }
 }
 
@@ -193,6 +199,11 @@ __device__ __noinline__ void op_attn_bwd_dq(const Ctx& c) {
     if (hd == 64) attn_dq_mfma<64>(c); else attn_dq_mfma<32>(c);
     return;
   }
+  if ((hd == 32 || hd == 64) && T % FA_KB == 0 && fa_ok_f32(c.buf(0), T) && fa_ok_f32(c.buf(1), T) && fa_ok_f32(c.buf(2), T) &&
+      fa_ok_f32(c.buf(3), T) && fa_ok_f32(c.buf(6), T) && c.buf(4).dtype == 0 && c.buf(5).dtype == 0) {
+    if (hd == 64) attn_dq_f32mfma<64>(c); else attn_dq_f32mfma<32>(c);
+    return;
+  }
   switch (c.i(13)) { case 16: attn_dq_t<16>(c); break; case 32: attn_dq_t<32>(c); break; case 64: attn_dq_t<64>(c); break; default: attn_dq_t<128>(c); }
 }
 
@@ -245,6 +256,11 @@ __device__ __noinline__ void op_attn_bwd_dkv(const Ctx& c) {
   if ((hd == 32 || hd == 64) && T % FA_KB == 0 && fa_ok(c.buf(0), T) && fa_ok(c.buf(1), T) && fa_ok(c.buf(2), T) && fa_ok(c.buf(3), T) &&
       fa_ok(c.buf(6), T) && fa_ok(c.buf(7), T) && c.buf(4).dtype == 0 && c.buf(5).dtype == 0) {
     if (hd == 64) attn_dkv_mfma<64>(c); else attn_dkv_mfma<32>(c);
+    return;
+  }
+  if ((hd == 32 || hd == 64) && T % FA_KB == 0 && fa_ok_f32(c.buf(0), T) && fa_ok_f32(c.buf(1), T) && fa_ok_f32(c.buf(2), T) &&
+      fa_ok_f32(c.buf(3), T) && fa_ok_f32(c.buf(6), T) && fa_ok_f32(c.buf(7), T) && c.buf(4).dtype == 0 && c.buf(5).dtype == 0) {
+    if (hd == 64) attn_dkv_f32mfma<64>(c); else attn_dkv_f32mfma<32>(c);
     return;
   }
   switch (c.i(13)) { case 16: attn_dkv_t<16>(c); break; case 32: attn_dkv_t<32>(c); break; case 64: attn_dkv_t<64>(c); break; default: attn_dkv_t<128>(c); }

@@ -927,12 +927,121 @@ __device__ __noinline__ void op_matmul_mma_bf16_kr(const Ctx& c) {
   else mfma_tile<128, 256>(c);
 }
 
+// The fp32 engine's pipelined form for whole tiles of f32 operands (16-byte aligned rows, K a multiple of 16): every
+// slab goes from HBM straight into LDS (buffer_load ... lds), NS stages deep, so no slab passes through registers and
+// the loads of NS - 1 slabs are always in flight behind the one being multiplied. A k-contiguous operand sits in LDS as
+// [row][16 k] (the register-staged form's swizzled layout); a row-contiguous one as [16 k][R rows], read one k per
+// ds_read_b32 (32 lanes: 128 contiguous bytes). Every stage slot issues its loads, also past the last slab (an offset
+// past every descriptor's range: no memory access), so every wait is a constant vmcnt.
+template <int R, bool KC> struct FOp {
+  static constexpr int NL = R * FKS * 4 / 1024 / KVM_WAVES;   // direct loads per thread per slab
+  static_assert(NL >= 1, "tile shape");
+  i32x4_t rs;
+  int voff[NL];
+  int sstep;
+  __device__ __forceinline__ void init(const View& X, int r0) {
+    if constexpr (KC) {
+      rs = dma_rsrc((const void*)(X.f() + (long long)r0 * X.cols), ((long long)X.rows - r0) * X.cols * 4);
+      sstep = FKS * 4;
+    } else {
+      rs = dma_rsrc((const void*)(X.f() + r0), (long long)X.rows * X.cols * 4 - (long long)r0 * 4);
+      sstep = FKS * X.cols * 4;
+    }
+#pragma unroll
+    for (int q = 0; q < NL; ++q) {
+      const int u = 64 * (q * KVM_WAVES + wave()) + lane();
+      if constexpr (KC) { const int row = u >> 2, ch = (u & 3) ^ ((row >> 2) & 3); voff[q] = (row * X.cols + 4 * ch) * 4; }
+      else { const int k = u / (R / 4), ph = u % (R / 4); voff[q] = (k * X.cols + 4 * ph) * 4; }
+    }
+  }
+  __device__ __forceinline__ void issue(LDS float* lds, int s, int nst) const {
+#pragma unroll
+    for (int q = 0; q < NL; ++q) dma16(rs, voff[q], s < nst ? s * sstep : (int)0x80000000, lds + (q * KVM_WAVES + wave()) * 256);
+  }
+  // four k values (8q + 4 (l / 32) + t) of row rb + l % 32
+  __device__ __forceinline__ f32x4n frag(const LDS float* lds, int rb, int q) const {
+    const int l = lane(), r = rb + (l & 31), ch = 2 * q + (l >> 5);
+    if constexpr (KC) return *(const LDS f32x4n*)(lds + fsw(r, ch));
+    else return f32x4n{lds[(4 * ch) * R + r], lds[(4 * ch + 1) * R + r], lds[(4 * ch + 2) * R + r], lds[(4 * ch + 3) * R + r]};
+  }
+};
+
+template <int TM, int TN, bool AKC, bool BKC> __device__ __noinline__ void gemm_f32_lds(const Ctx& c) {
+  constexpr int WM = TM / 2, WN = TN / 2, BM = WM / 32, BN = WN / 32, SA = TM * FKS, ST = (TM + TN) * FKS;
+  constexpr int NS = ST * 4 * 6 <= KVM_LDS_BYTES ? 6 : KVM_LDS_BYTES / (ST * 4);
+  static_assert(NS >= 3, "LDS");
+  const GemmArgs g = gemm_args(c);
+  const int wm0 = (wave() >> 1) * WM, wn0 = (wave() & 1) * WN;
+  FOp<TM, AKC> da;
+  FOp<TN, BKC> db;
+  da.init(g.A, g.m0);
+  db.init(g.B, g.n0);
+  LDS float* lds = (LDS float*)c.smem;
+  f32x16 acc[BM][BN];
+#pragma unroll
+  for (int i = 0; i < BM; ++i)
+#pragma unroll
+    for (int j = 0; j < BN; ++j) acc[i][j] = f32x16{};
+  const int nst = g.K / FKS;
+  constexpr int NLS = FOp<TM, AKC>::NL + FOp<TN, BKC>::NL;
+  __syncthreads();                                 // the previous task may still read this LDS
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p) { da.issue(lds + p * ST, p, nst); db.issue(lds + p * ST + SA, p, nst); }
+  for (int s = 0; s < nst; ++s) {
+    wait_vm_c<(NS - 2) * NLS>();                   // this thread's loads of slab s have landed
+    __syncthreads();                               // ... everyone's, and every wave is past slab s - 1
+    { const int sn = s + NS - 1; LDS float* nb = lds + (sn % NS) * ST; da.issue(nb, sn, nst); db.issue(nb + SA, sn, nst); }
+    const LDS float* la = lds + (s % NS) * ST;
+    const LDS float* lb = la + SA;
+#pragma unroll
+    for (int q = 0; q < FKS / 8; ++q) {
+      f32x4n av[BM], bv[BN];
+#pragma unroll
+      for (int i = 0; i < BM; ++i) av[i] = da.frag(la, wm0 + i * 32, q);
+#pragma unroll
+      for (int j = 0; j < BN; ++j) bv[j] = db.frag(lb, wn0 + j * 32, q);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < BM; ++i)
+#pragma unroll
+          for (int j = 0; j < BN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[j][t], av[i][t], acc[i][j], 0, 0, 0);
+    }
+  }
+  wait_vm_c<0>();                                  // the placeholder loads have written their LDS bytes
+  gemm_store<TM, TN>(c, acc, g);
+}
+
+// Whether an f32 operand takes the pipelined form: f32 storage, 16-byte rows, the tile's rows inside the matrix, K a
+// whole number of slabs, offsets within 32 bits.
+__device__ __forceinline__ bool gemm_f32_fast_operand(const View& X, bool kc, int r0, int R, int rows, int K) {
+  if (X.dtype != 0 || (X.cols & 3) || (K % FKS) || r0 + R > rows) return false;
+  if (kc) return (long long)R * X.cols * 4 + (long long)K * 4 < 0x7fffffffll;
+  return (r0 & 3) == 0 && (long long)K * X.cols * 4 < 0x7fffffffll;
+}
+template <int TM, int TN> __device__ __forceinline__ void f32_tile(const Ctx& c) {
+  const GemmArgs g = gemm_args(c);
+  const bool akc = !(g.fl & 1), bkc = (g.fl & 2) != 0;
+  if (gemm_f32_fast_operand(g.A, akc, g.m0, TM, g.M, g.K) && gemm_f32_fast_operand(g.B, bkc, g.n0, TN, g.N, g.K)) {
+    if (akc) { if (bkc) gemm_f32_lds<TM, TN, true, true>(c); else gemm_f32_lds<TM, TN, true, false>(c); }
+    else { if (bkc) gemm_f32_lds<TM, TN, false, true>(c); else gemm_f32_lds<TM, TN, false, false>(c); }
+    return;
+  }
+  gemm_f32<TM, TN>(c);
+}
+
 // Op 34 on the fp32 MFMA engine: 64x64 tiles by default, 128x128 with flag 32, 256x128 with flag 64.
 __device__ __noinline__ void op_matmul_tile(const Ctx& c) {
   const int fl = c.i(11);
+#ifndef KVM_F32_REGSTAGE
+  if (fl & 64) f32_tile<256, 128>(c);
+  else if (fl & 32) f32_tile<128, 128>(c);
+  else f32_tile<64, 64>(c);
+#else
   if (fl & 64) gemm_f32<256, 128>(c);
   else if (fl & 32) gemm_f32<128, 128>(c);
   else gemm_f32<64, 64>(c);
+#endif
 }
 
 }  // namespace kvm

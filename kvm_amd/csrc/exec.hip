@@ -1708,9 +1708,12 @@ int kvm_submit(KvmExec* ex, const MvmTaskDesc* tasks, int ntasks, const int32_t*
   return 0;
 }
 
-// Estimated task cost in microseconds for the static planner (only relative weights and the auto path's threshold use
-// it): a fixed per-task cost, plus for GEMM tiles their FLOPs at a typical in-task rate (bf16 MFMA about 3 TFLOP/s per
-// CU, fp32 about 0.25), for attention tasks their score pairs, for streaming operators the bytes of their range.
+// Planning cost of a task in microseconds, for the static planner's list schedule. Fitted to per-task traces of the
+// tiny GPT and the eight-MLP graph on MI355X: an fp32 GEMM tile costs about 9 us plus 1.55 us per MFLOP (least squares
+// over 72,500 traced tiles), the bf16 MFMA tiles about 3 us plus their flops at 3 TFLOP/s per CU; the other operators
+// take their traced medians (row norms and the fused cross entropy about 8 us, the layer-norm input gradient 15 us,
+// elementwise activations 5.5 us, a no-op well under 1 us) and 3 us when not listed. The ratios set the plan's
+// critical-path priorities and worker balance; the mean decides the auto path (KVM_STATIC_MAX_MEAN_US).
 static double task_cost_us(const MvmTaskDesc& d, const int32_t* a) {
   const int op = d.op_id;
   if (op == 34 || op == 114 || op == 122 || op == 302 || op == 304 || op == 308) {
@@ -1722,13 +1725,19 @@ static double task_cost_us(const MvmTaskDesc& d, const int32_t* a) {
     else if (fl & 64) { tm = 256; tn = 128; }
     else if (fl & 32) { tm = tn = 128; }
     const double flops = 2.0 * (double)std::max(0ll, std::min(M, m0 + tm) - m0) * (double)std::max(0ll, std::min(N, n0 + tn) - n0) * (double)K;
-    return 3.0 + flops / (op == 34 ? 0.25e6 : 3.0e6);
+    return op == 34 ? 9.0 + flops / 0.65e6 : 3.0 + flops / 3.0e6;
   }
-  if (op == 45 || op == 47 || op == 48) {   // q0 / k0 block of 128 rows against up to T keys: about T * 128 * hd * 4 flop
-    const int T = op == 48 ? a[11] : a[8], hd = op == 48 ? a[13] : a[11];
-    return 5.0 + 4.0 * 128.0 * (double)T * hd / 1.0e6;
+  switch (op) {
+    case 45: case 47: case 48: {   // q0 / k0 block of 128 rows against up to T keys: about T * 128 * hd * 4 flop
+      const int T = op == 48 ? a[11] : a[8], hd = op == 48 ? a[13] : a[11];
+      return 5.0 + 4.0 * 128.0 * (double)T * hd / 1.0e6;
+    }
+    case 0: return 0.7;                                              // noop
+    case 37: return 15.0;                                            // layernorm_bwd_dx
+    case 35: case 46: case 54: case 127: case 309: return 8.0;       // layernorm_fwd, attn_bwd_delta, adamw, softmax_ce_fused, layernorm_bwd_dx_res
+    case 33: case 96: case 97: return 5.5;                           // embedding_bwd, act_fwd, act_bwd
+    default: return 3.0;
   }
-  return 3.0;
 }
 
 // Bytes a task streams when its operator is bandwidth-bound, else -1: the reference's scheduler cost table

@@ -134,7 +134,8 @@ inline Plan plan(const MvmTaskDesc* t, int n, const int32_t* succ, const std::ve
   struct Set { std::vector<int> wk, need; std::vector<double> fin; double f1 = 0, f2 = 0; int w1 = -1; };
   std::vector<Set> sets(n);
   auto set_ready = [&](const Set& S, int w) {
-    double r = (w == S.w1 ? S.f2 : S.f1) + comm_us;
+    const double other = w == S.w1 ? S.f2 : S.f1;   // latest finish on a worker other than w (0: none)
+    double r = other > 0 ? other + comm_us : 0.0;
     auto it = std::lower_bound(S.wk.begin(), S.wk.end(), w);
     if (it != S.wk.end() && *it == w) r = std::max(r, S.fin[it - S.wk.begin()]);
     return r;

@@ -81,9 +81,20 @@ __device__ __forceinline__ bool fa_ok(const View& x, int T) {
   return x.ok() && x.dtype == 2 && (x.cols % 8) == 0 && (long long)T * x.cols * 2 < 0x7fffffffll;
 }
 
+// Forward for 128 queries of head h (op 45): lane l of wave w owns query q0 + 32w + l%32. Per 64-key block kb:
+// S^T = K Q^T, P^T = exp2(S^T * scale * log2(e) - m), O^T += V^T P^T, with a running maximum m per query.
+//   * Software pipeline over blocks: iteration kb computes the scores of block kb + 1 and then the softmax and P V of
+//     block kb, so the MFMAs of the next scores and the VALU work of the current softmax are independent and the
+//     scheduler interleaves them (one wave per SIMD: nothing else hides either). FA_FNS stages of K/V in LDS; the
+//     buffer a new block loads into held block kb - 1, which every wave finished before the barrier of iteration kb.
+//   * The causal mask is applied only in blocks that reach past the wave's first query.
+//   * Lazy rescaling: m moves (and O, l are rescaled) only when a query's block maximum exceeds m by more than 8 (in
+//     log2 units); P values are then at most 2^8, which fp32 sums and bf16 P hold with the same relative rounding. The
+//     result O / l and the log-sum-exp m + log2(l) do not depend on which m was used.
+constexpr int FA_FNS = 4;
 template <int HD> __device__ __noinline__ void attn_fwd_mfma(const Ctx& c) {
   typedef FaL<HD> L;
-  constexpr int NKK = HD / 16, NDB = HD / 32;
+  constexpr int NKK = HD / 16, NDB = HD / 32, NS = FA_FNS;
   const View q = uview(c, 0), k = uview(c, 1), v = uview(c, 2), o = uview(c, 3), lse = uview(c, 4);
   const int bb = rfl(c.i(5)), h = rfl(c.i(6)), q0 = rfl(c.i(7)), T = rfl(c.i(8)), H = rfl(c.i(9)), Hkv = rfl(c.i(10));
   const float sl2 = __int_as_float(rfl(__float_as_int(c.f(12)))) * 1.4426950408889634f;   // scale * log2(e)
@@ -95,49 +106,74 @@ template <int HD> __device__ __noinline__ void attn_fwd_mfma(const Ctx& c) {
   for (int kk = 0; kk < NKK; ++kk)
     qf[kk] = qok ? *(const GLOBAL bf16x8*)(q.h() + ((long long)bb * T + qrow) * q.cols + h * HD + kk * 16 + 8 * g) : bf16x8{};
   const int kend = min(T, q0 + 128), nkb = (kend + FA_KB - 1) / FA_KB;
-  const int wlast = min(T - 1, q0 + 32 * w + 31);
+  const int wfirst = rfl(q0 + 32 * w), wlast = rfl(min(T - 1, wfirst + 31));   // wave-uniform
   const i32x4_t rk = dma_rsrc((const void*)(k.h() + (long long)bb * T * k.cols), (long long)T * k.cols * 2);
   const i32x4_t rv = dma_rsrc((const void*)(v.h() + (long long)bb * T * v.cols), (long long)T * v.cols * 2);
   LDS uint16_t* lds = (LDS uint16_t*)c.smem;
   constexpr int ST = 2 * FA_KB * HD;                       // elements per stage: K then V
-  f32x16 oacc[NDB];
-#pragma unroll
-  for (int d = 0; d < NDB; ++d) oacc[d] = f32x16{};
-  float m = -INFINITY, lsum = 0.f;
-  __syncthreads();                                         // the previous task may still read this LDS
-#pragma unroll
-  for (int p = 0; p < FA_NS - 1; ++p)
-    if (p < nkb) { L::template issue<false>(lds + p * ST, rk, p * FA_KB, k.cols, kvh * HD); L::template issue<true>(lds + p * ST + FA_KB * HD, rv, p * FA_KB, v.cols, kvh * HD); }
-  for (int kb = 0; kb < nkb; ++kb) {
-    wait_vm(min(FA_NS - 2, nkb - 1 - kb) * 2 * L::NL);
-    __syncthreads();
-    if (kb + FA_NS - 1 < nkb) {
-      LDS uint16_t* nb = lds + ((kb + FA_NS - 1) % FA_NS) * ST;
-      L::template issue<false>(nb, rk, (kb + FA_NS - 1) * FA_KB, k.cols, kvh * HD);
-      L::template issue<true>(nb + FA_KB * HD, rv, (kb + FA_NS - 1) * FA_KB, v.cols, kvh * HD);
-    }
-    if (kb * FA_KB > wlast) continue;                      // every key of the block is after this wave's queries
-    const LDS uint16_t* Ks = lds + (kb % FA_NS) * ST;
-    const LDS uint16_t* Vs = Ks + FA_KB * HD;
-    f32x16 s[2];
+  static_assert(NS * ST * 2 <= KVM_LDS_BYTES, "LDS");
+  auto issue = [&](int blk) {
+    LDS uint16_t* d = lds + (blk % NS) * ST;
+    L::template issue<false>(d, rk, blk * FA_KB, k.cols, kvh * HD);
+    L::template issue<true>(d + FA_KB * HD, rv, blk * FA_KB, v.cols, kvh * HD);
+  };
+  auto scores = [&](int blk, f32x16 (&s)[2]) {
+    const LDS uint16_t* Ks = lds + (blk % NS) * ST;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       s[sb] = f32x16{};
 #pragma unroll
       for (int kk = 0; kk < NKK; ++kk) s[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(L::frag_kc(Ks, sb * 32, kk), qf[kk], s[sb], 0, 0, 0);
     }
-    float mloc = -INFINITY;
+  };
+  f32x16 oacc[NDB];
+#pragma unroll
+  for (int d = 0; d < NDB; ++d) oacc[d] = f32x16{};
+  float m = -INFINITY, lsum = 0.f;                         // m in units of scale * log2(e) * score
+  // One iteration: wait for block kb + 1, issue block kb + NS - 1, then (unless every key of block kb is after this
+  // wave's queries) the mask of a diagonal block and the rescale, each behind a wave-uniform branch, and one
+  // straight-line part: the fragment reads of block kb + 1's K and block kb's V, the softmax of kb, the scores of kb + 1
+  // and P V of kb. The scores of kb + 1 are computed even where the wave does not use them (its last block), so that
+  // the part has no branch and the scheduler can place the VALU softmax between the MFMAs. The barrier and the loads
+  // are outside every per-wave condition.
+  auto step = [&](int kb, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+    if (kb + 1 < nkb) wait_vm(min(NS - 3, nkb - 2 - kb) * 2 * L::NL);
+    __syncthreads();
+    if (kb + NS - 1 < nkb) issue(kb + NS - 1);
+    if (kb * FA_KB > wlast) return;                        // every key of the block is after this wave's queries
+    if (kb * FA_KB + FA_KB - 1 > wfirst) {                 // a diagonal block: mask keys after each query
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kb * FA_KB + sb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) > qrow) sc[sb][r] = -INFINITY;
+    }
+    float mx = sc[0][0];
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb * FA_KB + sb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        const float x = key > qrow ? -INFINITY : s[sb][r] * sl2;
-        s[sb][r] = x;
-        mloc = fmaxf(mloc, x);
-      }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float mn = fmaxf(m, mloc), f = __builtin_amdgcn_exp2f(m - mn);
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[sb][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sl2;
+    if (__ballot(mx > m + 8.f)) {                          // wave-uniform: some query's maximum moved far enough
+      const float mn = fmaxf(m, mx), f = __builtin_amdgcn_exp2f(m - mn);
+      lsum *= f;
+#pragma unroll
+      for (int d = 0; d < NDB; ++d) oacc[d] *= f;
+      m = mn;
+    }
+    const LDS uint16_t* Kn = lds + ((kb + 1) % NS) * ST;
+    const LDS uint16_t* Vs = lds + (kb % NS) * ST + FA_KB * HD;
+    bf16x8 kfr[2][NKK], vfr[NDB][2][2];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk) kfr[sb][kk] = L::frag_kc(Kn, sb * 32, kk);
+#pragma unroll
+    for (int d = 0; d < NDB; ++d)
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) vfr[d][sb][t] = L::frag_tr(Vs, d * 32, sb * 32 + 16 * t);
     float ps = 0.f;
     bf16x8 pf[2][2];
 #pragma unroll
@@ -146,21 +182,34 @@ template <int HD> __device__ __noinline__ void attn_fwd_mfma(const Ctx& c) {
       for (int t = 0; t < 2; ++t) {
         float pv[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { pv[i] = __builtin_amdgcn_exp2f(s[sb][8 * t + i] - mn); ps += pv[i]; }
+        for (int i = 0; i < 8; ++i) { pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[sb][8 * t + i], sl2, -m)); ps += pv[i]; }
         pf[sb][t] = pack_bf16(pv);
       }
-    ps += __shfl_xor(ps, 32, 64);
-    lsum = lsum * f + ps;
-    m = mn;
 #pragma unroll
-    for (int d = 0; d < NDB; ++d) {
-      oacc[d] *= f;
+    for (int sb = 0; sb < 2; ++sb) {
+      sn[sb] = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk) sn[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[sb][kk], qf[kk], sn[sb], 0, 0, 0);
+    }
+    lsum += ps + __shfl_xor(ps, 32, 64);
+#pragma unroll
+    for (int d = 0; d < NDB; ++d)
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(L::frag_tr(Vs, d * 32, sb * 32 + 16 * t), pf[sb][t], oacc[d], 0, 0, 0);
-    }
-  }
+        for (int t = 0; t < 2; ++t) oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfr[d][sb][t], pf[sb][t], oacc[d], 0, 0, 0);
+  };
+  __syncthreads();                                         // the previous task may still read this LDS
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p)
+    if (p < nkb) issue(p);
+  wait_vm(min(NS - 2, nkb - 1) * 2 * L::NL);
+  __syncthreads();
+  f32x16 sa[2], sb2[2];
+  scores(0, sa);                                           // block 0 holds key 0 <= every query of the task
+  int kb = 0;
+  for (; kb + 1 < nkb; kb += 2) { step(kb, sa, sb2); step(kb + 1, sb2, sa); }
+  if (kb < nkb) step(kb, sa, sb2);
   if (qok) {
     const float inv = 1.f / lsum;
     GLOBAL uint16_t* orow = o.h() + ((long long)bb * T + qrow) * o.cols + h * HD + 4 * g;

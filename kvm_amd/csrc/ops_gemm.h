@@ -558,7 +558,10 @@ __device__ __noinline__ void gemm_loop(const Ctx& c) {
 //     mb + 4*(i16%4) .. +3, lane i16 receives rows mb + i16 at k = kb .. kb+3, i.e. an MFMA operand (8 k values of one
 //     row) from two reads.
 constexpr int DK = 32;
-constexpr int DNS = 5;
+// Stages in flight: 4 (3 ahead of the one being multiplied). Measured on 512 independent 128x256 tiles: 4 stages run
+// K=768 tiles in 20.3 us against 23.9 with 5 (2.5 us less fixed cost, 0.44 instead of 0.48 us per stage), 3 stages in
+// 27.9 us; GPT-162M step 9.56 -> 9.42 ms. A power of two also makes the stage index a mask.
+constexpr int DNS = 4;
 
 // s_waitcnt vmcnt(n) for a wave-uniform runtime n (other counters untouched); n above 30 waits for everything. The
 // immediate must be a constant, so a (scalar) switch picks it; the wait is inline assembly with a memory clobber so

@@ -214,9 +214,15 @@ __device__ __forceinline__ void stwt_f4(GLOBAL float* p, f32x4n v) {
   const u64x2_t u = __builtin_bit_cast(u64x2_t, v);
   stwt64(p, u.x); stwt64(p + 2, u.y);
 }
+// Two floats rounded to bf16 (round to nearest even, as f2bf) and packed, a in the low half: one v_cvt_pk_bf16_f32.
+typedef float f32x2v_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_bf2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v_t{a, b}, bf16x2v_t));
+}
 // Four bf16 values as one 8-byte write-through store.
 __device__ __forceinline__ void stwt_bf4(GLOBAL uint16_t* p, float a, float b, float c, float d) {
-  stwt64(p, (uint64_t)f2bf(a) | ((uint64_t)f2bf(b) << 16) | ((uint64_t)f2bf(c) << 32) | ((uint64_t)f2bf(d) << 48));
+  stwt64(p, (uint64_t)pk_bf2(a, b) | ((uint64_t)pk_bf2(c, d) << 32));
 }
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 // 16-byte write-through stores through a buffer descriptor (cache policy SC1): one instruction, visible to the
@@ -226,6 +232,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t wt_rsrc(const void* base, long
 }
 __device__ __forceinline__ void stwt_buf(__amdgpu_buffer_rsrc_t r, int off, f32x4n v) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, off, 0, 16 /* SC1 */);
+}
+// Four floats as bf16, one 8-byte write-through store through a buffer descriptor (32-bit offsets: no 64-bit address
+// arithmetic per store).
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void stwt_bf4_buf(__amdgpu_buffer_rsrc_t r, int off, f32x4n v) {
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{pk_bf2(v.x, v.y), pk_bf2(v.z, v.w)}, r, off, 0, 16 /* SC1 */);
 }
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 

@@ -363,7 +363,7 @@ __device__ __forceinline__ void epi_rows(const Ctx& c, const GemmArgs& g) {
   const View& xv = KIND == 1 ? e.res : KIND == 2 ? e.out : e.pre;
   lx.init(xv, KIND >= 1 && KIND <= 3);
   const f32x4n bv = lb.get(n);
-  const __amdgpu_buffer_rsrc_t orsrc = wt_rsrc(e.out.p, (long long)g.M * e.out.cols * 4);   // f32 output rows (small: < 2^31 bytes)
+  const __amdgpu_buffer_rsrc_t orsrc = wt_rsrc(e.out.p, (long long)g.M * e.out.cols * (OBF ? 2 : 4));   // output rows (small: < 2^31 bytes)
   const int xc = xv.cols;
   for (int k0 = 0; k0 < NI; k0 += NB) {
     u32x4_t raw[NB];
@@ -390,7 +390,7 @@ __device__ __forceinline__ void epi_rows(const Ctx& c, const GemmArgs& g) {
         st4(e.pre, (long long)m * e.pre.cols + n, v);
         v.x = gelu_f(v.x); v.y = gelu_f(v.y); v.z = gelu_f(v.z); v.w = gelu_f(v.w);
       }
-      if constexpr (OBF) stwt_bf4(e.out.h() + (long long)m * e.out.cols + n, v.x, v.y, v.z, v.w);
+      if constexpr (OBF) stwt_bf4_buf(orsrc, (m * e.out.cols + n) * 2, v);
       else stwt_buf(orsrc, (m * e.out.cols + n) * 4, v);
     }
   }

@@ -857,6 +857,11 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
       }
     }
     Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
+    // The 128x256 bf16 GEMM tile (ops 122, 308: most of a GPT step's tiles) runs inlined here: called out of line, its
+    // body saves and restores the callee-saved registers it uses around every task (GPT-162M 9.38 -> 9.15 ms).
+    // The 256x256 tile (the compiler fails on it inlined here) and the attention bodies (inlined, they push the
+    // kernel's private segment past KVM_MAX_PRIVATE_BYTES) stay out of line.
+    if ((op == 122 || op == 308) && gemm_tile_inline<128, 256>(c)) { if (op == 308) mma_delta_tail(c); } else
     dispatch(op, c);
     // Every operator stores through write-through (agent-scope) stores only, which tests/test_wt_stores.py checks
     // in the compiled code: once each wave has waited for its own stores, they are agent-visible, and the barrier

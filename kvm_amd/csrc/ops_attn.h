@@ -429,8 +429,12 @@ __device__ __forceinline__ float row16_sum(float v) {
 // Op 308: the 128 x 256 tile of op 122 (plain epilogue, bf16 output), then, from the tile still staged in LDS, the
 // attention backward statistic of its four 64-column heads: per row, each lane takes its 4 columns (bf16-rounded as
 // stored) times o, and the 16 lanes of a head (one DPP row) are summed.
+__device__ __noinline__ void mma_delta_tail(const Ctx& c);
 __device__ __noinline__ void op_matmul_mma_bf16_delta(const Ctx& c) {
   mfma_tile<128, 256>(c);                                  // leaves the f32 tile staged in LDS (one 128 KiB half)
+  mma_delta_tail(c);
+}
+__device__ __noinline__ void mma_delta_tail(const Ctx& c) {
   const GemmArgs g = gemm_args(c);
   const View o = uniform_view(c.buf(13)), dl = uniform_view(c.buf(14));
   const int T = rfl(c.i(15)), H = rfl(c.i(16));

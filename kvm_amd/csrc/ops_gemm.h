@@ -643,7 +643,7 @@ template <int R, bool KC> struct DOp {
 };
 
 template <int TM, int TN, bool AKC, bool BKC>
-__device__ __noinline__ void gemm_lds(const Ctx& c) {
+__device__ __forceinline__ void gemm_lds_b(const Ctx& c) {
   constexpr int WM = TM / 2, WN = TN / 2, BM = WM / 32, BN = WN / 32;
   constexpr int SA = TM * DK, SB = TN * DK, ST = SA + SB;    // elements per stage
   constexpr int NS = DNS * ST * 2 <= KVM_LDS_BYTES ? DNS : KVM_LDS_BYTES / (ST * 2);   // stages that fit in LDS
@@ -735,6 +735,8 @@ __device__ __noinline__ void gemm_lds(const Ctx& c) {
   wait_vm_c<0>();                                  // the placeholder loads have written their LDS bytes
   gemm_store<TM, TN>(c, acc, g);
 }
+template <int TM, int TN, bool AKC, bool BKC>
+__device__ __noinline__ void gemm_lds(const Ctx& c) { gemm_lds_b<TM, TN, AKC, BKC>(c); }
 
 // Whether an operand slab sequence can use unconditional vector loads: bf16 storage, rows of whole 16-byte vectors,
 // the tile's rows inside the matrix and K a whole number of slabs.
@@ -890,6 +892,16 @@ __device__ __noinline__ void op_matmul_tile_bf16(const Ctx& c) {
   else mfma_tile<64, 64>(c);
 }
 __device__ __noinline__ void op_matmul_mma_bf16(const Ctx& c) { mfma_tile<128, 256>(c); }
+// Whole-tile shapes of a TM x TN tile with the direct-to-LDS main loop inlined into the caller (the persistent kernel):
+// false when the tile needs the general path.
+template <int TM, int TN> __device__ __forceinline__ bool gemm_tile_inline(const Ctx& c) {
+  const GemmArgs g = gemm_args(c);
+  const bool akc = !(g.fl & 1), bkc = (g.fl & 2) != 0;
+  if (!gemm_fast_operand(g.A, akc, g.m0, TM, g.M, g.K) || !gemm_fast_operand(g.B, bkc, g.n0, TN, g.N, g.K)) return false;
+  if (akc) { if (bkc) gemm_lds_b<TM, TN, true, true>(c); else gemm_lds_b<TM, TN, true, false>(c); }
+  else { if (bkc) gemm_lds_b<TM, TN, false, true>(c); else gemm_lds_b<TM, TN, false, false>(c); }
+  return true;
+}
 // Op 304: the 256x256 tile. Shapes outside the direct-to-LDS path (partial tiles, odd K, f32 operands) run as two
 // 128x256 tiles, rows m0 and m0 + 128 (the second by advancing m0 in the task's LDS copy of its arguments).
 __device__ __forceinline__ void tile_256(const Ctx& c) {

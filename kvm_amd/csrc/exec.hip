@@ -733,7 +733,14 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
     // The decode hot path's bodies are inlined here (no call: no callee-saved register spills and reloads per
     // task); every other operator goes through the dispatcher.
     const int op = d.op_id;
-    if (V == 0) dispatch(op, c);
+    // V 0 (the small fp32 training graphs): their 64x64 and 128x128 fp32 GEMM tiles inlined (tiny GPT 501 -> 484 us
+    // per step; the dynamic kernel's 256x128 fp32 tile measured slower inlined, 98.4 vs 97.2 ms for GPT-355M).
+    if (V == 0) {
+      const int fl = op == 34 ? c.i(11) & 96 : -1;
+      if (fl == 32 && f32_tile_inline<128, 128>(c)) {}
+      else if (fl == 0 && f32_tile_inline<64, 64>(c)) {}
+      else dispatch(op, c);
+    }
     else {
       constexpr int GR = V == 1 ? 12 : 4;          // the set's GEMV ring depth
       // (the fused SwiGLU GEMV, op 311, runs through the dispatcher: inlined beside the others it made the kernel spill)
@@ -857,11 +864,13 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_exec_kernel(KvmDevState S)
       }
     }
     Ctx c{(const LDS View*)s_rec.views, (const LDS int32_t*)s_rec.args, (LDS char*)smem, S.cnt, slot};
-    // The 128x256 bf16 GEMM tile (ops 122, 308: most of a GPT step's tiles) runs inlined here: called out of line, its
-    // body saves and restores the callee-saved registers it uses around every task (GPT-162M 9.38 -> 9.15 ms).
-    // The 256x256 tile (the compiler fails on it inlined here) and the attention bodies (inlined, they push the
-    // kernel's private segment past KVM_MAX_PRIVATE_BYTES) stay out of line.
+    // The 128x256 and 128x128 bf16 GEMM tiles (ops 122, 308, 114: most of a GPT step's tiles) run inlined here.
+    // Called out of line, a body saves and restores the callee-saved registers it uses around every task (GPT-162M
+    // 9.38 -> 9.15 ms with ops 122 / 308 inlined, 9.07 with op 114's 128x128 tiles too). The 256x256 tile (the
+    // compiler fails on it inlined here) and the attention bodies (inlined, they push the kernel's private segment
+    // past KVM_MAX_PRIVATE_BYTES) stay out of line.
     if ((op == 122 || op == 308) && gemm_tile_inline<128, 256>(c)) { if (op == 308) mma_delta_tail(c); } else
+    if (op == 114 && (c.i(11) & 96) == 32 && gemm_tile_inline<128, 128>(c)) {} else
     dispatch(op, c);
     // Every operator stores through write-through (agent-scope) stores only, which tests/test_wt_stores.py checks
     // in the compiled code: once each wave has waited for its own stores, they are agent-visible, and the barrier

@@ -981,7 +981,7 @@ template <int R, bool KC> struct FOp {
   }
 };
 
-template <int TM, int TN, bool AKC, bool BKC> __device__ __noinline__ void gemm_f32_lds(const Ctx& c) {
+template <int TM, int TN, bool AKC, bool BKC> __device__ __forceinline__ void gemm_f32_lds_b(const Ctx& c) {
   constexpr int WM = TM / 2, WN = TN / 2, BM = WM / 32, BN = WN / 32, SA = TM * FKS, ST = (TM + TN) * FKS;
   constexpr int NS = ST * 4 * 6 <= KVM_LDS_BYTES ? 6 : KVM_LDS_BYTES / (ST * 4);
   static_assert(NS >= 3, "LDS");
@@ -1026,6 +1026,7 @@ template <int TM, int TN, bool AKC, bool BKC> __device__ __noinline__ void gemm_
   wait_vm_c<0>();                                  // the placeholder loads have written their LDS bytes
   gemm_store<TM, TN>(c, acc, g);
 }
+template <int TM, int TN, bool AKC, bool BKC> __device__ __noinline__ void gemm_f32_lds(const Ctx& c) { gemm_f32_lds_b<TM, TN, AKC, BKC>(c); }
 
 // Whether an f32 operand takes the pipelined form: f32 storage, 16-byte rows, the tile's rows inside the matrix, K a
 // whole number of slabs, offsets within 32 bits.
@@ -1045,6 +1046,15 @@ template <int TM, int TN> __device__ __forceinline__ void f32_tile(const Ctx& c)
   gemm_f32<TM, TN>(c);
 }
 
+// The whole-tile fp32 form inlined into the caller (the persistent kernel); false when the tile needs the general path.
+template <int TM, int TN> __device__ __forceinline__ bool f32_tile_inline(const Ctx& c) {
+  const GemmArgs g = gemm_args(c);
+  const bool akc = !(g.fl & 1), bkc = (g.fl & 2) != 0;
+  if (!gemm_f32_fast_operand(g.A, akc, g.m0, TM, g.M, g.K) || !gemm_f32_fast_operand(g.B, bkc, g.n0, TN, g.N, g.K)) return false;
+  if (akc) { if (bkc) gemm_f32_lds_b<TM, TN, true, true>(c); else gemm_f32_lds_b<TM, TN, true, false>(c); }
+  else { if (bkc) gemm_f32_lds_b<TM, TN, false, true>(c); else gemm_f32_lds_b<TM, TN, false, false>(c); }
+  return true;
+}
 // Op 34 on the fp32 MFMA engine: 64x64 tiles by default, 128x128 with flag 32, 256x128 with flag 64.
 __device__ __noinline__ void op_matmul_tile(const Ctx& c) {
   const int fl = c.i(11);

@@ -20,6 +20,11 @@ ARCH = os.environ.get('KVM_ARCH', 'gfx950')
 # Packed-FP32 instructions are disabled for all device code (they have given silently wrong results on these boxes).
 FLAGS = ['-O3', '-std=c++17', f'--offload-arch={ARCH}', '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
          '-Wno-unused-result', '-Wno-unused-value']
+# The executor library's device code also keeps MFMA results in VGPRs: the operator bodies read their accumulators
+# with VALU instructions (softmax, epilogues), and with accumulators in AGPRs every read is a v_accvgpr_read first
+# (over half the VALU instructions of the attention loops) and the extra registers are saved around each call.
+# GPT-162M step 10.06 -> 9.66 ms.
+LIB_FLAGS = FLAGS + ['-mllvm', '-amdgpu-mfma-vgpr-form']
 
 
 def build(verbose: bool = False) -> Path:
@@ -29,11 +34,7 @@ def build(verbose: bool = False) -> Path:
     # (device_order.txt): measured decode times moved by up to 2% with their placement alone (identical kernel code),
     # and a fixed order keeps edits elsewhere in the library from moving them.
     order = ['-ffunction-sections', '-Xoffload-linker', f'--symbol-ordering-file={CSRC / "device_order.txt"}']
-    # MFMA results in VGPRs: the operator bodies read their accumulators with VALU instructions (softmax, epilogues),
-    # and with accumulators in AGPRs every read is a v_accvgpr_read first (over half the VALU instructions of the
-    # attention loops) and the extra registers are saved around each call. GPT-162M step 10.06 -> 9.66 ms.
-    vform = ['-mllvm', '-amdgpu-mfma-vgpr-form']
-    cmd = [HIPCC, *FLAGS, *vform, *order, '-fPIC', '-shared', str(CSRC / 'exec.hip'), '-o', str(LIB)]
+    cmd = [HIPCC, *LIB_FLAGS, *order, '-fPIC', '-shared', str(CSRC / 'exec.hip'), '-o', str(LIB)]
     _run(cmd, verbose)
     cli = [HIPCC, *FLAGS, str(CSRC / 'cli.cpp'), '-o', str(CLI), f'-L{OUT}', '-lkvm_exec', f'-Wl,-rpath,$ORIGIN']
     _run(cli, verbose)

@@ -8,7 +8,9 @@ assembly and checks the compiled code itself:
     (scratch stores, i.e. register spills, are private and not counted).
 
 The kernels' own plain stores are executor bookkeeping read by the host after the launch (trace records, error
-details), not operator data.
+details), not operator data. Bodies inlined into a kernel (the GEMM tile main loops, the decode GEMV and attention
+split) store operator data only through write-through helpers or called epilogues, so the dispatch-case test and the
+private-segment test below cover what inlining can change. The assembly is compiled with the library's own flags.
 """
 import re
 import shutil
@@ -27,7 +29,7 @@ def asm(tmp_path_factory):
     if not shutil.which(kb.HIPCC) and not kb.Path(kb.HIPCC).exists():
         pytest.skip('hipcc not available')
     out = tmp_path_factory.mktemp('wt') / 'exec.s'
-    r = subprocess.run([kb.HIPCC, *kb.FLAGS, '--cuda-device-only', '-S', str(kb.CSRC / 'exec.hip'), '-o', str(out)],
+    r = subprocess.run([kb.HIPCC, *kb.LIB_FLAGS, '--cuda-device-only', '-S', str(kb.CSRC / 'exec.hip'), '-o', str(out)],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr[-2000:]
     return out.read_text()

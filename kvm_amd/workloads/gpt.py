@@ -238,7 +238,9 @@ class GPTBuilder:
         self.dep.record(t, R, W)
         return t
 
-    TILES_256 = 256    # bf16 GEMMs with at least this many 256x256 output tiles use them (op 304)
+    # bf16 GEMMs with at least this many 256x256 output tiles use them (op 304). Off: with the 128x256 tile inlined
+    # into the executor kernel, 128x256 tiles run the GPT-162M step in 8.93 ms against 9.08 with 256x256 tiles from 256.
+    TILES_256 = 1 << 30
     TILES_ALONE = 128  # a GEMM running alone with fewer 128x256 tiles than this uses 128x128 tiles
     TILES_MMA = 16     # else at least this many 128x256 tiles: op 122; else 128x128 tiles (op 114), more of them
     F32_TILES_128 = 64   # f32 GEMMs with at least this many 128x128 output tiles use them (op 34), else 64x64 tiles

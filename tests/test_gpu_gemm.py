@@ -14,7 +14,7 @@ import oracle
 from gpu_check import compare_run
 from kvm_amd import bundle as bl
 from kvm_amd import compiler
-from kvm_amd.executor import Executor
+from kvm_amd.executor import PATH_DYNAMIC, PATH_STATIC, Executor
 from kvm_amd.workloads import Builder, Workload
 
 pytestmark = pytest.mark.gpu
@@ -42,14 +42,18 @@ def _gemm_graph(M, N, K, flags, op='matmul_mma_bf16', adt='bf16', bdt='bf16', od
 
 
 def _check(w, tol_f32=2e-5, tol_bf16=4e-3):
+    """Each graph on both device paths: the dynamic kernel runs the 128x256 and 128x128 whole tiles inlined, the static
+    kernel calls the operator bodies; both against the same oracle run."""
     lb = bl.load(compiler.compile_spec(w.spec))
     init = [oracle.materialize(m, w.init_override.get(m['name'])) for m in lb.metadata['buffers']]
     ref = oracle.run(lb, [x.copy() for x in init])
-    ex = Executor.from_bundle(lb, buffers=init)
-    ex.run()
-    bad = compare_run(ex, lb.metadata, ref, tol_f32=tol_f32, tol_bf16=tol_bf16)
-    ex.close()
-    assert not bad, bad
+    for path in (PATH_DYNAMIC, PATH_STATIC):
+        ex = Executor.from_bundle(lb, buffers=[x.copy() for x in init], path=path)
+        ex.run()
+        assert ex.path() == path
+        bad = compare_run(ex, lb.metadata, ref, tol_f32=tol_f32, tol_bf16=tol_bf16)
+        ex.close()
+        assert not bad, (path, bad)
 
 
 @pytest.mark.parametrize('flags', [0, 1, 2, 3])
@@ -177,3 +181,11 @@ def test_mma_delta_tiles(flags):
             b.task('matmul_mma_bf16_delta', a='A', b='B', out='C', bias=None, res=None, pre=None, m0=m0, n0=n0, M=M, N=N, K=K,
                    flags=flags, alpha=0.5, o='O', delta='D', T=T, H=H, hd=64)
     _check(Workload(b.spec(), b.init_override))
+
+
+@pytest.mark.parametrize('flags,tiles', [(0, (64, 64)), (32 | 2, (128, 128)), (64 | 1, (256, 128))])
+def test_f32_whole_tiles_both_paths(flags, tiles):
+    """matmul_tile (op 34) on fp32 operands, whole tiles of each size (flag 32: 128x128, flag 64: 256x128), with bias:
+    the direct-to-LDS fp32 form, inlined into the static kernel at 64x64 / 128x128 and called from the dynamic one."""
+    print(f'f32 whole tiles flags {flags}', flush=True)
+    _check(_gemm_graph(256, 256, 128, flags, op='matmul_tile', adt='f32', bdt='f32', odt='f32', tiles=tiles, bias=True))

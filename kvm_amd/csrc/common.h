@@ -47,6 +47,7 @@ struct KvmCounters {
 
 // One ready queue. Head (consumer tickets) and tail (producer slots) sit on separate 128-byte lines.
 #define KVM_MAX_QUEUES 8
+#define KVM_PSTRIDE_MAX 16      // ints: 64 bytes between two static-path workers' progress words when padded
 #define KVM_OPMASK_IDS 1024
 struct KvmQueue {
   unsigned head; int pad0[31];
@@ -136,7 +137,8 @@ struct KvmDevState {
   const int* swait_off;
   const int* sw;
   const int* sflag;
-  int* sprogress;            // [grid]
+  int* sprogress;            // [grid * KVM_PSTRIDE_MAX]: worker w's position at sprogress[w * pstride]
+  int pstride;               // ints between two workers' positions: KVM_PSTRIDE_MAX (64 bytes each) or 1 (packed)
   int svariant;              // the static kernel's inlined operator set (kvm_static_kernel<V>)
   // Stream mode (stream != 0): FIFO queues of reused cells, ready64[q * qcap + (ticket & (qcap - 1))] = (round << 32) |
   // slot with round = ticket / qcap + 1 (0: empty); qcap a power of two above the slots' capacity.

@@ -636,7 +636,7 @@ __device__ bool static_wait(const KvmDevState& S, const int* ent, int cnt, int s
     for (unsigned polls = 0;; ++polls) {
       int have[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) have[u] = ww[u] >= 0 ? ld_relaxed(&S.sprogress[ww[u]]) : 0x7fffffff;
+      for (int u = 0; u < 4; ++u) have[u] = ww[u] >= 0 ? ld_relaxed(&S.sprogress[ww[u] * S.pstride]) : 0x7fffffff;
       bool mine = true;
 #pragma unroll
       for (int u = 0; u < 4; ++u) mine = mine && have[u] >= need[u];
@@ -761,7 +761,7 @@ __global__ __launch_bounds__(KVM_THREADS, 1) void kvm_static_kernel(KvmDevState 
         tr.end = wall_clock64();
       }
       if (pub_var >= 0) publish(S, slot, pub_var, pub_ver);
-      if (pub_pos) st_relaxed(&S.sprogress[w], i - p0 + 1);
+      if (pub_pos) st_relaxed(&S.sprogress[w * S.pstride], i - p0 + 1);
       st_relaxed(&S.done_blk[w], i - p0 + 1);
     }
   }
@@ -993,7 +993,7 @@ __global__ void kvm_reset_kernel(KvmDevState S, const int* base_versions) {
   }
   for (long long k = i; k < (long long)S.ncells; k += stride) S.ready[k] = -1;
   for (int k = i; k < S.nvars; k += stride) { S.version[k] = base_versions[k]; S.park_head[k] = -1; }
-  for (int k = i; k < S.grid; k += stride) { S.done_blk[k] = 0; if (S.sprogress) S.sprogress[k] = 0; }
+  for (int k = i; k < S.grid; k += stride) { S.done_blk[k] = 0; if (S.sprogress) S.sprogress[k * S.pstride] = 0; }
   for (int k = i; k < S.nq * S.nb * (S.ncls ? S.ncls : 1); k += stride) { KvmQueue z = {}; S.queues[k] = z; }
   if (i == 0) { KvmCounters z = {}; *S.cnt = z; }
   if (S.ncls && i < S.ncls) {   // class hot and statistics lines; the parameter line stays as uploaded
@@ -1844,7 +1844,6 @@ static int static_variant(const KvmExec* ex) {
       else if (M >= 5 && M <= 8) ++rows8;
     }
   }
-  if (getenv("KVM_STATIC_VARIANT")) return atoi(getenv("KVM_STATIC_VARIANT")) % 3;
   return rows8 > deep ? 2 : deep > 0 || attn4 > 0 ? 1 : 0;
 }
 
@@ -1870,6 +1869,11 @@ static int plan_static(KvmExec* ex, bool forced) {
   }
   ex->path = KVM_PATH_STATIC;
   ex->S.svariant = static_variant(ex);
+  // Progress words: one per 64 bytes for the general kernel (its tasks wait on a few workers each, and packed words
+  // shared a line among 16-32 publishing workers: tiny GPT 477 -> 457 us per step), packed for the decode kernels (a
+  // task there waits on a whole phase of up to 256 workers, whose packed words a poll reads in 8 lines: padded, decode
+  // measured 0.5-1.4% slower).
+  ex->S.pstride = ex->S.svariant == 0 ? KVM_PSTRIDE_MAX : 1;
   return 0;
 }
 
@@ -1991,7 +1995,7 @@ static int do_upload(KvmExec* ex) {
       };
       bool ok = upload_plan(ex->splan_d, ex->sdis);
       if (ex->cfg.trace_on) ok = ok && (ex->splan_d.dissolved ? upload_plan(ex->splan, ex->sfull) : (ex->sfull = ex->sdis, true));
-      ex->S.sprogress = (int*)alloc(ex->grid * sizeof(int));
+      ex->S.sprogress = (int*)alloc(ex->grid * KVM_PSTRIDE_MAX * sizeof(int));
       if (!ok || !ex->S.sprogress) { ex->err = "static path: device memory"; return KVM_STATUS_HIP_ERROR; }
     }
   }

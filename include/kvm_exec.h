@@ -161,6 +161,9 @@ int kvm_ntasks(const KvmExec* ex);
 // buffer; tracing costs a read-modify-write at every task start). No counterpart in the reference, whose trace is
 // fixed at creation; for benchmarks that time untraced runs and trace one more.
 int kvm_set_trace(KvmExec* ex, int on);
+// Whether the next launch traces (1) or not (0): the last kvm_set_trace, else the creation's trace_on. No counterpart
+// in the reference (see kvm_set_trace).
+int kvm_get_trace(const KvmExec* ex);
 // Name of a registry operator id, or NULL (reference: --check-ops).
 const char* kvm_op_name(int op_id);
 // Fills `out` with n SplitMix64 seeded values on the device and copies them back (initialiser known-answer test).

@@ -1093,6 +1093,7 @@ struct KvmExec {
   struct StaticDev { const int *prog_off = nullptr, *prog = nullptr, *wait_off = nullptr, *sw = nullptr, *flag = nullptr; int dissolved = 0; };
   StaticDev sfull, sdis;
   int last_dissolved = 0;                  // no-ops the last launch dissolved (counted as done)
+  int trace_req = 1;                       // kvm_set_trace's last request (launches trace when the buffer exists and this is set)
   // stream mode
   bool streaming = false, closed = false;
   KvmHostCtl* hctl = nullptr;              // pinned control block (host address)
@@ -1491,7 +1492,7 @@ static int stream_launch(KvmExec* ex) {
   HIPCK(hipHostGetDevicePointer(&dver, ex->hver, 0));
   S.hctl = (KvmHostCtl*)dctl; S.hwin = (const char*)dwin; S.hver = (int*)dver;
   S.stream = 1; S.wcap = c.window_cap; S.wtasks = c.window_tasks; S.wedges = c.window_edges;
-  S.ntasks = cap; S.nvars = (int)ex->base_versions.size(); S.trace_on = c.trace_on ? 1 : 0;
+  S.ntasks = cap; S.nvars = (int)ex->base_versions.size(); S.trace_on = c.trace_on && ex->trace_req ? 1 : 0;
   S.nq = nq; S.qcap = qcap; S.grid = ex->grid; S.nb = 1; S.ncells = 0;
   S.timeout_ticks = c.timeout_us * 100ull;
   if (ncls) {   // deadlines and bandwidth caps may concern any class: their head cells are always inspected
@@ -1976,6 +1977,7 @@ static int do_upload(KvmExec* ex) {
   const int rc = place_graph(g, ex->tasks, (int)ex->base_versions.size(), ex->grid, ex->cfg.trace_on != 0, ex->cfg.aging_us,
                              ex->cfg.timeout_us, alloc, ex->stream, ex->S, ex->L, ex->err);
   if (rc) return rc == KVM_STATUS_TOO_BIG ? KVM_STATUS_HIP_ERROR : rc;
+  ex->S.trace_on = ex->cfg.trace_on && ex->trace_req ? 1 : 0;   // a kvm_set_trace before the first launch holds
   ex->path = KVM_PATH_DYNAMIC;
   if (ncls) { if (int r = upload_classes(ex, alloc, has_dl.data(), has_bw.data(), pubcls, tbw, false)) return r; }
   if (ex->cfg.path != KVM_PATH_DYNAMIC && !ncls) {
@@ -2237,8 +2239,13 @@ int kvm_static_plan(const MvmTaskDesc* tasks, int ntasks, const int32_t* succ, i
 
 int kvm_set_trace(KvmExec* ex, int on) {
   if (on && !ex->cfg.trace_on) { ex->err = "kvm_set_trace: the executor was created without a trace buffer"; return KVM_STATUS_INVALID; }
+  ex->trace_req = on ? 1 : 0;
   ex->S.trace_on = on ? 1 : 0;
   return 0;
+}
+int kvm_get_trace(const KvmExec* ex) {
+  if (!ex) return KVM_STATUS_INVALID;
+  return ex->uploaded || ex->streaming ? ex->S.trace_on : (ex->cfg.trace_on && ex->trace_req ? 1 : 0);   // the launch state once it exists
 }
 
 const char* kvm_op_name(int op_id) { return kvm_registry_name(op_id); }

@@ -85,7 +85,7 @@ def lib():
             'kvm_buffer_dtype': (I, [P, I]), 'kvm_buffer_device_ptr': (P, [P, I]), 'kvm_write_buffer': (I, [P, I, P, U]),
             'kvm_read_buffer': (I, [P, I, P, U]), 'kvm_read_raw': (I, [P, I, P, U]), 'kvm_set_version': (I, [P, I, I]),
             'kvm_submit': (I, [P, P, I, P, I, P, I]), 'kvm_start': (I, [P]), 'kvm_finish': (I, [P, P]), 'kvm_relaunch': (I, [P]),
-            'kvm_run_timed': (I, [P, I, P]), 'kvm_run_timed_split': (I, [P, I, P, P]), 'kvm_versions': (I, [P, P, I]), 'kvm_trace': (I, [P, P, I]), 'kvm_ntasks': (I, [P]), 'kvm_set_trace': (I, [P, I]),
+            'kvm_run_timed': (I, [P, I, P]), 'kvm_run_timed_split': (I, [P, I, P, P]), 'kvm_versions': (I, [P, P, I]), 'kvm_trace': (I, [P, P, I]), 'kvm_ntasks': (I, [P]), 'kvm_set_trace': (I, [P, I]), 'kvm_get_trace': (I, [P]),
             'kvm_op_name': (ctypes.c_char_p, [I]),
             'kvm_validate': (I, [P, I, P, I, P, I, P, I, I, ctypes.c_char_p, I]),
             'kvm_seeded_fill_test': (I, [ctypes.c_ulonglong, ctypes.c_longlong, I, ctypes.c_float, ctypes.c_float, P]),
@@ -288,6 +288,10 @@ class Executor:
     def set_trace(self, on: bool):
         """Per-task tracing on / off for the following launches (needs an executor created with trace=True)."""
         self._check(lib().kvm_set_trace(self._h, int(on)), 'set_trace')
+
+    def tracing(self) -> bool:
+        """Whether the next launch traces (the last set_trace, else the creation's trace flag)."""
+        return lib().kvm_get_trace(self._h) == 1
 
     def start(self):
         self._check(lib().kvm_start(self._h), 'start')

@@ -114,3 +114,23 @@ def test_untraced_launches_run_the_plan_with_dissolved_noops():
         ex.run()
         check_schedule(ex, lb)
         ex.close()
+
+
+def test_trace_setting_before_the_first_launch_holds():
+    """set_trace(False) on an executor created with a trace buffer, before its first launch: the launches run untraced
+    (the graph upload at the first launch keeps the request), on the static path and on the dynamic one."""
+    from kvm_amd.workloads import gpt
+    for path in (PATH_STATIC, PATH_DYNAMIC):
+        w = gpt.build(gpt.GPTConfig.tiny(steps=1))
+        lb = bl.load(compiler.compile_spec(w.spec))
+        ex = Executor.from_bundle(lb, path=path, trace=True)
+        ex.set_trace(False)
+        assert not ex.tracing()
+        res = ex.run()
+        assert res['err_code'] == 0 and res['done'] == lb.ntasks
+        assert ex.path() == path and not ex.tracing()
+        ex.set_trace(True)
+        ex.relaunch()
+        ex.finish()
+        assert ex.tracing() and (ex.trace()['exec_count'] == 1).all()
+        ex.close()
